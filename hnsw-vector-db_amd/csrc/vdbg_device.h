@@ -1,0 +1,255 @@
+// vdbg_device.h -- device-side building blocks shared by every vdbg kernel (gfx950).
+//
+//  * exact distance functions that reproduce vdb's AVX-512 kernels bit for bit
+//    (src/distance/avx512.cc:19-64): 16-lane FMA accumulators and GCC's horizontal
+//    reduction tree.  The library is compiled with -ffp-contract=off, so the only fused
+//    operations are the explicit fmaf() calls standing for _mm512_fmadd_ps.
+//  * (dist, id) ordering with vdb's tie rule (include/vdb/types.h:23-25).
+//  * wave64 bitonic sorting and a streaming "WaveTopK" that keeps the n smallest keys of
+//    a stream in registers spread over the 64 lanes of one wavefront.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vdbg {
+
+constexpr int kWave = 64;
+constexpr uint32_t kNoId = 0xffffffffu;
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
+
+// Neighbor::operator< (include/vdb/types.h:23-25): distance first, then id.  Float
+// comparison keeps -0.0 == +0.0, as the reference does.
+__device__ __forceinline__ bool nb_less(float ad, uint32_t ai, float bd, uint32_t bi) {
+  return ad < bd || (ad == bd && ai < bi);
+}
+
+// ----------------------------------------------------------------- exact distances
+
+// _mm512_reduce_add_ps as GCC expands it: upper 256 bits + lower, upper 128 + lower,
+// lanes {0,1} + {2,3}, then lane 0 + lane 1.
+__device__ __forceinline__ float reduce16(const float (&v)[16]) {
+  float t3[8], t6[4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) t3[i] = v[8 + i] + v[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t6[i] = t3[4 + i] + t3[i];
+  return (t6[0] + t6[2]) + (t6[1] + t6[3]);
+}
+
+// l2_sq_avx512 (avx512.cc:19-33) for one (query, row) pair.  q and x are pd floats
+// (pd % 16 == 0), 16-byte aligned.
+__device__ __forceinline__ float l2_exact(const float* __restrict__ q,
+                                          const float* __restrict__ x, int pd) {
+  float acc0[16], acc1[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) acc0[l] = acc1[l] = 0.f;
+  int i = 0;
+  for (; i + 32 <= pd; i += 32) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float4 a = *reinterpret_cast<const float4*>(q + i + 4 * v);
+      float4 b = *reinterpret_cast<const float4*>(x + i + 4 * v);
+      float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+      acc0[4 * v + 0] = fmaf(d0, d0, acc0[4 * v + 0]);
+      acc0[4 * v + 1] = fmaf(d1, d1, acc0[4 * v + 1]);
+      acc0[4 * v + 2] = fmaf(d2, d2, acc0[4 * v + 2]);
+      acc0[4 * v + 3] = fmaf(d3, d3, acc0[4 * v + 3]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float4 a = *reinterpret_cast<const float4*>(q + i + 16 + 4 * v);
+      float4 b = *reinterpret_cast<const float4*>(x + i + 16 + 4 * v);
+      float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+      acc1[4 * v + 0] = fmaf(d0, d0, acc1[4 * v + 0]);
+      acc1[4 * v + 1] = fmaf(d1, d1, acc1[4 * v + 1]);
+      acc1[4 * v + 2] = fmaf(d2, d2, acc1[4 * v + 2]);
+      acc1[4 * v + 3] = fmaf(d3, d3, acc1[4 * v + 3]);
+    }
+  }
+  if (i < pd) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float4 a = *reinterpret_cast<const float4*>(q + i + 4 * v);
+      float4 b = *reinterpret_cast<const float4*>(x + i + 4 * v);
+      float d0 = a.x - b.x, d1 = a.y - b.y, d2 = a.z - b.z, d3 = a.w - b.w;
+      acc0[4 * v + 0] = fmaf(d0, d0, acc0[4 * v + 0]);
+      acc0[4 * v + 1] = fmaf(d1, d1, acc0[4 * v + 1]);
+      acc0[4 * v + 2] = fmaf(d2, d2, acc0[4 * v + 2]);
+      acc0[4 * v + 3] = fmaf(d3, d3, acc0[4 * v + 3]);
+    }
+  }
+  float s[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) s[l] = acc0[l] + acc1[l];
+  return reduce16(s);
+}
+
+// dot_avx512 (avx512.cc:35-44); the IP/cosine distance is its negation (:46).
+__device__ __forceinline__ float dot_exact(const float* __restrict__ q,
+                                           const float* __restrict__ x, int pd) {
+  float acc0[16], acc1[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) acc0[l] = acc1[l] = 0.f;
+  int i = 0;
+  for (; i + 32 <= pd; i += 32) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float4 a = *reinterpret_cast<const float4*>(q + i + 4 * v);
+      float4 b = *reinterpret_cast<const float4*>(x + i + 4 * v);
+      acc0[4 * v + 0] = fmaf(a.x, b.x, acc0[4 * v + 0]);
+      acc0[4 * v + 1] = fmaf(a.y, b.y, acc0[4 * v + 1]);
+      acc0[4 * v + 2] = fmaf(a.z, b.z, acc0[4 * v + 2]);
+      acc0[4 * v + 3] = fmaf(a.w, b.w, acc0[4 * v + 3]);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float4 a = *reinterpret_cast<const float4*>(q + i + 16 + 4 * v);
+      float4 b = *reinterpret_cast<const float4*>(x + i + 16 + 4 * v);
+      acc1[4 * v + 0] = fmaf(a.x, b.x, acc1[4 * v + 0]);
+      acc1[4 * v + 1] = fmaf(a.y, b.y, acc1[4 * v + 1]);
+      acc1[4 * v + 2] = fmaf(a.z, b.z, acc1[4 * v + 2]);
+      acc1[4 * v + 3] = fmaf(a.w, b.w, acc1[4 * v + 3]);
+    }
+  }
+  if (i < pd) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      float4 a = *reinterpret_cast<const float4*>(q + i + 4 * v);
+      float4 b = *reinterpret_cast<const float4*>(x + i + 4 * v);
+      acc0[4 * v + 0] = fmaf(a.x, b.x, acc0[4 * v + 0]);
+      acc0[4 * v + 1] = fmaf(a.y, b.y, acc0[4 * v + 1]);
+      acc0[4 * v + 2] = fmaf(a.z, b.z, acc0[4 * v + 2]);
+      acc0[4 * v + 3] = fmaf(a.w, b.w, acc0[4 * v + 3]);
+    }
+  }
+  float s[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) s[l] = acc0[l] + acc1[l];
+  return reduce16(s);
+}
+
+// MetricDistance (src/distance/cpu_features.cc:71-73): 0 = L2, else minus the dot.
+__device__ __forceinline__ float metric_exact(int metric, const float* q, const float* x,
+                                              int pd) {
+  return metric == 0 ? l2_exact(q, x, pd) : -dot_exact(q, x, pd);
+}
+
+// ----------------------------------------------------------------- wave bitonic
+
+// Keys live in registers: element g = e * 64 + lane for e in [0, E).  All loops unroll
+// at compile time, so every shuffle distance is a constant.
+template <int E>
+struct WaveKeys {
+  float d[E];
+  uint32_t id[E];
+};
+
+// One compare-exchange layer of a bitonic network over 64*E elements: partner g ^ j,
+// ascending in blocks where (g & size) == 0.
+template <int E>
+__device__ __forceinline__ void bitonic_layer(WaveKeys<E>& k, int size, int j) {
+  const int lane = lane_id();
+  if (j >= kWave) {
+    const int je = j / kWave;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int pe = e ^ je;
+      if (pe > e) {
+        const int g = e * kWave + lane;
+        const bool up = (g & size) == 0;
+        const bool sw = up ? nb_less(k.d[pe], k.id[pe], k.d[e], k.id[e])
+                           : nb_less(k.d[e], k.id[e], k.d[pe], k.id[pe]);
+        if (sw) {
+          float td = k.d[e];
+          k.d[e] = k.d[pe];
+          k.d[pe] = td;
+          uint32_t ti = k.id[e];
+          k.id[e] = k.id[pe];
+          k.id[pe] = ti;
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int g = e * kWave + lane;
+      const float pd = __shfl_xor(k.d[e], j);
+      const uint32_t pi = __shfl_xor(k.id[e], j);
+      const bool up = (g & size) == 0;
+      const bool lower = (lane & j) == 0;
+      const bool take = (lower == up) ? nb_less(pd, pi, k.d[e], k.id[e])
+                                      : nb_less(k.d[e], k.id[e], pd, pi);
+      if (take) {
+        k.d[e] = pd;
+        k.id[e] = pi;
+      }
+    }
+  }
+}
+
+// Full ascending sort of 64*E keys.
+template <int E>
+__device__ __forceinline__ void bitonic_sort(WaveKeys<E>& k) {
+  constexpr int N = kWave * E;
+#pragma unroll
+  for (int size = 2; size <= N; size <<= 1) {
+#pragma unroll
+    for (int j = size >> 1; j > 0; j >>= 1) bitonic_layer<E>(k, size, j);
+  }
+}
+
+// Sorts a bitonic sequence of 64*E keys ascending.
+template <int E>
+__device__ __forceinline__ void bitonic_merge(WaveKeys<E>& k) {
+  constexpr int N = kWave * E;
+#pragma unroll
+  for (int j = N >> 1; j > 0; j >>= 1) bitonic_layer<E>(k, N, j);
+}
+
+// The n = 64*E smallest keys of a stream, kept sorted ascending across the wave.  Insert
+// a batch of up to 64 keys (one per lane, +inf/kNoId for none): the batch is sorted,
+// reversed against the tail of the list (the minimum of an ascending and a descending
+// sequence is bitonic and holds the n smallest), then merged.
+template <int E>
+struct WaveTopK {
+  WaveKeys<E> k;
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      k.d[e] = __builtin_inff();
+      k.id[e] = kNoId;
+    }
+  }
+
+  // The current n-th smallest key (broadcast to every lane).
+  __device__ __forceinline__ void threshold(float& td, uint32_t& ti) const {
+    td = __shfl(k.d[E - 1], kWave - 1);
+    ti = __shfl(k.id[E - 1], kWave - 1);
+  }
+
+  // Wave-uniform call.  Inserts the lanes' keys; lanes with nothing pass +inf/kNoId.
+  __device__ __forceinline__ void insert(float cd, uint32_t ci) {
+    float td;
+    uint32_t ti;
+    threshold(td, ti);
+    const bool want = nb_less(cd, ci, td, ti);
+    if (__ballot(want) == 0) return;
+    WaveKeys<1> b;
+    b.d[0] = want ? cd : __builtin_inff();
+    b.id[0] = want ? ci : kNoId;
+    bitonic_sort<1>(b);
+    const int lane = lane_id();
+    const float rd = __shfl(b.d[0], kWave - 1 - lane);
+    const uint32_t ri = __shfl(b.id[0], kWave - 1 - lane);
+    if (nb_less(rd, ri, k.d[E - 1], k.id[E - 1])) {
+      k.d[E - 1] = rd;
+      k.id[E - 1] = ri;
+    }
+    bitonic_merge<E>(k);
+  }
+};
+
+}  // namespace vdbg

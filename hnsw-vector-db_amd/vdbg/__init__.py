@@ -1,0 +1,190 @@
+"""vdbg: Python bindings (ctypes) for the gfx950 search backend in libvdbg.so.
+
+The product is the C ABI in include/vdbg.h; this module is a thin host-side mirror used by
+the tests and the benchmark.  Importing it loads libvdbg.so from this directory and fails
+loudly when the library is missing: there is no CPU fallback.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libvdbg.so")
+
+METRICS = {"l2": 0, "ip": 1, "cosine": 2}
+NO_ID = 0xFFFFFFFF
+
+# Status::Code names (include/vdb/status.h:14-26)
+CODE_NAMES = {
+    0: "OK", 1: "InvalidArgument", 2: "NotFound", 3: "AlreadyExists", 4: "IOError",
+    5: "Corruption", 6: "FailedPrecondition", 7: "ResourceExhausted", 8: "Unavailable",
+    9: "NotSupported", 10: "Internal",
+}
+
+
+class VdbgError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{CODE_NAMES.get(code, code)}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"libvdbg.so is not built ({LIB_PATH}); run __graft_entry__.build() first")
+    return C.CDLL(LIB_PATH)
+
+
+lib = _load()
+
+_vp = C.c_void_p
+_sz = C.c_size_t
+_SIGS = {
+    "vdbg_version": (C.c_int, []),
+    "vdbg_last_error": (C.c_char_p, []),
+    "vdbg_ctx_create": (C.c_int, [C.c_int, C.POINTER(_vp)]),
+    "vdbg_ctx_destroy": (C.c_int, [_vp]),
+    "vdbg_ctx_stream": (_vp, [_vp]),
+    "vdbg_ctx_synchronize": (C.c_int, [_vp]),
+    "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
+    "vdbg_profile_reset": (C.c_int, [_vp]),
+    "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
+                                   C.POINTER(C.c_uint64)]),
+    "vdbg_dataset_create": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, C.POINTER(_vp)]),
+    "vdbg_dataset_create_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int,
+                                             C.POINTER(_vp)]),
+    "vdbg_dataset_destroy": (C.c_int, [_vp]),
+    "vdbg_dataset_rows": (_vp, [_vp]),
+    "vdbg_flat_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp,
+                                        C.POINTER(C.c_uint64)]),
+    "vdbg_flat_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "vdbg_last_fallbacks": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
+}
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def _check(rc):
+    if rc != 0:
+        raise VdbgError(rc, lib.vdbg_last_error().decode(errors="replace"))
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(_vp)
+
+
+def padded_dim(dim):
+    """PaddedDim (include/vdb/types.h:30-32): a multiple of 16 floats."""
+    return (dim + 15) // 16 * 16
+
+
+def pad_rows(x, pd=None):
+    x = np.asarray(x, np.float32)
+    n, d = x.shape
+    pd = padded_dim(d) if pd is None else pd
+    if pd == d:
+        return np.ascontiguousarray(x)
+    out = np.zeros((n, pd), np.float32)
+    out[:, :d] = x
+    return out
+
+
+class Context:
+    """A device, its stream and workspace (vdbg_ctx)."""
+
+    def __init__(self, device=0):
+        h = _vp()
+        _check(lib.vdbg_ctx_create(device, C.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib.vdbg_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def stream(self):
+        return lib.vdbg_ctx_stream(self.h)
+
+    def synchronize(self):
+        _check(lib.vdbg_ctx_synchronize(self.h))
+
+    def profile(self, enable=True):
+        _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))
+
+    def profile_reset(self):
+        _check(lib.vdbg_profile_reset(self.h))
+
+    def profile_get(self, name):
+        ms = C.c_double()
+        n = C.c_uint64()
+        _check(lib.vdbg_profile_get(self.h, name.encode(), C.byref(ms), C.byref(n)))
+        return ms.value, n.value
+
+    def last_fallbacks(self):
+        n = C.c_uint64()
+        _check(lib.vdbg_last_fallbacks(self.h, C.byref(n)))
+        return n.value
+
+
+class Dataset:
+    """A segment's rows resident in HBM (vdbg_dataset)."""
+
+    def __init__(self, ctx, rows, dim, metric="l2"):
+        rows = np.ascontiguousarray(rows, np.float32)
+        n, pd = rows.shape
+        h = _vp()
+        _check(lib.vdbg_dataset_create(ctx.h, _ptr(rows), n, dim, pd, METRICS[metric],
+                                       C.byref(h)))
+        self.ctx, self.h, self.n, self.dim, self.pd = ctx, h, n, dim, pd
+        self.metric = metric
+
+    @classmethod
+    def from_device(cls, ctx, rows_ptr, n, dim, pd, metric="l2"):
+        self = cls.__new__(cls)
+        h = _vp()
+        _check(lib.vdbg_dataset_create_device(ctx.h, rows_ptr, n, dim, pd, METRICS[metric],
+                                              C.byref(h)))
+        self.ctx, self.h, self.n, self.dim, self.pd = ctx, h, n, dim, pd
+        self.metric = metric
+        return self
+
+    def close(self):
+        if self.h:
+            lib.vdbg_dataset_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def flat_search(self, queries, k, allow=None):
+        """Host arrays in and out: (ids uint32 [nq, k], dists float32 [nq, k])."""
+        q = np.ascontiguousarray(queries, np.float32)
+        nq = q.shape[0]
+        assert q.shape[1] == self.pd
+        ids = np.empty((nq, k), np.uint32)
+        dists = np.empty((nq, k), np.float32)
+        if allow is not None:
+            allow = np.ascontiguousarray(allow, np.uint64)
+        dc = C.c_uint64()
+        _check(lib.vdbg_flat_search_host(self.h, _ptr(q), nq, k, _ptr(allow), _ptr(ids),
+                                         _ptr(dists), C.byref(dc)))
+        return ids, dists
+
+    def flat_search_device(self, q_ptr, nq, k, ids_ptr, dists_ptr, allow_ptr=None,
+                           stream=None):
+        """Device pointers (ints), queued on `stream` (None = the context's stream)."""
+        _check(lib.vdbg_flat_search_device(self.h, q_ptr, nq, k, allow_ptr, ids_ptr,
+                                           dists_ptr, stream))

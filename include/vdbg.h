@@ -1,0 +1,123 @@
+/*
+ * vdbg.h -- C ABI of the MI355X (gfx950) search backend for vdb's nearest-neighbour path.
+ *
+ * This is the drop-in boundary: plain pointers and sizes, no C++ or framework types.  vdb's
+ * C++ Index implementations (or any FFI) bind these entry points; see INTEGRATION.md for the
+ * GpuFlatIndex / GpuSq8Index / GpuIvfPqIndex adapters a vdb maintainer would add.
+ *
+ * Conventions
+ *  - Every call returns an int equal to vdb::Status::Code (include/vdb/status.h:14-26):
+ *    0 ok, 1 invalid argument, 2 not found, 3 already exists, 4 I/O error, 5 corruption,
+ *    6 failed precondition, 7 resource exhausted, 8 unavailable, 9 not supported,
+ *    10 internal.  vdbg_last_error() gives the calling thread's last message.
+ *  - Metrics: 0 = L2 (squared), 1 = inner product (minus dot), 2 = cosine (minus dot over
+ *    vectors normalised at insert and at query), as include/vdb/types.h:13-17.
+ *  - Rows and queries are padded_dim floats, zero padded (padded_dim % 16 == 0,
+ *    include/vdb/types.h:30-32).  Results are row-major [nq][k], ascending by (dist, id)
+ *    with ties broken by id (include/vdb/types.h:23-25), padded with
+ *    (UINT32_MAX, +inf) when fewer than k rows are allowed (python/bindings.cc:131-136).
+ *  - Distances are the reference's AVX-512 kernels' values bit for bit
+ *    (src/distance/avx512.cc:19-64).
+ *  - Filters are dense bitmasks: bit r of word r/64 set = row r allowed.  They replace
+ *    RowFilter::allowed (src/index/index.h:23-27): a DeleteFilter (src/engine/planner.cc:12-19)
+ *    is the complement of the DeleteBits words (src/util/delete_bits.h:50-55); a BitmapFilter
+ *    (:21-29) is the roaring result minus deletes, expanded to words.
+ *  - "_host" entry points take host pointers and block until results are on the host.
+ *    "_device" entry points take device pointers, run on the given HIP stream (NULL = the
+ *    context's stream) and return once the work is queued; inputs must stay valid until the
+ *    stream reaches that point.
+ *  - All entry points on one context are serialised by the context; use one context per
+ *    thread for concurrency.
+ */
+#ifndef VDBG_H_
+#define VDBG_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vdbg_ctx vdbg_ctx;
+typedef struct vdbg_dataset vdbg_dataset;
+
+enum {
+  VDBG_OK = 0,
+  VDBG_INVALID_ARGUMENT = 1,
+  VDBG_NOT_FOUND = 2,
+  VDBG_ALREADY_EXISTS = 3,
+  VDBG_IO_ERROR = 4,
+  VDBG_CORRUPTION = 5,
+  VDBG_FAILED_PRECONDITION = 6,
+  VDBG_RESOURCE_EXHAUSTED = 7,
+  VDBG_UNAVAILABLE = 8,
+  VDBG_NOT_SUPPORTED = 9,
+  VDBG_INTERNAL = 10
+};
+
+enum { VDBG_METRIC_L2 = 0, VDBG_METRIC_IP = 1, VDBG_METRIC_COSINE = 2 };
+
+/* Library version, (major << 16) | minor. */
+int vdbg_version(void);
+
+/* The calling thread's last error message ("" when none). */
+const char* vdbg_last_error(void);
+
+/* ---------------------------------------------------------------- context */
+
+/* A device, its stream and reusable device workspace.  Replaces nothing in the reference
+ * (vdb's CPU indexes need no device state); owned by the GPU Index adapters. */
+int vdbg_ctx_create(int device, vdbg_ctx** out);
+int vdbg_ctx_destroy(vdbg_ctx* ctx);
+/* The context's HIP stream (a hipStream_t), for callers that order their own work with it. */
+void* vdbg_ctx_stream(vdbg_ctx* ctx);
+/* Waits for all work queued on the context's stream. */
+int vdbg_ctx_synchronize(vdbg_ctx* ctx);
+
+/* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
+ * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch
+ * count of kernel `name` since the last reset (after synchronising). */
+int vdbg_profile_enable(vdbg_ctx* ctx, int enable);
+int vdbg_profile_reset(vdbg_ctx* ctx);
+int vdbg_profile_get(vdbg_ctx* ctx, const char* name, double* total_ms, uint64_t* launches);
+
+/* ---------------------------------------------------------------- datasets */
+
+/* Makes a segment's rows resident in HBM: the device copy of the VectorView an Index reads
+ * (src/util/aligned_buffer.h:56-63, filled from the segment mmap at
+ * src/storage/segment_reader.cc:56-59).  rows is n x padded_dim floats on the host.  Row
+ * norms and value statistics used by the GEMM formulation are computed once here. */
+int vdbg_dataset_create(vdbg_ctx* ctx, const float* rows, size_t n, size_t dim,
+                        size_t padded_dim, int metric, vdbg_dataset** out);
+/* The same from rows already in device memory (copied; the caller keeps ownership). */
+int vdbg_dataset_create_device(vdbg_ctx* ctx, const float* rows_dev, size_t n, size_t dim,
+                               size_t padded_dim, int metric, vdbg_dataset** out);
+int vdbg_dataset_destroy(vdbg_dataset* ds);
+/* Device pointer to the resident rows (n x padded_dim floats). */
+const float* vdbg_dataset_rows(vdbg_dataset* ds);
+
+/* ---------------------------------------------------------------- flat exact search */
+
+/* Exact top-k for nq queries: FlatIndex::search (src/index/flat_index.cc:73-77, which is
+ * FlatSearch :11-39 without a pool) for every query, and FlatSearchBatch (:41-68), which
+ * returns the same results.  allow_words (nullable) has ceil(n/64) words.  dist_comps
+ * (nullable) receives IndexSearchStats::distance_computations for the batch (rows per
+ * query, as :75-76 adds).  Host pointers. */
+int vdbg_flat_search_host(vdbg_dataset* ds, const float* queries, size_t nq, size_t k,
+                          const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
+                          uint64_t* dist_comps);
+/* Device-pointer variant of vdbg_flat_search_host, queued on `stream`. */
+int vdbg_flat_search_device(vdbg_dataset* ds, const float* queries, size_t nq, size_t k,
+                            const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
+                            void* stream);
+
+/* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
+ * candidates could not be certified and were re-scanned exactly. */
+int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VDBG_H_ */

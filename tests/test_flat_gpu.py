@@ -1,0 +1,97 @@
+"""Flat exact search on the GPU against the oracle (FlatIndex::search semantics,
+src/index/flat_index.cc:11-39): ids bit-exact under the (dist, id) tie rule, distances
+bit-exact to the reference's AVX-512 kernel (the oracle restates it lane by lane)."""
+import numpy as np
+import pytest
+
+import vdbg
+from vdbg import datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_equal(gi, gd, oi, od):
+    assert gi.shape == oi.shape
+    bad = np.nonzero((gi != oi).any(axis=1) | (gd.view(np.uint32) != od.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, (
+        f"{bad.size} queries differ; first q={bad[0]} gpu={gi[bad[0]].tolist()} "
+        f"{gd[bad[0]].tolist()} oracle={oi[bad[0]].tolist()} {od[bad[0]].tolist()}")
+
+
+@pytest.mark.parametrize("n,nq,k", [(100, 5, 10), (5000, 40, 10), (20000, 300, 10),
+                                    (20000, 300, 100), (4099, 33, 1)])
+def test_flat_uniform_matches_oracle(ctx, oracle, n, nq, k):
+    print(f"flat uniform n={n} nq={nq} k={k}", flush=True)
+    base = datagen.uniform_rows(n, 128, 1001)
+    qs = datagen.uniform_rows(nq, 128, 1002)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, k)
+    od, oi = oracle.flat_search(base, qs, k)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("n,nq,k", [(50000, 200, 10), (50000, 130, 100)])
+def test_flat_sift_like_ties(ctx, oracle, n, nq, k):
+    # integer-valued data: exact GEMM arithmetic, many distance ties broken by id
+    print(f"flat sift-like n={n} nq={nq} k={k}", flush=True)
+    base = datagen.sift_like(n, 128, 2002)
+    qs = datagen.sift_like(nq, 128, 2003)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, k)
+    od, oi = oracle.flat_search(base, qs, k)
+    _check_equal(gi, gd, oi, od)
+    assert ctx.last_fallbacks() == 0
+
+
+def test_flat_k_larger_than_rows(ctx, oracle):
+    base = datagen.uniform_rows(5, 128, 7)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(base[:1], 100)
+    assert (gi[0, :5] != vdbg.NO_ID).all() and (gi[0, 5:] == vdbg.NO_ID).all()
+    assert gi[0, 0] == 0
+    assert np.isinf(gd[0, 5:]).all()
+
+
+def test_flat_duplicate_rows_tie_by_id(ctx, oracle):
+    rng = np.random.default_rng(3)
+    uniq = rng.random((50, 128), dtype=np.float32)
+    base = uniq[rng.integers(0, 50, 6000)]
+    qs = uniq[:40].copy()
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 10)
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_flat_filter_respected(ctx, oracle):
+    base = datagen.uniform_rows(20000, 128, 11)
+    qs = datagen.uniform_rows(64, 128, 12)
+    allow = np.zeros((20000 + 63) // 64, np.uint64)
+    rows = np.arange(1, 20000, 2)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 50, allow=allow)
+    assert (gi % 2 == 1).all()
+    od, oi = oracle.flat_search(base, qs, 50, allow=allow)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("metric", ["ip", "cosine"])
+def test_flat_inner_product(ctx, oracle, metric):
+    base = datagen.clustered_unit(20000, 128, 21, 22, 100, 0.5)
+    qs = datagen.clustered_unit(100, 128, 23, 22, 100, 0.5)
+    ds = vdbg.Dataset(ctx, base, 128, metric=metric)
+    gi, gd = ds.flat_search(qs, 10)
+    od, oi = oracle.flat_search(base, qs, 10, metric=metric)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("dim", [7, 37, 100, 384])
+def test_flat_other_dims(ctx, oracle, dim):
+    pd = vdbg.padded_dim(dim)
+    base = datagen.pad(datagen.uniform_rows(6000, dim, 31), pd)
+    qs = datagen.pad(datagen.uniform_rows(40, dim, 32), pd)
+    ds = vdbg.Dataset(ctx, base, dim)
+    gi, gd = ds.flat_search(qs, 10)
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
