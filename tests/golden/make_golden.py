@@ -1,0 +1,185 @@
+"""Writes the golden fixtures under tests/golden/ from the reference's own code.
+
+Runs only where oracle/_ref/libvdbref.so was built from the reference's sources (oracle/
+Makefile).  Every expected output below is produced by the reference's functions
+(src/distance/*.cc, src/util/topk.h, src/index/flat_index.cc, src/index/quant/*.cc,
+src/index/index.cc, src/util/dataset.cc, src/util/crc32c.cc) on small seeded inputs; the
+fixtures are data only (.npz without pickles): inputs and expected outputs.
+
+    python3 tests/golden/make_golden.py
+"""
+import ctypes as C
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(HERE))
+from oracle_lib import KSET, METRIC, load_reference  # noqa: E402
+
+KSETS = ["scalar", "avx2", "avx512"]
+
+
+def f32(x):
+    return np.ascontiguousarray(x, np.float32)
+
+
+def main():
+    ref = load_reference()
+    if ref is None:
+        sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+    L = ref.lib
+    rng = np.random.default_rng(20260101)
+
+    # ---- distance kernels: bit patterns for every kernel set
+    dims = [16, 32, 48, 128, 384]
+    rows = []
+    for d in dims:
+        for _ in range(64):
+            rows.append(d)
+    a = [f32(rng.standard_normal(d) * rng.choice([1e-3, 1.0, 100.0])) for d in rows]
+    b = [f32(rng.standard_normal(d) * rng.choice([1e-3, 1.0, 100.0])) for d in rows]
+    codes = [rng.integers(0, 256, d).astype(np.uint8) for d in rows]
+    vmin = [f32(rng.uniform(-2, 2, d)) for d in rows]
+    scale = [f32(np.abs(rng.uniform(-2, 2, d)) / 255) for d in rows]
+    maxd = max(dims)
+
+    def padm(v, dt):
+        out = np.zeros((len(v), maxd), dt)
+        for i, x in enumerate(v):
+            out[i, :len(x)] = x
+        return out
+
+    res = {}
+    for ks in KSETS:
+        e = ks.encode()
+        res[f"l2_{ks}"] = f32([L.ref_l2(e, x, y, len(x)) for x, y in zip(a, b)])
+        res[f"dot_{ks}"] = f32([L.ref_dot(e, x, y, len(x)) for x, y in zip(a, b)])
+        res[f"sq8l2_{ks}"] = f32([L.ref_sq8_l2(e, x, c, m, s, len(x))
+                                   for x, c, m, s in zip(a, codes, vmin, scale)])
+        res[f"sq8ip_{ks}"] = f32([L.ref_sq8_ip(e, x, c, m, s, len(x))
+                                   for x, c, m, s in zip(a, codes, vmin, scale)])
+    res["l2any"] = f32([L.ref_l2sq_any(x, y, len(x) - 3) for x, y in zip(a, b)])
+    res["dotany"] = f32([L.ref_dot_any(x, y, len(x) - 3) for x, y in zip(a, b)])
+    np.savez_compressed(os.path.join(HERE, "distances.npz"), dims=np.array(rows, np.int32),
+                        a=padm(a, np.float32), b=padm(b, np.float32),
+                        codes=padm(codes, np.uint8), vmin=padm(vmin, np.float32),
+                        scale=padm(scale, np.float32), **res)
+
+    # ---- top-k with heavy ties (pattern of tests/topk_test.cc:14-33)
+    tk = {}
+    for t in range(40):
+        n = int(rng.integers(1, 400))
+        k = int(rng.integers(1, 60))
+        vals = f32(rng.integers(0, 5 if t % 2 == 0 else 1000, n))
+        ids = rng.permutation(n).astype(np.uint32)
+        od = np.empty(k, np.float32)
+        oi = np.empty(k, np.uint32)
+        m = L.ref_topk(vals, ids, n, k, od, oi)
+        tk[f"d{t}"], tk[f"i{t}"], tk[f"k{t}"] = vals, ids, np.array([k])
+        tk[f"od{t}"], tk[f"oi{t}"] = od[:m], oi[:m]
+    np.savez_compressed(os.path.join(HERE, "topk.npz"), **tk)
+
+    # ---- flat search, every metric, a filter, k > rows
+    dim, pd = 37, 48
+    base = np.zeros((3000, pd), np.float32)
+    base[:, :dim] = rng.standard_normal((3000, dim))
+    base[1500:2000] = base[:500]  # duplicate rows: distance ties broken by id
+    qs = np.zeros((25, pd), np.float32)
+    qs[:, :dim] = rng.standard_normal((25, dim))
+    allow = np.zeros((3000 + 63) // 64, np.uint64)
+    r = np.arange(0, 3000, 3)
+    np.bitwise_or.at(allow, r // 64, np.uint64(1) << (r % 64).astype(np.uint64))
+    fl = {"base": base, "queries": qs, "allow": allow}
+    for met in ["l2", "ip"]:
+        for ks in KSETS:
+            od, oi = ref.flat_search(base, dim, qs, 10, metric=met, kset=ks)
+            fl[f"{met}_{ks}_d"], fl[f"{met}_{ks}_i"] = od, oi
+        od, oi = ref.flat_search(base, dim, qs, 10, metric=met, kset="avx512", allow=allow)
+        fl[f"{met}_allow_d"], fl[f"{met}_allow_i"] = od, oi
+    od, oi = ref.flat_search(base[:5], dim, qs[:3], 8, kset="avx512")
+    fl["small_d"], fl["small_i"] = od, oi
+    np.savez_compressed(os.path.join(HERE, "flat.npz"), **fl)
+
+    # ---- SQ8: train, encode, scan + rerank
+    dim, pd = 100, 112
+    sb = np.zeros((600, pd), np.float32)
+    sb[:, :dim] = rng.standard_normal((600, dim)) * 3.0
+    sb[:, 5] = 1.25  # a constant column: scale 0, code 0
+    vmin = np.empty(pd, np.float32)
+    scale = np.empty(pd, np.float32)
+    codes = np.empty((600, pd), np.uint8)
+    L.ref_sq8_train_encode(sb, 600, dim, pd, vmin, scale, codes)
+    sq = np.zeros((12, pd), np.float32)
+    sq[:, :dim] = rng.standard_normal((12, dim)) * 3.0
+    s8 = {"base": sb, "vmin": vmin, "scale": scale, "codes": codes, "queries": sq}
+    for met in ["l2", "ip"]:
+        od = np.empty((12, 10), np.float32)
+        oi = np.empty((12, 10), np.uint32)
+        L.ref_sq8_search_batch(b"avx512", METRIC[met], sb, codes, 600, dim, pd, vmin, scale,
+                               sq, 12, 10, 50, od, oi, 1)
+        s8[f"{met}_d"], s8[f"{met}_i"] = od, oi
+    np.savez_compressed(os.path.join(HERE, "sq8.npz"), **s8)
+
+    # ---- PQ: trained codebook, codes, tables, ADC
+    dim, m = 32, 8
+    pdata = f32(rng.standard_normal((2000, dim)))
+    cen = np.empty(m * 256 * (dim // m), np.float32)
+    assert L.ref_pq_train(pdata, 2000, dim, dim, m, 42, 256, cen) == 0
+    pcodes = np.empty((2000, m), np.uint8)
+    assert L.ref_pq_encode(cen, dim, m, pdata, 2000, dim, pcodes) == 0
+    pqq = f32(rng.standard_normal((4, dim)))
+    tabs = {}
+    for met in ["l2", "ip"]:
+        t = np.empty((4, m * 256), np.float32)
+        for i in range(4):
+            assert L.ref_pq_table(cen, dim, m, pqq[i], METRIC[met], t[i]) == 0
+        tabs[f"table_{met}"] = t
+        tabs[f"adc_{met}"] = f32([[L.ref_pq_adc(cen, dim, m, t[i], pcodes[j]) for j in range(50)]
+                                  for i in range(4)])
+    np.savez_compressed(os.path.join(HERE, "pq.npz"), data=pdata, centroids=cen, codes=pcodes,
+                        queries=pqq, **tabs)
+
+    # ---- k-means and AssignNearest
+    kd = f32(rng.standard_normal((3000, 16)))
+    kc = np.empty(40 * 16, np.float32)
+    assert L.ref_kmeans(kd, 3000, 16, 16, 40, 25, 1234, 256, 1, kc) == 0
+    kc2 = np.empty(40 * 16, np.float32)
+    assert L.ref_kmeans(kd, 3000, 16, 16, 40, 10, 99, 32, 0, kc2) == 0  # subsampled, random init
+    asg = np.empty(3000, np.uint32)
+    dist = np.empty(3000, np.float32)
+    L.ref_assign_nearest(kd, 3000, 16, 16, kc, 40, asg, dist)
+    np.savez_compressed(os.path.join(HERE, "kmeans.npz"), data=kd, centroids_pp=kc,
+                        centroids_rand=kc2, assign=asg, dist=dist)
+
+    # ---- IVF-PQ: an index built and saved by the reference, and its search results
+    dim = 32
+    ib = f32(rng.standard_normal((5000, dim)) * 2.0)
+    iq = f32(rng.standard_normal((30, dim)) * 2.0)
+    blob = ref.ivfpq_build(ib, dim, nlist=24, m=8, seed=42, max_points=64)
+    iv = {"base": ib, "queries": iq, "index_file": np.frombuffer(blob, np.uint8).copy()}
+    for nprobe, rr in [(1, 0), (4, 0), (4, -1), (24, 0), (24, 5000)]:
+        od = np.empty((30, 10), np.float32)
+        oi = np.empty((30, 10), np.uint32)
+        dc = np.empty(30, np.uint64)
+        assert L.ref_ivfpq_search_batch(0, blob, len(blob), ib, 5000, dim, dim, iq, 30, 10,
+                                        nprobe, rr, None, od, oi, dc, 1) == 0
+        tag = f"np{nprobe}_r{rr if rr >= 0 else 'auto'}"
+        iv[f"{tag}_d"], iv[f"{tag}_i"], iv[f"{tag}_dc"] = od, oi, dc
+    np.savez_compressed(os.path.join(HERE, "ivfpq.npz"), **iv)
+
+    # ---- NormalizeVector and CRC32C
+    nv = f32(rng.standard_normal((50, 33)) * rng.uniform(0.01, 100, (50, 1)))
+    nv[7] = 0.0
+    outn = nv.copy()
+    okn = np.array([L.ref_normalize(outn[i], 33) for i in range(50)], np.int32)
+    blobs = [b"", b"123456789", bytes(rng.integers(0, 256, 1000).astype(np.uint8))]
+    crc = np.array([L.ref_crc32c(x, len(x)) for x in blobs], np.uint32)
+    np.savez_compressed(os.path.join(HERE, "misc.npz"), norm_in=nv, norm_out=outn, norm_ok=okn,
+                        crc_blob=np.frombuffer(blobs[2], np.uint8).copy(), crc=crc)
+    print("golden fixtures written to", HERE)
+
+
+if __name__ == "__main__":
+    main()

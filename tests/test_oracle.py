@@ -1,0 +1,362 @@
+"""The oracle (oracle/vdb_oracle.c) pinned before it is trusted as the GPU's checker.
+
+Three kinds of evidence per function:
+  * golden vectors written by the reference's own code (tests/golden/make_golden.py);
+  * the compiled reference itself on fresh random inputs (skipped where oracle/_ref is
+    not built, e.g. on a box without the reference sources);
+  * closed forms and invariants the mathematics fixes (sorting, brute force, half-step
+    reconstruction, ADC == distance to the decoded vector, exhaustive IVF == flat).
+"""
+import os
+
+import numpy as np
+import pytest
+
+from ivf_file import parse_ivfpq
+from oracle_lib import KSET, METRIC
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def gold(name):
+    return np.load(os.path.join(GOLD, name + ".npz"), allow_pickle=False)
+
+
+def bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------------------ distances
+
+def test_distance_kernels_match_golden_bit_patterns(oracle):
+    g = gold("distances")
+    L = oracle.lib
+    for i, d in enumerate(g["dims"]):
+        a, b = g["a"][i, :d].copy(), g["b"][i, :d].copy()
+        c, vm, sc = g["codes"][i, :d].copy(), g["vmin"][i, :d].copy(), g["scale"][i, :d].copy()
+        for ks in ["scalar", "avx2", "avx512"]:
+            assert bits(L.or_l2(KSET[ks], a, b, d)) == bits(g[f"l2_{ks}"][i]), (ks, i, d)
+            assert bits(L.or_dot(KSET[ks], a, b, d)) == bits(g[f"dot_{ks}"][i]), (ks, i, d)
+            assert bits(L.or_sq8_l2(KSET[ks], a, c, vm, sc, d)) == bits(g[f"sq8l2_{ks}"][i])
+            assert bits(L.or_sq8_ip(KSET[ks], a, c, vm, sc, d)) == bits(g[f"sq8ip_{ks}"][i])
+        assert bits(L.or_l2sq_any(a, b, d - 3)) == bits(g["l2any"][i])
+        assert bits(L.or_dot_any(a, b, d - 3)) == bits(g["dotany"][i])
+
+
+def test_golden_distances_distinguish_summation_orders():
+    # The fixtures are sensitive to the accumulation order: a restatement that used the
+    # wrong order (scalar instead of AVX-512 tree, say) would fail the test above.
+    g = gold("distances")
+    assert (bits(g["l2_scalar"]) != bits(g["l2_avx512"])).sum() > 20
+    assert (bits(g["l2_avx2"]) != bits(g["l2_avx512"])).sum() > 20
+    assert (bits(g["sq8l2_scalar"]) != bits(g["sq8l2_avx512"])).sum() > 20
+
+
+def test_distance_closed_forms(oracle):
+    L = oracle.lib
+    # metric convention (tests/distance_test.cc:86-91)
+    a = np.zeros(16, np.float32)
+    b = np.zeros(16, np.float32)
+    a[0] = 1
+    b[:2] = 0.5
+    for ks in range(3):
+        assert L.or_metric_dist(ks, 0, a, b, 16) == np.float32(0.5)
+        assert L.or_metric_dist(ks, 1, a, b, 16) == np.float32(-0.5)
+        assert L.or_metric_dist(ks, 2, a, b, 16) == np.float32(-0.5)
+    # integer data: every order is exact, all kernel sets agree with numpy
+    rng = np.random.default_rng(1)
+    for d in [16, 48, 128]:
+        x = rng.integers(0, 256, d).astype(np.float32)
+        y = rng.integers(0, 256, d).astype(np.float32)
+        want = np.float32(((x.astype(np.int64) - y.astype(np.int64)) ** 2).sum())
+        for ks in range(3):
+            assert L.or_l2(ks, x, y, d) == want
+            assert L.or_dot(ks, x, y, d) == np.float32((x.astype(np.int64) * y).sum())
+
+
+def test_distance_kernels_match_reference_random(oracle, reference):
+    L, R = oracle.lib, reference.lib
+    rng = np.random.default_rng(7)
+    for d in [16, 32, 64, 96, 128, 384, 960]:
+        for _ in range(30):
+            a = rng.standard_normal(d).astype(np.float32)
+            b = rng.standard_normal(d).astype(np.float32)
+            c = rng.integers(0, 256, d).astype(np.uint8)
+            vm = rng.standard_normal(d).astype(np.float32)
+            sc = (np.abs(rng.standard_normal(d)) / 255).astype(np.float32)
+            for ks in ["scalar", "avx2", "avx512"]:
+                e = ks.encode()
+                assert bits(L.or_l2(KSET[ks], a, b, d)) == bits(R.ref_l2(e, a, b, d))
+                assert bits(L.or_dot(KSET[ks], a, b, d)) == bits(R.ref_dot(e, a, b, d))
+                assert bits(L.or_sq8_l2(KSET[ks], a, c, vm, sc, d)) == bits(
+                    R.ref_sq8_l2(e, a, c, vm, sc, d))
+                assert bits(L.or_sq8_ip(KSET[ks], a, c, vm, sc, d)) == bits(
+                    R.ref_sq8_ip(e, a, c, vm, sc, d))
+
+
+# ------------------------------------------------------------------ top-k
+
+def test_topk_matches_golden_and_sort(oracle):
+    g = gold("topk")
+    t = 0
+    while f"d{t}" in g:
+        d, i, k = g[f"d{t}"], g[f"i{t}"], int(g[f"k{t}"][0])
+        od = np.empty(k, np.float32)
+        oi = np.empty(k, np.uint32)
+        m = oracle.lib.or_topk(d, i, len(d), k, od, oi)
+        assert np.array_equal(od[:m], g[f"od{t}"]) and np.array_equal(oi[:m], g[f"oi{t}"])
+        # closed form: lexicographic sort by (dist, id), first k
+        order = np.lexsort((i, d))[:k]
+        assert np.array_equal(oi[:m], i[order]) and np.array_equal(od[:m], d[order])
+        t += 1
+    assert t == 40
+
+
+def test_topk_k_zero(oracle):
+    d = np.ones(5, np.float32)
+    i = np.arange(5, dtype=np.uint32)
+    od = np.empty(1, np.float32)
+    oi = np.empty(1, np.uint32)
+    assert oracle.lib.or_topk(d, i, 5, 0, od, oi) == 0
+
+
+# ------------------------------------------------------------------ flat
+
+def test_flat_matches_golden(oracle):
+    g = gold("flat")
+    base, qs, allow = g["base"], g["queries"], g["allow"]
+    for met in ["l2", "ip"]:
+        for ks in ["scalar", "avx2", "avx512"]:
+            od, oi = oracle.flat_search(base, qs, 10, metric=met, kset=ks)
+            assert np.array_equal(oi, g[f"{met}_{ks}_i"]), (met, ks)
+            assert np.array_equal(bits(od), bits(g[f"{met}_{ks}_d"])), (met, ks)
+        od, oi = oracle.flat_search(base, qs, 10, metric=met, allow=allow)
+        assert np.array_equal(oi, g[f"{met}_allow_i"])
+        assert (oi % 3 == 0).all()
+    od, oi = oracle.flat_search(base[:5], qs[:3], 8)
+    assert np.array_equal(oi, g["small_i"]) and (oi[:, 5:] == 0xFFFFFFFF).all()
+
+
+def test_flat_closed_form_integer_data(oracle):
+    # integer data: the distance is exact in any order, so brute force with int64 fixes it
+    rng = np.random.default_rng(5)
+    base = rng.integers(0, 16, (4000, 32)).astype(np.float32)
+    qs = rng.integers(0, 16, (20, 32)).astype(np.float32)
+    od, oi = oracle.flat_search(base, qs, 25)
+    d = ((qs[:, None, :].astype(np.int64) - base[None].astype(np.int64)) ** 2).sum(-1)
+    for q in range(20):
+        order = np.lexsort((np.arange(4000), d[q]))[:25]
+        assert np.array_equal(oi[q], order)
+        assert np.array_equal(od[q], d[q][order].astype(np.float32))
+
+
+def test_flat_matches_reference_random(oracle, reference):
+    rng = np.random.default_rng(9)
+    base = rng.random((5000, 128), dtype=np.float32)
+    qs = rng.random((30, 128), dtype=np.float32)
+    for met in ["l2", "ip"]:
+        od, oi = oracle.flat_search(base, qs, 20, metric=met)
+        rd, ri = reference.flat_search(base, 128, qs, 20, metric=met)
+        assert np.array_equal(oi, ri) and np.array_equal(bits(od), bits(rd))
+
+
+# ------------------------------------------------------------------ SQ8
+
+def test_sq8_matches_golden(oracle):
+    g = gold("sq8")
+    base, dim = g["base"], 100
+    vmin, scale = oracle.sq8_train(base, dim)
+    assert np.array_equal(bits(vmin), bits(g["vmin"])) and np.array_equal(bits(scale),
+                                                                             bits(g["scale"]))
+    codes = oracle.sq8_encode(base, dim, vmin, scale)
+    assert np.array_equal(codes, g["codes"])
+    assert (codes[:, 5] == 0).all() and (codes[:, dim:] == 0).all()
+    for met in ["l2", "ip"]:
+        od, oi = oracle.sq8_search(base, codes, vmin, scale, g["queries"], 10, 50, metric=met)
+        assert np.array_equal(oi, g[f"{met}_i"]) and np.array_equal(bits(od), bits(g[f"{met}_d"]))
+
+
+def test_sq8_reconstruction_within_half_step(oracle):
+    # tests/distance_test.cc:106-126
+    rng = np.random.default_rng(5)
+    n, dim, pd = 2000, 100, 112
+    base = np.zeros((n, pd), np.float32)
+    base[:, :dim] = rng.normal(0, 3, (n, dim))
+    vmin, scale = oracle.sq8_train(base, dim)
+    assert np.array_equal(vmin[:dim], base[:, :dim].min(0))
+    assert np.array_equal(scale[:dim], ((base[:, :dim].max(0) - vmin[:dim]) / np.float32(255)))
+    codes = oracle.sq8_encode(base, dim, vmin, scale)
+    back = vmin[None] + codes.astype(np.float32) * scale[None]
+    err = np.abs(back[:, :dim] - base[:, :dim])
+    assert (err <= scale[None, :dim] * 0.5 * 1.0001 + 1e-6).all()
+    assert (back[:, dim:] == 0).all()
+    # closed form of the encoder: IEEE divide, round half to even, clamp
+    c = np.clip(np.rint((base[:, :dim] - vmin[None, :dim]) / scale[None, :dim]), 0, 255)
+    assert np.array_equal(codes[:, :dim], c.astype(np.uint8))
+
+
+def test_sq8_matches_reference_random(oracle, reference):
+    rng = np.random.default_rng(11)
+    base = rng.random((3000, 64), dtype=np.float32) * 10
+    vmin = np.empty(64, np.float32)
+    scale = np.empty(64, np.float32)
+    codes = np.empty((3000, 64), np.uint8)
+    reference.lib.ref_sq8_train_encode(base, 3000, 64, 64, vmin, scale, codes)
+    v2, s2 = oracle.sq8_train(base, 64)
+    assert np.array_equal(bits(v2), bits(vmin)) and np.array_equal(bits(s2), bits(scale))
+    assert np.array_equal(oracle.sq8_encode(base, 64, v2, s2), codes)
+
+
+# ------------------------------------------------------------------ PQ
+
+def test_pq_matches_golden_and_adc_equals_decoded_distance(oracle):
+    g = gold("pq")
+    L = oracle.lib
+    data, cen, m = g["data"], g["centroids"], 8
+    dim = data.shape[1]
+    dsub = dim // m
+    codes = np.empty((len(data), m), np.uint8)
+    for i in range(len(data)):
+        L.or_pq_encode(cen, m, dsub, data[i], codes[i])
+    assert np.array_equal(codes, g["codes"])
+    cen3 = cen.reshape(m, 256, dsub)
+    for met in ["l2", "ip"]:
+        for qi in range(4):
+            t = np.empty(m * 256, np.float32)
+            L.or_pq_compute_table(cen, m, dsub, g["queries"][qi], METRIC[met], t)
+            assert np.array_equal(bits(t), bits(g[f"table_{met}"][qi]))
+            for j in range(50):
+                a = L.or_pq_adc(t, m, codes[j])
+                assert bits(a) == bits(g[f"adc_{met}"][qi][j])
+                dec = np.concatenate([cen3[s, codes[j, s]] for s in range(m)]).astype(np.float32)
+                q = g["queries"][qi]
+                exact = (L.or_l2sq_any(q, dec, dim) if met == "l2"
+                         else -L.or_dot_any(q, dec, dim))
+                assert abs(a - exact) <= 1e-3 * max(1.0, abs(exact))  # pq_test.cc:64-83
+
+
+def test_pq_encode_is_first_argmin(oracle):
+    # closed form: strict < keeps the lowest centroid index among equal distances
+    m, dsub = 2, 4
+    cen = np.zeros((m, 256, dsub), np.float32)
+    cen[:, :, 0] = np.arange(256) % 7  # many centroids at equal distance
+    x = np.full(m * dsub, 3.0, np.float32)
+    x[1::dsub] = 0
+    code = np.empty(m, np.uint8)
+    oracle.lib.or_pq_encode(np.ascontiguousarray(cen.ravel()), m, dsub, x, code)
+    assert list(code) == [3, 3]
+
+
+# ------------------------------------------------------------------ assignment
+
+def test_assign_nearest_matches_golden(oracle):
+    g = gold("kmeans")
+    data, cen = g["data"], g["centroids_pp"]
+    asg = np.empty(len(data), np.uint32)
+    dist = np.empty(len(data), np.float32)
+    oracle.lib.or_assign_nearest(2, data, len(data), 16, 16, cen, 40, asg, dist, 4)
+    assert np.array_equal(asg, g["assign"]) and np.array_equal(bits(dist), bits(g["dist"]))
+    # brute force: argmin with ties to the lowest index
+    d = ((data[:, None, :] - cen.reshape(40, 16)[None]) ** 2).sum(-1)
+    close = np.abs(d.min(1) - d[np.arange(len(data)), asg]) <= 1e-4 * d.min(1) + 1e-6
+    assert close.all()
+
+
+# ------------------------------------------------------------------ IVF-PQ
+
+def _ivf_search(oracle, ix, base, qs, k, nprobe, rerank, kset="avx512"):
+    nq = len(qs)
+    od = np.empty((nq, k), np.float32)
+    oi = np.empty((nq, k), np.uint32)
+    dc = np.empty(nq, np.uint64)
+    term2 = np.empty(ix["nlist"] * ix["m"] * 256, np.float32)
+    dsub = ix["dim"] // ix["m"]
+    oracle.lib.or_ivfpq_term2(ix["coarse"], ix["nlist"], ix["pd"], ix["pq_centroids"], ix["m"],
+                              dsub, term2)
+    oracle.lib.or_ivfpq_search_batch(KSET[kset], 0, base, ix["dim"], ix["pd"], ix["coarse"],
+                                     ix["nlist"], ix["pq_centroids"], ix["m"], ix["list_off"],
+                                     ix["list_ids"], ix["list_codes"], term2, qs, nq, k,
+                                     nprobe, rerank, None, od, oi, dc, 4)
+    return od, oi, dc
+
+
+def test_ivfpq_matches_golden(oracle):
+    g = gold("ivfpq")
+    ix = parse_ivfpq(g["index_file"])
+    assert oracle.lib.or_crc32c(0, ix["crc_covered"], len(ix["crc_covered"])) == ix["crc"]
+    assert int(ix["list_off"][-1]) == len(g["base"])
+    for nprobe, rr in [(1, 0), (4, 0), (4, -1), (24, 0), (24, 5000)]:
+        tag = f"np{nprobe}_r{rr if rr >= 0 else 'auto'}"
+        od, oi, dc = _ivf_search(oracle, ix, g["base"], g["queries"], 10, nprobe, rr)
+        assert np.array_equal(oi, g[f"{tag}_i"]), tag
+        assert np.array_equal(bits(od), bits(g[f"{tag}_d"])), tag
+        assert np.array_equal(dc, g[f"{tag}_dc"]), tag
+
+
+def test_ivfpq_exhaustive_rerank_equals_flat(oracle):
+    # nprobe = nlist and rerank >= n: every row is re-ranked exactly, so IVF-PQ == flat
+    g = gold("ivfpq")
+    ix = parse_ivfpq(g["index_file"])
+    od, oi, _ = _ivf_search(oracle, ix, g["base"], g["queries"], 10, ix["nlist"], 5000)
+    fd, fi = oracle.flat_search(g["base"], g["queries"], 10)
+    assert np.array_equal(oi, fi) and np.array_equal(bits(od), bits(fd))
+
+
+def test_ivfpq_matches_reference_random(oracle, reference):
+    rng = np.random.default_rng(13)
+    base = (rng.random((6000, 32), dtype=np.float32) * 4).astype(np.float32)
+    qs = rng.random((20, 32), dtype=np.float32) * 4
+    blob = reference.ivfpq_build(base, 32, nlist=32, m=8, seed=3, max_points=64)
+    ix = parse_ivfpq(blob)
+    for nprobe, rr in [(3, 0), (8, -1)]:
+        od, oi, dc = _ivf_search(oracle, ix, base, qs, 10, nprobe, rr)
+        rd = np.empty((20, 10), np.float32)
+        ri = np.empty((20, 10), np.uint32)
+        rdc = np.empty(20, np.uint64)
+        assert reference.lib.ref_ivfpq_search_batch(0, blob, len(blob), base, 6000, 32, 32, qs,
+                                                    20, 10, nprobe, rr, None, rd, ri, rdc,
+                                                    1) == 0
+        assert np.array_equal(oi, ri) and np.array_equal(bits(od), bits(rd))
+        assert np.array_equal(dc, rdc)
+
+
+# ------------------------------------------------------------------ misc
+
+def test_normalize_matches_golden(oracle):
+    g = gold("misc")
+    for i in range(len(g["norm_in"])):
+        v = g["norm_in"][i].copy()
+        ok = oracle.lib.or_normalize(v, len(v))
+        assert ok == g["norm_ok"][i]
+        if ok:
+            assert np.array_equal(bits(v), bits(g["norm_out"][i]))
+            assert abs(np.linalg.norm(v.astype(np.float64)) - 1) < 1e-6
+
+
+def test_crc32c_known_answers(oracle):
+    g = gold("misc")
+    L = oracle.lib
+    assert L.or_crc32c(0, b"123456789", 9) == 0xE3069283  # tests/distance_test.cc:94
+    assert L.or_crc32c(0, b"", 0) == 0
+    blob = g["crc_blob"].tobytes()
+    assert L.or_crc32c(0, blob, len(blob)) == g["crc"][2]
+    # Extend(Value(a), b) == Value(a + b)
+    assert L.or_crc32c(L.or_crc32c(0, blob[:123], 123), blob[123:], len(blob) - 123) == g["crc"][2]
+
+
+def test_merge_parts_closed_form(oracle):
+    # collection_impl.cc:1076-1112: sort by (dist, part, row), first occurrence of each
+    # external id, stop at k
+    k = 4
+    part_d = np.array([[1, 2, 5, np.inf], [1, 2, 3, 4], [0.5, 2, 2, 9]], np.float32)
+    part_r = np.array([[0, 1, 2, 0xFFFFFFFF], [0, 1, 2, 3], [0, 1, 2, 3]], np.uint32)
+    ext = np.array([10, 11, 12, 20, 21, 22, 23, 11, 30, 31, 32], np.uint64)
+    off = np.array([0, 3, 7], np.uint64)
+    od = np.empty(k, np.float32)
+    oe = np.empty(k, np.uint64)
+    n = oracle.lib.or_merge_parts(3, k, part_d.ravel().copy(), part_r.ravel().copy(), ext, off,
+                                  od, oe)
+    # candidates: (0.5,p2,r0)=11 (1,p0,r0)=10 (1,p1,r0)=20 (2,p0,r1)=11 dup (2,p1,r1)=21 ...
+    assert n == 4
+    assert list(oe) == [11, 10, 20, 21]
+    assert list(od) == [0.5, 1, 1, 2]
