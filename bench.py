@@ -129,7 +129,7 @@ def main():
     log(f"timed {args.steps} steps in {elapsed:.3f} s")
     gemm_ms, gemm_n = ctx.profile_get("flat_gemm")
     kernel_ms = {name: ctx.profile_get(name)[0] / max(1, args.steps)
-                 for name in ("query_prep", "prepass", "flat_gemm", "select", "exact_scan",
+                 for name in ("query_prep", "sample_gemm", "kth", "flat_gemm", "select", "exact_scan",
                               "merge")}
     ctx.profile(False)
 

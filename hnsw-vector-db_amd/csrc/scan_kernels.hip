@@ -1,0 +1,1268 @@
+// scan_kernels.hip -- exhaustive scans on gfx950: flat exact search and the SQ8 scan.
+//
+// vdb's FlatIndex scans every row with an AVX-512 distance kernel into a top-k heap
+// (src/index/flat_index.cc:11-39, 73-77); its SQ8 path scores uint8 codes with the
+// asymmetric SQ8 kernel into a top-R heap and re-ranks with float rows
+// (src/index/hnsw/hnsw_index.cc:82-100, src/index/index.cc:89-95).  Both run here as one
+// pipeline over a batch of queries:
+//
+//   k_query_prep   per query: the GEMM B operand, the shift between the GEMM value and the
+//                  exact distance, and a bound on their difference (zero when integer data
+//                  makes every partial sum exact).
+//   k_gemm (MODE 1) on a strided sample of rows: per lane the minimum GEMM value of each
+//                  16-row group.  k_kth turns the kk-th smallest group minimum into an
+//                  admission threshold that provably keeps the top kk.
+//   k_gemm (MODE 0) Q.X^T (or Q''.C^T over codes) on fp32 MFMA (v_mfma_f32_32x32x2f32),
+//                  rows streamed through LDS; the epilogue compares with the threshold and
+//                  appends the few passing rows to per-(query, chunk, half) buffers.
+//   k_select       per query: the K' smallest candidates by GEMM value (wave bitonic
+//                  top-k), exact re-scoring in the reference's AVX-512 order, sort by
+//                  (dist, id), and a certificate that no unselected row can enter the top
+//                  kk; failures and overflows are re-scanned exactly (k_exact_scan).
+//   k_rerank       (SQ8) exact fp32 distances of the top-R codes' rows, top k.
+//
+// Distances returned are always the reference's exact AVX-512-order values.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "vdbg_device.h"
+#include "vdbg_internal.h"
+
+namespace vdbg {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// ================================================================ small helpers
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_min(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fminf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+__device__ __forceinline__ int wave_and(int v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v &= __shfl_xor(v, o);
+  return v;
+}
+
+// Order-preserving float <-> uint32 map for atomicMin/atomicMax.
+__device__ __forceinline__ uint32_t ord_enc(float f) {
+  uint32_t b = __float_as_uint(f);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+static inline float ord_dec(uint32_t e) {
+  uint32_t b = (e & 0x80000000u) ? (e & 0x7fffffffu) : ~e;
+  float f;
+  std::memcpy(&f, &b, 4);
+  return f;
+}
+
+__device__ __forceinline__ bool row_allowed(const uint64_t* w, uint32_t r) {
+  return w == nullptr || ((w[r >> 6] >> (r & 63)) & 1ull);
+}
+
+__host__ __device__ __forceinline__ uint32_t bitrev(uint32_t v, int bits) {
+  uint32_t r = 0;
+  for (int i = 0; i < bits; ++i) r |= ((v >> i) & 1u) << (bits - 1 - i);
+  return r;
+}
+
+static int pow2_e(size_t n) {  // smallest E in {1,2,4,8,...} with 64*E >= n
+  int e = 1;
+  while (size_t(kWave) * e < n) e <<= 1;
+  return e;
+}
+
+// ================================================================ row statistics
+
+struct RowStatsDev {
+  uint32_t lo, hi, max_abs, xn_max;
+  int all_int;
+};
+
+// One wave per row: ||x||^2 (lane-strided fmaf, wave sum), min, max, max |x|, integrality,
+// folded in with atomics.
+__global__ __launch_bounds__(256) void k_row_stats(const float* __restrict__ X, size_t n,
+                                                   int pd, float* __restrict__ norms,
+                                                   RowStatsDev* __restrict__ st) {
+  const size_t r = blockIdx.x * size_t(4) + (threadIdx.x >> 6);
+  if (r >= n) return;
+  const float* x = X + r * size_t(pd);
+  float s = 0.f, lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f;
+  int ai = 1;
+  for (int i = lane_id(); i < pd; i += kWave) {
+    const float e = x[i];
+    s = fmaf(e, e, s);
+    lo = fminf(lo, e);
+    hi = fmaxf(hi, e);
+    ma = fmaxf(ma, fabsf(e));
+    ai &= (e == rintf(e)) ? 1 : 0;
+  }
+  s = wave_sum(s);
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  ma = wave_max(ma);
+  ai = wave_and(ai);
+  if (lane_id() == 0) {
+    norms[r] = s;
+    atomicMin(&st->lo, ord_enc(lo));
+    atomicMax(&st->hi, ord_enc(hi));
+    atomicMax(&st->max_abs, __float_as_uint(ma));
+    atomicMax(&st->xn_max, __float_as_uint(s));
+    if (!ai) atomicAnd(&st->all_int, 0);
+  }
+}
+
+int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, float* norms,
+                   RowStats* out) {
+  RowStatsDev init{0xffffffffu, 0u, 0u, 0u, 1};
+  RowStatsDev* d = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&d), sizeof(RowStatsDev), s));
+  VDBG_HIP(hipMemcpyAsync(d, &init, sizeof(init), hipMemcpyHostToDevice, s));
+  if (n > 0) {
+    ProfScope ps(c, "row_stats", s);
+    k_row_stats<<<dim3(unsigned((n + 3) / 4)), 256, 0, s>>>(rows, n, int(pd), norms, d);
+    VDBG_HIP(hipGetLastError());
+  }
+  RowStatsDev h;
+  VDBG_HIP(hipMemcpyAsync(&h, d, sizeof(h), hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  VDBG_HIP(hipFreeAsync(d, s));
+  if (n == 0) {
+    *out = RowStats{};
+    return kOk;
+  }
+  out->lo = ord_dec(h.lo);
+  out->hi = ord_dec(h.hi);
+  std::memcpy(&out->max_abs, &h.max_abs, 4);
+  std::memcpy(&out->xn_max, &h.xn_max, 4);
+  out->all_int = h.all_int;
+  return kOk;
+}
+
+// ================================================================ SQ8 train / encode
+
+// Sq8Quantizer::train (src/index/quant/sq8.cc:9-26) keeps the first of equal values
+// (std::min / std::max); the partial reductions carry the row index so that equal values
+// (which can differ only in the sign of zero) resolve to the earliest row as well.
+struct MinMax {
+  float mn;
+  uint32_t mn_row;
+  float mx;
+  uint32_t mx_row;
+};
+
+__device__ __forceinline__ void mm_take(MinMax& a, float v, uint32_t row) {
+  if (v < a.mn || (v == a.mn && row < a.mn_row)) {
+    a.mn = v;
+    a.mn_row = row;
+  }
+  if (v > a.mx || (v == a.mx && row < a.mx_row)) {
+    a.mx = v;
+    a.mx_row = row;
+  }
+}
+
+__device__ __forceinline__ void mm_merge(MinMax& a, const MinMax& b) {
+  if (b.mn < a.mn || (b.mn == a.mn && b.mn_row < a.mn_row)) {
+    a.mn = b.mn;
+    a.mn_row = b.mn_row;
+  }
+  if (b.mx > a.mx || (b.mx == a.mx && b.mx_row < a.mx_row)) {
+    a.mx = b.mx;
+    a.mx_row = b.mx_row;
+  }
+}
+
+// grid.x = row blocks.  Thread t covers dims t % pd, t % pd + 256, ... (pd > 256) and rows
+// r0 + t / pd, stepping max(1, 256 / pd) rows: each row is read contiguously.
+__global__ __launch_bounds__(256) void k_sq8_minmax(const float* __restrict__ X, uint32_t n,
+                                                    int pd, uint32_t rows_per_block,
+                                                    MinMax* __restrict__ part) {
+  __shared__ MinMax red[256];
+  const int lanes_per_row = pd < 256 ? pd : 256;
+  const int rsteps = 256 / lanes_per_row;
+  const int t = threadIdx.x;
+  const int roff = t / lanes_per_row;
+  const int d0 = t % lanes_per_row;
+  const uint32_t r0 = blockIdx.x * rows_per_block;
+  const uint32_t r1 = min(n, r0 + rows_per_block);
+  // uniform trip count: every thread reaches every barrier
+  for (int dbase = 0; dbase < pd; dbase += lanes_per_row) {
+    const int d = dbase + d0;
+    MinMax a{__builtin_inff(), 0xffffffffu, -__builtin_inff(), 0xffffffffu};
+    if (roff < rsteps && d < pd)
+      for (uint32_t r = r0 + roff; r < r1; r += rsteps) mm_take(a, X[size_t(r) * pd + d], r);
+    red[t] = a;
+    __syncthreads();
+    if (roff == 0 && d < pd) {
+      for (int o = 1; o < rsteps; ++o) mm_merge(a, red[t + o * lanes_per_row]);
+      part[size_t(blockIdx.x) * pd + d] = a;
+    }
+    __syncthreads();
+  }
+}
+
+// One thread per dimension: fold the block partials; scale = (max - min) / 255.f.
+__global__ void k_sq8_finish(const MinMax* __restrict__ part, int nblocks, int dim, int pd,
+                             float* __restrict__ vmin, float* __restrict__ scale) {
+  const int d = blockIdx.x * blockDim.x + threadIdx.x;
+  if (d >= pd) return;
+  if (d >= dim || nblocks == 0) {
+    vmin[d] = 0.f;
+    scale[d] = 0.f;
+    return;
+  }
+  MinMax a{__builtin_inff(), 0xffffffffu, -__builtin_inff(), 0xffffffffu};
+  for (int b = 0; b < nblocks; ++b) mm_merge(a, part[size_t(b) * pd + d]);
+  vmin[d] = a.mn;
+  scale[d] = (a.mx - a.mn) / 255.f;
+}
+
+// Sq8Quantizer::encode (sq8.cc:28-37), one wave per row: IEEE divide, rintf (round half to
+// even = std::nearbyint in the default mode), clamp to [0, 255]; padding dims and
+// scale <= 0 give 0.  Also ||c * scale||^2, the row norm of the GEMM form.
+__global__ __launch_bounds__(256) void k_sq8_encode(const float* __restrict__ X, uint32_t n,
+                                                    int dim, int pd,
+                                                    const float* __restrict__ vmin,
+                                                    const float* __restrict__ scale,
+                                                    uint8_t* __restrict__ codes,
+                                                    float* __restrict__ yn) {
+  const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= n) return;
+  const float* x = X + size_t(r) * pd;
+  uint8_t* c = codes + size_t(r) * pd;
+  float s = 0.f;
+  for (int i = lane_id(); i < pd; i += kWave) {
+    uint8_t code = 0;
+    if (i < dim && scale[i] > 0.f) {
+      const float v = rintf((x[i] - vmin[i]) / scale[i]);
+      const float cl = v < 0.f ? 0.f : (255.f < v ? 255.f : v);
+      code = uint8_t(cl);
+    }
+    c[i] = code;
+    const float y = float(code) * scale[i];
+    s = fmaf(y, y, s);
+  }
+  s = wave_sum(s);
+  if (lane_id() == 0) yn[r] = s;
+}
+
+int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipStream_t s) {
+  const uint32_t n = uint32_t(ds->n);
+  const int pd = int(ds->pd), dim = int(ds->dim);
+  const uint32_t rpb = 8192;
+  const int nb = int((n + rpb - 1) / rpb);
+  MinMax* part = nullptr;
+  if (nb > 0) {
+    VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&part), sizeof(MinMax) * nb * pd, s));
+    ProfScope ps(c, "sq8_minmax", s);
+    k_sq8_minmax<<<dim3(nb), 256, 0, s>>>(ds->rows, n, pd, rpb, part);
+    VDBG_HIP(hipGetLastError());
+  }
+  k_sq8_finish<<<dim3((pd + 127) / 128), 128, 0, s>>>(part, nb, dim, pd, vmin_dev, scale_dev);
+  VDBG_HIP(hipGetLastError());
+  if (part) VDBG_HIP(hipFreeAsync(part, s));
+  return kOk;
+}
+
+int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
+              uint8_t* codes, float* yn, hipStream_t s) {
+  const uint32_t n = uint32_t(ds->n);
+  if (n == 0) return kOk;
+  ProfScope ps(c, "sq8_encode", s);
+  k_sq8_encode<<<dim3((n + 3) / 4), 256, 0, s>>>(ds->rows, n, int(ds->dim), int(ds->pd),
+                                                 vmin_dev, scale_dev, codes, yn);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+// ================================================================ sample matrix
+
+// Sample position p holds row floor(bitrev(p) * N / Smax): every power-of-two prefix of the
+// sample is an evenly strided subset of the rows.
+__global__ void k_gather_sample(const float* __restrict__ X, const uint8_t* __restrict__ C,
+                                const float* __restrict__ rn, uint32_t N, int pd, int bits,
+                                uint32_t smax, float* __restrict__ SX,
+                                uint8_t* __restrict__ SC, float* __restrict__ Srn,
+                                uint32_t* __restrict__ Sid) {
+  const uint32_t p = blockIdx.x;
+  if (p >= smax) return;
+  const uint32_t row = uint32_t((uint64_t(bitrev(p, bits)) * N) / smax);
+  for (int i = threadIdx.x; i < pd; i += blockDim.x) {
+    if (X) SX[size_t(p) * pd + i] = X[size_t(row) * pd + i];
+    if (C) SC[size_t(p) * pd + i] = C[size_t(row) * pd + i];
+  }
+  if (threadIdx.x == 0) {
+    Srn[p] = rn[row];
+    Sid[p] = row;
+  }
+}
+
+int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
+  if (src->Smax != 0) return kOk;
+  uint32_t smax = 1;
+  while (smax * 2 <= std::min<uint32_t>(src->N, 65536u)) smax *= 2;
+  int bits = 0;
+  while ((1u << bits) < smax) ++bits;
+  const size_t pd = src->pd;
+  if (src->kind == 0)
+    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX), size_t(smax) * pd * sizeof(float)));
+  else
+    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SC), size_t(smax) * pd));
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Srn), size_t(smax) * sizeof(float)));
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Sid), size_t(smax) * sizeof(uint32_t)));
+  k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
+                                             src->kind == 1 ? src->C : nullptr, src->rn,
+                                             src->N, int(pd), bits, smax, src->SX, src->SC,
+                                             src->Srn, src->Sid);
+  VDBG_HIP(hipGetLastError());
+  src->Smax = smax;
+  return kOk;
+}
+
+void FreeSample(ScanSource* src) {
+  (void)hipFree(src->SX);
+  (void)hipFree(src->SC);
+  (void)hipFree(src->Srn);
+  (void)hipFree(src->Sid);
+  src->SX = nullptr;
+  src->SC = nullptr;
+  src->Srn = nullptr;
+  src->Sid = nullptr;
+  src->Smax = 0;
+}
+
+// ================================================================ query preparation
+
+struct PrepArgs {
+  const float* Q;
+  float* Qb;  // GEMM B operand (SQ8 only; the flat scan uses Q itself)
+  int nq, pd, kind, metric;
+  RowStats xs;
+  float rmag;
+  const float* vmin;
+  const float* scale;
+  float* shift;  // exact distance ~= GEMM value + shift
+  float* eb;     // bound on |GEMM value + shift - exact distance|
+  int* exact;    // the bound is zero
+};
+
+// One wave per query.
+//  flat L2:  GEMM value ||x||^2 - 2 q.x, shift ||q||^2.   flat IP: -q.x, shift 0.
+//  SQ8 L2:   B = (q - vmin) * scale, value ||c*scale||^2 - 2 c.B, shift ||q - vmin||^2.
+//  SQ8 IP:   B = q * scale, value -c.B, shift -q.vmin.
+// The flat GEMM form is exact when every value is an integer and every partial sum any
+// summation order can form stays below 2^24: pd*max|x|^2, pd*max|q|^2, pd*max|x|*max|q|
+// and pd*R^2 with R the value range.  Otherwise the bound is
+// (4*pd + 16) * 2^-24 * (query magnitude + row magnitude): the MFMA dot and the fp32 norms
+// carry at most pd roundings each on sums bounded by those magnitudes, the exact
+// AVX-512-order value at most pd/16 + 6, and the factor two covers forming thresholds and
+// the SQ8 decode roundings.
+__global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;
+  const float* v = a.Q + size_t(q) * a.pd;
+  float s = 0.f, s2 = 0.f, lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f;
+  int ai = 1;
+  for (int i = lane_id(); i < a.pd; i += kWave) {
+    const float e = v[i];
+    s = fmaf(e, e, s);
+    lo = fminf(lo, e);
+    hi = fmaxf(hi, e);
+    ma = fmaxf(ma, fabsf(e));
+    ai &= (e == rintf(e)) ? 1 : 0;
+    if (a.kind == 1) {
+      if (a.metric == 0) {
+        const float qp = e - a.vmin[i];
+        a.Qb[size_t(q) * a.pd + i] = qp * a.scale[i];
+        s2 = fmaf(qp, qp, s2);
+      } else {
+        a.Qb[size_t(q) * a.pd + i] = e * a.scale[i];
+        s2 = fmaf(e, a.vmin[i], s2);
+      }
+    }
+  }
+  s = wave_sum(s);
+  s2 = wave_sum(s2);
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  ma = wave_max(ma);
+  ai = wave_and(ai);
+  if (lane_id() == 0) {
+    const double pd = a.pd, lim = 16777216.0;
+    bool ex = false;
+    float shift, qmag;
+    if (a.kind == 0) {
+      const double mx = a.xs.max_abs, mq = ma;
+      const double range = double(fmaxf(hi, a.xs.hi)) - double(fminf(lo, a.xs.lo));
+      ex = a.xs.all_int && ai && pd * mx * mx < lim && pd * mq * mq < lim &&
+           pd * mx * mq < lim && pd * range * range < lim;
+      shift = a.metric == 0 ? s : 0.f;
+      qmag = s;
+    } else {
+      shift = a.metric == 0 ? s2 : -s2;
+      qmag = a.metric == 0 ? s + s2 : s;
+    }
+    a.shift[q] = shift;
+    a.exact[q] = ex ? 1 : 0;
+    a.eb[q] = ex ? 0.f
+                 : float((4.0 * pd + 16.0) * (1.0 / 16777216.0) *
+                         (double(qmag) + double(a.rmag)) * 1.001);
+  }
+}
+
+// ================================================================ MFMA GEMM
+
+struct GemmArgs {
+  const float* X;      // fp32 rows (KIND 0)
+  const uint8_t* C;    // code rows (KIND 1)
+  const float* rn;     // row norms of the GEMM form
+  const uint32_t* rid; // MODE 1: original row id of each sample row
+  const float* Qb;
+  const float* T;
+  const uint64_t* allow;
+  uint2* cand;         // MODE 0: [(q * nchunks + chunk) * 2 + half][caph]
+  uint32_t* counts;    // MODE 0: [(q * nchunks + chunk) * 2 + half]
+  int* ovf;            // MODE 0: [q]
+  float* gm;           // MODE 1: [q][ngroups] minimum GEMM value of each 16-row group
+  int ngroups;
+  uint32_t N;
+  int nq, nqt;
+  uint32_t chunk_rows;
+  int nchunks, caph;
+  int items;           // nqt * nchunks
+  int per_xcd;         // items assigned to each of the 8 XCDs
+};
+
+constexpr int kGemmRows = 64;  // rows per LDS tile (two 32-row MFMA blocks)
+
+// Block = 4 waves = 128 queries (32 per wave) x one chunk of rows.  Blocks are dispatched
+// round-robin over the 8 XCDs, so block b takes work item (b % 8) * per_xcd + b / 8: the
+// items of one XCD are consecutive and share row chunks in that XCD's L2.
+//
+// Each wave keeps its 32 queries in VGPRs as the MFMA B operand: lane l holds query l % 32,
+// dims [h*PD/2, (h+1)*PD/2) with h = l / 32, so MFMA step t contracts dims t and PD/2 + t
+// (the order is irrelevant: the GEMM value only ranks; exact distances are recomputed).
+// 64-row tiles are double-buffered in LDS and feed the A operand; code rows are widened to
+// fp32 on the way in.  The 32x32 accumulator gives lane l the values of query l % 32 for
+// rows 8*(r/4) + 4*h + (r%4), r = 0..15.
+template <int PD, int METRIC, int KIND, int MODE>
+__global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
+  constexpr int STR = PD + 4;  // padded LDS row stride (floats)
+  constexpr int HALF = PD / 2;
+  constexpr int VEC_PER_TILE = KIND == 0 ? kGemmRows * PD / 4 : kGemmRows * PD / 16;
+  constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
+  __shared__ __attribute__((aligned(16))) float xs[2][kGemmRows * STR];
+  __shared__ float xns[2][kGemmRows];
+
+  const int b = blockIdx.x;
+  const int item = (b & 7) * a.per_xcd + (b >> 3);
+  if (item >= a.items) return;
+  const int chunk = item / a.nqt;
+  const int qt = item - chunk * a.nqt;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int q = qt * 128 + wave * 32 + j;
+  const bool wave_live = qt * 128 + wave * 32 < a.nq;
+  const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
+  const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
+
+  float qv[HALF];
+  if (q < a.nq) {
+    const float* src = a.Qb + size_t(q) * PD + h * HALF;
+#pragma unroll
+    for (int t = 0; t < HALF; t += 4) {
+      const float4 v = *reinterpret_cast<const float4*>(src + t);
+      qv[t] = v.x;
+      qv[t + 1] = v.y;
+      qv[t + 2] = v.z;
+      qv[t + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < HALF; ++t) qv[t] = 0.f;
+  }
+  const float T = (MODE == 0 && q < a.nq) ? a.T[q] : -__builtin_inff();
+  const size_t seg = (size_t(q) * a.nchunks + chunk) * 2 + h;
+  uint2* out = MODE == 0 ? a.cand + seg * size_t(a.caph) : nullptr;
+  uint32_t cnt = 0;
+
+  uint4 pre[VEC_PER_THREAD];
+  float pre_n = 0.f;
+  auto load_tile = [&](uint32_t base) {
+    const uint32_t valid = r_end > base ? min(uint32_t(kGemmRows), r_end - base) : 0u;
+    const uint4* src = KIND == 0
+                           ? reinterpret_cast<const uint4*>(a.X + size_t(base) * PD)
+                           : reinterpret_cast<const uint4*>(a.C + size_t(base) * PD);
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int f = tid + 256 * i;
+      const int row = KIND == 0 ? f / (PD / 4) : f / (PD / 16);
+      if (f < VEC_PER_TILE && uint32_t(row) < valid)
+        pre[i] = src[f];
+      else
+        pre[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    pre_n = (tid < kGemmRows && uint32_t(tid) < valid) ? a.rn[base + tid] : 0.f;
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int f = tid + 256 * i;
+      if (f < VEC_PER_TILE) {
+        if (KIND == 0) {
+          const int row = f / (PD / 4), c4 = f % (PD / 4);
+          *reinterpret_cast<uint4*>(&xs[buf][row * STR + c4 * 4]) = pre[i];
+        } else {
+          const int row = f / (PD / 16), c16 = f % (PD / 16);
+          float* dst = &xs[buf][row * STR + c16 * 16];
+          const uint32_t w[4] = {pre[i].x, pre[i].y, pre[i].z, pre[i].w};
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            float4 v;
+            v.x = float(w[g] & 0xffu);
+            v.y = float((w[g] >> 8) & 0xffu);
+            v.z = float((w[g] >> 16) & 0xffu);
+            v.w = float(w[g] >> 24);
+            *reinterpret_cast<float4*>(dst + 4 * g) = v;
+          }
+        }
+      }
+    }
+    if (tid < kGemmRows) xns[buf][tid] = pre_n;
+  };
+
+  if (r_begin < r_end) {
+    load_tile(r_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  int buf = 0;
+  for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
+    const uint32_t next = base + kGemmRows;
+    if (next < r_end) load_tile(next);
+
+    if (wave_live) {
+      v16f acc0, acc1;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+      const float* xa0 = &xs[buf][j * STR + h * HALF];
+      const float* xa1 = xa0 + 32 * STR;
+#pragma unroll
+      for (int t = 0; t < HALF; t += 4) {
+        const float4 x0 = *reinterpret_cast<const float4*>(xa0 + t);
+        const float4 x1 = *reinterpret_cast<const float4*>(xa1 + t);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qv[t + 0], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qv[t + 0], acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.y, qv[t + 1], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.y, qv[t + 1], acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.z, qv[t + 2], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.z, qv[t + 2], acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qv[t + 3], acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qv[t + 3], acc1, 0, 0, 0);
+      }
+
+      if (MODE == 0) {
+        // threshold test on all 32 values; the rare passes go to the lane's buffer
+        uint32_t pass = 0;
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float g = blk == 0 ? acc0[r] : acc1[r];
+            const float v = METRIC == 0 ? fmaf(-2.f, g, xns[buf][rl]) : -g;
+            pass |= (v <= T ? 1u : 0u) << (blk * 16 + r);
+          }
+        if (__ballot(pass != 0) != 0) {
+#pragma unroll
+          for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              if (pass & (1u << (blk * 16 + r))) {
+                const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+                const float g = blk == 0 ? acc0[r] : acc1[r];
+                const float v = METRIC == 0 ? fmaf(-2.f, g, xns[buf][rl]) : -g;
+                const uint32_t row = base + rl;
+                if (q < a.nq && row < r_end && row_allowed(a.allow, row)) {
+                  if (cnt < uint32_t(a.caph)) out[cnt] = make_uint2(__float_as_uint(v), row);
+                  ++cnt;
+                }
+              }
+            }
+        }
+      } else {
+        // group minima over each lane's 16 rows of each 32-row block
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          float m = __builtin_inff();
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const float g = blk == 0 ? acc0[r] : acc1[r];
+            const float v = METRIC == 0 ? fmaf(-2.f, g, xns[buf][rl]) : -g;
+            const uint32_t row = base + rl;
+            if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, v);
+          }
+          if (q < a.nq) {
+            const uint32_t grp = ((base >> 5) + blk) * 2 + h;
+            if (grp < uint32_t(a.ngroups)) a.gm[size_t(q) * a.ngroups + grp] = m;
+          }
+        }
+      }
+    }
+
+    if (next < r_end) store_tile(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  if (MODE == 0 && q < a.nq) {
+    a.counts[seg] = min(cnt, uint32_t(a.caph));
+    if (cnt > uint32_t(a.caph)) a.ovf[q] = 1;
+  }
+}
+
+// ================================================================ threshold from groups
+
+struct KthArgs {
+  const float* gm;
+  int ngroups, nq, kk;
+  const float* eb;
+  float* T;
+};
+
+// One wave per query: the kk-th smallest group minimum A.  The kk groups at or below A hold
+// kk distinct rows with GEMM value <= A, so the kk-th smallest exact distance is at most
+// A + shift + eb and every row of the true top kk has GEMM value <= A + 2 eb.
+template <int E>
+__global__ __launch_bounds__(256) void k_kth(KthArgs a) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;
+  WaveTopK<E> top;
+  top.init();
+  const float* g = a.gm + size_t(q) * a.ngroups;
+  for (int i0 = 0; i0 < a.ngroups; i0 += kWave) {
+    const int i = i0 + lane_id();
+    top.insert(i < a.ngroups ? g[i] : __builtin_inff(), i < a.ngroups ? uint32_t(i) : kNoId);
+  }
+  const int kth = a.kk - 1;
+  float v = __builtin_inff();
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const float t = __shfl(top.k.d[e], kth & (kWave - 1));
+    if (e == kth / kWave) v = t;
+  }
+  if (lane_id() == 0) a.T[q] = v < __builtin_inff() ? v + 2.f * a.eb[q] : __builtin_inff();
+}
+
+// ================================================================ selection / merge
+
+struct SelectArgs {
+  const float* Q;
+  const uint2* cand;
+  const uint32_t* counts;
+  int nseg, cap;
+  const int* ovf;          // nullable
+  const float* shift;      // rescore mode
+  const float* eb;
+  const int* exact;
+  const uint32_t* qlist;   // nullable: slot i answers query qlist[i]
+  int nslots, k, pd;
+  int rescore;             // 1: candidates hold GEMM values; 0: exact distances
+  uint32_t* out_ids;
+  float* out_d;
+  uint32_t* fb_list;       // rescore mode: queries that need the exact re-scan
+  uint32_t* fb_count;
+};
+
+constexpr int kMaxSeg = 1024;
+
+// One wave per slot.  Candidates of the slot's segments are streamed (a prefix sum over the
+// segment counts maps a flat index to its segment) into a wave top-k of capacity 64*E.
+template <int E, class Scorer>
+__global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
+  __shared__ uint32_t pre_all[4][kMaxSeg + 1];
+  const int wave = threadIdx.x >> 6;
+  const int lane = lane_id();
+  const int slot = blockIdx.x * 4 + wave;
+  if (slot >= a.nslots) return;
+  const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
+  uint32_t* pre = pre_all[wave];
+
+  if (a.ovf != nullptr && a.ovf[q]) {
+    if (lane == 0) {
+      const uint32_t p = atomicAdd(a.fb_count, 1u);
+      a.fb_list[p] = q;
+    }
+    return;
+  }
+
+  uint32_t run = 0;
+  const uint32_t* cnts = a.counts + size_t(slot) * a.nseg;
+  for (int b = 0; b < a.nseg; b += kWave) {
+    const int s = b + lane;
+    const uint32_t c = s < a.nseg ? cnts[s] : 0u;
+    uint32_t incl = c;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const uint32_t t = __shfl_up(incl, o);
+      if (lane >= o) incl += t;
+    }
+    if (s < a.nseg) pre[s + 1] = run + incl;
+    run += __shfl(incl, kWave - 1);
+  }
+  if (lane == 0) pre[0] = 0;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const uint32_t total = run;
+
+  WaveTopK<E> top;
+  top.init();
+  const uint2* cbase = a.cand + size_t(slot) * a.nseg * size_t(a.cap);
+  for (uint32_t g0 = 0; g0 < total; g0 += kWave) {
+    const uint32_t g = g0 + lane;
+    float d = __builtin_inff();
+    uint32_t id = kNoId;
+    if (g < total) {
+      int lo = 0, hi = a.nseg;  // largest s with pre[s] <= g
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pre[mid] <= g) lo = mid; else hi = mid;
+      }
+      const uint2 c = cbase[size_t(lo) * a.cap + (g - pre[lo])];
+      d = __uint_as_float(c.x);
+      id = c.y;
+    }
+    top.insert(d, id);
+  }
+
+  constexpr int N = kWave * E;
+  uint32_t* oi = a.out_ids + size_t(q) * a.k;
+  float* od = a.out_d + size_t(q) * a.k;
+  if (!a.rescore) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int gi = e * kWave + lane;
+      if (gi < a.k) {
+        oi[gi] = top.k.id[e];
+        od[gi] = top.k.d[e];
+      }
+    }
+    return;
+  }
+
+  // exact re-scoring of the K' = N-1 best by GEMM value
+  const float* qv = a.Q + size_t(q) * a.pd;
+  const uint32_t nsel = min(total, uint32_t(N - 1));
+  const float a_next = __shfl(top.k.d[E - 1], kWave - 1);  // the (K'+1)-th GEMM value
+  WaveKeys<E> r;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const uint32_t gi = e * kWave + lane;
+    if (gi < nsel) {
+      r.d[e] = sc(qv, top.k.id[e]);
+      r.id[e] = top.k.id[e];
+    } else {
+      r.d[e] = __builtin_inff();
+      r.id[e] = kNoId;
+    }
+  }
+  bitonic_sort<E>(r);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int gi = e * kWave + lane;
+    if (gi < a.k) {
+      oi[gi] = r.id[e];
+      od[gi] = r.d[e];
+    }
+  }
+  // certificate: every unselected candidate's exact distance is at least its GEMM value
+  // plus the shift minus the bound; that must exceed the k-th exact distance.
+  if (total > nsel && !a.exact[q]) {
+    const int g = a.k - 1;
+    float dk = __builtin_inff();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float v = __shfl(r.d[e], g & (kWave - 1));
+      if (e == g / kWave) dk = v;
+    }
+    const float lower = (a_next + a.shift[q]) - a.eb[q];
+    if (!(dk < lower) && lane == 0) {
+      const uint32_t p = atomicAdd(a.fb_count, 1u);
+      a.fb_list[p] = q;
+    }
+  }
+}
+
+// ================================================================ exact scan
+
+struct ScanArgs {
+  const float* Q;
+  const uint64_t* allow;
+  int pd;
+  uint32_t N;
+  const uint32_t* qlist;  // nullable
+  int nslots;
+  uint32_t split_rows;
+  int nsplit;
+  uint2* part;            // [slot][split][64*E]
+  uint32_t* part_counts;  // [slot][split]
+};
+
+// Block = 4 waves on one (query, row split); each wave keeps a top-64E of its rows with
+// exact distances, then wave 0 merges the other three through LDS.
+template <int E, class Scorer>
+__global__ __launch_bounds__(256) void k_exact_scan(ScanArgs a, Scorer sc) {
+  constexpr int N = kWave * E;
+  __shared__ float md[3][N];
+  __shared__ uint32_t mi[3][N];
+  const int slot = blockIdx.x, split = blockIdx.y;
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
+  const float* qv = a.Q + size_t(q) * a.pd;
+  const uint32_t r0 = uint32_t(split) * a.split_rows;
+  const uint32_t r1 = min(a.N, r0 + a.split_rows);
+  WaveTopK<E> top;
+  top.init();
+  for (uint32_t base = r0 + wave * kWave; base < r1; base += 4 * kWave) {
+    const uint32_t r = base + lane;
+    float d = __builtin_inff();
+    uint32_t id = kNoId;
+    if (r < r1 && row_allowed(a.allow, r)) {
+      d = sc(qv, r);
+      id = r;
+    }
+    top.insert(d, id);
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      md[wave - 1][e * kWave + lane] = top.k.d[e];
+      mi[wave - 1][e * kWave + lane] = top.k.id[e];
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int e = 0; e < E; ++e) top.insert(md[w][e * kWave + lane], mi[w][e * kWave + lane]);
+  const size_t ps = size_t(slot) * a.nsplit + split;
+  uint2* out = a.part + ps * N;
+  uint32_t valid = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    out[e * kWave + lane] = make_uint2(__float_as_uint(top.k.d[e]), top.k.id[e]);
+    valid += __popcll(__ballot(top.k.id[e] != kNoId));
+  }
+  if (lane == 0) a.part_counts[ps] = valid;
+}
+
+// ================================================================ rerank
+
+struct RerankArgs {
+  const float* X;
+  const float* Q;
+  int pd, metric;
+  const uint32_t* cand;  // [nq][depth] ascending by SQ8 distance, kNoId padded
+  int depth, nq, k;
+  uint32_t* out_ids;
+  float* out_d;
+};
+
+// Rerank (src/index/index.cc:89-95): exact fp32 distances of the candidates' rows, the k
+// smallest by (dist, id).  One wave per query, up to 64*E candidates.
+template <int E>
+__global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;
+  const int lane = lane_id();
+  const float* qv = a.Q + size_t(q) * a.pd;
+  WaveKeys<E> r;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = e * kWave + lane;
+    const uint32_t id = i < a.depth ? a.cand[size_t(q) * a.depth + i] : kNoId;
+    if (id != kNoId) {
+      r.d[e] = metric_exact(a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
+      r.id[e] = id;
+    } else {
+      r.d[e] = __builtin_inff();
+      r.id[e] = kNoId;
+    }
+  }
+  bitonic_sort<E>(r);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = e * kWave + lane;
+    if (i < a.k) {
+      a.out_ids[size_t(q) * a.k + i] = r.id[e];
+      a.out_d[size_t(q) * a.k + i] = r.d[e];
+    }
+  }
+}
+
+// ================================================================ orchestration
+
+__global__ void k_fill_empty(uint32_t* ids, float* d, size_t n) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) {
+    ids[i] = kNoId;
+    d[i] = __builtin_inff();
+  }
+}
+
+template <int E, class Scorer>
+static void launch_select(hipStream_t s, const SelectArgs& a, const Scorer& sc) {
+  k_select<E, Scorer><<<dim3((a.nslots + 3) / 4), 256, 0, s>>>(a, sc);
+}
+template <int E, class Scorer>
+static void launch_scan(hipStream_t s, const ScanArgs& a, const Scorer& sc) {
+  k_exact_scan<E, Scorer><<<dim3(a.nslots, a.nsplit), 256, 0, s>>>(a, sc);
+}
+template <int E>
+static void launch_kth(hipStream_t s, const KthArgs& a) {
+  k_kth<E><<<dim3((a.nq + 3) / 4), 256, 0, s>>>(a);
+}
+template <int E>
+static void launch_rerank(hipStream_t s, const RerankArgs& a) {
+  k_rerank<E><<<dim3((a.nq + 3) / 4), 256, 0, s>>>(a);
+}
+
+#define VDBG_DISPATCH_E(E, FN, ...)                          \
+  switch (E) {                                               \
+    case 1: FN<1>(__VA_ARGS__); break;                       \
+    case 2: FN<2>(__VA_ARGS__); break;                       \
+    case 4: FN<4>(__VA_ARGS__); break;                       \
+    default: return SetError(kNotSupported, "k too large"); \
+  }
+#define VDBG_DISPATCH_ES(E, FN, SC, ...)                     \
+  switch (E) {                                               \
+    case 1: FN<1, SC>(__VA_ARGS__); break;                   \
+    case 2: FN<2, SC>(__VA_ARGS__); break;                   \
+    case 4: FN<4, SC>(__VA_ARGS__); break;                   \
+    default: return SetError(kNotSupported, "k too large"); \
+  }
+
+static FlatScorer FlatOf(const ScanSource& src) { return FlatScorer{src.X, src.pd, src.metric}; }
+static Sq8Scorer Sq8Of(const ScanSource& src) {
+  return Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric};
+}
+
+template <class Scorer>
+static int ExactScanT(Ctx* c, Workspace& w, const ScanSource& src, const Scorer& sc,
+                      const float* Q, const uint32_t* qlist, int nslots, size_t k,
+                      const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+  const int E = pow2_e(k);
+  const uint32_t N = src.N;
+  int nsplit = int(std::min<size_t>((2048 + nslots - 1) / nslots,
+                                    std::max<size_t>(1, (N + 1023) / 1024)));
+  nsplit = std::max(1, std::min(nsplit, kMaxSeg));
+  uint32_t split_rows = (N + nsplit - 1) / nsplit;
+  split_rows = (split_rows + 63) / 64 * 64;
+  nsplit = int((N + split_rows - 1) / split_rows);
+  const int cap = kWave * E;
+  const size_t need = size_t(nslots) * nsplit * cap * sizeof(uint2) +
+                      size_t(nslots) * nsplit * sizeof(uint32_t) + 4096;
+  w.used = 0;
+  VDBG_RETURN_IF_ERROR(w.reserve(need));
+  uint2* part = w.take<uint2>(size_t(nslots) * nsplit * cap);
+  uint32_t* pc = w.take<uint32_t>(size_t(nslots) * nsplit);
+  ScanArgs sa{Q, allow, src.pd, N, qlist, nslots, split_rows, nsplit, part, pc};
+  {
+    ProfScope ps(c, "exact_scan", s);
+    VDBG_DISPATCH_ES(E, launch_scan, Scorer, s, sa, sc);
+    VDBG_HIP(hipGetLastError());
+  }
+  SelectArgs se{};
+  se.Q = Q;
+  se.cand = part;
+  se.counts = pc;
+  se.nseg = nsplit;
+  se.cap = cap;
+  se.qlist = qlist;
+  se.nslots = nslots;
+  se.k = int(k);
+  se.pd = src.pd;
+  se.rescore = 0;
+  se.out_ids = out_ids;
+  se.out_d = out_d;
+  {
+    ProfScope ps(c, "merge", s);
+    VDBG_DISPATCH_ES(E, launch_select, Scorer, s, se, sc);
+    VDBG_HIP(hipGetLastError());
+  }
+  return kOk;
+}
+
+static int ExactScan(Ctx* c, Workspace& w, const ScanSource& src, const float* Q,
+                     const uint32_t* qlist, int nslots, size_t k, const uint64_t* allow,
+                     uint32_t* out_ids, float* out_d, hipStream_t s) {
+  if (nslots == 0) return kOk;
+  if (pow2_e(k) > 4) return SetError(kNotSupported, "k > 256 is not supported on the GPU path");
+  if (src.kind == 0)
+    return ExactScanT(c, w, src, FlatOf(src), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+  return ExactScanT(c, w, src, Sq8Of(src), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+}
+
+static bool GemmSupported(size_t pd) { return pd % 16 == 0 && pd >= 16 && pd <= 128; }
+
+template <int PD, int METRIC, int KIND, int MODE>
+static void launch_gemm(hipStream_t s, int blocks, const GemmArgs& a) {
+  k_gemm<PD, METRIC, KIND, MODE><<<dim3(blocks), 256, 0, s>>>(a);
+}
+
+template <int PD>
+static void launch_gemm_pd(int metric, int kind, int mode, hipStream_t s, int blocks,
+                           const GemmArgs& a) {
+  if (kind == 0) {
+    if (metric == 0) {
+      if (mode == 0) launch_gemm<PD, 0, 0, 0>(s, blocks, a);
+      else launch_gemm<PD, 0, 0, 1>(s, blocks, a);
+    } else {
+      if (mode == 0) launch_gemm<PD, 1, 0, 0>(s, blocks, a);
+      else launch_gemm<PD, 1, 0, 1>(s, blocks, a);
+    }
+  } else {
+    if (metric == 0) {
+      if (mode == 0) launch_gemm<PD, 0, 1, 0>(s, blocks, a);
+      else launch_gemm<PD, 0, 1, 1>(s, blocks, a);
+    } else {
+      if (mode == 0) launch_gemm<PD, 1, 1, 0>(s, blocks, a);
+      else launch_gemm<PD, 1, 1, 1>(s, blocks, a);
+    }
+  }
+}
+
+static int LaunchGemm(size_t pd, int metric, int kind, int mode, hipStream_t s, int blocks,
+                      const GemmArgs& a) {
+  switch (pd) {
+    case 16: launch_gemm_pd<16>(metric, kind, mode, s, blocks, a); break;
+    case 32: launch_gemm_pd<32>(metric, kind, mode, s, blocks, a); break;
+    case 48: launch_gemm_pd<48>(metric, kind, mode, s, blocks, a); break;
+    case 64: launch_gemm_pd<64>(metric, kind, mode, s, blocks, a); break;
+    case 80: launch_gemm_pd<80>(metric, kind, mode, s, blocks, a); break;
+    case 96: launch_gemm_pd<96>(metric, kind, mode, s, blocks, a); break;
+    case 112: launch_gemm_pd<112>(metric, kind, mode, s, blocks, a); break;
+    case 128: launch_gemm_pd<128>(metric, kind, mode, s, blocks, a); break;
+    default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
+  }
+  return kOk;
+}
+
+// Chunk count for nqt query tiles over N rows: balance the last round of blocks against
+// the resident slots (2 blocks per CU), prefer fewer chunks at equal balance.
+static int PlanChunks(int nqt, uint32_t N, int slots, int max_chunks) {
+  const int limit = std::max(1, std::min<int>(max_chunks, int((N + 63) / 64)));
+  int best = 1;
+  double best_score = -1;
+  for (int nc = 1; nc <= limit; ++nc) {
+    uint32_t rows = (N + nc - 1) / nc;
+    rows = (rows + 63) / 64 * 64;
+    const int real = int((N + rows - 1) / rows);
+    if (real != nc) continue;
+    const double items = double(nqt) * nc;
+    const double rounds = std::ceil(items / slots);
+    const double score = items / (rounds * slots) - 0.002 * nc;
+    if (score > best_score) {
+      best_score = score;
+      best = nc;
+    }
+  }
+  return best;
+}
+
+static void GemmGrid(GemmArgs& ga, int nqt, int nchunks, int* blocks) {
+  ga.nqt = nqt;
+  ga.nchunks = nchunks;
+  ga.items = nqt * nchunks;
+  ga.per_xcd = (ga.items + 7) / 8;
+  *blocks = ga.per_xcd * 8;
+}
+
+int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
+            const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+  c->last_fallbacks = 0;
+  if (nq == 0 || kk == 0) return kOk;
+  if (kk > 256) return SetError(kNotSupported, "k > 256 is not supported on the GPU path");
+  if (src->N == 0) {
+    k_fill_empty<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, out_d, nq * kk);
+    VDBG_HIP(hipGetLastError());
+    return kOk;
+  }
+  const uint32_t N = src->N;
+  const size_t pd = src->pd;
+  const bool gemm = GemmSupported(pd) && N >= 8192 && nq >= 32;
+  if (!gemm) return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
+  VDBG_RETURN_IF_ERROR(BuildSample(c, src, s));
+
+  // ---- plan
+  const int slots = 2 * c->cu_count;
+  const int nqt = int((nq + 127) / 128);
+  const int nchunks = PlanChunks(nqt, N, slots, 256);
+  uint32_t chunk_rows = (N + nchunks - 1) / nchunks;
+  chunk_rows = (chunk_rows + 63) / 64 * 64;
+  uint32_t S = 1;
+  while (S < 16u * std::max<uint32_t>(128, 4 * uint32_t(kk))) S *= 2;
+  S = std::min(S, src->Smax);
+  const int ngroups = int((S + 31) / 32) * 2;
+  const int schunks = PlanChunks(nqt, S, slots, int((S + 63) / 64));
+  uint32_t schunk_rows = (S + schunks - 1) / schunks;
+  schunk_rows = (schunk_rows + 63) / 64 * 64;
+  const double expect_seg = double(kk) * N / S * 1.5 / (2.0 * nchunks);
+  int caph = 32;
+  while (caph < 3.0 * expect_seg + 32) caph <<= 1;
+  const int nseg = 2 * nchunks;
+  const int Ek = pow2_e(kk);
+  const int Esel = pow2_e(kk + 16);
+  if (Esel > 4) return SetError(kNotSupported, "k too large for the GEMM path");
+
+  Workspace& w = c->ws;
+  w.used = 0;
+  const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + sizeof(uint32_t)) +
+                      (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
+                      size_t(nq) * ngroups * sizeof(float) +
+                      size_t(nq) * nseg * (sizeof(uint32_t) + size_t(caph) * sizeof(uint2)) +
+                      16 * 256;
+  VDBG_RETURN_IF_ERROR(w.reserve(need));
+  float* shift = w.take<float>(nq);
+  float* eb = w.take<float>(nq);
+  float* T = w.take<float>(nq);
+  int* exact = w.take<int>(nq);
+  int* ovf = w.take<int>(nq);
+  uint32_t* fb_list = w.take<uint32_t>(nq);
+  uint32_t* fb_count = w.take<uint32_t>(1);
+  float* Qb = src->kind == 1 ? w.take<float>(nq * pd) : nullptr;
+  float* gm = w.take<float>(size_t(nq) * ngroups);
+  uint32_t* counts = w.take<uint32_t>(size_t(nq) * nseg);
+  uint2* cand = w.take<uint2>(size_t(nq) * nseg * caph);
+  VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
+  VDBG_HIP(hipMemsetAsync(fb_count, 0, sizeof(uint32_t), s));
+
+  PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
+              src->vmin, src->scale, shift, eb, exact};
+  {
+    ProfScope ps(c, "query_prep", s);
+    k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
+    VDBG_HIP(hipGetLastError());
+  }
+  const float* B = src->kind == 1 ? Qb : Q;
+  const int metric = src->metric == 0 ? 0 : 1;
+
+  // sample pre-pass -> thresholds
+  GemmArgs sg{};
+  sg.X = src->SX;
+  sg.C = src->SC;
+  sg.rn = src->Srn;
+  sg.rid = src->Sid;
+  sg.Qb = B;
+  sg.allow = allow;
+  sg.gm = gm;
+  sg.ngroups = ngroups;
+  sg.N = S;
+  sg.nq = int(nq);
+  sg.chunk_rows = schunk_rows;
+  int sblocks = 0;
+  GemmGrid(sg, nqt, int((S + schunk_rows - 1) / schunk_rows), &sblocks);
+  {
+    ProfScope ps(c, "sample_gemm", s);
+    VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 1, s, sblocks, sg));
+    VDBG_HIP(hipGetLastError());
+  }
+  KthArgs ka{gm, ngroups, int(nq), int(kk), eb, T};
+  {
+    ProfScope ps(c, "kth", s);
+    VDBG_DISPATCH_E(Ek, launch_kth, s, ka);
+    VDBG_HIP(hipGetLastError());
+  }
+
+  // main pass
+  GemmArgs ga{};
+  ga.X = src->X;
+  ga.C = src->C;
+  ga.rn = src->rn;
+  ga.Qb = B;
+  ga.T = T;
+  ga.allow = allow;
+  ga.cand = cand;
+  ga.counts = counts;
+  ga.ovf = ovf;
+  ga.N = N;
+  ga.nq = int(nq);
+  ga.chunk_rows = chunk_rows;
+  ga.caph = caph;
+  int blocks = 0;
+  GemmGrid(ga, nqt, nchunks, &blocks);
+  {
+    ProfScope ps(c, src->kind == 0 ? "flat_gemm" : "sq8_gemm", s);
+    VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
+    VDBG_HIP(hipGetLastError());
+  }
+  SelectArgs se{};
+  se.Q = Q;
+  se.cand = cand;
+  se.counts = counts;
+  se.nseg = nseg;
+  se.cap = caph;
+  se.ovf = ovf;
+  se.shift = shift;
+  se.eb = eb;
+  se.exact = exact;
+  se.nslots = int(nq);
+  se.k = int(kk);
+  se.pd = int(pd);
+  se.rescore = 1;
+  se.out_ids = out_ids;
+  se.out_d = out_d;
+  se.fb_list = fb_list;
+  se.fb_count = fb_count;
+  {
+    ProfScope ps(c, "select", s);
+    if (src->kind == 0) {
+      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, se, FlatOf(*src));
+    } else {
+      VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, se, Sq8Of(*src));
+    }
+    VDBG_HIP(hipGetLastError());
+  }
+  VDBG_HIP(hipMemcpyAsync(c->host_pinned, fb_count, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  const uint32_t nfb = c->host_pinned[0];
+  c->last_fallbacks = nfb;
+  if (nfb > 0)
+    VDBG_RETURN_IF_ERROR(
+        ExactScan(c, c->ws2, *src, Q, fb_list, int(nfb), kk, allow, out_ids, out_d, s));
+  return kOk;
+}
+
+int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq,
+           const uint32_t* cand, size_t depth, size_t k, uint32_t* out_ids, float* out_d,
+           hipStream_t s) {
+  if (nq == 0 || k == 0) return kOk;
+  const int E = pow2_e(std::max(depth, k));
+  RerankArgs ra{X, Q, pd, metric, cand, int(depth), int(nq), int(k), out_ids, out_d};
+  ProfScope ps(c, "rerank", s);
+  VDBG_DISPATCH_E(E, launch_rerank, s, ra);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace vdbg

@@ -1,8 +1,11 @@
 // vdbg_api.hip -- the C ABI (include/vdbg.h): contexts, resident datasets, profiling and
 // the flat search entry points.
+#include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <string>
+#include <vector>
 
 #include "vdbg_internal.h"
 
@@ -129,8 +132,85 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
     delete ds;
     return rc;
   }
+  d.src.kind = 0;
+  d.src.X = d.rows;
+  d.src.rn = d.norms;
+  d.src.N = static_cast<uint32_t>(n);
+  d.src.pd = static_cast<int>(pd);
+  d.src.metric = metric;
+  d.src.rmag = d.stats.xn_max;
+  d.src.stats = d.stats;
   *out = ds;
   return kOk;
+}
+
+// The SQ8 search: top max(depth, k) by the SQ8 distance, then (depth > 0) Rerank with the
+// fp32 rows to k, as HnswSq8Index::search does with its beam
+// (src/index/hnsw/hnsw_index.cc:82-100).
+static int Sq8Search(Sq8Index* x, const float* Q, size_t nq, size_t k, size_t depth,
+                     const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+  Ctx* c = x->ds->ctx;
+  if (nq == 0 || k == 0) return kOk;
+  if (depth == 0) return RunScan(c, &x->src, Q, nq, k, allow, out_ids, out_d, s);
+  const size_t kk = std::max(depth, k);
+  uint32_t* ti = nullptr;
+  float* td = nullptr;
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&ti), nq * kk * 4, s);
+  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&td), nq * kk * 4, s);
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(ti, s);
+    return SetError(kResourceExhausted, std::string("sq8 search: ") + hipGetErrorString(e));
+  }
+  int rc = RunScan(c, &x->src, Q, nq, kk, allow, ti, td, s);
+  if (rc == kOk)
+    rc = Rerank(c, x->ds->rows, int(x->ds->pd), x->ds->metric, Q, nq, ti, kk, k, out_ids, out_d,
+                s);
+  (void)hipFreeAsync(ti, s);
+  (void)hipFreeAsync(td, s);
+  return rc;
+}
+
+// Host-pointer staging shared by the _host entry points: copies queries (and the filter)
+// in, runs `fn` on device pointers, copies results out and synchronises.
+template <class Fn>
+static int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, size_t nq,
+                     size_t k, const uint64_t* allow_words, uint32_t* out_ids,
+                     float* out_dists, Fn fn) {
+  hipStream_t s = c->stream;
+  const size_t words = (n_rows + 63) / 64;
+  float* dq = nullptr;
+  uint64_t* dm = nullptr;
+  uint32_t* di = nullptr;
+  float* dd = nullptr;
+  auto cleanup = [&]() {
+    (void)hipFreeAsync(dq, s);
+    (void)hipFreeAsync(dm, s);
+    (void)hipFreeAsync(di, s);
+    (void)hipFreeAsync(dd, s);
+  };
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dq), nq * pd * sizeof(float), s);
+  if (e == hipSuccess && allow_words)
+    e = hipMallocAsync(reinterpret_cast<void**>(&dm), words * sizeof(uint64_t) + 8, s);
+  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&di), nq * k * 4, s);
+  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dd), nq * k * 4, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(dq, queries, nq * pd * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && allow_words)
+    e = hipMemcpyAsync(dm, allow_words, words * sizeof(uint64_t), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) {
+    cleanup();
+    return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                    std::string("staging: ") + hipGetErrorString(e));
+  }
+  int rc = fn(dq, allow_words ? dm : nullptr, di, dd, s);
+  if (rc == kOk) {
+    e = hipMemcpyAsync(out_ids, di, nq * k * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(out_dists, dd, nq * k * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = SetError(kInternal, std::string("copy-out: ") + hipGetErrorString(e));
+  }
+  cleanup();
+  return rc;
 }
 
 }  // namespace vdbg
@@ -157,6 +237,7 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
   auto* ctx = new (std::nothrow) vdbg_ctx;
   if (ctx == nullptr) return SetError(kResourceExhausted, "out of host memory");
   ctx->c.device = device;
+  ctx->c.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   hipError_t e = hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&ctx->c.host_pinned), 4096, hipHostMallocDefault);
@@ -236,6 +317,7 @@ int vdbg_dataset_destroy(vdbg_dataset* ds) {
   std::lock_guard<std::recursive_mutex> g(c->mu);
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
+  FreeSample(&ds->d.src);
   (void)hipFree(ds->d.rows);
   (void)hipFree(ds->d.norms);
   delete ds;
@@ -255,58 +337,172 @@ int vdbg_flat_search_device(vdbg_dataset* ds, const float* queries, size_t nq, s
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
-  return FlatSearch(&ds->d, queries, nq, k, allow_words, out_ids, out_dists, s);
+  return RunScan(c, &ds->d.src, queries, nq, k, allow_words, out_ids, out_dists, s);
 }
 
 int vdbg_flat_search_host(vdbg_dataset* ds, const float* queries, size_t nq, size_t k,
                           const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
                           uint64_t* dist_comps) {
   if (ds == nullptr) return SetError(kInvalidArgument, "null dataset");
-  if (nq == 0 || k == 0) {
-    if (dist_comps) *dist_comps = 0;
-    return kOk;
-  }
+  if (dist_comps) *dist_comps = 0;
+  if (nq == 0 || k == 0) return kOk;
   if (queries == nullptr || out_ids == nullptr || out_dists == nullptr)
     return SetError(kInvalidArgument, "null pointer");
   Ctx* c = ds->d.ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
+  Dataset* d = &ds->d;
+  int rc = StageHost(c, d->n, d->pd, queries, nq, k, allow_words, out_ids, out_dists,
+                     [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
+                         hipStream_t s) {
+                       return RunScan(c, &d->src, dq, nq, k, dm, di, dd, s);
+                     });
+  if (rc == kOk && dist_comps) *dist_comps = uint64_t(nq) * d->n;
+  return rc;
+}
+
+int vdbg_sq8_train(vdbg_dataset* ds, float* vmin_out, float* scale_out) {
+  if (ds == nullptr || vmin_out == nullptr || scale_out == nullptr)
+    return SetError(kInvalidArgument, "null argument");
+  Ctx* c = ds->d.ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
   hipStream_t s = c->stream;
   const size_t pd = ds->d.pd;
-  const size_t words = (ds->d.n + 63) / 64;
-  float* dq = nullptr;
-  uint64_t* dm = nullptr;
-  uint32_t* di = nullptr;
-  float* dd = nullptr;
-  auto cleanup = [&]() {
-    (void)hipFreeAsync(dq, s);
-    (void)hipFreeAsync(dm, s);
-    (void)hipFreeAsync(di, s);
-    (void)hipFreeAsync(dd, s);
-  };
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dq), nq * pd * sizeof(float), s);
-  if (e == hipSuccess && allow_words)
-    e = hipMallocAsync(reinterpret_cast<void**>(&dm), words * sizeof(uint64_t) + 8, s);
-  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&di), nq * k * 4, s);
-  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dd), nq * k * 4, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(dq, queries, nq * pd * sizeof(float), hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && allow_words)
-    e = hipMemcpyAsync(dm, allow_words, words * sizeof(uint64_t), hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) {
-    cleanup();
-    return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
-                    std::string("flat search staging: ") + hipGetErrorString(e));
-  }
-  int rc = FlatSearch(&ds->d, dq, nq, k, allow_words ? dm : nullptr, di, dd, s);
+  float* dv = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dv), 2 * pd * sizeof(float), s));
+  int rc = Sq8Train(c, &ds->d, dv, dv + pd, s);
   if (rc == kOk) {
-    e = hipMemcpyAsync(out_ids, di, nq * k * 4, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(out_dists, dd, nq * k * 4, hipMemcpyDeviceToHost, s);
+    hipError_t e = hipMemcpyAsync(vmin_out, dv, pd * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(scale_out, dv + pd, pd * 4, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) rc = SetError(kInternal, std::string("flat search: ") + hipGetErrorString(e));
+    if (e != hipSuccess) rc = SetError(kInternal, std::string("sq8 train: ") + hipGetErrorString(e));
   }
-  cleanup();
-  if (rc == kOk && dist_comps) *dist_comps = uint64_t(nq) * ds->d.n;
+  (void)hipFreeAsync(dv, s);
+  return rc;
+}
+
+int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdbg_sq8** out) {
+  if (ds == nullptr || vmin == nullptr || scale == nullptr || out == nullptr)
+    return SetError(kInvalidArgument, "null argument");
+  Ctx* c = ds->d.ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  Dataset& d = ds->d;
+  const size_t pd = d.pd, n = d.n;
+  auto* h = new (std::nothrow) vdbg_sq8;
+  if (h == nullptr) return SetError(kResourceExhausted, "out of host memory");
+  Sq8Index& x = h->q;
+  x.ds = &d;
+  x.vmin_h.assign(vmin, vmin + pd);
+  x.scale_h.assign(scale, scale + pd);
+  auto fail = [&](int rc) {
+    (void)hipFree(x.codes);
+    (void)hipFree(x.yn);
+    (void)hipFree(x.vmin);
+    delete h;
+    return rc;
+  };
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&x.vmin), 2 * pd * sizeof(float));
+  if (e == hipSuccess && n > 0) e = hipMalloc(reinterpret_cast<void**>(&x.codes), n * pd);
+  if (e == hipSuccess && n > 0) e = hipMalloc(reinterpret_cast<void**>(&x.yn), n * sizeof(float));
+  if (e != hipSuccess)
+    return fail(SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                         std::string("sq8 create: ") + hipGetErrorString(e)));
+  x.scale = x.vmin + pd;
+  e = hipMemcpyAsync(x.vmin, vmin, pd * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(x.scale, scale, pd * 4, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) return fail(SetError(kInternal, hipGetErrorString(e)));
+  int rc = Sq8Encode(c, &d, x.vmin, x.scale, x.codes, x.yn, s);
+  if (rc != kOk) return fail(rc);
+  // magnitude term of the rounding bound: max ||code*scale||^2, a bound on the decoded
+  // row norm, and ||vmin||^2
+  std::vector<float> yn(n);
+  if (n > 0) {
+    e = hipMemcpyAsync(yn.data(), x.yn, n * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(SetError(kInternal, hipGetErrorString(e)));
+  }
+  double ymax = 0, xhat = 0, vn = 0;
+  for (float v : yn) ymax = std::max(ymax, double(v));
+  for (size_t i = 0; i < pd; ++i) {
+    const double a = std::fabs(double(vmin[i]));
+    const double b = std::fabs(double(vmin[i]) + 255.0 * double(scale[i]));
+    xhat += std::max(a, b) * std::max(a, b);
+    vn += double(vmin[i]) * vmin[i];
+  }
+  x.src.kind = 1;
+  x.src.C = x.codes;
+  x.src.rn = x.yn;
+  x.src.vmin = x.vmin;
+  x.src.scale = x.scale;
+  x.src.N = static_cast<uint32_t>(n);
+  x.src.pd = static_cast<int>(pd);
+  x.src.metric = d.metric;
+  x.src.rmag = float(ymax + xhat + vn);
+  *out = h;
+  return kOk;
+}
+
+int vdbg_sq8_destroy(vdbg_sq8* sq) {
+  if (sq == nullptr) return kOk;
+  Ctx* c = sq->q.ds->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  (void)hipSetDevice(c->device);
+  (void)hipDeviceSynchronize();
+  FreeSample(&sq->q.src);
+  (void)hipFree(sq->q.codes);
+  (void)hipFree(sq->q.yn);
+  (void)hipFree(sq->q.vmin);
+  delete sq;
+  return kOk;
+}
+
+int vdbg_sq8_codes(vdbg_sq8* sq, uint8_t* codes_out) {
+  if (sq == nullptr || codes_out == nullptr) return SetError(kInvalidArgument, "null argument");
+  Ctx* c = sq->q.ds->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  const size_t bytes = sq->q.ds->n * sq->q.ds->pd;
+  if (bytes == 0) return kOk;
+  VDBG_HIP(hipMemcpyAsync(codes_out, sq->q.codes, bytes, hipMemcpyDeviceToHost, c->stream));
+  VDBG_HIP(hipStreamSynchronize(c->stream));
+  return kOk;
+}
+
+int vdbg_sq8_search_device(vdbg_sq8* sq, const float* queries, size_t nq, size_t k,
+                           size_t depth, const uint64_t* allow_words, uint32_t* out_ids,
+                           float* out_dists, void* stream) {
+  if (sq == nullptr) return SetError(kInvalidArgument, "null index");
+  if (nq > 0 && k > 0 && (queries == nullptr || out_ids == nullptr || out_dists == nullptr))
+    return SetError(kInvalidArgument, "null pointer");
+  Ctx* c = sq->q.ds->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+  return Sq8Search(&sq->q, queries, nq, k, depth, allow_words, out_ids, out_dists, s);
+}
+
+int vdbg_sq8_search_host(vdbg_sq8* sq, const float* queries, size_t nq, size_t k, size_t depth,
+                         const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
+                         uint64_t* dist_comps) {
+  if (sq == nullptr) return SetError(kInvalidArgument, "null index");
+  if (dist_comps) *dist_comps = 0;
+  if (nq == 0 || k == 0) return kOk;
+  if (queries == nullptr || out_ids == nullptr || out_dists == nullptr)
+    return SetError(kInvalidArgument, "null pointer");
+  Ctx* c = sq->q.ds->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  Sq8Index* x = &sq->q;
+  int rc = StageHost(c, x->ds->n, x->ds->pd, queries, nq, k, allow_words, out_ids, out_dists,
+                     [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
+                         hipStream_t s) {
+                       return Sq8Search(x, dq, nq, k, depth, dm, di, dd, s);
+                     });
+  if (rc == kOk && dist_comps)
+    *dist_comps = uint64_t(nq) * (x->ds->n + (depth > 0 ? std::min(std::max(depth, k), x->ds->n) : 0));
   return rc;
 }
 

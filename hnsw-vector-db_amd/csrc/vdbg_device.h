@@ -136,6 +136,53 @@ __device__ __forceinline__ float metric_exact(int metric, const float* q, const 
   return metric == 0 ? l2_exact(q, x, pd) : -dot_exact(q, x, pd);
 }
 
+// sq8_l2_avx512 / sq8_ip_avx512 (avx512.cc:48-64): each code byte decodes as
+// fma(code, scale, vmin) (Decode16, :11-15); one 16-lane accumulator; GCC reduce tree.
+__device__ __forceinline__ float sq8_exact(int metric, const float* __restrict__ q,
+                                           const uint8_t* __restrict__ c,
+                                           const float* __restrict__ vmin,
+                                           const float* __restrict__ scale, int pd) {
+  float acc[16];
+#pragma unroll
+  for (int l = 0; l < 16; ++l) acc[l] = 0.f;
+  for (int i = 0; i < pd; i += 16) {
+    const uint4 cb = *reinterpret_cast<const uint4*>(c + i);
+    const uint32_t w[4] = {cb.x, cb.y, cb.z, cb.w};
+#pragma unroll
+    for (int l = 0; l < 16; ++l) {
+      const float code = float((w[l >> 2] >> (8 * (l & 3))) & 0xffu);
+      const float x = fmaf(code, scale[i + l], vmin[i + l]);
+      if (metric == 0) {
+        const float diff = q[i + l] - x;
+        acc[l] = fmaf(diff, diff, acc[l]);
+      } else {
+        acc[l] = fmaf(q[i + l], x, acc[l]);
+      }
+    }
+  }
+  const float s = reduce16(acc);
+  return metric == 0 ? s : -s;
+}
+
+// Exact scorers: the reference's distance of query q to row `row`.
+struct FlatScorer {
+  const float* X;
+  int pd, metric;
+  __device__ __forceinline__ float operator()(const float* q, uint32_t row) const {
+    return metric_exact(metric, q, X + size_t(row) * pd, pd);
+  }
+};
+
+struct Sq8Scorer {
+  const uint8_t* C;
+  const float* vmin;
+  const float* scale;
+  int pd, metric;
+  __device__ __forceinline__ float operator()(const float* q, uint32_t row) const {
+    return sq8_exact(metric, q, C + size_t(row) * pd, vmin, scale, pd);
+  }
+};
+
 // ----------------------------------------------------------------- wave bitonic
 
 // Keys live in registers: element g = e * 64 + lane for e in [0, E).  All loops unroll

@@ -82,7 +82,27 @@ struct Ctx {
   std::vector<hipEvent_t> free_events;
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
   uint64_t last_fallbacks = 0;
-  int device_arch_ok = 1;
+  int cu_count = 256;
+};
+
+// What an exhaustive scan reads: fp32 rows (kind 0, flat) or SQ8 codes (kind 1), the
+// GEMM-form row norms, and a bit-reversed strided sample of rows built on first use.
+struct ScanSource {
+  int kind = 0;
+  const float* X = nullptr;     // kind 0: n x pd rows
+  const uint8_t* C = nullptr;   // kind 1: n x pd codes
+  const float* rn = nullptr;    // ||x||^2 (flat) or ||code * scale||^2 (SQ8)
+  const float* vmin = nullptr;  // SQ8 quantizer (device)
+  const float* scale = nullptr;
+  uint32_t N = 0;
+  int pd = 0, metric = 0;
+  float rmag = 0.f;             // row magnitude term of the rounding bound
+  RowStats stats;               // flat: value statistics for the exactness test
+  float* SX = nullptr;          // sample rows (kind 0)
+  uint8_t* SC = nullptr;        // sample codes (kind 1)
+  float* Srn = nullptr;
+  uint32_t* Sid = nullptr;
+  uint32_t Smax = 0;
 };
 
 struct Dataset {
@@ -92,6 +112,19 @@ struct Dataset {
   size_t n = 0, dim = 0, pd = 0;
   int metric = 0;
   RowStats stats;
+  ScanSource src;          // the flat scan's view of these rows
+};
+
+// SQ8 codes of a dataset's rows (HnswSq8Index's codes_ and Sq8Quantizer,
+// src/index/hnsw/hnsw_index.h:89-95, without the graph).
+struct Sq8Index {
+  Dataset* ds = nullptr;
+  uint8_t* codes = nullptr;  // n x pd
+  float* yn = nullptr;       // ||code * scale||^2 per row
+  float* vmin = nullptr;     // pd (device)
+  float* scale = nullptr;
+  std::vector<float> vmin_h, scale_h;
+  ScanSource src;
 };
 
 // Brackets a launch with events when the context is profiling.
@@ -112,10 +145,18 @@ class ProfScope {
 int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
                    float* norms, RowStats* out);
 
-struct FlatPlan;
-// Flat exact search over a resident dataset; queries/outputs/allow are device pointers.
-int FlatSearch(Dataset* ds, const float* Q, size_t nq, size_t k, const uint64_t* allow,
-               uint32_t* out_ids, float* out_d, hipStream_t s);
+// Top-kk rows by the source's exact distance for nq queries (device pointers).
+int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
+            const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
+// Exact fp32 distances of `depth` candidate rows per query, the k smallest.
+int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq,
+           const uint32_t* cand, size_t depth, size_t k, uint32_t* out_ids, float* out_d,
+           hipStream_t s);
+int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipStream_t s);
+int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
+              uint8_t* codes, float* yn, hipStream_t s);
+int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);
+void FreeSample(ScanSource* src);
 
 }  // namespace vdbg
 
@@ -124,4 +165,7 @@ struct vdbg_ctx {
 };
 struct vdbg_dataset {
   vdbg::Dataset d;
+};
+struct vdbg_sq8 {
+  vdbg::Sq8Index q;
 };

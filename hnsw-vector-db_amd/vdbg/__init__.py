@@ -60,6 +60,13 @@ _SIGS = {
                                         C.POINTER(C.c_uint64)]),
     "vdbg_flat_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
     "vdbg_last_fallbacks": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
+    "vdbg_sq8_train": (C.c_int, [_vp, _vp, _vp]),
+    "vdbg_sq8_create": (C.c_int, [_vp, _vp, _vp, C.POINTER(_vp)]),
+    "vdbg_sq8_destroy": (C.c_int, [_vp]),
+    "vdbg_sq8_codes": (C.c_int, [_vp, _vp]),
+    "vdbg_sq8_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp,
+                                       C.POINTER(C.c_uint64)]),
+    "vdbg_sq8_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -188,3 +195,59 @@ class Dataset:
         """Device pointers (ints), queued on `stream` (None = the context's stream)."""
         _check(lib.vdbg_flat_search_device(self.h, q_ptr, nq, k, allow_ptr, ids_ptr,
                                            dists_ptr, stream))
+
+
+class Sq8Index:
+    """SQ8 codes of a dataset's rows, resident in HBM (vdbg_sq8)."""
+
+    def __init__(self, ds, vmin=None, scale=None):
+        if vmin is None:
+            vmin, scale = ds.sq8_train()
+        self.vmin = np.ascontiguousarray(vmin, np.float32)
+        self.scale = np.ascontiguousarray(scale, np.float32)
+        h = _vp()
+        _check(lib.vdbg_sq8_create(ds.h, _ptr(self.vmin), _ptr(self.scale), C.byref(h)))
+        self.ds, self.h = ds, h
+
+    def close(self):
+        if self.h:
+            lib.vdbg_sq8_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def codes(self):
+        out = np.empty((self.ds.n, self.ds.pd), np.uint8)
+        _check(lib.vdbg_sq8_codes(self.h, _ptr(out)))
+        return out
+
+    def search(self, queries, k, depth, allow=None):
+        q = np.ascontiguousarray(queries, np.float32)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), np.uint32)
+        dists = np.empty((nq, k), np.float32)
+        if allow is not None:
+            allow = np.ascontiguousarray(allow, np.uint64)
+        dc = C.c_uint64()
+        _check(lib.vdbg_sq8_search_host(self.h, _ptr(q), nq, k, depth, _ptr(allow), _ptr(ids),
+                                        _ptr(dists), C.byref(dc)))
+        return ids, dists
+
+    def search_device(self, q_ptr, nq, k, depth, ids_ptr, dists_ptr, allow_ptr=None,
+                      stream=None):
+        _check(lib.vdbg_sq8_search_device(self.h, q_ptr, nq, k, depth, allow_ptr, ids_ptr,
+                                          dists_ptr, stream))
+
+
+def _sq8_train(self):
+    vmin = np.empty(self.pd, np.float32)
+    scale = np.empty(self.pd, np.float32)
+    _check(lib.vdbg_sq8_train(self.h, _ptr(vmin), _ptr(scale)))
+    return vmin, scale
+
+
+Dataset.sq8_train = _sq8_train

@@ -112,6 +112,34 @@ int vdbg_flat_search_device(vdbg_dataset* ds, const float* queries, size_t nq, s
                             const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
                             void* stream);
 
+/* ---------------------------------------------------------------- SQ8 */
+
+typedef struct vdbg_sq8 vdbg_sq8;
+
+/* Sq8Quantizer::train (src/index/quant/sq8.cc:9-26) over the dataset's rows: per real
+ * dimension min and max, scale = (max - min) / 255; padding dimensions get 0.  vmin_out and
+ * scale_out receive padded_dim floats (host). */
+int vdbg_sq8_train(vdbg_dataset* ds, float* vmin_out, float* scale_out);
+/* Encodes every row with Sq8Quantizer::encode (sq8.cc:28-37), byte-identical to the CPU
+ * encoder, and keeps the codes resident: HnswSq8Index::build (src/index/hnsw/hnsw_index.cc:
+ * 66-79) without the graph.  vmin/scale are padded_dim floats (host), e.g. from
+ * vdbg_sq8_train or a deserialised quantizer (sq8.cc:43-63). */
+int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdbg_sq8** out);
+int vdbg_sq8_destroy(vdbg_sq8* sq);
+/* Copies the n x padded_dim code bytes to the host. */
+int vdbg_sq8_codes(vdbg_sq8* sq, uint8_t* codes_out);
+/* Exhaustive SQ8 search: the max(depth, k) smallest asymmetric SQ8 distances
+ * (MetricSq8Distance, src/distance/cpu_features.cc:75-78) by (dist, id), then, when
+ * depth > 0, Rerank (src/index/index.cc:89-95) with the fp32 rows to k; depth 0 returns the
+ * top k by SQ8 distance.  This is HnswSq8Index::search (hnsw_index.cc:82-100) with the
+ * graph beam replaced by a full scan. */
+int vdbg_sq8_search_host(vdbg_sq8* sq, const float* queries, size_t nq, size_t k, size_t depth,
+                         const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
+                         uint64_t* dist_comps);
+int vdbg_sq8_search_device(vdbg_sq8* sq, const float* queries, size_t nq, size_t k,
+                           size_t depth, const uint64_t* allow_words, uint32_t* out_ids,
+                           float* out_dists, void* stream);
+
 /* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
  * candidates could not be certified and were re-scanned exactly. */
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);

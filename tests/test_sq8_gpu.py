@@ -1,0 +1,87 @@
+"""SQ8 on the GPU against the oracle: training and encoding byte-identical to
+Sq8Quantizer (src/index/quant/sq8.cc:9-37); the exhaustive SQ8 scan into the top
+max(depth, k) plus fp32 Rerank (src/index/hnsw/hnsw_index.cc:82-100, src/index/index.cc:
+89-95) with ids and distances bit-exact."""
+import numpy as np
+import pytest
+
+import vdbg
+from vdbg import datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _eq(gi, gd, oi, od):
+    bad = np.nonzero((gi != oi).any(1) | (gd.view(np.uint32) != od.view(np.uint32)).any(1))[0]
+    assert bad.size == 0, (f"{bad.size} queries differ; q={bad[0]} gpu={gi[bad[0]].tolist()} "
+                           f"{gd[bad[0]].tolist()} oracle={oi[bad[0]].tolist()} "
+                           f"{od[bad[0]].tolist()}")
+
+
+@pytest.mark.parametrize("n,dim,seed", [(3000, 100, 1), (20000, 128, 2), (100, 7, 3)])
+def test_sq8_train_encode_byte_identical(ctx, oracle, n, dim, seed):
+    print(f"sq8 train/encode n={n} dim={dim}", flush=True)
+    pd = vdbg.padded_dim(dim)
+    rng = np.random.default_rng(seed)
+    base = datagen.pad(rng.normal(0, 3, (n, dim)).astype(np.float32), pd)
+    base[:, min(3, dim - 1)] = 0.5  # a constant column: scale 0
+    ds = vdbg.Dataset(ctx, base, dim)
+    vmin, scale = ds.sq8_train()
+    ov, osc = oracle.sq8_train(base, dim)
+    assert np.array_equal(vmin.view(np.uint32), ov.view(np.uint32))
+    assert np.array_equal(scale.view(np.uint32), osc.view(np.uint32))
+    sq = vdbg.Sq8Index(ds, vmin, scale)
+    assert np.array_equal(sq.codes(), oracle.sq8_encode(base, dim, ov, osc))
+
+
+def test_sq8_train_sift_like_full_size_invariants(ctx):
+    # 1M x 128 SIFT-like: min/max are exact values of the data, codes decode within half
+    # a step (tests/distance_test.cc:106-126), checked on a strided subset
+    base = datagen.sift_like(1_000_000, 128, 2002)
+    ds = vdbg.Dataset(ctx, base, 128)
+    vmin, scale = ds.sq8_train()
+    assert np.array_equal(vmin, base.min(0))
+    assert np.array_equal(scale, (base.max(0) - vmin) / np.float32(255))
+    sq = vdbg.Sq8Index(ds, vmin, scale)
+    codes = sq.codes()
+    sub = slice(0, None, 997)
+    back = vmin + codes[sub].astype(np.float32) * scale
+    assert (np.abs(back - base[sub]) <= scale * 0.5 * 1.0001 + 1e-6).all()
+
+
+@pytest.mark.parametrize("n,nq,k,depth", [(20000, 100, 10, 100), (20000, 64, 10, 0),
+                                          (5000, 10, 10, 50), (30000, 200, 100, 100)])
+def test_sq8_search_matches_oracle(ctx, oracle, n, nq, k, depth):
+    print(f"sq8 search n={n} nq={nq} k={k} depth={depth}", flush=True)
+    base = datagen.sift_like(n, 128, 2002)
+    qs = datagen.sift_like(nq, 128, 2003)
+    ds = vdbg.Dataset(ctx, base, 128)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, k, depth)
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth)
+    _eq(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("metric", ["ip", "cosine"])
+def test_sq8_inner_product(ctx, oracle, metric):
+    base = datagen.clustered_unit(20000, 128, 41, 42, 100, 0.5)
+    qs = datagen.clustered_unit(64, 128, 43, 42, 100, 0.5)
+    ds = vdbg.Dataset(ctx, base, 128, metric=metric)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, 10, 64)
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 64, metric=metric)
+    _eq(gi, gd, oi, od)
+
+
+def test_sq8_filter(ctx, oracle):
+    base = datagen.uniform_rows(20000, 128, 51)
+    qs = datagen.uniform_rows(40, 128, 52)
+    allow = np.zeros((20000 + 63) // 64, np.uint64)
+    rows = np.arange(0, 20000, 5)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 128)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, 10, 40, allow=allow)
+    assert (gi % 5 == 0).all()
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 40, allow=allow)
+    _eq(gi, gd, oi, od)
