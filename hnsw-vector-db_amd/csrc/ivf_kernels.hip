@@ -1,0 +1,332 @@
+// ivf_kernels.hip -- IVF-PQ on gfx950: per-list precomputed tables, per-query tables, the
+// ADC list scan with a top-R, and the PQ encoder.
+//
+// IvfPqIndex::search (src/index/quant/ivf_pq.cc:169-222) per query: coarse distances to
+// every centroid, the nprobe nearest by (dist, list id); for L2 with precomputed tables
+// table[i] = term2[l][i] + qtab[i] with qtab = 2 * (-<q_j, C_j[c]>) and offset = the coarse
+// distance; the list's codes scored as offset + adc(table, code) into TopK(max(R, k)); then
+// FinishSearch (:28-36).  Every float operation below follows that order, so scores match
+// the reference bit for bit:
+//   DotAny / L2SqAny  (src/distance/scalar.cc:43-73) four accumulators over i mod 4,
+//                     (s0 + s1) + (s2 + s3), products rounded before the add;
+//   adc               (src/index/quant/pq.h:36-46) four accumulators over j mod 4.
+#include <algorithm>
+#include <cstring>
+
+#include "vdbg_device.h"
+#include "vdbg_internal.h"
+
+namespace vdbg {
+
+constexpr int kKsub = 256;
+
+__device__ __forceinline__ float dot_any(const float* a, const float* b, int d) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int i = 0;
+  for (; i + 4 <= d; i += 4) {
+    s0 += a[i] * b[i];
+    s1 += a[i + 1] * b[i + 1];
+    s2 += a[i + 2] * b[i + 2];
+    s3 += a[i + 3] * b[i + 3];
+  }
+  for (; i < d; ++i) s0 += a[i] * b[i];
+  return (s0 + s1) + (s2 + s3);
+}
+
+__device__ __forceinline__ float l2sq_any(const float* a, const float* b, int d) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int i = 0;
+  for (; i + 4 <= d; i += 4) {
+    const float t0 = a[i] - b[i], t1 = a[i + 1] - b[i + 1];
+    const float t2 = a[i + 2] - b[i + 2], t3 = a[i + 3] - b[i + 3];
+    s0 += t0 * t0;
+    s1 += t1 * t1;
+    s2 += t2 * t2;
+    s3 += t3 * t3;
+  }
+  for (; i < d; ++i) {
+    const float t = a[i] - b[i];
+    s0 += t * t;
+  }
+  return (s0 + s1) + (s2 + s3);
+}
+
+__device__ __forceinline__ bool row_ok(const uint64_t* w, uint32_t r) {
+  return w == nullptr || ((w[r >> 6] >> (r & 63)) & 1ull);
+}
+
+// precompute_tables (ivf_pq.cc:152-167): term2[l][j][c] = DotAny(C, C) + 2 * DotAny(c_l,j, C).
+// grid (nlist, m), one thread per centroid c.
+__global__ void k_ivf_term2(const float* __restrict__ coarse, int pd,
+                            const float* __restrict__ cen, int m, int dsub,
+                            float* __restrict__ term2) {
+  const int l = blockIdx.x, j = blockIdx.y, c = threadIdx.x;
+  const float* cc = cen + (size_t(j) * kKsub + c) * dsub;
+  const float* cl = coarse + size_t(l) * pd + size_t(j) * dsub;
+  const float norm = dot_any(cc, cc, dsub);
+  term2[(size_t(l) * m + j) * kKsub + c] = norm + 2.f * dot_any(cl, cc, dsub);
+}
+
+// Per-query tables (ProductQuantizer::compute_table, src/index/quant/pq.cc:63-73): with
+// precomputed L2 tables, 2 * (-DotAny(q_j, C_j[c])) (ivf_pq.cc:192-196); for inner product
+// and cosine -DotAny(q_j, C_j[c]), shared by every list (:191).  One thread per entry.
+__global__ void k_ivf_qtab(const float* __restrict__ Q, int pd, int nq,
+                           const float* __restrict__ cen, int m, int dsub, int twice,
+                           float* __restrict__ qtab) {
+  const size_t e = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  const size_t per = size_t(m) * kKsub;
+  if (e >= per * nq) return;
+  const int q = int(e / per);
+  const int jc = int(e - size_t(q) * per);
+  const int j = jc / kKsub;
+  const float v = -dot_any(Q + size_t(q) * pd + size_t(j) * dsub, cen + size_t(jc) * dsub, dsub);
+  qtab[e] = twice ? v * 2.f : v;
+}
+
+struct IvfScanArgs {
+  const float* Q;
+  int pd, dim, m, dsub, metric;
+  const float* coarse;
+  const float* cen;
+  const uint32_t* off;     // nlist + 1
+  const uint32_t* ids;     // CSR row ids
+  const uint8_t* codes;    // CSR codes, m bytes per row
+  const float* term2;      // nullable
+  const float* qtab;       // [nq][m*256]: 2*(-<q_j,C>) (L2 with term2) or -<q_j,C> (IP)
+  const uint32_t* probe;   // [nq][nprobe] list ids, nearest first
+  const float* probe_d;    // [nq][nprobe] coarse distances
+  int nprobe, nq;
+  const uint64_t* allow;
+  int R;                   // TopK capacity max(depth, k)
+  uint32_t* out_ids;       // [nq][R]
+  float* out_d;
+  uint64_t* dc;            // [nq] distance computations (nullable)
+  uint64_t dc_base;        // nlist: the coarse distances
+  int count_top;           // add the candidates handed to Rerank
+};
+
+constexpr int kIvfWaves = 4;
+constexpr int kMaxTable = 32 * kKsub;  // m <= 32
+
+// One wave per query.  For each probed list the wave builds the list's table in LDS (one
+// fl(term2 + qtab) per entry, exactly table[i] of the reference), then each lane scores one
+// code per step with the reference's ADC order and stages the ones below the running
+// threshold; full stages of 64 enter the wave top-k.
+template <int E>
+__global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
+  extern __shared__ float lds[];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int q = blockIdx.x * kIvfWaves + wave;
+  if (q >= a.nq) return;
+  const int ts = a.m * kKsub;
+  float* table = lds + size_t(wave) * (ts + 2 * 2 * kWave);
+  float* st_d = table + ts;                                   // staging: 128 keys
+  uint32_t* st_i = reinterpret_cast<uint32_t*>(st_d + 2 * kWave);
+  const float* qv = a.Q + size_t(q) * a.pd;
+  const float* qt = a.qtab + size_t(q) * ts;
+  const bool l2 = a.metric == 0;
+  const bool pre = l2 && a.term2 != nullptr;
+
+  WaveTopK<E> top;
+  top.init();
+  int staged = 0;
+  uint64_t scanned = 0;
+
+  if (!l2) {  // the shared IP table
+    for (int e = lane; e < ts; e += kWave) table[e] = qt[e];
+  }
+  for (int pi = 0; pi < a.nprobe; ++pi) {
+    const uint32_t l = a.probe[size_t(q) * a.nprobe + pi];
+    const float* cl = a.coarse + size_t(l) * a.pd;
+    float offset = 0.f;
+    __builtin_amdgcn_wave_barrier();
+    if (pre) {
+      offset = a.probe_d[size_t(q) * a.nprobe + pi];
+      const float* t2 = a.term2 + size_t(l) * ts;
+      for (int e = lane * 4; e < ts; e += kWave * 4) {
+        const float4 x = *reinterpret_cast<const float4*>(t2 + e);
+        const float4 y = *reinterpret_cast<const float4*>(qt + e);
+        *reinterpret_cast<float4*>(table + e) = make_float4(x.x + y.x, x.y + y.y, x.z + y.z,
+                                                            x.w + y.w);
+      }
+    } else if (l2) {
+      // residual table: L2SqAny(q_j - c_l,j, C_j[c]) with the residual rounded per dim
+      for (int e = lane; e < ts; e += kWave) {
+        const int j = e / kKsub;
+        float r[64];
+        for (int t = 0; t < a.dsub; ++t) r[t] = qv[j * a.dsub + t] - cl[j * a.dsub + t];
+        table[e] = l2sq_any(r, a.cen + size_t(e) * a.dsub, a.dsub);
+      }
+    } else {
+      offset = -dot_any(qv, cl, a.dim);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const uint32_t b = a.off[l], e_ = a.off[l + 1];
+    scanned += e_ - b;
+    for (uint32_t i0 = b; i0 < e_; i0 += kWave) {
+      const uint32_t i = i0 + lane;
+      float d = __builtin_inff();
+      uint32_t id = kNoId;
+      if (i < e_) {
+        id = a.ids[i];
+        if (row_ok(a.allow, id)) {
+          const uint8_t* cd = a.codes + size_t(i) * a.m;
+          float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+          int j = 0;
+          for (; j + 4 <= a.m; j += 4) {
+            s0 += table[(j + 0) * kKsub + cd[j + 0]];
+            s1 += table[(j + 1) * kKsub + cd[j + 1]];
+            s2 += table[(j + 2) * kKsub + cd[j + 2]];
+            s3 += table[(j + 3) * kKsub + cd[j + 3]];
+          }
+          for (; j < a.m; ++j) s0 += table[j * kKsub + cd[j]];
+          d = offset + ((s0 + s1) + (s2 + s3));
+        } else {
+          id = kNoId;
+        }
+      }
+      // stage the keys below the running threshold
+      float td;
+      uint32_t ti;
+      top.threshold(td, ti);
+      const bool want = id != kNoId && nb_less(d, id, td, ti);
+      const uint64_t bal = __ballot(want);
+      if (bal != 0) {
+        const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
+        if (want) {
+          st_d[pos] = d;
+          st_i[pos] = id;
+        }
+        staged += __popcll(bal);
+        if (staged >= kWave) {
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+          const float sd = st_d[lane];
+          const uint32_t si = st_i[lane];
+          const float rd = lane + kWave < staged ? st_d[lane + kWave] : 0.f;
+          const uint32_t ri = lane + kWave < staged ? st_i[lane + kWave] : 0u;
+          __builtin_amdgcn_wave_barrier();
+          if (lane + kWave < staged) {
+            st_d[lane] = rd;
+            st_i[lane] = ri;
+          }
+          staged -= kWave;
+          top.insert(sd, si);
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (staged > 0) {
+    const bool have = lane < staged;
+    top.insert(have ? st_d[lane] : __builtin_inff(), have ? st_i[lane] : kNoId);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int gi = e * kWave + lane;
+    if (gi < a.R) {
+      a.out_ids[size_t(q) * a.R + gi] = top.k.id[e];
+      a.out_d[size_t(q) * a.R + gi] = top.k.d[e];
+    }
+  }
+  if (a.dc != nullptr) {
+    uint64_t valid = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      valid += __popcll(__ballot(top.k.id[e] != kNoId && e * kWave + lane < a.R));
+    if (lane == 0) a.dc[q] = a.dc_base + scanned + (a.count_top ? valid : 0);
+  }
+}
+
+// ProductQuantizer::encode (pq.cc:43-57) of the residual x - coarse[assign] (ivf_pq.cc:
+// 128-139): per subspace the first centroid with the smallest L2SqAny.  One thread per
+// (row, subspace).
+__global__ void k_pq_encode(const float* __restrict__ X, uint32_t n, int pd, int dim,
+                            const float* __restrict__ coarse, const uint32_t* __restrict__ assign,
+                            const float* __restrict__ cen, int m, int dsub,
+                            uint8_t* __restrict__ codes) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(n) * m) return;
+  const uint32_t r = uint32_t(t / m);
+  const int j = int(t - size_t(r) * m);
+  const float* x = X + size_t(r) * pd + size_t(j) * dsub;
+  const float* c = coarse != nullptr ? coarse + size_t(assign[r]) * pd + size_t(j) * dsub : nullptr;
+  float res[64];
+  for (int i = 0; i < dsub; ++i) res[i] = c != nullptr ? x[i] - c[i] : x[i];
+  float best = __builtin_inff();
+  int arg = 0;
+  for (int k = 0; k < kKsub; ++k) {
+    const float d = l2sq_any(res, cen + (size_t(j) * kKsub + k) * dsub, dsub);
+    if (d < best) {
+      best = d;
+      arg = k;
+    }
+  }
+  codes[size_t(r) * m + j] = uint8_t(arg);
+}
+
+// ---------------------------------------------------------------- launchers
+
+int IvfTerm2(Ctx* c, const float* coarse, int nlist, int pd, const float* cen, int m, int dsub,
+             float* term2, hipStream_t s) {
+  if (nlist == 0) return kOk;
+  ProfScope ps(c, "ivf_term2", s);
+  k_ivf_term2<<<dim3(nlist, m), kKsub, 0, s>>>(coarse, pd, cen, m, dsub, term2);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+int IvfQtab(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,
+            int twice, float* qtab, hipStream_t s) {
+  const size_t total = size_t(nq) * m * kKsub;
+  if (total == 0) return kOk;
+  ProfScope ps(c, "ivf_qtab", s);
+  k_ivf_qtab<<<dim3(unsigned((total + 255) / 256)), 256, 0, s>>>(Q, pd, nq, cen, m, dsub, twice,
+                                                                qtab);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+template <int E>
+static void launch_ivf(hipStream_t s, const IvfScanArgs& a, size_t lds) {
+  k_ivf_scan<E><<<dim3((a.nq + kIvfWaves - 1) / kIvfWaves), kIvfWaves * 64, lds, s>>>(a);
+}
+
+int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
+  if (a.nq == 0) return kOk;
+  if (a.m * kKsub > kMaxTable || a.dsub > 64)
+    return SetError(kNotSupported, "IVF-PQ scan: m <= 32 and dim/m <= 64 on the GPU path");
+  int e = 1;
+  while (kWave * e < a.R) e <<= 1;
+  const size_t lds = size_t(kIvfWaves) * (a.m * kKsub + 4 * kWave) * sizeof(float);
+  ProfScope ps(c, "ivf_scan", s);
+  switch (e) {
+    case 1: launch_ivf<1>(s, a, lds); break;
+    case 2: launch_ivf<2>(s, a, lds); break;
+    case 4: launch_ivf<4>(s, a, lds); break;
+    default: return SetError(kNotSupported, "IVF-PQ: max(rerank, k) > 256 on the GPU path");
+  }
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+int PqEncode(Ctx* c, const float* X, uint32_t n, int pd, int dim, const float* coarse,
+             const uint32_t* assign, const float* cen, int m, int dsub, uint8_t* codes,
+             hipStream_t s) {
+  const size_t total = size_t(n) * m;
+  if (total == 0) return kOk;
+  if (dsub > 64) return SetError(kNotSupported, "PQ encode: dim/m <= 64 on the GPU path");
+  ProfScope ps(c, "pq_encode", s);
+  k_pq_encode<<<dim3(unsigned((total + 255) / 256)), 256, 0, s>>>(X, n, pd, dim, coarse, assign,
+                                                                 cen, m, dsub, codes);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace vdbg

@@ -170,49 +170,6 @@ static int Sq8Search(Sq8Index* x, const float* Q, size_t nq, size_t k, size_t de
   return rc;
 }
 
-// Host-pointer staging shared by the _host entry points: copies queries (and the filter)
-// in, runs `fn` on device pointers, copies results out and synchronises.
-template <class Fn>
-static int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, size_t nq,
-                     size_t k, const uint64_t* allow_words, uint32_t* out_ids,
-                     float* out_dists, Fn fn) {
-  hipStream_t s = c->stream;
-  const size_t words = (n_rows + 63) / 64;
-  float* dq = nullptr;
-  uint64_t* dm = nullptr;
-  uint32_t* di = nullptr;
-  float* dd = nullptr;
-  auto cleanup = [&]() {
-    (void)hipFreeAsync(dq, s);
-    (void)hipFreeAsync(dm, s);
-    (void)hipFreeAsync(di, s);
-    (void)hipFreeAsync(dd, s);
-  };
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dq), nq * pd * sizeof(float), s);
-  if (e == hipSuccess && allow_words)
-    e = hipMallocAsync(reinterpret_cast<void**>(&dm), words * sizeof(uint64_t) + 8, s);
-  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&di), nq * k * 4, s);
-  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dd), nq * k * 4, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(dq, queries, nq * pd * sizeof(float), hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && allow_words)
-    e = hipMemcpyAsync(dm, allow_words, words * sizeof(uint64_t), hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) {
-    cleanup();
-    return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
-                    std::string("staging: ") + hipGetErrorString(e));
-  }
-  int rc = fn(dq, allow_words ? dm : nullptr, di, dd, s);
-  if (rc == kOk) {
-    e = hipMemcpyAsync(out_ids, di, nq * k * 4, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(out_dists, dd, nq * k * 4, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) rc = SetError(kInternal, std::string("copy-out: ") + hipGetErrorString(e));
-  }
-  cleanup();
-  return rc;
-}
-
 }  // namespace vdbg
 
 using namespace vdbg;
@@ -238,6 +195,7 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
   if (ctx == nullptr) return SetError(kResourceExhausted, "out of host memory");
   ctx->c.device = device;
   ctx->c.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+  ctx->c.handle = ctx;
   hipError_t e = hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&ctx->c.host_pinned), 4096, hipHostMallocDefault);

@@ -83,6 +83,7 @@ struct Ctx {
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
   uint64_t last_fallbacks = 0;
   int cu_count = 256;
+  vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 
 // What an exhaustive scan reads: fp32 rows (kind 0, flat) or SQ8 codes (kind 1), the
@@ -140,6 +141,23 @@ class ProfScope {
   bool on_;
 };
 
+// IvfPqIndex (src/index/quant/ivf_pq.h:42-81) made resident: coarse centroids (also a
+// dataset, so the coarse probe reuses the exhaustive scan), the PQ codebook, the inverted
+// lists in CSR form (ids ascending inside a list, codes contiguous) and, for L2, the
+// precomputed per-list tables.
+struct IvfIndex {
+  Dataset* ds = nullptr;             // the segment's rows (Rerank reads them)
+  vdbg_dataset* coarse_ds = nullptr; // nlist x pd coarse centroids
+  int nlist = 0, m = 0, dsub = 0, dim = 0, pd = 0, metric = 0;
+  float* cen = nullptr;              // m x 256 x dsub
+  uint32_t* off = nullptr;           // nlist + 1
+  uint32_t* ids = nullptr;           // n
+  uint8_t* codes = nullptr;          // n x m
+  float* term2 = nullptr;            // nlist x m x 256, or null
+  std::vector<float> coarse_h, cen_h;
+  std::vector<uint32_t> off_h;
+};
+
 // ---------------------------------------------------------------- launchers
 
 int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
@@ -158,6 +176,49 @@ int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* sca
 int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);
 void FreeSample(ScanSource* src);
 
+// Host-pointer staging shared by the _host entry points: copies queries (and the filter)
+// in, runs `fn` on device pointers, copies results out and synchronises.
+template <class Fn>
+inline int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, size_t nq,
+                     size_t k, const uint64_t* allow_words, uint32_t* out_ids,
+                     float* out_dists, Fn fn) {
+  hipStream_t s = c->stream;
+  const size_t words = (n_rows + 63) / 64;
+  float* dq = nullptr;
+  uint64_t* dm = nullptr;
+  uint32_t* di = nullptr;
+  float* dd = nullptr;
+  auto cleanup = [&]() {
+    (void)hipFreeAsync(dq, s);
+    (void)hipFreeAsync(dm, s);
+    (void)hipFreeAsync(di, s);
+    (void)hipFreeAsync(dd, s);
+  };
+  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dq), nq * pd * sizeof(float), s);
+  if (e == hipSuccess && allow_words)
+    e = hipMallocAsync(reinterpret_cast<void**>(&dm), words * sizeof(uint64_t) + 8, s);
+  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&di), nq * k * 4, s);
+  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dd), nq * k * 4, s);
+  if (e == hipSuccess)
+    e = hipMemcpyAsync(dq, queries, nq * pd * sizeof(float), hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && allow_words)
+    e = hipMemcpyAsync(dm, allow_words, words * sizeof(uint64_t), hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) {
+    cleanup();
+    return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                    std::string("staging: ") + hipGetErrorString(e));
+  }
+  int rc = fn(dq, allow_words ? dm : nullptr, di, dd, s);
+  if (rc == kOk) {
+    e = hipMemcpyAsync(out_ids, di, nq * k * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(out_dists, dd, nq * k * 4, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = SetError(kInternal, std::string("copy-out: ") + hipGetErrorString(e));
+  }
+  cleanup();
+  return rc;
+}
+
 }  // namespace vdbg
 
 struct vdbg_ctx {
@@ -168,4 +229,7 @@ struct vdbg_dataset {
 };
 struct vdbg_sq8 {
   vdbg::Sq8Index q;
+};
+struct vdbg_ivfpq {
+  vdbg::IvfIndex x;
 };

@@ -67,6 +67,14 @@ _SIGS = {
     "vdbg_sq8_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp,
                                        C.POINTER(C.c_uint64)]),
     "vdbg_sq8_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "vdbg_ivfpq_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
+    "vdbg_ivfpq_save": (C.c_int, [_vp, _vp, _sz, C.POINTER(_sz)]),
+    "vdbg_ivfpq_destroy": (C.c_int, [_vp]),
+    "vdbg_ivfpq_info": (C.c_int, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(C.c_int)]),
+    "vdbg_ivfpq_list_sizes": (C.c_int, [_vp, _vp]),
+    "vdbg_ivfpq_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp]),
+    "vdbg_ivfpq_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp,
+                                           _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -251,3 +259,63 @@ def _sq8_train(self):
 
 
 Dataset.sq8_train = _sq8_train
+
+
+class IvfPqIndex:
+    """An IVF-PQ index resident in HBM (vdbg_ivfpq), from a VDBIVFP1 file."""
+
+    def __init__(self, ds, h):
+        self.ds, self.h = ds, h
+
+    @classmethod
+    def load(cls, ds, blob):
+        blob = bytes(blob)
+        h = _vp()
+        _check(lib.vdbg_ivfpq_load(ds.h, blob, len(blob), C.byref(h)))
+        return cls(ds, h)
+
+    def close(self):
+        if self.h:
+            lib.vdbg_ivfpq_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def save(self):
+        n = _sz()
+        _check(lib.vdbg_ivfpq_save(self.h, None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value)
+        _check(lib.vdbg_ivfpq_save(self.h, buf, n.value, C.byref(n)))
+        return buf.raw[:n.value]
+
+    def info(self):
+        nl, m, pre = _sz(), _sz(), C.c_int()
+        _check(lib.vdbg_ivfpq_info(self.h, C.byref(nl), C.byref(m), C.byref(pre)))
+        return nl.value, m.value, bool(pre.value)
+
+    def list_sizes(self):
+        nl = self.info()[0]
+        out = np.empty(nl, np.uint64)
+        _check(lib.vdbg_ivfpq_list_sizes(self.h, _ptr(out)))
+        return out
+
+    def search(self, queries, k, nprobe, rerank=-1, allow=None):
+        q = np.ascontiguousarray(queries, np.float32)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), np.uint32)
+        dists = np.empty((nq, k), np.float32)
+        dc = np.empty(nq, np.uint64)
+        if allow is not None:
+            allow = np.ascontiguousarray(allow, np.uint64)
+        _check(lib.vdbg_ivfpq_search_host(self.h, _ptr(q), nq, k, nprobe, rerank, _ptr(allow),
+                                          _ptr(ids), _ptr(dists), _ptr(dc)))
+        return ids, dists, dc
+
+    def search_device(self, q_ptr, nq, k, nprobe, rerank, ids_ptr, dists_ptr, allow_ptr=None,
+                      dc_ptr=None, stream=None):
+        _check(lib.vdbg_ivfpq_search_device(self.h, q_ptr, nq, k, nprobe, rerank, allow_ptr,
+                                            ids_ptr, dists_ptr, dc_ptr, stream))

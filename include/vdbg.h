@@ -140,6 +140,39 @@ int vdbg_sq8_search_device(vdbg_sq8* sq, const float* queries, size_t nq, size_t
                            size_t depth, const uint64_t* allow_words, uint32_t* out_ids,
                            float* out_dists, void* stream);
 
+/* ---------------------------------------------------------------- IVF-PQ */
+
+typedef struct vdbg_ivfpq vdbg_ivfpq;
+
+/* LoadIndex for a VDBIVFP1 file (src/index/index.cc:38-87: magic and CRC32C footer) followed
+ * by IvfPqIndex::load (src/index/quant/ivf_pq.cc:251-278): coarse centroids, PQ codebook and
+ * inverted lists become resident, and the per-list tables of precompute_tables (:152-167) are
+ * derived on the GPU (L2, at most 1 GiB).  `ds` is the segment the index belongs to (rows
+ * must match).  Errors: 5 (corruption) for a bad file, as the reference returns. */
+int vdbg_ivfpq_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_ivfpq** out);
+/* Index::save for the resident index (ivf_pq.cc:236-249 + index.cc:110-117): writes the
+ * VDBIVFP1 file into buf (cap bytes); *len receives its size (buf may be NULL to ask). */
+int vdbg_ivfpq_save(vdbg_ivfpq* ix, void* buf, size_t cap, size_t* len);
+int vdbg_ivfpq_destroy(vdbg_ivfpq* ix);
+/* nlist, m and whether precomputed tables are in use (IvfPqIndex::nlist,
+ * precomputed_tables, ivf_pq.h:55-57). */
+int vdbg_ivfpq_info(vdbg_ivfpq* ix, size_t* nlist, size_t* m, int* precomputed_tables);
+/* IvfPqIndex::list_size for every list (ivf_pq.h:56); sizes has nlist entries. */
+int vdbg_ivfpq_list_sizes(vdbg_ivfpq* ix, uint64_t* sizes);
+/* IvfPqIndex::search (ivf_pq.cc:169-222) for nq queries: nprobe (SearchParams::nprobe,
+ * clamped to [1, nlist]) nearest lists by (dist, list id), ADC scores into
+ * TopK(max(R, k)) with R = RerankDepth(rerank) (:16-19: rerank < 0 -> max(10k, 100)), then
+ * FinishSearch (:28-36): R = 0 truncates, otherwise Rerank with the fp32 rows.  dist_comps
+ * (nullable, nq entries) receives IndexSearchStats::distance_computations per query. */
+int vdbg_ivfpq_search_host(vdbg_ivfpq* ix, const float* queries, size_t nq, size_t k,
+                           size_t nprobe, int rerank, const uint64_t* allow_words,
+                           uint32_t* out_ids, float* out_dists, uint64_t* dist_comps);
+/* Device-pointer variant; dist_comps (nullable) is a device array of nq entries. */
+int vdbg_ivfpq_search_device(vdbg_ivfpq* ix, const float* queries, size_t nq, size_t k,
+                             size_t nprobe, int rerank, const uint64_t* allow_words,
+                             uint32_t* out_ids, float* out_dists, uint64_t* dist_comps,
+                             void* stream);
+
 /* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
  * candidates could not be certified and were re-scanned exactly. */
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
