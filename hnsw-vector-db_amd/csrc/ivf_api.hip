@@ -222,8 +222,12 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
                      uint64_t* dc_dev, hipStream_t s) {
   Ctx* c = x->ds->ctx;
   if (nq == 0 || k == 0) return kOk;
-  if (x->nlist == 0) {
-    return SetError(kFailedPrecondition, "empty IVF-PQ index");
+  if (x->nlist == 0) {  // an empty segment's index returns nothing (ivf_pq.cc:172)
+    VDBG_HIP(hipMemsetAsync(out_ids, 0xff, nq * k * 4, s));
+    std::vector<float> inf(nq * k, __builtin_inff());
+    VDBG_HIP(hipMemcpyAsync(out_d, inf.data(), nq * k * 4, hipMemcpyHostToDevice, s));
+    if (dc_dev) VDBG_HIP(hipMemsetAsync(dc_dev, 0, nq * 8, s));
+    return hipStreamSynchronize(s) == hipSuccess ? kOk : SetError(kInternal, "sync");
   }
   const size_t nprobe = std::clamp<size_t>(nprobe_req, 1, size_t(x->nlist));
   const size_t depth = rerank < 0 ? std::max<size_t>(10 * k, 100) : size_t(rerank);

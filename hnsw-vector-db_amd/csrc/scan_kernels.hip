@@ -1110,7 +1110,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   }
   const uint32_t N = src->N;
   const size_t pd = src->pd;
-  const bool gemm = GemmSupported(pd) && N >= 8192 && nq >= 32;
+  const bool gemm = GemmSupported(pd) && N >= 1024 && nq >= 32;
   if (!gemm) return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
   VDBG_RETURN_IF_ERROR(BuildSample(c, src, s));
 

@@ -68,6 +68,10 @@ _SIGS = {
                                        C.POINTER(C.c_uint64)]),
     "vdbg_sq8_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
     "vdbg_ivfpq_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
+    "vdbg_ivfpq_build": (C.c_int, [_vp, _sz, _sz, C.c_uint64, _sz, _sz, C.POINTER(_vp)]),
+    "vdbg_kmeans": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, _sz, C.c_uint64, _sz, C.c_int, _vp,
+                              C.POINTER(C.c_double), C.POINTER(_sz)]),
+    "vdbg_assign_nearest": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _sz, _vp, _vp]),
     "vdbg_ivfpq_save": (C.c_int, [_vp, _vp, _sz, C.POINTER(_sz)]),
     "vdbg_ivfpq_destroy": (C.c_int, [_vp]),
     "vdbg_ivfpq_info": (C.c_int, [_vp, C.POINTER(_sz), C.POINTER(_sz), C.POINTER(C.c_int)]),
@@ -274,6 +278,14 @@ class IvfPqIndex:
         _check(lib.vdbg_ivfpq_load(ds.h, blob, len(blob), C.byref(h)))
         return cls(ds, h)
 
+    @classmethod
+    def build(cls, ds, nlist, m, seed=42, max_points=256, iters=25):
+        """IvfPqIndex::build on the GPU (IndexOptions nlist, pq_m, seed,
+        max_train_points_per_centroid; k-means iterations)."""
+        h = _vp()
+        _check(lib.vdbg_ivfpq_build(ds.h, nlist, m, seed, max_points, iters, C.byref(h)))
+        return cls(ds, h)
+
     def close(self):
         if self.h:
             lib.vdbg_ivfpq_destroy(self.h)
@@ -319,3 +331,28 @@ class IvfPqIndex:
                       dc_ptr=None, stream=None):
         _check(lib.vdbg_ivfpq_search_device(self.h, q_ptr, nq, k, nprobe, rerank, allow_ptr,
                                             ids_ptr, dists_ptr, dc_ptr, stream))
+
+
+def kmeans(ctx, data, k, iters=25, seed=1234, max_points=256, kmeanspp=True, d=None):
+    """KMeans over host rows (n x stride); returns (centroids k x d, inertia, reseeds)."""
+    data = np.ascontiguousarray(data, np.float32)
+    n, stride = data.shape
+    d = stride if d is None else d
+    cen = np.empty((k, d), np.float32)
+    inertia = C.c_double()
+    reseeds = _sz()
+    _check(lib.vdbg_kmeans(ctx.h, _ptr(data), n, d, stride, k, iters, seed, max_points,
+                           1 if kmeanspp else 0, _ptr(cen), C.byref(inertia), C.byref(reseeds)))
+    return cen, inertia.value, reseeds.value
+
+
+def assign_nearest(ctx, data, centroids, d=None):
+    data = np.ascontiguousarray(data, np.float32)
+    centroids = np.ascontiguousarray(centroids, np.float32)
+    n, stride = data.shape
+    d = stride if d is None else d
+    assign = np.empty(n, np.uint32)
+    dist = np.empty(n, np.float32)
+    _check(lib.vdbg_assign_nearest(ctx.h, _ptr(data), n, d, stride, _ptr(centroids),
+                                   centroids.shape[0], _ptr(assign), _ptr(dist)))
+    return assign, dist

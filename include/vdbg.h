@@ -154,6 +154,14 @@ int vdbg_ivfpq_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_ivfpq**
  * VDBIVFP1 file into buf (cap bytes); *len receives its size (buf may be NULL to ask). */
 int vdbg_ivfpq_save(vdbg_ivfpq* ix, void* buf, size_t cap, size_t* len);
 int vdbg_ivfpq_destroy(vdbg_ivfpq* ix);
+/* IvfPqIndex::build (src/index/quant/ivf_pq.cc:102-149) on the GPU over the dataset's rows:
+ * nlist clamped to [1, n/39], KMeans of the padded rows (kmeans_iters Lloyd steps; the
+ * reference uses 25), AssignNearest, PQ training on residuals of a strided <= 65,536-row
+ * sample (seed + j * 7919 per subspace, pq.cc:14-41), residual encoding, lists with ids
+ * ascending, precomputed tables.  The seeded draws follow the reference's
+ * std::mt19937_64 sequence, so the index equals the reference's (with kmeans_iters = 25). */
+int vdbg_ivfpq_build(vdbg_dataset* ds, size_t nlist, size_t pq_m, uint64_t seed,
+                     size_t max_train_points_per_centroid, size_t kmeans_iters, vdbg_ivfpq** out);
 /* nlist, m and whether precomputed tables are in use (IvfPqIndex::nlist,
  * precomputed_tables, ivf_pq.h:55-57). */
 int vdbg_ivfpq_info(vdbg_ivfpq* ix, size_t* nlist, size_t* m, int* precomputed_tables);
@@ -172,6 +180,19 @@ int vdbg_ivfpq_search_device(vdbg_ivfpq* ix, const float* queries, size_t nq, si
                              size_t nprobe, int rerank, const uint64_t* allow_words,
                              uint32_t* out_ids, float* out_dists, uint64_t* dist_comps,
                              void* stream);
+
+/* ---------------------------------------------------------------- k-means */
+
+/* KMeans (src/index/quant/kmeans.cc:57-174, options kmeans.h:13-20) with the assignment
+ * steps on the GPU: n rows of d floats at `stride` (host), k centroids written to
+ * centroids_out (k x d, host).  inertia / empty_reseeds (nullable) as KMeansStats. */
+int vdbg_kmeans(vdbg_ctx* ctx, const float* data, size_t n, size_t d, size_t stride, size_t k,
+                size_t iters, uint64_t seed, size_t max_points_per_centroid, int kmeanspp,
+                float* centroids_out, double* inertia, size_t* empty_reseeds);
+/* AssignNearest (kmeans.cc:23-55): the first nearest centroid of every row (padded rows use
+ * the AVX-512-order kernel, others L2SqAny), and its distance (dist nullable). */
+int vdbg_assign_nearest(vdbg_ctx* ctx, const float* data, size_t n, size_t d, size_t stride,
+                        const float* centroids, size_t k, uint32_t* assign, float* dist);
 
 /* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
  * candidates could not be certified and were re-scanned exactly. */
