@@ -1,14 +1,19 @@
-"""Benchmark: batch QPS of vdb's flat exact search on one MI355X.
+"""Benchmark: batch QPS of vdb's nearest-neighbour scans on one MI355X.
 
-Workload (one "step" = one batch search over resident data): flat exact L2 over 1M x 128
-fp32 SIFT-like rows (integer values in [0, 255] from a 1,000-centre mixture), a batch of
-10,000 queries from the same mixture, k = 10.  Rows, norms and queries are resident in HBM
-before the timed region; the step is the full search (sample pre-pass, MFMA GEMM + filter,
-selection, exact re-scoring and any exact re-scan).
-
-Printed: one JSON line with the metric, the MFMA roofline of the dominant kernel (GEMM time
-from HIP events on the stream it runs on) and the reference's CPU FlatIndex timed on a
-bounded query sample on this host's cores.
+Workload (one "step" = one batch search over data resident in HBM):
+  flat    exact L2 over 1M x 128 fp32 SIFT-like rows (integer values in [0, 255] from a
+          1,000-centre mixture), 10,000 queries from the same mixture, k = 10.  This is the
+          headline line (`value`).
+  sq8     the same rows as SQ8 codes (trained on all rows), top-100 by SQ8 distance, fp32
+          rerank to k = 10.
+  ivfpq   IVF-PQ over the same rows, nlist 4,096 (k-means 20 iterations, seed 42), m = 16,
+          nprobe 64, rerank 100 -> k = 10; built on the GPU.
+Queries, rows, codes and lists are resident before the timed region.  Each path's dominant
+kernel is timed with HIP events on the stream it runs on; its roofline fraction uses the
+algorithmic work (MFMA flops for the GEMM scans, code + id bytes for the IVF list scan).
+Next to each, the reference's own CPU code (oracle/_ref, or the oracle's restatement where
+that is not built) is timed on a bounded query sample on this host's cores, and the GPU
+results on that sample are compared with it.
 """
 import argparse
 import json
@@ -24,38 +29,30 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 
 METRIC = "batch QPS at k=10 (flat/SQ8/IVF-PQ, 1M×128); achieved HBM TB/s / MFMA %"
 FP32_MFMA_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(base, queries, k, sample_q, threads):
-    """The reference's FlatIndex (oracle/_ref) or, where it is not built, the oracle's
-    restatement, over `sample_q` queries fanned over `threads` host threads."""
-    from oracle_lib import load_oracle, load_reference
-
-    qs = np.ascontiguousarray(queries[:sample_q])
-    ref = load_reference()
-    od = np.empty((sample_q, k), np.float32)
-    oi = np.empty((sample_q, k), np.uint32)
-    if ref is not None:
-        kind = "reference"
-        t0 = time.perf_counter()
-        ref.lib.ref_flat_index_batch(0, base, base.shape[0], base.shape[1], base.shape[1], qs,
-                                     sample_q, k, od, oi, threads)
-        dt = time.perf_counter() - t0
-        kernels = ref.lib.ref_best_kernels().decode()
-    else:
-        kind = "port"
-        o = load_oracle()
-        t0 = time.perf_counter()
-        od, oi = o.flat_search(base, qs, k, threads=threads)
-        dt = time.perf_counter() - t0
-        kernels = "avx512-order emulation"
-    return {"value": sample_q / dt, "unit": "queries/s", "cores": threads, "kind": kind,
-            "sample": f"{sample_q} of the batch's queries, FlatIndex::search per query over "
-                      f"all {base.shape[0]} rows, {kernels} kernels, {dt:.1f} s"}, oi, od
+def timed(ctx, torch, fn, steps, warmup, kernels):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    ctx.profile(True)
+    ctx.profile_reset()
+    fallbacks = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+        fallbacks += ctx.last_fallbacks()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    prof = {k: ctx.profile_get(k) for k in kernels}
+    ctx.profile(False)
+    return elapsed, prof, fallbacks
 
 
 def main():
@@ -66,11 +63,14 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--k", type=int, default=10)
-    ap.add_argument("--cpu-sample", type=int, default=6400)
+    ap.add_argument("--paths", default="flat,sq8,ivfpq")
+    ap.add_argument("--nprobe", type=int, default=64)
+    ap.add_argument("--cpu-sample", type=int, default=6400,
+                    help="queries in the flat CPU-baseline sample (SQ8 uses half, IVF-PQ all)")
+    ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times); used "
                          "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
-    ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every box "
@@ -93,87 +93,199 @@ def main():
     import vdbg
     from vdbg import datagen
 
-    dim = 128
-    k = args.k
-    log(f"generating sift-like base {args.n}x{dim} and {args.nq} queries")
-    base = datagen.sift_like(args.n, dim, 2002)
-    queries = datagen.sift_like(args.nq, dim, 2003)
+    paths = set(args.paths.split(","))
+    dim, k, nq, N = 128, args.k, args.nq, args.n
+    threads = min(16, os.cpu_count() or 1)
+    log(f"generating sift-like base {N}x{dim} and {nq} queries")
+    base = datagen.sift_like(N, dim, 2002)
+    queries = datagen.sift_like(nq, dim, 2003)
+
+    ref = oracle = None
+    if not args.no_cpu:
+        from oracle_lib import load_oracle, load_reference
+        ref = load_reference()
+        oracle = load_oracle()
 
     ctx = vdbg.Context(0)
     ds = vdbg.Dataset(ctx, base, dim)
     dev = torch.device("cuda:0")
     q_dev = torch.from_numpy(queries).to(dev)
-    ids_dev = torch.empty((args.nq, k), dtype=torch.int32, device=dev)
-    d_dev = torch.empty((args.nq, k), dtype=torch.float32, device=dev)
+    ids_dev = torch.empty((nq, k), dtype=torch.int32, device=dev)
+    d_dev = torch.empty((nq, k), dtype=torch.float32, device=dev)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream().cuda_stream
 
-    def step():
-        ds.flat_search_device(q_dev.data_ptr(), args.nq, k, ids_dev.data_ptr(),
-                              d_dev.data_ptr(), stream=stream)
+    def gpu_out():
+        return ids_dev.cpu().numpy().view(np.uint32).copy(), d_dev.cpu().numpy().copy()
 
-    for i in range(args.warmup):
-        step()
-        log(f"warmup step {i + 1}/{args.warmup} done")
-    torch.cuda.synchronize()
-    ctx.profile(True)
-    ctx.profile_reset()
-    fallbacks = 0
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        step()
-        fallbacks += ctx.last_fallbacks()
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    log(f"timed {args.steps} steps in {elapsed:.3f} s")
-    gemm_ms, gemm_n = ctx.profile_get("flat_gemm")
-    kernel_ms = {name: ctx.profile_get(name)[0] / max(1, args.steps)
-                 for name in ("query_prep", "sample_gemm", "kth", "flat_gemm", "select", "exact_scan",
-                              "merge")}
-    ctx.profile(False)
+    def parity(gi, gd, oi, od):
+        s = len(oi)
+        return bool(np.array_equal(gi[:s], oi) and
+                    np.array_equal(gd[:s].view(np.uint32), od.view(np.uint32)))
 
-    ms_per_step = elapsed * 1000.0 / args.steps
-    qps = args.nq * args.steps / elapsed
-    flops = 2.0 * args.nq * args.n * dim
-    gemm_avg_ms = gemm_ms / max(1, gemm_n)
-    achieved = flops / (gemm_avg_ms * 1e-3) / 1e12
+    results = {}
 
-    ids = ids_dev.cpu().numpy().view(np.uint32)
-    dists = d_dev.cpu().numpy()
+    # ------------------------------------------------------------ flat
+    if "flat" in paths:
+        def step():
+            ds.flat_search_device(q_dev.data_ptr(), nq, k, ids_dev.data_ptr(), d_dev.data_ptr(),
+                                  stream=stream)
 
-    cpu = None
-    parity = None
-    if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        cpu, oi, od = cpu_baseline(base, queries, k, args.cpu_sample, threads)
-        parity = bool(np.array_equal(ids[:args.cpu_sample], oi) and
-                      np.array_equal(dists[:args.cpu_sample].view(np.uint32), od.view(np.uint32)))
-        log(f"cpu baseline: {cpu['value']:.1f} q/s ({cpu['kind']}), parity on sample: {parity}")
+        el, prof, fb = timed(ctx, torch, step, args.steps, args.warmup,
+                             ["query_prep", "sample_gemm", "kth", "flat_gemm", "select",
+                              "exact_scan", "merge"])
+        gi, gd = gpu_out()
+        g_ms = prof["flat_gemm"][0] / max(1, prof["flat_gemm"][1])
+        tflops = 2.0 * nq * N * dim / (g_ms * 1e-3) / 1e12
+        r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
+             "kernel": "k_gemm<128,L2,rows,filter>", "kernel_ms": g_ms, "achieved": tflops,
+             "unit": "TFLOP/s", "peak": FP32_MFMA_PEAK_TFLOPS, "bound": "mfma",
+             "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
+             "exact_rescans": fb}
+        log(f"flat: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} TFLOP/s")
+        if not args.no_cpu:
+            s = min(args.cpu_sample, nq)
+            qs = np.ascontiguousarray(queries[:s])
+            od = np.empty((s, k), np.float32)
+            oi = np.empty((s, k), np.uint32)
+            t0 = time.perf_counter()
+            if ref is not None:
+                ref.lib.ref_flat_index_batch(0, base, N, dim, dim, qs, s, k, od, oi, threads)
+                kind, kern = "reference", ref.lib.ref_best_kernels().decode()
+            else:
+                od, oi = oracle.flat_search(base, qs, k, threads=threads)
+                kind, kern = "port", "avx512-order restatement"
+            dt = time.perf_counter() - t0
+            r["cpu_baseline"] = {
+                "value": s / dt, "unit": "queries/s", "cores": threads, "kind": kind,
+                "sample": f"{s} of the {nq} queries, FlatIndex::search per query over all {N} "
+                          f"rows ({kern} kernels), queries over {threads} threads, {dt:.1f} s"}
+            r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
+            log(f"flat cpu: {s / dt:.1f} q/s ({kind}), parity {r['parity_on_cpu_sample']}")
+        results["flat"] = r
 
+    # ------------------------------------------------------------ SQ8
+    if "sq8" in paths:
+        depth = 100
+        sq = vdbg.Sq8Index(ds)
+
+        def step():
+            sq.search_device(q_dev.data_ptr(), nq, k, depth, ids_dev.data_ptr(),
+                             d_dev.data_ptr(), stream=stream)
+
+        el, prof, fb = timed(ctx, torch, step, args.steps, args.warmup,
+                             ["query_prep", "sample_gemm", "kth", "sq8_gemm", "select",
+                              "rerank", "exact_scan", "merge"])
+        gi, gd = gpu_out()
+        g_ms = prof["sq8_gemm"][0] / max(1, prof["sq8_gemm"][1])
+        tflops = 2.0 * nq * N * dim / (g_ms * 1e-3) / 1e12
+        r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
+             "kernel": "k_gemm<128,L2,codes,filter>", "kernel_ms": g_ms, "achieved": tflops,
+             "unit": "TFLOP/s", "peak": FP32_MFMA_PEAK_TFLOPS, "bound": "mfma",
+             "code_stream_TBps": nq * N * dim / (g_ms * 1e-3) / 1e12,
+             "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
+             "exact_rescans": fb, "depth": depth}
+        log(f"sq8: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} TFLOP/s")
+        if not args.no_cpu:
+            s = min(args.cpu_sample // 2, nq)
+            qs = np.ascontiguousarray(queries[:s])
+            codes = sq.codes()
+            od = np.empty((s, k), np.float32)
+            oi = np.empty((s, k), np.uint32)
+            t0 = time.perf_counter()
+            if ref is not None:
+                ref.lib.ref_sq8_search_batch(b"", 0, base, codes, N, dim, dim, sq.vmin, sq.scale,
+                                             qs, s, k, depth, od, oi, threads)
+                kind = "reference"
+            else:
+                od, oi = oracle.sq8_search(base, codes, sq.vmin, sq.scale, qs, k, depth,
+                                           threads=threads)
+                kind = "port"
+            dt = time.perf_counter() - t0
+            r["cpu_baseline"] = {
+                "value": s / dt, "unit": "queries/s", "cores": threads, "kind": kind,
+                "sample": f"{s} queries: SQ8 scan of all {N} codes into top-{depth} + fp32 "
+                          f"Rerank, {threads} threads, {dt:.1f} s"}
+            r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
+            log(f"sq8 cpu: {s / dt:.1f} q/s ({kind}), parity {r['parity_on_cpu_sample']}")
+        sq.close()
+        results["sq8"] = r
+
+    # ------------------------------------------------------------ IVF-PQ
+    if "ivfpq" in paths:
+        nlist, m, rerank, nprobe = 4096, 16, 100, args.nprobe
+        t0 = time.perf_counter()
+        ix = vdbg.IvfPqIndex.build(ds, nlist=nlist, m=m, seed=42, max_points=256, iters=20)
+        build_s = time.perf_counter() - t0
+        log(f"ivfpq: built nlist={nlist} m={m} in {build_s:.1f} s")
+        dc_dev = torch.empty(nq, dtype=torch.int64, device=dev)
+        # codes scanned per query (rerank 0: dist_comps = nlist + codes scanned)
+        ix.search_device(q_dev.data_ptr(), nq, k, nprobe, 0, ids_dev.data_ptr(),
+                         d_dev.data_ptr(), dc_ptr=dc_dev.data_ptr(), stream=stream)
+        torch.cuda.synchronize()
+        scanned = int(dc_dev.cpu().numpy().sum()) - nq * nlist
+
+        def step():
+            ix.search_device(q_dev.data_ptr(), nq, k, nprobe, rerank, ids_dev.data_ptr(),
+                             d_dev.data_ptr(), stream=stream)
+
+        el, prof, _ = timed(ctx, torch, step, args.steps, args.warmup,
+                            ["query_prep", "sample_gemm", "kth", "flat_gemm", "select",
+                             "exact_scan", "merge", "ivf_qtab", "ivf_scan", "rerank"])
+        gi, gd = gpu_out()
+        s_ms = prof["ivf_scan"][0] / max(1, prof["ivf_scan"][1])
+        gbs = scanned * (m + 4) / (s_ms * 1e-3) / 1e9
+        r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
+             "kernel": "k_ivf_scan", "kernel_ms": s_ms, "achieved": gbs, "unit": "GB/s",
+             "peak": HBM_PEAK_GBS, "bound": "hbm", "codes_scanned_per_query": scanned / nq,
+             "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
+             "nlist": nlist, "m": m, "nprobe": nprobe, "rerank": rerank,
+             "kmeans_iters": 20, "build_s": build_s}
+        log(f"ivfpq: {r['qps']:.0f} q/s, scan {s_ms:.3f} ms = {gbs:.0f} GB/s")
+        if not args.no_cpu and ref is not None:
+            blob = ix.save()
+            s = nq
+            qs = np.ascontiguousarray(queries[:s])
+            od = np.empty((s, k), np.float32)
+            oi = np.empty((s, k), np.uint32)
+            t0 = time.perf_counter()
+            rc = ref.lib.ref_ivfpq_search_batch(0, blob, len(blob), base, N, dim, dim, qs, s, k,
+                                                nprobe, rerank, None, od, oi, None, threads)
+            dt = time.perf_counter() - t0
+            if rc == 0:
+                r["cpu_baseline"] = {
+                    "value": s / dt, "unit": "queries/s", "cores": threads, "kind": "reference",
+                    "sample": f"all {s} queries, IvfPqIndex::search (nprobe {nprobe}, rerank "
+                              f"{rerank}) on the same index file, {threads} threads, {dt:.1f} s"}
+                r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
+                log(f"ivfpq cpu: {s / dt:.1f} q/s, parity {r['parity_on_cpu_sample']}")
+        ix.close()
+        results["ivfpq"] = r
+
+    head = results.get("flat") or next(iter(results.values()))
     out = {
         "metric": METRIC,
-        "value": round(qps, 1),
+        "value": round(head["qps"], 1),
         "unit": "queries/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 3),
+        "ms_per_step": round(head["ms_per_step"], 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic (seeded SIFT-like mixture, resident in HBM)",
-        "config": {"workload": f"flat_l2_sift_like_{args.n}x{dim}_k{k}_batch{args.nq}",
-                   "n": args.n, "dim": dim, "k": k, "batch": args.nq, "metric": "l2"},
-        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
-                     "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "k_flat_gemm<128,L2>", "kernel_ms": round(gemm_avg_ms, 3)},
-        "cpu_baseline": cpu,
-        "kernel_ms_per_step": {k_: round(v, 3) for k_, v in kernel_ms.items()},
-        "exact_rescans": fallbacks,
-        "parity_on_cpu_sample": parity,
+        "config": {"workload": f"flat_l2_sift_like_{N}x{dim}_k{k}_batch{nq}", "n": N,
+                   "dim": dim, "k": k, "batch": nq, "metric": "l2"},
+        "roofline": {"bound": head["bound"], "achieved": round(head["achieved"], 2),
+                     "peak": head["peak"], "unit": head["unit"],
+                     "frac": round(head["achieved"] / head["peak"], 4), "traffic": None,
+                     "kernel": head["kernel"], "kernel_ms": round(head["kernel_ms"], 3)},
+        "cpu_baseline": head.get("cpu_baseline"),
+        "parity_on_cpu_sample": head.get("parity_on_cpu_sample"),
+        "paths": {name: {kk: (round(v, 4) if isinstance(v, float) else v)
+                         for kk, v in r.items()} for name, r in results.items()},
     }
     print(json.dumps(out), flush=True)
 
