@@ -10,6 +10,8 @@
 //   DotAny / L2SqAny  (src/distance/scalar.cc:43-73) four accumulators over i mod 4,
 //                     (s0 + s1) + (s2 + s3), products rounded before the add;
 //   adc               (src/index/quant/pq.h:36-46) four accumulators over j mod 4.
+#include <hipcub/hipcub.hpp>
+
 #include <algorithm>
 #include <cstring>
 
@@ -244,6 +246,210 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
   }
 }
 
+// Per-(query, list) offsets for inner product and cosine: -DotAny(q, c_l, d) over the real
+// dims (ivf_pq.cc:209).  One thread per (query, probe).
+__global__ void k_ivf_offsets(const float* __restrict__ Q, int pd, int dim,
+                              const float* __restrict__ coarse, const uint32_t* __restrict__ probe,
+                              int nprobe, int nq, float* __restrict__ offs) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(nq) * nprobe) return;
+  const size_t q = t / nprobe;
+  offs[t] = -dot_any(Q + q * pd, coarse + size_t(probe[t]) * pd, dim);
+}
+
+__global__ void k_first_probe(const uint32_t* __restrict__ probe, int nprobe, int nq,
+                              uint32_t* __restrict__ key, uint32_t* __restrict__ val) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  key[q] = probe[size_t(q) * nprobe];
+  val[q] = uint32_t(q);
+}
+
+struct IvfFastArgs {
+  const uint32_t* qorder;  // queries sorted by nearest list (nullable)
+  const float* offs;       // [nq][nprobe] offsets when there are no precomputed tables
+  int items, per_xcd;
+};
+
+template <int M>
+__device__ __forceinline__ void load_code(const uint8_t* codes, uint32_t i, uint32_t (&w)[(M + 3) / 4]) {
+  if constexpr (M == 16) {
+    const uint4 v = reinterpret_cast<const uint4*>(codes)[i];
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else if constexpr (M == 8) {
+    const uint2 v = reinterpret_cast<const uint2*>(codes)[i];
+    w[0] = v.x; w[1] = v.y;
+  } else if constexpr (M == 4) {
+    w[0] = reinterpret_cast<const uint32_t*>(codes)[i];
+  } else {
+#pragma unroll
+    for (int t = 0; t < (M + 3) / 4; ++t) w[t] = 0;
+#pragma unroll
+    for (int j = 0; j < M; ++j) w[j >> 2] |= uint32_t(codes[size_t(i) * M + j]) << (8 * (j & 3));
+  }
+}
+
+// The list scan for tables that fit in registers (m <= 16, precomputed L2 tables or the
+// shared inner-product table).  One wave per query; queries run in nearest-list order and
+// consecutive ones land on one XCD, so the per-list tables they share stay in that XCD's
+// L2.  The query's 2 * (-<q_j, C>) table lives in VGPRs for the whole query; while list p
+// is scanned, list p+1's term2 slice is already in flight into VGPRs, and the list table
+// fl(term2 + qtab) (the reference's table[i]) is written to LDS per list.  Codes are read
+// CH per lane at a time; ADC follows pq.h:36-46.
+template <int E, int M>
+__global__ __launch_bounds__(kIvfWaves * 64, 2) void k_ivf_scan_fast(IvfScanArgs a, IvfFastArgs f) {
+  constexpr int TS = M * kKsub;
+  constexpr int V = M;  // float4 per lane: TS / 4 / 64
+  constexpr int CH = 4;
+  constexpr int W = (M + 3) / 4;
+  extern __shared__ float lds[];
+  const int b = blockIdx.x;
+  const int item = (b & 7) * f.per_xcd + (b >> 3);
+  if (item >= f.items) return;
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int slot = item * kIvfWaves + wave;
+  if (slot >= a.nq) return;
+  const uint32_t q = f.qorder ? f.qorder[slot] : uint32_t(slot);
+  float* table = lds + size_t(wave) * (TS + 4 * kWave);
+  float* st_d = table + TS;
+  uint32_t* st_i = reinterpret_cast<uint32_t*>(st_d + 2 * kWave);
+  float4* table4 = reinterpret_cast<float4*>(table);
+  const bool pre = a.term2 != nullptr;
+  const uint32_t* probe = a.probe + size_t(q) * a.nprobe;
+
+  float4 QT[V], T2[V];
+  {
+    const float4* qt4 = reinterpret_cast<const float4*>(a.qtab + size_t(q) * TS);
+#pragma unroll
+    for (int i = 0; i < V; ++i) QT[i] = qt4[i * kWave + lane];
+  }
+  if (pre) {
+    const float4* t4 = reinterpret_cast<const float4*>(a.term2 + size_t(probe[0]) * TS);
+#pragma unroll
+    for (int i = 0; i < V; ++i) T2[i] = t4[i * kWave + lane];
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) table4[i * kWave + lane] = QT[i];
+  }
+
+  WaveTopK<E> top;
+  top.init();
+  int staged = 0;
+  uint64_t scanned = 0;
+  auto push = [&](float d, uint32_t id, bool valid) {
+    float td;
+    uint32_t ti;
+    top.threshold(td, ti);
+    const bool want = valid && nb_less(d, id, td, ti);
+    const uint64_t bal = __ballot(want);
+    if (bal == 0) return;
+    const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
+    if (want) {
+      st_d[pos] = d;
+      st_i[pos] = id;
+    }
+    staged += __popcll(bal);
+    if (staged >= kWave) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float sd = st_d[lane];
+      const uint32_t si = st_i[lane];
+      const bool more = lane + kWave < staged;
+      const float rd = more ? st_d[lane + kWave] : 0.f;
+      const uint32_t ri = more ? st_i[lane + kWave] : 0u;
+      __builtin_amdgcn_wave_barrier();
+      if (more) {
+        st_d[lane] = rd;
+        st_i[lane] = ri;
+      }
+      staged -= kWave;
+      top.insert(sd, si);
+    }
+  };
+
+  for (int pi = 0; pi < a.nprobe; ++pi) {
+    const uint32_t l = probe[pi];
+    const float offset = pre ? a.probe_d[size_t(q) * a.nprobe + pi] : f.offs[size_t(q) * a.nprobe + pi];
+    if (pre) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int i = 0; i < V; ++i)
+        table4[i * kWave + lane] = make_float4(T2[i].x + QT[i].x, T2[i].y + QT[i].y,
+                                               T2[i].z + QT[i].z, T2[i].w + QT[i].w);
+      if (pi + 1 < a.nprobe) {
+        const float4* t4 = reinterpret_cast<const float4*>(a.term2 + size_t(probe[pi + 1]) * TS);
+#pragma unroll
+        for (int i = 0; i < V; ++i) T2[i] = t4[i * kWave + lane];
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const uint32_t b0 = a.off[l], e0 = a.off[l + 1];
+    scanned += e0 - b0;
+    for (uint32_t c0 = b0; c0 < e0; c0 += CH * kWave) {
+      uint32_t w[CH][W];
+      uint32_t id[CH];
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        const uint32_t i = c0 + t * kWave + lane;
+        id[t] = kNoId;
+        if (i < e0) {
+          load_code<M>(a.codes, i, w[t]);
+          id[t] = a.ids[i];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        const bool valid = id[t] != kNoId && row_ok(a.allow, id[t]);
+        float d = __builtin_inff();
+        if (valid) {
+          float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+          for (int j = 0; j + 4 <= M; j += 4) {
+            const uint32_t x = w[t][j >> 2];
+            s0 += table[(j + 0) * kKsub + (x & 0xffu)];
+            s1 += table[(j + 1) * kKsub + ((x >> 8) & 0xffu)];
+            s2 += table[(j + 2) * kKsub + ((x >> 16) & 0xffu)];
+            s3 += table[(j + 3) * kKsub + (x >> 24)];
+          }
+#pragma unroll
+          for (int j = (M / 4) * 4; j < M; ++j)
+            s0 += table[j * kKsub + ((w[t][j >> 2] >> (8 * (j & 3))) & 0xffu)];
+          d = offset + ((s0 + s1) + (s2 + s3));
+        }
+        if (__ballot(id[t] != kNoId) == 0) break;
+        push(d, id[t], valid);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (staged > 0) {
+    const bool have = lane < staged;
+    top.insert(have ? st_d[lane] : __builtin_inff(), have ? st_i[lane] : kNoId);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int gi = e * kWave + lane;
+    if (gi < a.R) {
+      a.out_ids[size_t(q) * a.R + gi] = top.k.id[e];
+      a.out_d[size_t(q) * a.R + gi] = top.k.d[e];
+    }
+  }
+  if (a.dc != nullptr) {
+    uint64_t valid = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      valid += __popcll(__ballot(top.k.id[e] != kNoId && e * kWave + lane < a.R));
+    if (lane == 0) a.dc[q] = a.dc_base + scanned + (a.count_top ? valid : 0);
+  }
+}
+
 // ProductQuantizer::encode (pq.cc:43-57) of the residual x - coarse[assign] (ivf_pq.cc:
 // 128-139): per subspace the first centroid with the smallest L2SqAny.  One thread per
 // (row, subspace).
@@ -298,12 +504,71 @@ static void launch_ivf(hipStream_t s, const IvfScanArgs& a, size_t lds) {
   k_ivf_scan<E><<<dim3((a.nq + kIvfWaves - 1) / kIvfWaves), kIvfWaves * 64, lds, s>>>(a);
 }
 
+template <int E, int M>
+static void launch_fast(hipStream_t s, const IvfScanArgs& a, const IvfFastArgs& f, size_t lds) {
+  k_ivf_scan_fast<E, M><<<dim3(f.per_xcd * 8), kIvfWaves * 64, lds, s>>>(a, f);
+}
+
+template <int M>
+static int launch_fast_m(int e, hipStream_t s, const IvfScanArgs& a, const IvfFastArgs& f) {
+  const size_t lds = size_t(kIvfWaves) * (M * kKsub + 4 * kWave) * sizeof(float);
+  switch (e) {
+    case 1: launch_fast<1, M>(s, a, f, lds); break;
+    case 2: launch_fast<2, M>(s, a, f, lds); break;
+    case 4: launch_fast<4, M>(s, a, f, lds); break;
+    default: return SetError(kNotSupported, "IVF-PQ: max(rerank, k) > 256 on the GPU path");
+  }
+  return kOk;
+}
+
 int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
   if (a.nq == 0) return kOk;
   if (a.m * kKsub > kMaxTable || a.dsub > 64)
     return SetError(kNotSupported, "IVF-PQ scan: m <= 32 and dim/m <= 64 on the GPU path");
   int e = 1;
   while (kWave * e < a.R) e <<= 1;
+  const bool l2 = a.metric == 0;
+  const bool fast_ok = (a.m == 4 || a.m == 8 || a.m == 16) && (!l2 || a.term2 != nullptr);
+  if (fast_ok) {
+    // queries in nearest-list order; offsets for the inner-product table
+    void* buf = nullptr;
+    const size_t nq = size_t(a.nq);
+    VDBG_HIP(hipMallocAsync(&buf, nq * 16 + nq * a.nprobe * 4 + 4096, s));
+    uint32_t* key = static_cast<uint32_t*>(buf);
+    uint32_t* val = key + nq;
+    uint32_t* key2 = val + nq;
+    uint32_t* order = key2 + nq;
+    float* offs = reinterpret_cast<float*>(order + nq);
+    k_first_probe<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, key, val);
+    VDBG_HIP(hipGetLastError());
+    size_t tmp_bytes = 0;
+    VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, key2, val, order, a.nq, 0,
+                                                32, s));
+    void* tmp = nullptr;
+    VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
+    VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, key2, val, order, a.nq, 0, 32, s));
+    if (!l2) {
+      k_ivf_offsets<<<dim3(unsigned((nq * a.nprobe + 255) / 256)), 256, 0, s>>>(
+          a.Q, a.pd, a.dim, a.coarse, a.probe, a.nprobe, a.nq, offs);
+      VDBG_HIP(hipGetLastError());
+    }
+    IvfFastArgs f{order, l2 ? nullptr : offs, 0, 0};
+    f.items = (a.nq + kIvfWaves - 1) / kIvfWaves;
+    f.per_xcd = (f.items + 7) / 8;
+    int rc = kOk;
+    {
+      ProfScope ps(c, "ivf_scan", s);
+      switch (a.m) {
+        case 4: rc = launch_fast_m<4>(e, s, a, f); break;
+        case 8: rc = launch_fast_m<8>(e, s, a, f); break;
+        default: rc = launch_fast_m<16>(e, s, a, f); break;
+      }
+      if (rc == kOk && hipGetLastError() != hipSuccess) rc = SetError(kInternal, "ivf scan launch");
+    }
+    (void)hipFreeAsync(tmp, s);
+    (void)hipFreeAsync(buf, s);
+    return rc;
+  }
   const size_t lds = size_t(kIvfWaves) * (a.m * kKsub + 4 * kWave) * sizeof(float);
   ProfScope ps(c, "ivf_scan", s);
   switch (e) {
