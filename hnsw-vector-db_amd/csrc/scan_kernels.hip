@@ -448,22 +448,31 @@ struct GemmArgs {
 
 constexpr int kGemmRows = 64;  // rows per LDS tile (two 32-row MFMA blocks)
 
+__host__ __device__ constexpr int GemmKc(int pd) {
+  return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : (pd % 32 == 0 ? 32 : 16)));
+}
+
 // Block = 4 waves = 128 queries (32 per wave) x one chunk of rows.  Blocks are dispatched
 // round-robin over the 8 XCDs, so block b takes work item (b % 8) * per_xcd + b / 8: the
 // items of one XCD are consecutive and share row chunks in that XCD's L2.
 //
-// Each wave keeps its 32 queries in VGPRs as the MFMA B operand: lane l holds query l % 32,
-// dims [h*PD/2, (h+1)*PD/2) with h = l / 32, so MFMA step t contracts dims t and PD/2 + t
-// (the order is irrelevant: the GEMM value only ranks; exact distances are recomputed).
-// 64-row tiles are double-buffered in LDS and feed the A operand; code rows are widened to
-// fp32 on the way in.  The 32x32 accumulator gives lane l the values of query l % 32 for
-// rows 8*(r/4) + 4*h + (r%4), r = 0..15.
+// Each wave keeps its 32 queries in VGPRs as the MFMA B operand: for a K chunk of KC dims,
+// lane l holds query l % 32, dims [h*KC/2, (h+1)*KC/2) of the chunk with h = l / 32, so MFMA
+// step t contracts dims t and KC/2 + t (the order is irrelevant: the GEMM value only ranks;
+// exact distances are recomputed).  Rows wider than 128 dims are streamed as (tile, chunk)
+// stages and the query fragment is reloaded per chunk.  Stages are double-buffered in LDS
+// and feed the A operand; code rows are widened to fp32 on the way in.  The 32x32
+// accumulator gives lane l the values of query l % 32 for rows 8*(r/4) + 4*h + (r%4).
 template <int PD, int METRIC, int KIND, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
-  constexpr int STR = PD + 4;  // padded LDS row stride (floats)
-  constexpr int HALF = PD / 2;
-  constexpr int VEC_PER_TILE = KIND == 0 ? kGemmRows * PD / 4 : kGemmRows * PD / 16;
+  constexpr int KC = GemmKc(PD);
+  constexpr int NKC = PD / KC;
+  constexpr int STR = KC + 4;  // padded LDS row stride (floats)
+  constexpr int HALF = KC / 2;
+  constexpr int VEC_PER_ROW = KIND == 0 ? KC / 4 : KC / 16;
+  constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
+  static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
   __shared__ __attribute__((aligned(16))) float xs[2][kGemmRows * STR];
   __shared__ float xns[2][kGemmRows];
 
@@ -484,20 +493,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
 
   float qv[HALF];
-  if (q < a.nq) {
-    const float* src = a.Qb + size_t(q) * PD + h * HALF;
+  auto load_q = [&](int kc) {
+    if (q < a.nq) {
+      const float* src = a.Qb + size_t(q) * PD + kc * KC + h * HALF;
 #pragma unroll
-    for (int t = 0; t < HALF; t += 4) {
-      const float4 v = *reinterpret_cast<const float4*>(src + t);
-      qv[t] = v.x;
-      qv[t + 1] = v.y;
-      qv[t + 2] = v.z;
-      qv[t + 3] = v.w;
+      for (int t = 0; t < HALF; t += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(src + t);
+        qv[t] = v.x;
+        qv[t + 1] = v.y;
+        qv[t + 2] = v.z;
+        qv[t + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < HALF; ++t) qv[t] = 0.f;
     }
-  } else {
-#pragma unroll
-    for (int t = 0; t < HALF; ++t) qv[t] = 0.f;
-  }
+  };
+  if (NKC == 1) load_q(0);
   const float T = (MODE == 0 && q < a.nq) ? a.T[q] : -__builtin_inff();
   const size_t seg = (size_t(q) * a.nchunks + chunk) * 2 + h;
   uint2* out = MODE == 0 ? a.cand + seg * size_t(a.caph) : nullptr;
@@ -505,33 +517,34 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
 
   uint4 pre[VEC_PER_THREAD];
   float pre_n = 0.f;
-  auto load_tile = [&](uint32_t base) {
+  // stage (base, kc): rows base..base+63, dims kc*KC..kc*KC+KC-1
+  auto load_stage = [&](uint32_t base, int kc) {
     const uint32_t valid = r_end > base ? min(uint32_t(kGemmRows), r_end - base) : 0u;
-    const uint4* src = KIND == 0
-                           ? reinterpret_cast<const uint4*>(a.X + size_t(base) * PD)
-                           : reinterpret_cast<const uint4*>(a.C + size_t(base) * PD);
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
-      const int row = KIND == 0 ? f / (PD / 4) : f / (PD / 16);
-      if (f < VEC_PER_TILE && uint32_t(row) < valid)
-        pre[i] = src[f];
-      else
+      const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
+      if (f < VEC_PER_TILE && uint32_t(row) < valid) {
+        if (KIND == 0)
+          pre[i] = *reinterpret_cast<const uint4*>(a.X + size_t(base + row) * PD + kc * KC + c * 4);
+        else
+          pre[i] = *reinterpret_cast<const uint4*>(a.C + size_t(base + row) * PD + kc * KC + c * 16);
+      } else {
         pre[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
     }
-    pre_n = (tid < kGemmRows && uint32_t(tid) < valid) ? a.rn[base + tid] : 0.f;
+    if (kc == 0) pre_n = (tid < kGemmRows && uint32_t(tid) < valid) ? a.rn[base + tid] : 0.f;
   };
-  auto store_tile = [&](int buf) {
+  auto store_stage = [&](int buf, int kc, int tile_parity) {
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
       if (f < VEC_PER_TILE) {
+        const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
         if (KIND == 0) {
-          const int row = f / (PD / 4), c4 = f % (PD / 4);
-          *reinterpret_cast<uint4*>(&xs[buf][row * STR + c4 * 4]) = pre[i];
+          *reinterpret_cast<uint4*>(&xs[buf][row * STR + c * 4]) = pre[i];
         } else {
-          const int row = f / (PD / 16), c16 = f % (PD / 16);
-          float* dst = &xs[buf][row * STR + c16 * 16];
+          float* dst = &xs[buf][row * STR + c * 16];
           const uint32_t w[4] = {pre[i].x, pre[i].y, pre[i].z, pre[i].w};
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
@@ -545,93 +558,102 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         }
       }
     }
-    if (tid < kGemmRows) xns[buf][tid] = pre_n;
+    if (kc == 0 && tid < kGemmRows) xns[tile_parity][tid] = pre_n;
   };
 
   if (r_begin < r_end) {
-    load_tile(r_begin);
-    store_tile(0);
+    load_stage(r_begin, 0);
+    store_stage(0, 0, 0);
   }
   __syncthreads();
 
   int buf = 0;
+  int tile_parity = 0;
   for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
-    const uint32_t next = base + kGemmRows;
-    if (next < r_end) load_tile(next);
+    v16f acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+#pragma unroll 1
+    for (int kc = 0; kc < NKC; ++kc) {
+      // prefetch the next stage: the next K chunk of this tile, or chunk 0 of the next tile
+      const bool last_kc = kc + 1 == NKC;
+      const uint32_t nbase = last_kc ? base + kGemmRows : base;
+      const int nkc = last_kc ? 0 : kc + 1;
+      const bool have_next = nbase < r_end;
+      if (have_next) load_stage(nbase, nkc);
+      if (NKC > 1 && wave_live) load_q(kc);
 
-    if (wave_live) {
-      v16f acc0, acc1;
+      if (wave_live) {
+        const float* xa0 = &xs[buf][j * STR + h * HALF];
+        const float* xa1 = xa0 + 32 * STR;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
-      const float* xa0 = &xs[buf][j * STR + h * HALF];
-      const float* xa1 = xa0 + 32 * STR;
-#pragma unroll
-      for (int t = 0; t < HALF; t += 4) {
-        const float4 x0 = *reinterpret_cast<const float4*>(xa0 + t);
-        const float4 x1 = *reinterpret_cast<const float4*>(xa1 + t);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qv[t + 0], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qv[t + 0], acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.y, qv[t + 1], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.y, qv[t + 1], acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.z, qv[t + 2], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.z, qv[t + 2], acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qv[t + 3], acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qv[t + 3], acc1, 0, 0, 0);
+        for (int t = 0; t < HALF; t += 4) {
+          const float4 x0 = *reinterpret_cast<const float4*>(xa0 + t);
+          const float4 x1 = *reinterpret_cast<const float4*>(xa1 + t);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qv[t + 0], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qv[t + 0], acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.y, qv[t + 1], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.y, qv[t + 1], acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.z, qv[t + 2], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.z, qv[t + 2], acc1, 0, 0, 0);
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.w, qv[t + 3], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.w, qv[t + 3], acc1, 0, 0, 0);
+        }
       }
 
-      if (MODE == 0) {
-        // threshold test on all 32 values; the rare passes go to the lane's buffer
-        uint32_t pass = 0;
+      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? tile_parity ^ 1 : tile_parity);
+      __syncthreads();
+      buf ^= 1;
+    }
+    if (wave_live && MODE == 0) {
+      // threshold test on all 32 values; the rare passes go to the lane's buffer
+      uint32_t pass = 0;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const float g = blk == 0 ? acc0[r] : acc1[r];
+          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[tile_parity][rl]) : -g;
+          pass |= (v <= T ? 1u : 0u) << (blk * 16 + r);
+        }
+      if (__ballot(pass != 0) != 0) {
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const float g = blk == 0 ? acc0[r] : acc1[r];
-            const float v = METRIC == 0 ? fmaf(-2.f, g, xns[buf][rl]) : -g;
-            pass |= (v <= T ? 1u : 0u) << (blk * 16 + r);
-          }
-        if (__ballot(pass != 0) != 0) {
-#pragma unroll
-          for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              if (pass & (1u << (blk * 16 + r))) {
-                const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-                const float g = blk == 0 ? acc0[r] : acc1[r];
-                const float v = METRIC == 0 ? fmaf(-2.f, g, xns[buf][rl]) : -g;
-                const uint32_t row = base + rl;
-                if (q < a.nq && row < r_end && row_allowed(a.allow, row)) {
-                  if (cnt < uint32_t(a.caph)) out[cnt] = make_uint2(__float_as_uint(v), row);
-                  ++cnt;
-                }
+            if (pass & (1u << (blk * 16 + r))) {
+              const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+              const float g = blk == 0 ? acc0[r] : acc1[r];
+              const float v = METRIC == 0 ? fmaf(-2.f, g, xns[tile_parity][rl]) : -g;
+              const uint32_t row = base + rl;
+              if (q < a.nq && row < r_end && row_allowed(a.allow, row)) {
+                if (cnt < uint32_t(a.caph)) out[cnt] = make_uint2(__float_as_uint(v), row);
+                ++cnt;
               }
             }
+          }
+      }
+    } else if (wave_live) {
+      // group minima over each lane's 16 rows of each 32-row block
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        float m = __builtin_inff();
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const float g = blk == 0 ? acc0[r] : acc1[r];
+          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[tile_parity][rl]) : -g;
+          const uint32_t row = base + rl;
+          if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, v);
         }
-      } else {
-        // group minima over each lane's 16 rows of each 32-row block
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-          float m = __builtin_inff();
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-            const float g = blk == 0 ? acc0[r] : acc1[r];
-            const float v = METRIC == 0 ? fmaf(-2.f, g, xns[buf][rl]) : -g;
-            const uint32_t row = base + rl;
-            if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, v);
-          }
-          if (q < a.nq) {
-            const uint32_t grp = ((base >> 5) + blk) * 2 + h;
-            if (grp < uint32_t(a.ngroups)) a.gm[size_t(q) * a.ngroups + grp] = m;
-          }
+        if (q < a.nq) {
+          const uint32_t grp = ((base >> 5) + blk) * 2 + h;
+          if (grp < uint32_t(a.ngroups)) a.gm[size_t(q) * a.ngroups + grp] = m;
         }
       }
     }
-
-    if (next < r_end) store_tile(buf ^ 1);
-    __syncthreads();
-    buf ^= 1;
+    tile_parity ^= 1;
   }
 
   if (MODE == 0 && q < a.nq) {
@@ -1023,7 +1045,15 @@ static int ExactScan(Ctx* c, Workspace& w, const ScanSource& src, const float* Q
   return ExactScanT(c, w, src, Sq8Of(src), Q, qlist, nslots, k, allow, out_ids, out_d, s);
 }
 
-static bool GemmSupported(size_t pd) { return pd % 16 == 0 && pd >= 16 && pd <= 128; }
+static bool GemmSupported(size_t pd) {
+  switch (pd) {
+    case 16: case 32: case 48: case 64: case 80: case 96: case 112: case 128:
+    case 192: case 256: case 384: case 512: case 768: case 960: case 1024:
+      return true;
+    default:
+      return false;
+  }
+}
 
 template <int PD, int METRIC, int KIND, int MODE>
 static void launch_gemm(hipStream_t s, int blocks, const GemmArgs& a) {
@@ -1063,6 +1093,13 @@ static int LaunchGemm(size_t pd, int metric, int kind, int mode, hipStream_t s, 
     case 96: launch_gemm_pd<96>(metric, kind, mode, s, blocks, a); break;
     case 112: launch_gemm_pd<112>(metric, kind, mode, s, blocks, a); break;
     case 128: launch_gemm_pd<128>(metric, kind, mode, s, blocks, a); break;
+    case 192: launch_gemm_pd<192>(metric, kind, mode, s, blocks, a); break;
+    case 256: launch_gemm_pd<256>(metric, kind, mode, s, blocks, a); break;
+    case 384: launch_gemm_pd<384>(metric, kind, mode, s, blocks, a); break;
+    case 512: launch_gemm_pd<512>(metric, kind, mode, s, blocks, a); break;
+    case 768: launch_gemm_pd<768>(metric, kind, mode, s, blocks, a); break;
+    case 960: launch_gemm_pd<960>(metric, kind, mode, s, blocks, a); break;
+    case 1024: launch_gemm_pd<1024>(metric, kind, mode, s, blocks, a); break;
     default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
   }
   return kOk;

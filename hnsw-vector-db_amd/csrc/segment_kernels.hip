@@ -1,0 +1,423 @@
+// segment_kernels.hip -- the collection-level pieces around the scans: dense row masks
+// (counting and compaction), query preparation, and the cross-segment merge.
+//
+//  * A filter reaches the scans as a dense bitmask (bit r of word r/64 = row r allowed):
+//    DeleteBits words complemented (src/util/delete_bits.h:50-55) or the roaring filter
+//    result minus deletes (src/engine/planner.cc:64-65) expanded to words.  When few rows
+//    are allowed the scan runs on a compacted copy of the allowed rows, kept in ascending
+//    row order so that ExactOverBitmap's tie rule (planner.cc:31-38) is unchanged.
+//  * PrepareQuery (src/engine/collection_impl.cc:1023-1034): pad, reject non-finite values,
+//    normalise for cosine with NormalizeVector (src/util/dataset.cc:33-41).
+//  * The merge of CollectionImpl::Search (collection_impl.cc:1076-1112): every part's hits
+//    sorted by (dist, part, row), the first hit of each external id kept, k returned.
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+#include "vdbg_device.h"
+#include "vdbg_internal.h"
+
+namespace vdbg {
+
+// ---------------------------------------------------------------- masks
+
+__global__ void k_word_counts(const uint64_t* __restrict__ w, size_t nwords, uint32_t N,
+                              uint32_t* __restrict__ cnt) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i >= nwords) return;
+  uint64_t v = w[i];
+  const size_t lo = i * 64;
+  if (lo + 64 > N) v &= (N - lo >= 64) ? ~0ull : ((1ull << (N - lo)) - 1ull);
+  cnt[i] = uint32_t(__popcll(v));
+}
+
+__global__ void k_compact_ids(const uint64_t* __restrict__ w, size_t nwords, uint32_t N,
+                              const uint32_t* __restrict__ pre, uint32_t* __restrict__ ids) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i >= nwords) return;
+  uint64_t v = w[i];
+  const size_t lo = i * 64;
+  if (lo + 64 > N) v &= (N - lo >= 64) ? ~0ull : ((1ull << (N - lo)) - 1ull);
+  uint32_t p = pre[i];
+  while (v != 0) {
+    const int b = __ffsll(static_cast<long long>(v)) - 1;
+    ids[p++] = uint32_t(lo + b);
+    v &= v - 1;
+  }
+}
+
+__global__ void k_gather_f4(const float4* __restrict__ src, size_t row_f4,
+                            const uint32_t* __restrict__ ids, uint32_t n, float4* __restrict__ dst) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(n) * row_f4) return;
+  const size_t r = t / row_f4, c = t - r * row_f4;
+  dst[t] = src[size_t(ids[r]) * row_f4 + c];
+}
+
+__global__ void k_gather_u4(const uint4* __restrict__ src, size_t row_u4,
+                            const uint32_t* __restrict__ ids, uint32_t n, uint4* __restrict__ dst) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(n) * row_u4) return;
+  const size_t r = t / row_u4, c = t - r * row_u4;
+  dst[t] = src[size_t(ids[r]) * row_u4 + c];
+}
+
+__global__ void k_gather_f(const float* __restrict__ src, const uint32_t* __restrict__ ids,
+                           uint32_t n, float* __restrict__ dst) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) dst[t] = src[ids[t]];
+}
+
+__global__ void k_map_ids(uint32_t* __restrict__ out, size_t n, const uint32_t* __restrict__ ids) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t < n && out[t] != kNoId) out[t] = ids[out[t]];
+}
+
+int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hipStream_t s) {
+  const size_t nwords = (size_t(N) + 63) / 64;
+  uint32_t* cnt = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&cnt), (nwords + 1) * 4, s));
+  k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
+  VDBG_HIP(hipGetLastError());
+  size_t tmp_bytes = 0;
+  VDBG_HIP(hipcub::DeviceReduce::Sum(nullptr, tmp_bytes, cnt, cnt + nwords, int(nwords), s));
+  void* tmp = nullptr;
+  VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
+  VDBG_HIP(hipcub::DeviceReduce::Sum(tmp, tmp_bytes, cnt, cnt + nwords, int(nwords), s));
+  VDBG_HIP(hipMemcpyAsync(c->host_pinned, cnt + nwords, 4, hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  *count = c->host_pinned[0];
+  (void)hipFreeAsync(tmp, s);
+  (void)hipFreeAsync(cnt, s);
+  return kOk;
+}
+
+// The scan over the allowed rows only: compact rows (ascending), scan without a mask, map
+// the compact indexes back to row ids.
+int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
+                const uint64_t* allow, uint32_t count, uint32_t* out_ids, float* out_d,
+                hipStream_t s) {
+  const uint32_t N = src->N;
+  const size_t pd = src->pd;
+  const size_t nwords = (size_t(N) + 63) / 64;
+  const size_t row_bytes = src->kind == 0 ? pd * sizeof(float) : pd;
+  void* buf = nullptr;
+  const size_t bytes = (nwords + 1) * 4 * 2 + size_t(count) * (4 + 4 + row_bytes) + 4096;
+  VDBG_HIP(hipMallocAsync(&buf, bytes, s));
+  char* p = static_cast<char*>(buf);
+  auto take = [&](size_t b) {
+    char* r = p;
+    p += (b + 255) & ~size_t(255);
+    return r;
+  };
+  uint32_t* cnt = reinterpret_cast<uint32_t*>(take((nwords + 1) * 4));
+  uint32_t* pre = reinterpret_cast<uint32_t*>(take((nwords + 1) * 4));
+  uint32_t* ids = reinterpret_cast<uint32_t*>(take(size_t(count) * 4 + 4));
+  float* rn = reinterpret_cast<float*>(take(size_t(count) * 4 + 4));
+  void* rows = take(size_t(count) * row_bytes + 16);
+  k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
+  size_t tmp_bytes = 0;
+  VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, cnt, pre, int(nwords), s));
+  void* tmp = nullptr;
+  VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
+  VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
+  k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre, ids);
+  if (src->kind == 0) {
+    const size_t row_f4 = pd / 4;
+    k_gather_f4<<<dim3(unsigned((count * row_f4 + 255) / 256)), 256, 0, s>>>(
+        reinterpret_cast<const float4*>(src->X), row_f4, ids, count, static_cast<float4*>(rows));
+  } else {
+    const size_t row_u4 = pd / 16;
+    k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
+        reinterpret_cast<const uint4*>(src->C), row_u4, ids, count, static_cast<uint4*>(rows));
+  }
+  k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
+  VDBG_HIP(hipGetLastError());
+  ScanSource cs = *src;
+  cs.X = src->kind == 0 ? static_cast<const float*>(rows) : nullptr;
+  cs.C = src->kind == 1 ? static_cast<const uint8_t*>(rows) : nullptr;
+  cs.rn = rn;
+  cs.N = count;
+  cs.SX = nullptr;
+  cs.SC = nullptr;
+  cs.Srn = nullptr;
+  cs.Sid = nullptr;
+  cs.Smax = 0;
+  int rc = RunScan(c, &cs, Q, nq, kk, nullptr, out_ids, out_d, s);
+  if (rc == kOk) {
+    k_map_ids<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, nq * kk, ids);
+    if (hipGetLastError() != hipSuccess) rc = SetError(kInternal, "map ids launch");
+  }
+  (void)hipStreamSynchronize(s);
+  FreeSample(&cs);
+  (void)hipFreeAsync(tmp, s);
+  (void)hipFreeAsync(buf, s);
+  return rc;
+}
+
+// The scans' entry for an optional filter: unfiltered and all-allowed filters scan every
+// row; when at most half the rows are allowed the allowed rows are compacted first;
+// otherwise the scan tests the mask per row.
+int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
+               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+  if (allow == nullptr || nq == 0 || kk == 0 || src->N == 0)
+    return RunScan(c, src, Q, nq, kk, allow, out_ids, out_d, s);
+  uint32_t count = 0;
+  VDBG_RETURN_IF_ERROR(CountAllowed(c, allow, src->N, &count, s));
+  if (count == src->N) return RunScan(c, src, Q, nq, kk, nullptr, out_ids, out_d, s);
+  if (count == 0) {  // nothing allowed: every slot is padding
+    ScanSource none = *src;
+    none.N = 0;
+    return RunScan(c, &none, Q, nq, kk, nullptr, out_ids, out_d, s);
+  }
+  if (2ull * count <= src->N)
+    return CompactScan(c, src, Q, nq, kk, allow, count, out_ids, out_d, s);
+  return RunScan(c, src, Q, nq, kk, allow, out_ids, out_d, s);
+}
+
+// ---------------------------------------------------------------- query preparation
+
+// PrepareQuery (collection_impl.cc:1023-1034): one wave per query copies dim values into a
+// zero-padded row and flags a non-finite value; for cosine, NormalizeVector
+// (dataset.cc:33-41): fp64 sum of squares in index order, inv = float(1 / sqrt(sum)), fp32
+// multiply.  status: 0 ok, 1 non-finite, 2 zero vector under cosine.
+__global__ __launch_bounds__(256) void k_prepare(const float* __restrict__ raw, int nq, int dim,
+                                                 int pd, int cosine, float* __restrict__ out,
+                                                 int* __restrict__ status) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;
+  const int lane = lane_id();
+  const float* v = raw + size_t(q) * dim;
+  float* o = out + size_t(q) * pd;
+  int bad = 0;
+  for (int i = lane; i < pd; i += kWave) {
+    const float x = i < dim ? v[i] : 0.f;
+    if (i < dim && !isfinite(x)) bad = 1;
+    o[i] = x;
+  }
+  bad = __ballot(bad != 0) != 0;
+  int st = bad ? 1 : 0;
+  float inv = 1.f;
+  if (!bad && cosine) {
+    if (lane == 0) {
+      double norm = 0;
+      for (int i = 0; i < dim; ++i) norm += static_cast<double>(v[i]) * static_cast<double>(v[i]);
+      if (!(norm > 0) || !isfinite(norm))
+        st = 2;
+      else
+        inv = static_cast<float>(1.0 / sqrt(norm));
+    }
+    st = __shfl(st, 0);
+    inv = __shfl(inv, 0);
+    if (st == 0)
+      for (int i = lane; i < dim; i += kWave) o[i] = v[i] * inv;
+  }
+  if (lane == 0) status[q] = st;
+}
+
+int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
+                   float* out, hipStream_t s) {
+  if (nq == 0) return kOk;
+  int* st = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&st), nq * sizeof(int), s));
+  k_prepare<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(raw, int(nq), int(dim), int(pd),
+                                                         metric == 2 ? 1 : 0, out, st);
+  VDBG_HIP(hipGetLastError());
+  std::vector<int> h(nq);
+  VDBG_HIP(hipMemcpyAsync(h.data(), st, nq * sizeof(int), hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  (void)hipFreeAsync(st, s);
+  for (size_t i = 0; i < nq; ++i) {
+    if (h[i] == 1) return SetError(kInvalidArgument, "query has a NaN or infinite value");
+    if (h[i] == 2) return SetError(kInvalidArgument, "a zero query cannot be normalized for cosine");
+  }
+  return kOk;
+}
+
+// ---------------------------------------------------------------- merge
+
+struct MergeArgs {
+  int nq, nparts, k;
+  const float* part_d;        // [nparts][nq][k]
+  const uint32_t* part_rows;  // [nparts][nq][k], UINT32_MAX padded
+  const uint64_t* ext;        // external ids, part p row r at ext[part_off[p] + r]
+  const uint64_t* part_off;
+  uint64_t* out_ext;          // [nq][k], UINT64_MAX padded
+  float* out_d;
+};
+
+// One wave per query.  Candidate c = p * k + i (part p, i-th hit) keeps (dist, part, row)
+// order as the key (dist, c): a part's hits arrive sorted by (dist, row).
+template <int E>
+__global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
+  __shared__ uint64_t ext_s[4][kWave * E];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int q = blockIdx.x * 4 + wave;
+  if (q >= a.nq) return;
+  const int total = a.nparts * a.k;
+  WaveKeys<E> r;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int c = e * kWave + lane;
+    r.d[e] = __builtin_inff();
+    r.id[e] = kNoId;
+    if (c < total) {
+      const int p = c / a.k, i = c - p * a.k;
+      const size_t at = (size_t(p) * a.nq + q) * a.k + i;
+      if (a.part_rows[at] != kNoId) {
+        r.d[e] = a.part_d[at];
+        r.id[e] = uint32_t(c);
+      }
+    }
+  }
+  bitonic_sort<E>(r);
+  uint64_t* ex = ext_s[wave];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    uint64_t v = ~0ull;
+    if (r.id[e] != kNoId) {
+      const int c = int(r.id[e]), p = c / a.k, i = c - p * a.k;
+      const uint32_t row = a.part_rows[(size_t(p) * a.nq + q) * a.k + i];
+      v = a.ext[a.part_off[p] + row];
+    }
+    ex[e * kWave + lane] = v;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  // keep the first occurrence of each external id
+  int written = 0;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int g = e * kWave + lane;
+    const uint64_t v = ex[g];
+    bool keep = r.id[e] != kNoId;
+    for (int t = 0; keep && t < g; ++t)
+      if (ex[t] == v) keep = false;
+    const uint64_t bal = __ballot(keep);
+    const int pos = written + __popcll(bal & ((1ull << lane) - 1ull));
+    if (keep && pos < a.k) {
+      a.out_ext[size_t(q) * a.k + pos] = v;
+      a.out_d[size_t(q) * a.k + pos] = r.d[e];
+    }
+    written += __popcll(bal);
+  }
+  for (int i = written + lane; i < a.k; i += kWave) {
+    a.out_ext[size_t(q) * a.k + i] = ~0ull;
+    a.out_d[size_t(q) * a.k + i] = __builtin_inff();
+  }
+}
+
+int MergeParts(Ctx* c, const MergeArgs& a, hipStream_t s) {
+  if (a.nq == 0 || a.k == 0) return kOk;
+  const int total = a.nparts * a.k;
+  int e = 1;
+  while (kWave * e < total) e <<= 1;
+  ProfScope ps(c, "merge_parts", s);
+  const dim3 grid((a.nq + 3) / 4);
+  switch (e) {
+    case 1: k_merge<1><<<grid, 256, 0, s>>>(a); break;
+    case 2: k_merge<2><<<grid, 256, 0, s>>>(a); break;
+    case 4: k_merge<4><<<grid, 256, 0, s>>>(a); break;
+    case 8: k_merge<8><<<grid, 256, 0, s>>>(a); break;
+    case 16: k_merge<16><<<grid, 256, 0, s>>>(a); break;
+    default: return SetError(kNotSupported, "merge: parts * k > 1024 on the GPU path");
+  }
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+}  // namespace vdbg
+
+using namespace vdbg;
+
+extern "C" {
+
+int vdbg_prepare_queries_device(vdbg_ctx* ctx, const float* raw, size_t nq, size_t dim,
+                                size_t padded_dim, int metric, float* out, void* stream) {
+  if (ctx == nullptr || (nq > 0 && (raw == nullptr || out == nullptr)) || dim == 0 ||
+      padded_dim < dim || padded_dim % 16 != 0 || metric < 0 || metric > 2)
+    return SetError(kInvalidArgument, "bad argument");
+  Ctx* c = &ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  return PrepareQueries(c, raw, nq, dim, padded_dim, metric,
+                        out, stream ? static_cast<hipStream_t>(stream) : c->stream);
+}
+
+int vdbg_prepare_queries_host(vdbg_ctx* ctx, const float* raw, size_t nq, size_t dim,
+                              size_t padded_dim, int metric, float* out) {
+  if (ctx == nullptr || (nq > 0 && (raw == nullptr || out == nullptr)))
+    return SetError(kInvalidArgument, "bad argument");
+  Ctx* c = &ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  if (nq == 0) return kOk;
+  float *dr = nullptr, *dout = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dr), nq * dim * 4, s));
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dout), nq * padded_dim * 4, s));
+  VDBG_HIP(hipMemcpyAsync(dr, raw, nq * dim * 4, hipMemcpyHostToDevice, s));
+  int rc = vdbg_prepare_queries_device(ctx, dr, nq, dim, padded_dim, metric, dout, s);
+  if (rc == kOk) {
+    VDBG_HIP(hipMemcpyAsync(out, dout, nq * padded_dim * 4, hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipStreamSynchronize(s));
+  }
+  (void)hipFreeAsync(dr, s);
+  (void)hipFreeAsync(dout, s);
+  return rc;
+}
+
+int vdbg_merge_parts_device(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
+                            const float* part_dists, const uint32_t* part_rows,
+                            const uint64_t* ext_ids, const uint64_t* part_offsets,
+                            uint64_t* out_ext, float* out_dists, void* stream) {
+  if (ctx == nullptr || (nq > 0 && k > 0 && nparts > 0 &&
+                         (part_dists == nullptr || part_rows == nullptr || ext_ids == nullptr ||
+                          part_offsets == nullptr || out_ext == nullptr || out_dists == nullptr)))
+    return SetError(kInvalidArgument, "bad argument");
+  Ctx* c = &ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  MergeArgs a{int(nq), int(nparts), int(k), part_dists, part_rows, ext_ids, part_offsets,
+              out_ext, out_dists};
+  return MergeParts(c, a, stream ? static_cast<hipStream_t>(stream) : c->stream);
+}
+
+int vdbg_merge_parts_host(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
+                          const float* part_dists, const uint32_t* part_rows,
+                          const uint64_t* ext_ids, size_t n_ext, const uint64_t* part_offsets,
+                          uint64_t* out_ext, float* out_dists) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  Ctx* c = &ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  if (nq == 0 || k == 0) return kOk;
+  const size_t nc = nparts * nq * k;
+  char* buf = nullptr;
+  const size_t bytes = nc * 8 + n_ext * 8 + nparts * 8 + nq * k * 12 + 4096;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&buf), bytes, s));
+  float* pd_ = reinterpret_cast<float*>(buf);
+  uint32_t* pr = reinterpret_cast<uint32_t*>(buf + nc * 4);
+  uint64_t* ex = reinterpret_cast<uint64_t*>(buf + ((nc * 8 + 255) & ~size_t(255)));
+  uint64_t* po = ex + n_ext;
+  uint64_t* oe = po + nparts;
+  float* od = reinterpret_cast<float*>(oe + nq * k);
+  VDBG_HIP(hipMemcpyAsync(pd_, part_dists, nc * 4, hipMemcpyHostToDevice, s));
+  VDBG_HIP(hipMemcpyAsync(pr, part_rows, nc * 4, hipMemcpyHostToDevice, s));
+  VDBG_HIP(hipMemcpyAsync(ex, ext_ids, n_ext * 8, hipMemcpyHostToDevice, s));
+  VDBG_HIP(hipMemcpyAsync(po, part_offsets, nparts * 8, hipMemcpyHostToDevice, s));
+  int rc = vdbg_merge_parts_device(ctx, nq, nparts, k, pd_, pr, ex, po, oe, od, s);
+  if (rc == kOk) {
+    VDBG_HIP(hipMemcpyAsync(out_ext, oe, nq * k * 8, hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipMemcpyAsync(out_dists, od, nq * k * 4, hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipStreamSynchronize(s));
+  }
+  (void)hipFreeAsync(buf, s);
+  return rc;
+}
+
+}  // extern "C"

@@ -151,7 +151,7 @@ static int Sq8Search(Sq8Index* x, const float* Q, size_t nq, size_t k, size_t de
                      const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
   Ctx* c = x->ds->ctx;
   if (nq == 0 || k == 0) return kOk;
-  if (depth == 0) return RunScan(c, &x->src, Q, nq, k, allow, out_ids, out_d, s);
+  if (depth == 0) return ScanMasked(c, &x->src, Q, nq, k, allow, out_ids, out_d, s);
   const size_t kk = std::max(depth, k);
   uint32_t* ti = nullptr;
   float* td = nullptr;
@@ -161,7 +161,7 @@ static int Sq8Search(Sq8Index* x, const float* Q, size_t nq, size_t k, size_t de
     (void)hipFreeAsync(ti, s);
     return SetError(kResourceExhausted, std::string("sq8 search: ") + hipGetErrorString(e));
   }
-  int rc = RunScan(c, &x->src, Q, nq, kk, allow, ti, td, s);
+  int rc = ScanMasked(c, &x->src, Q, nq, kk, allow, ti, td, s);
   if (rc == kOk)
     rc = Rerank(c, x->ds->rows, int(x->ds->pd), x->ds->metric, Q, nq, ti, kk, k, out_ids, out_d,
                 s);
@@ -295,7 +295,7 @@ int vdbg_flat_search_device(vdbg_dataset* ds, const float* queries, size_t nq, s
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
-  return RunScan(c, &ds->d.src, queries, nq, k, allow_words, out_ids, out_dists, s);
+  return ScanMasked(c, &ds->d.src, queries, nq, k, allow_words, out_ids, out_dists, s);
 }
 
 int vdbg_flat_search_host(vdbg_dataset* ds, const float* queries, size_t nq, size_t k,
@@ -313,7 +313,7 @@ int vdbg_flat_search_host(vdbg_dataset* ds, const float* queries, size_t nq, siz
   int rc = StageHost(c, d->n, d->pd, queries, nq, k, allow_words, out_ids, out_dists,
                      [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
                          hipStream_t s) {
-                       return RunScan(c, &d->src, dq, nq, k, dm, di, dd, s);
+                       return ScanMasked(c, &d->src, dq, nq, k, dm, di, dd, s);
                      });
   if (rc == kOk && dist_comps) *dist_comps = uint64_t(nq) * d->n;
   return rc;

@@ -173,6 +173,9 @@ int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq
 int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipStream_t s);
 int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
               uint8_t* codes, float* yn, hipStream_t s);
+// RunScan under an optional filter; compacts the allowed rows when they are few.
+int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
+               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
 int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);
 void FreeSample(ScanSource* src);
 

@@ -79,6 +79,11 @@ _SIGS = {
     "vdbg_ivfpq_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp]),
     "vdbg_ivfpq_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp,
                                            _vp]),
+    "vdbg_prepare_queries_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp]),
+    "vdbg_prepare_queries_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp]),
+    "vdbg_merge_parts_host": (C.c_int, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
+    "vdbg_merge_parts_device": (C.c_int, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -356,3 +361,28 @@ def assign_nearest(ctx, data, centroids, d=None):
     _check(lib.vdbg_assign_nearest(ctx.h, _ptr(data), n, d, stride, _ptr(centroids),
                                    centroids.shape[0], _ptr(assign), _ptr(dist)))
     return assign, dist
+
+
+def prepare_queries(ctx, raw, pd, metric="l2"):
+    """PrepareQuery for every row of raw (nq x dim): padded, checked, normalised for cosine."""
+    raw = np.ascontiguousarray(raw, np.float32)
+    nq, dim = raw.shape
+    out = np.empty((nq, pd), np.float32)
+    _check(lib.vdbg_prepare_queries_host(ctx.h, _ptr(raw), nq, dim, pd, METRICS[metric],
+                                         _ptr(out)))
+    return out
+
+
+def merge_parts(ctx, part_dists, part_rows, ext_ids, part_offsets):
+    """Cross-segment merge: part_* are (nparts, nq, k); returns (ext ids, dists), nq x k."""
+    part_dists = np.ascontiguousarray(part_dists, np.float32)
+    part_rows = np.ascontiguousarray(part_rows, np.uint32)
+    ext_ids = np.ascontiguousarray(ext_ids, np.uint64)
+    part_offsets = np.ascontiguousarray(part_offsets, np.uint64)
+    nparts, nq, k = part_dists.shape
+    out_ext = np.empty((nq, k), np.uint64)
+    out_d = np.empty((nq, k), np.float32)
+    _check(lib.vdbg_merge_parts_host(ctx.h, nq, nparts, k, _ptr(part_dists), _ptr(part_rows),
+                                     _ptr(ext_ids), ext_ids.size, _ptr(part_offsets),
+                                     _ptr(out_ext), _ptr(out_d)))
+    return out_ext, out_d

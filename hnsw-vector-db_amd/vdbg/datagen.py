@@ -96,7 +96,9 @@ def clustered_unit(n, dim, seed, centres_seed, n_centres, sigma, block=1 << 15):
 
 
 def normalize_rows(v):
-    """NormalizeVector per row: fp64 sum of squares, inv = float(1/sqrt), fp32 multiply."""
+    """Unit rows in NormalizeVector's manner (fp64 sum of squares, inv = float(1/sqrt), fp32
+    multiply); the fp64 sum is taken in numpy's order, so a row can differ from
+    NormalizeVector's in the last bit.  Test data only: the searches take rows as given."""
     v = np.asarray(v, np.float32)
     norm = np.einsum("ij,ij->i", v.astype(np.float64), v.astype(np.float64))
     ok = (norm > 0) & np.isfinite(norm)

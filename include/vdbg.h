@@ -194,6 +194,35 @@ int vdbg_kmeans(vdbg_ctx* ctx, const float* data, size_t n, size_t d, size_t str
 int vdbg_assign_nearest(vdbg_ctx* ctx, const float* data, size_t n, size_t d, size_t stride,
                         const float* centroids, size_t k, uint32_t* assign, float* dist);
 
+/* ---------------------------------------------------------------- collection read path */
+
+/* CollectionImpl::PrepareQuery (src/engine/collection_impl.cc:1023-1034) for nq raw queries
+ * of dim floats: each becomes a zero-padded row of padded_dim floats in `out`; a NaN or
+ * infinite value is InvalidArgument (1); under cosine (metric 2) NormalizeVector
+ * (src/util/dataset.cc:33-41: fp64 sum of squares in index order, fp32 scale by
+ * float(1 / sqrt(sum))) and a zero vector is InvalidArgument.  Device pointers. */
+int vdbg_prepare_queries_device(vdbg_ctx* ctx, const float* raw, size_t nq, size_t dim,
+                                size_t padded_dim, int metric, float* out, void* stream);
+/* Host-pointer variant. */
+int vdbg_prepare_queries_host(vdbg_ctx* ctx, const float* raw, size_t nq, size_t dim,
+                              size_t padded_dim, int metric, float* out);
+
+/* The merge of CollectionImpl::Search (collection_impl.cc:1076-1112) for nq queries over
+ * nparts per-segment results: part_dists / part_rows are [nparts][nq][k], each part's list
+ * sorted by (dist, row) and padded with UINT32_MAX rows, as the per-segment searches return
+ * them.  Row r of part p has external id ext_ids[part_offsets[p] + r].  All hits are ordered
+ * by (dist, part, row), the first hit of each external id is kept and k are written per
+ * query to out_ext / out_dists (padded with UINT64_MAX / +inf).  nparts * k <= 1024. */
+int vdbg_merge_parts_device(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
+                            const float* part_dists, const uint32_t* part_rows,
+                            const uint64_t* ext_ids, const uint64_t* part_offsets,
+                            uint64_t* out_ext, float* out_dists, void* stream);
+/* Host-pointer variant; ext_ids holds n_ext entries. */
+int vdbg_merge_parts_host(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
+                          const float* part_dists, const uint32_t* part_rows,
+                          const uint64_t* ext_ids, size_t n_ext, const uint64_t* part_offsets,
+                          uint64_t* out_ext, float* out_dists);
+
 /* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
  * candidates could not be certified and were re-scanned exactly. */
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
