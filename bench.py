@@ -7,7 +7,13 @@ Workload (one "step" = one batch search over data resident in HBM):
   sq8     the same rows as SQ8 codes (trained on all rows), top-100 by SQ8 distance, fp32
           rerank to k = 10.
   ivfpq   IVF-PQ over the same rows, nlist 4,096 (k-means 20 iterations, seed 42), m = 16,
-          nprobe 64, rerank 100 -> k = 10; built on the GPU.
+          nprobe 64, rerank 100 -> k = 10; built on the GPU.  Also swept over nprobe
+          16/32/64/128 at rerank 0 and 100.
+  filtered  the collection read path: 5M unit rows of 384 dims (10,000-centre mixture, cosine)
+          in 8 segments of 625,000, 2% of rows deleted, a filter passing 1%, 10% or 50% of
+          rows; 4,096 raw queries go through PrepareQuery, the filtered exact scan of every
+          segment and the cross-segment merge.
+The flat path also records batch sizes 1, 64 and 1,024 and k = 100 at the full batch.
 Queries, rows, codes and lists are resident before the timed region.  Each path's dominant
 kernel is timed with HIP events on the stream it runs on; its roofline fraction uses the
 algorithmic work (MFMA flops for the GEMM scans, code + id bytes for the IVF list scan).
@@ -40,7 +46,7 @@ def timed(ctx, torch, fn, steps, warmup, kernels):
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ctx.profile(True)
+    ctx.profile(bool(kernels))  # per-kernel events only when kernel times are wanted
     ctx.profile_reset()
     fallbacks = 0
     torch.cuda.synchronize()
@@ -55,6 +61,107 @@ def timed(ctx, torch, fn, steps, warmup, kernels):
     return elapsed, prof, fallbacks
 
 
+def _words(allowed):
+    """Dense row mask: bit r of word r / 64 set when row r is allowed."""
+    n = allowed.size
+    by = np.packbits(allowed, bitorder="little")
+    w = np.zeros(((n + 63) // 64) * 8, np.uint8)
+    w[:by.size] = by
+    return w.view(np.uint64)
+
+
+def run_filtered(args, ctx, torch, ref, threads):
+    import vdbg
+    from vdbg import datagen
+
+    dim = pd = 384
+    nseg, nq, k = 8, args.f_nq, args.k
+    seg_n = args.f_rows // nseg
+    N = seg_n * nseg
+    dev = torch.device("cuda:0")
+    stream = torch.cuda.current_stream().cuda_stream
+    want_cpu = not args.no_cpu and ref is not None
+    log(f"filtered: generating {N}x{dim} unit rows in {nseg} segments on the device")
+    t0 = time.perf_counter()
+    dss, host_rows = [], []
+    for p in range(nseg):
+        rows = datagen.clustered_unit_t(torch, seg_n, dim, 5002, 5001, 10000, 1.0, dev,
+                                        start_row=p * seg_n)
+        dss.append(vdbg.Dataset.from_device(ctx, rows.data_ptr(), seg_n, dim, pd, "cosine"))
+        if want_cpu:
+            host_rows.append(rows.cpu().numpy())
+        del rows
+    raw = datagen.clustered_unit_t(torch, nq, dim, 5005, 5001, 10000, 1.0, dev, unit=False)
+    raw_h = raw.cpu().numpy()
+    torch.cuda.synchronize()
+    # row attributes: deleted ~ Bernoulli(0.02), filter bucket ~ U{0..99}
+    deleted = datagen.uniform01(5004, 0, N) < np.float32(0.02)
+    bucket = datagen.rand_u64(5006, 0, N) % np.uint64(100)
+    log(f"filtered: data ready in {time.perf_counter() - t0:.1f} s")
+    ext_dev = torch.arange(N, dtype=torch.int64, device=dev)
+    off_dev = torch.arange(0, N, seg_n, dtype=torch.int64, device=dev)[:nseg].contiguous()
+    q_prep = torch.empty((nq, pd), dtype=torch.float32, device=dev)
+    part_ids = torch.empty((nseg, nq, k), dtype=torch.int32, device=dev)
+    part_d = torch.empty((nseg, nq, k), dtype=torch.float32, device=dev)
+    out_ext = torch.empty((nq, k), dtype=torch.int64, device=dev)
+    out_d = torch.empty((nq, k), dtype=torch.float32, device=dev)
+    out = {"rows": N, "segments": nseg, "dim": dim, "queries": nq, "k": k,
+           "deleted_frac": round(float(deleted.mean()), 5), "selectivity": {}}
+    samples = {1: 4096, 10: 1024, 50: 256}
+    for sel in (1, 10, 50):
+        allowed = (bucket < np.uint64(sel)) & ~deleted
+        words_h = [_words(allowed[p * seg_n:(p + 1) * seg_n]) for p in range(nseg)]
+        masks = [torch.from_numpy(w.view(np.int64)).to(dev) for w in words_h]
+        n_allowed = int(allowed.sum())
+
+        def step():
+            vdbg.prepare_queries_device(ctx, raw.data_ptr(), nq, dim, pd, "cosine",
+                                        q_prep.data_ptr(), stream)
+            for p in range(nseg):
+                dss[p].flat_search_device(q_prep.data_ptr(), nq, k, part_ids[p].data_ptr(),
+                                          part_d[p].data_ptr(), allow_ptr=masks[p].data_ptr(),
+                                          stream=stream)
+            vdbg.merge_parts_device(ctx, nq, nseg, k, part_d.data_ptr(), part_ids.data_ptr(),
+                                    ext_dev.data_ptr(), off_dev.data_ptr(), out_ext.data_ptr(),
+                                    out_d.data_ptr(), stream)
+
+        names = ["prepare_queries", "compact", "query_prep", "sample_gemm", "kth", "flat_gemm",
+                 "select", "exact_scan", "merge", "merge_parts"]
+        el, prof, fb = timed(ctx, torch, step, args.steps, args.warmup, names)
+        g_ms = prof["flat_gemm"][0] / args.steps
+        flops = 2.0 * n_allowed * pd * nq
+        r = {"allowed_rows": n_allowed, "qps": round(nq * args.steps / el, 1),
+             "ms_per_step": round(el * 1e3 / args.steps, 3),
+             "gemm_ms_per_step": round(g_ms, 3),
+             "gemm_TFLOPs": round(flops / (g_ms * 1e-3) / 1e12, 2) if g_ms > 0 else None,
+             "kernel_ms_per_step": {kk: round(v[0] / args.steps, 4) for kk, v in prof.items()},
+             "exact_rescans": fb}
+        log(f"filtered {sel}%: {r['qps']:.0f} q/s, {n_allowed} rows allowed")
+        if want_cpu:
+            s = min(samples[sel], nq)
+            t0 = time.perf_counter()
+            re_, rd_ = ref.filtered_collection_search(
+                host_rows, dim, words_h, np.arange(N, dtype=np.uint64), raw_h[:s], k,
+                threads=threads)
+            dt = time.perf_counter() - t0
+            ge = out_ext[:s].cpu().numpy().view(np.uint64)
+            gd = out_d[:s].cpu().numpy()
+            r["cpu_baseline"] = {
+                "value": round(s / dt, 2), "unit": "queries/s", "cores": threads,
+                "kind": "reference",
+                "sample": f"{s} of the {nq} queries: PrepareQuery, ExactOverBitmap over the "
+                          f"allowed rows of each of the {nseg} segments (reference kernels and "
+                          f"TopK), merge; {threads} threads, {dt:.1f} s"}
+            r["parity_on_cpu_sample"] = bool(np.array_equal(ge, re_) and np.array_equal(
+                gd.view(np.uint32), rd_.view(np.uint32)))
+            log(f"filtered {sel}% cpu: {s / dt:.1f} q/s, parity {r['parity_on_cpu_sample']}")
+        out["selectivity"][f"{sel}%"] = r
+        del masks
+    for d in dss:
+        d.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -63,18 +170,22 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--k", type=int, default=10)
-    ap.add_argument("--paths", default="flat,sq8,ivfpq")
+    ap.add_argument("--paths", default="flat,sq8,ivfpq,filtered")
     ap.add_argument("--nprobe", type=int, default=64)
     ap.add_argument("--cpu-sample", type=int, default=6400,
                     help="queries in the flat CPU-baseline sample (SQ8 uses half, IVF-PQ all)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sweeps", type=int, default=1,
+                    help="also time flat batch sizes / k=100 and the IVF-PQ nprobe sweep")
+    ap.add_argument("--f-rows", type=int, default=5_000_000, help="filtered: total rows")
+    ap.add_argument("--f-nq", type=int, default=4096, help="filtered: queries")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (3 times); used "
                          "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (every box "
-              "in this setup has one MI355X; the sharded design is described in DESIGN.md)",
+        print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported (one process "
+              "drives one MI355X; a run over several GPUs is not part of this build)",
               file=sys.stderr)
         sys.exit(2)
 
@@ -162,6 +273,23 @@ def main():
                           f"rows ({kern} kernels), queries over {threads} threads, {dt:.1f} s"}
             r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
             log(f"flat cpu: {s / dt:.1f} q/s ({kind}), parity {r['parity_on_cpu_sample']}")
+        if args.sweeps:
+            sweep = {}
+            for b, kb in ((1, k), (64, k), (1024, k), (nq, 100)):
+                ib = torch.empty((b, kb), dtype=torch.int32, device=dev)
+                db = torch.empty((b, kb), dtype=torch.float32, device=dev)
+
+                def step_b():
+                    ds.flat_search_device(q_dev.data_ptr(), b, kb, ib.data_ptr(), db.data_ptr(),
+                                          stream=stream)
+
+                reps = max(args.steps, 20) if b < 1024 else args.steps
+                elb, _, fbb = timed(ctx, torch, step_b, reps, 2, [])
+                sweep[f"batch{b}_k{kb}"] = {"qps": round(b * reps / elb, 1),
+                                            "ms_per_batch": round(elb * 1e3 / reps, 4),
+                                            "exact_rescans": fbb}
+                log(f"flat batch {b} k {kb}: {b * reps / elb:.0f} q/s")
+            r["sweep"] = sweep
         results["flat"] = r
 
     # ------------------------------------------------------------ SQ8
@@ -259,8 +387,33 @@ def main():
                               f"{rerank}) on the same index file, {threads} threads, {dt:.1f} s"}
                 r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
                 log(f"ivfpq cpu: {s / dt:.1f} q/s, parity {r['parity_on_cpu_sample']}")
+        if args.sweeps:
+            sweep = {}
+            for npb in (16, 32, 64, 128):
+                ix.search_device(q_dev.data_ptr(), nq, k, npb, 0, ids_dev.data_ptr(),
+                                 d_dev.data_ptr(), dc_ptr=dc_dev.data_ptr(), stream=stream)
+                torch.cuda.synchronize()
+                sc = int(dc_dev.cpu().numpy().sum()) - nq * nlist
+                for rr in (0, 100):
+                    def step_s():
+                        ix.search_device(q_dev.data_ptr(), nq, k, npb, rr, ids_dev.data_ptr(),
+                                         d_dev.data_ptr(), stream=stream)
+
+                    els, prs, _ = timed(ctx, torch, step_s, args.steps, 1, ["ivf_scan"])
+                    sms = prs["ivf_scan"][0] / max(1, prs["ivf_scan"][1])
+                    sweep[f"nprobe{npb}_rerank{rr}"] = {
+                        "qps": round(nq * args.steps / els, 1),
+                        "scan_ms": round(sms, 4),
+                        "scan_GBps": round(sc * (m + 4) / (sms * 1e-3) / 1e9, 1),
+                        "codes_scanned_per_query": round(sc / nq, 1)}
+                    log(f"ivfpq nprobe {npb} rerank {rr}: {nq * args.steps / els:.0f} q/s")
+            r["sweep"] = sweep
         ix.close()
         results["ivfpq"] = r
+
+    # ------------------------------------------------------------ filtered collection
+    if "filtered" in paths:
+        results["filtered"] = run_filtered(args, ctx, torch, ref, threads)
 
     head = results.get("flat") or next(iter(results.values()))
     out = {

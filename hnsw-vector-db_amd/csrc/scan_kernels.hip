@@ -417,9 +417,17 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     }
     a.shift[q] = shift;
     a.exact[q] = ex ? 1 : 0;
-    a.eb[q] = ex ? 0.f
-                 : float((4.0 * pd + 16.0) * (1.0 / 16777216.0) *
-                         (double(qmag) + double(a.rmag)) * 1.001);
+    // Rounding bound of |GEMM value + shift - exact distance|.  Any fp32 summation order of
+    // n products errs by at most ~n u sum|q_i x_i| (u = 2^-24), and sum|q_i x_i| <= |q||x|.
+    // Inner product of fp32 rows: the MFMA dot and the exact dot each err by that, so
+    // (2 pd + 16) u |q||x|.  Otherwise (L2 form, or SQ8 codes) the row norm, the shift and
+    // the exact distance add their own terms: (4 pd + 16) u (|q|^2 + |x|^2).
+    const double u = 1.0 / 16777216.0;
+    const double bound =
+        (a.kind == 0 && a.metric != 0)
+            ? (2.0 * pd + 16.0) * u * sqrt(double(qmag) * double(a.rmag))
+            : (4.0 * pd + 16.0) * u * (double(qmag) + double(a.rmag));
+    a.eb[q] = ex ? 0.f : float(bound * 1.001);
   }
 }
 
@@ -463,6 +471,9 @@ __host__ __device__ constexpr int GemmKc(int pd) {
 // stages and the query fragment is reloaded per chunk.  Stages are double-buffered in LDS
 // and feed the A operand; code rows are widened to fp32 on the way in.  The 32x32
 // accumulator gives lane l the values of query l % 32 for rows 8*(r/4) + 4*h + (r%4).
+// The epilogue of tile t reads that tile's row norms after the tile's last barrier, while
+// faster waves already stage tile t + 1 (norms of tile t + 2 are written only after the
+// barrier that follows), so the norms rotate through three slots.
 template <int PD, int METRIC, int KIND, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   constexpr int KC = GemmKc(PD);
@@ -474,7 +485,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
   static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
   __shared__ __attribute__((aligned(16))) float xs[2][kGemmRows * STR];
-  __shared__ float xns[2][kGemmRows];
+  __shared__ float xns[3][kGemmRows];
 
   const int b = blockIdx.x;
   const int item = (b & 7) * a.per_xcd + (b >> 3);
@@ -535,7 +546,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     }
     if (kc == 0) pre_n = (tid < kGemmRows && uint32_t(tid) < valid) ? a.rn[base + tid] : 0.f;
   };
-  auto store_stage = [&](int buf, int kc, int tile_parity) {
+  auto store_stage = [&](int buf, int kc, int nslot) {
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
@@ -558,7 +569,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         }
       }
     }
-    if (kc == 0 && tid < kGemmRows) xns[tile_parity][tid] = pre_n;
+    if (kc == 0 && tid < kGemmRows) xns[nslot][tid] = pre_n;
   };
 
   if (r_begin < r_end) {
@@ -568,7 +579,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   __syncthreads();
 
   int buf = 0;
-  int tile_parity = 0;
+  int slot = 0;  // norm slot of the current tile
   for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
     v16f acc0, acc1;
 #pragma unroll
@@ -601,7 +612,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         }
       }
 
-      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? tile_parity ^ 1 : tile_parity);
+      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? (slot == 2 ? 0 : slot + 1) : slot);
       __syncthreads();
       buf ^= 1;
     }
@@ -614,7 +625,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         for (int r = 0; r < 16; ++r) {
           const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           const float g = blk == 0 ? acc0[r] : acc1[r];
-          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[tile_parity][rl]) : -g;
+          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
           pass |= (v <= T ? 1u : 0u) << (blk * 16 + r);
         }
       if (__ballot(pass != 0) != 0) {
@@ -625,7 +636,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
             if (pass & (1u << (blk * 16 + r))) {
               const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
               const float g = blk == 0 ? acc0[r] : acc1[r];
-              const float v = METRIC == 0 ? fmaf(-2.f, g, xns[tile_parity][rl]) : -g;
+              const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
               const uint32_t row = base + rl;
               if (q < a.nq && row < r_end && row_allowed(a.allow, row)) {
                 if (cnt < uint32_t(a.caph)) out[cnt] = make_uint2(__float_as_uint(v), row);
@@ -643,7 +654,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         for (int r = 0; r < 16; ++r) {
           const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           const float g = blk == 0 ? acc0[r] : acc1[r];
-          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[tile_parity][rl]) : -g;
+          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
           const uint32_t row = base + rl;
           if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, v);
         }
@@ -653,7 +664,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         }
       }
     }
-    tile_parity ^= 1;
+    slot = slot == 2 ? 0 : slot + 1;
   }
 
   if (MODE == 0 && q < a.nq) {
@@ -708,7 +719,10 @@ struct SelectArgs {
   const int* exact;
   const uint32_t* qlist;   // nullable: slot i answers query qlist[i]
   int nslots, k, pd;
-  int rescore;             // 1: candidates hold GEMM values; 0: exact distances
+  int rescore;             // 0: candidates hold exact distances; 1: GEMM values, rescore
+                           // the best K'; 2: GEMM values, rescore every candidate
+  int by_query;            // candidate buffers are indexed by query (else by slot)
+  const float* T;          // rescore 2: the filter threshold of the GEMM pass
   uint32_t* out_ids;
   float* out_d;
   uint32_t* fb_list;       // rescore mode: queries that need the exact re-scan
@@ -719,6 +733,7 @@ constexpr int kMaxSeg = 1024;
 
 // One wave per slot.  Candidates of the slot's segments are streamed (a prefix sum over the
 // segment counts maps a flat index to its segment) into a wave top-k of capacity 64*E.
+// Queries that fail a certificate (or whose buffers overflowed) are appended to fb_list.
 template <int E, class Scorer>
 __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   __shared__ uint32_t pre_all[4][kMaxSeg + 1];
@@ -727,6 +742,7 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   const int slot = blockIdx.x * 4 + wave;
   if (slot >= a.nslots) return;
   const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
+  const uint32_t src = a.by_query ? q : uint32_t(slot);
   uint32_t* pre = pre_all[wave];
 
   if (a.ovf != nullptr && a.ovf[q]) {
@@ -738,7 +754,7 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   }
 
   uint32_t run = 0;
-  const uint32_t* cnts = a.counts + size_t(slot) * a.nseg;
+  const uint32_t* cnts = a.counts + size_t(src) * a.nseg;
   for (int b = 0; b < a.nseg; b += kWave) {
     const int s = b + lane;
     const uint32_t c = s < a.nseg ? cnts[s] : 0u;
@@ -759,7 +775,8 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
 
   WaveTopK<E> top;
   top.init();
-  const uint2* cbase = a.cand + size_t(slot) * a.nseg * size_t(a.cap);
+  const float* qv = a.Q + size_t(q) * a.pd;
+  const uint2* cbase = a.cand + size_t(src) * a.nseg * size_t(a.cap);
   for (uint32_t g0 = 0; g0 < total; g0 += kWave) {
     const uint32_t g = g0 + lane;
     float d = __builtin_inff();
@@ -771,8 +788,8 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
         if (pre[mid] <= g) lo = mid; else hi = mid;
       }
       const uint2 c = cbase[size_t(lo) * a.cap + (g - pre[lo])];
-      d = __uint_as_float(c.x);
       id = c.y;
+      d = a.rescore == 2 ? sc(qv, id) : __uint_as_float(c.x);
     }
     top.insert(d, id);
   }
@@ -780,6 +797,29 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   constexpr int N = kWave * E;
   uint32_t* oi = a.out_ids + size_t(q) * a.k;
   float* od = a.out_d + size_t(q) * a.k;
+  if (a.rescore == 2) {
+    // every row outside the buffers has GEMM value > T, so exact distance
+    // > T + shift - eb: certified when the k-th exact distance is at most that
+    float dk = __builtin_inff();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const int gi = e * kWave + lane;
+      if (gi < a.k) {
+        oi[gi] = top.k.id[e];
+        od[gi] = top.k.d[e];
+      }
+      const float v = __shfl(top.k.d[e], (a.k - 1) & (kWave - 1));
+      if (e == (a.k - 1) / kWave) dk = v;
+    }
+    if (!a.exact[q]) {
+      const float lower = (a.T[q] + a.shift[q]) - a.eb[q];
+      if (!(dk <= lower) && lane == 0) {
+        const uint32_t p = atomicAdd(a.fb_count, 1u);
+        a.fb_list[p] = q;
+      }
+    }
+    return;
+  }
   if (!a.rescore) {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -793,7 +833,6 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   }
 
   // exact re-scoring of the K' = N-1 best by GEMM value
-  const float* qv = a.Q + size_t(q) * a.pd;
   const uint32_t nsel = min(total, uint32_t(N - 1));
   const float a_next = __shfl(top.k.d[E - 1], kWave - 1);  // the (K'+1)-th GEMM value
   WaveKeys<E> r;
@@ -1105,26 +1144,24 @@ static int LaunchGemm(size_t pd, int metric, int kind, int mode, hipStream_t s, 
   return kOk;
 }
 
-// Chunk count for nqt query tiles over N rows: balance the last round of blocks against
-// the resident slots (2 blocks per CU), prefer fewer chunks at equal balance.
+// Chunk count for nqt query tiles over N rows: the fewest chunks whose last round of blocks
+// fills the resident slots (2 blocks per CU) within 3% of the best balance on offer.
 static int PlanChunks(int nqt, uint32_t N, int slots, int max_chunks) {
   const int limit = std::max(1, std::min<int>(max_chunks, int((N + 63) / 64)));
-  int best = 1;
-  double best_score = -1;
+  std::vector<std::pair<int, double>> opts;
+  double best = 0;
   for (int nc = 1; nc <= limit; ++nc) {
     uint32_t rows = (N + nc - 1) / nc;
     rows = (rows + 63) / 64 * 64;
-    const int real = int((N + rows - 1) / rows);
-    if (real != nc) continue;
+    if (int((N + rows - 1) / rows) != nc) continue;
     const double items = double(nqt) * nc;
-    const double rounds = std::ceil(items / slots);
-    const double score = items / (rounds * slots) - 0.002 * nc;
-    if (score > best_score) {
-      best_score = score;
-      best = nc;
-    }
+    const double util = items / (std::ceil(items / slots) * slots);
+    opts.emplace_back(nc, util);
+    best = std::max(best, util);
   }
-  return best;
+  for (const auto& o : opts)
+    if (o.second >= best - 0.03) return o.first;
+  return 1;
 }
 
 static void GemmGrid(GemmArgs& ga, int nqt, int nchunks, int* blocks) {
@@ -1154,7 +1191,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // ---- plan
   const int slots = 2 * c->cu_count;
   const int nqt = int((nq + 127) / 128);
-  const int nchunks = PlanChunks(nqt, N, slots, 256);
+  const int nchunks = PlanChunks(nqt, N, slots, kMaxSeg / 2);
   uint32_t chunk_rows = (N + nchunks - 1) / nchunks;
   chunk_rows = (chunk_rows + 63) / 64 * 64;
   uint32_t S = 1;
@@ -1174,7 +1211,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
 
   Workspace& w = c->ws;
   w.used = 0;
-  const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + sizeof(uint32_t)) +
+  const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
                       size_t(nq) * ngroups * sizeof(float) +
                       size_t(nq) * nseg * (sizeof(uint32_t) + size_t(caph) * sizeof(uint2)) +
@@ -1186,13 +1223,14 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   int* exact = w.take<int>(nq);
   int* ovf = w.take<int>(nq);
   uint32_t* fb_list = w.take<uint32_t>(nq);
-  uint32_t* fb_count = w.take<uint32_t>(1);
+  uint32_t* fb_count = w.take<uint32_t>(2);  // [0] first pass, [1] second chance
+  uint32_t* fb2_list = w.take<uint32_t>(nq);
   float* Qb = src->kind == 1 ? w.take<float>(nq * pd) : nullptr;
   float* gm = w.take<float>(size_t(nq) * ngroups);
   uint32_t* counts = w.take<uint32_t>(size_t(nq) * nseg);
   uint2* cand = w.take<uint2>(size_t(nq) * nseg * caph);
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
-  VDBG_HIP(hipMemsetAsync(fb_count, 0, sizeof(uint32_t), s));
+  VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact};
@@ -1283,10 +1321,34 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   VDBG_HIP(hipMemcpyAsync(c->host_pinned, fb_count, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
   VDBG_HIP(hipStreamSynchronize(s));
   const uint32_t nfb = c->host_pinned[0];
-  c->last_fallbacks = nfb;
-  if (nfb > 0)
+  c->last_fallbacks = 0;
+  if (nfb == 0) return kOk;
+  // second chance: rescore every buffered candidate of the uncertified queries
+  SelectArgs s2 = se;
+  s2.qlist = fb_list;
+  s2.nslots = int(nfb);
+  s2.by_query = 1;
+  s2.rescore = 2;
+  s2.T = T;
+  s2.fb_list = fb2_list;
+  s2.fb_count = fb_count + 1;
+  {
+    ProfScope ps(c, "rescore", s);
+    if (src->kind == 0) {
+      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, s2, FlatOf(*src));
+    } else {
+      VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, s2, Sq8Of(*src));
+    }
+    VDBG_HIP(hipGetLastError());
+  }
+  VDBG_HIP(hipMemcpyAsync(c->host_pinned, fb_count + 1, sizeof(uint32_t), hipMemcpyDeviceToHost,
+                          s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  const uint32_t nfb2 = c->host_pinned[0];
+  c->last_fallbacks = nfb2;
+  if (nfb2 > 0)
     VDBG_RETURN_IF_ERROR(
-        ExactScan(c, c->ws2, *src, Q, fb_list, int(nfb), kk, allow, out_ids, out_d, s));
+        ExactScan(c, c->ws2, *src, Q, fb2_list, int(nfb2), kk, allow, out_ids, out_d, s));
   return kOk;
 }
 

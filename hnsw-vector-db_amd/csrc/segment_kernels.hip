@@ -117,24 +117,27 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* ids = reinterpret_cast<uint32_t*>(take(size_t(count) * 4 + 4));
   float* rn = reinterpret_cast<float*>(take(size_t(count) * 4 + 4));
   void* rows = take(size_t(count) * row_bytes + 16);
-  k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
-  size_t tmp_bytes = 0;
-  VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, cnt, pre, int(nwords), s));
   void* tmp = nullptr;
-  VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
-  VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
-  k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre, ids);
-  if (src->kind == 0) {
-    const size_t row_f4 = pd / 4;
-    k_gather_f4<<<dim3(unsigned((count * row_f4 + 255) / 256)), 256, 0, s>>>(
-        reinterpret_cast<const float4*>(src->X), row_f4, ids, count, static_cast<float4*>(rows));
-  } else {
-    const size_t row_u4 = pd / 16;
-    k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
-        reinterpret_cast<const uint4*>(src->C), row_u4, ids, count, static_cast<uint4*>(rows));
+  {
+    ProfScope ps(c, "compact", s);
+    k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
+    size_t tmp_bytes = 0;
+    VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, cnt, pre, int(nwords), s));
+    VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
+    VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
+    k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre, ids);
+    if (src->kind == 0) {
+      const size_t row_f4 = pd / 4;
+      k_gather_f4<<<dim3(unsigned((count * row_f4 + 255) / 256)), 256, 0, s>>>(
+          reinterpret_cast<const float4*>(src->X), row_f4, ids, count, static_cast<float4*>(rows));
+    } else {
+      const size_t row_u4 = pd / 16;
+      k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
+          reinterpret_cast<const uint4*>(src->C), row_u4, ids, count, static_cast<uint4*>(rows));
+    }
+    k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
+    VDBG_HIP(hipGetLastError());
   }
-  k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
-  VDBG_HIP(hipGetLastError());
   ScanSource cs = *src;
   cs.X = src->kind == 0 ? static_cast<const float*>(rows) : nullptr;
   cs.C = src->kind == 1 ? static_cast<const uint8_t*>(rows) : nullptr;
@@ -222,9 +225,12 @@ int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, i
   if (nq == 0) return kOk;
   int* st = nullptr;
   VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&st), nq * sizeof(int), s));
-  k_prepare<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(raw, int(nq), int(dim), int(pd),
-                                                         metric == 2 ? 1 : 0, out, st);
-  VDBG_HIP(hipGetLastError());
+  {
+    ProfScope ps(c, "prepare_queries", s);
+    k_prepare<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(raw, int(nq), int(dim), int(pd),
+                                                           metric == 2 ? 1 : 0, out, st);
+    VDBG_HIP(hipGetLastError());
+  }
   std::vector<int> h(nq);
   VDBG_HIP(hipMemcpyAsync(h.data(), st, nq * sizeof(int), hipMemcpyDeviceToHost, s));
   VDBG_HIP(hipStreamSynchronize(s));

@@ -113,6 +113,9 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   if (n > 0) {
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&d.rows), bytes);
     if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d.norms), n * sizeof(float));
+    // device rows may still be in production on any stream of the caller: wait for the
+    // whole device before copying (the copy has completed when this call returns)
+    if (e == hipSuccess && rows_on_device) e = hipDeviceSynchronize();
     if (e == hipSuccess)
       e = hipMemcpyAsync(d.rows, rows, bytes,
                          rows_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,

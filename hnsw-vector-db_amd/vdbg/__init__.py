@@ -386,3 +386,14 @@ def merge_parts(ctx, part_dists, part_rows, ext_ids, part_offsets):
                                      _ptr(ext_ids), ext_ids.size, _ptr(part_offsets),
                                      _ptr(out_ext), _ptr(out_d)))
     return out_ext, out_d
+
+
+def prepare_queries_device(ctx, raw_ptr, nq, dim, pd, metric, out_ptr, stream=None):
+    _check(lib.vdbg_prepare_queries_device(ctx.h, raw_ptr, nq, dim, pd, METRICS[metric],
+                                           out_ptr, stream))
+
+
+def merge_parts_device(ctx, nq, nparts, k, dists_ptr, rows_ptr, ext_ptr, offsets_ptr,
+                       out_ext_ptr, out_dists_ptr, stream=None):
+    _check(lib.vdbg_merge_parts_device(ctx.h, nq, nparts, k, dists_ptr, rows_ptr, ext_ptr,
+                                       offsets_ptr, out_ext_ptr, out_dists_ptr, stream))

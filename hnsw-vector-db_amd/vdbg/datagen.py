@@ -104,3 +104,78 @@ def normalize_rows(v):
     ok = (norm > 0) & np.isfinite(norm)
     inv = np.where(ok, 1.0 / np.sqrt(np.where(ok, norm, 1.0)), 1.0).astype(np.float32)
     return (v * inv[:, None]).astype(np.float32)
+
+
+# ---------------------------------------------------------------- device generation
+#
+# The same streams computed with torch on any device, for workloads too large to generate
+# quickly on the host (5M x 384).  uint64 values are carried in int64 bit patterns: products
+# wrap modulo 2^64 as unsigned ones do, right shifts are made logical by masking, and the
+# unsigned remainder is taken on halves.  Integer outputs equal the numpy functions above;
+# fp64 transcendental results may differ from numpy's in the last bits, so rows generated
+# on a device are read back from it wherever a CPU baseline needs the same rows.
+
+def _s64(v):
+    return v - (1 << 64) if v >= 1 << 63 else v
+
+
+_GOLDEN_S = _s64(0x9E3779B97F4A7C15)
+_M1_S = _s64(0xBF58476D1CE4E5B9)
+_M2_S = _s64(0x94D049BB133111EB)
+
+
+def _srl(z, s):
+    return (z >> s) & ((1 << (64 - s)) - 1)
+
+
+def _mix_t(z):
+    z = (z ^ _srl(z, 30)) * _M1_S
+    z = (z ^ _srl(z, 27)) * _M2_S
+    return z ^ _srl(z, 31)
+
+
+def rand_u64_t(torch, seed, start, count, device):
+    """rand_u64 as an int64 tensor of the same bits."""
+    key = int(_mix(np.array([seed], np.uint64) + GOLDEN)[0])
+    i = torch.arange(start + 1, start + count + 1, dtype=torch.int64, device=device)
+    return _mix_t(_s64(key) + i * _GOLDEN_S)
+
+
+def umod_t(u, n):
+    """Unsigned remainder of int64-carried uint64 values by n (n < 2^31)."""
+    return (2 * (_srl(u, 1) % n) + (u & 1)) % n
+
+
+def normal_t(torch, seed, start, count, device):
+    p0 = start // 2
+    p1 = (start + count + 1) // 2
+    u = rand_u64_t(torch, seed, 2 * p0, 2 * (p1 - p0), device).view(-1, 2)
+    u1 = (_srl(u[:, 0], 11).to(torch.float64) + 1.0) * 2.0 ** -53
+    u2 = _srl(u[:, 1], 11).to(torch.float64) * 2.0 ** -53
+    r = torch.sqrt(-2.0 * torch.log(u1))
+    t = 2.0 * np.pi * u2
+    z = torch.stack([r * torch.cos(t), r * torch.sin(t)], dim=1).view(-1)
+    off = start - 2 * p0
+    return z[off:off + count]
+
+
+def clustered_unit_t(torch, n, dim, seed, centres_seed, n_centres, sigma, device, start_row=0,
+                     unit=True, block=1 << 16):
+    """clustered_unit rows [start_row, start_row + n) of stream `seed` as an fp32 tensor on
+    `device`; unit=False leaves them unnormalised (raw queries for PrepareQuery)."""
+    cen = normal_t(torch, centres_seed, 0, n_centres * dim, device).view(n_centres, dim)
+    pick = umod_t(rand_u64_t(torch, seed ^ 0x5BD1E995, start_row, n, device), n_centres)
+    out = torch.empty((n, dim), dtype=torch.float32, device=device)
+    for b in range(0, n, block):
+        e = min(n, b + block)
+        z = normal_t(torch, seed, (start_row + b) * dim, (e - b) * dim, device).view(e - b, dim)
+        v = (cen[pick[b:e]] + sigma * z).to(torch.float32)
+        if unit:
+            v64 = v.to(torch.float64)
+            norm = (v64 * v64).sum(dim=1)
+            ok = (norm > 0) & torch.isfinite(norm)
+            inv = torch.where(ok, 1.0 / torch.sqrt(torch.where(ok, norm, 1.0)),
+                              torch.ones_like(norm)).to(torch.float32)
+            v = v * inv[:, None]
+        out[b:e] = v
+    return out

@@ -2,8 +2,8 @@
  * vdbg.h -- C ABI of the MI355X (gfx950) search backend for vdb's nearest-neighbour path.
  *
  * This is the drop-in boundary: plain pointers and sizes, no C++ or framework types.  vdb's
- * C++ Index implementations (or any FFI) bind these entry points; see INTEGRATION.md for the
- * GpuFlatIndex / GpuSq8Index / GpuIvfPqIndex adapters a vdb maintainer would add.
+ * C++ Index implementations (or any FFI) bind these entry points; the C++20 classes in
+ * hnsw-vector-db_amd/host (GpuFlatIndex, GpuSq8Index, GpuIvfPqIndex) are such a binding.
  *
  * Conventions
  *  - Every call returns an int equal to vdb::Status::Code (include/vdb/status.h:14-26):
@@ -90,7 +90,9 @@ int vdbg_profile_get(vdbg_ctx* ctx, const char* name, double* total_ms, uint64_t
  * norms and value statistics used by the GEMM formulation are computed once here. */
 int vdbg_dataset_create(vdbg_ctx* ctx, const float* rows, size_t n, size_t dim,
                         size_t padded_dim, int metric, vdbg_dataset** out);
-/* The same from rows already in device memory (copied; the caller keeps ownership). */
+/* The same from rows already in device memory (copied; the caller keeps ownership).  Work
+ * queued on any stream of the device is waited for before the copy, and the copy has
+ * completed when the call returns. */
 int vdbg_dataset_create_device(vdbg_ctx* ctx, const float* rows_dev, size_t n, size_t dim,
                                size_t padded_dim, int metric, vdbg_dataset** out);
 int vdbg_dataset_destroy(vdbg_dataset* ds);

@@ -4,11 +4,17 @@
 // reference's src/util, src/distance and src/index files, read where they lie under
 // /root/reference, into oracle/_ref/libvdbref.so (never committed).  It is used to pin
 // the C restatement (vdb_oracle.c) and, in bench.py, as the timed CPU baseline.  Every
-// entry point calls the reference's real code; nothing here re-implements it.
+// entry point calls the reference's real code.  The one loop restated here is the
+// collection read path of ref_filtered_collection_search (planner.cc needs CRoaring, which
+// is absent): it still runs the reference's distance kernels, TopK and NormalizeVector.
+#include <algorithm>
+#include <atomic>
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <memory>
 #include <string>
+#include <unordered_set>
 #include <vector>
 
 #include "distance/distance.h"
@@ -311,5 +317,82 @@ int ref_ivfpq_search_batch(int metric, const char* file, size_t file_len, const 
 
 int ref_normalize(float* v, size_t dim) { return NormalizeVector(v, dim) ? 1 : 0; }
 uint32_t ref_crc32c(const void* data, size_t n) { return crc32c::Value(data, n); }
+
+// The filtered read path of CollectionImpl::Search over disk segments with flat indexes,
+// per query and fanned over a pool as SearchBatch does (collection_impl.cc:1121-1135):
+// PrepareQuery (:1023-1034, with the reference's NormalizeVector), for every segment the
+// prefilter exact scan ExactOverBitmap (planner.cc:31-38: allowed rows ascending, the
+// default kernel set's DistFn, the reference's TopK), then the merge of :1076-1112
+// (sort by (dist, part, row), first hit per external id).  The planner itself and the
+// roaring bitmaps need libraries absent here, so the allowed rows arrive as dense words
+// and this loop restates theirs.  Returns 1 (InvalidArgument) for a query PrepareQuery
+// rejects.
+int ref_filtered_collection_search(int metric, const float* const* seg_rows,
+                                   const size_t* seg_n, size_t nseg, size_t dim, size_t pd,
+                                   const uint64_t* const* allow, const uint64_t* ext,
+                                   const float* raw_queries, size_t nq, size_t k,
+                                   uint64_t* out_ext, float* out_d, int nthreads) {
+  DistFn fn = Fn(&Kernels(), metric);
+  std::vector<size_t> seg_off(nseg + 1, 0);
+  for (size_t p = 0; p < nseg; ++p) seg_off[p + 1] = seg_off[p] + seg_n[p];
+  std::atomic<int> bad{0};
+  ThreadPool pool(nthreads <= 0 ? 1 : static_cast<size_t>(nthreads));
+  pool.parallel_for(0, nq, [&](size_t qi) {
+    std::vector<float> q(pd, 0.f);
+    const float* v = raw_queries + qi * dim;
+    for (size_t i = 0; i < dim; ++i) {
+      if (!std::isfinite(v[i])) {
+        bad = 1;
+        return;
+      }
+      q[i] = v[i];
+    }
+    if (metric == 2 && !NormalizeVector(q.data(), dim)) {
+      bad = 1;
+      return;
+    }
+    struct Cand {
+      float dist;
+      uint32_t part;
+      uint32_t row;
+    };
+    std::vector<Cand> all;
+    std::vector<Neighbor> hits;
+    for (size_t p = 0; p < nseg; ++p) {
+      TopK top(k);
+      const uint64_t* w = allow[p];
+      for (size_t wi = 0; wi < (seg_n[p] + 63) / 64; ++wi) {
+        uint64_t bits = w[wi];
+        while (bits != 0) {
+          const uint32_t r = static_cast<uint32_t>(wi * 64 + __builtin_ctzll(bits));
+          bits &= bits - 1;
+          if (r >= seg_n[p]) break;
+          top.push(fn(q.data(), seg_rows[p] + static_cast<size_t>(r) * pd, pd), r);
+        }
+      }
+      top.sorted_into(&hits);
+      for (const Neighbor& h : hits) all.push_back({h.dist, static_cast<uint32_t>(p), h.id});
+    }
+    std::sort(all.begin(), all.end(), [](const Cand& a, const Cand& b) {
+      if (a.dist != b.dist) return a.dist < b.dist;
+      if (a.part != b.part) return a.part < b.part;
+      return a.row < b.row;
+    });
+    std::unordered_set<uint64_t> seen;
+    size_t out = 0;
+    for (const Cand& c : all) {
+      const uint64_t e = ext[seg_off[c.part] + c.row];
+      if (!seen.insert(e).second) continue;
+      out_ext[qi * k + out] = e;
+      out_d[qi * k + out] = c.dist;
+      if (++out >= k) break;
+    }
+    for (; out < k; ++out) {
+      out_ext[qi * k + out] = UINT64_MAX;
+      out_d[qi * k + out] = std::numeric_limits<float>::infinity();
+    }
+  });
+  return bad ? 1 : 0;
+}
 
 }  // extern "C"

@@ -1,7 +1,7 @@
 /*
  * vdb_oracle.c -- CPU restatement of vdb's nearest-neighbour hot path.
  *
- * TEST INFRASTRUCTURE ONLY (see vdb_oracle.h): the checker the HIP backend is compared
+ * TEST INFRASTRUCTURE ONLY (see vdb_oracle.h): the oracle the HIP backend is compared
  * against, never part of the product.  Citations are path:line in the reference
  * (KoduruChandrasekhar/HNSW-Vector-DB).  Built with -ffp-contract=off: the only fused
  * multiply-adds are the explicit fmaf() calls that stand for the reference's

@@ -1,7 +1,7 @@
 /*
  * vdb_oracle.h -- CPU restatement of vdb's nearest-neighbour hot path.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker that the HIP backend is
+ * TEST INFRASTRUCTURE ONLY.  This library is the oracle that the HIP backend is
  * compared against: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
  * leg may load it.  The product (libvdbg.so and the vdbg package) never links,
  * loads or calls it, and has no CPU fallback that routes through it.

@@ -1,4 +1,4 @@
-"""Shared test set-up: markers, import paths and the checker libraries."""
+"""Shared test set-up: markers, import paths and the oracle libraries."""
 import os
 import sys
 

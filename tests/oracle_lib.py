@@ -1,8 +1,8 @@
-"""ctypes bindings for the checkers (test infrastructure only).
+"""ctypes bindings for the oracle libraries (test infrastructure only).
 
 liboracle.so is the C restatement of vdb's hot path (oracle/vdb_oracle.c); libvdbref.so
 (oracle/_ref/, present only where it was built from the reference's sources) is the
-reference's own code behind a C driver.  Both are checkers: product code never loads them.
+reference's own code behind a C driver.  Both are test oracles: product code never loads them.
 """
 import ctypes as C
 import os
@@ -158,6 +158,33 @@ class Reference:
               f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "ref_normalize", C.c_int, [f32p, sz])
         _sig(lib, "ref_crc32c", C.c_uint32, [C.c_char_p, sz])
+        _sig(lib, "ref_filtered_collection_search", C.c_int,
+             [C.c_int, C.c_void_p, C.c_void_p, sz, sz, sz, C.c_void_p, u64p, f32p, sz, sz,
+              u64p, f32p, C.c_int])
+
+    def filtered_collection_search(self, segs, dim, allows, ext, raw, k, metric="cosine",
+                                   threads=8):
+        """CollectionImpl::Search over flat segments with a filter: segs are (n_p, pd)
+        arrays, allows their dense words, ext the concatenated external ids, raw the
+        unprepared queries (nq, dim).  Returns (ext ids, dists), nq x k."""
+        nseg = len(segs)
+        pd = segs[0].shape[1]
+        segs = [np.ascontiguousarray(s, np.float32) for s in segs]
+        allows = [np.ascontiguousarray(a, np.uint64) for a in allows]
+        rows_p = (C.c_void_p * nseg)(*[s.ctypes.data for s in segs])
+        n_p = (C.c_size_t * nseg)(*[s.shape[0] for s in segs])
+        allow_p = (C.c_void_p * nseg)(*[a.ctypes.data for a in allows])
+        raw = np.ascontiguousarray(raw, np.float32)
+        nq = raw.shape[0]
+        oe = np.empty((nq, k), np.uint64)
+        od = np.empty((nq, k), np.float32)
+        rc = self.lib.ref_filtered_collection_search(
+            METRIC[metric], C.cast(rows_p, C.c_void_p), C.cast(n_p, C.c_void_p), nseg, dim, pd,
+            C.cast(allow_p, C.c_void_p), np.ascontiguousarray(ext, np.uint64), raw, nq, k, oe,
+            od, threads)
+        if rc != 0:
+            raise ValueError("a query was rejected by PrepareQuery")
+        return oe, od
 
     def flat_search(self, base, dim, queries, k, metric="l2", kset="avx512", allow=None,
                     threads=8):

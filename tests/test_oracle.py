@@ -1,4 +1,4 @@
-"""The oracle (oracle/vdb_oracle.c) pinned before it is trusted as the GPU's checker.
+"""The oracle (oracle/vdb_oracle.c) pinned before it is trusted as the GPU path's reference.
 
 Three kinds of evidence per function:
   * golden vectors written by the reference's own code (tests/golden/make_golden.py);
@@ -360,3 +360,47 @@ def test_merge_parts_closed_form(oracle):
     assert n == 4
     assert list(oe) == [11, 10, 20, 21]
     assert list(od) == [0.5, 1, 1, 2]
+
+
+def test_filtered_collection_search_matches_reference(oracle, reference):
+    # the oracle's pieces (pad + NormalizeVector, per-segment filtered exact scan, merge)
+    # composed as CollectionImpl::Search composes them, against the reference's kernels,
+    # TopK and NormalizeVector driven by the planner's loop
+    from vdbg import datagen
+
+    dim, k = 40, 10
+    pd = 48
+    rng = np.random.default_rng(5)
+    sizes = [700, 1500, 64, 900]
+    segs, allows, exts = [], [], []
+    for i, n in enumerate(sizes):
+        segs.append(datagen.pad(datagen.clustered_unit(n, dim, 10 + i, 9, 20, 0.4), pd))
+        a = rng.random(n) < [0.05, 0.5, 1.0, 0.0][i]
+        w = np.zeros((n + 63) // 64, np.uint64)
+        rows = np.nonzero(a)[0]
+        np.bitwise_or.at(w, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+        allows.append(w)
+        exts.append(rng.permutation(10 ** 6)[:n].astype(np.uint64))
+    exts[1][:30] = exts[0][:30]  # the same external id in two segments
+    ext = np.concatenate(exts)
+    raw = datagen.clustered_unit(50, dim, 99, 9, 20, 0.4) * 2.5
+    re, rd = reference.filtered_collection_search(segs, dim, allows, ext, raw, k)
+    # oracle composition
+    q = np.zeros((50, pd), np.float32)
+    q[:, :dim] = raw
+    for i in range(50):
+        assert oracle.lib.or_normalize(q[i], dim) == 1
+    nseg = len(segs)
+    pdist = np.empty((nseg, 50, k), np.float32)
+    prow = np.empty((nseg, 50, k), np.uint32)
+    for p in range(nseg):
+        pdist[p], prow[p] = oracle.flat_search(segs[p], q, k, metric="cosine", allow=allows[p])
+    off = np.concatenate([[0], np.cumsum(sizes)[:-1]]).astype(np.uint64)
+    for i in range(50):
+        od = np.empty(k, np.float32)
+        oe = np.empty(k, np.uint64)
+        n = oracle.lib.or_merge_parts(nseg, k, np.ascontiguousarray(pdist[:, i]),
+                                      np.ascontiguousarray(prow[:, i]), ext, off, od, oe)
+        assert list(re[i, :n]) == list(oe[:n])
+        assert np.array_equal(rd[i, :n].view(np.uint32), od[:n].view(np.uint32))
+        assert (re[i, n:] == np.iinfo(np.uint64).max).all()
