@@ -265,6 +265,39 @@ __global__ void k_first_probe(const uint32_t* __restrict__ probe, int nprobe, in
   val[q] = uint32_t(q);
 }
 
+// Each query's probed lists with their coarse distances, reordered: the nearest list stays
+// first (it tightens the top-R threshold early), the others follow in ascending list id.
+// Queries that run together probe mostly the same lists, and walking them in one global
+// order makes them touch a shared list's tables at about the same time, while the list is
+// still in L2.  The scan's result does not depend on the order (TopK keeps the smallest
+// (dist, id) of all).  One wave per query; key = list id (exact in fp32, -1 for the nearest),
+// payload = position in the probe list.
+template <int E>
+__global__ __launch_bounds__(256) void k_sort_probes(const uint32_t* __restrict__ probe,
+                                                     const float* __restrict__ probe_d, int nprobe,
+                                                     int nq, uint32_t* __restrict__ sprobe,
+                                                     float* __restrict__ sprobe_d) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= nq) return;
+  const int lane = lane_id();
+  WaveKeys<E> k;
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = e * kWave + lane;
+    k.d[e] = i == 0 ? -1.f : i < nprobe ? float(probe[size_t(q) * nprobe + i]) : __builtin_inff();
+    k.id[e] = i < nprobe ? uint32_t(i) : kNoId;
+  }
+  bitonic_sort<E>(k);
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int i = e * kWave + lane;
+    if (i < nprobe) {
+      sprobe[size_t(q) * nprobe + i] = probe[size_t(q) * nprobe + k.id[e]];
+      if (probe_d != nullptr) sprobe_d[size_t(q) * nprobe + i] = probe_d[size_t(q) * nprobe + k.id[e]];
+    }
+  }
+}
+
 struct IvfFastArgs {
   const uint32_t* qorder;  // queries sorted by nearest list (nullable)
   const float* offs;       // [nq][nprobe] offsets when there are no precomputed tables
@@ -533,14 +566,29 @@ int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
     // queries in nearest-list order; offsets for the inner-product table
     void* buf = nullptr;
     const size_t nq = size_t(a.nq);
-    VDBG_HIP(hipMallocAsync(&buf, nq * 16 + nq * a.nprobe * 4 + 4096, s));
+    VDBG_HIP(hipMallocAsync(&buf, nq * 16 + nq * a.nprobe * 12 + 4096, s));
     uint32_t* key = static_cast<uint32_t*>(buf);
     uint32_t* val = key + nq;
     uint32_t* key2 = val + nq;
     uint32_t* order = key2 + nq;
     float* offs = reinterpret_cast<float*>(order + nq);
+    uint32_t* sprobe = reinterpret_cast<uint32_t*>(offs + nq * a.nprobe);
+    float* sprobe_d = reinterpret_cast<float*>(sprobe + nq * a.nprobe);
     k_first_probe<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, key, val);
     VDBG_HIP(hipGetLastError());
+    IvfScanArgs as = a;  // the scan's view: probes in ascending list id
+    if (a.nprobe > 1 && a.nprobe <= 4 * kWave) {
+      const dim3 g(unsigned((nq + 3) / 4));
+      if (a.nprobe <= kWave)
+        k_sort_probes<1><<<g, 256, 0, s>>>(a.probe, a.probe_d, a.nprobe, a.nq, sprobe, sprobe_d);
+      else if (a.nprobe <= 2 * kWave)
+        k_sort_probes<2><<<g, 256, 0, s>>>(a.probe, a.probe_d, a.nprobe, a.nq, sprobe, sprobe_d);
+      else
+        k_sort_probes<4><<<g, 256, 0, s>>>(a.probe, a.probe_d, a.nprobe, a.nq, sprobe, sprobe_d);
+      VDBG_HIP(hipGetLastError());
+      as.probe = sprobe;
+      as.probe_d = a.probe_d != nullptr ? sprobe_d : nullptr;
+    }
     size_t tmp_bytes = 0;
     VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, key2, val, order, a.nq, 0,
                                                 32, s));
@@ -549,7 +597,7 @@ int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
     VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, key2, val, order, a.nq, 0, 32, s));
     if (!l2) {
       k_ivf_offsets<<<dim3(unsigned((nq * a.nprobe + 255) / 256)), 256, 0, s>>>(
-          a.Q, a.pd, a.dim, a.coarse, a.probe, a.nprobe, a.nq, offs);
+          a.Q, a.pd, a.dim, a.coarse, as.probe, a.nprobe, a.nq, offs);
       VDBG_HIP(hipGetLastError());
     }
     IvfFastArgs f{order, l2 ? nullptr : offs, 0, 0};
@@ -559,9 +607,9 @@ int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
     {
       ProfScope ps(c, "ivf_scan", s);
       switch (a.m) {
-        case 4: rc = launch_fast_m<4>(e, s, a, f); break;
-        case 8: rc = launch_fast_m<8>(e, s, a, f); break;
-        default: rc = launch_fast_m<16>(e, s, a, f); break;
+        case 4: rc = launch_fast_m<4>(e, s, as, f); break;
+        case 8: rc = launch_fast_m<8>(e, s, as, f); break;
+        default: rc = launch_fast_m<16>(e, s, as, f); break;
       }
       if (rc == kOk && hipGetLastError() != hipSuccess) rc = SetError(kInternal, "ivf scan launch");
     }

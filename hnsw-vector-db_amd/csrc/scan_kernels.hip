@@ -1194,8 +1194,11 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int nchunks = PlanChunks(nqt, N, slots, kMaxSeg / 2);
   uint32_t chunk_rows = (N + nchunks - 1) / nchunks;
   chunk_rows = (chunk_rows + 63) / 64 * 64;
+  // Sample size: about kk * N / S rows pass the threshold per query, and every pass is a
+  // scattered buffer write plus a select insertion, while the pre-pass costs S / N of the
+  // main GEMM; N / 64 keeps both near 1.5%.
   uint32_t S = 1;
-  while (S < 16u * std::max<uint32_t>(128, 4 * uint32_t(kk))) S *= 2;
+  while (S < std::max<uint32_t>(16u * std::max<uint32_t>(128, 4 * uint32_t(kk)), N / 64)) S *= 2;
   S = std::min(S, src->Smax);
   const int ngroups = int((S + 31) / 32) * 2;
   const int schunks = PlanChunks(nqt, S, slots, int((S + 63) / 64));

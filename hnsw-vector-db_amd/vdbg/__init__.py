@@ -33,6 +33,13 @@ def _load():
     if not os.path.exists(LIB_PATH):
         raise ImportError(
             f"libvdbg.so is not built ({LIB_PATH}); run __graft_entry__.build() first")
+    # PyTorch-ROCm carries its own libamdhip64.so.7.  Loaded first, it also serves
+    # libvdbg.so (same soname); loaded second, it would bring a second HIP/HSA runtime into
+    # the process that finds no GPU.  So when torch is installed it is imported first.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     return C.CDLL(LIB_PATH)
 
 

@@ -95,3 +95,37 @@ def test_flat_other_dims(ctx, oracle, dim):
     gi, gd = ds.flat_search(qs, 10)
     od, oi = oracle.flat_search(base, qs, 10)
     _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("data", ["sift_like", "uniform"])
+def test_flat_large_batch_many_tiles(ctx, oracle, data):
+    # many 64-row tiles per block and many query tiles: the GEMM's staged tiles and row-norm
+    # slots are reused often while waves drift apart
+    n, nq, k = 300000, 1024 if data == "sift_like" else 256, 10
+    print(f"flat large {data} n={n} nq={nq}", flush=True)
+    gen = datagen.sift_like if data == "sift_like" else datagen.uniform_rows
+    base = gen(n, 128, 3101)
+    qs = gen(nq, 128, 3102)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, k)
+    od, oi = oracle.flat_search(base, qs, k)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_dataset_from_device_rows_in_flight(ctx, oracle):
+    # rows produced by torch kernels still queued on torch's stream, the source buffer
+    # released right after: every dataset must hold its own rows
+    import torch
+
+    dev = torch.device("cuda:0")
+    hosts, dss = [], []
+    for p in range(4):
+        rows = datagen.clustered_unit_t(torch, 40000, 96, 7000 + p, 7100, 64, 0.5, dev)
+        dss.append(vdbg.Dataset.from_device(ctx, rows.data_ptr(), 40000, 96, 96, "cosine"))
+        hosts.append(rows.cpu().numpy())
+        del rows
+    qs = hosts[0][:64].copy()
+    for p in range(4):
+        gi, gd = dss[p].flat_search(qs, 10)
+        od, oi = oracle.flat_search(hosts[p], qs, 10, metric="cosine")
+        _check_equal(gi, gd, oi, od)
