@@ -42,6 +42,26 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+PROFILES = {"flat": "flat_gemm_sift_like_1m_x128_k10_b10000.md",
+            "sq8": "sq8_gemm_sift_like_1m_x128_d100_b10000.md",
+            "ivfpq": "ivf_scan_sift_like_1m_nlist4096_m16_nprobe64.md"}
+
+
+def profiled_traffic(path):
+    """HBM bytes per launch of the path's dominant kernel, as measured by the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs summarised under profiles/ (None when absent)."""
+    f = os.path.join(ROOT, "profiles", PROFILES.get(path, ""))
+    if not os.path.isfile(f):
+        return None
+    for line in open(f):
+        if line.startswith("HBM bytes per launch (calibrated):"):
+            try:
+                return float(line.split(":")[1].split()[0])
+            except ValueError:
+                return None
+    return None
+
+
 def timed(ctx, torch, fn, steps, warmup, kernels):
     for _ in range(warmup):
         fn()
@@ -415,6 +435,10 @@ def main():
     if "filtered" in paths:
         results["filtered"] = run_filtered(args, ctx, torch, ref, threads)
 
+    if N == 1_000_000 and nq == 10_000 and k == 10:
+        for name in ("flat", "sq8", "ivfpq"):
+            if name in results and (name != "ivfpq" or args.nprobe == 64):
+                results[name]["traffic"] = profiled_traffic(name)
     head = results.get("flat") or next(iter(results.values()))
     out = {
         "metric": METRIC,
@@ -433,7 +457,8 @@ def main():
                    "dim": dim, "k": k, "batch": nq, "metric": "l2"},
         "roofline": {"bound": head["bound"], "achieved": round(head["achieved"], 2),
                      "peak": head["peak"], "unit": head["unit"],
-                     "frac": round(head["achieved"] / head["peak"], 4), "traffic": None,
+                     "frac": round(head["achieved"] / head["peak"], 4),
+                     "traffic": head.get("traffic"), "traffic_unit": "bytes per launch",
                      "kernel": head["kernel"], "kernel_ms": round(head["kernel_ms"], 3)},
         "cpu_baseline": head.get("cpu_baseline"),
         "parity_on_cpu_sample": head.get("parity_on_cpu_sample"),

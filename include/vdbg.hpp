@@ -1,0 +1,475 @@
+// vdbg.hpp -- C++20 host classes over the C ABI in vdbg.h, shaped like vdb's index interface.
+//
+// vdb's search path is `class Index` (src/index/index.h:36-55): search(q, k, params, filter,
+// out, stats) per query, with SearchParams (include/vdb/options.h:63-71), RowFilter
+// (index.h:23-27), IndexSearchStats (index.h:29-32) and results as ascending Neighbor
+// (include/vdb/types.h:19-28).  The classes below keep those names, argument meanings and
+// result order so that a vdb Index adapter (or any C++ caller) is a thin forwarding layer:
+//
+//   GpuFlatIndex   FlatIndex (src/index/flat_index.h:20-39) + FlatSearchBatch (:17-18)
+//   GpuSq8Index    the SQ8 codes and scan of HnswSq8Index (src/index/hnsw/hnsw_index.h:44-95)
+//                  with the graph beam replaced by an exhaustive scan
+//   GpuIvfPqIndex  IvfPqIndex (src/index/quant/ivf_pq.h:42-81), file format VDBIVFP1
+//   SearchSegments the read path of CollectionImpl::Search over flat segments
+//                  (src/engine/collection_impl.cc:1036-1112): PrepareQuery, per-segment
+//                  filtered scan, (dist, part, row) merge with one hit per external id
+//
+// Differences, all forced by the device: filters are dense bitmasks (DenseRowFilter) rather
+// than a virtual allowed() per row; searches return a Status (vdb's return void), since a
+// device call can fail; every search also has a batched form.  Header-only; link libvdbg.so.
+#pragma once
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <span>
+#include <string>
+#include <string_view>
+#include <utility>
+#include <vector>
+
+#include "vdbg.h"
+
+namespace vdbg {
+
+// ---------------------------------------------------------------- vocabulary (vdb's)
+
+enum class Metric : uint8_t { L2 = 0, InnerProduct = 1, Cosine = 2 };  // types.h:13-17
+using InternalId = uint32_t;
+using VectorId = uint64_t;
+constexpr InternalId kNoRow = 0xffffffffu;
+
+// Neighbor::operator< (types.h:23-25): distance, then id.
+struct Neighbor {
+  float dist = 0.f;
+  InternalId id = 0;
+  bool operator<(const Neighbor& o) const { return dist < o.dist || (dist == o.dist && id < o.id); }
+  bool operator==(const Neighbor& o) const = default;
+};
+
+constexpr size_t PaddedDim(size_t dim) { return (dim + 15) / 16 * 16; }  // types.h:30-32
+
+// The fields of SearchParams (options.h:63-71) that the scans read.
+struct SearchParams {
+  size_t ef = 64;      // SQ8: depth = max(ef, k) when rerank < 0 (hnsw_index.cc:88)
+  size_t nprobe = 16;  // IVF lists to scan
+  int rerank = -1;     // -1 = auto, 0 = none
+};
+
+// The fields of IndexOptions (options.h:20-33) the builds read, plus the k-means iteration
+// count (KMeansOptions::iters, src/index/quant/kmeans.h:13-20; vdb's build uses 25).
+struct IndexOptions {
+  size_t pq_m = 16;
+  size_t nlist = 1024;
+  size_t max_train_points_per_centroid = 256;
+  uint64_t seed = 42;
+  size_t kmeans_iters = 25;
+};
+
+struct IndexSearchStats {  // index.h:29-32
+  uint64_t distance_computations = 0;
+  size_t ef = 0;
+};
+
+// A segment's float rows: VectorView (src/util/aligned_buffer.h:56-63).
+struct VectorView {
+  const float* data = nullptr;
+  size_t rows = 0, dim = 0, padded_dim = 0;
+  const float* row(size_t r) const { return data + r * padded_dim; }
+};
+
+// vdb::Status with the same code numbering (include/vdb/status.h:14-26).
+class Status {
+ public:
+  Status() = default;
+  Status(int code, std::string msg) : code_(code), msg_(std::move(msg)) {}
+  static Status OK() { return {}; }
+  // The status of a C ABI call: its return code and the thread's last message.
+  static Status FromCall(int rc) { return rc == VDBG_OK ? Status() : Status(rc, vdbg_last_error()); }
+  bool ok() const { return code_ == VDBG_OK; }
+  int code() const { return code_; }
+  const std::string& message() const { return msg_; }
+  std::string ToString() const { return ok() ? "OK" : std::to_string(code_) + ": " + msg_; }
+
+ private:
+  int code_ = VDBG_OK;
+  std::string msg_;
+};
+
+#define VDBG_CXX_RETURN_IF_ERROR(expr)   \
+  do {                                   \
+    ::vdbg::Status s_ = (expr);          \
+    if (!s_.ok()) return s_;             \
+  } while (0)
+
+// RowFilter as a dense bitmask: bit r of word r / 64 set = row r allowed.  DeleteFilter
+// (src/engine/planner.cc:12-19) is FromDeleted(DeleteBits words); BitmapFilter (:21-29) is the
+// roaring result minus deletes, expanded with Allow().
+class DenseRowFilter {
+ public:
+  DenseRowFilter() = default;
+  explicit DenseRowFilter(size_t rows, bool all = false)
+      : rows_(rows), words_((rows + 63) / 64, all ? ~uint64_t(0) : 0) {}
+  static DenseRowFilter FromWords(const uint64_t* words, size_t rows) {
+    DenseRowFilter f(rows);
+    std::memcpy(f.words_.data(), words, f.words_.size() * sizeof(uint64_t));
+    return f;
+  }
+  // Every row not set in the deletion words (DeleteBits::test, delete_bits.h:50-55).
+  static DenseRowFilter FromDeleted(const uint64_t* deleted_words, size_t rows) {
+    DenseRowFilter f(rows);
+    for (size_t i = 0; i < f.words_.size(); ++i) f.words_[i] = ~deleted_words[i];
+    return f;
+  }
+  void Allow(InternalId r) { words_[r >> 6] |= uint64_t(1) << (r & 63); }
+  void Deny(InternalId r) { words_[r >> 6] &= ~(uint64_t(1) << (r & 63)); }
+  bool allowed(InternalId r) const { return r < rows_ && ((words_[r >> 6] >> (r & 63)) & 1u); }
+  const uint64_t* words() const { return words_.data(); }
+  size_t rows() const { return rows_; }
+
+ private:
+  size_t rows_ = 0;
+  std::vector<uint64_t> words_;
+};
+
+// ---------------------------------------------------------------- device
+
+// One GPU, its stream and workspace (vdbg_ctx).  Calls on one Device are serialised; use
+// one Device per thread for concurrency.
+class Device {
+ public:
+  static Status Open(int ordinal, std::unique_ptr<Device>* out) {
+    vdbg_ctx* c = nullptr;
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_ctx_create(ordinal, &c)));
+    out->reset(new Device(c));
+    return Status::OK();
+  }
+  ~Device() { vdbg_ctx_destroy(ctx_); }
+  Device(const Device&) = delete;
+  Device& operator=(const Device&) = delete;
+  vdbg_ctx* get() const { return ctx_; }
+  // Queries whose certificate failed in the last flat/SQ8 search and were re-scanned exactly.
+  uint64_t last_fallbacks() const {
+    uint64_t n = 0;
+    vdbg_last_fallbacks(ctx_, &n);
+    return n;
+  }
+
+ private:
+  explicit Device(vdbg_ctx* c) : ctx_(c) {}
+  vdbg_ctx* ctx_;
+};
+
+namespace detail {
+
+// [nq][k] padded ids/dists -> one ascending Neighbor list per query (padding dropped).
+inline void Unpack(const std::vector<uint32_t>& ids, const std::vector<float>& d, size_t nq,
+                   size_t k, std::vector<std::vector<Neighbor>>& out) {
+  out.assign(nq, {});
+  for (size_t q = 0; q < nq; ++q) {
+    auto& o = out[q];
+    o.reserve(k);
+    for (size_t i = 0; i < k && ids[q * k + i] != kNoRow; ++i) o.push_back({d[q * k + i], ids[q * k + i]});
+  }
+}
+
+struct DatasetDeleter {
+  void operator()(vdbg_dataset* d) const { vdbg_dataset_destroy(d); }
+};
+using DatasetPtr = std::unique_ptr<vdbg_dataset, DatasetDeleter>;
+
+inline Status MakeDataset(Device& dev, Metric m, const VectorView& v, DatasetPtr* out) {
+  vdbg_dataset* d = nullptr;
+  VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(
+      vdbg_dataset_create(dev.get(), v.data, v.rows, v.dim, v.padded_dim, int(m), &d)));
+  out->reset(d);
+  return Status::OK();
+}
+
+}  // namespace detail
+
+// ---------------------------------------------------------------- flat
+
+// FlatIndex: exact search over the resident rows (flat_index.cc:11-39, 70-83).
+class GpuFlatIndex {
+ public:
+  static Status Create(Device& dev, Metric metric, const VectorView& v,
+                       std::unique_ptr<GpuFlatIndex>* out) {
+    detail::DatasetPtr d;
+    VDBG_CXX_RETURN_IF_ERROR(detail::MakeDataset(dev, metric, v, &d));
+    out->reset(new GpuFlatIndex(dev, metric, v, std::move(d)));
+    return Status::OK();
+  }
+  const char* type() const { return "flat"; }
+  Status build() { return Status::OK(); }  // nothing to train: rows are resident
+  size_t size() const { return view_.rows; }
+  size_t memory_bytes() const { return 0; }  // FlatIndex holds no structures beyond the rows
+  Metric metric() const { return metric_; }
+  const VectorView& view() const { return view_; }
+  vdbg_dataset* dataset() const { return ds_.get(); }
+
+  // FlatIndex::search: the k nearest allowed rows, closest first; stats as :75-76 counts.
+  Status search(const float* q, size_t k, const SearchParams& p, const DenseRowFilter* filter,
+                std::vector<Neighbor>& out, IndexSearchStats* stats) const {
+    std::vector<std::vector<Neighbor>> all;
+    VDBG_CXX_RETURN_IF_ERROR(search_batch(q, 1, k, p, filter, all, stats));
+    out = std::move(all[0]);
+    return Status::OK();
+  }
+  // FlatSearchBatch (flat_index.cc:41-68): the same results as search() per query.
+  Status search_batch(const float* queries, size_t nq, size_t k, const SearchParams&,
+                      const DenseRowFilter* filter, std::vector<std::vector<Neighbor>>& out,
+                      IndexSearchStats* stats) const {
+    std::vector<uint32_t> ids(nq * k);
+    std::vector<float> d(nq * k);
+    uint64_t dc = 0;
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_flat_search_host(
+        ds_.get(), queries, nq, k, filter ? filter->words() : nullptr, ids.data(), d.data(), &dc)));
+    detail::Unpack(ids, d, nq, k, out);
+    if (stats) stats->distance_computations += dc;
+    return Status::OK();
+  }
+
+ private:
+  GpuFlatIndex(Device& dev, Metric m, const VectorView& v, detail::DatasetPtr d)
+      : dev_(dev), metric_(m), view_(v), ds_(std::move(d)) {}
+  Device& dev_;
+  Metric metric_;
+  VectorView view_;
+  detail::DatasetPtr ds_;
+};
+
+// ---------------------------------------------------------------- SQ8
+
+// HnswSq8Index's quantized scan (hnsw_index.h:44-95, hnsw_index.cc:66-100) without the graph:
+// build() trains Sq8Quantizer on the rows and encodes them; search scores every code with
+// the asymmetric SQ8 distance into TopK(depth), depth = rerank < 0 ? max(ef, k) : rerank,
+// then reranks with the float rows (depth 0: top k by SQ8 distance).
+class GpuSq8Index {
+ public:
+  static Status Create(Device& dev, Metric metric, const VectorView& v,
+                       std::unique_ptr<GpuSq8Index>* out) {
+    detail::DatasetPtr d;
+    VDBG_CXX_RETURN_IF_ERROR(detail::MakeDataset(dev, metric, v, &d));
+    out->reset(new GpuSq8Index(dev, metric, v, std::move(d)));
+    return Status::OK();
+  }
+  ~GpuSq8Index() {
+    if (sq_) vdbg_sq8_destroy(sq_);
+  }
+  const char* type() const { return "sq8_scan"; }
+  Status build() {
+    vmin_.assign(view_.padded_dim, 0.f);
+    scale_.assign(view_.padded_dim, 0.f);
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_sq8_train(ds_.get(), vmin_.data(), scale_.data())));
+    return encode();
+  }
+  // A deserialised quantizer (Sq8Quantizer::deserialize, sq8.cc:48-63) instead of training.
+  Status build_with(std::span<const float> vmin, std::span<const float> scale) {
+    vmin_.assign(vmin.begin(), vmin.end());
+    scale_.assign(scale.begin(), scale.end());
+    return encode();
+  }
+  size_t size() const { return view_.rows; }
+  size_t code_bytes() const { return view_.rows * view_.padded_dim; }
+  size_t memory_bytes() const { return code_bytes() + 2 * view_.padded_dim * sizeof(float); }
+  const std::vector<float>& vmin() const { return vmin_; }
+  const std::vector<float>& scale() const { return scale_; }
+  Status codes(std::vector<uint8_t>* out) const {
+    out->resize(code_bytes());
+    return Status::FromCall(vdbg_sq8_codes(sq_, out->data()));
+  }
+  static size_t Depth(const SearchParams& p, size_t k) {
+    return p.rerank < 0 ? std::max(p.ef, k) : size_t(p.rerank);
+  }
+
+  Status search(const float* q, size_t k, const SearchParams& p, const DenseRowFilter* filter,
+                std::vector<Neighbor>& out, IndexSearchStats* stats) const {
+    std::vector<std::vector<Neighbor>> all;
+    VDBG_CXX_RETURN_IF_ERROR(search_batch(q, 1, k, p, filter, all, stats));
+    out = std::move(all[0]);
+    return Status::OK();
+  }
+  Status search_batch(const float* queries, size_t nq, size_t k, const SearchParams& p,
+                      const DenseRowFilter* filter, std::vector<std::vector<Neighbor>>& out,
+                      IndexSearchStats* stats) const {
+    if (sq_ == nullptr) return Status(VDBG_FAILED_PRECONDITION, "build() first");
+    std::vector<uint32_t> ids(nq * k);
+    std::vector<float> d(nq * k);
+    uint64_t dc = 0;
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(
+        vdbg_sq8_search_host(sq_, queries, nq, k, Depth(p, k), filter ? filter->words() : nullptr,
+                             ids.data(), d.data(), &dc)));
+    detail::Unpack(ids, d, nq, k, out);
+    if (stats) stats->distance_computations += dc;
+    return Status::OK();
+  }
+
+ private:
+  GpuSq8Index(Device& dev, Metric m, const VectorView& v, detail::DatasetPtr d)
+      : dev_(dev), metric_(m), view_(v), ds_(std::move(d)) {}
+  Status encode() {
+    if (sq_) vdbg_sq8_destroy(sq_);
+    sq_ = nullptr;
+    return Status::FromCall(vdbg_sq8_create(ds_.get(), vmin_.data(), scale_.data(), &sq_));
+  }
+  Device& dev_;
+  Metric metric_;
+  VectorView view_;
+  detail::DatasetPtr ds_;
+  vdbg_sq8* sq_ = nullptr;
+  std::vector<float> vmin_, scale_;
+};
+
+// ---------------------------------------------------------------- IVF-PQ
+
+// IvfPqIndex (ivf_pq.h:42-81): build() trains and fills the lists on the GPU, Load() reads a
+// VDBIVFP1 file (LoadIndex + IvfPqIndex::load, index.cc:38-87, ivf_pq.cc:251-278), Save()
+// writes one (Index::save, ivf_pq.cc:236-249); search follows ivf_pq.cc:169-222.
+class GpuIvfPqIndex {
+ public:
+  static Status Create(Device& dev, const IndexOptions& opts, Metric metric, const VectorView& v,
+                       std::unique_ptr<GpuIvfPqIndex>* out) {
+    if (opts.pq_m == 0 || v.dim % opts.pq_m != 0)
+      return Status(VDBG_INVALID_ARGUMENT, "pq_m must divide dim");  // index.cc:27-29
+    detail::DatasetPtr d;
+    VDBG_CXX_RETURN_IF_ERROR(detail::MakeDataset(dev, metric, v, &d));
+    out->reset(new GpuIvfPqIndex(dev, opts, metric, v, std::move(d)));
+    return Status::OK();
+  }
+  ~GpuIvfPqIndex() {
+    if (ix_) vdbg_ivfpq_destroy(ix_);
+  }
+  const char* type() const { return "ivf_pq"; }
+  Status build() {
+    reset();
+    return Status::FromCall(vdbg_ivfpq_build(ds_.get(), opts_.nlist, opts_.pq_m, opts_.seed,
+                                             opts_.max_train_points_per_centroid,
+                                             opts_.kmeans_iters, &ix_));
+  }
+  Status Load(std::string_view file) {
+    reset();
+    return Status::FromCall(vdbg_ivfpq_load(ds_.get(), file.data(), file.size(), &ix_));
+  }
+  Status Save(std::string* file) const {
+    size_t len = 0;
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_ivfpq_save(ix_, nullptr, 0, &len)));
+    file->resize(len);
+    return Status::FromCall(vdbg_ivfpq_save(ix_, file->data(), len, &len));
+  }
+  size_t size() const { return view_.rows; }
+  size_t nlist() const { return info().nlist; }
+  size_t m() const { return info().m; }
+  bool precomputed_tables() const { return info().pre != 0; }
+  std::vector<uint64_t> list_sizes() const {
+    std::vector<uint64_t> s(nlist());
+    vdbg_ivfpq_list_sizes(ix_, s.data());
+    return s;
+  }
+  size_t code_bytes() const { return view_.rows * m(); }
+
+  Status search(const float* q, size_t k, const SearchParams& p, const DenseRowFilter* filter,
+                std::vector<Neighbor>& out, IndexSearchStats* stats) const {
+    std::vector<std::vector<Neighbor>> all;
+    VDBG_CXX_RETURN_IF_ERROR(search_batch(q, 1, k, p, filter, all, stats));
+    out = std::move(all[0]);
+    return Status::OK();
+  }
+  Status search_batch(const float* queries, size_t nq, size_t k, const SearchParams& p,
+                      const DenseRowFilter* filter, std::vector<std::vector<Neighbor>>& out,
+                      IndexSearchStats* stats) const {
+    if (ix_ == nullptr) return Status(VDBG_FAILED_PRECONDITION, "build() or Load() first");
+    std::vector<uint32_t> ids(nq * k);
+    std::vector<float> d(nq * k);
+    std::vector<uint64_t> dc(nq);
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_ivfpq_search_host(
+        ix_, queries, nq, k, p.nprobe, p.rerank, filter ? filter->words() : nullptr, ids.data(),
+        d.data(), dc.data())));
+    detail::Unpack(ids, d, nq, k, out);
+    if (stats)
+      for (uint64_t c : dc) stats->distance_computations += c;
+    return Status::OK();
+  }
+
+ private:
+  struct Info {
+    size_t nlist = 0, m = 0;
+    int pre = 0;
+  };
+  GpuIvfPqIndex(Device& dev, const IndexOptions& o, Metric metric, const VectorView& v,
+                detail::DatasetPtr d)
+      : dev_(dev), opts_(o), metric_(metric), view_(v), ds_(std::move(d)) {}
+  Info info() const {
+    Info i;
+    if (ix_) vdbg_ivfpq_info(ix_, &i.nlist, &i.m, &i.pre);
+    return i;
+  }
+  void reset() {
+    if (ix_) vdbg_ivfpq_destroy(ix_);
+    ix_ = nullptr;
+  }
+  Device& dev_;
+  IndexOptions opts_;
+  Metric metric_;
+  VectorView view_;
+  detail::DatasetPtr ds_;
+  vdbg_ivfpq* ix_ = nullptr;
+};
+
+// ---------------------------------------------------------------- collection read path
+
+// A flat segment as CollectionImpl::Search sees it: its index, the rows a query may return
+// (deletes and filter applied; nullptr = all) and the external id of every row.
+struct SegmentRef {
+  const GpuFlatIndex* index = nullptr;
+  const DenseRowFilter* allowed = nullptr;
+  const VectorId* external_ids = nullptr;
+};
+
+struct SearchHit {  // include/vdb/types.h SearchHit: id, distance, score
+  VectorId id = 0;
+  float distance = 0.f;
+  float score = 0.f;  // -distance for inner product and cosine, distance for L2
+};
+
+// CollectionImpl::Search (collection_impl.cc:1036-1112) for nq raw queries of dim floats
+// over flat segments of one metric: PrepareQuery (:1023-1034), each segment's filtered
+// exact scan, the merge by (dist, part, row) keeping the first hit of each external id.
+inline Status SearchSegments(Device& dev, std::span<const SegmentRef> segs, Metric metric,
+                             const float* raw_queries, size_t nq, size_t dim, size_t k,
+                             std::vector<std::vector<SearchHit>>& out,
+                             IndexSearchStats* stats = nullptr) {
+  if (k == 0 || k > 10000) return Status(VDBG_INVALID_ARGUMENT, "k must be in 1..10000");
+  const size_t pd = PaddedDim(dim);
+  std::vector<float> q(nq * pd);
+  VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(
+      vdbg_prepare_queries_host(dev.get(), raw_queries, nq, dim, pd, int(metric), q.data())));
+  const size_t np = segs.size();
+  std::vector<float> pdist(np * nq * k);
+  std::vector<uint32_t> prow(np * nq * k);
+  std::vector<uint64_t> ext, off(np);
+  for (size_t p = 0; p < np; ++p) {
+    const GpuFlatIndex* ix = segs[p].index;
+    uint64_t dc = 0;
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_flat_search_host(
+        ix->dataset(), q.data(), nq, k, segs[p].allowed ? segs[p].allowed->words() : nullptr,
+        prow.data() + p * nq * k, pdist.data() + p * nq * k, &dc)));
+    if (stats) stats->distance_computations += dc;
+    off[p] = ext.size();
+    ext.insert(ext.end(), segs[p].external_ids, segs[p].external_ids + ix->size());
+  }
+  std::vector<uint64_t> oe(nq * k);
+  std::vector<float> od(nq * k);
+  VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(
+      vdbg_merge_parts_host(dev.get(), nq, np, k, pdist.data(), prow.data(), ext.data(),
+                            ext.size(), off.data(), oe.data(), od.data())));
+  out.assign(nq, {});
+  for (size_t i = 0; i < nq; ++i)
+    for (size_t j = 0; j < k && oe[i * k + j] != ~uint64_t(0); ++j)
+      out[i].push_back({oe[i * k + j], od[i * k + j],
+                        metric == Metric::L2 ? od[i * k + j] : -od[i * k + j]});
+  return Status::OK();
+}
+
+}  // namespace vdbg
