@@ -116,21 +116,41 @@ class DenseRowFilter {
     std::memcpy(f.words_.data(), words, f.words_.size() * sizeof(uint64_t));
     return f;
   }
+  // A view of words the caller keeps alive (no copy); Allow/Deny copy them first.
+  static DenseRowFilter View(const uint64_t* words, size_t rows) {
+    DenseRowFilter f;
+    f.rows_ = rows;
+    f.view_ = words;
+    return f;
+  }
   // Every row not set in the deletion words (DeleteBits::test, delete_bits.h:50-55).
   static DenseRowFilter FromDeleted(const uint64_t* deleted_words, size_t rows) {
     DenseRowFilter f(rows);
     for (size_t i = 0; i < f.words_.size(); ++i) f.words_[i] = ~deleted_words[i];
     return f;
   }
-  void Allow(InternalId r) { words_[r >> 6] |= uint64_t(1) << (r & 63); }
-  void Deny(InternalId r) { words_[r >> 6] &= ~(uint64_t(1) << (r & 63)); }
-  bool allowed(InternalId r) const { return r < rows_ && ((words_[r >> 6] >> (r & 63)) & 1u); }
-  const uint64_t* words() const { return words_.data(); }
+  void Allow(InternalId r) {
+    own();
+    words_[r >> 6] |= uint64_t(1) << (r & 63);
+  }
+  void Deny(InternalId r) {
+    own();
+    words_[r >> 6] &= ~(uint64_t(1) << (r & 63));
+  }
+  bool allowed(InternalId r) const { return r < rows_ && ((words()[r >> 6] >> (r & 63)) & 1u); }
+  const uint64_t* words() const { return view_ != nullptr ? view_ : words_.data(); }
   size_t rows() const { return rows_; }
 
  private:
+  void own() {
+    if (view_ != nullptr) {
+      words_.assign(view_, view_ + (rows_ + 63) / 64);
+      view_ = nullptr;
+    }
+  }
   size_t rows_ = 0;
   std::vector<uint64_t> words_;
+  const uint64_t* view_ = nullptr;
 };
 
 // ---------------------------------------------------------------- device
