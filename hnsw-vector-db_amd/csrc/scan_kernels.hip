@@ -91,35 +91,57 @@ struct RowStatsDev {
   int all_int;
 };
 
-// One wave per row: ||x||^2 (lane-strided fmaf, wave sum), min, max, max |x|, integrality,
-// folded in with atomics.
+// Rows are spread over the waves of the grid: per row ||x||^2 (lane-strided fmaf, wave sum);
+// min, max, max |x|, the largest norm and integrality are kept per wave, reduced per block
+// in LDS and folded into the result with one set of atomics per block.
 __global__ __launch_bounds__(256) void k_row_stats(const float* __restrict__ X, size_t n,
                                                    int pd, float* __restrict__ norms,
                                                    RowStatsDev* __restrict__ st) {
-  const size_t r = blockIdx.x * size_t(4) + (threadIdx.x >> 6);
-  if (r >= n) return;
-  const float* x = X + r * size_t(pd);
-  float s = 0.f, lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f;
+  __shared__ float red[4][4];
+  __shared__ int red_i[4];
+  const int wave = threadIdx.x >> 6;
+  const size_t nwaves = size_t(gridDim.x) * 4;
+  float lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f, xn = 0.f;
   int ai = 1;
-  for (int i = lane_id(); i < pd; i += kWave) {
-    const float e = x[i];
-    s = fmaf(e, e, s);
-    lo = fminf(lo, e);
-    hi = fmaxf(hi, e);
-    ma = fmaxf(ma, fabsf(e));
-    ai &= (e == rintf(e)) ? 1 : 0;
+  for (size_t r = blockIdx.x * size_t(4) + wave; r < n; r += nwaves) {
+    const float* x = X + r * size_t(pd);
+    float s = 0.f;
+    for (int i = lane_id(); i < pd; i += kWave) {
+      const float e = x[i];
+      s = fmaf(e, e, s);
+      lo = fminf(lo, e);
+      hi = fmaxf(hi, e);
+      ma = fmaxf(ma, fabsf(e));
+      ai &= (e == rintf(e)) ? 1 : 0;
+    }
+    s = wave_sum(s);
+    if (lane_id() == 0) norms[r] = s;
+    xn = fmaxf(xn, s);
   }
-  s = wave_sum(s);
   lo = wave_min(lo);
   hi = wave_max(hi);
   ma = wave_max(ma);
   ai = wave_and(ai);
   if (lane_id() == 0) {
-    norms[r] = s;
+    red[wave][0] = lo;
+    red[wave][1] = hi;
+    red[wave][2] = ma;
+    red[wave][3] = xn;
+    red_i[wave] = ai;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < 4; ++w) {
+      lo = fminf(lo, red[w][0]);
+      hi = fmaxf(hi, red[w][1]);
+      ma = fmaxf(ma, red[w][2]);
+      xn = fmaxf(xn, red[w][3]);
+      ai &= red_i[w];
+    }
     atomicMin(&st->lo, ord_enc(lo));
     atomicMax(&st->hi, ord_enc(hi));
     atomicMax(&st->max_abs, __float_as_uint(ma));
-    atomicMax(&st->xn_max, __float_as_uint(s));
+    atomicMax(&st->xn_max, __float_as_uint(xn));
     if (!ai) atomicAnd(&st->all_int, 0);
   }
 }
@@ -132,7 +154,8 @@ int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
   VDBG_HIP(hipMemcpyAsync(d, &init, sizeof(init), hipMemcpyHostToDevice, s));
   if (n > 0) {
     ProfScope ps(c, "row_stats", s);
-    k_row_stats<<<dim3(unsigned((n + 3) / 4)), 256, 0, s>>>(rows, n, int(pd), norms, d);
+    const size_t blocks = std::min<size_t>((n + 3) / 4, size_t(c->cu_count) * 8);
+    k_row_stats<<<dim3(unsigned(blocks)), 256, 0, s>>>(rows, n, int(pd), norms, d);
     VDBG_HIP(hipGetLastError());
   }
   RowStatsDev h;
@@ -682,28 +705,41 @@ struct KthArgs {
   float* T;
 };
 
+__device__ __forceinline__ float ord_dec_dev(uint32_t e) {
+  return __uint_as_float((e & 0x80000000u) ? (e & 0x7fffffffu) : ~e);
+}
+
 // One wave per query: the kk-th smallest group minimum A.  The kk groups at or below A hold
 // kk distinct rows with GEMM value <= A, so the kk-th smallest exact distance is at most
 // A + shift + eb and every row of the true top kk has GEMM value <= A + 2 eb.
-template <int E>
+// A is found by a bitwise radix select over the order-preserving encodings, held V per lane:
+// from the top bit down, the answer keeps a 0 bit when at least kk keys lie at or below the
+// prefix with all lower bits set (ballot + popcount, no cross-lane data movement).
+template <int V>
 __global__ __launch_bounds__(256) void k_kth(KthArgs a) {
   const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= a.nq) return;
-  WaveTopK<E> top;
-  top.init();
+  const int lane = lane_id();
   const float* g = a.gm + size_t(q) * a.ngroups;
-  for (int i0 = 0; i0 < a.ngroups; i0 += kWave) {
-    const int i = i0 + lane_id();
-    top.insert(i < a.ngroups ? g[i] : __builtin_inff(), i < a.ngroups ? uint32_t(i) : kNoId);
-  }
-  const int kth = a.kk - 1;
-  float v = __builtin_inff();
+  uint32_t key[V];
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const float t = __shfl(top.k.d[e], kth & (kWave - 1));
-    if (e == kth / kWave) v = t;
+  for (int v = 0; v < V; ++v) {
+    const int i = v * kWave + lane;
+    key[v] = i < a.ngroups ? ord_enc(g[i]) : 0xffffffffu;
   }
-  if (lane_id() == 0) a.T[q] = v < __builtin_inff() ? v + 2.f * a.eb[q] : __builtin_inff();
+  float A = __builtin_inff();
+  if (a.kk <= a.ngroups) {
+    uint32_t ans = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t t = ans | ((1u << bit) - 1u);
+      int cnt = 0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) cnt += __popcll(__ballot(key[v] <= t));
+      if (cnt < a.kk) ans |= 1u << bit;
+    }
+    A = ord_dec_dev(ans);
+  }
+  if (lane == 0) a.T[q] = A < __builtin_inff() ? A + 2.f * a.eb[q] : __builtin_inff();
 }
 
 // ================================================================ selection / merge
@@ -777,21 +813,25 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   top.init();
   const float* qv = a.Q + size_t(q) * a.pd;
   const uint2* cbase = a.cand + size_t(src) * a.nseg * size_t(a.cap);
-  for (uint32_t g0 = 0; g0 < total; g0 += kWave) {
-    const uint32_t g = g0 + lane;
-    float d = __builtin_inff();
-    uint32_t id = kNoId;
-    if (g < total) {
-      int lo = 0, hi = a.nseg;  // largest s with pre[s] <= g
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (pre[mid] <= g) lo = mid; else hi = mid;
-      }
-      const uint2 c = cbase[size_t(lo) * a.cap + (g - pre[lo])];
-      id = c.y;
-      d = a.rescore == 2 ? sc(qv, id) : __uint_as_float(c.x);
+  // candidate g of the flat order: the segment is the largest s with pre[s] <= g
+  auto fetch = [&](uint32_t g) -> uint2 {
+    if (g >= total) return make_uint2(__float_as_uint(__builtin_inff()), kNoId);
+    int lo = 0, hi = a.nseg;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (pre[mid] <= g) lo = mid; else hi = mid;
     }
+    return cbase[size_t(lo) * a.cap + (g - pre[lo])];
+  };
+  // the next batch is loaded before the current one is inserted (hides the load latency)
+  uint2 cur = fetch(lane);
+  for (uint32_t g0 = 0; g0 < total; g0 += kWave) {
+    const uint2 nxt = fetch(g0 + kWave + lane);
+    const uint32_t id = cur.y;
+    float d = __uint_as_float(cur.x);
+    if (a.rescore == 2 && id != kNoId) d = sc(qv, id);
     top.insert(d, id);
+    cur = nxt;
   }
 
   constexpr int N = kWave * E;
@@ -999,9 +1039,24 @@ template <int E, class Scorer>
 static void launch_scan(hipStream_t s, const ScanArgs& a, const Scorer& sc) {
   k_exact_scan<E, Scorer><<<dim3(a.nslots, a.nsplit), 256, 0, s>>>(a, sc);
 }
-template <int E>
-static void launch_kth(hipStream_t s, const KthArgs& a) {
-  k_kth<E><<<dim3((a.nq + 3) / 4), 256, 0, s>>>(a);
+template <int V>
+static void launch_kth_v(hipStream_t s, const KthArgs& a) {
+  k_kth<V><<<dim3((a.nq + 3) / 4), 256, 0, s>>>(a);
+}
+static int LaunchKth(hipStream_t s, const KthArgs& a) {
+  int v = 1;
+  while (v * kWave < a.ngroups) v <<= 1;
+  switch (v) {
+    case 1: launch_kth_v<1>(s, a); break;
+    case 2: launch_kth_v<2>(s, a); break;
+    case 4: launch_kth_v<4>(s, a); break;
+    case 8: launch_kth_v<8>(s, a); break;
+    case 16: launch_kth_v<16>(s, a); break;
+    case 32: launch_kth_v<32>(s, a); break;
+    case 64: launch_kth_v<64>(s, a); break;
+    default: return SetError(kInternal, "threshold: more than 4096 sample groups");
+  }
+  return kOk;
 }
 template <int E>
 static void launch_rerank(hipStream_t s, const RerankArgs& a) {
@@ -1184,7 +1239,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   }
   const uint32_t N = src->N;
   const size_t pd = src->pd;
-  const bool gemm = GemmSupported(pd) && N >= 1024 && nq >= 32;
+  const bool gemm = GemmSupported(pd) && N >= 1024;
   if (!gemm) return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
   VDBG_RETURN_IF_ERROR(BuildSample(c, src, s));
 
@@ -1208,9 +1263,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   int caph = 32;
   while (caph < 3.0 * expect_seg + 32) caph <<= 1;
   const int nseg = 2 * nchunks;
-  const int Ek = pow2_e(kk);
   const int Esel = pow2_e(kk + 16);
-  if (Esel > 4) return SetError(kNotSupported, "k too large for the GEMM path");
+  if (Esel > 4)  // the select keeps K' = kk + 16 or more: the exact scan serves kk in (240, 256]
+    return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
 
   Workspace& w = c->ws;
   w.used = 0;
@@ -1268,7 +1323,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   KthArgs ka{gm, ngroups, int(nq), int(kk), eb, T};
   {
     ProfScope ps(c, "kth", s);
-    VDBG_DISPATCH_E(Ek, launch_kth, s, ka);
+    VDBG_RETURN_IF_ERROR(LaunchKth(s, ka));
     VDBG_HIP(hipGetLastError());
   }
 
