@@ -36,6 +36,7 @@ int IvfTerm2(Ctx* c, const float* coarse, int nlist, int pd, const float* cen, i
 int IvfQtab(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,
             int twice, float* qtab, hipStream_t s);
 int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s);
+int IvfScanDeep(Ctx* c, const IvfScanArgs& a, hipStream_t s);
 
 // Index::save / LoadIndex framing (src/index/index.cc:38-56, 110-128): magic, body, CRC32C
 // (reflected Castagnoli polynomial 0x82F63B78) of everything before the 4-byte footer.
@@ -232,7 +233,7 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
   const size_t nprobe = std::clamp<size_t>(nprobe_req, 1, size_t(x->nlist));
   const size_t depth = rerank < 0 ? std::max<size_t>(10 * k, 100) : size_t(rerank);
   const size_t R = std::max(depth, k);
-  if (R > 256) return SetError(kNotSupported, "IVF-PQ: max(rerank, k) > 256 on the GPU path");
+  if (k > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
   const bool l2 = x->metric == 0;
   const bool pre = l2 && x->term2 != nullptr;
   const size_t ts = size_t(x->m) * 256;
@@ -257,7 +258,7 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
     IvfScanArgs a{Q, x->pd, x->dim, x->m, x->dsub, x->metric, x->coarse_ds->d.rows, x->cen,
                   x->off, x->ids, x->codes, x->term2, qtab, probe, probe_d, int(nprobe),
                   int(nq), allow, int(R), ti, td, dc_dev, uint64_t(x->nlist), depth > 0 ? 1 : 0};
-    rc = IvfScan(c, a, s);
+    rc = R <= 256 ? IvfScan(c, a, s) : IvfScanDeep(c, a, s);
   }
   if (rc == kOk && depth > 0) {
     rc = Rerank(c, x->ds->rows, x->pd, x->metric, Q, nq, ti, R, k, out_ids, out_d, s);

@@ -14,6 +14,7 @@
 
 #include <algorithm>
 #include <cstring>
+#include <vector>
 
 #include "vdbg_device.h"
 #include "vdbg_internal.h"
@@ -627,6 +628,167 @@ int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
   }
   VDBG_HIP(hipGetLastError());
   return kOk;
+}
+
+// ---------------------------------------------------------------- deep top-R
+
+// Candidates per query: the sizes of its probed lists (every code is scored once).
+__global__ void k_probe_counts(const uint32_t* __restrict__ probe, int nprobe, int nq,
+                               const uint32_t* __restrict__ off, uint64_t* __restrict__ cnt) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  uint64_t n = 0;
+  for (int i = 0; i < nprobe; ++i) {
+    const uint32_t l = probe[size_t(q) * nprobe + i];
+    n += off[l + 1] - off[l];
+  }
+  cnt[q] = n;
+}
+
+// One wave per query of the chunk [q0, q0 + nc): the tables and ADC of k_ivf_scan, with
+// every scored code written as a (dist, id) key into the query's segment (disallowed rows
+// get kNoKey), for a segmented sort that keeps TopK(R) when R exceeds the wave top-k.
+__global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_score_all(IvfScanArgs a, int q0, int nc,
+                                                                 const int* __restrict__ seg,
+                                                                 uint64_t* __restrict__ keys) {
+  extern __shared__ float lds[];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int qi = blockIdx.x * kIvfWaves + wave;
+  if (qi >= nc) return;
+  const int q = q0 + qi;
+  const int ts = a.m * kKsub;
+  float* table = lds + size_t(wave) * ts;
+  const float* qv = a.Q + size_t(q) * a.pd;
+  const float* qt = a.qtab + size_t(q) * ts;
+  const bool l2 = a.metric == 0;
+  const bool pre = l2 && a.term2 != nullptr;
+  if (!l2)
+    for (int e = lane; e < ts; e += kWave) table[e] = qt[e];
+  int pos = seg[qi];
+  for (int pi = 0; pi < a.nprobe; ++pi) {
+    const uint32_t l = a.probe[size_t(q) * a.nprobe + pi];
+    const float* cl = a.coarse + size_t(l) * a.pd;
+    float offset = 0.f;
+    __builtin_amdgcn_wave_barrier();
+    if (pre) {
+      offset = a.probe_d[size_t(q) * a.nprobe + pi];
+      const float* t2 = a.term2 + size_t(l) * ts;
+      for (int e = lane; e < ts; e += kWave) table[e] = t2[e] + qt[e];
+    } else if (l2) {
+      for (int e = lane; e < ts; e += kWave) {
+        const int j = e / kKsub;
+        float r[64];
+        for (int t = 0; t < a.dsub; ++t) r[t] = qv[j * a.dsub + t] - cl[j * a.dsub + t];
+        table[e] = l2sq_any(r, a.cen + size_t(e) * a.dsub, a.dsub);
+      }
+    } else {
+      offset = -dot_any(qv, cl, a.dim);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t b = a.off[l], e_ = a.off[l + 1];
+    for (uint32_t i0 = b; i0 < e_; i0 += kWave) {
+      const uint32_t i = i0 + lane;
+      if (i < e_) {
+        const uint32_t id = a.ids[i];
+        uint64_t key = kNoKey;
+        if (row_ok(a.allow, id)) {
+          const uint8_t* cd = a.codes + size_t(i) * a.m;
+          float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+          int j = 0;
+          for (; j + 4 <= a.m; j += 4) {
+            s0 += table[(j + 0) * kKsub + cd[j + 0]];
+            s1 += table[(j + 1) * kKsub + cd[j + 1]];
+            s2 += table[(j + 2) * kKsub + cd[j + 2]];
+            s3 += table[(j + 3) * kKsub + cd[j + 3]];
+          }
+          for (; j < a.m; ++j) s0 += table[j * kKsub + cd[j]];
+          key = dist_key(offset + ((s0 + s1) + (s2 + s3)), id);
+        }
+        keys[pos + int(i - b)] = key;
+      }
+    }
+    pos += int(e_ - b);
+  }
+}
+
+__global__ void k_ivf_dc(const uint32_t* __restrict__ top_ids, int R, int nq,
+                         const uint64_t* __restrict__ cnt, uint64_t base, int count_top,
+                         uint64_t* __restrict__ dc) {
+  const int q = blockIdx.x * blockDim.x + threadIdx.x;
+  if (q >= nq) return;
+  uint64_t v = 0;
+  if (count_top)
+    for (int i = 0; i < R; ++i) v += top_ids[size_t(q) * R + i] != kNoId ? 1 : 0;
+  dc[q] = base + cnt[q] + v;
+}
+
+// The ADC scan for R > 256: every code scored into per-query key segments (chunks of at
+// most 2^25 keys), sorted, the first R kept in out_ids / out_d as the scan's TopK(R).
+int IvfScanDeep(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
+  if (a.nq == 0) return kOk;
+  if (a.m * kKsub > kMaxTable || a.dsub > 64)
+    return SetError(kNotSupported, "IVF-PQ scan: m <= 32 and dim/m <= 64 on the GPU path");
+  const size_t nq = size_t(a.nq);
+  uint64_t* cnt = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&cnt), nq * 8, s));
+  k_probe_counts<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, a.off, cnt);
+  VDBG_HIP(hipGetLastError());
+  std::vector<uint64_t> h(nq);
+  VDBG_HIP(hipMemcpyAsync(h.data(), cnt, nq * 8, hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  constexpr uint64_t kChunkKeys = uint64_t(1) << 25;
+  uint64_t maxc = 0;
+  for (uint64_t v : h) maxc = std::max(maxc, v);
+  const uint64_t cap = std::max(kChunkKeys, maxc);
+  uint64_t* keys = nullptr;
+  int* seg = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&keys), cap * 16 + 16, s));
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&seg), (nq + 1) * sizeof(int), s));
+  const size_t lds = size_t(kIvfWaves) * a.m * kKsub * sizeof(float);
+  int rc = kOk;
+  std::vector<int> off;
+  for (size_t q0 = 0; q0 < nq && rc == kOk;) {
+    off.assign(1, 0);
+    size_t q1 = q0;
+    uint64_t total = 0;
+    while (q1 < nq && (q1 == q0 || total + h[q1] <= cap)) {
+      total += h[q1];
+      off.push_back(int(total));
+      ++q1;
+    }
+    const int nc = int(q1 - q0);
+    if (hipMemcpyAsync(seg, off.data(), off.size() * sizeof(int), hipMemcpyHostToDevice, s) !=
+        hipSuccess) {
+      rc = SetError(kInternal, "segment offsets upload");
+      break;
+    }
+    {
+      ProfScope ps(c, "ivf_scan", s);
+      k_ivf_score_all<<<dim3(unsigned((nc + kIvfWaves - 1) / kIvfWaves)), kIvfWaves * 64, lds, s>>>(
+          a, int(q0), nc, seg, keys);
+    }
+    if (hipGetLastError() != hipSuccess) {
+      rc = SetError(kInternal, "ivf score launch");
+      break;
+    }
+    rc = SortSegmentsTopK(c, keys, keys + cap, seg, nc, int(total), a.R,
+                          a.out_ids + q0 * size_t(a.R), a.out_d + q0 * size_t(a.R), s);
+    // the offsets buffer is rewritten for the next chunk: finish this one first
+    if (rc == kOk && hipStreamSynchronize(s) != hipSuccess) rc = SetError(kInternal, "sync");
+    q0 = q1;
+  }
+  if (rc == kOk && a.dc != nullptr) {
+    k_ivf_dc<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.out_ids, a.R, a.nq, cnt, a.dc_base,
+                                                             a.count_top, a.dc);
+    if (hipGetLastError() != hipSuccess) rc = SetError(kInternal, "dist count launch");
+  }
+  (void)hipStreamSynchronize(s);
+  (void)hipFreeAsync(keys, s);
+  (void)hipFreeAsync(seg, s);
+  (void)hipFreeAsync(cnt, s);
+  return rc;
 }
 
 int PqEncode(Ctx* c, const float* X, uint32_t n, int pd, int dim, const float* coarse,

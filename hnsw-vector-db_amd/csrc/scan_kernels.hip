@@ -68,9 +68,6 @@ static inline float ord_dec(uint32_t e) {
   return f;
 }
 
-__device__ __forceinline__ bool row_allowed(const uint64_t* w, uint32_t r) {
-  return w == nullptr || ((w[r >> 6] >> (r & 63)) & 1ull);
-}
 
 __host__ __device__ __forceinline__ uint32_t bitrev(uint32_t v, int bits) {
   uint32_t r = 0;
@@ -1231,12 +1228,14 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
   c->last_fallbacks = 0;
   if (nq == 0 || kk == 0) return kOk;
-  if (kk > 256) return SetError(kNotSupported, "k > 256 is not supported on the GPU path");
+  if (kk > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
   if (src->N == 0) {
     k_fill_empty<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, out_d, nq * kk);
     VDBG_HIP(hipGetLastError());
     return kOk;
   }
+  // the select keeps K' >= kk + 16 keys in one wavefront (at most 256)
+  if (kk > 240) return ExactScanAll(c, *src, Q, nq, kk, allow, out_ids, out_d, s);
   const uint32_t N = src->N;
   const size_t pd = src->pd;
   const bool gemm = GemmSupported(pd) && N >= 1024;
@@ -1264,8 +1263,6 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   while (caph < 3.0 * expect_seg + 32) caph <<= 1;
   const int nseg = 2 * nchunks;
   const int Esel = pow2_e(kk + 16);
-  if (Esel > 4)  // the select keeps K' = kk + 16 or more: the exact scan serves kk in (240, 256]
-    return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
 
   Workspace& w = c->ws;
   w.used = 0;
@@ -1414,6 +1411,8 @@ int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq
            const uint32_t* cand, size_t depth, size_t k, uint32_t* out_ids, float* out_d,
            hipStream_t s) {
   if (nq == 0 || k == 0) return kOk;
+  if (std::max(depth, k) > 256)
+    return RerankLarge(c, X, pd, metric, Q, nq, cand, depth, k, out_ids, out_d, s);
   const int E = pow2_e(std::max(depth, k));
   RerankArgs ra{X, Q, pd, metric, cand, int(depth), int(nq), int(k), out_ids, out_d};
   ProfScope ps(c, "rerank", s);

@@ -316,9 +316,164 @@ __global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
   }
 }
 
+// ---- the merge for more than 1024 hits per query, by sorting
+//  1. per query, keys (dist, part * k + i) sorted: the (dist, part, row) order, rank r;
+//  2. (external id, r) pairs sorted stably by external id: the first of each id group is
+//     that id's first hit in the (dist, part, row) order;
+//  3. kept[q][r] marks those; one wave per query emits the first k kept in rank order.
+// Queries run in chunks [q0, q0 + nc); the inputs keep the batch's [part][nq][k] layout.
+
+struct MergeChunk {
+  MergeArgs a;
+  int q0, nc;
+  uint32_t per;  // nparts * k
+  __device__ __forceinline__ size_t at(int q, uint32_t cidx) const {
+    const uint32_t p = cidx / uint32_t(a.k), i = cidx - p * uint32_t(a.k);
+    return (size_t(p) * a.nq + (q0 + q)) * a.k + i;
+  }
+  __device__ __forceinline__ uint32_t part(uint32_t cidx) const { return cidx / uint32_t(a.k); }
+};
+
+__global__ void k_mkeys(MergeChunk m, uint64_t* __restrict__ keys) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(m.nc) * m.per) return;
+  const int q = int(t / m.per);
+  const uint32_t cidx = uint32_t(t - size_t(q) * m.per);
+  const size_t at = m.at(q, cidx);
+  keys[t] = m.a.part_rows[at] == kNoId ? kNoKey : dist_key(m.a.part_d[at], cidx);
+}
+
+__global__ void k_mext(MergeChunk m, const uint64_t* __restrict__ sorted,
+                       uint64_t* __restrict__ ext, uint32_t* __restrict__ rank) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(m.nc) * m.per) return;
+  const int q = int(t / m.per);
+  const uint64_t key = sorted[t];
+  rank[t] = uint32_t(t - size_t(q) * m.per);
+  if (key == kNoKey) {  // padding sorts last in step 1, so it follows every real id here
+    ext[t] = ~0ull;
+    return;
+  }
+  const uint32_t cidx = uint32_t(key);
+  ext[t] = m.a.ext[m.a.part_off[m.part(cidx)] + m.a.part_rows[m.at(q, cidx)]];
+}
+
+__global__ void k_mfirst(MergeChunk m, const uint64_t* __restrict__ sorted,
+                         const uint64_t* __restrict__ ext, const uint32_t* __restrict__ rank,
+                         uint8_t* __restrict__ kept) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t >= size_t(m.nc) * m.per) return;
+  const size_t q = t / m.per, j = t - q * m.per;
+  const uint32_t r = rank[t];
+  const bool real = sorted[q * m.per + r] != kNoKey;
+  kept[q * m.per + r] = (real && (j == 0 || ext[t - 1] != ext[t])) ? 1 : 0;
+}
+
+__global__ __launch_bounds__(256) void k_memit(MergeChunk m, const uint64_t* __restrict__ sorted,
+                                               const uint8_t* __restrict__ kept) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= m.nc) return;
+  const int lane = lane_id();
+  const int k = m.a.k;
+  const size_t gq = size_t(m.q0 + q);
+  int written = 0;
+  for (uint32_t r0 = 0; r0 < m.per && written < k; r0 += kWave) {
+    const uint32_t r = r0 + lane;
+    const bool keep = r < m.per && kept[size_t(q) * m.per + r];
+    const uint64_t bal = __ballot(keep);
+    const int pos = written + __popcll(bal & ((1ull << lane) - 1ull));
+    if (keep && pos < k) {
+      const uint64_t key = sorted[size_t(q) * m.per + r];
+      const uint32_t cidx = uint32_t(key);
+      m.a.out_ext[gq * k + pos] = m.a.ext[m.a.part_off[m.part(cidx)] + m.a.part_rows[m.at(q, cidx)]];
+      m.a.out_d[gq * k + pos] = key_dist(key);
+    }
+    written += __popcll(bal);
+  }
+  for (int i = written + lane; i < k; i += kWave) {
+    m.a.out_ext[gq * k + i] = ~0ull;
+    m.a.out_d[gq * k + i] = __builtin_inff();
+  }
+}
+
+__global__ void k_seg_off(int* off, int nseg, int len) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i <= nseg) off[i] = i * len;
+}
+
+static int MergePartsLarge(Ctx* c, const MergeArgs& a, hipStream_t s) {
+  const size_t per = size_t(a.nparts) * a.k;
+  if (per > (size_t(1) << 30)) return SetError(kInvalidArgument, "merge: too many hits per query");
+  const size_t chunk = std::max<size_t>(1, std::min<size_t>(a.nq, (size_t(1) << 24) / per));
+  const size_t n = chunk * per;
+  char* buf = nullptr;
+  const size_t bytes = n * (8 * 4 + 4 * 2 + 1) + (chunk + 1) * 4 + 8 * 256;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&buf), bytes, s));
+  char* p = buf;
+  auto take = [&](size_t b) {
+    char* r = p;
+    p += (b + 255) & ~size_t(255);
+    return r;
+  };
+  uint64_t* k1 = reinterpret_cast<uint64_t*>(take(n * 8));
+  uint64_t* k2 = reinterpret_cast<uint64_t*>(take(n * 8));
+  uint64_t* e1 = reinterpret_cast<uint64_t*>(take(n * 8));
+  uint64_t* e2 = reinterpret_cast<uint64_t*>(take(n * 8));
+  uint32_t* r1 = reinterpret_cast<uint32_t*>(take(n * 4));
+  uint32_t* r2 = reinterpret_cast<uint32_t*>(take(n * 4));
+  uint8_t* kept = reinterpret_cast<uint8_t*>(take(n));
+  int* off = reinterpret_cast<int*>(take((chunk + 1) * 4));
+  void* tmp = nullptr;
+  size_t tmp_cap = 0;
+  int rc = kOk;
+  auto sort_temp = [&](size_t b) -> bool {
+    if (b <= tmp_cap) return true;
+    if (tmp != nullptr) (void)hipFreeAsync(tmp, s);
+    tmp = nullptr;
+    tmp_cap = b;
+    return hipMallocAsync(&tmp, b + 16, s) == hipSuccess;
+  };
+  ProfScope ps(c, "merge_parts", s);
+  for (size_t q0 = 0; q0 < size_t(a.nq) && rc == kOk; q0 += chunk) {
+    MergeChunk m{a, int(q0), int(std::min(chunk, size_t(a.nq) - q0)), uint32_t(per)};
+    const int total = int(size_t(m.nc) * per);
+    const unsigned g = unsigned((size_t(total) + 255) / 256);
+    k_mkeys<<<dim3(g), 256, 0, s>>>(m, k1);
+    k_seg_off<<<dim3(unsigned((m.nc + 256) / 256)), 256, 0, s>>>(off, m.nc, int(per));
+    size_t tb = 0;
+    if (hipcub::DeviceSegmentedRadixSort::SortKeys(nullptr, tb, k1, k2, total, m.nc, off, off + 1,
+                                                   0, 64, s) != hipSuccess ||
+        !sort_temp(tb) ||
+        hipcub::DeviceSegmentedRadixSort::SortKeys(tmp, tb, k1, k2, total, m.nc, off, off + 1, 0,
+                                                   64, s) != hipSuccess) {
+      rc = SetError(kInternal, "merge: sort by distance");
+      break;
+    }
+    k_mext<<<dim3(g), 256, 0, s>>>(m, k2, e1, r1);
+    tb = 0;
+    if (hipcub::DeviceSegmentedRadixSort::SortPairs(nullptr, tb, e1, e2, r1, r2, total, m.nc, off,
+                                                    off + 1, 0, 64, s) != hipSuccess ||
+        !sort_temp(tb) ||
+        hipcub::DeviceSegmentedRadixSort::SortPairs(tmp, tb, e1, e2, r1, r2, total, m.nc, off,
+                                                    off + 1, 0, 64, s) != hipSuccess) {
+      rc = SetError(kInternal, "merge: sort by external id");
+      break;
+    }
+    k_mfirst<<<dim3(g), 256, 0, s>>>(m, k2, e2, r2, kept);
+    k_memit<<<dim3(unsigned((m.nc + 3) / 4)), 256, 0, s>>>(m, k2, kept);
+    if (hipGetLastError() != hipSuccess) rc = SetError(kInternal, "merge launch");
+    // the chunk's buffers are reused by the next chunk: the stream orders that
+  }
+  (void)hipStreamSynchronize(s);
+  if (tmp != nullptr) (void)hipFreeAsync(tmp, s);
+  (void)hipFreeAsync(buf, s);
+  return rc;
+}
+
 int MergeParts(Ctx* c, const MergeArgs& a, hipStream_t s) {
   if (a.nq == 0 || a.k == 0) return kOk;
   const int total = a.nparts * a.k;
+  if (total > 16 * kWave) return MergePartsLarge(c, a, s);
   int e = 1;
   while (kWave * e < total) e <<= 1;
   ProfScope ps(c, "merge_parts", s);
@@ -329,7 +484,7 @@ int MergeParts(Ctx* c, const MergeArgs& a, hipStream_t s) {
     case 4: k_merge<4><<<grid, 256, 0, s>>>(a); break;
     case 8: k_merge<8><<<grid, 256, 0, s>>>(a); break;
     case 16: k_merge<16><<<grid, 256, 0, s>>>(a); break;
-    default: return SetError(kNotSupported, "merge: parts * k > 1024 on the GPU path");
+    default: return MergePartsLarge(c, a, s);
   }
   VDBG_HIP(hipGetLastError());
   return kOk;

@@ -25,6 +25,24 @@ __device__ __forceinline__ bool nb_less(float ad, uint32_t ai, float bd, uint32_
   return ad < bd || (ad == bd && ai < bi);
 }
 
+// A dense row mask (bit r of word r / 64 set = row r allowed); null allows every row.
+__device__ __forceinline__ bool row_allowed(const uint64_t* w, uint32_t r) {
+  return w == nullptr || ((w[r >> 6] >> (r & 63)) & 1ull);
+}
+
+// 64-bit sort key of a (dist, id) pair ordered as Neighbor::operator<: the distance's
+// order-preserving bits (-0 folded into +0, which compares equal to it) above the id.
+constexpr uint64_t kNoKey = ~0ull;
+__device__ __forceinline__ uint64_t dist_key(float d, uint32_t id) {
+  const uint32_t b = __float_as_uint(d == 0.f ? 0.f : d);
+  const uint32_t e = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return (uint64_t(e) << 32) | id;
+}
+__device__ __forceinline__ float key_dist(uint64_t key) {
+  const uint32_t e = uint32_t(key >> 32);
+  return __uint_as_float((e & 0x80000000u) ? (e & 0x7fffffffu) : ~e);
+}
+
 // ----------------------------------------------------------------- exact distances
 
 // _mm512_reduce_add_ps as GCC expands it: upper 256 bits + lower, upper 128 + lower,

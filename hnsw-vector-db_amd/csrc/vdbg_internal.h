@@ -173,6 +173,18 @@ int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq
 int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipStream_t s);
 int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
               uint8_t* codes, float* yn, hipStream_t s);
+// Top-kk for kk beyond the wave kernels (up to 10,000): exact distance of every allowed row
+// per query, segmented sort.
+int ExactScanAll(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t kk,
+                 const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
+// Rerank for depths beyond 256 candidates per query.
+int RerankLarge(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq,
+                const uint32_t* cand, size_t depth, size_t k, uint32_t* out_ids, float* out_d,
+                hipStream_t s);
+// Sorts nseg key segments (int offsets off_dev[0..nseg]) from keys into keys_alt and writes
+// the first K of each as (id, dist), padded with (UINT32_MAX, +inf).
+int SortSegmentsTopK(Ctx* c, uint64_t* keys, uint64_t* keys_alt, const int* off_dev, int nseg,
+                     int total, int K, uint32_t* out_ids, float* out_d, hipStream_t s);
 // RunScan under an optional filter; compacts the allowed rows when they are few.
 int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);

@@ -214,7 +214,8 @@ int vdbg_prepare_queries_host(vdbg_ctx* ctx, const float* raw, size_t nq, size_t
  * sorted by (dist, row) and padded with UINT32_MAX rows, as the per-segment searches return
  * them.  Row r of part p has external id ext_ids[part_offsets[p] + r].  All hits are ordered
  * by (dist, part, row), the first hit of each external id is kept and k are written per
- * query to out_ext / out_dists (padded with UINT64_MAX / +inf).  nparts * k <= 1024. */
+ * query to out_ext / out_dists (padded with UINT64_MAX / +inf).  Up to 1024 hits per query
+ * merge in one wavefront; more are merged by segmented sorts. */
 int vdbg_merge_parts_device(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
                             const float* part_dists, const uint32_t* part_rows,
                             const uint64_t* ext_ids, const uint64_t* part_offsets,

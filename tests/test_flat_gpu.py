@@ -129,3 +129,26 @@ def test_dataset_from_device_rows_in_flight(ctx, oracle):
         gi, gd = dss[p].flat_search(qs, 10)
         od, oi = oracle.flat_search(hosts[p], qs, 10, metric="cosine")
         _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("k,metric,frac", [(250, "l2", None), (300, "l2", None),
+                                           (1000, "ip", None), (4000, "l2", 0.3),
+                                           (10000, "cosine", None)])
+def test_flat_large_k(ctx, oracle, k, metric, frac):
+    # k beyond the wave top-k, up to vdb's kMaxK = 10,000 (collection_impl.cc:26)
+    print(f"flat large k={k} {metric} filter={frac}", flush=True)
+    n, nq = 30000, 24
+    if metric == "l2":
+        base, qs = datagen.uniform_rows(n, 64, 4101), datagen.uniform_rows(nq, 64, 4102)
+    else:
+        base = datagen.clustered_unit(n, 64, 4103, 4104, 40, 0.5)
+        qs = datagen.clustered_unit(nq, 64, 4105, 4104, 40, 0.5)
+    allow = None
+    if frac is not None:
+        rows = np.nonzero(np.random.default_rng(7).random(n) < frac)[0]
+        allow = np.zeros((n + 63) // 64, np.uint64)
+        np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 64, metric=metric)
+    gi, gd = ds.flat_search(qs, k, allow=allow)
+    od, oi = oracle.flat_search(base, qs, k, metric=metric, allow=allow)
+    _check_equal(gi, gd, oi, od)

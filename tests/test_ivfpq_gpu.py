@@ -54,8 +54,6 @@ def test_ivfpq_reference_index_matches_reference_results(ctx):
     assert ix.info() == (24, 8, True)
     assert ix.save() == g["index_file"].tobytes()  # save(load(f)) == f
     for nprobe, rr in [(1, 0), (4, 0), (4, -1), (24, 0), (24, 5000)]:
-        if max(rr, 10) > 256:
-            continue  # the GPU path keeps R <= 256
         tag = f"np{nprobe}_r{rr if rr >= 0 else 'auto'}"
         gi, gd, dc = ix.search(qs, 10, nprobe, rr)
         _eq(gi, gd, g[f"{tag}_i"], g[f"{tag}_d"])
@@ -119,3 +117,20 @@ def test_ivfpq_corrupt_file_is_rejected(ctx):
     with pytest.raises(vdbg.VdbgError) as e:
         vdbg.IvfPqIndex.load(ds, g["index_file"].tobytes()[:-10])
     assert e.value.code == 5
+
+
+@pytest.mark.parametrize("nprobe,rerank,k", [(16, -1, 50), (64, -1, 100), (300, 0, 10),
+                                             (40, 1000, 20), (8, 0, 400)])
+def test_ivfpq_deep_top_r_matches_oracle(ctx, oracle, nprobe, rerank, k):
+    # R = max(rerank depth, k) beyond the wave top-k: the default depth max(10 k, 100) at
+    # k >= 26, explicit depths, k itself, and nprobe beyond 256 lists
+    print(f"ivfpq deep nprobe={nprobe} rerank={rerank} k={k}", flush=True)
+    base = datagen.sift_like(40000, 128, 2002)
+    qs = datagen.sift_like(70, 128, 2004)
+    blob = synth_ivfpq(base, 128, 512, 16, seed=2)
+    ds = vdbg.Dataset(ctx, base, 128)
+    ix = vdbg.IvfPqIndex.load(ds, blob)
+    gi, gd, dc = ix.search(qs, k, nprobe, rerank)
+    od, oi, odc = _oracle_ivf(oracle, blob, base, qs, k, nprobe, rerank)
+    _eq(gi, gd, oi, od)
+    assert np.array_equal(dc, odc)

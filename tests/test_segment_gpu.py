@@ -145,7 +145,7 @@ def _oracle_merge(oracle, pdist, prow, ext, off, k):
     return oe, od
 
 
-@pytest.mark.parametrize("nparts,k", [(9, 10), (3, 100), (16, 64), (1, 7)])
+@pytest.mark.parametrize("nparts,k", [(9, 10), (3, 100), (16, 64), (1, 7), (20, 100), (12, 500)])
 def test_merge_parts(ctx, oracle, nparts, k):
     rng = np.random.default_rng(nparts * 1000 + k)
     nq = 200

@@ -85,3 +85,15 @@ def test_sq8_filter(ctx, oracle):
     assert (gi % 5 == 0).all()
     od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 40, allow=allow)
     _eq(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("k,depth", [(10, 500), (300, 0), (100, 1000)])
+def test_sq8_deep(ctx, oracle, k, depth):
+    # SQ8 scan depth or k beyond the wave top-k, then the float rerank
+    base = datagen.sift_like(30000, 128, 4201)
+    qs = datagen.sift_like(20, 128, 4202)
+    ds = vdbg.Dataset(ctx, base, 128)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, k, depth)
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth)
+    _eq(gi, gd, oi, od)
