@@ -7,6 +7,7 @@
 #include <string>
 #include <vector>
 
+#include "vdbg_device.h"
 #include "vdbg_internal.h"
 
 namespace vdbg {
@@ -171,6 +172,64 @@ static int Sq8Search(Sq8Index* x, const float* Q, size_t nq, size_t k, size_t de
   (void)hipFreeAsync(ti, s);
   (void)hipFreeAsync(td, s);
   return rc;
+}
+
+__global__ void k_check_cand(const uint32_t* __restrict__ cand, size_t n, uint32_t rows,
+                             int* __restrict__ bad) {
+  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (t < n && cand[t] != kNoId && cand[t] >= rows) *bad = 1;
+}
+
+__global__ void k_count_cand(const uint32_t* __restrict__ cand, size_t nq, size_t depth,
+                             uint64_t* __restrict__ dc) {
+  const size_t q = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (q >= nq) return;
+  uint64_t n = 0;
+  for (size_t i = 0; i < depth; ++i) n += cand[q * depth + i] != kNoId ? 1 : 0;
+  dc[q] = n;
+}
+
+// Rerank (src/index/index.cc:89-95) on a batch: candidates [nq][depth] (UINT32_MAX = none),
+// rows checked against the dataset first; dist_comps[q] = the query's candidate count.
+__global__ void k_pad_results(uint32_t* ids, float* d, size_t n) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) {
+    ids[i] = kNoId;
+    d[i] = __builtin_inff();
+  }
+}
+
+static int RerankChecked(Ctx* c, Dataset* d, const float* Q, size_t nq, const uint32_t* cand,
+                         size_t depth, size_t k, uint32_t* out_ids, float* out_d,
+                         uint64_t* dist_comps, hipStream_t s) {
+  if (depth > 0) {
+    int* bad = nullptr;
+    VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&bad), sizeof(int), s));
+    VDBG_HIP(hipMemsetAsync(bad, 0, sizeof(int), s));
+    k_check_cand<<<dim3(unsigned((nq * depth + 255) / 256)), 256, 0, s>>>(cand, nq * depth,
+                                                                         uint32_t(d->n), bad);
+    VDBG_HIP(hipGetLastError());
+    VDBG_HIP(hipMemcpyAsync(c->host_pinned, bad, sizeof(int), hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipStreamSynchronize(s));
+    (void)hipFreeAsync(bad, s);
+    if (c->host_pinned[0] != 0) return SetError(kInvalidArgument, "candidate row out of range");
+  }
+  if (depth == 0) {
+    k_pad_results<<<dim3(unsigned((nq * k + 255) / 256)), 256, 0, s>>>(out_ids, out_d, nq * k);
+    VDBG_HIP(hipGetLastError());
+  } else {
+    VDBG_RETURN_IF_ERROR(Rerank(c, d->rows, int(d->pd), d->metric, Q, nq, cand, depth, k,
+                                out_ids, out_d, s));
+  }
+  if (dist_comps != nullptr) {
+    if (depth == 0) {
+      VDBG_HIP(hipMemsetAsync(dist_comps, 0, nq * 8, s));
+    } else {
+      k_count_cand<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(cand, nq, depth, dist_comps);
+      VDBG_HIP(hipGetLastError());
+    }
+  }
+  return kOk;
 }
 
 }  // namespace vdbg
@@ -464,6 +523,59 @@ int vdbg_sq8_search_host(vdbg_sq8* sq, const float* queries, size_t nq, size_t k
                      });
   if (rc == kOk && dist_comps)
     *dist_comps = uint64_t(nq) * (x->ds->n + (depth > 0 ? std::min(std::max(depth, k), x->ds->n) : 0));
+  return rc;
+}
+
+int vdbg_rerank_device(vdbg_dataset* ds, const float* queries, size_t nq, const uint32_t* cand,
+                       size_t depth, size_t k, uint32_t* out_ids, float* out_dists,
+                       uint64_t* dist_comps, void* stream) {
+  if (ds == nullptr) return SetError(kInvalidArgument, "null dataset");
+  if (nq == 0 || k == 0) return kOk;
+  if (queries == nullptr || out_ids == nullptr || out_dists == nullptr ||
+      (depth > 0 && cand == nullptr))
+    return SetError(kInvalidArgument, "null pointer");
+  if (k > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
+  Dataset* d = &ds->d;
+  Ctx* c = d->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+  return RerankChecked(c, d, queries, nq, cand, depth, k, out_ids, out_dists, dist_comps, s);
+}
+
+int vdbg_rerank_host(vdbg_dataset* ds, const float* queries, size_t nq, const uint32_t* cand,
+                     size_t depth, size_t k, uint32_t* out_ids, float* out_dists,
+                     uint64_t* dist_comps) {
+  if (ds == nullptr) return SetError(kInvalidArgument, "null dataset");
+  if (nq == 0 || k == 0) return kOk;
+  if (queries == nullptr || out_ids == nullptr || out_dists == nullptr ||
+      (depth > 0 && cand == nullptr))
+    return SetError(kInvalidArgument, "null pointer");
+  if (k > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
+  Dataset* d = &ds->d;
+  for (size_t i = 0; i < nq * depth; ++i)
+    if (cand[i] != kNoId && cand[i] >= d->n) return SetError(kInvalidArgument, "candidate row out of range");
+  Ctx* c = d->ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  uint32_t* dcand = nullptr;
+  uint64_t* ddc = nullptr;
+  const size_t nc = std::max<size_t>(nq * depth, 1);
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dcand), nc * 4, s));
+  if (dist_comps != nullptr) VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&ddc), nq * 8, s));
+  if (depth > 0) VDBG_HIP(hipMemcpyAsync(dcand, cand, nq * depth * 4, hipMemcpyHostToDevice, s));
+  int rc = StageHost(c, d->n, d->pd, queries, nq, k, nullptr, out_ids, out_dists,
+                     [&](const float* dq, const uint64_t*, uint32_t* di, float* dd,
+                         hipStream_t st) {
+                       return RerankChecked(c, d, dq, nq, dcand, depth, k, di, dd, ddc, st);
+                     });
+  if (rc == kOk && ddc != nullptr) {
+    VDBG_HIP(hipMemcpyAsync(dist_comps, ddc, nq * 8, hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipStreamSynchronize(s));
+  }
+  (void)hipFreeAsync(dcand, s);
+  if (ddc != nullptr) (void)hipFreeAsync(ddc, s);
   return rc;
 }
 

@@ -86,6 +86,8 @@ _SIGS = {
     "vdbg_ivfpq_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp]),
     "vdbg_ivfpq_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp,
                                            _vp]),
+    "vdbg_rerank_host": (C.c_int, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp]),
+    "vdbg_rerank_device": (C.c_int, [_vp, _vp, _sz, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
     "vdbg_prepare_queries_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp]),
     "vdbg_prepare_queries_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp]),
     "vdbg_merge_parts_host": (C.c_int, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
@@ -213,6 +215,20 @@ class Dataset:
         _check(lib.vdbg_flat_search_host(self.h, _ptr(q), nq, k, _ptr(allow), _ptr(ids),
                                          _ptr(dists), C.byref(dc)))
         return ids, dists
+
+    def rerank(self, queries, cand, k):
+        """Rerank: exact distances of each query's candidate rows (cand: (nq, depth) uint32,
+        UINT32_MAX = none), top k.  Returns (ids, dists, dist_comps)."""
+        q = np.ascontiguousarray(queries, np.float32)
+        cand = np.ascontiguousarray(cand, np.uint32)
+        nq, depth = cand.shape
+        assert q.shape == (nq, self.pd)
+        ids = np.empty((nq, k), np.uint32)
+        d = np.empty((nq, k), np.float32)
+        dc = np.empty(nq, np.uint64)
+        _check(lib.vdbg_rerank_host(self.h, _ptr(q), nq, _ptr(cand), depth, k, _ptr(ids), _ptr(d),
+                                    _ptr(dc)))
+        return ids, d, dc
 
     def flat_search_device(self, q_ptr, nq, k, ids_ptr, dists_ptr, allow_ptr=None,
                            stream=None):

@@ -196,6 +196,23 @@ int vdbg_kmeans(vdbg_ctx* ctx, const float* data, size_t n, size_t d, size_t str
 int vdbg_assign_nearest(vdbg_ctx* ctx, const float* data, size_t n, size_t d, size_t stride,
                         const float* centroids, size_t k, uint32_t* assign, float* dist);
 
+/* ---------------------------------------------------------------- rerank */
+
+/* Rerank (src/index/index.cc:89-95) against the resident rows, for nq queries at once: the
+ * exact fp32 distances (MetricDistance, AVX-512 order) of each query's `depth` candidate rows
+ * (cand is [nq][depth], UINT32_MAX = no candidate), the k smallest by (dist, id).  This is the
+ * float rerank of HnswSq8Index::search (src/index/hnsw/hnsw_index.cc:82-100) and of
+ * IvfPqIndex's FinishSearch (src/index/quant/ivf_pq.cc:28-36) for candidates found by vdb's
+ * CPU graph.  A row id beyond the dataset is InvalidArgument.  dist_comps (nullable, nq
+ * entries) receives each query's candidate count, as Rerank adds it. */
+int vdbg_rerank_host(vdbg_dataset* ds, const float* queries, size_t nq, const uint32_t* cand,
+                     size_t depth, size_t k, uint32_t* out_ids, float* out_dists,
+                     uint64_t* dist_comps);
+/* Device-pointer variant (dist_comps a device array); waits for the row check. */
+int vdbg_rerank_device(vdbg_dataset* ds, const float* queries, size_t nq, const uint32_t* cand,
+                       size_t depth, size_t k, uint32_t* out_ids, float* out_dists,
+                       uint64_t* dist_comps, void* stream);
+
 /* ---------------------------------------------------------------- collection read path */
 
 /* CollectionImpl::PrepareQuery (src/engine/collection_impl.cc:1023-1034) for nq raw queries

@@ -250,6 +250,22 @@ class GpuFlatIndex {
     if (stats) stats->distance_computations += dc;
     return Status::OK();
   }
+  // Rerank (src/index/index.cc:89-95) of candidates found elsewhere, e.g. by vdb's CPU
+  // HNSW-SQ8 beam or an IVF-PQ top-R: cand is [nq][depth] rows (kNoRow = none); the exact
+  // distances on the resident rows, the k best per query; stats add the candidate counts.
+  Status rerank_batch(const float* queries, size_t nq, const uint32_t* cand, size_t depth,
+                      size_t k, std::vector<std::vector<Neighbor>>& out,
+                      IndexSearchStats* stats) const {
+    std::vector<uint32_t> ids(nq * k);
+    std::vector<float> d(nq * k);
+    std::vector<uint64_t> dc(nq);
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_rerank_host(
+        ds_.get(), queries, nq, cand, depth, k, ids.data(), d.data(), dc.data())));
+    detail::Unpack(ids, d, nq, k, out);
+    if (stats)
+      for (uint64_t c : dc) stats->distance_computations += c;
+    return Status::OK();
+  }
 
  private:
   GpuFlatIndex(Device& dev, Metric m, const VectorView& v, detail::DatasetPtr d)

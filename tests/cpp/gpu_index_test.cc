@@ -162,6 +162,36 @@ void FlatKLargerThanRows() {
   CHECK(!out.empty() && out[0].id == 0u);
 }
 
+void RerankMatchesOracle() {
+  Data base = Clustered(20000, 48, 25, 15, false), qs = Clustered(30, 48, 25, 16, false);
+  std::unique_ptr<vdbg::GpuFlatIndex> ix;
+  CHECK_OK(vdbg::GpuFlatIndex::Create(*g_dev, vdbg::Metric::L2, base.view(), &ix));
+  for (size_t depth : {size_t(80), size_t(600)}) {
+    Rng r{depth};
+    std::vector<uint32_t> cand(qs.rows * depth);
+    for (auto& c : cand) c = uint32_t(r.next() % base.rows);
+    for (size_t q = 0; q < qs.rows; q += 4) cand[q * depth + depth - 1] = vdbg::kNoRow;
+    std::vector<std::vector<vdbg::Neighbor>> got;
+    vdbg::IndexSearchStats st;
+    CHECK_OK(ix->rerank_batch(qs.v.data(), qs.rows, cand.data(), depth, 10, got, &st));
+    uint64_t want_dc = 0;
+    for (size_t q = 0; q < qs.rows; ++q) {
+      std::vector<uint32_t> c;
+      for (size_t i = 0; i < depth; ++i)
+        if (cand[q * depth + i] != vdbg::kNoRow) c.push_back(cand[q * depth + i]);
+      want_dc += c.size();
+      std::vector<float> d(10);
+      std::vector<uint32_t> id(10);
+      const size_t n = or_rerank(Kset(), 0, base.v.data(), base.pd, qs.row(q), c.data(), c.size(), 10,
+                                 d.data(), id.data());
+      std::vector<vdbg::Neighbor> w;
+      for (size_t j = 0; j < n; ++j) w.push_back({d[j], id[j]});
+      CHECK(Same(got[q], w));
+    }
+    CHECK(st.distance_computations == want_dc);
+  }
+}
+
 // ---------------------------------------------------------------- SQ8
 
 void Sq8CodesAndSearchMatchOracle() {
@@ -433,6 +463,7 @@ int main() {
       {"FlatTest.BatchedMatchesSingleQuery", FlatBatchedMatchesSingleQuery},
       {"FlatTest.FilterIsRespected", FlatFilterIsRespected},
       {"FlatTest.KLargerThanRows", FlatKLargerThanRows},
+      {"RerankTest.MatchesOracle", RerankMatchesOracle},
       {"Sq8Test.CodesAndSearchMatchOracle", Sq8CodesAndSearchMatchOracle},
       {"IndexTest.IvfPqBuildSearchSaveLoad", IvfPqBuildSearchSaveLoad},
       {"IndexTest.IvfPqExhaustiveWithFullRerankEqualsFlat", IvfPqExhaustiveWithFullRerankEqualsFlat},
