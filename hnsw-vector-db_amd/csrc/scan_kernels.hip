@@ -551,6 +551,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   // stage (base, kc): rows base..base+63, dims kc*KC..kc*KC+KC-1
   auto load_stage = [&](uint32_t base, int kc) {
     const uint32_t valid = r_end > base ? min(uint32_t(kGemmRows), r_end - base) : 0u;
+    if constexpr (VEC_PER_TILE % 256 == 0) {
+      if (valid == kGemmRows) {  // a full tile: no per-vector bounds tests
+#pragma unroll
+        for (int i = 0; i < VEC_PER_THREAD; ++i) {
+          const int f = tid + 256 * i;
+          const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
+          if (KIND == 0)
+            pre[i] = *reinterpret_cast<const uint4*>(a.X + size_t(base + row) * PD + kc * KC + c * 4);
+          else
+            pre[i] = *reinterpret_cast<const uint4*>(a.C + size_t(base + row) * PD + kc * KC + c * 16);
+        }
+        if (kc == 0) pre_n = tid < kGemmRows ? a.rn[base + tid] : 0.f;
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
@@ -602,8 +617,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   int slot = 0;  // norm slot of the current tile
   for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
     v16f acc0, acc1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc0[r] = acc1[r] = 0.f;
+    const v16f zero = {};
+    if constexpr (NKC > 1) {
+      acc0 = zero;
+      acc1 = zero;
+    }
 #pragma unroll 1
     for (int kc = 0; kc < NKC; ++kc) {
       // prefetch the next stage: the next K chunk of this tile, or chunk 0 of the next tile
@@ -621,8 +639,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
         for (int t = 0; t < HALF; t += 4) {
           const float4 x0 = *reinterpret_cast<const float4*>(xa0 + t);
           const float4 x1 = *reinterpret_cast<const float4*>(xa1 + t);
-          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qv[t + 0], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qv[t + 0], acc1, 0, 0, 0);
+          // a single K chunk starts each tile from a zero accumulator operand
+          const bool first = NKC == 1 && t == 0;
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.x, qv[t + 0], first ? zero : acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.x, qv[t + 0], first ? zero : acc1, 0, 0, 0);
           acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.y, qv[t + 1], acc0, 0, 0, 0);
           acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(x1.y, qv[t + 1], acc1, 0, 0, 0);
           acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(x0.z, qv[t + 2], acc0, 0, 0, 0);
