@@ -78,7 +78,34 @@ float HostL2Any(const float* a, const float* b, size_t d) {
   return (s0 + s1) + (s2 + s3);
 }
 
-// PickL2 (src/index/quant/kmeans.cc:16-19): the SIMD kernel when rows are padded.
+// l2_sq_avx2 (src/distance/avx2.cc:26-35) and l2_sq_scalar (scalar.cc:8-15).
+float HostL2Avx2(const float* a, const float* b, size_t d) {
+  float acc0[8] = {0}, acc1[8] = {0};
+  for (size_t i = 0; i < d; i += 16)
+    for (int l = 0; l < 8; ++l) {
+      const float d0 = a[i + l] - b[i + l];
+      acc0[l] = std::fma(d0, d0, acc0[l]);
+      const float d1 = a[i + 8 + l] - b[i + 8 + l];
+      acc1[l] = std::fma(d1, d1, acc1[l]);
+    }
+  float v[8], h[4];
+  for (int l = 0; l < 8; ++l) v[l] = acc0[l] + acc1[l];
+  for (int l = 0; l < 4; ++l) h[l] = v[l] + v[4 + l];
+  return (h[0] + h[1]) + (h[2] + h[3]);
+}
+float HostL2Scalar(const float* a, const float* b, size_t d) {
+  float s = 0.f;
+  for (size_t i = 0; i < d; ++i) {
+    const float t = a[i] - b[i];
+    s += t * t;
+  }
+  return s;
+}
+float HostL2Kset(int kset, const float* a, const float* b, size_t d) {
+  return kset == 2 ? HostL2Avx512(a, b, d) : kset == 1 ? HostL2Avx2(a, b, d) : HostL2Scalar(a, b, d);
+}
+
+// PickL2 (src/index/quant/kmeans.cc:16-19): the kernel set's L2 when rows are padded.
 bool SimdL2(size_t d, size_t stride) { return d % 16 == 0 && stride % 16 == 0; }
 
 }  // namespace
@@ -302,7 +329,7 @@ int KMeansGpu(Ctx* c, const float* data, size_t n, size_t d, size_t stride, size
   }
   const bool simd = SimdL2(d, xs);
   auto fn = [&](const float* a, const float* b) {
-    return simd ? HostL2Avx512(a, b, d) : HostL2Any(a, b, d);
+    return simd ? HostL2Kset(c->kset, a, b, d) : HostL2Any(a, b, d);
   };
 
   // Initialisation.

@@ -999,7 +999,7 @@ __global__ __launch_bounds__(256) void k_exact_scan(ScanArgs a, Scorer sc) {
 struct RerankArgs {
   const float* X;
   const float* Q;
-  int pd, metric;
+  int pd, metric, kset;
   const uint32_t* cand;  // [nq][depth] ascending by SQ8 distance, kNoId padded
   int depth, nq, k;
   uint32_t* out_ids;
@@ -1020,7 +1020,7 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
     const int i = e * kWave + lane;
     const uint32_t id = i < a.depth ? a.cand[size_t(q) * a.depth + i] : kNoId;
     if (id != kNoId) {
-      r.d[e] = metric_exact(a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
+      r.d[e] = metric_exact_k(a.kset, a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
       r.id[e] = id;
     } else {
       r.d[e] = __builtin_inff();
@@ -1095,9 +1095,11 @@ static void launch_rerank(hipStream_t s, const RerankArgs& a) {
     default: return SetError(kNotSupported, "k too large"); \
   }
 
-static FlatScorer FlatOf(const ScanSource& src) { return FlatScorer{src.X, src.pd, src.metric}; }
-static Sq8Scorer Sq8Of(const ScanSource& src) {
-  return Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric};
+static FlatScorer FlatOf(const ScanSource& src, int kset) {
+  return FlatScorer{src.X, src.pd, src.metric, kset};
+}
+static Sq8Scorer Sq8Of(const ScanSource& src, int kset) {
+  return Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric, kset};
 }
 
 template <class Scorer>
@@ -1152,8 +1154,8 @@ static int ExactScan(Ctx* c, Workspace& w, const ScanSource& src, const float* Q
   if (nslots == 0) return kOk;
   if (pow2_e(k) > 4) return SetError(kNotSupported, "k > 256 is not supported on the GPU path");
   if (src.kind == 0)
-    return ExactScanT(c, w, src, FlatOf(src), Q, qlist, nslots, k, allow, out_ids, out_d, s);
-  return ExactScanT(c, w, src, Sq8Of(src), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+    return ExactScanT(c, w, src, FlatOf(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+  return ExactScanT(c, w, src, Sq8Of(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
 }
 
 static bool GemmSupported(size_t pd) {
@@ -1387,9 +1389,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   {
     ProfScope ps(c, "select", s);
     if (src->kind == 0) {
-      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, se, FlatOf(*src));
+      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, se, FlatOf(*src, c->kset));
     } else {
-      VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, se, Sq8Of(*src));
+      VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, se, Sq8Of(*src, c->kset));
     }
     VDBG_HIP(hipGetLastError());
   }
@@ -1410,9 +1412,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   {
     ProfScope ps(c, "rescore", s);
     if (src->kind == 0) {
-      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, s2, FlatOf(*src));
+      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, s2, FlatOf(*src, c->kset));
     } else {
-      VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, s2, Sq8Of(*src));
+      VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, s2, Sq8Of(*src, c->kset));
     }
     VDBG_HIP(hipGetLastError());
   }
@@ -1434,7 +1436,7 @@ int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq
   if (std::max(depth, k) > 256)
     return RerankLarge(c, X, pd, metric, Q, nq, cand, depth, k, out_ids, out_d, s);
   const int E = pow2_e(std::max(depth, k));
-  RerankArgs ra{X, Q, pd, metric, cand, int(depth), int(nq), int(k), out_ids, out_d};
+  RerankArgs ra{X, Q, pd, metric, c->kset, cand, int(depth), int(nq), int(k), out_ids, out_d};
   ProfScope ps(c, "rerank", s);
   VDBG_DISPATCH_E(E, launch_rerank, s, ra);
   VDBG_HIP(hipGetLastError());

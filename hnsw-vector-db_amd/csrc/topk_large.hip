@@ -116,23 +116,24 @@ int ExactScanAll(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_
   if (nq == 0 || kk == 0) return kOk;
   if (kk > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
   if (src.kind == 0)
-    return ExactAllT(c, src, FlatScorer{src.X, src.pd, src.metric}, Q, nq, kk, allow, out_ids,
-                     out_d, s);
-  return ExactAllT(c, src, Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric}, Q, nq, kk,
-                   allow, out_ids, out_d, s);
+    return ExactAllT(c, src, FlatScorer{src.X, src.pd, src.metric, c->kset}, Q, nq, kk, allow,
+                     out_ids, out_d, s);
+  return ExactAllT(c, src, Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric, c->kset}, Q,
+                   nq, kk, allow, out_ids, out_d, s);
 }
 
 // Rerank (src/index/index.cc:89-95) for depths beyond the wave kernel: exact distances of
 // the depth candidates per query, sorted, the first k.
 __global__ void k_rerank_keys(const float* __restrict__ X, const float* __restrict__ Q, int pd,
-                              int metric, const uint32_t* __restrict__ cand, int depth, int nq,
-                              uint64_t* __restrict__ keys) {
+                              int metric, int kset, const uint32_t* __restrict__ cand, int depth,
+                              int nq, uint64_t* __restrict__ keys) {
   const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
   if (t >= size_t(nq) * depth) return;
   const size_t q = t / depth;
   const uint32_t id = cand[t];
   keys[t] = id == kNoId ? kNoKey
-                        : dist_key(metric_exact(metric, Q + q * pd, X + size_t(id) * pd, pd), id);
+                        : dist_key(metric_exact_k(kset, metric, Q + q * pd, X + size_t(id) * pd, pd),
+                                   id);
 }
 
 int RerankLarge(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq,
@@ -153,7 +154,7 @@ int RerankLarge(Ctx* c, const float* X, int pd, int metric, const float* Q, size
     {
       ProfScope ps(c, "rerank", s);
       k_rerank_keys<<<dim3(unsigned((n + 255) / 256)), 256, 0, s>>>(
-          X, Q + q0 * pd, pd, metric, cand + q0 * depth, int(depth), nc, keys);
+          X, Q + q0 * pd, pd, metric, c->kset, cand + q0 * depth, int(depth), nc, keys);
     }
     k_seg_offsets<<<dim3(unsigned((nc + 256) / 256)), 256, 0, s>>>(off, nc, int(depth));
     if (hipGetLastError() != hipSuccess) {

@@ -2,6 +2,7 @@
 // the flat search entry points.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -242,6 +243,16 @@ int vdbg_version(void) { return (0 << 16) | 1; }
 
 const char* vdbg_last_error(void) { return g_error.c_str(); }
 
+static const char* const kKsetNames[] = {"scalar", "avx2", "avx512"};
+
+static int BestHostKset() { return vdbg::BestHostKernelSet(); }
+
+static int KsetByName(const char* name) {
+  for (int i = 0; i < 3; ++i)
+    if (std::strcmp(name, kKsetNames[i]) == 0) return i <= BestHostKset() ? i : -1;
+  return -1;
+}
+
 int vdbg_ctx_create(int device, vdbg_ctx** out) {
   if (out == nullptr) return SetError(kInvalidArgument, "null out");
   int n = 0;
@@ -258,6 +269,13 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
   ctx->c.device = device;
   ctx->c.cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   ctx->c.handle = ctx;
+  // Kernels() (cpu_features.cc:27-34): VDB_KERNELS when it names an available set, else the
+  // best set of this CPU, so distances match a vdb process on the same host.
+  ctx->c.kset = BestHostKset();
+  if (const char* env = std::getenv("VDB_KERNELS"); env != nullptr && *env != '\0') {
+    const int k = KsetByName(env);
+    if (k >= 0) ctx->c.kset = k;
+  }
   hipError_t e = hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&ctx->c.host_pinned), 4096, hipHostMallocDefault);
@@ -268,6 +286,19 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
   }
   *out = ctx;
   return kOk;
+}
+
+int vdbg_ctx_set_kernels(vdbg_ctx* ctx, const char* name) {
+  if (ctx == nullptr || name == nullptr) return SetError(kInvalidArgument, "null argument");
+  const int k = KsetByName(name);
+  if (k < 0) return SetError(kInvalidArgument, std::string("unknown or unavailable kernel set ") + name);
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.kset = k;
+  return kOk;
+}
+
+const char* vdbg_ctx_kernels(vdbg_ctx* ctx) {
+  return ctx == nullptr ? "" : kKsetNames[ctx->c.kset];
 }
 
 int vdbg_ctx_destroy(vdbg_ctx* ctx) {

@@ -148,7 +148,85 @@ __device__ __forceinline__ float dot_exact(const float* __restrict__ q,
   return reduce16(s);
 }
 
-// MetricDistance (src/distance/cpu_features.cc:71-73): 0 = L2, else minus the dot.
+// The kernel sets vdb picks from (src/distance/cpu_features.cc:33-58): the scalar kernels,
+// AVX2 and AVX-512.  Each restates its own summation order; the -ffp-contract=off build
+// keeps the scalar kernels' products and sums as separate roundings.
+enum KernelSet : int { kKsetScalar = 0, kKsetAvx2 = 1, kKsetAvx512 = 2 };
+
+// HorizontalSum of an 8-lane register (src/distance/avx2.cc:11-16): low 128 + high 128,
+// then two hadds: (s0 + s1) + (s2 + s3).
+__device__ __forceinline__ float hsum8(const float (&v)[8]) {
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = v[i] + v[4 + i];
+  return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
+// l2_sq_scalar / dot_scalar (src/distance/scalar.cc:8-21): one accumulator, in order.
+__device__ __forceinline__ float l2_scalar_k(const float* __restrict__ q,
+                                             const float* __restrict__ x, int pd) {
+  float s = 0.f;
+  for (int i = 0; i < pd; ++i) {
+    const float t = q[i] - x[i];
+    s += t * t;
+  }
+  return s;
+}
+__device__ __forceinline__ float dot_scalar_k(const float* __restrict__ q,
+                                              const float* __restrict__ x, int pd) {
+  float s = 0.f;
+  for (int i = 0; i < pd; ++i) s += q[i] * x[i];
+  return s;
+}
+
+// l2_sq_avx2 / dot_avx2 (src/distance/avx2.cc:26-44): per 16 floats, lanes 0-7 into one
+// 8-lane FMA accumulator and 8-15 into another; their sum, HorizontalSum.
+__device__ __forceinline__ float l2_avx2_k(const float* __restrict__ q,
+                                           const float* __restrict__ x, int pd) {
+  float acc0[8], acc1[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) acc0[l] = acc1[l] = 0.f;
+  for (int i = 0; i < pd; i += 16) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const float d0 = q[i + l] - x[i + l];
+      acc0[l] = fmaf(d0, d0, acc0[l]);
+      const float d1 = q[i + 8 + l] - x[i + 8 + l];
+      acc1[l] = fmaf(d1, d1, acc1[l]);
+    }
+  }
+  float s[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) s[l] = acc0[l] + acc1[l];
+  return hsum8(s);
+}
+__device__ __forceinline__ float dot_avx2_k(const float* __restrict__ q,
+                                            const float* __restrict__ x, int pd) {
+  float acc0[8], acc1[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) acc0[l] = acc1[l] = 0.f;
+  for (int i = 0; i < pd; i += 16) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      acc0[l] = fmaf(q[i + l], x[i + l], acc0[l]);
+      acc1[l] = fmaf(q[i + 8 + l], x[i + 8 + l], acc1[l]);
+    }
+  }
+  float s[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) s[l] = acc0[l] + acc1[l];
+  return hsum8(s);
+}
+
+// MetricDistance (src/distance/cpu_features.cc:71-73) of a kernel set: 0 = L2, else minus
+// the dot product.
+__device__ __forceinline__ float metric_exact_k(int kset, int metric, const float* q,
+                                                const float* x, int pd) {
+  if (kset == kKsetAvx512) return metric == 0 ? l2_exact(q, x, pd) : -dot_exact(q, x, pd);
+  if (kset == kKsetAvx2) return metric == 0 ? l2_avx2_k(q, x, pd) : -dot_avx2_k(q, x, pd);
+  return metric == 0 ? l2_scalar_k(q, x, pd) : -dot_scalar_k(q, x, pd);
+}
+// The AVX-512 set (the one vdb selects on AVX-512 hosts).
 __device__ __forceinline__ float metric_exact(int metric, const float* q, const float* x,
                                               int pd) {
   return metric == 0 ? l2_exact(q, x, pd) : -dot_exact(q, x, pd);
@@ -182,12 +260,71 @@ __device__ __forceinline__ float sq8_exact(int metric, const float* __restrict__
   return metric == 0 ? s : -s;
 }
 
-// Exact scorers: the reference's distance of query q to row `row`.
+// sq8_l2_scalar / sq8_ip_scalar (src/distance/scalar.cc:25-41): vmin + code * scale in two
+// roundings, one accumulator.
+__device__ __forceinline__ float sq8_scalar_k(int metric, const float* __restrict__ q,
+                                              const uint8_t* __restrict__ c,
+                                              const float* __restrict__ vmin,
+                                              const float* __restrict__ scale, int pd) {
+  float s = 0.f;
+  for (int i = 0; i < pd; ++i) {
+    const float x = vmin[i] + float(c[i]) * scale[i];
+    if (metric == 0) {
+      const float t = q[i] - x;
+      s += t * t;
+    } else {
+      s += q[i] * x;
+    }
+  }
+  return metric == 0 ? s : -s;
+}
+
+// sq8_l2_avx2 / sq8_ip_avx2 (src/distance/avx2.cc:48-74): Decode8 = fma(code, scale, vmin)
+// on each half of 16 code bytes, two 8-lane accumulators, HorizontalSum.
+__device__ __forceinline__ float sq8_avx2_k(int metric, const float* __restrict__ q,
+                                            const uint8_t* __restrict__ c,
+                                            const float* __restrict__ vmin,
+                                            const float* __restrict__ scale, int pd) {
+  float acc0[8], acc1[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) acc0[l] = acc1[l] = 0.f;
+  for (int i = 0; i < pd; i += 16) {
+#pragma unroll
+    for (int l = 0; l < 8; ++l) {
+      const float x0 = fmaf(float(c[i + l]), scale[i + l], vmin[i + l]);
+      const float x1 = fmaf(float(c[i + 8 + l]), scale[i + 8 + l], vmin[i + 8 + l]);
+      if (metric == 0) {
+        const float d0 = q[i + l] - x0, d1 = q[i + 8 + l] - x1;
+        acc0[l] = fmaf(d0, d0, acc0[l]);
+        acc1[l] = fmaf(d1, d1, acc1[l]);
+      } else {
+        acc0[l] = fmaf(q[i + l], x0, acc0[l]);
+        acc1[l] = fmaf(q[i + 8 + l], x1, acc1[l]);
+      }
+    }
+  }
+  float s[8];
+#pragma unroll
+  for (int l = 0; l < 8; ++l) s[l] = acc0[l] + acc1[l];
+  const float r = hsum8(s);
+  return metric == 0 ? r : -r;
+}
+
+// MetricSq8Distance (cpu_features.cc:75-78) of a kernel set.
+__device__ __forceinline__ float sq8_exact_k(int kset, int metric, const float* q,
+                                             const uint8_t* c, const float* vmin,
+                                             const float* scale, int pd) {
+  if (kset == kKsetAvx512) return sq8_exact(metric, q, c, vmin, scale, pd);
+  if (kset == kKsetAvx2) return sq8_avx2_k(metric, q, c, vmin, scale, pd);
+  return sq8_scalar_k(metric, q, c, vmin, scale, pd);
+}
+
+// Exact scorers: the reference's distance of query q to row `row` under kernel set kset.
 struct FlatScorer {
   const float* X;
-  int pd, metric;
+  int pd, metric, kset;
   __device__ __forceinline__ float operator()(const float* q, uint32_t row) const {
-    return metric_exact(metric, q, X + size_t(row) * pd, pd);
+    return metric_exact_k(kset, metric, q, X + size_t(row) * pd, pd);
   }
 };
 
@@ -195,9 +332,9 @@ struct Sq8Scorer {
   const uint8_t* C;
   const float* vmin;
   const float* scale;
-  int pd, metric;
+  int pd, metric, kset;
   __device__ __forceinline__ float operator()(const float* q, uint32_t row) const {
-    return sq8_exact(metric, q, C + size_t(row) * pd, vmin, scale, pd);
+    return sq8_exact_k(kset, metric, q, C + size_t(row) * pd, vmin, scale, pd);
   }
 };
 

@@ -25,6 +25,7 @@ enum Code : int {
 };
 
 int SetError(int code, const std::string& msg);  // records the thread's message, returns code
+int BestHostKernelSet();  // the host CPU's best distance kernel set (host_cpu.cc)
 
 #define VDBG_HIP(expr)                                                                  \
   do {                                                                                  \
@@ -83,6 +84,7 @@ struct Ctx {
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
   uint64_t last_fallbacks = 0;
   int cu_count = 256;
+  int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 

@@ -54,6 +54,8 @@ _SIGS = {
     "vdbg_ctx_destroy": (C.c_int, [_vp]),
     "vdbg_ctx_stream": (_vp, [_vp]),
     "vdbg_ctx_synchronize": (C.c_int, [_vp]),
+    "vdbg_ctx_set_kernels": (C.c_int, [_vp, C.c_char_p]),
+    "vdbg_ctx_kernels": (C.c_char_p, [_vp]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_reset": (C.c_int, [_vp]),
     "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
@@ -150,6 +152,14 @@ class Context:
 
     def synchronize(self):
         _check(lib.vdbg_ctx_synchronize(self.h))
+
+    @property
+    def kernels(self):
+        """The distance kernel set exact distances follow: scalar, avx2 or avx512."""
+        return lib.vdbg_ctx_kernels(self.h).decode()
+
+    def set_kernels(self, name):
+        _check(lib.vdbg_ctx_set_kernels(self.h, name.encode()))
 
     def profile(self, enable=True):
         _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))

@@ -74,6 +74,13 @@ int vdbg_ctx_destroy(vdbg_ctx* ctx);
 void* vdbg_ctx_stream(vdbg_ctx* ctx);
 /* Waits for all work queued on the context's stream. */
 int vdbg_ctx_synchronize(vdbg_ctx* ctx);
+/* The distance kernel set whose arithmetic order exact distances follow: "scalar", "avx2"
+ * or "avx512" (KernelSet, src/distance/distance.h:26-33).  A new context takes what
+ * Kernels() takes in a vdb process on this host (src/distance/cpu_features.cc:27-58): the
+ * VDB_KERNELS environment variable when it names a set this CPU offers, else the best set
+ * of this CPU.  Setting an unknown or unavailable set is InvalidArgument. */
+int vdbg_ctx_set_kernels(vdbg_ctx* ctx, const char* name);
+const char* vdbg_ctx_kernels(vdbg_ctx* ctx);
 
 /* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
  * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch
