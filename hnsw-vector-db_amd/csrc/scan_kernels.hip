@@ -171,6 +171,8 @@ int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
   return kOk;
 }
 
+static bool GemmSupported(size_t pd);
+
 // ================================================================ SQ8 train / encode
 
 // Sq8Quantizer::train (src/index/quant/sq8.cc:9-26) keeps the first of equal values
@@ -377,6 +379,8 @@ struct PrepArgs {
   float* shift;  // exact distance ~= GEMM value + shift
   float* eb;     // bound on |GEMM value + shift - exact distance|
   int* exact;    // the bound is zero
+  uint16_t* Q16;  // nullable: the queries as fp16 (for the exact-integer GEMM)
+  int* all16;     // nullable: cleared when a query is not exact or exceeds 2048 in magnitude
 };
 
 // One wave per query.
@@ -403,6 +407,7 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     hi = fmaxf(hi, e);
     ma = fmaxf(ma, fabsf(e));
     ai &= (e == rintf(e)) ? 1 : 0;
+    if (a.Q16 != nullptr) a.Q16[size_t(q) * a.pd + i] = __builtin_bit_cast(uint16_t, _Float16(e));
     if (a.kind == 1) {
       if (a.metric == 0) {
         const float qp = e - a.vmin[i];
@@ -437,6 +442,10 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     }
     a.shift[q] = shift;
     a.exact[q] = ex ? 1 : 0;
+    // fp16 holds every integer of magnitude <= 2048 exactly: with exact sums, an fp16-input
+    // GEMM then gives the fp32 GEMM's values bit for bit
+    if (a.all16 != nullptr && !(ex && ma <= 2048.f && a.xs.max_abs <= 2048.f))
+      atomicAnd(a.all16, 0);
     // Rounding bound of |GEMM value + shift - exact distance|.  Any fp32 summation order of
     // n products errs by at most ~n u sum|q_i x_i| (u = 2^-24), and sum|q_i x_i| <= |q||x|.
     // Inner product of fp32 rows: the MFMA dot and the exact dot each err by that, so
@@ -455,6 +464,8 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
 
 struct GemmArgs {
   const float* X;      // fp32 rows (KIND 0)
+  const uint16_t* X16; // fp16 rows (k_gemm16)
+  const uint16_t* Q16; // fp16 queries (k_gemm16)
   const uint8_t* C;    // code rows (KIND 1)
   const float* rn;     // row norms of the GEMM form
   const uint32_t* rid; // MODE 1: original row id of each sample row
@@ -712,6 +723,184 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     if (cnt > uint32_t(a.caph)) a.ovf[q] = 1;
   }
 }
+
+// ================================================================ exact-integer GEMM
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+
+// The main pass for integer-valued rows and queries (every value an integer of magnitude
+// <= 2048, every partial sum below 2^24): inputs in fp16 hold each value exactly, each fp16
+// product is exact in fp32 and so is every sum, so v_mfma_f32_32x32x16_f16 yields exactly
+// the values of the fp32 GEMM at 16 times its rate.  The structure is k_gemm's (block =
+// 4 waves = 128 queries x one row chunk, XCD-aware item order, double-buffered 64-row LDS
+// stages, three norm slots, threshold epilogue into per-(query, chunk, half) buffers); rows
+// are staged as fp16.  Lane l of a wave holds, per 16-dim K block, dims 8 (l / 32) .. + 7 of
+// query l % 32 as the B operand; the A operand is the same dims of row l % 32 of a 32-row
+// block.
+template <int PD, int METRIC>
+__global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
+  constexpr int KC = GemmKc(PD);
+  constexpr int NKC = PD / KC;
+  constexpr int NKB = KC / 16;     // 16-dim MFMA K blocks per stage
+  constexpr int STR = KC + 8;      // padded LDS row stride (halfs): 16 bytes of padding
+  constexpr int VEC_PER_ROW = KC / 8;             // uint4 = 8 halfs
+  constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
+  constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
+  static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmRows * STR];
+  __shared__ float xns[3][kGemmRows];
+
+  const int b = blockIdx.x;
+  const int item = (b & 7) * a.per_xcd + (b >> 3);
+  if (item >= a.items) return;
+  const int chunk = item / a.nqt;
+  const int qt = item - chunk * a.nqt;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int q = qt * 128 + wave * 32 + j;
+  const bool wave_live = qt * 128 + wave * 32 < a.nq;
+  const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
+  const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
+
+  half8 qb[NKB];
+  auto load_q = [&](int kc) {
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      if (q < a.nq) {
+        const uint4 v = *reinterpret_cast<const uint4*>(a.Q16 + size_t(q) * PD + kc * KC + kb * 16 + h * 8);
+        qb[kb] = __builtin_bit_cast(half8, v);
+      } else {
+        qb[kb] = half8{};
+      }
+    }
+  };
+  if (NKC == 1) load_q(0);
+  const float T = q < a.nq ? a.T[q] : -__builtin_inff();
+  const size_t seg = (size_t(q) * a.nchunks + chunk) * 2 + h;
+  uint2* out = a.cand + seg * size_t(a.caph);
+  uint32_t cnt = 0;
+
+  uint4 pre[VEC_PER_THREAD];
+  float pre_n = 0.f;
+  auto load_stage = [&](uint32_t base, int kc) {
+    const uint32_t valid = r_end > base ? min(uint32_t(kGemmRows), r_end - base) : 0u;
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int f = tid + 256 * i;
+      const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
+      if (f < VEC_PER_TILE && uint32_t(row) < valid)
+        pre[i] = *reinterpret_cast<const uint4*>(a.X16 + size_t(base + row) * PD + kc * KC + c * 8);
+      else
+        pre[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+    if (kc == 0) pre_n = (tid < kGemmRows && uint32_t(tid) < valid) ? a.rn[base + tid] : 0.f;
+  };
+  auto store_stage = [&](int buf, int kc, int nslot) {
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int f = tid + 256 * i;
+      if (f < VEC_PER_TILE) {
+        const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
+        *reinterpret_cast<uint4*>(&xs[buf][row * STR + c * 8]) = pre[i];
+      }
+    }
+    if (kc == 0 && tid < kGemmRows) xns[nslot][tid] = pre_n;
+  };
+
+  if (r_begin < r_end) {
+    load_stage(r_begin, 0);
+    store_stage(0, 0, 0);
+  }
+  __syncthreads();
+
+  int buf = 0;
+  int slot = 0;
+  for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
+    v16f acc0 = {}, acc1 = {};
+#pragma unroll 1
+    for (int kc = 0; kc < NKC; ++kc) {
+      const bool last_kc = kc + 1 == NKC;
+      const uint32_t nbase = last_kc ? base + kGemmRows : base;
+      const int nkc = last_kc ? 0 : kc + 1;
+      const bool have_next = nbase < r_end;
+      if (have_next) load_stage(nbase, nkc);
+      if (NKC > 1 && wave_live) load_q(kc);
+      if (wave_live) {
+        const uint16_t* xa0 = &xs[buf][j * STR + h * 8];
+        const uint16_t* xa1 = xa0 + 32 * STR;
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const half8 x0 = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(xa0 + kb * 16));
+          const half8 x1 = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(xa1 + kb * 16));
+          acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qb[kb], acc0, 0, 0, 0);
+          acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qb[kb], acc1, 0, 0, 0);
+        }
+      }
+      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? (slot == 2 ? 0 : slot + 1) : slot);
+      __syncthreads();
+      buf ^= 1;
+    }
+    if (wave_live) {
+      uint32_t pass = 0;
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const float g = blk == 0 ? acc0[r] : acc1[r];
+          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
+          pass |= (v <= T ? 1u : 0u) << (blk * 16 + r);
+        }
+      if (__ballot(pass != 0) != 0) {
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            if (pass & (1u << (blk * 16 + r))) {
+              const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+              const float g = blk == 0 ? acc0[r] : acc1[r];
+              const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
+              const uint32_t row = base + rl;
+              if (q < a.nq && row < r_end && row_allowed(a.allow, row)) {
+                if (cnt < uint32_t(a.caph)) out[cnt] = make_uint2(__float_as_uint(v), row);
+                ++cnt;
+              }
+            }
+          }
+      }
+    }
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+  if (q < a.nq) {
+    a.counts[seg] = min(cnt, uint32_t(a.caph));
+    if (cnt > uint32_t(a.caph)) a.ovf[q] = 1;
+  }
+}
+
+__global__ void k_to_f16(const float* __restrict__ x, size_t n, uint16_t* __restrict__ y) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(x[i]));
+}
+
+int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, const RowStats& st,
+               uint16_t** out) {
+  *out = nullptr;
+  if (n == 0 || !st.all_int || !(st.max_abs <= 2048.f) || !GemmSupported(pd)) return kOk;
+  uint16_t* y = nullptr;
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * sizeof(uint16_t)));
+  k_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, y);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    (void)hipFree(y);
+    return SetError(kInternal, std::string("fp16 rows: ") + hipGetErrorString(e));
+  }
+  *out = y;
+  return kOk;
+}
+
 
 // ================================================================ threshold from groups
 
@@ -1218,6 +1407,36 @@ static int LaunchGemm(size_t pd, int metric, int kind, int mode, hipStream_t s, 
   return kOk;
 }
 
+template <int PD>
+static void launch_gemm16_pd(int metric, hipStream_t s, int blocks, const GemmArgs& a) {
+  if (metric == 0)
+    k_gemm16<PD, 0><<<dim3(blocks), 256, 0, s>>>(a);
+  else
+    k_gemm16<PD, 1><<<dim3(blocks), 256, 0, s>>>(a);
+}
+
+static int LaunchGemm16(size_t pd, int metric, hipStream_t s, int blocks, const GemmArgs& a) {
+  switch (pd) {
+    case 16: launch_gemm16_pd<16>(metric, s, blocks, a); break;
+    case 32: launch_gemm16_pd<32>(metric, s, blocks, a); break;
+    case 48: launch_gemm16_pd<48>(metric, s, blocks, a); break;
+    case 64: launch_gemm16_pd<64>(metric, s, blocks, a); break;
+    case 80: launch_gemm16_pd<80>(metric, s, blocks, a); break;
+    case 96: launch_gemm16_pd<96>(metric, s, blocks, a); break;
+    case 112: launch_gemm16_pd<112>(metric, s, blocks, a); break;
+    case 128: launch_gemm16_pd<128>(metric, s, blocks, a); break;
+    case 192: launch_gemm16_pd<192>(metric, s, blocks, a); break;
+    case 256: launch_gemm16_pd<256>(metric, s, blocks, a); break;
+    case 384: launch_gemm16_pd<384>(metric, s, blocks, a); break;
+    case 512: launch_gemm16_pd<512>(metric, s, blocks, a); break;
+    case 768: launch_gemm16_pd<768>(metric, s, blocks, a); break;
+    case 960: launch_gemm16_pd<960>(metric, s, blocks, a); break;
+    case 1024: launch_gemm16_pd<1024>(metric, s, blocks, a); break;
+    default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
+  }
+  return kOk;
+}
+
 // Chunk count for nqt query tiles over N rows: the fewest chunks whose last round of blocks
 // fills the resident slots (2 blocks per CU) within 3% of the best balance on offer.
 static int PlanChunks(int nqt, uint32_t N, int slots, int max_chunks) {
@@ -1249,6 +1468,7 @@ static void GemmGrid(GemmArgs& ga, int nqt, int nchunks, int* blocks) {
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
   c->last_fallbacks = 0;
+  c->last_gemm_bits = 0;
   if (nq == 0 || kk == 0) return kOk;
   if (kk > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
   if (src->N == 0) {
@@ -1292,8 +1512,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
                       size_t(nq) * ngroups * sizeof(float) +
                       size_t(nq) * nseg * (sizeof(uint32_t) + size_t(caph) * sizeof(uint2)) +
-                      16 * 256;
+                      (src->X16 != nullptr ? nq * pd * sizeof(uint16_t) : 0) + 18 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
+  // integer-valued rows with an fp16 copy: the batch may take the exact-integer GEMM
+  const bool try16 = src->kind == 0 && src->X16 != nullptr;
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
   float* T = w.take<float>(nq);
@@ -1306,16 +1528,26 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   float* gm = w.take<float>(size_t(nq) * ngroups);
   uint32_t* counts = w.take<uint32_t>(size_t(nq) * nseg);
   uint2* cand = w.take<uint2>(size_t(nq) * nseg * caph);
+  uint16_t* Q16 = try16 ? w.take<uint16_t>(nq * pd) : nullptr;
+  int* all16 = try16 ? w.take<int>(1) : nullptr;
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
   VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
+  if (try16) VDBG_HIP(hipMemsetD32Async(all16, 1, 1, s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
-              src->vmin, src->scale, shift, eb, exact};
+              src->vmin, src->scale, shift, eb, exact, Q16, all16};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
     VDBG_HIP(hipGetLastError());
   }
+  bool use16 = false;
+  if (try16) {
+    VDBG_HIP(hipMemcpyAsync(c->host_pinned, all16, sizeof(int), hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipStreamSynchronize(s));
+    use16 = c->host_pinned[0] != 0;
+  }
+  c->last_gemm_bits = use16 ? 16 : 32;
   const float* B = src->kind == 1 ? Qb : Q;
   const int metric = src->metric == 0 ? 0 : 1;
 
@@ -1365,7 +1597,13 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   GemmGrid(ga, nqt, nchunks, &blocks);
   {
     ProfScope ps(c, src->kind == 0 ? "flat_gemm" : "sq8_gemm", s);
-    VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
+    if (use16) {
+      ga.X16 = src->X16;
+      ga.Q16 = Q16;
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, s, blocks, ga));
+    } else {
+      VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
+    }
     VDBG_HIP(hipGetLastError());
   }
   SelectArgs se{};

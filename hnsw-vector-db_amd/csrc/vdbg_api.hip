@@ -137,8 +137,18 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
     delete ds;
     return rc;
   }
+  if (n > 0) {
+    rc = MakeRows16(c, c->stream, d.rows, n, pd, d.stats, &d.rows16);
+    if (rc != kOk) {
+      (void)hipFree(d.rows);
+      (void)hipFree(d.norms);
+      delete ds;
+      return rc;
+    }
+  }
   d.src.kind = 0;
   d.src.X = d.rows;
+  d.src.X16 = d.rows16;
   d.src.rn = d.norms;
   d.src.N = static_cast<uint32_t>(n);
   d.src.pd = static_cast<int>(pd);
@@ -371,6 +381,7 @@ int vdbg_dataset_destroy(vdbg_dataset* ds) {
   FreeSample(&ds->d.src);
   (void)hipFree(ds->d.rows);
   (void)hipFree(ds->d.norms);
+  if (ds->d.rows16 != nullptr) (void)hipFree(ds->d.rows16);
   delete ds;
   return kOk;
 }
@@ -609,6 +620,8 @@ int vdbg_rerank_host(vdbg_dataset* ds, const float* queries, size_t nq, const ui
   if (ddc != nullptr) (void)hipFreeAsync(ddc, s);
   return rc;
 }
+
+int vdbg_last_gemm_bits(vdbg_ctx* ctx) { return ctx == nullptr ? 0 : ctx->c.last_gemm_bits; }
 
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries) {
   if (ctx == nullptr || fallback_queries == nullptr)

@@ -83,6 +83,7 @@ struct Ctx {
   std::vector<hipEvent_t> free_events;
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
   uint64_t last_fallbacks = 0;
+  int last_gemm_bits = 0;  // input width of the last scan's main GEMM: 32, 16 (exact), 0
   int cu_count = 256;
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
@@ -93,6 +94,8 @@ struct Ctx {
 struct ScanSource {
   int kind = 0;
   const float* X = nullptr;     // kind 0: n x pd rows
+  const uint16_t* X16 = nullptr;  // kind 0: the rows as fp16 when every value is an integer
+                                  // of magnitude <= 2048 (exact), else null
   const uint8_t* C = nullptr;   // kind 1: n x pd codes
   const float* rn = nullptr;    // ||x||^2 (flat) or ||code * scale||^2 (SQ8)
   const float* vmin = nullptr;  // SQ8 quantizer (device)
@@ -112,6 +115,7 @@ struct Dataset {
   Ctx* ctx = nullptr;
   float* rows = nullptr;   // n x pd
   float* norms = nullptr;  // n row norms (fp32, ||x||^2)
+  uint16_t* rows16 = nullptr;  // n x pd fp16 copy of integer-valued rows (see ScanSource::X16)
   size_t n = 0, dim = 0, pd = 0;
   int metric = 0;
   RowStats stats;
@@ -164,6 +168,10 @@ struct IvfIndex {
 
 int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
                    float* norms, RowStats* out);
+// The fp16 copy of rows whose values are all integers of magnitude <= 2048 (each exactly
+// representable), used by the exact-integer GEMM; *out stays null when not applicable.
+int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
+               const RowStats& st, uint16_t** out);
 
 // Top-kk rows by the source's exact distance for nq queries (device pointers).
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,

@@ -69,6 +69,7 @@ _SIGS = {
                                         C.POINTER(C.c_uint64)]),
     "vdbg_flat_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
     "vdbg_last_fallbacks": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
+    "vdbg_last_gemm_bits": (C.c_int, [_vp]),
     "vdbg_sq8_train": (C.c_int, [_vp, _vp, _vp]),
     "vdbg_sq8_create": (C.c_int, [_vp, _vp, _vp, C.POINTER(_vp)]),
     "vdbg_sq8_destroy": (C.c_int, [_vp]),
@@ -172,6 +173,10 @@ class Context:
         n = C.c_uint64()
         _check(lib.vdbg_profile_get(self.h, name.encode(), C.byref(ms), C.byref(n)))
         return ms.value, n.value
+
+    def last_gemm_bits(self):
+        """Input width of the last scan's ranking GEMM: 32, 16 (exact integers) or 0."""
+        return lib.vdbg_last_gemm_bits(self.h)
 
     def last_fallbacks(self):
         n = C.c_uint64()

@@ -253,6 +253,11 @@ int vdbg_merge_parts_host(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
 /* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
  * candidates could not be certified and were re-scanned exactly. */
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
+/* Input width of the last flat/SQ8 scan's ranking GEMM on this context: 32 (fp32 MFMA), 16
+ * (fp16 MFMA, taken only when every row and query value is an integer of magnitude <= 2048
+ * and every partial sum stays below 2^24, so its values equal the fp32 GEMM's bit for bit),
+ * or 0 (no GEMM: the exact scan ran). */
+int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 
 #ifdef __cplusplus
 }
