@@ -1,0 +1,61 @@
+// gemm.h -- what the ranking GEMMs of the flat/SQ8 scans share: the argument block, the row
+// tile and K-chunk geometry, and the padded dimensions with compiled GEMM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace vdbg {
+
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+struct GemmArgs {
+  const float* X;      // fp32 rows (KIND 0)
+  const uint16_t* X16; // fp16 rows (k_gemm16)
+  const uint16_t* Q16; // fp16 B operand: -2 q (L2) or -q (inner product) (k_gemm16)
+  const uint8_t* C;    // code rows (KIND 1)
+  const float* rn;     // row norms of the GEMM form
+  const uint32_t* rid; // MODE 1: original row id of each sample row
+  const float* Qb;
+  const float* T;
+  const uint64_t* allow;
+  uint2* cand;         // MODE 0: [(q * nchunks + chunk) * 2 + half][caph]
+  uint32_t* counts;    // MODE 0: [(q * nchunks + chunk) * 2 + half]
+  int* ovf;            // MODE 0: [q]
+  float* gm;           // MODE 1: [q][ngroups] minimum GEMM value of each 16-row group
+  int ngroups;
+  uint32_t N;
+  int nq, nqt;
+  uint32_t chunk_rows;
+  int nchunks, caph;
+  int items;           // nqt * nchunks
+  int per_xcd;         // items assigned to each of the 8 XCDs
+};
+
+constexpr int kGemmRows = 64;  // rows per LDS tile (two 32-row MFMA blocks)
+
+// Dimensions staged per LDS pass: the whole row up to 128 dims, else the largest of
+// 128/64/32/16 that divides it.
+__host__ __device__ constexpr int GemmKc(int pd) {
+  return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : (pd % 32 == 0 ? 32 : 16)));
+}
+
+// Padded dimensions with compiled GEMM kernels; others scan exactly.
+inline bool GemmSupported(size_t pd) {
+  switch (pd) {
+    case 16: case 32: case 48: case 64: case 80: case 96: case 112: case 128:
+    case 192: case 256: case 384: case 512: case 768: case 960: case 1024:
+      return true;
+    default:
+      return false;
+  }
+}
+
+// Exact-integer fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 =
+// threshold pass into candidate buffers, 1 = group minima of the sample.
+int LaunchGemm16(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+                 const GemmArgs& a);
+
+}  // namespace vdbg

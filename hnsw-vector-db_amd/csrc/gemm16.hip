@@ -1,0 +1,321 @@
+// gemm16.hip -- the ranking GEMM of the flat scan for integer-valued data, on fp16 MFMA.
+//
+// When every row and query value is an integer of magnitude <= 2048, fp16 holds each value
+// exactly, and so it holds -2 q (an even integer of magnitude <= 4096) and -q.  Every product
+// of two such values is an integer below 2^23 and exact in fp32.  With R the largest row norm
+// and |q| the query norm, every partial sum of
+//     ||x||^2 + sum_i (-2 q_i) x_i        (L2)        or        sum_i (-q_i) x_i     (IP)
+// is bounded by R^2 + 2 |q| R <= (|q| + R)^2 (Cauchy-Schwarz), so when (|q| + R)^2 < 2^24
+// every partial sum is an integer that fp32 represents and the accumulation is exact in any
+// order.  v_mfma_f32_32x32x16_f16 started from the row norms then yields exactly the value the
+// fp32 GEMM forms as fma(-2, q.x, ||x||^2) (or -q.x), at 16 times the fp32 MFMA rate, with the
+// threshold test reduced to one compare per value.  k_query_prep writes the fp16 B operand
+// and clears a flag when a query of the batch falls outside these bounds; the batch then takes
+// the fp32 GEMM.
+#include <algorithm>
+#include <string>
+
+#include "gemm.h"
+#include "vdbg_device.h"
+#include "vdbg_internal.h"
+
+namespace vdbg {
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (plain loads)
+
+// Block = 4 waves x (32 QB) queries each x one chunk of rows; block b takes work item
+// (b % 8) * per_xcd + b / 8 so the items of one XCD are consecutive and share row chunks in
+// its L2.  Rows stream through double-buffered 64-row LDS stages (K chunks of KC dims for
+// wide rows), row norms through three slots.
+//
+// Operand layout of v_mfma_f32_32x32x16_f16: per 16-dim K block, lane l holds dims
+// 8 (l / 32) .. 8 (l / 32) + 7 of row l % 32 (A, from LDS) and of query l % 32 (B, kept in
+// VGPRs for the whole launch); lane l's 16 outputs are rows 8 (r / 4) + 4 (l / 32) + r % 4 of
+// the 32-row block against query l % 32.  Each A fragment read from LDS feeds QB MFMAs.
+//
+// MODE 0: every value at or below the query's threshold T goes to the lane's candidate
+// buffer (per query, chunk and lane half).  The test is one compare per value; only a value
+// that passes on some lane of the wave (a wave-uniform branch) pays for the write.
+// MODE 1: minimum value of each 16-row group (the rows one lane holds of a 32-row block).
+template <int PD, int METRIC, int QB, int MODE>
+__global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
+  constexpr int KC = GemmKc(PD);
+  constexpr int NKC = PD / KC;
+  constexpr int NKB = KC / 16;                     // 16-dim MFMA K blocks per stage
+  constexpr int STR = KC + 8;                      // LDS row stride in halfs (16 B padding)
+  constexpr int VEC_PER_ROW = KC / 8;              // uint4 = 8 halfs
+  constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
+  constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
+  constexpr int QT = 128 * QB;                     // queries per block
+  static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmRows * STR];
+  __shared__ __attribute__((aligned(16))) float xns[3][kGemmRows];
+
+  const int b = blockIdx.x;
+  const int item = (b & 7) * a.per_xcd + (b >> 3);
+  if (item >= a.items) return;
+  const int chunk = item / a.nqt;
+  const int qt = item - chunk * a.nqt;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int q0 = qt * QT + wave * 32 * QB;  // first query of the wave
+  const bool wave_live = q0 < a.nq;
+  const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
+  const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
+
+  int q[QB];
+  float T[QB];
+  uint2* out[QB];
+  uint32_t cnt[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    q[qb] = q0 + qb * 32 + j;
+    cnt[qb] = 0;
+    if constexpr (MODE == 0) {
+      T[qb] = q[qb] < a.nq ? a.T[q[qb]] : -__builtin_inff();
+      out[qb] = a.cand + ((size_t(q[qb]) * a.nchunks + chunk) * 2 + h) * size_t(a.caph);
+    }
+  }
+
+  // Every load below is unconditional (addresses clamped into the rows, queries and norms
+  // that exist), so each wave has a fixed count of loads in flight and the waits before the
+  // LDS stores do not drain the prefetch early.  Lanes of queries past the batch read query
+  // nq - 1; their values are never emitted.
+  half8 qv[QB][NKB];
+  const uint16_t* qrow[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) qrow[qb] = a.Q16 + size_t(min(q[qb], a.nq - 1)) * PD + h * 8;
+  auto load_q = [&](int kc) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        qv[qb][kb] = *reinterpret_cast<const half8*>(qrow[qb] + kc * KC + kb * 16);
+  };
+  if (NKC == 1) load_q(0);
+
+  // lane offsets (in halfs) of the stage's 16-byte vectors: row f / VEC_PER_ROW, column
+  // f % VEC_PER_ROW of the 64 x KC stage
+  int voff[VEC_PER_THREAD];
+  int vrow[VEC_PER_THREAD];
+#pragma unroll
+  for (int i = 0; i < VEC_PER_THREAD; ++i) {
+    const int f = min(tid + 256 * i, VEC_PER_TILE - 1);
+    vrow[i] = f / VEC_PER_ROW;
+    voff[i] = vrow[i] * PD + (f % VEC_PER_ROW) * 8;
+  }
+  u32x4 pre[VEC_PER_THREAD];
+  float pre_n = 0.f;
+  // stage (base, kc): rows base..base+63, dims kc*KC..kc*KC+KC-1.  Rows past r_end repeat the
+  // last valid row and get a NaN accumulator start, so no compare passes them and no group
+  // minimum takes them.
+  auto load_stage = [&](uint32_t base, int kc) {
+    const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
+    const uint16_t* tile = a.X16 + size_t(base) * PD + kc * KC;
+    const int over = int(valid) - 1;  // rows past it read row `over`
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int o = voff[i] - max(0, vrow[i] - over) * PD;
+      pre[i] = *reinterpret_cast<const u32x4*>(tile + o);
+    }
+    if (kc == 0) {
+      const float n = a.rn[base + min(uint32_t(tid & 63), valid - 1)];
+      pre_n = uint32_t(tid & 63) < valid ? (METRIC == 0 ? n : 0.f) : __builtin_nanf("");
+    }
+  };
+  auto store_stage = [&](int buf, int kc, int nslot) {
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int f = tid + 256 * i;
+      if (VEC_PER_TILE % 256 == 0 || f < VEC_PER_TILE)
+        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) = pre[i];
+    }
+    if (kc == 0 && tid < kGemmRows) xns[nslot][tid] = pre_n;
+  };
+
+  if (r_begin >= r_end) return;  // (every planned chunk holds rows)
+  load_stage(r_begin, 0);
+  store_stage(0, 0, 0);
+  __syncthreads();
+
+  int buf = 0;
+  int slot = 0;  // norm slot of the current tile
+  for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
+    // accumulators start from the row norms (L2) or zero (inner product), NaN past r_end
+    v16f init[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 n4 = *reinterpret_cast<const float4*>(&xns[slot][blk * 32 + 8 * g + 4 * h]);
+        init[blk][4 * g + 0] = n4.x;
+        init[blk][4 * g + 1] = n4.y;
+        init[blk][4 * g + 2] = n4.z;
+        init[blk][4 * g + 3] = n4.w;
+      }
+    }
+    v16f acc[QB][2];
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      acc[qb][0] = init[0];
+      acc[qb][1] = init[1];
+    }
+#pragma unroll 1
+    for (int kc = 0; kc < NKC; ++kc) {
+      // prefetch the next stage: the next K chunk of this tile, or chunk 0 of the next tile
+      const bool last_kc = kc + 1 == NKC;
+      const uint32_t nbase = last_kc ? base + kGemmRows : base;
+      const int nkc = last_kc ? 0 : kc + 1;
+      const bool have_next = nbase < r_end;
+      if (have_next) load_stage(nbase, nkc);
+      if (NKC > 1) load_q(kc);
+
+      // waves past the batch run the MFMAs too (on query nq - 1): no branch splits the
+      // accumulator chains; their values are never emitted
+      const uint16_t* xa0 = &xs[buf][j * STR + h * 8];
+      const uint16_t* xa1 = xa0 + 32 * STR;
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const half8 x0 = *reinterpret_cast<const half8*>(xa0 + kb * 16);
+        const half8 x1 = *reinterpret_cast<const half8*>(xa1 + kb * 16);
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[qb][kb], acc[qb][0], 0, 0, 0);
+          acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[qb][kb], acc[qb][1], 0, 0, 0);
+        }
+      }
+
+      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? (slot == 2 ? 0 : slot + 1) : slot);
+      __syncthreads();
+      buf ^= 1;
+    }
+
+    const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
+    if (wave_live && MODE == 0) {
+      // one compare per value; a value passing on some lane of the wave branches to the write
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float v = acc[qb][blk][r];
+            if (__builtin_amdgcn_ballot_w64(v <= T[qb]) != 0) {
+              const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
+              if (v <= T[qb] && row_allowed(a.allow, row)) {
+                if (cnt[qb] < uint32_t(a.caph))
+                  out[qb][cnt[qb]] = make_uint2(__float_as_uint(v), row);
+                ++cnt[qb];
+              }
+            }
+          }
+    } else if (wave_live) {
+      // fminf skips the NaN values of rows past r_end
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          float m = __builtin_inff();
+          if (a.allow == nullptr) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) m = fminf(m, acc[qb][blk][r]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
+              if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, acc[qb][blk][r]);
+            }
+          }
+          if (q[qb] < a.nq) {
+            const uint32_t grp = ((base >> 5) + blk) * 2 + h;
+            if (grp < uint32_t(a.ngroups)) a.gm[size_t(q[qb]) * a.ngroups + grp] = m;
+          }
+        }
+    }
+    slot = slot == 2 ? 0 : slot + 1;
+  }
+
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (q[qb] < a.nq) {
+        const size_t seg = (size_t(q[qb]) * a.nchunks + chunk) * 2 + h;
+        a.counts[seg] = min(cnt[qb], uint32_t(a.caph));
+        if (cnt[qb] > uint32_t(a.caph)) a.ovf[q[qb]] = 1;
+      }
+    }
+  }
+}
+
+template <int PD>
+static void launch16_pd(int metric, int qb, int mode, hipStream_t s, int blocks,
+                        const GemmArgs& a) {
+  const dim3 g(blocks), t(256);
+  if (metric == 0) {
+    if (mode == 0) {
+      if (qb == 1) k_gemm16<PD, 0, 1, 0><<<g, t, 0, s>>>(a);
+      else k_gemm16<PD, 0, 2, 0><<<g, t, 0, s>>>(a);
+    } else {
+      k_gemm16<PD, 0, 2, 1><<<g, t, 0, s>>>(a);
+    }
+  } else {
+    if (mode == 0) {
+      if (qb == 1) k_gemm16<PD, 1, 1, 0><<<g, t, 0, s>>>(a);
+      else k_gemm16<PD, 1, 2, 0><<<g, t, 0, s>>>(a);
+    } else {
+      k_gemm16<PD, 1, 2, 1><<<g, t, 0, s>>>(a);
+    }
+  }
+}
+
+int LaunchGemm16(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+                 const GemmArgs& a) {
+  if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM16: query blocks per wave");
+  if (mode == 1 && qb != 2) return SetError(kInternal, "GEMM16: the sample pass runs 2 query blocks");
+  switch (pd) {
+    case 16: launch16_pd<16>(metric, qb, mode, s, blocks, a); break;
+    case 32: launch16_pd<32>(metric, qb, mode, s, blocks, a); break;
+    case 48: launch16_pd<48>(metric, qb, mode, s, blocks, a); break;
+    case 64: launch16_pd<64>(metric, qb, mode, s, blocks, a); break;
+    case 80: launch16_pd<80>(metric, qb, mode, s, blocks, a); break;
+    case 96: launch16_pd<96>(metric, qb, mode, s, blocks, a); break;
+    case 112: launch16_pd<112>(metric, qb, mode, s, blocks, a); break;
+    case 128: launch16_pd<128>(metric, qb, mode, s, blocks, a); break;
+    case 192: launch16_pd<192>(metric, qb, mode, s, blocks, a); break;
+    case 256: launch16_pd<256>(metric, qb, mode, s, blocks, a); break;
+    case 384: launch16_pd<384>(metric, qb, mode, s, blocks, a); break;
+    case 512: launch16_pd<512>(metric, qb, mode, s, blocks, a); break;
+    case 768: launch16_pd<768>(metric, qb, mode, s, blocks, a); break;
+    case 960: launch16_pd<960>(metric, qb, mode, s, blocks, a); break;
+    case 1024: launch16_pd<1024>(metric, qb, mode, s, blocks, a); break;
+    default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
+  }
+  return kOk;
+}
+
+__global__ void k_to_f16(const float* __restrict__ x, size_t n, uint16_t* __restrict__ y) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(x[i]));
+}
+
+int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, const RowStats& st,
+               uint16_t** out) {
+  *out = nullptr;
+  if (n == 0 || !st.all_int || !(st.max_abs <= 2048.f) || !GemmSupported(pd)) return kOk;
+  uint16_t* y = nullptr;
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * sizeof(uint16_t)));
+  k_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, y);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    (void)hipFree(y);
+    return SetError(kInternal, std::string("fp16 rows: ") + hipGetErrorString(e));
+  }
+  *out = y;
+  return kOk;
+}
+
+}  // namespace vdbg

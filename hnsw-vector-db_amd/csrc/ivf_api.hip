@@ -289,6 +289,7 @@ int vdbg_ivfpq_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_ivfpq**
     delete h;
     return rc;
   }
+  ++ds->d.live_indexes;
   *out = h;
   return kOk;
 }
@@ -313,6 +314,7 @@ int vdbg_ivfpq_destroy(vdbg_ivfpq* ix) {
   std::lock_guard<std::recursive_mutex> g(c->mu);
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
+  --ix->x.ds->live_indexes;
   FreeIvf(&ix->x);
   delete ix;
   return kOk;

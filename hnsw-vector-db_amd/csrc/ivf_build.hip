@@ -646,6 +646,7 @@ int vdbg_ivfpq_build(vdbg_dataset* ds, size_t nlist, size_t pq_m, uint64_t seed,
     delete h;
     return rc;
   }
+  ++ds->d.live_indexes;
   *out = h;
   return kOk;
 }

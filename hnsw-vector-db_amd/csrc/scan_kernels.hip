@@ -26,12 +26,11 @@
 #include <cmath>
 #include <cstring>
 
+#include "gemm.h"
 #include "vdbg_device.h"
 #include "vdbg_internal.h"
 
 namespace vdbg {
-
-typedef float v16f __attribute__((ext_vector_type(16)));
 
 // ================================================================ small helpers
 
@@ -170,8 +169,6 @@ int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
   out->all_int = h.all_int;
   return kOk;
 }
-
-static bool GemmSupported(size_t pd);
 
 // ================================================================ SQ8 train / encode
 
@@ -314,9 +311,10 @@ int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* sca
 
 // Sample position p holds row floor(bitrev(p) * N / Smax): every power-of-two prefix of the
 // sample is an evenly strided subset of the rows.
-__global__ void k_gather_sample(const float* __restrict__ X, const uint8_t* __restrict__ C,
-                                const float* __restrict__ rn, uint32_t N, int pd, int bits,
-                                uint32_t smax, float* __restrict__ SX,
+__global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __restrict__ X16,
+                                const uint8_t* __restrict__ C, const float* __restrict__ rn,
+                                uint32_t N, int pd, int bits, uint32_t smax,
+                                float* __restrict__ SX, uint16_t* __restrict__ SX16,
                                 uint8_t* __restrict__ SC, float* __restrict__ Srn,
                                 uint32_t* __restrict__ Sid) {
   const uint32_t p = blockIdx.x;
@@ -324,6 +322,7 @@ __global__ void k_gather_sample(const float* __restrict__ X, const uint8_t* __re
   const uint32_t row = uint32_t((uint64_t(bitrev(p, bits)) * N) / smax);
   for (int i = threadIdx.x; i < pd; i += blockDim.x) {
     if (X) SX[size_t(p) * pd + i] = X[size_t(row) * pd + i];
+    if (X16) SX16[size_t(p) * pd + i] = X16[size_t(row) * pd + i];
     if (C) SC[size_t(p) * pd + i] = C[size_t(row) * pd + i];
   }
   if (threadIdx.x == 0) {
@@ -341,14 +340,17 @@ int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
   const size_t pd = src->pd;
   if (src->kind == 0)
     VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX), size_t(smax) * pd * sizeof(float)));
-  else
+  if (src->kind == 0 && src->X16 != nullptr)
+    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX16), size_t(smax) * pd * sizeof(uint16_t)));
+  if (src->kind == 1)
     VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SC), size_t(smax) * pd));
   VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Srn), size_t(smax) * sizeof(float)));
   VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Sid), size_t(smax) * sizeof(uint32_t)));
   k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
+                                             src->kind == 0 ? src->X16 : nullptr,
                                              src->kind == 1 ? src->C : nullptr, src->rn,
-                                             src->N, int(pd), bits, smax, src->SX, src->SC,
-                                             src->Srn, src->Sid);
+                                             src->N, int(pd), bits, smax, src->SX, src->SX16,
+                                             src->SC, src->Srn, src->Sid);
   VDBG_HIP(hipGetLastError());
   src->Smax = smax;
   return kOk;
@@ -356,10 +358,12 @@ int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
 
 void FreeSample(ScanSource* src) {
   (void)hipFree(src->SX);
+  (void)hipFree(src->SX16);
   (void)hipFree(src->SC);
   (void)hipFree(src->Srn);
   (void)hipFree(src->Sid);
   src->SX = nullptr;
+  src->SX16 = nullptr;
   src->SC = nullptr;
   src->Srn = nullptr;
   src->Sid = nullptr;
@@ -379,8 +383,8 @@ struct PrepArgs {
   float* shift;  // exact distance ~= GEMM value + shift
   float* eb;     // bound on |GEMM value + shift - exact distance|
   int* exact;    // the bound is zero
-  uint16_t* Q16;  // nullable: the queries as fp16 (for the exact-integer GEMM)
-  int* all16;     // nullable: cleared when a query is not exact or exceeds 2048 in magnitude
+  uint16_t* Q16;  // nullable: the fp16 GEMM's B operand (gemm16.hip)
+  int* all16;     // nullable: cleared when a query is outside the fp16 GEMM's exact bounds
 };
 
 // One wave per query.
@@ -407,7 +411,9 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     hi = fmaxf(hi, e);
     ma = fmaxf(ma, fabsf(e));
     ai &= (e == rintf(e)) ? 1 : 0;
-    if (a.Q16 != nullptr) a.Q16[size_t(q) * a.pd + i] = __builtin_bit_cast(uint16_t, _Float16(e));
+    if (a.Q16 != nullptr)  // the fp16 GEMM's B operand: -2 q (L2) or -q (inner product)
+      a.Q16[size_t(q) * a.pd + i] =
+          __builtin_bit_cast(uint16_t, _Float16(a.metric == 0 ? -2.f * e : -e));
     if (a.kind == 1) {
       if (a.metric == 0) {
         const float qp = e - a.vmin[i];
@@ -442,10 +448,16 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     }
     a.shift[q] = shift;
     a.exact[q] = ex ? 1 : 0;
-    // fp16 holds every integer of magnitude <= 2048 exactly: with exact sums, an fp16-input
-    // GEMM then gives the fp32 GEMM's values bit for bit
-    if (a.all16 != nullptr && !(ex && ma <= 2048.f && a.xs.max_abs <= 2048.f))
-      atomicAnd(a.all16, 0);
+    // fp16 holds every integer of magnitude <= 2048 exactly (and -2 q, an even integer of
+    // magnitude <= 4096); the fp16 GEMM accumulates ||x||^2 - 2 q.x (or -q.x) from the row
+    // norm, every partial sum bounded by (|q| + R)^2 with R the largest row norm.  Below 2^24
+    // its values are the fp32 GEMM's bit for bit.
+    if (a.all16 != nullptr) {
+      const double rq = sqrt(double(s)), rx = sqrt(double(a.xs.xn_max));
+      const bool fits = ex && ma <= 2048.f && a.xs.max_abs <= 2048.f &&
+                        (rq + rx) * (rq + rx) * 1.001 < lim;
+      if (!fits) atomicAnd(a.all16, 0);
+    }
     // Rounding bound of |GEMM value + shift - exact distance|.  Any fp32 summation order of
     // n products errs by at most ~n u sum|q_i x_i| (u = 2^-24), and sum|q_i x_i| <= |q||x|.
     // Inner product of fp32 rows: the MFMA dot and the exact dot each err by that, so
@@ -461,35 +473,6 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
 }
 
 // ================================================================ MFMA GEMM
-
-struct GemmArgs {
-  const float* X;      // fp32 rows (KIND 0)
-  const uint16_t* X16; // fp16 rows (k_gemm16)
-  const uint16_t* Q16; // fp16 queries (k_gemm16)
-  const uint8_t* C;    // code rows (KIND 1)
-  const float* rn;     // row norms of the GEMM form
-  const uint32_t* rid; // MODE 1: original row id of each sample row
-  const float* Qb;
-  const float* T;
-  const uint64_t* allow;
-  uint2* cand;         // MODE 0: [(q * nchunks + chunk) * 2 + half][caph]
-  uint32_t* counts;    // MODE 0: [(q * nchunks + chunk) * 2 + half]
-  int* ovf;            // MODE 0: [q]
-  float* gm;           // MODE 1: [q][ngroups] minimum GEMM value of each 16-row group
-  int ngroups;
-  uint32_t N;
-  int nq, nqt;
-  uint32_t chunk_rows;
-  int nchunks, caph;
-  int items;           // nqt * nchunks
-  int per_xcd;         // items assigned to each of the 8 XCDs
-};
-
-constexpr int kGemmRows = 64;  // rows per LDS tile (two 32-row MFMA blocks)
-
-__host__ __device__ constexpr int GemmKc(int pd) {
-  return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : (pd % 32 == 0 ? 32 : 16)));
-}
 
 // Block = 4 waves = 128 queries (32 per wave) x one chunk of rows.  Blocks are dispatched
 // round-robin over the 8 XCDs, so block b takes work item (b % 8) * per_xcd + b / 8: the
@@ -723,184 +706,6 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
     if (cnt > uint32_t(a.caph)) a.ovf[q] = 1;
   }
 }
-
-// ================================================================ exact-integer GEMM
-
-typedef _Float16 half8 __attribute__((ext_vector_type(8)));
-
-// The main pass for integer-valued rows and queries (every value an integer of magnitude
-// <= 2048, every partial sum below 2^24): inputs in fp16 hold each value exactly, each fp16
-// product is exact in fp32 and so is every sum, so v_mfma_f32_32x32x16_f16 yields exactly
-// the values of the fp32 GEMM at 16 times its rate.  The structure is k_gemm's (block =
-// 4 waves = 128 queries x one row chunk, XCD-aware item order, double-buffered 64-row LDS
-// stages, three norm slots, threshold epilogue into per-(query, chunk, half) buffers); rows
-// are staged as fp16.  Lane l of a wave holds, per 16-dim K block, dims 8 (l / 32) .. + 7 of
-// query l % 32 as the B operand; the A operand is the same dims of row l % 32 of a 32-row
-// block.
-template <int PD, int METRIC>
-__global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
-  constexpr int KC = GemmKc(PD);
-  constexpr int NKC = PD / KC;
-  constexpr int NKB = KC / 16;     // 16-dim MFMA K blocks per stage
-  constexpr int STR = KC + 8;      // padded LDS row stride (halfs): 16 bytes of padding
-  constexpr int VEC_PER_ROW = KC / 8;             // uint4 = 8 halfs
-  constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
-  constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
-  static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
-  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmRows * STR];
-  __shared__ float xns[3][kGemmRows];
-
-  const int b = blockIdx.x;
-  const int item = (b & 7) * a.per_xcd + (b >> 3);
-  if (item >= a.items) return;
-  const int chunk = item / a.nqt;
-  const int qt = item - chunk * a.nqt;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6;
-  const int lane = tid & 63;
-  const int j = lane & 31;
-  const int h = lane >> 5;
-  const int q = qt * 128 + wave * 32 + j;
-  const bool wave_live = qt * 128 + wave * 32 < a.nq;
-  const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
-  const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
-
-  half8 qb[NKB];
-  auto load_q = [&](int kc) {
-#pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      if (q < a.nq) {
-        const uint4 v = *reinterpret_cast<const uint4*>(a.Q16 + size_t(q) * PD + kc * KC + kb * 16 + h * 8);
-        qb[kb] = __builtin_bit_cast(half8, v);
-      } else {
-        qb[kb] = half8{};
-      }
-    }
-  };
-  if (NKC == 1) load_q(0);
-  const float T = q < a.nq ? a.T[q] : -__builtin_inff();
-  const size_t seg = (size_t(q) * a.nchunks + chunk) * 2 + h;
-  uint2* out = a.cand + seg * size_t(a.caph);
-  uint32_t cnt = 0;
-
-  uint4 pre[VEC_PER_THREAD];
-  float pre_n = 0.f;
-  auto load_stage = [&](uint32_t base, int kc) {
-    const uint32_t valid = r_end > base ? min(uint32_t(kGemmRows), r_end - base) : 0u;
-#pragma unroll
-    for (int i = 0; i < VEC_PER_THREAD; ++i) {
-      const int f = tid + 256 * i;
-      const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
-      if (f < VEC_PER_TILE && uint32_t(row) < valid)
-        pre[i] = *reinterpret_cast<const uint4*>(a.X16 + size_t(base + row) * PD + kc * KC + c * 8);
-      else
-        pre[i] = make_uint4(0u, 0u, 0u, 0u);
-    }
-    if (kc == 0) pre_n = (tid < kGemmRows && uint32_t(tid) < valid) ? a.rn[base + tid] : 0.f;
-  };
-  auto store_stage = [&](int buf, int kc, int nslot) {
-#pragma unroll
-    for (int i = 0; i < VEC_PER_THREAD; ++i) {
-      const int f = tid + 256 * i;
-      if (f < VEC_PER_TILE) {
-        const int row = f / VEC_PER_ROW, c = f % VEC_PER_ROW;
-        *reinterpret_cast<uint4*>(&xs[buf][row * STR + c * 8]) = pre[i];
-      }
-    }
-    if (kc == 0 && tid < kGemmRows) xns[nslot][tid] = pre_n;
-  };
-
-  if (r_begin < r_end) {
-    load_stage(r_begin, 0);
-    store_stage(0, 0, 0);
-  }
-  __syncthreads();
-
-  int buf = 0;
-  int slot = 0;
-  for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
-    v16f acc0 = {}, acc1 = {};
-#pragma unroll 1
-    for (int kc = 0; kc < NKC; ++kc) {
-      const bool last_kc = kc + 1 == NKC;
-      const uint32_t nbase = last_kc ? base + kGemmRows : base;
-      const int nkc = last_kc ? 0 : kc + 1;
-      const bool have_next = nbase < r_end;
-      if (have_next) load_stage(nbase, nkc);
-      if (NKC > 1 && wave_live) load_q(kc);
-      if (wave_live) {
-        const uint16_t* xa0 = &xs[buf][j * STR + h * 8];
-        const uint16_t* xa1 = xa0 + 32 * STR;
-#pragma unroll
-        for (int kb = 0; kb < NKB; ++kb) {
-          const half8 x0 = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(xa0 + kb * 16));
-          const half8 x1 = __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(xa1 + kb * 16));
-          acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qb[kb], acc0, 0, 0, 0);
-          acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qb[kb], acc1, 0, 0, 0);
-        }
-      }
-      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? (slot == 2 ? 0 : slot + 1) : slot);
-      __syncthreads();
-      buf ^= 1;
-    }
-    if (wave_live) {
-      uint32_t pass = 0;
-#pragma unroll
-      for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const float g = blk == 0 ? acc0[r] : acc1[r];
-          const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
-          pass |= (v <= T ? 1u : 0u) << (blk * 16 + r);
-        }
-      if (__ballot(pass != 0) != 0) {
-#pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            if (pass & (1u << (blk * 16 + r))) {
-              const int rl = blk * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-              const float g = blk == 0 ? acc0[r] : acc1[r];
-              const float v = METRIC == 0 ? fmaf(-2.f, g, xns[slot][rl]) : -g;
-              const uint32_t row = base + rl;
-              if (q < a.nq && row < r_end && row_allowed(a.allow, row)) {
-                if (cnt < uint32_t(a.caph)) out[cnt] = make_uint2(__float_as_uint(v), row);
-                ++cnt;
-              }
-            }
-          }
-      }
-    }
-    slot = slot == 2 ? 0 : slot + 1;
-  }
-  if (q < a.nq) {
-    a.counts[seg] = min(cnt, uint32_t(a.caph));
-    if (cnt > uint32_t(a.caph)) a.ovf[q] = 1;
-  }
-}
-
-__global__ void k_to_f16(const float* __restrict__ x, size_t n, uint16_t* __restrict__ y) {
-  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
-  if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(x[i]));
-}
-
-int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, const RowStats& st,
-               uint16_t** out) {
-  *out = nullptr;
-  if (n == 0 || !st.all_int || !(st.max_abs <= 2048.f) || !GemmSupported(pd)) return kOk;
-  uint16_t* y = nullptr;
-  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * sizeof(uint16_t)));
-  k_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, y);
-  const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) {
-    (void)hipFree(y);
-    return SetError(kInternal, std::string("fp16 rows: ") + hipGetErrorString(e));
-  }
-  *out = y;
-  return kOk;
-}
-
 
 // ================================================================ threshold from groups
 
@@ -1347,16 +1152,6 @@ static int ExactScan(Ctx* c, Workspace& w, const ScanSource& src, const float* Q
   return ExactScanT(c, w, src, Sq8Of(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
 }
 
-static bool GemmSupported(size_t pd) {
-  switch (pd) {
-    case 16: case 32: case 48: case 64: case 80: case 96: case 112: case 128:
-    case 192: case 256: case 384: case 512: case 768: case 960: case 1024:
-      return true;
-    default:
-      return false;
-  }
-}
-
 template <int PD, int METRIC, int KIND, int MODE>
 static void launch_gemm(hipStream_t s, int blocks, const GemmArgs& a) {
   k_gemm<PD, METRIC, KIND, MODE><<<dim3(blocks), 256, 0, s>>>(a);
@@ -1402,36 +1197,6 @@ static int LaunchGemm(size_t pd, int metric, int kind, int mode, hipStream_t s, 
     case 768: launch_gemm_pd<768>(metric, kind, mode, s, blocks, a); break;
     case 960: launch_gemm_pd<960>(metric, kind, mode, s, blocks, a); break;
     case 1024: launch_gemm_pd<1024>(metric, kind, mode, s, blocks, a); break;
-    default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
-  }
-  return kOk;
-}
-
-template <int PD>
-static void launch_gemm16_pd(int metric, hipStream_t s, int blocks, const GemmArgs& a) {
-  if (metric == 0)
-    k_gemm16<PD, 0><<<dim3(blocks), 256, 0, s>>>(a);
-  else
-    k_gemm16<PD, 1><<<dim3(blocks), 256, 0, s>>>(a);
-}
-
-static int LaunchGemm16(size_t pd, int metric, hipStream_t s, int blocks, const GemmArgs& a) {
-  switch (pd) {
-    case 16: launch_gemm16_pd<16>(metric, s, blocks, a); break;
-    case 32: launch_gemm16_pd<32>(metric, s, blocks, a); break;
-    case 48: launch_gemm16_pd<48>(metric, s, blocks, a); break;
-    case 64: launch_gemm16_pd<64>(metric, s, blocks, a); break;
-    case 80: launch_gemm16_pd<80>(metric, s, blocks, a); break;
-    case 96: launch_gemm16_pd<96>(metric, s, blocks, a); break;
-    case 112: launch_gemm16_pd<112>(metric, s, blocks, a); break;
-    case 128: launch_gemm16_pd<128>(metric, s, blocks, a); break;
-    case 192: launch_gemm16_pd<192>(metric, s, blocks, a); break;
-    case 256: launch_gemm16_pd<256>(metric, s, blocks, a); break;
-    case 384: launch_gemm16_pd<384>(metric, s, blocks, a); break;
-    case 512: launch_gemm16_pd<512>(metric, s, blocks, a); break;
-    case 768: launch_gemm16_pd<768>(metric, s, blocks, a); break;
-    case 960: launch_gemm16_pd<960>(metric, s, blocks, a); break;
-    case 1024: launch_gemm16_pd<1024>(metric, s, blocks, a); break;
     default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
   }
   return kOk;
@@ -1484,12 +1249,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   if (!gemm) return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
   VDBG_RETURN_IF_ERROR(BuildSample(c, src, s));
 
-  // ---- plan
+  // ---- plan: the fp32 GEMM runs 128 queries per block; the fp16 GEMM 256 (64 per wave,
+  // each LDS row fragment feeding two MFMAs), or 128 for batches of at most 128 queries
   const int slots = 2 * c->cu_count;
-  const int nqt = int((nq + 127) / 128);
-  const int nchunks = PlanChunks(nqt, N, slots, kMaxSeg / 2);
-  uint32_t chunk_rows = (N + nchunks - 1) / nchunks;
-  chunk_rows = (chunk_rows + 63) / 64 * 64;
   // Sample size: about kk * N / S rows pass the threshold per query, and every pass is a
   // scattered buffer write plus a select insertion, while the pre-pass costs S / N of the
   // main GEMM; N / 64 keeps both near 1.5%.
@@ -1497,25 +1259,46 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   while (S < std::max<uint32_t>(16u * std::max<uint32_t>(128, 4 * uint32_t(kk)), N / 64)) S *= 2;
   S = std::min(S, src->Smax);
   const int ngroups = int((S + 31) / 32) * 2;
-  const int schunks = PlanChunks(nqt, S, slots, int((S + 63) / 64));
-  uint32_t schunk_rows = (S + schunks - 1) / schunks;
-  schunk_rows = (schunk_rows + 63) / 64 * 64;
-  const double expect_seg = double(kk) * N / S * 1.5 / (2.0 * nchunks);
-  int caph = 32;
-  while (caph < 3.0 * expect_seg + 32) caph <<= 1;
-  const int nseg = 2 * nchunks;
+  struct Plan {
+    int qb, nqt, nchunks, caph, nseg, schunks;
+    uint32_t chunk_rows, schunk_rows;
+  };
+  auto make_plan = [&](int qb) {
+    Plan p{};
+    p.qb = qb;
+    p.nqt = int((nq + 128 * qb - 1) / (128 * qb));
+    p.nchunks = PlanChunks(p.nqt, N, slots, kMaxSeg / 2);
+    p.chunk_rows = (N + p.nchunks - 1) / p.nchunks;
+    p.chunk_rows = (p.chunk_rows + 63) / 64 * 64;
+    p.nchunks = int((N + p.chunk_rows - 1) / p.chunk_rows);
+    p.schunks = PlanChunks(p.nqt, S, slots, int((S + 63) / 64));
+    p.schunk_rows = (S + p.schunks - 1) / p.schunks;
+    p.schunk_rows = (p.schunk_rows + 63) / 64 * 64;
+    p.schunks = int((S + p.schunk_rows - 1) / p.schunk_rows);
+    const double expect_seg = double(kk) * N / S * 1.5 / (2.0 * p.nchunks);
+    p.caph = 32;
+    while (p.caph < 3.0 * expect_seg + 32) p.caph <<= 1;
+    p.nseg = 2 * p.nchunks;
+    return p;
+  };
+  // integer-valued rows with an fp16 copy: the batch may take the exact-integer GEMM
+  const bool try16 = src->kind == 0 && src->X16 != nullptr;
+  const Plan p32 = make_plan(1);
+  const Plan p16 = make_plan(nq > 128 ? 2 : 1);
+  auto cand_bytes = [&](const Plan& p) {
+    return size_t(nq) * p.nseg * (sizeof(uint32_t) + size_t(p.caph) * sizeof(uint2));
+  };
+  // counts then candidates, the candidates 256-byte aligned
+  const size_t cand_need = std::max(cand_bytes(p32), try16 ? cand_bytes(p16) : 0) + 256;
   const int Esel = pow2_e(kk + 16);
 
   Workspace& w = c->ws;
   w.used = 0;
   const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
-                      size_t(nq) * ngroups * sizeof(float) +
-                      size_t(nq) * nseg * (sizeof(uint32_t) + size_t(caph) * sizeof(uint2)) +
-                      (src->X16 != nullptr ? nq * pd * sizeof(uint16_t) : 0) + 18 * 256;
+                      size_t(nq) * ngroups * sizeof(float) + cand_need +
+                      (try16 ? nq * pd * sizeof(uint16_t) : 0) + 18 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
-  // integer-valued rows with an fp16 copy: the batch may take the exact-integer GEMM
-  const bool try16 = src->kind == 0 && src->X16 != nullptr;
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
   float* T = w.take<float>(nq);
@@ -1526,8 +1309,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* fb2_list = w.take<uint32_t>(nq);
   float* Qb = src->kind == 1 ? w.take<float>(nq * pd) : nullptr;
   float* gm = w.take<float>(size_t(nq) * ngroups);
-  uint32_t* counts = w.take<uint32_t>(size_t(nq) * nseg);
-  uint2* cand = w.take<uint2>(size_t(nq) * nseg * caph);
+  char* cand_base = w.take<char>(cand_need);
   uint16_t* Q16 = try16 ? w.take<uint16_t>(nq * pd) : nullptr;
   int* all16 = try16 ? w.take<int>(1) : nullptr;
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
@@ -1548,6 +1330,13 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     use16 = c->host_pinned[0] != 0;
   }
   c->last_gemm_bits = use16 ? 16 : 32;
+  const Plan& P = use16 ? p16 : p32;
+  const int nchunks = P.nchunks;
+  const int caph = P.caph;
+  const int nseg = P.nseg;
+  uint32_t* counts = reinterpret_cast<uint32_t*>(cand_base);
+  uint2* cand = reinterpret_cast<uint2*>(
+      cand_base + ((size_t(nq) * nseg * sizeof(uint32_t) + 255) & ~size_t(255)));
   const float* B = src->kind == 1 ? Qb : Q;
   const int metric = src->metric == 0 ? 0 : 1;
 
@@ -1563,12 +1352,21 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   sg.ngroups = ngroups;
   sg.N = S;
   sg.nq = int(nq);
-  sg.chunk_rows = schunk_rows;
+  sg.chunk_rows = P.schunk_rows;
   int sblocks = 0;
-  GemmGrid(sg, nqt, int((S + schunk_rows - 1) / schunk_rows), &sblocks);
   {
     ProfScope ps(c, "sample_gemm", s);
-    VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 1, s, sblocks, sg));
+    if (use16 && P.qb == 2) {
+      sg.X16 = src->SX16;
+      sg.Q16 = Q16;
+      GemmGrid(sg, P.nqt, P.schunks, &sblocks);
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, s, sblocks, sg));
+    } else {
+      // the fp32 sample pass runs 128-query tiles
+      GemmGrid(sg, p32.nqt, p32.schunks, &sblocks);
+      sg.chunk_rows = p32.schunk_rows;
+      VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 1, s, sblocks, sg));
+    }
     VDBG_HIP(hipGetLastError());
   }
   KthArgs ka{gm, ngroups, int(nq), int(kk), eb, T};
@@ -1591,16 +1389,16 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   ga.ovf = ovf;
   ga.N = N;
   ga.nq = int(nq);
-  ga.chunk_rows = chunk_rows;
+  ga.chunk_rows = P.chunk_rows;
   ga.caph = caph;
   int blocks = 0;
-  GemmGrid(ga, nqt, nchunks, &blocks);
+  GemmGrid(ga, P.nqt, nchunks, &blocks);
   {
     ProfScope ps(c, src->kind == 0 ? "flat_gemm" : "sq8_gemm", s);
     if (use16) {
       ga.X16 = src->X16;
       ga.Q16 = Q16;
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, s, blocks, ga));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, s, blocks, ga));
     } else {
       VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
     }

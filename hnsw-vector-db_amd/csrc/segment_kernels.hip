@@ -153,6 +153,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   cs.rn = rn;
   cs.N = count;
   cs.SX = nullptr;
+  cs.SX16 = nullptr;
   cs.SC = nullptr;
   cs.Srn = nullptr;
   cs.Sid = nullptr;

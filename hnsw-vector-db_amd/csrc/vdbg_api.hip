@@ -155,6 +155,7 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   d.src.metric = metric;
   d.src.rmag = d.stats.xn_max;
   d.src.stats = d.stats;
+  ++c->live_datasets;
   *out = ds;
   return kOk;
 }
@@ -314,6 +315,11 @@ const char* vdbg_ctx_kernels(vdbg_ctx* ctx) {
 int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   if (ctx == nullptr) return kOk;
   Ctx& c = ctx->c;
+  {
+    std::lock_guard<std::recursive_mutex> g(c.mu);
+    if (c.live_datasets > 0)
+      return SetError(kInvalidArgument, "context still has datasets: destroy them first");
+  }
   (void)hipSetDevice(c.device);
   (void)hipStreamSynchronize(c.stream);
   DrainProfile(&c);
@@ -376,8 +382,11 @@ int vdbg_dataset_destroy(vdbg_dataset* ds) {
   if (ds == nullptr) return kOk;
   Ctx* c = ds->d.ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
+  if (ds->d.live_indexes > 0)
+    return SetError(kInvalidArgument, "dataset still has SQ8/IVF-PQ indexes: destroy them first");
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
+  --c->live_datasets;
   FreeSample(&ds->d.src);
   (void)hipFree(ds->d.rows);
   (void)hipFree(ds->d.norms);
@@ -503,6 +512,7 @@ int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdb
   x.src.pd = static_cast<int>(pd);
   x.src.metric = d.metric;
   x.src.rmag = float(ymax + xhat + vn);
+  ++d.live_indexes;
   *out = h;
   return kOk;
 }
@@ -513,6 +523,7 @@ int vdbg_sq8_destroy(vdbg_sq8* sq) {
   std::lock_guard<std::recursive_mutex> g(c->mu);
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
+  --sq->q.ds->live_indexes;
   FreeSample(&sq->q.src);
   (void)hipFree(sq->q.codes);
   (void)hipFree(sq->q.yn);

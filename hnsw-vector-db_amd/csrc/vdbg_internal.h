@@ -85,6 +85,7 @@ struct Ctx {
   uint64_t last_fallbacks = 0;
   int last_gemm_bits = 0;  // input width of the last scan's main GEMM: 32, 16 (exact), 0
   int cu_count = 256;
+  int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
@@ -105,6 +106,7 @@ struct ScanSource {
   float rmag = 0.f;             // row magnitude term of the rounding bound
   RowStats stats;               // flat: value statistics for the exactness test
   float* SX = nullptr;          // sample rows (kind 0)
+  uint16_t* SX16 = nullptr;     // sample rows as fp16 (kind 0 with X16)
   uint8_t* SC = nullptr;        // sample codes (kind 1)
   float* Srn = nullptr;
   uint32_t* Sid = nullptr;
@@ -120,6 +122,7 @@ struct Dataset {
   int metric = 0;
   RowStats stats;
   ScanSource src;          // the flat scan's view of these rows
+  int live_indexes = 0;    // SQ8 / IVF-PQ indexes over these rows not yet destroyed (ctx mu)
 };
 
 // SQ8 codes of a dataset's rows (HnswSq8Index's codes_ and Sq8Quantizer,

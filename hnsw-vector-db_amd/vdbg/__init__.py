@@ -6,6 +6,7 @@ loudly when the library is missing: there is no CPU fallback.
 """
 import ctypes as C
 import os
+import weakref
 
 import numpy as np
 
@@ -135,10 +136,13 @@ class Context:
         h = _vp()
         _check(lib.vdbg_ctx_create(device, C.byref(h)))
         self.h = h
+        self._children = weakref.WeakSet()  # live datasets: closed before the context
 
     def close(self):
         if self.h:
-            lib.vdbg_ctx_destroy(self.h)
+            for ch in list(self._children):
+                ch.close()
+            _check(lib.vdbg_ctx_destroy(self.h))
             self.h = None
 
     def __del__(self):
@@ -195,6 +199,8 @@ class Dataset:
                                        C.byref(h)))
         self.ctx, self.h, self.n, self.dim, self.pd = ctx, h, n, dim, pd
         self.metric = metric
+        self._children = weakref.WeakSet()  # live SQ8 / IVF-PQ indexes
+        ctx._children.add(self)
 
     @classmethod
     def from_device(cls, ctx, rows_ptr, n, dim, pd, metric="l2"):
@@ -204,11 +210,15 @@ class Dataset:
                                               C.byref(h)))
         self.ctx, self.h, self.n, self.dim, self.pd = ctx, h, n, dim, pd
         self.metric = metric
+        self._children = weakref.WeakSet()
+        ctx._children.add(self)
         return self
 
     def close(self):
         if self.h:
-            lib.vdbg_dataset_destroy(self.h)
+            for ch in list(self._children):
+                ch.close()
+            _check(lib.vdbg_dataset_destroy(self.h))
             self.h = None
 
     def __del__(self):
@@ -263,6 +273,7 @@ class Sq8Index:
         h = _vp()
         _check(lib.vdbg_sq8_create(ds.h, _ptr(self.vmin), _ptr(self.scale), C.byref(h)))
         self.ds, self.h = ds, h
+        ds._children.add(self)
 
     def close(self):
         if self.h:
@@ -313,6 +324,7 @@ class IvfPqIndex:
 
     def __init__(self, ds, h):
         self.ds, self.h = ds, h
+        ds._children.add(self)
 
     @classmethod
     def load(cls, ds, blob):

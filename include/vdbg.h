@@ -69,6 +69,8 @@ const char* vdbg_last_error(void);
 /* A device, its stream and reusable device workspace.  Replaces nothing in the reference
  * (vdb's CPU indexes need no device state); owned by the GPU Index adapters. */
 int vdbg_ctx_create(int device, vdbg_ctx** out);
+/* Fails (VDBG_INVALID_ARGUMENT, nothing released) while datasets of the context remain:
+ * destroy indexes, then datasets, then the context. */
 int vdbg_ctx_destroy(vdbg_ctx* ctx);
 /* The context's HIP stream (a hipStream_t), for callers that order their own work with it. */
 void* vdbg_ctx_stream(vdbg_ctx* ctx);
@@ -102,6 +104,8 @@ int vdbg_dataset_create(vdbg_ctx* ctx, const float* rows, size_t n, size_t dim,
  * completed when the call returns. */
 int vdbg_dataset_create_device(vdbg_ctx* ctx, const float* rows_dev, size_t n, size_t dim,
                                size_t padded_dim, int metric, vdbg_dataset** out);
+/* Fails (VDBG_INVALID_ARGUMENT, nothing released) while SQ8 or IVF-PQ indexes over the
+ * dataset remain. */
 int vdbg_dataset_destroy(vdbg_dataset* ds);
 /* Device pointer to the resident rows (n x padded_dim floats). */
 const float* vdbg_dataset_rows(vdbg_dataset* ds);
