@@ -21,6 +21,8 @@ struct GemmArgs {
   const float* Qb;
   const float* T;
   const uint64_t* allow;
+  const uint32_t* aw;  // k_gemm16 MODE 0: the filter as 32-bit words, or one all-ones word
+  uint32_t aw_mask;    // ~0 with a filter, 0 without (every row then reads aw[0])
   uint2* cand;         // MODE 0: [(q * nchunks + chunk) * 2 + half][caph]
   uint32_t* counts;    // MODE 0: [(q * nchunks + chunk) * 2 + half]
   int* ovf;            // MODE 0: [q]

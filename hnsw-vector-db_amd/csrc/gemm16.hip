@@ -36,7 +36,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (
 //
 // MODE 0: every value at or below the query's threshold T goes to the lane's candidate
 // buffer (per query, chunk and lane half).  The test is one compare per value; only a value
-// that passes on some lane of the wave (a wave-uniform branch) pays for the write.
+// that passes on some lane of the wave (a wave-uniform branch) pays for the write.  Rows the
+// filter excludes start their accumulators from NaN, which fails every compare.
 // MODE 1: minimum value of each 16-row group (the rows one lane holds of a 32-row block).
 template <int PD, int METRIC, int QB, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
@@ -50,7 +51,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int QT = 128 * QB;                     // queries per block
   static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmRows * STR];
-  __shared__ __attribute__((aligned(16))) float xns[3][kGemmRows];
+  __shared__ __attribute__((aligned(16))) float xns[2][kGemmRows];
 
   const int b = blockIdx.x;
   const int item = (b & 7) * a.per_xcd + (b >> 3);
@@ -108,91 +109,98 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     vrow[i] = f / VEC_PER_ROW;
     voff[i] = vrow[i] * PD + (f % VEC_PER_ROW) * 8;
   }
-  u32x4 pre[VEC_PER_THREAD];
-  float pre_n = 0.f;
-  // stage (base, kc): rows base..base+63, dims kc*KC..kc*KC+KC-1.  Rows past r_end repeat the
-  // last valid row and get a NaN accumulator start, so no compare passes them and no group
-  // minimum takes them.
-  auto load_stage = [&](uint32_t base, int kc) {
+  // The chunk's rows run as stages s = tile * NKC + kc (64 rows x KC dims each), staged
+  // through registers into two LDS buffers.  Stage s + 2 is loaded while stage s is
+  // multiplied, so each load has two stages of MFMA work to land:
+  //   step s:  load stage s + 2 -> set Y;  MFMA on LDS buffer s % 2;
+  //            store set X (stage s + 1, loaded during step s - 1) -> buffer (s + 1) % 2;
+  //            barrier;  after a tile's last K chunk, its threshold test.
+  // The sets swap roles each step (the loop body is unrolled twice).  Rows past r_end repeat
+  // the last valid row and get a NaN accumulator start, so no compare passes them and no
+  // group minimum takes them.  Norm slots alternate per tile.
+  struct Stage {
+    u32x4 v[VEC_PER_THREAD];
+    float n;
+    uint32_t aw;  // filter bits of the lane's half of the tile (tiles start on multiples of 64)
+  };
+  const int ntiles = int((r_end - r_begin + kGemmRows - 1) / kGemmRows);
+  const int nstages = ntiles * NKC;
+  auto load_stage = [&](Stage& st, int sidx) {
+    sidx = min(sidx, nstages - 1);  // past the end: a harmless repeat, so the count is fixed
+    const int tile = sidx / NKC, kc = sidx - tile * NKC;
+    const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
     const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
-    const uint16_t* tile = a.X16 + size_t(base) * PD + kc * KC;
+    const uint16_t* src = a.X16 + size_t(base) * PD + kc * KC;
     const int over = int(valid) - 1;  // rows past it read row `over`
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int o = voff[i] - max(0, vrow[i] - over) * PD;
-      pre[i] = *reinterpret_cast<const u32x4*>(tile + o);
+      st.v[i] = *reinterpret_cast<const u32x4*>(src + o);
     }
-    if (kc == 0) {
-      const float n = a.rn[base + min(uint32_t(tid & 63), valid - 1)];
-      pre_n = uint32_t(tid & 63) < valid ? (METRIC == 0 ? n : 0.f) : __builtin_nanf("");
-    }
+    st.n = a.rn[base + min(uint32_t(tid & 63), valid - 1)];  // (the store applies validity)
+    if constexpr (MODE == 0)  // a scan without a filter reads one all-ones word (mask 0)
+      st.aw = a.aw[((base >> 5) + (uint32_t(tid & 63) >> 5)) & a.aw_mask];
   };
-  auto store_stage = [&](int buf, int kc, int nslot) {
+  auto store_stage = [&](const Stage& st, int sidx) {
+    const int tile = sidx / NKC, kc = sidx - tile * NKC;
+    const int buf = sidx & 1;
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
       if (VEC_PER_TILE % 256 == 0 || f < VEC_PER_TILE)
-        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) = pre[i];
+        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) = st.v[i];
     }
-    if (kc == 0 && tid < kGemmRows) xns[nslot][tid] = pre_n;
+    if (kc == 0 && tid < kGemmRows) {
+      const uint32_t valid = min(uint32_t(kGemmRows), r_end - (r_begin + uint32_t(tile) * kGemmRows));
+      // rows past r_end, and in MODE 0 rows the filter excludes, start from NaN
+      const bool ok = uint32_t(tid) < valid && (MODE != 0 || ((st.aw >> (tid & 31)) & 1u));
+      xns[tile & 1][tid] = ok ? (METRIC == 0 ? st.n : 0.f) : __builtin_nanf("");
+    }
   };
 
-  if (r_begin >= r_end) return;  // (every planned chunk holds rows)
-  load_stage(r_begin, 0);
-  store_stage(0, 0, 0);
-  __syncthreads();
-
-  int buf = 0;
-  int slot = 0;  // norm slot of the current tile
-  for (uint32_t base = r_begin; base < r_end; base += kGemmRows) {
-    // accumulators start from the row norms (L2) or zero (inner product), NaN past r_end
-    v16f init[2];
+  v16f acc[QB][2];
+  auto step = [&](Stage& X, Stage& Y, int sidx) {
+    const int tile = sidx / NKC, kc = sidx - tile * NKC;
+    const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
+    if (NKC > 1) load_q(kc);  // before Y's loads: the MFMAs then wait for these alone
+    load_stage(Y, sidx + 2);
+    // keep the scheduler from sinking Y's loads below the MFMAs (which would shorten the
+    // time they have to land to a single step)
+    __builtin_amdgcn_sched_barrier(0);
+    if (kc == 0) {
+      // accumulators start from the row norms (L2) or zero (inner product), NaN past r_end
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
+      for (int blk = 0; blk < 2; ++blk) {
+        v16f init;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const float4 n4 = *reinterpret_cast<const float4*>(&xns[slot][blk * 32 + 8 * g + 4 * h]);
-        init[blk][4 * g + 0] = n4.x;
-        init[blk][4 * g + 1] = n4.y;
-        init[blk][4 * g + 2] = n4.z;
-        init[blk][4 * g + 3] = n4.w;
-      }
-    }
-    v16f acc[QB][2];
-#pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
-      acc[qb][0] = init[0];
-      acc[qb][1] = init[1];
-    }
-#pragma unroll 1
-    for (int kc = 0; kc < NKC; ++kc) {
-      // prefetch the next stage: the next K chunk of this tile, or chunk 0 of the next tile
-      const bool last_kc = kc + 1 == NKC;
-      const uint32_t nbase = last_kc ? base + kGemmRows : base;
-      const int nkc = last_kc ? 0 : kc + 1;
-      const bool have_next = nbase < r_end;
-      if (have_next) load_stage(nbase, nkc);
-      if (NKC > 1) load_q(kc);
-
-      // waves past the batch run the MFMAs too (on query nq - 1): no branch splits the
-      // accumulator chains; their values are never emitted
-      const uint16_t* xa0 = &xs[buf][j * STR + h * 8];
-      const uint16_t* xa1 = xa0 + 32 * STR;
-#pragma unroll
-      for (int kb = 0; kb < NKB; ++kb) {
-        const half8 x0 = *reinterpret_cast<const half8*>(xa0 + kb * 16);
-        const half8 x1 = *reinterpret_cast<const half8*>(xa1 + kb * 16);
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[qb][kb], acc[qb][0], 0, 0, 0);
-          acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[qb][kb], acc[qb][1], 0, 0, 0);
+        for (int g = 0; g < 4; ++g) {
+          const float4 n4 = *reinterpret_cast<const float4*>(&xns[tile & 1][blk * 32 + 8 * g + 4 * h]);
+          init[4 * g + 0] = n4.x;
+          init[4 * g + 1] = n4.y;
+          init[4 * g + 2] = n4.z;
+          init[4 * g + 3] = n4.w;
         }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) acc[qb][blk] = init;
       }
-
-      if (have_next) store_stage(buf ^ 1, nkc, last_kc ? (slot == 2 ? 0 : slot + 1) : slot);
-      __syncthreads();
-      buf ^= 1;
     }
+    // waves past the batch run the MFMAs too (on query nq - 1): no branch splits the
+    // accumulator chains; their values are never emitted
+    const uint16_t* xa0 = &xs[sidx & 1][j * STR + h * 8];
+    const uint16_t* xa1 = xa0 + 32 * STR;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const half8 x0 = *reinterpret_cast<const half8*>(xa0 + kb * 16);
+      const half8 x1 = *reinterpret_cast<const half8*>(xa1 + kb * 16);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[qb][kb], acc[qb][0], 0, 0, 0);
+        acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[qb][kb], acc[qb][1], 0, 0, 0);
+      }
+    }
+    if (sidx + 1 < nstages) store_stage(X, sidx + 1);
+    __syncthreads();
+    if (kc != NKC - 1) return;
 
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
     if (wave_live && MODE == 0) {
@@ -206,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
             const float v = acc[qb][blk][r];
             if (__builtin_amdgcn_ballot_w64(v <= T[qb]) != 0) {
               const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
-              if (v <= T[qb] && row_allowed(a.allow, row)) {
+              if (v <= T[qb]) {
                 if (cnt[qb] < uint32_t(a.caph))
                   out[qb][cnt[qb]] = make_uint2(__float_as_uint(v), row);
                 ++cnt[qb];
@@ -236,7 +244,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
           }
         }
     }
-    slot = slot == 2 ? 0 : slot + 1;
+  };
+
+  if (r_begin >= r_end) return;  // (every planned chunk holds rows)
+  Stage A, B;
+  load_stage(B, 0);
+  load_stage(A, 1);
+  store_stage(B, 0);
+  __syncthreads();
+  for (int sidx = 0; sidx < nstages; sidx += 2) {
+    step(A, B, sidx);
+    if (sidx + 1 < nstages) step(B, A, sidx + 1);
   }
 
   if constexpr (MODE == 0) {

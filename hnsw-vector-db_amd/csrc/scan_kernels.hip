@@ -1297,7 +1297,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
                       size_t(nq) * ngroups * sizeof(float) + cand_need +
-                      (try16 ? nq * pd * sizeof(uint16_t) : 0) + 18 * 256;
+                      (try16 ? nq * pd * sizeof(uint16_t) : 0) + 19 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
@@ -1312,9 +1312,11 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   char* cand_base = w.take<char>(cand_need);
   uint16_t* Q16 = try16 ? w.take<uint16_t>(nq * pd) : nullptr;
   int* all16 = try16 ? w.take<int>(1) : nullptr;
+  uint32_t* ones = try16 ? w.take<uint32_t>(1) : nullptr;  // the fp16 GEMM's no-filter word
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
   VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
   if (try16) VDBG_HIP(hipMemsetD32Async(all16, 1, 1, s));
+  if (try16) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16};
@@ -1398,6 +1400,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     if (use16) {
       ga.X16 = src->X16;
       ga.Q16 = Q16;
+      ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
+      ga.aw_mask = allow != nullptr ? ~0u : 0u;
       VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, s, blocks, ga));
     } else {
       VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
