@@ -43,7 +43,7 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-PROFILES = {"flat": "flat_gemm_sift_like_1m_x128_k10_b10000.md",
+PROFILES = {"flat": "flat_gemm16_sift_like_1m_x128_k10_b10000.md",
             "sq8": "sq8_gemm_sift_like_1m_x128_d100_b10000.md",
             "ivfpq": "ivf_scan_sift_like_1m_nlist4096_m16_nprobe64.md"}
 
@@ -281,6 +281,20 @@ def main():
              "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
              "exact_rescans": fb}
         log(f"flat: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} TFLOP/s")
+        if bits == 16:
+            # the same workload ranked on the fp32 GEMM (identical results), against the fp32
+            # MFMA peak
+            ctx.set_exact_fp16(False)
+            el32, prof32, _ = timed(ctx, torch, step, args.steps, 1, ["flat_gemm"])
+            ctx.set_exact_fp16(True)
+            g32 = prof32["flat_gemm"][0] / max(1, prof32["flat_gemm"][1])
+            t32 = 2.0 * nq * N * dim / (g32 * 1e-3) / 1e12
+            r["fp32_gemm"] = {"qps": round(nq * args.steps / el32, 1), "kernel": "k_gemm<128,L2,rows,filter>",
+                              "kernel_ms": round(g32, 4), "achieved_TFLOPs": round(t32, 2),
+                              "peak_TFLOPs": FP32_MFMA_PEAK_TFLOPS,
+                              "frac": round(t32 / FP32_MFMA_PEAK_TFLOPS, 4)}
+            log(f"flat (fp32 GEMM): {nq * args.steps / el32:.0f} q/s, GEMM {g32:.2f} ms = "
+                f"{t32:.1f} TFLOP/s")
         if not args.no_cpu:
             s = min(args.cpu_sample, nq)
             qs = np.ascontiguousarray(queries[:s])

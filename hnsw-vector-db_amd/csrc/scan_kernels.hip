@@ -1282,7 +1282,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     return p;
   };
   // integer-valued rows with an fp16 copy: the batch may take the exact-integer GEMM
-  const bool try16 = src->kind == 0 && src->X16 != nullptr;
+  const bool try16 = c->exact_fp16 && src->kind == 0 && src->X16 != nullptr;
   const Plan p32 = make_plan(1);
   const Plan p16 = make_plan(nq > 128 ? 2 : 1);
   auto cand_bytes = [&](const Plan& p) {

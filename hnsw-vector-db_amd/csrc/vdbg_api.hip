@@ -312,6 +312,13 @@ const char* vdbg_ctx_kernels(vdbg_ctx* ctx) {
   return ctx == nullptr ? "" : kKsetNames[ctx->c.kset];
 }
 
+int vdbg_ctx_set_exact_fp16(vdbg_ctx* ctx, int enable) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.exact_fp16 = enable != 0;
+  return kOk;
+}
+
 int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   if (ctx == nullptr) return kOk;
   Ctx& c = ctx->c;

@@ -87,6 +87,7 @@ struct Ctx {
   int cu_count = 256;
   int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
+  bool exact_fp16 = true;      // integer-valued flat scans may rank on the fp16 GEMM
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 

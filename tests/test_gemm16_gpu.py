@@ -106,6 +106,22 @@ def test_integer_filtered(ctx, oracle, frac):
     _check_equal(gi, gd, oi, od)
 
 
+def test_fp32_switch_gives_identical_results(ctx):
+    base = datagen.sift_like(40000, 128, 5801)
+    qs = datagen.sift_like(300, 128, 5802)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi16, gd16 = ds.flat_search(qs, 50)
+    assert ctx.last_gemm_bits() == 16
+    ctx.set_exact_fp16(False)
+    try:
+        gi32, gd32 = ds.flat_search(qs, 50)
+        assert ctx.last_gemm_bits() == 32
+    finally:
+        ctx.set_exact_fp16(True)
+    assert np.array_equal(gi16, gi32)
+    assert np.array_equal(gd16.view(np.uint32), gd32.view(np.uint32))
+
+
 def test_owner_closes_before_children(oracle):
     # closing a context first closes its datasets and their indexes; the library refuses to
     # destroy a context or dataset that still has children
