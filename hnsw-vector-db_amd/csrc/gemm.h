@@ -14,7 +14,9 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 struct GemmArgs {
   const float* X;      // fp32 rows (KIND 0)
   const uint16_t* X16; // fp16 rows (k_gemm16)
-  const uint16_t* Q16; // fp16 B operand: -2 q (L2) or -q (inner product) (k_gemm16)
+  const uint16_t* Q16; // fp16 B operand: -2 q (L2) or -q (inner product) (k_gemm16), or for
+                       // SQ8 the scaled query operand as two fp16 parts [q][2][pd]
+  const float* Qf;     // SQ8 split: per-query factor from split-GEMM to GEMM units
   const uint8_t* C;    // code rows (KIND 1)
   const float* rn;     // row norms of the GEMM form
   const uint32_t* rid; // MODE 1: original row id of each sample row
@@ -55,9 +57,10 @@ inline bool GemmSupported(size_t pd) {
   }
 }
 
-// Exact-integer fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 =
-// threshold pass into candidate buffers, 1 = group minima of the sample.
-int LaunchGemm16(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+// fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 = threshold pass
+// into candidate buffers, 1 = group minima of the sample; split = SQ8 codes against the
+// two-part query operand (qb 2, both register sets on the same 32 queries).
+int LaunchGemm16(size_t pd, int metric, int qb, int mode, bool split, hipStream_t s, int blocks,
                  const GemmArgs& a);
 
 }  // namespace vdbg

@@ -39,7 +39,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (
 // that passes on some lane of the wave (a wave-uniform branch) pays for the write.  Rows the
 // filter excludes start their accumulators from NaN, which fails every compare.
 // MODE 1: minimum value of each 16-row group (the rows one lane holds of a 32-row block).
-template <int PD, int METRIC, int QB, int MODE>
+//
+// SPLIT (SQ8): rows are uint8 codes held as fp16 (exact), and the query operand B (fp32) is
+// scaled by 2^sc and split into fp16 parts h + l (k_query_prep).  Both register sets hold the
+// same 32 queries, one per part; every product is exact in fp32, the accumulators start from
+// zero, and the epilogue forms fma(Qf, acc_h + acc_l, ||c scale||^2) (NaN for excluded rows)
+// with Qf = -2 (L2) or -1 (IP) times 2^-sc: the GEMM value of the fp32 SQ8 GEMM up to the
+// rounding bound k_query_prep accounts for.
+template <int PD, int METRIC, int QB, int MODE, int SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int KC = GemmKc(PD);
   constexpr int NKC = PD / KC;
@@ -48,10 +55,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int VEC_PER_ROW = KC / 8;              // uint4 = 8 halfs
   constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
-  constexpr int QT = 128 * QB;                     // queries per block
+  constexpr int NQB = SPLIT ? 1 : QB;              // distinct 32-query blocks per wave
+  constexpr int QT = 128 * NQB;                    // queries per block
   static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
+  static_assert(!SPLIT || QB == 2, "the split operand takes both register sets");
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmRows * STR];
-  __shared__ __attribute__((aligned(16))) float xns[2][kGemmRows];
+  __shared__ __attribute__((aligned(16))) float xns[3][kGemmRows];
 
   const int b = blockIdx.x;
   const int item = (b & 7) * a.per_xcd + (b >> 3);
@@ -63,17 +72,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   const int lane = tid & 63;
   const int j = lane & 31;
   const int h = lane >> 5;
-  const int q0 = qt * QT + wave * 32 * QB;  // first query of the wave
+  const int q0 = qt * QT + wave * 32 * NQB;  // first query of the wave
   const bool wave_live = q0 < a.nq;
   const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
   const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
 
-  int q[QB];
-  float T[QB];
-  uint2* out[QB];
-  uint32_t cnt[QB];
+  int q[NQB];
+  float T[NQB];
+  uint2* out[NQB];
+  uint32_t cnt[NQB];
+  const float F = SPLIT ? a.Qf[min(q0 + j, a.nq - 1)] : 1.f;
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
+  for (int qb = 0; qb < NQB; ++qb) {
     q[qb] = q0 + qb * 32 + j;
     cnt[qb] = 0;
     if constexpr (MODE == 0) {
@@ -89,7 +99,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   half8 qv[QB][NKB];
   const uint16_t* qrow[QB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) qrow[qb] = a.Q16 + size_t(min(q[qb], a.nq - 1)) * PD + h * 8;
+  for (int qb = 0; qb < QB; ++qb)
+    qrow[qb] = SPLIT ? a.Q16 + (size_t(min(q[0], a.nq - 1)) * 2 + qb) * PD + h * 8
+                     : a.Q16 + size_t(min(q[qb], a.nq - 1)) * PD + h * 8;
   auto load_q = [&](int kc) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
@@ -116,8 +128,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   //            store set X (stage s + 1, loaded during step s - 1) -> buffer (s + 1) % 2;
   //            barrier;  after a tile's last K chunk, its threshold test.
   // The sets swap roles each step (the loop body is unrolled twice).  Rows past r_end repeat
-  // the last valid row and get a NaN accumulator start, so no compare passes them and no
-  // group minimum takes them.  Norm slots alternate per tile.
+  // the last valid row and get a NaN accumulator start (SPLIT: a NaN norm), so no compare
+  // passes them and no group minimum takes them.  Norms rotate through three slots per tile.
   struct Stage {
     u32x4 v[VEC_PER_THREAD];
     float n;
@@ -154,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
       const uint32_t valid = min(uint32_t(kGemmRows), r_end - (r_begin + uint32_t(tile) * kGemmRows));
       // rows past r_end, and in MODE 0 rows the filter excludes, start from NaN
       const bool ok = uint32_t(tid) < valid && (MODE != 0 || ((st.aw >> (tid & 31)) & 1u));
-      xns[tile & 1][tid] = ok ? (METRIC == 0 ? st.n : 0.f) : __builtin_nanf("");
+      xns[tile % 3][tid] = ok ? (METRIC == 0 ? st.n : 0.f) : __builtin_nanf("");
     }
   };
 
@@ -168,17 +180,21 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     // time they have to land to a single step)
     __builtin_amdgcn_sched_barrier(0);
     if (kc == 0) {
-      // accumulators start from the row norms (L2) or zero (inner product), NaN past r_end
+      // accumulators start from the row norms (L2) or zero (inner product), NaN past r_end;
+      // SPLIT: from zero (the epilogue adds the norms)
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk) {
-        v16f init;
+        v16f init = {};
+        if constexpr (!SPLIT) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 n4 = *reinterpret_cast<const float4*>(&xns[tile & 1][blk * 32 + 8 * g + 4 * h]);
-          init[4 * g + 0] = n4.x;
-          init[4 * g + 1] = n4.y;
-          init[4 * g + 2] = n4.z;
-          init[4 * g + 3] = n4.w;
+          for (int g = 0; g < 4; ++g) {
+            const float4 n4 =
+                *reinterpret_cast<const float4*>(&xns[tile % 3][blk * 32 + 8 * g + 4 * h]);
+            init[4 * g + 0] = n4.x;
+            init[4 * g + 1] = n4.y;
+            init[4 * g + 2] = n4.z;
+            init[4 * g + 3] = n4.w;
+          }
         }
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) acc[qb][blk] = init;
@@ -202,16 +218,36 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     __syncthreads();
     if (kc != NKC - 1) return;
 
+    // the value of output r of block blk for query block qb (in GEMM units)
+    float xn[SPLIT ? 2 : 1][SPLIT ? 16 : 1];
+    if constexpr (SPLIT) {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 n4 = *reinterpret_cast<const float4*>(&xns[tile % 3][blk * 32 + 8 * g + 4 * h]);
+          xn[blk][4 * g + 0] = n4.x;
+          xn[blk][4 * g + 1] = n4.y;
+          xn[blk][4 * g + 2] = n4.z;
+          xn[blk][4 * g + 3] = n4.w;
+        }
+    }
+    auto value = [&](int qb, int blk, int r) {
+      if constexpr (SPLIT)
+        return fmaf(F, acc[0][blk][r] + acc[1][blk][r], xn[blk][r]);
+      else
+        return acc[qb][blk][r];
+    };
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
     if (wave_live && MODE == 0) {
       // one compare per value; a value passing on some lane of the wave branches to the write
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
+      for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            const float v = acc[qb][blk][r];
+            const float v = value(qb, blk, r);
             if (__builtin_amdgcn_ballot_w64(v <= T[qb]) != 0) {
               const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
               if (v <= T[qb]) {
@@ -224,18 +260,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     } else if (wave_live) {
       // fminf skips the NaN values of rows past r_end
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
+      for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
           float m = __builtin_inff();
           if (a.allow == nullptr) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) m = fminf(m, acc[qb][blk][r]);
+            for (int r = 0; r < 16; ++r) m = fminf(m, value(qb, blk, r));
           } else {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
-              if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, acc[qb][blk][r]);
+              if (row < r_end && row_allowed(a.allow, a.rid[row])) m = fminf(m, value(qb, blk, r));
             }
           }
           if (q[qb] < a.nq) {
@@ -259,7 +295,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
 
   if constexpr (MODE == 0) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int qb = 0; qb < NQB; ++qb) {
       if (q[qb] < a.nq) {
         const size_t seg = (size_t(q[qb]) * a.nchunks + chunk) * 2 + h;
         a.counts[seg] = min(cnt[qb], uint32_t(a.caph));
@@ -269,47 +305,42 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   }
 }
 
-template <int PD>
-static void launch16_pd(int metric, int qb, int mode, hipStream_t s, int blocks,
+template <int PD, int METRIC>
+static void launch16_pm(int qb, int mode, bool split, hipStream_t s, int blocks,
                         const GemmArgs& a) {
   const dim3 g(blocks), t(256);
-  if (metric == 0) {
-    if (mode == 0) {
-      if (qb == 1) k_gemm16<PD, 0, 1, 0><<<g, t, 0, s>>>(a);
-      else k_gemm16<PD, 0, 2, 0><<<g, t, 0, s>>>(a);
-    } else {
-      k_gemm16<PD, 0, 2, 1><<<g, t, 0, s>>>(a);
-    }
+  if (split) {
+    if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 1><<<g, t, 0, s>>>(a);
+    else k_gemm16<PD, METRIC, 2, 1, 1><<<g, t, 0, s>>>(a);
+  } else if (mode == 0) {
+    if (qb == 1) k_gemm16<PD, METRIC, 1, 0, 0><<<g, t, 0, s>>>(a);
+    else k_gemm16<PD, METRIC, 2, 0, 0><<<g, t, 0, s>>>(a);
   } else {
-    if (mode == 0) {
-      if (qb == 1) k_gemm16<PD, 1, 1, 0><<<g, t, 0, s>>>(a);
-      else k_gemm16<PD, 1, 2, 0><<<g, t, 0, s>>>(a);
-    } else {
-      k_gemm16<PD, 1, 2, 1><<<g, t, 0, s>>>(a);
-    }
+    k_gemm16<PD, METRIC, 2, 1, 0><<<g, t, 0, s>>>(a);
   }
 }
 
-int LaunchGemm16(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+template <int PD>
+static void launch16_pd(int metric, int qb, int mode, bool split, hipStream_t s, int blocks,
+                        const GemmArgs& a) {
+  if (metric == 0)
+    launch16_pm<PD, 0>(qb, mode, split, s, blocks, a);
+  else
+    launch16_pm<PD, 1>(qb, mode, split, s, blocks, a);
+}
+
+int LaunchGemm16(size_t pd, int metric, int qb, int mode, bool split, hipStream_t s, int blocks,
                  const GemmArgs& a) {
   if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM16: query blocks per wave");
-  if (mode == 1 && qb != 2) return SetError(kInternal, "GEMM16: the sample pass runs 2 query blocks");
+  if ((mode == 1 || split) && qb != 2)
+    return SetError(kInternal, "GEMM16: the sample pass and the split operand run 2 blocks");
   switch (pd) {
-    case 16: launch16_pd<16>(metric, qb, mode, s, blocks, a); break;
-    case 32: launch16_pd<32>(metric, qb, mode, s, blocks, a); break;
-    case 48: launch16_pd<48>(metric, qb, mode, s, blocks, a); break;
-    case 64: launch16_pd<64>(metric, qb, mode, s, blocks, a); break;
-    case 80: launch16_pd<80>(metric, qb, mode, s, blocks, a); break;
-    case 96: launch16_pd<96>(metric, qb, mode, s, blocks, a); break;
-    case 112: launch16_pd<112>(metric, qb, mode, s, blocks, a); break;
-    case 128: launch16_pd<128>(metric, qb, mode, s, blocks, a); break;
-    case 192: launch16_pd<192>(metric, qb, mode, s, blocks, a); break;
-    case 256: launch16_pd<256>(metric, qb, mode, s, blocks, a); break;
-    case 384: launch16_pd<384>(metric, qb, mode, s, blocks, a); break;
-    case 512: launch16_pd<512>(metric, qb, mode, s, blocks, a); break;
-    case 768: launch16_pd<768>(metric, qb, mode, s, blocks, a); break;
-    case 960: launch16_pd<960>(metric, qb, mode, s, blocks, a); break;
-    case 1024: launch16_pd<1024>(metric, qb, mode, s, blocks, a); break;
+#define VDBG_PD16(P) \
+  case P: launch16_pd<P>(metric, qb, mode, split, s, blocks, a); break;
+    VDBG_PD16(16) VDBG_PD16(32) VDBG_PD16(48) VDBG_PD16(64) VDBG_PD16(80) VDBG_PD16(96)
+    VDBG_PD16(112) VDBG_PD16(128) VDBG_PD16(192) VDBG_PD16(256) VDBG_PD16(384) VDBG_PD16(512)
+    VDBG_PD16(768) VDBG_PD16(960) VDBG_PD16(1024)
+#undef VDBG_PD16
     default: return SetError(kNotSupported, "GEMM path: unsupported padded_dim");
   }
   return kOk;
@@ -331,6 +362,26 @@ int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, co
   if (e != hipSuccess) {
     (void)hipFree(y);
     return SetError(kInternal, std::string("fp16 rows: ") + hipGetErrorString(e));
+  }
+  *out = y;
+  return kOk;
+}
+
+__global__ void k_u8_to_f16(const uint8_t* __restrict__ x, size_t n, uint16_t* __restrict__ y) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(float(x[i])));
+}
+
+int MakeCodes16(Ctx* c, hipStream_t s, const uint8_t* codes, size_t n, size_t pd, uint16_t** out) {
+  *out = nullptr;
+  if (n == 0 || !GemmSupported(pd)) return kOk;
+  uint16_t* y = nullptr;
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * sizeof(uint16_t)));
+  k_u8_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(codes, n * pd, y);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    (void)hipFree(y);
+    return SetError(kInternal, std::string("fp16 codes: ") + hipGetErrorString(e));
   }
   *out = y;
   return kOk;

@@ -340,14 +340,14 @@ int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
   const size_t pd = src->pd;
   if (src->kind == 0)
     VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX), size_t(smax) * pd * sizeof(float)));
-  if (src->kind == 0 && src->X16 != nullptr)
+  if (src->X16 != nullptr)
     VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX16), size_t(smax) * pd * sizeof(uint16_t)));
   if (src->kind == 1)
     VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SC), size_t(smax) * pd));
   VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Srn), size_t(smax) * sizeof(float)));
   VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Sid), size_t(smax) * sizeof(uint32_t)));
   k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
-                                             src->kind == 0 ? src->X16 : nullptr,
+                                             src->X16,
                                              src->kind == 1 ? src->C : nullptr, src->rn,
                                              src->N, int(pd), bits, smax, src->SX, src->SX16,
                                              src->SC, src->Srn, src->Sid);
@@ -384,7 +384,8 @@ struct PrepArgs {
   float* eb;     // bound on |GEMM value + shift - exact distance|
   int* exact;    // the bound is zero
   uint16_t* Q16;  // nullable: the fp16 GEMM's B operand (gemm16.hip)
-  int* all16;     // nullable: cleared when a query is outside the fp16 GEMM's exact bounds
+  int* all16;     // nullable: cleared when a query is outside the fp16 GEMM's bounds
+  float* Qf;      // SQ8 with Q16: per-query factor taking the split GEMM back to GEMM units
 };
 
 // One wave per query.
@@ -411,7 +412,7 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     hi = fmaxf(hi, e);
     ma = fmaxf(ma, fabsf(e));
     ai &= (e == rintf(e)) ? 1 : 0;
-    if (a.Q16 != nullptr)  // the fp16 GEMM's B operand: -2 q (L2) or -q (inner product)
+    if (a.Q16 != nullptr && a.kind == 0)  // the fp16 GEMM's B operand: -2 q (L2) or -q (IP)
       a.Q16[size_t(q) * a.pd + i] =
           __builtin_bit_cast(uint16_t, _Float16(a.metric == 0 ? -2.f * e : -e));
     if (a.kind == 1) {
@@ -431,6 +432,30 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
   hi = wave_max(hi);
   ma = wave_max(ma);
   ai = wave_and(ai);
+  // SQ8 on the fp16 GEMM: B scaled by 2^sc (max |B| 2^sc in [2^14, 2^15)) and split into
+  // fp16 h + l, |B 2^sc - h - l| <= 2^-22 |B 2^sc| (+ subnormal terms); codes are exact in
+  // fp16, so the GEMM runs as c.h + c.l and Qf = -2 (L2) or -1 (IP) times 2^-sc takes it back
+  int sc = 0;
+  bool split_ok = true;
+  if (a.kind == 1 && a.Q16 != nullptr) {
+    float mb = 0.f;
+    for (int i = lane_id(); i < a.pd; i += kWave) mb = fmaxf(mb, fabsf(a.Qb[size_t(q) * a.pd + i]));
+    mb = wave_max(mb);
+    split_ok = mb <= 3.0e38f;  // finite
+    if (split_ok && mb > 0.f) {
+      int ex = 0;
+      (void)frexpf(mb, &ex);  // mb = f 2^ex, f in [0.5, 1)
+      sc = 15 - ex;
+    }
+    uint16_t* hq = a.Q16 + size_t(q) * 2 * a.pd;
+    for (int i = lane_id(); i < a.pd; i += kWave) {
+      const float bs = ldexpf(a.Qb[size_t(q) * a.pd + i], sc);
+      const _Float16 hh = _Float16(bs);
+      const _Float16 ll = _Float16(bs - float(hh));
+      hq[i] = __builtin_bit_cast(uint16_t, hh);
+      hq[a.pd + i] = __builtin_bit_cast(uint16_t, ll);
+    }
+  }
   if (lane_id() == 0) {
     const double pd = a.pd, lim = 16777216.0;
     bool ex = false;
@@ -452,7 +477,10 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     // magnitude <= 4096); the fp16 GEMM accumulates ||x||^2 - 2 q.x (or -q.x) from the row
     // norm, every partial sum bounded by (|q| + R)^2 with R the largest row norm.  Below 2^24
     // its values are the fp32 GEMM's bit for bit.
-    if (a.all16 != nullptr) {
+    if (a.all16 != nullptr && a.kind == 1) {
+      a.Qf[q] = ldexpf(a.metric == 0 ? -2.f : -1.f, -sc);
+      if (!split_ok) atomicAnd(a.all16, 0);
+    } else if (a.all16 != nullptr) {
       const double rq = sqrt(double(s)), rx = sqrt(double(a.xs.xn_max));
       const bool fits = ex && ma <= 2048.f && a.xs.max_abs <= 2048.f &&
                         (rq + rx) * (rq + rx) * 1.001 < lim;
@@ -468,7 +496,14 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
         (a.kind == 0 && a.metric != 0)
             ? (2.0 * pd + 16.0) * u * sqrt(double(qmag) * double(a.rmag))
             : (4.0 * pd + 16.0) * u * (double(qmag) + double(a.rmag));
-    a.eb[q] = ex ? 0.f : float(bound * 1.001);
+    // SQ8 on the split fp16 GEMM: the two fp32 accumulations, their sum, the split residual
+    // (2^-22 relative) and the fma add at most (2 pd + 12) u sum c|B| <= (pd + 6) u (|q|^2 +
+    // |x|^2); the bound below triples it, and adds 1020 pd 2^-14 2^-sc for fp16 values
+    // below the normal range (each of h, l off by at most 2^-14 2^-sc, times c <= 255 and 2)
+    const double bound16 = (6.0 * pd + 48.0) * u * (double(qmag) + double(a.rmag)) +
+                           1020.0 * pd * ldexp(1.0, -14 - sc);
+    const bool split = a.kind == 1 && a.Q16 != nullptr;
+    a.eb[q] = ex ? 0.f : float((split ? bound16 : bound) * 1.001);
   }
 }
 
@@ -1254,19 +1289,22 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int slots = 2 * c->cu_count;
   // Sample size: about kk * N / S rows pass the threshold per query, and every pass is a
   // scattered buffer write plus a select insertion, while the pre-pass costs S / N of the
-  // main GEMM; N / 64 keeps both near 1.5%.
+  // main GEMM.  S >= kk * N / 640 keeps the passes near 640 per query (N / 64 at k = 10)
+  // until the sample cap.
   uint32_t S = 1;
-  while (S < std::max<uint32_t>(16u * std::max<uint32_t>(128, 4 * uint32_t(kk)), N / 64)) S *= 2;
+  const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,
+                                              uint64_t(N) * kk / 640});
+  while (S < s_want && S < (1u << 30)) S *= 2;
   S = std::min(S, src->Smax);
   const int ngroups = int((S + 31) / 32) * 2;
   struct Plan {
     int qb, nqt, nchunks, caph, nseg, schunks;
     uint32_t chunk_rows, schunk_rows;
   };
-  auto make_plan = [&](int qb) {
+  auto make_plan = [&](int qb, int tile_queries) {
     Plan p{};
     p.qb = qb;
-    p.nqt = int((nq + 128 * qb - 1) / (128 * qb));
+    p.nqt = int((nq + tile_queries - 1) / tile_queries);
     p.nchunks = PlanChunks(p.nqt, N, slots, kMaxSeg / 2);
     p.chunk_rows = (N + p.nchunks - 1) / p.nchunks;
     p.chunk_rows = (p.chunk_rows + 63) / 64 * 64;
@@ -1281,10 +1319,13 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     p.nseg = 2 * p.nchunks;
     return p;
   };
-  // integer-valued rows with an fp16 copy: the batch may take the exact-integer GEMM
-  const bool try16 = c->exact_fp16 && src->kind == 0 && src->X16 != nullptr;
-  const Plan p32 = make_plan(1);
-  const Plan p16 = make_plan(nq > 128 ? 2 : 1);
+  // Rows with an fp16 copy may rank on the fp16 GEMM: integer-valued flat rows exactly
+  // (64 queries per wave, or 32 for batches of at most 128), SQ8 codes with the query operand
+  // split in two fp16 parts (both register sets hold the same 32 queries).
+  const bool try16 = c->exact_fp16 && src->X16 != nullptr;
+  const bool split = src->kind == 1;
+  const Plan p32 = make_plan(1, 128);
+  const Plan p16 = split ? make_plan(2, 128) : (nq > 128 ? make_plan(2, 256) : make_plan(1, 128));
   auto cand_bytes = [&](const Plan& p) {
     return size_t(nq) * p.nseg * (sizeof(uint32_t) + size_t(p.caph) * sizeof(uint2));
   };
@@ -1297,7 +1338,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
                       size_t(nq) * ngroups * sizeof(float) + cand_need +
-                      (try16 ? nq * pd * sizeof(uint16_t) : 0) + 19 * 256;
+                      (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
+                      20 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
@@ -1310,7 +1352,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   float* Qb = src->kind == 1 ? w.take<float>(nq * pd) : nullptr;
   float* gm = w.take<float>(size_t(nq) * ngroups);
   char* cand_base = w.take<char>(cand_need);
-  uint16_t* Q16 = try16 ? w.take<uint16_t>(nq * pd) : nullptr;
+  uint16_t* Q16 = try16 ? w.take<uint16_t>((split ? 2 : 1) * nq * pd) : nullptr;
+  float* Qf = try16 && split ? w.take<float>(nq) : nullptr;
   int* all16 = try16 ? w.take<int>(1) : nullptr;
   uint32_t* ones = try16 ? w.take<uint32_t>(1) : nullptr;  // the fp16 GEMM's no-filter word
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
@@ -1319,7 +1362,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   if (try16) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
-              src->vmin, src->scale, shift, eb, exact, Q16, all16};
+              src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
@@ -1361,8 +1404,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     if (use16 && P.qb == 2) {
       sg.X16 = src->SX16;
       sg.Q16 = Q16;
+      sg.Qf = Qf;
       GemmGrid(sg, P.nqt, P.schunks, &sblocks);
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, s, sblocks, sg));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, split, s, sblocks, sg));
     } else {
       // the fp32 sample pass runs 128-query tiles
       GemmGrid(sg, p32.nqt, p32.schunks, &sblocks);
@@ -1400,9 +1444,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     if (use16) {
       ga.X16 = src->X16;
       ga.Q16 = Q16;
+      ga.Qf = Qf;
       ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
       ga.aw_mask = allow != nullptr ? ~0u : 0u;
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, s, blocks, ga));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, split, s, blocks, ga));
     } else {
       VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
     }

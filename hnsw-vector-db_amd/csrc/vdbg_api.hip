@@ -476,6 +476,7 @@ int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdb
   x.vmin_h.assign(vmin, vmin + pd);
   x.scale_h.assign(scale, scale + pd);
   auto fail = [&](int rc) {
+    (void)hipFree(x.codes16);
     (void)hipFree(x.codes);
     (void)hipFree(x.yn);
     (void)hipFree(x.vmin);
@@ -519,6 +520,9 @@ int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdb
   x.src.pd = static_cast<int>(pd);
   x.src.metric = d.metric;
   x.src.rmag = float(ymax + xhat + vn);
+  rc = MakeCodes16(c, s, x.codes, n, pd, &x.codes16);
+  if (rc != kOk) return fail(rc);
+  x.src.X16 = x.codes16;
   ++d.live_indexes;
   *out = h;
   return kOk;
@@ -533,6 +537,7 @@ int vdbg_sq8_destroy(vdbg_sq8* sq) {
   --sq->q.ds->live_indexes;
   FreeSample(&sq->q.src);
   (void)hipFree(sq->q.codes);
+  (void)hipFree(sq->q.codes16);
   (void)hipFree(sq->q.yn);
   (void)hipFree(sq->q.vmin);
   delete sq;

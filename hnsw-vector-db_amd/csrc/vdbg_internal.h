@@ -131,6 +131,7 @@ struct Dataset {
 struct Sq8Index {
   Dataset* ds = nullptr;
   uint8_t* codes = nullptr;  // n x pd
+  uint16_t* codes16 = nullptr;  // n x pd, the codes as fp16 (ScanSource::X16 of the scan)
   float* yn = nullptr;       // ||code * scale||^2 per row
   float* vmin = nullptr;     // pd (device)
   float* scale = nullptr;
@@ -174,6 +175,8 @@ int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
                    float* norms, RowStats* out);
 // The fp16 copy of rows whose values are all integers of magnitude <= 2048 (each exactly
 // representable), used by the exact-integer GEMM; *out stays null when not applicable.
+// SQ8 codes as fp16 (exact) for the split fp16 GEMM; null when pd has no GEMM kernel.
+int MakeCodes16(Ctx* c, hipStream_t s, const uint8_t* codes, size_t n, size_t pd, uint16_t** out);
 int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
                const RowStats& st, uint16_t** out);
 

@@ -97,3 +97,58 @@ def test_sq8_deep(ctx, oracle, k, depth):
     gi, gd = sq.search(qs, k, depth)
     od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth)
     _eq(gi, gd, oi, od)
+
+
+def _wide_range_rows(n, dim, seed):
+    # per-dimension scales from 1e-3 to 1e3 and signs: the split fp16 query operand spans
+    # many binades (small parts fall below fp16's normal range)
+    rng = np.random.default_rng(seed)
+    scales = np.float32(10.0) ** rng.uniform(-3, 3, dim).astype(np.float32)
+    return (rng.normal(0, 1, (n, dim)).astype(np.float32) * scales).astype(np.float32)
+
+
+@pytest.mark.parametrize("data,metric,nq,k,depth", [
+    ("sift_like", "l2", 300, 10, 100), ("uniform", "l2", 200, 10, 0),
+    ("unit", "cosine", 150, 10, 64), ("unit", "ip", 150, 20, 0),
+    ("wide", "l2", 130, 10, 100), ("wide", "ip", 100, 10, 50)])
+def test_sq8_split_fp16_matches_fp32_and_oracle(ctx, oracle, data, metric, nq, k, depth):
+    # the SQ8 scan ranks on fp16 MFMA (codes exact, query operand split in two fp16 parts);
+    # results must equal the fp32 GEMM's and the oracle's bit for bit
+    print(f"sq8 split {data} {metric} nq={nq} k={k} depth={depth}", flush=True)
+    n = 40000
+    if data == "sift_like":
+        base, qs = datagen.sift_like(n, 128, 6101), datagen.sift_like(nq, 128, 6102)
+    elif data == "uniform":
+        base, qs = datagen.uniform_rows(n, 128, 6103), datagen.uniform_rows(nq, 128, 6104)
+    elif data == "unit":
+        base = datagen.clustered_unit(n, 128, 6105, 6106, 200, 0.5)
+        qs = datagen.clustered_unit(nq, 128, 6107, 6106, 200, 0.5)
+    else:
+        base, qs = _wide_range_rows(n, 128, 6108), _wide_range_rows(nq, 128, 6108 + 1)
+    ds = vdbg.Dataset(ctx, base, 128, metric=metric)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, k, depth)
+    assert ctx.last_gemm_bits() == 16
+    ctx.set_exact_fp16(False)
+    try:
+        gi32, gd32 = sq.search(qs, k, depth)
+        assert ctx.last_gemm_bits() == 32
+    finally:
+        ctx.set_exact_fp16(True)
+    _eq(gi, gd, gi32, gd32)
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth, metric=metric)
+    _eq(gi, gd, oi, od)
+
+
+def test_sq8_split_large_batch_filtered(ctx, oracle):
+    n, nq = 120000, 700
+    base, qs = datagen.sift_like(n, 128, 6201), datagen.sift_like(nq, 128, 6202)
+    rows = np.nonzero(np.random.default_rng(6203).random(n) < 0.6)[0]
+    allow = np.zeros((n + 63) // 64, np.uint64)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 128)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, 10, 100, allow=allow)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 100, allow=allow)
+    _eq(gi, gd, oi, od)
