@@ -284,9 +284,9 @@ def main():
         if bits == 16:
             # the same workload ranked on the fp32 GEMM (identical results), against the fp32
             # MFMA peak
-            ctx.set_exact_fp16(False)
+            ctx.set_fp16_gemm(False)
             el32, prof32, _ = timed(ctx, torch, step, args.steps, 1, ["flat_gemm"])
-            ctx.set_exact_fp16(True)
+            ctx.set_fp16_gemm(True)
             g32 = prof32["flat_gemm"][0] / max(1, prof32["flat_gemm"][1])
             t32 = 2.0 * nq * N * dim / (g32 * 1e-3) / 1e12
             r["fp32_gemm"] = {"qps": round(nq * args.steps / el32, 1), "kernel": "k_gemm<128,L2,rows,filter>",

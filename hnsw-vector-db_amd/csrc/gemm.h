@@ -46,6 +46,16 @@ __host__ __device__ constexpr int GemmKc(int pd) {
   return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : (pd % 32 == 0 ? 32 : 16)));
 }
 
+// K chunk of the fp16 GEMM.  Two-part float rows (split 2) stage [h | l] per chunk, so their
+// chunk is at most 64 dims (the largest multiple of 16 dividing pd), which keeps two staging
+// register sets and both query parts within the wave's registers.
+__host__ __device__ constexpr int Gemm16Kc(int pd, int split) {
+  if (split != 2) return GemmKc(pd);
+  for (int kc = 64; kc > 16; kc -= 16)
+    if (pd % kc == 0) return kc;
+  return 16;
+}
+
 // Padded dimensions with compiled GEMM kernels; others scan exactly.
 inline bool GemmSupported(size_t pd) {
   switch (pd) {
@@ -58,9 +68,10 @@ inline bool GemmSupported(size_t pd) {
 }
 
 // fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 = threshold pass
-// into candidate buffers, 1 = group minima of the sample; split = SQ8 codes against the
-// two-part query operand (qb 2, both register sets on the same 32 queries).
-int LaunchGemm16(size_t pd, int metric, int qb, int mode, bool split, hipStream_t s, int blocks,
+// into candidate buffers, 1 = group minima of the sample; split 1 = SQ8 codes against the
+// two-part query operand (qb 2, both register sets on the same 32 queries), 2 = two-part
+// float rows against the two-part query operand.
+int LaunchGemm16(size_t pd, int metric, int qb, int mode, int split, hipStream_t s, int blocks,
                  const GemmArgs& a);
 
 }  // namespace vdbg

@@ -46,13 +46,21 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (
 // zero, and the epilogue forms fma(Qf, acc_h + acc_l, ||c scale||^2) (NaN for excluded rows)
 // with Qf = -2 (L2) or -1 (IP) times 2^-sc: the GEMM value of the fp32 SQ8 GEMM up to the
 // rounding bound k_query_prep accounts for.
+//
+// SPLIT 2 (float rows): rows scaled by 2^sx and split into fp16 h + l as well, stored per K
+// chunk as [h | l]; per 16-dim block the wave runs x_h q_h into one accumulator and x_h q_l,
+// x_l q_h into the other (x_l q_l, of relative size 2^-22, is left out), then the same
+// epilogue.
 template <int PD, int METRIC, int QB, int MODE, int SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
-  constexpr int KC = GemmKc(PD);
+  constexpr int KC = Gemm16Kc(PD, SPLIT);
   constexpr int NKC = PD / KC;
   constexpr int NKB = KC / 16;                     // 16-dim MFMA K blocks per stage
-  constexpr int STR = KC + 8;                      // LDS row stride in halfs (16 B padding)
-  constexpr int VEC_PER_ROW = KC / 8;              // uint4 = 8 halfs
+  constexpr int XP = SPLIT == 2 ? 2 : 1;           // fp16 parts per row value
+  constexpr int ROWW = XP * PD;                    // fp16 row width in halfs
+  constexpr int SKC = XP * KC;                     // stage width in halfs
+  constexpr int STR = SKC + 8;                     // LDS row stride in halfs (16 B padding)
+  constexpr int VEC_PER_ROW = SKC / 8;             // uint4 = 8 halfs
   constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
   constexpr int NQB = SPLIT ? 1 : QB;              // distinct 32-query blocks per wave
@@ -119,7 +127,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   for (int i = 0; i < VEC_PER_THREAD; ++i) {
     const int f = min(tid + 256 * i, VEC_PER_TILE - 1);
     vrow[i] = f / VEC_PER_ROW;
-    voff[i] = vrow[i] * PD + (f % VEC_PER_ROW) * 8;
+    voff[i] = vrow[i] * ROWW + (f % VEC_PER_ROW) * 8;
   }
   // The chunk's rows run as stages s = tile * NKC + kc (64 rows x KC dims each), staged
   // through registers into two LDS buffers.  Stage s + 2 is loaded while stage s is
@@ -142,11 +150,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
     const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
     const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
-    const uint16_t* src = a.X16 + size_t(base) * PD + kc * KC;
+    const uint16_t* src = a.X16 + size_t(base) * ROWW + kc * SKC;
     const int over = int(valid) - 1;  // rows past it read row `over`
 #pragma unroll
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
-      const int o = voff[i] - max(0, vrow[i] - over) * PD;
+      const int o = voff[i] - max(0, vrow[i] - over) * ROWW;
       st.v[i] = *reinterpret_cast<const u32x4*>(src + o);
     }
     st.n = a.rn[base + min(uint32_t(tid & 63), valid - 1)];  // (the store applies validity)
@@ -160,7 +168,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
       if (VEC_PER_TILE % 256 == 0 || f < VEC_PER_TILE)
-        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) = st.v[i];
+        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * ROWW)]) = st.v[i];
     }
     if (kc == 0 && tid < kGemmRows) {
       const uint32_t valid = min(uint32_t(kGemmRows), r_end - (r_begin + uint32_t(tile) * kGemmRows));
@@ -212,6 +220,12 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
       for (int qb = 0; qb < QB; ++qb) {
         acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[qb][kb], acc[qb][0], 0, 0, 0);
         acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[qb][kb], acc[qb][1], 0, 0, 0);
+      }
+      if constexpr (SPLIT == 2) {  // x_l q_h into the cross-term accumulator
+        const half8 y0 = *reinterpret_cast<const half8*>(xa0 + KC + kb * 16);
+        const half8 y1 = *reinterpret_cast<const half8*>(xa1 + KC + kb * 16);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y0, qv[0][kb], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y1, qv[0][kb], acc[1][1], 0, 0, 0);
       }
     }
     if (sidx + 1 < nstages) store_stage(X, sidx + 1);
@@ -306,12 +320,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
 }
 
 template <int PD, int METRIC>
-static void launch16_pm(int qb, int mode, bool split, hipStream_t s, int blocks,
+static void launch16_pm(int qb, int mode, int split, hipStream_t s, int blocks,
                         const GemmArgs& a) {
   const dim3 g(blocks), t(256);
-  if (split) {
+  if (split == 1) {
     if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 1><<<g, t, 0, s>>>(a);
     else k_gemm16<PD, METRIC, 2, 1, 1><<<g, t, 0, s>>>(a);
+  } else if (split == 2) {
+    if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 2><<<g, t, 0, s>>>(a);
+    else k_gemm16<PD, METRIC, 2, 1, 2><<<g, t, 0, s>>>(a);
   } else if (mode == 0) {
     if (qb == 1) k_gemm16<PD, METRIC, 1, 0, 0><<<g, t, 0, s>>>(a);
     else k_gemm16<PD, METRIC, 2, 0, 0><<<g, t, 0, s>>>(a);
@@ -321,7 +338,7 @@ static void launch16_pm(int qb, int mode, bool split, hipStream_t s, int blocks,
 }
 
 template <int PD>
-static void launch16_pd(int metric, int qb, int mode, bool split, hipStream_t s, int blocks,
+static void launch16_pd(int metric, int qb, int mode, int split, hipStream_t s, int blocks,
                         const GemmArgs& a) {
   if (metric == 0)
     launch16_pm<PD, 0>(qb, mode, split, s, blocks, a);
@@ -329,7 +346,7 @@ static void launch16_pd(int metric, int qb, int mode, bool split, hipStream_t s,
     launch16_pm<PD, 1>(qb, mode, split, s, blocks, a);
 }
 
-int LaunchGemm16(size_t pd, int metric, int qb, int mode, bool split, hipStream_t s, int blocks,
+int LaunchGemm16(size_t pd, int metric, int qb, int mode, int split, hipStream_t s, int blocks,
                  const GemmArgs& a) {
   if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM16: query blocks per wave");
   if ((mode == 1 || split) && qb != 2)
@@ -351,13 +368,44 @@ __global__ void k_to_f16(const float* __restrict__ x, size_t n, uint16_t* __rest
   if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(x[i]));
 }
 
-int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, const RowStats& st,
-               uint16_t** out) {
+// Two-part fp16 rows: x 2^e = h + l (h = fp16(x 2^e), l = fp16(x 2^e - h)), stored per
+// K chunk of kc dims as [h | l].
+__global__ void k_to_f16_split(const float* __restrict__ x, size_t n, int pd, int kc, int e,
+                               uint16_t* __restrict__ y) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i >= n) return;
+  const size_t r = i / pd;
+  const int col = int(i - r * pd);
+  const int c = col / kc, w = col - c * kc;
+  const float v = ldexpf(x[i], e);
+  const _Float16 hh = _Float16(v);
+  const _Float16 ll = _Float16(v - float(hh));
+  uint16_t* dst = y + r * 2 * pd + size_t(c) * 2 * kc + w;
+  dst[0] = __builtin_bit_cast(uint16_t, hh);
+  dst[kc] = __builtin_bit_cast(uint16_t, ll);
+}
+
+int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int* parts, int* exp,
+               const RowStats& st, uint16_t** out) {
   *out = nullptr;
-  if (n == 0 || !st.all_int || !(st.max_abs <= 2048.f) || !GemmSupported(pd)) return kOk;
+  *parts = 1;
+  *exp = 0;
+  if (n == 0 || !GemmSupported(pd) || !(st.max_abs <= 3.0e38f)) return kOk;
+  const bool exact = st.all_int && st.max_abs <= 2048.f;
+  if (!exact) {
+    // scale so the largest magnitude lands in [2^14, 2^15)
+    int ex = 0;
+    if (st.max_abs > 0.f) (void)frexpf(st.max_abs, &ex);
+    *exp = st.max_abs > 0.f ? 15 - ex : 0;
+    *parts = 2;
+  }
   uint16_t* y = nullptr;
-  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * sizeof(uint16_t)));
-  k_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, y);
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * *parts * sizeof(uint16_t)));
+  if (exact)
+    k_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, y);
+  else
+    k_to_f16_split<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(
+        rows, n * pd, int(pd), Gemm16Kc(int(pd), 2), *exp, y);
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) {
     (void)hipFree(y);

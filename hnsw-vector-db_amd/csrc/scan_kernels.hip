@@ -312,8 +312,9 @@ int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* sca
 // Sample position p holds row floor(bitrev(p) * N / Smax): every power-of-two prefix of the
 // sample is an evenly strided subset of the rows.
 __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __restrict__ X16,
-                                const uint8_t* __restrict__ C, const float* __restrict__ rn,
-                                uint32_t N, int pd, int bits, uint32_t smax,
+                                int pd16, const uint8_t* __restrict__ C,
+                                const float* __restrict__ rn, uint32_t N, int pd, int bits,
+                                uint32_t smax,
                                 float* __restrict__ SX, uint16_t* __restrict__ SX16,
                                 uint8_t* __restrict__ SC, float* __restrict__ Srn,
                                 uint32_t* __restrict__ Sid) {
@@ -322,32 +323,50 @@ __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __r
   const uint32_t row = uint32_t((uint64_t(bitrev(p, bits)) * N) / smax);
   for (int i = threadIdx.x; i < pd; i += blockDim.x) {
     if (X) SX[size_t(p) * pd + i] = X[size_t(row) * pd + i];
-    if (X16) SX16[size_t(p) * pd + i] = X16[size_t(row) * pd + i];
     if (C) SC[size_t(p) * pd + i] = C[size_t(row) * pd + i];
   }
+  for (int i = threadIdx.x; X16 != nullptr && i < pd16; i += blockDim.x)
+    SX16[size_t(p) * pd16 + i] = X16[size_t(row) * pd16 + i];
   if (threadIdx.x == 0) {
     Srn[p] = rn[row];
     Sid[p] = row;
   }
 }
 
-int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
-  if (src->Smax != 0) return kOk;
+uint32_t SampleRows(uint32_t N) {
   uint32_t smax = 1;
-  while (smax * 2 <= std::min<uint32_t>(src->N, 65536u)) smax *= 2;
+  while (smax * 2 <= std::min<uint32_t>(N, 65536u)) smax *= 2;
+  return smax;
+}
+
+size_t SampleBytes(const ScanSource& src, uint32_t smax) {
+  auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
+  const size_t pd = src.pd;
+  return al(src.kind == 0 ? size_t(smax) * pd * sizeof(float) : 0) +
+         al(src.X16 != nullptr ? size_t(smax) * pd * src.x16_parts * sizeof(uint16_t) : 0) +
+         al(src.kind == 1 ? size_t(smax) * pd : 0) + al(size_t(smax) * sizeof(float)) +
+         al(size_t(smax) * sizeof(uint32_t)) + 256;
+}
+
+int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
+  const uint32_t smax = SampleRows(src->N);
   int bits = 0;
   while ((1u << bits) < smax) ++bits;
   const size_t pd = src->pd;
-  if (src->kind == 0)
-    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX), size_t(smax) * pd * sizeof(float)));
-  if (src->X16 != nullptr)
-    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SX16), size_t(smax) * pd * sizeof(uint16_t)));
-  if (src->kind == 1)
-    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->SC), size_t(smax) * pd));
-  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Srn), size_t(smax) * sizeof(float)));
-  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&src->Sid), size_t(smax) * sizeof(uint32_t)));
+  char* p = reinterpret_cast<char*>((reinterpret_cast<uintptr_t>(buf) + 255) & ~uintptr_t(255));
+  auto take = [&](size_t b) {
+    char* r = b != 0 ? p : nullptr;
+    p += (b + 255) & ~size_t(255);
+    return r;
+  };
+  src->SX = reinterpret_cast<float*>(take(src->kind == 0 ? size_t(smax) * pd * sizeof(float) : 0));
+  src->SX16 = reinterpret_cast<uint16_t*>(
+      take(src->X16 != nullptr ? size_t(smax) * pd * src->x16_parts * sizeof(uint16_t) : 0));
+  src->SC = reinterpret_cast<uint8_t*>(take(src->kind == 1 ? size_t(smax) * pd : 0));
+  src->Srn = reinterpret_cast<float*>(take(size_t(smax) * sizeof(float)));
+  src->Sid = reinterpret_cast<uint32_t*>(take(size_t(smax) * sizeof(uint32_t)));
   k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
-                                             src->X16,
+                                             src->X16, int(pd) * src->x16_parts,
                                              src->kind == 1 ? src->C : nullptr, src->rn,
                                              src->N, int(pd), bits, smax, src->SX, src->SX16,
                                              src->SC, src->Srn, src->Sid);
@@ -356,12 +375,25 @@ int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
   return kOk;
 }
 
+// A persistent source's sample: one allocation, kept until FreeSample.
+int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
+  if (src->Smax != 0) return kOk;
+  void* buf = nullptr;
+  VDBG_HIP(hipMalloc(&buf, SampleBytes(*src, SampleRows(src->N))));
+  const int rc = GatherSample(c, src, s, buf);
+  if (rc != kOk) {
+    (void)hipFree(buf);
+    return rc;
+  }
+  src->Sbuf = buf;
+  return kOk;
+}
+
+// Frees a sample BuildSample allocated (a sample gathered into caller memory is only
+// forgotten).
 void FreeSample(ScanSource* src) {
-  (void)hipFree(src->SX);
-  (void)hipFree(src->SX16);
-  (void)hipFree(src->SC);
-  (void)hipFree(src->Srn);
-  (void)hipFree(src->Sid);
+  if (src->Sbuf != nullptr) (void)hipFree(src->Sbuf);
+  src->Sbuf = nullptr;
   src->SX = nullptr;
   src->SX16 = nullptr;
   src->SC = nullptr;
@@ -385,7 +417,9 @@ struct PrepArgs {
   int* exact;    // the bound is zero
   uint16_t* Q16;  // nullable: the fp16 GEMM's B operand (gemm16.hip)
   int* all16;     // nullable: cleared when a query is outside the fp16 GEMM's bounds
-  float* Qf;      // SQ8 with Q16: per-query factor taking the split GEMM back to GEMM units
+  float* Qf;      // split operands: per-query factor taking the split GEMM back to GEMM units
+  int x16_parts;  // flat rows: 2 when they are held as scaled fp16 h + l pairs
+  int x16_exp;    // their scale exponent
 };
 
 // One wave per query.
@@ -412,7 +446,7 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     hi = fmaxf(hi, e);
     ma = fmaxf(ma, fabsf(e));
     ai &= (e == rintf(e)) ? 1 : 0;
-    if (a.Q16 != nullptr && a.kind == 0)  // the fp16 GEMM's B operand: -2 q (L2) or -q (IP)
+    if (a.Q16 != nullptr && a.kind == 0 && a.x16_parts == 1)  // -2 q (L2) or -q (IP)
       a.Q16[size_t(q) * a.pd + i] =
           __builtin_bit_cast(uint16_t, _Float16(a.metric == 0 ? -2.f * e : -e));
     if (a.kind == 1) {
@@ -437,7 +471,23 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
   // fp16, so the GEMM runs as c.h + c.l and Qf = -2 (L2) or -1 (IP) times 2^-sc takes it back
   int sc = 0;
   bool split_ok = true;
-  if (a.kind == 1 && a.Q16 != nullptr) {
+  if (a.kind == 0 && a.x16_parts == 2 && a.Q16 != nullptr) {
+    // float rows held as h + l: q 2^sc split the same way (max |q| 2^sc in [2^14, 2^15))
+    split_ok = ma <= 3.0e38f;
+    if (split_ok && ma > 0.f) {
+      int ex = 0;
+      (void)frexpf(ma, &ex);
+      sc = 15 - ex;
+    }
+    uint16_t* hq = a.Q16 + size_t(q) * 2 * a.pd;
+    for (int i = lane_id(); i < a.pd; i += kWave) {
+      const float vs = ldexpf(v[i], sc);
+      const _Float16 hh = _Float16(vs);
+      const _Float16 ll = _Float16(vs - float(hh));
+      hq[i] = __builtin_bit_cast(uint16_t, hh);
+      hq[a.pd + i] = __builtin_bit_cast(uint16_t, ll);
+    }
+  } else if (a.kind == 1 && a.Q16 != nullptr) {
     float mb = 0.f;
     for (int i = lane_id(); i < a.pd; i += kWave) mb = fmaxf(mb, fabsf(a.Qb[size_t(q) * a.pd + i]));
     mb = wave_max(mb);
@@ -477,8 +527,8 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     // magnitude <= 4096); the fp16 GEMM accumulates ||x||^2 - 2 q.x (or -q.x) from the row
     // norm, every partial sum bounded by (|q| + R)^2 with R the largest row norm.  Below 2^24
     // its values are the fp32 GEMM's bit for bit.
-    if (a.all16 != nullptr && a.kind == 1) {
-      a.Qf[q] = ldexpf(a.metric == 0 ? -2.f : -1.f, -sc);
+    if (a.all16 != nullptr && (a.kind == 1 || a.x16_parts == 2)) {
+      a.Qf[q] = ldexpf(a.metric == 0 ? -2.f : -1.f, -sc - (a.kind == 0 ? a.x16_exp : 0));
       if (!split_ok) atomicAnd(a.all16, 0);
     } else if (a.all16 != nullptr) {
       const double rq = sqrt(double(s)), rx = sqrt(double(a.xs.xn_max));
@@ -502,8 +552,20 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     // below the normal range (each of h, l off by at most 2^-14 2^-sc, times c <= 255 and 2)
     const double bound16 = (6.0 * pd + 48.0) * u * (double(qmag) + double(a.rmag)) +
                            1020.0 * pd * ldexp(1.0, -14 - sc);
-    const bool split = a.kind == 1 && a.Q16 != nullptr;
-    a.eb[q] = ex ? 0.f : float((split ? bound16 : bound) * 1.001);
+    // Float rows on the split fp16 GEMM (x_h q_h + x_h q_l + x_l q_h): per product the
+    // parts miss at most 3 x 2^-22 relative (the dropped x_l q_l and the two split
+    // residuals), the fp32 accumulations of 3 pd exact products (and their sum and fma) add
+    // (3 pd + 4) u sum|q_i x_i|; doubled for margin, plus fp16 values below the normal range
+    // (each part of x off by at most 2^-14 2^-x16_exp, of q by 2^-14 2^-sc).
+    const double fsub = 4.0 * pd * ldexp(1.0, -14) *
+                        (ldexp(double(ma), -a.x16_exp) + ldexp(double(a.xs.max_abs), -sc));
+    const double bound16f =
+        a.metric != 0 ? (2.0 * pd + 16.0 + 6.0 * pd + 48.0) * u * sqrt(double(qmag) * double(a.rmag)) + fsub
+                      : (4.0 * pd + 16.0 + 6.0 * pd + 48.0) * u * (double(qmag) + double(a.rmag)) +
+                            2.0 * fsub;
+    const bool split = a.Q16 != nullptr && (a.kind == 1 || a.x16_parts == 2);
+    a.eb[q] = ex ? 0.f
+                 : float((split ? (a.kind == 1 ? bound16 : bound16f) : bound) * 1.001);
   }
 }
 
@@ -1322,8 +1384,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // Rows with an fp16 copy may rank on the fp16 GEMM: integer-valued flat rows exactly
   // (64 queries per wave, or 32 for batches of at most 128), SQ8 codes with the query operand
   // split in two fp16 parts (both register sets hold the same 32 queries).
-  const bool try16 = c->exact_fp16 && src->X16 != nullptr;
-  const bool split = src->kind == 1;
+  const bool try16 = c->fp16_gemm && src->X16 != nullptr;
+  const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
   const Plan p32 = make_plan(1, 128);
   const Plan p16 = split ? make_plan(2, 128) : (nq > 128 ? make_plan(2, 256) : make_plan(1, 128));
   auto cand_bytes = [&](const Plan& p) {
@@ -1362,14 +1424,19 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   if (try16) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
-              src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf};
+              src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
+              src->x16_exp};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
     VDBG_HIP(hipGetLastError());
   }
-  bool use16 = false;
-  if (try16) {
+  // The exact-integer GEMM needs every query of the batch inside its bounds, so the host
+  // reads the flag.  The split operands need no such check: a non-finite query only yields
+  // NaN or infinite GEMM values and bound, its certificate fails and it is re-scanned
+  // exactly, as on the fp32 GEMM.
+  bool use16 = try16 && split != 0;
+  if (try16 && split == 0) {
     VDBG_HIP(hipMemcpyAsync(c->host_pinned, all16, sizeof(int), hipMemcpyDeviceToHost, s));
     VDBG_HIP(hipStreamSynchronize(s));
     use16 = c->host_pinned[0] != 0;

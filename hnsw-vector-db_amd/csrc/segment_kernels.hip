@@ -104,9 +104,13 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t nwords = (size_t(N) + 63) / 64;
   const size_t row_bytes = src->kind == 0 ? pd * sizeof(float) : pd;
   void* buf = nullptr;
-  const size_t row16_bytes = src->X16 != nullptr ? pd * sizeof(uint16_t) : 0;
-  const size_t bytes =
-      (nwords + 1) * 4 * 2 + size_t(count) * (4 + 4 + row_bytes + row16_bytes) + 4096;
+  const size_t row16_bytes = src->X16 != nullptr ? src->x16_parts * pd * sizeof(uint16_t) : 0;
+  // the compacted source's sample lives in the same stream-ordered allocation
+  ScanSource cs = *src;
+  cs.N = count;
+  const size_t sample_bytes = SampleBytes(cs, SampleRows(count));
+  const size_t bytes = (nwords + 1) * 4 * 2 +
+                       size_t(count) * (4 + 4 + row_bytes + row16_bytes) + sample_bytes + 4096;
   VDBG_HIP(hipMallocAsync(&buf, bytes, s));
   char* p = static_cast<char*>(buf);
   auto take = [&](size_t b) {
@@ -120,6 +124,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   float* rn = reinterpret_cast<float*>(take(size_t(count) * 4 + 4));
   void* rows = take(size_t(count) * row_bytes + 16);
   void* rows16 = row16_bytes != 0 ? take(size_t(count) * row16_bytes + 16) : nullptr;
+  void* sample = take(sample_bytes);
   void* tmp = nullptr;
   {
     ProfScope ps(c, "compact", s);
@@ -138,27 +143,21 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
           reinterpret_cast<const uint4*>(src->C), row_u4, ids, count, static_cast<uint4*>(rows));
     }
-    if (rows16 != nullptr) {  // the fp16 copy of integer-valued rows follows the fp32 rows
-      const size_t row_u4 = pd / 8;
+    if (rows16 != nullptr) {  // the fp16 copy of the rows follows the fp32 rows
+      const size_t row_u4 = row16_bytes / 16;
       k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
           reinterpret_cast<const uint4*>(src->X16), row_u4, ids, count, static_cast<uint4*>(rows16));
     }
     k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
     VDBG_HIP(hipGetLastError());
   }
-  ScanSource cs = *src;
   cs.X = src->kind == 0 ? static_cast<const float*>(rows) : nullptr;
   cs.X16 = static_cast<const uint16_t*>(rows16);
   cs.C = src->kind == 1 ? static_cast<const uint8_t*>(rows) : nullptr;
   cs.rn = rn;
-  cs.N = count;
-  cs.SX = nullptr;
-  cs.SX16 = nullptr;
-  cs.SC = nullptr;
-  cs.Srn = nullptr;
-  cs.Sid = nullptr;
-  cs.Smax = 0;
-  int rc = RunScan(c, &cs, Q, nq, kk, nullptr, out_ids, out_d, s);
+  cs.Sbuf = nullptr;
+  int rc = GatherSample(c, &cs, s, sample);
+  if (rc == kOk) rc = RunScan(c, &cs, Q, nq, kk, nullptr, out_ids, out_d, s);
   if (rc == kOk) {
     k_map_ids<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, nq * kk, ids);
     if (hipGetLastError() != hipSuccess) rc = SetError(kInternal, "map ids launch");

@@ -138,7 +138,9 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
     return rc;
   }
   if (n > 0) {
-    rc = MakeRows16(c, c->stream, d.rows, n, pd, d.stats, &d.rows16);
+    if (c->fp16_gemm)
+      rc = MakeRows16(c, c->stream, d.rows, n, pd, &d.rows16_parts, &d.rows16_exp, d.stats,
+                      &d.rows16);
     if (rc != kOk) {
       (void)hipFree(d.rows);
       (void)hipFree(d.norms);
@@ -149,6 +151,8 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   d.src.kind = 0;
   d.src.X = d.rows;
   d.src.X16 = d.rows16;
+  d.src.x16_parts = d.rows16_parts;
+  d.src.x16_exp = d.rows16_exp;
   d.src.rn = d.norms;
   d.src.N = static_cast<uint32_t>(n);
   d.src.pd = static_cast<int>(pd);
@@ -312,10 +316,10 @@ const char* vdbg_ctx_kernels(vdbg_ctx* ctx) {
   return ctx == nullptr ? "" : kKsetNames[ctx->c.kset];
 }
 
-int vdbg_ctx_set_exact_fp16(vdbg_ctx* ctx, int enable) {
+int vdbg_ctx_set_fp16_gemm(vdbg_ctx* ctx, int enable) {
   if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
   std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
-  ctx->c.exact_fp16 = enable != 0;
+  ctx->c.fp16_gemm = enable != 0;
   return kOk;
 }
 

@@ -87,7 +87,7 @@ struct Ctx {
   int cu_count = 256;
   int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
-  bool exact_fp16 = true;      // integer-valued flat scans may rank on the fp16 GEMM
+  bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 
@@ -96,8 +96,12 @@ struct Ctx {
 struct ScanSource {
   int kind = 0;
   const float* X = nullptr;     // kind 0: n x pd rows
-  const uint16_t* X16 = nullptr;  // kind 0: the rows as fp16 when every value is an integer
-                                  // of magnitude <= 2048 (exact), else null
+  const uint16_t* X16 = nullptr;  // rows as fp16 for the fp16 GEMM (gemm16.hip), or null:
+                                  // kind 0 integer rows exactly (x16_parts 1), kind 0 float
+                                  // rows as 2^x16_exp-scaled h + l pairs (x16_parts 2, [h|l]
+                                  // per K chunk), kind 1 codes exactly (x16_parts 1)
+  int x16_parts = 1;
+  int x16_exp = 0;
   const uint8_t* C = nullptr;   // kind 1: n x pd codes
   const float* rn = nullptr;    // ||x||^2 (flat) or ||code * scale||^2 (SQ8)
   const float* vmin = nullptr;  // SQ8 quantizer (device)
@@ -107,18 +111,20 @@ struct ScanSource {
   float rmag = 0.f;             // row magnitude term of the rounding bound
   RowStats stats;               // flat: value statistics for the exactness test
   float* SX = nullptr;          // sample rows (kind 0)
-  uint16_t* SX16 = nullptr;     // sample rows as fp16 (kind 0 with X16)
+  uint16_t* SX16 = nullptr;     // sample rows of X16 (same layout)
   uint8_t* SC = nullptr;        // sample codes (kind 1)
   float* Srn = nullptr;
   uint32_t* Sid = nullptr;
   uint32_t Smax = 0;
+  void* Sbuf = nullptr;         // the sample's allocation when the source owns it
 };
 
 struct Dataset {
   Ctx* ctx = nullptr;
   float* rows = nullptr;   // n x pd
   float* norms = nullptr;  // n row norms (fp32, ||x||^2)
-  uint16_t* rows16 = nullptr;  // n x pd fp16 copy of integer-valued rows (see ScanSource::X16)
+  uint16_t* rows16 = nullptr;  // fp16 copy of the rows (see ScanSource::X16)
+  int rows16_parts = 1, rows16_exp = 0;
   size_t n = 0, dim = 0, pd = 0;
   int metric = 0;
   RowStats stats;
@@ -177,7 +183,10 @@ int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
 // representable), used by the exact-integer GEMM; *out stays null when not applicable.
 // SQ8 codes as fp16 (exact) for the split fp16 GEMM; null when pd has no GEMM kernel.
 int MakeCodes16(Ctx* c, hipStream_t s, const uint8_t* codes, size_t n, size_t pd, uint16_t** out);
-int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
+// fp16 copy of flat rows for the fp16 GEMM: integer rows of magnitude <= 2048 exactly
+// (*parts 1), other finite rows as h + l parts of x 2^*exp (*parts 2); null when pd has no
+// GEMM kernel.
+int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int* parts, int* exp,
                const RowStats& st, uint16_t** out);
 
 // Top-kk rows by the source's exact distance for nq queries (device pointers).
@@ -206,6 +215,11 @@ int SortSegmentsTopK(Ctx* c, uint64_t* keys, uint64_t* keys_alt, const int* off_
 int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
 int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);
+// The sample rows of an N-row source, its buffer size, and the gather into caller memory
+// (at least SampleBytes, any alignment) for sources that live one call.
+uint32_t SampleRows(uint32_t N);
+size_t SampleBytes(const ScanSource& src, uint32_t smax);
+int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf);
 void FreeSample(ScanSource* src);
 
 // Host-pointer staging shared by the _host entry points: copies queries (and the filter)

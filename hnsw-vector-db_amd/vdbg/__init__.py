@@ -57,7 +57,7 @@ _SIGS = {
     "vdbg_ctx_synchronize": (C.c_int, [_vp]),
     "vdbg_ctx_set_kernels": (C.c_int, [_vp, C.c_char_p]),
     "vdbg_ctx_kernels": (C.c_char_p, [_vp]),
-    "vdbg_ctx_set_exact_fp16": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_fp16_gemm": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_reset": (C.c_int, [_vp]),
     "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
@@ -167,10 +167,11 @@ class Context:
     def set_kernels(self, name):
         _check(lib.vdbg_ctx_set_kernels(self.h, name.encode()))
 
-    def set_exact_fp16(self, enable=True):
-        """Let integer-valued flat scans rank on the exact fp16 GEMM (the default); False
-        always ranks on the fp32 GEMM.  Results are identical."""
-        _check(lib.vdbg_ctx_set_exact_fp16(self.h, 1 if enable else 0))
+    def set_fp16_gemm(self, enable=True):
+        """Let flat and SQ8 scans rank on fp16 MFMA (the default): integer rows exactly,
+        SQ8 codes and float rows on split fp16 operands.  False always ranks on the fp32
+        GEMM.  Results are identical."""
+        _check(lib.vdbg_ctx_set_fp16_gemm(self.h, 1 if enable else 0))
 
     def profile(self, enable=True):
         _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))

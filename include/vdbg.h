@@ -83,10 +83,13 @@ int vdbg_ctx_synchronize(vdbg_ctx* ctx);
  * of this CPU.  Setting an unknown or unavailable set is InvalidArgument. */
 int vdbg_ctx_set_kernels(vdbg_ctx* ctx, const char* name);
 const char* vdbg_ctx_kernels(vdbg_ctx* ctx);
-/* Whether flat scans over integer-valued rows may rank on the fp16-input GEMM when a batch
- * fits its exact bounds (default 1).  Results are identical either way; 0 always ranks on
- * the fp32 GEMM (for comparisons).  No counterpart in the reference. */
-int vdbg_ctx_set_exact_fp16(vdbg_ctx* ctx, int enable);
+/* Whether flat and SQ8 scans may rank rows on fp16 MFMA (default 1): integer-valued rows
+ * exactly when a batch fits the exact bounds, SQ8 codes and float rows with the operands
+ * split into two fp16 parts under a widened rounding bound.  Datasets created while it is
+ * on keep an fp16 copy of their rows (2 bytes per value for integer rows, 4 for float rows;
+ * SQ8 indexes 2 bytes per code).  Returned results are identical either way; 0 ranks on the
+ * fp32 GEMM.  No counterpart in the reference. */
+int vdbg_ctx_set_fp16_gemm(vdbg_ctx* ctx, int enable);
 
 /* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
  * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch

@@ -1,0 +1,95 @@
+"""Float rows on the split fp16 GEMM: rows and queries scaled by powers of two and split into
+fp16 h + l parts, ranked by x_h q_h + x_h q_l + x_l q_h under a rounding bound widened for
+the split.  Returned ids and distances must equal the fp32 GEMM's and the oracle's
+(FlatIndex::search, src/index/flat_index.cc:11-39) bit for bit, across K-chunk shapes,
+metrics, value ranges, filters and batch sizes."""
+import numpy as np
+import pytest
+
+import vdbg
+from vdbg import datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_equal(gi, gd, oi, od):
+    assert gi.shape == oi.shape
+    bad = np.nonzero((gi != oi).any(axis=1) | (gd.view(np.uint32) != od.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, (
+        f"{bad.size} queries differ; first q={bad[0]} gpu={gi[bad[0]].tolist()} "
+        f"{gd[bad[0]].tolist()} ref={oi[bad[0]].tolist()} {od[bad[0]].tolist()}")
+
+
+def _data(kind, n, nq, dim, seed):
+    if kind == "uniform":
+        return datagen.uniform_rows(n, dim, seed), datagen.uniform_rows(nq, dim, seed + 1)
+    if kind == "unit":
+        return (datagen.clustered_unit(n, dim, seed, seed + 7, 300, 0.5),
+                datagen.clustered_unit(nq, dim, seed + 1, seed + 7, 300, 0.5))
+    rng = np.random.default_rng(seed)
+    if kind == "normal":
+        return (rng.normal(0, 1, (n, dim)).astype(np.float32),
+                rng.normal(0, 1, (nq, dim)).astype(np.float32))
+    # per-dimension scales over six decades: small parts fall below fp16's normal range
+    scales = (np.float32(10.0) ** rng.uniform(-3, 3, dim)).astype(np.float32)
+    return ((rng.normal(0, 1, (n, dim)) * scales).astype(np.float32),
+            (rng.normal(0, 1, (nq, dim)) * scales).astype(np.float32))
+
+
+def _search_both(ctx, ds, qs, k, allow=None):
+    gi, gd = ds.flat_search(qs, k, allow=allow)
+    assert ctx.last_gemm_bits() == 16
+    ctx.set_fp16_gemm(False)
+    try:
+        gi32, gd32 = ds.flat_search(qs, k, allow=allow)
+        assert ctx.last_gemm_bits() == 32
+    finally:
+        ctx.set_fp16_gemm(True)
+    _check_equal(gi, gd, gi32, gd32)
+    return gi, gd
+
+
+@pytest.mark.parametrize("kind,metric,dim,n,nq,k", [
+    ("uniform", "l2", 128, 30000, 200, 10),     # K chunk 64, two chunks
+    ("unit", "cosine", 384, 30000, 150, 10),    # the filtered benchmark's shape, six chunks
+    ("normal", "l2", 96, 20000, 130, 50),       # chunk 48
+    ("unit", "ip", 112, 20000, 100, 10),        # chunk 16, seven chunks
+    ("wide", "l2", 64, 20000, 100, 10),
+    ("wide", "ip", 128, 20000, 100, 20),
+    ("normal", "l2", 1024, 8000, 64, 10),
+    ("uniform", "l2", 16, 5000, 40, 5),
+])
+def test_split_matches_fp32_and_oracle(ctx, oracle, kind, metric, dim, n, nq, k):
+    print(f"split16 {kind} {metric} dim={dim} n={n} nq={nq} k={k}", flush=True)
+    base, qs = _data(kind, n, nq, dim, 7001 + dim)
+    pd = vdbg.padded_dim(dim)
+    base, qs = datagen.pad(base, pd), datagen.pad(qs, pd)
+    ds = vdbg.Dataset(ctx, base, dim, metric=metric)
+    gi, gd = _search_both(ctx, ds, qs, k)
+    od, oi = oracle.flat_search(base, qs, k, metric=metric)
+    _check_equal(gi, gd, oi, od)
+    assert ctx.last_fallbacks() == 0
+
+
+@pytest.mark.parametrize("frac", [0.15, 0.7])
+def test_split_filtered(ctx, oracle, frac):
+    # 0.15: allowed rows compacted (fp32 rows and fp16 pairs); 0.7: NaN starts per filtered row
+    n, dim = 40000, 384
+    base, qs = _data("unit", n, 128, dim, 7101)
+    rows = np.nonzero(np.random.default_rng(7102).random(n) < frac)[0]
+    allow = np.zeros((n + 63) // 64, np.uint64)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, dim, metric="cosine")
+    gi, gd = _search_both(ctx, ds, qs, 10, allow=allow)
+    od, oi = oracle.flat_search(base, qs, 10, metric="cosine", allow=allow)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_split_large_batch(ctx, oracle):
+    n, nq, dim = 150000, 1100, 128
+    base, qs = _data("normal", n, nq, dim, 7201)
+    ds = vdbg.Dataset(ctx, base, dim)
+    gi, gd = ds.flat_search(qs, 10)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)

@@ -129,12 +129,12 @@ def test_sq8_split_fp16_matches_fp32_and_oracle(ctx, oracle, data, metric, nq, k
     sq = vdbg.Sq8Index(ds)
     gi, gd = sq.search(qs, k, depth)
     assert ctx.last_gemm_bits() == 16
-    ctx.set_exact_fp16(False)
+    ctx.set_fp16_gemm(False)
     try:
         gi32, gd32 = sq.search(qs, k, depth)
         assert ctx.last_gemm_bits() == 32
     finally:
-        ctx.set_exact_fp16(True)
+        ctx.set_fp16_gemm(True)
     _eq(gi, gd, gi32, gd32)
     od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth, metric=metric)
     _eq(gi, gd, oi, od)
