@@ -2,8 +2,8 @@
  * vdbg.h -- C ABI of the MI355X (gfx950) search backend for vdb's nearest-neighbour path.
  *
  * This is the drop-in boundary: plain pointers and sizes, no C++ or framework types.  vdb's
- * C++ Index implementations (or any FFI) bind these entry points; the C++20 classes in
- * hnsw-vector-db_amd/host (GpuFlatIndex, GpuSq8Index, GpuIvfPqIndex) are such a binding.
+ * C++ Index implementations (or any FFI) bind these entry points; the header-only C++20
+ * classes in include/vdbg.hpp (GpuFlatIndex, GpuSq8Index, GpuIvfPqIndex) are such a binding.
  *
  * Conventions
  *  - Every call returns an int equal to vdb::Status::Code (include/vdb/status.h:14-26):

@@ -175,6 +175,13 @@ class Device {
     vdbg_last_fallbacks(ctx_, &n);
     return n;
   }
+  // Ranking on fp16 MFMA (default on; results are identical either way).  Datasets created
+  // while it is on keep an fp16 copy of their rows.
+  Status set_fp16_gemm(bool enable) {
+    return Status::FromCall(vdbg_ctx_set_fp16_gemm(ctx_, enable ? 1 : 0));
+  }
+  // The distance kernel set exact distances follow ("scalar", "avx2", "avx512").
+  Status set_kernels(const char* name) { return Status::FromCall(vdbg_ctx_set_kernels(ctx_, name)); }
 
  private:
   explicit Device(vdbg_ctx* c) : ctx_(c) {}
