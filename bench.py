@@ -44,7 +44,7 @@ def log(*a):
 
 
 PROFILES = {"flat": "flat_gemm16_sift_like_1m_x128_k10_b10000.md",
-            "sq8": "sq8_gemm_sift_like_1m_x128_d100_b10000.md",
+            "sq8": "sq8_gemm16_split_sift_like_1m_x128_d100_b10000.md",
             "ivfpq": "ivf_scan_sift_like_1m_nlist4096_m16_nprobe64.md"}
 
 
@@ -155,6 +155,8 @@ def run_filtered(args, ctx, torch, ref, threads):
              "ms_per_step": round(el * 1e3 / args.steps, 3),
              "gemm_ms_per_step": round(g_ms, 3),
              "gemm_TFLOPs": round(flops / (g_ms * 1e-3) / 1e12, 2) if g_ms > 0 else None,
+             "mfma_inputs": ("f16 two-part rows x two-part queries (3 MFMA products each)"
+                             if ctx.last_gemm_bits() == 16 else "f32"),
              "kernel_ms_per_step": {kk: round(v[0] / args.steps, 4) for kk, v in prof.items()},
              "exact_rescans": fb}
         log(f"filtered {sel}%: {r['qps']:.0f} q/s, {n_allowed} rows allowed")
@@ -348,10 +350,15 @@ def main():
         gi, gd = gpu_out()
         g_ms = prof["sq8_gemm"][0] / max(1, prof["sq8_gemm"][1])
         tflops = 2.0 * nq * N * dim / (g_ms * 1e-3) / 1e12
+        # the codes rank on fp16 MFMA against the query operand split in two fp16 parts
+        # (two MFMA products per code x query product); achieved counts the algorithmic flop
+        bits = ctx.last_gemm_bits()
         r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
-             "kernel": "k_gemm<128,L2,codes,filter>", "kernel_ms": g_ms, "achieved": tflops,
-             "unit": "TFLOP/s", "peak": FP32_MFMA_PEAK_TFLOPS, "bound": "mfma",
-             "code_stream_TBps": nq * N * dim / (g_ms * 1e-3) / 1e12,
+             "kernel": "k_gemm16<128,L2,split codes>" if bits == 16 else "k_gemm<128,L2,codes,filter>",
+             "kernel_ms": g_ms, "achieved": tflops, "unit": "TFLOP/s",
+             "peak": FP16_MFMA_PEAK_TFLOPS if bits == 16 else FP32_MFMA_PEAK_TFLOPS,
+             "bound": "mfma",
+             "mfma_inputs": "f16 codes x two-part f16 query operand" if bits == 16 else "f32",
              "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
              "exact_rescans": fb, "depth": depth}
         log(f"sq8: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} TFLOP/s")
