@@ -254,11 +254,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     };
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
     if (wave_live && MODE == 0) {
-      // one compare per value; a value passing on some lane of the wave branches to the write
+      // Per 32-row block: the minimum of the lane's 16 values (NaN skipped) against the
+      // threshold, one wave-uniform branch; only a block passing on some lane tests its
+      // values one by one, a value passing on some lane branching to the write.
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk)
+        for (int blk = 0; blk < 2; ++blk) {
+          float m = value(qb, blk, 0);
+#pragma unroll
+          for (int r = 1; r < 16; ++r) m = fminf(m, value(qb, blk, r));
+          if (__builtin_amdgcn_ballot_w64(m <= T[qb]) == 0) continue;
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             const float v = value(qb, blk, r);
@@ -271,6 +277,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
               }
             }
           }
+        }
     } else if (wave_live) {
       // fminf skips the NaN values of rows past r_end
 #pragma unroll

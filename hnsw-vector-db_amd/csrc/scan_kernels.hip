@@ -1349,13 +1349,18 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // ---- plan: the fp32 GEMM runs 128 queries per block; the fp16 GEMM 256 (64 per wave,
   // each LDS row fragment feeding two MFMAs), or 128 for batches of at most 128 queries
   const int slots = 2 * c->cu_count;
-  // Sample size: about kk * N / S rows pass the threshold per query, and every pass is a
-  // scattered buffer write plus a select insertion, while the pre-pass costs S / N of the
-  // main GEMM.  S >= kk * N / 640 keeps the passes near 640 per query (N / 64 at k = 10)
-  // until the sample cap.
+  const bool try16 = c->fp16_gemm && src->X16 != nullptr;
+  const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
+  // Sample size: about kk * N / S rows pass the threshold per query, and every pass costs a
+  // scattered buffer write and a select insertion (and on the exact fp16 GEMM every 32-row
+  // block holding one takes the per-value test), while the pre-pass costs S / N of the main
+  // GEMM.  S >= kk * N / P keeps the passes near P per query until the sample cap: P = 160
+  // for large batches on the exact fp16 GEMM, whose MFMA work per row is smallest, 640
+  // otherwise (N / 64 at k = 10).
   uint32_t S = 1;
+  const uint64_t passes = try16 && split == 0 && nq >= 1024 ? 160 : 640;
   const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,
-                                              uint64_t(N) * kk / 640});
+                                              uint64_t(N) * kk / passes});
   while (S < s_want && S < (1u << 30)) S *= 2;
   S = std::min(S, src->Smax);
   const int ngroups = int((S + 31) / 32) * 2;
@@ -1384,8 +1389,6 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // Rows with an fp16 copy may rank on the fp16 GEMM: integer-valued flat rows exactly
   // (64 queries per wave, or 32 for batches of at most 128), SQ8 codes with the query operand
   // split in two fp16 parts (both register sets hold the same 32 queries).
-  const bool try16 = c->fp16_gemm && src->X16 != nullptr;
-  const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
   const Plan p32 = make_plan(1, 128);
   const Plan p16 = split ? make_plan(2, 128) : (nq > 128 ? make_plan(2, 256) : make_plan(1, 128));
   auto cand_bytes = [&](const Plan& p) {
