@@ -150,12 +150,18 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
     const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
     const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
-    const uint16_t* src = a.X16 + size_t(base) * ROWW + kc * SKC;
-    const int over = int(valid) - 1;  // rows past it read row `over`
+    const char* src = reinterpret_cast<const char*>(a.X16 + size_t(base) * ROWW + kc * SKC);
+    if (valid == kGemmRows) {  // a full tile: the precomputed lane offsets
 #pragma unroll
-    for (int i = 0; i < VEC_PER_THREAD; ++i) {
-      const int o = voff[i] - max(0, vrow[i] - over) * ROWW;
-      st.v[i] = *reinterpret_cast<const u32x4*>(src + o);
+      for (int i = 0; i < VEC_PER_THREAD; ++i)
+        st.v[i] = *reinterpret_cast<const u32x4*>(src + uint32_t(voff[i]) * 2u);
+    } else {  // rows past it read row valid - 1 (the same count of loads)
+      const int over = int(valid) - 1;
+#pragma unroll
+      for (int i = 0; i < VEC_PER_THREAD; ++i) {
+        const int o = voff[i] - max(0, vrow[i] - over) * ROWW;
+        st.v[i] = *reinterpret_cast<const u32x4*>(src + uint32_t(o) * 2u);
+      }
     }
     st.n = a.rn[base + min(uint32_t(tid & 63), valid - 1)];  // (the store applies validity)
     if constexpr (MODE == 0)  // a scan without a filter reads one all-ones word (mask 0)
