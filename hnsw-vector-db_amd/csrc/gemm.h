@@ -46,11 +46,14 @@ __host__ __device__ constexpr int GemmKc(int pd) {
   return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : (pd % 32 == 0 ? 32 : 16)));
 }
 
-// K chunk of the fp16 GEMM.  Two-part float rows (split 2) stage [h | l] per chunk, so their
-// chunk is at most 64 dims (the largest multiple of 16 dividing pd), which keeps two staging
-// register sets and both query parts within the wave's registers.
+// K chunk of the fp16 GEMM.  Rows up to 128 dims stage whole (the query fragments then load
+// once); wider rows, and two-part float rows (split 2, staged as [h | l] per chunk), stage
+// chunks of at most 64 dims (the largest multiple of 16 dividing pd), which keeps two
+// staging register sets and two sets of query fragments (the next chunk's load a step
+// ahead) within the wave's registers.
 __host__ __device__ constexpr int Gemm16Kc(int pd, int split) {
-  if (split != 2) return GemmKc(pd);
+  if (split != 2 && pd <= 128) return pd;
+  if (split == 2 && pd <= 64) return pd;
   for (int kc = 64; kc > 16; kc -= 16)
     if (pd % kc == 0) return kc;
   return 16;

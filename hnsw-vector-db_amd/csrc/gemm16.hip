@@ -14,6 +14,7 @@
 // the fp32 GEMM.
 #include <algorithm>
 #include <string>
+#include <type_traits>
 
 #include "gemm.h"
 #include "vdbg_device.h"
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   float T[NQB];
   uint2* out[NQB];
   uint32_t cnt[NQB];
-  const float F = SPLIT ? a.Qf[min(q0 + j, a.nq - 1)] : 1.f;
+  const float qf = SPLIT ? a.Qf[min(q0 + j, a.nq - 1)] : 1.f;  // split: GEMM-unit factor
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     q[qb] = q0 + qb * 32 + j;
@@ -104,20 +105,23 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   // that exist), so each wave has a fixed count of loads in flight and the waits before the
   // LDS stores do not drain the prefetch early.  Lanes of queries past the batch read query
   // nq - 1; their values are never emitted.
-  half8 qv[QB][NKB];
+  // Query fragments of a stage's K chunk.  With one chunk they load once; with several, the
+  // next stage's fragments load a step ahead into the other set (QF sets in all).
+  constexpr int QF = NKC > 1 ? 2 : 1;
+  half8 qv[QF][QB][NKB];
   const uint16_t* qrow[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)
     qrow[qb] = SPLIT ? a.Q16 + (size_t(min(q[0], a.nq - 1)) * 2 + qb) * PD + h * 8
                      : a.Q16 + size_t(min(q[qb], a.nq - 1)) * PD + h * 8;
-  auto load_q = [&](int kc) {
+  auto load_q = [&](int f, int kc) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
       for (int kb = 0; kb < NKB; ++kb)
-        qv[qb][kb] = *reinterpret_cast<const half8*>(qrow[qb] + kc * KC + kb * 16);
+        qv[f][qb][kb] = *reinterpret_cast<const half8*>(qrow[qb] + kc * KC + kb * 16);
   };
-  if (NKC == 1) load_q(0);
+  load_q(0, 0);
 
   // lane offsets (in halfs) of the stage's 16-byte vectors: row f / VEC_PER_ROW, column
   // f % VEC_PER_ROW of the 64 x KC stage
@@ -185,10 +189,13 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   };
 
   v16f acc[QB][2];
-  auto step = [&](Stage& X, Stage& Y, int sidx) {
+  // step s multiplies with query set s % 2 (QF = 2) and loads set (s + 1) % 2 for stage s + 1
+  auto step = [&](Stage& X, Stage& Y, int sidx, auto fcur) {
+    constexpr int QS = decltype(fcur)::value;  // the query fragment set of this step
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
     const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
-    if (NKC > 1) load_q(kc);  // before Y's loads: the MFMAs then wait for these alone
+    if constexpr (QF == 2)  // the next stage's K chunk (a harmless repeat past the end)
+      load_q(QS ^ 1, (kc + 1 == NKC) ? 0 : kc + 1);
     load_stage(Y, sidx + 2);
     // keep the scheduler from sinking Y's loads below the MFMAs (which would shorten the
     // time they have to land to a single step)
@@ -224,14 +231,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
       const half8 x1 = *reinterpret_cast<const half8*>(xa1 + kb * 16);
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
-        acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[qb][kb], acc[qb][0], 0, 0, 0);
-        acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[qb][kb], acc[qb][1], 0, 0, 0);
+        acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[QS][qb][kb], acc[qb][0], 0, 0, 0);
+        acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[QS][qb][kb], acc[qb][1], 0, 0, 0);
       }
       if constexpr (SPLIT == 2) {  // x_l q_h into the cross-term accumulator
         const half8 y0 = *reinterpret_cast<const half8*>(xa0 + KC + kb * 16);
         const half8 y1 = *reinterpret_cast<const half8*>(xa1 + KC + kb * 16);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y0, qv[0][kb], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y1, qv[0][kb], acc[1][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y0, qv[QS][0][kb], acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y1, qv[QS][0][kb], acc[1][1], 0, 0, 0);
       }
     }
     if (sidx + 1 < nstages) store_stage(X, sidx + 1);
@@ -254,7 +261,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     }
     auto value = [&](int qb, int blk, int r) {
       if constexpr (SPLIT)
-        return fmaf(F, acc[0][blk][r] + acc[1][blk][r], xn[blk][r]);
+        return fmaf(qf, acc[0][blk][r] + acc[1][blk][r], xn[blk][r]);
       else
         return acc[qb][blk][r];
     };
@@ -316,8 +323,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   store_stage(B, 0);
   __syncthreads();
   for (int sidx = 0; sidx < nstages; sidx += 2) {
-    step(A, B, sidx);
-    if (sidx + 1 < nstages) step(B, A, sidx + 1);
+    step(A, B, sidx, std::integral_constant<int, 0>{});
+    if (sidx + 1 < nstages) step(B, A, sidx + 1, std::integral_constant<int, QF - 1>{});
   }
 
   if constexpr (MODE == 0) {

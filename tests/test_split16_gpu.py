@@ -58,6 +58,8 @@ def _search_both(ctx, ds, qs, k, allow=None):
     ("wide", "ip", 128, 20000, 100, 20),
     ("normal", "l2", 1024, 8000, 64, 10),
     ("uniform", "l2", 16, 5000, 40, 5),
+    ("normal", "ip", 37, 20000, 64, 20),        # padded to 48: one chunk of [h | l] 96 wide
+    ("unit", "cosine", 256, 20000, 100, 10),    # four chunks of 64, next chunk's queries ahead
 ])
 def test_split_matches_fp32_and_oracle(ctx, oracle, kind, metric, dim, n, nq, k):
     print(f"split16 {kind} {metric} dim={dim} n={n} nq={nq} k={k}", flush=True)

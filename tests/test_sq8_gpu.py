@@ -111,21 +111,22 @@ def _wide_range_rows(n, dim, seed):
     ("sift_like", "l2", 300, 10, 100), ("uniform", "l2", 200, 10, 0),
     ("unit", "cosine", 150, 10, 64), ("unit", "ip", 150, 20, 0),
     ("wide", "l2", 130, 10, 100), ("wide", "ip", 100, 10, 50)])
-def test_sq8_split_fp16_matches_fp32_and_oracle(ctx, oracle, data, metric, nq, k, depth):
+@pytest.mark.parametrize("dim", [128, 96, 384])
+def test_sq8_split_fp16_matches_fp32_and_oracle(ctx, oracle, data, metric, nq, k, depth, dim):
     # the SQ8 scan ranks on fp16 MFMA (codes exact, query operand split in two fp16 parts);
     # results must equal the fp32 GEMM's and the oracle's bit for bit
-    print(f"sq8 split {data} {metric} nq={nq} k={k} depth={depth}", flush=True)
-    n = 40000
+    print(f"sq8 split {data} {metric} dim={dim} nq={nq} k={k} depth={depth}", flush=True)
+    n = 40000 if dim <= 128 else 12000
     if data == "sift_like":
-        base, qs = datagen.sift_like(n, 128, 6101), datagen.sift_like(nq, 128, 6102)
+        base, qs = datagen.sift_like(n, dim, 6101), datagen.sift_like(nq, dim, 6102)
     elif data == "uniform":
-        base, qs = datagen.uniform_rows(n, 128, 6103), datagen.uniform_rows(nq, 128, 6104)
+        base, qs = datagen.uniform_rows(n, dim, 6103), datagen.uniform_rows(nq, dim, 6104)
     elif data == "unit":
-        base = datagen.clustered_unit(n, 128, 6105, 6106, 200, 0.5)
-        qs = datagen.clustered_unit(nq, 128, 6107, 6106, 200, 0.5)
+        base = datagen.clustered_unit(n, dim, 6105, 6106, 200, 0.5)
+        qs = datagen.clustered_unit(nq, dim, 6107, 6106, 200, 0.5)
     else:
-        base, qs = _wide_range_rows(n, 128, 6108), _wide_range_rows(nq, 128, 6108 + 1)
-    ds = vdbg.Dataset(ctx, base, 128, metric=metric)
+        base, qs = _wide_range_rows(n, dim, 6108), _wide_range_rows(nq, dim, 6108 + 1)
+    ds = vdbg.Dataset(ctx, base, dim, metric=metric)
     sq = vdbg.Sq8Index(ds)
     gi, gd = sq.search(qs, k, depth)
     assert ctx.last_gemm_bits() == 16
