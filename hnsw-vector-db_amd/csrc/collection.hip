@@ -1,0 +1,348 @@
+// collection.hip -- CollectionImpl::Search (src/engine/collection_impl.cc:1036-1112) over a
+// snapshot's disk segments for a whole batch of queries, in one call on one stream.
+//
+// vdb runs SearchBatch (:1121-1135) as one Search per query on a thread pool, each calling
+// SearchDiskSegment (src/engine/planner.cc:42-129) per segment and merging.  Here the batch
+// stays on the device: PrepareQuery once for all queries, one device search per segment into
+// a [segment][query][k] hit array (the planner's choice is per segment: it depends only on
+// the segment's filter and deletes, not on the query), one merge kernel that reads each
+// segment's resident external ids, one copy back.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "vdbg_device.h"
+#include "vdbg_internal.h"
+
+namespace vdbg {
+namespace {
+
+size_t CountRows(const uint64_t* w, size_t rows) {
+  size_t n = 0;
+  for (size_t i = 0; i < rows / 64; ++i) n += size_t(__builtin_popcountll(w[i]));
+  if (rows % 64) n += size_t(__builtin_popcountll(w[rows / 64] & ((uint64_t(1) << (rows % 64)) - 1)));
+  return n;
+}
+
+// A device buffer freed on the stream when the call ends.
+struct DevBuf {
+  void* p = nullptr;
+  hipStream_t s = nullptr;
+  ~DevBuf() {
+    if (p != nullptr) (void)hipFreeAsync(p, s);
+  }
+};
+
+int Alloc(DevBuf* b, size_t bytes, hipStream_t s) {
+  b->s = s;
+  VDBG_HIP(hipMallocAsync(&b->p, std::max<size_t>(bytes, 256), s));
+  return kOk;
+}
+
+struct SegPlan {
+  int plan = VDBG_PLAN_INDEX;
+  std::vector<uint64_t> allow;  // host words handed to the device search; empty = none
+  size_t matches = 0;
+  size_t nprobe = 0;
+};
+
+}  // namespace
+}  // namespace vdbg
+
+using namespace vdbg;
+
+extern "C" {
+
+int vdbg_dataset_set_external_ids(vdbg_dataset* ds, const uint64_t* ids) {
+  if (ds == nullptr || (ids == nullptr && ds->d.n > 0)) return SetError(kInvalidArgument, "null argument");
+  Dataset& d = ds->d;
+  Ctx* c = d.ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  if (d.n == 0) return kOk;
+  if (d.ext_ids == nullptr) VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&d.ext_ids), d.n * 8));
+  VDBG_HIP(hipMemcpyAsync(d.ext_ids, ids, d.n * 8, hipMemcpyHostToDevice, c->stream));
+  VDBG_HIP(hipStreamSynchronize(c->stream));
+  return kOk;
+}
+
+int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
+                                size_t dim, int metric, const float* queries, size_t nq,
+                                size_t k, const vdbg_search_params* params, uint64_t* out_ids,
+                                float* out_dists, uint64_t* dist_comps, int* seg_plans) {
+  if (ctx == nullptr || params == nullptr || (nseg > 0 && segs == nullptr) ||
+      (nq > 0 && (queries == nullptr || out_ids == nullptr || out_dists == nullptr)))
+    return SetError(kInvalidArgument, "null argument");
+  // collection_impl.cc:1038-1039
+  if (k == 0 || k > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
+  if (dim == 0 || metric < 0 || metric > 2) return SetError(kInvalidArgument, "bad dim or metric");
+  if (params->strategy < VDBG_STRATEGY_AUTO || params->strategy > VDBG_STRATEGY_POST_FILTER)
+    return SetError(kInvalidArgument, "unknown filter strategy");
+  if (nq > 0x7fffffffull) return SetError(kInvalidArgument, "too many queries");
+  const size_t pd = (dim + 15) / 16 * 16;
+  Ctx* c = &ctx->c;
+  for (size_t p = 0; p < nseg; ++p) {
+    const vdbg_segment& g = segs[p];
+    if (g.rows == nullptr) return SetError(kInvalidArgument, "segment without rows");
+    const Dataset& d = g.rows->d;
+    if (d.ctx != c) return SetError(kInvalidArgument, "segment on another context");
+    if (d.dim != dim || d.pd != pd || d.metric != metric)
+      return SetError(kInvalidArgument, "segment dim or metric differs from the collection's");
+    if (g.sq8 != nullptr && g.ivfpq != nullptr)
+      return SetError(kInvalidArgument, "a segment has one index: sq8 or ivfpq, not both");
+    if ((g.sq8 != nullptr && g.sq8->q.ds != &d) || (g.ivfpq != nullptr && g.ivfpq->x.ds != &d))
+      return SetError(kInvalidArgument, "index does not belong to the segment's rows");
+    if (d.n > 0 && d.ext_ids == nullptr)
+      return SetError(kFailedPrecondition, "segment has no external ids (vdbg_dataset_set_external_ids)");
+  }
+  std::lock_guard<std::recursive_mutex> lk(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  if (dist_comps != nullptr) std::fill(dist_comps, dist_comps + nq, uint64_t(0));
+
+  // ---- the plan of every segment (SearchDiskSegment, planner.cc:53-128)
+  const vdbg_search_params& P = *params;
+  std::vector<SegPlan> plan(nseg);
+  size_t allow_words_total = 0;
+  for (size_t p = 0; p < nseg; ++p) {
+    const vdbg_segment& g = segs[p];
+    const size_t rows = g.rows->d.n, nw = (rows + 63) / 64;
+    const size_t deleted = g.deleted_words ? CountRows(g.deleted_words, rows) : 0;
+    const size_t live = rows - std::min(rows, deleted);
+    SegPlan& sp = plan[p];
+    sp.nprobe = P.nprobe;
+    if (g.filter_words == nullptr) {
+      sp.plan = VDBG_PLAN_INDEX;  // :56-62, DeleteFilter when rows are deleted
+      if (deleted > 0) {
+        sp.allow.resize(nw);
+        for (size_t i = 0; i < nw; ++i) sp.allow[i] = ~g.deleted_words[i];
+      }
+    } else {
+      sp.allow.assign(g.filter_words, g.filter_words + nw);  // Evaluate, minus deletes (:64-65)
+      if (deleted > 0)
+        for (size_t i = 0; i < nw; ++i) sp.allow[i] &= ~g.deleted_words[i];
+      if (rows % 64 && nw > 0) sp.allow[nw - 1] &= (uint64_t(1) << (rows % 64)) - 1;
+      sp.matches = CountRows(sp.allow.data(), rows);
+      const double sel = live == 0 ? 0.0 : double(sp.matches) / double(live);
+      int strat = P.strategy;
+      const bool flat = g.sq8 == nullptr && g.ivfpq == nullptr;
+      if (strat == VDBG_STRATEGY_AUTO) {  // :70-80
+        const double sv = std::max(sel, 1e-9);
+        const double graph_cost = 10.0 * double(std::max(P.ef, k)) / sv;
+        strat = (sp.matches <= P.prefilter_threshold || double(sp.matches) <= graph_cost || flat)
+                    ? VDBG_STRATEGY_PREFILTER
+                    : VDBG_STRATEGY_GRAPH;
+      }
+      if (sp.matches == 0) {
+        sp.plan = VDBG_PLAN_EMPTY;
+        sp.allow.clear();
+      } else if (strat == VDBG_STRATEGY_PREFILTER) {
+        sp.plan = VDBG_PLAN_PREFILTER_EXACT;
+      } else if (strat == VDBG_STRATEGY_GRAPH) {
+        sp.plan = VDBG_PLAN_FILTERED_INDEX;
+        if (P.strategy == VDBG_STRATEGY_AUTO)  // :92-99
+          sp.nprobe = std::max(P.nprobe, size_t(std::ceil(double(P.nprobe) / std::max(sel, 1e-9))));
+      } else {
+        sp.plan = VDBG_PLAN_POST_FILTER;
+      }
+    }
+    allow_words_total += sp.allow.size();
+  }
+
+  if (nq == 0) {
+    if (seg_plans != nullptr)
+      for (size_t p = 0; p < nseg; ++p) seg_plans[p] = plan[p].plan;
+    return kOk;
+  }
+
+  // ---- PrepareQuery for the batch (collection_impl.cc:1023-1034)
+  DevBuf raw, Q, hits_d, hits_r, allow_dev, dcb, extp, oe, od;
+  VDBG_RETURN_IF_ERROR(Alloc(&raw, nq * dim * 4, s));
+  VDBG_RETURN_IF_ERROR(Alloc(&Q, nq * pd * 4, s));
+  VDBG_HIP(hipMemcpyAsync(raw.p, queries, nq * dim * 4, hipMemcpyHostToDevice, s));
+  VDBG_RETURN_IF_ERROR(PrepareQueries(c, static_cast<float*>(raw.p), nq, dim, pd, metric,
+                                      static_cast<float*>(Q.p), s));
+  const float* q = static_cast<const float*>(Q.p);
+
+  const size_t np = std::max<size_t>(nseg, 1), slice = nq * k;
+  VDBG_RETURN_IF_ERROR(Alloc(&hits_d, np * slice * 4, s));
+  VDBG_RETURN_IF_ERROR(Alloc(&hits_r, np * slice * 4, s));
+  VDBG_RETURN_IF_ERROR(Alloc(&allow_dev, allow_words_total * 8, s));
+  VDBG_RETURN_IF_ERROR(Alloc(&dcb, nq * 8, s));
+  std::vector<uint64_t> allow_all;
+  allow_all.reserve(allow_words_total);
+  std::vector<size_t> allow_at(nseg);
+  for (size_t p = 0; p < nseg; ++p) {
+    allow_at[p] = allow_all.size();
+    allow_all.insert(allow_all.end(), plan[p].allow.begin(), plan[p].allow.end());
+  }
+  if (!allow_all.empty())
+    VDBG_HIP(hipMemcpyAsync(allow_dev.p, allow_all.data(), allow_all.size() * 8,
+                            hipMemcpyHostToDevice, s));
+  std::vector<uint64_t> dch(nq);
+
+  // One index search of segment p into (ids, dists) [nq][kk] with the given allow words:
+  // Index::search of the segment's index type, adding its distance computations.
+  auto index_search = [&](size_t p, size_t kk, size_t nprobe, const uint64_t* allow,
+                          uint32_t* ids, float* dd) -> int {
+    const vdbg_segment& g = segs[p];
+    const size_t rows = g.rows->d.n;
+    if (g.ivfpq != nullptr) {
+      VDBG_RETURN_IF_ERROR(vdbg_ivfpq_search_device(g.ivfpq, q, nq, kk, nprobe, P.rerank, allow,
+                                                    ids, dd, static_cast<uint64_t*>(dcb.p), s));
+      VDBG_HIP(hipMemcpyAsync(dch.data(), dcb.p, nq * 8, hipMemcpyDeviceToHost, s));
+      VDBG_HIP(hipStreamSynchronize(s));
+      if (dist_comps != nullptr)
+        for (size_t i = 0; i < nq; ++i) dist_comps[i] += dch[i];
+    } else if (g.sq8 != nullptr) {
+      // HnswSq8Index::search's depth rule (hnsw_index.cc:88), over every code
+      const size_t depth = P.rerank < 0 ? std::max(P.ef, kk) : size_t(P.rerank);
+      VDBG_RETURN_IF_ERROR(vdbg_sq8_search_device(g.sq8, q, nq, kk, depth, allow, ids, dd, s));
+      if (dist_comps != nullptr)
+        for (size_t i = 0; i < nq; ++i)
+          dist_comps[i] += rows + (depth > 0 ? std::min(std::max(depth, kk), rows) : 0);
+    } else {
+      VDBG_RETURN_IF_ERROR(vdbg_flat_search_device(g.rows, q, nq, kk, allow, ids, dd, s));
+      if (dist_comps != nullptr)
+        for (size_t i = 0; i < nq; ++i) dist_comps[i] += rows;  // flat_index.cc:75-76
+    }
+    return kOk;
+  };
+  // ExactOverBitmap (planner.cc:31-38): the exact scan of the allowed rows.
+  auto exact = [&](size_t p, const uint64_t* allow, uint32_t* ids, float* dd) -> int {
+    VDBG_RETURN_IF_ERROR(vdbg_flat_search_device(segs[p].rows, q, nq, k, allow, ids, dd, s));
+    if (dist_comps != nullptr)
+      for (size_t i = 0; i < nq; ++i) dist_comps[i] += plan[p].matches;
+    return kOk;
+  };
+
+  std::vector<uint32_t> hr, xr;
+  std::vector<float> hd, xd;
+  for (size_t p = 0; p < nseg; ++p) {
+    SegPlan& sp = plan[p];
+    uint32_t* ids = static_cast<uint32_t*>(hits_r.p) + p * slice;
+    float* dd = static_cast<float*>(hits_d.p) + p * slice;
+    const uint64_t* allow = sp.allow.empty() ? nullptr : static_cast<const uint64_t*>(allow_dev.p) + allow_at[p];
+    switch (sp.plan) {
+      case VDBG_PLAN_INDEX:
+        VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd));
+        break;
+      case VDBG_PLAN_EMPTY:
+        VDBG_HIP(hipMemsetAsync(ids, 0xff, slice * 4, s));
+        VDBG_HIP(hipMemsetAsync(dd, 0, slice * 4, s));
+        break;
+      case VDBG_PLAN_PREFILTER_EXACT:
+        VDBG_RETURN_IF_ERROR(exact(p, allow, ids, dd));
+        break;
+      case VDBG_PLAN_FILTERED_INDEX: {
+        VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd));
+        if (P.strategy != VDBG_STRATEGY_AUTO) break;
+        // :103-108: never fewer than min(k, matches) hits; the short queries take the exact
+        // scan of the allowed rows
+        hr.resize(slice);
+        VDBG_HIP(hipMemcpyAsync(hr.data(), ids, slice * 4, hipMemcpyDeviceToHost, s));
+        VDBG_HIP(hipStreamSynchronize(s));
+        const size_t want = std::min(k, sp.matches);
+        std::vector<size_t> shortq;
+        for (size_t i = 0; i < nq; ++i) {
+          size_t h = 0;
+          while (h < k && hr[i * k + h] != kNoId) ++h;
+          if (h < want) shortq.push_back(i);
+        }
+        if (shortq.empty()) break;
+        sp.plan = VDBG_PLAN_FILTERED_INDEX_EXACT_FALLBACK;
+        DevBuf xi, xdd;
+        VDBG_RETURN_IF_ERROR(Alloc(&xi, slice * 4, s));
+        VDBG_RETURN_IF_ERROR(Alloc(&xdd, slice * 4, s));
+        VDBG_RETURN_IF_ERROR(vdbg_flat_search_device(segs[p].rows, q, nq, k, allow,
+                                                     static_cast<uint32_t*>(xi.p),
+                                                     static_cast<float*>(xdd.p), s));
+        for (size_t i : shortq) {
+          VDBG_HIP(hipMemcpyAsync(ids + i * k, static_cast<uint32_t*>(xi.p) + i * k, k * 4,
+                                  hipMemcpyDeviceToDevice, s));
+          VDBG_HIP(hipMemcpyAsync(dd + i * k, static_cast<float*>(xdd.p) + i * k, k * 4,
+                                  hipMemcpyDeviceToDevice, s));
+          if (dist_comps != nullptr) dist_comps[i] += sp.matches;
+        }
+        VDBG_HIP(hipStreamSynchronize(s));  // xi / xdd are released on return
+        break;
+      }
+      case VDBG_PLAN_POST_FILTER: {
+        // :110-127: search k * alpha under the delete filter, keep the hits the filter allows
+        const vdbg_segment& g = segs[p];
+        const size_t rows = g.rows->d.n;
+        const size_t deleted = g.deleted_words ? CountRows(g.deleted_words, rows) : 0;
+        const size_t live = rows - std::min(rows, deleted);
+        const size_t kk = std::min(std::max<size_t>(live, 1), k * std::max<size_t>(1, P.post_filter_alpha));
+        std::vector<uint64_t> del_allow;
+        DevBuf da, wi, wd;
+        const uint64_t* dallow = nullptr;
+        if (deleted > 0) {
+          const size_t nw = (rows + 63) / 64;
+          del_allow.resize(nw);
+          for (size_t i = 0; i < nw; ++i) del_allow[i] = ~g.deleted_words[i];
+          VDBG_RETURN_IF_ERROR(Alloc(&da, nw * 8, s));
+          VDBG_HIP(hipMemcpyAsync(da.p, del_allow.data(), nw * 8, hipMemcpyHostToDevice, s));
+          dallow = static_cast<const uint64_t*>(da.p);
+        }
+        VDBG_RETURN_IF_ERROR(Alloc(&wi, nq * kk * 4, s));
+        VDBG_RETURN_IF_ERROR(Alloc(&wd, nq * kk * 4, s));
+        // ef raised to kk (:113-114) leaves the SQ8 depth max(ef, kk) as index_search sets it
+        VDBG_RETURN_IF_ERROR(index_search(p, kk, sp.nprobe, dallow, static_cast<uint32_t*>(wi.p),
+                                          static_cast<float*>(wd.p)));
+        hr.resize(nq * kk);
+        hd.resize(nq * kk);
+        VDBG_HIP(hipMemcpyAsync(hr.data(), wi.p, nq * kk * 4, hipMemcpyDeviceToHost, s));
+        VDBG_HIP(hipMemcpyAsync(hd.data(), wd.p, nq * kk * 4, hipMemcpyDeviceToHost, s));
+        VDBG_HIP(hipStreamSynchronize(s));
+        xr.assign(slice, kNoId);
+        xd.assign(slice, __builtin_inff());
+        for (size_t i = 0; i < nq; ++i) {
+          size_t out = 0;
+          for (size_t j = 0; j < kk && out < k; ++j) {
+            const uint32_t r = hr[i * kk + j];
+            if (r == kNoId) break;
+            if ((sp.allow[r >> 6] >> (r & 63)) & 1u) {
+              xr[i * k + out] = r;
+              xd[i * k + out] = hd[i * kk + j];
+              ++out;
+            }
+          }
+        }
+        VDBG_HIP(hipMemcpyAsync(ids, xr.data(), slice * 4, hipMemcpyHostToDevice, s));
+        VDBG_HIP(hipMemcpyAsync(dd, xd.data(), slice * 4, hipMemcpyHostToDevice, s));
+        VDBG_HIP(hipStreamSynchronize(s));
+        break;
+      }
+      default:
+        return SetError(kInternal, "bad plan");
+    }
+  }
+
+  // ---- the merge (collection_impl.cc:1076-1112) and the copy back
+  std::vector<const uint64_t*> ext(np, nullptr);
+  for (size_t p = 0; p < nseg; ++p) ext[p] = segs[p].rows->d.ext_ids;
+  VDBG_RETURN_IF_ERROR(Alloc(&extp, np * sizeof(void*), s));
+  VDBG_RETURN_IF_ERROR(Alloc(&oe, slice * 8, s));
+  VDBG_RETURN_IF_ERROR(Alloc(&od, slice * 4, s));
+  VDBG_HIP(hipMemcpyAsync(extp.p, ext.data(), np * sizeof(void*), hipMemcpyHostToDevice, s));
+  if (nseg == 0) {
+    VDBG_HIP(hipMemsetAsync(hits_r.p, 0xff, slice * 4, s));
+    VDBG_HIP(hipMemsetAsync(hits_d.p, 0, slice * 4, s));
+  }
+  MergeArgs a{int(nq), int(np), int(k), static_cast<const float*>(hits_d.p),
+              static_cast<const uint32_t*>(hits_r.p), nullptr, nullptr,
+              static_cast<uint64_t*>(oe.p), static_cast<float*>(od.p)};
+  a.ext_parts = static_cast<const uint64_t* const*>(extp.p);
+  VDBG_RETURN_IF_ERROR(MergeParts(c, a, s));
+  VDBG_HIP(hipMemcpyAsync(out_ids, oe.p, slice * 8, hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipMemcpyAsync(out_dists, od.p, slice * 4, hipMemcpyDeviceToHost, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  if (seg_plans != nullptr)
+    for (size_t p = 0; p < nseg; ++p) seg_plans[p] = plan[p].plan;
+  return kOk;
+}
+
+}  // extern "C"

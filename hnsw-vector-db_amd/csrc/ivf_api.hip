@@ -38,25 +38,6 @@ int IvfQtab(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int
 int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s);
 int IvfScanDeep(Ctx* c, const IvfScanArgs& a, hipStream_t s);
 
-// Index::save / LoadIndex framing (src/index/index.cc:38-56, 110-128): magic, body, CRC32C
-// (reflected Castagnoli polynomial 0x82F63B78) of everything before the 4-byte footer.
-uint32_t Crc32c(const void* data, size_t n) {
-  static uint32_t table[256];
-  static bool init = false;
-  if (!init) {
-    for (uint32_t i = 0; i < 256; ++i) {
-      uint32_t c = i;
-      for (int b = 0; b < 8; ++b) c = (c >> 1) ^ (0x82F63B78u & (0u - (c & 1u)));
-      table[i] = c;
-    }
-    init = true;
-  }
-  const uint8_t* p = static_cast<const uint8_t*>(data);
-  uint32_t c = 0xffffffffu;
-  for (size_t i = 0; i < n; ++i) c = table[(c ^ p[i]) & 0xffu] ^ (c >> 8);
-  return ~c;
-}
-
 namespace {
 
 struct Reader {

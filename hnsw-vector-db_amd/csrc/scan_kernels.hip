@@ -251,7 +251,8 @@ __global__ void k_sq8_finish(const MinMax* __restrict__ part, int nblocks, int d
 
 // Sq8Quantizer::encode (sq8.cc:28-37), one wave per row: IEEE divide, rintf (round half to
 // even = std::nearbyint in the default mode), clamp to [0, 255]; padding dims and
-// scale <= 0 give 0.  Also ||c * scale||^2, the row norm of the GEMM form.
+// scale <= 0 give 0.  Also ||c * scale||^2, the row norm of the GEMM form.  With X null the
+// codes are given (an index file's) and only their norms are computed.
 __global__ __launch_bounds__(256) void k_sq8_encode(const float* __restrict__ X, uint32_t n,
                                                     int dim, int pd,
                                                     const float* __restrict__ vmin,
@@ -260,17 +261,21 @@ __global__ __launch_bounds__(256) void k_sq8_encode(const float* __restrict__ X,
                                                     float* __restrict__ yn) {
   const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= n) return;
-  const float* x = X + size_t(r) * pd;
+  const float* x = X == nullptr ? nullptr : X + size_t(r) * pd;
   uint8_t* c = codes + size_t(r) * pd;
   float s = 0.f;
   for (int i = lane_id(); i < pd; i += kWave) {
     uint8_t code = 0;
-    if (i < dim && scale[i] > 0.f) {
-      const float v = rintf((x[i] - vmin[i]) / scale[i]);
-      const float cl = v < 0.f ? 0.f : (255.f < v ? 255.f : v);
-      code = uint8_t(cl);
+    if (X == nullptr) {
+      code = c[i];  // codes read from an index file: only their norms are computed
+    } else {
+      if (i < dim && scale[i] > 0.f) {
+        const float v = rintf((x[i] - vmin[i]) / scale[i]);
+        const float cl = v < 0.f ? 0.f : (255.f < v ? 255.f : v);
+        code = uint8_t(cl);
+      }
+      c[i] = code;
     }
-    c[i] = code;
     const float y = float(code) * scale[i];
     s = fmaf(y, y, s);
   }
@@ -297,11 +302,12 @@ int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipSt
 }
 
 int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
-              uint8_t* codes, float* yn, hipStream_t s) {
+              uint8_t* codes, float* yn, hipStream_t s, bool codes_given) {
   const uint32_t n = uint32_t(ds->n);
   if (n == 0) return kOk;
   ProfScope ps(c, "sq8_encode", s);
-  k_sq8_encode<<<dim3((n + 3) / 4), 256, 0, s>>>(ds->rows, n, int(ds->dim), int(ds->pd),
+  k_sq8_encode<<<dim3((n + 3) / 4), 256, 0, s>>>(codes_given ? nullptr : ds->rows, n,
+                                                 int(ds->dim), int(ds->pd),
                                                  vmin_dev, scale_dev, codes, yn);
   VDBG_HIP(hipGetLastError());
   return kOk;

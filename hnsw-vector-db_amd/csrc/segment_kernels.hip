@@ -253,15 +253,11 @@ int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, i
 
 // ---------------------------------------------------------------- merge
 
-struct MergeArgs {
-  int nq, nparts, k;
-  const float* part_d;        // [nparts][nq][k]
-  const uint32_t* part_rows;  // [nparts][nq][k], UINT32_MAX padded
-  const uint64_t* ext;        // external ids, part p row r at ext[part_off[p] + r]
-  const uint64_t* part_off;
-  uint64_t* out_ext;          // [nq][k], UINT64_MAX padded
-  float* out_d;
-};
+// External id of row `row` of part p: from the per-part device tables when given, else from
+// the concatenated table.
+__device__ __forceinline__ uint64_t ext_of(const MergeArgs& a, uint32_t p, uint32_t row) {
+  return a.ext_parts != nullptr ? a.ext_parts[p][row] : a.ext[a.part_off[p] + row];
+}
 
 // One wave per query.  Candidate c = p * k + i (part p, i-th hit) keeps (dist, part, row)
 // order as the key (dist, c): a part's hits arrive sorted by (dist, row).
@@ -295,7 +291,7 @@ __global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
     if (r.id[e] != kNoId) {
       const int c = int(r.id[e]), p = c / a.k, i = c - p * a.k;
       const uint32_t row = a.part_rows[(size_t(p) * a.nq + q) * a.k + i];
-      v = a.ext[a.part_off[p] + row];
+      v = ext_of(a, uint32_t(p), row);
     }
     ex[e * kWave + lane] = v;
   }
@@ -364,7 +360,7 @@ __global__ void k_mext(MergeChunk m, const uint64_t* __restrict__ sorted,
     return;
   }
   const uint32_t cidx = uint32_t(key);
-  ext[t] = m.a.ext[m.a.part_off[m.part(cidx)] + m.a.part_rows[m.at(q, cidx)]];
+  ext[t] = ext_of(m.a, m.part(cidx), m.a.part_rows[m.at(q, cidx)]);
 }
 
 __global__ void k_mfirst(MergeChunk m, const uint64_t* __restrict__ sorted,
@@ -394,7 +390,7 @@ __global__ __launch_bounds__(256) void k_memit(MergeChunk m, const uint64_t* __r
     if (keep && pos < k) {
       const uint64_t key = sorted[size_t(q) * m.per + r];
       const uint32_t cidx = uint32_t(key);
-      m.a.out_ext[gq * k + pos] = m.a.ext[m.a.part_off[m.part(cidx)] + m.a.part_rows[m.at(q, cidx)]];
+      m.a.out_ext[gq * k + pos] = ext_of(m.a, m.part(cidx), m.a.part_rows[m.at(q, cidx)]);
       m.a.out_d[gq * k + pos] = key_dist(key);
     }
     written += __popcll(bal);

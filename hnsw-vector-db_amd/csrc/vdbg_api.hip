@@ -384,6 +384,18 @@ int vdbg_dataset_create(vdbg_ctx* ctx, const float* rows, size_t n, size_t dim,
   return CreateDataset(ctx, rows, false, n, dim, padded_dim, metric, out);
 }
 
+int vdbg_dataset_open_vectors(vdbg_ctx* ctx, const void* file, size_t len, size_t dim,
+                              int metric, uint64_t rows, int verify_crc, vdbg_dataset** out) {
+  if (ctx == nullptr || out == nullptr || (file == nullptr && len > 0))
+    return SetError(kInvalidArgument, "null argument");
+  if (dim == 0) return SetError(kInvalidArgument, "dim must be > 0");
+  if (metric < 0 || metric > 2) return SetError(kInvalidArgument, "unknown metric");
+  const float* data = nullptr;
+  uint64_t n = 0;
+  VDBG_RETURN_IF_ERROR(CheckSegmentVectors(file, len, dim, metric, rows, verify_crc, &data, &n));
+  return CreateDataset(ctx, data, false, size_t(n), dim, (dim + 15) / 16 * 16, metric, out);
+}
+
 int vdbg_dataset_create_device(vdbg_ctx* ctx, const float* rows_dev, size_t n, size_t dim,
                                size_t padded_dim, int metric, vdbg_dataset** out) {
   return CreateDataset(ctx, rows_dev, true, n, dim, padded_dim, metric, out);
@@ -402,6 +414,7 @@ int vdbg_dataset_destroy(vdbg_dataset* ds) {
   (void)hipFree(ds->d.rows);
   (void)hipFree(ds->d.norms);
   if (ds->d.rows16 != nullptr) (void)hipFree(ds->d.rows16);
+  if (ds->d.ext_ids != nullptr) (void)hipFree(ds->d.ext_ids);
   delete ds;
   return kOk;
 }
@@ -464,9 +477,10 @@ int vdbg_sq8_train(vdbg_dataset* ds, float* vmin_out, float* scale_out) {
   return rc;
 }
 
-int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdbg_sq8** out) {
-  if (ds == nullptr || vmin == nullptr || scale == nullptr || out == nullptr)
-    return SetError(kInvalidArgument, "null argument");
+// vdbg_sq8_create (codes == nullptr: encode the rows) and vdbg_sq8_load (codes: an index
+// file's n x pd code bytes on the host, uploaded as they are).
+static int CreateSq8(vdbg_dataset* ds, const float* vmin, const float* scale,
+                     const uint8_t* codes, vdbg_sq8** out) {
   Ctx* c = ds->d.ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
@@ -496,8 +510,10 @@ int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdb
   x.scale = x.vmin + pd;
   e = hipMemcpyAsync(x.vmin, vmin, pd * 4, hipMemcpyHostToDevice, s);
   if (e == hipSuccess) e = hipMemcpyAsync(x.scale, scale, pd * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && codes != nullptr && n > 0)
+    e = hipMemcpyAsync(x.codes, codes, n * pd, hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return fail(SetError(kInternal, hipGetErrorString(e)));
-  int rc = Sq8Encode(c, &d, x.vmin, x.scale, x.codes, x.yn, s);
+  int rc = Sq8Encode(c, &d, x.vmin, x.scale, x.codes, x.yn, s, codes != nullptr);
   if (rc != kOk) return fail(rc);
   // magnitude term of the rounding bound: max ||code*scale||^2, a bound on the decoded
   // row norm, and ||vmin||^2
@@ -530,6 +546,50 @@ int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdb
   ++d.live_indexes;
   *out = h;
   return kOk;
+}
+
+int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdbg_sq8** out) {
+  if (ds == nullptr || vmin == nullptr || scale == nullptr || out == nullptr)
+    return SetError(kInvalidArgument, "null argument");
+  return CreateSq8(ds, vmin, scale, nullptr, out);
+}
+
+// LoadIndex's framing check (src/index/index.cc:47-56) and HnswSq8Index::load
+// (src/index/hnsw/hnsw_index.cc:117-129) up to the graph: u64 rows, the serialised
+// Sq8Quantizer (src/index/quant/sq8.cc:43-63: u32 dim, u32 padded dim, vmin, scale), then
+// rows x padded_dim code bytes.  The graph that follows is not read: the device scans every
+// code.
+int vdbg_sq8_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_sq8** out) {
+  if (ds == nullptr || out == nullptr || (file == nullptr && len > 0))
+    return SetError(kInvalidArgument, "null argument");
+  const auto* b = static_cast<const uint8_t*>(file);
+  if (len < 12) return SetError(VDBG_CORRUPTION, "index file too short");
+  uint32_t stored;
+  std::memcpy(&stored, b + len - 4, 4);
+  if (Crc32c(b, len - 4) != stored) return SetError(VDBG_CORRUPTION, "index file checksum mismatch");
+  if (std::memcmp(b, "VDBHSQ81", 8) != 0)
+    return SetError(VDBG_CORRUPTION, "not an hnsw-sq8 index file (magic VDBHSQ81)");
+  const uint8_t* p = b + 8;
+  size_t left = len - 12;
+  auto take = [&](void* dst, size_t n) {
+    if (left < n) return false;
+    if (dst != nullptr) std::memcpy(dst, p, n);
+    p += n;
+    left -= n;
+    return true;
+  };
+  const Dataset& d = ds->d;
+  uint64_t n = 0;
+  uint32_t qd = 0, qp = 0;
+  if (!take(&n, 8) || n != d.n || !take(&qd, 4) || !take(&qp, 4) || qd > qp || qp % 16 != 0 ||
+      qp != d.pd)
+    return SetError(VDBG_CORRUPTION, "hnsw-sq8 index does not match the segment");
+  std::vector<float> vmin(qp), scale(qp);
+  if (!take(vmin.data(), qp * 4) || !take(scale.data(), qp * 4))
+    return SetError(VDBG_CORRUPTION, "hnsw-sq8 index does not match the segment");
+  const uint8_t* codes = p;
+  if (!take(nullptr, size_t(n) * d.pd)) return SetError(VDBG_CORRUPTION, "truncated sq8 codes");
+  return CreateSq8(ds, vmin.data(), scale.data(), codes, out);
 }
 
 int vdbg_sq8_destroy(vdbg_sq8* sq) {

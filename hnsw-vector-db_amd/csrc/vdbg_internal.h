@@ -27,6 +27,13 @@ enum Code : int {
 int SetError(int code, const std::string& msg);  // records the thread's message, returns code
 int BestHostKernelSet();  // the host CPU's best distance kernel set (host_cpu.cc)
 
+// File formats (files.cc): CRC32C of every vdb file, and Segment::Open's vectors.f32 checks
+// (src/storage/segment_reader.cc:37-55); *data is the first row, *rows the header's count.
+uint32_t Crc32c(const void* data, size_t n);
+int CheckSegmentVectors(const void* file, size_t len, size_t dim, int metric,
+                        uint64_t expect_rows, int verify_crc, const float** data,
+                        uint64_t* rows);
+
 #define VDBG_HIP(expr)                                                                  \
   do {                                                                                  \
     hipError_t e_ = (expr);                                                             \
@@ -130,6 +137,7 @@ struct Dataset {
   RowStats stats;
   ScanSource src;          // the flat scan's view of these rows
   int live_indexes = 0;    // SQ8 / IVF-PQ indexes over these rows not yet destroyed (ctx mu)
+  uint64_t* ext_ids = nullptr;  // n external ids (device) for the collection merge, or null
 };
 
 // SQ8 codes of a dataset's rows (HnswSq8Index's codes_ and Sq8Quantizer,
@@ -198,7 +206,7 @@ int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq
            hipStream_t s);
 int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipStream_t s);
 int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
-              uint8_t* codes, float* yn, hipStream_t s);
+              uint8_t* codes, float* yn, hipStream_t s, bool codes_given = false);
 // Top-kk for kk beyond the wave kernels (up to 10,000): exact distance of every allowed row
 // per query, segmented sort.
 int ExactScanAll(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t kk,
@@ -212,6 +220,23 @@ int RerankLarge(Ctx* c, const float* X, int pd, int metric, const float* Q, size
 int SortSegmentsTopK(Ctx* c, uint64_t* keys, uint64_t* keys_alt, const int* off_dev, int nseg,
                      int total, int K, uint32_t* out_ids, float* out_d, hipStream_t s);
 // RunScan under an optional filter; compacts the allowed rows when they are few.
+// CollectionImpl::Search's merge (segment_kernels.hip): hits of every part ordered by
+// (dist, part, row), first hit of each external id kept.
+struct MergeArgs {
+  int nq, nparts, k;
+  const float* part_d;        // [nparts][nq][k]
+  const uint32_t* part_rows;  // [nparts][nq][k], UINT32_MAX padded
+  const uint64_t* ext;        // external ids, part p row r at ext[part_off[p] + r]
+  const uint64_t* part_off;
+  uint64_t* out_ext;          // [nq][k], UINT64_MAX padded
+  float* out_d;
+  const uint64_t* const* ext_parts = nullptr;  // or row r of part p at ext_parts[p][r]
+};
+int MergeParts(Ctx* c, const MergeArgs& a, hipStream_t s);
+// PrepareQuery + NormalizeVector for nq raw queries into padded rows; waits for the result
+// (a query with a non-finite value, or a zero query under cosine, is InvalidArgument).
+int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
+                   float* out, hipStream_t s);
 int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
 int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);

@@ -65,6 +65,16 @@ _SIGS = {
     "vdbg_dataset_create": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, C.POINTER(_vp)]),
     "vdbg_dataset_create_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int,
                                              C.POINTER(_vp)]),
+    "vdbg_dataset_open_vectors": (C.c_int, [_vp, C.c_char_p, _sz, _sz, C.c_int, C.c_uint64,
+                                            C.c_int, C.POINTER(_vp)]),
+    "vdbg_crc32c_extend": (C.c_uint32, [C.c_uint32, C.c_char_p, _sz]),
+    "vdbg_blob_decode": (C.c_int, [C.c_char_p, _sz, C.c_char_p, C.POINTER(_sz),
+                                   C.POINTER(_sz)]),
+    "vdbg_deletes_decode": (C.c_int, [C.c_char_p, _sz, _sz, _vp, C.POINTER(C.c_uint64)]),
+    "vdbg_sq8_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
+    "vdbg_dataset_set_external_ids": (C.c_int, [_vp, _vp]),
+    "vdbg_collection_search_host": (C.c_int, [_vp, _vp, _sz, _sz, C.c_int, _vp, _sz, _sz, _vp,
+                                              _vp, _vp, _vp, _vp]),
     "vdbg_dataset_destroy": (C.c_int, [_vp]),
     "vdbg_dataset_rows": (_vp, [_vp]),
     "vdbg_flat_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp,
@@ -221,6 +231,24 @@ class Dataset:
         ctx._children.add(self)
         return self
 
+    @classmethod
+    def open_vectors(cls, ctx, data, dim, metric="l2", rows=None, verify_crc=True):
+        """A segment's vectors.f32 file (bytes) made resident, checked as Segment::Open
+        checks it; rows = the manifest's row count (None: the header's)."""
+        data = bytes(data)
+        self = cls.__new__(cls)
+        h = _vp()
+        _check(lib.vdbg_dataset_open_vectors(ctx.h, data, len(data), dim, METRICS[metric],
+                                             2**64 - 1 if rows is None else rows,
+                                             1 if verify_crc else 0, C.byref(h)))
+        pd = padded_dim(dim)
+        self.ctx, self.h, self.dim, self.pd = ctx, h, dim, pd
+        self.n = int.from_bytes(data[16:24], "little")
+        self.metric = metric
+        self._children = weakref.WeakSet()
+        ctx._children.add(self)
+        return self
+
     def close(self):
         if self.h:
             for ch in list(self._children):
@@ -233,6 +261,12 @@ class Dataset:
             self.close()
         except Exception:
             pass
+
+    def set_external_ids(self, ids):
+        """The segment's external ids (ids.u64), resident for collection_search."""
+        ids = np.ascontiguousarray(ids, np.uint64)
+        assert ids.shape == (self.n,)
+        _check(lib.vdbg_dataset_set_external_ids(self.h, _ptr(ids)))
 
     def flat_search(self, queries, k, allow=None):
         """Host arrays in and out: (ids uint32 [nq, k], dists float32 [nq, k])."""
@@ -281,6 +315,22 @@ class Sq8Index:
         _check(lib.vdbg_sq8_create(ds.h, _ptr(self.vmin), _ptr(self.scale), C.byref(h)))
         self.ds, self.h = ds, h
         ds._children.add(self)
+
+    @classmethod
+    def load(cls, ds, data):
+        """A segment's VDBHSQ81 index file (bytes): quantizer and codes made resident as
+        they are."""
+        data = bytes(data)
+        self = cls.__new__(cls)
+        h = _vp()
+        _check(lib.vdbg_sq8_load(ds.h, data, len(data), C.byref(h)))
+        q = np.frombuffer(data, np.uint8)
+        pd = ds.pd
+        self.vmin = q[24:24 + 4 * pd].view(np.float32).copy()
+        self.scale = q[24 + 4 * pd:24 + 8 * pd].view(np.float32).copy()
+        self.ds, self.h = ds, h
+        ds._children.add(self)
+        return self
 
     def close(self):
         if self.h:
@@ -393,6 +443,81 @@ class IvfPqIndex:
                       dc_ptr=None, stream=None):
         _check(lib.vdbg_ivfpq_search_device(self.h, q_ptr, nq, k, nprobe, rerank, allow_ptr,
                                             ids_ptr, dists_ptr, dc_ptr, stream))
+
+
+class SearchParams(C.Structure):
+    """SearchParams (include/vdb/options.h:59-67), vdbg_search_params."""
+    _fields_ = [("ef", _sz), ("nprobe", _sz), ("rerank", C.c_int), ("strategy", C.c_int),
+                ("prefilter_threshold", _sz), ("post_filter_alpha", _sz)]
+
+    def __init__(self, ef=64, nprobe=16, rerank=-1, strategy="auto", prefilter_threshold=10000,
+                 post_filter_alpha=10):
+        super().__init__(ef, nprobe, rerank, STRATEGIES[strategy], prefilter_threshold,
+                         post_filter_alpha)
+
+
+STRATEGIES = {"auto": 0, "prefilter": 1, "graph": 2, "post_filter": 3}
+PLANS = ["index", "empty", "prefilter_exact", "filtered_index",
+         "filtered_index+exact_fallback", "post_filter"]
+
+
+class _Segment(C.Structure):
+    _fields_ = [("rows", _vp), ("sq8", _vp), ("ivfpq", _vp), ("deleted_words", _vp),
+                ("filter_words", _vp)]
+
+
+def collection_search(ctx, segments, dim, metric, queries, k, params=None):
+    """CollectionImpl::SearchBatch over disk segments (vdbg_collection_search_host).
+    segments: (dataset, index or None, deleted words or None, filter words or None) per
+    segment, each dataset with its external ids set.  Returns (external ids uint64 [nq, k],
+    dists float32 [nq, k], distance computations per query, plan name per segment)."""
+    params = params or SearchParams()
+    q = np.ascontiguousarray(queries, np.float32)
+    nq = q.shape[0]
+    assert q.shape[1] == dim
+    keep = []
+    arr = (_Segment * max(len(segments), 1))()
+    for i, (ds, ix, deleted, filt) in enumerate(segments):
+        sq = ix.h if isinstance(ix, Sq8Index) else None
+        iv = ix.h if isinstance(ix, IvfPqIndex) else None
+        dw = None if deleted is None else np.ascontiguousarray(deleted, np.uint64)
+        fw = None if filt is None else np.ascontiguousarray(filt, np.uint64)
+        keep += [dw, fw]
+        arr[i] = _Segment(ds.h, sq, iv, None if dw is None else dw.ctypes.data,
+                          None if fw is None else fw.ctypes.data)
+    ids = np.empty((nq, k), np.uint64)
+    d = np.empty((nq, k), np.float32)
+    dc = np.empty(nq, np.uint64)
+    plans = np.empty(max(len(segments), 1), np.int32)
+    _check(lib.vdbg_collection_search_host(ctx.h, C.cast(arr, _vp), len(segments), dim,
+                                           METRICS[metric], _ptr(q), nq, k, C.byref(params),
+                                           _ptr(ids), _ptr(d), _ptr(dc), _ptr(plans)))
+    return ids, d, dc, [PLANS[p] for p in plans[:len(segments)]]
+
+
+def crc32c(data, crc=0):
+    """crc32c::Extend (src/util/crc32c.h:9-13)."""
+    data = bytes(data)
+    return int(lib.vdbg_crc32c_extend(crc, data, len(data)))
+
+
+def blob_payload(data, magic):
+    """DecodeBlob (src/storage/file_format.cc:21-33): the checked payload of a blob file."""
+    data = bytes(data)
+    off, n = _sz(), _sz()
+    _check(lib.vdbg_blob_decode(data, len(data), magic.encode(), C.byref(off), C.byref(n)))
+    return data[off.value:off.value + n.value]
+
+
+def decode_deletes(data, rows):
+    """A deletes-<n>.roar blob file as dense words (bit r set = row r deleted) and the
+    number of deleted rows."""
+    data = bytes(data)
+    words = np.zeros((rows + 63) // 64, np.uint64)
+    count = C.c_uint64()
+    _check(lib.vdbg_deletes_decode(data, len(data), rows, _ptr(words) if rows else None,
+                                   C.byref(count)))
+    return words, int(count.value)
 
 
 def kmeans(ctx, data, k, iters=25, seed=1234, max_points=256, kmeanspp=True, d=None):

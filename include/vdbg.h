@@ -117,6 +117,36 @@ int vdbg_dataset_destroy(vdbg_dataset* ds);
 /* Device pointer to the resident rows (n x padded_dim floats). */
 const float* vdbg_dataset_rows(vdbg_dataset* ds);
 
+/* ---------------------------------------------------------------- segment files */
+
+/* Segment::Open's read of vectors.f32 (src/storage/segment_reader.cc:37-59): the 4 KiB header
+ * (magic VDBSEG01, CRC32C of bytes 0..4091 at 4092, version 1, metric, rows, dim, padded
+ * dim, data offset 4096, data length rows x padded_dim x 4; src/storage/segment.h:9-12,
+ * segment_writer.cc:58-75) is checked as :41-52 checks it, the data CRC32C when verify_crc
+ * (:53-55), and the rows become a resident dataset, as vdbg_dataset_create.  file/len: the
+ * file's bytes (e.g. its mmap).  rows: the manifest's row count, or UINT64_MAX to take the
+ * header's.  Errors: 5 (corruption) with the reference's messages. */
+int vdbg_dataset_open_vectors(vdbg_ctx* ctx, const void* file, size_t len, size_t dim,
+                              int metric, uint64_t rows, int verify_crc, vdbg_dataset** out);
+/* crc32c::Extend (src/util/crc32c.h:9-13): CRC32C (Castagnoli) of n bytes continuing crc
+ * (0 to start).  Host-only. */
+uint32_t vdbg_crc32c_extend(uint32_t crc, const void* data, size_t n);
+/* DecodeBlob (src/storage/file_format.cc:21-33): checks a blob file ([magic 8][u32 version 1]
+ * [u32 CRC32C of the payload][u64 payload length][payload], file_format.h:3-4), e.g. ids.u64
+ * (magic "VDBIDS01") or a delete set ("VDBDEL01"); the payload is file[*payload_offset ..
+ * + *payload_len).  Errors: 5 with the reference's messages.  Host-only. */
+int vdbg_blob_decode(const void* file, size_t len, const char* magic, size_t* payload_offset,
+                     size_t* payload_len);
+/* The delete-set read of Segment::Open (segment_reader.cc:102-117): a deletes-<n>.roar blob
+ * file whose payload is a roaring bitmap in the portable serialization
+ * (segment_writer.cc:29-39), expanded into deleted_words[ceil(rows/64)] (bit r of word r/64
+ * set = row r deleted, the DeleteBits layout of src/util/delete_bits.h:50-55); *count
+ * (nullable) receives the number of deleted rows.  A row >= rows is corruption ("delete set
+ * out of range", :111).  The complement of the words is the DeleteFilter the searches take.
+ * Host-only. */
+int vdbg_deletes_decode(const void* file, size_t len, size_t rows, uint64_t* deleted_words,
+                        uint64_t* count);
+
 /* ---------------------------------------------------------------- flat exact search */
 
 /* Exact top-k for nq queries: FlatIndex::search (src/index/flat_index.cc:73-77, which is
@@ -145,6 +175,12 @@ int vdbg_sq8_train(vdbg_dataset* ds, float* vmin_out, float* scale_out);
  * 66-79) without the graph.  vmin/scale are padded_dim floats (host), e.g. from
  * vdbg_sq8_train or a deserialised quantizer (sq8.cc:43-63). */
 int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdbg_sq8** out);
+/* LoadIndex (src/index/index.cc:38-87) of a VDBHSQ81 file, the HNSW-SQ8 index of a segment
+ * (hnsw_index.cc:108-129): CRC32C footer, then rows, the Sq8Quantizer and the codes are read
+ * and made resident as they are (no re-encoding); the graph that follows is not read, since
+ * the device scans every code.  `ds` is the segment the index belongs to (rows and
+ * padded_dim must match).  Errors: 5 (corruption) for a bad file. */
+int vdbg_sq8_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_sq8** out);
 int vdbg_sq8_destroy(vdbg_sq8* sq);
 /* Copies the n x padded_dim code bytes to the host. */
 int vdbg_sq8_codes(vdbg_sq8* sq, uint8_t* codes_out);
@@ -269,6 +305,72 @@ int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
  * and every partial sum stays below 2^24, so its values equal the fp32 GEMM's bit for bit),
  * or 0 (no GEMM: the exact scan ran). */
 int vdbg_last_gemm_bits(vdbg_ctx* ctx);
+
+/* ---------------------------------------------------------------- collection search */
+
+/* One disk segment of a collection snapshot as CollectionImpl::Search reads it
+ * (src/engine/collection_impl.cc:1050-1064, src/storage/segment.h:56-79). */
+typedef struct vdbg_segment {
+  vdbg_dataset* rows;             /* the segment's rows, external ids set with
+                                     vdbg_dataset_set_external_ids */
+  vdbg_sq8* sq8;                  /* the segment's index: HNSW-SQ8 codes (scanned in full), */
+  vdbg_ivfpq* ivfpq;              /* or IVF-PQ lists; both NULL = a flat index */
+  const uint64_t* deleted_words;  /* host, nullable: DeleteBits words, ceil(rows/64) */
+  const uint64_t* filter_words;   /* host, nullable: the request's filter evaluated on this
+                                     segment (SegmentColumns::Evaluate, planner.cc:64) as
+                                     words; NULL = the request has no filter */
+} vdbg_segment;
+
+/* FilterStrategy (include/vdb/options.h:57). */
+enum {
+  VDBG_STRATEGY_AUTO = 0,
+  VDBG_STRATEGY_PREFILTER = 1,
+  VDBG_STRATEGY_GRAPH = 2,
+  VDBG_STRATEGY_POST_FILTER = 3
+};
+
+/* SearchParams (include/vdb/options.h:59-67). */
+typedef struct vdbg_search_params {
+  size_t ef;                   /* 64 */
+  size_t nprobe;               /* 16 */
+  int rerank;                  /* -1 = auto, 0 = none */
+  int strategy;                /* VDBG_STRATEGY_*, AUTO */
+  size_t prefilter_threshold;  /* 10000 */
+  size_t post_filter_alpha;    /* 10 */
+} vdbg_search_params;
+
+/* The per-segment plans of SearchDiskSegment (planner.cc:53-128), its SegmentExplain
+ * strategies "index", "empty", "prefilter_exact", "filtered_index",
+ * "filtered_index+exact_fallback" (some query of the batch fell back) and "post_filter". */
+enum {
+  VDBG_PLAN_INDEX = 0,
+  VDBG_PLAN_EMPTY = 1,
+  VDBG_PLAN_PREFILTER_EXACT = 2,
+  VDBG_PLAN_FILTERED_INDEX = 3,
+  VDBG_PLAN_FILTERED_INDEX_EXACT_FALLBACK = 4,
+  VDBG_PLAN_POST_FILTER = 5
+};
+
+/* Makes the segment's external ids (ids.u64, n entries, host) resident for the collection
+ * merge; replaces earlier ones. */
+int vdbg_dataset_set_external_ids(vdbg_dataset* ds, const uint64_t* ids);
+
+/* CollectionImpl::SearchBatch (collection_impl.cc:1121-1135) over the disk segments of a
+ * snapshot, in the snapshot's order: PrepareQuery for each raw query (nq x dim, host;
+ * :1023-1034; a non-finite value or a zero cosine query fails the batch with 1), each
+ * segment searched with SearchDiskSegment's plan (planner.cc:42-129: no filter -> the index
+ * under the delete filter; a filter -> matches = filter minus deletes, then empty,
+ * prefilter_exact, filtered_index with nprobe / selectivity and the exact fallback for
+ * queries short of min(k, matches), or post_filter), and the merge by (dist, part, row)
+ * keeping the first hit of each external id (:1076-1112).  Outputs [nq][k]: external ids
+ * (UINT64_MAX padded) and distances (+inf padded; the score is the distance for L2 and its
+ * negation otherwise).  dist_comps (nullable, nq) receives each query's distance
+ * computations; seg_plans (nullable, nseg) each segment's VDBG_PLAN_*.  k must be in
+ * 1..10000 (:1038-1039).  Host pointers; blocks until the results are on the host. */
+int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
+                                size_t dim, int metric, const float* queries, size_t nq,
+                                size_t k, const vdbg_search_params* params, uint64_t* out_ids,
+                                float* out_dists, uint64_t* dist_comps, int* seg_plans);
 
 #ifdef __cplusplus
 }

@@ -19,6 +19,7 @@
 
 #include "distance/distance.h"
 #include "index/flat_index.h"
+#include "index/hnsw/hnsw_index.h"
 #include "index/index.h"
 #include "index/quant/ivf_pq.h"
 #include "index/quant/kmeans.h"
@@ -167,6 +168,25 @@ void ref_sq8_train_encode(const float* base, size_t rows, size_t dim, size_t pd,
   std::memcpy(scale, sq.scale(), pd * sizeof(float));
   if (codes != nullptr)
     for (size_t r = 0; r < rows; ++r) sq.encode(v.row(r), codes + r * pd);
+}
+
+// HnswSq8Index::build + save (src/index/hnsw/hnsw_index.cc:66-79, 108-115): the VDBHSQ81
+// file a segment of that index type holds.  Returns the file size; writes it when it fits
+// in cap bytes.
+size_t ref_hnsw_sq8_file(int metric, const float* base, size_t rows, size_t dim, size_t pd,
+                         size_t M, size_t ef_construction, uint64_t seed, char* buf, size_t cap) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::HnswSq8;
+  o.M = M;
+  o.ef_construction = ef_construction;
+  o.seed = seed;
+  HnswSq8Index idx(o, static_cast<Metric>(metric), v);
+  if (!idx.build(nullptr).ok()) return 0;
+  StringSink sink;
+  if (!idx.save(sink).ok()) return 0;
+  if (buf != nullptr && sink.s.size() <= cap) std::memcpy(buf, sink.s.data(), sink.s.size());
+  return sink.s.size();
 }
 
 // SQ8 scan + rerank composed from the reference's parts (Sq8 kernel into TopK, Rerank).

@@ -914,6 +914,36 @@ size_t or_merge_parts(size_t nparts, size_t k, const float* part_d, const uint32
   return out;
 }
 
+/* SearchDiskSegment's choice for one segment (src/engine/planner.cc:53-108): no filter ->
+ * the index (0); matches == 0 -> empty (1); the Auto cost model (:70-80: exact when matches
+ * <= prefilter_threshold, or <= 10 * max(ef, k) / selectivity, or the index is flat) ->
+ * prefilter_exact (2) or filtered_index (3) with nprobe raised to ceil(nprobe / selectivity)
+ * under Auto (:92-99); post_filter (5).  Selectivity = matches / live rows, floored at 1e-9. */
+int or_plan_segment(int has_filter, size_t rows, size_t deleted, size_t matches, int index_flat,
+                    int strategy, size_t ef, size_t k, size_t nprobe,
+                    size_t prefilter_threshold, size_t* nprobe_out) {
+  *nprobe_out = nprobe;
+  if (!has_filter) return 0;
+  const size_t live = rows - (deleted < rows ? deleted : rows);
+  const double sel = live == 0 ? 0.0 : (double)matches / (double)live;
+  const double s = sel > 1e-9 ? sel : 1e-9;
+  int strat = strategy;
+  if (strat == 0) {
+    const double graph_cost = 10.0 * (double)(ef > k ? ef : k) / s;
+    strat = (matches <= prefilter_threshold || (double)matches <= graph_cost || index_flat) ? 1 : 2;
+  }
+  if (matches == 0) return 1;
+  if (strat == 1) return 2;
+  if (strat == 2) {
+    if (strategy == 0) {
+      const size_t boosted = (size_t)ceil((double)nprobe / s);
+      *nprobe_out = boosted > nprobe ? boosted : nprobe;
+    }
+    return 3;
+  }
+  return 5;
+}
+
 /* ------------------------------------------------------------------ crc32c */
 
 /* CRC32C with the reflected Castagnoli polynomial 0x82F63B78 (src/util/crc32c.cc:14),

@@ -133,6 +133,13 @@ size_t or_merge_parts(size_t nparts, size_t k, const float* part_d, const uint32
                       const uint64_t* ext, const uint64_t* part_off, float* out_d,
                       uint64_t* out_ext);
 
+/* ---- the per-segment plan of SearchDiskSegment (src/engine/planner.cc:53-108) ----
+ * Returns 0 index, 1 empty, 2 prefilter_exact, 3 filtered_index, 5 post_filter;
+ * *nprobe_out is the probe count of the index search. */
+int or_plan_segment(int has_filter, size_t rows, size_t deleted, size_t matches, int index_flat,
+                    int strategy, size_t ef, size_t k, size_t nprobe,
+                    size_t prefilter_threshold, size_t* nprobe_out);
+
 /* ---- CRC32C (src/util/crc32c.cc) ---- */
 uint32_t or_crc32c(uint32_t crc, const void* data, size_t n);
 

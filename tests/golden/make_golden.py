@@ -6,7 +6,8 @@ Makefile).  Every expected output below is produced by the reference's functions
 src/index/index.cc, src/util/dataset.cc, src/util/crc32c.cc) on small seeded inputs; the
 fixtures are data only (.npz without pickles): inputs and expected outputs.
 
-    python3 tests/golden/make_golden.py
+    python3 tests/golden/make_golden.py            # every fixture
+    python3 tests/golden/make_golden.py segment    # segment.npz only
 """
 import ctypes as C
 import os
@@ -178,8 +179,39 @@ def main():
     crc = np.array([L.ref_crc32c(x, len(x)) for x in blobs], np.uint32)
     np.savez_compressed(os.path.join(HERE, "misc.npz"), norm_in=nv, norm_out=outn, norm_ok=okn,
                         crc_blob=np.frombuffer(blobs[2], np.uint8).copy(), crc=crc)
+    make_segment(L)
     print("golden fixtures written to", HERE)
 
 
+def make_segment(L):
+    """segment.npz: VDBHSQ81 files written by the reference's HnswSq8Index::build + save
+    (src/index/hnsw/hnsw_index.cc:66-79, 108-115) over seeded rows, and the quantizer and
+    codes Sq8Quantizer::train/encode give for the same rows."""
+    rng = np.random.default_rng(20260301)
+    out = {}
+    for tag, n, dim, metric in [("a", 700, 40, 0), ("b", 300, 32, 1)]:
+        pd = (dim + 15) // 16 * 16
+        base = np.zeros((n, pd), np.float32)
+        base[:, :dim] = rng.uniform(-3, 5, (n, dim)).astype(np.float32)
+        size = L.ref_hnsw_sq8_file(metric, base, n, dim, pd, 8, 40, 42, None, 0)
+        buf = C.create_string_buffer(size)
+        assert L.ref_hnsw_sq8_file(metric, base, n, dim, pd, 8, 40, 42, buf, size) == size
+        vmin = np.empty(pd, np.float32)
+        scale = np.empty(pd, np.float32)
+        codes = np.empty((n, pd), np.uint8)
+        L.ref_sq8_train_encode(base, n, dim, pd, vmin, scale, codes)
+        out[f"{tag}_rows"], out[f"{tag}_metric"] = base, np.int32(metric)
+        out[f"{tag}_dim"] = np.int32(dim)
+        out[f"{tag}_file"] = np.frombuffer(buf.raw, np.uint8).copy()
+        out[f"{tag}_vmin"], out[f"{tag}_scale"], out[f"{tag}_codes"] = vmin, scale, codes
+    np.savez_compressed(os.path.join(HERE, "segment.npz"), **out)
+
+
 if __name__ == "__main__":
-    main()
+    if sys.argv[1:] == ["segment"]:
+        ref = load_reference()
+        if ref is None:
+            sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+        make_segment(ref.lib)
+    else:
+        main()

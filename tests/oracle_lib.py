@@ -74,6 +74,8 @@ class Oracle:
               f32p, sz, sz, sz, C.c_int, _opt(u64p), f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "or_normalize", C.c_int, [f32p, sz])
         _sig(lib, "or_merge_parts", sz, [sz, sz, f32p, u32p, u64p, u64p, f32p, u64p])
+        _sig(lib, "or_plan_segment", C.c_int,
+             [C.c_int, sz, sz, sz, C.c_int, C.c_int, sz, sz, sz, sz, C.POINTER(C.c_size_t)])
         _sig(lib, "or_crc32c", C.c_uint32, [C.c_uint32, C.c_char_p, sz])
 
     # -- convenience wrappers (numpy in, numpy out)
@@ -114,6 +116,147 @@ class Oracle:
                                      scale, np.ascontiguousarray(queries, np.float32), nq, k,
                                      depth, allow, od, oi, threads)
         return od, oi
+
+
+    def ivfpq_search(self, ix, term2, base, queries, k, nprobe, rerank, metric="l2",
+                     allow=None, kset="avx512"):
+        """IvfPqIndex::search over an index parsed with ivf_file.parse_ivfpq."""
+        nq = len(queries)
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.uint32)
+        dc = np.empty(nq, np.uint64)
+        self.lib.or_ivfpq_search_batch(KSET[kset], METRIC[metric], np.ascontiguousarray(base),
+                                       ix["dim"], ix["pd"], ix["coarse"], ix["nlist"],
+                                       ix["pq_centroids"], ix["m"], ix["list_off"],
+                                       ix["list_ids"], ix["list_codes"], term2,
+                                       np.ascontiguousarray(queries, np.float32), nq, k,
+                                       nprobe, rerank, allow, od, oi, dc, 8)
+        return od, oi, dc
+
+    def collection_search(self, segments, dim, metric, raw, k, ef=64, nprobe=16, rerank=-1,
+                          strategy=0, prefilter_threshold=10000, post_filter_alpha=10):
+        """CollectionImpl::SearchBatch (src/engine/collection_impl.cc:1036-1135) over disk
+        segments, composed from the oracle's parts: PrepareQuery (:1023-1034, or_normalize),
+        each segment's plan (SearchDiskSegment, planner.cc:42-129: or_plan_segment, the
+        index searches, the exact fallback of :103-108, the post filter of :110-127), and
+        the merge (:1076-1112, or_merge_parts), one query at a time.
+
+        segments: dicts with base (n, pd) fp32, ext (n,) uint64, kind "flat" | "sq8" | "ivf",
+        deleted / filter (dense words or None); sq8: codes, vmin, scale; ivf: ix (parsed
+        VDBIVFP1) and term2 (or None).  Returns (ext ids, dists, dist comps, plan names)."""
+        nq = raw.shape[0]
+        pd = (dim + 15) // 16 * 16
+        q = np.zeros((nq, pd), np.float32)
+        q[:, :dim] = raw
+        if not np.isfinite(raw).all():
+            raise ValueError("query has a NaN or infinite value")
+        if metric == "cosine":
+            for i in range(nq):
+                if self.lib.or_normalize(q[i], dim) != 1:
+                    raise ValueError("a zero query cannot be normalized for cosine")
+        names = ["index", "empty", "prefilter_exact", "filtered_index",
+                 "filtered_index+exact_fallback", "post_filter"]
+
+        def count(words, n):
+            bits = np.unpackbits(np.ascontiguousarray(words, np.uint64).view(np.uint8),
+                                 bitorder="little")[:n]
+            return int(bits.sum())
+
+        def clip(words, n):
+            w = np.ascontiguousarray(words, np.uint64).copy()
+            if n % 64:
+                w[-1] &= np.uint64((1 << (n % 64)) - 1)
+            return w
+
+        np_ = len(segments)
+        pdist = np.full((max(np_, 1), nq, k), np.inf, np.float32)
+        prow = np.full((max(np_, 1), nq, k), 0xFFFFFFFF, np.uint32)
+        dcs = np.zeros(nq, np.uint64)
+        plans = []
+        for p, sg in enumerate(segments):
+            base = np.ascontiguousarray(sg["base"], np.float32)
+            n = base.shape[0]
+            deleted = sg.get("deleted")
+            filt = sg.get("filter")
+            ndel = 0 if deleted is None else count(deleted, n)
+            live = n - min(n, ndel)
+            del_allow = None if ndel == 0 else clip(~np.asarray(deleted, np.uint64), n)
+            bm, matches = None, 0
+            if filt is not None:
+                bm = np.asarray(filt, np.uint64).copy()
+                if ndel > 0:
+                    bm &= ~np.asarray(deleted, np.uint64)
+                bm = clip(bm, n)
+                matches = count(bm, n)
+            npb = C.c_size_t()
+            plan = self.lib.or_plan_segment(1 if filt is not None else 0, n, ndel, matches,
+                                            1 if sg["kind"] == "flat" else 0, strategy, ef, k,
+                                            nprobe, prefilter_threshold, C.byref(npb))
+
+            def index_search(kk, allow):
+                if sg["kind"] == "ivf":
+                    od, oi, dc = self.ivfpq_search(sg["ix"], sg["term2"], base, q, kk,
+                                                   npb.value, rerank, metric, allow)
+                    return od, oi, dc
+                if sg["kind"] == "sq8":
+                    depth = max(ef, kk) if rerank < 0 else rerank
+                    od, oi = self.sq8_search(base, sg["codes"], sg["vmin"], sg["scale"], q, kk,
+                                             depth, metric=metric, allow=allow)
+                    extra = min(max(depth, kk), n) if depth > 0 else 0
+                    return od, oi, np.full(nq, n + extra, np.uint64)
+                od, oi = self.flat_search(base, q, kk, metric=metric, allow=allow)
+                return od, oi, np.full(nq, n, np.uint64)
+
+            if plan == 0:
+                od, oi, dc = index_search(k, del_allow)
+            elif plan == 1:
+                od = np.full((nq, k), np.inf, np.float32)
+                oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
+                dc = np.zeros(nq, np.uint64)
+            elif plan == 2:
+                od, oi = self.flat_search(base, q, k, metric=metric, allow=bm)
+                dc = np.full(nq, matches, np.uint64)
+            elif plan == 3:
+                od, oi, dc = index_search(k, bm)
+                if strategy == 0:
+                    hits = (oi != 0xFFFFFFFF).sum(axis=1)
+                    short = np.nonzero(hits < min(k, matches))[0]
+                    if short.size:
+                        plan = 4
+                        xd, xi = self.flat_search(base, q, k, metric=metric, allow=bm)
+                        od[short], oi[short] = xd[short], xi[short]
+                        dc = dc.copy()
+                        dc[short] += np.uint64(matches)
+            else:
+                kk = min(max(live, 1), k * max(1, post_filter_alpha))
+                wd, wi, dc = index_search(kk, del_allow)
+                od = np.full((nq, k), np.inf, np.float32)
+                oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
+                for i in range(nq):
+                    out = 0
+                    for j in range(kk):
+                        r = int(wi[i, j])
+                        if r == 0xFFFFFFFF or out >= k:
+                            break
+                        if (int(bm[r >> 6]) >> (r & 63)) & 1:
+                            oi[i, out], od[i, out] = r, wd[i, j]
+                            out += 1
+            pdist[p], prow[p] = od, oi
+            dcs += dc.astype(np.uint64)
+            plans.append(names[plan])
+        ext = np.ascontiguousarray(np.concatenate([sg["ext"] for sg in segments])
+                                   if segments else np.zeros(1, np.uint64), np.uint64)
+        off = np.concatenate([[0], np.cumsum([sg["base"].shape[0] for sg in segments])[:-1]]
+                             ).astype(np.uint64) if segments else np.zeros(1, np.uint64)
+        oe = np.full((nq, k), np.iinfo(np.uint64).max, np.uint64)
+        odd = np.full((nq, k), np.inf, np.float32)
+        for i in range(nq):
+            e = np.empty(k, np.uint64)
+            dd = np.empty(k, np.float32)
+            cnt = self.lib.or_merge_parts(max(np_, 1), k, np.ascontiguousarray(pdist[:, i, :]),
+                                          np.ascontiguousarray(prow[:, i, :]), ext, off, dd, e)
+            oe[i, :cnt], odd[i, :cnt] = e[:cnt], dd[:cnt]
+        return oe, odd, dcs, plans
 
 
 class Reference:
@@ -158,6 +301,8 @@ class Reference:
               f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "ref_normalize", C.c_int, [f32p, sz])
         _sig(lib, "ref_crc32c", C.c_uint32, [C.c_char_p, sz])
+        _sig(lib, "ref_hnsw_sq8_file", sz,
+             [C.c_int, f32p, sz, sz, sz, sz, sz, C.c_uint64, C.c_void_p, sz])
         _sig(lib, "ref_filtered_collection_search", C.c_int,
              [C.c_int, C.c_void_p, C.c_void_p, sz, sz, sz, C.c_void_p, u64p, f32p, sz, sz,
               u64p, f32p, C.c_int])

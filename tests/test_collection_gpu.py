@@ -1,0 +1,207 @@
+"""The collection read path in one batch (vdbg_collection_search_host) against the oracle's
+composition of the same steps: CollectionImpl::SearchBatch / Search
+(src/engine/collection_impl.cc:1023-1135), SearchDiskSegment's plan per segment
+(src/engine/planner.cc:42-129) over flat, SQ8 and IVF-PQ segments with deletes and filters,
+and the merge by (dist, part, row) with one hit per external id.  External ids, distances,
+distance computations and the plan chosen for every segment must all agree."""
+import numpy as np
+import pytest
+
+import vdbg
+from ivf_file import parse_ivfpq, synth_ivfpq
+from vdbg import datagen
+
+pytestmark = pytest.mark.gpu
+
+DIM = 64
+FAR = 6000  # rows of the IVF-PQ segment in the far cluster
+
+
+def _mask(n, frac, seed):
+    bits = np.random.default_rng(seed).random(n) < frac
+    w = np.zeros((n + 63) // 64, np.uint64)
+    r = np.nonzero(bits)[0]
+    np.bitwise_or.at(w, r // 64, np.uint64(1) << (r % 64).astype(np.uint64))
+    return w
+
+
+def _words(rows, n):
+    w = np.zeros((n + 63) // 64, np.uint64)
+    r = np.asarray(rows, np.int64)
+    np.bitwise_or.at(w, r // 64, np.uint64(1) << (r % 64).astype(np.uint64))
+    return w
+
+
+@pytest.fixture(scope="module")
+def coll(ctx, oracle):
+    """Four segments: flat (deletes), HNSW-SQ8 codes, IVF-PQ (deletes), a small flat one that
+    re-inserts external ids of the first (an upsert visible in both)."""
+    pd = vdbg.padded_dim(DIM)
+    sizes = [6000, 8000, 20000, 500]
+    kinds = ["flat", "sq8", "ivf", "flat"]
+    segs, handles = [], []
+    next_id = 1000
+    for i, (n, kind) in enumerate(zip(sizes, kinds)):
+        x = datagen.uniform_rows(n, DIM, 700 + i) * 10
+        if kind == "ivf":
+            x[:FAR] += 50.0  # a far cluster of 30 % of the rows, spread over ~10 lists
+        base = datagen.pad(x, pd)
+        ext = (np.arange(next_id, next_id + n, dtype=np.uint64) * 3)
+        next_id += n
+        if i == 3:
+            ext[:100] = segs[0]["ext"][:100]
+        ds = vdbg.Dataset(ctx, base, DIM)
+        ds.set_external_ids(ext)
+        sg = {"base": base, "ext": ext, "kind": kind}
+        ix = None
+        if kind == "sq8":
+            ix = vdbg.Sq8Index(ds)
+            sg.update(codes=ix.codes(), vmin=ix.vmin, scale=ix.scale)
+        elif kind == "ivf":
+            blob = synth_ivfpq(base, DIM, 32, 8, seed=3)
+            ix = vdbg.IvfPqIndex.load(ds, blob)
+            p = parse_ivfpq(blob)
+            t2 = np.empty(p["nlist"] * p["m"] * 256, np.float32)
+            oracle.lib.or_ivfpq_term2(p["coarse"], p["nlist"], p["pd"], p["pq_centroids"],
+                                      p["m"], p["dim"] // p["m"], t2)
+            sg.update(ix=p, term2=t2)
+        deleted = _mask(n, 0.03, 800 + i) if i in (0, 2) else None
+        sg["deleted"] = deleted
+        segs.append(sg)
+        handles.append((ds, ix))
+    yield segs, handles
+    for ds, ix in handles:
+        if ix is not None:
+            ix.close()
+        ds.close()
+
+
+def _run(ctx, oracle, coll, filters, raw, k, metric="l2", **kw):
+    segs, handles = coll
+    for sg, f in zip(segs, filters):
+        sg["filter"] = f
+    params = vdbg.SearchParams(**kw)
+    gi, gd, gdc, gplans = vdbg.collection_search(
+        ctx, [(ds, ix, sg["deleted"], sg["filter"]) for (ds, ix), sg in zip(handles, segs)],
+        DIM, metric, raw, k, params)
+    okw = dict(kw)
+    okw["strategy"] = vdbg.STRATEGIES[okw.get("strategy", "auto")]
+    oi, od, odc, oplans = oracle.collection_search(segs, DIM, metric, raw, k, **okw)
+    assert gplans == oplans
+    bad = np.nonzero((gi != oi).any(axis=1) | (gd.view(np.uint32) != od.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, (bad[:5], gi[bad[0]], oi[bad[0]], gd[bad[0]], od[bad[0]])
+    assert np.array_equal(gdc, odc)
+    return gplans
+
+
+def _queries(n, seed):
+    return (datagen.uniform_rows(n, DIM, seed) * 10).astype(np.float32)
+
+
+@pytest.mark.parametrize("k", [1, 10, 100])
+def test_no_filter_every_index_type(ctx, oracle, coll, k):
+    print(f"collection no filter k={k}", flush=True)
+    plans = _run(ctx, oracle, coll, [None] * 4, _queries(40, 901), k, nprobe=8)
+    assert plans == ["index"] * 4
+
+
+def test_filter_planned_per_segment(ctx, oracle, coll):
+    # 50 % of every segment: flat segments scan exactly, the SQ8 and IVF-PQ segments search
+    # their index under the filter (nprobe raised to 16 / 0.5 = 32)
+    print("collection filter 50%", flush=True)
+    n = [sg["base"].shape[0] for sg in coll[0]]
+    filt = [_mask(m, 0.5, 810 + i) for i, m in enumerate(n)]
+    plans = _run(ctx, oracle, coll, filt, _queries(32, 902), 10, prefilter_threshold=1000)
+    assert plans == ["prefilter_exact", "filtered_index", "filtered_index", "prefilter_exact"]
+    # the default threshold (10,000 matches) keeps everything exact
+    plans = _run(ctx, oracle, coll, filt, _queries(32, 903), 10)
+    assert plans == ["prefilter_exact"] * 4
+
+
+def test_filtered_ivf_falls_back_to_exact(ctx, oracle, coll):
+    # only the far cluster (30 % of the IVF-PQ segment) is allowed: nprobe 2 / 0.3 = 7 probes
+    # of the lists nearest each query find none of it, so every query takes the exact scan
+    # of the allowed rows (planner.cc:103-108)
+    print("collection ivf exact fallback", flush=True)
+    segs = coll[0]
+    filt = [None, None, _words(np.arange(FAR), segs[2]["base"].shape[0]), None]
+    plans = _run(ctx, oracle, coll, filt, _queries(24, 904), 10, ef=1, nprobe=2,
+                 prefilter_threshold=100)
+    assert plans == ["index", "index", "filtered_index+exact_fallback", "index"]
+
+
+@pytest.mark.parametrize("strategy", ["prefilter", "graph", "post_filter"])
+def test_explicit_strategies(ctx, oracle, coll, strategy):
+    print(f"collection strategy={strategy}", flush=True)
+    n = [sg["base"].shape[0] for sg in coll[0]]
+    filt = [_mask(m, 0.3, 820 + i) for i, m in enumerate(n)]
+    plans = _run(ctx, oracle, coll, filt, _queries(20, 905), 10, strategy=strategy,
+                 post_filter_alpha=3, nprobe=4)
+    want = {"prefilter": "prefilter_exact", "graph": "filtered_index",
+            "post_filter": "post_filter"}[strategy]
+    assert plans == [want] * 4
+
+
+def test_empty_segment_filter(ctx, oracle, coll):
+    n = [sg["base"].shape[0] for sg in coll[0]]
+    filt = [np.zeros((m + 63) // 64, np.uint64) for m in n]
+    filt[1] = _mask(n[1], 0.01, 830)
+    plans = _run(ctx, oracle, coll, filt, _queries(10, 906), 10)
+    assert plans == ["empty", "prefilter_exact", "empty", "empty"]
+
+
+def test_cosine_collection(ctx, oracle):
+    # cosine: queries normalised once (PrepareQuery), unit rows, flat and SQ8 segments
+    pd = vdbg.padded_dim(96)
+    segs, handles = [], []
+    for i, (n, kind) in enumerate([(5000, "flat"), (7000, "sq8")]):
+        base = datagen.pad(datagen.clustered_unit(n, 96, 840 + i, 79, 40, 0.5), pd)
+        ext = np.arange(n, dtype=np.uint64) + 100000 * (i + 1)
+        ds = vdbg.Dataset(ctx, base, 96, metric="cosine")
+        ds.set_external_ids(ext)
+        sg = {"base": base, "ext": ext, "kind": kind, "deleted": _mask(n, 0.02, 850 + i),
+              "filter": None}
+        ix = None
+        if kind == "sq8":
+            ix = vdbg.Sq8Index(ds)
+            sg.update(codes=ix.codes(), vmin=ix.vmin, scale=ix.scale)
+        segs.append(sg)
+        handles.append((ds, ix))
+    raw = datagen.clustered_unit(30, 96, 860, 79, 40, 0.5) * 2.5
+    gi, gd, gdc, gp = vdbg.collection_search(
+        ctx, [(ds, ix, sg["deleted"], None) for (ds, ix), sg in zip(handles, segs)], 96, "cosine",
+        raw, 10)
+    oi, od, odc, op = oracle.collection_search(segs, 96, "cosine", raw, 10)
+    assert gp == op == ["index", "index"]
+    assert np.array_equal(gi, oi) and np.array_equal(gd.view(np.uint32), od.view(np.uint32))
+    assert np.array_equal(gdc, odc)
+    for ds, ix in handles:
+        if ix is not None:
+            ix.close()
+        ds.close()
+
+
+def test_collection_errors(ctx, coll):
+    segs, handles = coll
+    args = [(ds, ix, sg["deleted"], None) for (ds, ix), sg in zip(handles, segs)]
+    q = _queries(4, 907)
+    for k in (0, 10001):
+        with pytest.raises(vdbg.VdbgError) as e:
+            vdbg.collection_search(ctx, args, DIM, "l2", q, k)
+        assert e.value.code == 1 and "k must be in 1..10000" in str(e.value)
+    bad = q.copy()
+    bad[2, 5] = np.nan
+    with pytest.raises(vdbg.VdbgError) as e:
+        vdbg.collection_search(ctx, args, DIM, "l2", bad, 10)
+    assert e.value.code == 1 and "NaN or infinite" in str(e.value)
+    ds = vdbg.Dataset(ctx, segs[0]["base"][:100], DIM)  # no external ids
+    with pytest.raises(vdbg.VdbgError) as e:
+        vdbg.collection_search(ctx, [(ds, None, None, None)], DIM, "l2", q, 10)
+    assert e.value.code == 6
+    with pytest.raises(vdbg.VdbgError) as e:
+        vdbg.collection_search(ctx, args, DIM, "ip", q, 10)
+    assert e.value.code == 1
+    ds.close()
+    # no segments: every query gets padding
+    gi, gd, gdc, gp = vdbg.collection_search(ctx, [], DIM, "l2", q, 5)
+    assert (gi == np.iinfo(np.uint64).max).all() and np.isinf(gd).all() and gp == []

@@ -404,3 +404,34 @@ def test_filtered_collection_search_matches_reference(oracle, reference):
         assert list(re[i, :n]) == list(oe[:n])
         assert np.array_equal(rd[i, :n].view(np.uint32), od[:n].view(np.uint32))
         assert (re[i, n:] == np.iinfo(np.uint64).max).all()
+
+
+def test_plan_segment_known_answers(oracle):
+    # SearchDiskSegment's choice (src/engine/planner.cc:53-108) at the edges of its cost
+    # model, worked by hand from the formulas: selectivity s = matches / live rows; exact when
+    # matches <= prefilter_threshold, or matches <= 10 * max(ef, k) / s, or the index is flat;
+    # an Auto filtered index search probes max(nprobe, ceil(nprobe / s)) lists.
+    import ctypes as C
+    L = oracle.lib
+    npb = C.c_size_t()
+
+    def plan(has_filter, rows, deleted, matches, flat=0, strategy=0, ef=64, k=10, nprobe=16,
+             threshold=10000):
+        p = L.or_plan_segment(has_filter, rows, deleted, matches, flat, strategy, ef, k, nprobe,
+                              threshold, C.byref(npb))
+        return p, npb.value
+
+    assert plan(0, 100000, 500, 0) == (0, 16)            # no filter: the index
+    assert plan(1, 100000, 0, 0) == (1, 16)              # nothing matches: empty
+    assert plan(1, 100000, 0, 10000) == (2, 16)          # at the threshold: exact
+    assert plan(1, 100000, 0, 10001) == (3, 160)         # s = .10001: cost 6399 < 10001
+    assert plan(1, 100000, 0, 50000) == (3, 32)          # s = .5: 16 / .5 probes
+    assert plan(1, 100000, 0, 50000, flat=1) == (2, 16)  # a flat index always scans exactly
+    assert plan(1, 100000, 50000, 50000) == (3, 16)      # deletes raise s to 1: no boost
+    # cost model: 2000 matches of 10,000 live (s = .2) cost 10 * 64 / .2 = 3200 > 2000
+    assert plan(1, 10000, 0, 2000, threshold=100) == (2, 16)
+    assert plan(1, 10000, 0, 2000, threshold=100, ef=10) == (3, 80)  # 10 * 10 / .2 = 500
+    assert plan(1, 100000, 0, 50000, strategy=1) == (2, 16)   # PreFilter
+    assert plan(1, 100000, 0, 50000, strategy=2) == (3, 16)   # Graph: no boost when explicit
+    assert plan(1, 100000, 0, 50000, strategy=3) == (5, 16)   # PostFilter
+    assert plan(1, 100000, 0, 0, strategy=3) == (1, 16)       # empty wins over the strategy
