@@ -1,7 +1,7 @@
 // vdbg.hpp -- C++20 host classes over the C ABI in vdbg.h, shaped like vdb's index interface.
 //
 // vdb's search path is `class Index` (src/index/index.h:36-55): search(q, k, params, filter,
-// out, stats) per query, with SearchParams (include/vdb/options.h:63-71), RowFilter
+// out, stats) per query, with SearchParams (include/vdb/options.h:59-67), RowFilter
 // (index.h:23-27), IndexSearchStats (index.h:29-32) and results as ascending Neighbor
 // (include/vdb/types.h:19-28).  The classes below keep those names, argument meanings and
 // result order so that a vdb Index adapter (or any C++ caller) is a thin forwarding layer:
@@ -13,11 +13,21 @@
 //   SearchSegments the read path of CollectionImpl::Search over flat segments
 //                  (src/engine/collection_impl.cc:1036-1112): PrepareQuery, per-segment
 //                  filtered scan, (dist, part, row) merge with one hit per external id
+//   GpuSegment     Segment::Open (src/storage/segment_reader.cc:20-122) straight into HBM:
+//                  vectors.f32, ids.u64, the index file by magic, deletes-<n>.roar
+//   SearchCollection  CollectionImpl::SearchBatch over GpuSegments of any index type with
+//                  SearchDiskSegment's plan per segment (src/engine/planner.cc:42-129), one
+//                  device batch and one merge
 //
 // Differences, all forced by the device: filters are dense bitmasks (DenseRowFilter) rather
 // than a virtual allowed() per row; searches return a Status (vdb's return void), since a
 // device call can fail; every search also has a batched form.  Header-only; link libvdbg.so.
 #pragma once
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
 #include <algorithm>
 #include <cstdint>
@@ -50,11 +60,16 @@ struct Neighbor {
 
 constexpr size_t PaddedDim(size_t dim) { return (dim + 15) / 16 * 16; }  // types.h:30-32
 
-// The fields of SearchParams (options.h:63-71) that the scans read.
+enum class FilterStrategy : uint8_t { Auto = 0, PreFilter = 1, Graph = 2, PostFilter = 3 };  // options.h:57
+
+// SearchParams (options.h:59-67).
 struct SearchParams {
   size_t ef = 64;      // SQ8: depth = max(ef, k) when rerank < 0 (hnsw_index.cc:88)
   size_t nprobe = 16;  // IVF lists to scan
   int rerank = -1;     // -1 = auto, 0 = none
+  FilterStrategy strategy = FilterStrategy::Auto;  // the planner's (planner.cc:66-80)
+  size_t prefilter_threshold = 10000;              // matches at or below -> exact
+  size_t post_filter_alpha = 10;                   // post filter searches k * alpha
 };
 
 // The fields of IndexOptions (options.h:20-33) the builds read, plus the k-means iteration
@@ -512,6 +527,254 @@ inline Status SearchSegments(Device& dev, std::span<const SegmentRef> segs, Metr
     for (size_t j = 0; j < k && oe[i * k + j] != ~uint64_t(0); ++j)
       out[i].push_back({oe[i * k + j], od[i * k + j],
                         metric == Metric::L2 ? od[i * k + j] : -od[i * k + j]});
+  return Status::OK();
+}
+
+// ---------------------------------------------------------------- segments on disk
+
+enum class IndexType : uint8_t { Flat = 0, Hnsw = 1, HnswSq8 = 2, PqFlat = 3, IvfPq = 4 };  // options.h:13
+
+inline const char* IndexTypeName(IndexType t) {  // src/util/status.cc:55-64
+  switch (t) {
+    case IndexType::Flat: return "flat";
+    case IndexType::Hnsw: return "hnsw";
+    case IndexType::HnswSq8: return "hnsw_sq8";
+    case IndexType::PqFlat: return "pq";
+    case IndexType::IvfPq: return "ivf_pq";
+  }
+  return "unknown";
+}
+
+// The fields of SegmentMeta (src/storage/manifest.h) that Segment::Open reads.
+struct SegmentMeta {
+  uint32_t id = 0;
+  uint64_t rows = 0;
+  std::string deletes_file;  // "deletes-<n>.roar", empty = none persisted
+};
+
+// The fields of CollectionOptions (options.h:35-41) that Segment::Open reads.
+struct CollectionOptions {
+  size_t dim = 0;
+  Metric metric = Metric::L2;
+  IndexType index_type = IndexType::Flat;
+};
+
+namespace detail {
+
+// A whole file mapped read-only (Env::map_file, src/storage/env.h), unmapped on destruction.
+class MappedFile {
+ public:
+  ~MappedFile() {
+    if (p_ != nullptr && p_ != MAP_FAILED) munmap(p_, n_);
+  }
+  Status Open(const std::string& path) {
+    const int fd = ::open(path.c_str(), O_RDONLY | O_CLOEXEC);
+    if (fd < 0) return Status(VDBG_IO_ERROR, path + ": cannot open");
+    struct stat st;
+    if (fstat(fd, &st) != 0) {
+      ::close(fd);
+      return Status(VDBG_IO_ERROR, path + ": cannot stat");
+    }
+    n_ = size_t(st.st_size);
+    if (n_ > 0) p_ = mmap(nullptr, n_, PROT_READ, MAP_PRIVATE, fd, 0);
+    ::close(fd);
+    if (p_ == MAP_FAILED) return Status(VDBG_IO_ERROR, path + ": cannot map");
+    return Status::OK();
+  }
+  const void* data() const { return p_; }
+  size_t size() const { return n_; }
+
+ private:
+  void* p_ = nullptr;
+  size_t n_ = 0;
+};
+
+inline std::string JoinPath(const std::string& a, const std::string& b) {
+  return a.empty() || a.back() == '/' ? a + b : a + "/" + b;
+}
+
+}  // namespace detail
+
+// Segment::Open (src/storage/segment_reader.cc:20-122) for what a search reads, made resident
+// on the device: vectors.f32 (header and CRC checks, the rows uploaded), ids.u64 (kept on
+// the host and resident for the merge), the index file (LoadIndex by magic, index.cc:38-87:
+// VDBFLAT1 needs nothing more, VDBHSQ81 brings its SQ8 codes, VDBIVFP1 its lists; a graph
+// index is NotSupported, since graph traversal stays on the CPU) and the persisted delete
+// set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
+// the reference's Corruption messages, prefixed with the file or directory.
+class GpuSegment {
+ public:
+  static Status Open(Device& dev, const std::string& dir, const SegmentMeta& meta,
+                     const CollectionOptions& opts, bool verify_crc,
+                     std::unique_ptr<GpuSegment>* out) {
+    std::unique_ptr<GpuSegment> s(new GpuSegment());
+    s->id_ = meta.id;
+    s->dim_ = opts.dim;
+    s->metric_ = opts.metric;
+    // ---- vectors.f32 (:37-59)
+    {
+      const std::string vpath = detail::JoinPath(dir, "vectors.f32");
+      detail::MappedFile f;
+      VDBG_CXX_RETURN_IF_ERROR(f.Open(vpath));
+      vdbg_dataset* d = nullptr;
+      Status st = Status::FromCall(vdbg_dataset_open_vectors(dev.get(), f.data(), f.size(), opts.dim,
+                                                             int(opts.metric), meta.rows,
+                                                             verify_crc ? 1 : 0, &d));
+      if (!st.ok()) return Status(st.code(), dir + "/" + st.message());
+      s->ds_.reset(d);
+      s->rows_ = meta.rows;
+    }
+    // ---- ids.u64 (:61-66)
+    {
+      std::string bytes;
+      VDBG_CXX_RETURN_IF_ERROR(ReadFile(detail::JoinPath(dir, "ids.u64"), &bytes));
+      size_t off = 0, len = 0;
+      Status st = Status::FromCall(vdbg_blob_decode(bytes.data(), bytes.size(), "VDBIDS01", &off, &len));
+      if (!st.ok()) return Status(st.code(), detail::JoinPath(dir, "ids.u64") + ": " + st.message());
+      if (len != s->rows_ * sizeof(VectorId)) return Status(VDBG_CORRUPTION, dir + ": ids.u64 size mismatch");
+      s->ids_.resize(s->rows_);
+      if (len > 0) std::memcpy(s->ids_.data(), bytes.data() + off, len);
+      VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_dataset_set_external_ids(s->ds_.get(), s->ids_.data())));
+    }
+    // ---- index.<type> (:90-99)
+    {
+      std::string bytes;
+      VDBG_CXX_RETURN_IF_ERROR(
+          ReadFile(detail::JoinPath(dir, std::string("index.") + IndexTypeName(opts.index_type)), &bytes));
+      Status st = s->LoadIndex(bytes);
+      if (!st.ok()) return Status(st.code(), dir + ": " + st.message());
+    }
+    // ---- deletes (:102-117)
+    s->deleted_.assign((s->rows_ + 63) / 64, 0);
+    if (!meta.deletes_file.empty()) {
+      std::string bytes;
+      VDBG_CXX_RETURN_IF_ERROR(ReadFile(detail::JoinPath(dir, meta.deletes_file), &bytes));
+      uint64_t n = 0;
+      Status st = Status::FromCall(vdbg_deletes_decode(bytes.data(), bytes.size(), s->rows_,
+                                                       s->deleted_.data(), &n));
+      if (!st.ok()) return Status(st.code(), dir + ": " + st.message());
+      s->deleted_count_ = n;
+    }
+    *out = std::move(s);
+    return Status::OK();
+  }
+  ~GpuSegment() {
+    if (sq8_) vdbg_sq8_destroy(sq8_);
+    if (ivf_) vdbg_ivfpq_destroy(ivf_);
+  }
+
+  uint32_t id() const { return id_; }
+  size_t rows() const { return rows_; }
+  size_t dim() const { return dim_; }
+  Metric metric() const { return metric_; }
+  IndexType index_type() const { return type_; }
+  VectorId external_id(InternalId r) const { return ids_[r]; }
+  // DeleteBits (src/util/delete_bits.h:18-114) as dense words, bit r = row r deleted.
+  const std::vector<uint64_t>& deleted_words() const { return deleted_; }
+  size_t deleted_count() const { return deleted_count_; }
+  size_t live_rows() const { return rows_ - std::min(rows_, deleted_count_); }
+  // DeleteBits::set: later searches skip the row.
+  void Delete(InternalId r) {
+    if (r >= rows_) return;
+    uint64_t& w = deleted_[r >> 6];
+    const uint64_t bit = uint64_t(1) << (r & 63);
+    if (!(w & bit)) ++deleted_count_;
+    w |= bit;
+  }
+  vdbg_dataset* dataset() const { return ds_.get(); }
+  vdbg_sq8* sq8() const { return sq8_; }
+  vdbg_ivfpq* ivfpq() const { return ivf_; }
+
+  static Status ReadFile(const std::string& path, std::string* out) {
+    detail::MappedFile f;
+    VDBG_CXX_RETURN_IF_ERROR(f.Open(path));
+    out->assign(static_cast<const char*>(f.data()), f.size());
+    return Status::OK();
+  }
+
+ private:
+  GpuSegment() = default;
+  // LoadIndex (index.cc:38-87): CRC32C footer, then the magic picks the index.
+  Status LoadIndex(const std::string& bytes) {
+    if (bytes.size() < 12) return Status(VDBG_CORRUPTION, "index file too short");
+    uint32_t stored;
+    std::memcpy(&stored, bytes.data() + bytes.size() - 4, 4);
+    if (vdbg_crc32c_extend(0, bytes.data(), bytes.size() - 4) != stored)
+      return Status(VDBG_CORRUPTION, "index file checksum mismatch");
+    const std::string_view magic(bytes.data(), 8);
+    if (magic == "VDBFLAT1") {
+      type_ = IndexType::Flat;
+      return Status::OK();
+    }
+    if (magic == "VDBHSQ81") {
+      type_ = IndexType::HnswSq8;
+      return Status::FromCall(vdbg_sq8_load(ds_.get(), bytes.data(), bytes.size(), &sq8_));
+    }
+    if (magic == "VDBIVFP1") {
+      type_ = IndexType::IvfPq;
+      return Status::FromCall(vdbg_ivfpq_load(ds_.get(), bytes.data(), bytes.size(), &ivf_));
+    }
+    if (magic == "VDBHNSW1" || magic == "VDBPQFL1")
+      return Status(VDBG_NOT_SUPPORTED, "graph and PQ-flat index files are searched on the CPU");
+    return Status(VDBG_CORRUPTION, "unknown index file magic");
+  }
+
+  uint32_t id_ = 0;
+  size_t rows_ = 0, dim_ = 0;
+  Metric metric_ = Metric::L2;
+  IndexType type_ = IndexType::Flat;
+  detail::DatasetPtr ds_;
+  vdbg_sq8* sq8_ = nullptr;
+  vdbg_ivfpq* ivf_ = nullptr;
+  std::vector<VectorId> ids_;
+  std::vector<uint64_t> deleted_;
+  size_t deleted_count_ = 0;
+};
+
+// CollectionImpl::SearchBatch (collection_impl.cc:1121-1135) over a snapshot's disk segments,
+// as one device batch (vdbg_collection_search_host): PrepareQuery, SearchDiskSegment's plan
+// per segment (planner.cc:42-129), the merge with one hit per external id.  filters: null
+// for a request without a filter, else one filter per segment (the request's filter
+// evaluated on that segment; deletes are removed here).  plans (optional) receives each
+// segment's SegmentExplain::strategy.
+inline Status SearchCollection(Device& dev, std::span<const GpuSegment* const> segs, size_t dim,
+                               Metric metric, const float* raw_queries, size_t nq, size_t k,
+                               const SearchParams& p,
+                               const std::vector<const DenseRowFilter*>* filters,
+                               std::vector<std::vector<SearchHit>>& out,
+                               std::vector<uint64_t>* dist_comps = nullptr,
+                               std::vector<std::string>* plans = nullptr) {
+  if (filters != nullptr && filters->size() != segs.size())
+    return Status(VDBG_INVALID_ARGUMENT, "one filter per segment");
+  std::vector<vdbg_segment> v(segs.size());
+  for (size_t i = 0; i < segs.size(); ++i) {
+    const GpuSegment& g = *segs[i];
+    v[i].rows = g.dataset();
+    v[i].sq8 = g.sq8();
+    v[i].ivfpq = g.ivfpq();
+    v[i].deleted_words = g.deleted_count() > 0 ? g.deleted_words().data() : nullptr;
+    v[i].filter_words = filters != nullptr ? (*filters)[i]->words() : nullptr;
+  }
+  const vdbg_search_params sp{p.ef, p.nprobe, p.rerank, int(p.strategy), p.prefilter_threshold,
+                              p.post_filter_alpha};
+  std::vector<uint64_t> ids(nq * k), dc(nq);
+  std::vector<float> d(nq * k);
+  std::vector<int> pl(segs.size());
+  VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_collection_search_host(
+      dev.get(), v.data(), v.size(), dim, int(metric), raw_queries, nq, k, &sp, ids.data(),
+      d.data(), dc.data(), pl.data())));
+  out.assign(nq, {});
+  for (size_t i = 0; i < nq; ++i)
+    for (size_t j = 0; j < k && ids[i * k + j] != ~uint64_t(0); ++j)
+      out[i].push_back({ids[i * k + j], d[i * k + j],
+                        metric == Metric::L2 ? d[i * k + j] : -d[i * k + j]});
+  if (dist_comps != nullptr) *dist_comps = dc;
+  if (plans != nullptr) {
+    static const char* const kNames[] = {"index", "empty", "prefilter_exact", "filtered_index",
+                                         "filtered_index+exact_fallback", "post_filter"};
+    plans->clear();
+    for (int x : pl) plans->push_back(kNames[x]);
+  }
   return Status::OK();
 }
 

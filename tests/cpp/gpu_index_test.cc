@@ -8,7 +8,10 @@
 // Run: tests/cpp/gpu_index_test  (exit status 0 = all passed).  Needs a gfx950 GPU.
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <functional>
 #include <string>
 #include <vector>
@@ -448,6 +451,272 @@ void CollectionSearchMatchesOracleAtEverySelectivity() {
         VDBG_INVALID_ARGUMENT);
 }
 
+// ---------------------------------------------------------------- segment files (segment_reader.cc)
+
+// File writers, field by field from the reference's layouts (segment_writer.cc:58-75,
+// file_format.cc:8-18, index.cc:38-45, hnsw_index.cc:108-115, the portable roaring format).
+template <class T>
+void Put(std::string* s, T v) {
+  s->append(reinterpret_cast<const char*>(&v), sizeof(T));
+}
+
+void WriteFile(const std::string& path, const std::string& bytes) {
+  std::ofstream f(path, std::ios::binary);
+  f.write(bytes.data(), std::streamsize(bytes.size()));
+}
+
+std::string Blob(const char* magic, const std::string& payload) {
+  std::string b(magic, 8);
+  Put<uint32_t>(&b, 1);
+  Put<uint32_t>(&b, or_crc32c(0, payload.data(), payload.size()));
+  Put<uint64_t>(&b, payload.size());
+  return b + payload;
+}
+
+std::string IndexFile(const char* magic, const std::string& body) {
+  std::string f = std::string(magic, 8) + body;
+  Put<uint32_t>(&f, or_crc32c(0, f.data(), f.size()));
+  return f;
+}
+
+std::string VectorsFile(const Data& d, vdbg::Metric m) {
+  std::string h(4096, '\0');
+  std::memcpy(h.data(), "VDBSEG01", 8);
+  const uint64_t len = d.rows * d.pd * 4;
+  auto put = [&](size_t off, auto v) { std::memcpy(h.data() + off, &v, sizeof(v)); };
+  put(8, uint32_t(1));
+  put(12, uint32_t(m));
+  put(16, uint64_t(d.rows));
+  put(24, uint32_t(d.dim));
+  put(28, uint32_t(d.pd));
+  put(32, uint64_t(4096));
+  put(40, len);
+  put(48, or_crc32c(0, d.v.data(), len));
+  put(64, uint64_t(9));
+  put(4092, or_crc32c(0, h.data(), 4092));
+  return h + std::string(reinterpret_cast<const char*>(d.v.data()), len);
+}
+
+// A roaring bitmap of `rows` (ascending) in the portable format with array containers only
+// (every container of at most 4096 rows): cookie 12346, count, (key, card - 1), offsets, values.
+std::string RoaringArrays(const std::vector<uint32_t>& rows) {
+  std::vector<std::pair<uint16_t, std::vector<uint16_t>>> cont;
+  for (uint32_t r : rows) {
+    if (cont.empty() || cont.back().first != (r >> 16)) cont.push_back({uint16_t(r >> 16), {}});
+    cont.back().second.push_back(uint16_t(r & 0xffff));
+  }
+  std::string s;
+  Put<uint32_t>(&s, 12346);
+  Put<uint32_t>(&s, uint32_t(cont.size()));
+  for (auto& [key, v] : cont) {
+    Put<uint16_t>(&s, key);
+    Put<uint16_t>(&s, uint16_t(v.size() - 1));
+  }
+  uint32_t off = uint32_t(s.size() + 4 * cont.size());
+  for (auto& c : cont) {
+    Put<uint32_t>(&s, off);
+    off += uint32_t(2 * c.second.size());
+  }
+  for (auto& c : cont)
+    for (uint16_t x : c.second) Put<uint16_t>(&s, x);
+  return s;
+}
+
+struct SegFiles {
+  Data rows;
+  std::vector<uint64_t> ext;
+  std::vector<uint32_t> deleted;
+  std::vector<float> vmin, scale;  // HNSW-SQ8
+  std::vector<uint8_t> codes;
+  IvfFile ivf;                     // IVF-PQ
+};
+
+std::string MakeSegmentDir(const std::string& root, uint32_t id, vdbg::IndexType t, vdbg::Metric m,
+                           SegFiles& sf, uint64_t first_ext) {
+  const std::string dir = root + "/seg-" + std::to_string(id);
+  std::filesystem::create_directories(dir);
+  WriteFile(dir + "/vectors.f32", VectorsFile(sf.rows, m));
+  for (size_t r = 0; r < sf.rows.rows; ++r) sf.ext.push_back(first_ext + 5 * r);
+  WriteFile(dir + "/ids.u64", Blob("VDBIDS01", std::string(reinterpret_cast<const char*>(sf.ext.data()),
+                                                          sf.ext.size() * 8)));
+  const Data& b = sf.rows;
+  std::string file;
+  if (t == vdbg::IndexType::Flat) {
+    file = IndexFile("VDBFLAT1", "");
+  } else if (t == vdbg::IndexType::HnswSq8) {
+    sf.vmin.resize(b.pd);
+    sf.scale.resize(b.pd);
+    sf.codes.resize(b.rows * b.pd);
+    or_sq8_train(b.v.data(), b.rows, b.dim, b.pd, sf.vmin.data(), sf.scale.data());
+    or_sq8_encode_rows(b.v.data(), b.rows, b.dim, b.pd, sf.vmin.data(), sf.scale.data(), sf.codes.data());
+    std::string body;
+    Put<uint64_t>(&body, b.rows);
+    Put<uint32_t>(&body, uint32_t(b.dim));
+    Put<uint32_t>(&body, uint32_t(b.pd));
+    body.append(reinterpret_cast<const char*>(sf.vmin.data()), b.pd * 4);
+    body.append(reinterpret_cast<const char*>(sf.scale.data()), b.pd * 4);
+    body.append(reinterpret_cast<const char*>(sf.codes.data()), sf.codes.size());
+    body.append(16, '\0');  // the graph (not read by the device)
+    file = IndexFile("VDBHSQ81", body);
+  } else {
+    std::unique_ptr<vdbg::GpuIvfPqIndex> ix;
+    vdbg::IndexOptions o;
+    o.nlist = 40;
+    o.pq_m = 8;
+    o.kmeans_iters = 8;
+    if (!vdbg::GpuIvfPqIndex::Create(*g_dev, o, m, b.view(), &ix).ok() || !ix->build().ok() ||
+        !ix->Save(&file).ok())
+      return "";
+    ParseIvf(file, &sf.ivf);
+  }
+  WriteFile(dir + "/index." + vdbg::IndexTypeName(t), file);
+  if (!sf.deleted.empty())
+    WriteFile(dir + "/deletes-000003.roar", Blob("VDBDEL01", RoaringArrays(sf.deleted)));
+  return dir;
+}
+
+// The oracle's view of one segment's index search (flat / SQ8 scan + rerank / IVF-PQ) for
+// every query, allowed rows only.
+std::vector<std::vector<vdbg::Neighbor>> OracleSegment(const SegFiles& sf, vdbg::IndexType t,
+                                                       vdbg::Metric m, const float* q, size_t nq,
+                                                       size_t k, const vdbg::SearchParams& p,
+                                                       const vdbg::DenseRowFilter* allow) {
+  if (t == vdbg::IndexType::Flat) return OracleFlat(sf.rows, q, nq, k, m, allow);
+  const Data& b = sf.rows;
+  std::vector<float> d(nq * k);
+  std::vector<uint32_t> id(nq * k);
+  if (t == vdbg::IndexType::HnswSq8) {
+    or_sq8_search_batch(Kset(), int(m), b.v.data(), sf.codes.data(), b.rows, b.pd, sf.vmin.data(),
+                        sf.scale.data(), q, nq, k, std::max(p.ef, k), allow ? allow->words() : nullptr,
+                        d.data(), id.data(), 8);
+  } else {
+    const IvfFile& f = sf.ivf;
+    std::vector<float> term2(f.nlist * f.m * 256);
+    or_ivfpq_term2(f.coarse.data(), f.nlist, f.pd, f.cen.data(), f.m, f.dim / f.m, term2.data());
+    std::vector<uint64_t> dc(nq);
+    or_ivfpq_search_batch(Kset(), int(m), b.v.data(), b.dim, b.pd, f.coarse.data(), f.nlist,
+                          f.cen.data(), f.m, f.off.data(), f.ids.data(), f.codes.data(),
+                          m == vdbg::Metric::L2 ? term2.data() : nullptr, q, nq, k, p.nprobe,
+                          p.rerank, allow ? allow->words() : nullptr, d.data(), id.data(),
+                          dc.data(), 8);
+  }
+  std::vector<std::vector<vdbg::Neighbor>> out(nq);
+  for (size_t i = 0; i < nq; ++i)
+    for (size_t j = 0; j < k && id[i * k + j] != UINT32_MAX; ++j) out[i].push_back({d[i * k + j], id[i * k + j]});
+  return out;
+}
+
+void SegmentOpenAndCollectionSearch() {
+  char tmpl[] = "/tmp/vdbg_segments_XXXXXX";
+  const char* root_c = mkdtemp(tmpl);
+  CHECK(root_c != nullptr);
+  if (root_c == nullptr) return;
+  const std::string root = root_c;
+  const size_t dim = 40, k = 10, nq = 24;
+  const vdbg::Metric m = vdbg::Metric::L2;
+  const vdbg::IndexType types[3] = {vdbg::IndexType::Flat, vdbg::IndexType::HnswSq8,
+                                    vdbg::IndexType::IvfPq};
+  std::vector<SegFiles> sf(3);
+  std::vector<std::unique_ptr<vdbg::GpuSegment>> seg(3);
+  for (size_t s = 0; s < 3; ++s) {
+    sf[s].rows = Clustered(3000 + 2000 * s, dim, 16, 50 + s, false);
+    if (s != 1)
+      for (uint32_t r = 7; r < sf[s].rows.rows; r += 31) sf[s].deleted.push_back(r);
+    const std::string dir = MakeSegmentDir(root, uint32_t(s), types[s], m, sf[s], 1000000 * (s + 1));
+    CHECK(!dir.empty());
+    vdbg::SegmentMeta meta{uint32_t(s), sf[s].rows.rows, sf[s].deleted.empty() ? "" : "deletes-000003.roar"};
+    vdbg::CollectionOptions opts{dim, m, types[s]};
+    CHECK_OK(vdbg::GpuSegment::Open(*g_dev, dir, meta, opts, true, &seg[s]));
+    CHECK(seg[s]->index_type() == types[s]);
+    CHECK(seg[s]->deleted_count() == sf[s].deleted.size());
+    CHECK(seg[s]->external_id(3) == sf[s].ext[3]);
+  }
+  Data raw = Clustered(nq, dim, 16, 70, false);
+  std::vector<float> rq(nq * dim);
+  for (size_t q = 0; q < nq; ++q) std::memcpy(&rq[q * dim], raw.row(q), dim * 4);
+  std::vector<const vdbg::GpuSegment*> segs{seg[0].get(), seg[1].get(), seg[2].get()};
+  vdbg::SearchParams p;
+  p.nprobe = 6;
+  for (int with_filter = 0; with_filter < 2; ++with_filter) {
+    std::vector<vdbg::DenseRowFilter> filt;
+    std::vector<const vdbg::DenseRowFilter*> fp;
+    std::vector<vdbg::DenseRowFilter> allow;  // what each segment's search may return
+    for (size_t s = 0; s < 3; ++s) {
+      filt.emplace_back(sf[s].rows.rows);
+      Rng r{900 + s};
+      for (uint32_t row = 0; row < sf[s].rows.rows; ++row)
+        if (r.uni() < 0.4f) filt[s].Allow(row);
+      allow.push_back(with_filter ? filt[s] : vdbg::DenseRowFilter(sf[s].rows.rows, true));
+      for (uint32_t d : sf[s].deleted) allow[s].Deny(d);
+    }
+    for (auto& f : filt) fp.push_back(&f);
+    std::vector<std::vector<vdbg::SearchHit>> got;
+    std::vector<uint64_t> dc;
+    std::vector<std::string> plans;
+    CHECK_OK(vdbg::SearchCollection(*g_dev, segs, dim, m, rq.data(), nq, k, p,
+                                    with_filter ? &fp : nullptr, got, &dc, &plans));
+    // every segment matches > 1000 rows but fewer than the 10,000 threshold: exact under a
+    // filter; otherwise each segment's own index under its deletes
+    for (size_t s = 0; s < 3; ++s) CHECK(plans[s] == (with_filter ? "prefilter_exact" : "index"));
+    const size_t pd = vdbg::PaddedDim(dim);
+    std::vector<float> q(nq * pd, 0.f);
+    for (size_t i = 0; i < nq; ++i) std::memcpy(&q[i * pd], &rq[i * dim], dim * 4);
+    std::vector<std::vector<std::vector<vdbg::Neighbor>>> parts;
+    std::vector<uint64_t> all_ext, off;
+    for (size_t s = 0; s < 3; ++s) {
+      parts.push_back(with_filter ? OracleFlat(sf[s].rows, q.data(), nq, k, m, &allow[s])
+                                  : OracleSegment(sf[s], types[s], m, q.data(), nq, k, p, &allow[s]));
+      off.push_back(all_ext.size());
+      all_ext.insert(all_ext.end(), sf[s].ext.begin(), sf[s].ext.end());
+    }
+    for (size_t i = 0; i < nq; ++i) {
+      std::vector<float> pdist(3 * k, INFINITY), od(k);
+      std::vector<uint32_t> prow(3 * k, UINT32_MAX);
+      std::vector<uint64_t> oe(k);
+      for (size_t s = 0; s < 3; ++s)
+        for (size_t j = 0; j < parts[s][i].size(); ++j) {
+          pdist[s * k + j] = parts[s][i][j].dist;
+          prow[s * k + j] = parts[s][i][j].id;
+        }
+      const size_t n = or_merge_parts(3, k, pdist.data(), prow.data(), all_ext.data(), off.data(),
+                                      od.data(), oe.data());
+      CHECK(got[i].size() == n);
+      for (size_t j = 0; j < std::min(n, got[i].size()); ++j) {
+        CHECK(got[i][j].id == oe[j]);
+        CHECK(std::memcmp(&got[i][j].distance, &od[j], 4) == 0);
+      }
+    }
+  }
+  // deletes after open: DeleteBits::set hides the row from the next search
+  std::vector<std::vector<vdbg::SearchHit>> a, b;
+  CHECK_OK(vdbg::SearchCollection(*g_dev, segs, dim, m, rq.data(), 1, 1, p, nullptr, a));
+  CHECK(a.size() == 1 && a[0].size() == 1);
+  for (size_t s = 0; s < 3; ++s)
+    for (uint32_t r = 0; r < seg[s]->rows(); ++r)
+      if (seg[s]->external_id(r) == a[0][0].id) seg[s]->Delete(r);
+  CHECK_OK(vdbg::SearchCollection(*g_dev, segs, dim, m, rq.data(), 1, 1, p, nullptr, b));
+  CHECK(b[0].size() == 1 && b[0][0].id != a[0][0].id);
+
+  // what Segment::Open rejects
+  std::unique_ptr<vdbg::GpuSegment> bad;
+  const std::string d0 = root + "/seg-0";
+  vdbg::CollectionOptions flat{dim, m, vdbg::IndexType::Flat};
+  CHECK(vdbg::GpuSegment::Open(*g_dev, root + "/none", {9, 3000, ""}, flat, true, &bad).code() == VDBG_IO_ERROR);
+  CHECK(vdbg::GpuSegment::Open(*g_dev, d0, {0, 3001, ""}, flat, true, &bad).code() == VDBG_CORRUPTION);
+  vdbg::CollectionOptions wrong_dim{dim + 1, m, vdbg::IndexType::Flat};
+  CHECK(vdbg::GpuSegment::Open(*g_dev, d0, {0, 3000, ""}, wrong_dim, true, &bad).code() == VDBG_CORRUPTION);
+  WriteFile(d0 + "/deletes-000004.roar", Blob("VDBDEL01", RoaringArrays({1, 2, 5000})));
+  CHECK(vdbg::GpuSegment::Open(*g_dev, d0, {0, 3000, "deletes-000004.roar"}, flat, true, &bad).code() ==
+        VDBG_CORRUPTION);  // a deleted row past the segment's end
+  WriteFile(d0 + "/index.hnsw", IndexFile("VDBHNSW1", std::string(8, '\0')));
+  vdbg::CollectionOptions hnsw{dim, m, vdbg::IndexType::Hnsw};
+  CHECK(vdbg::GpuSegment::Open(*g_dev, d0, {0, 3000, ""}, hnsw, true, &bad).code() == VDBG_NOT_SUPPORTED);
+  WriteFile(d0 + "/ids.u64", Blob("VDBIDS01", std::string(8 * 2999, '\0')));
+  CHECK(vdbg::GpuSegment::Open(*g_dev, d0, {0, 3000, ""}, flat, true, &bad).code() == VDBG_CORRUPTION);
+  seg.clear();
+  std::filesystem::remove_all(root);
+}
+
 }  // namespace
 
 int main() {
@@ -471,6 +740,7 @@ int main() {
       {"IndexTest.PqMustDivideDim", IvfPqMustDivideDim},
       {"FilteredSearchTest.CollectionSearchMatchesOracleAtEverySelectivity",
        CollectionSearchMatchesOracleAtEverySelectivity},
+      {"SegmentTest.OpenFromFilesAndSearchCollection", SegmentOpenAndCollectionSearch},
   };
   for (const auto& [name, fn] : tests) {
     g_test = name;
