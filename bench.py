@@ -36,6 +36,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 METRIC = "batch QPS at k=10 (flat/SQ8/IVF-PQ, 1M×128); achieved HBM TB/s / MFMA %"
 FP32_MFMA_PEAK_TFLOPS = 157.3
 FP16_MFMA_PEAK_TFLOPS = 2500.0  # dense
+INT8_MFMA_PEAK_TOPS = 5000.0    # dense
 HBM_PEAK_GBS = 8000.0
 
 
@@ -292,19 +293,37 @@ def main():
         gi, gd = gpu_out()
         g_ms = prof["flat_gemm"][0] / max(1, prof["flat_gemm"][1])
         tflops = 2.0 * nq * N * dim / (g_ms * 1e-3) / 1e12
-        # integer-valued rows and queries (SIFT-like) rank through the exact fp16-input GEMM:
-        # its values equal the fp32 GEMM's bit for bit, so it is priced at the fp16 MFMA peak
+        # integer-valued rows and queries (SIFT-like, values 0..120) rank on the int8 GEMM
+        # (rows and queries shifted into int8, exact int32 sums), priced at the int8 MFMA
+        # peak; the exact fp16-input GEMM and the fp32 GEMM run the same workload below
         bits = ctx.last_gemm_bits()
+        kern = {8: "k_gemm8<128,L2,2 query blocks,threshold>",
+                16: "k_gemm16<128,L2,2 query blocks,threshold>"}.get(bits, "k_gemm<128,L2,rows,filter>")
         r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
-             "kernel": "k_gemm16<128,L2>" if bits == 16 else "k_gemm<128,L2,rows,filter>",
-             "kernel_ms": g_ms, "achieved": tflops, "unit": "TFLOP/s",
-             "peak": FP16_MFMA_PEAK_TFLOPS if bits == 16 else FP32_MFMA_PEAK_TFLOPS,
+             "kernel": kern, "kernel_ms": g_ms, "achieved": tflops,
+             "unit": "TOP/s" if bits == 8 else "TFLOP/s",
+             "peak": {8: INT8_MFMA_PEAK_TOPS, 16: FP16_MFMA_PEAK_TFLOPS}.get(bits, FP32_MFMA_PEAK_TFLOPS),
              "bound": "mfma",
-             "mfma_inputs": "f16 (exact: integer values, sums < 2^24)" if bits == 16 else "f32",
+             "mfma_inputs": {8: "i8 (rows and queries shifted by one constant; exact int32 sums)",
+                             16: "f16 (exact: integer values, sums < 2^24)"}.get(bits, "f32"),
              "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
              "exact_rescans": fb}
-        log(f"flat: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} TFLOP/s")
-        if bits == 16:
+        log(f"flat: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} T(FL)OP/s ({bits}-bit inputs)")
+        if bits == 8:
+            # the same workload on the exact fp16-input GEMM (identical results)
+            ctx.set_int8_gemm(False)
+            el16, prof16, _ = timed(ctx, torch, step, args.steps, 1, ["flat_gemm"])
+            ctx.set_int8_gemm(True)
+            g16 = prof16["flat_gemm"][0] / max(1, prof16["flat_gemm"][1])
+            t16 = 2.0 * nq * N * dim / (g16 * 1e-3) / 1e12
+            r["fp16_gemm"] = {"qps": round(nq * args.steps / el16, 1),
+                              "kernel": "k_gemm16<128,L2,2 query blocks,threshold>",
+                              "kernel_ms": round(g16, 4), "achieved_TFLOPs": round(t16, 2),
+                              "peak_TFLOPs": FP16_MFMA_PEAK_TFLOPS,
+                              "frac": round(t16 / FP16_MFMA_PEAK_TFLOPS, 4)}
+            log(f"flat (fp16 GEMM): {nq * args.steps / el16:.0f} q/s, GEMM {g16:.2f} ms = "
+                f"{t16:.1f} TFLOP/s")
+        if bits in (8, 16):
             # the same workload ranked on the fp32 GEMM (identical results), against the fp32
             # MFMA peak
             ctx.set_fp16_gemm(False)
@@ -513,7 +532,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "i8 ranking GEMM (exact), f32 distances" if head.get("unit") == "TOP/s" else "f32",
         "data": "synthetic (seeded SIFT-like mixture, resident in HBM)",
         "config": {"workload": f"flat_l2_sift_like_{N}x{dim}_k{k}_batch{nq}", "n": N,
                    "dim": dim, "k": k, "batch": nq, "metric": "l2"},

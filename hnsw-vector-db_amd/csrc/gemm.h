@@ -27,6 +27,10 @@ struct GemmArgs {
   uint32_t aw_mask;    // ~0 with a filter, 0 without (every row then reads aw[0])
   uint2* cand;         // MODE 0: [(q * nchunks + chunk) * 2 + half][caph]
   uint32_t* counts;    // MODE 0: [(q * nchunks + chunk) * 2 + half]
+  const int8_t* X8;    // k_gemm8: rows shifted to int8
+  const int8_t* Q8;    // k_gemm8: queries shifted to int8
+  const int* rn8;      // k_gemm8: accumulator start per row
+  const int* Qd;       // k_gemm8: per-query constant between the integer GEMM and GEMM units
   int* ovf;            // MODE 0: [q]
   float* gm;           // MODE 1: [q][ngroups] minimum GEMM value of each 16-row group
   int ngroups;
@@ -59,6 +63,12 @@ __host__ __device__ constexpr int Gemm16Kc(int pd, int split) {
   return 16;
 }
 
+// K chunk of the int8 GEMM: the whole row up to 128 dims, else the largest of 128/64/32
+// dividing it.
+__host__ __device__ constexpr int Gemm8Kc(int pd) {
+  return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : 32));
+}
+
 // Padded dimensions with compiled GEMM kernels; others scan exactly.
 inline bool GemmSupported(size_t pd) {
   switch (pd) {
@@ -69,6 +79,14 @@ inline bool GemmSupported(size_t pd) {
       return false;
   }
 }
+
+// Padded dimensions with int8 GEMM kernels (multiples of 32).
+inline bool Gemm8Supported(size_t pd) { return pd % 32 == 0 && GemmSupported(pd); }
+
+// int8 GEMM (gemm8.hip): qb query blocks of 32 per wave, mode 0 = threshold pass, 1 = group
+// minima of the sample (qb 2).
+int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+                const GemmArgs& a);
 
 // fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 = threshold pass
 // into candidate buffers, 1 = group minima of the sample; split 1 = SQ8 codes against the

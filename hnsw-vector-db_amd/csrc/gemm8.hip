@@ -1,0 +1,372 @@
+// gemm8.hip -- the ranking GEMM of the flat scan for integer rows spanning at most 256
+// consecutive values, on int8 MFMA (v_mfma_i32_32x32x32_i8: twice the fp16 rate, half the
+// operand bytes).
+//
+// With a per-dataset integer shift c, every row value x and query value q becomes an int8
+// x' = x - c, q' = q - c (rows: c centres their range; queries: the batch qualifies when every
+// q' fits).  Over all padded dims
+//     ||x'||^2 - 2 q'.x' = (||x||^2 - 2 q.x) + 2 c sum(q) - c^2 pd          (L2)
+//     -q'.x' - c sum(x)  = -q.x + c sum(q) - c^2 pd                          (inner product)
+// so the GEMM value of the fp32 form is, per query, the integer GEMM plus a constant
+// delta_q = M c sum(q) - c^2 pd (M = 2 for L2, 1 for inner product).  The accumulator runs
+//     u = init(x) + q'.x'      init = -ceil(||x'||^2 / 2) (L2)  or  c sum(x) (inner product)
+// exactly in int32, and value = -M u - delta_q.  For inner product that is the GEMM value
+// exactly; for L2 it is the GEMM value plus (||x'||^2 mod 2), so at most 1 above it: the
+// batch carries a bound eb = 1 and the exact re-scoring decides, as on every inexact path.
+// The threshold test value <= T becomes u >= ceil((-T - delta_q) / M): one integer compare
+// per value, the same count as the fp16 GEMM's.  Rows that take no part start from -2^29,
+// below any threshold and any group maximum of a live row.
+#include <algorithm>
+#include <cmath>
+#include <string>
+#include <type_traits>
+
+#include "gemm.h"
+#include "vdbg_device.h"
+#include "vdbg_internal.h"
+
+namespace vdbg {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kDead8 = -(1 << 29);   // accumulator start of rows that take no part
+constexpr int kLive8 = -(1 << 28);   // every live row's u is above this
+
+// Block = 4 waves x (32 QB) queries each x one chunk of rows, blocks mapped to work items
+// XCD by XCD; rows stream through double-buffered 64-row LDS stages (K chunks of KC dims for
+// rows wider than 128), row starts through three slots.
+//
+// Operand layout of v_mfma_i32_32x32x32_i8: per 32-dim K block, lane l holds 16 bytes, dims
+// 16 (l / 32) .. 16 (l / 32) + 15 of row l % 32 (A, from LDS) and of query l % 32 (B, in
+// VGPRs); both operands use the same dim of a lane's byte, so the contraction covers every
+// dim once whatever order the unit sums in (integer sums are exact in any order).  Lane l's
+// 16 outputs are rows 8 (r / 4) + 4 (l / 32) + r % 4 of the 32-row block against query l % 32.
+//
+// MODE 0: every value at or below the query's threshold T goes to the lane's candidate
+// buffer; MODE 1: the minimum value of each 16-row group (the sample pass).
+template <int PD, int METRIC, int QB, int MODE>
+__global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
+  constexpr int KC = Gemm8Kc(PD);
+  constexpr int NKC = PD / KC;
+  constexpr int NKB = KC / 32;                     // 32-dim MFMA K blocks per stage
+  constexpr int STR = KC + 16;                     // LDS row stride in bytes (16 B padding)
+  constexpr int VEC_PER_ROW = KC / 16;             // 16-byte vectors per stage row
+  constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
+  constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
+  constexpr int QT = 128 * QB;                     // queries per block
+  constexpr int M = METRIC == 0 ? 2 : 1;
+  static_assert(PD % KC == 0 && KC % 32 == 0, "K chunking");
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][kGemmRows * STR];
+  __shared__ __attribute__((aligned(16))) int xns[3][kGemmRows];
+
+  const int b = blockIdx.x;
+  const int item = (b & 7) * a.per_xcd + (b >> 3);
+  if (item >= a.items) return;
+  const int chunk = item / a.nqt;
+  const int qt = item - chunk * a.nqt;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int j = lane & 31;
+  const int h = lane >> 5;
+  const int q0 = qt * QT + wave * 32 * QB;
+  const bool wave_live = q0 < a.nq;
+  const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
+  const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
+
+  int q[QB], ui[QB], dq[QB];
+  uint2* out[QB];
+  uint32_t cnt[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    q[qb] = q0 + qb * 32 + j;
+    cnt[qb] = 0;
+    dq[qb] = a.Qd[min(q[qb], a.nq - 1)];
+    if constexpr (MODE == 0) {
+      // value <= T  <=>  u >= ceil((-T - delta) / M); +inf admits every live row, -inf (a
+      // lane past the batch) none
+      const float T = q[qb] < a.nq ? a.T[q[qb]] : -__builtin_inff();
+      const double t = ceil((-double(T) - double(dq[qb])) / M);
+      ui[qb] = !(t <= double(1 << 30)) ? (1 << 30) : (t < double(kLive8) ? kLive8 : int(t));
+      out[qb] = a.cand + ((size_t(q[qb]) * a.nchunks + chunk) * 2 + h) * size_t(a.caph);
+    }
+  }
+
+  // Loads are unconditional (addresses clamped), as in the fp16 GEMM, so the waits before
+  // the LDS stores never drain the prefetch early.
+  constexpr int QF = NKC > 1 ? 2 : 1;
+  v4i qv[QF][QB][NKB];
+  const int8_t* qrow[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) qrow[qb] = a.Q8 + size_t(min(q[qb], a.nq - 1)) * PD + h * 16;
+  auto load_q = [&](int f, int kc) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb)
+        qv[f][qb][kb] = *reinterpret_cast<const v4i*>(qrow[qb] + kc * KC + kb * 32);
+  };
+  load_q(0, 0);
+
+  // byte offsets of the stage's 16-byte vectors: row f / VEC_PER_ROW, column f % VEC_PER_ROW
+  int voff[VEC_PER_THREAD];
+  int vrow[VEC_PER_THREAD];
+#pragma unroll
+  for (int i = 0; i < VEC_PER_THREAD; ++i) {
+    const int f = min(tid + 256 * i, VEC_PER_TILE - 1);
+    vrow[i] = f / VEC_PER_ROW;
+    voff[i] = vrow[i] * PD + (f % VEC_PER_ROW) * 16;
+  }
+  // Stages s = tile * NKC + kc (64 rows x KC dims), stage s + 2 loaded while stage s is
+  // multiplied, two register sets swapping roles each step, as in the fp16 GEMM.
+  struct Stage {
+    u32x4 v[VEC_PER_THREAD];
+    int n;
+    uint32_t aw;  // filter bits of the lane's half of the tile
+  };
+  const int ntiles = int((r_end - r_begin + kGemmRows - 1) / kGemmRows);
+  const int nstages = ntiles * NKC;
+  auto load_stage = [&](Stage& st, int sidx) {
+    sidx = min(sidx, nstages - 1);
+    const int tile = sidx / NKC, kc = sidx - tile * NKC;
+    const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
+    const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
+    const char* src = reinterpret_cast<const char*>(a.X8 + size_t(base) * PD + kc * KC);
+    if (valid == kGemmRows) {
+#pragma unroll
+      for (int i = 0; i < VEC_PER_THREAD; ++i)
+        st.v[i] = *reinterpret_cast<const u32x4*>(src + uint32_t(voff[i]));
+    } else {  // rows past the end read row valid - 1
+      const int over = int(valid) - 1;
+#pragma unroll
+      for (int i = 0; i < VEC_PER_THREAD; ++i) {
+        const int o = voff[i] - max(0, vrow[i] - over) * PD;
+        st.v[i] = *reinterpret_cast<const u32x4*>(src + uint32_t(o));
+      }
+    }
+    st.n = a.rn8[base + min(uint32_t(tid & 63), valid - 1)];
+    if constexpr (MODE == 0)
+      st.aw = a.aw[((base >> 5) + (uint32_t(tid & 63) >> 5)) & a.aw_mask];
+  };
+  auto store_stage = [&](const Stage& st, int sidx) {
+    const int tile = sidx / NKC, kc = sidx - tile * NKC;
+    const int buf = sidx & 1;
+#pragma unroll
+    for (int i = 0; i < VEC_PER_THREAD; ++i) {
+      const int f = tid + 256 * i;
+      if (VEC_PER_TILE % 256 == 0 || f < VEC_PER_TILE)
+        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) = st.v[i];
+    }
+    if (kc == 0 && tid < kGemmRows) {
+      const uint32_t valid = min(uint32_t(kGemmRows), r_end - (r_begin + uint32_t(tile) * kGemmRows));
+      const bool ok = uint32_t(tid) < valid && (MODE != 0 || ((st.aw >> (tid & 31)) & 1u));
+      xns[tile % 3][tid] = ok ? st.n : kDead8;
+    }
+  };
+
+  v16i acc[QB][2];
+  auto step = [&](Stage& X, Stage& Y, int sidx, auto fcur) {
+    constexpr int QS = decltype(fcur)::value;
+    const int tile = sidx / NKC, kc = sidx - tile * NKC;
+    const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
+    if constexpr (QF == 2) load_q(QS ^ 1, (kc + 1 == NKC) ? 0 : kc + 1);
+    load_stage(Y, sidx + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kc == 0) {
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk) {
+        v16i init;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int4 n4 = *reinterpret_cast<const int4*>(&xns[tile % 3][blk * 32 + 8 * g + 4 * h]);
+          init[4 * g + 0] = n4.x;
+          init[4 * g + 1] = n4.y;
+          init[4 * g + 2] = n4.z;
+          init[4 * g + 3] = n4.w;
+        }
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) acc[qb][blk] = init;
+      }
+    }
+    const uint8_t* xa0 = &xs[sidx & 1][j * STR + h * 16];
+    const uint8_t* xa1 = xa0 + 32 * STR;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) {
+      const v4i x0 = *reinterpret_cast<const v4i*>(xa0 + kb * 32);
+      const v4i x1 = *reinterpret_cast<const v4i*>(xa1 + kb * 32);
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        acc[qb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, qv[QS][qb][kb], acc[qb][0], 0, 0, 0);
+        acc[qb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, qv[QS][qb][kb], acc[qb][1], 0, 0, 0);
+      }
+    }
+    if (sidx + 1 < nstages) store_stage(X, sidx + 1);
+    __syncthreads();
+    if (kc != NKC - 1) return;
+
+    const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
+    if (wave_live && MODE == 0) {
+      // per 32-row block: the lane's largest u against the bound, one wave-uniform branch;
+      // only a block passing on some lane tests its values one by one
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          int m = acc[qb][blk][0];
+#pragma unroll
+          for (int r = 1; r < 16; ++r) m = max(m, acc[qb][blk][r]);
+          if (__builtin_amdgcn_ballot_w64(m >= ui[qb]) == 0) continue;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int u = acc[qb][blk][r];
+            if (__builtin_amdgcn_ballot_w64(u >= ui[qb]) != 0) {
+              const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
+              if (u >= ui[qb]) {
+                if (cnt[qb] < uint32_t(a.caph))
+                  out[qb][cnt[qb]] = make_uint2(__float_as_uint(float(-M * u - dq[qb])), row);
+                ++cnt[qb];
+              }
+            }
+          }
+        }
+    } else if (wave_live) {
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+        for (int blk = 0; blk < 2; ++blk) {
+          int m = kDead8;
+          if (a.allow == nullptr) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) m = max(m, acc[qb][blk][r]);
+          } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
+              if (row < r_end && row_allowed(a.allow, a.rid[row])) m = max(m, acc[qb][blk][r]);
+            }
+          }
+          if (q[qb] < a.nq) {
+            const uint32_t grp = ((base >> 5) + blk) * 2 + h;
+            if (grp < uint32_t(a.ngroups))
+              a.gm[size_t(q[qb]) * a.ngroups + grp] =
+                  m < kLive8 ? __builtin_inff() : float(-M * m - dq[qb]);
+          }
+        }
+    }
+  };
+
+  if (r_begin >= r_end) return;
+  Stage A, B;
+  load_stage(B, 0);
+  load_stage(A, 1);
+  store_stage(B, 0);
+  __syncthreads();
+  for (int sidx = 0; sidx < nstages; sidx += 2) {
+    step(A, B, sidx, std::integral_constant<int, 0>{});
+    if (sidx + 1 < nstages) step(B, A, sidx + 1, std::integral_constant<int, QF - 1>{});
+  }
+
+  if constexpr (MODE == 0) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (q[qb] < a.nq) {
+        const size_t seg = (size_t(q[qb]) * a.nchunks + chunk) * 2 + h;
+        a.counts[seg] = min(cnt[qb], uint32_t(a.caph));
+        if (cnt[qb] > uint32_t(a.caph)) a.ovf[q[qb]] = 1;
+      }
+    }
+  }
+}
+
+template <int PD, int METRIC>
+static void launch8_pm(int qb, int mode, hipStream_t s, int blocks, const GemmArgs& a) {
+  const dim3 g(blocks), t(256);
+  if (mode == 1)
+    k_gemm8<PD, METRIC, 2, 1><<<g, t, 0, s>>>(a);
+  else if (qb == 1)
+    k_gemm8<PD, METRIC, 1, 0><<<g, t, 0, s>>>(a);
+  else
+    k_gemm8<PD, METRIC, 2, 0><<<g, t, 0, s>>>(a);
+}
+
+template <int PD>
+static void launch8_pd(int metric, int qb, int mode, hipStream_t s, int blocks, const GemmArgs& a) {
+  if (metric == 0)
+    launch8_pm<PD, 0>(qb, mode, s, blocks, a);
+  else
+    launch8_pm<PD, 1>(qb, mode, s, blocks, a);
+}
+
+int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+                const GemmArgs& a) {
+  if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM8: query blocks per wave");
+  if (mode == 1 && qb != 2) return SetError(kInternal, "GEMM8: the sample pass runs 2 blocks");
+  switch (pd) {
+#define VDBG_PD8(P) \
+  case P: launch8_pd<P>(metric, qb, mode, s, blocks, a); break;
+    VDBG_PD8(32) VDBG_PD8(64) VDBG_PD8(96) VDBG_PD8(128) VDBG_PD8(192) VDBG_PD8(256)
+    VDBG_PD8(384) VDBG_PD8(512) VDBG_PD8(768) VDBG_PD8(960) VDBG_PD8(1024)
+#undef VDBG_PD8
+    default: return SetError(kNotSupported, "GEMM8: unsupported padded_dim");
+  }
+  return kOk;
+}
+
+// One wave per row: x' = x - c as int8 and the accumulator start, -ceil(||x'||^2 / 2) (L2)
+// or c sum(x) (inner product).
+__global__ __launch_bounds__(256) void k_to_i8(const float* __restrict__ X, uint32_t n, int pd,
+                                               int c, int metric, int8_t* __restrict__ y,
+                                               int* __restrict__ init) {
+  const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= n) return;
+  int sq = 0, sx = 0;
+  for (int i = lane_id(); i < pd; i += kWave) {
+    const int x = int(X[size_t(r) * pd + i]);
+    const int xp = x - c;
+    y[size_t(r) * pd + i] = int8_t(xp);
+    sq += xp * xp;
+    sx += x;
+  }
+  for (int o = kWave / 2; o > 0; o >>= 1) {
+    sq += __shfl_xor(sq, o);
+    sx += __shfl_xor(sx, o);
+  }
+  if (lane_id() == 0) init[r] = metric == 0 ? -((sq + 1) >> 1) : c * sx;
+}
+
+int MakeRows8(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int metric,
+              const RowStats& st, int8_t** out, int** init, int* shift) {
+  *out = nullptr;
+  *init = nullptr;
+  *shift = 0;
+  if (n == 0 || !Gemm8Supported(pd) || !st.all_int || !(st.max_abs <= 2048.f)) return kOk;
+  const double lo = st.lo, hi = st.hi;
+  if (hi - lo > 255.0) return kOk;
+  // centre the rows' range in [-128, 127], leaving queries equal room on both sides
+  const int cs = int(lo) + 128 - int((255.0 - (hi - lo)) / 2);
+  // every accumulator start stays inside (-2^27, 2^27): live rows' u inside (-2^28, 2^28)
+  if (double(pd) * 2048.0 * (std::abs(cs) + 1.0) >= 134217728.0) return kOk;
+  int8_t* y = nullptr;
+  int* in = nullptr;
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd));
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&in), n * sizeof(int));
+  if (e != hipSuccess) {
+    (void)hipFree(y);
+    return SetError(kResourceExhausted, std::string("int8 rows: ") + hipGetErrorString(e));
+  }
+  k_to_i8<<<dim3(unsigned((n + 3) / 4)), 256, 0, s>>>(rows, uint32_t(n), int(pd), cs, metric, y, in);
+  e = hipGetLastError();
+  if (e != hipSuccess) {
+    (void)hipFree(y);
+    (void)hipFree(in);
+    return SetError(kInternal, std::string("int8 rows: ") + hipGetErrorString(e));
+  }
+  *out = y;
+  *init = in;
+  *shift = cs;
+  return kOk;
+}
+
+}  // namespace vdbg

@@ -319,10 +319,12 @@ int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* sca
 // sample is an evenly strided subset of the rows.
 __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __restrict__ X16,
                                 int pd16, const uint8_t* __restrict__ C,
+                                const int8_t* __restrict__ X8, const int* __restrict__ init8,
                                 const float* __restrict__ rn, uint32_t N, int pd, int bits,
                                 uint32_t smax,
                                 float* __restrict__ SX, uint16_t* __restrict__ SX16,
-                                uint8_t* __restrict__ SC, float* __restrict__ Srn,
+                                uint8_t* __restrict__ SC, int8_t* __restrict__ SX8,
+                                int* __restrict__ Sinit8, float* __restrict__ Srn,
                                 uint32_t* __restrict__ Sid) {
   const uint32_t p = blockIdx.x;
   if (p >= smax) return;
@@ -330,12 +332,14 @@ __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __r
   for (int i = threadIdx.x; i < pd; i += blockDim.x) {
     if (X) SX[size_t(p) * pd + i] = X[size_t(row) * pd + i];
     if (C) SC[size_t(p) * pd + i] = C[size_t(row) * pd + i];
+    if (X8) SX8[size_t(p) * pd + i] = X8[size_t(row) * pd + i];
   }
   for (int i = threadIdx.x; X16 != nullptr && i < pd16; i += blockDim.x)
     SX16[size_t(p) * pd16 + i] = X16[size_t(row) * pd16 + i];
   if (threadIdx.x == 0) {
     Srn[p] = rn[row];
     Sid[p] = row;
+    if (X8) Sinit8[p] = init8[row];
   }
 }
 
@@ -351,7 +355,8 @@ size_t SampleBytes(const ScanSource& src, uint32_t smax) {
   return al(src.kind == 0 ? size_t(smax) * pd * sizeof(float) : 0) +
          al(src.X16 != nullptr ? size_t(smax) * pd * src.x16_parts * sizeof(uint16_t) : 0) +
          al(src.kind == 1 ? size_t(smax) * pd : 0) + al(size_t(smax) * sizeof(float)) +
-         al(size_t(smax) * sizeof(uint32_t)) + 256;
+         al(size_t(smax) * sizeof(uint32_t)) +
+         (src.X8 != nullptr ? al(size_t(smax) * pd) + al(size_t(smax) * sizeof(int)) : 0) + 256;
 }
 
 int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
@@ -371,11 +376,14 @@ int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
   src->SC = reinterpret_cast<uint8_t*>(take(src->kind == 1 ? size_t(smax) * pd : 0));
   src->Srn = reinterpret_cast<float*>(take(size_t(smax) * sizeof(float)));
   src->Sid = reinterpret_cast<uint32_t*>(take(size_t(smax) * sizeof(uint32_t)));
+  src->SX8 = reinterpret_cast<int8_t*>(take(src->X8 != nullptr ? size_t(smax) * pd : 0));
+  src->Sinit8 = reinterpret_cast<int*>(take(src->X8 != nullptr ? size_t(smax) * sizeof(int) : 0));
   k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
                                              src->X16, int(pd) * src->x16_parts,
-                                             src->kind == 1 ? src->C : nullptr, src->rn,
-                                             src->N, int(pd), bits, smax, src->SX, src->SX16,
-                                             src->SC, src->Srn, src->Sid);
+                                             src->kind == 1 ? src->C : nullptr, src->X8,
+                                             src->init8, src->rn, src->N, int(pd), bits, smax,
+                                             src->SX, src->SX16, src->SC, src->SX8,
+                                             src->Sinit8, src->Srn, src->Sid);
   VDBG_HIP(hipGetLastError());
   src->Smax = smax;
   return kOk;
@@ -402,6 +410,8 @@ void FreeSample(ScanSource* src) {
   src->Sbuf = nullptr;
   src->SX = nullptr;
   src->SX16 = nullptr;
+  src->SX8 = nullptr;
+  src->Sinit8 = nullptr;
   src->SC = nullptr;
   src->Srn = nullptr;
   src->Sid = nullptr;
@@ -426,6 +436,10 @@ struct PrepArgs {
   float* Qf;      // split operands: per-query factor taking the split GEMM back to GEMM units
   int x16_parts;  // flat rows: 2 when they are held as scaled fp16 h + l pairs
   int x16_exp;    // their scale exponent
+  int8_t* Q8;     // nullable: the int8 GEMM's B operand, q - c8 (gemm8.hip)
+  int* Qd;        // its per-query constant M c8 sum(q) - c8^2 pd
+  int* all8;      // cleared when a query is outside the int8 GEMM's bounds
+  int c8;
 };
 
 // One wave per query.
@@ -444,7 +458,8 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
   if (q >= a.nq) return;
   const float* v = a.Q + size_t(q) * a.pd;
   float s = 0.f, s2 = 0.f, lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f;
-  int ai = 1;
+  float sq = 0.f;  // sum(q) (exact: integers of magnitude < 2^24 when the int8 GEMM applies)
+  int ai = 1, in8 = 1;
   for (int i = lane_id(); i < a.pd; i += kWave) {
     const float e = v[i];
     s = fmaf(e, e, s);
@@ -452,6 +467,12 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     hi = fmaxf(hi, e);
     ma = fmaxf(ma, fabsf(e));
     ai &= (e == rintf(e)) ? 1 : 0;
+    if (a.Q8 != nullptr) {  // q - c8, in range when the batch takes the int8 GEMM
+      const float d = e - float(a.c8);
+      in8 &= (d >= -128.f && d <= 127.f) ? 1 : 0;
+      a.Q8[size_t(q) * a.pd + i] = int8_t(int(fminf(fmaxf(d, -128.f), 127.f)));
+      sq += e;
+    }
     if (a.Q16 != nullptr && a.kind == 0 && a.x16_parts == 1)  // -2 q (L2) or -q (IP)
       a.Q16[size_t(q) * a.pd + i] =
           __builtin_bit_cast(uint16_t, _Float16(a.metric == 0 ? -2.f * e : -e));
@@ -472,6 +493,10 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
   hi = wave_max(hi);
   ma = wave_max(ma);
   ai = wave_and(ai);
+  if (a.Q8 != nullptr) {
+    sq = wave_sum(sq);
+    in8 = wave_and(in8);
+  }
   // SQ8 on the fp16 GEMM: B scaled by 2^sc (max |B| 2^sc in [2^14, 2^15)) and split into
   // fp16 h + l, |B 2^sc - h - l| <= 2^-22 |B 2^sc| (+ subnormal terms); codes are exact in
   // fp16, so the GEMM runs as c.h + c.l and Qf = -2 (L2) or -1 (IP) times 2^-sc takes it back
@@ -528,7 +553,7 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
       qmag = a.metric == 0 ? s + s2 : s;
     }
     a.shift[q] = shift;
-    a.exact[q] = ex ? 1 : 0;
+    bool half_norm = false;  // L2 on the int8 GEMM: values up to 1 above the GEMM value
     // fp16 holds every integer of magnitude <= 2048 exactly (and -2 q, an even integer of
     // magnitude <= 4096); the fp16 GEMM accumulates ||x||^2 - 2 q.x (or -q.x) from the row
     // norm, every partial sum bounded by (|q| + R)^2 with R the largest row norm.  Below 2^24
@@ -541,6 +566,17 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
       const bool fits = ex && ma <= 2048.f && a.xs.max_abs <= 2048.f &&
                         (rq + rx) * (rq + rx) * 1.001 < lim;
       if (!fits) atomicAnd(a.all16, 0);
+      if (a.Q8 != nullptr) {
+        // the int8 GEMM: the same bounds, every q - c8 an int8, and its constant in int32
+        const double c = a.c8;
+        const double d = (a.metric == 0 ? 2.0 : 1.0) * c * double(sq) - c * c * pd;
+        const bool fits8 = fits && in8 && fabs(d) < 268435456.0;
+        a.Qd[q] = fits8 ? int(d) : 0;
+        if (!fits8) atomicAnd(a.all8, 0);
+        // L2 values on the int8 GEMM may exceed the GEMM value by 1 (the rounded half
+        // norm): such a query carries that bound whichever GEMM the batch takes
+        half_norm = fits8 && a.metric == 0;
+      }
     }
     // Rounding bound of |GEMM value + shift - exact distance|.  Any fp32 summation order of
     // n products errs by at most ~n u sum|q_i x_i| (u = 2^-24), and sum|q_i x_i| <= |q||x|.
@@ -570,8 +606,10 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
                       : (4.0 * pd + 16.0 + 6.0 * pd + 48.0) * u * (double(qmag) + double(a.rmag)) +
                             2.0 * fsub;
     const bool split = a.Q16 != nullptr && (a.kind == 1 || a.x16_parts == 2);
-    a.eb[q] = ex ? 0.f
-                 : float((split ? (a.kind == 1 ? bound16 : bound16f) : bound) * 1.001);
+    a.exact[q] = ex && !half_norm ? 1 : 0;
+    a.eb[q] = half_norm ? 1.f
+                        : ex ? 0.f
+                             : float((split ? (a.kind == 1 ? bound16 : bound16f) : bound) * 1.001);
   }
 }
 
@@ -1357,6 +1395,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int slots = 2 * c->cu_count;
   const bool try16 = c->fp16_gemm && src->X16 != nullptr;
   const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
+  // integer rows spanning at most 256 values may rank on the int8 GEMM (gemm8.hip)
+  const bool try8 = try16 && c->int8_gemm && split == 0 && src->X8 != nullptr;
   // Sample size: about kk * N / S rows pass the threshold per query, and every pass costs a
   // scattered buffer write and a select insertion (and on the exact fp16 GEMM every 32-row
   // block holding one takes the per-value test), while the pre-pass costs S / N of the main
@@ -1364,7 +1404,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // for large batches on the exact fp16 GEMM, whose MFMA work per row is smallest, 640
   // otherwise (N / 64 at k = 10).
   uint32_t S = 1;
-  const uint64_t passes = try16 && split == 0 && nq >= 1024 ? 160 : 640;
+  const uint64_t passes = try16 && split == 0 && nq >= 1024 ? 160 : 640;  // (int8 too)
   const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,
                                               uint64_t(N) * kk / passes});
   while (S < s_want && S < (1u << 30)) S *= 2;
@@ -1410,7 +1450,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
                       size_t(nq) * ngroups * sizeof(float) + cand_need +
                       (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
-                      20 * 256;
+                      (try8 ? nq * pd + nq * sizeof(int) : 0) + 22 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
@@ -1425,16 +1465,19 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   char* cand_base = w.take<char>(cand_need);
   uint16_t* Q16 = try16 ? w.take<uint16_t>((split ? 2 : 1) * nq * pd) : nullptr;
   float* Qf = try16 && split ? w.take<float>(nq) : nullptr;
-  int* all16 = try16 ? w.take<int>(1) : nullptr;
+  int* all16 = try16 ? w.take<int>(2) : nullptr;  // [0] fp16 bounds, [1] int8 bounds
+  int* all8 = try8 ? all16 + 1 : nullptr;
+  int8_t* Q8 = try8 ? w.take<int8_t>(nq * pd) : nullptr;
+  int* Qd = try8 ? w.take<int>(nq) : nullptr;
   uint32_t* ones = try16 ? w.take<uint32_t>(1) : nullptr;  // the fp16 GEMM's no-filter word
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
   VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
-  if (try16) VDBG_HIP(hipMemsetD32Async(all16, 1, 1, s));
+  if (try16) VDBG_HIP(hipMemsetD32Async(all16, 1, 2, s));
   if (try16) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
-              src->x16_exp};
+              src->x16_exp, Q8, Qd, all8, src->c8};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
@@ -1444,14 +1487,15 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // reads the flag.  The split operands need no such check: a non-finite query only yields
   // NaN or infinite GEMM values and bound, its certificate fails and it is re-scanned
   // exactly, as on the fp32 GEMM.
-  bool use16 = try16 && split != 0;
+  bool use16 = try16 && split != 0, use8 = false;
   if (try16 && split == 0) {
-    VDBG_HIP(hipMemcpyAsync(c->host_pinned, all16, sizeof(int), hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipMemcpyAsync(c->host_pinned, all16, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
     VDBG_HIP(hipStreamSynchronize(s));
-    use16 = c->host_pinned[0] != 0;
+    use8 = try8 && c->host_pinned[1] != 0;
+    use16 = !use8 && c->host_pinned[0] != 0;
   }
-  c->last_gemm_bits = use16 ? 16 : 32;
-  const Plan& P = use16 ? p16 : p32;
+  c->last_gemm_bits = use8 ? 8 : (use16 ? 16 : 32);
+  const Plan& P = use8 || use16 ? p16 : p32;
   const int nchunks = P.nchunks;
   const int caph = P.caph;
   const int nseg = P.nseg;
@@ -1477,7 +1521,14 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   int sblocks = 0;
   {
     ProfScope ps(c, "sample_gemm", s);
-    if (use16 && P.qb == 2) {
+    if (use8 && P.qb == 2) {
+      sg.X8 = src->SX8;
+      sg.rn8 = src->Sinit8;
+      sg.Q8 = Q8;
+      sg.Qd = Qd;
+      GemmGrid(sg, P.nqt, P.schunks, &sblocks);
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, 1, s, sblocks, sg));
+    } else if (use16 && P.qb == 2) {
       sg.X16 = src->SX16;
       sg.Q16 = Q16;
       sg.Qf = Qf;
@@ -1517,7 +1568,15 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   GemmGrid(ga, P.nqt, nchunks, &blocks);
   {
     ProfScope ps(c, src->kind == 0 ? "flat_gemm" : "sq8_gemm", s);
-    if (use16) {
+    if (use8) {
+      ga.X8 = src->X8;
+      ga.rn8 = src->init8;
+      ga.Q8 = Q8;
+      ga.Qd = Qd;
+      ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
+      ga.aw_mask = allow != nullptr ? ~0u : 0u;
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, P.qb, 0, s, blocks, ga));
+    } else if (use16) {
       ga.X16 = src->X16;
       ga.Q16 = Q16;
       ga.Qf = Qf;

@@ -70,6 +70,12 @@ __global__ void k_gather_f(const float* __restrict__ src, const uint32_t* __rest
   if (t < n) dst[t] = src[ids[t]];
 }
 
+__global__ void k_gather_u32(const uint32_t* __restrict__ src, const uint32_t* __restrict__ ids,
+                             uint32_t n, uint32_t* __restrict__ dst) {
+  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < n) dst[t] = src[ids[t]];
+}
+
 __global__ void k_map_ids(uint32_t* __restrict__ out, size_t n, const uint32_t* __restrict__ ids) {
   const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
   if (t < n && out[t] != kNoId) out[t] = ids[out[t]];
@@ -105,12 +111,15 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t row_bytes = src->kind == 0 ? pd * sizeof(float) : pd;
   void* buf = nullptr;
   const size_t row16_bytes = src->X16 != nullptr ? src->x16_parts * pd * sizeof(uint16_t) : 0;
+  const size_t row8_bytes = src->X8 != nullptr ? pd : 0;  // and the int8 copy's start
   // the compacted source's sample lives in the same stream-ordered allocation
   ScanSource cs = *src;
   cs.N = count;
   const size_t sample_bytes = SampleBytes(cs, SampleRows(count));
   const size_t bytes = (nwords + 1) * 4 * 2 +
-                       size_t(count) * (4 + 4 + row_bytes + row16_bytes) + sample_bytes + 4096;
+                       size_t(count) * (4 + 4 + row_bytes + row16_bytes + row8_bytes +
+                                        (row8_bytes != 0 ? 4 : 0)) +
+                       sample_bytes + 4096 + 512;
   VDBG_HIP(hipMallocAsync(&buf, bytes, s));
   char* p = static_cast<char*>(buf);
   auto take = [&](size_t b) {
@@ -124,6 +133,8 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   float* rn = reinterpret_cast<float*>(take(size_t(count) * 4 + 4));
   void* rows = take(size_t(count) * row_bytes + 16);
   void* rows16 = row16_bytes != 0 ? take(size_t(count) * row16_bytes + 16) : nullptr;
+  void* rows8 = row8_bytes != 0 ? take(size_t(count) * row8_bytes + 16) : nullptr;
+  int* init8 = row8_bytes != 0 ? reinterpret_cast<int*>(take(size_t(count) * 4 + 4)) : nullptr;
   void* sample = take(sample_bytes);
   void* tmp = nullptr;
   {
@@ -148,11 +159,21 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
           reinterpret_cast<const uint4*>(src->X16), row_u4, ids, count, static_cast<uint4*>(rows16));
     }
+    if (rows8 != nullptr) {
+      const size_t row_u4 = row8_bytes / 16;
+      k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
+          reinterpret_cast<const uint4*>(src->X8), row_u4, ids, count, static_cast<uint4*>(rows8));
+      k_gather_u32<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(
+          reinterpret_cast<const uint32_t*>(src->init8), ids, count,
+          reinterpret_cast<uint32_t*>(init8));
+    }
     k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
     VDBG_HIP(hipGetLastError());
   }
   cs.X = src->kind == 0 ? static_cast<const float*>(rows) : nullptr;
   cs.X16 = static_cast<const uint16_t*>(rows16);
+  cs.X8 = static_cast<const int8_t*>(rows8);
+  cs.init8 = init8;
   cs.C = src->kind == 1 ? static_cast<const uint8_t*>(rows) : nullptr;
   cs.rn = rn;
   cs.Sbuf = nullptr;

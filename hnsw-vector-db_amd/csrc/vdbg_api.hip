@@ -148,9 +148,22 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
       return rc;
     }
   }
+  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr && d.rows16_parts == 1) {
+    rc = MakeRows8(c, c->stream, d.rows, n, pd, metric, d.stats, &d.rows8, &d.init8, &d.c8);
+    if (rc != kOk) {
+      (void)hipFree(d.rows16);
+      (void)hipFree(d.rows);
+      (void)hipFree(d.norms);
+      delete ds;
+      return rc;
+    }
+  }
   d.src.kind = 0;
   d.src.X = d.rows;
   d.src.X16 = d.rows16;
+  d.src.X8 = d.rows8;
+  d.src.init8 = d.init8;
+  d.src.c8 = d.c8;
   d.src.x16_parts = d.rows16_parts;
   d.src.x16_exp = d.rows16_exp;
   d.src.rn = d.norms;
@@ -323,6 +336,13 @@ int vdbg_ctx_set_fp16_gemm(vdbg_ctx* ctx, int enable) {
   return kOk;
 }
 
+int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.int8_gemm = enable != 0;
+  return kOk;
+}
+
 int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   if (ctx == nullptr) return kOk;
   Ctx& c = ctx->c;
@@ -415,6 +435,8 @@ int vdbg_dataset_destroy(vdbg_dataset* ds) {
   (void)hipFree(ds->d.norms);
   if (ds->d.rows16 != nullptr) (void)hipFree(ds->d.rows16);
   if (ds->d.ext_ids != nullptr) (void)hipFree(ds->d.ext_ids);
+  if (ds->d.rows8 != nullptr) (void)hipFree(ds->d.rows8);
+  if (ds->d.init8 != nullptr) (void)hipFree(ds->d.init8);
   delete ds;
   return kOk;
 }

@@ -90,11 +90,12 @@ struct Ctx {
   std::vector<hipEvent_t> free_events;
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
   uint64_t last_fallbacks = 0;
-  int last_gemm_bits = 0;  // input width of the last scan's main GEMM: 32, 16 (exact), 0
+  int last_gemm_bits = 0;  // input width of the last scan's main GEMM: 32, 16, 8 or 0
   int cu_count = 256;
   int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
   bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
+  bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 
@@ -109,6 +110,9 @@ struct ScanSource {
                                   // per K chunk), kind 1 codes exactly (x16_parts 1)
   int x16_parts = 1;
   int x16_exp = 0;
+  const int8_t* X8 = nullptr;   // kind 0 rows - c8 as int8 for the int8 GEMM (gemm8.hip), or null
+  const int* init8 = nullptr;   // its accumulator start per row
+  int c8 = 0;
   const uint8_t* C = nullptr;   // kind 1: n x pd codes
   const float* rn = nullptr;    // ||x||^2 (flat) or ||code * scale||^2 (SQ8)
   const float* vmin = nullptr;  // SQ8 quantizer (device)
@@ -119,6 +123,8 @@ struct ScanSource {
   RowStats stats;               // flat: value statistics for the exactness test
   float* SX = nullptr;          // sample rows (kind 0)
   uint16_t* SX16 = nullptr;     // sample rows of X16 (same layout)
+  int8_t* SX8 = nullptr;        // sample rows of X8
+  int* Sinit8 = nullptr;
   uint8_t* SC = nullptr;        // sample codes (kind 1)
   float* Srn = nullptr;
   uint32_t* Sid = nullptr;
@@ -132,6 +138,9 @@ struct Dataset {
   float* norms = nullptr;  // n row norms (fp32, ||x||^2)
   uint16_t* rows16 = nullptr;  // fp16 copy of the rows (see ScanSource::X16)
   int rows16_parts = 1, rows16_exp = 0;
+  int8_t* rows8 = nullptr;     // int8 copy of the rows (see ScanSource::X8)
+  int* init8 = nullptr;
+  int c8 = 0;
   size_t n = 0, dim = 0, pd = 0;
   int metric = 0;
   RowStats stats;
@@ -196,6 +205,10 @@ int MakeCodes16(Ctx* c, hipStream_t s, const uint8_t* codes, size_t n, size_t pd
 // GEMM kernel.
 int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int* parts, int* exp,
                const RowStats& st, uint16_t** out);
+// int8 copy of integer rows spanning at most 256 values, shifted by *shift, with each row's
+// accumulator start (gemm8.hip); *out stays null when not applicable.
+int MakeRows8(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int metric,
+              const RowStats& st, int8_t** out, int** init, int* shift);
 
 // Top-kk rows by the source's exact distance for nq queries (device pointers).
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,

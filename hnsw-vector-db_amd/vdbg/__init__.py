@@ -58,6 +58,7 @@ _SIGS = {
     "vdbg_ctx_set_kernels": (C.c_int, [_vp, C.c_char_p]),
     "vdbg_ctx_kernels": (C.c_char_p, [_vp]),
     "vdbg_ctx_set_fp16_gemm": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_int8_gemm": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_reset": (C.c_int, [_vp]),
     "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
@@ -183,6 +184,11 @@ class Context:
         GEMM.  Results are identical."""
         _check(lib.vdbg_ctx_set_fp16_gemm(self.h, 1 if enable else 0))
 
+    def set_int8_gemm(self, enable=True):
+        """Let integer flat rows spanning at most 256 values rank on int8 MFMA (the
+        default).  Results are identical."""
+        _check(lib.vdbg_ctx_set_int8_gemm(self.h, 1 if enable else 0))
+
     def profile(self, enable=True):
         _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))
 
@@ -196,7 +202,7 @@ class Context:
         return ms.value, n.value
 
     def last_gemm_bits(self):
-        """Input width of the last scan's ranking GEMM: 32, 16 (exact integers) or 0."""
+        """Input width of the last scan's ranking GEMM: 32, 16, 8 (integers) or 0."""
         return lib.vdbg_last_gemm_bits(self.h)
 
     def last_fallbacks(self):

@@ -90,6 +90,12 @@ const char* vdbg_ctx_kernels(vdbg_ctx* ctx);
  * SQ8 indexes 2 bytes per code).  Returned results are identical either way; 0 ranks on the
  * fp32 GEMM.  No counterpart in the reference. */
 int vdbg_ctx_set_fp16_gemm(vdbg_ctx* ctx, int enable);
+/* Whether integer-valued flat rows spanning at most 256 consecutive values may rank on int8
+ * MFMA (default 1; it also needs fp16 ranking on): the rows and each batch's queries shifted
+ * into int8 by one per-dataset constant, products and sums exact in int32.  Datasets created
+ * while it is on keep an int8 copy of such rows (1 byte per value, 4 bytes per row).
+ * Returned results are identical either way.  No counterpart in the reference. */
+int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable);
 
 /* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
  * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch
@@ -301,9 +307,10 @@ int vdbg_merge_parts_host(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
  * candidates could not be certified and were re-scanned exactly. */
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
 /* Input width of the last flat/SQ8 scan's ranking GEMM on this context: 32 (fp32 MFMA), 16
- * (fp16 MFMA, taken only when every row and query value is an integer of magnitude <= 2048
- * and every partial sum stays below 2^24, so its values equal the fp32 GEMM's bit for bit),
- * or 0 (no GEMM: the exact scan ran). */
+ * (fp16 MFMA: integer rows and queries of magnitude <= 2048 with every partial sum below
+ * 2^24, exactly; SQ8 codes and float rows on split operands), 8 (int8 MFMA: such integer
+ * rows spanning at most 256 values, with every query value inside the same int8 window), or
+ * 0 (no GEMM: the exact scan ran). */
 int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 
 /* ---------------------------------------------------------------- collection search */

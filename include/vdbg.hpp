@@ -195,6 +195,11 @@ class Device {
   Status set_fp16_gemm(bool enable) {
     return Status::FromCall(vdbg_ctx_set_fp16_gemm(ctx_, enable ? 1 : 0));
   }
+  // Ranking of integer rows spanning at most 256 values on int8 MFMA (default on; results
+  // are identical either way).
+  Status set_int8_gemm(bool enable) {
+    return Status::FromCall(vdbg_ctx_set_int8_gemm(ctx_, enable ? 1 : 0));
+  }
   // The distance kernel set exact distances follow ("scalar", "avx2", "avx512").
   Status set_kernels(const char* name) { return Status::FromCall(vdbg_ctx_set_kernels(ctx_, name)); }
 

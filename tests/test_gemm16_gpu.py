@@ -12,6 +12,14 @@ from vdbg import datagen
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _fp16_not_int8(ctx):
+    # datasets created here keep no int8 copy, so integer rows rank on the fp16 GEMM
+    ctx.set_int8_gemm(False)
+    yield
+    ctx.set_int8_gemm(True)
+
+
 def _check_equal(gi, gd, oi, od):
     assert gi.shape == oi.shape
     bad = np.nonzero((gi != oi).any(axis=1) | (gd.view(np.uint32) != od.view(np.uint32)).any(axis=1))[0]

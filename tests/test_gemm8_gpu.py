@@ -1,0 +1,144 @@
+"""The int8 ranking GEMM (gemm8.hip): integer rows spanning at most 256 values and queries in
+the same int8 window (after one per-dataset shift) rank on int8 MFMA with exact int32
+products and sums.  Inner product values equal the fp32 GEMM's; L2 values exceed them by at
+most 1 (the half row norm rounded up) and the exact re-scoring decides.  Results must stay
+bit-exact to the oracle (FlatIndex::search, src/index/flat_index.cc:11-39), and batches or
+datasets outside the window must take the fp16 or fp32 GEMM."""
+import numpy as np
+import pytest
+
+import vdbg
+from vdbg import datagen
+
+pytestmark = pytest.mark.gpu
+
+
+def _check_equal(gi, gd, oi, od):
+    assert gi.shape == oi.shape
+    bad = np.nonzero((gi != oi).any(axis=1) | (gd.view(np.uint32) != od.view(np.uint32)).any(axis=1))[0]
+    assert bad.size == 0, (
+        f"{bad.size} queries differ; first q={bad[0]} gpu={gi[bad[0]].tolist()} "
+        f"{gd[bad[0]].tolist()} oracle={oi[bad[0]].tolist()} {od[bad[0]].tolist()}")
+
+
+def _ints(n, dim, seed, lo, hi):
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=(n, dim)).astype(np.float32)
+
+
+@pytest.mark.parametrize("n,nq,k", [(50000, 200, 10), (120000, 300, 100), (4100, 7, 1),
+                                    (70000, 1500, 10), (30000, 40, 200)])
+def test_sift_like_takes_int8(ctx, oracle, n, nq, k):
+    print(f"gemm8 sift-like n={n} nq={nq} k={k}", flush=True)
+    base = datagen.sift_like(n, 128, 6001)
+    qs = datagen.sift_like(nq, 128, 6002)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, k)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0  # the int8 candidates certify without exact re-scans
+    od, oi = oracle.flat_search(base, qs, k)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("dim,lo,hi,bits", [(960, 0, 30, 8), (64, 0, 255, 8), (96, -128, 127, 8),
+                                            (32, 5, 260, 8), (256, -3, 17, 8), (40, 0, 255, 16),
+                                            (100, 0, 255, 16), (64, 0, 300, 16)])
+def test_integer_dims_and_ranges(ctx, oracle, dim, lo, hi, bits):
+    # pd multiple of 32 and a value range of at most 256 take the int8 GEMM; a 48- or
+    # 112-dim pad, or rows spanning 301 values, the fp16 GEMM
+    print(f"gemm8 dim={dim} values {lo}..{hi}", flush=True)
+    pd = vdbg.padded_dim(dim)
+    base = datagen.pad(_ints(9000, dim, 6101 + dim, lo, hi), pd)
+    qs = datagen.pad(_ints(70, dim, 6201 + dim, lo, hi), pd)
+    ds = vdbg.Dataset(ctx, base, dim)
+    gi, gd = ds.flat_search(qs, 10)
+    assert ctx.last_gemm_bits() == bits
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_inner_product(ctx, oracle):
+    base = _ints(30000, 128, 6301, -20, 20)
+    qs = _ints(100, 128, 6302, -20, 20)
+    ds = vdbg.Dataset(ctx, base, 128, metric="ip")
+    gi, gd = ds.flat_search(qs, 10)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 10, metric="ip")
+    _check_equal(gi, gd, oi, od)
+
+
+def test_query_window(ctx, oracle):
+    # rows in [0, 100] centre at shift 51: queries may range over [-77, 178]
+    base = _ints(20000, 64, 6401, 0, 100)
+    ds = vdbg.Dataset(ctx, base, 64)
+    inside = _ints(50, 64, 6402, -77, 178)
+    gi, gd = ds.flat_search(inside, 10)
+    assert ctx.last_gemm_bits() == 8
+    od, oi = oracle.flat_search(base, inside, 10)
+    _check_equal(gi, gd, oi, od)
+    outside = inside.copy()
+    outside[13, 7] = 179  # one value past the window: the batch takes the fp16 GEMM
+    gi, gd = ds.flat_search(outside, 10)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.flat_search(base, outside, 10)
+    _check_equal(gi, gd, oi, od)
+    frac = inside.copy()
+    frac[3, 3] += 0.5  # a fractional query value: the fp32 GEMM
+    gi, gd = ds.flat_search(frac, 10)
+    assert ctx.last_gemm_bits() == 32
+    od, oi = oracle.flat_search(base, frac, 10)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("frac", [0.05, 0.2, 0.7])
+def test_filtered(ctx, oracle, frac):
+    # 0.05 / 0.2: the allowed rows are compacted (fp32, fp16 and int8 copies); 0.7: the mask
+    # is tested per row, in the sample pass too
+    n = 60000
+    base = datagen.sift_like(n, 128, 6501)
+    qs = datagen.sift_like(96, 128, 6502)
+    rows = np.nonzero(np.random.default_rng(6503).random(n) < frac)[0]
+    allow = np.zeros((n + 63) // 64, np.uint64)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 20, allow=allow)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 20, allow=allow)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_duplicate_rows_tie_by_id(ctx, oracle):
+    # every row four times: equal distances order by row id
+    one = _ints(5000, 128, 6601, 0, 255)
+    base = np.repeat(one, 4, axis=0)
+    qs = _ints(64, 128, 6602, 0, 255)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 17)
+    assert ctx.last_gemm_bits() == 8
+    od, oi = oracle.flat_search(base, qs, 17)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_switches_give_identical_results(ctx):
+    base = datagen.sift_like(40000, 128, 6701)
+    qs = datagen.sift_like(300, 128, 6702)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi8, gd8 = ds.flat_search(qs, 50)
+    assert ctx.last_gemm_bits() == 8
+    ctx.set_int8_gemm(False)
+    try:
+        gi16, gd16 = ds.flat_search(qs, 50)
+        assert ctx.last_gemm_bits() == 16
+    finally:
+        ctx.set_int8_gemm(True)
+    ctx.set_fp16_gemm(False)
+    try:
+        gi32, gd32 = ds.flat_search(qs, 50)
+        assert ctx.last_gemm_bits() == 32
+    finally:
+        ctx.set_fp16_gemm(True)
+    for gi, gd in ((gi16, gd16), (gi32, gd32)):
+        assert np.array_equal(gi8, gi)
+        assert np.array_equal(gd8.view(np.uint32), gd.view(np.uint32))
