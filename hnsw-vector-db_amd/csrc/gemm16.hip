@@ -268,8 +268,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
     if (wave_live && MODE == 0) {
       // Per 32-row block: the minimum of the lane's 16 values (NaN skipped) against the
-      // threshold, one wave-uniform branch; only a block passing on some lane tests its
-      // values one by one, a value passing on some lane branching to the write.
+      // threshold, one wave-uniform branch; a block passing on some lane tests its four groups
+      // of four values the same way, and only a passing group its values one by one, a value
+      // passing on some lane branching to the write.
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
@@ -279,14 +280,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
           for (int r = 1; r < 16; ++r) m = fminf(m, value(qb, blk, r));
           if (__builtin_amdgcn_ballot_w64(m <= T[qb]) == 0) continue;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float v = value(qb, blk, r);
-            if (__builtin_amdgcn_ballot_w64(v <= T[qb]) != 0) {
-              const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
-              if (v <= T[qb]) {
-                if (cnt[qb] < uint32_t(a.caph))
-                  out[qb][cnt[qb]] = make_uint2(__float_as_uint(v), row);
-                ++cnt[qb];
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const float m4 = fminf(fminf(value(qb, blk, 4 * g4), value(qb, blk, 4 * g4 + 1)),
+                                   fminf(value(qb, blk, 4 * g4 + 2), value(qb, blk, 4 * g4 + 3)));
+            if (__builtin_amdgcn_ballot_w64(m4 <= T[qb]) == 0) continue;
+#pragma unroll
+            for (int r = 4 * g4; r < 4 * g4 + 4; ++r) {
+              const float v = value(qb, blk, r);
+              if (__builtin_amdgcn_ballot_w64(v <= T[qb]) != 0) {
+                const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
+                if (v <= T[qb]) {
+                  if (cnt[qb] < uint32_t(a.caph))
+                    out[qb][cnt[qb]] = make_uint2(__float_as_uint(v), row);
+                  ++cnt[qb];
+                }
               }
             }
           }

@@ -209,7 +209,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
     if (wave_live && MODE == 0) {
       // per 32-row block: the lane's largest u against the bound, one wave-uniform branch;
-      // only a block passing on some lane tests its values one by one
+      // a block passing on some lane tests its four groups of four values the same way, and
+      // only a passing group its values one by one
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
@@ -219,14 +220,20 @@ __global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
           for (int r = 1; r < 16; ++r) m = max(m, acc[qb][blk][r]);
           if (__builtin_amdgcn_ballot_w64(m >= ui[qb]) == 0) continue;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int u = acc[qb][blk][r];
-            if (__builtin_amdgcn_ballot_w64(u >= ui[qb]) != 0) {
-              const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
-              if (u >= ui[qb]) {
-                if (cnt[qb] < uint32_t(a.caph))
-                  out[qb][cnt[qb]] = make_uint2(__float_as_uint(float(-M * u - dq[qb])), row);
-                ++cnt[qb];
+          for (int g4 = 0; g4 < 4; ++g4) {
+            const int m4 = max(max(acc[qb][blk][4 * g4], acc[qb][blk][4 * g4 + 1]),
+                               max(acc[qb][blk][4 * g4 + 2], acc[qb][blk][4 * g4 + 3]));
+            if (__builtin_amdgcn_ballot_w64(m4 >= ui[qb]) == 0) continue;
+#pragma unroll
+            for (int r = 4 * g4; r < 4 * g4 + 4; ++r) {
+              const int u = acc[qb][blk][r];
+              if (__builtin_amdgcn_ballot_w64(u >= ui[qb]) != 0) {
+                const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
+                if (u >= ui[qb]) {
+                  if (cnt[qb] < uint32_t(a.caph))
+                    out[qb][cnt[qb]] = make_uint2(__float_as_uint(float(-M * u - dq[qb])), row);
+                  ++cnt[qb];
+                }
               }
             }
           }
