@@ -44,6 +44,9 @@ struct GemmArgs {
 
 constexpr int kGemmRows = 64;  // rows per LDS tile (two 32-row MFMA blocks)
 
+// The int8 GEMM's compact sample pass keeps this many group minima per lane (a multiple of 4).
+constexpr int kTop8 = 8;
+
 // Dimensions staged per LDS pass: the whole row up to 128 dims, else the largest of
 // 128/64/32/16 that divides it.
 __host__ __device__ constexpr int GemmKc(int pd) {

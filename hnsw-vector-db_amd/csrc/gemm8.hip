@@ -45,7 +45,11 @@ constexpr int kLive8 = -(1 << 28);   // every live row's u is above this
 // 16 outputs are rows 8 (r / 4) + 4 (l / 32) + r % 4 of the 32-row block against query l % 32.
 //
 // MODE 0: every value at or below the query's threshold T goes to the lane's candidate
-// buffer; MODE 1: the minimum value of each 16-row group (the sample pass).
+// buffer; MODE 1: the minimum value of each 16-row group (the sample pass); MODE 2: the
+// sample pass keeping only the kTop8 smallest group minima each lane meets in its chunk (the
+// minima of kTop8 distinct groups, so the kk-th smallest of all lanes' lists is still a
+// value at least kk distinct rows reach), written once at the end: gm[q][(chunk * 2 + h) *
+// kTop8 + t].  It replaces a scattered store per group with two vector stores per lane.
 template <int PD, int METRIC, int QB, int MODE>
 __global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
   constexpr int KC = Gemm8Kc(PD);
@@ -79,10 +83,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
   int q[QB], ui[QB], dq[QB];
   uint2* out[QB];
   uint32_t cnt[QB];
+  int top[MODE == 2 ? QB : 1][kTop8];  // MODE 2: largest u of distinct groups, descending
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     q[qb] = q0 + qb * 32 + j;
     cnt[qb] = 0;
+    if constexpr (MODE == 2) {
+#pragma unroll
+      for (int t = 0; t < kTop8; ++t) top[qb][t] = kDead8;
+    }
     dq[qb] = a.Qd[min(q[qb], a.nq - 1)];
     if constexpr (MODE == 0) {
       // value <= T  <=>  u >= ceil((-T - delta) / M); +inf admits every live row, -inf (a
@@ -254,7 +263,14 @@ __global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
               if (row < r_end && row_allowed(a.allow, a.rid[row])) m = max(m, acc[qb][blk][r]);
             }
           }
-          if (q[qb] < a.nq) {
+          if constexpr (MODE == 2) {
+            // insert into the descending list: t' = clamp(m, top[t + 1], top[t]) from the
+            // bottom up, each step reading the entry above before it changes
+#pragma unroll
+            for (int t = kTop8 - 1; t > 0; --t)
+              top[qb][t] = max(top[qb][t], min(top[qb][t - 1], m));
+            top[qb][0] = max(top[qb][0], m);
+          } else if (q[qb] < a.nq) {
             const uint32_t grp = ((base >> 5) + blk) * 2 + h;
             if (grp < uint32_t(a.ngroups))
               a.gm[size_t(q[qb]) * a.ngroups + grp] =
@@ -275,6 +291,22 @@ __global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
     if (sidx + 1 < nstages) step(B, A, sidx + 1, std::integral_constant<int, QF - 1>{});
   }
 
+  if constexpr (MODE == 2) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      if (q[qb] < a.nq) {
+        float v[kTop8];
+#pragma unroll
+        for (int t = 0; t < kTop8; ++t)
+          v[t] = top[qb][t] < kLive8 ? __builtin_inff() : float(-M * top[qb][t] - dq[qb]);
+        float4* g = reinterpret_cast<float4*>(a.gm + size_t(q[qb]) * a.ngroups +
+                                              (size_t(chunk) * 2 + h) * kTop8);
+#pragma unroll
+        for (int t = 0; t < kTop8 / 4; ++t)
+          g[t] = make_float4(v[4 * t], v[4 * t + 1], v[4 * t + 2], v[4 * t + 3]);
+      }
+    }
+  }
   if constexpr (MODE == 0) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb) {
@@ -292,6 +324,8 @@ static void launch8_pm(int qb, int mode, hipStream_t s, int blocks, const GemmAr
   const dim3 g(blocks), t(256);
   if (mode == 1)
     k_gemm8<PD, METRIC, 2, 1><<<g, t, 0, s>>>(a);
+  else if (mode == 2)
+    k_gemm8<PD, METRIC, 2, 2><<<g, t, 0, s>>>(a);
   else if (qb == 1)
     k_gemm8<PD, METRIC, 1, 0><<<g, t, 0, s>>>(a);
   else
@@ -309,7 +343,7 @@ static void launch8_pd(int metric, int qb, int mode, hipStream_t s, int blocks, 
 int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
                 const GemmArgs& a) {
   if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM8: query blocks per wave");
-  if (mode == 1 && qb != 2) return SetError(kInternal, "GEMM8: the sample pass runs 2 blocks");
+  if (mode != 0 && qb != 2) return SetError(kInternal, "GEMM8: the sample pass runs 2 blocks");
   switch (pd) {
 #define VDBG_PD8(P) \
   case P: launch8_pd<P>(metric, qb, mode, s, blocks, a); break;

@@ -1024,22 +1024,47 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
     return;
   }
 
-  // exact re-scoring of the K' = N-1 best by GEMM value
+  // exact re-scoring of the K' = N-1 best by GEMM value, in two stages.  Stage 1 re-scores
+  // the best n1 = min(K', k + 8); its answer stands when every later candidate provably
+  // lies behind it: the (n1+1)-th GEMM value plus the shift minus the bound exceeds the k-th
+  // exact distance (always so in exact mode, where the GEMM order is the distance order).
+  // Otherwise stage 2 re-scores all K' and checks the same certificate at K'+1.
   const uint32_t nsel = min(total, uint32_t(N - 1));
-  const float a_next = __shfl(top.k.d[E - 1], kWave - 1);  // the (K'+1)-th GEMM value
+  const uint32_t n1 = min(nsel, uint32_t(a.k) + 8u);
+  const float shift = a.shift[q], ebq = a.eb[q];
+  const bool exact = a.exact[q] != 0;
   WaveKeys<E> r;
+  auto rescore_first = [&](uint32_t n) {
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    const uint32_t gi = e * kWave + lane;
-    if (gi < nsel) {
-      r.d[e] = sc(qv, top.k.id[e]);
-      r.id[e] = top.k.id[e];
-    } else {
-      r.d[e] = __builtin_inff();
-      r.id[e] = kNoId;
+    for (int e = 0; e < E; ++e) {
+      const uint32_t gi = e * kWave + lane;
+      if (gi < n) {
+        r.d[e] = sc(qv, top.k.id[e]);
+        r.id[e] = top.k.id[e];
+      } else {
+        r.d[e] = __builtin_inff();
+        r.id[e] = kNoId;
+      }
     }
+    bitonic_sort<E>(r);
+  };
+  // element g of a wave-sorted list (wave-uniform g)
+  auto at = [&](const float (&v)[E], uint32_t g) {
+    float x = __builtin_inff();
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      const float t = __shfl(v[e], int(g & (kWave - 1)));
+      if (uint32_t(e) == g / kWave) x = t;
+    }
+    return x;
+  };
+  rescore_first(n1);
+  bool certified = n1 >= total || exact ||
+                   at(r.d, uint32_t(a.k) - 1) < (at(top.k.d, n1) + shift) - ebq;
+  if (!certified && n1 < nsel) {
+    rescore_first(nsel);
+    certified = nsel >= total || at(r.d, uint32_t(a.k) - 1) < (at(top.k.d, nsel) + shift) - ebq;
   }
-  bitonic_sort<E>(r);
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int gi = e * kWave + lane;
@@ -1048,21 +1073,9 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
       od[gi] = r.d[e];
     }
   }
-  // certificate: every unselected candidate's exact distance is at least its GEMM value
-  // plus the shift minus the bound; that must exceed the k-th exact distance.
-  if (total > nsel && !a.exact[q]) {
-    const int g = a.k - 1;
-    float dk = __builtin_inff();
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      const float v = __shfl(r.d[e], g & (kWave - 1));
-      if (e == g / kWave) dk = v;
-    }
-    const float lower = (a_next + a.shift[q]) - a.eb[q];
-    if (!(dk < lower) && lane == 0) {
-      const uint32_t p = atomicAdd(a.fb_count, 1u);
-      a.fb_list[p] = q;
-    }
+  if (!certified && lane == 0) {
+    const uint32_t p = atomicAdd(a.fb_count, 1u);
+    a.fb_list[p] = q;
   }
 }
 
@@ -1443,12 +1456,18 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // counts then candidates, the candidates 256-byte aligned
   const size_t cand_need = std::max(cand_bytes(p32), try16 ? cand_bytes(p16) : 0) + 256;
   const int Esel = pow2_e(kk + 16);
+  // The int8 sample pass keeps the kTop8 smallest group minima per lane and chunk half when
+  // kk is small (at most 32 of the top kk meet in one lane's list only by rare chance, and
+  // then the threshold is merely looser); larger kk keep every group minimum.
+  const int ngroups8 = p16.schunks * 2 * kTop8;
+  const bool compact8 = try8 && kk <= 32 && ngroups8 <= 4096 && uint64_t(ngroups8) >= kk;
+  const int gm_groups = std::max(ngroups, compact8 ? ngroups8 : 0);
 
   Workspace& w = c->ws;
   w.used = 0;
   const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
-                      size_t(nq) * ngroups * sizeof(float) + cand_need +
+                      size_t(nq) * gm_groups * sizeof(float) + cand_need +
                       (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
                       (try8 ? nq * pd + nq * sizeof(int) : 0) + 22 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
@@ -1461,7 +1480,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* fb_count = w.take<uint32_t>(2);  // [0] first pass, [1] second chance
   uint32_t* fb2_list = w.take<uint32_t>(nq);
   float* Qb = src->kind == 1 ? w.take<float>(nq * pd) : nullptr;
-  float* gm = w.take<float>(size_t(nq) * ngroups);
+  float* gm = w.take<float>(size_t(nq) * gm_groups);
   char* cand_base = w.take<char>(cand_need);
   uint16_t* Q16 = try16 ? w.take<uint16_t>((split ? 2 : 1) * nq * pd) : nullptr;
   float* Qf = try16 && split ? w.take<float>(nq) : nullptr;
@@ -1515,6 +1534,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   sg.allow = allow;
   sg.gm = gm;
   sg.ngroups = ngroups;
+  const bool top8 = use8 && P.qb == 2 && compact8;
   sg.N = S;
   sg.nq = int(nq);
   sg.chunk_rows = P.schunk_rows;
@@ -1527,7 +1547,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       sg.Q8 = Q8;
       sg.Qd = Qd;
       GemmGrid(sg, P.nqt, P.schunks, &sblocks);
-      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, 1, s, sblocks, sg));
+      if (top8) sg.ngroups = ngroups8;
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, top8 ? 2 : 1, s, sblocks, sg));
     } else if (use16 && P.qb == 2) {
       sg.X16 = src->SX16;
       sg.Q16 = Q16;
@@ -1542,7 +1563,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  KthArgs ka{gm, ngroups, int(nq), int(kk), eb, T};
+  KthArgs ka{gm, sg.ngroups, int(nq), int(kk), eb, T};
   {
     ProfScope ps(c, "kth", s);
     VDBG_RETURN_IF_ERROR(LaunchKth(s, ka));

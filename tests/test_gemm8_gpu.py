@@ -142,3 +142,41 @@ def test_switches_give_identical_results(ctx):
     for gi, gd in ((gi16, gd16), (gi32, gd32)):
         assert np.array_equal(gi8, gi)
         assert np.array_equal(gd8.view(np.uint32), gd.view(np.uint32))
+
+
+@pytest.mark.parametrize("k", [32, 33])
+def test_compact_sample_boundary(ctx, oracle, k):
+    # k <= 32 on the int8 GEMM takes the compact sample pass (the 8 smallest group minima per
+    # lane and chunk half), k = 33 the pass that keeps every group minimum; both certify
+    print(f"gemm8 compact sample k={k}", flush=True)
+    base = datagen.sift_like(150000, 128, 6801)
+    qs = datagen.sift_like(1100, 128, 6802)
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, k)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, k)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_unit_neighbours_tie_within_the_bound(ctx, oracle):
+    # each query is a row, and 256 rows sit at squared distance 1 from it (+-1 on one dim):
+    # int8 L2 values run up to 1 above the GEMM value, so the staged re-scoring cannot
+    # certify from the GEMM order and the chain falls through to the exact scan; the answer
+    # (the query's row, then distance-1 rows by id) must still be the oracle's
+    rng = np.random.default_rng(6901)
+    centres = rng.integers(20, 200, size=(40, 128)).astype(np.float32)
+    eye = np.eye(128, dtype=np.float32)
+    rows = [centres]
+    for c in centres:
+        rows.append(c + eye)
+        rows.append(c - eye)
+    base = np.concatenate(rows + [rng.integers(0, 255, size=(30000, 128)).astype(np.float32)])
+    qs = np.concatenate([centres] * 4)  # 160 queries: the 256-query tile path
+    ds = vdbg.Dataset(ctx, base, 128)
+    for k in (10, 40):
+        gi, gd = ds.flat_search(qs, k)
+        assert ctx.last_gemm_bits() == 8
+        od, oi = oracle.flat_search(base, qs, k)
+        _check_equal(gi, gd, oi, od)
+        assert np.all(gd[:, 1:] == 1.0)
