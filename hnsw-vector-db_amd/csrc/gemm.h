@@ -88,6 +88,9 @@ inline bool Gemm8Supported(size_t pd) { return pd % 32 == 0 && GemmSupported(pd)
 
 // int8 GEMM (gemm8.hip): qb query blocks of 32 per wave, mode 0 = threshold pass, 1 = group
 // minima of the sample (qb 2).
+// Blocks per CU of the int8 main pass with two query blocks per wave (its launch bounds):
+// three for rows of at most 128 dims, whose kernel fits 168 registers, else two.
+int Gemm8Occupancy(size_t pd);
 int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
                 const GemmArgs& a);
 

@@ -50,8 +50,8 @@ constexpr int kLive8 = -(1 << 28);   // every live row's u is above this
 // minima of kTop8 distinct groups, so the kk-th smallest of all lanes' lists is still a
 // value at least kk distinct rows reach), written once at the end: gm[q][(chunk * 2 + h) *
 // kTop8 + t].  It replaces a scattered store per group with two vector stores per lane.
-template <int PD, int METRIC, int QB, int MODE>
-__global__ __launch_bounds__(256, 2) void k_gemm8(GemmArgs a) {
+template <int PD, int METRIC, int QB, int MODE, int OCC = 2>
+__global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   constexpr int KC = Gemm8Kc(PD);
   constexpr int NKC = PD / KC;
   constexpr int NKB = KC / 32;                     // 32-dim MFMA K blocks per stage
@@ -325,9 +325,11 @@ static void launch8_pm(int qb, int mode, hipStream_t s, int blocks, const GemmAr
   if (mode == 1)
     k_gemm8<PD, METRIC, 2, 1><<<g, t, 0, s>>>(a);
   else if (mode == 2)
-    k_gemm8<PD, METRIC, 2, 2><<<g, t, 0, s>>>(a);
+    k_gemm8<PD, METRIC, 2, 2, PD <= 128 ? 3 : 2><<<g, t, 0, s>>>(a);
   else if (qb == 1)
     k_gemm8<PD, METRIC, 1, 0><<<g, t, 0, s>>>(a);
+  else if constexpr (PD <= 128)
+    k_gemm8<PD, METRIC, 2, 0, 3><<<g, t, 0, s>>>(a);
   else
     k_gemm8<PD, METRIC, 2, 0><<<g, t, 0, s>>>(a);
 }
@@ -339,6 +341,8 @@ static void launch8_pd(int metric, int qb, int mode, hipStream_t s, int blocks, 
   else
     launch8_pm<PD, 1>(qb, mode, s, blocks, a);
 }
+
+int Gemm8Occupancy(size_t pd) { return pd <= 128 ? 3 : 2; }
 
 int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
                 const GemmArgs& a) {

@@ -1427,7 +1427,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     int qb, nqt, nchunks, caph, nseg, schunks;
     uint32_t chunk_rows, schunk_rows;
   };
-  auto make_plan = [&](int qb, int tile_queries) {
+  auto make_plan = [&](int qb, int tile_queries, int slots) {
     Plan p{};
     p.qb = qb;
     p.nqt = int((nq + tile_queries - 1) / tile_queries);
@@ -1447,19 +1447,23 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   };
   // Rows with an fp16 copy may rank on the fp16 GEMM: integer-valued flat rows exactly
   // (64 queries per wave, or 32 for batches of at most 128), SQ8 codes with the query operand
-  // split in two fp16 parts (both register sets hold the same 32 queries).
-  const Plan p32 = make_plan(1, 128);
-  const Plan p16 = split ? make_plan(2, 128) : (nq > 128 ? make_plan(2, 256) : make_plan(1, 128));
+  // split in two fp16 parts (both register sets hold the same 32 queries).  The int8 GEMM
+  // tiles as the exact fp16 one, its large-batch kernel with Gemm8Occupancy blocks per CU.
+  const Plan p32 = make_plan(1, 128, slots);
+  const Plan p16 = split ? make_plan(2, 128, slots)
+                         : (nq > 128 ? make_plan(2, 256, slots) : make_plan(1, 128, slots));
+  const Plan p8 = nq > 128 ? make_plan(2, 256, Gemm8Occupancy(pd) * c->cu_count) : p16;
   auto cand_bytes = [&](const Plan& p) {
     return size_t(nq) * p.nseg * (sizeof(uint32_t) + size_t(p.caph) * sizeof(uint2));
   };
   // counts then candidates, the candidates 256-byte aligned
-  const size_t cand_need = std::max(cand_bytes(p32), try16 ? cand_bytes(p16) : 0) + 256;
+  const size_t cand_need = std::max({cand_bytes(p32), try16 ? cand_bytes(p16) : 0,
+                                     try8 ? cand_bytes(p8) : 0}) + 256;
   const int Esel = pow2_e(kk + 16);
   // The int8 sample pass keeps the kTop8 smallest group minima per lane and chunk half when
   // kk is small (at most 32 of the top kk meet in one lane's list only by rare chance, and
   // then the threshold is merely looser); larger kk keep every group minimum.
-  const int ngroups8 = p16.schunks * 2 * kTop8;
+  const int ngroups8 = p8.schunks * 2 * kTop8;
   const bool compact8 = try8 && kk <= 32 && ngroups8 <= 4096 && uint64_t(ngroups8) >= kk;
   const int gm_groups = std::max(ngroups, compact8 ? ngroups8 : 0);
 
@@ -1514,7 +1518,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     use16 = !use8 && c->host_pinned[0] != 0;
   }
   c->last_gemm_bits = use8 ? 8 : (use16 ? 16 : 32);
-  const Plan& P = use8 || use16 ? p16 : p32;
+  const Plan& P = use8 ? p8 : (use16 ? p16 : p32);
   const int nchunks = P.nchunks;
   const int caph = P.caph;
   const int nseg = P.nseg;
