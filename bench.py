@@ -390,17 +390,32 @@ def main():
         gi, gd = gpu_out()
         g_ms = prof["sq8_gemm"][0] / max(1, prof["sq8_gemm"][1])
         tflops = 2.0 * nq * N * dim / (g_ms * 1e-3) / 1e12
-        # the codes rank on fp16 MFMA against the query operand split in two fp16 parts
-        # (two MFMA products per code x query product); achieved counts the algorithmic flop
+        # the codes rank on int8 MFMA against the query operand rounded to integers in two
+        # int8 parts (two MFMA products per code x query product), or, with the int8 GEMM
+        # switched off, on fp16 MFMA against two fp16 parts; achieved counts the algorithmic
+        # work (2 N d per query), priced at the peak of the MFMA type that ran
         bits = ctx.last_gemm_bits()
+        kern = {8: "k_gemm8<128,L2,SQ8 two-part operand,threshold>",
+                16: "k_gemm16<128,L2,split codes>"}.get(bits, "k_gemm<128,L2,codes,filter>")
         r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
-             "kernel": "k_gemm16<128,L2,split codes>" if bits == 16 else "k_gemm<128,L2,codes,filter>",
-             "kernel_ms": g_ms, "achieved": tflops, "unit": "TFLOP/s",
-             "peak": FP16_MFMA_PEAK_TFLOPS if bits == 16 else FP32_MFMA_PEAK_TFLOPS,
+             "kernel": kern, "kernel_ms": g_ms, "achieved": tflops,
+             "unit": "TOP/s" if bits == 8 else "TFLOP/s",
+             "peak": {8: INT8_MFMA_PEAK_TOPS, 16: FP16_MFMA_PEAK_TFLOPS}.get(bits, FP32_MFMA_PEAK_TFLOPS),
              "bound": "mfma",
-             "mfma_inputs": "f16 codes x two-part f16 query operand" if bits == 16 else "f32",
+             "mfma_inputs": {8: "i8 codes - 128 x query operand as two int8 parts (exact int32 sums)",
+                             16: "f16 codes x two-part f16 query operand"}.get(bits, "f32"),
              "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
              "exact_rescans": fb, "depth": depth}
+        if bits == 8:
+            ctx.set_int8_gemm(False)
+            el16, prof16, _ = timed(ctx, torch, step, args.steps, 1, ["sq8_gemm"])
+            ctx.set_int8_gemm(True)
+            g16 = prof16["sq8_gemm"][0] / max(1, prof16["sq8_gemm"][1])
+            r["fp16_gemm"] = {"qps": round(nq * args.steps / el16, 1),
+                              "kernel": "k_gemm16<128,L2,split codes>", "kernel_ms": round(g16, 4),
+                              "achieved_TFLOPs": round(2.0 * nq * N * dim / (g16 * 1e-3) / 1e12, 2),
+                              "peak_TFLOPs": FP16_MFMA_PEAK_TFLOPS}
+            log(f"sq8 (fp16 GEMM): {nq * args.steps / el16:.0f} q/s, GEMM {g16:.2f} ms")
         log(f"sq8: {r['qps']:.0f} q/s, GEMM {g_ms:.2f} ms = {tflops:.1f} TFLOP/s")
         if not args.no_cpu:
             s = min(args.cpu_sample // 2, nq)

@@ -31,6 +31,7 @@ struct GemmArgs {
   const int8_t* Q8;    // k_gemm8: queries shifted to int8
   const int* rn8;      // k_gemm8: accumulator start per row
   const int* Qd;       // k_gemm8: per-query constant between the integer GEMM and GEMM units
+  const int* e8;       // k_gemm8 on SQ8 codes: the batch's query scale exponent (device)
   int* ovf;            // MODE 0: [q]
   float* gm;           // MODE 1: [q][ngroups] minimum GEMM value of each 16-row group
   int ngroups;
@@ -91,7 +92,8 @@ inline bool Gemm8Supported(size_t pd) { return pd % 32 == 0 && GemmSupported(pd)
 // Blocks per CU of the int8 main pass with two query blocks per wave (its launch bounds):
 // three for rows of at most 128 dims, whose kernel fits 168 registers, else two.
 int Gemm8Occupancy(size_t pd);
-int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+// sq = 1: SQ8 codes against the two-part query operand (k_gemm8 SQ = 1, qb must be 2).
+int LaunchGemm8(size_t pd, int metric, int qb, int mode, int sq, hipStream_t s, int blocks,
                 const GemmArgs& a);
 
 // fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 = threshold pass

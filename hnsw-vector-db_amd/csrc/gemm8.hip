@@ -50,8 +50,18 @@ constexpr int kLive8 = -(1 << 28);   // every live row's u is above this
 // minima of kTop8 distinct groups, so the kk-th smallest of all lanes' lists is still a
 // value at least kk distinct rows reach), written once at the end: gm[q][(chunk * 2 + h) *
 // kTop8 + t].  It replaces a scattered store per group with two vector stores per lane.
-template <int PD, int METRIC, int QB, int MODE, int OCC = 2>
+//
+// SQ = 1: SQ8 codes against a query operand in two int8 parts.  Codes c (uint8) enter LDS as
+// c' = c - 128; the scaled query operand B 2^e (one exponent e for the whole batch, *a.e8) is
+// rounded to integers v = 256 hi + lo with hi, lo int8 ([q][2][pd] in Q8).  The two register
+// sets hold the same 32 queries (QB = 2 parts), the hi accumulator starts at 0 and the lo one
+// at the row start -rint(||c scale||^2 2^(e-1)) (L2) or 0 (inner product), and
+// u = 256 acc_hi + acc_lo.  With dq = M 128 sum(v) (a.Qd) the value in GEMM units is
+// (-M u - dq) 2^-e; its distance from the fp32 GEMM value is in the query's bound.
+template <int PD, int METRIC, int QB, int MODE, int OCC = 2, int SQ = 0>
 __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
+  static_assert(SQ == 0 || QB == 2, "the SQ8 operand runs two parts");
+  constexpr int NQ = SQ ? 1 : QB;                  // queries per lane
   constexpr int KC = Gemm8Kc(PD);
   constexpr int NKC = PD / KC;
   constexpr int NKB = KC / 32;                     // 32-dim MFMA K blocks per stage
@@ -59,7 +69,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   constexpr int VEC_PER_ROW = KC / 16;             // 16-byte vectors per stage row
   constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
-  constexpr int QT = 128 * QB;                     // queries per block
+  constexpr int QT = 128 * NQ;                     // queries per block
   constexpr int M = METRIC == 0 ? 2 : 1;
   static_assert(PD % KC == 0 && KC % 32 == 0, "K chunking");
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kGemmRows * STR];
@@ -75,17 +85,23 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   const int lane = tid & 63;
   const int j = lane & 31;
   const int h = lane >> 5;
-  const int q0 = qt * QT + wave * 32 * QB;
+  const int q0 = qt * QT + wave * 32 * NQ;
   const bool wave_live = q0 < a.nq;
   const uint32_t r_begin = uint32_t(chunk) * a.chunk_rows;
   const uint32_t r_end = min(a.N, r_begin + a.chunk_rows);
 
-  int q[QB], ui[QB], dq[QB];
-  uint2* out[QB];
-  uint32_t cnt[QB];
-  int top[MODE == 2 ? QB : 1][kTop8];  // MODE 2: largest u of distinct groups, descending
+  // SQ8: the batch exponent e; values leave the kernel as (-M u - dq) 2^-e
+  const int e8 = SQ ? *a.e8 : 0;
+  int q[NQ], ui[NQ], dq[NQ];
+  uint2* out[NQ];
+  uint32_t cnt[NQ];
+  int top[MODE == 2 ? NQ : 1][kTop8];  // MODE 2: largest u of distinct groups, descending
+  auto gemm_units = [&](int u, int d) {
+    const float v = float(-M * u - d);
+    return SQ ? ldexpf(v, -e8) : v;
+  };
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
+  for (int qb = 0; qb < NQ; ++qb) {
     q[qb] = q0 + qb * 32 + j;
     cnt[qb] = 0;
     if constexpr (MODE == 2) {
@@ -97,7 +113,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
       // value <= T  <=>  u >= ceil((-T - delta) / M); +inf admits every live row, -inf (a
       // lane past the batch) none
       const float T = q[qb] < a.nq ? a.T[q[qb]] : -__builtin_inff();
-      const double t = ceil((-double(T) - double(dq[qb])) / M);
+      const double t = ceil((-ldexp(double(T), e8) - double(dq[qb])) / M);
       ui[qb] = !(t <= double(1 << 30)) ? (1 << 30) : (t < double(kLive8) ? kLive8 : int(t));
       out[qb] = a.cand + ((size_t(q[qb]) * a.nchunks + chunk) * 2 + h) * size_t(a.caph);
     }
@@ -109,7 +125,9 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   v4i qv[QF][QB][NKB];
   const int8_t* qrow[QB];
 #pragma unroll
-  for (int qb = 0; qb < QB; ++qb) qrow[qb] = a.Q8 + size_t(min(q[qb], a.nq - 1)) * PD + h * 16;
+  for (int qb = 0; qb < QB; ++qb)
+    qrow[qb] = SQ ? a.Q8 + (size_t(min(q[0], a.nq - 1)) * 2 + qb) * PD + h * 16
+                  : a.Q8 + size_t(min(q[qb], a.nq - 1)) * PD + h * 16;
   auto load_q = [&](int f, int kc) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
@@ -155,7 +173,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
         st.v[i] = *reinterpret_cast<const u32x4*>(src + uint32_t(o));
       }
     }
-    st.n = a.rn8[base + min(uint32_t(tid & 63), valid - 1)];
+    if constexpr (SQ)  // L2: -rint(||c scale||^2 2^(e - 1)), inner product: 0
+      st.n = METRIC == 0
+                 ? -int(rintf(ldexpf(a.rn[base + min(uint32_t(tid & 63), valid - 1)], e8 - 1)))
+                 : 0;
+    else
+      st.n = a.rn8[base + min(uint32_t(tid & 63), valid - 1)];
     if constexpr (MODE == 0)
       st.aw = a.aw[((base >> 5) + (uint32_t(tid & 63) >> 5)) & a.aw_mask];
   };
@@ -166,7 +189,8 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
       if (VEC_PER_TILE % 256 == 0 || f < VEC_PER_TILE)
-        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) = st.v[i];
+        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) =
+            SQ ? (st.v[i] ^ 0x80808080u) : st.v[i];  // SQ8: codes c to int8 c - 128
     }
     if (kc == 0 && tid < kGemmRows) {
       const uint32_t valid = min(uint32_t(kGemmRows), r_end - (r_begin + uint32_t(tile) * kGemmRows));
@@ -196,7 +220,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
           init[4 * g + 3] = n4.w;
         }
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) acc[qb][blk] = init;
+        for (int qb = 0; qb < QB; ++qb) {
+          if (SQ && qb == 0)
+            acc[qb][blk] = v16i{};  // the hi part starts at 0, the lo part at the row start
+          else
+            acc[qb][blk] = init;
+        }
       }
     }
     const uint8_t* xa0 = &xs[sidx & 1][j * STR + h * 16];
@@ -216,12 +245,18 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     if (kc != NKC - 1) return;
 
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
+    if constexpr (SQ) {  // u = 256 acc_hi + acc_lo, into the first set
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[0][blk][r] = (acc[0][blk][r] << 8) + acc[1][blk][r];
+    }
     if (wave_live && MODE == 0) {
       // per 32-row block: the lane's largest u against the bound, one wave-uniform branch;
       // a block passing on some lane tests its four groups of four values the same way, and
       // only a passing group its values one by one
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
+      for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
           int m = acc[qb][blk][0];
@@ -240,7 +275,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
                 const uint32_t row = lane_base + (blk * 32 + 8 * (r >> 2) + (r & 3));
                 if (u >= ui[qb]) {
                   if (cnt[qb] < uint32_t(a.caph))
-                    out[qb][cnt[qb]] = make_uint2(__float_as_uint(float(-M * u - dq[qb])), row);
+                    out[qb][cnt[qb]] = make_uint2(__float_as_uint(gemm_units(u, dq[qb])), row);
                   ++cnt[qb];
                 }
               }
@@ -249,7 +284,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
         }
     } else if (wave_live) {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb)
+      for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
           int m = kDead8;
@@ -274,7 +309,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
             const uint32_t grp = ((base >> 5) + blk) * 2 + h;
             if (grp < uint32_t(a.ngroups))
               a.gm[size_t(q[qb]) * a.ngroups + grp] =
-                  m < kLive8 ? __builtin_inff() : float(-M * m - dq[qb]);
+                  m < kLive8 ? __builtin_inff() : gemm_units(m, dq[qb]);
           }
         }
     }
@@ -293,12 +328,12 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
 
   if constexpr (MODE == 2) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int qb = 0; qb < NQ; ++qb) {
       if (q[qb] < a.nq) {
         float v[kTop8];
 #pragma unroll
         for (int t = 0; t < kTop8; ++t)
-          v[t] = top[qb][t] < kLive8 ? __builtin_inff() : float(-M * top[qb][t] - dq[qb]);
+          v[t] = top[qb][t] < kLive8 ? __builtin_inff() : gemm_units(top[qb][t], dq[qb]);
         float4* g = reinterpret_cast<float4*>(a.gm + size_t(q[qb]) * a.ngroups +
                                               (size_t(chunk) * 2 + h) * kTop8);
 #pragma unroll
@@ -309,7 +344,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   }
   if constexpr (MODE == 0) {
 #pragma unroll
-    for (int qb = 0; qb < QB; ++qb) {
+    for (int qb = 0; qb < NQ; ++qb) {
       if (q[qb] < a.nq) {
         const size_t seg = (size_t(q[qb]) * a.nchunks + chunk) * 2 + h;
         a.counts[seg] = min(cnt[qb], uint32_t(a.caph));
@@ -320,37 +355,46 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
 }
 
 template <int PD, int METRIC>
-static void launch8_pm(int qb, int mode, hipStream_t s, int blocks, const GemmArgs& a) {
+static void launch8_pm(int qb, int mode, int sq, hipStream_t s, int blocks, const GemmArgs& a) {
   const dim3 g(blocks), t(256);
-  if (mode == 1)
+  constexpr int OCC = PD <= 128 ? 3 : 2;  // Gemm8Occupancy
+  if (sq) {
+    if (mode == 1)
+      k_gemm8<PD, METRIC, 2, 1, 2, 1><<<g, t, 0, s>>>(a);
+    else if (mode == 2)
+      k_gemm8<PD, METRIC, 2, 2, OCC, 1><<<g, t, 0, s>>>(a);
+    else
+      k_gemm8<PD, METRIC, 2, 0, OCC, 1><<<g, t, 0, s>>>(a);
+  } else if (mode == 1) {
     k_gemm8<PD, METRIC, 2, 1><<<g, t, 0, s>>>(a);
-  else if (mode == 2)
-    k_gemm8<PD, METRIC, 2, 2, PD <= 128 ? 3 : 2><<<g, t, 0, s>>>(a);
-  else if (qb == 1)
+  } else if (mode == 2) {
+    k_gemm8<PD, METRIC, 2, 2, OCC><<<g, t, 0, s>>>(a);
+  } else if (qb == 1) {
     k_gemm8<PD, METRIC, 1, 0><<<g, t, 0, s>>>(a);
-  else if constexpr (PD <= 128)
-    k_gemm8<PD, METRIC, 2, 0, 3><<<g, t, 0, s>>>(a);
-  else
-    k_gemm8<PD, METRIC, 2, 0><<<g, t, 0, s>>>(a);
+  } else {
+    k_gemm8<PD, METRIC, 2, 0, OCC><<<g, t, 0, s>>>(a);
+  }
 }
 
 template <int PD>
-static void launch8_pd(int metric, int qb, int mode, hipStream_t s, int blocks, const GemmArgs& a) {
+static void launch8_pd(int metric, int qb, int mode, int sq, hipStream_t s, int blocks,
+                       const GemmArgs& a) {
   if (metric == 0)
-    launch8_pm<PD, 0>(qb, mode, s, blocks, a);
+    launch8_pm<PD, 0>(qb, mode, sq, s, blocks, a);
   else
-    launch8_pm<PD, 1>(qb, mode, s, blocks, a);
+    launch8_pm<PD, 1>(qb, mode, sq, s, blocks, a);
 }
 
 int Gemm8Occupancy(size_t pd) { return pd <= 128 ? 3 : 2; }
 
-int LaunchGemm8(size_t pd, int metric, int qb, int mode, hipStream_t s, int blocks,
+int LaunchGemm8(size_t pd, int metric, int qb, int mode, int sq, hipStream_t s, int blocks,
                 const GemmArgs& a) {
   if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM8: query blocks per wave");
-  if (mode != 0 && qb != 2) return SetError(kInternal, "GEMM8: the sample pass runs 2 blocks");
+  if ((mode != 0 || sq) && qb != 2)
+    return SetError(kInternal, "GEMM8: the sample pass and the SQ8 operand run 2 blocks");
   switch (pd) {
 #define VDBG_PD8(P) \
-  case P: launch8_pd<P>(metric, qb, mode, s, blocks, a); break;
+  case P: launch8_pd<P>(metric, qb, mode, sq, s, blocks, a); break;
     VDBG_PD8(32) VDBG_PD8(64) VDBG_PD8(96) VDBG_PD8(128) VDBG_PD8(192) VDBG_PD8(256)
     VDBG_PD8(384) VDBG_PD8(512) VDBG_PD8(768) VDBG_PD8(960) VDBG_PD8(1024)
 #undef VDBG_PD8

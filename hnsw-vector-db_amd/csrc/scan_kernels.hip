@@ -440,6 +440,7 @@ struct PrepArgs {
   int* Qd;        // its per-query constant M c8 sum(q) - c8^2 pd
   int* all8;      // cleared when a query is outside the int8 GEMM's bounds
   int c8;
+  uint32_t* mb8;  // nullable: SQ8 on the int8 GEMM, the batch's max |B| (float bits, atomicMax)
 };
 
 // One wave per query.
@@ -522,6 +523,8 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     float mb = 0.f;
     for (int i = lane_id(); i < a.pd; i += kWave) mb = fmaxf(mb, fabsf(a.Qb[size_t(q) * a.pd + i]));
     mb = wave_max(mb);
+    // non-negative floats order as their bits; a NaN ends above +inf and stops the int8 GEMM
+    if (a.mb8 != nullptr && lane_id() == 0) atomicMax(a.mb8, __float_as_uint(mb));
     split_ok = mb <= 3.0e38f;  // finite
     if (split_ok && mb > 0.f) {
       int ex = 0;
@@ -610,6 +613,66 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     a.eb[q] = half_norm ? 1.f
                         : ex ? 0.f
                              : float((split ? (a.kind == 1 ? bound16 : bound16f) : bound) * 1.001);
+  }
+}
+
+// SQ8 on the int8 GEMM (gemm8.hip, SQ = 1): the B operand of every query of the batch scaled
+// by one 2^e, with 2^L <= 2^20 / pd (L <= 14) the bound on |B 2^e|, and rounded to integers
+// v = 256 hi + lo (hi, lo int8).  So |sum c' v| < 2^27 for codes c' = c - 128, and the L2 row
+// start rint(||c scale||^2 2^(e-1)) must stay below 2^27 too, or the batch takes the fp16 GEMM.
+// The value (-M (sum c' v - start) - M 128 sum v) 2^-e misses the fp32 GEMM value by at most
+// 2^-e (M 255 sum|B_i 2^e - v_i| + [L2] 1): that term is added to the query's bound (eb8).
+struct Sq8Op8Args {
+  const float* Qb;
+  int nq, pd, metric;
+  const uint32_t* mb8;
+  float rn_max;       // max ||code * scale||^2 over the rows
+  const float* eb;    // the fp32-side bound of k_query_prep
+  int8_t* Q8;         // [q][2][pd]: hi, lo
+  int* Qd;            // M 128 sum(v)
+  float* eb8;
+  int* e8;
+  int* all8;
+};
+
+__global__ __launch_bounds__(256) void k_sq8_operand8(Sq8Op8Args a) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;
+  const float mb = __uint_as_float(*a.mb8);
+  int L = 0;
+  while (L < 14 && (int64_t(2) << L) * a.pd <= (int64_t(1) << 20)) ++L;
+  int e = 0;
+  bool ok = mb <= 3.0e38f;
+  if (ok && mb > 0.f) {
+    int ex = 0;
+    (void)frexpf(mb, &ex);  // mb <= 2^ex
+    e = L - ex;
+  }
+  if (a.metric == 0 && !(ldexp(double(a.rn_max), e - 1) < 134217728.0)) ok = false;
+  const float* b = a.Qb + size_t(q) * a.pd;
+  int8_t* o = a.Q8 + size_t(q) * 2 * a.pd;
+  int sv = 0;
+  float sd = 0.f;
+  for (int i = lane_id(); i < a.pd; i += kWave) {
+    const float x = ok ? ldexpf(b[i], e) : 0.f;  // |x| <= 2^L
+    const float v = rintf(x);
+    const int vi = int(v);
+    const int hi = (vi + 128) >> 8;
+    o[i] = int8_t(hi);
+    o[a.pd + i] = int8_t(vi - 256 * hi);
+    sv += vi;
+    sd += fabsf(x - v);  // exact: x and its nearest integer share the exponent range
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) sv += __shfl_xor(sv, off);
+  sd = wave_sum(sd);
+  if (lane_id() == 0) {
+    const int M = a.metric == 0 ? 2 : 1;
+    a.Qd[q] = M * 128 * sv;
+    const double quant = ldexp(M * 255.0 * double(sd) * (1.0 + 1e-6 * a.pd) +
+                                   (a.metric == 0 ? 1.0 : 0.0), -e);
+    a.eb8[q] = float((double(a.eb[q]) + quant) * 1.001);
+    if (q == 0) *a.e8 = e;
+    if (!ok) atomicAnd(a.all8, 0);
   }
 }
 
@@ -1410,6 +1473,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
   // integer rows spanning at most 256 values may rank on the int8 GEMM (gemm8.hip)
   const bool try8 = try16 && c->int8_gemm && split == 0 && src->X8 != nullptr;
+  // SQ8 codes may rank on the int8 GEMM with the query operand in two int8 parts
+  const bool try8s = try16 && c->int8_gemm && src->kind == 1 && Gemm8Supported(pd);
+  const bool try8any = try8 || try8s;
   // Sample size: about kk * N / S rows pass the threshold per query, and every pass costs a
   // scattered buffer write and a select insertion (and on the exact fp16 GEMM every 32-row
   // block holding one takes the per-value test), while the pre-pass costs S / N of the main
@@ -1452,19 +1518,20 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const Plan p32 = make_plan(1, 128, slots);
   const Plan p16 = split ? make_plan(2, 128, slots)
                          : (nq > 128 ? make_plan(2, 256, slots) : make_plan(1, 128, slots));
-  const Plan p8 = nq > 128 ? make_plan(2, 256, Gemm8Occupancy(pd) * c->cu_count) : p16;
+  const Plan p8 = try8s ? make_plan(2, 128, Gemm8Occupancy(pd) * c->cu_count)
+                 : (nq > 128 ? make_plan(2, 256, Gemm8Occupancy(pd) * c->cu_count) : p16);
   auto cand_bytes = [&](const Plan& p) {
     return size_t(nq) * p.nseg * (sizeof(uint32_t) + size_t(p.caph) * sizeof(uint2));
   };
   // counts then candidates, the candidates 256-byte aligned
   const size_t cand_need = std::max({cand_bytes(p32), try16 ? cand_bytes(p16) : 0,
-                                     try8 ? cand_bytes(p8) : 0}) + 256;
+                                     try8any ? cand_bytes(p8) : 0}) + 256;
   const int Esel = pow2_e(kk + 16);
   // The int8 sample pass keeps the kTop8 smallest group minima per lane and chunk half when
   // kk is small (at most 32 of the top kk meet in one lane's list only by rare chance, and
   // then the threshold is merely looser); larger kk keep every group minimum.
   const int ngroups8 = p8.schunks * 2 * kTop8;
-  const bool compact8 = try8 && kk <= 32 && ngroups8 <= 4096 && uint64_t(ngroups8) >= kk;
+  const bool compact8 = try8any && kk <= 32 && ngroups8 <= 4096 && uint64_t(ngroups8) >= kk;
   const int gm_groups = std::max(ngroups, compact8 ? ngroups8 : 0);
 
   Workspace& w = c->ws;
@@ -1473,7 +1540,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                       (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
                       size_t(nq) * gm_groups * sizeof(float) + cand_need +
                       (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
-                      (try8 ? nq * pd + nq * sizeof(int) : 0) + 22 * 256;
+                      (try8 ? nq * pd + nq * sizeof(int) : 0) +
+                      (try8s ? 2 * nq * pd + nq * (sizeof(int) + sizeof(float)) : 0) + 26 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
@@ -1489,34 +1557,46 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint16_t* Q16 = try16 ? w.take<uint16_t>((split ? 2 : 1) * nq * pd) : nullptr;
   float* Qf = try16 && split ? w.take<float>(nq) : nullptr;
   int* all16 = try16 ? w.take<int>(2) : nullptr;  // [0] fp16 bounds, [1] int8 bounds
-  int* all8 = try8 ? all16 + 1 : nullptr;
-  int8_t* Q8 = try8 ? w.take<int8_t>(nq * pd) : nullptr;
-  int* Qd = try8 ? w.take<int>(nq) : nullptr;
+  int* all8 = try8any ? all16 + 1 : nullptr;
+  int8_t* Q8 = try8any ? w.take<int8_t>((try8s ? 2 : 1) * nq * pd) : nullptr;
+  int* Qd = try8any ? w.take<int>(nq) : nullptr;
+  float* eb8 = try8s ? w.take<float>(nq) : nullptr;
+  int* e8 = try8s ? w.take<int>(2) : nullptr;  // [0] exponent, [1] max |B| bits
+  uint32_t* mb8 = try8s ? reinterpret_cast<uint32_t*>(e8 + 1) : nullptr;
   uint32_t* ones = try16 ? w.take<uint32_t>(1) : nullptr;  // the fp16 GEMM's no-filter word
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
   VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
   if (try16) VDBG_HIP(hipMemsetD32Async(all16, 1, 2, s));
   if (try16) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
+  if (try8s) VDBG_HIP(hipMemsetAsync(e8, 0, 2 * sizeof(int), s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
-              src->x16_exp, Q8, Qd, all8, src->c8};
+              src->x16_exp, try8 ? Q8 : nullptr, try8 ? Qd : nullptr, try8 ? all8 : nullptr,
+              src->c8, mb8};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
     VDBG_HIP(hipGetLastError());
+    if (try8s) {
+      Sq8Op8Args oa{Qb, int(nq), int(pd), src->metric, mb8, src->rn_max, eb, Q8, Qd, eb8, e8, all8};
+      k_sq8_operand8<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(oa);
+      VDBG_HIP(hipGetLastError());
+    }
   }
   // The exact-integer GEMM needs every query of the batch inside its bounds, so the host
   // reads the flag.  The split operands need no such check: a non-finite query only yields
   // NaN or infinite GEMM values and bound, its certificate fails and it is re-scanned
   // exactly, as on the fp32 GEMM.
   bool use16 = try16 && split != 0, use8 = false;
-  if (try16 && split == 0) {
+  if ((try16 && split == 0) || try8s) {
     VDBG_HIP(hipMemcpyAsync(c->host_pinned, all16, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
     VDBG_HIP(hipStreamSynchronize(s));
-    use8 = try8 && c->host_pinned[1] != 0;
-    use16 = !use8 && c->host_pinned[0] != 0;
+    use8 = try8any && c->host_pinned[1] != 0;
+    use16 = !use8 && (split != 0 || c->host_pinned[0] != 0);
   }
+  // the bound of the GEMM the batch ranks on
+  const float* ebx = use8 && try8s ? eb8 : eb;
   c->last_gemm_bits = use8 ? 8 : (use16 ? 16 : 32);
   const Plan& P = use8 ? p8 : (use16 ? p16 : p32);
   const int nchunks = P.nchunks;
@@ -1546,13 +1626,15 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   {
     ProfScope ps(c, "sample_gemm", s);
     if (use8 && P.qb == 2) {
-      sg.X8 = src->SX8;
+      sg.X8 = try8s ? reinterpret_cast<const int8_t*>(src->SC) : src->SX8;
       sg.rn8 = src->Sinit8;
       sg.Q8 = Q8;
       sg.Qd = Qd;
+      sg.e8 = e8;
       GemmGrid(sg, P.nqt, P.schunks, &sblocks);
       if (top8) sg.ngroups = ngroups8;
-      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, top8 ? 2 : 1, s, sblocks, sg));
+      VDBG_RETURN_IF_ERROR(
+          LaunchGemm8(pd, metric, 2, top8 ? 2 : 1, try8s ? 1 : 0, s, sblocks, sg));
     } else if (use16 && P.qb == 2) {
       sg.X16 = src->SX16;
       sg.Q16 = Q16;
@@ -1567,7 +1649,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  KthArgs ka{gm, sg.ngroups, int(nq), int(kk), eb, T};
+  KthArgs ka{gm, sg.ngroups, int(nq), int(kk), ebx, T};
   {
     ProfScope ps(c, "kth", s);
     VDBG_RETURN_IF_ERROR(LaunchKth(s, ka));
@@ -1594,13 +1676,14 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   {
     ProfScope ps(c, src->kind == 0 ? "flat_gemm" : "sq8_gemm", s);
     if (use8) {
-      ga.X8 = src->X8;
+      ga.X8 = try8s ? reinterpret_cast<const int8_t*>(src->C) : src->X8;
       ga.rn8 = src->init8;
       ga.Q8 = Q8;
       ga.Qd = Qd;
+      ga.e8 = e8;
       ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
       ga.aw_mask = allow != nullptr ? ~0u : 0u;
-      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, P.qb, 0, s, blocks, ga));
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, P.qb, 0, try8s ? 1 : 0, s, blocks, ga));
     } else if (use16) {
       ga.X16 = src->X16;
       ga.Q16 = Q16;
@@ -1621,7 +1704,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   se.cap = caph;
   se.ovf = ovf;
   se.shift = shift;
-  se.eb = eb;
+  se.eb = ebx;
   se.exact = exact;
   se.nslots = int(nq);
   se.k = int(kk);

@@ -562,6 +562,7 @@ static int CreateSq8(vdbg_dataset* ds, const float* vmin, const float* scale,
   x.src.pd = static_cast<int>(pd);
   x.src.metric = d.metric;
   x.src.rmag = float(ymax + xhat + vn);
+  x.src.rn_max = float(ymax);
   rc = MakeCodes16(c, s, x.codes, n, pd, &x.codes16);
   if (rc != kOk) return fail(rc);
   x.src.X16 = x.codes16;

@@ -120,6 +120,7 @@ struct ScanSource {
   uint32_t N = 0;
   int pd = 0, metric = 0;
   float rmag = 0.f;             // row magnitude term of the rounding bound
+  float rn_max = 0.f;           // SQ8: max ||code * scale||^2 (the int8 GEMM's row-start bound)
   RowStats stats;               // flat: value statistics for the exactness test
   float* SX = nullptr;          // sample rows (kind 0)
   uint16_t* SX16 = nullptr;     // sample rows of X16 (same layout)

@@ -112,10 +112,12 @@ def _wide_range_rows(n, dim, seed):
     ("unit", "cosine", 150, 10, 64), ("unit", "ip", 150, 20, 0),
     ("wide", "l2", 130, 10, 100), ("wide", "ip", 100, 10, 50)])
 @pytest.mark.parametrize("dim", [128, 96, 384])
-def test_sq8_split_fp16_matches_fp32_and_oracle(ctx, oracle, data, metric, nq, k, depth, dim):
-    # the SQ8 scan ranks on fp16 MFMA (codes exact, query operand split in two fp16 parts);
-    # results must equal the fp32 GEMM's and the oracle's bit for bit
-    print(f"sq8 split {data} {metric} dim={dim} nq={nq} k={k} depth={depth}", flush=True)
+def test_sq8_int8_fp16_fp32_match_oracle(ctx, oracle, data, metric, nq, k, depth, dim):
+    # the SQ8 scan ranks on int8 MFMA (codes - 128 exact, the query operand rounded to
+    # integers in two int8 parts under a widened bound), on fp16 MFMA with the int8 GEMM off
+    # (codes exact, query operand split in two fp16 parts), or on the fp32 GEMM; results must
+    # be the same bit for bit and the oracle's
+    print(f"sq8 int8/fp16/fp32 {data} {metric} dim={dim} nq={nq} k={k} depth={depth}", flush=True)
     n = 40000 if dim <= 128 else 12000
     if data == "sift_like":
         base, qs = datagen.sift_like(n, dim, 6101), datagen.sift_like(nq, dim, 6102)
@@ -129,19 +131,27 @@ def test_sq8_split_fp16_matches_fp32_and_oracle(ctx, oracle, data, metric, nq, k
     ds = vdbg.Dataset(ctx, base, dim, metric=metric)
     sq = vdbg.Sq8Index(ds)
     gi, gd = sq.search(qs, k, depth)
-    assert ctx.last_gemm_bits() == 16
+    assert ctx.last_gemm_bits() == 8
+    ctx.set_int8_gemm(False)
+    try:
+        gi16, gd16 = sq.search(qs, k, depth)
+        assert ctx.last_gemm_bits() == 16
+    finally:
+        ctx.set_int8_gemm(True)
     ctx.set_fp16_gemm(False)
     try:
         gi32, gd32 = sq.search(qs, k, depth)
         assert ctx.last_gemm_bits() == 32
     finally:
         ctx.set_fp16_gemm(True)
+    _eq(gi, gd, gi16, gd16)
     _eq(gi, gd, gi32, gd32)
     od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth, metric=metric)
     _eq(gi, gd, oi, od)
 
 
-def test_sq8_split_large_batch_filtered(ctx, oracle):
+@pytest.mark.parametrize("int8", [True, False])
+def test_sq8_large_batch_filtered(ctx, oracle, int8):
     n, nq = 120000, 700
     base, qs = datagen.sift_like(n, 128, 6201), datagen.sift_like(nq, 128, 6202)
     rows = np.nonzero(np.random.default_rng(6203).random(n) < 0.6)[0]
@@ -149,7 +159,40 @@ def test_sq8_split_large_batch_filtered(ctx, oracle):
     np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
     ds = vdbg.Dataset(ctx, base, 128)
     sq = vdbg.Sq8Index(ds)
-    gi, gd = sq.search(qs, 10, 100, allow=allow)
-    assert ctx.last_gemm_bits() == 16
+    ctx.set_int8_gemm(int8)
+    try:
+        gi, gd = sq.search(qs, 10, 100, allow=allow)
+        assert ctx.last_gemm_bits() == (8 if int8 else 16)
+        assert ctx.last_fallbacks() == 0
+    finally:
+        ctx.set_int8_gemm(True)
     od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 100, allow=allow)
+    _eq(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("k,depth", [(10, 20), (10, 100)])
+def test_sq8_int8_compact_and_full_sample(ctx, oracle, k, depth):
+    # depth <= 32 takes the int8 GEMM's compact sample pass, depth 100 the full one
+    base, qs = datagen.sift_like(90000, 128, 6301), datagen.sift_like(600, 128, 6302)
+    ds = vdbg.Dataset(ctx, base, 128)
+    sq = vdbg.Sq8Index(ds)
+    gi, gd = sq.search(qs, k, depth)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, depth)
+    _eq(gi, gd, oi, od)
+
+
+def test_sq8_int8_falls_back_when_row_starts_overflow(ctx, oracle):
+    # queries within 1e-3 of the quantizer's minimum: the batch's query operand is so small
+    # that its scale exponent would push the L2 row starts past 2^27, so the batch takes the
+    # fp16 split GEMM, and the answers stay the oracle's
+    base = datagen.sift_like(20000, 128, 6401)
+    ds = vdbg.Dataset(ctx, base, 128)
+    sq = vdbg.Sq8Index(ds)
+    rng = np.random.default_rng(6402)
+    qs = (sq.vmin[None, :128] + rng.uniform(0, 1e-3, (40, 128))).astype(np.float32)
+    gi, gd = sq.search(qs, 10, 50)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 50)
     _eq(gi, gd, oi, od)
