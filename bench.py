@@ -45,7 +45,7 @@ def log(*a):
 
 
 PROFILES = {"flat": "flat_gemm8_sift_like_1m_x128_k10_b10000.md",
-            "sq8": "sq8_gemm16_split_sift_like_1m_x128_d100_b10000.md",
+            "sq8": "sq8_gemm8_sift_like_1m_x128_d100_b10000.md",
             "ivfpq": "ivf_scan_sift_like_1m_nlist4096_m16_nprobe64.md"}
 
 

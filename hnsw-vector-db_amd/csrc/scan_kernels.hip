@@ -1528,10 +1528,11 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                                      try8any ? cand_bytes(p8) : 0}) + 256;
   const int Esel = pow2_e(kk + 16);
   // The int8 sample pass keeps the kTop8 smallest group minima per lane and chunk half when
-  // kk is small (at most 32 of the top kk meet in one lane's list only by rare chance, and
-  // then the threshold is merely looser); larger kk keep every group minimum.
+  // the lists hold three times kk in all (more than kTop8 of the top kk groups meet in one
+  // lane's list only by rare chance, and then the threshold is merely looser); otherwise
+  // it keeps every group minimum.
   const int ngroups8 = p8.schunks * 2 * kTop8;
-  const bool compact8 = try8any && kk <= 32 && ngroups8 <= 4096 && uint64_t(ngroups8) >= kk;
+  const bool compact8 = try8any && ngroups8 <= 4096 && uint64_t(ngroups8) >= 3 * kk;
   const int gm_groups = std::max(ngroups, compact8 ? ngroups8 : 0);
 
   Workspace& w = c->ws;

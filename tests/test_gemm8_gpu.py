@@ -144,13 +144,15 @@ def test_switches_give_identical_results(ctx):
         assert np.array_equal(gd8.view(np.uint32), gd.view(np.uint32))
 
 
-@pytest.mark.parametrize("k", [32, 33])
-def test_compact_sample_boundary(ctx, oracle, k):
-    # k <= 32 on the int8 GEMM takes the compact sample pass (the 8 smallest group minima per
-    # lane and chunk half), k = 33 the pass that keeps every group minimum; both certify
-    print(f"gemm8 compact sample k={k}", flush=True)
+@pytest.mark.parametrize("nq,k", [(1100, 10), (1100, 33), (200, 150)])
+def test_compact_and_full_sample(ctx, oracle, nq, k):
+    # the int8 GEMM's sample pass keeps the 8 smallest group minima per lane and chunk half
+    # while those lists hold at least 3 k entries and at most 4096 in all (1100 queries), and
+    # every group minimum otherwise (200 queries: one query tile spreads the 65,536 sample
+    # rows over 512 chunks); both thresholds certify
+    print(f"gemm8 sample pass nq={nq} k={k}", flush=True)
     base = datagen.sift_like(150000, 128, 6801)
-    qs = datagen.sift_like(1100, 128, 6802)
+    qs = datagen.sift_like(nq, 128, 6802)
     ds = vdbg.Dataset(ctx, base, 128)
     gi, gd = ds.flat_search(qs, k)
     assert ctx.last_gemm_bits() == 8

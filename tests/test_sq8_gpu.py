@@ -170,10 +170,11 @@ def test_sq8_large_batch_filtered(ctx, oracle, int8):
     _eq(gi, gd, oi, od)
 
 
-@pytest.mark.parametrize("k,depth", [(10, 20), (10, 100)])
-def test_sq8_int8_compact_and_full_sample(ctx, oracle, k, depth):
-    # depth <= 32 takes the int8 GEMM's compact sample pass, depth 100 the full one
-    base, qs = datagen.sift_like(90000, 128, 6301), datagen.sift_like(600, 128, 6302)
+@pytest.mark.parametrize("nq,k,depth", [(600, 10, 20), (600, 10, 100), (100, 10, 100)])
+def test_sq8_int8_sample_passes(ctx, oracle, nq, k, depth):
+    # 600 queries take the int8 GEMM's compact sample pass; 100 queries (one tile, the
+    # sample spread over 512 chunks) the one keeping every group minimum
+    base, qs = datagen.sift_like(90000, 128, 6301), datagen.sift_like(nq, 128, 6302)
     ds = vdbg.Dataset(ctx, base, 128)
     sq = vdbg.Sq8Index(ds)
     gi, gd = sq.search(qs, k, depth)
