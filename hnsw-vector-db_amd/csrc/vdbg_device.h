@@ -22,7 +22,8 @@ __device__ __forceinline__ int lane_id() { return threadIdx.x & (kWave - 1); }
 // Neighbor::operator< (include/vdb/types.h:23-25): distance first, then id.  Float
 // comparison keeps -0.0 == +0.0, as the reference does.
 __device__ __forceinline__ bool nb_less(float ad, uint32_t ai, float bd, uint32_t bi) {
-  return ad < bd || (ad == bd && ai < bi);
+  // bitwise, not short-circuit: the comparisons combine as lane masks with no branch
+  return (ad < bd) | ((ad == bd) & (ai < bi));
 }
 
 // A dense row mask (bit r of word r / 64 set = row r allowed); null allows every row.
@@ -348,6 +349,20 @@ struct WaveKeys {
   uint32_t id[E];
 };
 
+// v of lane (lane ^ j), j a power of two below 64: a DPP quad permutation for j = 1, 2 (no
+// LDS round trip), a bit-mask ds_swizzle within 32-lane groups for j = 4..16, bpermute for 32.
+__device__ __forceinline__ uint32_t lane_xor(uint32_t v, int j) {
+  if (j == 1) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, true));
+  if (j == 2) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, true));
+  if (j == 4) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (4 << 10) | 0x1F));
+  if (j == 8) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (8 << 10) | 0x1F));
+  if (j == 16) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (16 << 10) | 0x1F));
+  return uint32_t(__shfl_xor(int(v), j));
+}
+__device__ __forceinline__ float lane_xor(float v, int j) {
+  return __uint_as_float(lane_xor(__float_as_uint(v), j));
+}
+
 // One compare-exchange layer of a bitonic network over 64*E elements: partner g ^ j,
 // ascending in blocks where (g & size) == 0.
 template <int E>
@@ -361,32 +376,30 @@ __device__ __forceinline__ void bitonic_layer(WaveKeys<E>& k, int size, int j) {
       if (pe > e) {
         const int g = e * kWave + lane;
         const bool up = (g & size) == 0;
-        const bool sw = up ? nb_less(k.d[pe], k.id[pe], k.d[e], k.id[e])
-                           : nb_less(k.d[e], k.id[e], k.d[pe], k.id[pe]);
-        if (sw) {
-          float td = k.d[e];
-          k.d[e] = k.d[pe];
-          k.d[pe] = td;
-          uint32_t ti = k.id[e];
-          k.id[e] = k.id[pe];
-          k.id[pe] = ti;
-        }
+        const bool lt = nb_less(k.d[pe], k.id[pe], k.d[e], k.id[e]);
+        const bool gt = nb_less(k.d[e], k.id[e], k.d[pe], k.id[pe]);
+        const bool sw = up ? lt : gt;
+        const float d0 = k.d[e], d1 = k.d[pe];
+        const uint32_t i0 = k.id[e], i1 = k.id[pe];
+        k.d[e] = sw ? d1 : d0;
+        k.d[pe] = sw ? d0 : d1;
+        k.id[e] = sw ? i1 : i0;
+        k.id[pe] = sw ? i0 : i1;
       }
     }
   } else {
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const int g = e * kWave + lane;
-      const float pd = __shfl_xor(k.d[e], j);
-      const uint32_t pi = __shfl_xor(k.id[e], j);
+      const float pd = lane_xor(k.d[e], j);
+      const uint32_t pi = lane_xor(k.id[e], j);
       const bool up = (g & size) == 0;
       const bool lower = (lane & j) == 0;
-      const bool take = (lower == up) ? nb_less(pd, pi, k.d[e], k.id[e])
-                                      : nb_less(k.d[e], k.id[e], pd, pi);
-      if (take) {
-        k.d[e] = pd;
-        k.id[e] = pi;
-      }
+      const bool lt = nb_less(pd, pi, k.d[e], k.id[e]);
+      const bool gt = nb_less(k.d[e], k.id[e], pd, pi);
+      const bool take = (lower == up) ? lt : gt;
+      k.d[e] = take ? pd : k.d[e];
+      k.id[e] = take ? pi : k.id[e];
     }
   }
 }
