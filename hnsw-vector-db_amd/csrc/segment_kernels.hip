@@ -83,20 +83,24 @@ __global__ void k_map_ids(uint32_t* __restrict__ out, size_t n, const uint32_t* 
 
 int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hipStream_t s) {
   const size_t nwords = (size_t(N) + 63) / 64;
-  uint32_t* cnt = nullptr;
-  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&cnt), (nwords + 1) * 4, s));
+  size_t tmp_bytes = 0;
+  VDBG_HIP(hipcub::DeviceReduce::Sum(nullptr, tmp_bytes, static_cast<uint32_t*>(nullptr),
+                                     static_cast<uint32_t*>(nullptr), int(nwords), s));
+  // the compaction scratch, kept across calls (reallocation would cost more than the scan at
+  // low selectivity); its contents are dead once the count is read back
+  Workspace& w = c->wsc;
+  w.used = 0;
+  // a call on another stream may still read the scratch: wait for its last reader
+  if (c->wsc_done != nullptr) VDBG_HIP(hipStreamWaitEvent(s, c->wsc_done, 0));
+  VDBG_RETURN_IF_ERROR(w.reserve((nwords + 1) * 4 + tmp_bytes + 1024));
+  uint32_t* cnt = w.take<uint32_t>(nwords + 1);
+  void* tmp = w.take<char>(tmp_bytes + 16);
   k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
   VDBG_HIP(hipGetLastError());
-  size_t tmp_bytes = 0;
-  VDBG_HIP(hipcub::DeviceReduce::Sum(nullptr, tmp_bytes, cnt, cnt + nwords, int(nwords), s));
-  void* tmp = nullptr;
-  VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
   VDBG_HIP(hipcub::DeviceReduce::Sum(tmp, tmp_bytes, cnt, cnt + nwords, int(nwords), s));
   VDBG_HIP(hipMemcpyAsync(c->host_pinned, cnt + nwords, 4, hipMemcpyDeviceToHost, s));
   VDBG_HIP(hipStreamSynchronize(s));
   *count = c->host_pinned[0];
-  (void)hipFreeAsync(tmp, s);
-  (void)hipFreeAsync(cnt, s);
   return kOk;
 }
 
@@ -116,17 +120,19 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   ScanSource cs = *src;
   cs.N = count;
   const size_t sample_bytes = SampleBytes(cs, SampleRows(count));
+  size_t tmp_bytes = 0;
+  VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, static_cast<uint32_t*>(nullptr),
+                                            static_cast<uint32_t*>(nullptr), int(nwords), s));
   const size_t bytes = (nwords + 1) * 4 * 2 +
                        size_t(count) * (4 + 4 + row_bytes + row16_bytes + row8_bytes +
                                         (row8_bytes != 0 ? 4 : 0)) +
-                       sample_bytes + 4096 + 512;
-  VDBG_HIP(hipMallocAsync(&buf, bytes, s));
-  char* p = static_cast<char*>(buf);
-  auto take = [&](size_t b) {
-    char* r = p;
-    p += (b + 255) & ~size_t(255);
-    return r;
-  };
+                       sample_bytes + tmp_bytes + 4096 + 512 + 16 * 256;
+  // the context's compaction scratch: reused in stream order by the next call
+  Workspace& w = c->wsc;
+  w.used = 0;
+  VDBG_RETURN_IF_ERROR(w.reserve(bytes));
+  buf = w.base;
+  auto take = [&](size_t b) { return w.take<char>(b); };
   uint32_t* cnt = reinterpret_cast<uint32_t*>(take((nwords + 1) * 4));
   uint32_t* pre = reinterpret_cast<uint32_t*>(take((nwords + 1) * 4));
   uint32_t* ids = reinterpret_cast<uint32_t*>(take(size_t(count) * 4 + 4));
@@ -140,9 +146,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   {
     ProfScope ps(c, "compact", s);
     k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
-    size_t tmp_bytes = 0;
-    VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, cnt, pre, int(nwords), s));
-    VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
+    tmp = take(tmp_bytes + 16);
     VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
     k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre, ids);
     if (src->kind == 0) {
@@ -183,10 +187,14 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     k_map_ids<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, nq * kk, ids);
     if (hipGetLastError() != hipSuccess) rc = SetError(kInternal, "map ids launch");
   }
-  (void)hipStreamSynchronize(s);
-  FreeSample(&cs);
-  (void)hipFreeAsync(tmp, s);
-  (void)hipFreeAsync(buf, s);
+  if (c->wsc_done == nullptr &&
+      hipEventCreateWithFlags(&c->wsc_done, hipEventDisableTiming) != hipSuccess)
+    c->wsc_done = nullptr;
+  if (c->wsc_done == nullptr || hipEventRecord(c->wsc_done, s) != hipSuccess) {
+    (void)hipStreamSynchronize(s);  // no event: drain before the scratch is reused
+  }
+  FreeSample(&cs);  // the sample lives in the scratch (cs.Sbuf is null): nothing to free
+  (void)buf;
   return rc;
 }
 

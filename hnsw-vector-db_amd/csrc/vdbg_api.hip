@@ -357,6 +357,8 @@ int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   for (auto ev : c.free_events) (void)hipEventDestroy(ev);
   c.ws.release();
   c.ws2.release();
+  c.wsc.release();
+  if (c.wsc_done) (void)hipEventDestroy(c.wsc_done);
   if (c.host_pinned) (void)hipHostFree(c.host_pinned);
   (void)hipStreamDestroy(c.stream);
   delete ctx;

@@ -84,6 +84,8 @@ struct Ctx {
   std::recursive_mutex mu;
   Workspace ws;   // per-call scratch
   Workspace ws2;  // scratch of the exact re-scan that runs while ws is live
+  Workspace wsc;  // scratch of the filtered scan's row compaction (kept across calls)
+  hipEvent_t wsc_done = nullptr;  // recorded after the last launch reading wsc
   uint32_t* host_pinned = nullptr;  // small pinned staging for counters
   bool profiling = false;
   std::vector<ProfEntry> pending;
