@@ -1591,8 +1591,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // exactly, as on the fp32 GEMM.
   bool use16 = try16 && split != 0, use8 = false;
   if ((try16 && split == 0) || try8s) {
-    VDBG_HIP(hipMemcpyAsync(c->host_pinned, all16, 2 * sizeof(int), hipMemcpyDeviceToHost, s));
-    VDBG_HIP(hipStreamSynchronize(s));
+    VDBG_RETURN_IF_ERROR(ReadWords(c, reinterpret_cast<const uint32_t*>(all16), 2, s));
     use8 = try8any && c->host_pinned[1] != 0;
     use16 = !use8 && (split != 0 || c->host_pinned[0] != 0);
   }
@@ -1724,8 +1723,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  VDBG_HIP(hipMemcpyAsync(c->host_pinned, fb_count, sizeof(uint32_t), hipMemcpyDeviceToHost, s));
-  VDBG_HIP(hipStreamSynchronize(s));
+  VDBG_RETURN_IF_ERROR(ReadWords(c, fb_count, 1, s));
   const uint32_t nfb = c->host_pinned[0];
   c->last_fallbacks = 0;
   if (nfb == 0) return kOk;
@@ -1747,9 +1745,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  VDBG_HIP(hipMemcpyAsync(c->host_pinned, fb_count + 1, sizeof(uint32_t), hipMemcpyDeviceToHost,
-                          s));
-  VDBG_HIP(hipStreamSynchronize(s));
+  VDBG_RETURN_IF_ERROR(ReadWords(c, fb_count + 1, 1, s));
   const uint32_t nfb2 = c->host_pinned[0];
   c->last_fallbacks = nfb2;
   if (nfb2 > 0)

@@ -98,8 +98,7 @@ int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hip
   k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
   VDBG_HIP(hipGetLastError());
   VDBG_HIP(hipcub::DeviceReduce::Sum(tmp, tmp_bytes, cnt, cnt + nwords, int(nwords), s));
-  VDBG_HIP(hipMemcpyAsync(c->host_pinned, cnt + nwords, 4, hipMemcpyDeviceToHost, s));
-  VDBG_HIP(hipStreamSynchronize(s));
+  VDBG_RETURN_IF_ERROR(ReadWords(c, cnt + nwords, 1, s));
   *count = c->host_pinned[0];
   return kOk;
 }

@@ -22,6 +22,41 @@ int SetError(int code, const std::string& msg) {
   return code;
 }
 
+__global__ void k_publish_words(const uint32_t* __restrict__ src, int n, uint32_t* dst,
+                                uint32_t seq) {
+  const int i = threadIdx.x;
+  if (i < n) dst[1 + i] = src[i];
+  __threadfence_system();
+  __syncthreads();
+  if (i == 0) __hip_atomic_store(dst, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s) {
+  if (n <= 0 || n > 64) return SetError(kInternal, "ReadWords: 1..64 words");
+  const uint32_t seq = ++c->flag_seq == 0 ? ++c->flag_seq : c->flag_seq;
+  k_publish_words<<<1, 64, 0, s>>>(dev, n, c->host_flag_dev, seq);
+  VDBG_HIP(hipGetLastError());
+  volatile uint32_t* f = c->host_flag;
+  for (uint32_t spin = 0;; ++spin) {
+    if (__atomic_load_n(&c->host_flag[0], __ATOMIC_ACQUIRE) == seq) {
+      for (int i = 0; i < n; ++i) c->host_pinned[i] = f[1 + i];
+      return kOk;
+    }
+    if ((spin & 1023u) == 1023u) {  // every ~1k polls: has the stream ended or failed?
+      const hipError_t q = hipStreamQuery(s);
+      if (q != hipErrorNotReady) {
+        VDBG_HIP(q);
+        if (__atomic_load_n(&c->host_flag[0], __ATOMIC_ACQUIRE) != seq) {
+          // the stream is done but the number did not show: copy the words the slow way
+          VDBG_HIP(hipMemcpy(c->host_pinned, dev, size_t(n) * 4, hipMemcpyDeviceToHost));
+          return kOk;
+        }
+      }
+    }
+    __builtin_ia32_pause();
+  }
+}
+
 int Workspace::reserve(size_t bytes) {
   if (bytes <= cap) return kOk;
   if (base != nullptr) {
@@ -307,7 +342,16 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
   hipError_t e = hipStreamCreateWithFlags(&ctx->c.stream, hipStreamNonBlocking);
   if (e == hipSuccess)
     e = hipHostMalloc(reinterpret_cast<void**>(&ctx->c.host_pinned), 4096, hipHostMallocDefault);
+  if (e == hipSuccess)
+    e = hipHostMalloc(reinterpret_cast<void**>(&ctx->c.host_flag), 4096,
+                      hipHostMallocMapped | hipHostMallocCoherent);
+  if (e == hipSuccess) {
+    ctx->c.host_flag[0] = 0;
+    e = hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->c.host_flag_dev), ctx->c.host_flag, 0);
+  }
   if (e != hipSuccess) {
+    if (ctx->c.host_flag) (void)hipHostFree(ctx->c.host_flag);
+    if (ctx->c.host_pinned) (void)hipHostFree(ctx->c.host_pinned);
     if (ctx->c.stream) (void)hipStreamDestroy(ctx->c.stream);
     delete ctx;
     return SetError(kInternal, std::string("context: ") + hipGetErrorString(e));
@@ -360,6 +404,7 @@ int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   c.wsc.release();
   if (c.wsc_done) (void)hipEventDestroy(c.wsc_done);
   if (c.host_pinned) (void)hipHostFree(c.host_pinned);
+  if (c.host_flag) (void)hipHostFree(c.host_flag);
   (void)hipStreamDestroy(c.stream);
   delete ctx;
   return kOk;

@@ -87,6 +87,11 @@ struct Ctx {
   Workspace wsc;  // scratch of the filtered scan's row compaction (kept across calls)
   hipEvent_t wsc_done = nullptr;  // recorded after the last launch reading wsc
   uint32_t* host_pinned = nullptr;  // small pinned staging for counters
+  // ReadWords: coherent pinned words the device publishes into ([0] sequence, then data),
+  // their device address, and the last sequence number used
+  uint32_t* host_flag = nullptr;
+  uint32_t* host_flag_dev = nullptr;
+  uint32_t flag_seq = 0;
   bool profiling = false;
   std::vector<ProfEntry> pending;
   std::vector<hipEvent_t> free_events;
@@ -305,6 +310,12 @@ inline int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, siz
   cleanup();
   return rc;
 }
+
+// Copies n <= 64 32-bit counters from device memory to c->host_pinned[0..n) after the work
+// queued on s: a one-wave kernel publishes them into coherent pinned memory with a sequence
+// number that the host polls (far less latency than a stream synchronisation); the host
+// falls back to synchronising when the stream ends without the number showing.
+int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s);
 
 }  // namespace vdbg
 
