@@ -158,8 +158,9 @@ def run_filtered(args, ctx, torch, ref, threads):
              "ms_per_step": round(el * 1e3 / args.steps, 3),
              "gemm_ms_per_step": round(g_ms, 3),
              "gemm_TFLOPs": round(flops / (g_ms * 1e-3) / 1e12, 2) if g_ms > 0 else None,
-             "mfma_inputs": ("f16 two-part rows x two-part queries (3 MFMA products each)"
-                             if ctx.last_gemm_bits() == 16 else "f32"),
+             "mfma_inputs": {8: "i8 two-part rows x two-part queries (4 int8 MFMA products each)",
+                             16: "f16 two-part rows x two-part queries (3 MFMA products each)"}
+                            .get(ctx.last_gemm_bits(), "f32"),
              "kernel_ms_per_step": {kk: round(v[0] / args.steps, 4) for kk, v in prof.items()},
              "exact_rescans": fb}
         log(f"filtered {sel}%: {r['qps']:.0f} q/s, {n_allowed} rows allowed")

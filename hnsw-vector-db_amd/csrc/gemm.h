@@ -73,6 +73,13 @@ __host__ __device__ constexpr int Gemm8Kc(int pd) {
   return pd <= 128 ? pd : (pd % 128 == 0 ? 128 : (pd % 64 == 0 ? 64 : 32));
 }
 
+// K chunk of the int8 GEMM on float rows held in two int8 parts (stored per chunk as
+// [h | l]): the whole row up to 64 dims, else 64 or 32 dims, which keeps both register sets
+// of the two-part stage and query fragments within two blocks per CU.
+__host__ __device__ constexpr int Gemm8KcSplit(int pd) {
+  return pd <= 64 ? pd : (pd % 64 == 0 ? 64 : 32);
+}
+
 // Padded dimensions with compiled GEMM kernels; others scan exactly.
 inline bool GemmSupported(size_t pd) {
   switch (pd) {

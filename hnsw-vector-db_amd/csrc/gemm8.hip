@@ -18,6 +18,7 @@
 // below any threshold and any group maximum of a live row.
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <string>
 #include <type_traits>
 
@@ -58,15 +59,26 @@ constexpr int kLive8 = -(1 << 28);   // every live row's u is above this
 // at the row start -rint(||c scale||^2 2^(e-1)) (L2) or 0 (inner product), and
 // u = 256 acc_hi + acc_lo.  With dq = M 128 sum(v) (a.Qd) the value in GEMM units is
 // (-M u - dq) 2^-e; its distance from the fp32 GEMM value is in the query's bound.
+//
+// SQ = 2: float rows, both operands in two int8 parts.  Rows x 2^ex and the batch's queries
+// q 2^eq rounded to integers 256 h + l (rows stored per K chunk as [h | l], row bytes
+// 2 pd), so sum v_x v_q = 2^16 (h.h) + 2^8 (h.l + l.h) + l.l: four MFMAs into three
+// accumulators, u = (acc_hh << 16) + (acc_mid << 8) + acc_ll exactly in int32 (the batch is
+// admitted only while |sum v_x v_q| + row start < 2^29).  e = ex + eq, dq = 0.
 template <int PD, int METRIC, int QB, int MODE, int OCC = 2, int SQ = 0>
 __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
-  static_assert(SQ == 0 || QB == 2, "the SQ8 operand runs two parts");
+  static_assert(SQ == 0 || QB == 2, "the two-part operands run two parts");
   constexpr int NQ = SQ ? 1 : QB;                  // queries per lane
-  constexpr int KC = Gemm8Kc(PD);
+  constexpr int NACC = SQ == 2 ? 3 : QB;           // accumulator sets
+  constexpr int RP = SQ == 2 ? 2 : 1;              // row parts
+  // accumulator start of rows that take no part, and the bound every live row's u exceeds
+  constexpr int kDead = SQ == 2 ? -(1 << 30) : kDead8;
+  constexpr int kLive = SQ == 2 ? -(1 << 29) : kLive8;
+  constexpr int KC = SQ == 2 ? Gemm8KcSplit(PD) : Gemm8Kc(PD);
   constexpr int NKC = PD / KC;
   constexpr int NKB = KC / 32;                     // 32-dim MFMA K blocks per stage
-  constexpr int STR = KC + 16;                     // LDS row stride in bytes (16 B padding)
-  constexpr int VEC_PER_ROW = KC / 16;             // 16-byte vectors per stage row
+  constexpr int STR = RP * KC + 16;                // LDS row stride in bytes (16 B padding)
+  constexpr int VEC_PER_ROW = RP * KC / 16;        // 16-byte vectors per stage row
   constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
   constexpr int QT = 128 * NQ;                     // queries per block
@@ -106,7 +118,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     cnt[qb] = 0;
     if constexpr (MODE == 2) {
 #pragma unroll
-      for (int t = 0; t < kTop8; ++t) top[qb][t] = kDead8;
+      for (int t = 0; t < kTop8; ++t) top[qb][t] = kDead;
     }
     dq[qb] = a.Qd[min(q[qb], a.nq - 1)];
     if constexpr (MODE == 0) {
@@ -114,7 +126,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
       // lane past the batch) none
       const float T = q[qb] < a.nq ? a.T[q[qb]] : -__builtin_inff();
       const double t = ceil((-ldexp(double(T), e8) - double(dq[qb])) / M);
-      ui[qb] = !(t <= double(1 << 30)) ? (1 << 30) : (t < double(kLive8) ? kLive8 : int(t));
+      ui[qb] = !(t <= double(1 << 30)) ? (1 << 30) : (t < double(kLive) ? kLive : int(t));
       out[qb] = a.cand + ((size_t(q[qb]) * a.nchunks + chunk) * 2 + h) * size_t(a.caph);
     }
   }
@@ -144,7 +156,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   for (int i = 0; i < VEC_PER_THREAD; ++i) {
     const int f = min(tid + 256 * i, VEC_PER_TILE - 1);
     vrow[i] = f / VEC_PER_ROW;
-    voff[i] = vrow[i] * PD + (f % VEC_PER_ROW) * 16;
+    voff[i] = vrow[i] * RP * PD + (f % VEC_PER_ROW) * 16;
   }
   // Stages s = tile * NKC + kc (64 rows x KC dims), stage s + 2 loaded while stage s is
   // multiplied, two register sets swapping roles each step, as in the fp16 GEMM.
@@ -160,7 +172,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
     const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
     const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
-    const char* src = reinterpret_cast<const char*>(a.X8 + size_t(base) * PD + kc * KC);
+    const char* src = reinterpret_cast<const char*>(a.X8 + size_t(base) * RP * PD + kc * RP * KC);
     if (valid == kGemmRows) {
 #pragma unroll
       for (int i = 0; i < VEC_PER_THREAD; ++i)
@@ -169,7 +181,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
       const int over = int(valid) - 1;
 #pragma unroll
       for (int i = 0; i < VEC_PER_THREAD; ++i) {
-        const int o = voff[i] - max(0, vrow[i] - over) * PD;
+        const int o = voff[i] - max(0, vrow[i] - over) * RP * PD;
         st.v[i] = *reinterpret_cast<const u32x4*>(src + uint32_t(o));
       }
     }
@@ -189,17 +201,17 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     for (int i = 0; i < VEC_PER_THREAD; ++i) {
       const int f = tid + 256 * i;
       if (VEC_PER_TILE % 256 == 0 || f < VEC_PER_TILE)
-        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * PD)]) =
-            SQ ? (st.v[i] ^ 0x80808080u) : st.v[i];  // SQ8: codes c to int8 c - 128
+        *reinterpret_cast<u32x4*>(&xs[buf][vrow[i] * STR + (voff[i] - vrow[i] * RP * PD)]) =
+            SQ == 1 ? (st.v[i] ^ 0x80808080u) : st.v[i];  // SQ8: codes c to int8 c - 128
     }
     if (kc == 0 && tid < kGemmRows) {
       const uint32_t valid = min(uint32_t(kGemmRows), r_end - (r_begin + uint32_t(tile) * kGemmRows));
       const bool ok = uint32_t(tid) < valid && (MODE != 0 || ((st.aw >> (tid & 31)) & 1u));
-      xns[tile % 3][tid] = ok ? st.n : kDead8;
+      xns[tile % 3][tid] = ok ? st.n : kDead;
     }
   };
 
-  v16i acc[QB][2];
+  v16i acc[NACC][2];
   auto step = [&](Stage& X, Stage& Y, int sidx, auto fcur) {
     constexpr int QS = decltype(fcur)::value;
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
@@ -220,11 +232,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
           init[4 * g + 3] = n4.w;
         }
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          if (SQ && qb == 0)
-            acc[qb][blk] = v16i{};  // the hi part starts at 0, the lo part at the row start
+        for (int s = 0; s < NACC; ++s) {
+          if (SQ && s + 1 < NACC)
+            acc[s][blk] = v16i{};  // the high parts start at 0, the lowest at the row start
           else
-            acc[qb][blk] = init;
+            acc[s][blk] = init;
         }
       }
     }
@@ -234,10 +246,24 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     for (int kb = 0; kb < NKB; ++kb) {
       const v4i x0 = *reinterpret_cast<const v4i*>(xa0 + kb * 32);
       const v4i x1 = *reinterpret_cast<const v4i*>(xa1 + kb * 32);
+      if constexpr (SQ == 2) {  // rows [h | l]: h.h, h.l + l.h, l.l
+        const v4i y0 = *reinterpret_cast<const v4i*>(xa0 + KC + kb * 32);
+        const v4i y1 = *reinterpret_cast<const v4i*>(xa1 + KC + kb * 32);
+        const v4i qh = qv[QS][0][kb], ql = qv[QS][1][kb];
+        acc[0][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, qh, acc[0][0], 0, 0, 0);
+        acc[0][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, qh, acc[0][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, ql, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, ql, acc[1][1], 0, 0, 0);
+        acc[1][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y0, qh, acc[1][0], 0, 0, 0);
+        acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y1, qh, acc[1][1], 0, 0, 0);
+        acc[2][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y0, ql, acc[2][0], 0, 0, 0);
+        acc[2][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y1, ql, acc[2][1], 0, 0, 0);
+      } else {
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        acc[qb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, qv[QS][qb][kb], acc[qb][0], 0, 0, 0);
-        acc[qb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, qv[QS][qb][kb], acc[qb][1], 0, 0, 0);
+        for (int qb = 0; qb < QB; ++qb) {
+          acc[qb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, qv[QS][qb][kb], acc[qb][0], 0, 0, 0);
+          acc[qb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, qv[QS][qb][kb], acc[qb][1], 0, 0, 0);
+        }
       }
     }
     if (sidx + 1 < nstages) store_stage(X, sidx + 1);
@@ -245,11 +271,17 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     if (kc != NKC - 1) return;
 
     const uint32_t lane_base = base + 4 * h;  // row of output r = 0 of block 0
-    if constexpr (SQ) {  // u = 256 acc_hi + acc_lo, into the first set
+    if constexpr (SQ == 1) {  // u = 256 acc_hi + acc_lo, into the first set
 #pragma unroll
       for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[0][blk][r] = (acc[0][blk][r] << 8) + acc[1][blk][r];
+    } else if constexpr (SQ == 2) {  // u = 2^16 acc_hh + 2^8 acc_mid + acc_ll
+#pragma unroll
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[0][blk][r] = (acc[0][blk][r] << 16) + (acc[1][blk][r] << 8) + acc[2][blk][r];
     }
     if (wave_live && MODE == 0) {
       // per 32-row block: the lane's largest u against the bound, one wave-uniform branch;
@@ -287,7 +319,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
       for (int qb = 0; qb < NQ; ++qb)
 #pragma unroll
         for (int blk = 0; blk < 2; ++blk) {
-          int m = kDead8;
+          int m = kDead;
           if (a.allow == nullptr) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) m = max(m, acc[qb][blk][r]);
@@ -309,7 +341,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
             const uint32_t grp = ((base >> 5) + blk) * 2 + h;
             if (grp < uint32_t(a.ngroups))
               a.gm[size_t(q[qb]) * a.ngroups + grp] =
-                  m < kLive8 ? __builtin_inff() : gemm_units(m, dq[qb]);
+                  m < kLive ? __builtin_inff() : gemm_units(m, dq[qb]);
           }
         }
     }
@@ -333,7 +365,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
         float v[kTop8];
 #pragma unroll
         for (int t = 0; t < kTop8; ++t)
-          v[t] = top[qb][t] < kLive8 ? __builtin_inff() : gemm_units(top[qb][t], dq[qb]);
+          v[t] = top[qb][t] < kLive ? __builtin_inff() : gemm_units(top[qb][t], dq[qb]);
         float4* g = reinterpret_cast<float4*>(a.gm + size_t(q[qb]) * a.ngroups +
                                               (size_t(chunk) * 2 + h) * kTop8);
 #pragma unroll
@@ -358,7 +390,14 @@ template <int PD, int METRIC>
 static void launch8_pm(int qb, int mode, int sq, hipStream_t s, int blocks, const GemmArgs& a) {
   const dim3 g(blocks), t(256);
   constexpr int OCC = PD <= 128 ? 3 : 2;  // Gemm8Occupancy
-  if (sq) {
+  if (sq == 2) {
+    if (mode == 1)
+      k_gemm8<PD, METRIC, 2, 1, 2, 2><<<g, t, 0, s>>>(a);
+    else if (mode == 2)
+      k_gemm8<PD, METRIC, 2, 2, 2, 2><<<g, t, 0, s>>>(a);
+    else
+      k_gemm8<PD, METRIC, 2, 0, 2, 2><<<g, t, 0, s>>>(a);
+  } else if (sq) {
     if (mode == 1)
       k_gemm8<PD, METRIC, 2, 1, 2, 1><<<g, t, 0, s>>>(a);
     else if (mode == 2)
@@ -455,6 +494,76 @@ int MakeRows8(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int
   *out = y;
   *init = in;
   *shift = cs;
+  return kOk;
+}
+
+// One wave per float row: v = rint(x 2^ex), v = 256 h + l, stored [h | l] per K chunk of kc
+// dims; the row's sum |v| and sum v^2 raise the dataset's maxima.
+__global__ __launch_bounds__(256) void k_to_i8_split(const float* __restrict__ X, uint32_t n,
+                                                     int pd, int kc, int ex,
+                                                     int8_t* __restrict__ y,
+                                                     uint32_t* __restrict__ l1max,
+                                                     unsigned long long* __restrict__ l2max) {
+  const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= n) return;
+  int s1 = 0;
+  unsigned long long s2 = 0;
+  int8_t* out = y + size_t(r) * 2 * pd;
+  for (int i = lane_id(); i < pd; i += kWave) {
+    const int v = int(rintf(ldexpf(X[size_t(r) * pd + i], ex)));
+    const int hi = (v + 128) >> 8;
+    const int c = i / kc, o = i - c * kc;
+    out[c * 2 * kc + o] = int8_t(hi);
+    out[c * 2 * kc + kc + o] = int8_t(v - 256 * hi);
+    s1 += v < 0 ? -v : v;
+    s2 += (unsigned long long)(int64_t(v) * v);
+  }
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    s1 += __shfl_xor(s1, off);
+    s2 += __shfl_xor(s2, off);
+  }
+  if (lane_id() == 0) {
+    atomicMax(l1max, uint32_t(s1));
+    atomicMax(l2max, s2);
+  }
+}
+
+int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
+                   const RowStats& st, int8_t** out, int* exp, float* l1max, float* l2max) {
+  *out = nullptr;
+  *exp = 0;
+  *l1max = *l2max = 0.f;
+  if (n == 0 || !Gemm8Supported(pd) || !(st.max_abs > 0.f) || !(st.max_abs <= 3.0e38f) ||
+      !(st.xn_max > 0.f) || !(st.xn_max <= 3.0e38f))
+    return kOk;
+  // the largest ||x 2^ex|| at most 2^13.9, so every |v| < 2^14 and, with a query scaled the
+  // same way, |sum v_x v_q| < 2^28
+  const int ex = int(std::floor(13.9 - 0.5 * std::log2(double(st.xn_max))));
+  int8_t* y = nullptr;
+  uint32_t* m1 = nullptr;
+  VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * 2));
+  hipError_t err = hipMalloc(reinterpret_cast<void**>(&m1), 16);
+  if (err == hipSuccess) err = hipMemsetAsync(m1, 0, 16, s);
+  if (err == hipSuccess) {
+    k_to_i8_split<<<dim3(unsigned((n + 3) / 4)), 256, 0, s>>>(
+        rows, uint32_t(n), int(pd), Gemm8KcSplit(int(pd)), ex, y, m1,
+        reinterpret_cast<unsigned long long*>(m1 + 2));
+    err = hipGetLastError();
+  }
+  uint32_t h[4] = {0, 0, 0, 0};
+  if (err == hipSuccess) err = hipMemcpyAsync(h, m1, 16, hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  (void)hipFree(m1);
+  if (err != hipSuccess) {
+    (void)hipFree(y);
+    return SetError(kInternal, std::string("int8 split rows: ") + hipGetErrorString(err));
+  }
+  unsigned long long q2 = 0;
+  std::memcpy(&q2, h + 2, 8);
+  *out = y;
+  *exp = ex;
+  *l1max = float(h[0]);
+  *l2max = float(std::sqrt(double(q2)) * (1.0 + 1e-6));
   return kOk;
 }
 

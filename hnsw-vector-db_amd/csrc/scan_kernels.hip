@@ -319,7 +319,8 @@ int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* sca
 // sample is an evenly strided subset of the rows.
 __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __restrict__ X16,
                                 int pd16, const uint8_t* __restrict__ C,
-                                const int8_t* __restrict__ X8, const int* __restrict__ init8,
+                                const int8_t* __restrict__ X8, int pd8,
+                                const int* __restrict__ init8,
                                 const float* __restrict__ rn, uint32_t N, int pd, int bits,
                                 uint32_t smax,
                                 float* __restrict__ SX, uint16_t* __restrict__ SX16,
@@ -332,14 +333,15 @@ __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __r
   for (int i = threadIdx.x; i < pd; i += blockDim.x) {
     if (X) SX[size_t(p) * pd + i] = X[size_t(row) * pd + i];
     if (C) SC[size_t(p) * pd + i] = C[size_t(row) * pd + i];
-    if (X8) SX8[size_t(p) * pd + i] = X8[size_t(row) * pd + i];
   }
+  for (int i = threadIdx.x; X8 != nullptr && i < pd8; i += blockDim.x)
+    SX8[size_t(p) * pd8 + i] = X8[size_t(row) * pd8 + i];
   for (int i = threadIdx.x; X16 != nullptr && i < pd16; i += blockDim.x)
     SX16[size_t(p) * pd16 + i] = X16[size_t(row) * pd16 + i];
   if (threadIdx.x == 0) {
     Srn[p] = rn[row];
     Sid[p] = row;
-    if (X8) Sinit8[p] = init8[row];
+    if (init8) Sinit8[p] = init8[row];
   }
 }
 
@@ -356,7 +358,8 @@ size_t SampleBytes(const ScanSource& src, uint32_t smax) {
          al(src.X16 != nullptr ? size_t(smax) * pd * src.x16_parts * sizeof(uint16_t) : 0) +
          al(src.kind == 1 ? size_t(smax) * pd : 0) + al(size_t(smax) * sizeof(float)) +
          al(size_t(smax) * sizeof(uint32_t)) +
-         (src.X8 != nullptr ? al(size_t(smax) * pd) + al(size_t(smax) * sizeof(int)) : 0) + 256;
+         (src.X8 != nullptr ? al(size_t(smax) * pd * src.x8_parts) + al(size_t(smax) * sizeof(int))
+                            : 0) + 256;
 }
 
 int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
@@ -376,12 +379,14 @@ int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
   src->SC = reinterpret_cast<uint8_t*>(take(src->kind == 1 ? size_t(smax) * pd : 0));
   src->Srn = reinterpret_cast<float*>(take(size_t(smax) * sizeof(float)));
   src->Sid = reinterpret_cast<uint32_t*>(take(size_t(smax) * sizeof(uint32_t)));
-  src->SX8 = reinterpret_cast<int8_t*>(take(src->X8 != nullptr ? size_t(smax) * pd : 0));
+  src->SX8 = reinterpret_cast<int8_t*>(
+      take(src->X8 != nullptr ? size_t(smax) * pd * src->x8_parts : 0));
   src->Sinit8 = reinterpret_cast<int*>(take(src->X8 != nullptr ? size_t(smax) * sizeof(int) : 0));
   k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
                                              src->X16, int(pd) * src->x16_parts,
                                              src->kind == 1 ? src->C : nullptr, src->X8,
-                                             src->init8, src->rn, src->N, int(pd), bits, smax,
+                                             int(pd) * src->x8_parts, src->init8, src->rn,
+                                             src->N, int(pd), bits, smax,
                                              src->SX, src->SX16, src->SC, src->SX8,
                                              src->Sinit8, src->Srn, src->Sid);
   VDBG_HIP(hipGetLastError());
@@ -490,6 +495,9 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
   }
   s = wave_sum(s);
   s2 = wave_sum(s2);
+  // float rows on the int8 GEMM: the batch is scaled by its largest ||q||
+  if (a.kind == 0 && a.mb8 != nullptr && lane_id() == 0)
+    atomicMax(a.mb8, __float_as_uint(sqrtf(s) * (1.f + 1e-6f)));
   lo = wave_min(lo);
   hi = wave_max(hi);
   ma = wave_max(ma);
@@ -561,7 +569,7 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     // magnitude <= 4096); the fp16 GEMM accumulates ||x||^2 - 2 q.x (or -q.x) from the row
     // norm, every partial sum bounded by (|q| + R)^2 with R the largest row norm.  Below 2^24
     // its values are the fp32 GEMM's bit for bit.
-    if (a.all16 != nullptr && (a.kind == 1 || a.x16_parts == 2)) {
+    if (a.Qf != nullptr && (a.kind == 1 || a.x16_parts == 2)) {
       a.Qf[q] = ldexpf(a.metric == 0 ? -2.f : -1.f, -sc - (a.kind == 0 ? a.x16_exp : 0));
       if (!split_ok) atomicAnd(a.all16, 0);
     } else if (a.all16 != nullptr) {
@@ -622,37 +630,56 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
 // start rint(||c scale||^2 2^(e-1)) must stay below 2^27 too, or the batch takes the fp16 GEMM.
 // The value (-M (sum c' v - start) - M 128 sum v) 2^-e misses the fp32 GEMM value by at most
 // 2^-e (M 255 sum|B_i 2^e - v_i| + [L2] 1): that term is added to the query's bound (eb8).
+//
+// Float rows (fr = 1, gemm8.hip SQ = 2): B = q itself scaled by 2^eq (||v|| <= 2^13.9 for the
+// batch's largest ||q||, mb8), the rows already held as v_x = rint(x 2^ex); e = ex + eq.
+// Every (row, query) must keep |sum v_x v_q| + row start below 2^29 (checked with the rows'
+// largest ||v_x||), and the value misses the fp32 GEMM value by at most
+// M 2^-e (sum|v_x| / 2 + sum|v_q| / 2 + pd / 4) (+ 2^-e for the L2 row start).
 struct Sq8Op8Args {
   const float* Qb;
   int nq, pd, metric;
   const uint32_t* mb8;
-  float rn_max;       // max ||code * scale||^2 over the rows
+  float rn_max;       // max ||code * scale||^2 (SQ8) or ||x||^2 (float rows) over the rows
   const float* eb;    // the fp32-side bound of k_query_prep
   int8_t* Q8;         // [q][2][pd]: hi, lo
-  int* Qd;            // M 128 sum(v)
+  int* Qd;            // M 128 sum(v) (SQ8), 0 (float rows)
   float* eb8;
   int* e8;
   int* all8;
+  int fr;             // float rows
+  int ex;             // their scale exponent
+  float l1max, l2max; // their largest sum |v_x| and ||v_x||
 };
 
 __global__ __launch_bounds__(256) void k_sq8_operand8(Sq8Op8Args a) {
   const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= a.nq) return;
   const float mb = __uint_as_float(*a.mb8);
-  int L = 0;
-  while (L < 14 && (int64_t(2) << L) * a.pd <= (int64_t(1) << 20)) ++L;
+  int L = 14;
+  if (!a.fr) {
+    L = 0;
+    while (L < 14 && (int64_t(2) << L) * a.pd <= (int64_t(1) << 20)) ++L;
+  }
   int e = 0;
   bool ok = mb <= 3.0e38f;
   if (ok && mb > 0.f) {
-    int ex = 0;
-    (void)frexpf(mb, &ex);  // mb <= 2^ex
-    e = L - ex;
+    if (a.fr) {
+      e = int(floor(13.9 - log2(double(mb))));  // ||q 2^e|| <= 2^13.9
+    } else {
+      int ex = 0;
+      (void)frexpf(mb, &ex);  // mb <= 2^ex
+      e = L - ex;
+    }
   }
-  if (a.metric == 0 && !(ldexp(double(a.rn_max), e - 1) < 134217728.0)) ok = false;
+  const int et = a.fr ? e + a.ex : e;  // the exponent of the values
+  const double start_lim = a.fr ? 536870912.0 : 134217728.0;  // 2^29 or 2^27
+  const double start = a.metric == 0 ? ldexp(double(a.rn_max), et - 1) : 0.0;
+  if (!(start < start_lim)) ok = false;
   const float* b = a.Qb + size_t(q) * a.pd;
   int8_t* o = a.Q8 + size_t(q) * 2 * a.pd;
-  int sv = 0;
-  float sd = 0.f;
+  int sv = 0, sa = 0;
+  float sd = 0.f, s2 = 0.f;
   for (int i = lane_id(); i < a.pd; i += kWave) {
     const float x = ok ? ldexpf(b[i], e) : 0.f;  // |x| <= 2^L
     const float v = rintf(x);
@@ -661,17 +688,34 @@ __global__ __launch_bounds__(256) void k_sq8_operand8(Sq8Op8Args a) {
     o[i] = int8_t(hi);
     o[a.pd + i] = int8_t(vi - 256 * hi);
     sv += vi;
+    sa += vi < 0 ? -vi : vi;
+    s2 = fmaf(v, v, s2);
     sd += fabsf(x - v);  // exact: x and its nearest integer share the exponent range
   }
-  for (int off = kWave / 2; off > 0; off >>= 1) sv += __shfl_xor(sv, off);
+  for (int off = kWave / 2; off > 0; off >>= 1) {
+    sv += __shfl_xor(sv, off);
+    sa += __shfl_xor(sa, off);
+  }
   sd = wave_sum(sd);
+  s2 = wave_sum(s2);
   if (lane_id() == 0) {
     const int M = a.metric == 0 ? 2 : 1;
-    a.Qd[q] = M * 128 * sv;
-    const double quant = ldexp(M * 255.0 * double(sd) * (1.0 + 1e-6 * a.pd) +
-                                   (a.metric == 0 ? 1.0 : 0.0), -e);
+    double quant;
+    if (a.fr) {
+      // |sum v_x v_q| <= ||v_x|| ||v_q||: with the row start it must stay below 2^29
+      if (!(double(a.l2max) * sqrt(double(s2) * (1.0 + 1e-6 * a.pd)) + start <
+            536870912.0 * (1.0 - 1e-3)))
+        atomicAnd(a.all8, 0);
+      a.Qd[q] = 0;
+      quant = ldexp(M * (0.5 * double(a.l1max) + 0.5 * double(sa) + 0.25 * a.pd) +
+                        (a.metric == 0 ? 1.0 : 0.0), -et);
+    } else {
+      a.Qd[q] = M * 128 * sv;
+      quant = ldexp(M * 255.0 * double(sd) * (1.0 + 1e-6 * a.pd) + (a.metric == 0 ? 1.0 : 0.0),
+                    -e);
+    }
     a.eb8[q] = float((double(a.eb[q]) + quant) * 1.001);
-    if (q == 0) *a.e8 = e;
+    if (q == 0) *a.e8 = et;
     if (!ok) atomicAnd(a.all8, 0);
   }
 }
@@ -1473,9 +1517,17 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
   // integer rows spanning at most 256 values may rank on the int8 GEMM (gemm8.hip)
   const bool try8 = try16 && c->int8_gemm && split == 0 && src->X8 != nullptr;
-  // SQ8 codes may rank on the int8 GEMM with the query operand in two int8 parts
+  // SQ8 codes may rank on the int8 GEMM with the query operand in two int8 parts, float rows
+  // with both operands in two parts
   const bool try8s = try16 && c->int8_gemm && src->kind == 1 && Gemm8Supported(pd);
-  const bool try8any = try8 || try8s;
+  // (float rows only for GEMMs large enough to repay the batch's operand pass and flag
+  // readback: the fp16 split GEMM costs about 2 N nq pd / 2e14 s, the int8 one 0.6 of that)
+  const bool try8f = c->fp16_gemm && c->int8_gemm && split == 2 && src->X8 != nullptr &&
+                     src->x8_parts == 2 && Gemm8Supported(pd) &&
+                     double(N) * double(nq) * double(pd) >= c->int8_float_min_work;
+  const bool try8op = try8s || try8f;  // the two-part query operand (k_sq8_operand8)
+  const bool try8any = try8 || try8op;
+  const int sq8 = try8s ? 1 : (try8f ? 2 : 0);
   // Sample size: about kk * N / S rows pass the threshold per query, and every pass costs a
   // scattered buffer write and a select insertion (and on the exact fp16 GEMM every 32-row
   // block holding one takes the per-value test), while the pre-pass costs S / N of the main
@@ -1518,7 +1570,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const Plan p32 = make_plan(1, 128, slots);
   const Plan p16 = split ? make_plan(2, 128, slots)
                          : (nq > 128 ? make_plan(2, 256, slots) : make_plan(1, 128, slots));
-  const Plan p8 = try8s ? make_plan(2, 128, Gemm8Occupancy(pd) * c->cu_count)
+  const Plan p8 = try8op ? make_plan(2, 128, (try8f ? 2 : Gemm8Occupancy(pd)) * c->cu_count)
                  : (nq > 128 ? make_plan(2, 256, Gemm8Occupancy(pd) * c->cu_count) : p16);
   auto cand_bytes = [&](const Plan& p) {
     return size_t(nq) * p.nseg * (sizeof(uint32_t) + size_t(p.caph) * sizeof(uint2));
@@ -1542,7 +1594,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                       size_t(nq) * gm_groups * sizeof(float) + cand_need +
                       (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
                       (try8 ? nq * pd + nq * sizeof(int) : 0) +
-                      (try8s ? 2 * nq * pd + nq * (sizeof(int) + sizeof(float)) : 0) + 26 * 256;
+                      (try8op ? 2 * nq * pd + nq * (sizeof(int) + sizeof(float)) : 0) + 26 * 256;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
@@ -1557,19 +1609,20 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   char* cand_base = w.take<char>(cand_need);
   uint16_t* Q16 = try16 ? w.take<uint16_t>((split ? 2 : 1) * nq * pd) : nullptr;
   float* Qf = try16 && split ? w.take<float>(nq) : nullptr;
-  int* all16 = try16 ? w.take<int>(2) : nullptr;  // [0] fp16 bounds, [1] int8 bounds
+  int* all16 = try16 || try8any ? w.take<int>(2) : nullptr;  // [0] fp16, [1] int8 bounds
   int* all8 = try8any ? all16 + 1 : nullptr;
-  int8_t* Q8 = try8any ? w.take<int8_t>((try8s ? 2 : 1) * nq * pd) : nullptr;
+  int8_t* Q8 = try8any ? w.take<int8_t>((try8op ? 2 : 1) * nq * pd) : nullptr;
   int* Qd = try8any ? w.take<int>(nq) : nullptr;
-  float* eb8 = try8s ? w.take<float>(nq) : nullptr;
-  int* e8 = try8s ? w.take<int>(2) : nullptr;  // [0] exponent, [1] max |B| bits
-  uint32_t* mb8 = try8s ? reinterpret_cast<uint32_t*>(e8 + 1) : nullptr;
-  uint32_t* ones = try16 ? w.take<uint32_t>(1) : nullptr;  // the fp16 GEMM's no-filter word
+  float* eb8 = try8op ? w.take<float>(nq) : nullptr;
+  int* e8 = try8op ? w.take<int>(2) : nullptr;  // [0] exponent, [1] max |B| bits
+  uint32_t* mb8 = try8op ? reinterpret_cast<uint32_t*>(e8 + 1) : nullptr;
+  // the no-filter word of the fp16 and int8 GEMMs
+  uint32_t* ones = try16 || try8any ? w.take<uint32_t>(1) : nullptr;
   VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
   VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
-  if (try16) VDBG_HIP(hipMemsetD32Async(all16, 1, 2, s));
-  if (try16) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
-  if (try8s) VDBG_HIP(hipMemsetAsync(e8, 0, 2 * sizeof(int), s));
+  if (all16 != nullptr) VDBG_HIP(hipMemsetD32Async(all16, 1, 2, s));
+  if (ones != nullptr) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
+  if (try8op) VDBG_HIP(hipMemsetAsync(e8, 0, 2 * sizeof(int), s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
@@ -1579,8 +1632,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
     VDBG_HIP(hipGetLastError());
-    if (try8s) {
-      Sq8Op8Args oa{Qb, int(nq), int(pd), src->metric, mb8, src->rn_max, eb, Q8, Qd, eb8, e8, all8};
+    if (try8op) {
+      Sq8Op8Args oa{try8s ? Qb : Q, int(nq), int(pd), src->metric, mb8,
+                    try8s ? src->rn_max : src->stats.xn_max, eb, Q8, Qd, eb8, e8, all8,
+                    try8f ? 1 : 0, src->x8_exp, src->x8_l1max, src->x8_l2max};
       k_sq8_operand8<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(oa);
       VDBG_HIP(hipGetLastError());
     }
@@ -1590,13 +1645,13 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // NaN or infinite GEMM values and bound, its certificate fails and it is re-scanned
   // exactly, as on the fp32 GEMM.
   bool use16 = try16 && split != 0, use8 = false;
-  if ((try16 && split == 0) || try8s) {
+  if ((try16 && split == 0) || try8op) {
     VDBG_RETURN_IF_ERROR(ReadWords(c, reinterpret_cast<const uint32_t*>(all16), 2, s));
     use8 = try8any && c->host_pinned[1] != 0;
-    use16 = !use8 && (split != 0 || c->host_pinned[0] != 0);
+    use16 = try16 && !use8 && (split != 0 || c->host_pinned[0] != 0);
   }
   // the bound of the GEMM the batch ranks on
-  const float* ebx = use8 && try8s ? eb8 : eb;
+  const float* ebx = use8 && try8op ? eb8 : eb;
   c->last_gemm_bits = use8 ? 8 : (use16 ? 16 : 32);
   const Plan& P = use8 ? p8 : (use16 ? p16 : p32);
   const int nchunks = P.nchunks;
@@ -1633,8 +1688,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       sg.e8 = e8;
       GemmGrid(sg, P.nqt, P.schunks, &sblocks);
       if (top8) sg.ngroups = ngroups8;
-      VDBG_RETURN_IF_ERROR(
-          LaunchGemm8(pd, metric, 2, top8 ? 2 : 1, try8s ? 1 : 0, s, sblocks, sg));
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, top8 ? 2 : 1, sq8, s, sblocks, sg));
     } else if (use16 && P.qb == 2) {
       sg.X16 = src->SX16;
       sg.Q16 = Q16;
@@ -1683,7 +1737,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       ga.e8 = e8;
       ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
       ga.aw_mask = allow != nullptr ? ~0u : 0u;
-      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, P.qb, 0, try8s ? 1 : 0, s, blocks, ga));
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, P.qb, 0, sq8, s, blocks, ga));
     } else if (use16) {
       ga.X16 = src->X16;
       ga.Q16 = Q16;

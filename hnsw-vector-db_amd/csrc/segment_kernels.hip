@@ -17,6 +17,7 @@
 #include <vector>
 
 #include "vdbg_device.h"
+#include "gemm.h"
 #include "vdbg_internal.h"
 
 namespace vdbg {
@@ -113,8 +114,17 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t nwords = (size_t(N) + 63) / 64;
   const size_t row_bytes = src->kind == 0 ? pd * sizeof(float) : pd;
   void* buf = nullptr;
-  const size_t row16_bytes = src->X16 != nullptr ? src->x16_parts * pd * sizeof(uint16_t) : 0;
-  const size_t row8_bytes = src->X8 != nullptr ? pd : 0;  // and the int8 copy's start
+  // Float rows: a batch large enough for the int8 two-part GEMM ranks on it, so their fp16
+  // pairs are not gathered (a batch failing the int8 check then takes the fp32 GEMM);
+  // smaller batches keep the fp16 pairs and skip the int8 copy.
+  bool keep16 = src->X16 != nullptr, keep8 = src->X8 != nullptr;
+  if (src->kind == 0 && src->x16_parts == 2 && src->x8_parts == 2 && keep8) {
+    const bool int8 = c->fp16_gemm && c->int8_gemm && Gemm8Supported(pd) &&
+                      double(count) * double(nq) * double(pd) >= c->int8_float_min_work;
+    (int8 ? keep16 : keep8) = false;
+  }
+  const size_t row16_bytes = keep16 ? src->x16_parts * pd * sizeof(uint16_t) : 0;
+  const size_t row8_bytes = keep8 ? pd * src->x8_parts : 0;  // the int8 copy
   // the compacted source's sample lives in the same stream-ordered allocation
   ScanSource cs = *src;
   cs.N = count;
@@ -124,7 +134,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                                             static_cast<uint32_t*>(nullptr), int(nwords), s));
   const size_t bytes = (nwords + 1) * 4 * 2 +
                        size_t(count) * (4 + 4 + row_bytes + row16_bytes + row8_bytes +
-                                        (row8_bytes != 0 ? 4 : 0)) +
+                                        (src->init8 != nullptr ? 4 : 0)) +
                        sample_bytes + tmp_bytes + 4096 + 512 + 16 * 256;
   // the context's compaction scratch: reused in stream order by the next call
   Workspace& w = c->wsc;
@@ -139,7 +149,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   void* rows = take(size_t(count) * row_bytes + 16);
   void* rows16 = row16_bytes != 0 ? take(size_t(count) * row16_bytes + 16) : nullptr;
   void* rows8 = row8_bytes != 0 ? take(size_t(count) * row8_bytes + 16) : nullptr;
-  int* init8 = row8_bytes != 0 ? reinterpret_cast<int*>(take(size_t(count) * 4 + 4)) : nullptr;
+  int* init8 = src->init8 != nullptr ? reinterpret_cast<int*>(take(size_t(count) * 4 + 4)) : nullptr;
   void* sample = take(sample_bytes);
   void* tmp = nullptr;
   {
@@ -166,9 +176,10 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       const size_t row_u4 = row8_bytes / 16;
       k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
           reinterpret_cast<const uint4*>(src->X8), row_u4, ids, count, static_cast<uint4*>(rows8));
-      k_gather_u32<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(
-          reinterpret_cast<const uint32_t*>(src->init8), ids, count,
-          reinterpret_cast<uint32_t*>(init8));
+      if (init8 != nullptr)
+        k_gather_u32<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(
+            reinterpret_cast<const uint32_t*>(src->init8), ids, count,
+            reinterpret_cast<uint32_t*>(init8));
     }
     k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
     VDBG_HIP(hipGetLastError());

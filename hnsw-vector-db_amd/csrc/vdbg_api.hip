@@ -183,8 +183,14 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
       return rc;
     }
   }
-  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr && d.rows16_parts == 1) {
-    rc = MakeRows8(c, c->stream, d.rows, n, pd, metric, d.stats, &d.rows8, &d.init8, &d.c8);
+  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr) {
+    if (d.rows16_parts == 1) {
+      rc = MakeRows8(c, c->stream, d.rows, n, pd, metric, d.stats, &d.rows8, &d.init8, &d.c8);
+    } else {
+      rc = MakeRows8Split(c, c->stream, d.rows, n, pd, d.stats, &d.rows8, &d.rows8_exp,
+                          &d.rows8_l1max, &d.rows8_l2max);
+      d.rows8_parts = 2;
+    }
     if (rc != kOk) {
       (void)hipFree(d.rows16);
       (void)hipFree(d.rows);
@@ -199,6 +205,10 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   d.src.X8 = d.rows8;
   d.src.init8 = d.init8;
   d.src.c8 = d.c8;
+  d.src.x8_parts = d.rows8_parts;
+  d.src.x8_exp = d.rows8_exp;
+  d.src.x8_l1max = d.rows8_l1max;
+  d.src.x8_l2max = d.rows8_l2max;
   d.src.x16_parts = d.rows16_parts;
   d.src.x16_exp = d.rows16_exp;
   d.src.rn = d.norms;
@@ -384,6 +394,14 @@ int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable) {
   if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
   std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
   ctx->c.int8_gemm = enable != 0;
+  return kOk;
+}
+
+int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  if (!(work >= 0.0)) return SetError(kInvalidArgument, "work must be >= 0");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.int8_float_min_work = work;
   return kOk;
 }
 

@@ -103,6 +103,7 @@ struct Ctx {
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
   bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
   bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
+  double int8_float_min_work = 2e10;  // float rows: smallest N nq pd for the int8 GEMM
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 
@@ -117,9 +118,15 @@ struct ScanSource {
                                   // per K chunk), kind 1 codes exactly (x16_parts 1)
   int x16_parts = 1;
   int x16_exp = 0;
-  const int8_t* X8 = nullptr;   // kind 0 rows - c8 as int8 for the int8 GEMM (gemm8.hip), or null
-  const int* init8 = nullptr;   // its accumulator start per row
+  const int8_t* X8 = nullptr;   // kind 0 rows for the int8 GEMM (gemm8.hip), or null: integer
+                                // rows - c8 (x8_parts 1), or float rows 2^x8_exp-scaled and
+                                // rounded, as int8 h + l pairs ([h | l] per K chunk, x8_parts 2)
+  const int* init8 = nullptr;   // x8_parts 1: its accumulator start per row
   int c8 = 0;
+  int x8_parts = 1;
+  int x8_exp = 0;
+  float x8_l1max = 0.f;         // x8_parts 2: the largest sum |v| and |v| of a row's integers
+  float x8_l2max = 0.f;
   const uint8_t* C = nullptr;   // kind 1: n x pd codes
   const float* rn = nullptr;    // ||x||^2 (flat) or ||code * scale||^2 (SQ8)
   const float* vmin = nullptr;  // SQ8 quantizer (device)
@@ -149,6 +156,8 @@ struct Dataset {
   int8_t* rows8 = nullptr;     // int8 copy of the rows (see ScanSource::X8)
   int* init8 = nullptr;
   int c8 = 0;
+  int rows8_parts = 1, rows8_exp = 0;
+  float rows8_l1max = 0.f, rows8_l2max = 0.f;
   size_t n = 0, dim = 0, pd = 0;
   int metric = 0;
   RowStats stats;
@@ -217,6 +226,11 @@ int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, in
 // accumulator start (gemm8.hip); *out stays null when not applicable.
 int MakeRows8(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int metric,
               const RowStats& st, int8_t** out, int** init, int* shift);
+// Float rows as two int8 parts for the int8 GEMM (gemm8.hip, SQ = 2): v = rint(x 2^*exp) with
+// ||v|| < 2^14, v = 256 h + l, stored [h | l] per Gemm8KcSplit chunk; *l1max / *l2max the
+// largest sum |v| / ||v|| of a row.  *out stays null when not applicable.
+int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
+                   const RowStats& st, int8_t** out, int* exp, float* l1max, float* l2max);
 
 // Top-kk rows by the source's exact distance for nq queries (device pointers).
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,

@@ -59,6 +59,7 @@ _SIGS = {
     "vdbg_ctx_kernels": (C.c_char_p, [_vp]),
     "vdbg_ctx_set_fp16_gemm": (C.c_int, [_vp, C.c_int]),
     "vdbg_ctx_set_int8_gemm": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_int8_float_min_work": (C.c_int, [_vp, C.c_double]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_reset": (C.c_int, [_vp]),
     "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
@@ -188,6 +189,11 @@ class Context:
         """Let integer flat rows spanning at most 256 values rank on int8 MFMA (the
         default).  Results are identical."""
         _check(lib.vdbg_ctx_set_int8_gemm(self.h, 1 if enable else 0))
+
+    def set_int8_float_min_work(self, work):
+        """Smallest rows x queries x padded_dim of a float-row batch that ranks on the int8
+        GEMM (default 2e10).  Results are identical either way."""
+        _check(lib.vdbg_ctx_set_int8_float_min_work(self.h, float(work)))
 
     def profile(self, enable=True):
         _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))

@@ -90,12 +90,19 @@ const char* vdbg_ctx_kernels(vdbg_ctx* ctx);
  * SQ8 indexes 2 bytes per code).  Returned results are identical either way; 0 ranks on the
  * fp32 GEMM.  No counterpart in the reference. */
 int vdbg_ctx_set_fp16_gemm(vdbg_ctx* ctx, int enable);
-/* Whether integer-valued flat rows spanning at most 256 consecutive values may rank on int8
- * MFMA (default 1; it also needs fp16 ranking on): the rows and each batch's queries shifted
- * into int8 by one per-dataset constant, products and sums exact in int32.  Datasets created
- * while it is on keep an int8 copy of such rows (1 byte per value, 4 bytes per row).
+/* Whether scans may rank on int8 MFMA (default 1; it also needs fp16 ranking on):
+ * integer-valued flat rows spanning at most 256 consecutive values shifted into int8 (exact);
+ * SQ8 codes against the query operand rounded to integers in two int8 parts; float rows and
+ * queries scaled by powers of two, rounded and split into two int8 parts each (under a
+ * widened rounding bound).  Datasets created while it is on keep an int8 copy of their rows
+ * (1 byte per value and 4 per row for integer rows, 2 bytes per value for float rows).
  * Returned results are identical either way.  No counterpart in the reference. */
 int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable);
+/* The smallest rows x queries x padded_dim product of a float-row batch that ranks on the
+ * int8 GEMM (default 2e10; smaller batches keep the fp16 split GEMM, whose extra operand pass
+ * and flag readback the int8 GEMM would not repay).  Results are identical either way.  No
+ * counterpart in the reference. */
+int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work);
 
 /* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
  * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch

@@ -200,6 +200,10 @@ class Device {
   Status set_int8_gemm(bool enable) {
     return Status::FromCall(vdbg_ctx_set_int8_gemm(ctx_, enable ? 1 : 0));
   }
+  // Smallest rows x queries x padded_dim of a float-row batch ranked on int8 MFMA.
+  Status set_int8_float_min_work(double work) {
+    return Status::FromCall(vdbg_ctx_set_int8_float_min_work(ctx_, work));
+  }
   // The distance kernel set exact distances follow ("scalar", "avx2", "avx512").
   Status set_kernels(const char* name) { return Status::FromCall(vdbg_ctx_set_kernels(ctx_, name)); }
 

@@ -1,8 +1,10 @@
-"""Float rows on the split fp16 GEMM: rows and queries scaled by powers of two and split into
-fp16 h + l parts, ranked by x_h q_h + x_h q_l + x_l q_h under a rounding bound widened for
-the split.  Returned ids and distances must equal the fp32 GEMM's and the oracle's
-(FlatIndex::search, src/index/flat_index.cc:11-39) bit for bit, across K-chunk shapes,
-metrics, value ranges, filters and batch sizes."""
+"""Float rows on the two-part GEMMs.  With the int8 GEMM on (the default), rows and queries
+scaled by powers of two are rounded to integers and split into int8 h + l parts, ranked by
+2^16 h.h + 2^8 (h.l + l.h) + l.l under a bound widened for the rounding; with it off, they
+are split into fp16 h + l parts and ranked by x_h q_h + x_h q_l + x_l q_h.  Returned ids and
+distances must equal the fp32 GEMM's and the oracle's (FlatIndex::search,
+src/index/flat_index.cc:11-39) bit for bit, across K-chunk shapes, metrics, value ranges,
+filters and batch sizes."""
 import numpy as np
 import pytest
 
@@ -10,6 +12,14 @@ import vdbg
 from vdbg import datagen
 
 pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _int8_at_any_size(ctx):
+    # the test batches are small: let them take the int8 two-part GEMM whatever their size
+    ctx.set_int8_float_min_work(0)
+    yield
+    ctx.set_int8_float_min_work(2e10)
 
 
 def _check_equal(gi, gd, oi, od):
@@ -36,15 +46,26 @@ def _data(kind, n, nq, dim, seed):
             (rng.normal(0, 1, (nq, dim)) * scales).astype(np.float32))
 
 
-def _search_both(ctx, ds, qs, k, allow=None):
+def _search_both(ctx, ds, qs, k, allow=None, expect8=None):
+    # default (int8 two-part where the padded dim and the batch allow it), fp16 two-part, fp32
     gi, gd = ds.flat_search(qs, k, allow=allow)
-    assert ctx.last_gemm_bits() == 16
+    bits = ctx.last_gemm_bits()
+    assert bits in (8, 16)
+    if expect8 is not None:
+        assert bits == (8 if expect8 else 16)
+    ctx.set_int8_gemm(False)
+    try:
+        gi16, gd16 = ds.flat_search(qs, k, allow=allow)
+        assert ctx.last_gemm_bits() == 16
+    finally:
+        ctx.set_int8_gemm(True)
     ctx.set_fp16_gemm(False)
     try:
         gi32, gd32 = ds.flat_search(qs, k, allow=allow)
         assert ctx.last_gemm_bits() == 32
     finally:
         ctx.set_fp16_gemm(True)
+    _check_equal(gi, gd, gi16, gd16)
     _check_equal(gi, gd, gi32, gd32)
     return gi, gd
 
@@ -67,7 +88,8 @@ def test_split_matches_fp32_and_oracle(ctx, oracle, kind, metric, dim, n, nq, k)
     pd = vdbg.padded_dim(dim)
     base, qs = datagen.pad(base, pd), datagen.pad(qs, pd)
     ds = vdbg.Dataset(ctx, base, dim, metric=metric)
-    gi, gd = _search_both(ctx, ds, qs, k)
+    # unit rows whose padded dim is a multiple of 32 must take the int8 two-part GEMM
+    gi, gd = _search_both(ctx, ds, qs, k, expect8=True if kind == "unit" and pd % 32 == 0 else None)
     od, oi = oracle.flat_search(base, qs, k, metric=metric)
     _check_equal(gi, gd, oi, od)
     assert ctx.last_fallbacks() == 0
@@ -82,16 +104,18 @@ def test_split_filtered(ctx, oracle, frac):
     allow = np.zeros((n + 63) // 64, np.uint64)
     np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
     ds = vdbg.Dataset(ctx, base, dim, metric="cosine")
-    gi, gd = _search_both(ctx, ds, qs, 10, allow=allow)
+    gi, gd = _search_both(ctx, ds, qs, 10, allow=allow, expect8=True)
     od, oi = oracle.flat_search(base, qs, 10, metric="cosine", allow=allow)
     _check_equal(gi, gd, oi, od)
 
 
-def test_split_large_batch(ctx, oracle):
+@pytest.mark.parametrize("kind,metric", [("normal", "l2"), ("unit", "cosine")])
+def test_split_large_batch(ctx, oracle, kind, metric):
     n, nq, dim = 150000, 1100, 128
-    base, qs = _data("normal", n, nq, dim, 7201)
-    ds = vdbg.Dataset(ctx, base, dim)
+    base, qs = _data(kind, n, nq, dim, 7201)
+    ds = vdbg.Dataset(ctx, base, dim, metric=metric)
     gi, gd = ds.flat_search(qs, 10)
-    assert ctx.last_gemm_bits() == 16
-    od, oi = oracle.flat_search(base, qs, 10)
+    assert ctx.last_gemm_bits() in (8, 16)
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 10, metric=metric)
     _check_equal(gi, gd, oi, od)
