@@ -497,34 +497,40 @@ int MakeRows8(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int
   return kOk;
 }
 
-// One wave per float row: v = rint(x 2^ex), v = 256 h + l, stored [h | l] per K chunk of kc
-// dims; the row's sum |v| and sum v^2 raise the dataset's maxima.
+// Float rows to v = rint(x 2^ex), v = 256 h + l, stored [h | l] per K chunk of kc dims; each
+// wave walks rows with a grid stride and raises the dataset's largest sum |v| and sum v^2
+// once at the end (one atomic per wave, not per row).
 __global__ __launch_bounds__(256) void k_to_i8_split(const float* __restrict__ X, uint32_t n,
                                                      int pd, int kc, int ex,
                                                      int8_t* __restrict__ y,
                                                      uint32_t* __restrict__ l1max,
                                                      unsigned long long* __restrict__ l2max) {
-  const uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= n) return;
-  int s1 = 0;
-  unsigned long long s2 = 0;
-  int8_t* out = y + size_t(r) * 2 * pd;
-  for (int i = lane_id(); i < pd; i += kWave) {
-    const int v = int(rintf(ldexpf(X[size_t(r) * pd + i], ex)));
-    const int hi = (v + 128) >> 8;
-    const int c = i / kc, o = i - c * kc;
-    out[c * 2 * kc + o] = int8_t(hi);
-    out[c * 2 * kc + kc + o] = int8_t(v - 256 * hi);
-    s1 += v < 0 ? -v : v;
-    s2 += (unsigned long long)(int64_t(v) * v);
-  }
-  for (int off = kWave / 2; off > 0; off >>= 1) {
-    s1 += __shfl_xor(s1, off);
-    s2 += __shfl_xor(s2, off);
+  const uint32_t waves = gridDim.x * 4;
+  int m1 = 0;
+  unsigned long long m2 = 0;
+  for (uint32_t r = blockIdx.x * 4 + (threadIdx.x >> 6); r < n; r += waves) {
+    int s1 = 0;
+    unsigned long long s2 = 0;
+    int8_t* out = y + size_t(r) * 2 * pd;
+    for (int i = lane_id(); i < pd; i += kWave) {
+      const int v = int(rintf(ldexpf(X[size_t(r) * pd + i], ex)));
+      const int hi = (v + 128) >> 8;
+      const int c = i / kc, o = i - c * kc;
+      out[c * 2 * kc + o] = int8_t(hi);
+      out[c * 2 * kc + kc + o] = int8_t(v - 256 * hi);
+      s1 += v < 0 ? -v : v;
+      s2 += (unsigned long long)(int64_t(v) * v);
+    }
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      s1 += __shfl_xor(s1, off);
+      s2 += __shfl_xor(s2, off);
+    }
+    m1 = max(m1, s1);
+    m2 = s2 > m2 ? s2 : m2;
   }
   if (lane_id() == 0) {
-    atomicMax(l1max, uint32_t(s1));
-    atomicMax(l2max, s2);
+    atomicMax(l1max, uint32_t(m1));
+    atomicMax(l2max, m2);
   }
 }
 
@@ -545,7 +551,8 @@ int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
   hipError_t err = hipMalloc(reinterpret_cast<void**>(&m1), 16);
   if (err == hipSuccess) err = hipMemsetAsync(m1, 0, 16, s);
   if (err == hipSuccess) {
-    k_to_i8_split<<<dim3(unsigned((n + 3) / 4)), 256, 0, s>>>(
+    const unsigned blocks = unsigned(std::min<size_t>((n + 3) / 4, size_t(c->cu_count) * 8));
+    k_to_i8_split<<<dim3(blocks), 256, 0, s>>>(
         rows, uint32_t(n), int(pd), Gemm8KcSplit(int(pd)), ex, y, m1,
         reinterpret_cast<unsigned long long*>(m1 + 2));
     err = hipGetLastError();
