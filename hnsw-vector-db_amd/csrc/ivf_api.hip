@@ -242,7 +242,8 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
     rc = R <= 256 ? IvfScan(c, a, s) : IvfScanDeep(c, a, s);
   }
   if (rc == kOk && depth > 0) {
-    rc = Rerank(c, x->ds->rows, x->pd, x->metric, Q, nq, ti, R, k, out_ids, out_d, s);
+    rc = Rerank(c, x->ds->rows, x->pd, x->metric, Q, nq, ti, R, k, out_ids, out_d, s,
+                &x->ds->src);
   }
   (void)hipFreeAsync(buf, s);
   return rc;

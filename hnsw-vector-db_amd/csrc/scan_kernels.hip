@@ -1259,6 +1259,9 @@ struct RerankArgs {
   int depth, nq, k;
   uint32_t* out_ids;
   float* out_d;
+  const int8_t* X8;      // nullable: the rows' int8 copy (integer rows, x = x8 + c8)
+  int c8;
+  RowStats xs;           // the rows' value statistics
 };
 
 // Rerank (src/index/index.cc:89-95): exact fp32 distances of the candidates' rows, the k
@@ -1269,13 +1272,50 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
   if (q >= a.nq) return;
   const int lane = lane_id();
   const float* qv = a.Q + size_t(q) * a.pd;
+  // Integer rows and an integer query whose every partial sum stays below 2^24: every fp32
+  // summation order, the reference's included, gives the exact integer, so the distance is
+  // computed from the rows' int8 copy (a quarter of the bytes) in int32.
+  bool ex8 = false;
+  if (a.X8 != nullptr && a.metric != 2) {
+    float mq = 0.f, lo = __builtin_inff(), hi = -__builtin_inff();
+    int ai = 1;
+    for (int i = lane; i < a.pd; i += kWave) {
+      const float v = qv[i];
+      mq = fmaxf(mq, fabsf(v));
+      lo = fminf(lo, v);
+      hi = fmaxf(hi, v);
+      ai &= v == rintf(v) ? 1 : 0;
+    }
+    mq = wave_max(mq);
+    lo = wave_min(lo);
+    hi = wave_max(hi);
+    ai = wave_and(ai);
+    const double pd = a.pd, lim = 16777216.0, mx = a.xs.max_abs, m = mq;
+    const double range = double(fmaxf(hi, a.xs.hi)) - double(fminf(lo, a.xs.lo));
+    ex8 = a.xs.all_int && ai && pd * mx * mx < lim && pd * m * m < lim && pd * mx * m < lim &&
+          pd * range * range < lim;
+  }
+  auto exact8 = [&](uint32_t id) {
+    const int8_t* xr = a.X8 + size_t(id) * a.pd;
+    int acc = 0;
+    for (int i = 0; i < a.pd; i += 16) {
+      const int4 w = *reinterpret_cast<const int4*>(xr + i);
+      const int8_t* b = reinterpret_cast<const int8_t*>(&w);
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int x = int(b[t]) + a.c8, y = int(qv[i + t]);
+        acc += a.metric == 0 ? (x - y) * (x - y) : x * y;
+      }
+    }
+    return a.metric == 0 ? float(acc) : -float(acc);  // -0 for a zero dot, as -dot gives
+  };
   WaveKeys<E> r;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int i = e * kWave + lane;
     const uint32_t id = i < a.depth ? a.cand[size_t(q) * a.depth + i] : kNoId;
     if (id != kNoId) {
-      r.d[e] = metric_exact_k(a.kset, a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
+      r.d[e] = ex8 ? exact8(id) : metric_exact_k(a.kset, a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
       r.id[e] = id;
     } else {
       r.d[e] = __builtin_inff();
@@ -1810,12 +1850,15 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
 
 int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq,
            const uint32_t* cand, size_t depth, size_t k, uint32_t* out_ids, float* out_d,
-           hipStream_t s) {
+           hipStream_t s, const ScanSource* rows) {
   if (nq == 0 || k == 0) return kOk;
   if (std::max(depth, k) > 256)
     return RerankLarge(c, X, pd, metric, Q, nq, cand, depth, k, out_ids, out_d, s);
   const int E = pow2_e(std::max(depth, k));
-  RerankArgs ra{X, Q, pd, metric, c->kset, cand, int(depth), int(nq), int(k), out_ids, out_d};
+  const bool int8 = rows != nullptr && rows->X8 != nullptr && rows->x8_parts == 1 && pd % 16 == 0;
+  RerankArgs ra{X, Q, pd, metric, c->kset, cand, int(depth), int(nq), int(k), out_ids, out_d,
+                int8 ? rows->X8 : nullptr, int8 ? rows->c8 : 0,
+                rows != nullptr ? rows->stats : RowStats{}};
   ProfScope ps(c, "rerank", s);
   VDBG_DISPATCH_E(E, launch_rerank, s, ra);
   VDBG_HIP(hipGetLastError());

@@ -242,7 +242,7 @@ static int Sq8Search(Sq8Index* x, const float* Q, size_t nq, size_t k, size_t de
   int rc = ScanMasked(c, &x->src, Q, nq, kk, allow, ti, td, s);
   if (rc == kOk)
     rc = Rerank(c, x->ds->rows, int(x->ds->pd), x->ds->metric, Q, nq, ti, kk, k, out_ids, out_d,
-                s);
+                s, &x->ds->src);
   (void)hipFreeAsync(ti, s);
   (void)hipFreeAsync(td, s);
   return rc;
@@ -293,7 +293,7 @@ static int RerankChecked(Ctx* c, Dataset* d, const float* Q, size_t nq, const ui
     VDBG_HIP(hipGetLastError());
   } else {
     VDBG_RETURN_IF_ERROR(Rerank(c, d->rows, int(d->pd), d->metric, Q, nq, cand, depth, k,
-                                out_ids, out_d, s));
+                                out_ids, out_d, s, &d->src));
   }
   if (dist_comps != nullptr) {
     if (depth == 0) {

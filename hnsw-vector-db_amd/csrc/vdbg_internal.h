@@ -236,9 +236,11 @@ int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
 // Exact fp32 distances of `depth` candidate rows per query, the k smallest.
+// rows (nullable): the dataset's scan source, whose int8 copy of integer rows serves
+// exact-integer queries.
 int Rerank(Ctx* c, const float* X, int pd, int metric, const float* Q, size_t nq,
            const uint32_t* cand, size_t depth, size_t k, uint32_t* out_ids, float* out_d,
-           hipStream_t s);
+           hipStream_t s, const ScanSource* rows = nullptr);
 int Sq8Train(Ctx* c, const Dataset* ds, float* vmin_dev, float* scale_dev, hipStream_t s);
 int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* scale_dev,
               uint8_t* codes, float* yn, hipStream_t s, bool codes_given = false);

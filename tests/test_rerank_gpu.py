@@ -12,13 +12,19 @@ from vdbg import datagen
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("metric,depth,k", [("l2", 100, 10), ("cosine", 64, 64),
-                                            ("ip", 700, 10), ("l2", 900, 300)])
-def test_rerank_matches_oracle(ctx, oracle, metric, depth, k):
+@pytest.mark.parametrize("metric,depth,k,data", [("l2", 100, 10, "sift"), ("cosine", 64, 64, "unit"),
+                                                 ("ip", 700, 10, "unit"), ("l2", 900, 300, "sift"),
+                                                 ("ip", 100, 10, "sift"), ("l2", 64, 10, "mixed")])
+def test_rerank_matches_oracle(ctx, oracle, metric, depth, k, data):
+    # SIFT-like integer rows and queries (depth <= 256) rerank from the rows' int8 copy in
+    # exact integer arithmetic; "mixed" gives every third query a fractional value, so those
+    # fall back to the fp32 rows within the same batch
     n, nq = 20000, 40
     rng = np.random.default_rng(depth + k)
-    if metric == "l2":
+    if data in ("sift", "mixed"):
         base, qs = datagen.sift_like(n, 128, 5101), datagen.sift_like(nq, 128, 5102)
+        if data == "mixed":
+            qs[::3, 5] += np.float32(0.25)
     else:
         base = datagen.clustered_unit(n, 128, 5103, 5104, 30, 0.5)
         qs = datagen.clustered_unit(nq, 128, 5105, 5104, 30, 0.5)
