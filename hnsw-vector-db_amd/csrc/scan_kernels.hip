@@ -1032,6 +1032,8 @@ constexpr int kMaxSeg = 1024;
 template <int E, class Scorer>
 __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   __shared__ uint32_t pre_all[4][kMaxSeg + 1];
+  __shared__ float stage_d[4][2 * kWave];
+  __shared__ uint32_t stage_i[4][2 * kWave];
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const int slot = blockIdx.x * 4 + wave;
@@ -1082,15 +1084,62 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
     }
     return cbase[size_t(lo) * a.cap + (g - pre[lo])];
   };
-  // the next batch is loaded before the current one is inserted (hides the load latency)
+  // Candidates that beat the current n-th key are packed into a per-wave staging area and
+  // inserted 64 at a time, so the sort-and-merge runs once per 64 wanted keys rather than
+  // once per 64 streamed ones (the key to beat only tightens, so filtering against an older
+  // one keeps every key the final list needs).
+  float* sd = stage_d[wave];
+  uint32_t* si = stage_i[wave];
+  int staged = 0;
+  auto push = [&](float d, uint32_t id) {
+    float td;
+    uint32_t ti;
+    top.threshold(td, ti);
+    const bool want = id != kNoId && nb_less(d, id, td, ti);
+    const uint64_t bal = __ballot(want);
+    if (bal == 0) return;
+    const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
+    if (want) {
+      sd[pos] = d;
+      si[pos] = id;
+    }
+    staged += __popcll(bal);
+    if (staged >= kWave) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float d0 = sd[lane];
+      const uint32_t i0 = si[lane];
+      const bool more = lane + kWave < staged;
+      const float d1 = more ? sd[lane + kWave] : 0.f;
+      const uint32_t i1 = more ? si[lane + kWave] : 0u;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (more) {
+        sd[lane] = d1;
+        si[lane] = i1;
+      }
+      staged -= kWave;
+      top.insert(d0, i0);
+    }
+  };
+  // the next batch is loaded before the current one is pushed (hides the load latency)
   uint2 cur = fetch(lane);
   for (uint32_t g0 = 0; g0 < total; g0 += kWave) {
     const uint2 nxt = fetch(g0 + kWave + lane);
     const uint32_t id = cur.y;
     float d = __uint_as_float(cur.x);
     if (a.rescore == 2 && id != kNoId) d = sc(qv, id);
-    top.insert(d, id);
+    push(d, id);
     cur = nxt;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (staged > 0) {
+    const bool have = lane < staged;
+    top.insert(have ? sd[lane] : __builtin_inff(), have ? si[lane] : kNoId);
   }
 
   constexpr int N = kWave * E;
