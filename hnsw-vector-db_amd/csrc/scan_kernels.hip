@@ -1018,6 +1018,7 @@ struct SelectArgs {
                            // the best K'; 2: GEMM values, rescore every candidate
   int by_query;            // candidate buffers are indexed by query (else by slot)
   const float* T;          // rescore 2: the filter threshold of the GEMM pass
+  int force_fallback;      // testing: 1 fails every rescore-1 certificate, 2 also rescore 2
   uint32_t* out_ids;
   float* out_d;
   uint32_t* fb_list;       // rescore mode: queries that need the exact re-scan
@@ -1159,9 +1160,9 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
       const float v = __shfl(top.k.d[e], (a.k - 1) & (kWave - 1));
       if (e == (a.k - 1) / kWave) dk = v;
     }
-    if (!a.exact[q]) {
+    if (!a.exact[q] || a.force_fallback >= 2) {
       const float lower = (a.T[q] + a.shift[q]) - a.eb[q];
-      if (!(dk <= lower) && lane == 0) {
+      if ((!(dk <= lower) || a.force_fallback >= 2) && lane == 0) {
         const uint32_t p = atomicAdd(a.fb_count, 1u);
         a.fb_list[p] = q;
       }
@@ -1221,6 +1222,7 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
     rescore_first(nsel);
     certified = nsel >= total || at(r.d, uint32_t(a.k) - 1) < (at(top.k.d, nsel) + shift) - ebq;
   }
+  if (a.force_fallback >= 1) certified = false;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     const int gi = e * kWave + lane;
@@ -1446,21 +1448,39 @@ static Sq8Scorer Sq8Of(const ScanSource& src, int kset) {
   return Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric, kset};
 }
 
+// The exact scan's row splits for nslots queries over N rows, and its scratch bytes.
+struct ExactPlan {
+  int nsplit;
+  uint32_t split_rows;
+  size_t need;
+};
+static ExactPlan PlanExact(uint32_t N, int nslots, size_t k) {
+  ExactPlan p{};
+  int nsplit = int(std::min<size_t>((2048 + nslots - 1) / nslots,
+                                    std::max<size_t>(1, (N + 1023) / 1024)));
+  nsplit = std::max(1, std::min(nsplit, kMaxSeg));
+  p.split_rows = (N + nsplit - 1) / nsplit;
+  p.split_rows = (p.split_rows + 63) / 64 * 64;
+  p.nsplit = int((N + p.split_rows - 1) / p.split_rows);
+  const int cap = kWave * pow2_e(k);
+  p.need = size_t(nslots) * p.nsplit * cap * sizeof(uint2) +
+           size_t(nslots) * p.nsplit * sizeof(uint32_t) + 4096;
+  return p;
+}
+
 template <class Scorer>
 static int ExactScanT(Ctx* c, Workspace& w, const ScanSource& src, const Scorer& sc,
                       const float* Q, const uint32_t* qlist, int nslots, size_t k,
                       const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
   const int E = pow2_e(k);
   const uint32_t N = src.N;
-  int nsplit = int(std::min<size_t>((2048 + nslots - 1) / nslots,
-                                    std::max<size_t>(1, (N + 1023) / 1024)));
-  nsplit = std::max(1, std::min(nsplit, kMaxSeg));
-  uint32_t split_rows = (N + nsplit - 1) / nsplit;
-  split_rows = (split_rows + 63) / 64 * 64;
-  nsplit = int((N + split_rows - 1) / split_rows);
+  const ExactPlan ep = PlanExact(N, nslots, k);
+  const int nsplit = ep.nsplit;
+  const uint32_t split_rows = ep.split_rows;
   const int cap = kWave * E;
-  const size_t need = size_t(nslots) * nsplit * cap * sizeof(uint2) +
-                      size_t(nslots) * nsplit * sizeof(uint32_t) + 4096;
+  const size_t need = ep.need;
+  WsUse wuse(&w, s);
+  VDBG_RETURN_IF_ERROR(wuse.status());
   w.used = 0;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   uint2* part = w.take<uint2>(size_t(nslots) * nsplit * cap);
@@ -1581,7 +1601,10 @@ static void GemmGrid(GemmArgs& ga, int nqt, int nchunks, int* blocks) {
 }
 
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
-            const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+            const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
+            Workspace* ws, Workspace* ws2) {
+  Workspace& W = ws != nullptr ? *ws : c->ws;
+  Workspace& W2 = ws2 != nullptr ? *ws2 : c->ws2;
   c->last_fallbacks = 0;
   c->last_gemm_bits = 0;
   if (nq == 0 || kk == 0) return kOk;
@@ -1596,7 +1619,15 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const uint32_t N = src->N;
   const size_t pd = src->pd;
   const bool gemm = GemmSupported(pd) && N >= 1024;
-  if (!gemm) return ExactScan(c, c->ws, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
+  if (!gemm) return ExactScan(c, W, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
+  // A re-scan workspace that cannot grow must hold the re-scan of every query, checked
+  // before anything is queued (which queries fall back is known only on the device).
+  if (W2.fixed && PlanExact(N, int(nq), kk).need > W2.cap)
+    return SetError(kResourceExhausted,
+                    std::string(W2.name) + ": the batch's exact re-scan could need " +
+                        std::to_string(PlanExact(N, int(nq), kk).need) +
+                        " bytes of scratch, more than the " + std::to_string(W2.cap) +
+                        " this path holds");
   VDBG_RETURN_IF_ERROR(BuildSample(c, src, s));
 
   // ---- plan: the fp32 GEMM runs 128 queries per block; the fp16 GEMM 256 (64 per wave,
@@ -1634,11 +1665,11 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     int qb, nqt, nchunks, caph, nseg, schunks;
     uint32_t chunk_rows, schunk_rows;
   };
-  auto make_plan = [&](int qb, int tile_queries, int slots) {
+  auto make_plan = [&](int qb, int tile_queries, int slots, int max_chunks = kMaxSeg / 2) {
     Plan p{};
     p.qb = qb;
     p.nqt = int((nq + tile_queries - 1) / tile_queries);
-    p.nchunks = PlanChunks(p.nqt, N, slots, kMaxSeg / 2);
+    p.nchunks = PlanChunks(p.nqt, N, slots, max_chunks);
     p.chunk_rows = (N + p.nchunks - 1) / p.nchunks;
     p.chunk_rows = (p.chunk_rows + 63) / 64 * 64;
     p.nchunks = int((N + p.chunk_rows - 1) / p.chunk_rows);
@@ -1656,17 +1687,26 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // (64 queries per wave, or 32 for batches of at most 128), SQ8 codes with the query operand
   // split in two fp16 parts (both register sets hold the same 32 queries).  The int8 GEMM
   // tiles as the exact fp16 one, its large-batch kernel with Gemm8Occupancy blocks per CU.
-  const Plan p32 = make_plan(1, 128, slots);
-  const Plan p16 = split ? make_plan(2, 128, slots)
-                         : (nq > 128 ? make_plan(2, 256, slots) : make_plan(1, 128, slots));
-  const Plan p8 = try8op ? make_plan(2, 128, (try8f ? 2 : Gemm8Occupancy(pd)) * c->cu_count)
-                 : (nq > 128 ? make_plan(2, 256, Gemm8Occupancy(pd) * c->cu_count) : p16);
+  const int slots8 = (try8op ? (try8f ? 2 : Gemm8Occupancy(pd)) : Gemm8Occupancy(pd)) * c->cu_count;
+  auto plan_all = [&](Plan* p32, Plan* p16, Plan* p8, int max_chunks) {
+    *p32 = make_plan(1, 128, slots, max_chunks);
+    *p16 = split ? make_plan(2, 128, slots, max_chunks)
+                 : (nq > 128 ? make_plan(2, 256, slots, max_chunks)
+                             : make_plan(1, 128, slots, max_chunks));
+    *p8 = try8op ? make_plan(2, 128, slots8, max_chunks)
+                 : (nq > 128 ? make_plan(2, 256, slots8, max_chunks) : *p16);
+  };
+  Plan p32, p16, p8;
+  plan_all(&p32, &p16, &p8, kMaxSeg / 2);
   auto cand_bytes = [&](const Plan& p) {
     return size_t(nq) * p.nseg * (sizeof(uint32_t) + size_t(p.caph) * sizeof(uint2));
   };
   // counts then candidates, the candidates 256-byte aligned
-  const size_t cand_need = std::max({cand_bytes(p32), try16 ? cand_bytes(p16) : 0,
-                                     try8any ? cand_bytes(p8) : 0}) + 256;
+  auto cand_total = [&]() {
+    return std::max({cand_bytes(p32), try16 ? cand_bytes(p16) : 0,
+                     try8any ? cand_bytes(p8) : 0}) + 256;
+  };
+  size_t cand_need = cand_total();
   const int Esel = pow2_e(kk + 16);
   // The int8 sample pass keeps the kTop8 smallest group minima per lane and chunk half when
   // the lists hold three times kk in all (more than kTop8 of the top kk groups meet in one
@@ -1676,14 +1716,29 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const bool compact8 = try8any && ngroups8 <= 4096 && uint64_t(ngroups8) >= 3 * kk;
   const int gm_groups = std::max(ngroups, compact8 ? ngroups8 : 0);
 
-  Workspace& w = c->ws;
+  Workspace& w = W;
+  // launches of an earlier call on another stream may still read this workspace
+  WsUse wuse(&w, s);
+  VDBG_RETURN_IF_ERROR(wuse.status());
   w.used = 0;
-  const size_t need = nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
-                      (src->kind == 1 ? nq * pd * sizeof(float) : 0) +
-                      size_t(nq) * gm_groups * sizeof(float) + cand_need +
-                      (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
-                      (try8 ? nq * pd + nq * sizeof(int) : 0) +
-                      (try8op ? 2 * nq * pd + nq * (sizeof(int) + sizeof(float)) : 0) + 26 * 256;
+  const size_t other_need =
+      nq * (4 * sizeof(float) + 2 * sizeof(int) + 2 * sizeof(uint32_t)) +
+      (src->kind == 1 ? nq * pd * sizeof(float) : 0) + size_t(nq) * gm_groups * sizeof(float) +
+      (try16 ? (split ? 2 : 1) * nq * pd * sizeof(uint16_t) + nq * sizeof(float) : 0) +
+      (try8 ? nq * pd + nq * sizeof(int) : 0) +
+      (try8op ? 2 * nq * pd + nq * (sizeof(int) + sizeof(float)) : 0) + 26 * 256;
+  // A workspace that cannot grow caps the candidate buffers instead: fewer, longer row
+  // chunks (fewer blocks, so a less filled GPU) until they fit in what the rest leaves.
+  // The sample pass and everything else are planned as before.
+  if (w.fixed && other_need < w.cap && other_need + cand_need > w.cap) {
+    int limit = std::max({p32.nchunks, p16.nchunks, p8.nchunks});
+    while (limit > 1 && other_need + cand_need > w.cap) {
+      limit = std::max(1, limit / 2);
+      plan_all(&p32, &p16, &p8, limit);
+      cand_need = cand_total();
+    }
+  }
+  const size_t need = other_need + cand_need;
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   float* shift = w.take<float>(nq);
   float* eb = w.take<float>(nq);
@@ -1707,11 +1762,11 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* mb8 = try8op ? reinterpret_cast<uint32_t*>(e8 + 1) : nullptr;
   // the no-filter word of the fp16 and int8 GEMMs
   uint32_t* ones = try16 || try8any ? w.take<uint32_t>(1) : nullptr;
-  VDBG_HIP(hipMemsetAsync(ovf, 0, nq * sizeof(int), s));
-  VDBG_HIP(hipMemsetAsync(fb_count, 0, 2 * sizeof(uint32_t), s));
-  if (all16 != nullptr) VDBG_HIP(hipMemsetD32Async(all16, 1, 2, s));
-  if (ones != nullptr) VDBG_HIP(hipMemsetD32Async(ones, int(0xffffffffu), 1, s));
-  if (try8op) VDBG_HIP(hipMemsetAsync(e8, 0, 2 * sizeof(int), s));
+  VDBG_RETURN_IF_ERROR(Fill32(ovf, 0, nq, s));
+  VDBG_RETURN_IF_ERROR(Fill32(fb_count, 0, 2, s));
+  if (all16 != nullptr) VDBG_RETURN_IF_ERROR(Fill32(all16, 1, 2, s));
+  if (ones != nullptr) VDBG_RETURN_IF_ERROR(Fill32(ones, 0xffffffffu, 1, s));
+  if (try8op) VDBG_RETURN_IF_ERROR(Fill32(e8, 0, 2, s));
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
@@ -1857,6 +1912,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   se.out_d = out_d;
   se.fb_list = fb_list;
   se.fb_count = fb_count;
+  se.force_fallback = c->test_fallbacks;
   {
     ProfScope ps(c, "select", s);
     if (src->kind == 0) {
@@ -1893,7 +1949,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   c->last_fallbacks = nfb2;
   if (nfb2 > 0)
     VDBG_RETURN_IF_ERROR(
-        ExactScan(c, c->ws2, *src, Q, fb2_list, int(nfb2), kk, allow, out_ids, out_d, s));
+        ExactScan(c, W2, *src, Q, fb2_list, int(nfb2), kk, allow, out_ids, out_d, s));
   return kOk;
 }
 

@@ -8,6 +8,7 @@
 #include <string>
 #include <vector>
 
+#include "gemm.h"
 #include "vdbg_device.h"
 #include "vdbg_internal.h"
 
@@ -59,6 +60,11 @@ int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s) {
 
 int Workspace::reserve(size_t bytes) {
   if (bytes <= cap) return kOk;
+  if (fixed)
+    return SetError(kResourceExhausted,
+                    std::string(name) + ": the call needs " + std::to_string(bytes) +
+                        " bytes of scratch, more than the " + std::to_string(cap) +
+                        " this path holds");
   if (base != nullptr) {
     // Earlier launches may still read the old block.
     VDBG_HIP(hipDeviceSynchronize());
@@ -74,9 +80,38 @@ int Workspace::reserve(size_t bytes) {
 }
 
 void Workspace::release() {
-  if (base != nullptr) (void)hipFree(base);
+  if (base != nullptr && !fixed) (void)hipFree(base);
+  if (done != nullptr) (void)hipEventDestroy(done);
+  done = nullptr;
   base = nullptr;
   cap = used = 0;
+}
+
+WsUse::WsUse(Workspace* w, hipStream_t s) : w_(w), s_(s) {
+  if (w_->done == nullptr &&
+      hipEventCreateWithFlags(&w_->done, hipEventDisableTiming) != hipSuccess) {
+    w_->done = nullptr;
+    rc_ = SetError(kInternal, "workspace event");
+    return;
+  }
+  if (hipStreamWaitEvent(s_, w_->done, 0) != hipSuccess)
+    rc_ = SetError(kInternal, "workspace event wait");
+}
+
+WsUse::~WsUse() {
+  if (w_->done != nullptr) (void)hipEventRecord(w_->done, s_);
+}
+
+__global__ void k_fill32(uint32_t* __restrict__ p, uint32_t v, size_t n) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+int Fill32(void* p, uint32_t v, size_t n, hipStream_t s) {
+  if (n == 0) return kOk;
+  k_fill32<<<dim3(unsigned((n + 255) / 256)), 256, 0, s>>>(static_cast<uint32_t*>(p), v, n);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
 }
 
 ProfScope::ProfScope(Ctx* c, const char* name, hipStream_t s) : c_(c), s_(s), on_(c->profiling) {
@@ -217,6 +252,22 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   d.src.metric = metric;
   d.src.rmag = d.stats.xn_max;
   d.src.stats = d.stats;
+  // The threshold sample of the GEMM path is gathered now, so that no search allocates it.
+  if (n >= 1024 && GemmSupported(pd)) {
+    rc = BuildSample(c, &d.src, c->stream);
+    if (rc == kOk && hipStreamSynchronize(c->stream) != hipSuccess)
+      rc = SetError(kInternal, "dataset sample");
+    if (rc != kOk) {
+      FreeSample(&d.src);
+      (void)hipFree(d.rows8);
+      (void)hipFree(d.init8);
+      (void)hipFree(d.rows16);
+      (void)hipFree(d.rows);
+      (void)hipFree(d.norms);
+      delete ds;
+      return rc;
+    }
+  }
   ++c->live_datasets;
   *out = ds;
   return kOk;
@@ -402,6 +453,14 @@ int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work) {
   if (!(work >= 0.0)) return SetError(kInvalidArgument, "work must be >= 0");
   std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
   ctx->c.int8_float_min_work = work;
+  return kOk;
+}
+
+int vdbg_ctx_set_test_fallbacks(vdbg_ctx* ctx, int level) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  if (level < 0 || level > 2) return SetError(kInvalidArgument, "level must be 0, 1 or 2");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.test_fallbacks = level;
   return kOk;
 }
 

@@ -58,11 +58,16 @@ struct RowStats {
   int all_int = 1;           // every value is an integer
 };
 
-// Grow-only device scratch, carved into aligned slices per call.
+// Grow-only device scratch, carved into aligned slices per call.  A fixed workspace wraps
+// memory it does not own (the allocation-free entry point's static array) and never grows:
+// reserve() beyond its capacity is ResourceExhausted.
 struct Workspace {
   void* base = nullptr;
   size_t cap = 0;
   size_t used = 0;
+  bool fixed = false;
+  const char* name = "workspace";  // for the fixed workspace's capacity error
+  hipEvent_t done = nullptr;  // recorded after the last launch of the last call that used it
   int reserve(size_t bytes);  // makes `bytes` available (may reallocate; call before carving)
   template <class T>
   T* take(size_t count) {
@@ -71,6 +76,22 @@ struct Workspace {
     return reinterpret_cast<T*>(static_cast<char*>(base) + off);
   }
   void release();
+};
+
+// Orders one call's use of a workspace after every earlier call's, whatever stream each
+// ran on: the constructor makes stream s wait (on the device) for the event the previous
+// user recorded; the destructor records it on s, after every launch the call queued that
+// reads the workspace.  The host-side order comes from the owner's mutex.
+class WsUse {
+ public:
+  WsUse(Workspace* w, hipStream_t s);
+  ~WsUse();
+  int status() const { return rc_; }
+
+ private:
+  Workspace* w_;
+  hipStream_t s_;
+  int rc_ = 0;
 };
 
 struct ProfEntry {
@@ -101,6 +122,8 @@ struct Ctx {
   int cu_count = 256;
   int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
+  int test_fallbacks = 0;      // testing: 1 fails every first certificate (second chance),
+                               // 2 also every second one (exact re-scan)
   bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
   bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
   double int8_float_min_work = 2e10;  // float rows: smallest N nq pd for the int8 GEMM
@@ -232,9 +255,15 @@ int MakeRows8(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int
 int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
                    const RowStats& st, int8_t** out, int* exp, float* l1max, float* l2max);
 
-// Top-kk rows by the source's exact distance for nq queries (device pointers).
+// Top-kk rows by the source's exact distance for nq queries (device pointers).  Scratch comes
+// from ws (the pipeline) and ws2 (the exact re-scan of uncertified queries), by default the
+// context's own; with fixed workspaces and a source whose sample is built, nothing is
+// allocated (kk <= 240).
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
-            const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
+            const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
+            Workspace* ws = nullptr, Workspace* ws2 = nullptr);
+// Fills n 32-bit words with v on stream s (a kernel, so a captured graph holds no memset).
+int Fill32(void* p, uint32_t v, size_t n, hipStream_t s);
 // Exact fp32 distances of `depth` candidate rows per query, the k smallest.
 // rows (nullable): the dataset's scan source, whose int8 copy of integer rows serves
 // exact-integer queries.

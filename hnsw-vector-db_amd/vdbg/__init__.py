@@ -60,6 +60,7 @@ _SIGS = {
     "vdbg_ctx_set_fp16_gemm": (C.c_int, [_vp, C.c_int]),
     "vdbg_ctx_set_int8_gemm": (C.c_int, [_vp, C.c_int]),
     "vdbg_ctx_set_int8_float_min_work": (C.c_int, [_vp, C.c_double]),
+    "vdbg_ctx_set_test_fallbacks": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_reset": (C.c_int, [_vp]),
     "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
@@ -194,6 +195,12 @@ class Context:
         """Smallest rows x queries x padded_dim of a float-row batch that ranks on the int8
         GEMM (default 2e10).  Results are identical either way."""
         _check(lib.vdbg_ctx_set_int8_float_min_work(self.h, float(work)))
+
+    def set_test_fallbacks(self, level):
+        """Testing: 1 fails every first certificate of the flat / SQ8 scans (second chance),
+        2 also every second one (exact re-scan); 0 is the normal path.  Results are
+        identical."""
+        _check(lib.vdbg_ctx_set_test_fallbacks(self.h, int(level)))
 
     def profile(self, enable=True):
         _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))

@@ -25,9 +25,15 @@
  *  - "_host" entry points take host pointers and block until results are on the host.
  *    "_device" entry points take device pointers, run on the given HIP stream (NULL = the
  *    context's stream) and return once the work is queued; inputs must stay valid until the
- *    stream reaches that point.
- *  - All entry points on one context are serialised by the context; use one context per
- *    thread for concurrency.
+ *    stream reaches that point.  The flat, SQ8 and IVF-PQ searches are not fully
+ *    asynchronous: before queuing their later launches they read a few device-side words
+ *    on the host (whether the batch fits the integer GEMM, how many queries need the
+ *    exact re-scan), so such a call returns only after the stream has reached those
+ *    points.
+ *  - All entry points on one context are serialised by the context (host threads may share
+ *    it).  Calls on different streams of one context are ordered on the device where they
+ *    share scratch: a call's launches wait for the previous call's last launch that reads
+ *    it.
  */
 #ifndef VDBG_H_
 #define VDBG_H_
@@ -103,6 +109,13 @@ int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable);
  * and flag readback the int8 GEMM would not repay).  Results are identical either way.  No
  * counterpart in the reference. */
 int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work);
+
+/* Testing: forces the fallbacks of the flat and SQ8 scans' certificates so that tests can
+ * check them.  1 fails every first certificate, so every query takes the second chance
+ * (exact re-scoring of all its buffered candidates); 2 also fails the second one, so every
+ * query is re-scanned exactly.  Results are identical at every level; 0 (the default) is
+ * the normal path.  No counterpart in the reference. */
+int vdbg_ctx_set_test_fallbacks(vdbg_ctx* ctx, int level);
 
 /* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
  * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch
