@@ -252,7 +252,8 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   d.src.metric = metric;
   d.src.rmag = d.stats.xn_max;
   d.src.stats = d.stats;
-  // The threshold sample of the GEMM path is gathered now, so that no search allocates it.
+  // The threshold sample of the GEMM path is gathered now, so that no search allocates it
+  // (the allocation-free flat search relies on this).
   if (n >= 1024 && GemmSupported(pd)) {
     rc = BuildSample(c, &d.src, c->stream);
     if (rc == kOk && hipStreamSynchronize(c->stream) != hipSuccess)
@@ -388,6 +389,7 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
     return SetError(kFailedPrecondition,
                     std::string("vdbg is built for gfx950, device is ") + prop.gcnArchName);
+  VDBG_RETURN_IF_ERROR(InitNoAllocScratch(device));
   auto* ctx = new (std::nothrow) vdbg_ctx;
   if (ctx == nullptr) return SetError(kResourceExhausted, "out of host memory");
   ctx->c.device = device;

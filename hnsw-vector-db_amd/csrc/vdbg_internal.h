@@ -262,6 +262,9 @@ int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
             Workspace* ws = nullptr, Workspace* ws2 = nullptr);
+// Sets up the allocation-free flat search's scratch on `device` (its address there), once per
+// device; called by vdbg_ctx_create with the device current (noalloc.hip).
+int InitNoAllocScratch(int device);
 // Fills n 32-bit words with v on stream s (a kernel, so a captured graph holds no memset).
 int Fill32(void* p, uint32_t v, size_t n, hipStream_t s);
 // Exact fp32 distances of `depth` candidate rows per query, the k smallest.

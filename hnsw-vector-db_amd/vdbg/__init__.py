@@ -83,6 +83,7 @@ _SIGS = {
     "vdbg_flat_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp,
                                         C.POINTER(C.c_uint64)]),
     "vdbg_flat_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "vdbg_flat_search_device_noalloc": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp, _vp]),
     "vdbg_last_fallbacks": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
     "vdbg_last_gemm_bits": (C.c_int, [_vp]),
     "vdbg_sq8_train": (C.c_int, [_vp, _vp, _vp]),
@@ -320,6 +321,13 @@ class Dataset:
         """Device pointers (ints), queued on `stream` (None = the context's stream)."""
         _check(lib.vdbg_flat_search_device(self.h, q_ptr, nq, k, allow_ptr, ids_ptr,
                                            dists_ptr, stream))
+
+    def flat_search_device_noalloc(self, q_ptr, nq, k, ids_ptr, dists_ptr, allow_ptr=None,
+                                   stream=None):
+        """The allocation-free variant (vdbg_flat_search_device_noalloc): k <= 240, scratch
+        in a static device array of fixed size."""
+        _check(lib.vdbg_flat_search_device_noalloc(self.h, q_ptr, nq, k, allow_ptr, ids_ptr,
+                                                   dists_ptr, stream))
 
 
 class Sq8Index:

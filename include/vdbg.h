@@ -188,6 +188,25 @@ int vdbg_flat_search_device(vdbg_dataset* ds, const float* queries, size_t nq, s
                             const uint64_t* allow_words, uint32_t* out_ids, float* out_dists,
                             void* stream);
 
+/* vdbg_flat_search_device without any device allocation, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments, results and stream semantics as
+ * vdbg_flat_search_device, with these limits:
+ *  - k <= 240 (InvalidArgument otherwise);
+ *  - the scratch is one static device array of 32 MiB per GPU (24 MiB for the scan
+ *    pipeline, 8 MiB for the exact re-scan of uncertified queries), held by every GPU the
+ *    library runs on until the process ends.  Batches that would need more scan into fewer,
+ *    longer row chunks; a batch that still does not fit fails with ResourceExhausted before
+ *    anything is queued: at 1M x 128 rows and k = 10 about 500 queries fit per call;
+ *  - under a filter the rows are tested in place rather than compacted (same results).
+ * All calls on one GPU share its array, and its contents persist between calls (everything
+ * that must start cleared is cleared by each call with a fill kernel).  Calls that overlap
+ * on one GPU would race for it, so the library orders them: a call's launches wait, on the
+ * device, for the previous call's last launch that reads the array. */
+int vdbg_flat_search_device_noalloc(vdbg_dataset* ds, const float* queries, size_t nq,
+                                    size_t k, const uint64_t* allow_words, uint32_t* out_ids,
+                                    float* out_dists, void* stream);
+
 /* ---------------------------------------------------------------- SQ8 */
 
 typedef struct vdbg_sq8 vdbg_sq8;
