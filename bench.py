@@ -64,6 +64,38 @@ def profiled_traffic(path):
     return None
 
 
+def cpu_threads():
+    """Host threads for the CPU baseline: every core this process may run on, capped by
+    OMP_NUM_THREADS when the environment sets one (the host share of one GPU)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    if cap.isdigit() and int(cap) > 0:
+        n = min(n, int(cap))
+    return max(1, n)
+
+
+def cpu_model_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_rate(fn, nq, reps=3):
+    """Queries per second of a call that takes host queries and returns host results (query
+    upload, search, result download), the best of `reps` calls after one warm-up."""
+    fn()
+    best = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best = min(best, time.perf_counter() - t0)
+    return round(nq / best, 1), round(best * 1e3, 3)
+
+
 def timed(ctx, torch, fn, steps, warmup, kernels):
     for _ in range(warmup):
         fn()
@@ -92,7 +124,7 @@ def _words(allowed):
     return w.view(np.uint64)
 
 
-def run_filtered(args, ctx, torch, ref, threads):
+def run_filtered(args, ctx, torch, ref, threads, cpu_model):
     import vdbg
     from vdbg import datagen
 
@@ -194,7 +226,7 @@ def run_filtered(args, ctx, torch, ref, threads):
             gd = out_d[:s].cpu().numpy()
             r["cpu_baseline"] = {
                 "value": round(s / dt, 2), "unit": "queries/s", "cores": threads,
-                "kind": "reference",
+                "kind": "reference", "cpu_model": cpu_model,
                 "sample": f"{s} of the {nq} queries: PrepareQuery, ExactOverBitmap over the "
                           f"allowed rows of each of the {nseg} segments (reference kernels and "
                           f"TopK), merge; {threads} threads, {dt:.1f} s"}
@@ -252,7 +284,8 @@ def main():
 
     paths = set(args.paths.split(","))
     dim, k, nq, N = 128, args.k, args.nq, args.n
-    threads = min(16, os.cpu_count() or 1)
+    threads, cpu_model = cpu_threads(), cpu_model_name()
+    log(f"cpu baseline: {threads} threads on {cpu_model}")
     log(f"generating sift-like base {N}x{dim} and {nq} queries")
     base = datagen.sift_like(N, dim, 2002)
     queries = datagen.sift_like(nq, dim, 2003)
@@ -353,10 +386,36 @@ def main():
             dt = time.perf_counter() - t0
             r["cpu_baseline"] = {
                 "value": s / dt, "unit": "queries/s", "cores": threads, "kind": kind,
+                "cpu_model": cpu_model,
                 "sample": f"{s} of the {nq} queries, FlatIndex::search per query over all {N} "
                           f"rows ({kern} kernels), queries over {threads} threads, {dt:.1f} s"}
             r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
             log(f"flat cpu: {s / dt:.1f} q/s ({kind}), parity {r['parity_on_cpu_sample']}")
+            if ref is not None:
+                # one thread (the per-thread rate vdb's own figures quote) and the blocked
+                # FlatSearchBatch (flat_index.cc:41-68), vdb's best CPU batch form
+                s1 = min(s, 160)
+                t0 = time.perf_counter()
+                ref.lib.ref_flat_index_batch(0, base, N, dim, dim, qs, s1, k, od, oi, 1)
+                dt1 = time.perf_counter() - t0
+                r["cpu_baseline"]["one_thread"] = {
+                    "value": s1 / dt1, "sample": f"{s1} queries, FlatIndex::search, 1 thread, "
+                                                 f"{dt1:.1f} s"}
+                t0 = time.perf_counter()
+                ref.lib.ref_flat_search_blocked(b"", 0, base, N, dim, dim, qs, s, k, od, oi,
+                                                threads)
+                dtb = time.perf_counter() - t0
+                r["cpu_baseline"]["flat_search_batch"] = {
+                    "value": s / dtb, "parity": parity(gi, gd, oi, od),
+                    "sample": f"{s} queries, FlatSearchBatch (64-query x 512-row blocks), "
+                              f"{threads} threads, {dtb:.1f} s"}
+                log(f"flat cpu: 1 thread {s1 / dt1:.1f} q/s, FlatSearchBatch {s / dtb:.1f} q/s")
+        # host queries in, host results out (vdbg_flat_search_host): PCIe included
+        qps_h, ms_h = host_rate(lambda: ds.flat_search(queries, k), nq)
+        r["host_in_out"] = {"qps": qps_h, "ms_per_batch": ms_h,
+                            "note": "vdbg_flat_search_host: query upload + search + result "
+                                    "download, best of 3"}
+        log(f"flat host in/out: {qps_h:.0f} q/s")
         if args.sweeps:
             sweep = {}
             for b, kb in ((1, k), (64, k), (1024, k), (nq, 100)):
@@ -436,10 +495,15 @@ def main():
             dt = time.perf_counter() - t0
             r["cpu_baseline"] = {
                 "value": s / dt, "unit": "queries/s", "cores": threads, "kind": kind,
+                "cpu_model": cpu_model,
                 "sample": f"{s} queries: SQ8 scan of all {N} codes into top-{depth} + fp32 "
                           f"Rerank, {threads} threads, {dt:.1f} s"}
             r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
             log(f"sq8 cpu: {s / dt:.1f} q/s ({kind}), parity {r['parity_on_cpu_sample']}")
+        qps_h, ms_h = host_rate(lambda: sq.search(queries, k, depth), nq)
+        r["host_in_out"] = {"qps": qps_h, "ms_per_batch": ms_h,
+                            "note": "vdbg_sq8_search_host: PCIe included, best of 3"}
+        log(f"sq8 host in/out: {qps_h:.0f} q/s")
         sq.close()
         results["sq8"] = r
 
@@ -466,15 +530,19 @@ def main():
                              "exact_scan", "merge", "ivf_qtab", "ivf_scan", "rerank"])
         gi, gd = gpu_out()
         s_ms = prof["ivf_scan"][0] / max(1, prof["ivf_scan"][1])
-        # the reference's scan (ivf_pq.cc:197-217) reads, per probed list, the list's
-        # precomputed term-2 table (m x 256 floats) and its codes and ids
+        # algorithmic bytes of the list scan: the codes and ids of every scanned row (m + 4
+        # bytes each).  The per-list term-2 tables the scan also reads (m x 256 floats per
+        # probed list, ivf_pq.cc:197-217) are reported beside it, not counted in `achieved`.
         t2_bytes = nq * nprobe * m * 256 * 4
-        gbs = (scanned * (m + 4) + t2_bytes) / (s_ms * 1e-3) / 1e9
+        alg_bytes = scanned * (m + 4)
+        gbs = alg_bytes / (s_ms * 1e-3) / 1e9
         r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
              "kernel": "k_ivf_scan", "kernel_ms": s_ms, "achieved": gbs, "unit": "GB/s",
              "peak": HBM_PEAK_GBS, "bound": "hbm",
-             "algorithmic_bytes": "codes + ids of the scanned rows + term-2 table per probed list",
-             "code_stream_GBps": scanned * (m + 4) / (s_ms * 1e-3) / 1e9,
+             "algorithmic_bytes": "codes + ids of the scanned rows",
+             "algorithmic_bytes_per_launch": alg_bytes,
+             "term2_bytes_per_launch": t2_bytes,
+             "term2_GBps": t2_bytes / (s_ms * 1e-3) / 1e9,
              "codes_scanned_per_query": scanned / nq,
              "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
              "nlist": nlist, "m": m, "nprobe": nprobe, "rerank": rerank,
@@ -493,10 +561,15 @@ def main():
             if rc == 0:
                 r["cpu_baseline"] = {
                     "value": s / dt, "unit": "queries/s", "cores": threads, "kind": "reference",
+                    "cpu_model": cpu_model,
                     "sample": f"all {s} queries, IvfPqIndex::search (nprobe {nprobe}, rerank "
                               f"{rerank}) on the same index file, {threads} threads, {dt:.1f} s"}
                 r["parity_on_cpu_sample"] = parity(gi, gd, oi, od)
                 log(f"ivfpq cpu: {s / dt:.1f} q/s, parity {r['parity_on_cpu_sample']}")
+        qps_h, ms_h = host_rate(lambda: ix.search(queries, k, nprobe, rerank), nq)
+        r["host_in_out"] = {"qps": qps_h, "ms_per_batch": ms_h,
+                            "note": "vdbg_ivfpq_search_host: PCIe included, best of 3"}
+        log(f"ivfpq host in/out: {qps_h:.0f} q/s")
         if args.sweeps:
             sweep = {}
             for npb in (16, 32, 64, 128):
@@ -514,7 +587,8 @@ def main():
                     sweep[f"nprobe{npb}_rerank{rr}"] = {
                         "qps": round(nq * args.steps / els, 1),
                         "scan_ms": round(sms, 4),
-                        "scan_GBps": round((sc * (m + 4) + nq * npb * m * 1024) / (sms * 1e-3) / 1e9, 1),
+                        "scan_GBps": round(sc * (m + 4) / (sms * 1e-3) / 1e9, 1),
+                        "term2_GBps": round(nq * npb * m * 1024 / (sms * 1e-3) / 1e9, 1),
                         "codes_scanned_per_query": round(sc / nq, 1)}
                     log(f"ivfpq nprobe {npb} rerank {rr}: {nq * args.steps / els:.0f} q/s")
             r["sweep"] = sweep
@@ -523,7 +597,7 @@ def main():
 
     # ------------------------------------------------------------ filtered collection
     if "filtered" in paths:
-        results["filtered"] = run_filtered(args, ctx, torch, ref, threads)
+        results["filtered"] = run_filtered(args, ctx, torch, ref, threads, cpu_model)
 
     if N == 1_000_000 and nq == 10_000 and k == 10:
         for name in ("flat", "sq8", "ivfpq"):

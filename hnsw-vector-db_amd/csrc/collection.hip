@@ -186,7 +186,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
   // One index search of segment p into (ids, dists) [nq][kk] with the given allow words:
   // Index::search of the segment's index type, adding its distance computations.
   auto index_search = [&](size_t p, size_t kk, size_t nprobe, const uint64_t* allow,
-                          uint32_t* ids, float* dd) -> int {
+                          uint32_t* ids, float* dd, size_t ef) -> int {
     const vdbg_segment& g = segs[p];
     const size_t rows = g.rows->d.n;
     if (g.ivfpq != nullptr) {
@@ -196,9 +196,19 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
       VDBG_HIP(hipStreamSynchronize(s));
       if (dist_comps != nullptr)
         for (size_t i = 0; i < nq; ++i) dist_comps[i] += dch[i];
+    } else if (g.sq8 != nullptr && g.sq8->q.graph != nullptr) {
+      // HnswSq8Index::search (hnsw_index.cc:82-100): the graph walk on the host, the rerank
+      // on the device; ef as the caller's plan sets it
+      VDBG_RETURN_IF_ERROR(vdbg_sq8_hnsw_search_device(g.sq8, q, nq, kk, ef, P.rerank, allow, ids,
+                                                       dd, static_cast<uint64_t*>(dcb.p), s));
+      VDBG_HIP(hipMemcpyAsync(dch.data(), dcb.p, nq * 8, hipMemcpyDeviceToHost, s));
+      VDBG_HIP(hipStreamSynchronize(s));
+      if (dist_comps != nullptr)
+        for (size_t i = 0; i < nq; ++i) dist_comps[i] += dch[i];
     } else if (g.sq8 != nullptr) {
-      // HnswSq8Index::search's depth rule (hnsw_index.cc:88), over every code
-      const size_t depth = P.rerank < 0 ? std::max(P.ef, kk) : size_t(P.rerank);
+      // this library's SQ8 scan index (vdbg_sq8_create, no graph): every code, with
+      // HnswSq8Index::search's depth rule (hnsw_index.cc:88)
+      const size_t depth = P.rerank < 0 ? std::max(ef, kk) : size_t(P.rerank);
       VDBG_RETURN_IF_ERROR(vdbg_sq8_search_device(g.sq8, q, nq, kk, depth, allow, ids, dd, s));
       if (dist_comps != nullptr)
         for (size_t i = 0; i < nq; ++i)
@@ -227,7 +237,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     const uint64_t* allow = sp.allow.empty() ? nullptr : static_cast<const uint64_t*>(allow_dev.p) + allow_at[p];
     switch (sp.plan) {
       case VDBG_PLAN_INDEX:
-        VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd));
+        VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd, P.ef));
         break;
       case VDBG_PLAN_EMPTY:
         VDBG_HIP(hipMemsetAsync(ids, 0xff, slice * 4, s));
@@ -237,7 +247,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
         VDBG_RETURN_IF_ERROR(exact(p, allow, ids, dd));
         break;
       case VDBG_PLAN_FILTERED_INDEX: {
-        VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd));
+        VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd, P.ef));
         if (P.strategy != VDBG_STRATEGY_AUTO) break;
         // :103-108: never fewer than min(k, matches) hits; the short queries take the exact
         // scan of the allowed rows
@@ -289,9 +299,9 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
         }
         VDBG_RETURN_IF_ERROR(Alloc(&wi, nq * kk * 4, s));
         VDBG_RETURN_IF_ERROR(Alloc(&wd, nq * kk * 4, s));
-        // ef raised to kk (:113-114) leaves the SQ8 depth max(ef, kk) as index_search sets it
+        // ef raised to kk (:113-114)
         VDBG_RETURN_IF_ERROR(index_search(p, kk, sp.nprobe, dallow, static_cast<uint32_t*>(wi.p),
-                                          static_cast<float*>(wd.p)));
+                                          static_cast<float*>(wd.p), std::max(P.ef, kk)));
         hr.resize(nq * kk);
         hd.resize(nq * kk);
         VDBG_HIP(hipMemcpyAsync(hr.data(), wi.p, nq * kk * 4, hipMemcpyDeviceToHost, s));

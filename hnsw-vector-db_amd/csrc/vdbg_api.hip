@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "gemm.h"
+#include "hnsw_host.h"
 #include "vdbg_device.h"
 #include "vdbg_internal.h"
 
@@ -458,6 +459,13 @@ int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work) {
   return kOk;
 }
 
+int vdbg_ctx_set_host_threads(vdbg_ctx* ctx, int n) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.host_threads = n > 0 ? n : 0;
+  return kOk;
+}
+
 int vdbg_ctx_set_test_fallbacks(vdbg_ctx* ctx, int level) {
   if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
   if (level < 0 || level > 2) return SetError(kInvalidArgument, "level must be 0, 1 or 2");
@@ -704,10 +712,10 @@ int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdb
 }
 
 // LoadIndex's framing check (src/index/index.cc:47-56) and HnswSq8Index::load
-// (src/index/hnsw/hnsw_index.cc:117-129) up to the graph: u64 rows, the serialised
-// Sq8Quantizer (src/index/quant/sq8.cc:43-63: u32 dim, u32 padded dim, vmin, scale), then
-// rows x padded_dim code bytes.  The graph that follows is not read: the device scans every
-// code.
+// (src/index/hnsw/hnsw_index.cc:117-129): u64 rows, the serialised Sq8Quantizer
+// (src/index/quant/sq8.cc:43-63: u32 dim, u32 padded dim, vmin, scale), rows x padded_dim
+// code bytes, then the graph (HnswGraph::Deserialize, hnsw_graph.h:368-413), kept on the host
+// with a host copy of the codes for the walk.
 int vdbg_sq8_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_sq8** out) {
   if (ds == nullptr || out == nullptr || (file == nullptr && len > 0))
     return SetError(kInvalidArgument, "null argument");
@@ -738,7 +746,201 @@ int vdbg_sq8_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_sq8** out
     return SetError(VDBG_CORRUPTION, "hnsw-sq8 index does not match the segment");
   const uint8_t* codes = p;
   if (!take(nullptr, size_t(n) * d.pd)) return SetError(VDBG_CORRUPTION, "truncated sq8 codes");
-  return CreateSq8(ds, vmin.data(), scale.data(), codes, out);
+  HnswGraph* graph = nullptr;
+  size_t used = 0;
+  const char* err = nullptr;
+  if (HnswParse(p, left, n, &graph, &used, &err) != 0) return SetError(VDBG_CORRUPTION, err);
+  std::vector<uint8_t> codes_h;
+  try {
+    codes_h.assign(codes, codes + size_t(n) * d.pd);
+  } catch (...) {
+    HnswFree(graph);
+    return SetError(kResourceExhausted, "out of host memory for the sq8 codes");
+  }
+  const int rc = CreateSq8(ds, vmin.data(), scale.data(), codes, out);
+  if (rc != kOk) {
+    HnswFree(graph);
+    return rc;
+  }
+  (*out)->q.graph = graph;
+  (*out)->q.codes_h = std::move(codes_h);
+  return kOk;
+}
+
+int vdbg_sq8_graph_info(vdbg_sq8* sq, int64_t out[5]) {
+  if (sq == nullptr || out == nullptr) return SetError(kInvalidArgument, "null argument");
+  if (sq->q.graph == nullptr)
+    return SetError(kFailedPrecondition, "the index has no graph (made by vdbg_sq8_create)");
+  HnswInfo(sq->q.graph, out);
+  return kOk;
+}
+
+namespace {
+
+// HnswSq8Index::search's depth and beam width (src/index/hnsw/hnsw_index.cc:88-89).
+void HnswDepth(size_t k, size_t ef, int rerank, size_t* depth, size_t* beam) {
+  *depth = rerank < 0 ? std::max(ef, k) : size_t(rerank);
+  *beam = std::max({ef, k, *depth});
+}
+
+// The walk of every query on the host (no lock held: the graph and host codes are read-only).
+// cand: nq x kk ids and SQ8 distances, padded; dc: the walk's distance computations.
+void WalkBatch(const Sq8Index& x, int kset, int threads, const float* Qh, size_t nq, size_t kk,
+               size_t beam, const uint64_t* allow_h, std::vector<uint32_t>* cand,
+               std::vector<float>* cand_d, std::vector<uint32_t>* found,
+               std::vector<uint64_t>* dc) {
+  const Dataset& d = *x.ds;
+  cand->resize(nq * kk);
+  cand_d->resize(nq * kk);
+  found->resize(nq);
+  dc->resize(nq);
+  HnswWalkArgs a{x.graph, x.codes_h.data(), x.vmin_h.data(), x.scale_h.data(), d.pd,
+                 HostSq8Kernel(kset, d.metric), Qh, nq, kk, beam, allow_h, cand->data(),
+                 cand_d->data(), found->data(), dc->data(),
+                 threads > 0 ? threads : DefaultHostThreads()};
+  HnswWalk(a);
+}
+
+int CheckHnswArgs(vdbg_sq8* sq, size_t nq, size_t k, const void* queries, const void* ids,
+                  const void* dists) {
+  if (sq == nullptr) return SetError(kInvalidArgument, "null index");
+  if (sq->q.graph == nullptr)
+    return SetError(kFailedPrecondition, "the index has no graph (made by vdbg_sq8_create)");
+  if (nq > 0 && k > 0 && (queries == nullptr || ids == nullptr || dists == nullptr))
+    return SetError(kInvalidArgument, "null pointer");
+  if (k > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
+  if (nq > 0x7fffffffull) return SetError(kInvalidArgument, "too many queries");
+  return kOk;
+}
+
+}  // namespace
+
+int vdbg_sq8_hnsw_search_host(vdbg_sq8* sq, const float* queries, size_t nq, size_t k,
+                              size_t ef, int rerank, const uint64_t* allow_words,
+                              uint32_t* out_ids, float* out_dists, uint64_t* dist_comps) {
+  VDBG_RETURN_IF_ERROR(CheckHnswArgs(sq, nq, k, queries, out_ids, out_dists));
+  if (nq == 0) return kOk;
+  Sq8Index& x = sq->q;
+  Dataset& d = *x.ds;
+  Ctx* c = d.ctx;
+  if (k == 0) {
+    if (dist_comps != nullptr) std::fill(dist_comps, dist_comps + nq, uint64_t(0));
+    return kOk;
+  }
+  int kset, threads;
+  {
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    kset = c->kset;
+    threads = c->host_threads;
+  }
+  size_t depth, beam;
+  HnswDepth(k, ef, rerank, &depth, &beam);
+  const size_t kk = depth == 0 ? k : std::max(depth, k);
+  std::vector<uint32_t> cand, found;
+  std::vector<float> cand_d;
+  std::vector<uint64_t> dc;
+  WalkBatch(x, kset, threads, queries, nq, kk, beam, allow_words, &cand, &cand_d, &found, &dc);
+  if (depth == 0) {  // the beam's k best by SQ8 distance (hnsw_index.cc:90-91)
+    for (size_t i = 0; i < nq; ++i) {
+      std::memcpy(out_ids + i * k, cand.data() + i * kk, k * 4);
+      std::memcpy(out_dists + i * k, cand_d.data() + i * kk, k * 4);
+      if (dist_comps != nullptr) dist_comps[i] = dc[i];
+    }
+    return kOk;
+  }
+  // Rerank of every query's beam on the GPU (hnsw_index.cc:93-94, index.cc:89-95)
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  uint32_t* dcand = nullptr;
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dcand), nq * kk * 4, s));
+  hipError_t e = hipMemcpyAsync(dcand, cand.data(), nq * kk * 4, hipMemcpyHostToDevice, s);
+  if (e != hipSuccess) {
+    (void)hipFreeAsync(dcand, s);
+    return SetError(kInternal, std::string("candidates: ") + hipGetErrorString(e));
+  }
+  const int rc = StageHost(c, d.n, d.pd, queries, nq, k, nullptr, out_ids, out_dists,
+                           [&](const float* dq, const uint64_t*, uint32_t* di, float* dd,
+                               hipStream_t st) {
+                             return Rerank(c, d.rows, int(d.pd), d.metric, dq, nq, dcand, kk,
+                                           k, di, dd, st, &d.src);
+                           });
+  (void)hipFreeAsync(dcand, s);
+  if (rc == kOk && dist_comps != nullptr)
+    for (size_t i = 0; i < nq; ++i) dist_comps[i] = dc[i] + found[i];
+  return rc;
+}
+
+int vdbg_sq8_hnsw_search_device(vdbg_sq8* sq, const float* queries, size_t nq, size_t k,
+                                size_t ef, int rerank, const uint64_t* allow_words,
+                                uint32_t* out_ids, float* out_dists, uint64_t* dist_comps,
+                                void* stream) {
+  VDBG_RETURN_IF_ERROR(CheckHnswArgs(sq, nq, k, queries, out_ids, out_dists));
+  if (nq == 0) return kOk;
+  Sq8Index& x = sq->q;
+  Dataset& d = *x.ds;
+  Ctx* c = d.ctx;
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : c->stream;
+  int kset, threads;
+  std::vector<float> qh(nq * d.pd);
+  std::vector<uint64_t> allow_h;
+  {  // the queries (and the filter) to the host for the walk
+    std::lock_guard<std::recursive_mutex> g(c->mu);
+    VDBG_HIP(hipSetDevice(c->device));
+    kset = c->kset;
+    threads = c->host_threads;
+    VDBG_HIP(hipMemcpyAsync(qh.data(), queries, qh.size() * 4, hipMemcpyDeviceToHost, s));
+    if (allow_words != nullptr) {
+      allow_h.resize((d.n + 63) / 64);
+      if (!allow_h.empty())
+        VDBG_HIP(hipMemcpyAsync(allow_h.data(), allow_words, allow_h.size() * 8,
+                                hipMemcpyDeviceToHost, s));
+    }
+    VDBG_HIP(hipStreamSynchronize(s));
+  }
+  std::vector<uint64_t> dch(nq, 0);
+  size_t depth, beam;
+  HnswDepth(k, ef, rerank, &depth, &beam);
+  const size_t kk = depth == 0 ? k : std::max(depth, k);
+  std::vector<uint32_t> cand, found;
+  std::vector<float> cand_d;
+  std::vector<uint64_t> dc;
+  if (k > 0)
+    WalkBatch(x, kset, threads, qh.data(), nq, kk, beam,
+              allow_words != nullptr ? allow_h.data() : nullptr, &cand, &cand_d, &found, &dc);
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  if (k == 0) {
+    if (dist_comps != nullptr) {
+      VDBG_HIP(hipMemcpyAsync(dist_comps, dch.data(), nq * 8, hipMemcpyHostToDevice, s));
+      VDBG_HIP(hipStreamSynchronize(s));
+    }
+    return kOk;
+  }
+  for (size_t i = 0; i < nq; ++i) dch[i] = dc[i] + (depth == 0 ? 0 : found[i]);
+  if (depth == 0) {
+    for (size_t i = 0; i < nq; ++i) {  // compact [nq][kk] to [nq][k] (kk == k here)
+      VDBG_HIP(hipMemcpyAsync(out_ids + i * k, cand.data() + i * kk, k * 4,
+                              hipMemcpyHostToDevice, s));
+      VDBG_HIP(hipMemcpyAsync(out_dists + i * k, cand_d.data() + i * kk, k * 4,
+                              hipMemcpyHostToDevice, s));
+    }
+  } else {
+    uint32_t* dcand = nullptr;
+    VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dcand), nq * kk * 4, s));
+    hipError_t e = hipMemcpyAsync(dcand, cand.data(), nq * kk * 4, hipMemcpyHostToDevice, s);
+    int rc = e == hipSuccess ? kOk : SetError(kInternal, hipGetErrorString(e));
+    if (rc == kOk)
+      rc = Rerank(c, d.rows, int(d.pd), d.metric, queries, nq, dcand, kk, k, out_ids, out_dists,
+                  s, &d.src);
+    (void)hipFreeAsync(dcand, s);
+    VDBG_RETURN_IF_ERROR(rc);
+  }
+  if (dist_comps != nullptr)
+    VDBG_HIP(hipMemcpyAsync(dist_comps, dch.data(), nq * 8, hipMemcpyHostToDevice, s));
+  // the host vectors above are sources of queued copies: wait before they go away
+  VDBG_HIP(hipStreamSynchronize(s));
+  return kOk;
 }
 
 int vdbg_sq8_destroy(vdbg_sq8* sq) {
@@ -748,6 +950,7 @@ int vdbg_sq8_destroy(vdbg_sq8* sq) {
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
   --sq->q.ds->live_indexes;
+  HnswFree(sq->q.graph);
   FreeSample(&sq->q.src);
   (void)hipFree(sq->q.codes);
   (void)hipFree(sq->q.codes16);

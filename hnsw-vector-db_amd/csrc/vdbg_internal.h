@@ -127,6 +127,7 @@ struct Ctx {
   bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
   bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
   double int8_float_min_work = 2e10;  // float rows: smallest N nq pd for the int8 GEMM
+  int host_threads = 0;        // host threads of the HNSW walk; 0 = DefaultHostThreads()
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
 };
 
@@ -191,8 +192,12 @@ struct Dataset {
 
 // SQ8 codes of a dataset's rows (HnswSq8Index's codes_ and Sq8Quantizer,
 // src/index/hnsw/hnsw_index.h:89-95, without the graph).
+struct HnswGraph;  // hnsw_host.h
+
 struct Sq8Index {
   Dataset* ds = nullptr;
+  HnswGraph* graph = nullptr;     // the VDBHSQ81 file's graph (host), or null
+  std::vector<uint8_t> codes_h;   // host copy of the codes for the graph walk (with a graph)
   uint8_t* codes = nullptr;  // n x pd
   uint16_t* codes16 = nullptr;  // n x pd, the codes as fp16 (ScanSource::X16 of the scan)
   float* yn = nullptr;       // ||code * scale||^2 per row

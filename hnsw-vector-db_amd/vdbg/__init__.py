@@ -93,6 +93,14 @@ _SIGS = {
     "vdbg_sq8_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp,
                                        C.POINTER(C.c_uint64)]),
     "vdbg_sq8_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp]),
+    "vdbg_sq8_graph_info": (C.c_int, [_vp, _vp]),
+    "vdbg_sq8_hnsw_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp,
+                                            _vp]),
+    "vdbg_sq8_hnsw_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp,
+                                              _vp, _vp]),
+    "vdbg_ctx_set_host_threads": (C.c_int, [_vp, C.c_int]),
+    "vdbg_host_sq8_distance": (C.c_float, [C.c_char_p, C.c_int, _vp, _vp, _vp, _vp, _sz,
+                                           C.c_int]),
     "vdbg_ivfpq_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
     "vdbg_ivfpq_build": (C.c_int, [_vp, _sz, _sz, C.c_uint64, _sz, _sz, C.POINTER(_vp)]),
     "vdbg_kmeans": (C.c_int, [_vp, _vp, _sz, _sz, _sz, _sz, _sz, C.c_uint64, _sz, C.c_int, _vp,
@@ -196,6 +204,9 @@ class Context:
         """Smallest rows x queries x padded_dim of a float-row batch that ranks on the int8
         GEMM (default 2e10).  Results are identical either way."""
         _check(lib.vdbg_ctx_set_int8_float_min_work(self.h, float(work)))
+
+    def set_host_threads(self, n):
+        _check(lib.vdbg_ctx_set_host_threads(self.h, n))
 
     def set_test_fallbacks(self, level):
         """Testing: 1 fails every first certificate of the flat / SQ8 scans (second chance),
@@ -391,6 +402,42 @@ class Sq8Index:
                       stream=None):
         _check(lib.vdbg_sq8_search_device(self.h, q_ptr, nq, k, depth, allow_ptr, ids_ptr,
                                           dists_ptr, stream))
+
+    def graph_info(self):
+        """(nodes, M, ef_construction, top layer, entry point) of a loaded graph."""
+        out = np.empty(5, np.int64)
+        _check(lib.vdbg_sq8_graph_info(self.h, _ptr(out)))
+        return tuple(int(v) for v in out)
+
+    def hnsw_search(self, queries, k, ef=64, rerank=-1, allow=None):
+        """HnswSq8Index::search for a batch: the graph walk on the host, the rerank on the
+        GPU.  Returns (ids, dists, distance computations)."""
+        q = np.ascontiguousarray(queries, np.float32)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), np.uint32)
+        dists = np.empty((nq, k), np.float32)
+        dc = np.empty(nq, np.uint64)
+        if allow is not None:
+            allow = np.ascontiguousarray(allow, np.uint64)
+        _check(lib.vdbg_sq8_hnsw_search_host(self.h, _ptr(q), nq, k, ef, rerank, _ptr(allow),
+                                             _ptr(ids), _ptr(dists), _ptr(dc)))
+        return ids, dists, dc
+
+    def hnsw_search_device(self, q_ptr, nq, k, ef, rerank, ids_ptr, dists_ptr, allow_ptr=None,
+                           dc_ptr=None, stream=None):
+        _check(lib.vdbg_sq8_hnsw_search_device(self.h, q_ptr, nq, k, ef, rerank, allow_ptr,
+                                               ids_ptr, dists_ptr, dc_ptr, stream))
+
+
+def host_sq8_distance(kernels, metric, q, codes, vmin, scale, portable=False):
+    """The SQ8 distance the HNSW walk computes on the host (pure host code)."""
+    q = np.ascontiguousarray(q, np.float32)
+    c = np.ascontiguousarray(codes, np.uint8)
+    vmin = np.ascontiguousarray(vmin, np.float32)
+    scale = np.ascontiguousarray(scale, np.float32)
+    m = {"l2": 0, "ip": 1, "cosine": 2}.get(metric, metric)
+    return lib.vdbg_host_sq8_distance(kernels.encode(), m, _ptr(q), _ptr(c), _ptr(vmin),
+                                      _ptr(scale), q.size, 1 if portable else 0)
 
 
 def _sq8_train(self):

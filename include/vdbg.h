@@ -110,6 +110,17 @@ int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable);
  * counterpart in the reference. */
 int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work);
 
+/* Host threads for the CPU side of a search (the HNSW walk); n <= 0 restores the default:
+ * the cores this process may run on, capped by OMP_NUM_THREADS when set. */
+int vdbg_ctx_set_host_threads(vdbg_ctx* ctx, int n);
+/* The SQ8 distance the HNSW walk computes on the host for a kernel set ("scalar", "avx2",
+ * "avx512") and metric: vdb's sq8_l2_* / sq8_ip_* (src/distance/scalar.cc:25-41,
+ * avx2.cc:48-74, avx512.cc:48-64) bit for bit; portable != 0 takes the lane-by-lane form used
+ * on hosts without the instructions.  Pure host code (no device work), so it can be checked
+ * on any machine.  Returns NaN for an unknown set. */
+float vdbg_host_sq8_distance(const char* kernels, int metric, const float* q, const uint8_t* c,
+                             const float* vmin, const float* scale, size_t d, int portable);
+
 /* Testing: forces the fallbacks of the flat and SQ8 scans' certificates so that tests can
  * check them.  1 fails every first certificate, so every query takes the second chance
  * (exact re-scoring of all its buffered candidates); 2 also fails the second one, so every
@@ -222,10 +233,33 @@ int vdbg_sq8_train(vdbg_dataset* ds, float* vmin_out, float* scale_out);
 int vdbg_sq8_create(vdbg_dataset* ds, const float* vmin, const float* scale, vdbg_sq8** out);
 /* LoadIndex (src/index/index.cc:38-87) of a VDBHSQ81 file, the HNSW-SQ8 index of a segment
  * (hnsw_index.cc:108-129): CRC32C footer, then rows, the Sq8Quantizer and the codes are read
- * and made resident as they are (no re-encoding); the graph that follows is not read, since
- * the device scans every code.  `ds` is the segment the index belongs to (rows and
- * padded_dim must match).  Errors: 5 (corruption) for a bad file. */
+ * and made resident as they are (no re-encoding), and the graph that follows is read with
+ * HnswGraph::Deserialize's checks (src/index/hnsw/hnsw_graph.h:368-413) into host memory,
+ * together with a host copy of the codes, for vdbg_sq8_hnsw_search_*.  `ds` is the segment
+ * the index belongs to (rows and padded_dim must match).  Errors: 5 (corruption) for a bad
+ * file, with the reference's messages. */
 int vdbg_sq8_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_sq8** out);
+/* The loaded graph: out[0] nodes, [1] M, [2] ef_construction, [3] top layer (-1 when empty),
+ * [4] entry point.  FailedPrecondition for an index made by vdbg_sq8_create (no graph). */
+int vdbg_sq8_graph_info(vdbg_sq8* sq, int64_t out[5]);
+/* HnswSq8Index::search (src/index/hnsw/hnsw_index.cc:82-100) for a batch of queries, over a
+ * graph loaded by vdbg_sq8_load.  The graph walk stays on the CPU, as in vdb: greedy descent
+ * through the upper layers and the layer-0 beam of HnswGraph::search (hnsw_graph.h:301-324,
+ * 467-548) on the SQ8 distance of the context's kernel set, with ef = max(ef, k, depth) and
+ * depth = rerank < 0 ? max(ef, k) : rerank; queries run on the context's host threads
+ * (vdbg_ctx_set_host_threads).  The float Rerank of each query's beam (index.cc:89-95) runs
+ * on the GPU over the resident rows; depth 0 returns the beam's k best by SQ8 distance.
+ * allow_words (nullable) is the RowFilter: rejected rows are walked through but never
+ * returned.  dist_comps (nullable, nq) receives IndexSearchStats::distance_computations.
+ * The _device form takes device queries, words and outputs and synchronises the stream
+ * twice (queries to the host for the walk, candidates back). */
+int vdbg_sq8_hnsw_search_host(vdbg_sq8* sq, const float* queries, size_t nq, size_t k,
+                              size_t ef, int rerank, const uint64_t* allow_words,
+                              uint32_t* out_ids, float* out_dists, uint64_t* dist_comps);
+int vdbg_sq8_hnsw_search_device(vdbg_sq8* sq, const float* queries, size_t nq, size_t k,
+                                size_t ef, int rerank, const uint64_t* allow_words,
+                                uint32_t* out_ids, float* out_dists, uint64_t* dist_comps,
+                                void* stream);
 int vdbg_sq8_destroy(vdbg_sq8* sq);
 /* Copies the n x padded_dim code bytes to the host. */
 int vdbg_sq8_codes(vdbg_sq8* sq, uint8_t* codes_out);
@@ -359,7 +393,9 @@ int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 typedef struct vdbg_segment {
   vdbg_dataset* rows;             /* the segment's rows, external ids set with
                                      vdbg_dataset_set_external_ids */
-  vdbg_sq8* sq8;                  /* the segment's index: HNSW-SQ8 codes (scanned in full), */
+  vdbg_sq8* sq8;                  /* the segment's index: HNSW-SQ8 (vdbg_sq8_load: the
+                                     graph walk with GPU rerank) or this library's SQ8 scan
+                                     index (vdbg_sq8_create: every code scanned), */
   vdbg_ivfpq* ivfpq;              /* or IVF-PQ lists; both NULL = a flat index */
   const uint64_t* deleted_words;  /* host, nullable: DeleteBits words, ceil(rows/64) */
   const uint64_t* filter_words;   /* host, nullable: the request's filter evaluated on this

@@ -389,6 +389,59 @@ class GpuSq8Index {
   std::vector<float> vmin_, scale_;
 };
 
+// HnswSq8Index (src/index/hnsw/hnsw_index.h:64-97) loaded from its VDBHSQ81 file: the graph
+// walk stays on the host (HnswGraph::search), the float rerank of each beam runs on the GPU
+// (hnsw_index.cc:82-100).  The graph is built by vdb's own CPU code; this class only serves it.
+class GpuHnswSq8Index {
+ public:
+  static Status Load(Device& dev, Metric metric, const VectorView& v, std::string_view file,
+                     std::unique_ptr<GpuHnswSq8Index>* out) {
+    detail::DatasetPtr d;
+    VDBG_CXX_RETURN_IF_ERROR(detail::MakeDataset(dev, metric, v, &d));
+    vdbg_sq8* sq = nullptr;
+    VDBG_CXX_RETURN_IF_ERROR(
+        Status::FromCall(vdbg_sq8_load(d.get(), file.data(), file.size(), &sq)));
+    out->reset(new GpuHnswSq8Index(v, std::move(d), sq));
+    return Status::OK();
+  }
+  ~GpuHnswSq8Index() {
+    if (sq_) vdbg_sq8_destroy(sq_);
+  }
+  const char* type() const { return "hnsw_sq8"; }
+  size_t size() const { return view_.rows; }
+  size_t code_bytes() const { return view_.rows * view_.padded_dim; }
+
+  Status search(const float* q, size_t k, const SearchParams& p, const DenseRowFilter* filter,
+                std::vector<Neighbor>& out, IndexSearchStats* stats) const {
+    std::vector<std::vector<Neighbor>> all;
+    VDBG_CXX_RETURN_IF_ERROR(search_batch(q, 1, k, p, filter, all, stats));
+    out = std::move(all[0]);
+    return Status::OK();
+  }
+  Status search_batch(const float* queries, size_t nq, size_t k, const SearchParams& p,
+                      const DenseRowFilter* filter, std::vector<std::vector<Neighbor>>& out,
+                      IndexSearchStats* stats) const {
+    std::vector<uint32_t> ids(nq * k);
+    std::vector<float> d(nq * k);
+    std::vector<uint64_t> dc(nq);
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_sq8_hnsw_search_host(
+        sq_, queries, nq, k, p.ef, p.rerank, filter ? filter->words() : nullptr, ids.data(),
+        d.data(), dc.data())));
+    detail::Unpack(ids, d, nq, k, out);
+    if (stats)
+      for (uint64_t x : dc) stats->distance_computations += x;
+    return Status::OK();
+  }
+  vdbg_sq8* handle() const { return sq_; }
+
+ private:
+  GpuHnswSq8Index(const VectorView& v, detail::DatasetPtr d, vdbg_sq8* sq)
+      : view_(v), ds_(std::move(d)), sq_(sq) {}
+  VectorView view_;
+  detail::DatasetPtr ds_;
+  vdbg_sq8* sq_ = nullptr;
+};
+
 // ---------------------------------------------------------------- IVF-PQ
 
 // IvfPqIndex (ivf_pq.h:42-81): build() trains and fills the lists on the GPU, Load() reads a
@@ -607,9 +660,9 @@ inline std::string JoinPath(const std::string& a, const std::string& b) {
 // Segment::Open (src/storage/segment_reader.cc:20-122) for what a search reads, made resident
 // on the device: vectors.f32 (header and CRC checks, the rows uploaded), ids.u64 (kept on
 // the host and resident for the merge), the index file (LoadIndex by magic, index.cc:38-87:
-// VDBFLAT1 needs nothing more, VDBHSQ81 brings its SQ8 codes, VDBIVFP1 its lists; a graph
-// index is NotSupported, since graph traversal stays on the CPU) and the persisted delete
-// set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
+// VDBFLAT1 needs nothing more, VDBHSQ81 brings its SQ8 codes and its graph, walked on the
+// host with the rerank on the GPU, VDBIVFP1 its lists; a float-row HNSW index and PQ-flat
+// are NotSupported) and the persisted delete set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
 // the reference's Corruption messages, prefixed with the file or directory.
 class GpuSegment {
  public:

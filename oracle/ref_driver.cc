@@ -189,6 +189,36 @@ size_t ref_hnsw_sq8_file(int metric, const float* base, size_t rows, size_t dim,
   return sink.s.size();
 }
 
+// LoadIndex of a VDBHSQ81 file (index.cc:38-87) and HnswSq8Index::search
+// (src/index/hnsw/hnsw_index.cc:82-100) per query: graph beam over the codes with the
+// reference's own kernel set, then Rerank.  allow_words (nullable) is the RowFilter (bit r of
+// word r / 64 = row r allowed).  Returns 0, or 1 when the file does not load.
+int ref_hnsw_sq8_search_batch(int metric, const char* file, size_t file_len, const float* base,
+                              size_t rows, size_t dim, size_t pd, const float* queries,
+                              size_t nq, size_t k, size_t ef, int rerank,
+                              const uint64_t* allow_words, float* od, uint32_t* oi,
+                              uint64_t* dc, int nthreads) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::HnswSq8;
+  auto idx = LoadIndex(std::string_view(file, file_len), o, static_cast<Metric>(metric), v);
+  if (!idx.ok()) return 1;
+  const Index& ix = **idx;
+  SearchParams p;
+  p.ef = ef;
+  p.rerank = rerank;
+  DenseFilter filt(allow_words);
+  ThreadPool pool(nthreads <= 0 ? 1 : static_cast<size_t>(nthreads));
+  pool.parallel_for(0, nq, [&](size_t qi) {
+    std::vector<Neighbor> out;
+    IndexSearchStats st;
+    ix.search(queries + qi * pd, k, p, allow_words != nullptr ? &filt : nullptr, out, &st);
+    WritePadded(out, k, od + qi * k, oi + qi * k);
+    if (dc != nullptr) dc[qi] = st.distance_computations;
+  });
+  return 0;
+}
+
 // SQ8 scan + rerank composed from the reference's parts (Sq8 kernel into TopK, Rerank).
 void ref_sq8_search_batch(const char* ks, int metric, const float* base, const uint8_t* codes,
                           size_t rows, size_t dim, size_t pd, const float* vmin,

@@ -957,3 +957,281 @@ uint32_t or_crc32c(uint32_t crc, const void* data, size_t n) {
   }
   return ~c;
 }
+
+/* ------------------------------------------------------------------ HNSW-SQ8 search */
+
+/* A VDBHSQ81 file's parts (HnswSq8Index::save, src/index/hnsw/hnsw_index.cc:108-115): u64
+ * rows, the Sq8Quantizer (sq8.cc:43-63), rows x pd codes, then the graph (HnswGraph::serialize,
+ * hnsw_graph.h:352-366). */
+typedef struct {
+  uint64_t cap, size;
+  uint32_t M, M0;
+  int max_level;
+  uint32_t ep;
+  uint8_t* level;
+  uint32_t* links0; /* cap x (1 + M0): [count][links] */
+  uint64_t* up_at;  /* per node: offset of its layer-1 list in up */
+  uint32_t* up;     /* per node with level > 0: level x (1 + M) */
+  size_t pd;
+  const float* vmin;
+  const float* scale;
+  const uint8_t* codes;
+  float* vbuf;
+} or_hnsw_t;
+
+static int rd_take(const uint8_t** p, size_t* left, void* dst, size_t n) {
+  if (*left < n) return 0;
+  if (dst != NULL) memcpy(dst, *p, n);
+  *p += n;
+  *left -= n;
+  return 1;
+}
+
+static void or_hnsw_free(or_hnsw_t* g) {
+  free(g->level);
+  free(g->links0);
+  free(g->up_at);
+  free(g->up);
+  free(g->vbuf);
+}
+
+/* Parses the file (LoadIndex's footer check, index.cc:47-56, then HnswSq8Index::load,
+ * hnsw_index.cc:117-129, and HnswGraph::Deserialize, hnsw_graph.h:368-413, without its
+ * validation: the files here are written by the reference). */
+static int or_hnsw_parse(const uint8_t* f, size_t len, size_t rows, size_t pd, or_hnsw_t* g) {
+  memset(g, 0, sizeof(*g));
+  if (len < 12 || memcmp(f, "VDBHSQ81", 8) != 0) return -1;
+  const uint8_t* p = f + 8;
+  size_t left = len - 12;
+  uint64_t n = 0, cap = 0, sz = 0, seed = 0;
+  uint32_t qd = 0, qp = 0, m = 0, efc = 0, maxl = 0, ep = 0;
+  if (!rd_take(&p, &left, &n, 8) || n != rows || !rd_take(&p, &left, &qd, 4) ||
+      !rd_take(&p, &left, &qp, 4) || qp != pd)
+    return -1;
+  g->pd = pd;
+  g->vbuf = (float*)malloc(sizeof(float) * 2 * pd + 4);
+  if (!rd_take(&p, &left, g->vbuf, 4 * pd) || !rd_take(&p, &left, g->vbuf + pd, 4 * pd)) return -1;
+  g->vmin = g->vbuf;
+  g->scale = g->vbuf + pd;
+  g->codes = p;
+  if (!rd_take(&p, &left, NULL, rows * pd)) return -1;
+  if (!rd_take(&p, &left, &cap, 8) || !rd_take(&p, &left, &sz, 8) || !rd_take(&p, &left, &m, 4) ||
+      !rd_take(&p, &left, &efc, 4) || !rd_take(&p, &left, &seed, 8) ||
+      !rd_take(&p, &left, &maxl, 4) || !rd_take(&p, &left, &ep, 4) || cap != rows || m < 2)
+    return -1;
+  g->cap = cap;
+  g->size = sz;
+  g->M = m;
+  g->M0 = 2 * m;
+  g->max_level = (int)maxl;
+  g->ep = ep;
+  g->level = (uint8_t*)malloc(cap + 1);
+  g->links0 = (uint32_t*)malloc(sizeof(uint32_t) * (cap * (1 + g->M0) + 1));
+  g->up_at = (uint64_t*)calloc(cap + 1, sizeof(uint64_t));
+  if (!rd_take(&p, &left, g->level, cap) ||
+      !rd_take(&p, &left, g->links0, sizeof(uint32_t) * cap * (1 + g->M0)))
+    return -1;
+  uint64_t tot = 0;
+  for (uint64_t i = 0; i < cap; ++i) {
+    g->up_at[i] = tot;
+    tot += (uint64_t)g->level[i] * (1 + m);
+  }
+  g->up = (uint32_t*)malloc(sizeof(uint32_t) * (tot + 1));
+  if (!rd_take(&p, &left, g->up, sizeof(uint32_t) * tot)) return -1;
+  return 0;
+}
+
+/* links_at (hnsw_graph.h:425-428). */
+static const uint32_t* or_links(const or_hnsw_t* g, uint32_t id, int layer) {
+  if (layer == 0) return g->links0 + (size_t)id * (1 + g->M0);
+  return g->up + g->up_at[id] + (size_t)(layer - 1) * (1 + g->M);
+}
+
+/* Binary heaps of (dist, id): max-heap (the results, worst on top) when max_heap, else
+ * min-heap (the candidates, closest on top); std::push_heap / pop_heap with Neighbor's
+ * order (types.h:23-26).  Only the top is ever read, and the order is total, so any heap
+ * holds the same top. */
+static inline int heap_before(nb_t a, nb_t b, int max_heap) {
+  return max_heap ? nb_lt(b, a) : nb_lt(a, b);
+}
+static void heap_push(nb_t* h, size_t* n, nb_t x, int max_heap) {
+  size_t i = (*n)++;
+  h[i] = x;
+  while (i > 0) {
+    size_t p = (i - 1) / 2;
+    if (!heap_before(h[i], h[p], max_heap)) break;
+    nb_t t = h[p];
+    h[p] = h[i];
+    h[i] = t;
+    i = p;
+  }
+}
+static void heap_pop(nb_t* h, size_t* n, int max_heap) {
+  h[0] = h[--(*n)];
+  size_t i = 0;
+  for (;;) {
+    size_t l = 2 * i + 1, r = l + 1, b = i;
+    if (l < *n && heap_before(h[l], h[b], max_heap)) b = l;
+    if (r < *n && heap_before(h[r], h[b], max_heap)) b = r;
+    if (b == i) break;
+    nb_t t = h[b];
+    h[b] = h[i];
+    h[i] = t;
+    i = b;
+  }
+}
+
+typedef struct {
+  int kset, metric;
+  const or_hnsw_t* g;
+  const float* base;
+  const float* queries;
+  size_t k, ef;
+  int rerank;
+  const uint64_t* allow;
+  float* out_d;
+  uint32_t* out_id;
+  uint64_t* dc;
+} hnsw_ctx_t;
+
+static inline float or_hnsw_dist(const hnsw_ctx_t* c, const float* q, uint32_t id) {
+  const or_hnsw_t* g = c->g;
+  return or_metric_sq8(c->kset, c->metric, q, g->codes + (size_t)id * g->pd, g->vmin, g->scale,
+                       g->pd);
+}
+
+/* HnswGraph::search (hnsw_graph.h:301-324) with the greedy descent (:467-496) and the layer-0
+ * beam search_layer<false, kFiltered> (:501-548).  Writes up to kk results ascending into
+ * out and returns their count; *dc counts distance computations as the reference does. */
+static size_t or_hnsw_walk(const hnsw_ctx_t* c, const float* q, size_t kk, size_t ef,
+                           uint8_t* seen, nb_t* res, nb_t* cand, nb_t* out, uint64_t* dc) {
+  const or_hnsw_t* g = c->g;
+  if (g->max_level < 0 || kk == 0) return 0;
+  uint64_t n_dc = 1;
+  uint32_t cur = g->ep;
+  float curd = or_hnsw_dist(c, q, cur);
+  for (int l = g->max_level; l > 0; --l) {
+    for (int changed = 1; changed;) {
+      changed = 0;
+      const uint32_t* ll = or_links(g, cur, l);
+      const uint32_t cnt = ll[0];
+      const uint32_t* nb = ll + 1;
+      for (uint32_t j = 0; j < cnt; ++j) {
+        float d = or_hnsw_dist(c, q, nb[j]);
+        ++n_dc;
+        if (d < curd) {
+          curd = d;
+          cur = nb[j];
+          changed = 1;
+        }
+      }
+    }
+  }
+  if (ef < kk) ef = kk;
+  const int filtered = c->allow != NULL;
+  size_t nr = 0, nc = 0;
+  memset(seen, 0, g->cap);
+  seen[cur] = 1;
+  float lower = INFINITY;
+  nb_t e0 = {curd, cur};
+  if (!filtered || row_allowed(c->allow, cur)) {
+    heap_push(res, &nr, e0, 1);
+    lower = curd;
+  }
+  heap_push(cand, &nc, e0, 0);
+  while (nc > 0) {
+    const nb_t top = cand[0];
+    if (top.d > lower && (!filtered || nr >= ef)) break;
+    heap_pop(cand, &nc, 0);
+    const uint32_t* ll = or_links(g, top.id, 0);
+    const uint32_t cnt = ll[0];
+    for (uint32_t j = 0; j < cnt; ++j) {
+      const uint32_t e = ll[1 + j];
+      if (seen[e]) continue;
+      seen[e] = 1;
+      const float de = or_hnsw_dist(c, q, e);
+      ++n_dc;
+      if (nr < ef || de < lower) {
+        nb_t x = {de, e};
+        heap_push(cand, &nc, x, 0);
+        if (!filtered || row_allowed(c->allow, e)) {
+          heap_push(res, &nr, x, 1);
+          if (nr > ef) heap_pop(res, &nr, 1);
+          lower = res[0].d;
+        }
+      }
+    }
+  }
+  while (nr > kk) heap_pop(res, &nr, 1);
+  memcpy(out, res, sizeof(nb_t) * nr);
+  qsort(out, nr, sizeof(nb_t), nb_cmp);
+  *dc += n_dc;
+  return nr;
+}
+
+static void hnsw_task(void* p, size_t b, size_t e) {
+  hnsw_ctx_t* c = (hnsw_ctx_t*)p;
+  const or_hnsw_t* g = c->g;
+  /* depth and ef of HnswSq8Index::search (hnsw_index.cc:88-89) */
+  const size_t depth = c->rerank < 0 ? (c->ef > c->k ? c->ef : c->k) : (size_t)c->rerank;
+  size_t ef = c->ef > c->k ? c->ef : c->k;
+  if (depth > ef) ef = depth;
+  const size_t kk = depth > c->k ? depth : c->k;
+  uint8_t* seen = (uint8_t*)malloc(g->cap + 1);
+  /* the candidate heap holds at most every node once, the results ef + 1 */
+  nb_t* cand = (nb_t*)malloc(sizeof(nb_t) * (g->cap + 1));
+  nb_t* res = (nb_t*)malloc(sizeof(nb_t) * (ef + 2));
+  nb_t* out = (nb_t*)malloc(sizeof(nb_t) * (ef + 2));
+  uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * (ef + 2));
+  float* rd = (float*)malloc(sizeof(float) * (c->k + 1));
+  uint32_t* ri = (uint32_t*)malloc(sizeof(uint32_t) * (c->k + 1));
+  for (size_t qi = b; qi < e; ++qi) {
+    const float* q = c->queries + qi * g->pd;
+    float* od = c->out_d + qi * c->k;
+    uint32_t* oi = c->out_id + qi * c->k;
+    uint64_t dc = 0;
+    if (c->k == 0) {
+      if (c->dc) c->dc[qi] = 0;
+      continue;
+    }
+    if (depth == 0) {
+      size_t m = or_hnsw_walk(c, q, c->k, ef, seen, res, cand, out, &dc);
+      write_padded(out, m, c->k, od, oi);
+    } else {
+      size_t m = or_hnsw_walk(c, q, kk, ef, seen, res, cand, out, &dc);
+      for (size_t i = 0; i < m; ++i) ids[i] = out[i].id;
+      /* Rerank (index.cc:89-95): exact distances of every candidate, TopK(k) */
+      size_t n2 = or_rerank(c->kset, c->metric, c->base, g->pd, q, ids, m, c->k, rd, ri);
+      dc += m;
+      for (size_t i = 0; i < c->k; ++i) {
+        od[i] = i < n2 ? rd[i] : INFINITY;
+        oi[i] = i < n2 ? ri[i] : UINT32_MAX;
+      }
+    }
+    if (c->dc) c->dc[qi] = dc;
+  }
+  free(ri);
+  free(rd);
+  free(ids);
+  free(out);
+  free(res);
+  free(cand);
+  free(seen);
+}
+
+int or_hnsw_sq8_search_file(int kset, int metric, const uint8_t* file, size_t len,
+                            const float* base, size_t rows, size_t pd, const float* queries,
+                            size_t nq, size_t k, size_t ef, int rerank,
+                            const uint64_t* allow_words, float* out_d, uint32_t* out_id,
+                            uint64_t* dist_comps, int nthreads) {
+  or_hnsw_t g;
+  if (or_hnsw_parse(file, len, rows, pd, &g) != 0) {
+    or_hnsw_free(&g);
+    return -1;
+  }
+  hnsw_ctx_t c = {kset, metric, &g, base, queries, k, ef, rerank, allow_words, out_d, out_id,
+                  dist_comps};
+  or_parallel(nq, nthreads, hnsw_task, &c);
+  or_hnsw_free(&g);
+  return 0;
+}

@@ -33,6 +33,8 @@
  *   normalize      compiled reference + closed form
  *   merge          closed form (sort by (dist, part, row), dedupe external id)
  *   crc32c         known answer 0xE3069283 for "123456789" (tests/distance_test.cc:94)
+ *   hnsw-sq8       compiled reference (HnswSq8Index::search on files it built and saved)
+ *                  + closed form (ef >= rows walks every node: equals exact flat search)
  */
 #ifndef VDB_ORACLE_H_
 #define VDB_ORACLE_H_
@@ -139,6 +141,18 @@ size_t or_merge_parts(size_t nparts, size_t k, const float* part_d, const uint32
 int or_plan_segment(int has_filter, size_t rows, size_t deleted, size_t matches, int index_flat,
                     int strategy, size_t ef, size_t k, size_t nprobe,
                     size_t prefilter_threshold, size_t* nprobe_out);
+
+/* ---- HNSW-SQ8 search (src/index/hnsw/hnsw_index.cc:82-100) ----
+ * HnswSq8Index::search per query over a VDBHSQ81 file (quantizer, codes and graph read from
+ * it): HnswGraph::search's greedy descent and layer-0 beam (hnsw_graph.h:301-324, 467-548)
+ * on SQ8 distances, then Rerank on the float rows.  ef and rerank are SearchParams' (rerank
+ * -1 = auto).  dist_comps (nullable) receives IndexSearchStats::distance_computations.
+ * Returns 0, or -1 when the file does not parse. */
+int or_hnsw_sq8_search_file(int kset, int metric, const uint8_t* file, size_t len,
+                            const float* base, size_t rows, size_t pd, const float* queries,
+                            size_t nq, size_t k, size_t ef, int rerank,
+                            const uint64_t* allow_words, float* out_d, uint32_t* out_id,
+                            uint64_t* dist_comps, int nthreads);
 
 /* ---- CRC32C (src/util/crc32c.cc) ---- */
 uint32_t or_crc32c(uint32_t crc, const void* data, size_t n);

@@ -528,8 +528,34 @@ struct SegFiles {
   std::vector<uint32_t> deleted;
   std::vector<float> vmin, scale;  // HNSW-SQ8
   std::vector<uint8_t> codes;
+  std::string file;                // the VDBHSQ81 index file
   IvfFile ivf;                     // IVF-PQ
 };
+
+// A small valid HNSW graph in HnswGraph::serialize's layout (hnsw_graph.h:352-366): every node
+// on layer 0 only, linked to the nodes up to four places before and after it (M = 4, M0 = 8).
+std::string ChainGraph(size_t rows) {
+  const uint32_t M = 4, M0 = 2 * M;
+  std::string g;
+  Put<uint64_t>(&g, rows);
+  Put<uint64_t>(&g, rows);
+  Put<uint32_t>(&g, M);
+  Put<uint32_t>(&g, 40);
+  Put<uint64_t>(&g, 42);
+  Put<uint32_t>(&g, 0);  // top layer
+  Put<uint32_t>(&g, 0);  // entry point
+  g.append(rows, '\0');  // levels
+  for (size_t i = 0; i < rows; ++i) {
+    std::vector<uint32_t> nb;
+    for (int d = 1; d <= 4; ++d) {
+      if (i + d < rows) nb.push_back(uint32_t(i + d));
+      if (i >= size_t(d)) nb.push_back(uint32_t(i - d));
+    }
+    Put<uint32_t>(&g, uint32_t(nb.size()));
+    for (uint32_t j = 0; j < M0; ++j) Put<uint32_t>(&g, j < nb.size() ? nb[j] : 0u);
+  }
+  return g;
+}
 
 std::string MakeSegmentDir(const std::string& root, uint32_t id, vdbg::IndexType t, vdbg::Metric m,
                            SegFiles& sf, uint64_t first_ext) {
@@ -556,8 +582,9 @@ std::string MakeSegmentDir(const std::string& root, uint32_t id, vdbg::IndexType
     body.append(reinterpret_cast<const char*>(sf.vmin.data()), b.pd * 4);
     body.append(reinterpret_cast<const char*>(sf.scale.data()), b.pd * 4);
     body.append(reinterpret_cast<const char*>(sf.codes.data()), sf.codes.size());
-    body.append(16, '\0');  // the graph (not read by the device)
+    body += ChainGraph(b.rows);
     file = IndexFile("VDBHSQ81", body);
+    sf.file = file;
   } else {
     std::unique_ptr<vdbg::GpuIvfPqIndex> ix;
     vdbg::IndexOptions o;
@@ -585,10 +612,11 @@ std::vector<std::vector<vdbg::Neighbor>> OracleSegment(const SegFiles& sf, vdbg:
   const Data& b = sf.rows;
   std::vector<float> d(nq * k);
   std::vector<uint32_t> id(nq * k);
-  if (t == vdbg::IndexType::HnswSq8) {
-    or_sq8_search_batch(Kset(), int(m), b.v.data(), sf.codes.data(), b.rows, b.pd, sf.vmin.data(),
-                        sf.scale.data(), q, nq, k, std::max(p.ef, k), allow ? allow->words() : nullptr,
-                        d.data(), id.data(), 8);
+  if (t == vdbg::IndexType::HnswSq8) {  // HnswSq8Index::search over the file's graph
+    CHECK(or_hnsw_sq8_search_file(Kset(), int(m), reinterpret_cast<const uint8_t*>(sf.file.data()),
+                                  sf.file.size(), b.v.data(), b.rows, b.pd, q, nq, k, p.ef,
+                                  p.rerank, allow && !sf.deleted.empty() ? allow->words() : nullptr,
+                                  d.data(), id.data(), nullptr, 8) == 0);
   } else {
     const IvfFile& f = sf.ivf;
     std::vector<float> term2(f.nlist * f.m * 256);
@@ -637,6 +665,26 @@ void SegmentOpenAndCollectionSearch() {
   std::vector<const vdbg::GpuSegment*> segs{seg[0].get(), seg[1].get(), seg[2].get()};
   vdbg::SearchParams p;
   p.nprobe = 6;
+  {  // GpuHnswSq8Index on its own over segment 1's file: graph walk + GPU rerank
+    std::unique_ptr<vdbg::GpuHnswSq8Index> hx;
+    CHECK_OK(vdbg::GpuHnswSq8Index::Load(*g_dev, m, sf[1].rows.view(), sf[1].file, &hx));
+    const size_t pd = vdbg::PaddedDim(dim);
+    std::vector<float> q(nq * pd, 0.f);
+    for (size_t i = 0; i < nq; ++i) std::memcpy(&q[i * pd], &rq[i * dim], dim * 4);
+    for (int rr : {-1, 0, 25}) {
+      vdbg::SearchParams hp;
+      hp.ef = 20;
+      hp.rerank = rr;
+      std::vector<std::vector<vdbg::Neighbor>> got;
+      CHECK_OK(hx->search_batch(q.data(), nq, k, hp, nullptr, got, nullptr));
+      const auto want = OracleSegment(sf[1], vdbg::IndexType::HnswSq8, m, q.data(), nq, k, hp, nullptr);
+      for (size_t i = 0; i < nq; ++i) {
+        CHECK(got[i].size() == want[i].size());
+        for (size_t j = 0; j < std::min(got[i].size(), want[i].size()); ++j)
+          CHECK(got[i][j].id == want[i][j].id && std::memcmp(&got[i][j].dist, &want[i][j].dist, 4) == 0);
+      }
+    }
+  }
   for (int with_filter = 0; with_filter < 2; ++with_filter) {
     std::vector<vdbg::DenseRowFilter> filt;
     std::vector<const vdbg::DenseRowFilter*> fp;

@@ -180,6 +180,7 @@ def main():
     np.savez_compressed(os.path.join(HERE, "misc.npz"), norm_in=nv, norm_out=outn, norm_ok=okn,
                         crc_blob=np.frombuffer(blobs[2], np.uint8).copy(), crc=crc)
     make_segment(L)
+    make_hnsw(L)
     print("golden fixtures written to", HERE)
 
 
@@ -207,8 +208,75 @@ def make_segment(L):
     np.savez_compressed(os.path.join(HERE, "segment.npz"), **out)
 
 
+def _words(allowed):
+    w = np.zeros(((allowed.size + 63) // 64) * 8, np.uint8)
+    b = np.packbits(allowed, bitorder="little")
+    w[:b.size] = b
+    return w.view(np.uint64)
+
+
+def make_hnsw(L):
+    """hnsw.npz: VDBHSQ81 files built and saved by the reference (HnswSq8Index::build + save,
+    single-threaded so the graph is deterministic) and the results of its own
+    HnswSq8Index::search (hnsw_index.cc:82-100) on them: ids, distances and
+    distance_computations per query, for several (k, ef, rerank) settings, without a filter
+    and with RowFilters allowing about 98 %, 30 % and 2 % of the rows."""
+    from oracle_lib import Reference
+    R = Reference()
+    rng = np.random.default_rng(20261202)
+    out = {}
+    cases = [("c", 2500, 48, 0, 16, 100), ("d", 1200, 32, 2, 12, 80), ("e", 1000, 24, 1, 8, 40)]
+    settings = np.array([(10, 64, -1), (5, 16, 0), (20, 32, 100), (1, 8, -1), (40, 10, 3),
+                         (60, 40, -1)], np.int64)
+    for tag, n, dim, metric, M, efc in cases:
+        pd = (dim + 15) // 16 * 16
+        base = np.zeros((n, pd), np.float32)
+        nq = 32
+        q = np.zeros((nq, pd), np.float32)
+        if metric == 0:  # integer-valued clustered rows, as the SIFT-like workload
+            cen = rng.uniform(0, 64, (40, dim))
+            base[:, :dim] = np.clip(np.rint(cen[rng.integers(0, 40, n)] +
+                                            8 * rng.standard_normal((n, dim))), 0, 255)
+            q[:, :dim] = np.clip(np.rint(cen[rng.integers(0, 40, nq)] +
+                                         8 * rng.standard_normal((nq, dim))), 0, 255)
+        else:
+            cen = rng.standard_normal((30, dim))
+            base[:, :dim] = cen[rng.integers(0, 30, n)] + 0.4 * rng.standard_normal((n, dim))
+            q[:, :dim] = cen[rng.integers(0, 30, nq)] + 0.4 * rng.standard_normal((nq, dim))
+            if metric == 2:
+                base /= np.linalg.norm(base, axis=1, keepdims=True)
+                q /= np.linalg.norm(q, axis=1, keepdims=True)
+        size = L.ref_hnsw_sq8_file(metric, base, n, dim, pd, M, efc, 42, None, 0)
+        buf = C.create_string_buffer(size)
+        assert L.ref_hnsw_sq8_file(metric, base, n, dim, pd, M, efc, 42, buf, size) == size
+        f = buf.raw
+        # integer rows (0..255) are stored as bytes, exactly
+        out[f"{tag}_rows"] = base.astype(np.uint8) if metric == 0 else base
+        out[f"{tag}_q"] = q
+        out[f"{tag}_metric"], out[f"{tag}_dim"] = np.int32(metric), np.int32(dim)
+        out[f"{tag}_file"] = np.frombuffer(f, np.uint8).copy()
+        for fi, frac in enumerate((None, 0.98, 0.30, 0.02)):
+            allow = None
+            if frac is not None:
+                allow = _words(rng.random(n) < frac)
+                out[f"{tag}_allow{fi}"] = allow
+            for si, (k, ef, rr) in enumerate(settings):
+                od, oi, dc = R.hnsw_sq8_search(f, base, dim, q, int(k), int(ef), int(rr),
+                                               ["l2", "ip", "cosine"][metric], allow)
+                out[f"{tag}_f{fi}_s{si}_d"], out[f"{tag}_f{fi}_s{si}_i"] = od, oi
+                out[f"{tag}_f{fi}_s{si}_dc"] = dc
+    out["settings"] = settings
+    out["kernels"] = np.array(R.lib.ref_best_kernels().decode())
+    np.savez_compressed(os.path.join(HERE, "hnsw.npz"), **out)
+
+
 if __name__ == "__main__":
-    if sys.argv[1:] == ["segment"]:
+    if sys.argv[1:] == ["hnsw"]:
+        ref = load_reference()
+        if ref is None:
+            sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+        make_hnsw(ref.lib)
+    elif sys.argv[1:] == ["segment"]:
         ref = load_reference()
         if ref is None:
             sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")

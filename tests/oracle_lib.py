@@ -77,6 +77,9 @@ class Oracle:
         _sig(lib, "or_plan_segment", C.c_int,
              [C.c_int, sz, sz, sz, C.c_int, C.c_int, sz, sz, sz, sz, C.POINTER(C.c_size_t)])
         _sig(lib, "or_crc32c", C.c_uint32, [C.c_uint32, C.c_char_p, sz])
+        _sig(lib, "or_hnsw_sq8_search_file", C.c_int,
+             [C.c_int, C.c_int, C.c_char_p, sz, f32p, sz, sz, f32p, sz, sz, sz, C.c_int,
+              _opt(u64p), f32p, u32p, _opt(u64p), C.c_int])
 
     # -- convenience wrappers (numpy in, numpy out)
     def flat_search(self, base, queries, k, metric="l2", kset="avx512", allow=None,
@@ -118,6 +121,24 @@ class Oracle:
         return od, oi
 
 
+    def hnsw_sq8_search(self, file, base, queries, k, ef=64, rerank=-1, metric="l2",
+                        allow=None, kset="avx512", threads=8):
+        """HnswSq8Index::search per query over a VDBHSQ81 file's quantizer, codes and graph,
+        reranked on base.  Returns (dists, ids, distance computations)."""
+        base = np.ascontiguousarray(base, np.float32)
+        queries = np.ascontiguousarray(queries, np.float32)
+        nq, pd = queries.shape
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.uint32)
+        dc = np.empty(nq, np.uint64)
+        file = bytes(file)
+        rc = self.lib.or_hnsw_sq8_search_file(KSET[kset], METRIC[metric], file, len(file), base,
+                                              base.shape[0], pd, queries, nq, k, ef, rerank,
+                                              allow, od, oi, dc, threads)
+        if rc != 0:
+            raise ValueError("the index file does not parse")
+        return od, oi, dc
+
     def ivfpq_search(self, ix, term2, base, queries, k, nprobe, rerank, metric="l2",
                      allow=None, kset="avx512"):
         """IvfPqIndex::search over an index parsed with ivf_file.parse_ivfpq."""
@@ -134,16 +155,19 @@ class Oracle:
         return od, oi, dc
 
     def collection_search(self, segments, dim, metric, raw, k, ef=64, nprobe=16, rerank=-1,
-                          strategy=0, prefilter_threshold=10000, post_filter_alpha=10):
+                          strategy=0, prefilter_threshold=10000, post_filter_alpha=10,
+                          kset="avx512"):
         """CollectionImpl::SearchBatch (src/engine/collection_impl.cc:1036-1135) over disk
         segments, composed from the oracle's parts: PrepareQuery (:1023-1034, or_normalize),
         each segment's plan (SearchDiskSegment, planner.cc:42-129: or_plan_segment, the
         index searches, the exact fallback of :103-108, the post filter of :110-127), and
         the merge (:1076-1112, or_merge_parts), one query at a time.
 
-        segments: dicts with base (n, pd) fp32, ext (n,) uint64, kind "flat" | "sq8" | "ivf",
-        deleted / filter (dense words or None); sq8: codes, vmin, scale; ivf: ix (parsed
-        VDBIVFP1) and term2 (or None).  Returns (ext ids, dists, dist comps, plan names)."""
+        segments: dicts with base (n, pd) fp32, ext (n,) uint64, kind "flat" | "sq8" |
+        "hnsw_sq8" | "ivf", deleted / filter (dense words or None); sq8 (the GPU's exhaustive
+        SQ8 scan index, built from rows, no graph): codes, vmin, scale; hnsw_sq8 (vdb's
+        HnswSq8Index): file (the VDBHSQ81 bytes); ivf: ix (parsed VDBIVFP1) and term2 (or
+        None).  Returns (ext ids, dists, dist comps, plan names)."""
         nq = raw.shape[0]
         pd = (dim + 15) // 16 * 16
         q = np.zeros((nq, pd), np.float32)
@@ -193,18 +217,22 @@ class Oracle:
                                             1 if sg["kind"] == "flat" else 0, strategy, ef, k,
                                             nprobe, prefilter_threshold, C.byref(npb))
 
-            def index_search(kk, allow):
+            def index_search(kk, allow, ef_=ef):
+                if sg["kind"] == "hnsw_sq8":
+                    od, oi, dc = self.hnsw_sq8_search(sg["file"], base, q, kk, ef_, rerank,
+                                                      metric=metric, allow=allow, kset=kset)
+                    return od, oi, dc
                 if sg["kind"] == "ivf":
                     od, oi, dc = self.ivfpq_search(sg["ix"], sg["term2"], base, q, kk,
-                                                   npb.value, rerank, metric, allow)
+                                                   npb.value, rerank, metric, allow, kset=kset)
                     return od, oi, dc
                 if sg["kind"] == "sq8":
-                    depth = max(ef, kk) if rerank < 0 else rerank
+                    depth = max(ef_, kk) if rerank < 0 else rerank
                     od, oi = self.sq8_search(base, sg["codes"], sg["vmin"], sg["scale"], q, kk,
-                                             depth, metric=metric, allow=allow)
+                                             depth, metric=metric, kset=kset, allow=allow)
                     extra = min(max(depth, kk), n) if depth > 0 else 0
                     return od, oi, np.full(nq, n + extra, np.uint64)
-                od, oi = self.flat_search(base, q, kk, metric=metric, allow=allow)
+                od, oi = self.flat_search(base, q, kk, metric=metric, kset=kset, allow=allow)
                 return od, oi, np.full(nq, n, np.uint64)
 
             if plan == 0:
@@ -214,7 +242,7 @@ class Oracle:
                 oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
                 dc = np.zeros(nq, np.uint64)
             elif plan == 2:
-                od, oi = self.flat_search(base, q, k, metric=metric, allow=bm)
+                od, oi = self.flat_search(base, q, k, metric=metric, kset=kset, allow=bm)
                 dc = np.full(nq, matches, np.uint64)
             elif plan == 3:
                 od, oi, dc = index_search(k, bm)
@@ -223,13 +251,14 @@ class Oracle:
                     short = np.nonzero(hits < min(k, matches))[0]
                     if short.size:
                         plan = 4
-                        xd, xi = self.flat_search(base, q, k, metric=metric, allow=bm)
+                        xd, xi = self.flat_search(base, q, k, metric=metric, kset=kset,
+                                                  allow=bm)
                         od[short], oi[short] = xd[short], xi[short]
                         dc = dc.copy()
                         dc[short] += np.uint64(matches)
             else:
                 kk = min(max(live, 1), k * max(1, post_filter_alpha))
-                wd, wi, dc = index_search(kk, del_allow)
+                wd, wi, dc = index_search(kk, del_allow, max(ef, kk))  # pp.ef (:113-114)
                 od = np.full((nq, k), np.inf, np.float32)
                 oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
                 for i in range(nq):
@@ -303,6 +332,9 @@ class Reference:
         _sig(lib, "ref_crc32c", C.c_uint32, [C.c_char_p, sz])
         _sig(lib, "ref_hnsw_sq8_file", sz,
              [C.c_int, f32p, sz, sz, sz, sz, sz, C.c_uint64, C.c_void_p, sz])
+        _sig(lib, "ref_hnsw_sq8_search_batch", C.c_int,
+             [C.c_int, C.c_char_p, sz, f32p, sz, sz, sz, f32p, sz, sz, sz, C.c_int, _opt(u64p),
+              f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "ref_filtered_collection_search", C.c_int,
              [C.c_int, C.c_void_p, C.c_void_p, sz, sz, sz, C.c_void_p, u64p, f32p, sz, sz,
               u64p, f32p, C.c_int])
@@ -330,6 +362,24 @@ class Reference:
         if rc != 0:
             raise ValueError("a query was rejected by PrepareQuery")
         return oe, od
+
+    def hnsw_sq8_search(self, file, base, dim, queries, k, ef=64, rerank=-1, metric="l2",
+                        allow=None, threads=8):
+        """LoadIndex of a VDBHSQ81 file and HnswSq8Index::search per query, with the
+        reference's own kernel set.  Returns (dists, ids, distance computations)."""
+        base = np.ascontiguousarray(base, np.float32)
+        queries = np.ascontiguousarray(queries, np.float32)
+        nq, pd = queries.shape
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.uint32)
+        dc = np.empty(nq, np.uint64)
+        file = bytes(file)
+        rc = self.lib.ref_hnsw_sq8_search_batch(METRIC[metric], file, len(file), base,
+                                                base.shape[0], dim, pd, queries, nq, k, ef,
+                                                rerank, allow, od, oi, dc, threads)
+        if rc != 0:
+            raise ValueError("LoadIndex refused the file")
+        return od, oi, dc
 
     def flat_search(self, base, dim, queries, k, metric="l2", kset="avx512", allow=None,
                     threads=8):

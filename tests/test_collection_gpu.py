@@ -34,8 +34,9 @@ def _words(rows, n):
 
 @pytest.fixture(scope="module")
 def coll(ctx, oracle):
-    """Four segments: flat (deletes), HNSW-SQ8 codes, IVF-PQ (deletes), a small flat one that
-    re-inserts external ids of the first (an upsert visible in both)."""
+    """Four segments: flat (deletes), SQ8 codes made on the GPU (this library's SQ8 scan index,
+    no graph), IVF-PQ (deletes), a small flat one that re-inserts external ids of the first (an
+    upsert visible in both)."""
     pd = vdbg.padded_dim(DIM)
     sizes = [6000, 8000, 20000, 500]
     kinds = ["flat", "sq8", "ivf", "flat"]
@@ -205,3 +206,79 @@ def test_collection_errors(ctx, coll):
     # no segments: every query gets padding
     gi, gd, gdc, gp = vdbg.collection_search(ctx, [], DIM, "l2", q, 5)
     assert (gi == np.iinfo(np.uint64).max).all() and np.isinf(gd).all() and gp == []
+
+
+def test_hnsw_sq8_segment_is_the_references(ctx, oracle):
+    """An HnswSq8Index segment (a VDBHSQ81 file the reference built and saved) inside the
+    one-batch collection search: its graph is walked and its beam reranked, so the answer is
+    HnswSq8Index::search's.  Alone in a collection it must return exactly what the reference's
+    own search returned on that file (tests/golden/hnsw.npz), with no filter and under a
+    DeleteFilter; mixed with flat segments, filters and every strategy, the oracle's
+    composition (whose HNSW search the same fixtures pin)."""
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hnsw.npz"))
+    ctx.set_kernels(str(g["kernels"]))
+    rows = np.ascontiguousarray(g["c_rows"], np.float32)
+    q, f, dim = g["c_q"], g["c_file"].tobytes(), int(g["c_dim"])
+    n, pd = rows.shape
+    assert list(g["settings"][0]) == [10, 64, -1]  # SearchParams' defaults, k = 10
+    ds = vdbg.Dataset(ctx, rows, dim)
+    ext = np.arange(n, dtype=np.uint64) * 7 + 5
+    ds.set_external_ids(ext)
+    sq = vdbg.Sq8Index.load(ds, f)
+    print(f"collection hnsw-sq8 segment n={n} dim={dim}", flush=True)
+    # alone, no filter: the "index" plan, HnswSq8Index::search with the default params
+    gi, gd, gdc, gp = vdbg.collection_search(ctx, [(ds, sq, None, None)], dim, "l2", q, 10)
+    want = g["c_f0_s0_i"]
+    assert gp == ["index"]
+    assert np.array_equal(gi, np.where(want == 0xFFFFFFFF, np.iinfo(np.uint64).max,
+                                       ext[np.minimum(want, n - 1)]))
+    assert np.array_equal(gd.view(np.uint32), g["c_f0_s0_d"].view(np.uint32))
+    assert np.array_equal(gdc, g["c_f0_s0_dc"])
+    # alone, the rows outside the ~98 % filter deleted: the DeleteFilter of planner.cc:56-61
+    deleted = ~np.asarray(g["c_allow1"], np.uint64)
+    gi, gd, gdc, gp = vdbg.collection_search(ctx, [(ds, sq, deleted, None)], dim, "l2", q, 10)
+    want = g["c_f1_s0_i"]
+    assert gp == ["index"]
+    assert np.array_equal(gi, np.where(want == 0xFFFFFFFF, np.iinfo(np.uint64).max,
+                                       ext[np.minimum(want, n - 1)]))
+    assert np.array_equal(gd.view(np.uint32), g["c_f1_s0_d"].view(np.uint32))
+    assert np.array_equal(gdc, g["c_f1_s0_dc"])
+    # with two flat segments, deletes and filters, against the oracle's composition
+    segs = [{"base": rows, "ext": ext, "kind": "hnsw_sq8", "file": f,
+             "deleted": _mask(n, 0.05, 870), "filter": None}]
+    handles = [(ds, sq)]
+    for i, m in enumerate((3000, 800)):
+        b = np.clip(np.rint(rows[np.random.default_rng(880 + i).integers(0, n, m)] +
+                            np.random.default_rng(890 + i).normal(0, 3, (m, pd))), 0, 255)
+        b = np.ascontiguousarray(b * (np.arange(pd) < dim), np.float32)
+        e = np.arange(m, dtype=np.uint64) + 10 ** 6 * (i + 1)
+        if i == 1:
+            e[:50] = ext[:50]  # an upsert seen in both segments
+        d2 = vdbg.Dataset(ctx, b, dim)
+        d2.set_external_ids(e)
+        segs.append({"base": b, "ext": e, "kind": "flat", "deleted": None, "filter": None})
+        handles.append((d2, None))
+    qq = q[:24]
+    try:
+        for filt, kw in ((None, {}), ("f", {"prefilter_threshold": 100}),
+                         ("f", {"strategy": "graph"}), ("f", {"strategy": "post_filter",
+                                                              "post_filter_alpha": 4}),
+                         (None, {"ef": 16, "rerank": 0}), (None, {"ef": 8, "rerank": 30})):
+            for i, sg in enumerate(segs):
+                sg["filter"] = None if filt is None else _mask(sg["base"].shape[0], 0.4, 900 + i)
+            k = 10
+            gi, gd, gdc, gplans = vdbg.collection_search(
+                ctx, [(d_, ix, sg["deleted"], sg["filter"]) for (d_, ix), sg in zip(handles, segs)],
+                dim, "l2", qq, k, vdbg.SearchParams(**kw))
+            okw = dict(kw)
+            okw["strategy"] = vdbg.STRATEGIES[okw.get("strategy", "auto")]
+            oi, od, odc, oplans = oracle.collection_search(segs, dim, "l2", qq, k,
+                                                           kset=str(g["kernels"]), **okw)
+            assert gplans == oplans, (filt, kw)
+            assert np.array_equal(gi, oi) and np.array_equal(gd.view(np.uint32), od.view(np.uint32)), (filt, kw)
+            assert np.array_equal(gdc, odc), (filt, kw)
+    finally:
+        sq.close()
+        for d_, _ in handles:
+            d_.close()

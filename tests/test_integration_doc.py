@@ -40,3 +40,23 @@ def test_integration_adapter_compiles_against_vdb_headers(tmp_path):
                         "-I", os.path.join(REF, "src"), "-I", os.path.join(ROOT, "include"),
                         str(src)], capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_integration_search_batch_compiles_against_vdb_headers(tmp_path):
+    """The SearchBatch device branch, with the adapter header where vdb would keep it."""
+    if not os.path.isdir(os.path.join(REF, "src", "index")):
+        pytest.skip("the reference sources are not present here")
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    a = re.search(r"<!-- adapter:begin -->\s*```cpp\n(.*?)```\s*<!-- adapter:end -->", doc, re.S)
+    b = re.search(r"<!-- batch:begin -->\s*```cpp\n(.*?)```\s*<!-- batch:end -->", doc, re.S)
+    assert a and b, "adapter or batch block not found in INTEGRATION.md"
+    hdr = tmp_path / "index" / "gpu"
+    hdr.mkdir(parents=True)
+    (hdr / "gpu_index.h").write_text(a.group(1))
+    src = tmp_path / "gpu_search_batch.cc"
+    src.write_text(b.group(1))
+    r = subprocess.run([_gxx(), "-std=c++20", "-Wall", "-fsyntax-only", "-I", str(tmp_path),
+                        "-I", os.path.join(REF, "include"), "-I", os.path.join(REF, "src"),
+                        "-I", os.path.join(ROOT, "include"), str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr

@@ -435,3 +435,96 @@ def test_plan_segment_known_answers(oracle):
     assert plan(1, 100000, 0, 50000, strategy=2) == (3, 16)   # Graph: no boost when explicit
     assert plan(1, 100000, 0, 50000, strategy=3) == (5, 16)   # PostFilter
     assert plan(1, 100000, 0, 0, strategy=3) == (1, 16)       # empty wins over the strategy
+
+
+# ------------------------------------------------------------------ HNSW-SQ8 search
+
+METRICS = ["l2", "ip", "cosine"]
+
+
+def hnsw_case(g, tag):
+    rows = np.ascontiguousarray(g[f"{tag}_rows"], np.float32)
+    return (rows, g[f"{tag}_q"], METRICS[int(g[f"{tag}_metric"])], int(g[f"{tag}_dim"]),
+            g[f"{tag}_file"].tobytes())
+
+
+def test_hnsw_sq8_matches_golden(oracle):
+    """HnswSq8Index::search results recorded from the reference (graph beam on SQ8 codes,
+    then Rerank): ids, distances and distance computations, every setting and filter."""
+    g = gold("hnsw")
+    ks = str(g["kernels"])
+    for tag in ("c", "d", "e"):
+        rows, q, metric, dim, f = hnsw_case(g, tag)
+        for fi in range(4):
+            allow = g[f"{tag}_allow{fi}"] if fi else None
+            for si, (k, ef, rr) in enumerate(g["settings"]):
+                od, oi, dc = oracle.hnsw_sq8_search(f, rows, q, int(k), int(ef), int(rr),
+                                                    metric=metric, allow=allow, kset=ks)
+                key = f"{tag}_f{fi}_s{si}"
+                assert np.array_equal(oi, g[key + "_i"]), key
+                assert np.array_equal(bits(od), bits(g[key + "_d"])), key
+                assert np.array_equal(dc, g[key + "_dc"]), key
+
+
+def test_hnsw_sq8_golden_exercises_every_branch():
+    """The recorded cases reach the parts of the walk a slip would change: the upper-layer
+    descent (several layers), short results under a sparse filter, depth 0 (no rerank) and
+    rerank depths below, at and above k."""
+    g = gold("hnsw")
+    for tag in ("c", "d", "e"):
+        f = g[f"{tag}_file"].tobytes()
+        n = int.from_bytes(f[8:16], "little")
+        pd = int.from_bytes(f[20:24], "little")
+        off = 8 + 8 + 8 + 8 * pd + n * pd + 16 + 8 + 8
+        assert int.from_bytes(f[off:off + 4], "little") >= 2, tag  # max level
+        short = g[f"{tag}_f3_s5_i"]  # about 2 % of the rows allowed, k = 60
+        assert (short == 0xFFFFFFFF).any(), tag
+    assert {int(s[2]) for s in g["settings"]} >= {-1, 0, 3, 100}
+
+
+def test_hnsw_sq8_beam_over_every_node_equals_flat(oracle):
+    """Closed form: with ef at least the row count the beam never fills, so it visits every
+    node reachable from the entry point (all of them: vdb repairs connectivity after the
+    build), and rerank depth max(ef, k) re-scores them all: exact flat search."""
+    g = gold("segment")
+    for tag in ("a", "b"):
+        rows = g[f"{tag}_rows"]
+        n, pd = rows.shape
+        metric = ["l2", "ip", "cosine"][int(g[f"{tag}_metric"])]
+        rng = np.random.default_rng(3)
+        q = np.zeros((20, pd), np.float32)
+        q[:, :int(g[f"{tag}_dim"])] = rng.uniform(-3, 5, (20, int(g[f"{tag}_dim"])))
+        f = g[f"{tag}_file"].tobytes()
+        for k in (1, 10, 33):
+            od, oi, dc = oracle.hnsw_sq8_search(f, rows, q, k, n, -1, metric=metric)
+            fd, fi = oracle.flat_search(rows, q, k, metric=metric)
+            assert np.array_equal(oi, fi) and np.array_equal(bits(od), bits(fd)), (tag, k)
+            assert (dc >= n + n).all()  # every node scored by the walk, then reranked
+
+
+def test_hnsw_sq8_matches_reference_random(oracle, reference):
+    g = gold("segment")
+    rng = np.random.default_rng(11)
+    for tag in ("a", "b"):
+        rows = g[f"{tag}_rows"]
+        n, pd = rows.shape
+        dim = int(g[f"{tag}_dim"])
+        metric = ["l2", "ip", "cosine"][int(g[f"{tag}_metric"])]
+        f = g[f"{tag}_file"].tobytes()
+        q = np.zeros((30, pd), np.float32)
+        q[:, :dim] = rng.uniform(-3, 5, (30, dim))
+        for k, ef, rr in ((10, 64, -1), (7, 12, 0), (15, 20, 50), (3, 5, 2)):
+            for frac in (None, 0.4):
+                allow = None
+                if frac is not None:
+                    a = rng.random(n) < frac
+                    w = np.zeros(((n + 63) // 64) * 8, np.uint8)
+                    b = np.packbits(a, bitorder="little")
+                    w[:b.size] = b
+                    allow = w.view(np.uint64)
+                rd, ri, rdc = reference.hnsw_sq8_search(f, rows, dim, q, k, ef, rr, metric, allow)
+                od, oi, dc = oracle.hnsw_sq8_search(f, rows, q, k, ef, rr, metric=metric,
+                                                    allow=allow,
+                                                    kset=reference.lib.ref_best_kernels().decode())
+                assert np.array_equal(oi, ri) and np.array_equal(bits(od), bits(rd))
+                assert np.array_equal(dc, rdc)
