@@ -90,9 +90,10 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     if (d.ctx != c) return SetError(kInvalidArgument, "segment on another context");
     if (d.dim != dim || d.pd != pd || d.metric != metric)
       return SetError(kInvalidArgument, "segment dim or metric differs from the collection's");
-    if (g.sq8 != nullptr && g.ivfpq != nullptr)
-      return SetError(kInvalidArgument, "a segment has one index: sq8 or ivfpq, not both");
-    if ((g.sq8 != nullptr && g.sq8->q.ds != &d) || (g.ivfpq != nullptr && g.ivfpq->x.ds != &d))
+    if (int(g.sq8 != nullptr) + int(g.ivfpq != nullptr) + int(g.pqflat != nullptr) > 1)
+      return SetError(kInvalidArgument, "a segment has one index: sq8, ivfpq or pqflat");
+    if ((g.sq8 != nullptr && g.sq8->q.ds != &d) || (g.ivfpq != nullptr && g.ivfpq->x.ds != &d) ||
+        (g.pqflat != nullptr && g.pqflat->p.ds != &d))
       return SetError(kInvalidArgument, "index does not belong to the segment's rows");
     if (d.n > 0 && d.ext_ids == nullptr)
       return SetError(kFailedPrecondition, "segment has no external ids (vdbg_dataset_set_external_ids)");
@@ -127,7 +128,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
       sp.matches = CountRows(sp.allow.data(), rows);
       const double sel = live == 0 ? 0.0 : double(sp.matches) / double(live);
       int strat = P.strategy;
-      const bool flat = g.sq8 == nullptr && g.ivfpq == nullptr;
+      const bool flat = g.sq8 == nullptr && g.ivfpq == nullptr && g.pqflat == nullptr;
       if (strat == VDBG_STRATEGY_AUTO) {  // :70-80
         const double sv = std::max(sel, 1e-9);
         const double graph_cost = 10.0 * double(std::max(P.ef, k)) / sv;
@@ -189,7 +190,14 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
                           uint32_t* ids, float* dd, size_t ef) -> int {
     const vdbg_segment& g = segs[p];
     const size_t rows = g.rows->d.n;
-    if (g.ivfpq != nullptr) {
+    if (g.pqflat != nullptr) {  // PqFlatIndex::search (ivf_pq.cc:59-79)
+      VDBG_RETURN_IF_ERROR(vdbg_pqflat_search_device(g.pqflat, q, nq, kk, P.rerank, allow, ids, dd,
+                                                     static_cast<uint64_t*>(dcb.p), s));
+      VDBG_HIP(hipMemcpyAsync(dch.data(), dcb.p, nq * 8, hipMemcpyDeviceToHost, s));
+      VDBG_HIP(hipStreamSynchronize(s));
+      if (dist_comps != nullptr)
+        for (size_t i = 0; i < nq; ++i) dist_comps[i] += dch[i];
+    } else if (g.ivfpq != nullptr) {
       VDBG_RETURN_IF_ERROR(vdbg_ivfpq_search_device(g.ivfpq, q, nq, kk, nprobe, P.rerank, allow,
                                                     ids, dd, static_cast<uint64_t*>(dcb.p), s));
       VDBG_HIP(hipMemcpyAsync(dch.data(), dcb.p, nq * 8, hipMemcpyDeviceToHost, s));

@@ -485,6 +485,18 @@ int PqTrainGpu(Ctx* c, const float* data, size_t n, size_t stride, size_t dim, s
   return kOk;
 }
 
+// ProductQuantizer::train with IndexOptions' k-means settings (MakeKMeansOptions,
+// ivf_pq.cc:21-26), for callers outside this file (PqFlatIndex::build).
+int PqTrainRows(Ctx* c, const float* data, size_t n, size_t stride, size_t dim, size_t m,
+                uint64_t seed, size_t max_points, size_t iters, std::vector<float>* centroids,
+                hipStream_t s) {
+  KMeansOpts ko;
+  ko.seed = seed;
+  ko.max_points = max_points;
+  ko.iters = iters;
+  return PqTrainGpu(c, data, n, stride, dim, m, ko, centroids, s);
+}
+
 // IvfPqIndex::build (ivf_pq.cc:102-149).
 int IvfBuildGpu(Ctx* c, IvfIndex* x, size_t nlist_req, size_t m, uint64_t seed, size_t max_points,
                 size_t iters, hipStream_t s) {

@@ -23,37 +23,6 @@ namespace vdbg {
 
 constexpr int kKsub = 256;
 
-__device__ __forceinline__ float dot_any(const float* a, const float* b, int d) {
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  int i = 0;
-  for (; i + 4 <= d; i += 4) {
-    s0 += a[i] * b[i];
-    s1 += a[i + 1] * b[i + 1];
-    s2 += a[i + 2] * b[i + 2];
-    s3 += a[i + 3] * b[i + 3];
-  }
-  for (; i < d; ++i) s0 += a[i] * b[i];
-  return (s0 + s1) + (s2 + s3);
-}
-
-__device__ __forceinline__ float l2sq_any(const float* a, const float* b, int d) {
-  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
-  int i = 0;
-  for (; i + 4 <= d; i += 4) {
-    const float t0 = a[i] - b[i], t1 = a[i + 1] - b[i + 1];
-    const float t2 = a[i + 2] - b[i + 2], t3 = a[i + 3] - b[i + 3];
-    s0 += t0 * t0;
-    s1 += t1 * t1;
-    s2 += t2 * t2;
-    s3 += t3 * t3;
-  }
-  for (; i < d; ++i) {
-    const float t = a[i] - b[i];
-    s0 += t * t;
-  }
-  return (s0 + s1) + (s2 + s3);
-}
-
 __device__ __forceinline__ bool row_ok(const uint64_t* w, uint32_t r) {
   return w == nullptr || ((w[r >> 6] >> (r & 63)) & 1ull);
 }

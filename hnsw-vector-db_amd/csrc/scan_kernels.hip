@@ -1519,6 +1519,9 @@ static int ExactScan(Ctx* c, Workspace& w, const ScanSource& src, const float* Q
   if (pow2_e(k) > 4) return SetError(kNotSupported, "k > 256 is not supported on the GPU path");
   if (src.kind == 0)
     return ExactScanT(c, w, src, FlatOf(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+  if (src.kind == 2)
+    return ExactScanT(c, w, src, PqScorer{src.C, src.pq_m}, Q, qlist, nslots, k, allow, out_ids,
+                      out_d, s);
   return ExactScanT(c, w, src, Sq8Of(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
 }
 
@@ -1598,6 +1601,20 @@ static void GemmGrid(GemmArgs& ga, int nqt, int nchunks, int* blocks) {
   ga.items = nqt * nchunks;
   ga.per_xcd = (ga.items + 7) / 8;
   *blocks = ga.per_xcd * 8;
+}
+
+int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t kk,
+              const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+  c->last_fallbacks = 0;
+  c->last_gemm_bits = 0;
+  if (nq == 0 || kk == 0) return kOk;
+  if (src.N == 0) {
+    k_fill_empty<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, out_d, nq * kk);
+    VDBG_HIP(hipGetLastError());
+    return kOk;
+  }
+  if (kk > 240) return ExactScanAll(c, src, Q, nq, kk, allow, out_ids, out_d, s);
+  return ExactScan(c, c->ws, src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
 }
 
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,

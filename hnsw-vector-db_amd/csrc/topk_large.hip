@@ -114,10 +114,12 @@ static int ExactAllT(Ctx* c, const ScanSource& src, const Scorer& sc, const floa
 int ExactScanAll(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t kk,
                  const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
   if (nq == 0 || kk == 0) return kOk;
-  if (kk > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
+  if (kk > (size_t(1) << 30)) return SetError(kInvalidArgument, "too many results per query");
   if (src.kind == 0)
     return ExactAllT(c, src, FlatScorer{src.X, src.pd, src.metric, c->kset}, Q, nq, kk, allow,
                      out_ids, out_d, s);
+  if (src.kind == 2)
+    return ExactAllT(c, src, PqScorer{src.C, src.pq_m}, Q, nq, kk, allow, out_ids, out_d, s);
   return ExactAllT(c, src, Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric, c->kset}, Q,
                    nq, kk, allow, out_ids, out_d, s);
 }

@@ -321,6 +321,60 @@ __device__ __forceinline__ float sq8_exact_k(int kset, int metric, const float* 
 }
 
 // Exact scorers: the reference's distance of query q to row `row` under kernel set kset.
+// DotAny / L2SqAny (src/distance/scalar.cc:43-73): four accumulators over i mod 4,
+// (s0 + s1) + (s2 + s3), products rounded before the add.
+__device__ __forceinline__ float dot_any(const float* a, const float* b, int d) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int i = 0;
+  for (; i + 4 <= d; i += 4) {
+    s0 += a[i] * b[i];
+    s1 += a[i + 1] * b[i + 1];
+    s2 += a[i + 2] * b[i + 2];
+    s3 += a[i + 3] * b[i + 3];
+  }
+  for (; i < d; ++i) s0 += a[i] * b[i];
+  return (s0 + s1) + (s2 + s3);
+}
+
+__device__ __forceinline__ float l2sq_any(const float* a, const float* b, int d) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int i = 0;
+  for (; i + 4 <= d; i += 4) {
+    const float t0 = a[i] - b[i], t1 = a[i + 1] - b[i + 1];
+    const float t2 = a[i + 2] - b[i + 2], t3 = a[i + 3] - b[i + 3];
+    s0 += t0 * t0;
+    s1 += t1 * t1;
+    s2 += t2 * t2;
+    s3 += t3 * t3;
+  }
+  for (; i < d; ++i) {
+    const float t = a[i] - b[i];
+    s0 += t * t;
+  }
+  return (s0 + s1) + (s2 + s3);
+}
+
+// ProductQuantizer::adc (src/index/quant/pq.h:36-46) of row `row`'s code against a query's
+// table (m x 256 floats, the "query" pointer the scans hand the scorer): four accumulators
+// over j mod 4.
+struct PqScorer {
+  const uint8_t* codes;  // n x m
+  int m;
+  __device__ __forceinline__ float operator()(const float* table, uint32_t row) const {
+    const uint8_t* cd = codes + size_t(row) * m;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    int j = 0;
+    for (; j + 4 <= m; j += 4) {
+      s0 += table[(j + 0) * 256 + cd[j + 0]];
+      s1 += table[(j + 1) * 256 + cd[j + 1]];
+      s2 += table[(j + 2) * 256 + cd[j + 2]];
+      s3 += table[(j + 3) * 256 + cd[j + 3]];
+    }
+    for (; j < m; ++j) s0 += table[j * 256 + cd[j]];
+    return (s0 + s1) + (s2 + s3);
+  }
+};
+
 struct FlatScorer {
   const float* X;
   int pd, metric, kset;

@@ -132,9 +132,12 @@ struct Ctx {
 };
 
 // What an exhaustive scan reads: fp32 rows (kind 0, flat) or SQ8 codes (kind 1), the
-// GEMM-form row norms, and a bit-reversed strided sample of rows built on first use.
+// GEMM-form row norms, and a bit-reversed strided sample of rows built on first use; or PQ
+// codes (kind 2, scored by ADC against per-query tables of pd = m x 256 floats, ScoreScan
+// only).
 struct ScanSource {
   int kind = 0;
+  int pq_m = 0;                 // kind 2: bytes per code
   const float* X = nullptr;     // kind 0: n x pd rows
   const uint16_t* X16 = nullptr;  // rows as fp16 for the fp16 GEMM (gemm16.hip), or null:
                                   // kind 0 integer rows exactly (x16_parts 1), kind 0 float
@@ -237,7 +240,29 @@ struct IvfIndex {
   std::vector<uint32_t> off_h;
 };
 
+// PqFlatIndex (src/index/quant/ivf_pq.h:12-36) made resident: the PQ codebook and every
+// row's code, scanned in full by ADC against per-query tables.
+struct PqFlatIndex {
+  Dataset* ds = nullptr;   // the segment's rows (Rerank reads them)
+  int m = 0, dsub = 0;
+  float* cen = nullptr;    // m x 256 x dsub (device)
+  uint8_t* codes = nullptr;  // n x m
+  std::vector<float> cen_h;
+  bool trained = false;    // false for an index built over no rows (no codebook)
+};
+
 // ---------------------------------------------------------------- launchers
+
+// ProductQuantizer::train (pq.cc:14-41) of n device rows at `stride` on the GPU's k-means,
+// with IndexOptions' seed and sample cap and `iters` Lloyd iterations.
+int PqTrainRows(Ctx* c, const float* data, size_t n, size_t stride, size_t dim, size_t m,
+                uint64_t seed, size_t max_points, size_t iters, std::vector<float>* centroids,
+                hipStream_t s);
+// ProductQuantizer::encode (pq.cc:43-57) of n rows, of their residuals against
+// coarse[assign] when coarse is not null.
+int PqEncode(Ctx* c, const float* X, uint32_t n, int pd, int dim, const float* coarse,
+             const uint32_t* assign, const float* cen, int m, int dsub, uint8_t* codes,
+             hipStream_t s);
 
 int LaunchRowStats(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd,
                    float* norms, RowStats* out);
@@ -267,6 +292,10 @@ int MakeRows8Split(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
             Workspace* ws = nullptr, Workspace* ws2 = nullptr);
+// Top-kk by the source's exact score without a ranking GEMM: every allowed row scored, wave
+// top-k per row split then a merge (kk <= 240), or a segmented sort (kk up to 10,000).
+int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t kk,
+              const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
 // Sets up the allocation-free flat search's scratch on `device` (its address there), once per
 // device; called by vdbg_ctx_create with the device current (noalloc.hip).
 int InitNoAllocScratch(int device);
@@ -383,4 +412,7 @@ struct vdbg_sq8 {
 };
 struct vdbg_ivfpq {
   vdbg::IvfIndex x;
+};
+struct vdbg_pqflat {
+  vdbg::PqFlatIndex p;
 };

@@ -99,6 +99,15 @@ _SIGS = {
     "vdbg_sq8_hnsw_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp,
                                               _vp, _vp]),
     "vdbg_ctx_set_host_threads": (C.c_int, [_vp, C.c_int]),
+    "vdbg_pqflat_build": (C.c_int, [_vp, _sz, C.c_uint64, _sz, _sz, C.POINTER(_vp)]),
+    "vdbg_pqflat_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
+    "vdbg_pqflat_save": (C.c_int, [_vp, _vp, _sz, C.POINTER(_sz)]),
+    "vdbg_pqflat_destroy": (C.c_int, [_vp]),
+    "vdbg_pqflat_info": (C.c_int, [_vp, C.POINTER(_sz), _vp]),
+    "vdbg_pqflat_codes": (C.c_int, [_vp, _vp]),
+    "vdbg_pqflat_search_host": (C.c_int, [_vp, _vp, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp]),
+    "vdbg_pqflat_search_device": (C.c_int, [_vp, _vp, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp,
+                                            _vp]),
     "vdbg_host_sq8_distance": (C.c_float, [C.c_char_p, C.c_int, _vp, _vp, _vp, _vp, _sz,
                                            C.c_int]),
     "vdbg_ivfpq_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
@@ -519,6 +528,70 @@ class IvfPqIndex:
                                             ids_ptr, dists_ptr, dc_ptr, stream))
 
 
+class PqFlatIndex:
+    """A PQ-flat index resident in HBM (vdbg_pqflat): PqFlatIndex built on the GPU or loaded
+    from a VDBPQFL1 file."""
+
+    def __init__(self, ds, h):
+        self.ds, self.h = ds, h
+        ds._children.add(self)
+
+    @classmethod
+    def build(cls, ds, m, seed=42, max_points=256, iters=25):
+        h = _vp()
+        _check(lib.vdbg_pqflat_build(ds.h, m, seed, max_points, iters, C.byref(h)))
+        return cls(ds, h)
+
+    @classmethod
+    def load(cls, ds, blob):
+        blob = bytes(blob)
+        h = _vp()
+        _check(lib.vdbg_pqflat_load(ds.h, blob, len(blob), C.byref(h)))
+        return cls(ds, h)
+
+    def close(self):
+        if self.h:
+            lib.vdbg_pqflat_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def save(self):
+        n = _sz()
+        _check(lib.vdbg_pqflat_save(self.h, None, 0, C.byref(n)))
+        buf = C.create_string_buffer(n.value)
+        _check(lib.vdbg_pqflat_save(self.h, buf, n.value, C.byref(n)))
+        return buf.raw[:n.value]
+
+    def codes(self):
+        m = _sz()
+        _check(lib.vdbg_pqflat_info(self.h, C.byref(m), None))
+        out = np.empty((self.ds.n, m.value), np.uint8)
+        _check(lib.vdbg_pqflat_codes(self.h, _ptr(out)))
+        return out
+
+    def search(self, queries, k, rerank=-1, allow=None):
+        q = np.ascontiguousarray(queries, np.float32)
+        nq = q.shape[0]
+        ids = np.empty((nq, k), np.uint32)
+        dists = np.empty((nq, k), np.float32)
+        dc = np.empty(nq, np.uint64)
+        if allow is not None:
+            allow = np.ascontiguousarray(allow, np.uint64)
+        _check(lib.vdbg_pqflat_search_host(self.h, _ptr(q), nq, k, rerank, _ptr(allow),
+                                           _ptr(ids), _ptr(dists), _ptr(dc)))
+        return ids, dists, dc
+
+    def search_device(self, q_ptr, nq, k, rerank, ids_ptr, dists_ptr, allow_ptr=None,
+                      dc_ptr=None, stream=None):
+        _check(lib.vdbg_pqflat_search_device(self.h, q_ptr, nq, k, rerank, allow_ptr, ids_ptr,
+                                             dists_ptr, dc_ptr, stream))
+
+
 class SearchParams(C.Structure):
     """SearchParams (include/vdb/options.h:59-67), vdbg_search_params."""
     _fields_ = [("ef", _sz), ("nprobe", _sz), ("rerank", C.c_int), ("strategy", C.c_int),
@@ -537,7 +610,7 @@ PLANS = ["index", "empty", "prefilter_exact", "filtered_index",
 
 class _Segment(C.Structure):
     _fields_ = [("rows", _vp), ("sq8", _vp), ("ivfpq", _vp), ("deleted_words", _vp),
-                ("filter_words", _vp)]
+                ("filter_words", _vp), ("pqflat", _vp)]
 
 
 def collection_search(ctx, segments, dim, metric, queries, k, params=None):
@@ -554,11 +627,12 @@ def collection_search(ctx, segments, dim, metric, queries, k, params=None):
     for i, (ds, ix, deleted, filt) in enumerate(segments):
         sq = ix.h if isinstance(ix, Sq8Index) else None
         iv = ix.h if isinstance(ix, IvfPqIndex) else None
+        pf = ix.h if isinstance(ix, PqFlatIndex) else None
         dw = None if deleted is None else np.ascontiguousarray(deleted, np.uint64)
         fw = None if filt is None else np.ascontiguousarray(filt, np.uint64)
         keep += [dw, fw]
         arr[i] = _Segment(ds.h, sq, iv, None if dw is None else dw.ctypes.data,
-                          None if fw is None else fw.ctypes.data)
+                          None if fw is None else fw.ctypes.data, pf)
     ids = np.empty((nq, k), np.uint64)
     d = np.empty((nq, k), np.float32)
     dc = np.empty(nq, np.uint64)

@@ -386,6 +386,41 @@ int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
  * 0 (no GEMM: the exact scan ran). */
 int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 
+/* ---------------------------------------------------------------- PQ-flat */
+
+typedef struct vdbg_pqflat vdbg_pqflat;
+
+/* PqFlatIndex::build (src/index/quant/ivf_pq.cc:45-57): ProductQuantizer::train over every row
+ * (pq.cc:14-41: per subspace a strided sample of at most 256 x max_points_per_centroid rows,
+ * k-means seeded with seed + 7919 j) and every row encoded, on the GPU.  pq_m must divide the
+ * dimension (InvalidArgument otherwise, index.cc:27-29); dim / pq_m above 64 is NotSupported.
+ * vdb builds with kmeans_iters 25. */
+int vdbg_pqflat_build(vdbg_dataset* ds, size_t pq_m, uint64_t seed,
+                      size_t max_points_per_centroid, size_t kmeans_iters, vdbg_pqflat** out);
+/* LoadIndex of a VDBPQFL1 file (index.cc:38-87) and PqFlatIndex::load (ivf_pq.cc:89-98):
+ * the codebook and the codes made resident as they are.  Errors: 5 (corruption) for a bad
+ * file, with the reference's messages. */
+int vdbg_pqflat_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_pqflat** out);
+/* PqFlatIndex::save (ivf_pq.cc:81-87): the VDBPQFL1 file; *len its size, written to buf
+ * when cap allows (ResourceExhausted otherwise; buf NULL asks for the size). */
+int vdbg_pqflat_save(vdbg_pqflat* ix, void* buf, size_t cap, size_t* len);
+int vdbg_pqflat_destroy(vdbg_pqflat* ix);
+/* *m, and the m x 256 x (dim / m) codebook floats when centroids_out is not NULL. */
+int vdbg_pqflat_info(vdbg_pqflat* ix, size_t* m, float* centroids_out);
+/* Copies the n x m code bytes to the host. */
+int vdbg_pqflat_codes(vdbg_pqflat* ix, uint8_t* codes_out);
+/* PqFlatIndex::search (ivf_pq.cc:59-79): every allowed row's code scored by ADC against the
+ * query's table (compute_table, pq.cc:63-73; adc, pq.h:36-46), the max(depth, k) best by
+ * (ADC, id), then FinishSearch (:28-36) with depth = rerank < 0 ? max(10 k, 100) : rerank:
+ * the float Rerank to k, or with depth 0 the k best by ADC.  dist_comps (nullable, nq):
+ * rows + the candidates reranked. */
+int vdbg_pqflat_search_host(vdbg_pqflat* ix, const float* queries, size_t nq, size_t k,
+                            int rerank, const uint64_t* allow_words, uint32_t* out_ids,
+                            float* out_dists, uint64_t* dist_comps);
+int vdbg_pqflat_search_device(vdbg_pqflat* ix, const float* queries, size_t nq, size_t k,
+                              int rerank, const uint64_t* allow_words, uint32_t* out_ids,
+                              float* out_dists, uint64_t* dist_comps, void* stream);
+
 /* ---------------------------------------------------------------- collection search */
 
 /* One disk segment of a collection snapshot as CollectionImpl::Search reads it
@@ -401,6 +436,7 @@ typedef struct vdbg_segment {
   const uint64_t* filter_words;   /* host, nullable: the request's filter evaluated on this
                                      segment (SegmentColumns::Evaluate, planner.cc:64) as
                                      words; NULL = the request has no filter */
+  vdbg_pqflat* pqflat;            /* or a PQ-flat index (at most one of sq8, ivfpq, pqflat) */
 } vdbg_segment;
 
 /* FilterStrategy (include/vdb/options.h:57). */

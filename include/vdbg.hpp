@@ -661,8 +661,8 @@ inline std::string JoinPath(const std::string& a, const std::string& b) {
 // on the device: vectors.f32 (header and CRC checks, the rows uploaded), ids.u64 (kept on
 // the host and resident for the merge), the index file (LoadIndex by magic, index.cc:38-87:
 // VDBFLAT1 needs nothing more, VDBHSQ81 brings its SQ8 codes and its graph, walked on the
-// host with the rerank on the GPU, VDBIVFP1 its lists; a float-row HNSW index and PQ-flat
-// are NotSupported) and the persisted delete set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
+// host with the rerank on the GPU, VDBIVFP1 its lists, VDBPQFL1 its codebook and codes; a
+// float-row HNSW index is NotSupported) and the persisted delete set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
 // the reference's Corruption messages, prefixed with the file or directory.
 class GpuSegment {
  public:
@@ -723,6 +723,7 @@ class GpuSegment {
   ~GpuSegment() {
     if (sq8_) vdbg_sq8_destroy(sq8_);
     if (ivf_) vdbg_ivfpq_destroy(ivf_);
+    if (pqf_) vdbg_pqflat_destroy(pqf_);
   }
 
   uint32_t id() const { return id_; }
@@ -746,6 +747,7 @@ class GpuSegment {
   vdbg_dataset* dataset() const { return ds_.get(); }
   vdbg_sq8* sq8() const { return sq8_; }
   vdbg_ivfpq* ivfpq() const { return ivf_; }
+  vdbg_pqflat* pqflat() const { return pqf_; }
 
   static Status ReadFile(const std::string& path, std::string* out) {
     detail::MappedFile f;
@@ -776,8 +778,12 @@ class GpuSegment {
       type_ = IndexType::IvfPq;
       return Status::FromCall(vdbg_ivfpq_load(ds_.get(), bytes.data(), bytes.size(), &ivf_));
     }
-    if (magic == "VDBHNSW1" || magic == "VDBPQFL1")
-      return Status(VDBG_NOT_SUPPORTED, "graph and PQ-flat index files are searched on the CPU");
+    if (magic == "VDBPQFL1") {
+      type_ = IndexType::PqFlat;
+      return Status::FromCall(vdbg_pqflat_load(ds_.get(), bytes.data(), bytes.size(), &pqf_));
+    }
+    if (magic == "VDBHNSW1")
+      return Status(VDBG_NOT_SUPPORTED, "float-row HNSW index files are searched on the CPU");
     return Status(VDBG_CORRUPTION, "unknown index file magic");
   }
 
@@ -788,6 +794,7 @@ class GpuSegment {
   detail::DatasetPtr ds_;
   vdbg_sq8* sq8_ = nullptr;
   vdbg_ivfpq* ivf_ = nullptr;
+  vdbg_pqflat* pqf_ = nullptr;
   std::vector<VectorId> ids_;
   std::vector<uint64_t> deleted_;
   size_t deleted_count_ = 0;
@@ -814,6 +821,7 @@ inline Status SearchCollection(Device& dev, std::span<const GpuSegment* const> s
     v[i].rows = g.dataset();
     v[i].sq8 = g.sq8();
     v[i].ivfpq = g.ivfpq();
+    v[i].pqflat = g.pqflat();
     v[i].deleted_words = g.deleted_count() > 0 ? g.deleted_words().data() : nullptr;
     v[i].filter_words = filters != nullptr ? (*filters)[i]->words() : nullptr;
   }

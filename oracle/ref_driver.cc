@@ -219,6 +219,50 @@ int ref_hnsw_sq8_search_batch(int metric, const char* file, size_t file_len, con
   return 0;
 }
 
+// PqFlatIndex::build + save (src/index/quant/ivf_pq.cc:45-57, 81-87) through CreateIndex
+// (index.cc:16-36): the VDBPQFL1 file.  Returns its size (0 on failure); writes it when it
+// fits in cap bytes.
+size_t ref_pqflat_file(int metric, const float* base, size_t rows, size_t dim, size_t pd,
+                       size_t m, uint64_t seed, size_t max_points, char* buf, size_t cap) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::PqFlat;
+  o.pq_m = m;
+  o.seed = seed;
+  o.max_train_points_per_centroid = max_points;
+  auto idx = CreateIndex(o, static_cast<Metric>(metric), v);
+  if (!idx.ok() || !(*idx)->build(nullptr).ok()) return 0;
+  StringSink sink;
+  if (!(*idx)->save(sink).ok()) return 0;
+  if (buf != nullptr && sink.s.size() <= cap) std::memcpy(buf, sink.s.data(), sink.s.size());
+  return sink.s.size();
+}
+
+// LoadIndex of a VDBPQFL1 file and PqFlatIndex::search (ivf_pq.cc:59-79) per query.
+int ref_pqflat_search_batch(int metric, const char* file, size_t file_len, const float* base,
+                            size_t rows, size_t dim, size_t pd, const float* queries, size_t nq,
+                            size_t k, int rerank, const uint64_t* allow_words, float* od,
+                            uint32_t* oi, uint64_t* dc, int nthreads) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::PqFlat;
+  auto idx = LoadIndex(std::string_view(file, file_len), o, static_cast<Metric>(metric), v);
+  if (!idx.ok()) return 1;
+  const Index& ix = **idx;
+  SearchParams p;
+  p.rerank = rerank;
+  DenseFilter filt(allow_words);
+  ThreadPool pool(nthreads <= 0 ? 1 : static_cast<size_t>(nthreads));
+  pool.parallel_for(0, nq, [&](size_t qi) {
+    std::vector<Neighbor> out;
+    IndexSearchStats st;
+    ix.search(queries + qi * pd, k, p, allow_words != nullptr ? &filt : nullptr, out, &st);
+    WritePadded(out, k, od + qi * k, oi + qi * k);
+    if (dc != nullptr) dc[qi] = st.distance_computations;
+  });
+  return 0;
+}
+
 // SQ8 scan + rerank composed from the reference's parts (Sq8 kernel into TopK, Rerank).
 void ref_sq8_search_batch(const char* ks, int metric, const float* base, const uint8_t* codes,
                           size_t rows, size_t dim, size_t pd, const float* vmin,

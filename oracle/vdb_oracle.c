@@ -1235,3 +1235,82 @@ int or_hnsw_sq8_search_file(int kset, int metric, const uint8_t* file, size_t le
   or_hnsw_free(&g);
   return 0;
 }
+
+/* ------------------------------------------------------------------ PQ-flat search */
+
+typedef struct {
+  int kset, metric;
+  const float* base;
+  size_t rows, pd;
+  const float* cen;
+  size_t m, dsub;
+  const uint8_t* codes;
+  const float* queries;
+  size_t k;
+  int rerank;
+  const uint64_t* allow;
+  float* out_d;
+  uint32_t* out_id;
+  uint64_t* dc;
+} pqflat_ctx_t;
+
+/* PqFlatIndex::search (src/index/quant/ivf_pq.cc:59-79): compute_table, ADC of every allowed
+ * row into TopK(max(depth, k)), FinishSearch (:28-36) with RerankDepth (:16-19). */
+static void pqflat_task(void* p, size_t b, size_t e) {
+  pqflat_ctx_t* c = (pqflat_ctx_t*)p;
+  const size_t depth = c->rerank < 0 ? (10 * c->k > 100 ? 10 * c->k : 100) : (size_t)c->rerank;
+  const size_t cap = depth > c->k ? depth : c->k;
+  float* table = (float*)malloc(sizeof(float) * c->m * OR_KSUB);
+  topk_t t;
+  topk_init(&t, cap);
+  nb_t* s = (nb_t*)malloc(sizeof(nb_t) * (cap + 1));
+  uint32_t* ids = (uint32_t*)malloc(sizeof(uint32_t) * (cap + 1));
+  float* rd = (float*)malloc(sizeof(float) * (c->k + 1));
+  uint32_t* ri = (uint32_t*)malloc(sizeof(uint32_t) * (c->k + 1));
+  for (size_t qi = b; qi < e; ++qi) {
+    const float* q = c->queries + qi * c->pd;
+    float* od = c->out_d + qi * c->k;
+    uint32_t* oi = c->out_id + qi * c->k;
+    if (c->rows == 0 || c->k == 0) {
+      write_padded(s, 0, c->k, od, oi);
+      if (c->dc) c->dc[qi] = 0;
+      continue;
+    }
+    or_pq_compute_table(c->cen, c->m, c->dsub, q, c->metric == OR_METRIC_L2 ? 0 : 1, table);
+    t.n = 0;
+    for (size_t r = 0; r < c->rows; ++r) {
+      if (!row_allowed(c->allow, r)) continue;
+      topk_push(&t, or_pq_adc(table, c->m, c->codes + r * c->m), (uint32_t)r);
+    }
+    size_t m = topk_sorted(&t, s);
+    uint64_t dc = c->rows;
+    if (depth == 0) {
+      write_padded(s, m < c->k ? m : c->k, c->k, od, oi);
+    } else {
+      for (size_t i = 0; i < m; ++i) ids[i] = s[i].id;
+      size_t n2 = or_rerank(c->kset, c->metric, c->base, c->pd, q, ids, m, c->k, rd, ri);
+      dc += m;
+      for (size_t i = 0; i < c->k; ++i) {
+        od[i] = i < n2 ? rd[i] : INFINITY;
+        oi[i] = i < n2 ? ri[i] : UINT32_MAX;
+      }
+    }
+    if (c->dc) c->dc[qi] = dc;
+  }
+  free(ri);
+  free(rd);
+  free(ids);
+  free(s);
+  topk_free(&t);
+  free(table);
+}
+
+void or_pqflat_search_batch(int kset, int metric, const float* base, size_t rows, size_t pd,
+                            const float* pq_centroids, size_t m, size_t dsub,
+                            const uint8_t* codes, const float* queries, size_t nq, size_t k,
+                            int rerank, const uint64_t* allow_words, float* out_d,
+                            uint32_t* out_id, uint64_t* dist_comps, int nthreads) {
+  pqflat_ctx_t c = {kset, metric, base, rows, pd, pq_centroids, m, dsub, codes, queries, k,
+                    rerank, allow_words, out_d, out_id, dist_comps};
+  or_parallel(nq, nthreads, pqflat_task, &c);
+}

@@ -33,6 +33,8 @@
  *   normalize      compiled reference + closed form
  *   merge          closed form (sort by (dist, part, row), dedupe external id)
  *   crc32c         known answer 0xE3069283 for "123456789" (tests/distance_test.cc:94)
+ *   pq-flat        compiled reference (PqFlatIndex::search on files it built and saved)
+ *                  + closed form (rerank over every row equals exact flat search)
  *   hnsw-sq8       compiled reference (HnswSq8Index::search on files it built and saved)
  *                  + closed form (ef >= rows walks every node: equals exact flat search)
  */
@@ -141,6 +143,16 @@ size_t or_merge_parts(size_t nparts, size_t k, const float* part_d, const uint32
 int or_plan_segment(int has_filter, size_t rows, size_t deleted, size_t matches, int index_flat,
                     int strategy, size_t ef, size_t k, size_t nprobe,
                     size_t prefilter_threshold, size_t* nprobe_out);
+
+/* ---- PQ-flat search (src/index/quant/ivf_pq.cc:59-79) ----
+ * PqFlatIndex::search per query: ADC of every allowed row's code (rows x m bytes) against
+ * compute_table(q), TopK(max(depth, k)) with depth = rerank < 0 ? max(10 k, 100) : rerank,
+ * then Rerank (or the k best by ADC at depth 0).  dist_comps (nullable): rows + reranked. */
+void or_pqflat_search_batch(int kset, int metric, const float* base, size_t rows, size_t pd,
+                            const float* pq_centroids, size_t m, size_t dsub,
+                            const uint8_t* codes, const float* queries, size_t nq, size_t k,
+                            int rerank, const uint64_t* allow_words, float* out_d,
+                            uint32_t* out_id, uint64_t* dist_comps, int nthreads);
 
 /* ---- HNSW-SQ8 search (src/index/hnsw/hnsw_index.cc:82-100) ----
  * HnswSq8Index::search per query over a VDBHSQ81 file (quantizer, codes and graph read from

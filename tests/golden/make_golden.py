@@ -8,6 +8,8 @@ fixtures are data only (.npz without pickles): inputs and expected outputs.
 
     python3 tests/golden/make_golden.py            # every fixture
     python3 tests/golden/make_golden.py segment    # segment.npz only
+    python3 tests/golden/make_golden.py hnsw       # hnsw.npz only
+    python3 tests/golden/make_golden.py pqflat     # pqflat.npz only
 """
 import ctypes as C
 import os
@@ -181,6 +183,7 @@ def main():
                         crc_blob=np.frombuffer(blobs[2], np.uint8).copy(), crc=crc)
     make_segment(L)
     make_hnsw(L)
+    make_pqflat(L)
     print("golden fixtures written to", HERE)
 
 
@@ -270,8 +273,49 @@ def make_hnsw(L):
     np.savez_compressed(os.path.join(HERE, "hnsw.npz"), **out)
 
 
+def make_pqflat(L):
+    """pqflat.npz: VDBPQFL1 files the reference's PqFlatIndex::build + save wrote over seeded
+    rows, and its PqFlatIndex::search results on them (ids, distances, distance
+    computations) per (k, rerank) setting, without a filter and with one allowing ~40 %."""
+    from oracle_lib import Reference
+    R = Reference()
+    rng = np.random.default_rng(20261203)
+    out = {}
+    settings = np.array([(10, -1), (5, 0), (20, 50), (1, -1), (30, -1), (10, 3)], np.int64)
+    for tag, n, dim, m, metric in [("a", 2000, 32, 8, "l2"), ("b", 1200, 24, 6, "ip"),
+                                   ("c", 800, 48, 12, "cosine")]:
+        pd = (dim + 15) // 16 * 16
+        base = np.zeros((n, pd), np.float32)
+        # values on a 1/32 grid keep the fixture small (they compress); cosine rows are
+        # normalised below and are not
+        base[:, :dim] = np.rint(rng.standard_normal((n, dim)) * 32) / 32
+        q = np.zeros((24, pd), np.float32)
+        q[:, :dim] = np.rint(rng.standard_normal((24, dim)) * 32) / 32
+        if metric == "cosine":
+            base /= np.linalg.norm(base, axis=1, keepdims=True)
+            q /= np.linalg.norm(q, axis=1, keepdims=True)
+        f = R.pqflat_file(base, dim, m, metric)
+        out[f"{tag}_rows"], out[f"{tag}_q"], out[f"{tag}_file"] = base, q, np.frombuffer(f, np.uint8).copy()
+        out[f"{tag}_dim"], out[f"{tag}_metric"] = np.int32(dim), np.array(metric)
+        allow = _words(rng.random(n) < 0.4)
+        out[f"{tag}_allow"] = allow
+        for fi, aw in enumerate((None, allow)):
+            for si, (k, rr) in enumerate(settings):
+                od, oi, dc = R.pqflat_search(f, base, dim, q, int(k), int(rr), metric, aw)
+                key = f"{tag}_f{fi}_s{si}"
+                out[key + "_d"], out[key + "_i"], out[key + "_dc"] = od, oi, dc
+    out["settings"] = settings
+    out["kernels"] = np.array(R.lib.ref_best_kernels().decode())
+    np.savez_compressed(os.path.join(HERE, "pqflat.npz"), **out)
+
+
 if __name__ == "__main__":
-    if sys.argv[1:] == ["hnsw"]:
+    if sys.argv[1:] == ["pqflat"]:
+        ref = load_reference()
+        if ref is None:
+            sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+        make_pqflat(ref.lib)
+    elif sys.argv[1:] == ["hnsw"]:
         ref = load_reference()
         if ref is None:
             sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")

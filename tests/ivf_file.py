@@ -94,3 +94,19 @@ def synth_ivfpq(base, dim, nlist, m, seed=0, metric="l2"):
     list_ids = [order[bounds[l]:bounds[l + 1]].astype(np.uint32) for l in range(nlist)]
     list_codes = [codes[ids] for ids in list_ids]
     return write_ivfpq(n, pd, coarse, dim, m, cen, list_ids, list_codes)
+
+
+def parse_pqflat(blob):
+    """A VDBPQFL1 file (src/index/quant/ivf_pq.cc:81-87): magic, u64 rows, the product
+    quantizer (u32 dim, u32 m, m x 256 x dim/m fp32), rows x m code bytes, CRC32C footer."""
+    blob = bytes(blob)
+    assert blob[:8] == b"VDBPQFL1", blob[:8]
+    rows, dim, m = struct.unpack_from("<QII", blob, 8)
+    p = 24
+    dsub = dim // m
+    cen = np.frombuffer(blob, np.float32, m * 256 * dsub, p).copy()
+    p += m * 256 * dsub * 4
+    codes = np.frombuffer(blob, np.uint8, rows * m, p).reshape(rows, m).copy()
+    p += rows * m
+    assert p == len(blob) - 4, (p, len(blob))
+    return {"rows": rows, "dim": dim, "m": m, "pq_centroids": cen, "codes": codes}

@@ -77,6 +77,9 @@ class Oracle:
         _sig(lib, "or_plan_segment", C.c_int,
              [C.c_int, sz, sz, sz, C.c_int, C.c_int, sz, sz, sz, sz, C.POINTER(C.c_size_t)])
         _sig(lib, "or_crc32c", C.c_uint32, [C.c_uint32, C.c_char_p, sz])
+        _sig(lib, "or_pqflat_search_batch", None,
+             [C.c_int, C.c_int, f32p, sz, sz, f32p, sz, sz, u8p, f32p, sz, sz, C.c_int,
+              _opt(u64p), f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "or_hnsw_sq8_search_file", C.c_int,
              [C.c_int, C.c_int, C.c_char_p, sz, f32p, sz, sz, f32p, sz, sz, sz, C.c_int,
               _opt(u64p), f32p, u32p, _opt(u64p), C.c_int])
@@ -120,6 +123,21 @@ class Oracle:
                                      depth, allow, od, oi, threads)
         return od, oi
 
+
+    def pqflat_search(self, ix, base, queries, k, rerank=-1, metric="l2", allow=None,
+                      kset="avx512", threads=8):
+        """PqFlatIndex::search over an index parsed with ivf_file.parse_pqflat."""
+        base = np.ascontiguousarray(base, np.float32)
+        queries = np.ascontiguousarray(queries, np.float32)
+        nq, pd = queries.shape
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.uint32)
+        dc = np.empty(nq, np.uint64)
+        self.lib.or_pqflat_search_batch(KSET[kset], METRIC[metric], base, base.shape[0], pd,
+                                        ix["pq_centroids"], ix["m"], ix["dim"] // ix["m"],
+                                        ix["codes"], queries, nq, k, rerank, allow, od, oi, dc,
+                                        threads)
+        return od, oi, dc
 
     def hnsw_sq8_search(self, file, base, queries, k, ef=64, rerank=-1, metric="l2",
                         allow=None, kset="avx512", threads=8):
@@ -167,7 +185,7 @@ class Oracle:
         "hnsw_sq8" | "ivf", deleted / filter (dense words or None); sq8 (the GPU's exhaustive
         SQ8 scan index, built from rows, no graph): codes, vmin, scale; hnsw_sq8 (vdb's
         HnswSq8Index): file (the VDBHSQ81 bytes); ivf: ix (parsed VDBIVFP1) and term2 (or
-        None).  Returns (ext ids, dists, dist comps, plan names)."""
+        None); pqflat: pq (a parsed VDBPQFL1).  Returns (ext ids, dists, dist comps, plan names)."""
         nq = raw.shape[0]
         pd = (dim + 15) // 16 * 16
         q = np.zeros((nq, pd), np.float32)
@@ -218,6 +236,9 @@ class Oracle:
                                             nprobe, prefilter_threshold, C.byref(npb))
 
             def index_search(kk, allow, ef_=ef):
+                if sg["kind"] == "pqflat":
+                    return self.pqflat_search(sg["pq"], base, q, kk, rerank, metric, allow,
+                                              kset=kset)
                 if sg["kind"] == "hnsw_sq8":
                     od, oi, dc = self.hnsw_sq8_search(sg["file"], base, q, kk, ef_, rerank,
                                                       metric=metric, allow=allow, kset=kset)
@@ -332,6 +353,11 @@ class Reference:
         _sig(lib, "ref_crc32c", C.c_uint32, [C.c_char_p, sz])
         _sig(lib, "ref_hnsw_sq8_file", sz,
              [C.c_int, f32p, sz, sz, sz, sz, sz, C.c_uint64, C.c_void_p, sz])
+        _sig(lib, "ref_pqflat_file", sz,
+             [C.c_int, f32p, sz, sz, sz, sz, C.c_uint64, sz, C.c_void_p, sz])
+        _sig(lib, "ref_pqflat_search_batch", C.c_int,
+             [C.c_int, C.c_char_p, sz, f32p, sz, sz, sz, f32p, sz, sz, C.c_int, _opt(u64p),
+              f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "ref_hnsw_sq8_search_batch", C.c_int,
              [C.c_int, C.c_char_p, sz, f32p, sz, sz, sz, f32p, sz, sz, sz, C.c_int, _opt(u64p),
               f32p, u32p, _opt(u64p), C.c_int])
@@ -362,6 +388,33 @@ class Reference:
         if rc != 0:
             raise ValueError("a query was rejected by PrepareQuery")
         return oe, od
+
+    def pqflat_file(self, base, dim, m, metric="l2", seed=42, max_points=256):
+        base = np.ascontiguousarray(base, np.float32)
+        n, pd = base.shape
+        size = self.lib.ref_pqflat_file(METRIC[metric], base, n, dim, pd, m, seed, max_points,
+                                        None, 0)
+        if size == 0:
+            raise RuntimeError("ref_pqflat_file failed")
+        buf = C.create_string_buffer(size)
+        self.lib.ref_pqflat_file(METRIC[metric], base, n, dim, pd, m, seed, max_points, buf, size)
+        return buf.raw
+
+    def pqflat_search(self, file, base, dim, queries, k, rerank=-1, metric="l2", allow=None,
+                      threads=8):
+        base = np.ascontiguousarray(base, np.float32)
+        queries = np.ascontiguousarray(queries, np.float32)
+        nq, pd = queries.shape
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.uint32)
+        dc = np.empty(nq, np.uint64)
+        file = bytes(file)
+        rc = self.lib.ref_pqflat_search_batch(METRIC[metric], file, len(file), base,
+                                              base.shape[0], dim, pd, queries, nq, k, rerank,
+                                              allow, od, oi, dc, threads)
+        if rc != 0:
+            raise ValueError("LoadIndex refused the file")
+        return od, oi, dc
 
     def hnsw_sq8_search(self, file, base, dim, queries, k, ef=64, rerank=-1, metric="l2",
                         allow=None, threads=8):

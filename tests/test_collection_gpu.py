@@ -282,3 +282,47 @@ def test_hnsw_sq8_segment_is_the_references(ctx, oracle):
         sq.close()
         for d_, _ in handles:
             d_.close()
+
+
+def test_pqflat_segment(ctx, oracle):
+    """A PQ-flat segment (VDBPQFL1, built on the GPU) next to a flat one, with deletes,
+    filters and the planner's strategies, against the oracle's composition."""
+    from ivf_file import parse_pqflat
+    dim = 32
+    pd = vdbg.padded_dim(dim)
+    segs, handles = [], []
+    for i, (n, kind) in enumerate([(6000, "pqflat"), (2500, "flat")]):
+        base = datagen.pad(datagen.uniform_rows(n, dim, 930 + i) * 10, pd)
+        ext = np.arange(n, dtype=np.uint64) * 11 + 100000 * (i + 1)
+        ds = vdbg.Dataset(ctx, base, dim)
+        ds.set_external_ids(ext)
+        sg = {"base": base, "ext": ext, "kind": kind, "deleted": _mask(n, 0.03, 940 + i),
+              "filter": None}
+        ix = None
+        if kind == "pqflat":
+            ix = vdbg.PqFlatIndex.build(ds, 8, seed=5)
+            sg["pq"] = parse_pqflat(ix.save())
+        segs.append(sg)
+        handles.append((ds, ix))
+    print("collection pq-flat segment", flush=True)
+    raw = _queries(20, 950)[:, :dim].copy()
+    try:
+        for filt, kw in ((None, {}), (None, {"rerank": 0}), ("f", {"prefilter_threshold": 500}),
+                         ("f", {"strategy": "post_filter", "post_filter_alpha": 3}),
+                         (None, {"rerank": 40})):
+            for i, sg in enumerate(segs):
+                sg["filter"] = None if filt is None else _mask(sg["base"].shape[0], 0.5, 960 + i)
+            gi, gd, gdc, gp = vdbg.collection_search(
+                ctx, [(d_, ix, sg["deleted"], sg["filter"]) for (d_, ix), sg in zip(handles, segs)],
+                dim, "l2", raw, 10, vdbg.SearchParams(**kw))
+            okw = dict(kw)
+            okw["strategy"] = vdbg.STRATEGIES[okw.get("strategy", "auto")]
+            oi, od, odc, op = oracle.collection_search(segs, dim, "l2", raw, 10, **okw)
+            assert gp == op, (filt, kw)
+            assert np.array_equal(gi, oi) and np.array_equal(gd.view(np.uint32), od.view(np.uint32)), (filt, kw)
+            assert np.array_equal(gdc, odc), (filt, kw)
+    finally:
+        for d_, ix in handles:
+            if ix is not None:
+                ix.close()
+            d_.close()

@@ -528,3 +528,55 @@ def test_hnsw_sq8_matches_reference_random(oracle, reference):
                                                     kset=reference.lib.ref_best_kernels().decode())
                 assert np.array_equal(oi, ri) and np.array_equal(bits(od), bits(rd))
                 assert np.array_equal(dc, rdc)
+
+
+# ------------------------------------------------------------------ PQ-flat search
+
+def test_pqflat_matches_golden(oracle):
+    from ivf_file import parse_pqflat
+    g = gold("pqflat")
+    ks = str(g["kernels"])
+    for tag in ("a", "b", "c"):
+        ix = parse_pqflat(g[f"{tag}_file"].tobytes())
+        rows, q, metric = g[f"{tag}_rows"], g[f"{tag}_q"], str(g[f"{tag}_metric"])
+        for fi, allow in enumerate((None, g[f"{tag}_allow"])):
+            for si, (k, rr) in enumerate(g["settings"]):
+                od, oi, dc = oracle.pqflat_search(ix, rows, q, int(k), int(rr), metric, allow,
+                                                  kset=ks)
+                key = f"{tag}_f{fi}_s{si}"
+                assert np.array_equal(oi, g[key + "_i"]), key
+                assert np.array_equal(bits(od), bits(g[key + "_d"])), key
+                assert np.array_equal(dc, g[key + "_dc"]), key
+
+
+def test_pqflat_full_rerank_equals_flat(oracle):
+    """Closed form: a rerank depth of at least the row count re-scores every row exactly."""
+    from ivf_file import parse_pqflat
+    g = gold("pqflat")
+    for tag in ("a", "b", "c"):
+        ix = parse_pqflat(g[f"{tag}_file"].tobytes())
+        rows, q, metric = g[f"{tag}_rows"], g[f"{tag}_q"], str(g[f"{tag}_metric"])
+        n = rows.shape[0]
+        od, oi, dc = oracle.pqflat_search(ix, rows, q, 10, n, metric)
+        fd, fi = oracle.flat_search(rows, q, 10, metric=metric)
+        assert np.array_equal(oi, fi) and np.array_equal(bits(od), bits(fd)), tag
+        assert (dc == 2 * n).all()
+
+
+def test_pqflat_matches_reference_random(oracle, reference):
+    from ivf_file import parse_pqflat
+    rng = np.random.default_rng(21)
+    for n, dim, m, metric in ((900, 32, 8, "l2"), (700, 20, 5, "ip")):
+        pd = (dim + 15) // 16 * 16
+        base = np.zeros((n, pd), np.float32)
+        base[:, :dim] = rng.uniform(-2, 3, (n, dim))
+        f = reference.pqflat_file(base, dim, m, metric, seed=7)
+        ix = parse_pqflat(f)
+        q = np.zeros((20, pd), np.float32)
+        q[:, :dim] = rng.uniform(-2, 3, (20, dim))
+        for k, rr in ((10, -1), (4, 0), (12, 30)):
+            rd, ri, rdc = reference.pqflat_search(f, base, dim, q, k, rr, metric)
+            od, oi, dc = oracle.pqflat_search(ix, base, q, k, rr, metric,
+                                              kset=reference.lib.ref_best_kernels().decode())
+            assert np.array_equal(oi, ri) and np.array_equal(bits(od), bits(rd))
+            assert np.array_equal(dc, rdc)
