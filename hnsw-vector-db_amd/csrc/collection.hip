@@ -92,6 +92,8 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
       return SetError(kInvalidArgument, "segment dim or metric differs from the collection's");
     if (int(g.sq8 != nullptr) + int(g.ivfpq != nullptr) + int(g.pqflat != nullptr) > 1)
       return SetError(kInvalidArgument, "a segment has one index: sq8, ivfpq or pqflat");
+    if (g.memory_part && (g.sq8 != nullptr || g.ivfpq != nullptr || g.pqflat != nullptr))
+      return SetError(kInvalidArgument, "an in-memory part has no index");
     if ((g.sq8 != nullptr && g.sq8->q.ds != &d) || (g.ivfpq != nullptr && g.ivfpq->x.ds != &d) ||
         (g.pqflat != nullptr && g.pqflat->p.ds != &d))
       return SetError(kInvalidArgument, "index does not belong to the segment's rows");
@@ -114,6 +116,24 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     const size_t live = rows - std::min(rows, deleted);
     SegPlan& sp = plan[p];
     sp.nprobe = P.nprobe;
+    if (g.memory_part) {
+      // SearchMutable (planner.cc:131-151): MutableSegment::Search scores every row that is
+      // not deleted and matches the filter (mutable_segment.cc:46-64)
+      sp.plan = g.filter_words != nullptr ? VDBG_PLAN_SCAN_FILTER : VDBG_PLAN_SCAN;
+      if (g.filter_words != nullptr || deleted > 0) {
+        sp.allow.assign(nw, ~uint64_t(0));
+        if (g.filter_words != nullptr)
+          for (size_t i = 0; i < nw; ++i) sp.allow[i] &= g.filter_words[i];
+        if (deleted > 0)
+          for (size_t i = 0; i < nw; ++i) sp.allow[i] &= ~g.deleted_words[i];
+        if (rows % 64 && nw > 0) sp.allow[nw - 1] &= (uint64_t(1) << (rows % 64)) - 1;
+        sp.matches = CountRows(sp.allow.data(), rows);
+      } else {
+        sp.matches = rows;
+      }
+      allow_words_total += sp.allow.size();
+      continue;
+    }
     if (g.filter_words == nullptr) {
       sp.plan = VDBG_PLAN_INDEX;  // :56-62, DeleteFilter when rows are deleted
       if (deleted > 0) {
@@ -244,6 +264,12 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     float* dd = static_cast<float*>(hits_d.p) + p * slice;
     const uint64_t* allow = sp.allow.empty() ? nullptr : static_cast<const uint64_t*>(allow_dev.p) + allow_at[p];
     switch (sp.plan) {
+      case VDBG_PLAN_SCAN:
+      case VDBG_PLAN_SCAN_FILTER:
+        VDBG_RETURN_IF_ERROR(vdbg_flat_search_device(segs[p].rows, q, nq, k, allow, ids, dd, s));
+        if (dist_comps != nullptr)
+          for (size_t i = 0; i < nq; ++i) dist_comps[i] += sp.matches;
+        break;
       case VDBG_PLAN_INDEX:
         VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd, P.ef));
         break;

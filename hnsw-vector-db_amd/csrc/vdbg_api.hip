@@ -555,6 +555,135 @@ int vdbg_dataset_create_device(vdbg_ctx* ctx, const float* rows_dev, size_t n, s
   return CreateDataset(ctx, rows_dev, true, n, dim, padded_dim, metric, out);
 }
 
+// MutableSegment (src/engine/mutable_segment.cc:10-40): an empty dataset whose rows arrive
+// by vdbg_dataset_append.  Capacity is reserved up front and doubles when exceeded.
+int vdbg_dataset_create_appendable(vdbg_ctx* ctx, size_t dim, size_t pd, int metric,
+                                   size_t capacity, vdbg_dataset** out) {
+  if (ctx == nullptr || out == nullptr) return SetError(kInvalidArgument, "null argument");
+  VDBG_RETURN_IF_ERROR(CheckDims(dim, pd));
+  if (metric < 0 || metric > 2) return SetError(kInvalidArgument, "unknown metric");
+  if (capacity > 0xfffffffeull) return SetError(kInvalidArgument, "more rows than InternalId holds");
+  Ctx* c = &ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  auto* ds = new (std::nothrow) vdbg_dataset;
+  if (ds == nullptr) return SetError(kResourceExhausted, "out of host memory");
+  Dataset& d = ds->d;
+  d.ctx = c;
+  d.n = 0;
+  d.dim = dim;
+  d.pd = pd;
+  d.metric = metric;
+  d.appendable = true;
+  d.cap = std::max<size_t>(capacity, 1024);
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&d.rows), d.cap * pd * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d.norms), d.cap * sizeof(float));
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&d.ext_ids), d.cap * 8);
+  if (e != hipSuccess) {
+    (void)hipFree(d.rows);
+    (void)hipFree(d.norms);
+    (void)hipFree(d.ext_ids);
+    delete ds;
+    return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                    std::string("appendable dataset: ") + hipGetErrorString(e));
+  }
+  d.src.kind = 0;
+  d.src.X = d.rows;
+  d.src.rn = d.norms;
+  d.src.N = 0;
+  d.src.pd = int(pd);
+  d.src.metric = metric;
+  ++c->live_datasets;
+  *out = ds;
+  return kOk;
+}
+
+// MutableSegment::Append (mutable_segment.cc:24-44) for n rows at once: the rows (n x pd,
+// host), their external ids (host, nullable: left unset), published together when the call
+// returns.  *first_row (nullable) receives the row number of the first.
+int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uint64_t* ext_ids,
+                        uint64_t* first_row) {
+  if (ds == nullptr || (n > 0 && rows == nullptr)) return SetError(kInvalidArgument, "null argument");
+  Dataset& d = ds->d;
+  if (!d.appendable)
+    return SetError(kFailedPrecondition, "rows are appended only to a dataset made by "
+                                         "vdbg_dataset_create_appendable");
+  if (d.live_indexes > 0)
+    return SetError(kFailedPrecondition, "an appendable dataset with an index takes no rows");
+  if (d.n + n > 0xfffffffeull) return SetError(kResourceExhausted, "mutable segment is full");
+  Ctx* c = d.ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
+  VDBG_HIP(hipSetDevice(c->device));
+  hipStream_t s = c->stream;
+  if (first_row != nullptr) *first_row = d.n;
+  if (n == 0) return kOk;
+  if (d.n + n > d.cap) {  // grow: every search queued on any stream finishes first
+    const size_t cap = std::max(2 * d.cap, d.n + n);
+    float *nr = nullptr, *nn = nullptr;
+    uint64_t* ne = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&nr), cap * d.pd * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&nn), cap * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ne), cap * 8);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess && d.n > 0)
+      e = hipMemcpyAsync(nr, d.rows, d.n * d.pd * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess && d.n > 0)
+      e = hipMemcpyAsync(nn, d.norms, d.n * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess && d.n > 0)
+      e = hipMemcpyAsync(ne, d.ext_ids, d.n * 8, hipMemcpyDeviceToDevice, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+      (void)hipFree(nr);
+      (void)hipFree(nn);
+      (void)hipFree(ne);
+      return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                      std::string("append: ") + hipGetErrorString(e));
+    }
+    (void)hipFree(d.rows);
+    (void)hipFree(d.norms);
+    (void)hipFree(d.ext_ids);
+    d.rows = nr;
+    d.norms = nn;
+    d.ext_ids = ne;
+    d.cap = cap;
+  }
+  float* at = d.rows + d.n * d.pd;
+  VDBG_HIP(hipMemcpyAsync(at, rows, n * d.pd * sizeof(float), hipMemcpyHostToDevice, s));
+  if (ext_ids != nullptr)
+    VDBG_HIP(hipMemcpyAsync(d.ext_ids + d.n, ext_ids, n * 8, hipMemcpyHostToDevice, s));
+  RowStats st;
+  VDBG_RETURN_IF_ERROR(LaunchRowStats(c, s, at, n, d.pd, d.norms + d.n, &st));
+  if (d.n == 0) {
+    d.stats = st;
+  } else {
+    d.stats.lo = std::min(d.stats.lo, st.lo);
+    d.stats.hi = std::max(d.stats.hi, st.hi);
+    d.stats.max_abs = std::max(d.stats.max_abs, st.max_abs);
+    d.stats.xn_max = std::max(d.stats.xn_max, st.xn_max);
+    d.stats.all_int = d.stats.all_int & st.all_int;
+  }
+  d.n += n;
+  d.src.X = d.rows;
+  d.src.rn = d.norms;
+  d.src.N = uint32_t(d.n);
+  d.src.stats = d.stats;
+  d.src.rmag = d.stats.xn_max;
+  // the threshold sample follows the rows (any rows of the set give a valid threshold; a
+  // fresh one keeps it tight)
+  if (d.src.Sbuf != nullptr) VDBG_HIP(hipDeviceSynchronize());  // searches may read it
+  FreeSample(&d.src);
+  if (d.n >= 1024 && GemmSupported(d.pd)) VDBG_RETURN_IF_ERROR(BuildSample(c, &d.src, s));
+  VDBG_HIP(hipStreamSynchronize(s));
+  return kOk;
+}
+
+int vdbg_dataset_size(vdbg_dataset* ds, uint64_t* rows) {
+  if (ds == nullptr || rows == nullptr) return SetError(kInvalidArgument, "null argument");
+  std::lock_guard<std::recursive_mutex> g(ds->d.ctx->mu);
+  *rows = ds->d.n;
+  return kOk;
+}
+
 int vdbg_dataset_destroy(vdbg_dataset* ds) {
   if (ds == nullptr) return kOk;
   Ctx* c = ds->d.ctx;

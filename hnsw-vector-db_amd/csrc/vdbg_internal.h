@@ -191,6 +191,10 @@ struct Dataset {
   ScanSource src;          // the flat scan's view of these rows
   int live_indexes = 0;    // SQ8 / IVF-PQ indexes over these rows not yet destroyed (ctx mu)
   uint64_t* ext_ids = nullptr;  // n external ids (device) for the collection merge, or null
+  // appendable datasets (vdb's MutableSegment): rows, norms and external ids are reserved
+  // for cap rows and grow in place; no fp16 / int8 copies are kept
+  bool appendable = false;
+  size_t cap = 0;
 };
 
 // SQ8 codes of a dataset's rows (HnswSq8Index's codes_ and Sq8Quantizer,

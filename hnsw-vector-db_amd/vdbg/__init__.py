@@ -99,6 +99,9 @@ _SIGS = {
     "vdbg_sq8_hnsw_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp,
                                               _vp, _vp]),
     "vdbg_ctx_set_host_threads": (C.c_int, [_vp, C.c_int]),
+    "vdbg_dataset_create_appendable": (C.c_int, [_vp, _sz, _sz, C.c_int, _sz, C.POINTER(_vp)]),
+    "vdbg_dataset_append": (C.c_int, [_vp, _vp, _sz, _vp, C.POINTER(C.c_uint64)]),
+    "vdbg_dataset_size": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
     "vdbg_pqflat_build": (C.c_int, [_vp, _sz, C.c_uint64, _sz, _sz, C.POINTER(_vp)]),
     "vdbg_pqflat_load": (C.c_int, [_vp, C.c_char_p, _sz, C.POINTER(_vp)]),
     "vdbg_pqflat_save": (C.c_int, [_vp, _vp, _sz, C.POINTER(_sz)]),
@@ -270,6 +273,36 @@ class Dataset:
         self._children = weakref.WeakSet()
         ctx._children.add(self)
         return self
+
+    @classmethod
+    def appendable(cls, ctx, dim, metric="l2", capacity=1024):
+        """An empty dataset that takes rows by append (vdb's MutableSegment)."""
+        self = cls.__new__(cls)
+        h = _vp()
+        pd = padded_dim(dim)
+        _check(lib.vdbg_dataset_create_appendable(ctx.h, dim, pd, METRICS[metric], capacity,
+                                                  C.byref(h)))
+        self.ctx, self.h, self.n, self.dim, self.pd = ctx, h, 0, dim, pd
+        self.metric = metric
+        self._children = weakref.WeakSet()
+        ctx._children.add(self)
+        return self
+
+    def append(self, rows, ext_ids=None):
+        """MutableSegment::Append of rows (n x padded_dim) and their external ids; returns
+        the first new row's number."""
+        rows = np.ascontiguousarray(rows, np.float32)
+        assert rows.ndim == 2 and rows.shape[1] == self.pd
+        if ext_ids is not None:
+            ext_ids = np.ascontiguousarray(ext_ids, np.uint64)
+            assert ext_ids.shape == (rows.shape[0],)
+        first = C.c_uint64()
+        _check(lib.vdbg_dataset_append(self.h, _ptr(rows), rows.shape[0], _ptr(ext_ids),
+                                       C.byref(first)))
+        n = C.c_uint64()
+        _check(lib.vdbg_dataset_size(self.h, C.byref(n)))
+        self.n = n.value
+        return first.value
 
     @classmethod
     def open_vectors(cls, ctx, data, dim, metric="l2", rows=None, verify_crc=True):
@@ -605,18 +638,19 @@ class SearchParams(C.Structure):
 
 STRATEGIES = {"auto": 0, "prefilter": 1, "graph": 2, "post_filter": 3}
 PLANS = ["index", "empty", "prefilter_exact", "filtered_index",
-         "filtered_index+exact_fallback", "post_filter"]
+         "filtered_index+exact_fallback", "post_filter", "scan", "scan_filter"]
 
 
 class _Segment(C.Structure):
     _fields_ = [("rows", _vp), ("sq8", _vp), ("ivfpq", _vp), ("deleted_words", _vp),
-                ("filter_words", _vp), ("pqflat", _vp)]
+                ("filter_words", _vp), ("pqflat", _vp), ("memory_part", C.c_int)]
 
 
 def collection_search(ctx, segments, dim, metric, queries, k, params=None):
     """CollectionImpl::SearchBatch over disk segments (vdbg_collection_search_host).
-    segments: (dataset, index or None, deleted words or None, filter words or None) per
-    segment, each dataset with its external ids set.  Returns (external ids uint64 [nq, k],
+    segments: (dataset, index or None, deleted words or None, filter words or None[,
+    memory part]) per segment, each dataset with its external ids set; a true fifth entry
+    marks an in-memory part (the active or a frozen mutable segment), which vdb lists first.  Returns (external ids uint64 [nq, k],
     dists float32 [nq, k], distance computations per query, plan name per segment)."""
     params = params or SearchParams()
     q = np.ascontiguousarray(queries, np.float32)
@@ -624,7 +658,9 @@ def collection_search(ctx, segments, dim, metric, queries, k, params=None):
     assert q.shape[1] == dim
     keep = []
     arr = (_Segment * max(len(segments), 1))()
-    for i, (ds, ix, deleted, filt) in enumerate(segments):
+    for i, seg in enumerate(segments):
+        ds, ix, deleted, filt = seg[:4]
+        memory = bool(seg[4]) if len(seg) > 4 else False
         sq = ix.h if isinstance(ix, Sq8Index) else None
         iv = ix.h if isinstance(ix, IvfPqIndex) else None
         pf = ix.h if isinstance(ix, PqFlatIndex) else None
@@ -632,7 +668,7 @@ def collection_search(ctx, segments, dim, metric, queries, k, params=None):
         fw = None if filt is None else np.ascontiguousarray(filt, np.uint64)
         keep += [dw, fw]
         arr[i] = _Segment(ds.h, sq, iv, None if dw is None else dw.ctypes.data,
-                          None if fw is None else fw.ctypes.data, pf)
+                          None if fw is None else fw.ctypes.data, pf, 1 if memory else 0)
     ids = np.empty((nq, k), np.uint64)
     d = np.empty((nq, k), np.float32)
     dc = np.empty(nq, np.uint64)

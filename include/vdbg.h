@@ -386,6 +386,25 @@ int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
  * 0 (no GEMM: the exact scan ran). */
 int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 
+/* ---------------------------------------------------------------- mutable segments */
+
+/* MutableSegment (src/engine/mutable_segment.cc:10-64): an empty dataset that takes rows by
+ * vdbg_dataset_append, with room reserved for `capacity` rows (doubling when exceeded).  It
+ * is searched like any dataset (vdbg_flat_search_*: the exact top k over the allowed rows, as
+ * MutableSegment::Search) and joins a collection search as an in-memory part.  It keeps no
+ * fp16 / int8 copies, and takes no index. */
+int vdbg_dataset_create_appendable(vdbg_ctx* ctx, size_t dim, size_t padded_dim, int metric,
+                                   size_t capacity, vdbg_dataset** out);
+/* MutableSegment::Append (mutable_segment.cc:24-44) of n rows (n x padded_dim floats, host)
+ * and their external ids (host, nullable), published together when the call returns (later
+ * searches see them; rows never move for readers of earlier calls).  *first_row (nullable)
+ * receives the first new row's number.  FailedPrecondition for a dataset not made appendable
+ * or one with an index. */
+int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uint64_t* ext_ids,
+                        uint64_t* first_row);
+/* The dataset's row count. */
+int vdbg_dataset_size(vdbg_dataset* ds, uint64_t* rows);
+
 /* ---------------------------------------------------------------- PQ-flat */
 
 typedef struct vdbg_pqflat vdbg_pqflat;
@@ -437,6 +456,12 @@ typedef struct vdbg_segment {
                                      segment (SegmentColumns::Evaluate, planner.cc:64) as
                                      words; NULL = the request has no filter */
   vdbg_pqflat* pqflat;            /* or a PQ-flat index (at most one of sq8, ivfpq, pqflat) */
+  int memory_part;                /* 1: an in-memory part (the active or a frozen mutable
+                                     segment, MutableSegment::Search through SearchMutable,
+                                     planner.cc:131-151): every row not deleted and matching
+                                     the filter is scored exactly, no planner, no index.
+                                     In-memory parts come first in the array, as in vdb's
+                                     snapshot order (active, frozen, then disk). */
 } vdbg_segment;
 
 /* FilterStrategy (include/vdb/options.h:57). */
@@ -466,7 +491,9 @@ enum {
   VDBG_PLAN_PREFILTER_EXACT = 2,
   VDBG_PLAN_FILTERED_INDEX = 3,
   VDBG_PLAN_FILTERED_INDEX_EXACT_FALLBACK = 4,
-  VDBG_PLAN_POST_FILTER = 5
+  VDBG_PLAN_POST_FILTER = 5,
+  VDBG_PLAN_SCAN = 6,        /* an in-memory part without a filter (SearchMutable "scan") */
+  VDBG_PLAN_SCAN_FILTER = 7  /* an in-memory part under a filter ("scan_filter") */
 };
 
 /* Makes the segment's external ids (ids.u64, n entries, host) resident for the collection

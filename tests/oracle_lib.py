@@ -185,7 +185,8 @@ class Oracle:
         "hnsw_sq8" | "ivf", deleted / filter (dense words or None); sq8 (the GPU's exhaustive
         SQ8 scan index, built from rows, no graph): codes, vmin, scale; hnsw_sq8 (vdb's
         HnswSq8Index): file (the VDBHSQ81 bytes); ivf: ix (parsed VDBIVFP1) and term2 (or
-        None); pqflat: pq (a parsed VDBPQFL1).  Returns (ext ids, dists, dist comps, plan names)."""
+        None); pqflat: pq (a parsed VDBPQFL1); memory: an in-memory part (the active or a
+        frozen mutable segment, listed first), scanned exactly.  Returns (ext ids, dists, dist comps, plan names)."""
         nq = raw.shape[0]
         pd = (dim + 15) // 16 * 16
         q = np.zeros((nq, pd), np.float32)
@@ -197,7 +198,7 @@ class Oracle:
                 if self.lib.or_normalize(q[i], dim) != 1:
                     raise ValueError("a zero query cannot be normalized for cosine")
         names = ["index", "empty", "prefilter_exact", "filtered_index",
-                 "filtered_index+exact_fallback", "post_filter"]
+                 "filtered_index+exact_fallback", "post_filter", "scan", "scan_filter"]
 
         def count(words, n):
             bits = np.unpackbits(np.ascontiguousarray(words, np.uint64).view(np.uint8),
@@ -230,6 +231,24 @@ class Oracle:
                     bm &= ~np.asarray(deleted, np.uint64)
                 bm = clip(bm, n)
                 matches = count(bm, n)
+            if sg["kind"] == "memory":
+                # SearchMutable (planner.cc:131-151) -> MutableSegment::Search
+                # (mutable_segment.cc:46-64): the rows not deleted and matching the filter,
+                # exactly, counted as distance computations
+                allow = None
+                if filt is not None or ndel > 0:
+                    allow = np.full((n + 63) // 64, np.iinfo(np.uint64).max, np.uint64)
+                    if filt is not None:
+                        allow &= np.asarray(filt, np.uint64)
+                    if ndel > 0:
+                        allow &= ~np.asarray(deleted, np.uint64)
+                    allow = clip(allow, n)
+                matches = n if allow is None else count(allow, n)
+                od, oi = self.flat_search(base, q, k, metric=metric, kset=kset, allow=allow)
+                pdist[p], prow[p] = od, oi
+                dcs += np.uint64(matches)
+                plans.append(names[7 if filt is not None else 6])
+                continue
             npb = C.c_size_t()
             plan = self.lib.or_plan_segment(1 if filt is not None else 0, n, ndel, matches,
                                             1 if sg["kind"] == "flat" else 0, strategy, ef, k,
