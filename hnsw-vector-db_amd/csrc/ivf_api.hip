@@ -10,27 +10,7 @@
 
 namespace vdbg {
 
-struct IvfScanArgs {
-  const float* Q;
-  int pd, dim, m, dsub, metric;
-  const float* coarse;
-  const float* cen;
-  const uint32_t* off;
-  const uint32_t* ids;
-  const uint8_t* codes;
-  const float* term2;
-  const float* qtab;
-  const uint32_t* probe;
-  const float* probe_d;
-  int nprobe, nq;
-  const uint64_t* allow;
-  int R;
-  uint32_t* out_ids;
-  float* out_d;
-  uint64_t* dc;
-  uint64_t dc_base;
-  int count_top;
-};
+
 int IvfTerm2(Ctx* c, const float* coarse, int nlist, int pd, const float* cen, int m, int dsub,
              float* term2, hipStream_t s);
 int IvfQtab(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,

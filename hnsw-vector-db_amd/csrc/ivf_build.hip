@@ -161,6 +161,28 @@ __global__ __launch_bounds__(256) void k_assign_any(const float* __restrict__ x,
   if (dist != nullptr) dist[p] = best;
 }
 
+// The same for rows too wide to stage (d > 64): rows and centroids read where they lie.
+__global__ __launch_bounds__(256) void k_assign_wide(const float* __restrict__ x, uint32_t n,
+                                                     int d, int stride,
+                                                     const float* __restrict__ cen, int k,
+                                                     uint32_t* __restrict__ assign,
+                                                     float* __restrict__ dist) {
+  const uint32_t p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= n) return;
+  const float* xr = x + size_t(p) * stride;
+  float best = __builtin_inff();
+  uint32_t arg = 0;
+  for (int c = 0; c < k; ++c) {
+    const float v = l2sq_any(xr, cen + size_t(c) * d, d);
+    if (v < best) {
+      best = v;
+      arg = uint32_t(c);
+    }
+  }
+  assign[p] = arg;
+  if (dist != nullptr) dist[p] = best;
+}
+
 __global__ void k_iota(uint32_t* v, uint32_t n) {
   const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) v[i] = i;
@@ -251,11 +273,15 @@ int AssignNearestGpu(Ctx* c, const float* x, size_t n, size_t d, size_t stride, 
     vdbg_dataset_destroy(cds);
     return rc;
   }
-  if (d > 64) return SetError(kNotSupported, "AssignNearest: unpadded rows of more than 64 dims");
   const size_t lds = k * d * sizeof(float);
-  if (lds > 64 * 1024) return SetError(kNotSupported, "AssignNearest: centroids exceed LDS");
   ProfScope ps(c, "assign_any", s);
   const dim3 grid(unsigned((n + 255) / 256));
+  if (d > 64 || lds > 64 * 1024) {
+    k_assign_wide<<<grid, 256, 0, s>>>(x, uint32_t(n), int(d), int(stride), cen, int(k), assign,
+                                       dist);
+    VDBG_HIP(hipGetLastError());
+    return kOk;
+  }
 #define VDBG_ASSIGN(DD) k_assign_any<DD><<<grid, 256, lds, s>>>(x, uint32_t(n), int(d), int(stride), cen, int(k), assign, dist)
   switch (d) {
     case 4: VDBG_ASSIGN(4); break;

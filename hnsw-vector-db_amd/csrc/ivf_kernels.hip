@@ -55,27 +55,18 @@ __global__ void k_ivf_qtab(const float* __restrict__ Q, int pd, int nq,
   qtab[e] = twice ? v * 2.f : v;
 }
 
-struct IvfScanArgs {
-  const float* Q;
-  int pd, dim, m, dsub, metric;
-  const float* coarse;
-  const float* cen;
-  const uint32_t* off;     // nlist + 1
-  const uint32_t* ids;     // CSR row ids
-  const uint8_t* codes;    // CSR codes, m bytes per row
-  const float* term2;      // nullable
-  const float* qtab;       // [nq][m*256]: 2*(-<q_j,C>) (L2 with term2) or -<q_j,C> (IP)
-  const uint32_t* probe;   // [nq][nprobe] list ids, nearest first
-  const float* probe_d;    // [nq][nprobe] coarse distances
-  int nprobe, nq;
-  const uint64_t* allow;
-  int R;                   // TopK capacity max(depth, k)
-  uint32_t* out_ids;       // [nq][R]
-  float* out_d;
-  uint64_t* dc;            // [nq] distance computations (nullable)
-  uint64_t dc_base;        // nlist: the coarse distances
-  int count_top;           // add the candidates handed to Rerank
-};
+
+
+// table[j * 256 + c] of probed list l for query q, computed where it is needed: the same
+// float operations as the table the reference builds per list (ivf_pq.cc:203-209).
+__device__ __forceinline__ float ivf_entry(const IvfScanArgs& a, const float* qv,
+                                           const float* qt, uint32_t l, int j, int c) {
+  const int e = j * 256 + c;
+  if (a.metric != 0) return qt[e];
+  if (a.term2 != nullptr) return a.term2[size_t(l) * a.m * 256 + e] + qt[e];
+  return l2sq_res_any(qv + size_t(j) * a.dsub, a.coarse + size_t(l) * a.pd + size_t(j) * a.dsub,
+                      a.cen + size_t(e) * a.dsub, a.dsub);
+}
 
 constexpr int kIvfWaves = 4;
 constexpr int kMaxTable = 32 * kKsub;  // m <= 32
@@ -91,8 +82,9 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
   const int q = blockIdx.x * kIvfWaves + wave;
   if (q >= a.nq) return;
   const int ts = a.m * kKsub;
-  float* table = lds + size_t(wave) * (ts + 2 * 2 * kWave);
-  float* st_d = table + ts;                                   // staging: 128 keys
+  const int tl = a.ondemand ? 0 : ts;  // table floats held in LDS
+  float* table = lds + size_t(wave) * (tl + 2 * 2 * kWave);
+  float* st_d = table + tl;                                   // staging: 128 keys
   uint32_t* st_i = reinterpret_cast<uint32_t*>(st_d + 2 * kWave);
   const float* qv = a.Q + size_t(q) * a.pd;
   const float* qt = a.qtab + size_t(q) * ts;
@@ -104,7 +96,7 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
   int staged = 0;
   uint64_t scanned = 0;
 
-  if (!l2) {  // the shared IP table
+  if (!l2 && !a.ondemand) {  // the shared IP table
     for (int e = lane; e < ts; e += kWave) table[e] = qt[e];
   }
   for (int pi = 0; pi < a.nprobe; ++pi) {
@@ -115,20 +107,21 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
     if (pre) {
       offset = a.probe_d[size_t(q) * a.nprobe + pi];
       const float* t2 = a.term2 + size_t(l) * ts;
-      for (int e = lane * 4; e < ts; e += kWave * 4) {
-        const float4 x = *reinterpret_cast<const float4*>(t2 + e);
-        const float4 y = *reinterpret_cast<const float4*>(qt + e);
-        *reinterpret_cast<float4*>(table + e) = make_float4(x.x + y.x, x.y + y.y, x.z + y.z,
-                                                            x.w + y.w);
-      }
+      if (!a.ondemand)
+        for (int e = lane * 4; e < ts; e += kWave * 4) {
+          const float4 x = *reinterpret_cast<const float4*>(t2 + e);
+          const float4 y = *reinterpret_cast<const float4*>(qt + e);
+          *reinterpret_cast<float4*>(table + e) = make_float4(x.x + y.x, x.y + y.y, x.z + y.z,
+                                                              x.w + y.w);
+        }
     } else if (l2) {
       // residual table: L2SqAny(q_j - c_l,j, C_j[c]) with the residual rounded per dim
-      for (int e = lane; e < ts; e += kWave) {
-        const int j = e / kKsub;
-        float r[64];
-        for (int t = 0; t < a.dsub; ++t) r[t] = qv[j * a.dsub + t] - cl[j * a.dsub + t];
-        table[e] = l2sq_any(r, a.cen + size_t(e) * a.dsub, a.dsub);
-      }
+      if (!a.ondemand)
+        for (int e = lane; e < ts; e += kWave) {
+          const int j = e / kKsub;
+          table[e] = l2sq_res_any(qv + j * a.dsub, cl + j * a.dsub, a.cen + size_t(e) * a.dsub,
+                                  a.dsub);
+        }
     } else {
       offset = -dot_any(qv, cl, a.dim);
     }
@@ -146,15 +139,18 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
         id = a.ids[i];
         if (row_ok(a.allow, id)) {
           const uint8_t* cd = a.codes + size_t(i) * a.m;
+          auto T = [&](int j) {
+            return a.ondemand ? ivf_entry(a, qv, qt, l, j, cd[j]) : table[j * kKsub + cd[j]];
+          };
           float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
           int j = 0;
           for (; j + 4 <= a.m; j += 4) {
-            s0 += table[(j + 0) * kKsub + cd[j + 0]];
-            s1 += table[(j + 1) * kKsub + cd[j + 1]];
-            s2 += table[(j + 2) * kKsub + cd[j + 2]];
-            s3 += table[(j + 3) * kKsub + cd[j + 3]];
+            s0 += T(j + 0);
+            s1 += T(j + 1);
+            s2 += T(j + 2);
+            s3 += T(j + 3);
           }
-          for (; j < a.m; ++j) s0 += table[j * kKsub + cd[j]];
+          for (; j < a.m; ++j) s0 += T(j);
           d = offset + ((s0 + s1) + (s2 + s3));
         } else {
           id = kNoId;
@@ -466,12 +462,10 @@ __global__ void k_pq_encode(const float* __restrict__ X, uint32_t n, int pd, int
   const int j = int(t - size_t(r) * m);
   const float* x = X + size_t(r) * pd + size_t(j) * dsub;
   const float* c = coarse != nullptr ? coarse + size_t(assign[r]) * pd + size_t(j) * dsub : nullptr;
-  float res[64];
-  for (int i = 0; i < dsub; ++i) res[i] = c != nullptr ? x[i] - c[i] : x[i];
   float best = __builtin_inff();
   int arg = 0;
   for (int k = 0; k < kKsub; ++k) {
-    const float d = l2sq_any(res, cen + (size_t(j) * kKsub + k) * dsub, dsub);
+    const float d = l2sq_res_any(x, c, cen + (size_t(j) * kKsub + k) * dsub, dsub);
     if (d < best) {
       best = d;
       arg = k;
@@ -524,10 +518,10 @@ static int launch_fast_m(int e, hipStream_t s, const IvfScanArgs& a, const IvfFa
   return kOk;
 }
 
-int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
-  if (a.nq == 0) return kOk;
-  if (a.m * kKsub > kMaxTable || a.dsub > 64)
-    return SetError(kNotSupported, "IVF-PQ scan: m <= 32 and dim/m <= 64 on the GPU path");
+int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
+  if (a_in.nq == 0) return kOk;
+  IvfScanArgs a = a_in;
+  a.ondemand = a.m * kKsub > kMaxTable ? 1 : 0;  // tables above 32 KB: entries per lookup
   int e = 1;
   while (kWave * e < a.R) e <<= 1;
   const bool l2 = a.metric == 0;
@@ -587,7 +581,7 @@ int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
     (void)hipFreeAsync(buf, s);
     return rc;
   }
-  const size_t lds = size_t(kIvfWaves) * (a.m * kKsub + 4 * kWave) * sizeof(float);
+  const size_t lds = size_t(kIvfWaves) * ((a.ondemand ? 0 : a.m * kKsub) + 4 * kWave) * sizeof(float);
   ProfScope ps(c, "ivf_scan", s);
   switch (e) {
     case 1: launch_ivf<1>(s, a, lds); break;
@@ -626,12 +620,12 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_score_all(IvfScanArgs a,
   if (qi >= nc) return;
   const int q = q0 + qi;
   const int ts = a.m * kKsub;
-  float* table = lds + size_t(wave) * ts;
+  float* table = lds + size_t(wave) * (a.ondemand ? 0 : ts);
   const float* qv = a.Q + size_t(q) * a.pd;
   const float* qt = a.qtab + size_t(q) * ts;
   const bool l2 = a.metric == 0;
   const bool pre = l2 && a.term2 != nullptr;
-  if (!l2)
+  if (!l2 && !a.ondemand)
     for (int e = lane; e < ts; e += kWave) table[e] = qt[e];
   int pos = seg[qi];
   for (int pi = 0; pi < a.nprobe; ++pi) {
@@ -642,14 +636,15 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_score_all(IvfScanArgs a,
     if (pre) {
       offset = a.probe_d[size_t(q) * a.nprobe + pi];
       const float* t2 = a.term2 + size_t(l) * ts;
-      for (int e = lane; e < ts; e += kWave) table[e] = t2[e] + qt[e];
+      if (!a.ondemand)
+        for (int e = lane; e < ts; e += kWave) table[e] = t2[e] + qt[e];
     } else if (l2) {
-      for (int e = lane; e < ts; e += kWave) {
-        const int j = e / kKsub;
-        float r[64];
-        for (int t = 0; t < a.dsub; ++t) r[t] = qv[j * a.dsub + t] - cl[j * a.dsub + t];
-        table[e] = l2sq_any(r, a.cen + size_t(e) * a.dsub, a.dsub);
-      }
+      if (!a.ondemand)
+        for (int e = lane; e < ts; e += kWave) {
+          const int j = e / kKsub;
+          table[e] = l2sq_res_any(qv + j * a.dsub, cl + j * a.dsub, a.cen + size_t(e) * a.dsub,
+                                  a.dsub);
+        }
     } else {
       offset = -dot_any(qv, cl, a.dim);
     }
@@ -664,15 +659,18 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_score_all(IvfScanArgs a,
         uint64_t key = kNoKey;
         if (row_ok(a.allow, id)) {
           const uint8_t* cd = a.codes + size_t(i) * a.m;
+          auto T = [&](int j) {
+            return a.ondemand ? ivf_entry(a, qv, qt, l, j, cd[j]) : table[j * kKsub + cd[j]];
+          };
           float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
           int j = 0;
           for (; j + 4 <= a.m; j += 4) {
-            s0 += table[(j + 0) * kKsub + cd[j + 0]];
-            s1 += table[(j + 1) * kKsub + cd[j + 1]];
-            s2 += table[(j + 2) * kKsub + cd[j + 2]];
-            s3 += table[(j + 3) * kKsub + cd[j + 3]];
+            s0 += T(j + 0);
+            s1 += T(j + 1);
+            s2 += T(j + 2);
+            s3 += T(j + 3);
           }
-          for (; j < a.m; ++j) s0 += table[j * kKsub + cd[j]];
+          for (; j < a.m; ++j) s0 += T(j);
           key = dist_key(offset + ((s0 + s1) + (s2 + s3)), id);
         }
         keys[pos + int(i - b)] = key;
@@ -695,10 +693,10 @@ __global__ void k_ivf_dc(const uint32_t* __restrict__ top_ids, int R, int nq,
 
 // The ADC scan for R > 256: every code scored into per-query key segments (chunks of at
 // most 2^25 keys), sorted, the first R kept in out_ids / out_d as the scan's TopK(R).
-int IvfScanDeep(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
-  if (a.nq == 0) return kOk;
-  if (a.m * kKsub > kMaxTable || a.dsub > 64)
-    return SetError(kNotSupported, "IVF-PQ scan: m <= 32 and dim/m <= 64 on the GPU path");
+int IvfScanDeep(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
+  if (a_in.nq == 0) return kOk;
+  IvfScanArgs a = a_in;
+  a.ondemand = a.m * kKsub > kMaxTable ? 1 : 0;
   const size_t nq = size_t(a.nq);
   uint64_t* cnt = nullptr;
   VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&cnt), nq * 8, s));
@@ -715,7 +713,7 @@ int IvfScanDeep(Ctx* c, const IvfScanArgs& a, hipStream_t s) {
   int* seg = nullptr;
   VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&keys), cap * 16 + 16, s));
   VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&seg), (nq + 1) * sizeof(int), s));
-  const size_t lds = size_t(kIvfWaves) * a.m * kKsub * sizeof(float);
+  const size_t lds = size_t(kIvfWaves) * (a.ondemand ? 0 : a.m * kKsub) * sizeof(float);
   int rc = kOk;
   std::vector<int> off;
   for (size_t q0 = 0; q0 < nq && rc == kOk;) {
@@ -765,7 +763,6 @@ int PqEncode(Ctx* c, const float* X, uint32_t n, int pd, int dim, const float* c
              hipStream_t s) {
   const size_t total = size_t(n) * m;
   if (total == 0) return kOk;
-  if (dsub > 64) return SetError(kNotSupported, "PQ encode: dim/m <= 64 on the GPU path");
   ProfScope ps(c, "pq_encode", s);
   k_pq_encode<<<dim3(unsigned((total + 255) / 256)), 256, 0, s>>>(X, n, pd, dim, coarse, assign,
                                                                  cen, m, dsub, codes);

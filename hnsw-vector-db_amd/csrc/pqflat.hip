@@ -162,7 +162,6 @@ int vdbg_pqflat_build(vdbg_dataset* ds, size_t pq_m, uint64_t seed,
   Dataset& d = ds->d;
   if (pq_m == 0 || d.dim % pq_m != 0)
     return SetError(kInvalidArgument, "pq_m must divide the dimension");  // index.cc:27-29
-  if (d.dim / pq_m > 64) return SetError(kNotSupported, "PQ-flat: dim / m <= 64 on the GPU path");
   Ctx* c = d.ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
@@ -232,7 +231,6 @@ int vdbg_pqflat_load(vdbg_dataset* ds, const void* file, size_t len, vdbg_pqflat
     return SetError(VDBG_CORRUPTION, mismatch);
   const uint8_t* codes = p;
   if (!take(nullptr, size_t(n) * m)) return SetError(VDBG_CORRUPTION, "truncated pq codes");
-  if (dsub > 64) return SetError(kNotSupported, "PQ-flat: dim / m <= 64 on the GPU path");
   Ctx* c = d.ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));

@@ -354,6 +354,30 @@ __device__ __forceinline__ float l2sq_any(const float* a, const float* b, int d)
   return (s0 + s1) + (s2 + s3);
 }
 
+// L2SqAny(r, b, d) of the residual r = q - c, each r_i rounded to fp32 as the reference
+// stores it before the call (ivf_pq.cc:207-208, 128-139); c null means r = q.
+__device__ __forceinline__ float l2sq_res_any(const float* q, const float* c, const float* b,
+                                              int d) {
+  float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+  int i = 0;
+  for (; i + 4 <= d; i += 4) {
+    const float r0 = c ? q[i] - c[i] : q[i], r1 = c ? q[i + 1] - c[i + 1] : q[i + 1];
+    const float r2 = c ? q[i + 2] - c[i + 2] : q[i + 2], r3 = c ? q[i + 3] - c[i + 3] : q[i + 3];
+    const float t0 = r0 - b[i], t1 = r1 - b[i + 1];
+    const float t2 = r2 - b[i + 2], t3 = r3 - b[i + 3];
+    s0 += t0 * t0;
+    s1 += t1 * t1;
+    s2 += t2 * t2;
+    s3 += t3 * t3;
+  }
+  for (; i < d; ++i) {
+    const float r = c ? q[i] - c[i] : q[i];
+    const float t = r - b[i];
+    s0 += t * t;
+  }
+  return (s0 + s1) + (s2 + s3);
+}
+
 // ProductQuantizer::adc (src/index/quant/pq.h:36-46) of row `row`'s code against a query's
 // table (m x 256 floats, the "query" pointer the scans hand the scorer): four accumulators
 // over j mod 4.

@@ -244,6 +244,30 @@ struct IvfIndex {
   std::vector<uint32_t> off_h;
 };
 
+// The IVF-PQ list scan of a batch (ivf_kernels.hip), as IvfSearch (ivf_api.hip) hands it over.
+struct IvfScanArgs {
+  const float* Q;
+  int pd, dim, m, dsub, metric;
+  const float* coarse;
+  const float* cen;
+  const uint32_t* off;     // nlist + 1
+  const uint32_t* ids;     // CSR row ids
+  const uint8_t* codes;    // CSR codes, m bytes per row
+  const float* term2;      // nullable
+  const float* qtab;       // [nq][m*256]: 2*(-<q_j,C>) (L2 with term2) or -<q_j,C> (IP)
+  const uint32_t* probe;   // [nq][nprobe] list ids, nearest first
+  const float* probe_d;    // [nq][nprobe] coarse distances
+  int nprobe, nq;
+  const uint64_t* allow;
+  int R;                   // TopK capacity max(depth, k)
+  uint32_t* out_ids;       // [nq][R]
+  float* out_d;
+  uint64_t* dc;            // [nq] distance computations (nullable)
+  uint64_t dc_base;        // nlist: the coarse distances
+  int count_top;           // add the candidates handed to Rerank
+  int ondemand;            // the table does not fit LDS (m > 32): entries computed per lookup
+};
+
 // PqFlatIndex (src/index/quant/ivf_pq.h:12-36) made resident: the PQ codebook and every
 // row's code, scanned in full by ADC against per-query tables.
 struct PqFlatIndex {

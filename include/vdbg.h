@@ -412,8 +412,7 @@ typedef struct vdbg_pqflat vdbg_pqflat;
 /* PqFlatIndex::build (src/index/quant/ivf_pq.cc:45-57): ProductQuantizer::train over every row
  * (pq.cc:14-41: per subspace a strided sample of at most 256 x max_points_per_centroid rows,
  * k-means seeded with seed + 7919 j) and every row encoded, on the GPU.  pq_m must divide the
- * dimension (InvalidArgument otherwise, index.cc:27-29); dim / pq_m above 64 is NotSupported.
- * vdb builds with kmeans_iters 25. */
+ * dimension (InvalidArgument otherwise, index.cc:27-29).  vdb builds with kmeans_iters 25. */
 int vdbg_pqflat_build(vdbg_dataset* ds, size_t pq_m, uint64_t seed,
                       size_t max_points_per_centroid, size_t kmeans_iters, vdbg_pqflat** out);
 /* LoadIndex of a VDBPQFL1 file (index.cc:38-87) and PqFlatIndex::load (ivf_pq.cc:89-98):

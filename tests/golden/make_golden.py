@@ -10,6 +10,7 @@ fixtures are data only (.npz without pickles): inputs and expected outputs.
     python3 tests/golden/make_golden.py segment    # segment.npz only
     python3 tests/golden/make_golden.py hnsw       # hnsw.npz only
     python3 tests/golden/make_golden.py pqflat     # pqflat.npz only
+    python3 tests/golden/make_golden.py ivf_shapes # ivf_shapes.npz only
 """
 import ctypes as C
 import os
@@ -19,6 +20,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(HERE))
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.dirname(HERE)), "hnsw-vector-db_amd"))
 from oracle_lib import KSET, METRIC, load_reference  # noqa: E402
 
 KSETS = ["scalar", "avx2", "avx512"]
@@ -184,6 +186,7 @@ def main():
     make_segment(L)
     make_hnsw(L)
     make_pqflat(L)
+    make_ivf_shapes(L)
     print("golden fixtures written to", HERE)
 
 
@@ -309,8 +312,53 @@ def make_pqflat(L):
     np.savez_compressed(os.path.join(HERE, "pqflat.npz"), **out)
 
 
+def ivf_shape_rows(n, dim, seed):
+    """The rows of an ivf_shapes case, regenerated by the tests from the same counter-based
+    generator (vdbg.datagen), so the fixture holds only the files and the results."""
+    from vdbg import datagen
+    pd = (dim + 15) // 16 * 16
+    return datagen.pad(datagen.sift_like(n, dim, seed, n_centres=20), pd)
+
+
+def make_ivf_shapes(L):
+    """ivf_shapes.npz: IVF-PQ indexes the reference built and saved (VDBIVFP1) for shapes past
+    the GPU's table staging (m = 64 over 64 dims, m = 48 over 96: one- and two-dim
+    sub-vectors) and past 64-dim sub-vectors (m = 2 over 136 dims: 68 each), and its
+    IvfPqIndex::search results on them per (nprobe, rerank) setting.  Rows and queries come
+    from ivf_shape_rows (seeded)."""
+    from oracle_lib import Reference
+    R = Reference()
+    out = {}
+    settings = np.array([(1, 0), (4, -1), (4, 300), (1000, 0)], np.int64)
+    cases = [("w", 800, 64, 64, 8, "l2", 71), ("x", 700, 136, 2, 6, "l2", 72),
+             ("y", 600, 96, 48, 6, "ip", 73)]
+    for tag, n, dim, m, nlist, metric, seed in cases:
+        pd = (dim + 15) // 16 * 16
+        base = ivf_shape_rows(n, dim, seed)
+        q = ivf_shape_rows(20, dim, seed + 100)
+        f = R.ivfpq_build(base, dim, nlist, m, seed=42, max_points=256, metric=metric)
+        out[f"{tag}_shape"] = np.array([n, dim, m, nlist, seed], np.int64)
+        out[f"{tag}_file"] = np.frombuffer(f, np.uint8).copy()
+        out[f"{tag}_metric"] = np.array(metric)
+        for si, (nprobe, rr) in enumerate(settings):
+            od = np.empty((20, 10), np.float32)
+            oi = np.empty((20, 10), np.uint32)
+            dc = np.empty(20, np.uint64)
+            assert L.ref_ivfpq_search_batch(METRIC[metric], f, len(f), base, n, dim, pd, q, 20,
+                                            10, int(nprobe), int(rr), None, od, oi, dc, 4) == 0
+            out[f"{tag}_s{si}_d"], out[f"{tag}_s{si}_i"], out[f"{tag}_s{si}_dc"] = od, oi, dc
+    out["settings"] = settings
+    out["kernels"] = np.array(R.lib.ref_best_kernels().decode())
+    np.savez_compressed(os.path.join(HERE, "ivf_shapes.npz"), **out)
+
+
 if __name__ == "__main__":
-    if sys.argv[1:] == ["pqflat"]:
+    if sys.argv[1:] == ["ivf_shapes"]:
+        ref = load_reference()
+        if ref is None:
+            sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+        make_ivf_shapes(ref.lib)
+    elif sys.argv[1:] == ["pqflat"]:
         ref = load_reference()
         if ref is None:
             sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")

@@ -264,16 +264,18 @@ def test_assign_nearest_matches_golden(oracle):
 
 # ------------------------------------------------------------------ IVF-PQ
 
-def _ivf_search(oracle, ix, base, qs, k, nprobe, rerank, kset="avx512"):
+def _ivf_search(oracle, ix, base, qs, k, nprobe, rerank, kset="avx512", metric="l2"):
     nq = len(qs)
     od = np.empty((nq, k), np.float32)
     oi = np.empty((nq, k), np.uint32)
     dc = np.empty(nq, np.uint64)
-    term2 = np.empty(ix["nlist"] * ix["m"] * 256, np.float32)
-    dsub = ix["dim"] // ix["m"]
-    oracle.lib.or_ivfpq_term2(ix["coarse"], ix["nlist"], ix["pd"], ix["pq_centroids"], ix["m"],
-                              dsub, term2)
-    oracle.lib.or_ivfpq_search_batch(KSET[kset], 0, base, ix["dim"], ix["pd"], ix["coarse"],
+    term2 = None
+    if metric == "l2":  # precompute_tables keeps term2 for L2 only (ivf_pq.cc:152-167)
+        term2 = np.empty(ix["nlist"] * ix["m"] * 256, np.float32)
+        dsub = ix["dim"] // ix["m"]
+        oracle.lib.or_ivfpq_term2(ix["coarse"], ix["nlist"], ix["pd"], ix["pq_centroids"],
+                                  ix["m"], dsub, term2)
+    oracle.lib.or_ivfpq_search_batch(KSET[kset], METRIC[metric], base, ix["dim"], ix["pd"], ix["coarse"],
                                      ix["nlist"], ix["pq_centroids"], ix["m"], ix["list_off"],
                                      ix["list_ids"], ix["list_codes"], term2, qs, nq, k,
                                      nprobe, rerank, None, od, oi, dc, 4)
@@ -580,3 +582,30 @@ def test_pqflat_matches_reference_random(oracle, reference):
                                               kset=reference.lib.ref_best_kernels().decode())
             assert np.array_equal(oi, ri) and np.array_equal(bits(od), bits(rd))
             assert np.array_equal(dc, rdc)
+
+
+# ------------------------------------------------------------------ IVF-PQ shapes
+
+def ivf_shape_case(g, tag):
+    import sys
+    sys.path.insert(0, GOLD)
+    from make_golden import ivf_shape_rows
+    n, dim, m, nlist, seed = (int(v) for v in g[f"{tag}_shape"])
+    return ivf_shape_rows(n, dim, seed), ivf_shape_rows(20, dim, seed + 100), dim, m, nlist
+
+
+def test_ivfpq_shapes_match_golden(oracle):
+    """m = 64 and 48 (one- and two-dim sub-vectors) and m = 2 over 136 dims (68-dim
+    sub-vectors): the oracle's IVF-PQ search equals the reference's on indexes it built."""
+    g = gold("ivf_shapes")
+    for tag in ("w", "x", "y"):
+        base, q, dim, m, nlist = ivf_shape_case(g, tag)
+        metric = str(g[f"{tag}_metric"])
+        ix = parse_ivfpq(g[f"{tag}_file"].tobytes())
+        assert ix["m"] == m and ix["dim"] == dim and ix["nlist"] == nlist
+        for si, (nprobe, rr) in enumerate(g["settings"]):
+            od, oi, dc = _ivf_search(oracle, ix, base, q, 10, int(nprobe), int(rr), metric=metric)
+            key = f"{tag}_s{si}"
+            assert np.array_equal(oi, g[key + "_i"]), key
+            assert np.array_equal(bits(od), bits(g[key + "_d"])), key
+            assert np.array_equal(dc, g[key + "_dc"]), key
