@@ -9,6 +9,8 @@ Workload (one "step" = one batch search over data resident in HBM):
   ivfpq   IVF-PQ over the same rows, nlist 4,096 (k-means 20 iterations, seed 42), m = 16,
           nprobe 64, rerank 100 -> k = 10; built on the GPU.  Also swept over nprobe
           16/32/64/128 at rerank 0 and 100.
+  flat_uniform  exact L2 over 100,000 x 128 rows uniform in [0, 1), 1,000 queries, k = 10
+          (real-valued rows: the two-part operand GEMMs with certificates).
   filtered  the collection read path: 5M unit rows of 384 dims (10,000-centre mixture, cosine)
           in 8 segments of 625,000, 2% of rows deleted, a filter passing 1%, 10% or 50% of
           rows; 4,096 raw queries go through PrepareQuery, the filtered exact scan of every
@@ -248,7 +250,7 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--k", type=int, default=10)
-    ap.add_argument("--paths", default="flat,sq8,ivfpq,filtered")
+    ap.add_argument("--paths", default="flat,flat_uniform,sq8,ivfpq,filtered")
     ap.add_argument("--nprobe", type=int, default=64)
     ap.add_argument("--cpu-sample", type=int, default=6400,
                     help="queries in the flat CPU-baseline sample (SQ8 uses half, IVF-PQ all)")
@@ -434,6 +436,59 @@ def main():
                 log(f"flat batch {b} k {kb}: {b * reps / elb:.0f} q/s")
             r["sweep"] = sweep
         results["flat"] = r
+
+    # ------------------------------------------------------------ flat, real-valued rows
+    if "flat_uniform" in paths:
+        # 100,000 x 128 rows uniform in [0, 1), 1,000 queries from the same distribution, k = 10:
+        # float rows rank on the two-part fp16 (or int8) operands and every answer is re-scored
+        # in the reference's AVX-512 order
+        nu, nqu = 100_000, 1000
+        ubase = datagen.uniform_rows(nu, dim, 1001)
+        uq = datagen.uniform_rows(nqu, dim, 1002)
+        uds = vdbg.Dataset(ctx, ubase, dim)
+        uq_dev = torch.from_numpy(uq).to(dev)
+        ui = torch.empty((nqu, k), dtype=torch.int32, device=dev)
+        ud = torch.empty((nqu, k), dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+
+        def step_u():
+            uds.flat_search_device(uq_dev.data_ptr(), nqu, k, ui.data_ptr(), ud.data_ptr(),
+                                   stream=stream)
+
+        reps = max(args.steps, 20)
+        el, prof, fb = timed(ctx, torch, step_u, reps, args.warmup,
+                             ["query_prep", "sample_gemm", "kth", "flat_gemm", "select",
+                              "exact_scan", "merge"])
+        g_ms = prof["flat_gemm"][0] / max(1, prof["flat_gemm"][1])
+        bits = ctx.last_gemm_bits()
+        peak = {8: INT8_MFMA_PEAK_TOPS, 16: FP16_MFMA_PEAK_TFLOPS}.get(bits, FP32_MFMA_PEAK_TFLOPS)
+        ach = 2.0 * nqu * nu * dim / (g_ms * 1e-3) / 1e12
+        r = {"qps": nqu * reps / el, "ms_per_step": el * 1e3 / reps, "rows": nu, "queries": nqu,
+             "kernel_ms": g_ms, "achieved": ach, "peak": peak,
+             "unit": "TOP/s" if bits == 8 else "TFLOP/s", "frac": ach / peak,
+             "mfma_inputs": {8: "i8 two-part rows x two-part queries",
+                             16: "f16 two-part rows x two-part queries"}.get(bits, "f32"),
+             "kernel_ms_per_step": {kk: v[0] / reps for kk, v in prof.items()},
+             "exact_rescans": fb}
+        ugi = ui.cpu().numpy().view(np.uint32).copy()
+        ugd = ud.cpu().numpy().copy()
+        if ref is not None:
+            s_ = nqu
+            qs = np.ascontiguousarray(uq[:s_])
+            od = np.empty((s_, k), np.float32)
+            oi = np.empty((s_, k), np.uint32)
+            t0 = time.perf_counter()
+            ref.lib.ref_flat_index_batch(0, ubase, nu, dim, dim, qs, s_, k, od, oi, threads)
+            dt = time.perf_counter() - t0
+            r["cpu_baseline"] = {"value": s_ / dt, "unit": "queries/s", "cores": threads,
+                                 "kind": "reference", "cpu_model": cpu_model,
+                                 "sample": f"{s_} queries, FlatIndex::search, {threads} threads, "
+                                           f"{dt:.2f} s"}
+            r["parity_on_cpu_sample"] = parity(ugi, ugd, oi, od)
+        log(f"flat uniform 100k: {r['qps']:.0f} q/s, GEMM {g_ms:.3f} ms ({bits}-bit), "
+            f"parity {r.get('parity_on_cpu_sample')}")
+        uds.close()
+        results["flat_uniform"] = r
 
     # ------------------------------------------------------------ SQ8
     if "sq8" in paths:
