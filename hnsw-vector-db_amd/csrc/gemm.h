@@ -41,7 +41,23 @@ struct GemmArgs {
   int nchunks, caph;
   int items;           // nqt * nchunks
   int per_xcd;         // items assigned to each of the 8 XCDs
+  const int* gate;     // nullable: per-query int8 fitness [gate_n]; the launch runs only
+  int gate_n, gate_on; // when (every query fits) == gate_on
 };
+
+// A gated launch: the batch's GEMM is chosen on the device (every query inside the int8
+// GEMM's bounds, or not), the other launch exits at once.  Block-uniform; call it before
+// any other barrier.
+__device__ __forceinline__ bool gemm_gated_off(const GemmArgs& a) {
+  if (a.gate == nullptr) return false;
+  __shared__ int s_fit;
+  if (threadIdx.x == 0) s_fit = 1;
+  __syncthreads();
+  for (int i = threadIdx.x; i < a.gate_n; i += blockDim.x)
+    if (a.gate[i] == 0) s_fit = 0;
+  __syncthreads();
+  return (s_fit != 0) != (a.gate_on != 0);
+}
 
 constexpr int kGemmRows = 64;  // rows per LDS tile (two 32-row MFMA blocks)
 

@@ -86,6 +86,7 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
   static_assert(PD % KC == 0 && KC % 32 == 0, "K chunking");
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][kGemmRows * STR];
   __shared__ __attribute__((aligned(16))) int xns[3][kGemmRows];
+  if (gemm_gated_off(a)) return;
 
   const int b = blockIdx.x;
   const int item = (b & 7) * a.per_xcd + (b >> 3);

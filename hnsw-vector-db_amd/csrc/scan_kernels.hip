@@ -60,6 +60,9 @@ __device__ __forceinline__ uint32_t ord_enc(float f) {
   uint32_t b = __float_as_uint(f);
   return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
+__device__ __forceinline__ float ord_dec_dev(uint32_t e) {
+  return __uint_as_float((e & 0x80000000u) ? (e & 0x7fffffffu) : ~e);
+}
 static inline float ord_dec(uint32_t e) {
   uint32_t b = (e & 0x80000000u) ? (e & 0x7fffffffu) : ~e;
   float f;
@@ -444,6 +447,7 @@ struct PrepArgs {
   int8_t* Q8;     // nullable: the int8 GEMM's B operand, q - c8 (gemm8.hip)
   int* Qd;        // its per-query constant M c8 sum(q) - c8^2 pd
   int* all8;      // cleared when a query is outside the int8 GEMM's bounds
+  int* fit8q;     // nullable: per query, 1 when it is inside the int8 GEMM's bounds
   int c8;
   uint32_t* mb8;  // nullable: SQ8 on the int8 GEMM, the batch's max |B| (float bits, atomicMax)
 };
@@ -459,9 +463,7 @@ struct PrepArgs {
 // carry at most pd roundings each on sums bounded by those magnitudes, the exact
 // AVX-512-order value at most pd/16 + 6, and the factor two covers forming thresholds and
 // the SQ8 decode roundings.
-__global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
-  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (q >= a.nq) return;
+__device__ void query_prep_wave(const PrepArgs& a, int q) {
   const float* v = a.Q + size_t(q) * a.pd;
   float s = 0.f, s2 = 0.f, lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f;
   float sq = 0.f;  // sum(q) (exact: integers of magnitude < 2^24 when the int8 GEMM applies)
@@ -572,18 +574,19 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
     if (a.Qf != nullptr && (a.kind == 1 || a.x16_parts == 2)) {
       a.Qf[q] = ldexpf(a.metric == 0 ? -2.f : -1.f, -sc - (a.kind == 0 ? a.x16_exp : 0));
       if (!split_ok) atomicAnd(a.all16, 0);
-    } else if (a.all16 != nullptr) {
+    } else if (a.all16 != nullptr || a.fit8q != nullptr) {
       const double rq = sqrt(double(s)), rx = sqrt(double(a.xs.xn_max));
       const bool fits = ex && ma <= 2048.f && a.xs.max_abs <= 2048.f &&
                         (rq + rx) * (rq + rx) * 1.001 < lim;
-      if (!fits) atomicAnd(a.all16, 0);
+      if (!fits && a.all16 != nullptr) atomicAnd(a.all16, 0);
       if (a.Q8 != nullptr) {
         // the int8 GEMM: the same bounds, every q - c8 an int8, and its constant in int32
         const double c = a.c8;
         const double d = (a.metric == 0 ? 2.0 : 1.0) * c * double(sq) - c * c * pd;
         const bool fits8 = fits && in8 && fabs(d) < 268435456.0;
         a.Qd[q] = fits8 ? int(d) : 0;
-        if (!fits8) atomicAnd(a.all8, 0);
+        if (!fits8 && a.all8 != nullptr) atomicAnd(a.all8, 0);
+        if (a.fit8q != nullptr) a.fit8q[q] = fits8 ? 1 : 0;
         // L2 values on the int8 GEMM may exceed the GEMM value by 1 (the rounded half
         // norm): such a query carries that bound whichever GEMM the batch takes
         half_norm = fits8 && a.metric == 0;
@@ -622,6 +625,33 @@ __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
                         : ex ? 0.f
                              : float((split ? (a.kind == 1 ? bound16 : bound16f) : bound) * 1.001);
   }
+}
+
+__global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
+  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (q >= a.nq) return;
+  query_prep_wave(a, q);
+}
+
+// The scan's per-call words in one launch: overflow flags, fallback counts, the batch's GEMM
+// eligibility flags, the all-ones filter word and the int8 operand exponent words.
+struct ScanInit {
+  int* ovf;              // [nq] 0
+  int nq;
+  uint32_t* fb_count;    // [2] 0
+  int* all16;            // nullable, [2] 1
+  uint32_t* ones;        // nullable, [1] all ones
+  int* e8;               // nullable, [2] 0
+};
+__global__ void k_scan_init(ScanInit a) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < a.nq) a.ovf[i] = 0;
+  if (i < 2) {
+    a.fb_count[i] = 0;
+    if (a.all16 != nullptr) a.all16[i] = 1;
+    if (a.e8 != nullptr) a.e8[i] = 0;
+  }
+  if (i == 0 && a.ones != nullptr) a.ones[0] = 0xffffffffu;
 }
 
 // SQ8 on the int8 GEMM (gemm8.hip, SQ = 1): the B operand of every query of the batch scaled
@@ -748,6 +778,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
   static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
   __shared__ __attribute__((aligned(16))) float xs[2][kGemmRows * STR];
   __shared__ float xns[3][kGemmRows];
+  if (gemm_gated_off(a)) return;
 
   const int b = blockIdx.x;
   const int item = (b & 7) * a.per_xcd + (b >> 3);
@@ -964,9 +995,6 @@ struct KthArgs {
   float* T;
 };
 
-__device__ __forceinline__ float ord_dec_dev(uint32_t e) {
-  return __uint_as_float((e & 0x80000000u) ? (e & 0x7fffffffu) : ~e);
-}
 
 // One wave per query: the kk-th smallest group minimum A.  The kk groups at or below A hold
 // kk distinct rows with GEMM value <= A, so the kk-th smallest exact distance is at most
@@ -1001,6 +1029,40 @@ __global__ __launch_bounds__(256) void k_kth(KthArgs a) {
   if (lane == 0) a.T[q] = A < __builtin_inff() ? A + 2.f * a.eb[q] : __builtin_inff();
 }
 
+// The same radix select with a block of 16 waves per query (small batches): V keys per
+// thread, the per-bit counts summed across the waves through LDS, one barrier per bit.
+template <int V>
+__global__ __launch_bounds__(1024) void k_kth_block(KthArgs a) {
+  __shared__ int s_cnt[2][16];
+  const int q = blockIdx.x;
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const float* g = a.gm + size_t(q) * a.ngroups;
+  uint32_t key[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int i = v * 1024 + int(threadIdx.x);
+    key[v] = i < a.ngroups ? ord_enc(g[i]) : 0xffffffffu;
+  }
+  float A = __builtin_inff();
+  if (a.kk <= a.ngroups) {
+    uint32_t ans = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t t = ans | ((1u << bit) - 1u);
+      int cnt = 0;
+#pragma unroll
+      for (int v = 0; v < V; ++v) cnt += __popcll(__ballot(key[v] <= t));
+      if (lane == 0) s_cnt[bit & 1][wave] = cnt;
+      __syncthreads();
+      int total = 0;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) total += s_cnt[bit & 1][w];
+      if (total < a.kk) ans |= 1u << bit;
+    }
+    A = ord_dec_dev(ans);
+  }
+  if (threadIdx.x == 0) a.T[q] = A < __builtin_inff() ? A + 2.f * a.eb[q] : __builtin_inff();
+}
+
 // ================================================================ selection / merge
 
 struct SelectArgs {
@@ -1027,58 +1089,68 @@ struct SelectArgs {
 
 constexpr int kMaxSeg = 1024;
 
-// One wave per slot.  Candidates of the slot's segments are streamed (a prefix sum over the
-// segment counts maps a flat index to its segment) into a wave top-k of capacity 64*E.
-// Queries that fail a certificate (or whose buffers overflowed) are appended to fb_list.
-template <int E, class Scorer>
-__global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
-  __shared__ uint32_t pre_all[4][kMaxSeg + 1];
-  __shared__ float stage_d[4][2 * kWave];
-  __shared__ uint32_t stage_i[4][2 * kWave];
+// One wave per slot (WPS = 1, four slots per block), or WPS waves per slot for small
+// batches: each wave streams the candidates of its share of the slot's segments (a prefix
+// sum over the segment counts maps a flat index to its segment) into a wave top-k of
+// capacity 64*E, and wave 0 merges the others' lists before the re-scoring.  Queries that
+// fail a certificate (or whose buffers overflowed) are appended to fb_list.
+template <int E, class Scorer, int WPS>
+__global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs a, Scorer sc) {
+  constexpr int WAVES = WPS == 1 ? 4 : WPS;
+  constexpr int PRE = WPS == 1 ? kMaxSeg : kMaxSeg / WPS;  // segments per wave
+  __shared__ uint32_t pre_all[WAVES][PRE + 1];
+  __shared__ float stage_d[WAVES][2 * kWave];
+  __shared__ uint32_t stage_i[WAVES][2 * kWave];
+  __shared__ float md[WPS == 1 ? 1 : WPS - 1][WPS == 1 ? 1 : kWave * E];
+  __shared__ uint32_t mi[WPS == 1 ? 1 : WPS - 1][WPS == 1 ? 1 : kWave * E];
+  __shared__ uint32_t mtot[WAVES];
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
-  const int slot = blockIdx.x * 4 + wave;
+  const int slot = WPS == 1 ? blockIdx.x * 4 + wave : blockIdx.x;
+  const int sub = WPS == 1 ? 0 : wave;  // the wave's share of the slot's segments
   if (slot >= a.nslots) return;
   const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
   const uint32_t src = a.by_query ? q : uint32_t(slot);
   uint32_t* pre = pre_all[wave];
 
   if (a.ovf != nullptr && a.ovf[q]) {
-    if (lane == 0) {
+    if (lane == 0 && sub == 0) {
       const uint32_t p = atomicAdd(a.fb_count, 1u);
       a.fb_list[p] = q;
     }
     return;
   }
 
+  const int per = (a.nseg + WPS - 1) / WPS;
+  const int s_lo = min(a.nseg, sub * per), nseg_w = min(a.nseg, s_lo + per) - s_lo;
   uint32_t run = 0;
-  const uint32_t* cnts = a.counts + size_t(src) * a.nseg;
-  for (int b = 0; b < a.nseg; b += kWave) {
+  const uint32_t* cnts = a.counts + size_t(src) * a.nseg + s_lo;
+  for (int b = 0; b < nseg_w; b += kWave) {
     const int s = b + lane;
-    const uint32_t c = s < a.nseg ? cnts[s] : 0u;
+    const uint32_t c = s < nseg_w ? cnts[s] : 0u;
     uint32_t incl = c;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
       const uint32_t t = __shfl_up(incl, o);
       if (lane >= o) incl += t;
     }
-    if (s < a.nseg) pre[s + 1] = run + incl;
+    if (s < nseg_w) pre[s + 1] = run + incl;
     run += __shfl(incl, kWave - 1);
   }
   if (lane == 0) pre[0] = 0;
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const uint32_t total = run;
+  const uint32_t total_w = run;
 
   WaveTopK<E> top;
   top.init();
   const float* qv = a.Q + size_t(q) * a.pd;
-  const uint2* cbase = a.cand + size_t(src) * a.nseg * size_t(a.cap);
-  // candidate g of the flat order: the segment is the largest s with pre[s] <= g
+  const uint2* cbase = a.cand + (size_t(src) * a.nseg + s_lo) * size_t(a.cap);
+  // candidate g of the wave's flat order: the segment is the largest s with pre[s] <= g
   auto fetch = [&](uint32_t g) -> uint2 {
-    if (g >= total) return make_uint2(__float_as_uint(__builtin_inff()), kNoId);
-    int lo = 0, hi = a.nseg;
+    if (g >= total_w) return make_uint2(__float_as_uint(__builtin_inff()), kNoId);
+    int lo = 0, hi = nseg_w;
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
       if (pre[mid] <= g) lo = mid; else hi = mid;
@@ -1127,7 +1199,7 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   };
   // the next batch is loaded before the current one is pushed (hides the load latency)
   uint2 cur = fetch(lane);
-  for (uint32_t g0 = 0; g0 < total; g0 += kWave) {
+  for (uint32_t g0 = 0; g0 < total_w; g0 += kWave) {
     const uint2 nxt = fetch(g0 + kWave + lane);
     const uint32_t id = cur.y;
     float d = __uint_as_float(cur.x);
@@ -1141,6 +1213,25 @@ __global__ __launch_bounds__(256) void k_select(SelectArgs a, Scorer sc) {
   if (staged > 0) {
     const bool have = lane < staged;
     top.insert(have ? sd[lane] : __builtin_inff(), have ? si[lane] : kNoId);
+  }
+  uint32_t total = total_w;
+  if constexpr (WPS > 1) {
+    // the other waves' lists and candidate counts into wave 0
+    if (wave > 0) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        md[wave - 1][e * kWave + lane] = top.k.d[e];
+        mi[wave - 1][e * kWave + lane] = top.k.id[e];
+      }
+    }
+    if (lane == 0) mtot[wave] = total_w;
+    __syncthreads();
+    if (wave > 0) return;
+    for (int w = 1; w < WPS; ++w) {
+      total += mtot[w];
+#pragma unroll
+      for (int e = 0; e < E; ++e) top.insert(md[w - 1][e * kWave + lane], mi[w - 1][e * kWave + lane]);
+    }
   }
 
   constexpr int N = kWave * E;
@@ -1394,9 +1485,17 @@ __global__ void k_fill_empty(uint32_t* ids, float* d, size_t n) {
   }
 }
 
+// Small batches split each slot's segments over 16 (up to 64 slots, k <= 112: 128 registers
+// per lane hold that list) or 4 waves (up to 256) so the slot's candidates stream in
+// parallel; larger ones run one wave per slot.
 template <int E, class Scorer>
 static void launch_select(hipStream_t s, const SelectArgs& a, const Scorer& sc) {
-  k_select<E, Scorer><<<dim3((a.nslots + 3) / 4), 256, 0, s>>>(a, sc);
+  if (E <= 2 && a.nslots <= 64 && a.nseg >= 64)
+    k_select<E, Scorer, (E <= 2 ? 16 : 4)><<<dim3(a.nslots), E <= 2 ? 1024 : 256, 0, s>>>(a, sc);
+  else if (a.nslots <= 256 && a.nseg >= 16)
+    k_select<E, Scorer, 4><<<dim3(a.nslots), 256, 0, s>>>(a, sc);
+  else
+    k_select<E, Scorer, 1><<<dim3((a.nslots + 3) / 4), 256, 0, s>>>(a, sc);
 }
 template <int E, class Scorer>
 static void launch_scan(hipStream_t s, const ScanArgs& a, const Scorer& sc) {
@@ -1407,6 +1506,12 @@ static void launch_kth_v(hipStream_t s, const KthArgs& a) {
   k_kth<V><<<dim3((a.nq + 3) / 4), 256, 0, s>>>(a);
 }
 static int LaunchKth(hipStream_t s, const KthArgs& a) {
+  if (a.nq <= 64 && a.ngroups <= 4096) {  // a block per query
+    if (a.ngroups <= 1024) k_kth_block<1><<<dim3(a.nq), 1024, 0, s>>>(a);
+    else if (a.ngroups <= 2048) k_kth_block<2><<<dim3(a.nq), 1024, 0, s>>>(a);
+    else k_kth_block<4><<<dim3(a.nq), 1024, 0, s>>>(a);
+    return kOk;
+  }
   int v = 1;
   while (v * kWave < a.ngroups) v <<= 1;
   switch (v) {
@@ -1607,6 +1712,7 @@ int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t k
               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
   c->last_fallbacks = 0;
   c->last_gemm_bits = 0;
+  c->last_gemm_gate = nullptr;
   if (nq == 0 || kk == 0) return kOk;
   if (src.N == 0) {
     k_fill_empty<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, out_d, nq * kk);
@@ -1617,6 +1723,415 @@ int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t k
   return ExactScan(c, c->ws, src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
 }
 
+// ================================================================ tiny batches
+//
+// At most kTinyQ queries over integer rows with an int8 copy: two launches and no threshold
+// pre-pass.  k_tiny_scan: each block streams a contiguous chunk of rows once, scores every
+// row against every query as the int8 GEMM does (u = row start + sum x8 q8, exact in int32;
+// key = -M u, the GEMM value plus the query's constant Qd) and keeps, per query, the kp
+// smallest keys of its chunk with their rows, plus the chunk's kp-th key (+inf when the
+// chunk holds fewer rows).  k_tiny_merge: one block per query takes the query's operands and
+// bound (query_prep_wave), the best keys of all chunks, re-scores the best n1 = min(K', k +
+// 8) exactly (the reference's distance) and certifies the answer when the k-th exact
+// distance lies strictly below every unscored row's lower bound: the (n1+1)-th key, and each
+// full chunk's kp-th key (a row outside a chunk's list has a key at least that), taken back
+// to distances by -Qd + shift - eb.  Queries that are outside the int8 bounds or fail the
+// certificate go to the exact re-scan.  The last block publishes the fallback count to the
+// host (as ReadWords does), so the call makes no other launch.
+
+constexpr int kTinyQ = 2;       // queries
+constexpr int kTinyK = 48;      // k (kp = k + 16 <= 64 keys per chunk)
+constexpr int kTinyMaxPd = 256; // |key| < 2^23 stays exact in fp32
+
+struct TinyArgs {
+  const float* Q;
+  int nq, pd, metric, c8, k, kp;
+  const int8_t* X8;
+  const int* init8;
+  const uint64_t* allow;
+  uint32_t N, chunk_rows;
+  uint2* part;            // [q][chunk][kp] (key bits, row)
+  float* bound;           // [q][chunk] the chunk's kp-th key, +inf when not full
+  uint32_t* fb_count;     // [2] zeroed by the scan's block 0; [1] counts finished merges
+};
+
+// Rows reach the lanes through a per-wave LDS tile: the wave reads 64 consecutive rows with
+// coalesced 16-byte loads (consecutive lanes, consecutive bytes), then each lane reads its
+// own row from the tile (row stride padded by 16 bytes against bank conflicts).
+template <int NQ, int VPR>
+__global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
+  __shared__ int s_q8[NQ][kTinyMaxPd / 4];
+  __shared__ float sd[4][NQ][2 * kWave];
+  __shared__ uint32_t si[4][NQ][2 * kWave];
+  __shared__ float md[3][NQ][kWave];
+  __shared__ uint32_t mi[3][NQ][kWave];
+  extern __shared__ int4 tile_all[];  // [4][64][pd / 16 + 1]
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  constexpr int vpr = VPR;             // 16-byte vectors per row (pd / 16)
+  int4* tile = tile_all + size_t(wave) * kWave * (vpr + 1);
+  if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
+  const int pw = a.pd / 4;
+  for (int e = tid; e < NQ * pw; e += 256) {
+    const int q = e / pw, w = e - q * pw;
+    uint32_t packed = 0;
+    if (q < a.nq) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        // q - c8 clamped into int8 (queries outside the window are re-scanned exactly)
+        const float d = a.Q[size_t(q) * a.pd + 4 * w + t] - float(a.c8);
+        packed |= uint32_t(uint8_t(int8_t(int(fminf(fmaxf(d, -128.f), 127.f))))) << (8 * t);
+      }
+    }
+    s_q8[q][w] = int(packed);
+  }
+  __syncthreads();
+  const uint32_t r0 = blockIdx.x * a.chunk_rows, r1 = min(a.N, r0 + a.chunk_rows);
+  const int M = a.metric == 0 ? 2 : 1;
+  WaveTopK<1> top[NQ];
+  int staged[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    top[q].init();
+    staged[q] = 0;
+  }
+  const int rl = (a.kp - 1) & (kWave - 1);
+  // the 64 rows of a step, coalesced (vector e of the 64-row block: consecutive lanes read
+  // consecutive bytes); the next step's rows load while this one is scored
+  auto load_step = [&](uint32_t base, int4 (&v)[VPR]) {
+    const uint32_t nrow = base < r1 ? min(uint32_t(kWave), r1 - base) : 0u;
+    const int4* src = reinterpret_cast<const int4*>(a.X8 + size_t(base) * a.pd);
+#pragma unroll
+    for (int t = 0; t < VPR; ++t) {
+      const int e = t * kWave + lane;
+      v[t] = e < int(nrow) * vpr ? src[e] : make_int4(0, 0, 0, 0);
+    }
+  };
+  int4 vn[VPR];
+  load_step(r0 + wave * kWave, vn);
+  for (uint32_t base = r0 + wave * kWave; base < r1; base += 4 * kWave) {
+    const uint32_t r = base + lane;
+    const bool live = r < r1 && row_allowed(a.allow, r);
+    {
+      const uint32_t nrow = min(uint32_t(kWave), r1 - base);
+      int4 v[VPR];
+#pragma unroll
+      for (int t = 0; t < VPR; ++t) v[t] = vn[t];
+      load_step(base + 4 * kWave, vn);
+#pragma unroll
+      for (int t = 0; t < VPR; ++t) {
+        const int e = t * kWave + lane;
+        if (e < int(nrow) * vpr) tile[(e / vpr) * (vpr + 1) + e % vpr] = v[t];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+    int u[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) u[q] = live ? a.init8[r] : 0;
+    if (live) {
+      const int4* xr = tile + lane * (vpr + 1);
+      int4 xw[VPR];
+#pragma unroll
+      for (int i = 0; i < VPR; ++i) xw[i] = xr[i];
+#pragma unroll
+      for (int i = 0; i < VPR; ++i) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          u[q] = __builtin_amdgcn_sdot4(xw[i].x, s_q8[q][4 * i + 0], u[q], false);
+          u[q] = __builtin_amdgcn_sdot4(xw[i].y, s_q8[q][4 * i + 1], u[q], false);
+          u[q] = __builtin_amdgcn_sdot4(xw[i].z, s_q8[q][4 * i + 2], u[q], false);
+          u[q] = __builtin_amdgcn_sdot4(xw[i].w, s_q8[q][4 * i + 3], u[q], false);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();  // every lane has read its row before the next tile
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if (q >= a.nq) break;
+      // stage the keys below the wave's current kp-th key; insert 64 at a time
+      const float key = float(-M * u[q]);
+      const float td = __shfl(top[q].k.d[0], rl);
+      const uint32_t ti = __shfl(top[q].k.id[0], rl);
+      const bool want = live && nb_less(key, r, td, ti);
+      const uint64_t bal = __ballot(want);
+      if (bal == 0) continue;
+      const int pos = staged[q] + __popcll(bal & ((1ull << lane) - 1ull));
+      if (want) {
+        sd[wave][q][pos] = key;
+        si[wave][q][pos] = r;
+      }
+      staged[q] += __popcll(bal);
+      if (staged[q] >= kWave) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const float d0 = sd[wave][q][lane];
+        const uint32_t i0 = si[wave][q][lane];
+        const bool more = lane + kWave < staged[q];
+        const float d1 = more ? sd[wave][q][lane + kWave] : 0.f;
+        const uint32_t i1 = more ? si[wave][q][lane + kWave] : 0u;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (more) {
+          sd[wave][q][lane] = d1;
+          si[wave][q][lane] = i1;
+        }
+        staged[q] -= kWave;
+        top[q].insert(d0, i0);
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (q >= a.nq) break;
+    if (staged[q] > 0) {
+      const bool have = lane < staged[q];
+      top[q].insert(have ? sd[wave][q][lane] : __builtin_inff(), have ? si[wave][q][lane] : kNoId);
+    }
+    if (wave > 0) {
+      md[wave - 1][q][lane] = top[q].k.d[0];
+      mi[wave - 1][q][lane] = top[q].k.id[0];
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (q >= a.nq) break;
+    for (int w = 0; w < 3; ++w) top[q].insert(md[w][q][lane], mi[w][q][lane]);
+    const size_t o = size_t(q) * gridDim.x + blockIdx.x;
+    if (lane < a.kp) a.part[o * a.kp + lane] = make_uint2(__float_as_uint(top[q].k.d[0]), top[q].k.id[0]);
+    const float kth = __shfl(top[q].k.d[0], rl);
+    const uint32_t kid = __shfl(top[q].k.id[0], rl);
+    if (lane == 0) a.bound[o] = kid == kNoId ? __builtin_inff() : kth;
+  }
+}
+
+struct TinyMergeArgs {
+  PrepArgs pa;            // the query's operands and bound (fit8q set)
+  const uint2* part;
+  const float* bound;
+  int nchunks, kp, k;
+  FlatScorer sc;
+  uint32_t* out_ids;
+  float* out_d;
+  uint32_t* fb_list;
+  uint32_t* fb_count;     // [0] fallbacks, [1] finished merges
+  uint32_t* host_flag;    // pinned host words: [0] sequence, [1] fallback count
+  uint32_t seq;
+  int force_fallback;
+};
+
+// One block of 8 waves per query.  Each wave loads its share of the chunks' keys with all
+// loads in flight (up to 8 per lane at a time), keeps the k + 9 best (staged inserts), and
+// the 8 lists merge as a tree (three rounds); wave 0 then re-scores and certifies.
+__global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
+  constexpr int W = 8;
+  constexpr int B = 8;   // keys per lane loaded at once
+  __shared__ float md[W / 2][kWave];
+  __shared__ uint32_t mi[W / 2][kWave];
+  __shared__ float s_lb[W];
+  __shared__ float sd[W][2 * kWave];
+  __shared__ uint32_t si[W][2 * kWave];
+  const int q = blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  if (wave == 0) query_prep_wave(a.pa, q);
+  WaveTopK<1> top;
+  top.init();
+  float lb = __builtin_inff();
+  const int per = (a.nchunks + W - 1) / W;
+  const int c0 = min(a.nchunks, wave * per), c1 = min(a.nchunks, c0 + per);
+  const size_t total = size_t(c1 - c0) * a.kp;
+  const uint2* src = a.part + (size_t(q) * a.nchunks + c0) * a.kp;
+  // the key to beat: the (k + 9)-th (the certificate reads the key after the k + 8 scored)
+  const int rl = (a.k + 9 - 1) & (kWave - 1);
+  int staged = 0;
+  auto push = [&](uint2 v) {
+    const float td = __shfl(top.k.d[0], rl);
+    const uint32_t ti = __shfl(top.k.id[0], rl);
+    const bool want = v.y != kNoId && nb_less(__uint_as_float(v.x), v.y, td, ti);
+    const uint64_t bal = __ballot(want);
+    if (bal == 0) return;
+    const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
+    if (want) {
+      sd[wave][pos] = __uint_as_float(v.x);
+      si[wave][pos] = v.y;
+    }
+    staged += __popcll(bal);
+    if (staged >= kWave) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float d0 = sd[wave][lane];
+      const uint32_t i0 = si[wave][lane];
+      const bool more = lane + kWave < staged;
+      const float d1 = more ? sd[wave][lane + kWave] : 0.f;
+      const uint32_t i1 = more ? si[wave][lane + kWave] : 0u;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (more) {
+        sd[wave][lane] = d1;
+        si[wave][lane] = i1;
+      }
+      staged -= kWave;
+      top.insert(d0, i0);
+    }
+  };
+  for (size_t g0 = 0; g0 < total; g0 += size_t(B) * kWave) {
+    uint2 v[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const size_t g = g0 + size_t(b) * kWave + lane;
+      v[b] = g < total ? src[g] : make_uint2(__float_as_uint(__builtin_inff()), kNoId);
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) push(v[b]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  if (staged > 0) {
+    const bool have = lane < staged;
+    top.insert(have ? sd[wave][lane] : __builtin_inff(), have ? si[wave][lane] : kNoId);
+  }
+  for (int ch = c0 + lane; ch < c1; ch += kWave) lb = fminf(lb, a.bound[size_t(q) * a.nchunks + ch]);
+  lb = wave_min(lb);
+  if (lane == 0) s_lb[wave] = lb;
+  // tree merge: at step h, wave w (w % 2h == h) hands its list to wave w - h
+  for (int h = 1; h < W; h <<= 1) {
+    const bool give = (wave % (2 * h)) == h;
+    if (give) {
+      md[wave >> 1][lane] = top.k.d[0];
+      mi[wave >> 1][lane] = top.k.id[0];
+    }
+    __syncthreads();
+    if ((wave % (2 * h)) == 0) top.insert(md[(wave + h) >> 1][lane], mi[(wave + h) >> 1][lane]);
+    __syncthreads();
+  }
+  if (wave != 0) return;
+  lb = __builtin_inff();
+  for (int w = 0; w < W; ++w) lb = fminf(lb, s_lb[w]);
+  const float* qv = a.pa.Q + size_t(q) * a.pa.pd;
+  const float shift = a.pa.shift[q], eb = a.pa.eb[q];
+  const float Qd = float(a.pa.Qd[q]);
+  const bool fits = a.pa.fit8q[q] != 0;
+  // exact re-scoring of the best n1 keys, certificate against every unscored row
+  const int n1 = min(kWave - 1, a.k + 8);
+  float d = __builtin_inff();
+  uint32_t id = kNoId;
+  if (lane < n1 && top.k.id[0] != kNoId) {
+    id = top.k.id[0];
+    d = a.sc(qv, id);
+  }
+  WaveKeys<1> r;
+  r.d[0] = d;
+  r.id[0] = id;
+  bitonic_sort<1>(r);
+  const float dk = __shfl(r.d[0], a.k - 1);
+  const float next = __shfl(top.k.d[0], n1);   // the (n1+1)-th key (+inf when none)
+  const float lower = (fminf(next, lb) - Qd + shift) - eb;
+  // every row scored (fewer keys than n1 + 1 and no full chunk): the answer is complete
+  const bool all_scored = next == __builtin_inff() && lb == __builtin_inff();
+  const bool certified = fits && a.force_fallback == 0 && (dk < lower || all_scored);
+  if (lane < a.k) {
+    a.out_ids[size_t(q) * a.k + lane] = r.id[0];
+    a.out_d[size_t(q) * a.k + lane] = r.d[0];
+  }
+  if (lane == 0) {
+    if (!certified) a.fb_list[atomicAdd(a.fb_count, 1u)] = uint32_t(q);
+    __threadfence();
+    if (atomicAdd(a.fb_count + 1, 1u) == uint32_t(gridDim.x - 1)) {
+      // the last merge: publish the fallback count (seq written last, with release)
+      a.host_flag[1] = __hip_atomic_load(a.fb_count, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence_system();
+      __hip_atomic_store(a.host_flag, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
+// Whether a batch takes the tiny-batch path: integer rows with their int8 copy, the int8
+// GEMM on, at most kTinyQ queries, k <= kTinyK, rows of 64, 128 or 256 dims.
+static bool TinyEligible(const Ctx* c, const ScanSource& src, size_t nq, size_t kk,
+                         const Workspace& w) {
+  return nq >= 1 && nq <= size_t(kTinyQ) && kk <= size_t(kTinyK) && src.kind == 0 &&
+         src.metric <= 1 && src.X8 != nullptr && src.x8_parts == 1 && src.init8 != nullptr &&
+         c->fp16_gemm && c->int8_gemm && src.x16_parts == 1 &&
+         (src.pd == 64 || src.pd == 128 || src.pd == 256) && src.N >= 1024 && !w.fixed;
+}
+
+template <int NQ>
+static void launch_tiny(hipStream_t s, int blocks, const TinyArgs& a) {
+  const size_t tile = size_t(4) * kWave * (a.pd / 16 + 1) * sizeof(int4);
+  switch (a.pd) {
+    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks), 256, tile, s>>>(a); break;
+    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks), 256, tile, s>>>(a); break;
+    default: k_tiny_scan<NQ, 16><<<dim3(blocks), 256, tile, s>>>(a); break;
+  }
+}
+
+static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
+                    const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
+                    Workspace& W, Workspace& W2) {
+  const uint32_t N = src->N;
+  const int pd = int(src->pd);
+  const int kp = int(kk) + 9;
+  const int blocks = 2 * c->cu_count;
+  uint32_t chunk = (N + blocks - 1) / blocks;
+  chunk = (chunk + 255) / 256 * 256;
+  const int nchunks = int((N + chunk - 1) / chunk);
+  WsUse wuse(&W, s);
+  VDBG_RETURN_IF_ERROR(wuse.status());
+  W.used = 0;
+  const size_t need = nq * size_t(nchunks) * (size_t(kp) * sizeof(uint2) + sizeof(float)) +
+                      nq * (3 * sizeof(float) + 3 * sizeof(int) + 2 * sizeof(uint32_t) + pd) +
+                      16 * 256;
+  VDBG_RETURN_IF_ERROR(W.reserve(need));
+  uint2* part = W.take<uint2>(nq * size_t(nchunks) * kp);
+  float* bound = W.take<float>(nq * size_t(nchunks));
+  float* shift = W.take<float>(nq);
+  float* eb = W.take<float>(nq);
+  int* exact = W.take<int>(nq);
+  int* Qd = W.take<int>(nq);
+  int* fit8q = W.take<int>(nq);
+  int8_t* Q8 = W.take<int8_t>(nq * size_t(pd));
+  uint32_t* fb_list = W.take<uint32_t>(nq);
+  uint32_t* fb_count = W.take<uint32_t>(2);
+  c->last_gemm_bits = 8;
+  TinyArgs ta{Q, int(nq), pd, src->metric, src->c8, int(kk), kp, src->X8, src->init8, allow, N,
+              chunk, part, bound, fb_count};
+  {
+    ProfScope ps(c, "flat_gemm", s);
+    if (nq == 1) launch_tiny<1>(s, nchunks, ta);
+    else launch_tiny<2>(s, nchunks, ta);
+    VDBG_HIP(hipGetLastError());
+  }
+  PrepArgs pa{Q, nullptr, int(nq), pd, src->kind, src->metric, src->stats, src->rmag,
+              src->vmin, src->scale, shift, eb, exact, nullptr, nullptr, nullptr,
+              src->x16_parts, src->x16_exp, Q8, Qd, nullptr, fit8q, src->c8, nullptr};
+  const uint32_t seq = NextFlagSeq(c);
+  TinyMergeArgs ma{pa, part, bound, nchunks, kp, int(kk), FlatOf(*src, c->kset), out_ids, out_d,
+                   fb_list, fb_count, c->host_flag_dev, seq, c->test_fallbacks};
+  {
+    ProfScope ps(c, "select", s);
+    k_tiny_merge<<<dim3(unsigned(nq)), 512, 0, s>>>(ma);
+    VDBG_HIP(hipGetLastError());
+  }
+  VDBG_RETURN_IF_ERROR(WaitWords(c, seq, fb_count, 1, s));
+  const uint32_t nfb = c->host_pinned[0];
+  c->last_fallbacks = nfb;
+  if (nfb > 0)
+    VDBG_RETURN_IF_ERROR(ExactScan(c, W2, *src, Q, fb_list, int(nfb), kk, allow, out_ids, out_d, s));
+  return kOk;
+}
+
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
             Workspace* ws, Workspace* ws2) {
@@ -1624,6 +2139,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   Workspace& W2 = ws2 != nullptr ? *ws2 : c->ws2;
   c->last_fallbacks = 0;
   c->last_gemm_bits = 0;
+  c->last_gemm_gate = nullptr;
   if (nq == 0 || kk == 0) return kOk;
   if (kk > 10000) return SetError(kInvalidArgument, "k must be in 1..10000");
   if (src->N == 0) {
@@ -1637,6 +2153,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t pd = src->pd;
   const bool gemm = GemmSupported(pd) && N >= 1024;
   if (!gemm) return ExactScan(c, W, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
+  if (TinyEligible(c, *src, nq, kk, W))
+    return TinyScan(c, src, Q, nq, kk, allow, out_ids, out_d, s, W, W2);
   // A re-scan workspace that cannot grow must hold the re-scan of every query, checked
   // before anything is queued (which queries fall back is known only on the device).
   if (W2.fixed && PlanExact(N, int(nq), kk).need > W2.cap)
@@ -1676,6 +2194,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,
                                               uint64_t(N) * kk / passes});
   while (S < s_want && S < (1u << 30)) S *= 2;
+  // Small batches of integer rows (at most 128 queries) choose between the int8 and the
+  // fp32 main pass on the device (no host round trip before the main pass).
+  const bool gated = nq <= 128 && split == 0 && try8 && !try8op;
   S = std::min(S, src->Smax);
   const int ngroups = int((S + 31) / 32) * 2;
   struct Plan {
@@ -1779,16 +2300,17 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* mb8 = try8op ? reinterpret_cast<uint32_t*>(e8 + 1) : nullptr;
   // the no-filter word of the fp16 and int8 GEMMs
   uint32_t* ones = try16 || try8any ? w.take<uint32_t>(1) : nullptr;
-  VDBG_RETURN_IF_ERROR(Fill32(ovf, 0, nq, s));
-  VDBG_RETURN_IF_ERROR(Fill32(fb_count, 0, 2, s));
-  if (all16 != nullptr) VDBG_RETURN_IF_ERROR(Fill32(all16, 1, 2, s));
-  if (ones != nullptr) VDBG_RETURN_IF_ERROR(Fill32(ones, 0xffffffffu, 1, s));
-  if (try8op) VDBG_RETURN_IF_ERROR(Fill32(e8, 0, 2, s));
+  int* fit8q = gated ? w.take<int>(nq) : nullptr;  // per query: inside the int8 bounds
+  {
+    const ScanInit si{ovf, int(nq), fb_count, all16, ones, try8op ? e8 : nullptr};
+    k_scan_init<<<dim3(unsigned((std::max<size_t>(nq, 2) + 255) / 256)), 256, 0, s>>>(si);
+    VDBG_HIP(hipGetLastError());
+  }
 
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
               src->x16_exp, try8 ? Q8 : nullptr, try8 ? Qd : nullptr, try8 ? all8 : nullptr,
-              src->c8, mb8};
+              fit8q, src->c8, mb8};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
@@ -1804,9 +2326,11 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // The exact-integer GEMM needs every query of the batch inside its bounds, so the host
   // reads the flag.  The split operands need no such check: a non-finite query only yields
   // NaN or infinite GEMM values and bound, its certificate fails and it is re-scanned
-  // exactly, as on the fp32 GEMM.
+  // exactly, as on the fp32 GEMM.  Small batches of integer rows make no round trip: the
+  // int8 and the fp32 main pass are both queued, gated on the per-query flags (their plans,
+  // candidate layout and bound coincide at nq <= 128), and the one they rule out exits.
   bool use16 = try16 && split != 0, use8 = false;
-  if ((try16 && split == 0) || try8op) {
+  if (((try16 && split == 0) || try8op) && !gated) {
     VDBG_RETURN_IF_ERROR(ReadWords(c, reinterpret_cast<const uint32_t*>(all16), 2, s));
     use8 = try8any && c->host_pinned[1] != 0;
     use16 = try16 && !use8 && (split != 0 || c->host_pinned[0] != 0);
@@ -1814,6 +2338,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // the bound of the GEMM the batch ranks on
   const float* ebx = use8 && try8op ? eb8 : eb;
   c->last_gemm_bits = use8 ? 8 : (use16 ? 16 : 32);
+  c->last_gemm_gate = gated ? fit8q : nullptr;
+  c->last_gemm_gate_n = int(nq);
   const Plan& P = use8 ? p8 : (use16 ? p16 : p32);
   const int nchunks = P.nchunks;
   const int caph = P.caph;
@@ -1890,7 +2416,25 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   GemmGrid(ga, P.nqt, nchunks, &blocks);
   {
     ProfScope ps(c, src->kind == 0 ? "flat_gemm" : "sq8_gemm", s);
-    if (use8) {
+    if (gated) {
+      // the int8 pass when every query fits it, else the fp32 pass (one grid, one plan)
+      GemmArgs g8 = ga;
+      g8.X8 = src->X8;
+      g8.rn8 = src->init8;
+      g8.Q8 = Q8;
+      g8.Qd = Qd;
+      g8.e8 = e8;
+      g8.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
+      g8.aw_mask = allow != nullptr ? ~0u : 0u;
+      g8.gate = fit8q;
+      g8.gate_n = int(nq);
+      g8.gate_on = 1;
+      VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, P.qb, 0, 0, s, blocks, g8));
+      ga.gate = fit8q;
+      ga.gate_n = int(nq);
+      ga.gate_on = 0;
+      VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
+    } else if (use8) {
       ga.X8 = try8s ? reinterpret_cast<const int8_t*>(src->C) : src->X8;
       ga.rn8 = src->init8;
       ga.Q8 = Q8;

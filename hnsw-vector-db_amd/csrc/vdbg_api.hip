@@ -33,11 +33,17 @@ __global__ void k_publish_words(const uint32_t* __restrict__ src, int n, uint32_
   if (i == 0) __hip_atomic_store(dst, seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
+uint32_t NextFlagSeq(Ctx* c) { return ++c->flag_seq == 0 ? ++c->flag_seq : c->flag_seq; }
+
 int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s) {
   if (n <= 0 || n > 64) return SetError(kInternal, "ReadWords: 1..64 words");
-  const uint32_t seq = ++c->flag_seq == 0 ? ++c->flag_seq : c->flag_seq;
+  const uint32_t seq = NextFlagSeq(c);
   k_publish_words<<<1, 64, 0, s>>>(dev, n, c->host_flag_dev, seq);
   VDBG_HIP(hipGetLastError());
+  return WaitWords(c, seq, dev, n, s);
+}
+
+int WaitWords(Ctx* c, uint32_t seq, const uint32_t* dev, int n, hipStream_t s) {
   volatile uint32_t* f = c->host_flag;
   for (uint32_t spin = 0;; ++spin) {
     if (__atomic_load_n(&c->host_flag[0], __ATOMIC_ACQUIRE) == seq) {
@@ -1189,7 +1195,24 @@ int vdbg_rerank_host(vdbg_dataset* ds, const float* queries, size_t nq, const ui
   return rc;
 }
 
-int vdbg_last_gemm_bits(vdbg_ctx* ctx) { return ctx == nullptr ? 0 : ctx->c.last_gemm_bits; }
+int vdbg_last_gemm_bits(vdbg_ctx* ctx) {
+  if (ctx == nullptr) return 0;
+  Ctx& c = ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c.mu);
+  if (c.last_gemm_gate != nullptr) {  // chosen on the device: read the flag
+    std::vector<int> v(size_t(std::max(c.last_gemm_gate_n, 1)), 0);
+    // (the scan may have run on any stream)
+    if (hipSetDevice(c.device) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
+        hipMemcpy(v.data(), c.last_gemm_gate, size_t(c.last_gemm_gate_n) * sizeof(int),
+                  hipMemcpyDeviceToHost) != hipSuccess)
+      return 0;
+    bool all = true;
+    for (int i = 0; i < c.last_gemm_gate_n; ++i) all = all && v[size_t(i)] != 0;
+    c.last_gemm_bits = all ? 8 : 32;
+    c.last_gemm_gate = nullptr;
+  }
+  return c.last_gemm_bits;
+}
 
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries) {
   if (ctx == nullptr || fallback_queries == nullptr)

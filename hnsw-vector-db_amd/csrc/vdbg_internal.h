@@ -119,6 +119,8 @@ struct Ctx {
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
   uint64_t last_fallbacks = 0;
   int last_gemm_bits = 0;  // input width of the last scan's main GEMM: 32, 16, 8 or 0
+  const int* last_gemm_gate = nullptr;  // when the batch chose its GEMM on the device: the
+  int last_gemm_gate_n = 0;             // per-query int8 flags (all 1: int8, else fp32)
   int cu_count = 256;
   int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
@@ -426,6 +428,11 @@ inline int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, siz
 // number that the host polls (far less latency than a stream synchronisation); the host
 // falls back to synchronising when the stream ends without the number showing.
 int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s);
+// The host side of ReadWords for a kernel that publishes the words itself: waits until the
+// flag carries seq (NextFlagSeq), then copies the n words to host_pinned (or, should the
+// stream end without the number showing, copies them from dev).
+uint32_t NextFlagSeq(Ctx* c);
+int WaitWords(Ctx* c, uint32_t seq, const uint32_t* dev, int n, hipStream_t s);
 
 }  // namespace vdbg
 

@@ -383,7 +383,9 @@ int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
  * (fp16 MFMA: integer rows and queries of magnitude <= 2048 with every partial sum below
  * 2^24, exactly; SQ8 codes and float rows on split operands), 8 (int8 MFMA: such integer
  * rows spanning at most 256 values, with every query value inside the same int8 window), or
- * 0 (no GEMM: the exact scan ran). */
+ * 0 (no GEMM: the exact scan ran).  Batches of at most 128 queries over such integer rows
+ * choose between the int8 and the fp32 GEMM on the device (no host round trip); for them
+ * this call waits for the device and reads the choice. */
 int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 
 /* ---------------------------------------------------------------- mutable segments */

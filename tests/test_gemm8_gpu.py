@@ -78,10 +78,17 @@ def test_query_window(ctx, oracle):
     od, oi = oracle.flat_search(base, inside, 10)
     _check_equal(gi, gd, oi, od)
     outside = inside.copy()
-    outside[13, 7] = 179  # one value past the window: the batch takes the fp16 GEMM
+    outside[13, 7] = 179  # one value past the window
+    # a batch of at most 128 queries chooses on the device between int8 and fp32
     gi, gd = ds.flat_search(outside, 10)
-    assert ctx.last_gemm_bits() == 16
+    assert ctx.last_gemm_bits() == 32
     od, oi = oracle.flat_search(base, outside, 10)
+    _check_equal(gi, gd, oi, od)
+    # a larger batch reads the flags on the host and takes the fp16 GEMM
+    big = np.ascontiguousarray(np.concatenate([outside, inside, inside, inside])[:180])
+    gi, gd = ds.flat_search(big, 10)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.flat_search(base, big, 10)
     _check_equal(gi, gd, oi, od)
     frac = inside.copy()
     frac[3, 3] += 0.5  # a fractional query value: the fp32 GEMM
@@ -182,3 +189,76 @@ def test_unit_neighbours_tie_within_the_bound(ctx, oracle):
         od, oi = oracle.flat_search(base, qs, k)
         _check_equal(gi, gd, oi, od)
         assert np.all(gd[:, 1:] == 1.0)
+
+
+@pytest.mark.parametrize("nq,k,metric", [(1, 10, "l2"), (2, 1, "l2"), (1, 48, "l2"),
+                                         (2, 10, "ip"), (7, 100, "l2"), (5, 48, "l2"),
+                                         (8, 10, "ip"), (64, 10, "l2"), (128, 20, "l2"),
+                                         (1, 10, "ip"), (33, 10, "ip")])
+def test_small_batches_choose_on_device(ctx, oracle, nq, k, metric):
+    # up to 2 queries and k <= 48: the tiny-batch path (one pass over the int8 rows keeping
+    # each chunk's best keys, one merge with the exact re-score and certificate); up to 128
+    # queries: the int8 / fp32 main pass chosen on the device, no host read before it
+    base = datagen.sift_like(60000, 128, 6601)
+    qs = datagen.sift_like(nq, 128, 6602)
+    ds = vdbg.Dataset(ctx, base, 128, metric=metric)
+    gi, gd = ds.flat_search(qs, k)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, k, metric=metric)
+    _check_equal(gi, gd, oi, od)
+    # one fractional query value: on the tiny-batch path that query alone is re-scanned
+    # exactly; other small batches move to the fp32 pass
+    qf = qs.copy()
+    qf[nq - 1, 5] += 0.25
+    gi, gd = ds.flat_search(qf, k)
+    if nq <= 2 and k <= 48:
+        assert ctx.last_gemm_bits() == 8 and ctx.last_fallbacks() == 1
+    else:
+        assert ctx.last_gemm_bits() == 32
+    od, oi = oracle.flat_search(base, qf, k, metric=metric)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("frac", [0.002, 0.3])
+def test_small_batches_filtered(ctx, oracle, frac):
+    # the fused thresholds skip sampled rows the filter rejects; at 0.2 % fewer than k of
+    # the 4096 sampled rows may pass, and the threshold is then open
+    n = 80000
+    base = datagen.sift_like(n, 128, 6611)
+    qs = datagen.sift_like(5, 128, 6612)
+    rng = np.random.default_rng(6613)
+    rows = np.sort(rng.choice(n, size=max(1, int(n * frac)), replace=False))
+    allow = np.zeros((n + 63) // 64, np.uint64)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 10, allow=allow)
+    od, oi = oracle.flat_search(base, qs, 10, allow=allow)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("nq", [1, 2])
+def test_tiny_batches_forced_fallback_and_filter(ctx, oracle, nq):
+    # the tiny-batch path with its certificate failed on purpose (every query re-scanned
+    # exactly) and with a filter that leaves whole chunks empty
+    n = 50000
+    base = datagen.sift_like(n, 128, 6621)
+    qs = datagen.sift_like(nq, 128, 6622)
+    ds = vdbg.Dataset(ctx, base, 128)
+    try:
+        ctx.set_test_fallbacks(1)
+        gi, gd = ds.flat_search(qs, 10)
+        assert ctx.last_fallbacks() == nq
+    finally:
+        ctx.set_test_fallbacks(0)
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
+    allowed = np.zeros(n, bool)
+    allowed[20000:20500] = True  # one stretch: most chunks hold no allowed row
+    allowed[::97] = True
+    words = np.zeros((n + 63) // 64, np.uint64)
+    rows = np.nonzero(allowed)[0]
+    np.bitwise_or.at(words, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    gi, gd = ds.flat_search(qs, 10, allow=words)
+    od, oi = oracle.flat_search(base, qs, 10, allow=words)
+    _check_equal(gi, gd, oi, od)
