@@ -26,10 +26,10 @@
  *    "_device" entry points take device pointers, run on the given HIP stream (NULL = the
  *    context's stream) and return once the work is queued; inputs must stay valid until the
  *    stream reaches that point.  The flat, SQ8 and IVF-PQ searches are not fully
- *    asynchronous: before queuing their later launches they read a few device-side words
- *    on the host (whether the batch fits the integer GEMM, how many queries need the
- *    exact re-scan), so such a call returns only after the stream has reached those
- *    points.
+ *    asynchronous: they read a few device-side words on the host (whether a batch of more
+ *    than 128 queries fits the integer GEMM, how many queries need the exact re-scan), so
+ *    such a call returns only after the stream has reached its last ranking kernel.  Flat
+ *    batches of at most 128 queries over integer rows make no read before that point.
  *  - All entry points on one context are serialised by the context (host threads may share
  *    it).  Calls on different streams of one context are ordered on the device where they
  *    share scratch: a call's launches wait for the previous call's last launch that reads
