@@ -10,7 +10,7 @@ Workload (one "step" = one batch search over data resident in HBM):
           nprobe 64, rerank 100 -> k = 10; built on the GPU.  Also swept over nprobe
           16/32/64/128 at rerank 0 and 100.
   flat_uniform  exact L2 over 100,000 x 128 rows uniform in [0, 1), 1,000 queries, k = 10
-          (real-valued rows: the two-part operand GEMMs with certificates).
+          (real-valued rows: the high-half fp16 GEMM with certificates).
   filtered  the collection read path: 5M unit rows of 384 dims (10,000-centre mixture, cosine)
           in 8 segments of 625,000, 2% of rows deleted, a filter passing 1%, 10% or 50% of
           rows; 4,096 raw queries go through PrepareQuery, the filtered exact scan of every
@@ -193,7 +193,7 @@ def run_filtered(args, ctx, torch, ref, threads, cpu_model):
              "gemm_ms_per_step": round(g_ms, 3),
              "gemm_TFLOPs": round(flops / (g_ms * 1e-3) / 1e12, 2) if g_ms > 0 else None,
              "mfma_inputs": {8: "i8 two-part rows x two-part queries (4 int8 MFMA products each)",
-                             16: "f16 two-part rows x two-part queries (3 MFMA products each)"}
+                             16: "f16 high halves of rows and queries (1 MFMA product each)"}
                             .get(ctx.last_gemm_bits(), "f32"),
              "kernel_ms_per_step": {kk: round(v[0] / args.steps, 4) for kk, v in prof.items()},
              "exact_rescans": fb}
@@ -440,8 +440,9 @@ def main():
     # ------------------------------------------------------------ flat, real-valued rows
     if "flat_uniform" in paths:
         # 100,000 x 128 rows uniform in [0, 1), 1,000 queries from the same distribution, k = 10:
-        # float rows rank on the two-part fp16 (or int8) operands and every answer is re-scored
-        # in the reference's AVX-512 order
+        # float rows rank on the high fp16 halves of rows and queries (one MFMA product per
+        # product, under a widened bound) and every answer is re-scored in the reference's
+        # AVX-512 order
         nu, nqu = 100_000, 1000
         ubase = datagen.uniform_rows(nu, dim, 1001)
         uq = datagen.uniform_rows(nqu, dim, 1002)
@@ -467,7 +468,7 @@ def main():
              "kernel_ms": g_ms, "achieved": ach, "peak": peak,
              "unit": "TOP/s" if bits == 8 else "TFLOP/s", "frac": ach / peak,
              "mfma_inputs": {8: "i8 two-part rows x two-part queries",
-                             16: "f16 two-part rows x two-part queries"}.get(bits, "f32"),
+                             16: "f16 high halves of rows and queries"}.get(bits, "f32"),
              "kernel_ms_per_step": {kk: v[0] / reps for kk, v in prof.items()},
              "exact_rescans": fb}
         ugi = ui.cpu().numpy().view(np.uint32).copy()

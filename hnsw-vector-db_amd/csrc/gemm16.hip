@@ -52,19 +52,27 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (
 // chunk as [h | l]; per 16-dim block the wave runs x_h q_h into one accumulator and x_h q_l,
 // x_l q_h into the other (x_l q_l, of relative size 2^-22, is left out), then the same
 // epilogue.
+//
+// SPLIT 3 (float rows, one product): the same stored rows and query operand, but only the
+// h halves take part: x_h q_h, one MFMA per product, two distinct 32-query blocks per wave
+// as in the exact path, and the epilogue fma(Qf, acc, norm).  The dropped x_h q_l + x_l q_h
+// + x_l q_l is at most (2^-10 + 2^-22) |x_i q_i| per product; k_query_prep widens the
+// query's bound by it.
 template <int PD, int METRIC, int QB, int MODE, int SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int KC = Gemm16Kc(PD, SPLIT);
   constexpr int NKC = PD / KC;
   constexpr int NKB = KC / 16;                     // 16-dim MFMA K blocks per stage
-  constexpr int XP = SPLIT == 2 ? 2 : 1;           // fp16 parts per row value
-  constexpr int ROWW = XP * PD;                    // fp16 row width in halfs
+  constexpr int XP = SPLIT == 2 ? 2 : 1;           // fp16 parts per staged row value
+  constexpr int XS = SPLIT >= 2 ? 2 : 1;           // fp16 parts per stored row value
+  constexpr int ROWW = XS * PD;                    // fp16 row width in halfs
   constexpr int SKC = XP * KC;                     // stage width in halfs
+  constexpr int CSTR = XS * KC;                    // stored K chunk width in halfs
   constexpr int STR = SKC + 8;                     // LDS row stride in halfs (16 B padding)
   constexpr int VEC_PER_ROW = SKC / 8;             // uint4 = 8 halfs
   constexpr int VEC_PER_TILE = kGemmRows * VEC_PER_ROW;
   constexpr int VEC_PER_THREAD = (VEC_PER_TILE + 255) / 256;
-  constexpr int NQB = SPLIT ? 1 : QB;              // distinct 32-query blocks per wave
+  constexpr int NQB = (SPLIT == 1 || SPLIT == 2) ? 1 : QB;  // distinct 32-query blocks per wave
   constexpr int QT = 128 * NQB;                    // queries per block
   static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
   static_assert(!SPLIT || QB == 2, "the split operand takes both register sets");
@@ -90,10 +98,11 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   float T[NQB];
   uint2* out[NQB];
   uint32_t cnt[NQB];
-  const float qf = SPLIT ? a.Qf[min(q0 + j, a.nq - 1)] : 1.f;  // split: GEMM-unit factor
+  float qf[NQB];  // split operands: the GEMM-unit factor of the lane's query
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     q[qb] = q0 + qb * 32 + j;
+    qf[qb] = SPLIT ? a.Qf[min(q[qb], a.nq - 1)] : 1.f;
     cnt[qb] = 0;
     if constexpr (MODE == 0) {
       T[qb] = q[qb] < a.nq ? a.T[q[qb]] : -__builtin_inff();
@@ -112,8 +121,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   const uint16_t* qrow[QB];
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb)
-    qrow[qb] = SPLIT ? a.Q16 + (size_t(min(q[0], a.nq - 1)) * 2 + qb) * PD + h * 8
-                     : a.Q16 + size_t(min(q[qb], a.nq - 1)) * PD + h * 8;
+    qrow[qb] = SPLIT == 3 ? a.Q16 + size_t(min(q[qb], a.nq - 1)) * 2 * PD + h * 8
+               : SPLIT    ? a.Q16 + (size_t(min(q[0], a.nq - 1)) * 2 + qb) * PD + h * 8
+                          : a.Q16 + size_t(min(q[qb], a.nq - 1)) * PD + h * 8;
   auto load_q = [&](int f, int kc) {
 #pragma unroll
     for (int qb = 0; qb < QB; ++qb)
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
     const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
     const uint32_t valid = min(uint32_t(kGemmRows), r_end - base);  // >= 1
-    const char* src = reinterpret_cast<const char*>(a.X16 + size_t(base) * ROWW + kc * SKC);
+    const char* src = reinterpret_cast<const char*>(a.X16 + size_t(base) * ROWW + kc * CSTR);
     if (valid == kGemmRows) {  // a full tile: the precomputed lane offsets
 #pragma unroll
       for (int i = 0; i < VEC_PER_THREAD; ++i)
@@ -260,8 +270,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
         }
     }
     auto value = [&](int qb, int blk, int r) {
-      if constexpr (SPLIT)
-        return fmaf(qf, acc[0][blk][r] + acc[1][blk][r], xn[blk][r]);
+      if constexpr (SPLIT == 3)
+        return fmaf(qf[qb], acc[qb][blk][r], xn[blk][r]);
+      else if constexpr (SPLIT)
+        return fmaf(qf[0], acc[0][blk][r] + acc[1][blk][r], xn[blk][r]);
       else
         return acc[qb][blk][r];
     };
@@ -356,6 +368,9 @@ static void launch16_pm(int qb, int mode, int split, hipStream_t s, int blocks,
   } else if (split == 2) {
     if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 2><<<g, t, 0, s>>>(a);
     else k_gemm16<PD, METRIC, 2, 1, 2><<<g, t, 0, s>>>(a);
+  } else if (split == 3) {
+    if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 3><<<g, t, 0, s>>>(a);
+    else k_gemm16<PD, METRIC, 2, 1, 3><<<g, t, 0, s>>>(a);
   } else if (mode == 0) {
     if (qb == 1) k_gemm16<PD, METRIC, 1, 0, 0><<<g, t, 0, s>>>(a);
     else k_gemm16<PD, METRIC, 2, 0, 0><<<g, t, 0, s>>>(a);

@@ -450,6 +450,7 @@ struct PrepArgs {
   int* fit8q;     // nullable: per query, 1 when it is inside the int8 GEMM's bounds
   int c8;
   uint32_t* mb8;  // nullable: SQ8 on the int8 GEMM, the batch's max |B| (float bits, atomicMax)
+  int single16;   // float rows ranked on the h halves alone (gemm16.hip SPLIT 3)
 };
 
 // One wave per query.
@@ -619,11 +620,17 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
         a.metric != 0 ? (2.0 * pd + 16.0 + 6.0 * pd + 48.0) * u * sqrt(double(qmag) * double(a.rmag)) + fsub
                       : (4.0 * pd + 16.0 + 6.0 * pd + 48.0) * u * (double(qmag) + double(a.rmag)) +
                             2.0 * fsub;
+    // Float rows on the h halves alone (x_h q_h): the dropped x_h q_l + x_l q_h + x_l q_l is
+    // at most (2^-10 + 2^-22) |x_i q_i| per product (each h within 2^-11 of its value), so
+    // (2^-10 + 2^-21) |q||x| on the dot, twice that on the L2 form's 2 q.x.
+    const double drop = ldexp(1.0, -10) + ldexp(1.0, -21);
+    const double bound16h =
+        bound16f + (a.metric != 0 ? drop * sqrt(double(qmag) * double(a.rmag))
+                                  : drop * (double(qmag) + double(a.rmag)));
     const bool split = a.Q16 != nullptr && (a.kind == 1 || a.x16_parts == 2);
+    const double bsplit = a.kind == 1 ? bound16 : (a.single16 ? bound16h : bound16f);
     a.exact[q] = ex && !half_norm ? 1 : 0;
-    a.eb[q] = half_norm ? 1.f
-                        : ex ? 0.f
-                             : float((split ? (a.kind == 1 ? bound16 : bound16f) : bound) * 1.001);
+    a.eb[q] = half_norm ? 1.f : ex ? 0.f : float((split ? bsplit : bound) * 1.001);
   }
 }
 
@@ -2177,8 +2184,12 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const bool try8s = try16 && c->int8_gemm && src->kind == 1 && Gemm8Supported(pd);
   // (float rows only for GEMMs large enough to repay the batch's operand pass and flag
   // readback: the fp16 split GEMM costs about 2 N nq pd / 2e14 s, the int8 one 0.6 of that)
-  const bool try8f = c->fp16_gemm && c->int8_gemm && split == 2 && src->X8 != nullptr &&
-                     src->x8_parts == 2 && Gemm8Supported(pd) &&
+  // Float rows may instead rank on the h halves of their fp16 copy alone (one fp16 MFMA per
+  // product, SPLIT 3) under the wider bound; that replaces both the split and the int8 pass.
+  const bool single = split == 2 && try16 && c->fp16_single;
+  const int split16 = single ? 3 : split;  // the fp16 GEMM's operand mode
+  const bool try8f = c->fp16_gemm && c->int8_gemm && split == 2 && !single &&
+                     src->X8 != nullptr && src->x8_parts == 2 && Gemm8Supported(pd) &&
                      double(N) * double(nq) * double(pd) >= c->int8_float_min_work;
   const bool try8op = try8s || try8f;  // the two-part query operand (k_sq8_operand8)
   const bool try8any = try8 || try8op;
@@ -2228,9 +2239,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int slots8 = (try8op ? (try8f ? 2 : Gemm8Occupancy(pd)) : Gemm8Occupancy(pd)) * c->cu_count;
   auto plan_all = [&](Plan* p32, Plan* p16, Plan* p8, int max_chunks) {
     *p32 = make_plan(1, 128, slots, max_chunks);
-    *p16 = split ? make_plan(2, 128, slots, max_chunks)
-                 : (nq > 128 ? make_plan(2, 256, slots, max_chunks)
-                             : make_plan(1, 128, slots, max_chunks));
+    *p16 = single  ? make_plan(2, 256, slots, max_chunks)
+           : split ? make_plan(2, 128, slots, max_chunks)
+                   : (nq > 128 ? make_plan(2, 256, slots, max_chunks)
+                               : make_plan(1, 128, slots, max_chunks));
     *p8 = try8op ? make_plan(2, 128, slots8, max_chunks)
                  : (nq > 128 ? make_plan(2, 256, slots8, max_chunks) : *p16);
   };
@@ -2310,7 +2322,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   PrepArgs pa{Q, Qb, int(nq), int(pd), src->kind, src->metric, src->stats, src->rmag,
               src->vmin, src->scale, shift, eb, exact, Q16, all16, Qf, src->x16_parts,
               src->x16_exp, try8 ? Q8 : nullptr, try8 ? Qd : nullptr, try8 ? all8 : nullptr,
-              fit8q, src->c8, mb8};
+              fit8q, src->c8, mb8, single ? 1 : 0};
   {
     ProfScope ps(c, "query_prep", s);
     k_query_prep<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(pa);
@@ -2381,7 +2393,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       sg.Q16 = Q16;
       sg.Qf = Qf;
       GemmGrid(sg, P.nqt, P.schunks, &sblocks);
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, split, s, sblocks, sg));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, split16, s, sblocks, sg));
     } else {
       // the fp32 sample pass runs 128-query tiles
       GemmGrid(sg, p32.nqt, p32.schunks, &sblocks);
@@ -2449,7 +2461,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       ga.Qf = Qf;
       ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
       ga.aw_mask = allow != nullptr ? ~0u : 0u;
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, split, s, blocks, ga));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, split16, s, blocks, ga));
     } else {
       VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
     }

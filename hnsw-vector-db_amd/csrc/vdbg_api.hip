@@ -225,7 +225,9 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
       return rc;
     }
   }
-  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr) {
+  // (float rows ranking on the fp16 h halves need no int8 copy)
+  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr &&
+      (d.rows16_parts == 1 || !c->fp16_single)) {
     if (d.rows16_parts == 1) {
       rc = MakeRows8(c, c->stream, d.rows, n, pd, metric, d.stats, &d.rows8, &d.init8, &d.c8);
     } else {
@@ -469,6 +471,13 @@ int vdbg_ctx_set_host_threads(vdbg_ctx* ctx, int n) {
   if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
   std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
   ctx->c.host_threads = n > 0 ? n : 0;
+  return kOk;
+}
+
+int vdbg_ctx_set_fp16_single(vdbg_ctx* ctx, int enable) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.fp16_single = enable != 0;
   return kOk;
 }
 

@@ -127,6 +127,7 @@ struct Ctx {
   int test_fallbacks = 0;      // testing: 1 fails every first certificate (second chance),
                                // 2 also every second one (exact re-scan)
   bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
+  bool fp16_single = true;     // float rows rank on the h halves alone (gemm16.hip SPLIT 3)
   bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
   double int8_float_min_work = 2e10;  // float rows: smallest N nq pd for the int8 GEMM
   int host_threads = 0;        // host threads of the HNSW walk; 0 = DefaultHostThreads()

@@ -99,6 +99,7 @@ _SIGS = {
     "vdbg_sq8_hnsw_search_device": (C.c_int, [_vp, _vp, _sz, _sz, _sz, C.c_int, _vp, _vp, _vp,
                                               _vp, _vp]),
     "vdbg_ctx_set_host_threads": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_fp16_single": (C.c_int, [_vp, C.c_int]),
     "vdbg_dataset_create_appendable": (C.c_int, [_vp, _sz, _sz, C.c_int, _sz, C.POINTER(_vp)]),
     "vdbg_dataset_append": (C.c_int, [_vp, _vp, _sz, _vp, C.POINTER(C.c_uint64)]),
     "vdbg_dataset_size": (C.c_int, [_vp, C.POINTER(C.c_uint64)]),
@@ -219,6 +220,10 @@ class Context:
 
     def set_host_threads(self, n):
         _check(lib.vdbg_ctx_set_host_threads(self.h, n))
+
+    def set_fp16_single(self, enable):
+        """Float rows rank on the high fp16 half alone (one MFMA per product)."""
+        _check(lib.vdbg_ctx_set_fp16_single(self.h, 1 if enable else 0))
 
     def set_test_fallbacks(self, level):
         """Testing: 1 fails every first certificate of the flat / SQ8 scans (second chance),

@@ -1,4 +1,5 @@
-"""Float rows on the two-part GEMMs.  With the int8 GEMM on (the default), rows and queries
+"""Float rows on the two-part GEMMs, and on the high fp16 halves alone (the default, last
+tests).  With the high-half ranking off and the int8 GEMM on, rows and queries
 scaled by powers of two are rounded to integers and split into int8 h + l parts, ranked by
 2^16 h.h + 2^8 (h.l + l.h) + l.l under a bound widened for the rounding; with it off, they
 are split into fp16 h + l parts and ranked by x_h q_h + x_h q_l + x_l q_h.  Returned ids and
@@ -16,10 +17,13 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture(autouse=True)
 def _int8_at_any_size(ctx):
-    # the test batches are small: let them take the int8 two-part GEMM whatever their size
+    # the two-part paths: the high-half fp16 ranking off (datasets then keep an int8 copy),
+    # and the test batches take the int8 two-part GEMM whatever their size
+    ctx.set_fp16_single(False)
     ctx.set_int8_float_min_work(0)
     yield
     ctx.set_int8_float_min_work(2e10)
+    ctx.set_fp16_single(True)
 
 
 def _check_equal(gi, gd, oi, od):
@@ -118,4 +122,49 @@ def test_split_large_batch(ctx, oracle, kind, metric):
     assert ctx.last_gemm_bits() in (8, 16)
     assert ctx.last_fallbacks() == 0
     od, oi = oracle.flat_search(base, qs, 10, metric=metric)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.fixture
+def single(ctx):
+    ctx.set_fp16_single(True)
+    yield ctx
+    ctx.set_fp16_single(False)
+
+
+_CASES = [("uniform", "l2", 128, 30000, 200, 10), ("unit", "cosine", 384, 30000, 150, 10),
+          ("normal", "l2", 96, 20000, 130, 50), ("unit", "ip", 112, 20000, 100, 10),
+          ("wide", "l2", 64, 20000, 100, 10), ("wide", "ip", 128, 20000, 100, 20),
+          ("normal", "l2", 1024, 8000, 64, 10), ("normal", "ip", 37, 20000, 64, 20),
+          ("unit", "cosine", 256, 20000, 300, 10)]
+
+
+@pytest.mark.parametrize("kind,metric,dim,n,nq,k", _CASES)
+def test_single_part_matches_oracle(single, oracle, kind, metric, dim, n, nq, k):
+    # float rows ranked on the high fp16 halves alone (one MFMA per product), the bound
+    # widened by (2^-10 + 2^-21) |q||x|: same ids and distances as the oracle
+    ctx = single
+    print(f"single16 {kind} {metric} dim={dim} n={n} nq={nq} k={k}", flush=True)
+    base, qs = _data(kind, n, nq, dim, 7301 + dim)
+    pd = vdbg.padded_dim(dim)
+    base, qs = datagen.pad(base, pd), datagen.pad(qs, pd)
+    ds = vdbg.Dataset(ctx, base, dim, metric=metric)
+    gi, gd = ds.flat_search(qs, k)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.flat_search(base, qs, k, metric=metric)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("frac", [0.15, 0.7])
+def test_single_part_filtered(single, oracle, frac):
+    ctx = single
+    n, dim = 40000, 384
+    base, qs = _data("unit", n, 128, dim, 7111)
+    rows = np.nonzero(np.random.default_rng(7112).random(n) < frac)[0]
+    allow = np.zeros((n + 63) // 64, np.uint64)
+    np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, dim, metric="cosine")
+    gi, gd = ds.flat_search(qs, 10, allow=allow)
+    assert ctx.last_gemm_bits() == 16
+    od, oi = oracle.flat_search(base, qs, 10, metric="cosine", allow=allow)
     _check_equal(gi, gd, oi, od)
