@@ -76,8 +76,6 @@ __host__ __device__ constexpr int GemmKc(int pd) {
 // staging register sets and two sets of query fragments (the next chunk's load a step
 // ahead) within the wave's registers.
 __host__ __device__ constexpr int Gemm16Kc(int pd, int split) {
-  // split 3 reads the h halves of the split-2 layout, so it stages the same chunks
-  if (split == 3) split = 2;
   if (split != 2 && pd <= 128) return pd;
   if (split == 2 && pd <= 64) return pd;
   for (int kc = 64; kc > 16; kc -= 16)

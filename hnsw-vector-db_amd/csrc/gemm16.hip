@@ -53,18 +53,18 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (
 // x_l q_h into the other (x_l q_l, of relative size 2^-22, is left out), then the same
 // epilogue.
 //
-// SPLIT 3 (float rows, one product): the same stored rows and query operand, but only the
-// h halves take part: x_h q_h, one MFMA per product, two distinct 32-query blocks per wave
-// as in the exact path, and the epilogue fma(Qf, acc, norm).  The dropped x_h q_l + x_l q_h
-// + x_l q_l is at most (2^-10 + 2^-22) |x_i q_i| per product; k_query_prep widens the
-// query's bound by it.
+// SPLIT 3 (float rows, one product): rows held as their h halves alone (fp16(x 2^sx), one
+// part, whole rows as in the exact path) against the h part of the split query operand:
+// x_h q_h, one MFMA per product, two distinct 32-query blocks per wave, and the epilogue
+// fma(Qf, acc, norm).  The dropped x_h q_l + x_l q_h + x_l q_l is at most
+// (2^-10 + 2^-22) |x_i q_i| per product; k_query_prep widens the query's bound by it.
 template <int PD, int METRIC, int QB, int MODE, int SPLIT>
 __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int KC = Gemm16Kc(PD, SPLIT);
   constexpr int NKC = PD / KC;
   constexpr int NKB = KC / 16;                     // 16-dim MFMA K blocks per stage
   constexpr int XP = SPLIT == 2 ? 2 : 1;           // fp16 parts per staged row value
-  constexpr int XS = SPLIT >= 2 ? 2 : 1;           // fp16 parts per stored row value
+  constexpr int XS = SPLIT == 2 ? 2 : 1;           // fp16 parts per stored row value
   constexpr int ROWW = XS * PD;                    // fp16 row width in halfs
   constexpr int SKC = XP * KC;                     // stage width in halfs
   constexpr int CSTR = XS * KC;                    // stored K chunk width in halfs
@@ -410,6 +410,13 @@ __global__ void k_to_f16(const float* __restrict__ x, size_t n, uint16_t* __rest
   if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(x[i]));
 }
 
+// Rows as their h halves alone: fp16(x 2^e).
+__global__ void k_to_f16_scaled(const float* __restrict__ x, size_t n, int e,
+                                uint16_t* __restrict__ y) {
+  const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
+  if (i < n) y[i] = __builtin_bit_cast(uint16_t, _Float16(ldexpf(x[i], e)));
+}
+
 // Two-part fp16 rows: x 2^e = h + l (h = fp16(x 2^e), l = fp16(x 2^e - h)), stored per
 // K chunk of kc dims as [h | l].
 __global__ void k_to_f16_split(const float* __restrict__ x, size_t n, int pd, int kc, int e,
@@ -428,10 +435,11 @@ __global__ void k_to_f16_split(const float* __restrict__ x, size_t n, int pd, in
 }
 
 int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int* parts, int* exp,
-               const RowStats& st, uint16_t** out) {
+               int* approx, const RowStats& st, uint16_t** out) {
   *out = nullptr;
   *parts = 1;
   *exp = 0;
+  *approx = 0;
   if (n == 0 || !GemmSupported(pd) || !(st.max_abs <= 3.0e38f)) return kOk;
   const bool exact = st.all_int && st.max_abs <= 2048.f;
   if (!exact) {
@@ -439,12 +447,14 @@ int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, in
     int ex = 0;
     if (st.max_abs > 0.f) (void)frexpf(st.max_abs, &ex);
     *exp = st.max_abs > 0.f ? 15 - ex : 0;
-    *parts = 2;
+    if (c->fp16_single) *approx = 1; else *parts = 2;
   }
   uint16_t* y = nullptr;
   VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&y), n * pd * *parts * sizeof(uint16_t)));
   if (exact)
     k_to_f16<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, y);
+  else if (*approx)
+    k_to_f16_scaled<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(rows, n * pd, *exp, y);
   else
     k_to_f16_split<<<dim3(unsigned((n * pd + 255) / 256)), 256, 0, s>>>(
         rows, n * pd, int(pd), Gemm16Kc(int(pd), 2), *exp, y);

@@ -443,14 +443,14 @@ struct PrepArgs {
   int* all16;     // nullable: cleared when a query is outside the fp16 GEMM's bounds
   float* Qf;      // split operands: per-query factor taking the split GEMM back to GEMM units
   int x16_parts;  // flat rows: 2 when they are held as scaled fp16 h + l pairs
-  int x16_exp;    // their scale exponent
+  int x16_exp;    // their scale exponent (two parts, or the h halves alone: single16)
   int8_t* Q8;     // nullable: the int8 GEMM's B operand, q - c8 (gemm8.hip)
   int* Qd;        // its per-query constant M c8 sum(q) - c8^2 pd
   int* all8;      // cleared when a query is outside the int8 GEMM's bounds
   int* fit8q;     // nullable: per query, 1 when it is inside the int8 GEMM's bounds
   int c8;
   uint32_t* mb8;  // nullable: SQ8 on the int8 GEMM, the batch's max |B| (float bits, atomicMax)
-  int single16;   // float rows ranked on the h halves alone (gemm16.hip SPLIT 3)
+  int single16;   // float rows held as their scaled h halves alone (gemm16.hip SPLIT 3)
 };
 
 // One wave per query.
@@ -482,7 +482,7 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
       a.Q8[size_t(q) * a.pd + i] = int8_t(int(fminf(fmaxf(d, -128.f), 127.f)));
       sq += e;
     }
-    if (a.Q16 != nullptr && a.kind == 0 && a.x16_parts == 1)  // -2 q (L2) or -q (IP)
+    if (a.Q16 != nullptr && a.kind == 0 && a.x16_parts == 1 && !a.single16)  // -2 q or -q
       a.Q16[size_t(q) * a.pd + i] =
           __builtin_bit_cast(uint16_t, _Float16(a.metric == 0 ? -2.f * e : -e));
     if (a.kind == 1) {
@@ -514,8 +514,9 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
   // fp16, so the GEMM runs as c.h + c.l and Qf = -2 (L2) or -1 (IP) times 2^-sc takes it back
   int sc = 0;
   bool split_ok = true;
-  if (a.kind == 0 && a.x16_parts == 2 && a.Q16 != nullptr) {
-    // float rows held as h + l: q 2^sc split the same way (max |q| 2^sc in [2^14, 2^15))
+  if (a.kind == 0 && (a.x16_parts == 2 || a.single16) && a.Q16 != nullptr) {
+    // float rows held as h + l (or h alone): q 2^sc split the same way (max |q| 2^sc in
+    // [2^14, 2^15))
     split_ok = ma <= 3.0e38f;
     if (split_ok && ma > 0.f) {
       int ex = 0;
@@ -572,7 +573,7 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
     // magnitude <= 4096); the fp16 GEMM accumulates ||x||^2 - 2 q.x (or -q.x) from the row
     // norm, every partial sum bounded by (|q| + R)^2 with R the largest row norm.  Below 2^24
     // its values are the fp32 GEMM's bit for bit.
-    if (a.Qf != nullptr && (a.kind == 1 || a.x16_parts == 2)) {
+    if (a.Qf != nullptr && (a.kind == 1 || a.x16_parts == 2 || a.single16)) {
       a.Qf[q] = ldexpf(a.metric == 0 ? -2.f : -1.f, -sc - (a.kind == 0 ? a.x16_exp : 0));
       if (!split_ok) atomicAnd(a.all16, 0);
     } else if (a.all16 != nullptr || a.fit8q != nullptr) {
@@ -627,7 +628,7 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
     const double bound16h =
         bound16f + (a.metric != 0 ? drop * sqrt(double(qmag) * double(a.rmag))
                                   : drop * (double(qmag) + double(a.rmag)));
-    const bool split = a.Q16 != nullptr && (a.kind == 1 || a.x16_parts == 2);
+    const bool split = a.Q16 != nullptr && (a.kind == 1 || a.x16_parts == 2 || a.single16);
     const double bsplit = a.kind == 1 ? bound16 : (a.single16 ? bound16h : bound16f);
     a.exact[q] = ex && !half_norm ? 1 : 0;
     a.eb[q] = half_norm ? 1.f : ex ? 0.f : float((split ? bsplit : bound) * 1.001);
@@ -2070,7 +2071,7 @@ static bool TinyEligible(const Ctx* c, const ScanSource& src, size_t nq, size_t 
                          const Workspace& w) {
   return nq >= 1 && nq <= size_t(kTinyQ) && kk <= size_t(kTinyK) && src.kind == 0 &&
          src.metric <= 1 && src.X8 != nullptr && src.x8_parts == 1 && src.init8 != nullptr &&
-         c->fp16_gemm && c->int8_gemm && src.x16_parts == 1 &&
+         c->fp16_gemm && c->int8_gemm && src.x16_parts == 1 && !src.x16_approx &&
          (src.pd == 64 || src.pd == 128 || src.pd == 256) && src.N >= 1024 && !w.fixed;
 }
 
@@ -2176,7 +2177,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // each LDS row fragment feeding two MFMAs), or 128 for batches of at most 128 queries
   const int slots = 2 * c->cu_count;
   const bool try16 = c->fp16_gemm && src->X16 != nullptr;
-  const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : 0);
+  // the fp16 GEMM's operand mode (gemm16.hip): exact rows 0, SQ8 codes 1, float rows in two
+  // parts 2, float rows as their h halves alone 3 (one fp16 MFMA per product, ranked under
+  // the wider bound, replacing both the split and the int8 pass)
+  const int split = src->kind == 1 ? 1 : (src->x16_parts == 2 ? 2 : (src->x16_approx ? 3 : 0));
   // integer rows spanning at most 256 values may rank on the int8 GEMM (gemm8.hip)
   const bool try8 = try16 && c->int8_gemm && split == 0 && src->X8 != nullptr;
   // SQ8 codes may rank on the int8 GEMM with the query operand in two int8 parts, float rows
@@ -2184,11 +2188,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const bool try8s = try16 && c->int8_gemm && src->kind == 1 && Gemm8Supported(pd);
   // (float rows only for GEMMs large enough to repay the batch's operand pass and flag
   // readback: the fp16 split GEMM costs about 2 N nq pd / 2e14 s, the int8 one 0.6 of that)
-  // Float rows may instead rank on the h halves of their fp16 copy alone (one fp16 MFMA per
-  // product, SPLIT 3) under the wider bound; that replaces both the split and the int8 pass.
-  const bool single = split == 2 && try16 && c->fp16_single;
-  const int split16 = single ? 3 : split;  // the fp16 GEMM's operand mode
-  const bool try8f = c->fp16_gemm && c->int8_gemm && split == 2 && !single &&
+  const bool single = split == 3 && try16;
+  const bool try8f = c->fp16_gemm && c->int8_gemm && split == 2 &&
                      src->X8 != nullptr && src->x8_parts == 2 && Gemm8Supported(pd) &&
                      double(N) * double(nq) * double(pd) >= c->int8_float_min_work;
   const bool try8op = try8s || try8f;  // the two-part query operand (k_sq8_operand8)
@@ -2393,7 +2394,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       sg.Q16 = Q16;
       sg.Qf = Qf;
       GemmGrid(sg, P.nqt, P.schunks, &sblocks);
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, split16, s, sblocks, sg));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, split, s, sblocks, sg));
     } else {
       // the fp32 sample pass runs 128-query tiles
       GemmGrid(sg, p32.nqt, p32.schunks, &sblocks);
@@ -2461,7 +2462,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       ga.Qf = Qf;
       ga.aw = allow != nullptr ? reinterpret_cast<const uint32_t*>(allow) : ones;
       ga.aw_mask = allow != nullptr ? ~0u : 0u;
-      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, split16, s, blocks, ga));
+      VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, P.qb, 0, split, s, blocks, ga));
     } else {
       VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 0, s, blocks, ga));
     }

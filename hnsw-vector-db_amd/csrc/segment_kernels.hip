@@ -114,13 +114,13 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t nwords = (size_t(N) + 63) / 64;
   const size_t row_bytes = src->kind == 0 ? pd * sizeof(float) : pd;
   void* buf = nullptr;
-  // Float rows: a batch large enough for the int8 two-part GEMM ranks on it, so their fp16
-  // pairs are not gathered (a batch failing the int8 check then takes the fp32 GEMM);
-  // smaller batches, and every batch when float rows rank on the fp16 h halves alone, keep
-  // the fp16 pairs and skip the int8 copy.
+  // Float rows in two parts: a batch large enough for the int8 two-part GEMM ranks on it, so
+  // their fp16 pairs are not gathered (a batch failing the int8 check then takes the fp32
+  // GEMM); smaller batches keep the fp16 pairs and skip the int8 copy.  (Float rows held as
+  // fp16 h halves alone have no int8 copy.)
   bool keep16 = src->X16 != nullptr, keep8 = src->X8 != nullptr;
   if (src->kind == 0 && src->x16_parts == 2 && src->x8_parts == 2 && keep8) {
-    const bool int8 = c->fp16_gemm && c->int8_gemm && !c->fp16_single && Gemm8Supported(pd) &&
+    const bool int8 = c->fp16_gemm && c->int8_gemm && Gemm8Supported(pd) &&
                       double(count) * double(nq) * double(pd) >= c->int8_float_min_work;
     (int8 ? keep16 : keep8) = false;
   }

@@ -216,8 +216,8 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   }
   if (n > 0) {
     if (c->fp16_gemm)
-      rc = MakeRows16(c, c->stream, d.rows, n, pd, &d.rows16_parts, &d.rows16_exp, d.stats,
-                      &d.rows16);
+      rc = MakeRows16(c, c->stream, d.rows, n, pd, &d.rows16_parts, &d.rows16_exp,
+                      &d.rows16_approx, d.stats, &d.rows16);
     if (rc != kOk) {
       (void)hipFree(d.rows);
       (void)hipFree(d.norms);
@@ -226,8 +226,7 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
     }
   }
   // (float rows ranking on the fp16 h halves need no int8 copy)
-  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr &&
-      (d.rows16_parts == 1 || !c->fp16_single)) {
+  if (n > 0 && c->fp16_gemm && c->int8_gemm && d.rows16 != nullptr && !d.rows16_approx) {
     if (d.rows16_parts == 1) {
       rc = MakeRows8(c, c->stream, d.rows, n, pd, metric, d.stats, &d.rows8, &d.init8, &d.c8);
     } else {
@@ -255,6 +254,7 @@ static int CreateDataset(vdbg_ctx* ctx, const float* rows, bool rows_on_device, 
   d.src.x8_l2max = d.rows8_l2max;
   d.src.x16_parts = d.rows16_parts;
   d.src.x16_exp = d.rows16_exp;
+  d.src.x16_approx = d.rows16_approx;
   d.src.rn = d.norms;
   d.src.N = static_cast<uint32_t>(n);
   d.src.pd = static_cast<int>(pd);

@@ -127,7 +127,8 @@ struct Ctx {
   int test_fallbacks = 0;      // testing: 1 fails every first certificate (second chance),
                                // 2 also every second one (exact re-scan)
   bool fp16_gemm = true;       // flat and SQ8 scans may rank on the fp16 GEMM (gemm16.hip)
-  bool fp16_single = true;     // float rows rank on the h halves alone (gemm16.hip SPLIT 3)
+  bool fp16_single = true;     // new float datasets hold their fp16 h halves alone
+                               // (x16_approx, gemm16.hip SPLIT 3) instead of h + l pairs
   bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
   double int8_float_min_work = 2e10;  // float rows: smallest N nq pd for the int8 GEMM
   int host_threads = 0;        // host threads of the HNSW walk; 0 = DefaultHostThreads()
@@ -148,6 +149,8 @@ struct ScanSource {
                                   // per K chunk), kind 1 codes exactly (x16_parts 1)
   int x16_parts = 1;
   int x16_exp = 0;
+  int x16_approx = 0;           // kind 0 float rows held as fp16(x 2^x16_exp) alone (one part,
+                                // ranked under a widened bound, gemm16.hip SPLIT 3)
   const int8_t* X8 = nullptr;   // kind 0 rows for the int8 GEMM (gemm8.hip), or null: integer
                                 // rows - c8 (x8_parts 1), or float rows 2^x8_exp-scaled and
                                 // rounded, as int8 h + l pairs ([h | l] per K chunk, x8_parts 2)
@@ -182,7 +185,7 @@ struct Dataset {
   float* rows = nullptr;   // n x pd
   float* norms = nullptr;  // n row norms (fp32, ||x||^2)
   uint16_t* rows16 = nullptr;  // fp16 copy of the rows (see ScanSource::X16)
-  int rows16_parts = 1, rows16_exp = 0;
+  int rows16_parts = 1, rows16_exp = 0, rows16_approx = 0;
   int8_t* rows8 = nullptr;     // int8 copy of the rows (see ScanSource::X8)
   int* init8 = nullptr;
   int c8 = 0;
@@ -305,6 +308,7 @@ int MakeCodes16(Ctx* c, hipStream_t s, const uint8_t* codes, size_t n, size_t pd
 // (*parts 1), other finite rows as h + l parts of x 2^*exp (*parts 2); null when pd has no
 // GEMM kernel.
 int MakeRows16(Ctx* c, hipStream_t s, const float* rows, size_t n, size_t pd, int* parts, int* exp,
+               int* approx,
                const RowStats& st, uint16_t** out);
 // int8 copy of integer rows spanning at most 256 values, shifted by *shift, with each row's
 // accumulator start (gemm8.hip); *out stays null when not applicable.

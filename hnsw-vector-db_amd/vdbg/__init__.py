@@ -222,7 +222,8 @@ class Context:
         _check(lib.vdbg_ctx_set_host_threads(self.h, n))
 
     def set_fp16_single(self, enable):
-        """Float rows rank on the high fp16 half alone (one MFMA per product)."""
+        """Float datasets created from now on hold their high fp16 halves alone (one MFMA
+        per product) instead of two-part pairs."""
         _check(lib.vdbg_ctx_set_fp16_single(self.h, 1 if enable else 0))
 
     def set_test_fallbacks(self, level):

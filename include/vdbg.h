@@ -104,11 +104,12 @@ int vdbg_ctx_set_fp16_gemm(vdbg_ctx* ctx, int enable);
  * (1 byte per value and 4 per row for integer rows, 2 bytes per value for float rows).
  * Returned results are identical either way.  No counterpart in the reference. */
 int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable);
-/* Whether float rows rank on the high fp16 half of their two-part copy alone (default 1):
- * one fp16 MFMA per product instead of three (fp16 split) or four int8 ones, under a bound
- * widened by (2^-10 + 2^-21) |q||x|.  Float datasets created while it is on keep no int8
- * copy (with it off later they rank on the fp16 split).  Returned results are identical
- * either way.  No counterpart in the reference. */
+/* How float datasets created from now on hold their fp16 copy (default 1): on, as the high
+ * fp16 halves fp16(x 2^e) alone (2 bytes per value, no int8 copy), ranked with one fp16 MFMA
+ * per product under a bound widened by (2^-10 + 2^-21) |q||x|; off, as two-part h + l pairs
+ * (4 bytes per value, plus the int8 copy while the int8 GEMM is on), ranked with three fp16
+ * or four int8 MFMAs per product.  A dataset keeps the form it was created with.  Returned
+ * results are identical either way.  No counterpart in the reference. */
 int vdbg_ctx_set_fp16_single(vdbg_ctx* ctx, int enable);
 /* The smallest rows x queries x padded_dim product of a float-row batch that ranks on the
  * int8 GEMM (default 2e10; smaller batches keep the fp16 split GEMM, whose extra operand pass
