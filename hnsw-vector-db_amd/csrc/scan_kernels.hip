@@ -10,8 +10,10 @@
 //                  exact distance, and a bound on their difference (zero when integer data
 //                  makes every partial sum exact).
 //   k_gemm (MODE 1) on a strided sample of rows: per lane the minimum GEMM value of each
-//                  16-row group.  k_kth turns the kk-th smallest group minimum into an
-//                  admission threshold that provably keeps the top kk.
+//                  16-row group.  k_kth turns the r-th smallest group minimum into an
+//                  admission threshold: r = kk provably keeps the top kk; a smaller r
+//                  (ThresholdRank) keeps them except with probability below 1e-6, and
+//                  k_select's certificate checks that they were kept.
 //   k_gemm (MODE 0) Q.X^T (or Q''.C^T over codes) on fp32 MFMA (v_mfma_f32_32x32x2f32),
 //                  rows streamed through LDS; the epilogue compares with the threshold and
 //                  appends the few passing rows to per-(query, chunk, half) buffers.
@@ -998,15 +1000,17 @@ __global__ __launch_bounds__(256, 2) void k_gemm(GemmArgs a) {
 
 struct KthArgs {
   const float* gm;
-  int ngroups, nq, kk;
+  int ngroups, nq, rank;  // the rank of the group minimum taken (ThresholdRank)
   const float* eb;
   float* T;
 };
 
 
-// One wave per query: the kk-th smallest group minimum A.  The kk groups at or below A hold
-// kk distinct rows with GEMM value <= A, so the kk-th smallest exact distance is at most
-// A + shift + eb and every row of the true top kk has GEMM value <= A + 2 eb.
+// One wave per query: the rank-th smallest group minimum A.  At rank kk, the kk groups at
+// or below A hold kk distinct rows with GEMM value <= A, so the kk-th smallest exact
+// distance is at most A + shift + eb and every row of the true top kk has GEMM value
+// <= A + 2 eb.  At a lower rank the same holds unless the sample took more than rank - 1
+// of the top kk - 1 rows (ThresholdRank), which the certificate detects.
 // A is found by a bitwise radix select over the order-preserving encodings, held V per lane:
 // from the top bit down, the answer keeps a 0 bit when at least kk keys lie at or below the
 // prefix with all lower bits set (ballot + popcount, no cross-lane data movement).
@@ -1023,14 +1027,14 @@ __global__ __launch_bounds__(256) void k_kth(KthArgs a) {
     key[v] = i < a.ngroups ? ord_enc(g[i]) : 0xffffffffu;
   }
   float A = __builtin_inff();
-  if (a.kk <= a.ngroups) {
+  if (a.rank <= a.ngroups) {
     uint32_t ans = 0;
     for (int bit = 31; bit >= 0; --bit) {
       const uint32_t t = ans | ((1u << bit) - 1u);
       int cnt = 0;
 #pragma unroll
       for (int v = 0; v < V; ++v) cnt += __popcll(__ballot(key[v] <= t));
-      if (cnt < a.kk) ans |= 1u << bit;
+      if (cnt < a.rank) ans |= 1u << bit;
     }
     A = ord_dec_dev(ans);
   }
@@ -1052,7 +1056,7 @@ __global__ __launch_bounds__(1024) void k_kth_block(KthArgs a) {
     key[v] = i < a.ngroups ? ord_enc(g[i]) : 0xffffffffu;
   }
   float A = __builtin_inff();
-  if (a.kk <= a.ngroups) {
+  if (a.rank <= a.ngroups) {
     uint32_t ans = 0;
     for (int bit = 31; bit >= 0; --bit) {
       const uint32_t t = ans | ((1u << bit) - 1u);
@@ -1064,7 +1068,7 @@ __global__ __launch_bounds__(1024) void k_kth_block(KthArgs a) {
       int total = 0;
 #pragma unroll
       for (int w = 0; w < 16; ++w) total += s_cnt[bit & 1][w];
-      if (total < a.kk) ans |= 1u << bit;
+      if (total < a.rank) ans |= 1u << bit;
     }
     A = ord_dec_dev(ans);
   }
@@ -1087,7 +1091,7 @@ struct SelectArgs {
   int rescore;             // 0: candidates hold exact distances; 1: GEMM values, rescore
                            // the best K'; 2: GEMM values, rescore every candidate
   int by_query;            // candidate buffers are indexed by query (else by slot)
-  const float* T;          // rescore 2: the filter threshold of the GEMM pass
+  const float* T;          // rescore 1 and 2: the admission threshold of the GEMM pass
   int force_fallback;      // testing: 1 fails every rescore-1 certificate, 2 also rescore 2
   uint32_t* out_ids;
   float* out_d;
@@ -1259,9 +1263,9 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
       const float v = __shfl(top.k.d[e], (a.k - 1) & (kWave - 1));
       if (e == (a.k - 1) / kWave) dk = v;
     }
-    if (!a.exact[q] || a.force_fallback >= 2) {
-      const float lower = (a.T[q] + a.shift[q]) - a.eb[q];
-      if ((!(dk <= lower) || a.force_fallback >= 2) && lane == 0) {
+    {
+      const double lower = (double(a.T[q]) + double(a.shift[q])) - double(a.eb[q]);
+      if ((!(double(dk) <= lower) || a.force_fallback >= 2) && lane == 0) {
         const uint32_t p = atomicAdd(a.fb_count, 1u);
         a.fb_list[p] = q;
       }
@@ -1283,7 +1287,11 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   // exact re-scoring of the K' = N-1 best by GEMM value, in two stages.  Stage 1 re-scores
   // the best n1 = min(K', k + 8); its answer stands when every later candidate provably
   // lies behind it: the (n1+1)-th GEMM value plus the shift minus the bound exceeds the k-th
-  // exact distance (always so in exact mode, where the GEMM order is the distance order).
+  // exact distance.  Rows outside the buffers have GEMM value > T, at least that (n1+1)-th
+  // value, so they lie behind it too.  When no later candidate exists, or in exact mode
+  // (the GEMM order is the distance order), the outside rows are checked against T itself:
+  // the k-th exact distance is at most T + shift - eb (always so when T came from the kk-th
+  // group minimum; a threshold of lower rank fails it when it kept fewer than the top k).
   // Otherwise stage 2 re-scores all K' and checks the same certificate at K'+1.
   const uint32_t nsel = min(total, uint32_t(N - 1));
   const uint32_t n1 = min(nsel, uint32_t(a.k) + 8u);
@@ -1314,12 +1322,17 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     }
     return x;
   };
+  const double lower = (double(a.T[q]) + double(shift)) - double(ebq);
+  auto certify = [&](uint32_t n) {
+    const float dk = at(r.d, uint32_t(a.k) - 1);
+    if ((n >= total || exact) && double(dk) <= lower) return true;
+    return n < total && dk < (at(top.k.d, n) + shift) - ebq;
+  };
   rescore_first(n1);
-  bool certified = n1 >= total || exact ||
-                   at(r.d, uint32_t(a.k) - 1) < (at(top.k.d, n1) + shift) - ebq;
+  bool certified = certify(n1);
   if (!certified && n1 < nsel) {
     rescore_first(nsel);
-    certified = nsel >= total || at(r.d, uint32_t(a.k) - 1) < (at(top.k.d, nsel) + shift) - ebq;
+    certified = certify(nsel);
   }
   if (a.force_fallback >= 1) certified = false;
 #pragma unroll
@@ -2065,6 +2078,28 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   }
 }
 
+// The rank r of the sample's group minimum that becomes the admission threshold.  The sample
+// holds a fraction f = S / N of the rows, spread evenly; the r-th smallest group minimum
+// lies below the kk-th smallest GEMM value of all rows only when the sample holds at least
+// r of the kk - 1 rows before it, which for rows taken independently with probability f is
+// the binomial tail P(Bin(kk - 1, f) >= r).  r is the smallest rank with that tail below
+// 1e-6 (at most kk, which keeps the top kk with certainty).  About r / f rows then pass the
+// threshold per query instead of kk / f; k_select's certificate catches the rare query
+// whose threshold fell short, and the second chance and the exact re-scan answer it.
+static int ThresholdRank(size_t kk, uint32_t S, uint32_t N) {
+  if (kk <= 1 || S >= N) return int(kk);
+  const double f = double(S) / double(N), n = double(kk - 1);
+  const double lf = std::log(f), lg = std::log1p(-f);
+  double cdf = 0.0;  // P(Bin(n, f) < r)
+  for (size_t r = 1; r < kk; ++r) {
+    const double j = double(r - 1);
+    cdf += std::exp(std::lgamma(n + 1.0) - std::lgamma(j + 1.0) - std::lgamma(n - j + 1.0) +
+                    j * lf + (n - j) * lg);
+    if (1.0 - cdf <= 1e-6) return int(r);
+  }
+  return int(kk);
+}
+
 // Whether a batch takes the tiny-batch path: integer rows with their int8 copy, the int8
 // GEMM on, at most kTinyQ queries, k <= kTinyK, rows of 64, 128 or 256 dims.
 static bool TinyEligible(const Ctx* c, const ScanSource& src, size_t nq, size_t kk,
@@ -2210,6 +2245,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // fp32 main pass on the device (no host round trip before the main pass).
   const bool gated = nq <= 128 && split == 0 && try8 && !try8op;
   S = std::min(S, src->Smax);
+  const int rank = ThresholdRank(kk, S, N);
   const int ngroups = int((S + 31) / 32) * 2;
   struct Plan {
     int qb, nqt, nchunks, caph, nseg, schunks;
@@ -2227,7 +2263,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     p.schunk_rows = (S + p.schunks - 1) / p.schunks;
     p.schunk_rows = (p.schunk_rows + 63) / 64 * 64;
     p.schunks = int((S + p.schunk_rows - 1) / p.schunk_rows);
-    const double expect_seg = double(kk) * N / S * 1.5 / (2.0 * p.nchunks);
+    const double expect_seg = double(rank) * N / S * 2.0 / (2.0 * p.nchunks);
     p.caph = 32;
     while (p.caph < 3.0 * expect_seg + 32) p.caph <<= 1;
     p.nseg = 2 * p.nchunks;
@@ -2403,7 +2439,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  KthArgs ka{gm, sg.ngroups, int(nq), int(kk), ebx, T};
+  KthArgs ka{gm, sg.ngroups, int(nq), rank, ebx, T};
   {
     ProfScope ps(c, "kth", s);
     VDBG_RETURN_IF_ERROR(LaunchKth(s, ka));
@@ -2482,6 +2518,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   se.k = int(kk);
   se.pd = int(pd);
   se.rescore = 1;
+  se.T = T;
   se.out_ids = out_ids;
   se.out_d = out_d;
   se.fb_list = fb_list;
