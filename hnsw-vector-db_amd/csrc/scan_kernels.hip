@@ -1285,30 +1285,37 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   }
 
   // exact re-scoring of the K' = N-1 best by GEMM value, in two stages.  Stage 1 re-scores
-  // the best n1 = min(K', k + 8); its answer stands when every later candidate provably
+  // the best n1 = min(K', k + 8), rounded up to whole 64-lane passes when k + 8 takes more
+  // than one (the extra lanes cost no extra pass); its answer stands when every later
+  // candidate provably
   // lies behind it: the (n1+1)-th GEMM value plus the shift minus the bound exceeds the k-th
   // exact distance.  Rows outside the buffers have GEMM value > T, at least that (n1+1)-th
   // value, so they lie behind it too.  When no later candidate exists, or in exact mode
   // (the GEMM order is the distance order), the outside rows are checked against T itself:
   // the k-th exact distance is at most T + shift - eb (always so when T came from the kk-th
   // group minimum; a threshold of lower rank fails it when it kept fewer than the top k).
-  // Otherwise stage 2 re-scores all K' and checks the same certificate at K'+1.
+  // Otherwise stage 2 scores the rest of the K' and checks the same certificate at K'+1.
   const uint32_t nsel = min(total, uint32_t(N - 1));
-  const uint32_t n1 = min(nsel, uint32_t(a.k) + 8u);
+  const uint32_t want = uint32_t(a.k) + 8u;
+  const uint32_t n1 = min(nsel, want > uint32_t(kWave) ? (want + kWave - 1) / kWave * kWave : want);
   const float shift = a.shift[q], ebq = a.eb[q];
   const bool exact = a.exact[q] != 0;
   WaveKeys<E> r;
-  auto rescore_first = [&](uint32_t n) {
+  float ud[E];  // exact distances of the scored keys, in top.k's order
+  // scores keys [lo, hi) of top.k (passes with no key in range are skipped), then sorts the
+  // first hi scored keys into r
+  auto rescore_first = [&](uint32_t lo, uint32_t hi) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      if (uint32_t(e + 1) * kWave <= lo || uint32_t(e) * kWave >= hi) continue;
+      const uint32_t gi = e * kWave + lane;
+      if (gi >= lo && gi < hi) ud[e] = sc(qv, top.k.id[e]);
+    }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
       const uint32_t gi = e * kWave + lane;
-      if (gi < n) {
-        r.d[e] = sc(qv, top.k.id[e]);
-        r.id[e] = top.k.id[e];
-      } else {
-        r.d[e] = __builtin_inff();
-        r.id[e] = kNoId;
-      }
+      r.d[e] = gi < hi ? ud[e] : __builtin_inff();
+      r.id[e] = gi < hi ? top.k.id[e] : kNoId;
     }
     bitonic_sort<E>(r);
   };
@@ -1328,10 +1335,10 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     if ((n >= total || exact) && double(dk) <= lower) return true;
     return n < total && dk < (at(top.k.d, n) + shift) - ebq;
   };
-  rescore_first(n1);
+  rescore_first(0, n1);
   bool certified = certify(n1);
   if (!certified && n1 < nsel) {
-    rescore_first(nsel);
+    rescore_first(n1, nsel);
     certified = certify(nsel);
   }
   if (a.force_fallback >= 1) certified = false;

@@ -152,3 +152,34 @@ def test_flat_large_k(ctx, oracle, k, metric, frac):
     gi, gd = ds.flat_search(qs, k, allow=allow)
     od, oi = oracle.flat_search(base, qs, k, metric=metric, allow=allow)
     _check_equal(gi, gd, oi, od)
+
+
+def _sample_aligned_rows(n, dim, near):
+    # The threshold sample takes every (n / 65536)-th row.  Here every near row sits on a
+    # sampled position (rows 4 i, n = 4 x 65536) and every other row is far away, so the
+    # sample holds all of the near rows and the lower-rank admission threshold keeps fewer
+    # rows than the depth asks for: the certificate must refuse it and the re-scan answer.
+    rng = np.random.default_rng(5151)
+    base = (100.0 + rng.random((n, dim), dtype=np.float32)).astype(np.float32)
+    base[4 * np.arange(near), :] = 0.0
+    base[4 * np.arange(near), 0] = 0.01 * (1 + np.arange(near, dtype=np.float32))
+    qs = np.zeros((8, dim), np.float32)
+    qs[:, 1] = 1e-3 * np.arange(8, dtype=np.float32)
+    return base, qs
+
+
+@pytest.mark.parametrize("kind", ["flat", "sq8"])
+def test_threshold_short_of_depth_falls_back(ctx, oracle, kind):
+    n, dim, near = 4 * 65536, 32, 60
+    print(f"threshold short of depth: {kind} n={n} near={near}", flush=True)
+    base, qs = _sample_aligned_rows(n, dim, near)
+    ds = vdbg.Dataset(ctx, base, dim)
+    if kind == "flat":
+        gi, gd = ds.flat_search(qs, 100)
+        od, oi = oracle.flat_search(base, qs, 100)
+    else:
+        sq = vdbg.Sq8Index(ds)
+        gi, gd = sq.search(qs, 10, 100)
+        od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 100)
+    assert ctx.last_fallbacks() > 0
+    _check_equal(gi, gd, oi, od)
