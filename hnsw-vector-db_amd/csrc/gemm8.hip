@@ -243,11 +243,23 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     }
     const uint8_t* xa0 = &xs[sidx & 1][j * STR + h * 16];
     const uint8_t* xa1 = xa0 + 32 * STR;
+    if constexpr (SQ != 2) {
+      // row block 0 over every K block, then row block 1: block 0's accumulators are final
+      // while block 1's MFMAs still run, so its threshold test starts a block earlier
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const v4i x0 = *reinterpret_cast<const v4i*>(xa0 + kb * 32);
-      const v4i x1 = *reinterpret_cast<const v4i*>(xa1 + kb * 32);
-      if constexpr (SQ == 2) {  // rows [h | l]: h.h, h.l + l.h, l.l
+      for (int blk = 0; blk < 2; ++blk)
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          const v4i x = *reinterpret_cast<const v4i*>((blk ? xa1 : xa0) + kb * 32);
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+            acc[qb][blk] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x, qv[QS][qb][kb], acc[qb][blk], 0, 0, 0);
+        }
+    } else {  // rows [h | l]: h.h, h.l + l.h, l.l
+#pragma unroll
+      for (int kb = 0; kb < NKB; ++kb) {
+        const v4i x0 = *reinterpret_cast<const v4i*>(xa0 + kb * 32);
+        const v4i x1 = *reinterpret_cast<const v4i*>(xa1 + kb * 32);
         const v4i y0 = *reinterpret_cast<const v4i*>(xa0 + KC + kb * 32);
         const v4i y1 = *reinterpret_cast<const v4i*>(xa1 + KC + kb * 32);
         const v4i qh = qv[QS][0][kb], ql = qv[QS][1][kb];
@@ -259,12 +271,6 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
         acc[1][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y1, qh, acc[1][1], 0, 0, 0);
         acc[2][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y0, ql, acc[2][0], 0, 0, 0);
         acc[2][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(y1, ql, acc[2][1], 0, 0, 0);
-      } else {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          acc[qb][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x0, qv[QS][qb][kb], acc[qb][0], 0, 0, 0);
-          acc[qb][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(x1, qv[QS][qb][kb], acc[qb][1], 0, 0, 0);
-        }
       }
     }
     if (sidx + 1 < nstages) store_stage(X, sidx + 1);
@@ -287,11 +293,11 @@ __global__ __launch_bounds__(256, OCC) void k_gemm8(GemmArgs a) {
     if (wave_live && MODE == 0) {
       // per 32-row block: the lane's largest u against the bound, one wave-uniform branch;
       // a block passing on some lane tests its four groups of four values the same way, and
-      // only a passing group its values one by one
+      // only a passing group its values one by one (row block 0 first)
 #pragma unroll
-      for (int qb = 0; qb < NQ; ++qb)
+      for (int blk = 0; blk < 2; ++blk)
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
+        for (int qb = 0; qb < NQ; ++qb) {
           int m = acc[qb][blk][0];
 #pragma unroll
           for (int r = 1; r < 16; ++r) m = max(m, acc[qb][blk][r]);
