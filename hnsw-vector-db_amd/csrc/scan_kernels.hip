@@ -466,7 +466,10 @@ struct PrepArgs {
 // carry at most pd roundings each on sums bounded by those magnitudes, the exact
 // AVX-512-order value at most pd/16 + 6, and the factor two covers forming thresholds and
 // the SQ8 decode roundings.
-__device__ void query_prep_wave(const PrepArgs& a, int q) {
+// Returns the query's contribution to the batch maximum *a.mb8 (float bits, 0 without one);
+// the caller folds it in.
+__device__ uint32_t query_prep_wave(const PrepArgs& a, int q) {
+  uint32_t mbq = 0;
   const float* v = a.Q + size_t(q) * a.pd;
   float s = 0.f, s2 = 0.f, lo = __builtin_inff(), hi = -__builtin_inff(), ma = 0.f;
   float sq = 0.f;  // sum(q) (exact: integers of magnitude < 2^24 when the int8 GEMM applies)
@@ -501,8 +504,7 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
   s = wave_sum(s);
   s2 = wave_sum(s2);
   // float rows on the int8 GEMM: the batch is scaled by its largest ||q||
-  if (a.kind == 0 && a.mb8 != nullptr && lane_id() == 0)
-    atomicMax(a.mb8, __float_as_uint(sqrtf(s) * (1.f + 1e-6f)));
+  if (a.kind == 0 && a.mb8 != nullptr) mbq = __float_as_uint(sqrtf(s) * (1.f + 1e-6f));
   lo = wave_min(lo);
   hi = wave_max(hi);
   ma = wave_max(ma);
@@ -538,7 +540,7 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
     for (int i = lane_id(); i < a.pd; i += kWave) mb = fmaxf(mb, fabsf(a.Qb[size_t(q) * a.pd + i]));
     mb = wave_max(mb);
     // non-negative floats order as their bits; a NaN ends above +inf and stops the int8 GEMM
-    if (a.mb8 != nullptr && lane_id() == 0) atomicMax(a.mb8, __float_as_uint(mb));
+    if (a.mb8 != nullptr) mbq = max(mbq, __float_as_uint(mb));
     split_ok = mb <= 3.0e38f;  // finite
     if (split_ok && mb > 0.f) {
       int ex = 0;
@@ -635,12 +637,21 @@ __device__ void query_prep_wave(const PrepArgs& a, int q) {
     a.exact[q] = ex && !half_norm ? 1 : 0;
     a.eb[q] = half_norm ? 1.f : ex ? 0.f : float((split ? bsplit : bound) * 1.001);
   }
+  return mbq;
 }
 
+// Four queries per block; the batch maximum takes one atomic per block (one per query would
+// serialise thousands of atomics on one word).
 __global__ __launch_bounds__(256) void k_query_prep(PrepArgs a) {
-  const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (q >= a.nq) return;
-  query_prep_wave(a, q);
+  __shared__ uint32_t s_mb[4];
+  const int wave = threadIdx.x >> 6;
+  const int q = blockIdx.x * 4 + wave;
+  const uint32_t mbq = q < a.nq ? query_prep_wave(a, q) : 0u;
+  if (a.mb8 == nullptr) return;
+  if (lane_id() == 0) s_mb[wave] = mbq;
+  __syncthreads();
+  if (threadIdx.x == 0)
+    atomicMax(a.mb8, max(max(s_mb[0], s_mb[1]), max(s_mb[2], s_mb[3])));
 }
 
 // The scan's per-call words in one launch: overflow flags, fallback counts, the batch's GEMM
@@ -1438,14 +1449,20 @@ struct RerankArgs {
 // smallest by (dist, id).  One wave per query, up to 64*E candidates.
 template <int E>
 __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
+  __shared__ uint32_t ys_all[4][256];  // the query as int8 y - c8, four dims a word
   const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= a.nq) return;
   const int lane = lane_id();
   const float* qv = a.Q + size_t(q) * a.pd;
+  uint32_t* ys = ys_all[threadIdx.x >> 6];
   // Integer rows and an integer query whose every partial sum stays below 2^24: every fp32
   // summation order, the reference's included, gives the exact integer, so the distance is
-  // computed from the rows' int8 copy (a quarter of the bytes) in int32.
-  bool ex8 = false;
+  // computed from the rows' int8 copy (a quarter of the bytes) in int32.  With the query
+  // shifted into int8 as well (y8 = y - c8), four dims go per packed dot product:
+  //   L2:  sum (x - y)^2 = sum x8^2 - 2 sum x8 y8 + sum y8^2
+  //   IP:  sum x y = sum x8 y8 + c8 sum x8 + c8 sum y8 + pd c8^2.
+  bool ex8 = false, packed = false;
+  int ysum = 0;  // sum y8^2 (L2) or sum y8 (IP)
   if (a.X8 != nullptr && a.metric != 2) {
     float mq = 0.f, lo = __builtin_inff(), hi = -__builtin_inff();
     int ai = 1;
@@ -1464,7 +1481,46 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
     const double range = double(fmaxf(hi, a.xs.hi)) - double(fminf(lo, a.xs.lo));
     ex8 = a.xs.all_int && ai && pd * mx * mx < lim && pd * m * m < lim && pd * mx * m < lim &&
           pd * range * range < lim;
+    packed = ex8 && a.pd % 16 == 0 && a.pd <= 1024 && lo - float(a.c8) >= -128.f &&
+             hi - float(a.c8) <= 127.f;
+    if (packed) {
+      for (int w = lane; w < a.pd / 4; w += kWave) {
+        uint32_t word = 0;
+        for (int t = 0; t < 4; ++t) {
+          const int y8 = int(qv[4 * w + t]) - a.c8;
+          ysum += a.metric == 0 ? y8 * y8 : y8;
+          word |= uint32_t(y8 & 0xff) << (8 * t);
+        }
+        ys[w] = word;
+      }
+      for (int o = kWave / 2; o > 0; o >>= 1) ysum += __shfl_xor(ysum, o);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
   }
+  auto packed8 = [&](uint32_t id) {
+    const int4* xr = reinterpret_cast<const int4*>(a.X8 + size_t(id) * a.pd);
+    const int4* yr = reinterpret_cast<const int4*>(ys);
+    int xy = 0, xx = 0;
+    for (int i = 0; i < a.pd / 16; ++i) {
+      const int4 x = xr[i], y = yr[i];
+      xy = __builtin_amdgcn_sdot4(x.x, y.x, xy, false);
+      xy = __builtin_amdgcn_sdot4(x.y, y.y, xy, false);
+      xy = __builtin_amdgcn_sdot4(x.z, y.z, xy, false);
+      xy = __builtin_amdgcn_sdot4(x.w, y.w, xy, false);
+      // L2: sum x8^2; IP: sum x8 (against bytes of ones)
+      const int ox = a.metric == 0 ? x.x : 0x01010101, oy = a.metric == 0 ? x.y : 0x01010101;
+      const int oz = a.metric == 0 ? x.z : 0x01010101, ow = a.metric == 0 ? x.w : 0x01010101;
+      xx = __builtin_amdgcn_sdot4(x.x, ox, xx, false);
+      xx = __builtin_amdgcn_sdot4(x.y, oy, xx, false);
+      xx = __builtin_amdgcn_sdot4(x.z, oz, xx, false);
+      xx = __builtin_amdgcn_sdot4(x.w, ow, xx, false);
+    }
+    if (a.metric == 0) return float(xx - 2 * xy + ysum);
+    const int dot = xy + a.c8 * xx + a.c8 * ysum + a.pd * a.c8 * a.c8;
+    return -float(dot);  // -0 for a zero dot, as -dot gives
+  };
   auto exact8 = [&](uint32_t id) {
     const int8_t* xr = a.X8 + size_t(id) * a.pd;
     int acc = 0;
@@ -1485,7 +1541,9 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
     const int i = e * kWave + lane;
     const uint32_t id = i < a.depth ? a.cand[size_t(q) * a.depth + i] : kNoId;
     if (id != kNoId) {
-      r.d[e] = ex8 ? exact8(id) : metric_exact_k(a.kset, a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
+      r.d[e] = packed ? packed8(id)
+               : ex8  ? exact8(id)
+                      : metric_exact_k(a.kset, a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
       r.id[e] = id;
     } else {
       r.d[e] = __builtin_inff();
