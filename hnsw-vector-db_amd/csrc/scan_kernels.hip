@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 
 #include "gemm.h"
 #include "vdbg_device.h"
@@ -55,6 +56,84 @@ __device__ __forceinline__ int wave_and(int v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v &= __shfl_xor(v, o);
   return v;
+}
+
+// ================================================================ integer rows on int8
+
+// Integer rows held in int8 as x8 = x - c8, and an integer query y whose every partial sum
+// of any order stays below 2^24 (so the reference's fp32 distance is the exact integer): the
+// query goes to LDS as int8 y8 = y - c8, four dims a word, and each distance takes four dims
+// per packed dot product:
+//   L2:  sum (x - y)^2 = sum x8^2 - 2 sum x8 y8 + sum y8^2
+//   IP:  sum x y = sum x8 y8 + c8 sum x8 + c8 sum y8 + pd c8^2    (the distance is -sum x y)
+struct Int8Query {
+  int on;                // the query qualifies
+  int ysum;              // sum y8^2 (L2) or sum y8 (IP)
+  const uint32_t* ys;    // [pd / 4] packed y8
+};
+
+// Wave-level: decides and packs (ys: pd / 4 words of the wave's LDS, pd <= 1024).
+__device__ Int8Query int8_query(const int8_t* X8, int c8, float xlo, float xhi, float xmax,
+                                int xint, int metric, int pd, const float* qv, uint32_t* ys) {
+  Int8Query r{0, 0, ys};
+  if (X8 == nullptr || !xint || metric == 2 || pd % 16 != 0 || pd > 1024) return r;
+  float mq = 0.f, lo = __builtin_inff(), hi = -__builtin_inff();
+  int ai = 1;
+  for (int i = lane_id(); i < pd; i += kWave) {
+    const float v = qv[i];
+    mq = fmaxf(mq, fabsf(v));
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+    ai &= v == rintf(v) ? 1 : 0;
+  }
+  mq = wave_max(mq);
+  lo = wave_min(lo);
+  hi = wave_max(hi);
+  ai = wave_and(ai);
+  const double dpd = pd, lim = 16777216.0, mx = xmax, m = mq;
+  const double range = double(fmaxf(hi, xhi)) - double(fminf(lo, xlo));
+  if (!(ai && dpd * mx * mx < lim && dpd * m * m < lim && dpd * mx * m < lim &&
+        dpd * range * range < lim && lo - float(c8) >= -128.f && hi - float(c8) <= 127.f))
+    return r;
+  int ysum = 0;
+  for (int w = lane_id(); w < pd / 4; w += kWave) {
+    uint32_t word = 0;
+    for (int t = 0; t < 4; ++t) {
+      const int y8 = int(qv[4 * w + t]) - c8;
+      ysum += metric == 0 ? y8 * y8 : y8;
+      word |= uint32_t(y8 & 0xff) << (8 * t);
+    }
+    ys[w] = word;
+  }
+  for (int o = kWave / 2; o > 0; o >>= 1) ysum += __shfl_xor(ysum, o);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  r.on = 1;
+  r.ysum = ysum;
+  return r;
+}
+
+__device__ __forceinline__ float int8_distance(const int8_t* X8, int c8, int metric, int pd,
+                                               const Int8Query& p, uint32_t row) {
+  const int4* xr = reinterpret_cast<const int4*>(X8 + size_t(row) * pd);
+  const int4* yr = reinterpret_cast<const int4*>(p.ys);
+  const int one = 0x01010101;
+  int xy = 0, xx = 0;
+  for (int i = 0; i < pd / 16; ++i) {
+    const int4 x = xr[i], y = yr[i];
+    xy = __builtin_amdgcn_sdot4(x.x, y.x, xy, false);
+    xy = __builtin_amdgcn_sdot4(x.y, y.y, xy, false);
+    xy = __builtin_amdgcn_sdot4(x.z, y.z, xy, false);
+    xy = __builtin_amdgcn_sdot4(x.w, y.w, xy, false);
+    // L2: sum x8^2; IP: sum x8 (against bytes of ones)
+    xx = __builtin_amdgcn_sdot4(x.x, metric == 0 ? x.x : one, xx, false);
+    xx = __builtin_amdgcn_sdot4(x.y, metric == 0 ? x.y : one, xx, false);
+    xx = __builtin_amdgcn_sdot4(x.z, metric == 0 ? x.z : one, xx, false);
+    xx = __builtin_amdgcn_sdot4(x.w, metric == 0 ? x.w : one, xx, false);
+  }
+  if (metric == 0) return float(xx - 2 * xy + p.ysum);
+  return -float(xy + c8 * xx + c8 * p.ysum + pd * c8 * c8);  // -0 for a zero dot, as -dot
 }
 
 // Order-preserving float <-> uint32 map for atomicMin/atomicMax.
@@ -1127,6 +1206,10 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   __shared__ float md[WPS == 1 ? 1 : WPS - 1][WPS == 1 ? 1 : kWave * E];
   __shared__ uint32_t mi[WPS == 1 ? 1 : WPS - 1][WPS == 1 ? 1 : kWave * E];
   __shared__ uint32_t mtot[WAVES];
+  // flat rows with an int8 copy (FlatScorer8): the query packed into int8 when its
+  // distances are exact integers (Int8Query)
+  constexpr bool kI8 = std::is_same<Scorer, FlatScorer8>::value;
+  __shared__ uint32_t ys_all[kI8 ? WAVES : 1][kI8 ? 256 : 1];
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
   const int slot = WPS == 1 ? blockIdx.x * 4 + wave : blockIdx.x;
@@ -1169,6 +1252,16 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   WaveTopK<E> top;
   top.init();
   const float* qv = a.Q + size_t(q) * a.pd;
+  Int8Query p8{0, 0, nullptr};
+  if constexpr (kI8)
+    p8 = int8_query(sc.X8, sc.c8, sc.xlo, sc.xhi, sc.xmax, sc.xint, sc.metric, sc.pd, qv,
+                    ys_all[wave]);
+  auto score = [&](uint32_t id) -> float {
+    if constexpr (kI8) {
+      if (p8.on) return int8_distance(sc.X8, sc.c8, sc.metric, sc.pd, p8, id);
+    }
+    return sc(qv, id);
+  };
   const uint2* cbase = a.cand + (size_t(src) * a.nseg + s_lo) * size_t(a.cap);
   // candidate g of the wave's flat order: the segment is the largest s with pre[s] <= g
   auto fetch = [&](uint32_t g) -> uint2 {
@@ -1226,7 +1319,7 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     const uint2 nxt = fetch(g0 + kWave + lane);
     const uint32_t id = cur.y;
     float d = __uint_as_float(cur.x);
-    if (a.rescore == 2 && id != kNoId) d = sc(qv, id);
+    if (a.rescore == 2 && id != kNoId) d = score(id);
     push(d, id);
     cur = nxt;
   }
@@ -1320,7 +1413,7 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     for (int e = 0; e < E; ++e) {
       if (uint32_t(e + 1) * kWave <= lo || uint32_t(e) * kWave >= hi) continue;
       const uint32_t gi = e * kWave + lane;
-      if (gi >= lo && gi < hi) ud[e] = sc(qv, top.k.id[e]);
+      if (gi >= lo && gi < hi) ud[e] = score(top.k.id[e]);
     }
 #pragma unroll
     for (int e = 0; e < E; ++e) {
@@ -1454,16 +1547,14 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
   if (q >= a.nq) return;
   const int lane = lane_id();
   const float* qv = a.Q + size_t(q) * a.pd;
-  uint32_t* ys = ys_all[threadIdx.x >> 6];
   // Integer rows and an integer query whose every partial sum stays below 2^24: every fp32
   // summation order, the reference's included, gives the exact integer, so the distance is
-  // computed from the rows' int8 copy (a quarter of the bytes) in int32.  With the query
-  // shifted into int8 as well (y8 = y - c8), four dims go per packed dot product:
-  //   L2:  sum (x - y)^2 = sum x8^2 - 2 sum x8 y8 + sum y8^2
-  //   IP:  sum x y = sum x8 y8 + c8 sum x8 + c8 sum y8 + pd c8^2.
-  bool ex8 = false, packed = false;
-  int ysum = 0;  // sum y8^2 (L2) or sum y8 (IP)
-  if (a.X8 != nullptr && a.metric != 2) {
+  // computed from the rows' int8 copy (a quarter of the bytes) in int32: on packed dot
+  // products when the shifted query fits int8 (Int8Query), else value by value.
+  const Int8Query p8 = int8_query(a.X8, a.c8, a.xs.lo, a.xs.hi, a.xs.max_abs, a.xs.all_int,
+                                  a.metric, a.pd, qv, ys_all[threadIdx.x >> 6]);
+  bool ex8 = false;
+  if (!p8.on && a.X8 != nullptr && a.metric != 2) {
     float mq = 0.f, lo = __builtin_inff(), hi = -__builtin_inff();
     int ai = 1;
     for (int i = lane; i < a.pd; i += kWave) {
@@ -1481,46 +1572,7 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
     const double range = double(fmaxf(hi, a.xs.hi)) - double(fminf(lo, a.xs.lo));
     ex8 = a.xs.all_int && ai && pd * mx * mx < lim && pd * m * m < lim && pd * mx * m < lim &&
           pd * range * range < lim;
-    packed = ex8 && a.pd % 16 == 0 && a.pd <= 1024 && lo - float(a.c8) >= -128.f &&
-             hi - float(a.c8) <= 127.f;
-    if (packed) {
-      for (int w = lane; w < a.pd / 4; w += kWave) {
-        uint32_t word = 0;
-        for (int t = 0; t < 4; ++t) {
-          const int y8 = int(qv[4 * w + t]) - a.c8;
-          ysum += a.metric == 0 ? y8 * y8 : y8;
-          word |= uint32_t(y8 & 0xff) << (8 * t);
-        }
-        ys[w] = word;
-      }
-      for (int o = kWave / 2; o > 0; o >>= 1) ysum += __shfl_xor(ysum, o);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    }
   }
-  auto packed8 = [&](uint32_t id) {
-    const int4* xr = reinterpret_cast<const int4*>(a.X8 + size_t(id) * a.pd);
-    const int4* yr = reinterpret_cast<const int4*>(ys);
-    int xy = 0, xx = 0;
-    for (int i = 0; i < a.pd / 16; ++i) {
-      const int4 x = xr[i], y = yr[i];
-      xy = __builtin_amdgcn_sdot4(x.x, y.x, xy, false);
-      xy = __builtin_amdgcn_sdot4(x.y, y.y, xy, false);
-      xy = __builtin_amdgcn_sdot4(x.z, y.z, xy, false);
-      xy = __builtin_amdgcn_sdot4(x.w, y.w, xy, false);
-      // L2: sum x8^2; IP: sum x8 (against bytes of ones)
-      const int ox = a.metric == 0 ? x.x : 0x01010101, oy = a.metric == 0 ? x.y : 0x01010101;
-      const int oz = a.metric == 0 ? x.z : 0x01010101, ow = a.metric == 0 ? x.w : 0x01010101;
-      xx = __builtin_amdgcn_sdot4(x.x, ox, xx, false);
-      xx = __builtin_amdgcn_sdot4(x.y, oy, xx, false);
-      xx = __builtin_amdgcn_sdot4(x.z, oz, xx, false);
-      xx = __builtin_amdgcn_sdot4(x.w, ow, xx, false);
-    }
-    if (a.metric == 0) return float(xx - 2 * xy + ysum);
-    const int dot = xy + a.c8 * xx + a.c8 * ysum + a.pd * a.c8 * a.c8;
-    return -float(dot);  // -0 for a zero dot, as -dot gives
-  };
   auto exact8 = [&](uint32_t id) {
     const int8_t* xr = a.X8 + size_t(id) * a.pd;
     int acc = 0;
@@ -1541,7 +1593,7 @@ __global__ __launch_bounds__(256) void k_rerank(RerankArgs a) {
     const int i = e * kWave + lane;
     const uint32_t id = i < a.depth ? a.cand[size_t(q) * a.depth + i] : kNoId;
     if (id != kNoId) {
-      r.d[e] = packed ? packed8(id)
+      r.d[e] = p8.on ? int8_distance(a.X8, a.c8, a.metric, a.pd, p8, id)
                : ex8  ? exact8(id)
                       : metric_exact_k(a.kset, a.metric, qv, a.X + size_t(id) * a.pd, a.pd);
       r.id[e] = id;
@@ -1634,6 +1686,24 @@ static void launch_rerank(hipStream_t s, const RerankArgs& a) {
 
 static FlatScorer FlatOf(const ScanSource& src, int kset) {
   return FlatScorer{src.X, src.pd, src.metric, kset};
+}
+// Whether a selection takes FlatScorer8: rows with a one-part int8 copy, and more keys to
+// re-score than one 64-lane pass (for a few keys the query packing costs more than it saves)
+// or every buffered candidate (the second chance).
+static bool UseFlat8(const ScanSource& src, size_t kk, int rescore) {
+  return src.kind == 0 && src.X8 != nullptr && src.x8_parts == 1 &&
+         (rescore == 2 || kk + 8 > size_t(kWave));
+}
+static FlatScorer8 Flat8Of(const ScanSource& src, int kset) {
+  FlatScorer8 f;
+  static_cast<FlatScorer&>(f) = FlatOf(src, kset);
+  f.X8 = src.X8;
+  f.c8 = src.c8;
+  f.xlo = src.stats.lo;
+  f.xhi = src.stats.hi;
+  f.xmax = src.stats.max_abs;
+  f.xint = src.stats.all_int;
+  return f;
 }
 static Sq8Scorer Sq8Of(const ScanSource& src, int kset) {
   return Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric, kset};
@@ -2591,7 +2661,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   se.force_fallback = c->test_fallbacks;
   {
     ProfScope ps(c, "select", s);
-    if (src->kind == 0) {
+    if (UseFlat8(*src, kk, 1)) {
+      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer8, s, se, Flat8Of(*src, c->kset));
+    } else if (src->kind == 0) {
       VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, se, FlatOf(*src, c->kset));
     } else {
       VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, se, Sq8Of(*src, c->kset));
@@ -2613,7 +2685,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   s2.fb_count = fb_count + 1;
   {
     ProfScope ps(c, "rescore", s);
-    if (src->kind == 0) {
+    if (UseFlat8(*src, kk, 2)) {
+      VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer8, s, s2, Flat8Of(*src, c->kset));
+    } else if (src->kind == 0) {
       VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, s2, FlatOf(*src, c->kset));
     } else {
       VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, s2, Sq8Of(*src, c->kset));

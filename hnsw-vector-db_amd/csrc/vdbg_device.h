@@ -407,6 +407,16 @@ struct FlatScorer {
   }
 };
 
+// The same, with the rows' int8 copy x8 = x - c8 (integer rows) and their value range: a
+// selection re-scoring many keys takes them from the int8 copy for queries whose distances
+// are exact integers (scan_kernels.hip, Int8Query).
+struct FlatScorer8 : FlatScorer {
+  const int8_t* X8;
+  int c8;
+  float xlo, xhi, xmax;
+  int xint;
+};
+
 struct Sq8Scorer {
   const uint8_t* C;
   const float* vmin;
