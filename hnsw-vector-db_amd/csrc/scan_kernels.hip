@@ -1628,9 +1628,7 @@ __global__ void k_fill_empty(uint32_t* ids, float* d, size_t n) {
 // parallel; larger ones run one wave per slot.
 template <int E, class Scorer>
 static void launch_select(hipStream_t s, const SelectArgs& a, const Scorer& sc) {
-  if (E <= 2 && a.nslots <= 64 && a.nseg >= 64)
-    k_select<E, Scorer, (E <= 2 ? 16 : 4)><<<dim3(a.nslots), E <= 2 ? 1024 : 256, 0, s>>>(a, sc);
-  else if (a.nslots <= 256 && a.nseg >= 16)
+  if (a.nslots <= 256 && a.nseg >= 16)
     k_select<E, Scorer, 4><<<dim3(a.nslots), 256, 0, s>>>(a, sc);
   else
     k_select<E, Scorer, 1><<<dim3((a.nslots + 3) / 4), 256, 0, s>>>(a, sc);
@@ -1644,7 +1642,7 @@ static void launch_kth_v(hipStream_t s, const KthArgs& a) {
   k_kth<V><<<dim3((a.nq + 3) / 4), 256, 0, s>>>(a);
 }
 static int LaunchKth(hipStream_t s, const KthArgs& a) {
-  if (a.nq <= 64 && a.ngroups <= 4096) {  // a block per query
+  if (a.nq <= 1024 && a.ngroups <= 4096) {  // a block per query
     if (a.ngroups <= 1024) k_kth_block<1><<<dim3(a.nq), 1024, 0, s>>>(a);
     else if (a.ngroups <= 2048) k_kth_block<2><<<dim3(a.nq), 1024, 0, s>>>(a);
     else k_kth_block<4><<<dim3(a.nq), 1024, 0, s>>>(a);
