@@ -2568,6 +2568,23 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       // the fp32 sample pass runs 128-query tiles
       GemmGrid(sg, p32.nqt, p32.schunks, &sblocks);
       sg.chunk_rows = p32.schunk_rows;
+      if (gated) {
+        // the int8 sample pass when every query fits the int8 GEMM (one 256-query tile
+        // covers the batch, so the fp32 plan's sample chunks serve it), else the fp32 one;
+        // both write every group minimum (MODE 1)
+        GemmArgs s8 = sg;
+        s8.X8 = src->SX8;
+        s8.rn8 = src->Sinit8;
+        s8.Q8 = Q8;
+        s8.Qd = Qd;
+        s8.gate = fit8q;
+        s8.gate_n = int(nq);
+        s8.gate_on = 1;
+        VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, 1, 0, s, sblocks, s8));
+        sg.gate = fit8q;
+        sg.gate_n = int(nq);
+        sg.gate_on = 0;
+      }
       VDBG_RETURN_IF_ERROR(LaunchGemm(pd, metric, src->kind, 1, s, sblocks, sg));
     }
     VDBG_HIP(hipGetLastError());
