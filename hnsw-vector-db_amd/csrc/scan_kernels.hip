@@ -1686,11 +1686,13 @@ static FlatScorer FlatOf(const ScanSource& src, int kset) {
   return FlatScorer{src.X, src.pd, src.metric, kset};
 }
 // Whether a selection takes FlatScorer8: rows with a one-part int8 copy, and more keys to
-// re-score than one 64-lane pass (for a few keys the query packing costs more than it saves)
-// or every buffered candidate (the second chance).
-static bool UseFlat8(const ScanSource& src, size_t kk, int rescore) {
+// re-score than one 64-lane pass, every buffered candidate (the second chance), or a small
+// batch (latency-bound: the fp32 rows' loads form a chain of dependent rounds per lane, the
+// int8 rows' loads issue together).  For one pass over many queries the query packing costs
+// more than it saves.
+static bool UseFlat8(const ScanSource& src, size_t nq, size_t kk, int rescore) {
   return src.kind == 0 && src.X8 != nullptr && src.x8_parts == 1 &&
-         (rescore == 2 || kk + 8 > size_t(kWave));
+         (rescore == 2 || kk + 8 > size_t(kWave) || nq <= 256);
 }
 static FlatScorer8 Flat8Of(const ScanSource& src, int kset) {
   FlatScorer8 f;
@@ -1907,6 +1909,8 @@ struct TinyArgs {
   uint2* part;            // [q][chunk][kp] (key bits, row)
   float* bound;           // [q][chunk] the chunk's kp-th key, +inf when not full
   uint32_t* fb_count;     // [2] zeroed by the scan's block 0; [1] counts finished merges
+  int nchunks;            // blocks [0, nchunks) scan; block nchunks prepares the queries
+  PrepArgs pa;            // the queries' operands and bounds, for the merge's certificate
 };
 
 // Rows reach the lanes through a per-wave LDS tile: the wave reads 64 consecutive rows with
@@ -1923,6 +1927,10 @@ __global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
   constexpr int vpr = VPR;             // 16-byte vectors per row (pd / 16)
   int4* tile = tile_all + size_t(wave) * kWave * (vpr + 1);
+  if (int(blockIdx.x) == a.nchunks) {  // the extra block: one wave per query
+    if (wave < a.nq) (void)query_prep_wave(a.pa, wave);
+    return;
+  }
   if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
   const int pw = a.pd / 4;
   for (int e = tid; e < NQ * pw; e += 256) {
@@ -2073,7 +2081,7 @@ struct TinyMergeArgs {
   const uint2* part;
   const float* bound;
   int nchunks, kp, k;
-  FlatScorer sc;
+  FlatScorer8 sc;         // the rows and their int8 copy (the re-scoring reads the copy)
   uint32_t* out_ids;
   float* out_d;
   uint32_t* fb_list;
@@ -2084,19 +2092,23 @@ struct TinyMergeArgs {
 };
 
 // One block of 8 waves per query.  Each wave loads its share of the chunks' keys with all
-// loads in flight (up to 8 per lane at a time), keeps the k + 9 best (staged inserts), and
-// the 8 lists merge as a tree (three rounds); wave 0 then re-scores and certifies.
+// loads in flight (up to 8 per lane at a time) and keeps the 64 best (staged inserts).  The
+// 8 sorted lists merge by rank: every key counts the keys of the other lists below it
+// (binary searches in LDS) and lands at its rank among all 512, the first 64 kept; wave 0
+// then re-scores and certifies (the scan's extra block prepared the query's bound).
 __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   constexpr int W = 8;
   constexpr int B = 8;   // keys per lane loaded at once
-  __shared__ float md[W / 2][kWave];
-  __shared__ uint32_t mi[W / 2][kWave];
+  __shared__ float md[W][kWave];      // the waves' sorted lists
+  __shared__ uint32_t mi[W][kWave];
+  __shared__ float rd[kWave];         // the best 64 of all, by rank
+  __shared__ uint32_t ri[kWave];
   __shared__ float s_lb[W];
   __shared__ float sd[W][2 * kWave];
   __shared__ uint32_t si[W][2 * kWave];
+  __shared__ uint32_t ys[256];  // the query packed into int8 (Int8Query)
   const int q = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
-  if (wave == 0) query_prep_wave(a.pa, q);
   WaveTopK<1> top;
   top.init();
   float lb = __builtin_inff();
@@ -2104,13 +2116,32 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   const int c0 = min(a.nchunks, wave * per), c1 = min(a.nchunks, c0 + per);
   const size_t total = size_t(c1 - c0) * a.kp;
   const uint2* src = a.part + (size_t(q) * a.nchunks + c0) * a.kp;
+  // the first keys load while the bounds are reduced
+  auto load_keys = [&](size_t g0, uint2 (&v)[B]) {
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const size_t g = g0 + size_t(b) * kWave + lane;
+      v[b] = g < total ? src[g] : make_uint2(__float_as_uint(__builtin_inff()), kNoId);
+    }
+  };
+  uint2 v[B];
+  load_keys(0, v);
+  // Every chunk holds kp keys at or below its bound, so the best kp keys of all lie at or
+  // below the smallest bound LB: keys above it are skipped.
+  for (int ch = c0 + lane; ch < c1; ch += kWave) lb = fminf(lb, a.bound[size_t(q) * a.nchunks + ch]);
+  lb = wave_min(lb);
+  if (lane == 0) s_lb[wave] = lb;
+  __syncthreads();
+  float LB = s_lb[0];
+  for (int w = 1; w < W; ++w) LB = fminf(LB, s_lb[w]);
   // the key to beat: the (k + 9)-th (the certificate reads the key after the k + 8 scored)
   const int rl = (a.k + 9 - 1) & (kWave - 1);
   int staged = 0;
   auto push = [&](uint2 v) {
     const float td = __shfl(top.k.d[0], rl);
     const uint32_t ti = __shfl(top.k.id[0], rl);
-    const bool want = v.y != kNoId && nb_less(__uint_as_float(v.x), v.y, td, ti);
+    const bool want = v.y != kNoId && __uint_as_float(v.x) <= LB &&
+                      nb_less(__uint_as_float(v.x), v.y, td, ti);
     const uint64_t bal = __ballot(want);
     if (bal == 0) return;
     const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
@@ -2140,14 +2171,12 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
     }
   };
   for (size_t g0 = 0; g0 < total; g0 += size_t(B) * kWave) {
-    uint2 v[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const size_t g = g0 + size_t(b) * kWave + lane;
-      v[b] = g < total ? src[g] : make_uint2(__float_as_uint(__builtin_inff()), kNoId);
-    }
+    uint2 vn[B];
+    if (g0 + size_t(B) * kWave < total) load_keys(g0 + size_t(B) * kWave, vn);
 #pragma unroll
     for (int b = 0; b < B; ++b) push(v[b]);
+#pragma unroll
+    for (int b = 0; b < B; ++b) v[b] = vn[b];
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -2156,21 +2185,34 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
     const bool have = lane < staged;
     top.insert(have ? sd[wave][lane] : __builtin_inff(), have ? si[wave][lane] : kNoId);
   }
-  for (int ch = c0 + lane; ch < c1; ch += kWave) lb = fminf(lb, a.bound[size_t(q) * a.nchunks + ch]);
-  lb = wave_min(lb);
-  if (lane == 0) s_lb[wave] = lb;
-  // tree merge: at step h, wave w (w % 2h == h) hands its list to wave w - h
-  for (int h = 1; h < W; h <<= 1) {
-    const bool give = (wave % (2 * h)) == h;
-    if (give) {
-      md[wave >> 1][lane] = top.k.d[0];
-      mi[wave >> 1][lane] = top.k.id[0];
+  // rank merge: the key of lane i of wave w has rank i + sum over the other lists of the keys
+  // below it ((dist, id) order: real keys are distinct; the padding keys (+inf, none) of
+  // different lists share ranks past the real ones and write the same value)
+  md[wave][lane] = top.k.d[0];
+  mi[wave][lane] = top.k.id[0];
+  __syncthreads();
+  {
+    const float kd = top.k.d[0];
+    const uint32_t ki = top.k.id[0];
+    int rank = lane;
+    for (int w = 0; w < W; ++w) {
+      if (w == wave) continue;
+      int lo = 0, hi = kWave;  // the count of keys of list w below (kd, ki)
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (nb_less(md[w][mid], mi[w][mid], kd, ki)) lo = mid + 1; else hi = mid;
+      }
+      rank += lo;
     }
-    __syncthreads();
-    if ((wave % (2 * h)) == 0) top.insert(md[(wave + h) >> 1][lane], mi[(wave + h) >> 1][lane]);
-    __syncthreads();
+    if (rank < kWave) {
+      rd[rank] = kd;
+      ri[rank] = ki;
+    }
   }
+  __syncthreads();
   if (wave != 0) return;
+  top.k.d[0] = rd[lane];
+  top.k.id[0] = ri[lane];
   lb = __builtin_inff();
   for (int w = 0; w < W; ++w) lb = fminf(lb, s_lb[w]);
   const float* qv = a.pa.Q + size_t(q) * a.pa.pd;
@@ -2178,12 +2220,16 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   const float Qd = float(a.pa.Qd[q]);
   const bool fits = a.pa.fit8q[q] != 0;
   // exact re-scoring of the best n1 keys, certificate against every unscored row
+  // (rows of 128 bytes from the int8 copy: their loads issue together, where the fp32
+  // rows' 512 bytes per lane form a chain of dependent load rounds)
   const int n1 = min(kWave - 1, a.k + 8);
+  const Int8Query p8 = int8_query(a.sc.X8, a.sc.c8, a.sc.xlo, a.sc.xhi, a.sc.xmax, a.sc.xint,
+                                  a.sc.metric, a.sc.pd, qv, ys);
   float d = __builtin_inff();
   uint32_t id = kNoId;
   if (lane < n1 && top.k.id[0] != kNoId) {
     id = top.k.id[0];
-    d = a.sc(qv, id);
+    d = p8.on ? int8_distance(a.sc.X8, a.sc.c8, a.sc.metric, a.sc.pd, p8, id) : a.sc(qv, id);
   }
   WaveKeys<1> r;
   r.d[0] = d;
@@ -2247,9 +2293,9 @@ template <int NQ>
 static void launch_tiny(hipStream_t s, int blocks, const TinyArgs& a) {
   const size_t tile = size_t(4) * kWave * (a.pd / 16 + 1) * sizeof(int4);
   switch (a.pd) {
-    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks), 256, tile, s>>>(a); break;
-    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks), 256, tile, s>>>(a); break;
-    default: k_tiny_scan<NQ, 16><<<dim3(blocks), 256, tile, s>>>(a); break;
+    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks + 1), 256, tile, s>>>(a); break;
+    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks + 1), 256, tile, s>>>(a); break;
+    default: k_tiny_scan<NQ, 16><<<dim3(blocks + 1), 256, tile, s>>>(a); break;
   }
 }
 
@@ -2281,19 +2327,19 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
   uint32_t* fb_list = W.take<uint32_t>(nq);
   uint32_t* fb_count = W.take<uint32_t>(2);
   c->last_gemm_bits = 8;
+  PrepArgs pa{Q, nullptr, int(nq), pd, src->kind, src->metric, src->stats, src->rmag,
+              src->vmin, src->scale, shift, eb, exact, nullptr, nullptr, nullptr,
+              src->x16_parts, src->x16_exp, Q8, Qd, nullptr, fit8q, src->c8, nullptr};
   TinyArgs ta{Q, int(nq), pd, src->metric, src->c8, int(kk), kp, src->X8, src->init8, allow, N,
-              chunk, part, bound, fb_count};
+              chunk, part, bound, fb_count, nchunks, pa};
   {
     ProfScope ps(c, "flat_gemm", s);
     if (nq == 1) launch_tiny<1>(s, nchunks, ta);
     else launch_tiny<2>(s, nchunks, ta);
     VDBG_HIP(hipGetLastError());
   }
-  PrepArgs pa{Q, nullptr, int(nq), pd, src->kind, src->metric, src->stats, src->rmag,
-              src->vmin, src->scale, shift, eb, exact, nullptr, nullptr, nullptr,
-              src->x16_parts, src->x16_exp, Q8, Qd, nullptr, fit8q, src->c8, nullptr};
   const uint32_t seq = NextFlagSeq(c);
-  TinyMergeArgs ma{pa, part, bound, nchunks, kp, int(kk), FlatOf(*src, c->kset), out_ids, out_d,
+  TinyMergeArgs ma{pa, part, bound, nchunks, kp, int(kk), Flat8Of(*src, c->kset), out_ids, out_d,
                    fb_list, fb_count, c->host_flag_dev, seq, c->test_fallbacks};
   {
     ProfScope ps(c, "select", s);
@@ -2676,7 +2722,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   se.force_fallback = c->test_fallbacks;
   {
     ProfScope ps(c, "select", s);
-    if (UseFlat8(*src, kk, 1)) {
+    if (UseFlat8(*src, nq, kk, 1)) {
       VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer8, s, se, Flat8Of(*src, c->kset));
     } else if (src->kind == 0) {
       VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, se, FlatOf(*src, c->kset));
@@ -2700,7 +2746,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   s2.fb_count = fb_count + 1;
   {
     ProfScope ps(c, "rescore", s);
-    if (UseFlat8(*src, kk, 2)) {
+    if (UseFlat8(*src, nq, kk, 2)) {
       VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer8, s, s2, Flat8Of(*src, c->kset));
     } else if (src->kind == 0) {
       VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, s2, FlatOf(*src, c->kset));
