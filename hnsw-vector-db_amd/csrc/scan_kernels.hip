@@ -2068,7 +2068,7 @@ __global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
   for (int q = 0; q < NQ; ++q) {
     if (q >= a.nq) break;
     for (int w = 0; w < 3; ++w) top[q].insert(md[w][q][lane], mi[w][q][lane]);
-    const size_t o = size_t(q) * gridDim.x + blockIdx.x;
+    const size_t o = size_t(q) * a.nchunks + blockIdx.x;  // (the grid has one more block)
     if (lane < a.kp) a.part[o * a.kp + lane] = make_uint2(__float_as_uint(top[q].k.d[0]), top[q].k.id[0]);
     const float kth = __shfl(top[q].k.d[0], rl);
     const uint32_t kid = __shfl(top[q].k.id[0], rl);

@@ -262,3 +262,17 @@ def test_tiny_batches_forced_fallback_and_filter(ctx, oracle, nq):
     gi, gd = ds.flat_search(qs, 10, allow=words)
     od, oi = oracle.flat_search(base, qs, 10, allow=words)
     _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("pick", [(0, -1), (-1, 0), (-1, -2)])
+def test_tiny_two_queries_edge_chunks(ctx, oracle, pick):
+    # two queries on the tiny-batch path whose nearest rows sit in the first and the last
+    # row chunk: each query's chunk lists and bounds must be the ones the merge reads
+    base = datagen.sift_like(60000, 128, 6621)
+    qs = np.ascontiguousarray(base[list(pick)])
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 10)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
