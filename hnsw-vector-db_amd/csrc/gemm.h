@@ -83,6 +83,14 @@ __host__ __device__ constexpr int Gemm16Kc(int pd, int split) {
   return 16;
 }
 
+// The fp16 GEMM on float rows held as high halves (split 3) keeps each wave's query fragments
+// for every K chunk in registers (one 32-query block per wave) when the rows span several
+// chunks and the fragments fit: up to 512 dims (128 VGPRs of fragments).
+constexpr int kGemm16ResMaxPd = 512;
+inline bool Gemm16ResQueries(size_t pd) {
+  return Gemm16Kc(int(pd), 3) < int(pd) && pd <= size_t(kGemm16ResMaxPd);
+}
+
 // K chunk of the int8 GEMM: the whole row up to 128 dims, else the largest of 128/64/32
 // dividing it.
 __host__ __device__ constexpr int Gemm8Kc(int pd) {
@@ -122,7 +130,8 @@ int LaunchGemm8(size_t pd, int metric, int qb, int mode, int sq, hipStream_t s, 
 // fp16 GEMM (gemm16.hip): qb query blocks of 32 per wave (1 or 2), mode 0 = threshold pass
 // into candidate buffers, 1 = group minima of the sample; split 1 = SQ8 codes against the
 // two-part query operand (qb 2, both register sets on the same 32 queries), 2 = two-part
-// float rows against the two-part query operand.
+// float rows against the two-part query operand, 3 = float rows as high halves (qb 2, or
+// qb 1 with resident query fragments where Gemm16ResQueries).
 int LaunchGemm16(size_t pd, int metric, int qb, int mode, int split, hipStream_t s, int blocks,
                  const GemmArgs& a);
 

@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <string>
 #include <type_traits>
+#include <utility>
 
 #include "gemm.h"
 #include "vdbg_device.h"
@@ -58,7 +59,20 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));  // 16-byte vector (
 // x_h q_h, one MFMA per product, two distinct 32-query blocks per wave, and the epilogue
 // fma(Qf, acc, norm).  The dropped x_h q_l + x_l q_h + x_l q_l is at most
 // (2^-10 + 2^-22) |x_i q_i| per product; k_query_prep widens the query's bound by it.
-template <int PD, int METRIC, int QB, int MODE, int SPLIT>
+//
+// QRES (rows wider than one K chunk, SPLIT 3, one 32-query block per wave): the wave's query
+// fragments for every K chunk stay in registers for the whole launch, so each stage loads
+// only its rows.  Otherwise they are reloaded for every stage of every tile: at 384 dims
+// with 64 queries per wave that was four times the row bytes through the vector cache, which
+// then bounds the kernel.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  [&]<int... I>(std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+  }(std::make_integer_sequence<int, N>{});
+}
+
+template <int PD, int METRIC, int QB, int MODE, int SPLIT, int QRES = 0>
 __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int KC = Gemm16Kc(PD, SPLIT);
   constexpr int NKC = PD / KC;
@@ -75,7 +89,8 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   constexpr int NQB = (SPLIT == 1 || SPLIT == 2) ? 1 : QB;  // distinct 32-query blocks per wave
   constexpr int QT = 128 * NQB;                    // queries per block
   static_assert(PD % KC == 0 && KC % 16 == 0, "K chunking");
-  static_assert(!SPLIT || QB == 2, "the split operand takes both register sets");
+  static_assert(!SPLIT || QB == 2 || (SPLIT == 3 && QRES), "the split operand takes both register sets");
+  static_assert(!QRES || (SPLIT == 3 && QB == 1 && NKC > 1), "resident queries: SPLIT 3, one block");
   __shared__ __attribute__((aligned(16))) uint16_t xs[2][kGemmRows * STR];
   __shared__ __attribute__((aligned(16))) float xns[3][kGemmRows];
 
@@ -116,7 +131,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
   // nq - 1; their values are never emitted.
   // Query fragments of a stage's K chunk.  With one chunk they load once; with several, the
   // next stage's fragments load a step ahead into the other set (QF sets in all).
-  constexpr int QF = NKC > 1 ? 2 : 1;
+  constexpr int QF = QRES ? NKC : (NKC > 1 ? 2 : 1);
   half8 qv[QF][QB][NKB];
   const uint16_t* qrow[QB];
 #pragma unroll
@@ -131,7 +146,10 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
       for (int kb = 0; kb < NKB; ++kb)
         qv[f][qb][kb] = *reinterpret_cast<const half8*>(qrow[qb] + kc * KC + kb * 16);
   };
-  load_q(0, 0);
+  if constexpr (QRES)
+    static_for<NKC>([&](auto I) { load_q(decltype(I)::value, decltype(I)::value); });
+  else
+    load_q(0, 0);
 
   // lane offsets (in halfs) of the stage's 16-byte vectors: row f / VEC_PER_ROW, column
   // f % VEC_PER_ROW of the 64 x KC stage
@@ -204,7 +222,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     constexpr int QS = decltype(fcur)::value;  // the query fragment set of this step
     const int tile = sidx / NKC, kc = sidx - tile * NKC;
     const uint32_t base = r_begin + uint32_t(tile) * kGemmRows;
-    if constexpr (QF == 2)  // the next stage's K chunk (a harmless repeat past the end)
+    if constexpr (QF == 2 && !QRES)  // the next stage's K chunk (a harmless repeat past the end)
       load_q(QS ^ 1, (kc + 1 == NKC) ? 0 : kc + 1);
     load_stage(Y, sidx + 2);
     // keep the scheduler from sinking Y's loads below the MFMAs (which would shorten the
@@ -235,22 +253,29 @@ __global__ __launch_bounds__(256, 2) void k_gemm16(GemmArgs a) {
     // accumulator chains; their values are never emitted
     const uint16_t* xa0 = &xs[sidx & 1][j * STR + h * 8];
     const uint16_t* xa1 = xa0 + 32 * STR;
+    auto mfma_stage = [&](auto qsel) {  // with query fragment set QI
+      constexpr int QI = decltype(qsel)::value;
 #pragma unroll
-    for (int kb = 0; kb < NKB; ++kb) {
-      const half8 x0 = *reinterpret_cast<const half8*>(xa0 + kb * 16);
-      const half8 x1 = *reinterpret_cast<const half8*>(xa1 + kb * 16);
+      for (int kb = 0; kb < NKB; ++kb) {
+        const half8 x0 = *reinterpret_cast<const half8*>(xa0 + kb * 16);
+        const half8 x1 = *reinterpret_cast<const half8*>(xa1 + kb * 16);
 #pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[QS][qb][kb], acc[qb][0], 0, 0, 0);
-        acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[QS][qb][kb], acc[qb][1], 0, 0, 0);
+        for (int qb = 0; qb < QB; ++qb) {
+          acc[qb][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x0, qv[QI][qb][kb], acc[qb][0], 0, 0, 0);
+          acc[qb][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(x1, qv[QI][qb][kb], acc[qb][1], 0, 0, 0);
+        }
+        if constexpr (SPLIT == 2) {  // x_l q_h into the cross-term accumulator
+          const half8 y0 = *reinterpret_cast<const half8*>(xa0 + KC + kb * 16);
+          const half8 y1 = *reinterpret_cast<const half8*>(xa1 + KC + kb * 16);
+          acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y0, qv[QI][0][kb], acc[1][0], 0, 0, 0);
+          acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y1, qv[QI][0][kb], acc[1][1], 0, 0, 0);
+        }
       }
-      if constexpr (SPLIT == 2) {  // x_l q_h into the cross-term accumulator
-        const half8 y0 = *reinterpret_cast<const half8*>(xa0 + KC + kb * 16);
-        const half8 y1 = *reinterpret_cast<const half8*>(xa1 + KC + kb * 16);
-        acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y0, qv[QS][0][kb], acc[1][0], 0, 0, 0);
-        acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(y1, qv[QS][0][kb], acc[1][1], 0, 0, 0);
-      }
-    }
+    };
+    if constexpr (QRES)  // the stage's K chunk selects the resident set (one branch per set)
+      static_for<NKC>([&](auto I) { if (kc == decltype(I)::value) mfma_stage(I); });
+    else
+      mfma_stage(std::integral_constant<int, QS>{});
     if (sidx + 1 < nstages) store_stage(X, sidx + 1);
     __syncthreads();
     if (kc != NKC - 1) return;
@@ -369,6 +394,12 @@ static void launch16_pm(int qb, int mode, int split, hipStream_t s, int blocks,
     if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 2><<<g, t, 0, s>>>(a);
     else k_gemm16<PD, METRIC, 2, 1, 2><<<g, t, 0, s>>>(a);
   } else if (split == 3) {
+    if constexpr (Gemm16Kc(PD, 3) < PD && PD <= kGemm16ResMaxPd) {
+      if (mode == 0 && qb == 1) {  // resident query fragments
+        k_gemm16<PD, METRIC, 1, 0, 3, 1><<<g, t, 0, s>>>(a);
+        return;
+      }
+    }
     if (mode == 0) k_gemm16<PD, METRIC, 2, 0, 3><<<g, t, 0, s>>>(a);
     else k_gemm16<PD, METRIC, 2, 1, 3><<<g, t, 0, s>>>(a);
   } else if (mode == 0) {
@@ -391,7 +422,7 @@ static void launch16_pd(int metric, int qb, int mode, int split, hipStream_t s, 
 int LaunchGemm16(size_t pd, int metric, int qb, int mode, int split, hipStream_t s, int blocks,
                  const GemmArgs& a) {
   if (qb != 1 && qb != 2) return SetError(kInternal, "GEMM16: query blocks per wave");
-  if ((mode == 1 || split) && qb != 2)
+  if ((mode == 1 || split) && qb != 2 && !(split == 3 && mode == 0 && Gemm16ResQueries(pd)))
     return SetError(kInternal, "GEMM16: the sample pass and the split operand run 2 blocks");
   switch (pd) {
 #define VDBG_PD16(P) \

@@ -2403,6 +2403,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // (float rows only for GEMMs large enough to repay the batch's operand pass and flag
   // readback: the fp16 split GEMM costs about 2 N nq pd / 2e14 s, the int8 one 0.6 of that)
   const bool single = split == 3 && try16;
+  // rows wider than one K chunk keep each wave's query fragments resident (one 32-query
+  // block per wave, gemm16.hip QRES); the sample pass keeps two blocks per wave
+  const bool wide16 = single && Gemm16ResQueries(pd);
   const bool try8f = c->fp16_gemm && c->int8_gemm && split == 2 &&
                      src->X8 != nullptr && src->x8_parts == 2 && Gemm8Supported(pd) &&
                      double(N) * double(nq) * double(pd) >= c->int8_float_min_work;
@@ -2428,17 +2431,20 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int ngroups = int((S + 31) / 32) * 2;
   struct Plan {
     int qb, nqt, nchunks, caph, nseg, schunks;
+    int snqt;  // query tiles of the sample pass
     uint32_t chunk_rows, schunk_rows;
   };
-  auto make_plan = [&](int qb, int tile_queries, int slots, int max_chunks = kMaxSeg / 2) {
+  auto make_plan = [&](int qb, int tile_queries, int slots, int max_chunks = kMaxSeg / 2,
+                       int sample_tile = 0) {
     Plan p{};
     p.qb = qb;
     p.nqt = int((nq + tile_queries - 1) / tile_queries);
+    p.snqt = sample_tile ? int((nq + sample_tile - 1) / sample_tile) : p.nqt;
     p.nchunks = PlanChunks(p.nqt, N, slots, max_chunks);
     p.chunk_rows = (N + p.nchunks - 1) / p.nchunks;
     p.chunk_rows = (p.chunk_rows + 63) / 64 * 64;
     p.nchunks = int((N + p.chunk_rows - 1) / p.chunk_rows);
-    p.schunks = PlanChunks(p.nqt, S, slots, int((S + 63) / 64));
+    p.schunks = PlanChunks(p.snqt, S, slots, int((S + 63) / 64));
     p.schunk_rows = (S + p.schunks - 1) / p.schunks;
     p.schunk_rows = (p.schunk_rows + 63) / 64 * 64;
     p.schunks = int((S + p.schunk_rows - 1) / p.schunk_rows);
@@ -2455,7 +2461,8 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const int slots8 = (try8op ? (try8f ? 2 : Gemm8Occupancy(pd)) : Gemm8Occupancy(pd)) * c->cu_count;
   auto plan_all = [&](Plan* p32, Plan* p16, Plan* p8, int max_chunks) {
     *p32 = make_plan(1, 128, slots, max_chunks);
-    *p16 = single  ? make_plan(2, 256, slots, max_chunks)
+    *p16 = wide16  ? make_plan(1, 128, slots, max_chunks, 256)
+           : single ? make_plan(2, 256, slots, max_chunks)
            : split ? make_plan(2, 128, slots, max_chunks)
                    : (nq > 128 ? make_plan(2, 256, slots, max_chunks)
                                : make_plan(1, 128, slots, max_chunks));
@@ -2601,14 +2608,14 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
       sg.Q8 = Q8;
       sg.Qd = Qd;
       sg.e8 = e8;
-      GemmGrid(sg, P.nqt, P.schunks, &sblocks);
+      GemmGrid(sg, P.snqt, P.schunks, &sblocks);
       if (top8) sg.ngroups = ngroups8;
       VDBG_RETURN_IF_ERROR(LaunchGemm8(pd, metric, 2, top8 ? 2 : 1, sq8, s, sblocks, sg));
-    } else if (use16 && P.qb == 2) {
+    } else if (use16 && (P.qb == 2 || wide16)) {
       sg.X16 = src->SX16;
       sg.Q16 = Q16;
       sg.Qf = Qf;
-      GemmGrid(sg, P.nqt, P.schunks, &sblocks);
+      GemmGrid(sg, P.snqt, P.schunks, &sblocks);
       VDBG_RETURN_IF_ERROR(LaunchGemm16(pd, metric, 2, 1, split, s, sblocks, sg));
     } else {
       // the fp32 sample pass runs 128-query tiles
