@@ -401,7 +401,8 @@ int Sq8Encode(Ctx* c, const Dataset* ds, const float* vmin_dev, const float* sca
 
 // Sample position p holds row floor(bitrev(p) * N / Smax): every power-of-two prefix of the
 // sample is an evenly strided subset of the rows.
-__global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __restrict__ X16,
+__global__ void k_gather_sample(const float* __restrict__ X, const uint32_t* __restrict__ Xmap,
+                                const uint16_t* __restrict__ X16,
                                 int pd16, const uint8_t* __restrict__ C,
                                 const int8_t* __restrict__ X8, int pd8,
                                 const int* __restrict__ init8,
@@ -414,8 +415,9 @@ __global__ void k_gather_sample(const float* __restrict__ X, const uint16_t* __r
   const uint32_t p = blockIdx.x;
   if (p >= smax) return;
   const uint32_t row = uint32_t((uint64_t(bitrev(p, bits)) * N) / smax);
+  const size_t xrow = Xmap != nullptr ? Xmap[row] : row;
   for (int i = threadIdx.x; i < pd; i += blockDim.x) {
-    if (X) SX[size_t(p) * pd + i] = X[size_t(row) * pd + i];
+    if (X) SX[size_t(p) * pd + i] = X[xrow * pd + i];
     if (C) SC[size_t(p) * pd + i] = C[size_t(row) * pd + i];
   }
   for (int i = threadIdx.x; X8 != nullptr && i < pd8; i += blockDim.x)
@@ -438,7 +440,8 @@ uint32_t SampleRows(uint32_t N) {
 size_t SampleBytes(const ScanSource& src, uint32_t smax) {
   auto al = [](size_t b) { return (b + 255) & ~size_t(255); };
   const size_t pd = src.pd;
-  return al(src.kind == 0 ? size_t(smax) * pd * sizeof(float) : 0) +
+  // (a source reading its parent's rows through Xmap ranks on its fp16 copy: no fp32 sample)
+  return al(src.kind == 0 && src.Xmap == nullptr ? size_t(smax) * pd * sizeof(float) : 0) +
          al(src.X16 != nullptr ? size_t(smax) * pd * src.x16_parts * sizeof(uint16_t) : 0) +
          al(src.kind == 1 ? size_t(smax) * pd : 0) + al(size_t(smax) * sizeof(float)) +
          al(size_t(smax) * sizeof(uint32_t)) +
@@ -457,7 +460,8 @@ int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
     p += (b + 255) & ~size_t(255);
     return r;
   };
-  src->SX = reinterpret_cast<float*>(take(src->kind == 0 ? size_t(smax) * pd * sizeof(float) : 0));
+  const bool fp32 = src->kind == 0 && src->Xmap == nullptr;
+  src->SX = reinterpret_cast<float*>(take(fp32 ? size_t(smax) * pd * sizeof(float) : 0));
   src->SX16 = reinterpret_cast<uint16_t*>(
       take(src->X16 != nullptr ? size_t(smax) * pd * src->x16_parts * sizeof(uint16_t) : 0));
   src->SC = reinterpret_cast<uint8_t*>(take(src->kind == 1 ? size_t(smax) * pd : 0));
@@ -466,7 +470,7 @@ int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
   src->SX8 = reinterpret_cast<int8_t*>(
       take(src->X8 != nullptr ? size_t(smax) * pd * src->x8_parts : 0));
   src->Sinit8 = reinterpret_cast<int*>(take(src->X8 != nullptr ? size_t(smax) * sizeof(int) : 0));
-  k_gather_sample<<<dim3(smax), 128, 0, s>>>(src->kind == 0 ? src->X : nullptr,
+  k_gather_sample<<<dim3(smax), 128, 0, s>>>(fp32 ? src->X : nullptr, src->Xmap,
                                              src->X16, int(pd) * src->x16_parts,
                                              src->kind == 1 ? src->C : nullptr, src->X8,
                                              int(pd) * src->x8_parts, src->init8, src->rn,
@@ -1683,7 +1687,7 @@ static void launch_rerank(hipStream_t s, const RerankArgs& a) {
   }
 
 static FlatScorer FlatOf(const ScanSource& src, int kset) {
-  return FlatScorer{src.X, src.pd, src.metric, kset};
+  return FlatScorer{src.X, src.pd, src.metric, kset, src.Xmap};
 }
 // Whether a selection takes FlatScorer8: rows with a one-part int8 copy, and more keys to
 // re-score than one 64-lane pass, every buffered candidate (the second chance), or a small
@@ -2570,6 +2574,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     use8 = try8any && c->host_pinned[1] != 0;
     use16 = try16 && !use8 && (split != 0 || c->host_pinned[0] != 0);
   }
+  // a source reading its parent's rows through Xmap ranks on its fp16 copy (no fp32 GEMM)
+  if (src->Xmap != nullptr && !use8 && !use16)
+    return SetError(kInternal, "scan: remapped fp32 rows on the fp32 GEMM");
   // the bound of the GEMM the batch ranks on
   const float* ebx = use8 && try8op ? eb8 : eb;
   c->last_gemm_bits = use8 ? 8 : (use16 ? 16 : 32);

@@ -126,6 +126,9 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   }
   const size_t row16_bytes = keep16 ? src->x16_parts * pd * sizeof(uint16_t) : 0;
   const size_t row8_bytes = keep8 ? pd * src->x8_parts : 0;  // the int8 copy
+  // Float rows held as high fp16 halves rank on that copy alone, so the fp32 rows are not
+  // gathered: the exact re-scoring reads the parent's rows through the id map.
+  const bool map32 = src->kind == 0 && src->x16_approx && keep16 && c->fp16_gemm;
   // the compacted source's sample lives in the same stream-ordered allocation
   ScanSource cs = *src;
   cs.N = count;
@@ -134,7 +137,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(nullptr, tmp_bytes, static_cast<uint32_t*>(nullptr),
                                             static_cast<uint32_t*>(nullptr), int(nwords), s));
   const size_t bytes = (nwords + 1) * 4 * 2 +
-                       size_t(count) * (4 + 4 + row_bytes + row16_bytes + row8_bytes +
+                       size_t(count) * (4 + 4 + (map32 ? 0 : row_bytes) + row16_bytes + row8_bytes +
                                         (src->init8 != nullptr ? 4 : 0)) +
                        sample_bytes + tmp_bytes + 4096 + 512 + 16 * 256;
   // the context's compaction scratch: reused in stream order by the next call
@@ -147,7 +150,7 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* pre = reinterpret_cast<uint32_t*>(take((nwords + 1) * 4));
   uint32_t* ids = reinterpret_cast<uint32_t*>(take(size_t(count) * 4 + 4));
   float* rn = reinterpret_cast<float*>(take(size_t(count) * 4 + 4));
-  void* rows = take(size_t(count) * row_bytes + 16);
+  void* rows = map32 ? nullptr : take(size_t(count) * row_bytes + 16);
   void* rows16 = row16_bytes != 0 ? take(size_t(count) * row16_bytes + 16) : nullptr;
   void* rows8 = row8_bytes != 0 ? take(size_t(count) * row8_bytes + 16) : nullptr;
   int* init8 = src->init8 != nullptr ? reinterpret_cast<int*>(take(size_t(count) * 4 + 4)) : nullptr;
@@ -159,7 +162,9 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     tmp = take(tmp_bytes + 16);
     VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
     k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre, ids);
-    if (src->kind == 0) {
+    if (map32) {
+      // (no fp32 rows: see cs.Xmap below)
+    } else if (src->kind == 0) {
       const size_t row_f4 = pd / 4;
       k_gather_f4<<<dim3(unsigned((count * row_f4 + 255) / 256)), 256, 0, s>>>(
           reinterpret_cast<const float4*>(src->X), row_f4, ids, count, static_cast<float4*>(rows));
@@ -185,7 +190,8 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
     VDBG_HIP(hipGetLastError());
   }
-  cs.X = src->kind == 0 ? static_cast<const float*>(rows) : nullptr;
+  cs.X = src->kind == 0 ? (map32 ? src->X : static_cast<const float*>(rows)) : nullptr;
+  cs.Xmap = map32 ? ids : nullptr;
   cs.X16 = static_cast<const uint16_t*>(rows16);
   cs.X8 = static_cast<const int8_t*>(rows8);
   cs.init8 = init8;

@@ -116,7 +116,7 @@ int ExactScanAll(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_
   if (nq == 0 || kk == 0) return kOk;
   if (kk > (size_t(1) << 30)) return SetError(kInvalidArgument, "too many results per query");
   if (src.kind == 0)
-    return ExactAllT(c, src, FlatScorer{src.X, src.pd, src.metric, c->kset}, Q, nq, kk, allow,
+    return ExactAllT(c, src, FlatScorer{src.X, src.pd, src.metric, c->kset, src.Xmap}, Q, nq, kk, allow,
                      out_ids, out_d, s);
   if (src.kind == 2)
     return ExactAllT(c, src, PqScorer{src.C, src.pq_m}, Q, nq, kk, allow, out_ids, out_d, s);

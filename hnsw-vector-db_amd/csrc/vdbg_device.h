@@ -402,8 +402,10 @@ struct PqScorer {
 struct FlatScorer {
   const float* X;
   int pd, metric, kset;
+  const uint32_t* map = nullptr;  // nullable: row r is row map[r] of X
   __device__ __forceinline__ float operator()(const float* q, uint32_t row) const {
-    return metric_exact_k(kset, metric, q, X + size_t(row) * pd, pd);
+    const size_t r = map != nullptr ? map[row] : row;
+    return metric_exact_k(kset, metric, q, X + r * pd, pd);
   }
 };
 

@@ -143,6 +143,8 @@ struct ScanSource {
   int kind = 0;
   int pq_m = 0;                 // kind 2: bytes per code
   const float* X = nullptr;     // kind 0: n x pd rows
+  const uint32_t* Xmap = nullptr;  // kind 0, nullable: row r of this source is row Xmap[r] of
+                                   // X (a compacted source reading its parent's fp32 rows)
   const uint16_t* X16 = nullptr;  // rows as fp16 for the fp16 GEMM (gemm16.hip), or null:
                                   // kind 0 integer rows exactly (x16_parts 1), kind 0 float
                                   // rows as 2^x16_exp-scaled h + l pairs (x16_parts 2, [h|l]
