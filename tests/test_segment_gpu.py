@@ -211,3 +211,27 @@ def test_collection_search_end_to_end(ctx, oracle):
     ge, gd = vdbg.merge_parts(ctx, pdist, prow, ext, off)
     oe, od = _oracle_merge(oracle, odist, orow, ext, off, k)
     assert (ge == oe).all() and (gd.view(np.uint32) == od.view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("k,fallbacks", [(10, 0), (10, 1), (10, 2), (300, 0)])
+def test_flat_filter_float_rows_remapped(ctx, oracle, k, fallbacks):
+    # float rows held as high fp16 halves, at most half allowed: the compacted source keeps
+    # no fp32 rows and re-scores through the id map, on the first pass, the second chance
+    # (fallbacks 1), the exact re-scan (fallbacks 2) and the k > 240 exact path
+    n, nq = 30000, 48
+    print(f"remapped compaction k={k} fallbacks={fallbacks}", flush=True)
+    base = datagen.clustered_unit(n, 384, 61, 40, 100, 0.5)
+    qs = datagen.clustered_unit(nq, 384, 62, 40, 100, 0.5)
+    allow, rows = _mask(n, 0.2, 63)
+    ds = vdbg.Dataset(ctx, base, 384, metric="cosine")
+    ctx.set_test_fallbacks(fallbacks)
+    try:
+        gi, gd = ds.flat_search(qs, k, allow=allow)
+        if fallbacks == 2:
+            assert ctx.last_fallbacks() == nq
+    finally:
+        ctx.set_test_fallbacks(0)
+    od, oi = oracle.flat_search(base, qs, k, metric="cosine", allow=allow)
+    _same(gi, gd, oi, od)
+    real = gi[gi != vdbg.NO_ID]
+    assert np.isin(real, rows).all()
