@@ -2416,12 +2416,13 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const bool try8op = try8s || try8f;  // the two-part query operand (k_sq8_operand8)
   const bool try8any = try8 || try8op;
   const int sq8 = try8s ? 1 : (try8f ? 2 : 0);
-  // Sample size: about kk * N / S rows pass the threshold per query, and every pass costs a
-  // scattered buffer write and a select insertion (and on the exact fp16 GEMM every 32-row
-  // block holding one takes the per-value test), while the pre-pass costs S / N of the main
-  // GEMM.  S >= kk * N / P keeps the passes near P per query until the sample cap: P = 160
-  // for large batches on the exact fp16 GEMM, whose MFMA work per row is smallest, 640
-  // otherwise (N / 64 at k = 10).
+  // Sample size: every row passing the threshold costs a scattered buffer write and a select
+  // insertion (and on the exact fp16 and int8 GEMMs every 32-row block holding one takes the
+  // per-value test), while the pre-pass costs S / N of the main GEMM.  S >= kk * N / P until
+  // the sample cap: P = 160 for large batches on the exact GEMMs, whose MFMA work per row is
+  // smallest, 640 otherwise (N / 64 at k = 10).  (Measured at 1M x 128, k = 10, on the int8
+  // GEMM: a 16,384-row sample saved 0.07 ms of pre-pass but its threshold admitted ~300 rows
+  // per query instead of ~110, and the main pass and select lost 0.17 ms.)
   uint32_t S = 1;
   const uint64_t passes = try16 && split == 0 && nq >= 1024 ? 160 : 640;  // (int8 too)
   const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,

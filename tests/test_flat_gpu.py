@@ -155,14 +155,16 @@ def test_flat_large_k(ctx, oracle, k, metric, frac):
 
 
 def _sample_aligned_rows(n, dim, near):
-    # The threshold sample takes every (n / 65536)-th row.  Here every near row sits on a
-    # sampled position (rows 4 i, n = 4 x 65536) and every other row is far away, so the
-    # sample holds all of the near rows and the lower-rank admission threshold keeps fewer
-    # rows than the depth asks for: the certificate must refuse it and the re-scan answer.
+    # A threshold sample of S rows takes every (n / S)-th row (its first 2^b positions hold
+    # the multiples of n / 2^b).  Here every near row sits on a multiple of n / 2048, so any
+    # sample of at least 2,048 rows holds all of them, and every other row is far away: the
+    # lower-rank admission threshold then keeps fewer rows than the depth asks for, and the
+    # certificate must refuse it and the re-scan answer.
     rng = np.random.default_rng(5151)
     base = (100.0 + rng.random((n, dim), dtype=np.float32)).astype(np.float32)
-    base[4 * np.arange(near), :] = 0.0
-    base[4 * np.arange(near), 0] = 0.01 * (1 + np.arange(near, dtype=np.float32))
+    at = (n // 2048) * np.arange(near)
+    base[at, :] = 0.0
+    base[at, 0] = 0.01 * (1 + np.arange(near, dtype=np.float32))
     qs = np.zeros((8, dim), np.float32)
     qs[:, 1] = 1e-3 * np.arange(8, dtype=np.float32)
     return base, qs
