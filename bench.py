@@ -587,23 +587,38 @@ def main():
         gi, gd = gpu_out()
         s_ms = prof["ivf_scan"][0] / max(1, prof["ivf_scan"][1])
         # algorithmic bytes of the list scan: the codes and ids of every scanned row (m + 4
-        # bytes each).  The per-list term-2 tables the scan also reads (m x 256 floats per
-        # probed list, ivf_pq.cc:197-217) are reported beside it, not counted in `achieved`.
-        t2_bytes = nq * nprobe * m * 256 * 4
+        # bytes each).  The row-sum scan reads each row's code and its 4-byte term-2 sum (ids
+        # only for the rows it scores exactly); the per-list term-2 tables the reference reads
+        # (m x 256 floats per probed list, ivf_pq.cc:197-217) are not streamed.
         alg_bytes = scanned * (m + 4)
         gbs = alg_bytes / (s_ms * 1e-3) / 1e9
         r = {"qps": nq * args.steps / el, "ms_per_step": el * 1e3 / args.steps,
-             "kernel": "k_ivf_scan", "kernel_ms": s_ms, "achieved": gbs, "unit": "GB/s",
+             "kernel": "k_ivf_scan_rs", "kernel_ms": s_ms, "achieved": gbs, "unit": "GB/s",
              "peak": HBM_PEAK_GBS, "bound": "hbm",
              "algorithmic_bytes": "codes + ids of the scanned rows",
              "algorithmic_bytes_per_launch": alg_bytes,
-             "term2_bytes_per_launch": t2_bytes,
-             "term2_GBps": t2_bytes / (s_ms * 1e-3) / 1e9,
+             "stream_bytes_per_launch": scanned * (m + 4),
+             "stream_note": "codes + per-row term-2 sums (m + 4 bytes per scanned row)",
              "codes_scanned_per_query": scanned / nq,
              "kernel_ms_per_step": {kk: v[0] / args.steps for kk, v in prof.items()},
              "nlist": nlist, "m": m, "nprobe": nprobe, "rerank": rerank,
              "kmeans_iters": 20, "build_s": build_s}
         log(f"ivfpq: {r['qps']:.0f} q/s, scan {s_ms:.3f} ms = {gbs:.0f} GB/s")
+        # the per-list table scan (one table fl(term2 + qtab) per probed list) beside it
+        ctx.set_ivf_row_sums(False)
+        try:
+            el_t, prof_t, _ = timed(ctx, torch, step, args.steps, 1, ["ivf_qtab", "ivf_scan"])
+            gi_t, gd_t = gpu_out()
+        finally:
+            ctx.set_ivf_row_sums(True)
+        t_ms = prof_t["ivf_scan"][0] / max(1, prof_t["ivf_scan"][1])
+        r["table_scan"] = {
+            "qps": nq * args.steps / el_t, "kernel": "k_ivf_scan_fast", "kernel_ms": t_ms,
+            "achieved": alg_bytes / (t_ms * 1e-3) / 1e9,
+            "term2_bytes_per_launch": nq * nprobe * m * 256 * 4,
+            "same_results": bool(np.array_equal(gi_t, gi) and
+                                 np.array_equal(gd_t.view(np.uint32), gd.view(np.uint32)))}
+        log(f"ivfpq table scan: scan {t_ms:.3f} ms, same {r['table_scan']['same_results']}")
         if not args.no_cpu and ref is not None:
             blob = ix.save()
             s = nq
@@ -644,7 +659,6 @@ def main():
                         "qps": round(nq * args.steps / els, 1),
                         "scan_ms": round(sms, 4),
                         "scan_GBps": round(sc * (m + 4) / (sms * 1e-3) / 1e9, 1),
-                        "term2_GBps": round(nq * npb * m * 1024 / (sms * 1e-3) / 1e9, 1),
                         "codes_scanned_per_query": round(sc / nq, 1)}
                     log(f"ivfpq nprobe {npb} rerank {rr}: {nq * args.steps / els:.0f} q/s")
             r["sweep"] = sweep

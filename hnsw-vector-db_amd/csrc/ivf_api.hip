@@ -13,6 +13,10 @@ namespace vdbg {
 
 int IvfTerm2(Ctx* c, const float* coarse, int nlist, int pd, const float* cen, int m, int dsub,
              float* term2, hipStream_t s);
+int IvfQtabRs(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,
+              float* qtab, float* qmax, hipStream_t s);
+int IvfRowSums(Ctx* c, const uint32_t* off, int nlist, const uint8_t* codes, int m,
+               const float* term2, float* rowsum, float* t2abs, hipStream_t s);
 int IvfQtab(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,
             int twice, float* qtab, hipStream_t s);
 int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s);
@@ -55,6 +59,10 @@ void FreeIvf(IvfIndex* x) {
   (void)hipFree(x->ids);
   (void)hipFree(x->codes);
   (void)hipFree(x->term2);
+  (void)hipFree(x->rowsum);
+  (void)hipFree(x->t2abs);
+  x->rowsum = nullptr;
+  x->t2abs = nullptr;
   x->coarse_ds = nullptr;
   x->cen = nullptr;
   x->term2 = nullptr;
@@ -83,6 +91,12 @@ int InstallIvf(Ctx* c, IvfIndex* x, hipStream_t s) {
     VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&x->term2), nlist * x->m * 256 * sizeof(float)));
     VDBG_RETURN_IF_ERROR(IvfTerm2(c, x->coarse_ds->d.rows, int(nlist), int(pd), x->cen, x->m,
                                   x->dsub, x->term2, s));
+    // the scan's ranking inputs: term-2 sums per row and their per-list bound
+    const size_t n = x->off_h.empty() ? 0 : x->off_h.back();  // CSR entries
+    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&x->rowsum), std::max<size_t>(1, n) * sizeof(float)));
+    VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&x->t2abs), nlist * sizeof(float)));
+    VDBG_RETURN_IF_ERROR(IvfRowSums(c, x->off, int(nlist), x->codes, x->m, x->term2, x->rowsum,
+                                    x->t2abs, s));
   }
   VDBG_HIP(hipStreamSynchronize(s));
   return kOk;
@@ -198,8 +212,13 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
   const bool l2 = x->metric == 0;
   const bool pre = l2 && x->term2 != nullptr;
   const size_t ts = size_t(x->m) * 256;
+  // the row-sum scan (k_ivf_scan_rs) also takes each query's per-subspace table maxima
+  const bool rs = pre && c->ivf_row_sums && x->rowsum != nullptr && R <= 256 &&
+                  (x->m == 4 || x->m == 8 || x->m == 16);
+  const bool want_qtab = pre || !l2;
   void* buf = nullptr;
-  const size_t bytes = nq * nprobe * 8 + (pre || !l2 ? nq * ts * 4 : 0) + nq * R * 8 + 4096;
+  const size_t bytes = nq * nprobe * 8 + (want_qtab ? nq * ts * 4 : 0) + (rs ? nq * x->m * 4 : 0) +
+                       nq * R * 8 + 4096;
   VDBG_HIP(hipMallocAsync(&buf, bytes, s));
   char* p = static_cast<char*>(buf);
   auto take = [&](size_t b) {
@@ -209,16 +228,24 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
   };
   uint32_t* probe = reinterpret_cast<uint32_t*>(take(nq * nprobe * 4));
   float* probe_d = reinterpret_cast<float*>(take(nq * nprobe * 4));
-  float* qtab = (pre || !l2) ? reinterpret_cast<float*>(take(nq * ts * 4)) : nullptr;
+  float* qtab = want_qtab ? reinterpret_cast<float*>(take(nq * ts * 4)) : nullptr;
+  float* qmax = rs ? reinterpret_cast<float*>(take(nq * x->m * 4)) : nullptr;
   uint32_t* ti = R == k ? out_ids : reinterpret_cast<uint32_t*>(take(nq * R * 4));
   float* td = R == k ? out_d : reinterpret_cast<float*>(take(nq * R * 4));
   int rc = RunScan(c, &x->coarse_ds->d.src, Q, nq, nprobe, nullptr, probe, probe_d, s);
-  if (rc == kOk && qtab != nullptr)
+  if (rc == kOk && rs)
+    rc = IvfQtabRs(c, Q, x->pd, int(nq), x->cen, x->m, x->dsub, qtab, qmax, s);
+  else if (rc == kOk && qtab != nullptr)
     rc = IvfQtab(c, Q, x->pd, int(nq), x->cen, x->m, x->dsub, pre ? 1 : 0, qtab, s);
   if (rc == kOk) {
     IvfScanArgs a{Q, x->pd, x->dim, x->m, x->dsub, x->metric, x->coarse_ds->d.rows, x->cen,
                   x->off, x->ids, x->codes, x->term2, qtab, probe, probe_d, int(nprobe),
                   int(nq), allow, int(R), ti, td, dc_dev, uint64_t(x->nlist), depth > 0 ? 1 : 0};
+    if (rs) {
+      a.rowsum = x->rowsum;
+      a.t2abs = x->t2abs;
+      a.qmax = qmax;
+    }
     rc = R <= 256 ? IvfScan(c, a, s) : IvfScanDeep(c, a, s);
   }
   if (rc == kOk && depth > 0) {

@@ -449,6 +449,362 @@ __global__ __launch_bounds__(kIvfWaves * 64, 2) void k_ivf_scan_fast(IvfScanArgs
   }
 }
 
+// ---------------------------------------------------------------- row sums of the term-2 tables
+//
+// The reference scores a code of list l as offset + adc(table) with table[j][c] =
+// fl(term2[l][j][c] + qtab[j][c]) (ivf_pq.cc:203-214).  The term-2 half of that sum depends on
+// the row alone, so it is summed once per row when the index is installed:
+//   rowsum[i] = sum_j term2[l][j][code_j(i)]   (CSR row i of list l, j ascending, fp32)
+//   t2abs[l]  = sum_j max_c |term2[l][j][c]|   (bounds sum_j |term2| of any row of l)
+// k_ivf_scan_rs ranks a row by offset + rowsum[i] + sum_j qtab[j][code_j], which reads only the
+// query's table, and computes the reference's exact score for the rows ranking near the
+// running threshold.
+
+// One block per list, one thread per row.
+__global__ __launch_bounds__(256) void k_ivf_rowsum(const uint32_t* __restrict__ off,
+                                                     const uint8_t* __restrict__ codes, int m,
+                                                     const float* __restrict__ term2,
+                                                     float* __restrict__ rowsum) {
+  const uint32_t l = blockIdx.x;
+  const uint32_t b = off[l], e = off[l + 1];
+  const float* t2 = term2 + size_t(l) * m * kKsub;
+  for (uint32_t i = b + threadIdx.x; i < e; i += blockDim.x) {
+    const uint8_t* cd = codes + size_t(i) * m;
+    float s = 0.f;
+    for (int j = 0; j < m; ++j) s += t2[j * kKsub + cd[j]];
+    rowsum[i] = s;
+  }
+}
+
+// One wave per list.  The fp32 sum of m non-negative maxima is raised by 2^-16 relative, more
+// than its own rounding (m <= 256 additions of relative error 2^-24 each).
+__global__ __launch_bounds__(64) void k_ivf_t2abs(const float* __restrict__ term2, int m,
+                                                  float* __restrict__ t2abs) {
+  const uint32_t l = blockIdx.x;
+  const float* t2 = term2 + size_t(l) * m * kKsub;
+  float tot = 0.f;
+  for (int j = 0; j < m; ++j) {
+    float mx = 0.f;
+    for (int c = lane_id(); c < kKsub; c += kWave) mx = fmaxf(mx, fabsf(t2[j * kKsub + c]));
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    tot += mx;
+  }
+  if (lane_id() == 0) t2abs[l] = tot * (1.f + 0x1p-16f);
+}
+
+constexpr int kRsWaves = 4;
+constexpr int kRsChunk = kWave;  // probed lists whose metadata sits in LDS at a time
+constexpr int kQtabQueries = 32; // queries per block of k_ivf_qtab_rs
+
+// The per-query tables of the row-sum scan: qtab[q][j][c] = 2 * (-DotAny(q_j, C_j[c])), the
+// same operations as k_ivf_qtab (ivf_pq.cc:192-196), and qmax[q][j] = max_c |qtab[q][j][c]|.
+// grid (m, query groups of 32), one thread per centroid c: subspace j's 8 KB of centroids stay
+// in L1 while the block's queries pass.
+__global__ __launch_bounds__(256) void k_ivf_qtab_rs(const float* __restrict__ Q, int pd, int nq,
+                                                     const float* __restrict__ cen, int m, int dsub,
+                                                     float* __restrict__ qtab,
+                                                     float* __restrict__ qmax) {
+  __shared__ float wmax[4][kQtabQueries];
+  const int j = blockIdx.x, c = threadIdx.x, wave = c >> 6, lane = lane_id();
+  const int q0 = blockIdx.y * kQtabQueries;
+  const int nqb = min(kQtabQueries, nq - q0);
+  const float* cc = cen + (size_t(j) * kKsub + c) * dsub;
+  for (int t = 0; t < nqb; ++t) {
+    const int q = q0 + t;
+    const float v = -dot_any(Q + size_t(q) * pd + size_t(j) * dsub, cc, dsub);
+    const float x = v * 2.f;
+    qtab[(size_t(q) * m + j) * kKsub + c] = x;
+    float mx = fabsf(x);
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) wmax[wave][t] = mx;
+  }
+  __syncthreads();
+  if (c < nqb)
+    qmax[size_t(q0 + c) * m + j] =
+        fmaxf(fmaxf(wmax[0][c], wmax[1][c]), fmaxf(wmax[2][c], wmax[3][c]));
+}
+
+// The precomputed-table L2 scan on row sums.  One block (four waves) per query; the query's
+// table 2 * (-<q_j, C_j[c]>) sits in LDS for the whole query.  The rows of a chunk of 64 probed
+// lists (nearest first) are numbered consecutively and dealt to the block's 256 threads CH at a
+// time, so every thread streams contiguous code rows whatever the list sizes; the next CH rows
+// are in flight while these are ranked.
+//
+// Ranking value of row i in probed list s: A = offset_s + (rowsum[i] + sum_j qtab[j][c_j]).
+// The reference's score E = fl(offset_s + adc) with adc summing fl(term2 + qtab) entries in
+// four accumulators (pq.h:36-46) differs from the real value V = offset + sum_j (term2_j +
+// qtab_j) by at most gamma_7 * S, and A by at most gamma_17 * S, where S = |offset| +
+// sum_j |term2_j| + sum_j |qtab_j| <= |offset| + t2abs[l] + Bq (Bq = sum_j max_c |qtab[j][c]|)
+// and gamma_n = n u / (1 - n u), u = 2^-24.  So |A - E| <= gamma_24 * S < 2^-19 * S, and
+// U = A + 2^-17 * S_bound >= E.  A row is skipped only when A > tau + 2^-17 * (S_bound + |tau|)
+// for a tau no smaller than the d of the answer's R-th key: the margin covers |A - E| with
+// room for the rounding of the bound and the comparison itself, so a skipped row has E > tau
+// and cannot be in the answer.  tau is the smallest of
+//   - the seed: the first 256 rows (the nearest lists) give U bounds; each wave sorts its 64
+//     and the largest of the four waves' ceil(R/4)-th bounds has at least R rows at or below;
+//   - every wave's current R-th key (published by LDS atomic min after each flush).
+// Rows not skipped (NaN included) are staged and scored exactly, as the reference scores them,
+// and those below the wave's R-th key enter its top-R; the filter is tested on those alone,
+// which skips nothing the reference would keep.  The four waves' tops merge at the end.
+template <int E, int M, int CH>
+__global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a, IvfFastArgs f) {
+  constexpr int TS = M * kKsub;
+  constexpr int W = (M + 3) / 4;
+  constexpr int NT = kRsWaves * kWave;
+  constexpr int MG = 2 * (kRsWaves - 1) * E * kWave;  // floats of the final merge
+  constexpr float kRel = 0x1p-17f;
+  __shared__ float smem[TS > MG ? TS : MG];  // the query's table, then the merge
+  __shared__ uint32_t p_end[kRsChunk + 1];   // consecutive numbering of the chunk's rows
+  __shared__ uint32_t p_beg[kRsChunk], p_list[kRsChunk];
+  __shared__ float p_off[kRsChunk], p_bnd[kRsChunk];
+  __shared__ float seedv[kRsWaves];
+  __shared__ float tau_blk;
+  __shared__ uint32_t st_row[kRsWaves][2 * kWave];
+  __shared__ uint32_t st_slot[kRsWaves][2 * kWave];
+
+  const int b = blockIdx.x;
+  const int item = (b & 7) * f.per_xcd + (b >> 3);
+  if (item >= f.items) return;  // uniform over the block
+  const uint32_t q = f.qorder ? f.qorder[item] : uint32_t(item);
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  float* qt = smem;
+  {
+    const float4* g = reinterpret_cast<const float4*>(a.qtab + size_t(q) * TS);
+    for (int e = tid; e < TS / 4; e += NT) reinterpret_cast<float4*>(qt)[e] = g[e];
+  }
+  if (tid == 0) tau_blk = __builtin_inff();
+  float bq = 0.f;
+#pragma unroll
+  for (int j = 0; j < M; ++j) bq += a.qmax[size_t(q) * M + j];
+  bq *= 1.f + 0x1p-16f;
+  __syncthreads();
+
+  const int eR = (a.R - 1) / kWave, lR = (a.R - 1) % kWave;  // the R-th key of a top
+  const int r4 = (a.R + kRsWaves - 1) / kRsWaves - 1;         // each wave's share of the seed
+  WaveTopK<E> top;
+  top.init();
+  int staged = 0;
+  uint64_t scanned = 0;
+  float tau0 = __builtin_inff();
+  const uint32_t* probe = a.probe + size_t(q) * a.nprobe;
+  const float* probe_d = a.probe_d + size_t(q) * a.nprobe;
+
+  // Scores the first min(staged, 64) staged rows exactly and inserts them (wave-uniform).
+  auto flush = [&]() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float d = __builtin_inff();
+    uint32_t id = kNoId;
+    if (lane < staged) {
+      // id and code are loaded together, the filter tested last: two round trips
+      const uint32_t i = st_row[wave][lane];
+      const int s = int(st_slot[wave][lane]);
+      const uint32_t rid = a.ids[i];
+      uint32_t w[W];
+      load_code<M>(a.codes, i, w);
+      const float* t2 = a.term2 + size_t(p_list[s]) * TS;
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+      for (int j = 0; j + 4 <= M; j += 4) {
+        const uint32_t x = w[j >> 2];
+        const int e0 = (j + 0) * kKsub + int(x & 0xffu);
+        const int e1 = (j + 1) * kKsub + int((x >> 8) & 0xffu);
+        const int e2 = (j + 2) * kKsub + int((x >> 16) & 0xffu);
+        const int e3 = (j + 3) * kKsub + int(x >> 24);
+        s0 += t2[e0] + qt[e0];
+        s1 += t2[e1] + qt[e1];
+        s2 += t2[e2] + qt[e2];
+        s3 += t2[e3] + qt[e3];
+      }
+      if (row_ok(a.allow, rid)) {
+        d = p_off[s] + ((s0 + s1) + (s2 + s3));
+        id = rid;
+      }
+    }
+    const bool more = lane + kWave < staged;
+    const uint32_t rr = more ? st_row[wave][lane + kWave] : 0u;
+    const uint32_t rs = more ? st_slot[wave][lane + kWave] : 0u;
+    __builtin_amdgcn_wave_barrier();
+    if (more) {
+      st_row[wave][lane] = rr;
+      st_slot[wave][lane] = rs;
+    }
+    staged = staged > kWave ? staged - kWave : 0;
+    // only keys below the R-th key can reach the answer (slots past R are never read)
+    float rd = __builtin_inff();
+    uint32_t ri = kNoId;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (e == eR) {
+        rd = top.k.d[e];
+        ri = top.k.id[e];
+      }
+    rd = __shfl(rd, lR);
+    ri = __shfl(ri, lR);
+    if (!nb_less(d, id, rd, ri)) {
+      d = __builtin_inff();
+      id = kNoId;
+    }
+    top.insert(d, id);
+    rd = __builtin_inff();
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      if (e == eR) rd = top.k.d[e];
+    rd = __shfl(rd, lR);
+    if (lane == 0)
+      __hip_atomic_fetch_min(&tau_blk, rd, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  };
+
+  for (int p0 = 0; p0 < a.nprobe; p0 += kRsChunk) {
+    const int np = min(kRsChunk, a.nprobe - p0);
+    __syncthreads();  // the previous chunk's metadata is no longer read
+    if (wave == 0) {
+      uint32_t n = 0;
+      if (lane < np) {
+        const uint32_t l = probe[p0 + lane];
+        const uint32_t beg = a.off[l];
+        n = a.off[l + 1] - beg;
+        const float off = probe_d[p0 + lane];
+        p_list[lane] = l;
+        p_beg[lane] = beg;
+        p_off[lane] = off;
+        p_bnd[lane] = fabsf(off) + a.t2abs[l] + bq;
+      }
+      uint32_t incl = n;
+#pragma unroll
+      for (int o = 1; o < kWave; o <<= 1) {
+        const uint32_t t = __shfl_up(incl, o);
+        if (lane >= o) incl += t;
+      }
+      p_end[lane + 1] = incl;
+      if (lane == 0) p_end[0] = 0;
+    }
+    __syncthreads();
+    const uint32_t total = p_end[np];
+    scanned += total;
+    int s = 0;  // this thread's probe slot; its rows only move forward
+    struct Rows {
+      uint32_t w[CH][W], row[CH];
+      float rs[CH];
+      int sl[CH];
+      bool ok[CH];
+    };
+    auto fetch = [&](uint32_t v0, Rows& r) {
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        const uint32_t v = v0 + uint32_t(t * NT + tid);
+        r.ok[t] = v < total;
+        r.sl[t] = 0;
+        r.row[t] = 0;
+        r.rs[t] = 0.f;
+        if (r.ok[t]) {
+          while (v >= p_end[s + 1]) ++s;
+          r.sl[t] = s;
+          r.row[t] = p_beg[s] + (v - p_end[s]);
+          load_code<M>(a.codes, r.row[t], r.w[t]);
+          r.rs[t] = a.rowsum[r.row[t]];
+        }
+      }
+    };
+    Rows cur, nxt;
+    if (total > 0) fetch(0, cur);
+    for (uint32_t v0 = 0; v0 < total; v0 += NT * CH) {
+      if (v0 + NT * CH < total) fetch(v0 + NT * CH, nxt);
+      float A[CH];
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        A[t] = __builtin_nanf("");
+        if (cur.ok[t]) {
+          // any summation order: the bound covers it
+          const uint32_t x0 = cur.w[t][0];
+          float q0 = qt[0 * kKsub + int(x0 & 0xffu)];
+          float q1 = qt[1 * kKsub + int((x0 >> 8) & 0xffu)];
+          float q2 = qt[2 * kKsub + int((x0 >> 16) & 0xffu)];
+          float q3 = qt[3 * kKsub + int(x0 >> 24)];
+#pragma unroll
+          for (int j = 4; j + 4 <= M; j += 4) {
+            const uint32_t x = cur.w[t][j >> 2];
+            q0 += qt[(j + 0) * kKsub + int(x & 0xffu)];
+            q1 += qt[(j + 1) * kKsub + int((x >> 8) & 0xffu)];
+            q2 += qt[(j + 2) * kKsub + int((x >> 16) & 0xffu)];
+            q3 += qt[(j + 3) * kKsub + int(x >> 24)];
+          }
+          A[t] = p_off[cur.sl[t]] + (cur.rs[t] + ((q0 + q1) + (q2 + q3)));
+        }
+      }
+      if (p0 == 0 && v0 == 0) {  // the seed, from rows 0..255 (uniform branch)
+        float U = __builtin_inff();
+        if (cur.ok[0] && (a.allow == nullptr || row_ok(a.allow, a.ids[cur.row[0]])))
+          U = A[0] + kRel * p_bnd[cur.sl[0]];
+        if (!(U < __builtin_inff())) U = __builtin_inff();  // NaN bounds nothing
+        WaveKeys<1> kk;
+        kk.d[0] = U;
+        kk.id[0] = uint32_t(lane);
+        bitonic_sort<1>(kk);
+        const float mine = __shfl(kk.d[0], r4);
+        if (lane == 0) seedv[wave] = mine;
+        __syncthreads();
+        tau0 = fmaxf(fmaxf(seedv[0], seedv[1]), fmaxf(seedv[2], seedv[3]));
+      }
+      const float tau = fminf(tau0, __hip_atomic_load(&tau_blk, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_WORKGROUP));
+#pragma unroll
+      for (int t = 0; t < CH; ++t) {
+        const bool cand = cur.ok[t] && !(A[t] > tau + kRel * (p_bnd[cur.sl[t]] + fabsf(tau)));
+        const uint64_t bal = __ballot(cand);
+        if (bal != 0) {
+          const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
+          if (cand) {
+            st_row[wave][pos] = cur.row[t];
+            st_slot[wave][pos] = uint32_t(cur.sl[t]);
+          }
+          staged += __popcll(bal);
+          if (staged >= kWave) flush();
+        }
+      }
+      cur = nxt;
+    }
+    while (staged > 0) flush();  // staged rows name this chunk's slots
+  }
+
+  // merge the four waves' tops into wave 0's
+  __syncthreads();
+  float* mg_d = smem;
+  uint32_t* mg_i = reinterpret_cast<uint32_t*>(smem + (kRsWaves - 1) * E * kWave);
+  if (wave > 0) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      mg_d[((wave - 1) * E + e) * kWave + lane] = top.k.d[e];
+      mg_i[((wave - 1) * E + e) * kWave + lane] = top.k.id[e];
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  for (int v = 0; v < kRsWaves - 1; ++v) {
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      top.insert(mg_d[(v * E + e) * kWave + lane], mg_i[(v * E + e) * kWave + lane]);
+  }
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    const int gi = e * kWave + lane;
+    if (gi < a.R) {
+      a.out_ids[size_t(q) * a.R + gi] = top.k.id[e];
+      a.out_d[size_t(q) * a.R + gi] = top.k.d[e];
+    }
+  }
+  if (a.dc != nullptr) {
+    uint64_t valid = 0;
+#pragma unroll
+    for (int e = 0; e < E; ++e)
+      valid += __popcll(__ballot(top.k.id[e] != kNoId && e * kWave + lane < a.R));
+    if (lane == 0) a.dc[q] = a.dc_base + scanned + (a.count_top ? valid : 0);
+  }
+}
+
 // ProductQuantizer::encode (pq.cc:43-57) of the residual x - coarse[assign] (ivf_pq.cc:
 // 128-139): per subspace the first centroid with the smallest L2SqAny.  One thread per
 // (row, subspace).
@@ -518,6 +874,42 @@ static int launch_fast_m(int e, hipStream_t s, const IvfScanArgs& a, const IvfFa
   return kOk;
 }
 
+template <int M>
+static int launch_rs_m(int e, hipStream_t s, const IvfScanArgs& a, const IvfFastArgs& f) {
+  constexpr int CH = 2;
+  const dim3 g(unsigned(f.per_xcd * 8)), blk(kRsWaves * 64);
+  switch (e) {
+    case 1: k_ivf_scan_rs<1, M, CH><<<g, blk, 0, s>>>(a, f); break;
+    case 2: k_ivf_scan_rs<2, M, CH><<<g, blk, 0, s>>>(a, f); break;
+    case 4: k_ivf_scan_rs<4, M, CH><<<g, blk, 0, s>>>(a, f); break;
+    default: return SetError(kNotSupported, "IVF-PQ: max(rerank, k) > 256 on the GPU path");
+  }
+  return kOk;
+}
+
+// The row-sum scan's per-query tables and their per-subspace maxima (k_ivf_qtab_rs).
+int IvfQtabRs(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,
+              float* qtab, float* qmax, hipStream_t s) {
+  if (nq == 0) return kOk;
+  ProfScope ps(c, "ivf_qtab", s);
+  k_ivf_qtab_rs<<<dim3(unsigned(m), unsigned((nq + kQtabQueries - 1) / kQtabQueries)), kKsub, 0,
+                  s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+// rowsum / t2abs of an index with precomputed tables (k_ivf_rowsum, k_ivf_t2abs).
+int IvfRowSums(Ctx* c, const uint32_t* off, int nlist, const uint8_t* codes, int m,
+               const float* term2, float* rowsum, float* t2abs, hipStream_t s) {
+  if (nlist == 0) return kOk;
+  ProfScope ps(c, "ivf_rowsum", s);
+  k_ivf_rowsum<<<dim3(unsigned(nlist)), 256, 0, s>>>(off, codes, m, term2, rowsum);
+  VDBG_HIP(hipGetLastError());
+  k_ivf_t2abs<<<dim3(unsigned(nlist)), 64, 0, s>>>(term2, m, t2abs);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
 int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
   if (a_in.nq == 0) return kOk;
   IvfScanArgs a = a_in;
@@ -540,8 +932,12 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
     float* sprobe_d = reinterpret_cast<float*>(sprobe + nq * a.nprobe);
     k_first_probe<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, key, val);
     VDBG_HIP(hipGetLastError());
-    IvfScanArgs as = a;  // the scan's view: probes in ascending list id
-    if (a.nprobe > 1 && a.nprobe <= 4 * kWave) {
+    // with row sums: one block per query (k_ivf_scan_rs) walking its lists nearest first, so
+    // the threshold falls early; otherwise one wave per query
+    const bool rs = l2 && a.rowsum != nullptr && a.t2abs != nullptr && a.qmax != nullptr &&
+                    a.qtab != nullptr && a.probe_d != nullptr;
+    IvfScanArgs as = a;  // the per-list table scan's view: probes in ascending list id
+    if (!rs && a.nprobe > 1 && a.nprobe <= 4 * kWave) {
       const dim3 g(unsigned((nq + 3) / 4));
       if (a.nprobe <= kWave)
         k_sort_probes<1><<<g, 256, 0, s>>>(a.probe, a.probe_d, a.nprobe, a.nq, sprobe, sprobe_d);
@@ -565,15 +961,23 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
       VDBG_HIP(hipGetLastError());
     }
     IvfFastArgs f{order, l2 ? nullptr : offs, 0, 0};
-    f.items = (a.nq + kIvfWaves - 1) / kIvfWaves;
+    f.items = rs ? a.nq : (a.nq + kIvfWaves - 1) / kIvfWaves;
     f.per_xcd = (f.items + 7) / 8;
     int rc = kOk;
     {
       ProfScope ps(c, "ivf_scan", s);
-      switch (a.m) {
-        case 4: rc = launch_fast_m<4>(e, s, as, f); break;
-        case 8: rc = launch_fast_m<8>(e, s, as, f); break;
-        default: rc = launch_fast_m<16>(e, s, as, f); break;
+      if (rs) {
+        switch (a.m) {
+          case 4: rc = launch_rs_m<4>(e, s, as, f); break;
+          case 8: rc = launch_rs_m<8>(e, s, as, f); break;
+          default: rc = launch_rs_m<16>(e, s, as, f); break;
+        }
+      } else {
+        switch (a.m) {
+          case 4: rc = launch_fast_m<4>(e, s, as, f); break;
+          case 8: rc = launch_fast_m<8>(e, s, as, f); break;
+          default: rc = launch_fast_m<16>(e, s, as, f); break;
+        }
       }
       if (rc == kOk && hipGetLastError() != hipSuccess) rc = SetError(kInternal, "ivf scan launch");
     }

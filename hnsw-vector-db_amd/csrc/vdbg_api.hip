@@ -459,6 +459,13 @@ int vdbg_ctx_set_int8_gemm(vdbg_ctx* ctx, int enable) {
   return kOk;
 }
 
+int vdbg_ctx_set_ivf_row_sums(vdbg_ctx* ctx, int enable) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.ivf_row_sums = enable != 0;
+  return kOk;
+}
+
 int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work) {
   if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
   if (!(work >= 0.0)) return SetError(kInvalidArgument, "work must be >= 0");

@@ -130,6 +130,7 @@ struct Ctx {
   bool fp16_single = true;     // new float datasets hold their fp16 h halves alone
                                // (x16_approx, gemm16.hip SPLIT 3) instead of h + l pairs
   bool int8_gemm = true;       // integer flat rows may rank on the int8 GEMM (gemm8.hip)
+  bool ivf_row_sums = true;    // IVF-PQ L2 scans rank on per-row term-2 sums (k_ivf_scan_rs)
   double int8_float_min_work = 2e10;  // float rows: smallest N nq pd for the int8 GEMM
   int host_threads = 0;        // host threads of the HNSW walk; 0 = DefaultHostThreads()
   vdbg_ctx* handle = nullptr;  // the C-ABI handle that owns this context
@@ -248,6 +249,8 @@ struct IvfIndex {
   uint32_t* ids = nullptr;           // n
   uint8_t* codes = nullptr;          // n x m
   float* term2 = nullptr;            // nlist x m x 256, or null
+  float* rowsum = nullptr;           // n: sum_j term2[l][j][code_j] per CSR row (with term2)
+  float* t2abs = nullptr;            // nlist: sum_j max_c |term2[l][j][c]| (with term2)
   std::vector<float> coarse_h, cen_h;
   std::vector<uint32_t> off_h;
 };
@@ -274,6 +277,9 @@ struct IvfScanArgs {
   uint64_t dc_base;        // nlist: the coarse distances
   int count_top;           // add the candidates handed to Rerank
   int ondemand;            // the table does not fit LDS (m > 32): entries computed per lookup
+  const float* rowsum;     // per CSR row term-2 sums (nullable: the per-list table scan)
+  const float* t2abs;      // per list bound of sum_j |term2| (with rowsum)
+  const float* qmax;       // [nq][m] max_c |qtab[q][j][c]| (with rowsum)
 };
 
 // PqFlatIndex (src/index/quant/ivf_pq.h:12-36) made resident: the PQ codebook and every

@@ -59,6 +59,7 @@ _SIGS = {
     "vdbg_ctx_kernels": (C.c_char_p, [_vp]),
     "vdbg_ctx_set_fp16_gemm": (C.c_int, [_vp, C.c_int]),
     "vdbg_ctx_set_int8_gemm": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_ivf_row_sums": (C.c_int, [_vp, C.c_int]),
     "vdbg_ctx_set_int8_float_min_work": (C.c_int, [_vp, C.c_double]),
     "vdbg_ctx_set_test_fallbacks": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
@@ -212,6 +213,12 @@ class Context:
         """Let integer flat rows spanning at most 256 values rank on int8 MFMA (the
         default).  Results are identical."""
         _check(lib.vdbg_ctx_set_int8_gemm(self.h, 1 if enable else 0))
+
+    def set_ivf_row_sums(self, enable=True):
+        """Let IVF-PQ L2 scans with precomputed tables rank rows on their per-row term-2
+        sums (the default); False builds each probed list's table per query.  Results are
+        identical."""
+        _check(lib.vdbg_ctx_set_ivf_row_sums(self.h, 1 if enable else 0))
 
     def set_int8_float_min_work(self, work):
         """Smallest rows x queries x padded_dim of a float-row batch that ranks on the int8

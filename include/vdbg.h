@@ -116,6 +116,13 @@ int vdbg_ctx_set_fp16_single(vdbg_ctx* ctx, int enable);
  * and flag readback the int8 GEMM would not repay).  Results are identical either way.  No
  * counterpart in the reference. */
 int vdbg_ctx_set_int8_float_min_work(vdbg_ctx* ctx, double work);
+/* How IVF-PQ L2 indexes with precomputed tables (ivf_pq.cc:152-167) are scanned (default 1):
+ * on, each row is ranked by its term-2 sum, kept per row (4 bytes per row, made when the index
+ * is loaded or built), plus the query's table, and the rows near the running threshold are
+ * scored exactly as the reference scores them; off, each probed list's table
+ * fl(term2 + qtab) is built per query and every code scored on it.  Results are identical
+ * either way.  No counterpart in the reference. */
+int vdbg_ctx_set_ivf_row_sums(vdbg_ctx* ctx, int enable);
 
 /* Host threads for the CPU side of a search (the HNSW walk); n <= 0 restores the default:
  * the cores this process may run on, capped by OMP_NUM_THREADS when set. */
