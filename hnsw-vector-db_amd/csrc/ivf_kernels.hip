@@ -539,9 +539,10 @@ __global__ __launch_bounds__(256) void k_ivf_qtab_rs(const float* __restrict__ Q
 // sum_j |term2_j| + sum_j |qtab_j| <= |offset| + t2abs[l] + Bq (Bq = sum_j max_c |qtab[j][c]|)
 // and gamma_n = n u / (1 - n u), u = 2^-24.  So |A - E| <= gamma_24 * S < 2^-19 * S, and
 // U = A + 2^-17 * S_bound >= E.  A row is skipped only when A > tau + 2^-17 * (S_bound + |tau|)
-// for a tau no smaller than the d of the answer's R-th key: the margin covers |A - E| with
-// room for the rounding of the bound and the comparison itself, so a skipped row has E > tau
-// and cannot be in the answer.  tau is the smallest of
+// for a tau no smaller than the d of the answer's R-th key, tested as rowsum + table sum >
+// fl(tau + 2^-17 |tau|) + fl(2^-17 S_bound - offset): the margin (128 u of S + |tau|) covers
+// |A - E| (24 u of S) with room for the few roundings of these terms (each at most u of
+// |tau| + 2 S), so a skipped row has E > tau and cannot be in the answer.  tau is the smallest of
 //   - the seed: the first 256 rows (the nearest lists) give U bounds; each wave sorts its 64
 //     and the largest of the four waves' ceil(R/4)-th bounds has at least R rows at or below;
 //   - every wave's current R-th key (published by LDS atomic min after each flush).
@@ -558,7 +559,7 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
   __shared__ float smem[TS > MG ? TS : MG];  // the query's table, then the merge
   __shared__ uint32_t p_end[kRsChunk + 1];   // consecutive numbering of the chunk's rows
   __shared__ uint32_t p_beg[kRsChunk], p_list[kRsChunk];
-  __shared__ float p_off[kRsChunk], p_bnd[kRsChunk];
+  __shared__ float p_off[kRsChunk], p_bnd[kRsChunk], p_c[kRsChunk];
   __shared__ float seedv[kRsWaves];
   __shared__ float tau_blk;
   __shared__ uint32_t st_row[kRsWaves][2 * kWave];
@@ -672,6 +673,7 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
         p_beg[lane] = beg;
         p_off[lane] = off;
         p_bnd[lane] = fabsf(off) + a.t2abs[l] + bq;
+        p_c[lane] = kRel * p_bnd[lane] - off;
       }
       uint32_t incl = n;
 #pragma unroll
@@ -713,10 +715,10 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
     if (total > 0) fetch(0, cur);
     for (uint32_t v0 = 0; v0 < total; v0 += NT * CH) {
       if (v0 + NT * CH < total) fetch(v0 + NT * CH, nxt);
-      float A[CH];
+      float rq[CH];  // rowsum + table sum: the ranking value less the list's offset
 #pragma unroll
       for (int t = 0; t < CH; ++t) {
-        A[t] = __builtin_nanf("");
+        rq[t] = __builtin_nanf("");
         if (cur.ok[t]) {
           // any summation order: the bound covers it
           const uint32_t x0 = cur.w[t][0];
@@ -732,13 +734,13 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
             q2 += qt[(j + 2) * kKsub + int((x >> 16) & 0xffu)];
             q3 += qt[(j + 3) * kKsub + int(x >> 24)];
           }
-          A[t] = p_off[cur.sl[t]] + (cur.rs[t] + ((q0 + q1) + (q2 + q3)));
+          rq[t] = cur.rs[t] + ((q0 + q1) + (q2 + q3));
         }
       }
       if (p0 == 0 && v0 == 0) {  // the seed, from rows 0..255 (uniform branch)
         float U = __builtin_inff();
         if (cur.ok[0] && (a.allow == nullptr || row_ok(a.allow, a.ids[cur.row[0]])))
-          U = A[0] + kRel * p_bnd[cur.sl[0]];
+          U = (p_off[cur.sl[0]] + rq[0]) + kRel * p_bnd[cur.sl[0]];
         if (!(U < __builtin_inff())) U = __builtin_inff();  // NaN bounds nothing
         WaveKeys<1> kk;
         kk.d[0] = U;
@@ -751,9 +753,11 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
       }
       const float tau = fminf(tau0, __hip_atomic_load(&tau_blk, __ATOMIC_RELAXED,
                                                       __HIP_MEMORY_SCOPE_WORKGROUP));
+      const float T0 = tau + kRel * fabsf(tau);
 #pragma unroll
       for (int t = 0; t < CH; ++t) {
-        const bool cand = cur.ok[t] && !(A[t] > tau + kRel * (p_bnd[cur.sl[t]] + fabsf(tau)));
+        // A > tau + 2^-17 (S_bound + |tau|) rearranged: rq > T0 + (2^-17 S_bound - offset)
+        const bool cand = cur.ok[t] && !(rq[t] > T0 + p_c[cur.sl[t]]);
         const uint64_t bal = __ballot(cand);
         if (bal != 0) {
           const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
