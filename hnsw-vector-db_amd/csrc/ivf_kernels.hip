@@ -543,8 +543,9 @@ __global__ __launch_bounds__(256) void k_ivf_qtab_rs(const float* __restrict__ Q
 // fl(tau + 2^-17 |tau|) + fl(2^-17 S_bound - offset): the margin (128 u of S + |tau|) covers
 // |A - E| (24 u of S) with room for the few roundings of these terms (each at most u of
 // |tau| + 2 S), so a skipped row has E > tau and cannot be in the answer.  tau is the smallest of
-//   - the seed: the first 256 rows (the nearest lists) give U bounds; each wave sorts its 64
-//     and the largest of the four waves' ceil(R/4)-th bounds has at least R rows at or below;
+//   - the seed: the first 256 CH rows (the nearest lists) give U bounds; each wave sorts its
+//     64 CH and the largest of the four waves' ceil(R/4)-th bounds has at least R rows at or
+//     below;
 //   - every wave's current R-th key (published by LDS atomic min after each flush).
 // Rows not skipped (NaN included) are staged and scored exactly, as the reference scores them,
 // and those below the wave's R-th key enter its top-R; the filter is tested on those alone,
@@ -737,15 +738,18 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
           rq[t] = cur.rs[t] + ((q0 + q1) + (q2 + q3));
         }
       }
-      if (p0 == 0 && v0 == 0) {  // the seed, from rows 0..255 (uniform branch)
-        float U = __builtin_inff();
-        if (cur.ok[0] && (a.allow == nullptr || row_ok(a.allow, a.ids[cur.row[0]])))
-          U = (p_off[cur.sl[0]] + rq[0]) + kRel * p_bnd[cur.sl[0]];
-        if (!(U < __builtin_inff())) U = __builtin_inff();  // NaN bounds nothing
-        WaveKeys<1> kk;
-        kk.d[0] = U;
-        kk.id[0] = uint32_t(lane);
-        bitonic_sort<1>(kk);
+      if (p0 == 0 && v0 == 0) {  // the seed, from the first NT * CH rows (uniform branch)
+        WaveKeys<CH> kk;
+#pragma unroll
+        for (int t = 0; t < CH; ++t) {
+          float U = __builtin_inff();
+          if (cur.ok[t] && (a.allow == nullptr || row_ok(a.allow, a.ids[cur.row[t]])))
+            U = (p_off[cur.sl[t]] + rq[t]) + kRel * p_bnd[cur.sl[t]];
+          if (!(U < __builtin_inff())) U = __builtin_inff();  // NaN bounds nothing
+          kk.d[t] = U;
+          kk.id[t] = uint32_t(t * kWave + lane);
+        }
+        bitonic_sort<CH>(kk);
         const float mine = __shfl(kk.d[0], r4);
         if (lane == 0) seedv[wave] = mine;
         __syncthreads();
@@ -1179,3 +1183,4 @@ int PqEncode(Ctx* c, const float* X, uint32_t n, int pd, int dim, const float* c
 }
 
 }  // namespace vdbg
+
