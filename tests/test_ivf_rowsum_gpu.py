@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import vdbg
-from ivf_file import synth_ivfpq
+from ivf_file import parse_ivfpq, synth_ivfpq, write_ivfpq
 from vdbg import datagen
 from test_ivfpq_gpu import _eq, _oracle_ivf
 
@@ -100,3 +100,33 @@ def test_rowsum_scan_other_code_sizes(ctx, oracle, m):
         od, oi, odc = _oracle_ivf(oracle, blob, base, qs, k, nprobe, rerank)
         _eq(gi, gd, oi, od)
         assert np.array_equal(dc, odc)
+
+
+def test_rowsum_scan_empty_lists_and_fewer_rows_than_r(ctx, oracle):
+    # 1,500 rows over 256 lists, each list's centroid repeated by an empty twin: every chunk
+    # of 64 probed lists holds empty lists at the same coarse distance as full ones, and the
+    # probed rows can number fewer than R (the seed then bounds nothing and answers are padded)
+    print("ivf rowsum empty lists", flush=True)
+    base = datagen.sift_like(1500, 128, 3141)
+    qs = datagen.sift_like(40, 128, 3142)
+    ix0 = parse_ivfpq(synth_ivfpq(base, 128, 256, 16, seed=9))
+    off = ix0["list_off"].astype(np.int64)
+    coarse, ids, codes = [], [], []
+    for l in range(ix0["nlist"]):
+        for twin in range(2):
+            coarse.append(ix0["coarse"][l])
+            if twin == 0:
+                ids.append(ix0["list_ids"][off[l]:off[l + 1]])
+                codes.append(ix0["list_codes"][off[l] * 16:off[l + 1] * 16])
+            else:
+                ids.append(np.zeros(0, np.uint32))
+                codes.append(np.zeros(0, np.uint8))
+    blob = write_ivfpq(1500, 128, np.array(coarse), 128, 16, ix0["pq_centroids"], ids, codes)
+    ds = vdbg.Dataset(ctx, base, 128)
+    ix = vdbg.IvfPqIndex.load(ds, blob)
+    for nprobe, rerank, k in [(1, 0, 10), (8, 100, 10), (40, 0, 200), (200, -1, 10), (512, 0, 64)]:
+        (gi, gd, dc), (ti, td, tdc) = _both(ctx, ix, qs, k, nprobe, rerank)
+        od, oi, odc = _oracle_ivf(oracle, blob, base, qs, k, nprobe, rerank)
+        _eq(gi, gd, oi, od)
+        assert np.array_equal(dc, odc)
+        _eq(ti, td, oi, od)
