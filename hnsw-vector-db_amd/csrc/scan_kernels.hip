@@ -1902,6 +1902,7 @@ int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t k
 constexpr int kTinyQ = 2;       // queries
 constexpr int kTinyK = 48;      // k (kp = k + 16 <= 64 keys per chunk)
 constexpr int kTinyMaxPd = 256; // |key| < 2^23 stays exact in fp32
+constexpr int kTinyWaves = 4;   // waves per scan block
 
 struct TinyArgs {
   const float* Q;
@@ -1921,12 +1922,12 @@ struct TinyArgs {
 // coalesced 16-byte loads (consecutive lanes, consecutive bytes), then each lane reads its
 // own row from the tile (row stride padded by 16 bytes against bank conflicts).
 template <int NQ, int VPR>
-__global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
+__global__ __launch_bounds__(kTinyWaves * 64) void k_tiny_scan(TinyArgs a) {
   __shared__ int s_q8[NQ][kTinyMaxPd / 4];
-  __shared__ float sd[4][NQ][2 * kWave];
-  __shared__ uint32_t si[4][NQ][2 * kWave];
-  __shared__ float md[3][NQ][kWave];
-  __shared__ uint32_t mi[3][NQ][kWave];
+  __shared__ float sd[kTinyWaves][NQ][2 * kWave];
+  __shared__ uint32_t si[kTinyWaves][NQ][2 * kWave];
+  __shared__ float md[kTinyWaves - 1][NQ][kWave];
+  __shared__ uint32_t mi[kTinyWaves - 1][NQ][kWave];
   extern __shared__ int4 tile_all[];  // [4][64][pd / 16 + 1]
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
   constexpr int vpr = VPR;             // 16-byte vectors per row (pd / 16)
@@ -1937,7 +1938,7 @@ __global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
   }
   if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
   const int pw = a.pd / 4;
-  for (int e = tid; e < NQ * pw; e += 256) {
+  for (int e = tid; e < NQ * pw; e += kTinyWaves * 64) {
     const int q = e / pw, w = e - q * pw;
     uint32_t packed = 0;
     if (q < a.nq) {
@@ -1974,7 +1975,7 @@ __global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
   };
   int4 vn[VPR];
   load_step(r0 + wave * kWave, vn);
-  for (uint32_t base = r0 + wave * kWave; base < r1; base += 4 * kWave) {
+  for (uint32_t base = r0 + wave * kWave; base < r1; base += kTinyWaves * kWave) {
     const uint32_t r = base + lane;
     const bool live = r < r1 && row_allowed(a.allow, r);
     {
@@ -1982,7 +1983,7 @@ __global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
       int4 v[VPR];
 #pragma unroll
       for (int t = 0; t < VPR; ++t) v[t] = vn[t];
-      load_step(base + 4 * kWave, vn);
+      load_step(base + kTinyWaves * kWave, vn);
 #pragma unroll
       for (int t = 0; t < VPR; ++t) {
         const int e = t * kWave + lane;
@@ -2071,7 +2072,7 @@ __global__ __launch_bounds__(256) void k_tiny_scan(TinyArgs a) {
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     if (q >= a.nq) break;
-    for (int w = 0; w < 3; ++w) top[q].insert(md[w][q][lane], mi[w][q][lane]);
+    for (int w = 0; w < kTinyWaves - 1; ++w) top[q].insert(md[w][q][lane], mi[w][q][lane]);
     const size_t o = size_t(q) * a.nchunks + blockIdx.x;  // (the grid has one more block)
     if (lane < a.kp) a.part[o * a.kp + lane] = make_uint2(__float_as_uint(top[q].k.d[0]), top[q].k.id[0]);
     const float kth = __shfl(top[q].k.d[0], rl);
@@ -2295,11 +2296,12 @@ static bool TinyEligible(const Ctx* c, const ScanSource& src, size_t nq, size_t 
 
 template <int NQ>
 static void launch_tiny(hipStream_t s, int blocks, const TinyArgs& a) {
-  const size_t tile = size_t(4) * kWave * (a.pd / 16 + 1) * sizeof(int4);
+  const size_t tile = size_t(kTinyWaves) * kWave * (a.pd / 16 + 1) * sizeof(int4);
+  const int threads = kTinyWaves * 64;
   switch (a.pd) {
-    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks + 1), 256, tile, s>>>(a); break;
-    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks + 1), 256, tile, s>>>(a); break;
-    default: k_tiny_scan<NQ, 16><<<dim3(blocks + 1), 256, tile, s>>>(a); break;
+    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks + 1), threads, tile, s>>>(a); break;
+    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks + 1), threads, tile, s>>>(a); break;
+    default: k_tiny_scan<NQ, 16><<<dim3(blocks + 1), threads, tile, s>>>(a); break;
   }
 }
 
