@@ -615,7 +615,7 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
         const int e0 = (j + 0) * kKsub + int(x & 0xffu);
         const int e1 = (j + 1) * kKsub + int((x >> 8) & 0xffu);
         const int e2 = (j + 2) * kKsub + int((x >> 16) & 0xffu);
-        const int e3 = (j + 3) * kKsub + int(x >> 24);
+        const int e3 = (j + 3) * kKsub + int((x >> 24) & 0xffu);
         s0 += t2[e0] + qt[e0];
         s1 += t2[e1] + qt[e1];
         s2 += t2[e2] + qt[e2];
@@ -726,14 +726,14 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
           float q0 = qt[0 * kKsub + int(x0 & 0xffu)];
           float q1 = qt[1 * kKsub + int((x0 >> 8) & 0xffu)];
           float q2 = qt[2 * kKsub + int((x0 >> 16) & 0xffu)];
-          float q3 = qt[3 * kKsub + int(x0 >> 24)];
+          float q3 = qt[3 * kKsub + int((x0 >> 24) & 0xffu)];
 #pragma unroll
           for (int j = 4; j + 4 <= M; j += 4) {
             const uint32_t x = cur.w[t][j >> 2];
             q0 += qt[(j + 0) * kKsub + int(x & 0xffu)];
             q1 += qt[(j + 1) * kKsub + int((x >> 8) & 0xffu)];
             q2 += qt[(j + 2) * kKsub + int((x >> 16) & 0xffu)];
-            q3 += qt[(j + 3) * kKsub + int(x >> 24)];
+            q3 += qt[(j + 3) * kKsub + int((x >> 24) & 0xffu)];
           }
           rq[t] = cur.rs[t] + ((q0 + q1) + (q2 + q3));
         }
