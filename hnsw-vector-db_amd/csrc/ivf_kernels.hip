@@ -499,25 +499,49 @@ constexpr int kQtabQueries = 32; // queries per block of k_ivf_qtab_rs
 
 // The per-query tables of the row-sum scan: qtab[q][j][c] = 2 * (-DotAny(q_j, C_j[c])), the
 // same operations as k_ivf_qtab (ivf_pq.cc:192-196), and qmax[q][j] = max_c |qtab[q][j][c]|.
-// grid (m, query groups of 32), one thread per centroid c: subspace j's 8 KB of centroids stay
-// in L1 while the block's queries pass.
+// grid (m, query groups of 32), one thread per centroid c: with DS = dsub known at compile
+// time the centroid stays in registers and each query's sub-vector is read once per block
+// (a uniform address); DS = 0 takes dsub at run time.
+template <int DS>
 __global__ __launch_bounds__(256) void k_ivf_qtab_rs(const float* __restrict__ Q, int pd, int nq,
-                                                     const float* __restrict__ cen, int m, int dsub,
-                                                     float* __restrict__ qtab,
+                                                     const float* __restrict__ cen, int m,
+                                                     int dsub_rt, float* __restrict__ qtab,
                                                      float* __restrict__ qmax) {
   __shared__ float wmax[4][kQtabQueries];
+  const int dsub = DS > 0 ? DS : dsub_rt;
   const int j = blockIdx.x, c = threadIdx.x, wave = c >> 6, lane = lane_id();
   const int q0 = blockIdx.y * kQtabQueries;
   const int nqb = min(kQtabQueries, nq - q0);
   const float* cc = cen + (size_t(j) * kKsub + c) * dsub;
+  float cr[DS > 0 ? DS : 1];
+  if constexpr (DS > 0) {
+#pragma unroll
+    for (int i = 0; i < DS; ++i) cr[i] = cc[i];
+  }
   for (int t = 0; t < nqb; ++t) {
     const int q = q0 + t;
-    const float v = -dot_any(Q + size_t(q) * pd + size_t(j) * dsub, cc, dsub);
+    const float* qv = Q + size_t(q) * pd + size_t(j) * dsub;
+    float v;
+    if constexpr (DS > 0) {
+      // DotAny (scalar.cc:43-73): four accumulators over i mod 4, (s0 + s1) + (s2 + s3)
+      static_assert(DS % 4 == 0, "whole groups of four");
+      float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+#pragma unroll
+      for (int i = 0; i < DS; i += 4) {
+        s0 += qv[i] * cr[i];
+        s1 += qv[i + 1] * cr[i + 1];
+        s2 += qv[i + 2] * cr[i + 2];
+        s3 += qv[i + 3] * cr[i + 3];
+      }
+      v = -((s0 + s1) + (s2 + s3));
+    } else {
+      v = -dot_any(qv, cc, dsub);
+    }
     const float x = v * 2.f;
     qtab[(size_t(q) * m + j) * kKsub + c] = x;
     float mx = fabsf(x);
 #pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, lane_xor(mx, o));
     if (lane == 0) wmax[wave][t] = mx;
   }
   __syncthreads();
@@ -900,8 +924,14 @@ int IvfQtabRs(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, i
               float* qtab, float* qmax, hipStream_t s) {
   if (nq == 0) return kOk;
   ProfScope ps(c, "ivf_qtab", s);
-  k_ivf_qtab_rs<<<dim3(unsigned(m), unsigned((nq + kQtabQueries - 1) / kQtabQueries)), kKsub, 0,
-                  s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax);
+  const dim3 g(unsigned(m), unsigned((nq + kQtabQueries - 1) / kQtabQueries));
+  switch (dsub) {
+    case 4: k_ivf_qtab_rs<4><<<g, kKsub, 0, s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax); break;
+    case 8: k_ivf_qtab_rs<8><<<g, kKsub, 0, s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax); break;
+    case 16: k_ivf_qtab_rs<16><<<g, kKsub, 0, s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax); break;
+    case 32: k_ivf_qtab_rs<32><<<g, kKsub, 0, s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax); break;
+    default: k_ivf_qtab_rs<0><<<g, kKsub, 0, s>>>(Q, pd, nq, cen, m, dsub, qtab, qmax); break;
+  }
   VDBG_HIP(hipGetLastError());
   return kOk;
 }
