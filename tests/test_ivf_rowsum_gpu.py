@@ -87,13 +87,15 @@ def test_rowsum_scan_with_filter(ctx, oracle, frac):
         _eq(ti, td, oi, od)
 
 
-@pytest.mark.parametrize("m", [4, 8])
-def test_rowsum_scan_other_code_sizes(ctx, oracle, m):
-    print(f"ivf rowsum m={m}", flush=True)
-    base = datagen.sift_like(20000, 64, 3131)
-    qs = datagen.sift_like(50, 64, 3132)
-    blob = synth_ivfpq(base, 64, 128, m, seed=8)
-    ds = vdbg.Dataset(ctx, base, 64)
+@pytest.mark.parametrize("dim,m", [(64, 4), (64, 8), (128, 4), (96, 8), (48, 16)])
+def test_rowsum_scan_other_code_sizes(ctx, oracle, dim, m):
+    # sub-vectors of 16, 8 and 32 dims take the table kernel's compiled widths, 12 and 3 its
+    # run-time width
+    print(f"ivf rowsum dim={dim} m={m}", flush=True)
+    base = datagen.sift_like(20000, dim, 3131)
+    qs = datagen.sift_like(50, dim, 3132)
+    blob = synth_ivfpq(base, dim, 128, m, seed=8)
+    ds = vdbg.Dataset(ctx, base, dim)
     ix = vdbg.IvfPqIndex.load(ds, blob)
     for nprobe, rerank, k in [(16, 0, 10), (70, -1, 10), (24, 0, 130)]:
         gi, gd, dc = ix.search(qs, k, nprobe, rerank)
