@@ -241,6 +241,7 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
     IvfScanArgs a{Q, x->pd, x->dim, x->m, x->dsub, x->metric, x->coarse_ds->d.rows, x->cen,
                   x->off, x->ids, x->codes, x->term2, qtab, probe, probe_d, int(nprobe),
                   int(nq), allow, int(R), ti, td, dc_dev, uint64_t(x->nlist), depth > 0 ? 1 : 0};
+    a.nlist = uint32_t(x->nlist);
     if (rs) {
       a.rowsum = x->rowsum;
       a.t2abs = x->t2abs;

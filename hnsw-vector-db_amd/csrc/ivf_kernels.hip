@@ -100,7 +100,11 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
     for (int e = lane; e < ts; e += kWave) table[e] = qt[e];
   }
   for (int pi = 0; pi < a.nprobe; ++pi) {
-    const uint32_t l = a.probe[size_t(q) * a.nprobe + pi];
+    // a probe at or past nlist (a query whose coarse distances are all NaN leaves no-id
+    // slots) scans as an empty list
+    uint32_t l = a.probe[size_t(q) * a.nprobe + pi];
+    const bool lv = l < a.nlist;
+    if (!lv) l = 0;
     const float* cl = a.coarse + size_t(l) * a.pd;
     float offset = 0.f;
     __builtin_amdgcn_wave_barrier();
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    const uint32_t b = a.off[l], e_ = a.off[l + 1];
+    const uint32_t b = lv ? a.off[l] : 0u, e_ = lv ? a.off[l + 1] : 0u;
     scanned += e_ - b;
     for (uint32_t i0 = b; i0 < e_; i0 += kWave) {
       const uint32_t i = i0 + lane;
@@ -216,11 +220,12 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_scan(IvfScanArgs a) {
 // dims (ivf_pq.cc:209).  One thread per (query, probe).
 __global__ void k_ivf_offsets(const float* __restrict__ Q, int pd, int dim,
                               const float* __restrict__ coarse, const uint32_t* __restrict__ probe,
-                              int nprobe, int nq, float* __restrict__ offs) {
+                              int nprobe, int nq, uint32_t nlist, float* __restrict__ offs) {
   const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
   if (t >= size_t(nq) * nprobe) return;
   const size_t q = t / nprobe;
-  offs[t] = -dot_any(Q + q * pd, coarse + size_t(probe[t]) * pd, dim);
+  const uint32_t l = probe[t];  // past nlist: an empty list (the scans skip it)
+  offs[t] = l < nlist ? -dot_any(Q + q * pd, coarse + size_t(l) * pd, dim) : 0.f;
 }
 
 __global__ void k_first_probe(const uint32_t* __restrict__ probe, int nprobe, int nq,
@@ -323,7 +328,8 @@ __global__ __launch_bounds__(kIvfWaves * 64, 2) void k_ivf_scan_fast(IvfScanArgs
     for (int i = 0; i < V; ++i) QT[i] = qt4[i * kWave + lane];
   }
   if (pre) {
-    const float4* t4 = reinterpret_cast<const float4*>(a.term2 + size_t(probe[0]) * TS);
+    const uint32_t l0 = probe[0] < a.nlist ? probe[0] : 0u;  // (a no-id probe scans nothing)
+    const float4* t4 = reinterpret_cast<const float4*>(a.term2 + size_t(l0) * TS);
 #pragma unroll
     for (int i = 0; i < V; ++i) T2[i] = t4[i * kWave + lane];
   } else {
@@ -369,6 +375,7 @@ __global__ __launch_bounds__(kIvfWaves * 64, 2) void k_ivf_scan_fast(IvfScanArgs
 
   for (int pi = 0; pi < a.nprobe; ++pi) {
     const uint32_t l = probe[pi];
+    const bool lv = l < a.nlist;  // past nlist: an empty list
     const float offset = pre ? a.probe_d[size_t(q) * a.nprobe + pi] : f.offs[size_t(q) * a.nprobe + pi];
     if (pre) {
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -378,7 +385,8 @@ __global__ __launch_bounds__(kIvfWaves * 64, 2) void k_ivf_scan_fast(IvfScanArgs
         table4[i * kWave + lane] = make_float4(T2[i].x + QT[i].x, T2[i].y + QT[i].y,
                                                T2[i].z + QT[i].z, T2[i].w + QT[i].w);
       if (pi + 1 < a.nprobe) {
-        const float4* t4 = reinterpret_cast<const float4*>(a.term2 + size_t(probe[pi + 1]) * TS);
+        const uint32_t ln = probe[pi + 1] < a.nlist ? probe[pi + 1] : 0u;
+        const float4* t4 = reinterpret_cast<const float4*>(a.term2 + size_t(ln) * TS);
 #pragma unroll
         for (int i = 0; i < V; ++i) T2[i] = t4[i * kWave + lane];
       }
@@ -387,7 +395,7 @@ __global__ __launch_bounds__(kIvfWaves * 64, 2) void k_ivf_scan_fast(IvfScanArgs
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    const uint32_t b0 = a.off[l], e0 = a.off[l + 1];
+    const uint32_t b0 = lv ? a.off[l] : 0u, e0 = lv ? a.off[l + 1] : 0u;
     scanned += e0 - b0;
     for (uint32_t c0 = b0; c0 < e0; c0 += CH * kWave) {
       uint32_t w[CH][W];
@@ -690,9 +698,11 @@ __global__ __launch_bounds__(kRsWaves * 64, 6) void k_ivf_scan_rs(IvfScanArgs a,
     if (wave == 0) {
       uint32_t n = 0;
       if (lane < np) {
-        const uint32_t l = probe[p0 + lane];
-        const uint32_t beg = a.off[l];
-        n = a.off[l + 1] - beg;
+        const uint32_t lp = probe[p0 + lane];
+        const bool lv = lp < a.nlist;  // past nlist: an empty list
+        const uint32_t l = lv ? lp : 0u;
+        const uint32_t beg = lv ? a.off[l] : 0u;
+        n = lv ? a.off[l + 1] - beg : 0u;
         const float off = probe_d[p0 + lane];
         p_list[lane] = l;
         p_beg[lane] = beg;
@@ -987,15 +997,19 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
       as.probe = sprobe;
       as.probe_d = a.probe_d != nullptr ? sprobe_d : nullptr;
     }
+    // the keys are list ids below nlist (dc_base): only their low bits take sort passes
+    int end_bit = 1;
+    while (end_bit < 32 && (uint64_t(1) << end_bit) < a.dc_base) ++end_bit;
     size_t tmp_bytes = 0;
     VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, key2, val, order, a.nq, 0,
-                                                32, s));
+                                                end_bit, s));
     void* tmp = nullptr;
     VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
-    VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, key2, val, order, a.nq, 0, 32, s));
+    VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, key2, val, order, a.nq, 0,
+                                                end_bit, s));
     if (!l2) {
       k_ivf_offsets<<<dim3(unsigned((nq * a.nprobe + 255) / 256)), 256, 0, s>>>(
-          a.Q, a.pd, a.dim, a.coarse, as.probe, a.nprobe, a.nq, offs);
+          a.Q, a.pd, a.dim, a.coarse, as.probe, a.nprobe, a.nq, a.nlist, offs);
       VDBG_HIP(hipGetLastError());
     }
     IvfFastArgs f{order, l2 ? nullptr : offs, 0, 0};
@@ -1039,13 +1053,14 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
 
 // Candidates per query: the sizes of its probed lists (every code is scored once).
 __global__ void k_probe_counts(const uint32_t* __restrict__ probe, int nprobe, int nq,
-                               const uint32_t* __restrict__ off, uint64_t* __restrict__ cnt) {
+                               uint32_t nlist, const uint32_t* __restrict__ off,
+                               uint64_t* __restrict__ cnt) {
   const int q = blockIdx.x * blockDim.x + threadIdx.x;
   if (q >= nq) return;
   uint64_t n = 0;
   for (int i = 0; i < nprobe; ++i) {
     const uint32_t l = probe[size_t(q) * nprobe + i];
-    n += off[l + 1] - off[l];
+    if (l < nlist) n += off[l + 1] - off[l];
   }
   cnt[q] = n;
 }
@@ -1071,7 +1086,11 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_score_all(IvfScanArgs a,
     for (int e = lane; e < ts; e += kWave) table[e] = qt[e];
   int pos = seg[qi];
   for (int pi = 0; pi < a.nprobe; ++pi) {
-    const uint32_t l = a.probe[size_t(q) * a.nprobe + pi];
+    // a probe at or past nlist (a query whose coarse distances are all NaN leaves no-id
+    // slots) scans as an empty list
+    uint32_t l = a.probe[size_t(q) * a.nprobe + pi];
+    const bool lv = l < a.nlist;
+    if (!lv) l = 0;
     const float* cl = a.coarse + size_t(l) * a.pd;
     float offset = 0.f;
     __builtin_amdgcn_wave_barrier();
@@ -1093,7 +1112,7 @@ __global__ __launch_bounds__(kIvfWaves * 64) void k_ivf_score_all(IvfScanArgs a,
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const uint32_t b = a.off[l], e_ = a.off[l + 1];
+    const uint32_t b = lv ? a.off[l] : 0u, e_ = lv ? a.off[l + 1] : 0u;
     for (uint32_t i0 = b; i0 < e_; i0 += kWave) {
       const uint32_t i = i0 + lane;
       if (i < e_) {
@@ -1142,7 +1161,8 @@ int IvfScanDeep(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
   const size_t nq = size_t(a.nq);
   uint64_t* cnt = nullptr;
   VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&cnt), nq * 8, s));
-  k_probe_counts<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, a.off, cnt);
+  k_probe_counts<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, a.nlist,
+                                                                  a.off, cnt);
   VDBG_HIP(hipGetLastError());
   std::vector<uint64_t> h(nq);
   VDBG_HIP(hipMemcpyAsync(h.data(), cnt, nq * 8, hipMemcpyDeviceToHost, s));

@@ -280,6 +280,7 @@ struct IvfScanArgs {
   const float* rowsum;     // per CSR row term-2 sums (nullable: the per-list table scan)
   const float* t2abs;      // per list bound of sum_j |term2| (with rowsum)
   const float* qmax;       // [nq][m] max_c |qtab[q][j][c]| (with rowsum)
+  uint32_t nlist;          // probes at or past it (no-id slots) scan as empty lists
 };
 
 // PqFlatIndex (src/index/quant/ivf_pq.h:12-36) made resident: the PQ codebook and every

@@ -132,3 +132,23 @@ def test_rowsum_scan_empty_lists_and_fewer_rows_than_r(ctx, oracle):
         _eq(gi, gd, oi, od)
         assert np.array_equal(dc, odc)
         _eq(ti, td, oi, od)
+
+
+@pytest.mark.parametrize("rerank,k", [(0, 10), (-1, 10), (0, 300)])
+def test_query_with_nan_leaves_the_batch_intact(ctx, oracle, rerank, k):
+    # a query whose coarse distances are all NaN can leave no-id probe slots: every scan
+    # (row sums, per-list tables, the deep top-R past 256) takes them as empty lists, and the
+    # batch's finite queries are answered as the oracle answers them
+    print(f"ivf nan query rerank={rerank} k={k}", flush=True)
+    base = datagen.sift_like(20000, 128, 3151)
+    qs = datagen.sift_like(30, 128, 3152)
+    qs[7, :] = np.nan
+    finite = np.arange(30) != 7
+    blob = synth_ivfpq(base, 128, 128, 16, seed=11)
+    ds = vdbg.Dataset(ctx, base, 128)
+    ix = vdbg.IvfPqIndex.load(ds, blob)
+    od, oi, odc = _oracle_ivf(oracle, blob, base, np.ascontiguousarray(qs[finite]), k, 16, rerank)
+    (gi, gd, dc), (ti, td, tdc) = _both(ctx, ix, qs, k, 16, rerank)
+    _eq(gi[finite], gd[finite], oi, od)
+    assert np.array_equal(dc[finite], odc)
+    _eq(ti[finite], td[finite], oi, od)
