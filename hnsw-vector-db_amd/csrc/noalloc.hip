@@ -1,6 +1,8 @@
 // noalloc.hip -- the allocation-free flat search: vdbg_flat_search_device's pipeline with all
 // of its scratch in a static device array, for callers that cannot allocate device memory
-// (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+// (tight serving loops, harnesses that forbid hipMalloc).  It is not capturable into a HIP
+// graph: like vdbg_flat_search_device it reads the count of uncertified queries back on the
+// host before it queues their exact re-scan.
 #include <mutex>
 #include <string>
 

@@ -479,6 +479,7 @@ int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
                                              src->Sinit8, src->Srn, src->Sid);
   VDBG_HIP(hipGetLastError());
   src->Smax = smax;
+  src->SN = src->N;
   return kOk;
 }
 
@@ -509,6 +510,7 @@ void FreeSample(ScanSource* src) {
   src->Srn = nullptr;
   src->Sid = nullptr;
   src->Smax = 0;
+  src->SN = 0;
 }
 
 // ================================================================ query preparation
@@ -2434,7 +2436,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // fp32 main pass on the device (no host round trip before the main pass).
   const bool gated = nq <= 128 && split == 0 && try8 && !try8op;
   S = std::min(S, src->Smax);
-  const int rank = ThresholdRank(kk, S, N);
+  // the sample's positions spread over its first SN rows (an appendable dataset's sample
+  // may trail its rows): a top row there is sampled with probability S / SN, one past
+  // them never, so the tail bound takes f = S / SN
+  const int rank = ThresholdRank(kk, S, std::min(N, src->SN != 0 ? src->SN : N));
   const int ngroups = int((S + 31) / 32) * 2;
   struct Plan {
     int qb, nqt, nchunks, caph, nseg, schunks;

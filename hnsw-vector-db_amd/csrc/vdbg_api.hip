@@ -109,6 +109,12 @@ WsUse::~WsUse() {
   if (w_->done != nullptr) (void)hipEventRecord(w_->done, s_);
 }
 
+// External ids of appended rows given none: each row's own row number.
+__global__ void k_iota64(uint64_t* __restrict__ p, uint64_t first, size_t n) {
+  const size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = first + i;
+}
+
 __global__ void k_fill32(uint32_t* __restrict__ p, uint32_t v, size_t n) {
   const size_t i = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
   if (i < n) p[i] = v;
@@ -621,20 +627,23 @@ int vdbg_dataset_create_appendable(vdbg_ctx* ctx, size_t dim, size_t pd, int met
 }
 
 // MutableSegment::Append (mutable_segment.cc:24-44) for n rows at once: the rows (n x pd,
-// host), their external ids (host, nullable: left unset), published together when the call
-// returns.  *first_row (nullable) receives the row number of the first.
+// host), their external ids (host; null gives each new row its row number), published
+// together when the call returns.  *first_row (nullable) receives the row number of the first.
+// Only growth past the reserved capacity waits for the whole device (old buffers are freed
+// once no search can read them); otherwise the call waits only for its own copies and the
+// statistics of the new rows on the context's stream.
 int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uint64_t* ext_ids,
                         uint64_t* first_row) {
   if (ds == nullptr || (n > 0 && rows == nullptr)) return SetError(kInvalidArgument, "null argument");
   Dataset& d = ds->d;
+  Ctx* c = d.ctx;
+  std::lock_guard<std::recursive_mutex> g(c->mu);
   if (!d.appendable)
     return SetError(kFailedPrecondition, "rows are appended only to a dataset made by "
                                          "vdbg_dataset_create_appendable");
   if (d.live_indexes > 0)
     return SetError(kFailedPrecondition, "an appendable dataset with an index takes no rows");
   if (d.n + n > 0xfffffffeull) return SetError(kResourceExhausted, "mutable segment is full");
-  Ctx* c = d.ctx;
-  std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
   hipStream_t s = c->stream;
   if (first_row != nullptr) *first_row = d.n;
@@ -664,6 +673,8 @@ int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uin
     (void)hipFree(d.rows);
     (void)hipFree(d.norms);
     (void)hipFree(d.ext_ids);
+    for (void* p : d.retired) (void)hipFree(p);
+    d.retired.clear();
     d.rows = nr;
     d.norms = nn;
     d.ext_ids = ne;
@@ -671,9 +682,13 @@ int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uin
   }
   float* at = d.rows + d.n * d.pd;
   VDBG_HIP(hipMemcpyAsync(at, rows, n * d.pd * sizeof(float), hipMemcpyHostToDevice, s));
-  if (ext_ids != nullptr)
+  if (ext_ids != nullptr) {
     VDBG_HIP(hipMemcpyAsync(d.ext_ids + d.n, ext_ids, n * 8, hipMemcpyHostToDevice, s));
-  RowStats st;
+  } else {
+    k_iota64<<<dim3(unsigned((n + 255) / 256)), 256, 0, s>>>(d.ext_ids + d.n, d.n, n);
+    VDBG_HIP(hipGetLastError());
+  }
+  RowStats st;  // (reads the statistics back: the copies above have completed on return)
   VDBG_RETURN_IF_ERROR(LaunchRowStats(c, s, at, n, d.pd, d.norms + d.n, &st));
   if (d.n == 0) {
     d.stats = st;
@@ -690,12 +705,22 @@ int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uin
   d.src.N = uint32_t(d.n);
   d.src.stats = d.stats;
   d.src.rmag = d.stats.xn_max;
-  // the threshold sample follows the rows (any rows of the set give a valid threshold; a
-  // fresh one keeps it tight)
-  if (d.src.Sbuf != nullptr) VDBG_HIP(hipDeviceSynchronize());  // searches may read it
-  FreeSample(&d.src);
-  if (d.n >= 1024 && GemmSupported(d.pd)) VDBG_RETURN_IF_ERROR(BuildSample(c, &d.src, s));
-  VDBG_HIP(hipStreamSynchronize(s));
+  // The threshold sample: any rows of the set give a valid threshold, and RunScan sizes its
+  // rank by the rows the sample spans, so a sample that trails the rows stays correct; it is
+  // gathered anew once the rows have doubled since (or reached 1024), which keeps the
+  // refreshes logarithmic in the appends.  The replaced sample is kept until the device is
+  // next idle, since searches queued earlier on any stream may still read it.
+  if (d.n >= 1024 && GemmSupported(d.pd) &&
+      (d.src.Smax == 0 || d.n >= 2 * size_t(d.src.SN))) {
+    if (d.src.Sbuf != nullptr) {
+      d.retired.push_back(d.src.Sbuf);
+      d.src.Sbuf = nullptr;  // FreeSample then only forgets it
+    }
+    FreeSample(&d.src);
+    VDBG_RETURN_IF_ERROR(BuildSample(c, &d.src, s));
+    // searches on other streams read the new sample only after its gather has completed
+    VDBG_HIP(hipStreamSynchronize(s));
+  }
   return kOk;
 }
 
@@ -716,6 +741,7 @@ int vdbg_dataset_destroy(vdbg_dataset* ds) {
   (void)hipDeviceSynchronize();
   --c->live_datasets;
   FreeSample(&ds->d.src);
+  for (void* p : ds->d.retired) (void)hipFree(p);
   (void)hipFree(ds->d.rows);
   (void)hipFree(ds->d.norms);
   if (ds->d.rows16 != nullptr) (void)hipFree(ds->d.rows16);

@@ -180,6 +180,8 @@ struct ScanSource {
   float* Srn = nullptr;
   uint32_t* Sid = nullptr;
   uint32_t Smax = 0;
+  uint32_t SN = 0;              // rows the sample's positions spread over (N when gathered;
+                                // an appendable dataset's sample may trail its rows)
   void* Sbuf = nullptr;         // the sample's allocation when the source owns it
 };
 
@@ -204,6 +206,8 @@ struct Dataset {
   // for cap rows and grow in place; no fp16 / int8 copies are kept
   bool appendable = false;
   size_t cap = 0;
+  std::vector<void*> retired;  // replaced samples, freed once the device is idle (growth,
+                               // destroy): searches queued earlier may still read them
 };
 
 // SQ8 codes of a dataset's rows (HnswSq8Index's codes_ and Sq8Quantizer,

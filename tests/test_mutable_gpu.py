@@ -42,7 +42,10 @@ def test_append_then_search(ctx, oracle, kind):
     ds = vdbg.Dataset.appendable(ctx, dim, metric, capacity=1000)
     ext = np.arange(total, dtype=np.uint64) * 3 + 7
     at = 0
-    for step, chunk in enumerate((1, 700, 1, 1500, 2798)):  # grows past the capacity twice
+    # grows past the capacity three times; the threshold sample is gathered at 2,202 rows and
+    # again at 5,000 (the rows doubled), so the search at 3,202 rows reads a sample that
+    # trails the rows
+    for step, chunk in enumerate((1, 700, 1, 1500, 1000, 1798)):
         first = ds.append(rows[at:at + chunk], ext[at:at + chunk])
         assert first == at
         at += chunk
@@ -111,6 +114,37 @@ def test_memory_parts_in_a_collection(ctx, oracle):
     finally:
         for ds in handles:
             ds.close()
+
+
+def test_memory_part_appended_without_ids(ctx, oracle):
+    """Rows appended without external ids take their row numbers as external ids: an
+    in-memory part built that way merges with a disk segment as if its ids were 0..n-1."""
+    dim = 32
+    pd = vdbg.padded_dim(dim)
+    mem = datagen.pad(datagen.uniform_rows(1500, dim, 1010) * 4, pd)
+    disk = datagen.pad(datagen.uniform_rows(4000, dim, 1011) * 4, pd)
+    ap = vdbg.Dataset.appendable(ctx, dim, "l2", capacity=256)
+    for a in range(0, 1500, 500):
+        ap.append(mem[a:a + 500])  # no external ids
+    ds = vdbg.Dataset(ctx, disk, dim)
+    dext = np.arange(4000, dtype=np.uint64) + 1000  # ids 1000..1499 also name memory rows
+    ds.set_external_ids(dext)
+    segs = [{"base": mem, "ext": np.arange(1500, dtype=np.uint64), "kind": "memory",
+             "deleted": None, "filter": None},
+            {"base": disk, "ext": dext, "kind": "flat", "deleted": None, "filter": None}]
+    q = np.ascontiguousarray(disk[np.random.default_rng(1012).integers(0, 4000, 20)] + np.float32(0.02))
+    try:
+        for k in (1, 10, 40):
+            gi, gd, gdc, gp = vdbg.collection_search(
+                ctx, [(ap, None, None, None, True), (ds, None, None, None, False)], dim, "l2",
+                q, k, vdbg.SearchParams())
+            oi, od, odc, op = oracle.collection_search(segs, dim, "l2", q, k, strategy=0)
+            assert gp == op
+            assert np.array_equal(gi, oi), k
+            assert np.array_equal(gd.view(np.uint32), od.view(np.uint32)), k
+    finally:
+        ds.close()
+        ap.close()
 
 
 def test_append_errors(ctx):
