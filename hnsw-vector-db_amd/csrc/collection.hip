@@ -6,7 +6,9 @@
 // stays on the device: PrepareQuery once for all queries, one device search per segment into
 // a [segment][query][k] hit array (the planner's choice is per segment: it depends only on
 // the segment's filter and deletes, not on the query), one merge kernel that reads each
-// segment's resident external ids, one copy back.
+// segment's resident external ids, one copy back.  A segment whose index this library does
+// not hold (vdb's float-row HNSW) is searched by the caller on the host; its hits take the
+// segment's place in the merge.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -85,6 +87,29 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
   Ctx* c = &ctx->c;
   for (size_t p = 0; p < nseg; ++p) {
     const vdbg_segment& g = segs[p];
+    if (g.host_rows != nullptr) {  // searched on the host: its lists are checked below
+      if (g.memory_part)
+        return SetError(kInvalidArgument, "an in-memory part is searched here, not on the host");
+      if (nq > 0 && (g.host_dists == nullptr || g.host_ext == nullptr))
+        return SetError(kInvalidArgument, "host-searched segment without distances or ids");
+      for (size_t i = 0; i < nq; ++i) {
+        const float* d = g.host_dists + i * k;
+        const uint32_t* r = g.host_rows + i * k;
+        size_t j = 0;
+        for (; j < k && r[j] != kNoId; ++j) {
+          if (std::isnan(d[j]))
+            return SetError(kInvalidArgument, "host-searched segment: NaN distance");
+          if (j > 0 && (d[j] < d[j - 1] || (d[j] == d[j - 1] && r[j] <= r[j - 1])))
+            return SetError(kInvalidArgument, "host-searched segment: hits not in ascending "
+                                              "(dist, row) order");
+        }
+        for (; j < k; ++j)
+          if (r[j] != kNoId)
+            return SetError(kInvalidArgument, "host-searched segment: a hit after the end of "
+                                              "its list");
+      }
+      continue;
+    }
     if (g.rows == nullptr) return SetError(kInvalidArgument, "segment without rows");
     const Dataset& d = g.rows->d;
     if (d.ctx != c) return SetError(kInvalidArgument, "segment on another context");
@@ -111,6 +136,10 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
   size_t allow_words_total = 0;
   for (size_t p = 0; p < nseg; ++p) {
     const vdbg_segment& g = segs[p];
+    if (g.host_rows != nullptr) {
+      plan[p].plan = VDBG_PLAN_HOST;
+      continue;
+    }
     const size_t rows = g.rows->d.n, nw = (rows + 63) / 64;
     const size_t deleted = g.deleted_words ? CountRows(g.deleted_words, rows) : 0;
     const size_t live = rows - std::min(rows, deleted);
@@ -258,6 +287,10 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
 
   std::vector<uint32_t> hr, xr;
   std::vector<float> hd, xd;
+  // host-searched segments: each hit's external id, resident for the merge, which reads it
+  // as row q * k + i of the segment
+  std::vector<DevBuf> host_ext(nseg);
+  std::vector<std::vector<uint32_t>> host_pos(nseg);  // (kept until the copies complete)
   for (size_t p = 0; p < nseg; ++p) {
     SegPlan& sp = plan[p];
     uint32_t* ids = static_cast<uint32_t*>(hits_r.p) + p * slice;
@@ -273,6 +306,19 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
       case VDBG_PLAN_INDEX:
         VDBG_RETURN_IF_ERROR(index_search(p, k, sp.nprobe, allow, ids, dd, P.ef));
         break;
+      case VDBG_PLAN_HOST: {
+        const vdbg_segment& g = segs[p];
+        std::vector<uint32_t>& pos = host_pos[p];
+        pos.resize(slice);
+        for (size_t i = 0; i < slice; ++i) pos[i] = g.host_rows[i] == kNoId ? kNoId : uint32_t(i);
+        VDBG_RETURN_IF_ERROR(Alloc(&host_ext[p], slice * 8, s));
+        VDBG_HIP(hipMemcpyAsync(ids, pos.data(), slice * 4, hipMemcpyHostToDevice, s));
+        VDBG_HIP(hipMemcpyAsync(dd, g.host_dists, slice * 4, hipMemcpyHostToDevice, s));
+        VDBG_HIP(hipMemcpyAsync(host_ext[p].p, g.host_ext, slice * 8, hipMemcpyHostToDevice, s));
+        if (dist_comps != nullptr && g.host_dist_comps != nullptr)
+          for (size_t i = 0; i < nq; ++i) dist_comps[i] += g.host_dist_comps[i];
+        break;
+      }
       case VDBG_PLAN_EMPTY:
         VDBG_HIP(hipMemsetAsync(ids, 0xff, slice * 4, s));
         VDBG_HIP(hipMemsetAsync(dd, 0, slice * 4, s));
@@ -367,7 +413,9 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
 
   // ---- the merge (collection_impl.cc:1076-1112) and the copy back
   std::vector<const uint64_t*> ext(np, nullptr);
-  for (size_t p = 0; p < nseg; ++p) ext[p] = segs[p].rows->d.ext_ids;
+  for (size_t p = 0; p < nseg; ++p)
+    ext[p] = plan[p].plan == VDBG_PLAN_HOST ? static_cast<const uint64_t*>(host_ext[p].p)
+                                            : segs[p].rows->d.ext_ids;
   VDBG_RETURN_IF_ERROR(Alloc(&extp, np * sizeof(void*), s));
   VDBG_RETURN_IF_ERROR(Alloc(&oe, slice * 8, s));
   VDBG_RETURN_IF_ERROR(Alloc(&od, slice * 4, s));

@@ -651,20 +651,38 @@ class SearchParams(C.Structure):
 
 STRATEGIES = {"auto": 0, "prefilter": 1, "graph": 2, "post_filter": 3}
 PLANS = ["index", "empty", "prefilter_exact", "filtered_index",
-         "filtered_index+exact_fallback", "post_filter", "scan", "scan_filter"]
+         "filtered_index+exact_fallback", "post_filter", "scan", "scan_filter", "host"]
 
 
 class _Segment(C.Structure):
     _fields_ = [("rows", _vp), ("sq8", _vp), ("ivfpq", _vp), ("deleted_words", _vp),
-                ("filter_words", _vp), ("pqflat", _vp), ("memory_part", C.c_int)]
+                ("filter_words", _vp), ("pqflat", _vp), ("memory_part", C.c_int),
+                ("host_dists", _vp), ("host_rows", _vp), ("host_ext", _vp),
+                ("host_dist_comps", _vp)]
+
+
+class HostHits:
+    """The hits of a disk segment searched on the host (vdb's own SearchDiskSegment over an
+    index this library does not hold, such as a float-row HNSW): per query [nq, k] distances
+    and rows in ascending (dist, row) order (rows 0xFFFFFFFF after the last hit), each hit's
+    external id, and optionally the distance computations per query."""
+
+    def __init__(self, dists, rows, ext, dist_comps=None):
+        self.dists = np.ascontiguousarray(dists, np.float32)
+        self.rows = np.ascontiguousarray(rows, np.uint32)
+        self.ext = np.ascontiguousarray(ext, np.uint64)
+        self.dist_comps = None if dist_comps is None else np.ascontiguousarray(dist_comps, np.uint64)
+        assert self.dists.shape == self.rows.shape == self.ext.shape
 
 
 def collection_search(ctx, segments, dim, metric, queries, k, params=None):
     """CollectionImpl::SearchBatch over disk segments (vdbg_collection_search_host).
     segments: (dataset, index or None, deleted words or None, filter words or None[,
     memory part]) per segment, each dataset with its external ids set; a true fifth entry
-    marks an in-memory part (the active or a frozen mutable segment), which vdb lists first.  Returns (external ids uint64 [nq, k],
-    dists float32 [nq, k], distance computations per query, plan name per segment)."""
+    marks an in-memory part (the active or a frozen mutable segment), which vdb lists first;
+    a HostHits in place of the tuple is a disk segment searched on the host.  Returns
+    (external ids uint64 [nq, k], dists float32 [nq, k], distance computations per query,
+    plan name per segment)."""
     params = params or SearchParams()
     q = np.ascontiguousarray(queries, np.float32)
     nq = q.shape[0]
@@ -672,6 +690,13 @@ def collection_search(ctx, segments, dim, metric, queries, k, params=None):
     keep = []
     arr = (_Segment * max(len(segments), 1))()
     for i, seg in enumerate(segments):
+        if isinstance(seg, HostHits):
+            assert seg.dists.shape == (nq, k), "host hits are [nq, k]"
+            keep.append(seg)
+            arr[i] = _Segment(None, None, None, None, None, None, 0, seg.dists.ctypes.data,
+                              seg.rows.ctypes.data, seg.ext.ctypes.data,
+                              None if seg.dist_comps is None else seg.dist_comps.ctypes.data)
+            continue
         ds, ix, deleted, filt = seg[:4]
         memory = bool(seg[4]) if len(seg) > 4 else False
         sq = ix.h if isinstance(ix, Sq8Index) else None
@@ -681,7 +706,8 @@ def collection_search(ctx, segments, dim, metric, queries, k, params=None):
         fw = None if filt is None else np.ascontiguousarray(filt, np.uint64)
         keep += [dw, fw]
         arr[i] = _Segment(ds.h, sq, iv, None if dw is None else dw.ctypes.data,
-                          None if fw is None else fw.ctypes.data, pf, 1 if memory else 0)
+                          None if fw is None else fw.ctypes.data, pf, 1 if memory else 0,
+                          None, None, None, None)
     ids = np.empty((nq, k), np.uint64)
     d = np.empty((nq, k), np.float32)
     dc = np.empty(nq, np.uint64)

@@ -214,8 +214,9 @@ int vdbg_flat_search_device(vdbg_dataset* ds, const float* queries, size_t nq, s
                             void* stream);
 
 /* vdbg_flat_search_device without any device allocation, for callers that cannot allocate
- * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
- * counterpart in the reference.  Same arguments, results and stream semantics as
+ * (tight serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.
+ * It cannot be captured into a HIP graph: it reads the count of uncertified queries back on
+ * the host (as vdbg_flat_search_device does) before it queues their exact re-scan.  Same arguments, results and stream semantics as
  * vdbg_flat_search_device, with these limits:
  *  - k <= 240 (InvalidArgument otherwise);
  *  - the scratch is one static device array of 32 MiB per GPU (24 MiB for the scan
@@ -412,10 +413,12 @@ int vdbg_last_gemm_bits(vdbg_ctx* ctx);
 int vdbg_dataset_create_appendable(vdbg_ctx* ctx, size_t dim, size_t padded_dim, int metric,
                                    size_t capacity, vdbg_dataset** out);
 /* MutableSegment::Append (mutable_segment.cc:24-44) of n rows (n x padded_dim floats, host)
- * and their external ids (host, nullable), published together when the call returns (later
- * searches see them; rows never move for readers of earlier calls).  *first_row (nullable)
- * receives the first new row's number.  FailedPrecondition for a dataset not made appendable
- * or one with an index. */
+ * and their external ids (host, nullable: NULL gives each new row its row number as external
+ * id), published together when the call returns (later searches see them; rows never move
+ * for readers of earlier calls).  *first_row (nullable) receives the first new row's number.
+ * The call waits for its own copies on the context's stream; only growth past the reserved
+ * capacity (capacity doubles) waits for the whole device.  FailedPrecondition for a dataset
+ * not made appendable or one with an index. */
 int vdbg_dataset_append(vdbg_dataset* ds, const float* rows, size_t n, const uint64_t* ext_ids,
                         uint64_t* first_row);
 /* The dataset's row count. */
@@ -477,6 +480,15 @@ typedef struct vdbg_segment {
                                      the filter is scored exactly, no planner, no index.
                                      In-memory parts come first in the array, as in vdb's
                                      snapshot order (active, frozen, then disk). */
+  /* A disk segment searched on the host: vdb's own SearchDiskSegment (planner.cc:42-129)
+   * over an index this library does not hold, such as HnswIndex over a VDBHNSW1 file
+   * (vdb's default IndexType::Hnsw, options.h:22).  When host_rows is set, rows and the
+   * index pointers are ignored (rows may be NULL) and the segment's hits join the merge in
+   * its place of the array: */
+  const float* host_dists;        /* host [nq][k]: each query's hits, ascending (dist, row) */
+  const uint32_t* host_rows;      /* host [nq][k]: their rows; UINT32_MAX after the last hit */
+  const uint64_t* host_ext;       /* host [nq][k]: their external ids (Segment::external_id) */
+  const uint64_t* host_dist_comps;/* host [nq], nullable: SegmentExplain distance_computations */
 } vdbg_segment;
 
 /* FilterStrategy (include/vdb/options.h:57). */
@@ -508,7 +520,8 @@ enum {
   VDBG_PLAN_FILTERED_INDEX_EXACT_FALLBACK = 4,
   VDBG_PLAN_POST_FILTER = 5,
   VDBG_PLAN_SCAN = 6,        /* an in-memory part without a filter (SearchMutable "scan") */
-  VDBG_PLAN_SCAN_FILTER = 7  /* an in-memory part under a filter ("scan_filter") */
+  VDBG_PLAN_SCAN_FILTER = 7, /* an in-memory part under a filter ("scan_filter") */
+  VDBG_PLAN_HOST = 8         /* a disk segment whose hits the caller searched on the host */
 };
 
 /* Makes the segment's external ids (ids.u64, n entries, host) resident for the collection
@@ -526,7 +539,10 @@ int vdbg_dataset_set_external_ids(vdbg_dataset* ds, const uint64_t* ids);
  * (UINT64_MAX padded) and distances (+inf padded; the score is the distance for L2 and its
  * negation otherwise).  dist_comps (nullable, nq) receives each query's distance
  * computations; seg_plans (nullable, nseg) each segment's VDBG_PLAN_*.  k must be in
- * 1..10000 (:1038-1039).  Host pointers; blocks until the results are on the host. */
+ * 1..10000 (:1038-1039).  A segment with host_rows set is taken as searched: its hits (which
+ * must be in ascending (dist, row) order per query, InvalidArgument otherwise) merge in its
+ * place with the others, and its plan reads VDBG_PLAN_HOST.  Host pointers; blocks until the
+ * results are on the host. */
 int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
                                 size_t dim, int metric, const float* queries, size_t nq,
                                 size_t k, const vdbg_search_params* params, uint64_t* out_ids,

@@ -662,7 +662,8 @@ inline std::string JoinPath(const std::string& a, const std::string& b) {
 // the host and resident for the merge), the index file (LoadIndex by magic, index.cc:38-87:
 // VDBFLAT1 needs nothing more, VDBHSQ81 brings its SQ8 codes and its graph, walked on the
 // host with the rerank on the GPU, VDBIVFP1 its lists, VDBPQFL1 its codebook and codes; a
-// float-row HNSW index is NotSupported) and the persisted delete set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
+// float-row HNSW index is NotSupported: vdb keeps such a segment on its CPU path and hands
+// its hits to SearchCollection as a host part) and the persisted delete set.  meta.bin is not read: filters arrive already evaluated, as dense words.  Errors are
 // the reference's Corruption messages, prefixed with the file or directory.
 class GpuSegment {
  public:
@@ -800,24 +801,57 @@ class GpuSegment {
   size_t deleted_count_ = 0;
 };
 
+// The hits of a disk segment searched on the host: vdb's own SearchDiskSegment
+// (planner.cc:42-129) over an index this library does not hold, such as HnswIndex over a
+// VDBHNSW1 file (vdb's default IndexType::Hnsw, options.h:22; GpuSegment::Open is
+// NotSupported for it).  [nq][k] each: per query ascending (dist, row), kNoRow after the last
+// hit, and each hit's external id.
+struct HostSegmentHits {
+  std::vector<float> dists;
+  std::vector<InternalId> rows;
+  std::vector<VectorId> ids;
+  std::vector<uint64_t> dist_comps;  // [nq] SegmentExplain::distance_computations, or empty
+};
+
+// One disk segment of a snapshot: on the device, or searched on the host.
+struct DiskPart {
+  const GpuSegment* gpu = nullptr;
+  const HostSegmentHits* host = nullptr;
+};
+
 // CollectionImpl::SearchBatch (collection_impl.cc:1121-1135) over a snapshot's disk segments,
 // as one device batch (vdbg_collection_search_host): PrepareQuery, SearchDiskSegment's plan
-// per segment (planner.cc:42-129), the merge with one hit per external id.  filters: null
-// for a request without a filter, else one filter per segment (the request's filter
-// evaluated on that segment; deletes are removed here).  plans (optional) receives each
-// segment's SegmentExplain::strategy.
-inline Status SearchCollection(Device& dev, std::span<const GpuSegment* const> segs, size_t dim,
+// per segment (planner.cc:42-129), the merge with one hit per external id.  parts are in the
+// snapshot's order; a host part's hits merge in its place.  filters: null for a request
+// without a filter, else one filter per part (the request's filter evaluated on that
+// segment; deletes are removed here; a host part's entry is not read).  plans (optional)
+// receives each part's SegmentExplain::strategy ("host" for a host part).
+inline Status SearchCollection(Device& dev, std::span<const DiskPart> parts, size_t dim,
                                Metric metric, const float* raw_queries, size_t nq, size_t k,
                                const SearchParams& p,
                                const std::vector<const DenseRowFilter*>* filters,
                                std::vector<std::vector<SearchHit>>& out,
                                std::vector<uint64_t>* dist_comps = nullptr,
                                std::vector<std::string>* plans = nullptr) {
-  if (filters != nullptr && filters->size() != segs.size())
+  if (filters != nullptr && filters->size() != parts.size())
     return Status(VDBG_INVALID_ARGUMENT, "one filter per segment");
-  std::vector<vdbg_segment> v(segs.size());
-  for (size_t i = 0; i < segs.size(); ++i) {
-    const GpuSegment& g = *segs[i];
+  std::vector<vdbg_segment> v(parts.size());
+  for (size_t i = 0; i < parts.size(); ++i) {
+    if (const HostSegmentHits* h = parts[i].host) {
+      if (h->dists.size() != nq * k || h->rows.size() != nq * k || h->ids.size() != nq * k ||
+          (!h->dist_comps.empty() && h->dist_comps.size() != nq))
+        return Status(VDBG_INVALID_ARGUMENT, "host segment hits are [nq][k]");
+      v[i].host_dists = h->dists.data();
+      v[i].host_rows = h->rows.data();
+      v[i].host_ext = h->ids.data();
+      v[i].host_dist_comps = h->dist_comps.empty() ? nullptr : h->dist_comps.data();
+      // (a null pointer would read as "not searched on the host")
+      static const InternalId kNone = kNoRow;
+      if (nq * k == 0) v[i].host_rows = &kNone;
+      continue;
+    }
+    if (parts[i].gpu == nullptr) return Status(VDBG_INVALID_ARGUMENT, "empty disk part");
+    const GpuSegment& g = *parts[i].gpu;
     v[i].rows = g.dataset();
     v[i].sq8 = g.sq8();
     v[i].ivfpq = g.ivfpq();
@@ -829,7 +863,7 @@ inline Status SearchCollection(Device& dev, std::span<const GpuSegment* const> s
                               p.post_filter_alpha};
   std::vector<uint64_t> ids(nq * k), dc(nq);
   std::vector<float> d(nq * k);
-  std::vector<int> pl(segs.size());
+  std::vector<int> pl(parts.size());
   VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_collection_search_host(
       dev.get(), v.data(), v.size(), dim, int(metric), raw_queries, nq, k, &sp, ids.data(),
       d.data(), dc.data(), pl.data())));
@@ -841,11 +875,26 @@ inline Status SearchCollection(Device& dev, std::span<const GpuSegment* const> s
   if (dist_comps != nullptr) *dist_comps = dc;
   if (plans != nullptr) {
     static const char* const kNames[] = {"index", "empty", "prefilter_exact", "filtered_index",
-                                         "filtered_index+exact_fallback", "post_filter"};
+                                         "filtered_index+exact_fallback", "post_filter", "scan",
+                                         "scan_filter", "host"};
     plans->clear();
     for (int x : pl) plans->push_back(kNames[x]);
   }
   return Status::OK();
+}
+
+// The same over segments that are all on the device.
+inline Status SearchCollection(Device& dev, std::span<const GpuSegment* const> segs, size_t dim,
+                               Metric metric, const float* raw_queries, size_t nq, size_t k,
+                               const SearchParams& p,
+                               const std::vector<const DenseRowFilter*>* filters,
+                               std::vector<std::vector<SearchHit>>& out,
+                               std::vector<uint64_t>* dist_comps = nullptr,
+                               std::vector<std::string>* plans = nullptr) {
+  std::vector<DiskPart> parts(segs.size());
+  for (size_t i = 0; i < segs.size(); ++i) parts[i].gpu = segs[i];
+  return SearchCollection(dev, std::span<const DiskPart>(parts), dim, metric, raw_queries, nq, k,
+                          p, filters, out, dist_comps, plans);
 }
 
 }  // namespace vdbg

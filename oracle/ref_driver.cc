@@ -189,6 +189,51 @@ size_t ref_hnsw_sq8_file(int metric, const float* base, size_t rows, size_t dim,
   return sink.s.size();
 }
 
+// HnswIndex::build + save (src/index/hnsw/hnsw_index.cc:18-40): the VDBHNSW1 file a segment
+// of vdb's default index type (IndexType::Hnsw, options.h:22) holds.  Returns the file size;
+// writes it when it fits in cap bytes.
+size_t ref_hnsw_file(int metric, const float* base, size_t rows, size_t dim, size_t pd,
+                     size_t M, size_t ef_construction, uint64_t seed, char* buf, size_t cap) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::Hnsw;
+  o.M = M;
+  o.ef_construction = ef_construction;
+  o.seed = seed;
+  HnswIndex idx(o, static_cast<Metric>(metric), v);
+  if (!idx.build(nullptr).ok()) return 0;
+  StringSink sink;
+  if (!idx.save(sink).ok()) return 0;
+  if (buf != nullptr && sink.s.size() <= cap) std::memcpy(buf, sink.s.data(), sink.s.size());
+  return sink.s.size();
+}
+
+// LoadIndex of a VDBHNSW1 file (index.cc:63-67) and HnswIndex::search per query, under a
+// RowFilter given as dense words (nullable).  Returns 0, or 1 when the file does not load.
+int ref_hnsw_search_batch(int metric, const char* file, size_t file_len, const float* base,
+                          size_t rows, size_t dim, size_t pd, const float* queries, size_t nq,
+                          size_t k, size_t ef, const uint64_t* allow_words, float* od,
+                          uint32_t* oi, uint64_t* dc, int nthreads) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::Hnsw;
+  auto idx = LoadIndex(std::string_view(file, file_len), o, static_cast<Metric>(metric), v);
+  if (!idx.ok() || (*idx)->type() != IndexType::Hnsw) return 1;
+  const Index& ix = **idx;
+  SearchParams p;
+  p.ef = ef;
+  DenseFilter filt(allow_words);
+  ThreadPool pool(nthreads <= 0 ? 1 : static_cast<size_t>(nthreads));
+  pool.parallel_for(0, nq, [&](size_t qi) {
+    std::vector<Neighbor> out;
+    IndexSearchStats st;
+    ix.search(queries + qi * pd, k, p, allow_words != nullptr ? &filt : nullptr, out, &st);
+    WritePadded(out, k, od + qi * k, oi + qi * k);
+    if (dc != nullptr) dc[qi] = st.distance_computations;
+  });
+  return 0;
+}
+
 // LoadIndex of a VDBHSQ81 file (index.cc:38-87) and HnswSq8Index::search
 // (src/index/hnsw/hnsw_index.cc:82-100) per query: graph beam over the codes with the
 // reference's own kernel set, then Rerank.  allow_words (nullable) is the RowFilter (bit r of

@@ -11,6 +11,8 @@ fixtures are data only (.npz without pickles): inputs and expected outputs.
     python3 tests/golden/make_golden.py hnsw       # hnsw.npz only
     python3 tests/golden/make_golden.py pqflat     # pqflat.npz only
     python3 tests/golden/make_golden.py ivf_shapes # ivf_shapes.npz only
+    python3 tests/golden/make_golden.py hnswf      # hnswf.npz only
+    python3 tests/golden/make_golden.py ivf1m      # ivf1m.npz only (a few minutes)
 """
 import ctypes as C
 import os
@@ -312,6 +314,94 @@ def make_pqflat(L):
     np.savez_compressed(os.path.join(HERE, "pqflat.npz"), **out)
 
 
+HNSWF_N, HNSWF_DIM, HNSWF_NQ, HNSWF_EF = 3000, 64, 24, 32
+
+
+def hnswf_inputs():
+    """The float-row HNSW segment of hnswf.npz, regenerated by the tests from the same
+    generators: rows (uniform x 10, 64 dims), raw queries, the deleted rows (2 %) and three
+    filters (1 %, 10 %, 50 %) as dense words."""
+    from vdbg import datagen
+    rows = datagen.pad(datagen.uniform_rows(HNSWF_N, HNSWF_DIM, 1701) * 10, HNSWF_DIM)
+    raw = (datagen.uniform_rows(HNSWF_NQ, HNSWF_DIM, 1702) * 10).astype(np.float32)
+
+    def mask(frac, seed):
+        return _words(np.random.default_rng(seed).random(HNSWF_N) < frac)
+
+    deleted = mask(0.02, 1703)
+    filters = {"f01": mask(0.01, 1704), "f10": mask(0.10, 1705), "f50": mask(0.50, 1706)}
+    return rows, raw, deleted, filters
+
+
+def hnswf_allows(deleted, filters):
+    """The RowFilters SearchDiskSegment hands HnswIndex::search on this segment: the delete
+    filter (no request filter, or post-filter) and each filter minus the deleted rows."""
+    n = HNSWF_N
+    clip = np.full_like(deleted, np.iinfo(np.uint64).max)
+    if n % 64:
+        clip[-1] = np.uint64((1 << (n % 64)) - 1)
+    out = {"del": ~deleted & clip}
+    for name, w in filters.items():
+        out[name] = w & ~deleted & clip
+    return out
+
+
+def make_hnswf(L):
+    """hnswf.npz: a VDBHNSW1 file (vdb's default index type, HnswIndex over float rows) that
+    the reference built and saved, and its own HnswIndex::search results (ids, distances,
+    distance computations) on the prepared queries for every (k, ef, RowFilter) that
+    SearchDiskSegment (planner.cc:42-129) issues on this segment in the collection tests:
+    k 1 / 10 / 40 under the delete filter and under each filter minus deletes, and the
+    post-filter widths k x 10 under the delete filter (ef = max(32, k))."""
+    from oracle_lib import Reference
+    R = Reference()
+    rows, raw, deleted, filters = hnswf_inputs()
+    q = np.ascontiguousarray(raw)  # L2: PrepareQuery only pads (64 dims are already padded)
+    f = R.hnsw_file(rows, HNSWF_DIM, M=12, ef_construction=60, seed=42, metric="l2")
+    allows = hnswf_allows(deleted, filters)
+    out = {"index_file": np.frombuffer(f, np.uint8).copy(), "deleted": deleted}
+    out.update({name: w for name, w in filters.items()})
+    keys = []
+    for name, aw in allows.items():
+        for k in (1, 10, 40):
+            keys.append((k, name))
+    keys += [(100, "del"), (400, "del")]
+    for i, (k, name) in enumerate(keys):
+        ef = max(HNSWF_EF, k)
+        od, oi, dc = R.hnsw_search(f, rows, HNSWF_DIM, q, k, ef, "l2", allows[name])
+        out[f"r{i}_d"], out[f"r{i}_i"], out[f"r{i}_dc"] = od, oi, dc
+    out["keys_k"] = np.array([k for k, _ in keys], np.int64)
+    out["keys_allow"] = np.array([name for _, name in keys])
+    out["kernels"] = np.array(R.lib.ref_best_kernels().decode())
+    np.savez_compressed(os.path.join(HERE, "hnswf.npz"), **out)
+
+
+def make_ivf1m(L):
+    """ivf1m.npz: vdb's own IvfPqIndex::build (ivf_pq.cc:102-149, k-means at its fixed 25
+    iterations, kmeans.h:14) over the bench's 1M x 128 SIFT-like rows (vdbg.datagen.sift_like,
+    seed 2002) at nlist 4,096, m 16, seed 42, 256 points per centroid, on 8 threads: the
+    VDBIVFP1 file's length and CRC32C, SHA-256 digests of its coarse centroids, codebook and
+    list ids, and its list sizes (the file itself, 36 MB, is not kept)."""
+    import hashlib
+    import time
+    from ivf_file import parse_ivfpq
+    from oracle_lib import Reference
+    from vdbg import datagen
+    R = Reference()
+    base = datagen.sift_like(1_000_000, 128, 2002)
+    t0 = time.time()
+    f = R.ivfpq_build(base, 128, 4096, 16, seed=42, max_points=256, metric="l2", threads=8)
+    p = parse_ivfpq(f)
+    sha = lambda a: np.frombuffer(hashlib.sha256(np.ascontiguousarray(a).tobytes()).digest(), np.uint8)
+    out = {"file_len": np.int64(len(f)),
+           "file_crc": np.uint32(int.from_bytes(f[-4:], "little")),
+           "coarse_sha": sha(p["coarse"]), "codebook_sha": sha(p["pq_centroids"]),
+           "ids_sha": sha(p["list_ids"]), "codes_sha": sha(p["list_codes"]),
+           "list_sizes": np.diff(p["list_off"].astype(np.int64)).astype(np.uint32),
+           "build_s": np.float64(time.time() - t0)}
+    np.savez_compressed(os.path.join(HERE, "ivf1m.npz"), **out)
+
+
 def ivf_shape_rows(n, dim, seed):
     """The rows of an ivf_shapes case, regenerated by the tests from the same counter-based
     generator (vdbg.datagen), so the fixture holds only the files and the results."""
@@ -353,7 +443,17 @@ def make_ivf_shapes(L):
 
 
 if __name__ == "__main__":
-    if sys.argv[1:] == ["ivf_shapes"]:
+    if sys.argv[1:] == ["ivf1m"]:
+        ref = load_reference()
+        if ref is None:
+            sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+        make_ivf1m(ref.lib)
+    elif sys.argv[1:] == ["hnswf"]:
+        ref = load_reference()
+        if ref is None:
+            sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")
+        make_hnswf(ref.lib)
+    elif sys.argv[1:] == ["ivf_shapes"]:
         ref = load_reference()
         if ref is None:
             sys.exit("oracle/_ref/libvdbref.so is not built: run `make -C oracle` first")

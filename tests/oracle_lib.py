@@ -172,6 +172,130 @@ class Oracle:
                                        nprobe, rerank, allow, od, oi, dc, 8)
         return od, oi, dc
 
+    def segment_hits(self, sg, metric, q, k, ef=64, nprobe=16, rerank=-1, strategy=0,
+                     prefilter_threshold=10000, post_filter_alpha=10, kset="avx512"):
+        """SearchDiskSegment (planner.cc:42-129) of one segment of collection_search on
+        prepared queries q (nq, pd): (dists, rows) [nq, k], distance computations per query
+        and the plan name.  A "host" segment returns its given hits; an "hnsw" one (vdb's
+        HnswIndex over a VDBHNSW1 file) takes each HnswIndex::search from sg["recorded"],
+        keyed by (k, ef, allowed words or None as bytes)."""
+        nq = q.shape[0]
+        names = ["index", "empty", "prefilter_exact", "filtered_index",
+                 "filtered_index+exact_fallback", "post_filter", "scan", "scan_filter", "host"]
+        if sg["kind"] == "host":
+            od, oi, dc = sg["hits"]
+            return od, oi, np.asarray(dc, np.uint64), "host"
+
+        def count(words, n):
+            bits = np.unpackbits(np.ascontiguousarray(words, np.uint64).view(np.uint8),
+                                 bitorder="little")[:n]
+            return int(bits.sum())
+
+        def clip(words, n):
+            w = np.ascontiguousarray(words, np.uint64).copy()
+            if n % 64:
+                w[-1] &= np.uint64((1 << (n % 64)) - 1)
+            return w
+
+        base = np.ascontiguousarray(sg["base"], np.float32)
+        n = base.shape[0]
+        deleted = sg.get("deleted")
+        filt = sg.get("filter")
+        ndel = 0 if deleted is None else count(deleted, n)
+        live = n - min(n, ndel)
+        del_allow = None if ndel == 0 else clip(~np.asarray(deleted, np.uint64), n)
+        bm, matches = None, 0
+        if filt is not None:
+            bm = np.asarray(filt, np.uint64).copy()
+            if ndel > 0:
+                bm &= ~np.asarray(deleted, np.uint64)
+            bm = clip(bm, n)
+            matches = count(bm, n)
+        if sg["kind"] == "memory":
+            # SearchMutable (planner.cc:131-151) -> MutableSegment::Search
+            # (mutable_segment.cc:46-64): the rows not deleted and matching the filter,
+            # exactly, counted as distance computations
+            allow = None
+            if filt is not None or ndel > 0:
+                allow = np.full((n + 63) // 64, np.iinfo(np.uint64).max, np.uint64)
+                if filt is not None:
+                    allow &= np.asarray(filt, np.uint64)
+                if ndel > 0:
+                    allow &= ~np.asarray(deleted, np.uint64)
+                allow = clip(allow, n)
+            matches = n if allow is None else count(allow, n)
+            od, oi = self.flat_search(base, q, k, metric=metric, kset=kset, allow=allow)
+            return od, oi, np.full(nq, matches, np.uint64), names[7 if filt is not None else 6]
+        npb = C.c_size_t()
+        plan = self.lib.or_plan_segment(1 if filt is not None else 0, n, ndel, matches,
+                                        1 if sg["kind"] == "flat" else 0, strategy, ef, k,
+                                        nprobe, prefilter_threshold, C.byref(npb))
+
+        def index_search(kk, allow, ef_=ef):
+            if sg["kind"] == "hnsw":
+                key = (int(kk), int(max(ef_, kk)),
+                       None if allow is None else np.ascontiguousarray(allow, np.uint64).tobytes())
+                if key not in sg["recorded"]:
+                    raise KeyError(f"no recorded HnswIndex::search for k={kk}, ef={ef_}")
+                od, oi, dc = sg["recorded"][key]
+                return od.copy(), oi.copy(), dc.copy()
+            if sg["kind"] == "pqflat":
+                return self.pqflat_search(sg["pq"], base, q, kk, rerank, metric, allow,
+                                          kset=kset)
+            if sg["kind"] == "hnsw_sq8":
+                od, oi, dc = self.hnsw_sq8_search(sg["file"], base, q, kk, ef_, rerank,
+                                                  metric=metric, allow=allow, kset=kset)
+                return od, oi, dc
+            if sg["kind"] == "ivf":
+                od, oi, dc = self.ivfpq_search(sg["ix"], sg["term2"], base, q, kk,
+                                               npb.value, rerank, metric, allow, kset=kset)
+                return od, oi, dc
+            if sg["kind"] == "sq8":
+                depth = max(ef_, kk) if rerank < 0 else rerank
+                od, oi = self.sq8_search(base, sg["codes"], sg["vmin"], sg["scale"], q, kk,
+                                         depth, metric=metric, kset=kset, allow=allow)
+                extra = min(max(depth, kk), n) if depth > 0 else 0
+                return od, oi, np.full(nq, n + extra, np.uint64)
+            od, oi = self.flat_search(base, q, kk, metric=metric, kset=kset, allow=allow)
+            return od, oi, np.full(nq, n, np.uint64)
+
+        if plan == 0:
+            od, oi, dc = index_search(k, del_allow)
+        elif plan == 1:
+            od = np.full((nq, k), np.inf, np.float32)
+            oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
+            dc = np.zeros(nq, np.uint64)
+        elif plan == 2:
+            od, oi = self.flat_search(base, q, k, metric=metric, kset=kset, allow=bm)
+            dc = np.full(nq, matches, np.uint64)
+        elif plan == 3:
+            od, oi, dc = index_search(k, bm)
+            if strategy == 0:
+                hits = (oi != 0xFFFFFFFF).sum(axis=1)
+                short = np.nonzero(hits < min(k, matches))[0]
+                if short.size:
+                    plan = 4
+                    xd, xi = self.flat_search(base, q, k, metric=metric, kset=kset,
+                                              allow=bm)
+                    od[short], oi[short] = xd[short], xi[short]
+                    dc = dc.copy()
+                    dc[short] += np.uint64(matches)
+        else:
+            kk = min(max(live, 1), k * max(1, post_filter_alpha))
+            wd, wi, dc = index_search(kk, del_allow, max(ef, kk))  # pp.ef (:113-114)
+            od = np.full((nq, k), np.inf, np.float32)
+            oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
+            for i in range(nq):
+                out = 0
+                for j in range(kk):
+                    r = int(wi[i, j])
+                    if r == 0xFFFFFFFF or out >= k:
+                        break
+                    if (int(bm[r >> 6]) >> (r & 63)) & 1:
+                        oi[i, out], od[i, out] = r, wd[i, j]
+                        out += 1
+        return od, oi, dc.astype(np.uint64), names[plan]
+
     def collection_search(self, segments, dim, metric, raw, k, ef=64, nprobe=16, rerank=-1,
                           strategy=0, prefilter_threshold=10000, post_filter_alpha=10,
                           kset="avx512"):
@@ -186,7 +310,10 @@ class Oracle:
         SQ8 scan index, built from rows, no graph): codes, vmin, scale; hnsw_sq8 (vdb's
         HnswSq8Index): file (the VDBHSQ81 bytes); ivf: ix (parsed VDBIVFP1) and term2 (or
         None); pqflat: pq (a parsed VDBPQFL1); memory: an in-memory part (the active or a
-        frozen mutable segment, listed first), scanned exactly.  Returns (ext ids, dists, dist comps, plan names)."""
+        frozen mutable segment, listed first), scanned exactly; hnsw (vdb's HnswIndex over a
+        VDBHNSW1 file): recorded, its HnswIndex::search results (segment_hits); host: hits,
+        (dists, rows, dist comps) of a segment already searched.  Returns (ext ids, dists,
+        dist comps, plan names)."""
         nq = raw.shape[0]
         pd = (dim + 15) // 16 * 16
         q = np.zeros((nq, pd), np.float32)
@@ -197,122 +324,17 @@ class Oracle:
             for i in range(nq):
                 if self.lib.or_normalize(q[i], dim) != 1:
                     raise ValueError("a zero query cannot be normalized for cosine")
-        names = ["index", "empty", "prefilter_exact", "filtered_index",
-                 "filtered_index+exact_fallback", "post_filter", "scan", "scan_filter"]
-
-        def count(words, n):
-            bits = np.unpackbits(np.ascontiguousarray(words, np.uint64).view(np.uint8),
-                                 bitorder="little")[:n]
-            return int(bits.sum())
-
-        def clip(words, n):
-            w = np.ascontiguousarray(words, np.uint64).copy()
-            if n % 64:
-                w[-1] &= np.uint64((1 << (n % 64)) - 1)
-            return w
-
         np_ = len(segments)
         pdist = np.full((max(np_, 1), nq, k), np.inf, np.float32)
         prow = np.full((max(np_, 1), nq, k), 0xFFFFFFFF, np.uint32)
         dcs = np.zeros(nq, np.uint64)
         plans = []
         for p, sg in enumerate(segments):
-            base = np.ascontiguousarray(sg["base"], np.float32)
-            n = base.shape[0]
-            deleted = sg.get("deleted")
-            filt = sg.get("filter")
-            ndel = 0 if deleted is None else count(deleted, n)
-            live = n - min(n, ndel)
-            del_allow = None if ndel == 0 else clip(~np.asarray(deleted, np.uint64), n)
-            bm, matches = None, 0
-            if filt is not None:
-                bm = np.asarray(filt, np.uint64).copy()
-                if ndel > 0:
-                    bm &= ~np.asarray(deleted, np.uint64)
-                bm = clip(bm, n)
-                matches = count(bm, n)
-            if sg["kind"] == "memory":
-                # SearchMutable (planner.cc:131-151) -> MutableSegment::Search
-                # (mutable_segment.cc:46-64): the rows not deleted and matching the filter,
-                # exactly, counted as distance computations
-                allow = None
-                if filt is not None or ndel > 0:
-                    allow = np.full((n + 63) // 64, np.iinfo(np.uint64).max, np.uint64)
-                    if filt is not None:
-                        allow &= np.asarray(filt, np.uint64)
-                    if ndel > 0:
-                        allow &= ~np.asarray(deleted, np.uint64)
-                    allow = clip(allow, n)
-                matches = n if allow is None else count(allow, n)
-                od, oi = self.flat_search(base, q, k, metric=metric, kset=kset, allow=allow)
-                pdist[p], prow[p] = od, oi
-                dcs += np.uint64(matches)
-                plans.append(names[7 if filt is not None else 6])
-                continue
-            npb = C.c_size_t()
-            plan = self.lib.or_plan_segment(1 if filt is not None else 0, n, ndel, matches,
-                                            1 if sg["kind"] == "flat" else 0, strategy, ef, k,
-                                            nprobe, prefilter_threshold, C.byref(npb))
-
-            def index_search(kk, allow, ef_=ef):
-                if sg["kind"] == "pqflat":
-                    return self.pqflat_search(sg["pq"], base, q, kk, rerank, metric, allow,
-                                              kset=kset)
-                if sg["kind"] == "hnsw_sq8":
-                    od, oi, dc = self.hnsw_sq8_search(sg["file"], base, q, kk, ef_, rerank,
-                                                      metric=metric, allow=allow, kset=kset)
-                    return od, oi, dc
-                if sg["kind"] == "ivf":
-                    od, oi, dc = self.ivfpq_search(sg["ix"], sg["term2"], base, q, kk,
-                                                   npb.value, rerank, metric, allow, kset=kset)
-                    return od, oi, dc
-                if sg["kind"] == "sq8":
-                    depth = max(ef_, kk) if rerank < 0 else rerank
-                    od, oi = self.sq8_search(base, sg["codes"], sg["vmin"], sg["scale"], q, kk,
-                                             depth, metric=metric, kset=kset, allow=allow)
-                    extra = min(max(depth, kk), n) if depth > 0 else 0
-                    return od, oi, np.full(nq, n + extra, np.uint64)
-                od, oi = self.flat_search(base, q, kk, metric=metric, kset=kset, allow=allow)
-                return od, oi, np.full(nq, n, np.uint64)
-
-            if plan == 0:
-                od, oi, dc = index_search(k, del_allow)
-            elif plan == 1:
-                od = np.full((nq, k), np.inf, np.float32)
-                oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
-                dc = np.zeros(nq, np.uint64)
-            elif plan == 2:
-                od, oi = self.flat_search(base, q, k, metric=metric, kset=kset, allow=bm)
-                dc = np.full(nq, matches, np.uint64)
-            elif plan == 3:
-                od, oi, dc = index_search(k, bm)
-                if strategy == 0:
-                    hits = (oi != 0xFFFFFFFF).sum(axis=1)
-                    short = np.nonzero(hits < min(k, matches))[0]
-                    if short.size:
-                        plan = 4
-                        xd, xi = self.flat_search(base, q, k, metric=metric, kset=kset,
-                                                  allow=bm)
-                        od[short], oi[short] = xd[short], xi[short]
-                        dc = dc.copy()
-                        dc[short] += np.uint64(matches)
-            else:
-                kk = min(max(live, 1), k * max(1, post_filter_alpha))
-                wd, wi, dc = index_search(kk, del_allow, max(ef, kk))  # pp.ef (:113-114)
-                od = np.full((nq, k), np.inf, np.float32)
-                oi = np.full((nq, k), 0xFFFFFFFF, np.uint32)
-                for i in range(nq):
-                    out = 0
-                    for j in range(kk):
-                        r = int(wi[i, j])
-                        if r == 0xFFFFFFFF or out >= k:
-                            break
-                        if (int(bm[r >> 6]) >> (r & 63)) & 1:
-                            oi[i, out], od[i, out] = r, wd[i, j]
-                            out += 1
+            od, oi, dc, plan = self.segment_hits(sg, metric, q, k, ef, nprobe, rerank, strategy,
+                                                 prefilter_threshold, post_filter_alpha, kset)
             pdist[p], prow[p] = od, oi
-            dcs += dc.astype(np.uint64)
-            plans.append(names[plan])
+            dcs += np.asarray(dc).astype(np.uint64)
+            plans.append(plan)
         ext = np.ascontiguousarray(np.concatenate([sg["ext"] for sg in segments])
                                    if segments else np.zeros(1, np.uint64), np.uint64)
         off = np.concatenate([[0], np.cumsum([sg["base"].shape[0] for sg in segments])[:-1]]
@@ -380,6 +402,11 @@ class Reference:
         _sig(lib, "ref_hnsw_sq8_search_batch", C.c_int,
              [C.c_int, C.c_char_p, sz, f32p, sz, sz, sz, f32p, sz, sz, sz, C.c_int, _opt(u64p),
               f32p, u32p, _opt(u64p), C.c_int])
+        _sig(lib, "ref_hnsw_file", sz,
+             [C.c_int, f32p, sz, sz, sz, sz, sz, C.c_uint64, C.c_void_p, sz])
+        _sig(lib, "ref_hnsw_search_batch", C.c_int,
+             [C.c_int, C.c_char_p, sz, f32p, sz, sz, sz, f32p, sz, sz, sz, _opt(u64p),
+              f32p, u32p, _opt(u64p), C.c_int])
         _sig(lib, "ref_filtered_collection_search", C.c_int,
              [C.c_int, C.c_void_p, C.c_void_p, sz, sz, sz, C.c_void_p, u64p, f32p, sz, sz,
               u64p, f32p, C.c_int])
@@ -431,6 +458,35 @@ class Reference:
         rc = self.lib.ref_pqflat_search_batch(METRIC[metric], file, len(file), base,
                                               base.shape[0], dim, pd, queries, nq, k, rerank,
                                               allow, od, oi, dc, threads)
+        if rc != 0:
+            raise ValueError("LoadIndex refused the file")
+        return od, oi, dc
+
+    def hnsw_file(self, base, dim, M=16, ef_construction=100, seed=42, metric="l2"):
+        """HnswIndex::build (single-threaded) + save: the VDBHNSW1 file bytes."""
+        base = np.ascontiguousarray(base, np.float32)
+        n, pd = base.shape
+        size = self.lib.ref_hnsw_file(METRIC[metric], base, n, dim, pd, M, ef_construction,
+                                      seed, None, 0)
+        buf = C.create_string_buffer(size)
+        assert self.lib.ref_hnsw_file(METRIC[metric], base, n, dim, pd, M, ef_construction,
+                                      seed, buf, size) == size
+        return buf.raw
+
+    def hnsw_search(self, file, base, dim, queries, k, ef=64, metric="l2", allow=None,
+                    threads=8):
+        """LoadIndex of a VDBHNSW1 file and HnswIndex::search per query.  Returns (dists,
+        ids, distance computations)."""
+        base = np.ascontiguousarray(base, np.float32)
+        queries = np.ascontiguousarray(queries, np.float32)
+        nq, pd = queries.shape
+        od = np.empty((nq, k), np.float32)
+        oi = np.empty((nq, k), np.uint32)
+        dc = np.empty(nq, np.uint64)
+        file = bytes(file)
+        rc = self.lib.ref_hnsw_search_batch(METRIC[metric], file, len(file), base, base.shape[0],
+                                            dim, pd, queries, nq, k, ef, allow, od, oi, dc,
+                                            threads)
         if rc != 0:
             raise ValueError("LoadIndex refused the file")
         return od, oi, dc

@@ -326,3 +326,124 @@ def test_pqflat_segment(ctx, oracle):
             if ix is not None:
                 ix.close()
             d_.close()
+
+
+# ---------------------------------------------------------------- a segment searched on the host
+
+def _hnswf():
+    """vdb's default index type: a float-row HNSW segment (VDBHNSW1) the reference built, and
+    its own HnswIndex::search results recorded on it (tests/golden/hnswf.npz), keyed as the
+    oracle's segment_hits looks them up: (k, ef, allowed words)."""
+    import os
+    import sys
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    from make_golden import HNSWF_EF, hnswf_allows, hnswf_inputs
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hnswf.npz"))
+    rows, raw, deleted, filters = hnswf_inputs()
+    assert np.array_equal(deleted, z["deleted"])
+    for name, w in filters.items():
+        assert np.array_equal(w, z[name])
+    allows = hnswf_allows(deleted, filters)
+    recorded = {}
+    for i, (k, name) in enumerate(zip(z["keys_k"], z["keys_allow"])):
+        k = int(k)
+        recorded[(k, max(HNSWF_EF, k), allows[str(name)].tobytes())] = (
+            z[f"r{i}_d"], z[f"r{i}_i"], z[f"r{i}_dc"])
+    return rows, raw, deleted, filters, recorded, HNSWF_EF
+
+
+def test_host_searched_hnsw_segment(ctx, oracle):
+    """vdb's default index type (IndexType::Hnsw, options.h:22) keeps its graph search on the
+    CPU: its segment has no GPU copy, and vdb's own SearchDiskSegment result for it (here the
+    reference's recorded HnswIndex::search calls, composed by the planner's rules) joins the
+    device batch as a host part, in its snapshot position between device-searched flat and
+    IVF-PQ segments with deletes and filters.  External ids (one hit per id, an id shared
+    with the HNSW segment included), distances, distance computations and plans must equal the
+    oracle's composition of the whole collection."""
+    rows_h, raw, del_h, filt_h, recorded, ef = _hnswf()
+    dim = rows_h.shape[1]
+    nh = rows_h.shape[0]
+    ext_h = np.arange(nh, dtype=np.uint64) * 7 + 5
+    segs, handles = [], []
+    for i, (n, kind) in enumerate([(5000, "flat"), (None, "hnsw"), (9000, "ivf"), (800, "flat")]):
+        if kind == "hnsw":
+            segs.append({"base": rows_h, "ext": ext_h, "kind": "hnsw", "recorded": recorded,
+                         "deleted": del_h})
+            handles.append(None)
+            continue
+        base = datagen.pad(datagen.uniform_rows(n, dim, 1720 + i) * 10, dim)
+        ext = np.arange(n, dtype=np.uint64) * 7 + 6 + 100000 * i
+        if i == 3:
+            ext[:50] = ext_h[:50]  # upserted rows of the HNSW segment
+        ds = vdbg.Dataset(ctx, base, dim)
+        ds.set_external_ids(ext)
+        sg = {"base": base, "ext": ext, "kind": kind, "deleted": _mask(n, 0.03, 1730 + i)}
+        ix = None
+        if kind == "ivf":
+            blob = synth_ivfpq(base, dim, 24, 8, seed=5)
+            ix = vdbg.IvfPqIndex.load(ds, blob)
+            p = parse_ivfpq(blob)
+            t2 = np.empty(p["nlist"] * p["m"] * 256, np.float32)
+            oracle.lib.or_ivfpq_term2(p["coarse"], p["nlist"], p["pd"], p["pq_centroids"],
+                                      p["m"], p["dim"] // p["m"], t2)
+            sg.update(ix=p, term2=t2)
+        segs.append(sg)
+        handles.append((ds, ix))
+    q = np.zeros((raw.shape[0], dim), np.float32)
+    q[:, :raw.shape[1]] = raw  # L2: the prepared query is the raw one (64 dims)
+    cases = [(None, {}), ("f50", {"prefilter_threshold": 100}),
+             ("f01", {"strategy": "graph"}), ("f10", {"strategy": "graph"}),
+             ("f50", {"strategy": "graph"}), ("f10", {"strategy": "post_filter"}),
+             ("f10", {})]
+    try:
+        for fname, kw in cases:
+            for i, sg in enumerate(segs):
+                if sg["kind"] == "hnsw":
+                    sg["filter"] = None if fname is None else filt_h[fname]
+                else:
+                    n = sg["base"].shape[0]
+                    sg["filter"] = None if fname is None else _mask(n, {"f01": .01, "f10": .1, "f50": .5}[fname], 1740 + i)
+            for k in (1, 10, 40):
+                print(f"host-searched HNSW segment: filter {fname} {kw} k={k}", flush=True)
+                okw = dict(kw, ef=ef)
+                okw["strategy"] = vdbg.STRATEGIES[okw.get("strategy", "auto")]
+                # the host part: vdb's SearchDiskSegment on the HNSW segment
+                hd, hr, hdc, hplan = oracle.segment_hits(segs[1], "l2", q, k, **okw)
+                hext = np.where(hr == 0xFFFFFFFF, np.uint64(0), ext_h[np.minimum(hr, nh - 1)])
+                host = vdbg.HostHits(hd, hr, hext, hdc)
+                parts = []
+                for sg, h in zip(segs, handles):
+                    if h is None:
+                        parts.append(host)
+                    else:
+                        parts.append((h[0], h[1], sg["deleted"], sg["filter"]))
+                gi, gd, gdc, gp = vdbg.collection_search(
+                    ctx, parts, dim, "l2", raw, k, vdbg.SearchParams(ef=ef, **kw))
+                oi, od, odc, op = oracle.collection_search(segs, dim, "l2", raw, k, **okw)
+                assert gp[1] == "host" and gp[0] == op[0] and gp[2:] == op[2:], (gp, op)
+                assert np.array_equal(gi, oi), (fname, kw, k)
+                assert np.array_equal(gd.view(np.uint32), od.view(np.uint32)), (fname, kw, k)
+                assert np.array_equal(gdc, odc), (fname, kw, k)
+                if fname == "f50" and kw.get("prefilter_threshold") == 100:
+                    assert hplan == "filtered_index", hplan  # the HNSW walk under the filter
+    finally:
+        for h in handles:
+            if h is not None:
+                if h[1] is not None:
+                    h[1].close()
+                h[0].close()
+
+
+def test_host_part_rejects_unsorted_hits(ctx):
+    """A host part's lists must be in ascending (dist, row) order, as Index::search returns
+    them: the device merge keeps that order as the (dist, part, row) tie rule."""
+    d = np.array([[1.0, 0.5, np.inf]], np.float32)
+    r = np.array([[3, 4, 0xFFFFFFFF]], np.uint32)
+    e = np.array([[30, 40, 0]], np.uint64)
+    raw = np.zeros((1, 16), np.float32)
+    with pytest.raises(vdbg.VdbgError) as ex:
+        vdbg.collection_search(ctx, [vdbg.HostHits(d, r, e)], 16, "l2", raw, 3)
+    assert ex.value.code == 1
+    d2 = np.array([[0.5, 1.0, np.inf]], np.float32)
+    gi, gd, gdc, gp = vdbg.collection_search(ctx, [vdbg.HostHits(d2, r, e, [9])], 16, "l2", raw, 3)
+    assert gp == ["host"] and list(gi[0]) == [30, 40, 2**64 - 1] and gdc[0] == 9

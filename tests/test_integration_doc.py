@@ -60,3 +60,25 @@ def test_integration_search_batch_compiles_against_vdb_headers(tmp_path):
                         "-I", os.path.join(ROOT, "include"), str(src)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_integration_segment_open_compiles_against_vdb_headers(tmp_path):
+    """The GPU branch of Segment::Open, which keeps a segment whose index the GPU does not
+    hold (VDBHNSW1, vdb's default index type) on the CPU path instead of failing its open."""
+    if not os.path.isdir(os.path.join(REF, "src", "index")):
+        pytest.skip("the reference sources are not present here")
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    a = re.search(r"<!-- adapter:begin -->\s*```cpp\n(.*?)```\s*<!-- adapter:end -->", doc, re.S)
+    o = re.search(r"<!-- open:begin -->\s*```cpp\n(.*?)```\s*<!-- open:end -->", doc, re.S)
+    assert a and o, "adapter or Segment::Open block not found in INTEGRATION.md"
+    assert "VDBG_NOT_SUPPORTED" in o.group(1), "NotSupported must mean no GPU copy"
+    hdr = tmp_path / "index" / "gpu"
+    hdr.mkdir(parents=True)
+    (hdr / "gpu_index.h").write_text(a.group(1))
+    src = tmp_path / "gpu_segment_open.cc"
+    src.write_text(o.group(1))
+    r = subprocess.run([_gxx(), "-std=c++20", "-Wall", "-fsyntax-only", "-I", str(tmp_path),
+                        "-I", os.path.join(REF, "include"), "-I", os.path.join(REF, "src"),
+                        "-I", os.path.join(ROOT, "include"), str(src)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
