@@ -12,7 +12,16 @@ checks on query subsets where the CPU restatement would take minutes).
   test_build_gpu.py.)
 - Every point of the bench's sweeps: flat batches 1, 2, 8, 64, 1,024 at k = 10 and k = 100,
   IVF-PQ nprobe 16 / 32 / 64 / 128 x rerank 0 / 100, ids, distances and distance counts
-  against the oracle."""
+  against the oracle.
+- The bench's own calls at full batch: the flat headline (10,000 queries, k = 10, and the
+  k = 100 sweep point) and the SQ8 scan (depth 100, k = 10), each checked on 64 queries
+  spread over the whole batch, its last query tile included.
+- vdb's own IVF-PQ build at this size (its fixed 25 k-means iterations): the GPU build writes
+  the reference's file (tests/golden/ivf1m.npz holds its length, CRC32C and digests).
+- A collection shaped as the filtered benchmark: 384-dim cosine rows in 8 segments of
+  100,000, 2 % deleted, filters of 1 / 10 / 50 %, merged, against the oracle's composition."""
+import os
+
 import numpy as np
 import pytest
 
@@ -113,3 +122,118 @@ def test_ivfpq_sweep_points_match_oracle(big, ivf, oracle, nprobe, rerank):
     od, oi, odc = oracle.ivfpq_search(f, f["term2"], base, q[:s], 10, nprobe, rerank)
     _eq(gi[:s], gd[:s], oi, od)
     assert np.array_equal(dc[:s], odc)
+
+
+def _spread(nq, count=64):
+    """count query positions over a batch of nq: evenly spaced from the first to the last,
+    and the last 8 (the batch's last query tile)."""
+    return np.unique(np.concatenate([np.linspace(0, nq - 1, count - 8).astype(np.int64),
+                                     np.arange(nq - 8, nq)]))
+
+
+@pytest.mark.parametrize("k", [10, 100])
+def test_flat_headline_batch_matches_oracle(big, oracle, k):
+    """The headline call as the bench makes it: all 10,000 queries in one batch."""
+    base, qs, ds = big
+    print(f"config-size: flat 10,000 queries k={k}", flush=True)
+    gi, gd = ds.flat_search(qs, k)
+    sel = _spread(len(qs))
+    od, oi = oracle.flat_search(base, np.ascontiguousarray(qs[sel]), k, threads=16)
+    _eq(gi[sel], gd[sel], oi, od)
+
+
+def test_sq8_search_1m_matches_oracle(big, oracle):
+    """The SQ8 path as the bench runs it: every 1M code scanned for 10,000 queries, the top
+    100 reranked to 10 (Sq8Quantizer + TopK + Rerank, index.cc:89-95)."""
+    base, qs, ds = big
+    print("config-size: SQ8 10,000 queries depth 100", flush=True)
+    sq = vdbg.Sq8Index(ds)
+    try:
+        gi, gd = sq.search(qs, 10, 100)
+        sel = _spread(len(qs))
+        od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale,
+                                   np.ascontiguousarray(qs[sel]), 10, 100, threads=16)
+        _eq(gi[sel], gd[sel], oi, od)
+    finally:
+        sq.close()
+
+
+def test_ivfpq_build_1m_is_vdbs_own_build(big):
+    """IvfPqIndex::build (ivf_pq.cc:102-149) at vdb's fixed 25 k-means iterations
+    (kmeans.h:14, kmeans.cc:57-174) over the 1M rows writes the file vdb's own build wrote:
+    the same list sizes, coarse centroids, codebook, list ids and codes, length and CRC32C
+    (recorded from the reference's build by tests/golden/make_golden.py ivf1m)."""
+    import hashlib
+    base, _, ds = big
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "ivf1m.npz"))
+    print("config-size: IVF-PQ build at 25 iterations", flush=True)
+    ix = vdbg.IvfPqIndex.build(ds, nlist=4096, m=16, seed=42, max_points=256, iters=25)
+    try:
+        f = ix.save()
+    finally:
+        ix.close()
+    p = parse_ivfpq(f)
+    sha = lambda a: np.frombuffer(hashlib.sha256(np.ascontiguousarray(a).tobytes()).digest(),
+                                  np.uint8)
+    sizes = np.diff(p["list_off"].astype(np.int64)).astype(np.uint32)
+    diff = np.nonzero(sizes != z["list_sizes"])[0]
+    assert diff.size == 0, f"{diff.size} lists differ in size, first list {diff[:5].tolist()}"
+    assert np.array_equal(sha(p["coarse"]), z["coarse_sha"]), "coarse centroids differ"
+    assert np.array_equal(sha(p["pq_centroids"]), z["codebook_sha"]), "codebook differs"
+    assert np.array_equal(sha(p["list_ids"]), z["ids_sha"]), "list ids differ"
+    assert np.array_equal(sha(p["list_codes"]), z["codes_sha"]), "codes differ"
+    assert len(f) == int(z["file_len"])
+    assert int.from_bytes(f[-4:], "little") == int(z["file_crc"])
+
+
+def test_filtered_collection_at_benchmark_shape(ctx, oracle):
+    """The filtered benchmark's shape at 100,000 rows per segment: 384-dim unit rows from the
+    10,000-centre mixture in 8 segments, 2 % deleted, the bucket filters at 1 / 10 / 50 %
+    and no filter, k = 10, 32 raw queries prepared on the device, each segment planned and
+    searched, merged by (dist, part, row)."""
+    import torch
+
+    dim, nseg, seg_n, nq, k = 384, 8, 100_000, 32, 10
+    dev = torch.device("cuda:0")
+    print("config-size: filtered collection 8 x 100,000 x 384", flush=True)
+    dss, segs = [], []
+    N = nseg * seg_n
+    deleted = datagen.uniform01(5004, 0, N) < np.float32(0.02)
+    bucket = datagen.rand_u64(5006, 0, N) % np.uint64(100)
+
+    def words(bits):
+        w = np.zeros((bits.size + 63) // 64 * 8, np.uint8)
+        b = np.packbits(bits, bitorder="little")
+        w[:b.size] = b
+        return w.view(np.uint64)
+
+    try:
+        for p in range(nseg):
+            rows = datagen.clustered_unit_t(torch, seg_n, dim, 5002, 5001, 10000, 1.0, dev,
+                                            start_row=p * seg_n)
+            ds = vdbg.Dataset.from_device(ctx, rows.data_ptr(), seg_n, dim, dim, "cosine")
+            ext = np.arange(p * seg_n, (p + 1) * seg_n, dtype=np.uint64)
+            ds.set_external_ids(ext)
+            dss.append(ds)
+            segs.append({"base": rows.cpu().numpy(), "ext": ext, "kind": "flat",
+                         "deleted": words(deleted[p * seg_n:(p + 1) * seg_n])})
+            del rows
+        raw = datagen.clustered_unit_t(torch, nq, dim, 5005, 5001, 10000, 1.0, dev,
+                                       unit=False).cpu().numpy()
+        for sel in (None, 1, 10, 50):
+            for p, sg in enumerate(segs):
+                sg["filter"] = None if sel is None else words(
+                    bucket[p * seg_n:(p + 1) * seg_n] < np.uint64(sel))
+            print(f"config-size: filtered collection selectivity {sel}", flush=True)
+            gi, gd, gdc, gp = vdbg.collection_search(
+                ctx, [(ds, None, sg["deleted"], sg["filter"]) for ds, sg in zip(dss, segs)],
+                dim, "cosine", raw, k)
+            oi, od, odc, op = oracle.collection_search(segs, dim, "cosine", raw, k)
+            assert gp == op
+            assert gp == (["index"] if sel is None else ["prefilter_exact"]) * nseg
+            bad = np.nonzero((gi != oi).any(1) | (gd.view(np.uint32) != od.view(np.uint32)).any(1))[0]
+            assert bad.size == 0, (sel, bad[:5])
+            assert np.array_equal(gdc, odc)
+    finally:
+        for ds in dss:
+            ds.close()
