@@ -13,6 +13,8 @@
 #include <cstdlib>
 #include <cstring>
 #include <limits>
+#include <memory>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -21,6 +23,13 @@
 namespace vdbg {
 
 // ---------------------------------------------------------------- the graph
+
+// A walk's visited set: one epoch tag per node; a query bumps the epoch instead of clearing
+// the array (cleared once when the epoch wraps).
+struct Visited {
+  std::vector<uint32_t> mark;
+  uint32_t epoch = 0;
+};
 
 struct HnswGraph {
   uint64_t cap = 0, size = 0;
@@ -36,6 +45,28 @@ struct HnswGraph {
   const uint32_t* links(uint32_t id, int layer) const {
     if (layer == 0) return links0.data() + size_t(id) * (1 + M0);
     return up.data() + up_at[id] + size_t(layer - 1) * (1 + M);
+  }
+
+  // Visited sets kept between walks (a fresh one costs a cap-sized allocation and clear,
+  // more than a whole one-query walk), as vdb's VisitedPool keeps its SearchContexts.
+  mutable std::mutex pool_mu;
+  mutable std::vector<std::unique_ptr<Visited>> pool;
+  std::unique_ptr<Visited> take() const {
+    {
+      std::lock_guard<std::mutex> g(pool_mu);
+      if (!pool.empty()) {
+        std::unique_ptr<Visited> v = std::move(pool.back());
+        pool.pop_back();
+        return v;
+      }
+    }
+    auto v = std::make_unique<Visited>();
+    v->mark.assign(cap, 0);
+    return v;
+  }
+  void give(std::unique_ptr<Visited> v) const {
+    std::lock_guard<std::mutex> g(pool_mu);
+    pool.push_back(std::move(v));
   }
 };
 
@@ -295,11 +326,14 @@ inline bool NbGreater(const Nb& a, const Nb& b) { return NbLess(b, a); }
 // Per-thread state of the walk: an epoch-tagged visited set and the two heaps.
 struct Walker {
   const HnswWalkArgs& a;
-  std::vector<uint32_t> mark;
-  uint32_t epoch = 0;
+  std::unique_ptr<Visited> vis;  // from the graph's pool, returned when the walker ends
+  std::vector<uint32_t>& mark;
+  uint32_t& epoch;
   std::vector<Nb> res, cand;
 
-  explicit Walker(const HnswWalkArgs& args) : a(args), mark(args.g->cap, 0) {}
+  explicit Walker(const HnswWalkArgs& args)
+      : a(args), vis(args.g->take()), mark(vis->mark), epoch(vis->epoch) {}
+  ~Walker() { a.g->give(std::move(vis)); }
 
   float dist(const float* q, uint32_t id) const {
     return a.dist(q, a.codes + size_t(id) * a.pd, a.vmin, a.scale, a.pd);
