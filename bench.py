@@ -99,19 +99,28 @@ def host_rate(fn, nq, reps=3):
 
 
 def timed(ctx, torch, fn, steps, warmup, kernels):
+    """Wall time of `steps` calls after `warmup`, with per-kernel profiling off (its events
+    add host work to every launch), then, when kernel times are wanted, the same number of
+    calls again with profiling on for the per-kernel event times (kernel totals over those
+    calls, so per-step figures divide by `steps` as before).  Exact re-scans are counted call
+    by call in that second pass (reading the count waits for the device, so the timed pass
+    does not read it; the calls are deterministic)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    ctx.profile(bool(kernels))  # per-kernel events only when kernel times are wanted
+    ctx.profile(False)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ctx.profile(bool(kernels))
     ctx.profile_reset()
     fallbacks = 0
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
     for _ in range(steps):
         fn()
         fallbacks += ctx.last_fallbacks()
     torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
     prof = {k: ctx.profile_get(k) for k in kernels}
     ctx.profile(False)
     return elapsed, prof, fallbacks
@@ -172,7 +181,45 @@ def run_filtered(args, ctx, torch, ref, threads, cpu_model):
         masks = [torch.from_numpy(w.view(np.int64)).to(dev) for w in words_h]
         n_allowed = int(allowed.sum())
 
+        # the batch as vdb's SearchBatch sees it, in one device call
+        # (vdbg_collection_search_device): the raw queries and the results in HBM, each
+        # segment's filter and delete words on the host (SegmentColumns::Evaluate and
+        # DeleteBits), from which the planner takes its counts; the segments' filtered scans
+        # run side by side on the call's lanes, then the merge
+        filt_h = [_words(bucket[p * seg_n:(p + 1) * seg_n] < np.uint64(sel)) for p in range(nseg)]
+        del_h = [_words(deleted[p * seg_n:(p + 1) * seg_n]) for p in range(nseg)]
+        segs = [(dss[p], None, del_h[p], filt_h[p]) for p in range(nseg)]
+        out_ext2 = torch.empty((nq, k), dtype=torch.int64, device=dev)
+        out_d2 = torch.empty((nq, k), dtype=torch.float32, device=dev)
+
         def step():
+            vdbg.collection_search_device(ctx, segs, dim, "cosine", raw.data_ptr(), nq, k,
+                                          out_ext2.data_ptr(), out_d2.data_ptr(), stream=stream)
+
+        names = ["prepare_queries", "compact", "query_prep", "sample_gemm", "kth", "flat_gemm",
+                 "select", "exact_scan", "merge", "merge_parts"]
+        el, prof, fb = timed(ctx, torch, step, args.steps, args.warmup, names)
+        g_ms = prof["flat_gemm"][0] / args.steps
+        flops = 2.0 * n_allowed * pd * nq
+        r = {"allowed_rows": n_allowed, "qps": round(nq * args.steps / el, 1),
+             "ms_per_step": round(el * 1e3 / args.steps, 3),
+             "call": "vdbg_collection_search_device (plans from host words; the segments' "
+                     "allowed rows scanned as one set up to 262,144 rows, else each segment "
+                     "on 2 threaded lanes; merge)",
+             "gemm_ms_per_step": round(g_ms, 3),
+             "gemm_TFLOPs": round(flops / (g_ms * 1e-3) / 1e12, 2) if g_ms > 0 else None,
+             "gemm_note": "GEMM time summed over the segments' launches, which overlap on the "
+                          "lanes",
+             "mfma_inputs": {8: "i8 two-part rows x two-part queries (4 int8 MFMA products each)",
+                             16: "f16 high halves of rows and queries (1 MFMA product each)"}
+                            .get(ctx.last_gemm_bits(), "f32"),
+             "kernel_ms_per_step": {kk: round(v[0] / args.steps, 4) for kk, v in prof.items()},
+             "exact_rescans": fb}
+        log(f"filtered {sel}%: {r['qps']:.0f} q/s, {n_allowed} rows allowed")
+
+        # the same batch composed from the single-segment calls: PrepareQuery, a filtered
+        # scan per segment under device words (each counts its words on the device), merge
+        def step_c():
             vdbg.prepare_queries_device(ctx, raw.data_ptr(), nq, dim, pd, "cosine",
                                         q_prep.data_ptr(), stream)
             for p in range(nseg):
@@ -183,38 +230,36 @@ def run_filtered(args, ctx, torch, ref, threads, cpu_model):
                                     ext_dev.data_ptr(), off_dev.data_ptr(), out_ext.data_ptr(),
                                     out_d.data_ptr(), stream)
 
-        names = ["prepare_queries", "compact", "query_prep", "sample_gemm", "kth", "flat_gemm",
-                 "select", "exact_scan", "merge", "merge_parts"]
-        el, prof, fb = timed(ctx, torch, step, args.steps, args.warmup, names)
-        g_ms = prof["flat_gemm"][0] / args.steps
-        flops = 2.0 * n_allowed * pd * nq
-        r = {"allowed_rows": n_allowed, "qps": round(nq * args.steps / el, 1),
-             "ms_per_step": round(el * 1e3 / args.steps, 3),
-             "gemm_ms_per_step": round(g_ms, 3),
-             "gemm_TFLOPs": round(flops / (g_ms * 1e-3) / 1e12, 2) if g_ms > 0 else None,
-             "mfma_inputs": {8: "i8 two-part rows x two-part queries (4 int8 MFMA products each)",
-                             16: "f16 high halves of rows and queries (1 MFMA product each)"}
-                            .get(ctx.last_gemm_bits(), "f32"),
-             "kernel_ms_per_step": {kk: round(v[0] / args.steps, 4) for kk, v in prof.items()},
-             "exact_rescans": fb}
-        log(f"filtered {sel}%: {r['qps']:.0f} q/s, {n_allowed} rows allowed")
-        # the same batch through the one-call C ABI (vdbg_collection_search_host): host
-        # queries in, filter and delete words per segment, the planner, host results out
-        filt_h = [_words(bucket[p * seg_n:(p + 1) * seg_n] < np.uint64(sel)) for p in range(nseg)]
-        del_h = [_words(deleted[p * seg_n:(p + 1) * seg_n]) for p in range(nseg)]
-        segs = [(dss[p], None, del_h[p], filt_h[p]) for p in range(nseg)]
+        el_c, _, fb_c = timed(ctx, torch, step_c, args.steps, 1, [])
+        r["composed_device_path"] = {
+            "qps": round(nq * args.steps / el_c, 1), "ms_per_step": round(el_c * 1e3 / args.steps, 3),
+            "exact_rescans": fb_c,
+            "equal_to_one_call": bool(
+                np.array_equal(out_ext2.cpu().numpy(), out_ext.cpu().numpy()) and
+                np.array_equal(out_d2.cpu().numpy().view(np.uint32),
+                               out_d.cpu().numpy().view(np.uint32)))}
+        log(f"filtered {sel}% composed: {r['composed_device_path']['qps']:.0f} q/s, equal "
+            f"{r['composed_device_path']['equal_to_one_call']}")
+        # the one-call C ABI with host queries in and host results out
+        # (vdbg_collection_search_host): PCIe included
         ce, cd, _, plans = vdbg.collection_search(ctx, segs, dim, "cosine", raw_h, k)
+        for _ in range(args.warmup):
+            vdbg.collection_search(ctx, segs, dim, "cosine", raw_h, k)
         torch.cuda.synchronize()
+        per_call = []
         t0 = time.perf_counter()
         for _ in range(args.steps):
+            t1 = time.perf_counter()
             vdbg.collection_search(ctx, segs, dim, "cosine", raw_h, k)
+            per_call.append(time.perf_counter() - t1)
         dt = time.perf_counter() - t0
         r["one_call_host"] = {
             "qps": round(nq * args.steps / dt, 1), "ms_per_step": round(dt * 1e3 / args.steps, 3),
+            "median_ms_per_call": round(float(np.median(per_call)) * 1e3, 3),
             "plans": sorted(set(plans)),
             "equal_to_device_path": bool(
-                np.array_equal(ce, out_ext.cpu().numpy().view(np.uint64)) and
-                np.array_equal(cd.view(np.uint32), out_d.cpu().numpy().view(np.uint32)))}
+                np.array_equal(ce, out_ext2.cpu().numpy().view(np.uint64)) and
+                np.array_equal(cd.view(np.uint32), out_d2.cpu().numpy().view(np.uint32)))}
         log(f"filtered {sel}% one call (host in/out): {r['one_call_host']['qps']:.0f} q/s, "
             f"equal {r['one_call_host']['equal_to_device_path']}")
         if want_cpu:
@@ -224,8 +269,8 @@ def run_filtered(args, ctx, torch, ref, threads, cpu_model):
                 host_rows, dim, words_h, np.arange(N, dtype=np.uint64), raw_h[:s], k,
                 threads=threads)
             dt = time.perf_counter() - t0
-            ge = out_ext[:s].cpu().numpy().view(np.uint64)
-            gd = out_d[:s].cpu().numpy()
+            ge = out_ext2[:s].cpu().numpy().view(np.uint64)
+            gd = out_d2[:s].cpu().numpy()
             r["cpu_baseline"] = {
                 "value": round(s / dt, 2), "unit": "queries/s", "cores": threads,
                 "kind": "reference", "cpu_model": cpu_model,
@@ -242,6 +287,209 @@ def run_filtered(args, ctx, torch, ref, threads, cpu_model):
     return out
 
 
+def run_hnsw_sq8(args, ctx, torch, ref, base, queries, threads, cpu_model):
+    """HnswSq8Index::search (hnsw_index.cc:82-100) on a segment of vdb's third compaction tier
+    (320,000 of the SIFT-like rows, options.h:46-48: 20,000 x 4^2) with vdb's default graph
+    (M 16, ef_construction 200, seed 42): the graph walk on the host threads, the beams'
+    float rerank in one GPU launch.  vdb builds a segment's graph on the CPU and the backend
+    reads the saved VDBHSQ81 file, so the file here is vdb's own build (HnswSq8Index::build on
+    a thread pool, through the reference's code); without it the path is skipped."""
+    import vdbg
+
+    if ref is None:
+        return {"skipped": "the VDBHSQ81 file is vdb's own CPU build (oracle/_ref not built or "
+                           "--no-cpu)"}
+    n, dim, k, ef, rr = 320_000, base.shape[1], args.k, 64, -1
+    rows = np.ascontiguousarray(base[:n])
+    t0 = time.perf_counter()
+    blob = ref.hnsw_sq8_file(rows, dim, M=16, ef_construction=200, seed=42, threads=threads)
+    build_s = time.perf_counter() - t0
+    log(f"hnsw_sq8: vdb's graph over {n} rows built on {threads} threads in {build_s:.1f} s")
+    ds = vdbg.Dataset(ctx, rows, dim)
+    sq = vdbg.Sq8Index.load(ds, blob)
+    nq = len(queries)
+    dev = torch.device("cuda:0")
+    q_dev = torch.from_numpy(np.ascontiguousarray(queries)).to(dev)
+    ids = torch.empty((nq, k), dtype=torch.int32, device=dev)
+    dd = torch.empty((nq, k), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        sq.hnsw_search_device(q_dev.data_ptr(), nq, k, ef, rr, ids.data_ptr(), dd.data_ptr(),
+                              stream=stream)
+
+    steps = max(1, min(args.steps, 5))
+    el, prof, _ = timed(ctx, torch, step, steps, 1, ["rerank"])
+    gi = ids.cpu().numpy().view(np.uint32).copy()
+    gd = dd.cpu().numpy().copy()
+    rr_ms = prof["rerank"][0] / max(1, prof["rerank"][1])
+    depth = ef  # rerank -1: depth max(ef, k) (hnsw_index.cc:88)
+    r = {"qps": nq * steps / el, "ms_per_step": el * 1e3 / steps, "rows": n, "dim": dim,
+         "k": k, "ef": ef, "rerank": rr, "M": 16, "ef_construction": 200,
+         "graph_build_s": round(build_s, 2), "walk_threads": threads,
+         "kernel": "k_rerank", "kernel_ms": rr_ms, "bound": "hbm",
+         "rerank_bytes_per_launch": nq * depth * dim * 4,
+         "achieved": nq * depth * dim * 4 / (rr_ms * 1e-3) / 1e9, "unit": "GB/s",
+         "peak": HBM_PEAK_GBS,
+         "note": "walk on the host threads (vdb's HnswGraph::search over the SQ8 codes, "
+                 "restated), the beams of the whole batch reranked in one GPU launch"}
+    log(f"hnsw_sq8: {r['qps']:.0f} q/s batched (walk on {threads} threads), rerank "
+        f"{rr_ms:.3f} ms per {nq} queries")
+    # one query per call, as vdb's Index::search sends it (host query in, host result out)
+    s1 = 400
+    sq.hnsw_search(queries[:1], k, ef, rr)
+    t0 = time.perf_counter()
+    for i in range(s1):
+        sq.hnsw_search(queries[i:i + 1], k, ef, rr)
+    per_q = (time.perf_counter() - t0) / s1
+    r["one_query_per_call"] = {"us_per_query": round(per_q * 1e6, 1),
+                               "qps_one_thread": round(1.0 / per_q, 1)}
+    s = min(nq, 4000)
+    qs = np.ascontiguousarray(queries[:s])
+    t0 = time.perf_counter()
+    od, oi, _ = ref.hnsw_sq8_search(blob, rows, dim, qs, k, ef, rr, "l2", None, threads)
+    dt = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ref.hnsw_sq8_search(blob, rows, dim, np.ascontiguousarray(queries[:s1]), k, ef, rr, "l2",
+                        None, 1)
+    dt1 = (time.perf_counter() - t0) / s1
+    r["cpu_baseline"] = {
+        "value": s / dt, "unit": "queries/s", "cores": threads, "kind": "reference",
+        "cpu_model": cpu_model,
+        "sample": f"{s} queries, HnswSq8Index::search (ef {ef}, rerank max(ef, k)) on the same "
+                  f"file, {threads} threads, {dt:.1f} s",
+        "one_thread_us_per_query": round(dt1 * 1e6, 1)}
+    r["parity_on_cpu_sample"] = bool(np.array_equal(gi[:s], oi) and
+                                     np.array_equal(gd[:s].view(np.uint32), od.view(np.uint32)))
+    log(f"hnsw_sq8: one query per call {per_q * 1e6:.1f} us (reference, one thread: "
+        f"{dt1 * 1e6:.1f} us); cpu {s / dt:.0f} q/s, parity {r['parity_on_cpu_sample']}")
+    sq.close()
+    ds.close()
+    return r
+
+
+def run_pqflat(args, ctx, torch, ref, ds, base, queries, threads, cpu_model):
+    """PqFlatIndex (ivf_pq.cc:41-98) over the 1M SIFT-like rows, built on the GPU as vdb builds
+    it (m 16, seed 42, 256 points per centroid, 25 k-means iterations): per query the ADC of
+    every code, then the float rerank of the top max(10 k, 100) (RerankDepth, :16-19)."""
+    import vdbg
+
+    N, dim = base.shape
+    k, m = args.k, 16
+    t0 = time.perf_counter()
+    pq = vdbg.PqFlatIndex.build(ds, m, seed=42, max_points=256, iters=25)
+    build_s = time.perf_counter() - t0
+    nq = min(len(queries), 2000)
+    dev = torch.device("cuda:0")
+    q_dev = torch.from_numpy(np.ascontiguousarray(queries[:nq])).to(dev)
+    ids = torch.empty((nq, k), dtype=torch.int32, device=dev)
+    dd = torch.empty((nq, k), dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        pq.search_device(q_dev.data_ptr(), nq, k, -1, ids.data_ptr(), dd.data_ptr(),
+                         stream=stream)
+
+    steps = max(1, min(args.steps, 5))
+    el, prof, _ = timed(ctx, torch, step, steps, 1, ["pq_tables", "exact_scan", "merge",
+                                                     "rerank"])
+    gi = ids.cpu().numpy().view(np.uint32).copy()
+    gd = dd.cpu().numpy().copy()
+    sc_ms = prof["exact_scan"][0] / max(1, prof["exact_scan"][1])
+    code_bytes = nq * N * m
+    r = {"qps": nq * steps / el, "ms_per_step": el * 1e3 / steps, "batch": nq, "m": m,
+         "build_s": round(build_s, 2), "kernel": "k_exact_scan over PQ codes (ADC, wave top-k per row split)",
+         "kernel_ms": sc_ms, "bound": "hbm", "algorithmic_bytes_per_launch": code_bytes,
+         "achieved": code_bytes / (sc_ms * 1e-3) / 1e9 if sc_ms > 0 else None, "unit": "GB/s",
+         "peak": HBM_PEAK_GBS,
+         "kernel_ms_per_step": {kk: v[0] / steps for kk, v in prof.items()},
+         "note": "the 16 MB of codes stay in L2 / MALL across queries: 'achieved' counts the "
+                 "codes each query reads (n m bytes), not HBM traffic"}
+    log(f"pqflat: {r['qps']:.0f} q/s, scan {sc_ms:.3f} ms per {nq} queries")
+    if ref is not None:
+        blob = pq.save()
+        s = 500
+        qs = np.ascontiguousarray(queries[:s])
+        t0 = time.perf_counter()
+        od, oi, _ = ref.pqflat_search(blob, base, dim, qs, k, -1, "l2", None, threads)
+        dt = time.perf_counter() - t0
+        r["cpu_baseline"] = {
+            "value": s / dt, "unit": "queries/s", "cores": threads, "kind": "reference",
+            "cpu_model": cpu_model,
+            "sample": f"{s} queries, PqFlatIndex::search (rerank max(10 k, 100)) on the same "
+                      f"VDBPQFL1 file, {threads} threads, {dt:.1f} s"}
+        r["parity_on_cpu_sample"] = bool(np.array_equal(gi[:s], oi) and
+                                         np.array_equal(gd[:s].view(np.uint32), od.view(np.uint32)))
+        log(f"pqflat cpu: {s / dt:.1f} q/s, parity {r['parity_on_cpu_sample']}")
+    pq.close()
+    return r
+
+
+def run_append(args, ctx, torch, base):
+    """MutableSegment::Append (mutable_segment.cc:24-44) on an appendable dataset: single rows
+    (vdb appends one row per upsert) and 100-row calls, alone and while another context
+    searches on another thread (batches of 64 queries over 100,000 rows)."""
+    import threading
+
+    import vdbg
+
+    dim = base.shape[1]
+
+    def appends(rows_per_call, calls):
+        ap = vdbg.Dataset.appendable(ctx, dim, "l2", capacity=1 << 20)
+        ext = np.arange(rows_per_call * calls, dtype=np.uint64)
+        t0 = time.perf_counter()
+        for c in range(calls):
+            a = c * rows_per_call
+            ap.append(base[a:a + rows_per_call], ext[a:a + rows_per_call])
+        dt = time.perf_counter() - t0
+        ap.close()
+        return {"calls": calls, "rows_per_call": rows_per_call,
+                "us_per_call": round(dt / calls * 1e6, 1),
+                "rows_per_s": round(rows_per_call * calls / dt, 1)}
+
+    r = {"alone": {"one_row": appends(1, 2000), "hundred_rows": appends(100, 300)}}
+    ctx2 = vdbg.Context(0)
+    ds2 = vdbg.Dataset(ctx2, np.ascontiguousarray(base[:100_000]), dim)
+    q = np.ascontiguousarray(base[200_000:200_064])
+    stop = threading.Event()
+    done = [0]
+
+    def searcher():
+        while not stop.is_set():
+            ds2.flat_search(q, 10)
+            done[0] += 1
+
+    th = threading.Thread(target=searcher)
+    th.start()
+    time.sleep(0.2)
+    try:
+        t0 = time.perf_counter()
+        n0 = done[0]
+        one = appends(1, 2000)
+        hundred = appends(100, 300)
+        dt = time.perf_counter() - t0
+        r["with_search_on_another_context"] = {
+            "one_row": one, "hundred_rows": hundred,
+            "searches_per_s": round((done[0] - n0) / dt, 1)}
+    finally:
+        stop.set()
+        th.join()
+    t0 = time.perf_counter()
+    for _ in range(200):
+        ds2.flat_search(q, 10)
+    r["searches_per_s_alone"] = round(200 / (time.perf_counter() - t0), 1)
+    ds2.close()
+    ctx2.close()
+    log(f"append: one row {r['alone']['one_row']['us_per_call']} us, 100 rows "
+        f"{r['alone']['hundred_rows']['us_per_call']} us per call; beside a search: "
+        f"{r['with_search_on_another_context']['one_row']['us_per_call']} / "
+        f"{r['with_search_on_another_context']['hundred_rows']['us_per_call']} us, searches "
+        f"{r['with_search_on_another_context']['searches_per_s']} /s (alone "
+        f"{r['searches_per_s_alone']} /s)")
+    return r
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -250,7 +498,8 @@ def main():
     ap.add_argument("--n", type=int, default=1_000_000)
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--k", type=int, default=10)
-    ap.add_argument("--paths", default="flat,flat_uniform,sq8,ivfpq,filtered")
+    ap.add_argument("--paths", default="flat,flat_uniform,sq8,ivfpq,filtered,hnsw_sq8,pqflat,"
+                                        "append")
     ap.add_argument("--nprobe", type=int, default=64)
     ap.add_argument("--cpu-sample", type=int, default=6400,
                     help="queries in the flat CPU-baseline sample (SQ8 uses half, IVF-PQ all)")
@@ -668,6 +917,16 @@ def main():
     # ------------------------------------------------------------ filtered collection
     if "filtered" in paths:
         results["filtered"] = run_filtered(args, ctx, torch, ref, threads, cpu_model)
+
+    # ------------------------------------------------------------ the next rows
+    if "hnsw_sq8" in paths:
+        results["hnsw_sq8"] = run_hnsw_sq8(args, ctx, torch, ref, base, queries, threads,
+                                           cpu_model)
+    if "pqflat" in paths:
+        results["pqflat"] = run_pqflat(args, ctx, torch, ref, ds, base, queries, threads,
+                                       cpu_model)
+    if "append" in paths:
+        results["append"] = run_append(args, ctx, torch, base)
 
     if N == 1_000_000 and nq == 10_000 and k == 10:
         for name in ("flat", "sq8", "ivfpq"):

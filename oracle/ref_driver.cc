@@ -234,6 +234,28 @@ int ref_hnsw_search_batch(int metric, const char* file, size_t file_len, const f
   return 0;
 }
 
+// ref_hnsw_sq8_file with the build on a thread pool of nthreads (HnswSq8Index::build(pool),
+// as vdb builds a segment's graph): the graph depends on the threads' interleaving, so two
+// builds may differ; the file is what the segment would hold.
+size_t ref_hnsw_sq8_file_mt(int metric, const float* base, size_t rows, size_t dim, size_t pd,
+                            size_t M, size_t ef_construction, uint64_t seed, int nthreads,
+                            const char** file) {
+  VectorView v{base, rows, dim, pd};
+  IndexOptions o;
+  o.type = IndexType::HnswSq8;
+  o.M = M;
+  o.ef_construction = ef_construction;
+  o.seed = seed;
+  HnswSq8Index idx(o, static_cast<Metric>(metric), v);
+  ThreadPool pool(nthreads <= 0 ? 1 : static_cast<size_t>(nthreads));
+  if (!idx.build(&pool).ok()) return 0;
+  StringSink sink;
+  if (!idx.save(sink).ok()) return 0;
+  g_last_file = std::move(sink.s);
+  *file = g_last_file.data();
+  return g_last_file.size();
+}
+
 // LoadIndex of a VDBHSQ81 file (index.cc:38-87) and HnswSq8Index::search
 // (src/index/hnsw/hnsw_index.cc:82-100) per query: graph beam over the codes with the
 // reference's own kernel set, then Rerank.  allow_words (nullable) is the RowFilter (bit r of

@@ -402,6 +402,8 @@ class Reference:
         _sig(lib, "ref_hnsw_sq8_search_batch", C.c_int,
              [C.c_int, C.c_char_p, sz, f32p, sz, sz, sz, f32p, sz, sz, sz, C.c_int, _opt(u64p),
               f32p, u32p, _opt(u64p), C.c_int])
+        _sig(lib, "ref_hnsw_sq8_file_mt", sz,
+             [C.c_int, f32p, sz, sz, sz, sz, sz, C.c_uint64, C.c_int, C.c_void_p])
         _sig(lib, "ref_hnsw_file", sz,
              [C.c_int, f32p, sz, sz, sz, sz, sz, C.c_uint64, C.c_void_p, sz])
         _sig(lib, "ref_hnsw_search_batch", C.c_int,
@@ -461,6 +463,18 @@ class Reference:
         if rc != 0:
             raise ValueError("LoadIndex refused the file")
         return od, oi, dc
+
+    def hnsw_sq8_file(self, base, dim, M=16, ef_construction=200, seed=42, metric="l2",
+                      threads=8):
+        """HnswSq8Index::build on a pool of threads + save: the VDBHSQ81 file bytes."""
+        base = np.ascontiguousarray(base, np.float32)
+        n, pd = base.shape
+        p = C.c_void_p()
+        size = self.lib.ref_hnsw_sq8_file_mt(METRIC[metric], base, n, dim, pd, M,
+                                             ef_construction, seed, threads, C.byref(p))
+        if size == 0:
+            raise RuntimeError("HnswSq8Index::build failed")
+        return C.string_at(p.value, size)
 
     def hnsw_file(self, base, dim, M=16, ef_construction=100, seed=42, metric="l2"):
         """HnswIndex::build (single-threaded) + save: the VDBHNSW1 file bytes."""
