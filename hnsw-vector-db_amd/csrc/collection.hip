@@ -13,6 +13,7 @@
 #include <cmath>
 #include <cstring>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "vdbg_device.h"
@@ -48,7 +49,25 @@ struct SegPlan {
   std::vector<uint64_t> allow;  // host words handed to the device search; empty = none
   size_t matches = 0;
   size_t nprobe = 0;
+  int64_t allowed = -1;         // rows the words allow, when the scan may take it as known
 };
+
+// Lanes of the collection search: flat scans of different segments run side by side, each
+// on its own stream with its own scratch (a segment's scan alone is too small to fill the
+// GPU, and lanes keep the host from waiting on one before queuing the next).
+int EnsureLanes(Ctx* c, int n) {
+  while (int(c->lanes.size()) < n) {
+    auto* l = new (std::nothrow) ScanScratch;
+    if (l == nullptr) return SetError(kResourceExhausted, "out of host memory");
+    if (hipStreamCreateWithFlags(&l->stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&l->done, hipEventDisableTiming) != hipSuccess) {
+      delete l;
+      return SetError(kInternal, "collection search lane");
+    }
+    c->lanes.push_back(l);
+  }
+  return kOk;
+}
 
 }  // namespace
 }  // namespace vdbg
@@ -66,14 +85,133 @@ int vdbg_dataset_set_external_ids(vdbg_dataset* ds, const uint64_t* ids) {
   if (d.n == 0) return kOk;
   if (d.ext_ids == nullptr) VDBG_HIP(hipMalloc(reinterpret_cast<void**>(&d.ext_ids), d.n * 8));
   VDBG_HIP(hipMemcpyAsync(d.ext_ids, ids, d.n * 8, hipMemcpyHostToDevice, c->stream));
+  // whether every row has its own external id (the combined scan of the collection search
+  // relies on it; vdb's segments hold each id once)
+  std::vector<uint64_t> sorted(ids, ids + d.n);
+  std::sort(sorted.begin(), sorted.end());
+  d.ext_unique = std::adjacent_find(sorted.begin(), sorted.end()) == sorted.end();
   VDBG_HIP(hipStreamSynchronize(c->stream));
   return kOk;
 }
 
-int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
-                                size_t dim, int metric, const float* queries, size_t nq,
-                                size_t k, const vdbg_search_params* params, uint64_t* out_ids,
-                                float* out_dists, uint64_t* dist_comps, int* seg_plans) {
+}  // extern "C"
+
+namespace {
+
+// Largest number of allowed rows, over all segments, scanned as one combined source (past it,
+// gathering the rows costs more than the separate scans' fixed costs: measured at 8 x 625,000
+// x 384, 49k rows 1.09 ms combined against 1.50 on lanes, 490k rows 4.28 against 3.66).
+constexpr size_t kCombinedMaxRows = size_t(1) << 18;
+
+// A collection of flat segments whose allowed rows are few in all, scanned as one source:
+// every segment's allowed rows (ascending, segment by segment) gathered into one row set with
+// their external ids, one scan for the top k x nseg of that set by (dist, index), then the
+// merge keeping the first hit of each external id, k of them.  The index order is the
+// (part, row) order, so the order is vdb's merge order.  With every external id held once
+// inside its segment, the first k distinct ids of all rows in that order are the first k of
+// vdb's merge of per-segment top-k lists (a hit in the answer has fewer than k hits of its
+// own segment before it: each is either in the answer or repeats an answer id held by another
+// segment), and every one of them is among the first k x nseg rows of the order (at most
+// nseg rows carry each answer id).
+int CombinedScan(Ctx* c, const vdbg_segment* segs, size_t nseg, const std::vector<int64_t>& rows,
+                 const std::vector<const uint64_t*>& allow, const float* q, size_t nq,
+                 size_t k, uint64_t* out_ext, float* out_d, hipStream_t s) {
+  const Dataset& d0 = segs[0].rows->d;
+  const ScanSource& s0 = d0.src;
+  const size_t pd = d0.pd;
+  const size_t kk = k * nseg;
+  size_t total = 0;
+  for (int64_t r : rows) total += size_t(r);
+  ScanSource cs;
+  cs.kind = 0;
+  cs.N = uint32_t(total);
+  cs.pd = int(pd);
+  cs.metric = s0.metric;
+  cs.x16_parts = s0.x16_parts;
+  cs.x16_exp = s0.x16_exp;
+  cs.x16_approx = s0.x16_approx;
+  cs.X16 = s0.X16;  // (non-null while the sample is sized: the sample keeps an fp16 part)
+  cs.stats = s0.stats;
+  cs.rmag = s0.rmag;
+  for (size_t p = 1; p < nseg; ++p) {
+    const ScanSource& sp = segs[p].rows->d.src;
+    cs.stats.lo = std::min(cs.stats.lo, sp.stats.lo);
+    cs.stats.hi = std::max(cs.stats.hi, sp.stats.hi);
+    cs.stats.max_abs = std::max(cs.stats.max_abs, sp.stats.max_abs);
+    cs.stats.xn_max = std::max(cs.stats.xn_max, sp.stats.xn_max);
+    cs.stats.all_int &= sp.stats.all_int;
+    cs.rmag = std::max(cs.rmag, sp.rmag);
+  }
+  const size_t row16 = s0.X16 != nullptr ? pd * size_t(s0.x16_parts) * 2 : 0;
+  const size_t sample_bytes = SampleBytes(cs, SampleRows(uint32_t(total)));
+  Workspace& w = c->wcomb;
+  if (c->wcomb_done != nullptr) VDBG_HIP(hipStreamWaitEvent(s, c->wcomb_done, 0));
+  w.used = 0;
+  const size_t bytes = total * (4 + 8 + pd * 4 + row16 + 4) + sample_bytes +
+                       nq * kk * 8 + 12 * 256;
+  VDBG_RETURN_IF_ERROR(w.reserve(bytes));
+  uint32_t* ids = w.take<uint32_t>(total);
+  uint64_t* ext = w.take<uint64_t>(total);
+  float* X = w.take<float>(total * pd);
+  uint16_t* X16 = row16 != 0 ? reinterpret_cast<uint16_t*>(w.take<char>(total * row16)) : nullptr;
+  float* rn = w.take<float>(total);
+  void* sample = w.take<char>(sample_bytes);
+  uint32_t* cids = w.take<uint32_t>(nq * kk);
+  float* cd = w.take<float>(nq * kk);
+  {
+    ProfScope ps(c, "compact", s);
+    size_t at = 0;
+    for (size_t p = 0; p < nseg; ++p) {
+      const Dataset& d = segs[p].rows->d;
+      const uint32_t n = uint32_t(rows[p]);
+      if (n == 0) continue;
+      if (allow[p] != nullptr)
+        VDBG_RETURN_IF_ERROR(CompactIdsSmall(allow[p], uint32_t(d.n), n, ids + at, s));
+      GatherParts g{};
+      g.a = reinterpret_cast<const uint4*>(d.src.X);
+      g.ao = reinterpret_cast<uint4*>(X + at * pd);
+      g.wa = uint32_t(pd * 4 / 16);
+      if (row16 != 0) {
+        g.b = reinterpret_cast<const uint4*>(d.src.X16);
+        g.bo = reinterpret_cast<uint4*>(reinterpret_cast<char*>(X16) + at * row16);
+        g.wb = uint32_t(row16 / 16);
+      }
+      g.rn = d.src.rn;
+      g.rno = rn + at;
+      g.ext = d.ext_ids;
+      g.exto = ext + at;
+      g.ids = allow[p] != nullptr ? ids + at : nullptr;
+      g.n = n;
+      VDBG_RETURN_IF_ERROR(GatherRows(g, s));
+      at += n;
+    }
+  }
+  cs.X = X;
+  cs.X16 = X16;
+  cs.rn = rn;
+  cs.Sbuf = nullptr;
+  VDBG_RETURN_IF_ERROR(GatherSample(c, &cs, s, sample));
+  int rc = RunScan(c, &cs, q, nq, kk, nullptr, cids, cd, s);
+  if (rc == kOk) {
+    MergeArgs a{int(nq), 1, int(kk), cd, cids, ext, nullptr, out_ext, out_d};
+    a.kout = int(k);
+    rc = MergeParts(c, a, s);
+  }
+  if (c->wcomb_done == nullptr &&
+      hipEventCreateWithFlags(&c->wcomb_done, hipEventDisableTiming) != hipSuccess)
+    c->wcomb_done = nullptr;
+  if (c->wcomb_done == nullptr || hipEventRecord(c->wcomb_done, s) != hipSuccess)
+    (void)hipStreamSynchronize(s);  // no event: drain before the rows are reused
+  FreeSample(&cs);  // (the sample lives in the workspace: nothing is freed)
+  return rc;
+}
+
+// The collection search of vdbg_collection_search_host (queries and results in host memory)
+// and vdbg_collection_search_device (in device memory, on `stream`).
+int CollectionSearch(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg, size_t dim,
+                     int metric, const float* queries, size_t nq, size_t k,
+                     const vdbg_search_params* params, uint64_t* out_ids, float* out_dists,
+                     uint64_t* dist_comps, int* seg_plans, bool device_io, void* stream) {
   if (ctx == nullptr || params == nullptr || (nseg > 0 && segs == nullptr) ||
       (nq > 0 && (queries == nullptr || out_ids == nullptr || out_dists == nullptr)))
     return SetError(kInvalidArgument, "null argument");
@@ -127,7 +265,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
   }
   std::lock_guard<std::recursive_mutex> lk(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
-  hipStream_t s = c->stream;
+  hipStream_t s = device_io && stream != nullptr ? static_cast<hipStream_t>(stream) : c->stream;
   if (dist_comps != nullptr) std::fill(dist_comps, dist_comps + nq, uint64_t(0));
 
   // ---- the plan of every segment (SearchDiskSegment, planner.cc:53-128)
@@ -160,6 +298,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
       } else {
         sp.matches = rows;
       }
+      sp.allowed = int64_t(sp.matches);
       allow_words_total += sp.allow.size();
       continue;
     }
@@ -168,6 +307,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
       if (deleted > 0) {
         sp.allow.resize(nw);
         for (size_t i = 0; i < nw; ++i) sp.allow[i] = ~g.deleted_words[i];
+        sp.allowed = int64_t(live);
       }
     } else {
       sp.allow.assign(g.filter_words, g.filter_words + nw);  // Evaluate, minus deletes (:64-65)
@@ -175,6 +315,7 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
         for (size_t i = 0; i < nw; ++i) sp.allow[i] &= ~g.deleted_words[i];
       if (rows % 64 && nw > 0) sp.allow[nw - 1] &= (uint64_t(1) << (rows % 64)) - 1;
       sp.matches = CountRows(sp.allow.data(), rows);
+      sp.allowed = int64_t(sp.matches);
       const double sel = live == 0 ? 0.0 : double(sp.matches) / double(live);
       int strat = P.strategy;
       const bool flat = g.sq8 == nullptr && g.ivfpq == nullptr && g.pqflat == nullptr;
@@ -209,10 +350,14 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
 
   // ---- PrepareQuery for the batch (collection_impl.cc:1023-1034)
   DevBuf raw, Q, hits_d, hits_r, allow_dev, dcb, extp, oe, od;
-  VDBG_RETURN_IF_ERROR(Alloc(&raw, nq * dim * 4, s));
+  const float* raw_q = queries;
+  if (!device_io) {
+    VDBG_RETURN_IF_ERROR(Alloc(&raw, nq * dim * 4, s));
+    VDBG_HIP(hipMemcpyAsync(raw.p, queries, nq * dim * 4, hipMemcpyHostToDevice, s));
+    raw_q = static_cast<const float*>(raw.p);
+  }
   VDBG_RETURN_IF_ERROR(Alloc(&Q, nq * pd * 4, s));
-  VDBG_HIP(hipMemcpyAsync(raw.p, queries, nq * dim * 4, hipMemcpyHostToDevice, s));
-  VDBG_RETURN_IF_ERROR(PrepareQueries(c, static_cast<float*>(raw.p), nq, dim, pd, metric,
+  VDBG_RETURN_IF_ERROR(PrepareQueries(c, raw_q, nq, dim, pd, metric,
                                       static_cast<float*>(Q.p), s));
   const float* q = static_cast<const float*>(Q.p);
 
@@ -285,6 +430,95 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     return kOk;
   };
 
+  // flat scans (in-memory parts, flat segments under their index plan, the exact scan of a
+  // prefilter plan) go to the lanes; every other plan runs on s in turn
+  auto on_lane = [&](size_t p) {
+    const int pl = plan[p].plan;
+    const vdbg_segment& g = segs[p];
+    return pl == VDBG_PLAN_SCAN || pl == VDBG_PLAN_SCAN_FILTER || pl == VDBG_PLAN_PREFILTER_EXACT ||
+           (pl == VDBG_PLAN_INDEX && g.sq8 == nullptr && g.ivfpq == nullptr && g.pqflat == nullptr);
+  };
+
+  // ---- every segment a flat scan and few allowed rows in all: one combined scan
+  {
+    bool ok = c->combine_segments && nseg >= 2 && nq >= 3 && k * nseg <= 240;
+    std::vector<int64_t> rows(nseg, 0);
+    std::vector<const uint64_t*> allow_p(nseg, nullptr);
+    size_t total = 0;
+    const ScanSource* s0 = nseg > 0 && segs[0].host_rows == nullptr ? &segs[0].rows->d.src : nullptr;
+    for (size_t p = 0; p < nseg && ok; ++p) {
+      const vdbg_segment& g = segs[p];
+      ok = g.host_rows == nullptr && on_lane(p);
+      if (!ok) break;
+      const Dataset& d = g.rows->d;
+      const ScanSource& sp = d.src;
+      ok = d.ext_unique && sp.kind == 0 && sp.Xmap == nullptr && s0 != nullptr &&
+           (sp.X16 == nullptr) == (s0->X16 == nullptr) && sp.x16_parts == s0->x16_parts &&
+           sp.x16_exp == s0->x16_exp && sp.x16_approx == s0->x16_approx;
+      if (!ok) break;
+      const SegPlan& pl = plan[p];
+      if (pl.allow.empty()) {
+        rows[p] = int64_t(d.n);
+      } else {
+        rows[p] = pl.allowed;
+        allow_p[p] = static_cast<const uint64_t*>(allow_dev.p) + allow_at[p];
+        ok = pl.allowed >= 0 && uint64_t(pl.allowed) <= kCompactBlockIds &&
+             (d.n + 63) / 64 <= size_t(kCompactBlockWords);
+      }
+      total += size_t(std::max<int64_t>(rows[p], 0));
+    }
+    if (ok && total >= 1 && total <= kCombinedMaxRows) {
+      for (size_t p = 0; p < nseg; ++p) {
+        if (dist_comps != nullptr) {
+          const size_t n = plan[p].plan == VDBG_PLAN_INDEX ? segs[p].rows->d.n : plan[p].matches;
+          for (size_t i = 0; i < nq; ++i) dist_comps[i] += n;  // flat_index.cc:75-76
+        }
+      }
+      uint64_t* merge_ext = device_io ? out_ids : nullptr;
+      float* merge_d = device_io ? out_dists : nullptr;
+      if (!device_io) {
+        VDBG_RETURN_IF_ERROR(Alloc(&oe, slice * 8, s));
+        VDBG_RETURN_IF_ERROR(Alloc(&od, slice * 4, s));
+        merge_ext = static_cast<uint64_t*>(oe.p);
+        merge_d = static_cast<float*>(od.p);
+      }
+      VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
+      VDBG_RETURN_IF_ERROR(CombinedScan(c, segs, nseg, rows, allow_p, q, nq, k, merge_ext,
+                                        merge_d, s));
+      if (!device_io) {
+        VDBG_HIP(hipMemcpyAsync(out_ids, oe.p, slice * 8, hipMemcpyDeviceToHost, s));
+        VDBG_HIP(hipMemcpyAsync(out_dists, od.p, slice * 4, hipMemcpyDeviceToHost, s));
+      }
+      VDBG_HIP(hipStreamSynchronize(s));
+      if (seg_plans != nullptr)
+        for (size_t p = 0; p < nseg; ++p) seg_plans[p] = plan[p].plan;
+      return kOk;
+    }
+  }
+  size_t nlane_segs = 0;
+  for (size_t p = 0; p < nseg; ++p) nlane_segs += on_lane(p) ? 1 : 0;
+  const int nlanes = nlane_segs >= 2 && c->collection_lanes > 1
+                         ? int(std::min<size_t>(size_t(c->collection_lanes), nlane_segs))
+                         : 0;
+  hipEvent_t fork = nullptr;
+  if (nlanes > 0) {
+    VDBG_RETURN_IF_ERROR(EnsureLanes(c, nlanes));
+    VDBG_HIP(hipEventCreateWithFlags(&fork, hipEventDisableTiming));
+    VDBG_HIP(hipEventRecord(fork, s));  // the prepared queries and the allow words
+    for (int l = 0; l < nlanes; ++l) VDBG_HIP(hipStreamWaitEvent(c->lanes[l]->stream, fork, 0));
+  }
+  // the scans' fallback counts add up over the call's segments
+  VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
+  struct Accumulate {
+    Ctx* c;
+    ~Accumulate() { c->fb_accumulate = false; }
+  } acc{c};
+  c->fb_accumulate = true;
+  // each lane's segments, issued by the lane's own host thread (lane 0: this thread) when the
+  // context runs lanes threaded: one thread alone spends more time issuing a segment's
+  // launches than the GPU spends running them
+  std::vector<std::vector<size_t>> lane_jobs(size_t(std::max(nlanes, 1)));
+  int next_lane = 0;
   std::vector<uint32_t> hr, xr;
   std::vector<float> hd, xd;
   // host-searched segments: each hit's external id, resident for the merge, which reads it
@@ -296,6 +530,15 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     uint32_t* ids = static_cast<uint32_t*>(hits_r.p) + p * slice;
     float* dd = static_cast<float*>(hits_d.p) + p * slice;
     const uint64_t* allow = sp.allow.empty() ? nullptr : static_cast<const uint64_t*>(allow_dev.p) + allow_at[p];
+    if (nlanes > 0 && on_lane(p)) {
+      lane_jobs[size_t(next_lane)].push_back(p);
+      next_lane = (next_lane + 1) % nlanes;
+      if (dist_comps != nullptr) {
+        const size_t n = sp.plan == VDBG_PLAN_INDEX ? segs[p].rows->d.n : sp.matches;  // flat_index.cc:75-76
+        for (size_t i = 0; i < nq; ++i) dist_comps[i] += n;
+      }
+      continue;
+    }
     switch (sp.plan) {
       case VDBG_PLAN_SCAN:
       case VDBG_PLAN_SCAN_FILTER:
@@ -411,30 +654,109 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
     }
   }
 
+  if (nlanes > 0) {
+    // the lanes' flat scans: ScanMasked with the count of allowed rows the host words give
+    auto run_lane = [&](int l) -> int {
+      ScanScratch* lane = c->lanes[size_t(l)];
+      for (size_t p : lane_jobs[size_t(l)]) {
+        const SegPlan& sp = plan[p];
+        const uint64_t* allow =
+            sp.allow.empty() ? nullptr : static_cast<const uint64_t*>(allow_dev.p) + allow_at[p];
+        VDBG_RETURN_IF_ERROR(ScanMasked(c, &segs[p].rows->d.src, q, nq, k, allow,
+                                        static_cast<uint32_t*>(hits_r.p) + p * slice,
+                                        static_cast<float*>(hits_d.p) + p * slice, lane->stream,
+                                        allow != nullptr ? sp.allowed : -1, lane));
+      }
+      return kOk;
+    };
+    int rc = kOk;
+    if (c->lane_threads && nlanes > 1) {
+      std::vector<int> rcs(size_t(nlanes), kOk);
+      std::vector<std::string> errs{size_t(nlanes), std::string()};
+      std::vector<std::thread> th;
+      th.reserve(size_t(nlanes - 1));
+      for (int l = 1; l < nlanes; ++l)
+        th.emplace_back([&, l]() {
+          if (hipSetDevice(c->device) != hipSuccess) {
+            rcs[size_t(l)] = kInternal;
+            errs[size_t(l)] = "lane thread: hipSetDevice";
+            return;
+          }
+          rcs[size_t(l)] = run_lane(l);
+          if (rcs[size_t(l)] != kOk) errs[size_t(l)] = vdbg_last_error();
+        });
+      rcs[0] = run_lane(0);
+      if (rcs[0] != kOk) errs[0] = vdbg_last_error();
+      for (auto& t : th) t.join();
+      for (int l = 0; l < nlanes && rc == kOk; ++l)
+        if (rcs[size_t(l)] != kOk) rc = SetError(rcs[size_t(l)], errs[size_t(l)]);
+    } else {
+      for (int l = 0; l < nlanes && rc == kOk; ++l) rc = run_lane(l);
+    }
+    // the merge waits for every lane (also after an error: nothing may still be queued on a
+    // lane when this call's buffers are released)
+    for (int l = 0; l < nlanes; ++l) {
+      VDBG_HIP(hipEventRecord(c->lanes[l]->done, c->lanes[l]->stream));
+      VDBG_HIP(hipStreamWaitEvent(s, c->lanes[l]->done, 0));
+    }
+    (void)hipEventDestroy(fork);
+    if (rc != kOk) {
+      (void)hipStreamSynchronize(s);
+      return rc;
+    }
+  }
+
   // ---- the merge (collection_impl.cc:1076-1112) and the copy back
   std::vector<const uint64_t*> ext(np, nullptr);
   for (size_t p = 0; p < nseg; ++p)
     ext[p] = plan[p].plan == VDBG_PLAN_HOST ? static_cast<const uint64_t*>(host_ext[p].p)
                                             : segs[p].rows->d.ext_ids;
   VDBG_RETURN_IF_ERROR(Alloc(&extp, np * sizeof(void*), s));
-  VDBG_RETURN_IF_ERROR(Alloc(&oe, slice * 8, s));
-  VDBG_RETURN_IF_ERROR(Alloc(&od, slice * 4, s));
+  if (!device_io) {
+    VDBG_RETURN_IF_ERROR(Alloc(&oe, slice * 8, s));
+    VDBG_RETURN_IF_ERROR(Alloc(&od, slice * 4, s));
+  }
+  uint64_t* merge_ext = device_io ? out_ids : static_cast<uint64_t*>(oe.p);
+  float* merge_d = device_io ? out_dists : static_cast<float*>(od.p);
   VDBG_HIP(hipMemcpyAsync(extp.p, ext.data(), np * sizeof(void*), hipMemcpyHostToDevice, s));
   if (nseg == 0) {
     VDBG_HIP(hipMemsetAsync(hits_r.p, 0xff, slice * 4, s));
     VDBG_HIP(hipMemsetAsync(hits_d.p, 0, slice * 4, s));
   }
   MergeArgs a{int(nq), int(np), int(k), static_cast<const float*>(hits_d.p),
-              static_cast<const uint32_t*>(hits_r.p), nullptr, nullptr,
-              static_cast<uint64_t*>(oe.p), static_cast<float*>(od.p)};
+              static_cast<const uint32_t*>(hits_r.p), nullptr, nullptr, merge_ext, merge_d};
   a.ext_parts = static_cast<const uint64_t* const*>(extp.p);
   VDBG_RETURN_IF_ERROR(MergeParts(c, a, s));
-  VDBG_HIP(hipMemcpyAsync(out_ids, oe.p, slice * 8, hipMemcpyDeviceToHost, s));
-  VDBG_HIP(hipMemcpyAsync(out_dists, od.p, slice * 4, hipMemcpyDeviceToHost, s));
+  if (!device_io) {
+    VDBG_HIP(hipMemcpyAsync(out_ids, oe.p, slice * 8, hipMemcpyDeviceToHost, s));
+    VDBG_HIP(hipMemcpyAsync(out_dists, od.p, slice * 4, hipMemcpyDeviceToHost, s));
+  }
+  // (the host arrays handed to asynchronous copies above live until here)
   VDBG_HIP(hipStreamSynchronize(s));
   if (seg_plans != nullptr)
     for (size_t p = 0; p < nseg; ++p) seg_plans[p] = plan[p].plan;
   return kOk;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
+                                size_t dim, int metric, const float* queries, size_t nq,
+                                size_t k, const vdbg_search_params* params, uint64_t* out_ids,
+                                float* out_dists, uint64_t* dist_comps, int* seg_plans) {
+  return CollectionSearch(ctx, segs, nseg, dim, metric, queries, nq, k, params, out_ids,
+                          out_dists, dist_comps, seg_plans, false, nullptr);
+}
+
+int vdbg_collection_search_device(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
+                                  size_t dim, int metric, const float* queries, size_t nq,
+                                  size_t k, const vdbg_search_params* params,
+                                  uint64_t* out_ids, float* out_dists, uint64_t* dist_comps,
+                                  int* seg_plans, void* stream) {
+  return CollectionSearch(ctx, segs, nseg, dim, metric, queries, nq, k, params, out_ids,
+                          out_dists, dist_comps, seg_plans, true, stream);
 }
 
 }  // extern "C"

@@ -1193,6 +1193,10 @@ struct SelectArgs {
   float* out_d;
   uint32_t* fb_list;       // rescore mode: queries that need the exact re-scan
   uint32_t* fb_count;
+  const uint32_t* nslots_dev;  // nullable: slots at or past *nslots_dev exit (a pass queued
+                               // for every slot whose count an earlier kernel decides)
+  uint32_t* fb_acc;            // nullable: *nslots_dev is added here once (the context's count
+                               // of exact re-scans queued without a host read)
 };
 
 constexpr int kMaxSeg = 1024;
@@ -1220,7 +1224,9 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   const int lane = lane_id();
   const int slot = WPS == 1 ? blockIdx.x * 4 + wave : blockIdx.x;
   const int sub = WPS == 1 ? 0 : wave;  // the wave's share of the slot's segments
+  if (a.fb_acc != nullptr && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(a.fb_acc, *a.nslots_dev);
   if (slot >= a.nslots) return;
+  if (a.nslots_dev != nullptr && uint32_t(slot) >= *a.nslots_dev) return;
   const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
   const uint32_t src = a.by_query ? q : uint32_t(slot);
   uint32_t* pre = pre_all[wave];
@@ -1479,6 +1485,7 @@ struct ScanArgs {
   int nsplit;
   uint2* part;            // [slot][split][64*E]
   uint32_t* part_counts;  // [slot][split]
+  const uint32_t* nslots_dev;  // nullable: slots at or past *nslots_dev exit
 };
 
 // Block = 4 waves on one (query, row split); each wave keeps a top-64E of its rows with
@@ -1489,6 +1496,7 @@ __global__ __launch_bounds__(256) void k_exact_scan(ScanArgs a, Scorer sc) {
   __shared__ float md[3][N];
   __shared__ uint32_t mi[3][N];
   const int slot = blockIdx.x, split = blockIdx.y;
+  if (a.nslots_dev != nullptr && uint32_t(slot) >= *a.nslots_dev) return;  // block-uniform
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
   const float* qv = a.Q + size_t(q) * a.pd;
@@ -1715,6 +1723,27 @@ static Sq8Scorer Sq8Of(const ScanSource& src, int kset) {
   return Sq8Scorer{src.C, src.vmin, src.scale, src.pd, src.metric, kset};
 }
 
+__global__ void k_fb_reset(uint32_t* __restrict__ acc) {
+  if (threadIdx.x == 0) *acc = 0;
+}
+
+// A new call's count of exact re-scans starts from zero: the host's, and the device's when
+// an earlier call left one there (a call spanning several scans, the collection search,
+// clears it once and sets fb_accumulate for its scans).
+int ResetFallbacks(Ctx* c, hipStream_t s) {
+  if (c->fb_accumulate) return kOk;
+  c->last_fallbacks = 0;
+  if (c->fb_dev_used) {
+    k_fb_reset<<<1, 64, 0, s>>>(c->fb_dev);
+    VDBG_HIP(hipGetLastError());
+  }
+  return kOk;
+}
+
+// Largest worst-case exact re-scan scratch (every query of the batch re-scanned) for which
+// the fallback passes are queued without reading their counts on the host.
+constexpr size_t kGatedExactBytes = size_t(64) << 20;
+
 // The exact scan's row splits for nslots queries over N rows, and its scratch bytes.
 struct ExactPlan {
   int nsplit;
@@ -1738,7 +1767,8 @@ static ExactPlan PlanExact(uint32_t N, int nslots, size_t k) {
 template <class Scorer>
 static int ExactScanT(Ctx* c, Workspace& w, const ScanSource& src, const Scorer& sc,
                       const float* Q, const uint32_t* qlist, int nslots, size_t k,
-                      const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+                      const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
+                      const uint32_t* nslots_dev = nullptr, uint32_t* fb_acc = nullptr) {
   const int E = pow2_e(k);
   const uint32_t N = src.N;
   const ExactPlan ep = PlanExact(N, nslots, k);
@@ -1752,7 +1782,7 @@ static int ExactScanT(Ctx* c, Workspace& w, const ScanSource& src, const Scorer&
   VDBG_RETURN_IF_ERROR(w.reserve(need));
   uint2* part = w.take<uint2>(size_t(nslots) * nsplit * cap);
   uint32_t* pc = w.take<uint32_t>(size_t(nslots) * nsplit);
-  ScanArgs sa{Q, allow, src.pd, N, qlist, nslots, split_rows, nsplit, part, pc};
+  ScanArgs sa{Q, allow, src.pd, N, qlist, nslots, split_rows, nsplit, part, pc, nslots_dev};
   {
     ProfScope ps(c, "exact_scan", s);
     VDBG_DISPATCH_ES(E, launch_scan, Scorer, s, sa, sc);
@@ -1771,6 +1801,8 @@ static int ExactScanT(Ctx* c, Workspace& w, const ScanSource& src, const Scorer&
   se.rescore = 0;
   se.out_ids = out_ids;
   se.out_d = out_d;
+  se.nslots_dev = nslots_dev;
+  se.fb_acc = fb_acc;
   {
     ProfScope ps(c, "merge", s);
     VDBG_DISPATCH_ES(E, launch_select, Scorer, s, se, sc);
@@ -1781,15 +1813,18 @@ static int ExactScanT(Ctx* c, Workspace& w, const ScanSource& src, const Scorer&
 
 static int ExactScan(Ctx* c, Workspace& w, const ScanSource& src, const float* Q,
                      const uint32_t* qlist, int nslots, size_t k, const uint64_t* allow,
-                     uint32_t* out_ids, float* out_d, hipStream_t s) {
+                     uint32_t* out_ids, float* out_d, hipStream_t s,
+                     const uint32_t* nslots_dev = nullptr, uint32_t* fb_acc = nullptr) {
   if (nslots == 0) return kOk;
   if (pow2_e(k) > 4) return SetError(kNotSupported, "k > 256 is not supported on the GPU path");
   if (src.kind == 0)
-    return ExactScanT(c, w, src, FlatOf(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+    return ExactScanT(c, w, src, FlatOf(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d,
+                      s, nslots_dev, fb_acc);
   if (src.kind == 2)
     return ExactScanT(c, w, src, PqScorer{src.C, src.pq_m}, Q, qlist, nslots, k, allow, out_ids,
-                      out_d, s);
-  return ExactScanT(c, w, src, Sq8Of(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d, s);
+                      out_d, s, nslots_dev, fb_acc);
+  return ExactScanT(c, w, src, Sq8Of(src, c->kset), Q, qlist, nslots, k, allow, out_ids, out_d,
+                    s, nslots_dev, fb_acc);
 }
 
 template <int PD, int METRIC, int KIND, int MODE>
@@ -1872,7 +1907,7 @@ static void GemmGrid(GemmArgs& ga, int nqt, int nchunks, int* blocks) {
 
 int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t kk,
               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
-  c->last_fallbacks = 0;
+  VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
   c->last_gemm_bits = 0;
   c->last_gemm_gate = nullptr;
   if (nq == 0 || kk == 0) return kOk;
@@ -2346,17 +2381,21 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
     else launch_tiny<2>(s, nchunks, ta);
     VDBG_HIP(hipGetLastError());
   }
-  const uint32_t seq = NextFlagSeq(c);
-  TinyMergeArgs ma{pa, part, bound, nchunks, kp, int(kk), Flat8Of(*src, c->kset), out_ids, out_d,
-                   fb_list, fb_count, c->host_flag_dev, seq, c->test_fallbacks};
-  {
-    ProfScope ps(c, "select", s);
-    k_tiny_merge<<<dim3(unsigned(nq)), 512, 0, s>>>(ma);
-    VDBG_HIP(hipGetLastError());
+  uint32_t nfb = 0;
+  {  // the merge publishes the fallback count through the context's host flag
+    std::lock_guard<std::mutex> g(c->flag_mu);
+    const uint32_t seq = NextFlagSeq(c);
+    TinyMergeArgs ma{pa, part, bound, nchunks, kp, int(kk), Flat8Of(*src, c->kset), out_ids,
+                     out_d, fb_list, fb_count, c->host_flag_dev, seq, c->test_fallbacks};
+    {
+      ProfScope ps(c, "select", s);
+      k_tiny_merge<<<dim3(unsigned(nq)), 512, 0, s>>>(ma);
+      VDBG_HIP(hipGetLastError());
+    }
+    VDBG_RETURN_IF_ERROR(WaitWords(c, seq, fb_count, 1, s));
+    nfb = c->host_pinned[0];
   }
-  VDBG_RETURN_IF_ERROR(WaitWords(c, seq, fb_count, 1, s));
-  const uint32_t nfb = c->host_pinned[0];
-  c->last_fallbacks = nfb;
+  c->last_fallbacks += nfb;
   if (nfb > 0)
     VDBG_RETURN_IF_ERROR(ExactScan(c, W2, *src, Q, fb_list, int(nfb), kk, allow, out_ids, out_d, s));
   return kOk;
@@ -2367,7 +2406,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             Workspace* ws, Workspace* ws2) {
   Workspace& W = ws != nullptr ? *ws : c->ws;
   Workspace& W2 = ws2 != nullptr ? *ws2 : c->ws2;
-  c->last_fallbacks = 0;
+  VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
   c->last_gemm_bits = 0;
   c->last_gemm_gate = nullptr;
   if (nq == 0 || kk == 0) return kOk;
@@ -2578,9 +2617,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // candidate layout and bound coincide at nq <= 128), and the one they rule out exits.
   bool use16 = try16 && split != 0, use8 = false;
   if (((try16 && split == 0) || try8op) && !gated) {
-    VDBG_RETURN_IF_ERROR(ReadWords(c, reinterpret_cast<const uint32_t*>(all16), 2, s));
-    use8 = try8any && c->host_pinned[1] != 0;
-    use16 = try16 && !use8 && (split != 0 || c->host_pinned[0] != 0);
+    uint32_t fl[2];
+    VDBG_RETURN_IF_ERROR(ReadWords(c, reinterpret_cast<const uint32_t*>(all16), 2, s, fl));
+    use8 = try8any && fl[1] != 0;
+    use16 = try16 && !use8 && (split != 0 || fl[0] != 0);
   }
   // a source reading its parent's rows through Xmap ranks on its fp16 copy (no fp32 GEMM)
   if (src->Xmap != nullptr && !use8 && !use16)
@@ -2753,9 +2793,39 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  VDBG_RETURN_IF_ERROR(ReadWords(c, fb_count, 1, s));
-  const uint32_t nfb = c->host_pinned[0];
-  c->last_fallbacks = 0;
+  // Uncertified queries take a second chance (every buffered candidate re-scored) and, if it
+  // fails too, the exact re-scan.  When the re-scan's scratch for every query of the batch is
+  // small, both passes are queued for every slot and run only for the slots the pass before
+  // listed (its count stays on the device): nothing waits on the host.  Otherwise the host
+  // reads each count and sizes the pass to it.
+  if (c->gate_fallbacks && PlanExact(N, int(nq), kk).need <= kGatedExactBytes) {
+    SelectArgs s2 = se;
+    s2.qlist = fb_list;
+    s2.nslots = int(nq);
+    s2.nslots_dev = fb_count;
+    s2.by_query = 1;
+    s2.rescore = 2;
+    s2.T = T;
+    s2.fb_list = fb2_list;
+    s2.fb_count = fb_count + 1;
+    {
+      ProfScope ps(c, "rescore", s);
+      if (UseFlat8(*src, nq, kk, 2)) {
+        VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer8, s, s2, Flat8Of(*src, c->kset));
+      } else if (src->kind == 0) {
+        VDBG_DISPATCH_ES(Esel, launch_select, FlatScorer, s, s2, FlatOf(*src, c->kset));
+      } else {
+        VDBG_DISPATCH_ES(Esel, launch_select, Sq8Scorer, s, s2, Sq8Of(*src, c->kset));
+      }
+      VDBG_HIP(hipGetLastError());
+    }
+    VDBG_RETURN_IF_ERROR(ExactScan(c, W2, *src, Q, fb2_list, int(nq), kk, allow, out_ids, out_d,
+                                   s, fb_count + 1, c->fb_dev));
+    c->fb_dev_used = true;
+    return kOk;
+  }
+  uint32_t nfb = 0;
+  VDBG_RETURN_IF_ERROR(ReadWords(c, fb_count, 1, s, &nfb));
   if (nfb == 0) return kOk;
   // second chance: rescore every buffered candidate of the uncertified queries
   SelectArgs s2 = se;
@@ -2777,9 +2847,9 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
     }
     VDBG_HIP(hipGetLastError());
   }
-  VDBG_RETURN_IF_ERROR(ReadWords(c, fb_count + 1, 1, s));
-  const uint32_t nfb2 = c->host_pinned[0];
-  c->last_fallbacks = nfb2;
+  uint32_t nfb2 = 0;
+  VDBG_RETURN_IF_ERROR(ReadWords(c, fb_count + 1, 1, s, &nfb2));
+  c->last_fallbacks += nfb2;
   if (nfb2 > 0)
     VDBG_RETURN_IF_ERROR(
         ExactScan(c, W2, *src, Q, fb2_list, int(nfb2), kk, allow, out_ids, out_d, s));

@@ -49,32 +49,86 @@ __global__ void k_compact_ids(const uint64_t* __restrict__ w, size_t nwords, uin
   }
 }
 
-__global__ void k_gather_f4(const float4* __restrict__ src, size_t row_f4,
-                            const uint32_t* __restrict__ ids, uint32_t n, float4* __restrict__ dst) {
+// The ascending ids of the allowed rows of a mask of at most kCompactBlockWords words and
+// kCompactBlockIds allowed rows, in one block: each thread takes a run of consecutive words,
+// the block scans the runs' counts in LDS, and each thread writes its run's ids from its
+// offset.  (One launch instead of the count / scan / write sequence, for sparse masks.)
+__global__ __launch_bounds__(1024) void k_compact_block(const uint64_t* __restrict__ w,
+                                                        uint32_t nwords, uint32_t N,
+                                                        uint32_t* __restrict__ ids) {
+  __shared__ uint32_t wave_tot[16];
+  const uint32_t t = threadIdx.x;
+  const uint32_t per = (nwords + 1023) / 1024;
+  const uint32_t lo = min(nwords, t * per), hi = min(nwords, lo + per);
+  auto word = [&](uint32_t i) {
+    uint64_t v = w[i];
+    const size_t b0 = size_t(i) * 64;
+    if (b0 + 64 > N) v &= (N - b0 >= 64) ? ~0ull : ((1ull << (N - b0)) - 1ull);
+    return v;
+  };
+  uint32_t cnt = 0;
+  for (uint32_t i = lo; i < hi; ++i) cnt += uint32_t(__popcll(word(i)));
+  // block exclusive scan of cnt: within each wave, then over the 16 wave totals
+  const int lane = lane_id(), wv = int(t) >> 6;
+  uint32_t incl = cnt;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t x = __shfl_up(incl, o);
+    if (lane >= o) incl += x;
+  }
+  if (lane == kWave - 1) wave_tot[wv] = incl;
+  __syncthreads();
+  uint32_t base = 0;
+  for (int i = 0; i < wv; ++i) base += wave_tot[i];
+  uint32_t p = base + incl - cnt;
+  for (uint32_t i = lo; i < hi; ++i) {
+    uint64_t v = word(i);
+    while (v != 0) {
+      const int b = __ffsll(static_cast<long long>(v)) - 1;
+      ids[p++] = i * 64 + uint32_t(b);
+      v &= v - 1;
+    }
+  }
+}
+
+// The compacted rows' parts in one launch (GatherParts, vdbg_internal.h).
+__global__ __launch_bounds__(256) void k_gather_compact(GatherParts g) {
+  const uint32_t W = g.wa + g.wb + g.wc + 1;
   const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
-  if (t >= size_t(n) * row_f4) return;
-  const size_t r = t / row_f4, c = t - r * row_f4;
-  dst[t] = src[size_t(ids[r]) * row_f4 + c];
+  if (t >= size_t(g.n) * W) return;
+  const uint32_t r = uint32_t(t / W), col = uint32_t(t - size_t(r) * W);
+  const size_t src = g.ids != nullptr ? g.ids[r] : r;
+  if (col < g.wa) {
+    g.ao[size_t(r) * g.wa + col] = g.a[src * g.wa + col];
+  } else if (col < g.wa + g.wb) {
+    const uint32_t c = col - g.wa;
+    g.bo[size_t(r) * g.wb + c] = g.b[src * g.wb + c];
+  } else if (col < g.wa + g.wb + g.wc) {
+    const uint32_t c = col - g.wa - g.wb;
+    g.co[size_t(r) * g.wc + c] = g.c8[src * g.wc + c];
+  } else {
+    g.rno[r] = g.rn[src];
+    if (g.i8 != nullptr) g.i8o[r] = g.i8[src];
+    if (g.ext != nullptr) g.exto[r] = g.ext[src];
+  }
 }
 
-__global__ void k_gather_u4(const uint4* __restrict__ src, size_t row_u4,
-                            const uint32_t* __restrict__ ids, uint32_t n, uint4* __restrict__ dst) {
-  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
-  if (t >= size_t(n) * row_u4) return;
-  const size_t r = t / row_u4, c = t - r * row_u4;
-  dst[t] = src[size_t(ids[r]) * row_u4 + c];
+int GatherRows(const GatherParts& g, hipStream_t s) {
+  const size_t total = size_t(g.n) * (g.wa + g.wb + g.wc + 1);
+  if (total == 0) return kOk;
+  k_gather_compact<<<dim3(unsigned((total + 255) / 256)), 256, 0, s>>>(g);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
 }
 
-__global__ void k_gather_f(const float* __restrict__ src, const uint32_t* __restrict__ ids,
-                           uint32_t n, float* __restrict__ dst) {
-  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) dst[t] = src[ids[t]];
-}
-
-__global__ void k_gather_u32(const uint32_t* __restrict__ src, const uint32_t* __restrict__ ids,
-                             uint32_t n, uint32_t* __restrict__ dst) {
-  const uint32_t t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < n) dst[t] = src[ids[t]];
+int CompactIdsSmall(const uint64_t* allow, uint32_t N, uint32_t count, uint32_t* ids,
+                    hipStream_t s) {
+  const size_t nwords = (size_t(N) + 63) / 64;
+  if (nwords > size_t(kCompactBlockWords) || count > kCompactBlockIds)
+    return SetError(kInternal, "CompactIdsSmall: mask too large");
+  k_compact_block<<<1, 1024, 0, s>>>(allow, uint32_t(nwords), N, ids);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
 }
 
 __global__ void k_map_ids(uint32_t* __restrict__ out, size_t n, const uint32_t* __restrict__ ids) {
@@ -82,25 +136,26 @@ __global__ void k_map_ids(uint32_t* __restrict__ out, size_t n, const uint32_t* 
   if (t < n && out[t] != kNoId) out[t] = ids[out[t]];
 }
 
-int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hipStream_t s) {
+int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hipStream_t s,
+                 ScanScratch* lane) {
   const size_t nwords = (size_t(N) + 63) / 64;
   size_t tmp_bytes = 0;
   VDBG_HIP(hipcub::DeviceReduce::Sum(nullptr, tmp_bytes, static_cast<uint32_t*>(nullptr),
                                      static_cast<uint32_t*>(nullptr), int(nwords), s));
   // the compaction scratch, kept across calls (reallocation would cost more than the scan at
   // low selectivity); its contents are dead once the count is read back
-  Workspace& w = c->wsc;
+  Workspace& w = lane != nullptr ? lane->wsc : c->wsc;
+  hipEvent_t done = lane != nullptr ? lane->wsc_done : c->wsc_done;
   w.used = 0;
   // a call on another stream may still read the scratch: wait for its last reader
-  if (c->wsc_done != nullptr) VDBG_HIP(hipStreamWaitEvent(s, c->wsc_done, 0));
+  if (done != nullptr) VDBG_HIP(hipStreamWaitEvent(s, done, 0));
   VDBG_RETURN_IF_ERROR(w.reserve((nwords + 1) * 4 + tmp_bytes + 1024));
   uint32_t* cnt = w.take<uint32_t>(nwords + 1);
   void* tmp = w.take<char>(tmp_bytes + 16);
   k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
   VDBG_HIP(hipGetLastError());
   VDBG_HIP(hipcub::DeviceReduce::Sum(tmp, tmp_bytes, cnt, cnt + nwords, int(nwords), s));
-  VDBG_RETURN_IF_ERROR(ReadWords(c, cnt + nwords, 1, s));
-  *count = c->host_pinned[0];
+  VDBG_RETURN_IF_ERROR(ReadWords(c, cnt + nwords, 1, s, count));
   return kOk;
 }
 
@@ -108,7 +163,7 @@ int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hip
 // the compact indexes back to row ids.
 int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                 const uint64_t* allow, uint32_t count, uint32_t* out_ids, float* out_d,
-                hipStream_t s) {
+                hipStream_t s, ScanScratch* lane) {
   const uint32_t N = src->N;
   const size_t pd = src->pd;
   const size_t nwords = (size_t(N) + 63) / 64;
@@ -140,8 +195,11 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                        size_t(count) * (4 + 4 + (map32 ? 0 : row_bytes) + row16_bytes + row8_bytes +
                                         (src->init8 != nullptr ? 4 : 0)) +
                        sample_bytes + tmp_bytes + 4096 + 512 + 16 * 256;
-  // the context's compaction scratch: reused in stream order by the next call
-  Workspace& w = c->wsc;
+  // the compaction scratch (the context's or the lane's): reused in stream order by the next
+  // call, whose stream waits for the event recorded below
+  Workspace& w = lane != nullptr ? lane->wsc : c->wsc;
+  hipEvent_t& wsc_done = lane != nullptr ? lane->wsc_done : c->wsc_done;
+  if (wsc_done != nullptr) VDBG_HIP(hipStreamWaitEvent(s, wsc_done, 0));
   w.used = 0;
   VDBG_RETURN_IF_ERROR(w.reserve(bytes));
   buf = w.base;
@@ -158,36 +216,43 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   void* tmp = nullptr;
   {
     ProfScope ps(c, "compact", s);
-    k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
-    tmp = take(tmp_bytes + 16);
-    VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
-    k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre, ids);
-    if (map32) {
-      // (no fp32 rows: see cs.Xmap below)
-    } else if (src->kind == 0) {
-      const size_t row_f4 = pd / 4;
-      k_gather_f4<<<dim3(unsigned((count * row_f4 + 255) / 256)), 256, 0, s>>>(
-          reinterpret_cast<const float4*>(src->X), row_f4, ids, count, static_cast<float4*>(rows));
+    if (nwords <= size_t(kCompactBlockWords) && count <= kCompactBlockIds) {
+      k_compact_block<<<1, 1024, 0, s>>>(allow, uint32_t(nwords), N, ids);
     } else {
-      const size_t row_u4 = pd / 16;
-      k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
-          reinterpret_cast<const uint4*>(src->C), row_u4, ids, count, static_cast<uint4*>(rows));
+      k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
+      tmp = take(tmp_bytes + 16);
+      VDBG_HIP(hipcub::DeviceScan::ExclusiveSum(tmp, tmp_bytes, cnt, pre, int(nwords), s));
+      k_compact_ids<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, pre,
+                                                                          ids);
     }
-    if (rows16 != nullptr) {  // the fp16 copy of the rows follows the fp32 rows
-      const size_t row_u4 = row16_bytes / 16;
-      k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
-          reinterpret_cast<const uint4*>(src->X16), row_u4, ids, count, static_cast<uint4*>(rows16));
+    // every part of the rows in one launch (padded dims are multiples of 16, so each part is
+    // whole 16-byte columns); float rows held as high fp16 halves gather no fp32 rows (the
+    // compacted source reads its parent's through the id map, cs.Xmap below)
+    GatherParts g{};
+    if (!map32) {
+      g.a = reinterpret_cast<const uint4*>(src->kind == 0 ? static_cast<const void*>(src->X)
+                                                          : static_cast<const void*>(src->C));
+      g.ao = static_cast<uint4*>(rows);
+      g.wa = uint32_t(row_bytes / 16);
+    }
+    if (rows16 != nullptr) {
+      g.b = reinterpret_cast<const uint4*>(src->X16);
+      g.bo = static_cast<uint4*>(rows16);
+      g.wb = uint32_t(row16_bytes / 16);
     }
     if (rows8 != nullptr) {
-      const size_t row_u4 = row8_bytes / 16;
-      k_gather_u4<<<dim3(unsigned((count * row_u4 + 255) / 256)), 256, 0, s>>>(
-          reinterpret_cast<const uint4*>(src->X8), row_u4, ids, count, static_cast<uint4*>(rows8));
-      if (init8 != nullptr)
-        k_gather_u32<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(
-            reinterpret_cast<const uint32_t*>(src->init8), ids, count,
-            reinterpret_cast<uint32_t*>(init8));
+      g.c8 = reinterpret_cast<const uint4*>(src->X8);
+      g.co = static_cast<uint4*>(rows8);
+      g.wc = uint32_t(row8_bytes / 16);
+      g.i8 = init8 != nullptr ? src->init8 : nullptr;
+      g.i8o = init8;
     }
-    k_gather_f<<<dim3(unsigned((count + 255) / 256)), 256, 0, s>>>(src->rn, ids, count, rn);
+    g.rn = src->rn;
+    g.rno = rn;
+    g.ids = ids;
+    g.n = count;
+    const size_t total = size_t(count) * (g.wa + g.wb + g.wc + 1);
+    k_gather_compact<<<dim3(unsigned((total + 255) / 256)), 256, 0, s>>>(g);
     VDBG_HIP(hipGetLastError());
   }
   cs.X = src->kind == 0 ? (map32 ? src->X : static_cast<const float*>(rows)) : nullptr;
@@ -199,15 +264,17 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   cs.rn = rn;
   cs.Sbuf = nullptr;
   int rc = GatherSample(c, &cs, s, sample);
-  if (rc == kOk) rc = RunScan(c, &cs, Q, nq, kk, nullptr, out_ids, out_d, s);
+  if (rc == kOk)
+    rc = RunScan(c, &cs, Q, nq, kk, nullptr, out_ids, out_d, s,
+                 lane != nullptr ? &lane->ws : nullptr, lane != nullptr ? &lane->ws2 : nullptr);
   if (rc == kOk) {
     k_map_ids<<<dim3(unsigned((nq * kk + 255) / 256)), 256, 0, s>>>(out_ids, nq * kk, ids);
     if (hipGetLastError() != hipSuccess) rc = SetError(kInternal, "map ids launch");
   }
-  if (c->wsc_done == nullptr &&
-      hipEventCreateWithFlags(&c->wsc_done, hipEventDisableTiming) != hipSuccess)
-    c->wsc_done = nullptr;
-  if (c->wsc_done == nullptr || hipEventRecord(c->wsc_done, s) != hipSuccess) {
+  if (wsc_done == nullptr &&
+      hipEventCreateWithFlags(&wsc_done, hipEventDisableTiming) != hipSuccess)
+    wsc_done = nullptr;
+  if (wsc_done == nullptr || hipEventRecord(wsc_done, s) != hipSuccess) {
     (void)hipStreamSynchronize(s);  // no event: drain before the scratch is reused
   }
   FreeSample(&cs);  // the sample lives in the scratch (cs.Sbuf is null): nothing to free
@@ -219,20 +286,35 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
 // row; when at most half the rows are allowed the allowed rows are compacted first;
 // otherwise the scan tests the mask per row.
 int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
-               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s) {
+               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
+               int64_t allowed, ScanScratch* lane) {
+  Workspace* ws = lane != nullptr ? &lane->ws : nullptr;
+  Workspace* ws2 = lane != nullptr ? &lane->ws2 : nullptr;
   if (allow == nullptr || nq == 0 || kk == 0 || src->N == 0)
-    return RunScan(c, src, Q, nq, kk, allow, out_ids, out_d, s);
+    return RunScan(c, src, Q, nq, kk, allow, out_ids, out_d, s, ws, ws2);
   uint32_t count = 0;
-  VDBG_RETURN_IF_ERROR(CountAllowed(c, allow, src->N, &count, s));
-  if (count == src->N) return RunScan(c, src, Q, nq, kk, nullptr, out_ids, out_d, s);
+  if (allowed >= 0)
+    count = uint32_t(std::min<int64_t>(allowed, src->N));
+  else
+    VDBG_RETURN_IF_ERROR(CountAllowed(c, allow, src->N, &count, s, lane));
+  if (count == src->N) return RunScan(c, src, Q, nq, kk, nullptr, out_ids, out_d, s, ws, ws2);
   if (count == 0) {  // nothing allowed: every slot is padding
     ScanSource none = *src;
     none.N = 0;
-    return RunScan(c, &none, Q, nq, kk, nullptr, out_ids, out_d, s);
+    return RunScan(c, &none, Q, nq, kk, nullptr, out_ids, out_d, s, ws, ws2);
   }
   if (2ull * count <= src->N)
-    return CompactScan(c, src, Q, nq, kk, allow, count, out_ids, out_d, s);
-  return RunScan(c, src, Q, nq, kk, allow, out_ids, out_d, s);
+    return CompactScan(c, src, Q, nq, kk, allow, count, out_ids, out_d, s, lane);
+  return RunScan(c, src, Q, nq, kk, allow, out_ids, out_d, s, ws, ws2);
+}
+
+ScanScratch::~ScanScratch() {
+  ws.release();
+  ws2.release();
+  wsc.release();
+  if (wsc_done != nullptr) (void)hipEventDestroy(wsc_done);
+  if (done != nullptr) (void)hipEventDestroy(done);
+  if (stream != nullptr) (void)hipStreamDestroy(stream);
 }
 
 // ---------------------------------------------------------------- query preparation
@@ -302,7 +384,8 @@ int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, i
 // External id of row `row` of part p: from the per-part device tables when given, else from
 // the concatenated table.
 __device__ __forceinline__ uint64_t ext_of(const MergeArgs& a, uint32_t p, uint32_t row) {
-  return a.ext_parts != nullptr ? a.ext_parts[p][row] : a.ext[a.part_off[p] + row];
+  return a.ext_parts != nullptr ? a.ext_parts[p][row]
+                                : a.ext[(a.part_off != nullptr ? a.part_off[p] : 0) + row];
 }
 
 // One wave per query.  Candidate c = p * k + i (part p, i-th hit) keeps (dist, part, row)
@@ -314,6 +397,7 @@ __global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
   const int q = blockIdx.x * 4 + wave;
   if (q >= a.nq) return;
   const int total = a.nparts * a.k;
+  const int ko = a.kout > 0 ? a.kout : a.k;  // results written per query
   WaveKeys<E> r;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -355,15 +439,15 @@ __global__ __launch_bounds__(256) void k_merge(MergeArgs a) {
       if (ex[t] == v) keep = false;
     const uint64_t bal = __ballot(keep);
     const int pos = written + __popcll(bal & ((1ull << lane) - 1ull));
-    if (keep && pos < a.k) {
-      a.out_ext[size_t(q) * a.k + pos] = v;
-      a.out_d[size_t(q) * a.k + pos] = r.d[e];
+    if (keep && pos < ko) {
+      a.out_ext[size_t(q) * ko + pos] = v;
+      a.out_d[size_t(q) * ko + pos] = r.d[e];
     }
     written += __popcll(bal);
   }
-  for (int i = written + lane; i < a.k; i += kWave) {
-    a.out_ext[size_t(q) * a.k + i] = ~0ull;
-    a.out_d[size_t(q) * a.k + i] = __builtin_inff();
+  for (int i = written + lane; i < ko; i += kWave) {
+    a.out_ext[size_t(q) * ko + i] = ~0ull;
+    a.out_d[size_t(q) * ko + i] = __builtin_inff();
   }
 }
 
@@ -425,7 +509,7 @@ __global__ __launch_bounds__(256) void k_memit(MergeChunk m, const uint64_t* __r
   const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= m.nc) return;
   const int lane = lane_id();
-  const int k = m.a.k;
+  const int k = m.a.kout > 0 ? m.a.kout : m.a.k;  // results written per query
   const size_t gq = size_t(m.q0 + q);
   int written = 0;
   for (uint32_t r0 = 0; r0 < m.per && written < k; r0 += kWave) {

@@ -35,12 +35,15 @@ __global__ void k_publish_words(const uint32_t* __restrict__ src, int n, uint32_
 
 uint32_t NextFlagSeq(Ctx* c) { return ++c->flag_seq == 0 ? ++c->flag_seq : c->flag_seq; }
 
-int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s) {
+int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s, uint32_t* out) {
   if (n <= 0 || n > 64) return SetError(kInternal, "ReadWords: 1..64 words");
+  std::lock_guard<std::mutex> g(c->flag_mu);
   const uint32_t seq = NextFlagSeq(c);
   k_publish_words<<<1, 64, 0, s>>>(dev, n, c->host_flag_dev, seq);
   VDBG_HIP(hipGetLastError());
-  return WaitWords(c, seq, dev, n, s);
+  VDBG_RETURN_IF_ERROR(WaitWords(c, seq, dev, n, s));
+  for (int i = 0; i < n; ++i) out[i] = c->host_pinned[i];
+  return kOk;
 }
 
 int WaitWords(Ctx* c, uint32_t seq, const uint32_t* dev, int n, hipStream_t s) {
@@ -130,6 +133,7 @@ int Fill32(void* p, uint32_t v, size_t n, hipStream_t s) {
 ProfScope::ProfScope(Ctx* c, const char* name, hipStream_t s) : c_(c), s_(s), on_(c->profiling) {
   if (!on_) return;
   e_.name = name;
+  std::lock_guard<std::mutex> g(c_->prof_mu);
   auto grab = [&]() {
     hipEvent_t ev;
     if (!c_->free_events.empty()) {
@@ -152,10 +156,12 @@ ProfScope::ProfScope(Ctx* c, const char* name, hipStream_t s) : c_(c), s_(s), on
 ProfScope::~ProfScope() {
   if (!on_) return;
   (void)hipEventRecord(e_.stop, s_);
+  std::lock_guard<std::mutex> g(c_->prof_mu);
   c_->pending.push_back(e_);
 }
 
 static void DrainProfile(Ctx* c) {
+  std::lock_guard<std::mutex> g(c->prof_mu);
   for (auto& p : c->pending) {
     float ms = 0.f;
     if (hipEventSynchronize(p.stop) == hipSuccess &&
@@ -427,7 +433,10 @@ int vdbg_ctx_create(int device, vdbg_ctx** out) {
     ctx->c.host_flag[0] = 0;
     e = hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->c.host_flag_dev), ctx->c.host_flag, 0);
   }
+  if (e == hipSuccess) e = hipMalloc(reinterpret_cast<void**>(&ctx->c.fb_dev), 256);
+  if (e == hipSuccess) e = hipMemset(ctx->c.fb_dev, 0, 256);
   if (e != hipSuccess) {
+    if (ctx->c.fb_dev) (void)hipFree(ctx->c.fb_dev);
     if (ctx->c.host_flag) (void)hipHostFree(ctx->c.host_flag);
     if (ctx->c.host_pinned) (void)hipHostFree(ctx->c.host_pinned);
     if (ctx->c.stream) (void)hipStreamDestroy(ctx->c.stream);
@@ -494,6 +503,23 @@ int vdbg_ctx_set_fp16_single(vdbg_ctx* ctx, int enable) {
   return kOk;
 }
 
+int vdbg_ctx_set_collection_schedule(vdbg_ctx* ctx, int combine, int lanes, int threaded) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  if (lanes < 0 || lanes > 16) return SetError(kInvalidArgument, "lanes must be in 0..16");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.combine_segments = combine != 0;
+  ctx->c.collection_lanes = lanes;
+  ctx->c.lane_threads = threaded != 0;
+  return kOk;
+}
+
+int vdbg_ctx_set_gated_fallbacks(vdbg_ctx* ctx, int enable) {
+  if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
+  std::lock_guard<std::recursive_mutex> g(ctx->c.mu);
+  ctx->c.gate_fallbacks = enable != 0;
+  return kOk;
+}
+
 int vdbg_ctx_set_test_fallbacks(vdbg_ctx* ctx, int level) {
   if (ctx == nullptr) return SetError(kInvalidArgument, "null ctx");
   if (level < 0 || level > 2) return SetError(kInvalidArgument, "level must be 0, 1 or 2");
@@ -514,11 +540,19 @@ int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   (void)hipStreamSynchronize(c.stream);
   DrainProfile(&c);
   for (auto ev : c.free_events) (void)hipEventDestroy(ev);
+  for (ScanScratch* l : c.lanes) {
+    (void)hipStreamSynchronize(l->stream);
+    delete l;
+  }
+  c.lanes.clear();
   c.ws.release();
   c.ws2.release();
   c.wsc.release();
+  c.wcomb.release();
+  if (c.wcomb_done) (void)hipEventDestroy(c.wcomb_done);
   if (c.wsc_done) (void)hipEventDestroy(c.wsc_done);
   if (c.host_pinned) (void)hipHostFree(c.host_pinned);
+  if (c.fb_dev) (void)hipFree(c.fb_dev);
   if (c.host_flag) (void)hipHostFree(c.host_flag);
   (void)hipStreamDestroy(c.stream);
   delete ctx;
@@ -1242,7 +1276,7 @@ int vdbg_last_gemm_bits(vdbg_ctx* ctx) {
   Ctx& c = ctx->c;
   std::lock_guard<std::recursive_mutex> g(c.mu);
   if (c.last_gemm_gate != nullptr) {  // chosen on the device: read the flag
-    std::vector<int> v(size_t(std::max(c.last_gemm_gate_n, 1)), 0);
+    std::vector<int> v(size_t(std::max(c.last_gemm_gate_n.load(), 1)), 0);
     // (the scan may have run on any stream)
     if (hipSetDevice(c.device) != hipSuccess || hipDeviceSynchronize() != hipSuccess ||
         hipMemcpy(v.data(), c.last_gemm_gate, size_t(c.last_gemm_gate_n) * sizeof(int),
@@ -1259,7 +1293,19 @@ int vdbg_last_gemm_bits(vdbg_ctx* ctx) {
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries) {
   if (ctx == nullptr || fallback_queries == nullptr)
     return SetError(kInvalidArgument, "null argument");
-  *fallback_queries = ctx->c.last_fallbacks;
+  Ctx& c = ctx->c;
+  std::lock_guard<std::recursive_mutex> g(c.mu);
+  uint64_t n = c.last_fallbacks;
+  if (c.fb_dev_used) {  // passes queued without a host read: their count is on the device
+    VDBG_HIP(hipSetDevice(c.device));
+    VDBG_HIP(hipDeviceSynchronize());
+    uint32_t v = 0;
+    VDBG_HIP(hipMemcpy(&v, c.fb_dev, 4, hipMemcpyDeviceToHost));
+    VDBG_HIP(hipMemset(c.fb_dev, 0, 4));
+    c.fb_dev_used = false;
+    n += v;
+  }
+  *fallback_queries = n;
   return kOk;
 }
 

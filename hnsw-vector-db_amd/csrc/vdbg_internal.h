@@ -7,6 +7,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <atomic>
 #include <vector>
 
 #include "../../include/vdbg.h"
@@ -99,6 +100,8 @@ struct ProfEntry {
   hipEvent_t start, stop;
 };
 
+struct ScanScratch;  // below
+
 struct Ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -113,14 +116,29 @@ struct Ctx {
   uint32_t* host_flag = nullptr;
   uint32_t* host_flag_dev = nullptr;
   uint32_t flag_seq = 0;
+  std::mutex flag_mu;  // one readback through host_flag at a time (scan lanes may run on
+                       // worker threads of one call)
+  std::mutex prof_mu;  // guards pending / free_events against those threads
   bool profiling = false;
   std::vector<ProfEntry> pending;
   std::vector<hipEvent_t> free_events;
   std::map<std::string, std::pair<double, uint64_t>> prof;  // name -> (ms, launches)
-  uint64_t last_fallbacks = 0;
-  int last_gemm_bits = 0;  // input width of the last scan's main GEMM: 32, 16, 8 or 0
-  const int* last_gemm_gate = nullptr;  // when the batch chose its GEMM on the device: the
-  int last_gemm_gate_n = 0;             // per-query int8 flags (all 1: int8, else fp32)
+  std::atomic<uint64_t> last_fallbacks{0};
+  // exact re-scans of fallback passes queued without a host read (RunScan), accumulated on
+  // the device until vdbg_last_fallbacks reads them
+  bool gate_fallbacks = true;
+  uint32_t* fb_dev = nullptr;
+  std::atomic<bool> fb_dev_used{false};
+  bool fb_accumulate = false;  // set while one call runs several scans (ResetFallbacks)
+  std::vector<ScanScratch*> lanes;  // the collection search's side-by-side scan lanes
+  Workspace wcomb;                  // the collection search's combined rows (kept across calls)
+  hipEvent_t wcomb_done = nullptr;  // recorded after the last launch reading wcomb
+  bool combine_segments = true;     // small flat segments scanned as one (collection.hip)
+  int collection_lanes = 2;         // lanes a collection search may use (0: none)
+  bool lane_threads = true;         // each lane issued by its own host thread
+  std::atomic<int> last_gemm_bits{0};  // input width of the last scan's main GEMM: 32, 16, 8, 0
+  std::atomic<const int*> last_gemm_gate{nullptr};  // when the batch chose its GEMM on the
+  std::atomic<int> last_gemm_gate_n{0};  // device: the per-query int8 flags (all 1: int8)
   int cu_count = 256;
   int live_datasets = 0;       // datasets created on this context and not yet destroyed
   int kset = 2;                // distance kernel set: 0 scalar, 1 avx2, 2 avx512 (KernelSet)
@@ -202,6 +220,7 @@ struct Dataset {
   ScanSource src;          // the flat scan's view of these rows
   int live_indexes = 0;    // SQ8 / IVF-PQ indexes over these rows not yet destroyed (ctx mu)
   uint64_t* ext_ids = nullptr;  // n external ids (device) for the collection merge, or null
+  bool ext_unique = false;      // no two rows share an external id (checked when they are set)
   // appendable datasets (vdb's MutableSegment): rows, norms and external ids are reserved
   // for cap rows and grow in place; no fp16 / int8 copies are kept
   bool appendable = false;
@@ -378,19 +397,56 @@ struct MergeArgs {
   const float* part_d;        // [nparts][nq][k]
   const uint32_t* part_rows;  // [nparts][nq][k], UINT32_MAX padded
   const uint64_t* ext;        // external ids, part p row r at ext[part_off[p] + r]
-  const uint64_t* part_off;
+  const uint64_t* part_off;   // (null: ext[r], one part)
   uint64_t* out_ext;          // [nq][k], UINT64_MAX padded
   float* out_d;
   const uint64_t* const* ext_parts = nullptr;  // or row r of part p at ext_parts[p][r]
+  int kout = 0;  // results per query written to out_ext / out_d ([nq][kout]); 0: k
 };
 int MergeParts(Ctx* c, const MergeArgs& a, hipStream_t s);
 // PrepareQuery + NormalizeVector for nq raw queries into padded rows; waits for the result
 // (a query with a non-finite value, or a zero query under cosine, is InvalidArgument).
 int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
                    float* out, hipStream_t s);
+// The scratch of one scan pipeline other than the context's own (a lane of a collection
+// search running several segments' scans side by side on their own streams).
+struct ScanScratch {
+  Workspace ws, ws2, wsc;          // as Ctx::ws, ws2, wsc
+  hipEvent_t wsc_done = nullptr;   // as Ctx::wsc_done
+  hipStream_t stream = nullptr;
+  hipEvent_t done = nullptr;       // recorded after the lane's last launch of a call
+  ~ScanScratch();
+};
+// Rows gathered by id into compact arrays, every part in one launch: per row, 16-byte columns
+// of up to three row arrays (fp32 rows or codes, the fp16 copy, the int8 copy) and one column
+// for the row's scalars (norm, int8 accumulator start, external id).
+struct GatherParts {
+  const uint4* a;  uint4* ao;  uint32_t wa;   // fp32 rows or codes (wa columns per row)
+  const uint4* b;  uint4* bo;  uint32_t wb;   // fp16 copy
+  const uint4* c8; uint4* co;  uint32_t wc;   // int8 copy
+  const float* rn; float* rno;
+  const int* i8;   int* i8o;                  // nullable
+  const uint64_t* ext; uint64_t* exto;        // nullable
+  const uint32_t* ids;                        // null: rows 0..n-1
+  uint32_t n;
+};
+int GatherRows(const GatherParts& g, hipStream_t s);
+// The ascending ids of the rows a mask allows, in one launch, for masks of at most
+// kCompactBlockWords words allowing at most kCompactBlockIds rows (count, known).
+constexpr int kCompactBlockWords = 32 * 1024;
+constexpr uint32_t kCompactBlockIds = 65536;
+int CompactIdsSmall(const uint64_t* allow, uint32_t N, uint32_t count, uint32_t* ids,
+                    hipStream_t s);
+
+// The exhaustive scan under dense allow words (null: every row): rows compacted when at most
+// half are allowed.  allowed: the number of allowed rows when the caller knows it (read on the
+// device otherwise, one host round trip); lane: scratch other than the context's.
 int ScanMasked(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
-               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s);
+               const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
+               int64_t allowed = -1, ScanScratch* lane = nullptr);
 int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);
+// Starts a call's count of exact re-scans at zero (host and, when needed, device).
+int ResetFallbacks(Ctx* c, hipStream_t s);
 // The sample rows of an N-row source, its buffer size, and the gather into caller memory
 // (at least SampleBytes, any alignment) for sources that live one call.
 uint32_t SampleRows(uint32_t N);
@@ -445,7 +501,7 @@ inline int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, siz
 // queued on s: a one-wave kernel publishes them into coherent pinned memory with a sequence
 // number that the host polls (far less latency than a stream synchronisation); the host
 // falls back to synchronising when the stream ends without the number showing.
-int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s);
+int ReadWords(Ctx* c, const uint32_t* dev, int n, hipStream_t s, uint32_t* out);
 // The host side of ReadWords for a kernel that publishes the words itself: waits until the
 // flag carries seq (NextFlagSeq), then copies the n words to host_pinned (or, should the
 // stream end without the number showing, copies them from dev).

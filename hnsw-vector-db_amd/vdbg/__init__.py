@@ -62,6 +62,8 @@ _SIGS = {
     "vdbg_ctx_set_ivf_row_sums": (C.c_int, [_vp, C.c_int]),
     "vdbg_ctx_set_int8_float_min_work": (C.c_int, [_vp, C.c_double]),
     "vdbg_ctx_set_test_fallbacks": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_gated_fallbacks": (C.c_int, [_vp, C.c_int]),
+    "vdbg_ctx_set_collection_schedule": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int]),
     "vdbg_profile_enable": (C.c_int, [_vp, C.c_int]),
     "vdbg_profile_reset": (C.c_int, [_vp]),
     "vdbg_profile_get": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_double),
@@ -79,6 +81,8 @@ _SIGS = {
     "vdbg_dataset_set_external_ids": (C.c_int, [_vp, _vp]),
     "vdbg_collection_search_host": (C.c_int, [_vp, _vp, _sz, _sz, C.c_int, _vp, _sz, _sz, _vp,
                                               _vp, _vp, _vp, _vp]),
+    "vdbg_collection_search_device": (C.c_int, [_vp, _vp, _sz, _sz, C.c_int, _vp, _sz, _sz,
+                                                _vp, _vp, _vp, _vp, _vp, _vp]),
     "vdbg_dataset_destroy": (C.c_int, [_vp]),
     "vdbg_dataset_rows": (_vp, [_vp]),
     "vdbg_flat_search_host": (C.c_int, [_vp, _vp, _sz, _sz, _vp, _vp, _vp,
@@ -238,6 +242,18 @@ class Context:
         2 also every second one (exact re-scan); 0 is the normal path.  Results are
         identical."""
         _check(lib.vdbg_ctx_set_test_fallbacks(self.h, int(level)))
+
+    def set_collection_schedule(self, combine=True, lanes=2, threaded=True):
+        """How a collection search schedules its segments' flat scans: one combined scan
+        where it applies, else each segment on its own, side by side on `lanes` streams
+        (0/1: in turn), each lane issued by its own host thread when threaded."""
+        _check(lib.vdbg_ctx_set_collection_schedule(self.h, 1 if combine else 0, int(lanes),
+                                                    1 if threaded else 0))
+
+    def set_gated_fallbacks(self, enable=True):
+        """Fallback passes queued without host reads (on) or sized from host reads of their
+        counts (off); results are identical."""
+        _check(lib.vdbg_ctx_set_gated_fallbacks(self.h, 1 if enable else 0))
 
     def profile(self, enable=True):
         _check(lib.vdbg_profile_enable(self.h, 1 if enable else 0))
@@ -716,6 +732,41 @@ def collection_search(ctx, segments, dim, metric, queries, k, params=None):
                                            METRICS[metric], _ptr(q), nq, k, C.byref(params),
                                            _ptr(ids), _ptr(d), _ptr(dc), _ptr(plans)))
     return ids, d, dc, [PLANS[p] for p in plans[:len(segments)]]
+
+
+def collection_search_device(ctx, segments, dim, metric, q_ptr, nq, k, out_ids_ptr,
+                             out_dists_ptr, params=None, stream=None):
+    """vdbg_collection_search_device: raw queries (nq x dim floats) and the outputs (uint64
+    and float32 [nq, k]) in device memory; segments as for collection_search.  Returns
+    (distance computations per query, plan name per segment)."""
+    params = params or SearchParams()
+    keep = []
+    arr = (_Segment * max(len(segments), 1))()
+    for i, seg in enumerate(segments):
+        if isinstance(seg, HostHits):
+            keep.append(seg)
+            arr[i] = _Segment(None, None, None, None, None, None, 0, seg.dists.ctypes.data,
+                              seg.rows.ctypes.data, seg.ext.ctypes.data,
+                              None if seg.dist_comps is None else seg.dist_comps.ctypes.data)
+            continue
+        ds, ix, deleted, filt = seg[:4]
+        memory = bool(seg[4]) if len(seg) > 4 else False
+        sq = ix.h if isinstance(ix, Sq8Index) else None
+        iv = ix.h if isinstance(ix, IvfPqIndex) else None
+        pf = ix.h if isinstance(ix, PqFlatIndex) else None
+        dw = None if deleted is None else np.ascontiguousarray(deleted, np.uint64)
+        fw = None if filt is None else np.ascontiguousarray(filt, np.uint64)
+        keep += [dw, fw]
+        arr[i] = _Segment(ds.h, sq, iv, None if dw is None else dw.ctypes.data,
+                          None if fw is None else fw.ctypes.data, pf, 1 if memory else 0,
+                          None, None, None, None)
+    dc = np.empty(max(nq, 1), np.uint64)
+    plans = np.empty(max(len(segments), 1), np.int32)
+    _check(lib.vdbg_collection_search_device(ctx.h, C.cast(arr, _vp), len(segments), dim,
+                                             METRICS[metric], q_ptr, nq, k, C.byref(params),
+                                             out_ids_ptr, out_dists_ptr, _ptr(dc), _ptr(plans),
+                                             stream))
+    return dc[:nq], [PLANS[p] for p in plans[:len(segments)]]
 
 
 def crc32c(data, crc=0):

@@ -141,6 +141,25 @@ float vdbg_host_sq8_distance(const char* kernels, int metric, const float* q, co
  * query is re-scanned exactly.  Results are identical at every level; 0 (the default) is
  * the normal path.  No counterpart in the reference. */
 int vdbg_ctx_set_test_fallbacks(vdbg_ctx* ctx, int level);
+/* How the flat and SQ8 scans run their fallback passes (the second chance and the exact
+ * re-scan of uncertified queries).  On (the default), when the re-scan's scratch for every
+ * query of the batch is at most 64 MiB, both passes are queued for every query and run only
+ * for those the pass before listed, with no host wait; the fallback count then stays on the
+ * device until vdbg_last_fallbacks reads it (which waits for the device).  Off, the host reads
+ * each count and sizes the passes to it.  Results are identical either way.  No counterpart
+ * in the reference. */
+int vdbg_ctx_set_gated_fallbacks(vdbg_ctx* ctx, int enable);
+/* How vdbg_collection_search_* schedules its segments' flat scans.  combine != 0 (the
+ * default): when every segment is a flat scan (in-memory parts, flat indexes, prefilter
+ * plans) whose external ids are unique within it (checked by vdbg_dataset_set_external_ids),
+ * with k x segments <= 240 and at most 262,144 allowed rows in all, the allowed rows of every
+ * segment are gathered into one row set and scanned once for the top k x segments, then
+ * merged (the same results as vdb's merge of per-segment lists).  Otherwise each segment is
+ * scanned on its own, side by side on `lanes` streams (0..16; 0 or 1: in turn on the call's
+ * stream; default 2) with their own scratch, each lane issued by its own host thread when
+ * threaded != 0 (the default).  Results are identical under every schedule.  No counterpart
+ * in the reference. */
+int vdbg_ctx_set_collection_schedule(vdbg_ctx* ctx, int combine, int lanes, int threaded);
 
 /* Per-kernel timing with HIP events on the stream each kernel runs on.  When enabled, every
  * launch is bracketed by events; vdbg_profile_get returns the summed milliseconds and launch
@@ -391,8 +410,9 @@ int vdbg_merge_parts_host(vdbg_ctx* ctx, size_t nq, size_t nparts, size_t k,
                           const uint64_t* ext_ids, size_t n_ext, const uint64_t* part_offsets,
                           uint64_t* out_ext, float* out_dists);
 
-/* Diagnostics of the last flat/SQ8 search on this context: queries whose GEMM-ranked
- * candidates could not be certified and were re-scanned exactly. */
+/* Diagnostics of the last flat/SQ8 search on this context (all segments of the last
+ * collection search): queries whose GEMM-ranked candidates could not be certified and were
+ * re-scanned exactly.  Waits for the device when the count is still there. */
 int vdbg_last_fallbacks(vdbg_ctx* ctx, uint64_t* fallback_queries);
 /* Input width of the last flat/SQ8 scan's ranking GEMM on this context: 32 (fp32 MFMA), 16
  * (fp16 MFMA: integer rows and queries of magnitude <= 2048 with every partial sum below
@@ -547,6 +567,17 @@ int vdbg_collection_search_host(vdbg_ctx* ctx, const vdbg_segment* segs, size_t 
                                 size_t dim, int metric, const float* queries, size_t nq,
                                 size_t k, const vdbg_search_params* params, uint64_t* out_ids,
                                 float* out_dists, uint64_t* dist_comps, int* seg_plans);
+/* vdbg_collection_search_host with the raw queries (nq x dim) and the outputs in device
+ * memory, queued on `stream` (NULL = the context's): the same plans, results and counts
+ * without the query upload and the result download.  Segment words, host parts, dist_comps
+ * and seg_plans stay host memory.  Returns once the results are written (the call reads a
+ * few device words on the host on the way: the queries' status, and the counts some plans
+ * need). */
+int vdbg_collection_search_device(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg,
+                                  size_t dim, int metric, const float* queries, size_t nq,
+                                  size_t k, const vdbg_search_params* params,
+                                  uint64_t* out_ids, float* out_dists, uint64_t* dist_comps,
+                                  int* seg_plans, void* stream);
 
 #ifdef __cplusplus
 }

@@ -447,3 +447,96 @@ def test_host_part_rejects_unsorted_hits(ctx):
     d2 = np.array([[0.5, 1.0, np.inf]], np.float32)
     gi, gd, gdc, gp = vdbg.collection_search(ctx, [vdbg.HostHits(d2, r, e, [9])], 16, "l2", raw, 3)
     assert gp == ["host"] and list(gi[0]) == [30, 40, 2**64 - 1] and gdc[0] == 9
+
+
+def test_device_entry_equals_host_entry(ctx, oracle, coll):
+    """vdbg_collection_search_device (raw queries and results in device memory, the segments'
+    flat scans on the call's lanes) returns what vdbg_collection_search_host returns: ids,
+    distances, distance computations and plans, with and without filters."""
+    import torch
+
+    segs, handles = coll
+    dev = torch.device("cuda:0")
+    for fkind in (None, 0.5, 0.02):
+        n = [sg["base"].shape[0] for sg in segs]
+        filt = [None if fkind is None else _mask(m, fkind, 1800 + i) for i, m in enumerate(n)]
+        parts = [(ds, ix, sg["deleted"], f) for (ds, ix), sg, f in zip(handles, segs, filt)]
+        raw = _queries(37, 1810)
+        for k in (1, 10, 100):
+            print(f"collection device entry filter={fkind} k={k}", flush=True)
+            hi, hd, hdc, hp = vdbg.collection_search(ctx, parts, DIM, "l2", raw, k,
+                                                     vdbg.SearchParams(nprobe=8))
+            q = torch.from_numpy(raw).to(dev)
+            oi = torch.empty((37, k), dtype=torch.int64, device=dev)
+            od = torch.empty((37, k), dtype=torch.float32, device=dev)
+            ddc, dp = vdbg.collection_search_device(
+                ctx, parts, DIM, "l2", q.data_ptr(), 37, k, oi.data_ptr(), od.data_ptr(),
+                vdbg.SearchParams(nprobe=8), stream=torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            assert dp == hp
+            assert np.array_equal(oi.cpu().numpy().view(np.uint64), hi)
+            assert np.array_equal(od.cpu().numpy().view(np.uint32), hd.view(np.uint32))
+            assert np.array_equal(ddc, hdc)
+
+
+@pytest.mark.parametrize("metric,memory", [("l2", False), ("cosine", False), ("l2", True)])
+def test_collection_schedules_agree(ctx, oracle, metric, memory):
+    """Flat segments (deletes, filters from 0.5 % to 60 %, an external id held by two segments,
+    optionally an in-memory part first) searched under every schedule of the collection
+    search: one combined scan of all allowed rows (taken when no part is an in-memory one,
+    whose appended ids are not checked for uniqueness), segments side by side on threaded
+    lanes, on unthreaded lanes, and in turn.  Every schedule returns the oracle's composition
+    of vdb's per-segment searches and merge."""
+    dim = 48
+    pd = vdbg.padded_dim(dim)
+    sizes = [(1200, memory), (9000, False), (7000, False), (20000, False), (3000, False)]
+    segs, handles = [], []
+    for i, (n, in_memory) in enumerate(sizes):
+        x = datagen.uniform_rows(n, dim, 1900 + i) * (3 if metric == "l2" else 1)
+        if metric == "cosine":
+            x = x - np.float32(0.5)
+        base = datagen.pad(x, pd)
+        if metric == "cosine":
+            base = base / np.linalg.norm(base, axis=1, keepdims=True).astype(np.float32)
+        ext = np.arange(n, dtype=np.uint64) * 5 + 100000 * i
+        if i == 4:
+            ext[:40] = segs[1]["ext"][:40]  # upserted rows of segment 1
+        if in_memory:
+            ds = vdbg.Dataset.appendable(ctx, dim, metric, capacity=512)
+            ds.append(base, ext)
+        else:
+            ds = vdbg.Dataset(ctx, base, dim, metric=metric)
+            ds.set_external_ids(ext)
+        segs.append({"base": base, "ext": ext, "kind": "memory" if in_memory else "flat",
+                     "deleted": _mask(n, 0.02, 1910 + i)})
+        handles.append(ds)
+    raw = (datagen.uniform_rows(33, dim, 1920) * 3).astype(np.float32)
+    if metric == "cosine":
+        raw = raw - np.float32(0.5)
+    schedules = [(True, 4, True), (False, 4, True), (False, 3, False), (False, 0, False)]
+    try:
+        for frac in (None, 0.005, 0.05, 0.6):
+            for i, sg in enumerate(segs):
+                sg["filter"] = None if frac is None else _mask(sg["base"].shape[0], frac, 1930 + i)
+            for k in (1, 10, 25):
+                oi, od, odc, op = oracle.collection_search(segs, dim, metric, raw, k)
+                for combine, lanes, threaded in schedules:
+                    print(f"schedules {metric} filter={frac} k={k} combine={combine} "
+                          f"lanes={lanes} threaded={threaded}", flush=True)
+                    ctx.set_collection_schedule(combine, lanes, threaded)
+                    ctx.profile(True)
+                    ctx.profile_reset()
+                    gi, gd, gdc, gp = vdbg.collection_search(
+                        ctx, [(ds, None, sg["deleted"], sg["filter"], sg["kind"] == "memory")
+                              for ds, sg in zip(handles, segs)], dim, metric, raw, k)
+                    if combine and not memory:  # one gather of every segment's rows
+                        assert ctx.profile_get("compact")[1] == 1
+                    ctx.profile(False)
+                    assert gp == op, (frac, k, combine, lanes)
+                    assert np.array_equal(gi, oi), (frac, k, combine, lanes)
+                    assert np.array_equal(gd.view(np.uint32), od.view(np.uint32)), (frac, k, combine, lanes)
+                    assert np.array_equal(gdc, odc), (frac, k, combine, lanes)
+    finally:
+        ctx.set_collection_schedule(True, 2, True)
+        for ds in handles:
+            ds.close()

@@ -185,3 +185,44 @@ def test_threshold_short_of_depth_falls_back(ctx, oracle, kind):
         od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, 10, 100)
     assert ctx.last_fallbacks() > 0
     _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("gated", [True, False])
+@pytest.mark.parametrize("level", [0, 1, 2])
+@pytest.mark.parametrize("kind", ["flat_int", "flat_float", "sq8", "filtered"])
+def test_fallback_passes_queued_or_read(ctx, oracle, gated, level, kind):
+    """The second chance and the exact re-scan, forced for every query (level 1: the first
+    certificate fails; 2: the second too), queued for every slot with their counts left on
+    the device (gated) or sized from host reads of the counts: the same results as the
+    oracle's either way, and the same number of exact re-scans."""
+    n, nq, k = 40000, 150, 10
+    print(f"fallback passes {kind} level={level} gated={gated}", flush=True)
+    if kind == "flat_int":
+        base, qs = datagen.sift_like(n, 128, 7101), datagen.sift_like(nq, 128, 7102)
+    else:
+        base, qs = datagen.uniform_rows(n, 128, 7103), datagen.uniform_rows(nq, 128, 7104)
+    allow = None
+    if kind == "filtered":  # a third of the rows: the compacted scan
+        allow = np.zeros((n + 63) // 64, np.uint64)
+        rows = np.arange(0, n, 3)
+        np.bitwise_or.at(allow, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    ds = vdbg.Dataset(ctx, base, 128)
+    ctx.set_gated_fallbacks(gated)
+    ctx.set_test_fallbacks(level)
+    try:
+        if kind == "sq8":
+            sq = vdbg.Sq8Index(ds)
+            gi, gd = sq.search(qs, k, 100)
+        else:
+            gi, gd = ds.flat_search(qs, k, allow=allow)
+        assert ctx.last_fallbacks() == (nq if level == 2 else 0)
+    finally:
+        ctx.set_test_fallbacks(0)
+        ctx.set_gated_fallbacks(True)
+    if kind == "sq8":
+        od, oi = oracle.sq8_search(base, sq.codes(), sq.vmin, sq.scale, qs, k, 100)
+        sq.close()
+    else:
+        od, oi = oracle.flat_search(base, qs, k, allow=allow)
+    _check_equal(gi, gd, oi, od)
+    ds.close()
