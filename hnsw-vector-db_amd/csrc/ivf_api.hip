@@ -351,22 +351,14 @@ int vdbg_ivfpq_search_host(vdbg_ivfpq* ix, const float* queries, size_t nq, size
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
   IvfIndex* x = &ix->x;
-  hipStream_t s = c->stream;
-  uint64_t* dc = nullptr;
-  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dc), nq * 8, s));
-  int rc = StageHost(c, x->ds->n, x->pd, queries, nq, k, allow_words, out_ids, out_dists,
-                     [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
-                         hipStream_t st) {
-                       return IvfSearch(x, dq, nq, k, nprobe, rerank, dm, di, dd, dc, st);
-                     });
-  if (rc == kOk && dist_comps) {
-    // IndexSearchStats::distance_computations per query (ivf_pq.cc:199, 241, 243): nlist +
-    // codes scanned + candidates re-ranked
-    hipError_t e = hipMemcpy(dist_comps, dc, nq * 8, hipMemcpyDeviceToHost);
-    if (e != hipSuccess) rc = SetError(kInternal, hipGetErrorString(e));
-  }
-  (void)hipFreeAsync(dc, s);
-  return rc;
+  // IndexSearchStats::distance_computations per query (ivf_pq.cc:199, 241, 243): nlist +
+  // codes scanned + candidates re-ranked, returned with the results when asked for
+  return StageHost(c, x->ds->n, x->pd, queries, nq, k, allow_words, out_ids, out_dists,
+                   dist_comps,
+                   [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
+                       uint64_t* ddc, hipStream_t st) {
+                     return IvfSearch(x, dq, nq, k, nprobe, rerank, dm, di, dd, ddc, st);
+                   });
 }
 
 }  // extern "C"

@@ -350,21 +350,11 @@ int vdbg_pqflat_search_host(vdbg_pqflat* ix, const float* queries, size_t nq, si
   Ctx* c = d.ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
-  hipStream_t s = c->stream;
-  uint64_t* ddc = nullptr;
-  if (dist_comps != nullptr) VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&ddc), nq * 8, s));
-  int rc = StageHost(c, d.n, d.pd, queries, nq, k, allow_words, out_ids, out_dists,
-                     [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
-                         hipStream_t st) {
-                       return PqFlatSearch(&ix->p, dq, nq, k, rerank, dm, di, dd, ddc, st);
-                     });
-  if (rc == kOk && ddc != nullptr) {
-    hipError_t e = hipMemcpyAsync(dist_comps, ddc, nq * 8, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) rc = SetError(kInternal, hipGetErrorString(e));
-  }
-  if (ddc != nullptr) (void)hipFreeAsync(ddc, s);
-  return rc;
+  return StageHost(c, d.n, d.pd, queries, nq, k, allow_words, out_ids, out_dists, dist_comps,
+                   [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
+                       uint64_t* ddc, hipStream_t st) {
+                     return PqFlatSearch(&ix->p, dq, nq, k, rerank, dm, di, dd, ddc, st);
+                   });
 }
 
 }  // extern "C"

@@ -68,6 +68,161 @@ int WaitWords(Ctx* c, uint32_t seq, const uint32_t* dev, int n, hipStream_t s) {
   }
 }
 
+// ------------------------------------------------------------ host staging
+
+// Inputs: the device reads the mapped pinned block (16-byte vectors, grid-strided).
+__global__ void k_stage_in(const uint4* __restrict__ src, uint4* __restrict__ dst, size_t n16) {
+  const size_t step = size_t(gridDim.x) * blockDim.x;
+  for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += step)
+    dst[i] = src[i];
+}
+
+// Results: every block writes its share into the mapped pinned block and fences at system
+// scope; the last block to finish (a device counter, reset by that block) raises the flag.
+struct StageOutArgs {
+  const uint4* src[3];
+  uint4* dst[3];
+  size_t n16[3];
+  int n;
+  uint32_t* counter;
+  uint32_t* flag;
+  uint32_t seq;
+};
+
+__global__ void k_stage_out(StageOutArgs a) {
+  const size_t step = size_t(gridDim.x) * blockDim.x;
+  for (int r = 0; r < a.n; ++r)
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < a.n16[r]; i += step)
+      a.dst[r][i] = a.src[r][i];
+  __threadfence_system();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t before =
+        __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (before == gridDim.x - 1) {
+      __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __threadfence_system();
+      __hip_atomic_store(a.flag, a.seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  }
+}
+
+// Grows the pinned block to `host` bytes and the device block to kStageAlign + `dev` bytes.
+// An outgrown pinned block stays allocated until the context ends (a kernel may have read
+// it); an outgrown device block is freed once the stream has drained.
+static int StageReserve(Ctx* c, size_t host, size_t dev, hipStream_t s) {
+  if (host > c->stage_h_cap) {
+    const size_t want = std::max<size_t>(host + host / 2, size_t(1) << 20);
+    uint8_t* h = nullptr;
+    uint8_t* hd = nullptr;
+    hipError_t e = hipHostMalloc(reinterpret_cast<void**>(&h), want,
+                                 hipHostMallocMapped | hipHostMallocCoherent);
+    if (e == hipSuccess) e = hipHostGetDevicePointer(reinterpret_cast<void**>(&hd), h, 0);
+    if (e != hipSuccess) {
+      if (h != nullptr) (void)hipHostFree(h);
+      return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                      std::string("staging (host): ") + hipGetErrorString(e));
+    }
+    if (c->stage_h != nullptr) c->stage_h_retired.push_back(c->stage_h);
+    c->stage_h = h;
+    c->stage_h_dev = hd;
+    c->stage_h_cap = want;
+  }
+  if (kStageAlign + dev > c->stage_d_cap) {
+    const size_t want = kStageAlign + std::max<size_t>(dev + dev / 2, size_t(1) << 20);
+    if (c->stage_d != nullptr) {
+      VDBG_HIP(hipStreamSynchronize(s));
+      VDBG_HIP(hipFree(c->stage_d));
+      c->stage_d = nullptr;
+      c->stage_d_cap = 0;
+    }
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&c->stage_d), want);
+    if (e == hipSuccess) e = hipMemset(c->stage_d, 0, kStageAlign);  // the completion counter
+    if (e != hipSuccess) {
+      if (c->stage_d != nullptr) (void)hipFree(c->stage_d);
+      c->stage_d = nullptr;
+      return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
+                      std::string("staging (device): ") + hipGetErrorString(e));
+    }
+    c->stage_d_cap = want;
+  }
+  return kOk;
+}
+
+int StageIn(Ctx* c, const void* const* src, const size_t* bytes, int nin, size_t out,
+            hipStream_t s, uint8_t** dev) {
+  size_t in = 0;
+  for (int i = 0; i < nin; ++i) in += StageSpan(bytes[i]);
+  VDBG_RETURN_IF_ERROR(StageReserve(c, std::max(in, out), in + out, s));
+  uint8_t* h = c->stage_h;
+  for (int i = 0; i < nin; ++i) {
+    if (bytes[i] > 0) std::memcpy(h, src[i], bytes[i]);
+    std::memset(h + bytes[i], 0, StageSpan(bytes[i]) - bytes[i]);
+    h += StageSpan(bytes[i]);
+  }
+  uint8_t* base = c->stage_d + kStageAlign;
+  const size_t n16 = in / 16;
+  const unsigned blocks = unsigned(std::min<size_t>(256, (n16 + 255) / 256));
+  k_stage_in<<<blocks, 256, 0, s>>>(reinterpret_cast<const uint4*>(c->stage_h_dev),
+                                    reinterpret_cast<uint4*>(base), n16);
+  VDBG_HIP(hipGetLastError());
+  *dev = base;
+  return kOk;
+}
+
+int StageOut(Ctx* c, const uint8_t* const* src, const size_t* bytes, void* const* dst, int nout,
+             hipStream_t s) {
+  if (nout < 1 || nout > 3) return SetError(kInternal, "StageOut: 1 to 3 regions");
+  // the results land at the start of the pinned block (the inputs there have been read: the
+  // copy-in kernel ran before everything queued after it)
+  StageOutArgs a{};
+  a.n = nout;
+  size_t off = 0, total16 = 0;
+  for (int r = 0; r < nout; ++r) {
+    a.src[r] = reinterpret_cast<const uint4*>(src[r]);
+    a.dst[r] = reinterpret_cast<uint4*>(c->stage_h_dev + off);
+    a.n16[r] = (bytes[r] + 15) / 16;
+    total16 += a.n16[r];
+    off += StageRound(bytes[r]);
+  }
+  VDBG_RETURN_IF_ERROR(StageReserve(c, off, 0, s));  // (reserved by StageIn already)
+  a.counter = reinterpret_cast<uint32_t*>(c->stage_d);
+  std::lock_guard<std::mutex> g(c->flag_mu);
+  a.flag = c->host_flag_dev;
+  a.seq = NextFlagSeq(c);
+  const unsigned blocks = unsigned(std::max<size_t>(1, std::min<size_t>(64, (total16 + 255) / 256)));
+  k_stage_out<<<blocks, 256, 0, s>>>(a);
+  VDBG_HIP(hipGetLastError());
+  bool seen = false;
+  for (uint32_t spin = 0; !seen; ++spin) {
+    if (__atomic_load_n(&c->host_flag[0], __ATOMIC_ACQUIRE) == a.seq) {
+      seen = true;
+      break;
+    }
+    if ((spin & 1023u) == 1023u) {  // has the stream ended or failed?
+      const hipError_t q = hipStreamQuery(s);
+      if (q != hipErrorNotReady) {
+        VDBG_HIP(q);
+        if (__atomic_load_n(&c->host_flag[0], __ATOMIC_ACQUIRE) == a.seq) {
+          seen = true;
+          break;
+        }
+        // the stream is done but the flag did not show: copy the results the slow way
+        for (int r = 0; r < nout; ++r)
+          VDBG_HIP(hipMemcpy(dst[r], src[r], bytes[r], hipMemcpyDeviceToHost));
+        return kOk;
+      }
+    }
+    __builtin_ia32_pause();
+  }
+  off = 0;
+  for (int r = 0; r < nout; ++r) {
+    std::memcpy(dst[r], c->stage_h + off, bytes[r]);
+    off += StageRound(bytes[r]);
+  }
+  return kOk;
+}
+
 int Workspace::reserve(size_t bytes) {
   if (bytes <= cap) return kOk;
   if (fixed)
@@ -348,8 +503,8 @@ __global__ void k_pad_results(uint32_t* ids, float* d, size_t n) {
 
 static int RerankChecked(Ctx* c, Dataset* d, const float* Q, size_t nq, const uint32_t* cand,
                          size_t depth, size_t k, uint32_t* out_ids, float* out_d,
-                         uint64_t* dist_comps, hipStream_t s) {
-  if (depth > 0) {
+                         uint64_t* dist_comps, hipStream_t s, bool host_checked = false) {
+  if (depth > 0 && !host_checked) {
     int* bad = nullptr;
     VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&bad), sizeof(int), s));
     VDBG_HIP(hipMemsetAsync(bad, 0, sizeof(int), s));
@@ -552,6 +707,9 @@ int vdbg_ctx_destroy(vdbg_ctx* ctx) {
   if (c.wcomb_done) (void)hipEventDestroy(c.wcomb_done);
   if (c.wsc_done) (void)hipEventDestroy(c.wsc_done);
   if (c.host_pinned) (void)hipHostFree(c.host_pinned);
+  if (c.stage_h) (void)hipHostFree(c.stage_h);
+  for (uint8_t* h : c.stage_h_retired) (void)hipHostFree(h);
+  if (c.stage_d) (void)hipFree(c.stage_d);
   if (c.fb_dev) (void)hipFree(c.fb_dev);
   if (c.host_flag) (void)hipHostFree(c.host_flag);
   (void)hipStreamDestroy(c.stream);
@@ -814,9 +972,9 @@ int vdbg_flat_search_host(vdbg_dataset* ds, const float* queries, size_t nq, siz
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
   Dataset* d = &ds->d;
-  int rc = StageHost(c, d->n, d->pd, queries, nq, k, allow_words, out_ids, out_dists,
+  int rc = StageHost(c, d->n, d->pd, queries, nq, k, allow_words, out_ids, out_dists, nullptr,
                      [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
-                         hipStream_t s) {
+                         uint64_t*, hipStream_t s) {
                        return ScanMasked(c, &d->src, dq, nq, k, dm, di, dd, s);
                      });
   if (rc == kOk && dist_comps) *dist_comps = uint64_t(nq) * d->n;
@@ -1059,24 +1217,18 @@ int vdbg_sq8_hnsw_search_host(vdbg_sq8* sq, const float* queries, size_t nq, siz
     }
     return kOk;
   }
-  // Rerank of every query's beam on the GPU (hnsw_index.cc:93-94, index.cc:89-95)
+  // Rerank of every query's beam on the GPU (hnsw_index.cc:93-94, index.cc:89-95): the
+  // queries and the beams go in through the staging block
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
-  hipStream_t s = c->stream;
-  uint32_t* dcand = nullptr;
-  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dcand), nq * kk * 4, s));
-  hipError_t e = hipMemcpyAsync(dcand, cand.data(), nq * kk * 4, hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) {
-    (void)hipFreeAsync(dcand, s);
-    return SetError(kInternal, std::string("candidates: ") + hipGetErrorString(e));
-  }
-  const int rc = StageHost(c, d.n, d.pd, queries, nq, k, nullptr, out_ids, out_dists,
-                           [&](const float* dq, const uint64_t*, uint32_t* di, float* dd,
-                               hipStream_t st) {
-                             return Rerank(c, d.rows, int(d.pd), d.metric, dq, nq, dcand, kk,
-                                           k, di, dd, st, &d.src);
-                           });
-  (void)hipFreeAsync(dcand, s);
+  const int rc = StageRegions(c, queries, nq * d.pd * 4, cand.data(), nq * kk * 4, nq, k,
+                              out_ids, out_dists, nullptr,
+                              [&](const float* dq, const void* dx, uint32_t* di, float* dd,
+                                  uint64_t*, hipStream_t st) {
+                                return Rerank(c, d.rows, int(d.pd), d.metric, dq, nq,
+                                              static_cast<const uint32_t*>(dx), kk, k, di, dd,
+                                              st, &d.src);
+                              });
   if (rc == kOk && dist_comps != nullptr)
     for (size_t i = 0; i < nq; ++i) dist_comps[i] = dc[i] + found[i];
   return rc;
@@ -1209,8 +1361,9 @@ int vdbg_sq8_search_host(vdbg_sq8* sq, const float* queries, size_t nq, size_t k
   VDBG_HIP(hipSetDevice(c->device));
   Sq8Index* x = &sq->q;
   int rc = StageHost(c, x->ds->n, x->ds->pd, queries, nq, k, allow_words, out_ids, out_dists,
+                     nullptr,
                      [&](const float* dq, const uint64_t* dm, uint32_t* di, float* dd,
-                         hipStream_t s) {
+                         uint64_t*, hipStream_t s) {
                        return Sq8Search(x, dq, nq, k, depth, dm, di, dd, s);
                      });
   if (rc == kOk && dist_comps)
@@ -1250,25 +1403,15 @@ int vdbg_rerank_host(vdbg_dataset* ds, const float* queries, size_t nq, const ui
   Ctx* c = d->ctx;
   std::lock_guard<std::recursive_mutex> g(c->mu);
   VDBG_HIP(hipSetDevice(c->device));
-  hipStream_t s = c->stream;
-  uint32_t* dcand = nullptr;
-  uint64_t* ddc = nullptr;
-  const size_t nc = std::max<size_t>(nq * depth, 1);
-  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&dcand), nc * 4, s));
-  if (dist_comps != nullptr) VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&ddc), nq * 8, s));
-  if (depth > 0) VDBG_HIP(hipMemcpyAsync(dcand, cand, nq * depth * 4, hipMemcpyHostToDevice, s));
-  int rc = StageHost(c, d->n, d->pd, queries, nq, k, nullptr, out_ids, out_dists,
-                     [&](const float* dq, const uint64_t*, uint32_t* di, float* dd,
-                         hipStream_t st) {
-                       return RerankChecked(c, d, dq, nq, dcand, depth, k, di, dd, ddc, st);
-                     });
-  if (rc == kOk && ddc != nullptr) {
-    VDBG_HIP(hipMemcpyAsync(dist_comps, ddc, nq * 8, hipMemcpyDeviceToHost, s));
-    VDBG_HIP(hipStreamSynchronize(s));
-  }
-  (void)hipFreeAsync(dcand, s);
-  if (ddc != nullptr) (void)hipFreeAsync(ddc, s);
-  return rc;
+  // (a zero-length candidate region still gets a device address: RerankChecked reads none)
+  static const uint32_t kNone = kNoId;
+  return StageRegions(c, queries, nq * d->pd * 4, depth > 0 ? static_cast<const void*>(cand) : &kNone,
+                      depth > 0 ? nq * depth * 4 : 4, nq, k, out_ids, out_dists, dist_comps,
+                      [&](const float* dq, const void* dx, uint32_t* di, float* dd,
+                          uint64_t* ddc, hipStream_t st) {
+                        return RerankChecked(c, d, dq, nq, static_cast<const uint32_t*>(dx),
+                                             depth, k, di, dd, ddc, st, true);
+                      });
 }
 
 int vdbg_last_gemm_bits(vdbg_ctx* ctx) {

@@ -116,6 +116,15 @@ struct Ctx {
   uint32_t* host_flag = nullptr;
   uint32_t* host_flag_dev = nullptr;
   uint32_t flag_seq = 0;
+  // StageHost's blocks: pinned host memory mapped into the device (coherent: the device's
+  // writes reach the host without a copy engine), outgrown host blocks (freed with the
+  // context), and the device block ([256-byte completion counter][inputs][outputs])
+  uint8_t* stage_h = nullptr;
+  uint8_t* stage_h_dev = nullptr;
+  size_t stage_h_cap = 0;
+  std::vector<uint8_t*> stage_h_retired;
+  uint8_t* stage_d = nullptr;
+  size_t stage_d_cap = 0;
   std::mutex flag_mu;  // one readback through host_flag at a time (scan lanes may run on
                        // worker threads of one call)
   std::mutex prof_mu;  // guards pending / free_events against those threads
@@ -454,47 +463,70 @@ size_t SampleBytes(const ScanSource& src, uint32_t smax);
 int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf);
 void FreeSample(ScanSource* src);
 
-// Host-pointer staging shared by the _host entry points: copies queries (and the filter)
-// in, runs `fn` on device pointers, copies results out and synchronises.
+// Host-pointer staging shared by the _host entry points.  The host writes the queries (and
+// the filter words) into the context's pinned, mapped, coherent block; one kernel copies them
+// to the device block; `fn` runs on device pointers; one kernel writes the results back into
+// the pinned block and then raises host_flag, which the host polls (no allocation, no
+// pageable copy and no stream synchronisation per call).  Regions start on 256-byte bounds.
+constexpr size_t kStageAlign = 256;
+inline size_t StageRound(size_t b) { return (b + kStageAlign - 1) & ~(kStageAlign - 1); }
+// The bytes an input region of b bytes takes: at least one zero word past its end.
+inline size_t StageSpan(size_t b) { return StageRound(b + 8); }
+// Copies the nin host regions src[i] (bytes[i] each, zero-padded to StageSpan) into the
+// device block back to back from its base, after reserving `out` more bytes for results;
+// *dev receives the device block's base.
+int StageIn(Ctx* c, const void* const* src, const size_t* bytes, int nin, size_t out,
+            hipStream_t s, uint8_t** dev);
+// Copies the nout <= 3 device regions src[i] (inside the device block) to the host pointers
+// dst[i] after the work queued on s, through the pinned block.
+int StageOut(Ctx* c, const uint8_t* const* src, const size_t* bytes, void* const* dst, int nout,
+             hipStream_t s);
+
+// The general form: nq queries of qb bytes in all, an optional second input region (extra,
+// eb bytes: filter words or candidate lists), nq x k results, and per-query counts when
+// dist_comps is non-null; fn(dq, dextra, di, dd, ddc, s) runs on the device copies (dextra,
+// ddc null when absent).
+template <class Fn>
+inline int StageRegions(Ctx* c, const float* queries, size_t qb, const void* extra, size_t eb,
+                        size_t nq, size_t k, uint32_t* out_ids, float* out_dists,
+                        uint64_t* dist_comps, Fn fn) {
+  hipStream_t s = c->stream;
+  const size_t ob = nq * k * 4;
+  const size_t cb = dist_comps ? nq * sizeof(uint64_t) : 0;
+  const void* src[2] = {queries, extra};
+  const size_t bytes[2] = {qb, eb};
+  uint8_t* base = nullptr;
+  VDBG_RETURN_IF_ERROR(StageIn(c, src, bytes, extra ? 2 : 1,
+                               2 * StageRound(ob) + StageRound(cb), s, &base));
+  const size_t in_end = StageSpan(qb) + (extra ? StageSpan(eb) : 0);
+  const float* dq = reinterpret_cast<const float*>(base);
+  const void* dx = extra ? static_cast<const void*>(base + StageSpan(qb)) : nullptr;
+  uint32_t* di = reinterpret_cast<uint32_t*>(base + in_end);
+  float* dd = reinterpret_cast<float*>(base + in_end + StageRound(ob));
+  uint64_t* ddc = dist_comps ? reinterpret_cast<uint64_t*>(base + in_end + 2 * StageRound(ob))
+                             : nullptr;
+  VDBG_RETURN_IF_ERROR(fn(dq, dx, di, dd, ddc, s));
+  const uint8_t* osrc[3] = {reinterpret_cast<const uint8_t*>(di),
+                            reinterpret_cast<const uint8_t*>(dd),
+                            reinterpret_cast<const uint8_t*>(ddc)};
+  const size_t obytes[3] = {ob, ob, cb};
+  void* const odst[3] = {out_ids, out_dists, dist_comps};
+  return StageOut(c, osrc, obytes, odst, dist_comps ? 3 : 2, s);
+}
+
+// Queries of pd floats over an n_rows source with optional dense allow words (ceil(n/64)
+// words, one zero word past them on the device); fn(dq, dm, di, dd, ddc, s).
 template <class Fn>
 inline int StageHost(Ctx* c, size_t n_rows, size_t pd, const float* queries, size_t nq,
                      size_t k, const uint64_t* allow_words, uint32_t* out_ids,
-                     float* out_dists, Fn fn) {
-  hipStream_t s = c->stream;
-  const size_t words = (n_rows + 63) / 64;
-  float* dq = nullptr;
-  uint64_t* dm = nullptr;
-  uint32_t* di = nullptr;
-  float* dd = nullptr;
-  auto cleanup = [&]() {
-    (void)hipFreeAsync(dq, s);
-    (void)hipFreeAsync(dm, s);
-    (void)hipFreeAsync(di, s);
-    (void)hipFreeAsync(dd, s);
-  };
-  hipError_t e = hipMallocAsync(reinterpret_cast<void**>(&dq), nq * pd * sizeof(float), s);
-  if (e == hipSuccess && allow_words)
-    e = hipMallocAsync(reinterpret_cast<void**>(&dm), words * sizeof(uint64_t) + 8, s);
-  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&di), nq * k * 4, s);
-  if (e == hipSuccess) e = hipMallocAsync(reinterpret_cast<void**>(&dd), nq * k * 4, s);
-  if (e == hipSuccess)
-    e = hipMemcpyAsync(dq, queries, nq * pd * sizeof(float), hipMemcpyHostToDevice, s);
-  if (e == hipSuccess && allow_words)
-    e = hipMemcpyAsync(dm, allow_words, words * sizeof(uint64_t), hipMemcpyHostToDevice, s);
-  if (e != hipSuccess) {
-    cleanup();
-    return SetError(e == hipErrorOutOfMemory ? kResourceExhausted : kInternal,
-                    std::string("staging: ") + hipGetErrorString(e));
-  }
-  int rc = fn(dq, allow_words ? dm : nullptr, di, dd, s);
-  if (rc == kOk) {
-    e = hipMemcpyAsync(out_ids, di, nq * k * 4, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipMemcpyAsync(out_dists, dd, nq * k * 4, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) rc = SetError(kInternal, std::string("copy-out: ") + hipGetErrorString(e));
-  }
-  cleanup();
-  return rc;
+                     float* out_dists, uint64_t* dist_comps, Fn fn) {
+  const size_t wb = allow_words ? ((n_rows + 63) / 64) * sizeof(uint64_t) : 0;
+  return StageRegions(c, queries, nq * pd * sizeof(float), allow_words, wb, nq, k, out_ids,
+                      out_dists, dist_comps,
+                      [&](const float* dq, const void* dx, uint32_t* di, float* dd,
+                          uint64_t* ddc, hipStream_t s) {
+                        return fn(dq, static_cast<const uint64_t*>(dx), di, dd, ddc, s);
+                      });
 }
 
 // Copies n <= 64 32-bit counters from device memory to c->host_pinned[0..n) after the work
