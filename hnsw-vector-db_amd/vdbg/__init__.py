@@ -138,6 +138,14 @@ _SIGS = {
     "vdbg_merge_parts_host": (C.c_int, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _sz, _vp, _vp, _vp]),
     "vdbg_merge_parts_device": (C.c_int, [_vp, _sz, _sz, _sz, _vp, _vp, _vp, _vp, _vp, _vp,
                                           _vp]),
+    "vdbg_coalescer_create_flat": (C.c_int, [_vp, _sz, C.c_uint32, C.POINTER(_vp)]),
+    "vdbg_coalescer_create_sq8": (C.c_int, [_vp, _sz, C.c_uint32, C.POINTER(_vp)]),
+    "vdbg_coalescer_create_sq8_hnsw": (C.c_int, [_vp, _sz, C.c_uint32, C.POINTER(_vp)]),
+    "vdbg_coalescer_create_ivfpq": (C.c_int, [_vp, _sz, C.c_uint32, C.POINTER(_vp)]),
+    "vdbg_coalescer_create_pqflat": (C.c_int, [_vp, _sz, C.c_uint32, C.POINTER(_vp)]),
+    "vdbg_coalescer_search": (C.c_int, [_vp, _vp, _sz, _sz, C.c_int, _vp, _vp, _vp, _vp]),
+    "vdbg_coalescer_stats": (C.c_int, [_vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]),
+    "vdbg_coalescer_destroy": (C.c_int, [_vp]),
 }
 for _name, (_res, _args) in _SIGS.items():
     _f = getattr(lib, _name)
@@ -652,6 +660,60 @@ class PqFlatIndex:
                       dc_ptr=None, stream=None):
         _check(lib.vdbg_pqflat_search_device(self.h, q_ptr, nq, k, rerank, allow_ptr, ids_ptr,
                                              dists_ptr, dc_ptr, stream))
+
+
+class Coalescer:
+    """Concurrent one-query searches of one index gathered into device batches
+    (vdbg_coalescer_*).  index: a Dataset (flat), Sq8Index (scan, or the HNSW walk with
+    hnsw=True), IvfPqIndex or PqFlatIndex.  search() may be called from many threads at once
+    (ctypes releases the GIL for the call); each call returns what the index's one-query
+    search returns."""
+
+    def __init__(self, index, max_batch=16, max_wait_us=50, hnsw=False):
+        h = _vp()
+        if isinstance(index, Dataset):
+            fn, self.pd = lib.vdbg_coalescer_create_flat, index.pd
+        elif isinstance(index, Sq8Index):
+            fn = lib.vdbg_coalescer_create_sq8_hnsw if hnsw else lib.vdbg_coalescer_create_sq8
+            self.pd = index.ds.pd
+        elif isinstance(index, IvfPqIndex):
+            fn, self.pd = lib.vdbg_coalescer_create_ivfpq, index.ds.pd
+        elif isinstance(index, PqFlatIndex):
+            fn, self.pd = lib.vdbg_coalescer_create_pqflat, index.ds.pd
+        else:
+            raise TypeError("unsupported index type")
+        _check(fn(index.h, max_batch, max_wait_us, C.byref(h)))
+        self.index, self.h = index, h
+
+    def search(self, query, k, param=0, rerank=0, allow=None):
+        """One query (pd floats): (ids uint32 [k], dists float32 [k], dist_comps)."""
+        q = np.ascontiguousarray(query, np.float32).reshape(-1)
+        assert q.size == self.pd
+        ids = np.empty(k, np.uint32)
+        d = np.empty(k, np.float32)
+        dc = C.c_uint64()
+        if allow is not None:
+            assert allow.dtype == np.uint64 and allow.flags.c_contiguous
+        _check(lib.vdbg_coalescer_search(self.h, _ptr(q), k, param, rerank, _ptr(allow),
+                                         _ptr(ids), _ptr(d), C.byref(dc)))
+        return ids, d, dc.value
+
+    def stats(self):
+        """(batches, queries) run so far."""
+        b, q = C.c_uint64(), C.c_uint64()
+        _check(lib.vdbg_coalescer_stats(self.h, C.byref(b), C.byref(q)))
+        return b.value, q.value
+
+    def close(self):
+        if self.h:
+            _check(lib.vdbg_coalescer_destroy(self.h))
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 class SearchParams(C.Structure):

@@ -579,6 +579,50 @@ int vdbg_collection_search_device(vdbg_ctx* ctx, const vdbg_segment* segs, size_
                                   uint64_t* out_ids, float* out_dists, uint64_t* dist_comps,
                                   int* seg_plans, void* stream);
 
+/* ---------------------------------------------------------------- coalesced one-query calls */
+
+/* vdb searches an index with one query per call: CollectionImpl::SearchBatch gives each query
+ * to a pool worker (src/engine/collection_impl.cc:1120-1130) and CollectionImpl::Search runs
+ * Index::search (src/index/index.h:36-55) on every segment for it (:1060-1073), so these
+ * calls arrive concurrently from many host threads.  A coalescer gathers concurrent calls on
+ * one index that share k, the index parameters and the allow-words pointer into one device
+ * batch of that index's *_host entry point.  The first call of a batch leads it; the batch
+ * closes when it holds max_batch queries, or once max_wait_us has passed since it opened and
+ * the coalescer's previous batch has left the device (so batches grow while one runs; 0 =
+ * close as soon as the device is free).  Every query of a batch is searched independently:
+ * each call returns exactly what the one-query *_host call returns (ids, distances, and its
+ * IndexSearchStats::distance_computations in dist_comps).  Thread-safe; a call blocks until
+ * its batch is done.  max_batch in 1..4096, max_wait_us at most 1,000,000.  The coalescer
+ * holds the index pointer: destroy it before the index.  No counterpart in vdb (its indexes
+ * are called directly); for the Index adapters of GPU-resident indexes. */
+typedef struct vdbg_coalescer vdbg_coalescer;
+int vdbg_coalescer_create_flat(vdbg_dataset* ds, size_t max_batch, uint32_t max_wait_us,
+                               vdbg_coalescer** out);
+/* SQ8 scan (vdbg_sq8_search_host; param = rerank depth). */
+int vdbg_coalescer_create_sq8(vdbg_sq8* sq, size_t max_batch, uint32_t max_wait_us,
+                              vdbg_coalescer** out);
+/* HNSW-SQ8 walk + GPU rerank (vdbg_sq8_hnsw_search_host; param = ef, rerank as there). */
+int vdbg_coalescer_create_sq8_hnsw(vdbg_sq8* sq, size_t max_batch, uint32_t max_wait_us,
+                                   vdbg_coalescer** out);
+/* IVF-PQ (vdbg_ivfpq_search_host; param = nprobe, rerank as there). */
+int vdbg_coalescer_create_ivfpq(vdbg_ivfpq* ix, size_t max_batch, uint32_t max_wait_us,
+                                vdbg_coalescer** out);
+/* PQ-flat (vdbg_pqflat_search_host; rerank as there). */
+int vdbg_coalescer_create_pqflat(vdbg_pqflat* ix, size_t max_batch, uint32_t max_wait_us,
+                                 vdbg_coalescer** out);
+/* One query (padded_dim floats, host) through the coalescer: k nearest ids and distances
+ * (host, k each, UINT32_MAX / +inf padded as the *_host call pads), dist_comps (nullable) the
+ * query's distance computations.  param and rerank as the index's create call names them
+ * (ignored where the index has none); allow_words as the *_host call takes them, and calls
+ * passing the same pointer share batches (the words must not change while calls use them). */
+int vdbg_coalescer_search(vdbg_coalescer* co, const float* query, size_t k, size_t param,
+                          int rerank, const uint64_t* allow_words, uint32_t* out_ids,
+                          float* out_dists, uint64_t* dist_comps);
+/* Batches run so far and the queries they held (their mean size is queries / batches). */
+int vdbg_coalescer_stats(vdbg_coalescer* co, uint64_t* batches, uint64_t* queries);
+/* FailedPrecondition while calls are inside vdbg_coalescer_search. */
+int vdbg_coalescer_destroy(vdbg_coalescer* co);
+
 #ifdef __cplusplus
 }
 #endif
