@@ -15,6 +15,13 @@ Workload (one "step" = one batch search over data resident in HBM):
           in 8 segments of 625,000, 2% of rows deleted, a filter passing 1%, 10% or 50% of
           rows; 4,096 raw queries go through PrepareQuery, the filtered exact scan of every
           segment and the cross-segment merge.
+  hnsw_sq8  vdb's HNSW-SQ8 index (a VDBHSQ81 file built by vdb's own code over 320,000 of the
+          rows): the graph walk on host threads and the beams reranked on the GPU, batched and
+          one query per call, against the reference's HnswSq8Index::search.
+  pqflat  the PQ flat scan (m = 16) over the 1M rows, against PqFlatIndex::search.
+  append  appends of one and 100 rows to an appendable dataset, alone and beside searches.
+  per_query  one-query calls from 16, 32 and 64 native threads (tests/cpp/per_query_load)
+          through the coalescer, and direct one-query calls for comparison.
 The flat path also records batch sizes 1, 64 and 1,024 and k = 100 at the full batch.
 Queries, rows, codes and lists are resident before the timed region.  Each path's dominant
 kernel is timed with HIP events on the stream it runs on; its roofline fraction uses the
@@ -26,6 +33,7 @@ results on that sample are compared with it.
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -425,6 +433,36 @@ def run_pqflat(args, ctx, torch, ref, ds, base, queries, threads, cpu_model):
     return r
 
 
+def run_per_query(args):
+    """vdb's per-query path: pool workers each call Index::search with one query
+    (collection_impl.cc:1120-1130).  tests/cpp/per_query_load drives T native threads of
+    one-query calls on a 1M x 128 integer-row flat dataset of its own (k = 10), through the
+    coalescer (vdbg_coalescer_search) and, for comparison, as direct one-query host calls;
+    every answer of its first pass is checked against one batched call."""
+    drv = os.path.join(ROOT, "tests", "cpp", "per_query_load")
+    if not os.path.exists(drv):
+        log("per_query: tests/cpp/per_query_load is not built")
+        return None
+    out = {}
+    for name, extra in (("direct_16_threads", ["--direct", "--threads", "16"]),
+                        ("coalesced_16_threads", ["--threads", "16", "--max-batch", "16"]),
+                        ("coalesced_32_threads", ["--threads", "32", "--max-batch", "32"]),
+                        ("coalesced_64_threads", ["--threads", "64", "--max-batch", "64"])):
+        r = subprocess.run([drv, "--rows", str(args.n), "--dim", "128", "--k", str(args.k),
+                            "--queries", "2048", "--seconds", "2", "--wait-us", "50", *extra],
+                           capture_output=True, text=True, timeout=300)
+        if r.returncode != 0:
+            raise RuntimeError(f"per_query_load {name}: rc {r.returncode}: {r.stderr[-500:]}")
+        rep = json.loads(r.stdout.strip().splitlines()[-1])
+        out[name] = {"qps": rep["qps"], "mean_batch": rep["mean_batch"],
+                     "differ_from_batch": rep["differ_from_batch"]}
+        log(f"per_query {name}: {rep['qps']:.0f} q/s, mean batch {rep['mean_batch']:.1f}")
+    out["note"] = ("one-query flat calls (1M x 128 integer rows, k = 10) from native threads; "
+                   "differ_from_batch counts queries whose answer differs from the same "
+                   "query's row of one batched call (2,048 checked)")
+    return out
+
+
 def run_append(args, ctx, torch, base):
     """MutableSegment::Append (mutable_segment.cc:24-44) on an appendable dataset: single rows
     (vdb appends one row per upsert) and 100-row calls, alone and while another context
@@ -499,7 +537,7 @@ def main():
     ap.add_argument("--nq", type=int, default=10_000)
     ap.add_argument("--k", type=int, default=10)
     ap.add_argument("--paths", default="flat,flat_uniform,sq8,ivfpq,filtered,hnsw_sq8,pqflat,"
-                                        "append")
+                                        "append,per_query")
     ap.add_argument("--nprobe", type=int, default=64)
     ap.add_argument("--cpu-sample", type=int, default=6400,
                     help="queries in the flat CPU-baseline sample (SQ8 uses half, IVF-PQ all)")
@@ -927,6 +965,10 @@ def main():
                                        cpu_model)
     if "append" in paths:
         results["append"] = run_append(args, ctx, torch, base)
+    if "per_query" in paths:
+        pq = run_per_query(args)
+        if pq is not None:
+            results["per_query"] = pq
 
     if N == 1_000_000 and nq == 10_000 and k == 10:
         for name in ("flat", "sq8", "ivfpq"):
