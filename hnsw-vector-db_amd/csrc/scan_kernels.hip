@@ -2118,6 +2118,233 @@ __global__ __launch_bounds__(kTinyWaves * 64) void k_tiny_scan(TinyArgs a) {
   }
 }
 
+// ================================================================ small batches
+//
+// More than kTinyQ and at most kSmallQ queries over the same rows: k_small_scan replaces
+// k_tiny_scan ahead of the same merge.  Each wave walks its own range of rows in 32-row
+// blocks and scores them against every query at once on int8 MFMA
+// (v_mfma_i32_32x32x32_i8, k_gemm8's operand layout: lane l holds 16 bytes of row l % 32 and
+// of query l % 32, dims 16 (l / 32) + 32 kb onward; its 16 outputs are rows 8 (r / 4) +
+// 4 (l / 32) + r % 4 of the block against query l % 32).  The row bytes load straight from
+// memory in that layout, two blocks ahead of the one multiplied, and the accumulators start
+// from the rows' init8, so u and the key -M u are k_tiny_scan's.  Every lane keeps the
+// kSmallKp smallest (key, row) of the rows it scores for its query, sorted.  The two lanes
+// of a query in a wave merge their lists into one of kSmallKp (a row either dropped is at
+// least its own list's last key, which is at least the merged list's last), and the block's
+// four waves' lists merge into the block's chunk of kSmallBlockKp keys, whose bound is the
+// smaller of that list's last key and every full wave list's last: every row the block
+// left out has a key at least its chunk's bound, so k_tiny_merge's certificate holds as it
+// does over k_tiny_scan's chunks.  Blocks past the scan's prepare the queries, one wave per
+// query.
+constexpr int kSmallQ = 32;
+constexpr int kSmallKp = 4;      // keys a lane keeps
+constexpr int kSmallBlockKp = 8; // keys a block's chunk keeps
+constexpr int kSmallWaves = 4;
+
+// Inserts (key, row) into a sorted list of L whose last entry it beats: into the last slot,
+// then up to its place.
+template <int L>
+__device__ __forceinline__ void small_push(float (&kd)[L], uint32_t (&ki)[L], float key,
+                                           uint32_t row) {
+  kd[L - 1] = key;
+  ki[L - 1] = row;
+#pragma unroll
+  for (int s = L - 1; s > 0; --s) {
+    const bool sw = nb_less(kd[s], ki[s], kd[s - 1], ki[s - 1]);
+    const float td = kd[s];
+    const uint32_t ti = ki[s];
+    kd[s] = sw ? kd[s - 1] : kd[s];
+    ki[s] = sw ? ki[s - 1] : ki[s];
+    kd[s - 1] = sw ? td : kd[s - 1];
+    ki[s - 1] = sw ? ti : ki[s - 1];
+  }
+}
+
+// A scored 32-row block into the lane's list: value r is row rb + 8 (r / 4) + 4 h + r % 4,
+// its key -M u.  The lane's largest u is tested first: nothing of the block enters a list
+// whose last key is below the block's best (ties go by row, so the test is <=).
+template <class V16>
+__device__ __forceinline__ void small_take(const TinyArgs& a, const V16& acc, uint32_t rb,
+                                           uint32_t r1, int h, int M, bool qlive,
+                                           float (&kd)[kSmallKp], uint32_t (&ki)[kSmallKp]) {
+  int m = acc[0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) m = max(m, acc[r]);
+  if (__ballot(qlive && float(-M * m) <= kd[kSmallKp - 1]) == 0) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const uint32_t row = rb + uint32_t(8 * (r >> 2) + 4 * h + (r & 3));
+    const float key = float(-M * acc[r]);
+    if (qlive && row < r1 && row_allowed(a.allow, row) &&
+        nb_less(key, row, kd[kSmallKp - 1], ki[kSmallKp - 1]))
+      small_push(kd, ki, key, row);
+  }
+}
+
+// The two half-wave lists of a query into one (a row either half dropped is at least that
+// half's last key, hence at least the merged list's last), then the block's four waves'
+// lists into the block's list of kSmallBlockKp, written as the block's chunk.  A row a
+// wave dropped is at least that wave's last key and a key the block dropped at least the
+// block list's last, so the chunk's bound is the smaller of the block list's last key and
+// every full wave list's last (+inf when neither holds).  bk / bi: LDS for
+// kSmallWaves x 32 lists, free of other use.
+__device__ __forceinline__ void small_finish(const TinyArgs& a, float (&kd)[kSmallKp],
+                                             uint32_t (&ki)[kSmallKp], int j, int h, int wave,
+                                             bool qlive, float* bk, uint32_t* bi) {
+  float od[kSmallKp];
+  uint32_t oi[kSmallKp];
+#pragma unroll
+  for (int s = 0; s < kSmallKp; ++s) {
+    od[s] = __shfl_xor(kd[s], 32);
+    oi[s] = __shfl_xor(ki[s], 32);
+  }
+  if (h == 0) {
+#pragma unroll
+    for (int s = 0; s < kSmallKp; ++s)
+      if (oi[s] != kNoId && nb_less(od[s], oi[s], kd[kSmallKp - 1], ki[kSmallKp - 1]))
+        small_push(kd, ki, od[s], oi[s]);
+#pragma unroll
+    for (int s = 0; s < kSmallKp; ++s) {
+      bk[(wave * 32 + j) * kSmallKp + s] = kd[s];
+      bi[(wave * 32 + j) * kSmallKp + s] = ki[s];
+    }
+  }
+  __syncthreads();
+  if (wave != 0 || h != 0 || !qlive) return;
+  float md[kSmallBlockKp];
+  uint32_t mi[kSmallBlockKp];
+#pragma unroll
+  for (int s = 0; s < kSmallBlockKp; ++s) {
+    md[s] = s < kSmallKp ? kd[s] : __builtin_inff();
+    mi[s] = s < kSmallKp ? ki[s] : kNoId;
+  }
+  float wb = ki[kSmallKp - 1] == kNoId ? __builtin_inff() : kd[kSmallKp - 1];
+  for (int w = 1; w < kSmallWaves; ++w) {
+    const int o = (w * 32 + j) * kSmallKp;
+    if (bi[o + kSmallKp - 1] != kNoId) wb = fminf(wb, bk[o + kSmallKp - 1]);
+#pragma unroll
+    for (int t = 0; t < kSmallKp; ++t) {
+      const float key = bk[o + t];
+      const uint32_t row = bi[o + t];
+      if (row != kNoId && nb_less(key, row, md[kSmallBlockKp - 1], mi[kSmallBlockKp - 1]))
+        small_push(md, mi, key, row);
+    }
+  }
+  const size_t o = size_t(j) * a.nchunks + blockIdx.x;  // the block's chunk of this query
+#pragma unroll
+  for (int s = 0; s < kSmallBlockKp; ++s)
+    a.part[o * kSmallBlockKp + s] = make_uint2(__float_as_uint(md[s]), mi[s]);
+  a.bound[o] = fminf(wb, mi[kSmallBlockKp - 1] == kNoId ? __builtin_inff()
+                                                        : md[kSmallBlockKp - 1]);
+}
+
+// The query's int8 bytes in the MFMA B layout (q - c8 clamped: a query outside the window
+// fails the merge's fitness test and is re-scanned exactly).
+template <int NKB, class V4>
+__device__ __forceinline__ void small_query(const TinyArgs& a, int j, int h, V4 (&qv)[NKB]) {
+  const float* qr = a.Q + size_t(min(j, a.nq - 1)) * a.pd + 16 * h;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float d = qr[32 * kb + 4 * t + b] - float(a.c8);
+        packed |= uint32_t(uint8_t(int8_t(int(fminf(fmaxf(d, -128.f), 127.f))))) << (8 * b);
+      }
+      qv[kb][t] = int(packed);
+    }
+}
+
+// Each wave's blocks load into registers two blocks ahead of the one multiplied (three
+// block buffers with fixed roles in a three-way unrolled loop: no copies between them).
+// Blocks per CU of k_small_scan (its launch bounds): three up to 128 dims, two at 256.
+constexpr int SmallOccupancy(int pd) { return pd <= 128 ? 3 : 2; }
+
+template <int NKB>
+__global__ __launch_bounds__(kSmallWaves * 64, SmallOccupancy(NKB * 32)) void k_small_scan(
+    TinyArgs a, int scan_blocks) {
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  typedef int v16i __attribute__((ext_vector_type(16)));
+  const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
+  if (int(blockIdx.x) >= scan_blocks) {
+    const int qq = (int(blockIdx.x) - scan_blocks) * kSmallWaves + wave;
+    if (qq < a.nq) (void)query_prep_wave(a.pa, qq);
+    return;
+  }
+  if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
+  const int j = lane & 31, h = lane >> 5;
+  const int M = a.metric == 0 ? 2 : 1;
+  const bool qlive = j < a.nq;
+  constexpr int PD = NKB * 32;
+  v4i qv[NKB];
+  small_query<NKB>(a, j, h, qv);
+  const uint32_t gw = blockIdx.x * kSmallWaves + wave;  // the wave's range of rows
+  const uint32_t r0 = min(a.N, gw * a.chunk_rows), r1 = min(a.N, r0 + a.chunk_rows);
+  float kd[kSmallKp];
+  uint32_t ki[kSmallKp];
+#pragma unroll
+  for (int s = 0; s < kSmallKp; ++s) {
+    kd[s] = __builtin_inff();
+    ki[s] = kNoId;
+  }
+  // one block's row fragments and accumulator starts (rows past the end read the last row;
+  // they are not live)
+  struct Blk {
+    v4i x[NKB];
+    int4 n[4];
+  };
+  auto load = [&](Blk& B, uint32_t rb) {
+    const uint32_t ra = min(rb + uint32_t(j), a.N - 1);
+    const int8_t* xr = a.X8 + size_t(ra) * PD + 16 * h;
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb) B.x[kb] = *reinterpret_cast<const v4i*>(xr + 32 * kb);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t rg = rb + uint32_t(8 * g + 4 * h);
+      if (rg + 3 < a.N) {
+        B.n[g] = *reinterpret_cast<const int4*>(a.init8 + rg);
+      } else {
+        B.n[g] = make_int4(a.init8[min(rg, a.N - 1)], a.init8[min(rg + 1, a.N - 1)],
+                           a.init8[min(rg + 2, a.N - 1)], a.init8[min(rg + 3, a.N - 1)]);
+      }
+    }
+  };
+  const int nblk = int((r1 - r0 + 31) / 32);
+  auto compute = [&](const Blk& B, int b) __attribute__((always_inline)) {
+    const uint32_t rb = r0 + uint32_t(b) * 32;
+    v16i acc;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      acc[4 * g + 0] = B.n[g].x;
+      acc[4 * g + 1] = B.n[g].y;
+      acc[4 * g + 2] = B.n[g].z;
+      acc[4 * g + 3] = B.n[g].w;
+    }
+#pragma unroll
+    for (int kb = 0; kb < NKB; ++kb)
+      acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(B.x[kb], qv[kb], acc, 0, 0, 0);
+    small_take(a, acc, rb, r1, h, M, qlive, kd, ki);
+  };
+  Blk B0, B1, B2;
+  if (nblk > 0) load(B0, r0);
+  if (nblk > 1) load(B1, r0 + 32);
+  for (int b = 0; b < nblk; b += 3) {
+    if (b + 2 < nblk) load(B2, r0 + uint32_t(b + 2) * 32);
+    compute(B0, b);
+    if (b + 1 >= nblk) break;
+    if (b + 3 < nblk) load(B0, r0 + uint32_t(b + 3) * 32);
+    compute(B1, b + 1);
+    if (b + 2 >= nblk) break;
+    if (b + 4 < nblk) load(B1, r0 + uint32_t(b + 4) * 32);
+    compute(B2, b + 2);
+  }
+  __shared__ float bk[kSmallWaves * 32 * kSmallKp];
+  __shared__ uint32_t bi[kSmallWaves * 32 * kSmallKp];
+  small_finish(a, kd, ki, j, h, wave, qlive, bk, bi);
+}
+
 struct TinyMergeArgs {
   PrepArgs pa;            // the query's operands and bound (fit8q set)
   const uint2* part;
@@ -2322,10 +2549,11 @@ static int ThresholdRank(size_t kk, uint32_t S, uint32_t N) {
 }
 
 // Whether a batch takes the tiny-batch path: integer rows with their int8 copy, the int8
-// GEMM on, at most kTinyQ queries, k <= kTinyK, rows of 64, 128 or 256 dims.
+// GEMM on, at most kSmallQ queries (k_tiny_scan up to kTinyQ, k_small_scan above),
+// k <= kTinyK, rows of 64, 128 or 256 dims.
 static bool TinyEligible(const Ctx* c, const ScanSource& src, size_t nq, size_t kk,
                          const Workspace& w) {
-  return nq >= 1 && nq <= size_t(kTinyQ) && kk <= size_t(kTinyK) && src.kind == 0 &&
+  return nq >= 1 && nq <= size_t(kSmallQ) && kk <= size_t(kTinyK) && src.kind == 0 &&
          src.metric <= 1 && src.X8 != nullptr && src.x8_parts == 1 && src.init8 != nullptr &&
          c->fp16_gemm && c->int8_gemm && src.x16_parts == 1 && !src.x16_approx &&
          (src.pd == 64 || src.pd == 128 || src.pd == 256) && src.N >= 1024 && !w.fixed;
@@ -2342,16 +2570,30 @@ static void launch_tiny(hipStream_t s, int blocks, const TinyArgs& a) {
   }
 }
 
+static void launch_small(hipStream_t s, int scan_blocks, int nq, const TinyArgs& a) {
+  const int blocks = scan_blocks + (nq + kSmallWaves - 1) / kSmallWaves;
+  switch (a.pd) {
+    case 64: k_small_scan<2><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a, scan_blocks); break;
+    case 128: k_small_scan<4><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a, scan_blocks); break;
+    default: k_small_scan<8><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a, scan_blocks); break;
+  }
+}
+
 static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                     const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
                     Workspace& W, Workspace& W2) {
   const uint32_t N = src->N;
   const int pd = int(src->pd);
-  const int kp = int(kk) + 9;
-  const int blocks = 2 * c->cu_count;
-  uint32_t chunk = (N + blocks - 1) / blocks;
-  chunk = (chunk + 255) / 256 * 256;
-  const int nchunks = int((N + chunk - 1) / chunk);
+  // k_tiny_scan: a chunk of rows per block, kk + 9 keys each.  k_small_scan: a range of
+  // rows per wave, each block one chunk of kSmallBlockKp keys per query
+  const bool small = nq > size_t(kTinyQ);
+  const int kp = small ? kSmallBlockKp : int(kk) + 9;
+  // k_small_scan: as many blocks as fit the device at once (one round)
+  const int blocks = small ? c->cu_count * SmallOccupancy(pd) : 2 * c->cu_count;
+  const uint32_t units = small ? uint32_t(blocks) * kSmallWaves : uint32_t(blocks);
+  uint32_t chunk = (N + units - 1) / units;
+  chunk = small ? (chunk + 31) / 32 * 32 : (chunk + 255) / 256 * 256;
+  const int nchunks = small ? blocks : int((N + chunk - 1) / chunk);
   WsUse wuse(&W, s);
   VDBG_RETURN_IF_ERROR(wuse.status());
   W.used = 0;
@@ -2377,7 +2619,8 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
               chunk, part, bound, fb_count, nchunks, pa};
   {
     ProfScope ps(c, "flat_gemm", s);
-    if (nq == 1) launch_tiny<1>(s, nchunks, ta);
+    if (small) launch_small(s, blocks, int(nq), ta);
+    else if (nq == 1) launch_tiny<1>(s, nchunks, ta);
     else launch_tiny<2>(s, nchunks, ta);
     VDBG_HIP(hipGetLastError());
   }

@@ -196,9 +196,10 @@ def test_unit_neighbours_tie_within_the_bound(ctx, oracle):
                                          (8, 10, "ip"), (64, 10, "l2"), (128, 20, "l2"),
                                          (1, 10, "ip"), (33, 10, "ip")])
 def test_small_batches_choose_on_device(ctx, oracle, nq, k, metric):
-    # up to 2 queries and k <= 48: the tiny-batch path (one pass over the int8 rows keeping
-    # each chunk's best keys, one merge with the exact re-score and certificate); up to 128
-    # queries: the int8 / fp32 main pass chosen on the device, no host read before it
+    # up to 32 queries and k <= 48: the tiny-batch path (one pass over the int8 rows keeping
+    # each chunk's best keys, one merge with the exact re-score and certificate; k_tiny_scan
+    # up to 2 queries, k_small_scan above); up to 128 queries: the int8 / fp32 main pass
+    # chosen on the device, no host read before it
     base = datagen.sift_like(60000, 128, 6601)
     qs = datagen.sift_like(nq, 128, 6602)
     ds = vdbg.Dataset(ctx, base, 128, metric=metric)
@@ -212,7 +213,7 @@ def test_small_batches_choose_on_device(ctx, oracle, nq, k, metric):
     qf = qs.copy()
     qf[nq - 1, 5] += 0.25
     gi, gd = ds.flat_search(qf, k)
-    if nq <= 2 and k <= 48:
+    if nq <= 32 and k <= 48:
         assert ctx.last_gemm_bits() == 8 and ctx.last_fallbacks() == 1
     else:
         assert ctx.last_gemm_bits() == 32
@@ -274,5 +275,55 @@ def test_tiny_two_queries_edge_chunks(ctx, oracle, pick):
     gi, gd = ds.flat_search(qs, 10)
     assert ctx.last_gemm_bits() == 8
     assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
+
+
+@pytest.mark.parametrize("pd,nq,k,metric", [(128, 3, 10, "l2"), (128, 16, 10, "l2"),
+                                            (128, 32, 48, "l2"), (128, 17, 1, "ip"),
+                                            (64, 9, 10, "l2"), (256, 32, 20, "ip"),
+                                            (64, 32, 48, "ip"), (256, 5, 1, "l2")])
+def test_small_scan_shapes(ctx, oracle, pd, nq, k, metric):
+    # k_small_scan: 3..32 queries scored together on int8 MFMA, every lane a chunk of four
+    # keys for the merge; rows not a multiple of 32 (the last wave's block runs past them)
+    print(f"small scan pd={pd} nq={nq} k={k} {metric}", flush=True)
+    n = 50003
+    base = datagen.sift_like(n, pd, 6631 + pd)
+    qs = datagen.sift_like(nq, pd, 6632 + nq)
+    ds = vdbg.Dataset(ctx, base, pd, metric=metric)
+    gi, gd = ds.flat_search(qs, k)
+    assert ctx.last_gemm_bits() == 8
+    assert ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, k, metric=metric)
+    _check_equal(gi, gd, oi, od)
+
+
+def test_small_scan_edges_filter_and_fallback(ctx, oracle):
+    # nearest rows in the first and the last wave's rows, a filter that leaves most waves
+    # without an allowed row, and the certificate failed on purpose
+    n = 70001
+    base = datagen.sift_like(n, 128, 6641)
+    qs = np.ascontiguousarray(np.concatenate([base[[0, 1, n - 1, n - 2, n // 2]],
+                                              datagen.sift_like(7, 128, 6642)]))
+    ds = vdbg.Dataset(ctx, base, 128)
+    gi, gd = ds.flat_search(qs, 10)
+    assert ctx.last_gemm_bits() == 8 and ctx.last_fallbacks() == 0
+    od, oi = oracle.flat_search(base, qs, 10)
+    _check_equal(gi, gd, oi, od)
+    allowed = np.zeros(n, bool)
+    allowed[30000:30300] = True
+    allowed[::211] = True
+    words = np.zeros((n + 63) // 64, np.uint64)
+    rows = np.nonzero(allowed)[0]
+    np.bitwise_or.at(words, rows // 64, np.uint64(1) << (rows % 64).astype(np.uint64))
+    gi, gd = ds.flat_search(qs, 10, allow=words)
+    od, oi = oracle.flat_search(base, qs, 10, allow=words)
+    _check_equal(gi, gd, oi, od)
+    try:
+        ctx.set_test_fallbacks(1)
+        gi, gd = ds.flat_search(qs, 10)
+        assert ctx.last_fallbacks() == len(qs)
+    finally:
+        ctx.set_test_fallbacks(0)
     od, oi = oracle.flat_search(base, qs, 10)
     _check_equal(gi, gd, oi, od)
