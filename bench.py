@@ -447,7 +447,7 @@ def run_per_query(args):
     for name, extra in (("direct_16_threads", ["--direct", "--threads", "16"]),
                         ("coalesced_16_threads", ["--threads", "16", "--max-batch", "16"]),
                         ("coalesced_32_threads", ["--threads", "32", "--max-batch", "32"]),
-                        ("coalesced_64_threads", ["--threads", "64", "--max-batch", "64"])):
+                        ("coalesced_64_threads", ["--threads", "64", "--max-batch", "32"])):
         r = subprocess.run([drv, "--rows", str(args.n), "--dim", "128", "--k", str(args.k),
                             "--queries", "2048", "--seconds", "2", "--wait-us", "50", *extra],
                            capture_output=True, text=True, timeout=300)

@@ -4,9 +4,10 @@
 // hands each query to a pool worker (src/engine/collection_impl.cc:1120-1130) and Search fans
 // a query out over the segments (:1069-1073), so every call reaching an index is a batch of
 // one.  A coalescer queues concurrent calls that share (k, parameters, allow words) into one
-// batch.  The first caller of a batch leads it: the batch stops taking queries when it holds
-// max_batch of them, or once max_wait has passed since it opened and no earlier batch of this
-// coalescer is still on the device (a batch keeps filling while an earlier one runs).  The
+// batch.  The first caller of a batch leads it: the batch takes queries while an earlier batch
+// of this coalescer is on the device, and then, until every caller of the batch that just left
+// the device has called again or max_wait has passed since it left (those callers can join
+// again); it closes sooner once it holds max_batch queries.  A lone caller never waits.  The
 // leader runs the index's host entry point over the whole batch and every caller copies out
 // its own row.  Queries of a batch are searched independently, so each caller gets what the
 // one-query call returns.
@@ -14,12 +15,15 @@
 #include <atomic>
 #include <chrono>
 #include <condition_variable>
+#include <cstdint>
 #include <cstring>
 #include <memory>
 #include <mutex>
 #include <new>
 #include <string>
 #include <vector>
+
+#include <sys/prctl.h>
 
 #include "vdbg_internal.h"
 
@@ -31,12 +35,21 @@ enum Kind { kFlat = 0, kSq8 = 1, kIvfPq = 2, kPqFlat = 3, kHnswSq8 = 4 };
 
 using Clock = std::chrono::steady_clock;
 
+// The calling thread's timer slack cut to 1 us for a scope (PR_SET_TIMERSLACK), then restored.
+struct TightTimers {
+  int old = prctl(PR_GET_TIMERSLACK, 0, 0, 0, 0);
+  TightTimers() { prctl(PR_SET_TIMERSLACK, 1000, 0, 0, 0); }
+  ~TightTimers() {
+    if (old > 0) prctl(PR_SET_TIMERSLACK, old, 0, 0, 0);
+  }
+};
+
 struct Batch {
+  uint64_t seq = 0;             // a number no other batch of the process has
   // the key every query of the batch shares (written under the coalescer's mutex)
   size_t k = 0, param = 0;
   int rerank = 0;
   const uint64_t* allow = nullptr;
-  Clock::time_point opened;
   std::vector<float> q;         // [n][pd], rows written under the mutex
   std::atomic<size_t> n{0};     // queries joined
   std::atomic<uint32_t> done{0};
@@ -47,6 +60,18 @@ struct Batch {
   std::vector<uint64_t> dc;     // [n]
   std::atomic<size_t> readers{0};  // callers that have not yet taken their row
 };
+
+std::atomic<uint64_t> g_batch_seq{0};
+
+// The last batch this thread took part in, per coalescer (a small direct-mapped table): a
+// call tells its coalescer that a caller of its last batch is back.
+struct Recent {
+  const void* co = nullptr;
+  uint64_t seq = 0;
+};
+thread_local Recent t_recent[8];
+
+Recent& RecentFor(const void* co) { return t_recent[(reinterpret_cast<uintptr_t>(co) >> 6) & 7]; }
 
 }  // namespace
 
@@ -63,6 +88,11 @@ struct vdbg_coalescer {
   uint64_t batches = 0, queries = 0;  // batches run and the queries they held
   std::condition_variable filled;  // a leader waits here for its batch to fill
   std::mutex exec;                // held while a batch of this coalescer is on the device
+  // the batch that last left the device (under mu): its number, its callers, when it left,
+  // and how many of its callers have called again since
+  uint64_t last_seq = 0;
+  size_t last_n = 0, back = 0;
+  Clock::time_point freed{};
 };
 
 namespace {
@@ -168,6 +198,11 @@ int vdbg_coalescer_search(vdbg_coalescer* co, const float* query, size_t k, size
   if (co->kind == kFlat || co->kind == kPqFlat) param = 0;
   std::unique_lock<std::mutex> lk(co->mu);
   ++co->calls;
+  Recent& mine = RecentFor(co);
+  if (mine.co == co && mine.seq != 0 && mine.seq == co->last_seq) {
+    mine.seq = 0;
+    if (++co->back >= co->last_n) co->filled.notify_all();
+  }
   Batch* b = nullptr;
   for (Batch* o : co->open)
     if (o->k == k && o->param == param && o->rerank == rerank && o->allow == allow_words) {
@@ -186,11 +221,11 @@ int vdbg_coalescer_search(vdbg_coalescer* co, const float* query, size_t k, size
         return SetError(kResourceExhausted, "out of host memory");
       }
     }
+    b->seq = g_batch_seq.fetch_add(1, std::memory_order_relaxed) + 1;
     b->k = k;
     b->param = param;
     b->rerank = rerank;
     b->allow = allow_words;
-    b->opened = Clock::now();
     b->n.store(0, std::memory_order_relaxed);
     b->done.store(0, std::memory_order_relaxed);
     b->rc = kOk;
@@ -212,21 +247,39 @@ int vdbg_coalescer_search(vdbg_coalescer* co, const float* query, size_t k, size
     co->filled.notify_all();
   }
   if (lead) {
-    // until the batch is full or its time is up, then until the device is free (joins go on
-    // meanwhile); the batch closes under the mutex, so every row joined is in place
-    co->filled.wait_until(lk, b->opened + co->wait, [&] {
-      return b->n.load(std::memory_order_relaxed) >= co->max_batch;
-    });
-    lk.unlock();
+    // The batch takes joins until the device is free, and then, while callers of the batch
+    // that just left the device have not all called again, until max_wait has passed since it
+    // left (or until full): those callers return just then and may join.  A lone caller, or
+    // one after an idle spell, does not wait.  A timed wait can sleep for the thread's timer
+    // slack (50 us by default) past its deadline, so the slack is cut to 1 us meanwhile.
+    auto ready = [&] {
+      return b->n.load(std::memory_order_relaxed) >= co->max_batch || co->back >= co->last_n;
+    };
     {
-      std::lock_guard<std::mutex> ex(co->exec);
-      lk.lock();
+      std::unique_lock<std::mutex> ex(co->exec, std::try_to_lock);
+      if (!ex.owns_lock()) {
+        lk.unlock();
+        ex.lock();
+        lk.lock();
+      }
+      const Clock::time_point deadline = co->freed + co->wait;
+      if (!ready() && Clock::now() < deadline) {
+        TightTimers tight;
+        co->filled.wait_until(lk, deadline, ready);
+      }
       close();
       ++co->batches;
-      co->queries += b->n.load(std::memory_order_relaxed);
+      const size_t n = b->n.load(std::memory_order_relaxed);
+      co->queries += n;
       lk.unlock();
       b->rc = RunBatch(co, b);
       if (b->rc != kOk) b->err = vdbg_last_error();
+      lk.lock();
+      co->last_seq = b->seq;
+      co->last_n = n;
+      co->back = 0;
+      co->freed = Clock::now();
+      lk.unlock();
     }
     b->done.store(1, std::memory_order_release);
     b->done.notify_all();  // (C++20 atomic wait: each follower sleeps on this word)
@@ -234,6 +287,8 @@ int vdbg_coalescer_search(vdbg_coalescer* co, const float* query, size_t k, size
     lk.unlock();
     b->done.wait(0, std::memory_order_acquire);
   }
+  mine.co = co;
+  mine.seq = b->seq;
   const int rc = b->rc;
   if (rc == kOk) {
     std::memcpy(out_ids, b->ids.data() + slot * k, k * sizeof(uint32_t));

@@ -669,7 +669,7 @@ class Coalescer:
     (ctypes releases the GIL for the call); each call returns what the index's one-query
     search returns."""
 
-    def __init__(self, index, max_batch=16, max_wait_us=50, hnsw=False):
+    def __init__(self, index, max_batch=32, max_wait_us=50, hnsw=False):
         h = _vp()
         if isinstance(index, Dataset):
             fn, self.pd = lib.vdbg_coalescer_create_flat, index.pd

@@ -587,9 +587,10 @@ int vdbg_collection_search_device(vdbg_ctx* ctx, const vdbg_segment* segs, size_
  * calls arrive concurrently from many host threads.  A coalescer gathers concurrent calls on
  * one index that share k, the index parameters and the allow-words pointer into one device
  * batch of that index's *_host entry point.  The first call of a batch leads it; the batch
- * closes when it holds max_batch queries, or once max_wait_us has passed since it opened and
- * the coalescer's previous batch has left the device (so batches grow while one runs; 0 =
- * close as soon as the device is free).  Every query of a batch is searched independently:
+ * takes calls while the coalescer's previous batch is on the device, then until every caller
+ * of that batch has called again or max_wait_us has passed since it left the device (so those
+ * callers can join again; 0 = no such wait), and closes sooner once it holds max_batch
+ * queries.  A lone caller never waits.  Every query of a batch is searched independently:
  * each call returns exactly what the one-query *_host call returns (ids, distances, and its
  * IndexSearchStats::distance_computations in dist_comps).  Thread-safe; a call blocks until
  * its batch is done.  max_batch in 1..4096, max_wait_us at most 1,000,000.  The coalescer

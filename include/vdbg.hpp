@@ -18,6 +18,8 @@
 //   SearchCollection  CollectionImpl::SearchBatch over GpuSegments of any index type with
 //                  SearchDiskSegment's plan per segment (src/engine/planner.cc:42-129), one
 //                  device batch and one merge
+//   Coalescer      concurrent Index::search calls of one index (one query each, from vdb's
+//                  pool workers) answered as device batches, each call's result unchanged
 //
 // Differences, all forced by the device: filters are dense bitmasks (DenseRowFilter) rather
 // than a virtual allowed() per row; searches return a Status (vdb's return void), since a
@@ -170,8 +172,8 @@ class DenseRowFilter {
 
 // ---------------------------------------------------------------- device
 
-// One GPU, its stream and workspace (vdbg_ctx).  Calls on one Device are serialised; use
-// one Device per thread for concurrency.
+// One GPU, its stream and workspace (vdbg_ctx).  Calls on one Device are serialised; for
+// concurrent one-query calls on one index use a Coalescer, or one Device per thread.
 class Device {
  public:
   static Status Open(int ordinal, std::unique_ptr<Device>* out) {
@@ -343,6 +345,7 @@ class GpuSq8Index {
   size_t memory_bytes() const { return code_bytes() + 2 * view_.padded_dim * sizeof(float); }
   const std::vector<float>& vmin() const { return vmin_; }
   const std::vector<float>& scale() const { return scale_; }
+  vdbg_sq8* handle() const { return sq_; }  // nullptr before build()
   Status codes(std::vector<uint8_t>* out) const {
     out->resize(code_bytes());
     return Status::FromCall(vdbg_sq8_codes(sq_, out->data()));
@@ -488,6 +491,7 @@ class GpuIvfPqIndex {
     return s;
   }
   size_t code_bytes() const { return view_.rows * m(); }
+  vdbg_ivfpq* handle() const { return ix_; }  // nullptr before build() or Load()
 
   Status search(const float* q, size_t k, const SearchParams& p, const DenseRowFilter* filter,
                 std::vector<Neighbor>& out, IndexSearchStats* stats) const {
@@ -535,6 +539,85 @@ class GpuIvfPqIndex {
   VectorView view_;
   detail::DatasetPtr ds_;
   vdbg_ivfpq* ix_ = nullptr;
+};
+
+// ---------------------------------------------------------------- coalesced one-query calls
+
+// Concurrent one-query searches of one index gathered into device batches (vdbg_coalescer_*).
+// vdb's pool workers call Index::search once per query (src/engine/collection_impl.cc:
+// 1120-1130); a Coalescer answers each such call with exactly what the index's own search()
+// returns, while concurrent calls that share k, the parameters the index reads and the
+// filter's words pointer run as one batch.  A filter expanded per call has a pointer of its
+// own and runs alone: keep one set of words per segment state (deletes) and pass it as a
+// view.  Destroy the Coalescer before its index.
+class Coalescer {
+ public:
+  struct Options {
+    size_t max_batch = 32;     // queries per device batch, 1..4096
+    uint32_t max_wait_us = 50;  // longest wait for the previous batch's callers to call again
+  };
+  static Status Create(const GpuFlatIndex& ix, const Options& o, std::unique_ptr<Coalescer>* out) {
+    vdbg_coalescer* c = nullptr;
+    const int rc = vdbg_coalescer_create_flat(ix.dataset(), o.max_batch, o.max_wait_us, &c);
+    return Make(Kind::Flat, rc, c, out);
+  }
+  static Status Create(const GpuSq8Index& ix, const Options& o, std::unique_ptr<Coalescer>* out) {
+    vdbg_coalescer* c = nullptr;
+    const int rc = vdbg_coalescer_create_sq8(ix.handle(), o.max_batch, o.max_wait_us, &c);
+    return Make(Kind::Sq8, rc, c, out);
+  }
+  static Status Create(const GpuHnswSq8Index& ix, const Options& o,
+                       std::unique_ptr<Coalescer>* out) {
+    vdbg_coalescer* c = nullptr;
+    const int rc = vdbg_coalescer_create_sq8_hnsw(ix.handle(), o.max_batch, o.max_wait_us, &c);
+    return Make(Kind::HnswSq8, rc, c, out);
+  }
+  static Status Create(const GpuIvfPqIndex& ix, const Options& o, std::unique_ptr<Coalescer>* out) {
+    vdbg_coalescer* c = nullptr;
+    const int rc = vdbg_coalescer_create_ivfpq(ix.handle(), o.max_batch, o.max_wait_us, &c);
+    return Make(Kind::IvfPq, rc, c, out);
+  }
+  // PqFlatIndex (src/index/quant/ivf_pq.cc:59-79) through its C handle (vdbg_pqflat_*).
+  static Status Create(vdbg_pqflat* ix, const Options& o, std::unique_ptr<Coalescer>* out) {
+    vdbg_coalescer* c = nullptr;
+    const int rc = vdbg_coalescer_create_pqflat(ix, o.max_batch, o.max_wait_us, &c);
+    return Make(Kind::PqFlat, rc, c, out);
+  }
+  ~Coalescer() { vdbg_coalescer_destroy(co_); }
+  Coalescer(const Coalescer&) = delete;
+  Coalescer& operator=(const Coalescer&) = delete;
+
+  // The index's search() for one query (padded_dim floats): the same neighbours, order and
+  // distance computations.  Blocks until the query's batch is done.
+  Status search(const float* q, size_t k, const SearchParams& p, const DenseRowFilter* filter,
+                std::vector<Neighbor>& out, IndexSearchStats* stats) const {
+    size_t param = 0;
+    if (kind_ == Kind::Sq8) param = GpuSq8Index::Depth(p, k);
+    if (kind_ == Kind::HnswSq8) param = p.ef;
+    if (kind_ == Kind::IvfPq) param = p.nprobe;
+    std::vector<uint32_t> ids(k);
+    std::vector<float> d(k);
+    uint64_t dc = 0;
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(vdbg_coalescer_search(
+        co_, q, k, param, p.rerank, filter ? filter->words() : nullptr, ids.data(), d.data(), &dc)));
+    out.clear();
+    for (size_t i = 0; i < k && ids[i] != kNoRow; ++i) out.push_back({d[i], ids[i]});
+    if (stats) stats->distance_computations += dc;
+    return Status::OK();
+  }
+  // Batches run so far and the queries they held.
+  void counts(uint64_t* batches, uint64_t* queries) const { vdbg_coalescer_stats(co_, batches, queries); }
+
+ private:
+  enum class Kind { Flat, Sq8, HnswSq8, IvfPq, PqFlat };
+  static Status Make(Kind kind, int rc, vdbg_coalescer* c, std::unique_ptr<Coalescer>* out) {
+    VDBG_CXX_RETURN_IF_ERROR(Status::FromCall(rc));
+    out->reset(new Coalescer(kind, c));
+    return Status::OK();
+  }
+  Coalescer(Kind kind, vdbg_coalescer* co) : kind_(kind), co_(co) {}
+  Kind kind_;
+  vdbg_coalescer* co_;
 };
 
 // ---------------------------------------------------------------- collection read path

@@ -14,6 +14,7 @@
 #include <fstream>
 #include <functional>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/vdbg.hpp"
@@ -767,6 +768,105 @@ void SegmentOpenAndCollectionSearch() {
 
 }  // namespace
 
+// ---------------------------------------------------------------- coalesced one-query calls
+
+// T threads each send one query at a time through a Coalescer, as vdb's pool workers call
+// Index::search; every answer must equal the index's own search() of that query, neighbours,
+// order, distance bits and distance computations.
+template <class Ix>
+void ConcurrentCallsMatch(const Ix& ix, const Data& qs, const std::vector<vdbg::SearchParams>& ps,
+                          const vdbg::DenseRowFilter* filter, size_t max_batch) {
+  std::unique_ptr<vdbg::Coalescer> co;
+  CHECK_OK(vdbg::Coalescer::Create(ix, {max_batch, 20}, &co));
+  struct Call {
+    size_t q, k, p;
+    bool filtered;
+  };
+  std::vector<Call> calls;
+  for (size_t q = 0; q < qs.rows; ++q)
+    for (size_t p = 0; p < ps.size(); ++p)
+      for (size_t k : {size_t(1), size_t(10)})
+        for (bool f : {false, true}) calls.push_back({q, k, p, f && filter != nullptr});
+  std::vector<std::vector<vdbg::Neighbor>> got(calls.size());
+  std::vector<uint64_t> dc(calls.size());
+  std::vector<std::string> errs(16);
+  std::vector<std::thread> pool;
+  for (size_t t = 0; t < 16; ++t)
+    pool.emplace_back([&, t] {
+      for (size_t i = t; i < calls.size(); i += 16) {
+        const Call& c = calls[i];
+        vdbg::IndexSearchStats st;
+        const vdbg::Status s = co->search(qs.row(c.q), c.k, ps[c.p], c.filtered ? filter : nullptr,
+                                          got[i], &st);
+        if (!s.ok()) {
+          errs[t] = s.ToString();
+          return;
+        }
+        dc[i] = st.distance_computations;
+      }
+    });
+  for (auto& t : pool) t.join();
+  for (const auto& e : errs) {
+    CHECK(e.empty());
+    if (!e.empty()) std::fprintf(stderr, "  %s: %s\n", g_test.c_str(), e.c_str());
+  }
+  for (size_t i = 0; i < calls.size(); ++i) {
+    const Call& c = calls[i];
+    std::vector<vdbg::Neighbor> want;
+    vdbg::IndexSearchStats st;
+    CHECK_OK(ix.search(qs.row(c.q), c.k, ps[c.p], c.filtered ? filter : nullptr, want, &st));
+    CHECK(Same(got[i], want));
+    CHECK(dc[i] == st.distance_computations);
+  }
+  uint64_t batches = 0, queries = 0;
+  co->counts(&batches, &queries);
+  CHECK(queries == calls.size() && batches >= 1 && batches <= queries);
+}
+
+void CoalescedCallsMatchSearch() {
+  Data base = Clustered(20000, 64, 40, 21, false), qs = Clustered(40, 64, 40, 22, false);
+  vdbg::DenseRowFilter some(base.rows);
+  for (uint32_t r = 0; r < base.rows; ++r)
+    if (r % 3 != 1) some.Allow(r);
+  {
+    std::unique_ptr<vdbg::GpuFlatIndex> ix;
+    CHECK_OK(vdbg::GpuFlatIndex::Create(*g_dev, vdbg::Metric::L2, base.view(), &ix));
+    ConcurrentCallsMatch(*ix, qs, {vdbg::SearchParams{}}, &some, 8);
+    // and the oracle, for the unfiltered k = 10 answers
+    std::unique_ptr<vdbg::Coalescer> co;
+    CHECK_OK(vdbg::Coalescer::Create(*ix, {}, &co));
+    auto want = OracleFlat(base, qs.v.data(), qs.rows, 10, vdbg::Metric::L2, nullptr);
+    for (size_t q = 0; q < qs.rows; ++q) {
+      std::vector<vdbg::Neighbor> out;
+      CHECK_OK(co->search(qs.row(q), 10, {}, nullptr, out, nullptr));
+      CHECK(Same(out, want[q]));
+    }
+  }
+  {
+    std::unique_ptr<vdbg::GpuSq8Index> ix;
+    CHECK_OK(vdbg::GpuSq8Index::Create(*g_dev, vdbg::Metric::L2, base.view(), &ix));
+    CHECK_OK(ix->build());
+    vdbg::SearchParams a, b;
+    a.ef = 40;
+    b.rerank = 0;
+    ConcurrentCallsMatch(*ix, qs, {a, b}, &some, 16);
+  }
+  {
+    vdbg::IndexOptions opts;
+    opts.nlist = 64;
+    opts.pq_m = 16;
+    std::unique_ptr<vdbg::GpuIvfPqIndex> ix;
+    CHECK_OK(vdbg::GpuIvfPqIndex::Create(*g_dev, opts, vdbg::Metric::L2, base.view(), &ix));
+    CHECK_OK(ix->build());
+    vdbg::SearchParams a, b;
+    a.nprobe = 8;
+    a.rerank = 0;
+    b.nprobe = 16;
+    b.rerank = 50;
+    ConcurrentCallsMatch(*ix, qs, {a, b}, &some, 12);
+  }
+}
+
 int main() {
   std::unique_ptr<vdbg::Device> dev;
   vdbg::Status s = vdbg::Device::Open(0, &dev);
@@ -789,6 +889,7 @@ int main() {
       {"FilteredSearchTest.CollectionSearchMatchesOracleAtEverySelectivity",
        CollectionSearchMatchesOracleAtEverySelectivity},
       {"SegmentTest.OpenFromFilesAndSearchCollection", SegmentOpenAndCollectionSearch},
+      {"CoalescerTest.ConcurrentCallsMatchSearch", CoalescedCallsMatchSearch},
   };
   for (const auto& [name, fn] : tests) {
     g_test = name;
