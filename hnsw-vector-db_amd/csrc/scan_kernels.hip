@@ -25,6 +25,7 @@
 //
 // Distances returned are always the reference's exact AVX-512-order values.
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <type_traits>
@@ -72,19 +73,37 @@ struct Int8Query {
   const uint32_t* ys;    // [pd / 4] packed y8
 };
 
-// Wave-level: decides and packs (ys: pd / 4 words of the wave's LDS, pd <= 1024).
+// Wave-level: decides and packs (ys: pd / 4 words of the wave's LDS, pd <= 1024).  The query
+// is read in rounds of 256 dims, each round's loads issued before any is used (a single
+// round trip up to 256 dims, whose values the packing reuses): dim i is lane i % 64's value
+// (i / 64) % 4 of round i / 256, written to byte i of ys.
 __device__ Int8Query int8_query(const int8_t* X8, int c8, float xlo, float xhi, float xmax,
                                 int xint, int metric, int pd, const float* qv, uint32_t* ys) {
   Int8Query r{0, 0, ys};
   if (X8 == nullptr || !xint || metric == 2 || pd % 16 != 0 || pd > 1024) return r;
+  constexpr int kRound = 4 * kWave;
+  const int lane = lane_id();
+  float v[4];
+  auto load = [&](int base) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = base + lane + j * kWave;
+      v[j] = i < pd ? qv[i] : 0.f;
+    }
+  };
   float mq = 0.f, lo = __builtin_inff(), hi = -__builtin_inff();
   int ai = 1;
-  for (int i = lane_id(); i < pd; i += kWave) {
-    const float v = qv[i];
-    mq = fmaxf(mq, fabsf(v));
-    lo = fminf(lo, v);
-    hi = fmaxf(hi, v);
-    ai &= v == rintf(v) ? 1 : 0;
+  for (int base = 0; base < pd; base += kRound) {
+    load(base);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (base + lane + j * kWave < pd) {
+        mq = fmaxf(mq, fabsf(v[j]));
+        lo = fminf(lo, v[j]);
+        hi = fmaxf(hi, v[j]);
+        ai &= v[j] == rintf(v[j]) ? 1 : 0;
+      }
+    }
   }
   mq = wave_max(mq);
   lo = wave_min(lo);
@@ -96,14 +115,18 @@ __device__ Int8Query int8_query(const int8_t* X8, int c8, float xlo, float xhi, 
         dpd * range * range < lim && lo - float(c8) >= -128.f && hi - float(c8) <= 127.f))
     return r;
   int ysum = 0;
-  for (int w = lane_id(); w < pd / 4; w += kWave) {
-    uint32_t word = 0;
-    for (int t = 0; t < 4; ++t) {
-      const int y8 = int(qv[4 * w + t]) - c8;
-      ysum += metric == 0 ? y8 * y8 : y8;
-      word |= uint32_t(y8 & 0xff) << (8 * t);
+  int8_t* yb = reinterpret_cast<int8_t*>(ys);
+  for (int base = 0; base < pd; base += kRound) {
+    if (pd > kRound) load(base);  // one round: its values are still in v
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = base + lane + j * kWave;
+      if (i < pd) {
+        const int y8 = int(v[j]) - c8;
+        ysum += metric == 0 ? y8 * y8 : y8;
+        yb[i] = int8_t(y8);
+      }
     }
-    ys[w] = word;
   }
   for (int o = kWave / 2; o > 0; o >>= 1) ysum += __shfl_xor(ysum, o);
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -114,23 +137,34 @@ __device__ Int8Query int8_query(const int8_t* X8, int c8, float xlo, float xhi, 
   return r;
 }
 
+// The row's 16-byte vectors load G at a time, all G in flight together (G = 8 covers a
+// 128-dim row in one round trip; kernels short of registers take fewer).
+template <int G = 8>
 __device__ __forceinline__ float int8_distance(const int8_t* X8, int c8, int metric, int pd,
                                                const Int8Query& p, uint32_t row) {
   const int4* xr = reinterpret_cast<const int4*>(X8 + size_t(row) * pd);
   const int4* yr = reinterpret_cast<const int4*>(p.ys);
   const int one = 0x01010101;
+  const int nv = pd / 16;
   int xy = 0, xx = 0;
-  for (int i = 0; i < pd / 16; ++i) {
-    const int4 x = xr[i], y = yr[i];
-    xy = __builtin_amdgcn_sdot4(x.x, y.x, xy, false);
-    xy = __builtin_amdgcn_sdot4(x.y, y.y, xy, false);
-    xy = __builtin_amdgcn_sdot4(x.z, y.z, xy, false);
-    xy = __builtin_amdgcn_sdot4(x.w, y.w, xy, false);
-    // L2: sum x8^2; IP: sum x8 (against bytes of ones)
-    xx = __builtin_amdgcn_sdot4(x.x, metric == 0 ? x.x : one, xx, false);
-    xx = __builtin_amdgcn_sdot4(x.y, metric == 0 ? x.y : one, xx, false);
-    xx = __builtin_amdgcn_sdot4(x.z, metric == 0 ? x.z : one, xx, false);
-    xx = __builtin_amdgcn_sdot4(x.w, metric == 0 ? x.w : one, xx, false);
+  for (int i0 = 0; i0 < nv; i0 += G) {
+    int4 x[G];
+#pragma unroll
+    for (int j = 0; j < G; ++j) x[j] = i0 + j < nv ? xr[i0 + j] : make_int4(0, 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      if (i0 + j >= nv) break;
+      const int4 y = yr[i0 + j];
+      xy = __builtin_amdgcn_sdot4(x[j].x, y.x, xy, false);
+      xy = __builtin_amdgcn_sdot4(x[j].y, y.y, xy, false);
+      xy = __builtin_amdgcn_sdot4(x[j].z, y.z, xy, false);
+      xy = __builtin_amdgcn_sdot4(x[j].w, y.w, xy, false);
+      // L2: sum x8^2; IP: sum x8 (against bytes of ones)
+      xx = __builtin_amdgcn_sdot4(x[j].x, metric == 0 ? x[j].x : one, xx, false);
+      xx = __builtin_amdgcn_sdot4(x[j].y, metric == 0 ? x[j].y : one, xx, false);
+      xx = __builtin_amdgcn_sdot4(x[j].z, metric == 0 ? x[j].z : one, xx, false);
+      xx = __builtin_amdgcn_sdot4(x[j].w, metric == 0 ? x[j].w : one, xx, false);
+    }
   }
   if (metric == 0) return float(xx - 2 * xy + p.ysum);
   return -float(xy + c8 * xx + c8 * p.ysum + pd * c8 * c8);  // -0 for a zero dot, as -dot
@@ -1270,7 +1304,7 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
                     ys_all[wave]);
   auto score = [&](uint32_t id) -> float {
     if constexpr (kI8) {
-      if (p8.on) return int8_distance(sc.X8, sc.c8, sc.metric, sc.pd, p8, id);
+      if (p8.on) return int8_distance<1>(sc.X8, sc.c8, sc.metric, sc.pd, p8, id);
     }
     return sc(qv, id);
   };
@@ -2161,23 +2195,66 @@ __device__ __forceinline__ void small_push(float (&kd)[L], uint32_t (&ki)[L], fl
 }
 
 // A scored 32-row block into the lane's list: value r is row rb + 8 (r / 4) + 4 h + r % 4,
-// its key -M u.  The lane's largest u is tested first: nothing of the block enters a list
-// whose last key is below the block's best (ties go by row, so the test is <=).
+// its key -M u.  Every lane publishes its list's last key in LDS (thr[query][list], one
+// list per half-wave of each of the block's waves) and a value is a candidate only when its
+// key is at most the smallest of the query's eight published keys T: a row above a full
+// list's last key is above that wave's merged list's last key, hence above the chunk's
+// bound, so dropping it keeps the certificate (a stale published key is larger, so it
+// drops less).  In u, key <= T is u >= ceil(-T / M), one integer compare per value.  The
+// candidates form a 16-bit mask and only its set bits are pushed (their value picked by a
+// select tree), each checked again against the lane's own list as it tightens.
 template <class V16>
 __device__ __forceinline__ void small_take(const TinyArgs& a, const V16& acc, uint32_t rb,
                                            uint32_t r1, int h, int M, bool qlive,
-                                           float (&kd)[kSmallKp], uint32_t (&ki)[kSmallKp]) {
+                                           float (&kd)[kSmallKp], uint32_t (&ki)[kSmallKp],
+                                           float* thr, int j, int slot) {
+  thr[slot] = kd[kSmallKp - 1];
+  const float4 t0 = *reinterpret_cast<const float4*>(thr + 8 * j);
+  const float4 t1 = *reinterpret_cast<const float4*>(thr + 8 * j + 4);
+  const float T = fminf(fminf(fminf(t0.x, t0.y), fminf(t0.z, t0.w)),
+                        fminf(fminf(t1.x, t1.y), fminf(t1.z, t1.w)));
+  // keys are -M u for integers u (|u| < 2^24), so -T / M is exact when T is finite
+  const int tu = T == __builtin_inff() ? INT_MIN : int(ceilf(-T / float(M)));
   int m = acc[0];
 #pragma unroll
   for (int r = 1; r < 16; ++r) m = max(m, acc[r]);
-  if (__ballot(qlive && float(-M * m) <= kd[kSmallKp - 1]) == 0) return;
+  if (__ballot(qlive && m >= tu) == 0) return;
+  const bool whole = rb + 32u <= r1 && a.allow == nullptr;  // every row in range and allowed
+  const uint32_t hb = rb + uint32_t(4 * h);
+  uint32_t mask = 0;
+  if (qlive) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const uint32_t row = rb + uint32_t(8 * (r >> 2) + 4 * h + (r & 3));
-    const float key = float(-M * acc[r]);
-    if (qlive && row < r1 && row_allowed(a.allow, row) &&
-        nb_less(key, row, kd[kSmallKp - 1], ki[kSmallKp - 1]))
-      small_push(kd, ki, key, row);
+    for (int r = 0; r < 16; ++r) mask |= acc[r] >= tu ? 1u << r : 0u;
+    if (!whole) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = hb + uint32_t(8 * (r >> 2) + (r & 3));
+        if (!(row < r1 && row_allowed(a.allow, row))) mask &= ~(1u << r);
+      }
+    }
+  }
+  while (mask != 0) {
+    const int r = __builtin_ctz(mask);
+    mask &= mask - 1u;
+    // acc[r] by the bits of r: a tree of register selects, each result pinned so that the
+    // tree is not folded into a dynamic index (which would go through scratch memory)
+    auto pick = [](bool c, int x1, int x0) __attribute__((always_inline)) {
+      int v = c ? x1 : x0;
+      asm volatile("" : "+v"(v));
+      return v;
+    };
+    const bool b0 = r & 1, b1 = r & 2, b2 = r & 4, b3 = r & 8;
+    const int p0 = pick(b0, acc[1], acc[0]), p1 = pick(b0, acc[3], acc[2]);
+    const int p2 = pick(b0, acc[5], acc[4]), p3 = pick(b0, acc[7], acc[6]);
+    const int p4 = pick(b0, acc[9], acc[8]), p5 = pick(b0, acc[11], acc[10]);
+    const int p6 = pick(b0, acc[13], acc[12]), p7 = pick(b0, acc[15], acc[14]);
+    const int q0 = pick(b1, p1, p0), q1 = pick(b1, p3, p2), q2 = pick(b1, p5, p4),
+              q3 = pick(b1, p7, p6);
+    const int s0 = pick(b2, q1, q0), s1 = pick(b2, q3, q2);
+    const int u = pick(b3, s1, s0);
+    const float key = float(-M * u);
+    const uint32_t row = hb + uint32_t(8 * (r >> 2) + (r & 3));
+    if (nb_less(key, row, kd[kSmallKp - 1], ki[kSmallKp - 1])) small_push(kd, ki, key, row);
   }
 }
 
@@ -2278,10 +2355,13 @@ __global__ __launch_bounds__(kSmallWaves * 64, SmallOccupancy(NKB * 32)) void k_
   const int M = a.metric == 0 ? 2 : 1;
   const bool qlive = j < a.nq;
   constexpr int PD = NKB * 32;
-  v4i qv[NKB];
-  small_query<NKB>(a, j, h, qv);
+  // each list's last key, published for the block's threshold per query (see small_take)
+  __shared__ __align__(16) float s_thr[32 * 2 * kSmallWaves];
+  if (tid < 32 * 2 * kSmallWaves) s_thr[tid] = __builtin_inff();
+  __syncthreads();
   const uint32_t gw = blockIdx.x * kSmallWaves + wave;  // the wave's range of rows
   const uint32_t r0 = min(a.N, gw * a.chunk_rows), r1 = min(a.N, r0 + a.chunk_rows);
+  v4i qv[NKB];  // the queries, packed once the first rows are on their way
   float kd[kSmallKp];
   uint32_t ki[kSmallKp];
 #pragma unroll
@@ -2325,11 +2405,13 @@ __global__ __launch_bounds__(kSmallWaves * 64, SmallOccupancy(NKB * 32)) void k_
 #pragma unroll
     for (int kb = 0; kb < NKB; ++kb)
       acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(B.x[kb], qv[kb], acc, 0, 0, 0);
-    small_take(a, acc, rb, r1, h, M, qlive, kd, ki);
+    small_take(a, acc, rb, r1, h, M, qlive, kd, ki, s_thr, j, 8 * j + 2 * wave + h);
   };
   Blk B0, B1, B2;
   if (nblk > 0) load(B0, r0);
   if (nblk > 1) load(B1, r0 + 32);
+  // the queries pack while the first rows load
+  small_query<NKB>(a, j, h, qv);
   for (int b = 0; b < nblk; b += 3) {
     if (b + 2 < nblk) load(B2, r0 + uint32_t(b + 2) * 32);
     compute(B0, b);
@@ -2361,20 +2443,19 @@ struct TinyMergeArgs {
 };
 
 // One block of 8 waves per query.  Each wave loads its share of the chunks' keys with all
-// loads in flight (up to 8 per lane at a time) and keeps the 64 best (staged inserts).  The
-// 8 sorted lists merge by rank: every key counts the keys of the other lists below it
-// (binary searches in LDS) and lands at its rank among all 512, the first 64 kept; wave 0
-// then re-scores and certifies (the scan's extra block prepared the query's bound).
+// loads in flight (up to 32 per lane at a time) and keeps the 64 best (staged, then inserted
+// 64 at a time).  The 8 sorted lists merge in a three-level tree of bitonic merges into
+// wave 0, which then re-scores and certifies (the scan's extra block prepared the query's
+// bound).
 __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   constexpr int W = 8;
-  constexpr int B = 8;   // keys per lane loaded at once
-  __shared__ float md[W][kWave];      // the waves' sorted lists
+  constexpr int B = 8;   // keys per lane of a group
+  constexpr int G = 4;   // groups in flight: 32 keys per lane (all of them, for k up to ~30)
+  __shared__ float md[W][kWave];      // the waves' sorted lists, handed down the merge tree
   __shared__ uint32_t mi[W][kWave];
-  __shared__ float rd[kWave];         // the best 64 of all, by rank
-  __shared__ uint32_t ri[kWave];
   __shared__ float s_lb[W];
-  __shared__ float sd[W][2 * kWave];
-  __shared__ uint32_t si[W][2 * kWave];
+  __shared__ float sd[W][(B + 1) * kWave];  // staged keys: below 64 left over + a group's
+  __shared__ uint32_t si[W][(B + 1) * kWave];
   __shared__ uint32_t ys[256];  // the query packed into int8 (Int8Query)
   const int q = blockIdx.x;
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
@@ -2385,67 +2466,89 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   const int c0 = min(a.nchunks, wave * per), c1 = min(a.nchunks, c0 + per);
   const size_t total = size_t(c1 - c0) * a.kp;
   const uint2* src = a.part + (size_t(q) * a.nchunks + c0) * a.kp;
-  // the first keys load while the bounds are reduced
-  auto load_keys = [&](size_t g0, uint2 (&v)[B]) {
+  constexpr size_t kGroup = size_t(B) * kWave;
+  auto load_keys = [&](size_t g0, uint2 (&v)[B]) __attribute__((always_inline)) {
 #pragma unroll
     for (int b = 0; b < B; ++b) {
       const size_t g = g0 + size_t(b) * kWave + lane;
       v[b] = g < total ? src[g] : make_uint2(__float_as_uint(__builtin_inff()), kNoId);
     }
   };
-  uint2 v[B];
-  load_keys(0, v);
+  // every key of the first round in flight before any is used
+  uint2 v0[B], v1[B], v2[B], v3[B];
+  load_keys(0, v0);
+  load_keys(kGroup, v1);
+  load_keys(2 * kGroup, v2);
+  load_keys(3 * kGroup, v3);
+  // wave 0 prepares the query for the re-scoring now: its loads go out behind the keys, so
+  // the round trip overlaps theirs
+  const float* qv = a.pa.Q + size_t(q) * a.pa.pd;
+  const float shift = a.pa.shift[q], eb = a.pa.eb[q];
+  const float Qd = float(a.pa.Qd[q]);
+  const bool fits = a.pa.fit8q[q] != 0;
+  Int8Query p8{0, 0, ys};
+  if (wave == 0)
+    p8 = int8_query(a.sc.X8, a.sc.c8, a.sc.xlo, a.sc.xhi, a.sc.xmax, a.sc.xint, a.sc.metric,
+                    a.sc.pd, qv, ys);
   // Every chunk holds kp keys at or below its bound, so the best kp keys of all lie at or
   // below the smallest bound LB: keys above it are skipped.
+#pragma unroll 4
   for (int ch = c0 + lane; ch < c1; ch += kWave) lb = fminf(lb, a.bound[size_t(q) * a.nchunks + ch]);
   lb = wave_min(lb);
   if (lane == 0) s_lb[wave] = lb;
   __syncthreads();
   float LB = s_lb[0];
   for (int w = 1; w < W; ++w) LB = fminf(LB, s_lb[w]);
-  // the key to beat: the (k + 9)-th (the certificate reads the key after the k + 8 scored)
+  // the key to beat: the (k + 9)-th (the certificate reads the key after the k + 8 scored).
+  // A group stages its keys below LB and below the list's current (k + 9)-th key (read once
+  // per group: it only tightens, so a stale one admits more keys, never fewer); the staged
+  // keys then go into the list 64 at a time and fewer than 64 stay staged.
   const int rl = (a.k + 9 - 1) & (kWave - 1);
   int staged = 0;
-  auto push = [&](uint2 v) {
+  auto group = [&](const uint2 (&v)[B]) __attribute__((always_inline)) {
     const float td = __shfl(top.k.d[0], rl);
     const uint32_t ti = __shfl(top.k.id[0], rl);
-    const bool want = v.y != kNoId && __uint_as_float(v.x) <= LB &&
-                      nb_less(__uint_as_float(v.x), v.y, td, ti);
-    const uint64_t bal = __ballot(want);
-    if (bal == 0) return;
-    const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
-    if (want) {
-      sd[wave][pos] = __uint_as_float(v.x);
-      si[wave][pos] = v.y;
-    }
-    staged += __popcll(bal);
-    if (staged >= kWave) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      const float d0 = sd[wave][lane];
-      const uint32_t i0 = si[wave][lane];
-      const bool more = lane + kWave < staged;
-      const float d1 = more ? sd[wave][lane + kWave] : 0.f;
-      const uint32_t i1 = more ? si[wave][lane + kWave] : 0u;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      if (more) {
-        sd[wave][lane] = d1;
-        si[wave][lane] = i1;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const bool want = v[b].y != kNoId && __uint_as_float(v[b].x) <= LB &&
+                        nb_less(__uint_as_float(v[b].x), v[b].y, td, ti);
+      const uint64_t bal = __ballot(want);
+      if (want) {
+        const int pos = staged + __popcll(bal & ((1ull << lane) - 1ull));
+        sd[wave][pos] = __uint_as_float(v[b].x);
+        si[wave][pos] = v[b].y;
       }
-      staged -= kWave;
-      top.insert(d0, i0);
+      staged += __popcll(bal);
     }
+    if (staged < kWave) return;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int base = 0;
+    for (; base + kWave <= staged; base += kWave) top.insert(sd[wave][base + lane], si[wave][base + lane]);
+    const int rest = staged - base;
+    const float dr = lane < rest ? sd[wave][base + lane] : 0.f;
+    const uint32_t ir = lane < rest ? si[wave][base + lane] : 0u;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (lane < rest) {
+      sd[wave][lane] = dr;
+      si[wave][lane] = ir;
+    }
+    staged = rest;
   };
-  for (size_t g0 = 0; g0 < total; g0 += size_t(B) * kWave) {
-    uint2 vn[B];
-    if (g0 + size_t(B) * kWave < total) load_keys(g0 + size_t(B) * kWave, vn);
-#pragma unroll
-    for (int b = 0; b < B; ++b) push(v[b]);
-#pragma unroll
-    for (int b = 0; b < B; ++b) v[b] = vn[b];
+  for (size_t g0 = 0; g0 < total; g0 += G * kGroup) {
+    if (g0 > 0) {
+      load_keys(g0, v0);
+      load_keys(g0 + kGroup, v1);
+      load_keys(g0 + 2 * kGroup, v2);
+      load_keys(g0 + 3 * kGroup, v3);
+    }
+    group(v0);
+    group(v1);
+    group(v2);
+    group(v3);
   }
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -2454,46 +2557,34 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
     const bool have = lane < staged;
     top.insert(have ? sd[wave][lane] : __builtin_inff(), have ? si[wave][lane] : kNoId);
   }
-  // rank merge: the key of lane i of wave w has rank i + sum over the other lists of the keys
-  // below it ((dist, id) order: real keys are distinct; the padding keys (+inf, none) of
-  // different lists share ranks past the real ones and write the same value)
-  md[wave][lane] = top.k.d[0];
-  mi[wave][lane] = top.k.id[0];
-  __syncthreads();
-  {
-    const float kd = top.k.d[0];
-    const uint32_t ki = top.k.id[0];
-    int rank = lane;
-    for (int w = 0; w < W; ++w) {
-      if (w == wave) continue;
-      int lo = 0, hi = kWave;  // the count of keys of list w below (kd, ki)
-      while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (nb_less(md[w][mid], mi[w][mid], kd, ki)) lo = mid + 1; else hi = mid;
-      }
-      rank += lo;
+  // Tree merge: at level L the waves w with w % 2L == L hand their lists to waves w - L,
+  // which keep the 64 smallest of both (the partner's list reversed against their own is
+  // a bitonic sequence holding them), so wave 0 ends with the best 64 of all, sorted.  A
+  // wave hands its list down once, to a slot no wave reads at any other level.
+#pragma unroll
+  for (int L = 1; L < W; L <<= 1) {
+    if ((wave & (2 * L - 1)) == L) {
+      md[wave][lane] = top.k.d[0];
+      mi[wave][lane] = top.k.id[0];
     }
-    if (rank < kWave) {
-      rd[rank] = kd;
-      ri[rank] = ki;
+    __syncthreads();
+    if ((wave & (2 * L - 1)) == 0) {
+      const float pd = md[wave + L][kWave - 1 - lane];
+      const uint32_t pi = mi[wave + L][kWave - 1 - lane];
+      if (nb_less(pd, pi, top.k.d[0], top.k.id[0])) {
+        top.k.d[0] = pd;
+        top.k.id[0] = pi;
+      }
+      bitonic_merge<1>(top.k);
     }
   }
-  __syncthreads();
   if (wave != 0) return;
-  top.k.d[0] = rd[lane];
-  top.k.id[0] = ri[lane];
   lb = __builtin_inff();
   for (int w = 0; w < W; ++w) lb = fminf(lb, s_lb[w]);
-  const float* qv = a.pa.Q + size_t(q) * a.pa.pd;
-  const float shift = a.pa.shift[q], eb = a.pa.eb[q];
-  const float Qd = float(a.pa.Qd[q]);
-  const bool fits = a.pa.fit8q[q] != 0;
   // exact re-scoring of the best n1 keys, certificate against every unscored row
   // (rows of 128 bytes from the int8 copy: their loads issue together, where the fp32
   // rows' 512 bytes per lane form a chain of dependent load rounds)
   const int n1 = min(kWave - 1, a.k + 8);
-  const Int8Query p8 = int8_query(a.sc.X8, a.sc.c8, a.sc.xlo, a.sc.xhi, a.sc.xmax, a.sc.xint,
-                                  a.sc.metric, a.sc.pd, qv, ys);
   float d = __builtin_inff();
   uint32_t id = kNoId;
   if (lane < n1 && top.k.id[0] != kNoId) {
