@@ -1961,8 +1961,8 @@ int ScoreScan(Ctx* c, const ScanSource& src, const float* Q, size_t nq, size_t k
 // row against every query as the int8 GEMM does (u = row start + sum x8 q8, exact in int32;
 // key = -M u, the GEMM value plus the query's constant Qd) and keeps, per query, the kp
 // smallest keys of its chunk with their rows, plus the chunk's kp-th key (+inf when the
-// chunk holds fewer rows).  k_tiny_merge: one block per query takes the query's operands and
-// bound (query_prep_wave), the best keys of all chunks, re-scores the best n1 = min(K', k +
+// chunk holds fewer rows).  k_tiny_merge: one block per query prepares the query's operands
+// and bound (query_prep_wave) beside merging the best keys of all chunks, re-scores the best n1 = min(K', k +
 // 8) exactly (the reference's distance) and certifies the answer when the k-th exact
 // distance lies strictly below every unscored row's lower bound: the (n1+1)-th key, and each
 // full chunk's kp-th key (a row outside a chunk's list has a key at least that), taken back
@@ -1985,8 +1985,7 @@ struct TinyArgs {
   uint2* part;            // [q][chunk][kp] (key bits, row)
   float* bound;           // [q][chunk] the chunk's kp-th key, +inf when not full
   uint32_t* fb_count;     // [2] zeroed by the scan's block 0; [1] counts finished merges
-  int nchunks;            // blocks [0, nchunks) scan; block nchunks prepares the queries
-  PrepArgs pa;            // the queries' operands and bounds, for the merge's certificate
+  int nchunks;            // the scan's blocks
 };
 
 // Rows reach the lanes through a per-wave LDS tile: the wave reads 64 consecutive rows with
@@ -2003,10 +2002,6 @@ __global__ __launch_bounds__(kTinyWaves * 64) void k_tiny_scan(TinyArgs a) {
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
   constexpr int vpr = VPR;             // 16-byte vectors per row (pd / 16)
   int4* tile = tile_all + size_t(wave) * kWave * (vpr + 1);
-  if (int(blockIdx.x) == a.nchunks) {  // the extra block: one wave per query
-    if (wave < a.nq) (void)query_prep_wave(a.pa, wave);
-    return;
-  }
   if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
   const int pw = a.pd / 4;
   for (int e = tid; e < NQ * pw; e += kTinyWaves * 64) {
@@ -2144,7 +2139,7 @@ __global__ __launch_bounds__(kTinyWaves * 64) void k_tiny_scan(TinyArgs a) {
   for (int q = 0; q < NQ; ++q) {
     if (q >= a.nq) break;
     for (int w = 0; w < kTinyWaves - 1; ++w) top[q].insert(md[w][q][lane], mi[w][q][lane]);
-    const size_t o = size_t(q) * a.nchunks + blockIdx.x;  // (the grid has one more block)
+    const size_t o = size_t(q) * a.nchunks + blockIdx.x;
     if (lane < a.kp) a.part[o * a.kp + lane] = make_uint2(__float_as_uint(top[q].k.d[0]), top[q].k.id[0]);
     const float kth = __shfl(top[q].k.d[0], rl);
     const uint32_t kid = __shfl(top[q].k.id[0], rl);
@@ -2168,8 +2163,7 @@ __global__ __launch_bounds__(kTinyWaves * 64) void k_tiny_scan(TinyArgs a) {
 // four waves' lists merge into the block's chunk of kSmallBlockKp keys, whose bound is the
 // smaller of that list's last key and every full wave list's last: every row the block
 // left out has a key at least its chunk's bound, so k_tiny_merge's certificate holds as it
-// does over k_tiny_scan's chunks.  Blocks past the scan's prepare the queries, one wave per
-// query.
+// does over k_tiny_scan's chunks.
 constexpr int kSmallQ = 32;
 constexpr int kSmallKp = 4;      // keys a lane keeps
 constexpr int kSmallBlockKp = 8; // keys a block's chunk keeps
@@ -2341,15 +2335,10 @@ constexpr int SmallOccupancy(int pd) { return pd <= 128 ? 3 : 2; }
 
 template <int NKB>
 __global__ __launch_bounds__(kSmallWaves * 64, SmallOccupancy(NKB * 32)) void k_small_scan(
-    TinyArgs a, int scan_blocks) {
+    TinyArgs a) {
   typedef int v4i __attribute__((ext_vector_type(4)));
   typedef int v16i __attribute__((ext_vector_type(16)));
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
-  if (int(blockIdx.x) >= scan_blocks) {
-    const int qq = (int(blockIdx.x) - scan_blocks) * kSmallWaves + wave;
-    if (qq < a.nq) (void)query_prep_wave(a.pa, qq);
-    return;
-  }
   if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
   const int j = lane & 31, h = lane >> 5;
   const int M = a.metric == 0 ? 2 : 1;
@@ -2427,6 +2416,8 @@ __global__ __launch_bounds__(kSmallWaves * 64, SmallOccupancy(NKB * 32)) void k_
   small_finish(a, kd, ki, j, h, wave, qlive, bk, bi);
 }
 
+constexpr int kMergeWaves = 8;  // key-merging waves of k_tiny_merge (plus one preparing)
+
 struct TinyMergeArgs {
   PrepArgs pa;            // the query's operands and bound (fit8q set)
   const uint2* part;
@@ -2442,13 +2433,13 @@ struct TinyMergeArgs {
   int force_fallback;
 };
 
-// One block of 8 waves per query.  Each wave loads its share of the chunks' keys with all
-// loads in flight (up to 32 per lane at a time) and keeps the 64 best (staged, then inserted
-// 64 at a time).  The 8 sorted lists merge in a three-level tree of bitonic merges into
-// wave 0, which then re-scores and certifies (the scan's extra block prepared the query's
-// bound).
-__global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
-  constexpr int W = 8;
+// One block of 8 + 1 waves per query.  Each of 8 waves loads its share of the chunks' keys
+// with all loads in flight (up to 32 per lane at a time) and keeps the 64 best (staged, then
+// inserted 64 at a time); the ninth prepares the query's operands and bound meanwhile.  The
+// 8 sorted lists merge in a three-level tree of bitonic merges into wave 0, which then
+// re-scores and certifies.
+__global__ __launch_bounds__(kMergeWaves * 64 + 64) void k_tiny_merge(TinyMergeArgs a) {
+  constexpr int W = kMergeWaves;  // waves that merge keys; wave W prepares the query
   constexpr int B = 8;   // keys per lane of a group
   constexpr int G = 4;   // groups in flight: 32 keys per lane (all of them, for k up to ~30)
   __shared__ float md[W][kWave];      // the waves' sorted lists, handed down the merge tree
@@ -2462,8 +2453,9 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   WaveTopK<1> top;
   top.init();
   float lb = __builtin_inff();
+  const bool keys = wave < W;
   const int per = (a.nchunks + W - 1) / W;
-  const int c0 = min(a.nchunks, wave * per), c1 = min(a.nchunks, c0 + per);
+  const int c0 = keys ? min(a.nchunks, wave * per) : a.nchunks, c1 = min(a.nchunks, c0 + per);
   const size_t total = size_t(c1 - c0) * a.kp;
   const uint2* src = a.part + (size_t(q) * a.nchunks + c0) * a.kp;
   constexpr size_t kGroup = size_t(B) * kWave;
@@ -2480,12 +2472,12 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   load_keys(kGroup, v1);
   load_keys(2 * kGroup, v2);
   load_keys(3 * kGroup, v3);
-  // wave 0 prepares the query for the re-scoring now: its loads go out behind the keys, so
-  // the round trip overlaps theirs
+  // Wave W prepares the query's operands and bound (shift, eb, Qd, fit8q, and the exact
+  // fallback's inputs) while the others merge keys; wave 0 reads them after the merge's
+  // barriers.  Wave 0 also packs the query for the re-scoring now: its loads go out behind
+  // the keys, so the round trip overlaps theirs.
+  if (wave == W) (void)query_prep_wave(a.pa, q);
   const float* qv = a.pa.Q + size_t(q) * a.pa.pd;
-  const float shift = a.pa.shift[q], eb = a.pa.eb[q];
-  const float Qd = float(a.pa.Qd[q]);
-  const bool fits = a.pa.fit8q[q] != 0;
   Int8Query p8{0, 0, ys};
   if (wave == 0)
     p8 = int8_query(a.sc.X8, a.sc.c8, a.sc.xlo, a.sc.xhi, a.sc.xmax, a.sc.xint, a.sc.metric,
@@ -2495,7 +2487,7 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
 #pragma unroll 4
   for (int ch = c0 + lane; ch < c1; ch += kWave) lb = fminf(lb, a.bound[size_t(q) * a.nchunks + ch]);
   lb = wave_min(lb);
-  if (lane == 0) s_lb[wave] = lb;
+  if (lane == 0 && keys) s_lb[wave] = lb;
   __syncthreads();
   float LB = s_lb[0];
   for (int w = 1; w < W; ++w) LB = fminf(LB, s_lb[w]);
@@ -2563,12 +2555,12 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
   // wave hands its list down once, to a slot no wave reads at any other level.
 #pragma unroll
   for (int L = 1; L < W; L <<= 1) {
-    if ((wave & (2 * L - 1)) == L) {
+    if (keys && (wave & (2 * L - 1)) == L) {
       md[wave][lane] = top.k.d[0];
       mi[wave][lane] = top.k.id[0];
     }
     __syncthreads();
-    if ((wave & (2 * L - 1)) == 0) {
+    if (keys && (wave & (2 * L - 1)) == 0) {
       const float pd = md[wave + L][kWave - 1 - lane];
       const uint32_t pi = mi[wave + L][kWave - 1 - lane];
       if (nb_less(pd, pi, top.k.d[0], top.k.id[0])) {
@@ -2579,6 +2571,9 @@ __global__ __launch_bounds__(512) void k_tiny_merge(TinyMergeArgs a) {
     }
   }
   if (wave != 0) return;
+  const float shift = a.pa.shift[q], eb = a.pa.eb[q];
+  const float Qd = float(a.pa.Qd[q]);
+  const bool fits = a.pa.fit8q[q] != 0;
   lb = __builtin_inff();
   for (int w = 0; w < W; ++w) lb = fminf(lb, s_lb[w]);
   // exact re-scoring of the best n1 keys, certificate against every unscored row
@@ -2655,18 +2650,17 @@ static void launch_tiny(hipStream_t s, int blocks, const TinyArgs& a) {
   const size_t tile = size_t(kTinyWaves) * kWave * (a.pd / 16 + 1) * sizeof(int4);
   const int threads = kTinyWaves * 64;
   switch (a.pd) {
-    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks + 1), threads, tile, s>>>(a); break;
-    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks + 1), threads, tile, s>>>(a); break;
-    default: k_tiny_scan<NQ, 16><<<dim3(blocks + 1), threads, tile, s>>>(a); break;
+    case 64: k_tiny_scan<NQ, 4><<<dim3(blocks), threads, tile, s>>>(a); break;
+    case 128: k_tiny_scan<NQ, 8><<<dim3(blocks), threads, tile, s>>>(a); break;
+    default: k_tiny_scan<NQ, 16><<<dim3(blocks), threads, tile, s>>>(a); break;
   }
 }
 
-static void launch_small(hipStream_t s, int scan_blocks, int nq, const TinyArgs& a) {
-  const int blocks = scan_blocks + (nq + kSmallWaves - 1) / kSmallWaves;
+static void launch_small(hipStream_t s, int blocks, const TinyArgs& a) {
   switch (a.pd) {
-    case 64: k_small_scan<2><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a, scan_blocks); break;
-    case 128: k_small_scan<4><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a, scan_blocks); break;
-    default: k_small_scan<8><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a, scan_blocks); break;
+    case 64: k_small_scan<2><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a); break;
+    case 128: k_small_scan<4><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a); break;
+    default: k_small_scan<8><<<dim3(blocks), kSmallWaves * 64, 0, s>>>(a); break;
   }
 }
 
@@ -2707,10 +2701,10 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
               src->vmin, src->scale, shift, eb, exact, nullptr, nullptr, nullptr,
               src->x16_parts, src->x16_exp, Q8, Qd, nullptr, fit8q, src->c8, nullptr};
   TinyArgs ta{Q, int(nq), pd, src->metric, src->c8, int(kk), kp, src->X8, src->init8, allow, N,
-              chunk, part, bound, fb_count, nchunks, pa};
+              chunk, part, bound, fb_count, nchunks};
   {
     ProfScope ps(c, "flat_gemm", s);
-    if (small) launch_small(s, blocks, int(nq), ta);
+    if (small) launch_small(s, blocks, ta);
     else if (nq == 1) launch_tiny<1>(s, nchunks, ta);
     else launch_tiny<2>(s, nchunks, ta);
     VDBG_HIP(hipGetLastError());
@@ -2723,7 +2717,7 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
                      out_d, fb_list, fb_count, c->host_flag_dev, seq, c->test_fallbacks};
     {
       ProfScope ps(c, "select", s);
-      k_tiny_merge<<<dim3(unsigned(nq)), 512, 0, s>>>(ma);
+      k_tiny_merge<<<dim3(unsigned(nq)), kMergeWaves * 64 + 64, 0, s>>>(ma);
       VDBG_HIP(hipGetLastError());
     }
     VDBG_RETURN_IF_ERROR(WaitWords(c, seq, fb_count, 1, s));
