@@ -439,15 +439,28 @@ struct WaveKeys {
   uint32_t id[E];
 };
 
-// v of lane (lane ^ j), j a power of two below 64: a DPP quad permutation for j = 1, 2 (no
-// LDS round trip), a bit-mask ds_swizzle within 32-lane groups for j = 4..16, bpermute for 32.
+// v of lane (lane ^ j), j a power of two below 64, in the VALU (no trip through the LDS
+// unit): a DPP quad permutation for j = 1, 2; DPP row rotates for j = 4, 8 (row_ror:n gives
+// lane i the value of lane (i - n) mod 16 of its 16-lane row: lane ^ 8 is ror 8, lane ^ 4 is
+// ror 12 where bit 2 of the lane is clear and ror 4 where it is set); v_permlane16_swap and
+// v_permlane32_swap for j = 16, 32 (each returns the even and the odd row, or half, of the
+// lane's pair: the partner's is the one the lane is not in).
 __device__ __forceinline__ uint32_t lane_xor(uint32_t v, int j) {
   if (j == 1) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, true));
   if (j == 2) return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, true));
-  if (j == 4) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (4 << 10) | 0x1F));
-  if (j == 8) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (8 << 10) | 0x1F));
-  if (j == 16) return uint32_t(__builtin_amdgcn_ds_swizzle(int(v), (16 << 10) | 0x1F));
-  return uint32_t(__shfl_xor(int(v), j));
+  const uint32_t lane = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  if (j == 4) {
+    const uint32_t up = uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x12C, 0xF, 0xF, false));
+    const uint32_t down = uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x124, 0xF, 0xF, false));
+    return (lane & 4u) ? down : up;
+  }
+  if (j == 8) return uint32_t(__builtin_amdgcn_update_dpp(0, int(v), 0x128, 0xF, 0xF, false));
+  if (j == 16) {
+    const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16u) ? p[0] : p[1];
+  }
+  const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (lane & 32u) ? p[0] : p[1];
 }
 __device__ __forceinline__ float lane_xor(float v, int j) {
   return __uint_as_float(lane_xor(__float_as_uint(v), j));
