@@ -1986,6 +1986,7 @@ struct TinyArgs {
   float* bound;           // [q][chunk] the chunk's kp-th key, +inf when not full
   uint32_t* fb_count;     // [2] zeroed by the scan's block 0; [1] counts finished merges
   int nchunks;            // the scan's blocks
+  uint32_t* fb_zero;      // nullable: the call's device fallback count, zeroed by block 0
 };
 
 // Rows reach the lanes through a per-wave LDS tile: the wave reads 64 consecutive rows with
@@ -2003,6 +2004,7 @@ __global__ __launch_bounds__(kTinyWaves * 64) void k_tiny_scan(TinyArgs a) {
   constexpr int vpr = VPR;             // 16-byte vectors per row (pd / 16)
   int4* tile = tile_all + size_t(wave) * kWave * (vpr + 1);
   if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
+  if (blockIdx.x == 0 && tid == 0 && a.fb_zero != nullptr) *a.fb_zero = 0;
   const int pw = a.pd / 4;
   for (int e = tid; e < NQ * pw; e += kTinyWaves * 64) {
     const int q = e / pw, w = e - q * pw;
@@ -2340,6 +2342,7 @@ __global__ __launch_bounds__(kSmallWaves * 64, SmallOccupancy(NKB * 32)) void k_
   typedef int v16i __attribute__((ext_vector_type(16)));
   const int tid = threadIdx.x, wave = tid >> 6, lane = lane_id();
   if (blockIdx.x == 0 && tid < 2) a.fb_count[tid] = 0;
+  if (blockIdx.x == 0 && tid == 0 && a.fb_zero != nullptr) *a.fb_zero = 0;
   const int j = lane & 31, h = lane >> 5;
   const int M = a.metric == 0 ? 2 : 1;
   const bool qlive = j < a.nq;
@@ -2428,7 +2431,8 @@ struct TinyMergeArgs {
   float* out_d;
   uint32_t* fb_list;
   uint32_t* fb_count;     // [0] fallbacks, [1] finished merges
-  uint32_t* host_flag;    // pinned host words: [0] sequence, [1] fallback count
+  uint32_t* host_flag;    // nullable: pinned host words ([0] sequence, [1] fallback count)
+                          // the last merge publishes the count into
   uint32_t seq;
   int force_fallback;
 };
@@ -2602,6 +2606,7 @@ __global__ __launch_bounds__(kMergeWaves * 64 + 64) void k_tiny_merge(TinyMergeA
   }
   if (lane == 0) {
     if (!certified) a.fb_list[atomicAdd(a.fb_count, 1u)] = uint32_t(q);
+    if (a.host_flag == nullptr) return;  // the re-scan is gated on the device count
     __threadfence();
     if (atomicAdd(a.fb_count + 1, 1u) == uint32_t(gridDim.x - 1)) {
       // the last merge: publish the fallback count (seq written last, with release)
@@ -2669,6 +2674,18 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
                     Workspace& W, Workspace& W2) {
   const uint32_t N = src->N;
   const int pd = int(src->pd);
+  // Uncertified queries go to the exact re-scan.  When its scratch for every query of the
+  // batch is small (always, at these batch sizes) it is queued for every query and runs for
+  // those the merge listed, their count staying on the device (added to the call's count,
+  // which the scan's first block clears unless several scans of one call accumulate into
+  // it): nothing waits on the host.  Otherwise the merge publishes the count to the host.
+  const bool gated = c->gate_fallbacks && PlanExact(N, int(nq), kk).need <= kGatedExactBytes;
+  if (!gated) VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
+  uint32_t* fb_zero = nullptr;
+  if (gated && !c->fb_accumulate) {
+    c->last_fallbacks = 0;
+    fb_zero = c->fb_dev;
+  }
   // k_tiny_scan: a chunk of rows per block, kk + 9 keys each.  k_small_scan: a range of
   // rows per wave, each block one chunk of kSmallBlockKp keys per query
   const bool small = nq > size_t(kTinyQ);
@@ -2701,13 +2718,26 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
               src->vmin, src->scale, shift, eb, exact, nullptr, nullptr, nullptr,
               src->x16_parts, src->x16_exp, Q8, Qd, nullptr, fit8q, src->c8, nullptr};
   TinyArgs ta{Q, int(nq), pd, src->metric, src->c8, int(kk), kp, src->X8, src->init8, allow, N,
-              chunk, part, bound, fb_count, nchunks};
+              chunk, part, bound, fb_count, nchunks, fb_zero};
   {
     ProfScope ps(c, "flat_gemm", s);
     if (small) launch_small(s, blocks, ta);
     else if (nq == 1) launch_tiny<1>(s, nchunks, ta);
     else launch_tiny<2>(s, nchunks, ta);
     VDBG_HIP(hipGetLastError());
+  }
+  if (gated) {
+    TinyMergeArgs ma{pa, part, bound, nchunks, kp, int(kk), Flat8Of(*src, c->kset), out_ids,
+                     out_d, fb_list, fb_count, nullptr, 0u, c->test_fallbacks};
+    {
+      ProfScope ps(c, "select", s);
+      k_tiny_merge<<<dim3(unsigned(nq)), kMergeWaves * 64 + 64, 0, s>>>(ma);
+      VDBG_HIP(hipGetLastError());
+    }
+    VDBG_RETURN_IF_ERROR(ExactScan(c, W2, *src, Q, fb_list, int(nq), kk, allow, out_ids, out_d,
+                                   s, fb_count, c->fb_dev));
+    c->fb_dev_used = true;
+    return kOk;
   }
   uint32_t nfb = 0;
   {  // the merge publishes the fallback count through the context's host flag
@@ -2734,7 +2764,10 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             Workspace* ws, Workspace* ws2) {
   Workspace& W = ws != nullptr ? *ws : c->ws;
   Workspace& W2 = ws2 != nullptr ? *ws2 : c->ws2;
-  VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
+  // (the tiny path clears the call's fallback count itself, in its scan kernel)
+  const bool tiny = nq > 0 && kk > 0 && kk <= 10000 && src->N > 0 &&
+                    GemmSupported(src->pd) && TinyEligible(c, *src, nq, kk, W);
+  if (!tiny) VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
   c->last_gemm_bits = 0;
   c->last_gemm_gate = nullptr;
   if (nq == 0 || kk == 0) return kOk;
@@ -2750,8 +2783,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   const size_t pd = src->pd;
   const bool gemm = GemmSupported(pd) && N >= 1024;
   if (!gemm) return ExactScan(c, W, *src, Q, nullptr, int(nq), kk, allow, out_ids, out_d, s);
-  if (TinyEligible(c, *src, nq, kk, W))
-    return TinyScan(c, src, Q, nq, kk, allow, out_ids, out_d, s, W, W2);
+  if (tiny) return TinyScan(c, src, Q, nq, kk, allow, out_ids, out_d, s, W, W2);
   // A re-scan workspace that cannot grow must hold the re-scan of every query, checked
   // before anything is queued (which queries fall back is known only on the device).
   if (W2.fixed && PlanExact(N, int(nq), kk).need > W2.cap)

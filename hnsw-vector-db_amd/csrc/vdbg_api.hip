@@ -248,6 +248,8 @@ void Workspace::release() {
   if (base != nullptr && !fixed) (void)hipFree(base);
   if (done != nullptr) (void)hipEventDestroy(done);
   done = nullptr;
+  last = nullptr;
+  used_once = false;
   base = nullptr;
   cap = used = 0;
 }
@@ -259,12 +261,16 @@ WsUse::WsUse(Workspace* w, hipStream_t s) : w_(w), s_(s) {
     rc_ = SetError(kInternal, "workspace event");
     return;
   }
-  if (hipStreamWaitEvent(s_, w_->done, 0) != hipSuccess)
+  // the previous user's launches on this same stream are ordered by the stream itself
+  if (!(w_->used_once && w_->last == s_) && hipStreamWaitEvent(s_, w_->done, 0) != hipSuccess)
     rc_ = SetError(kInternal, "workspace event wait");
 }
 
 WsUse::~WsUse() {
-  if (w_->done != nullptr) (void)hipEventRecord(w_->done, s_);
+  if (w_->done != nullptr && hipEventRecord(w_->done, s_) == hipSuccess) {
+    w_->last = s_;
+    w_->used_once = true;
+  }
 }
 
 // External ids of appended rows given none: each row's own row number.

@@ -69,6 +69,8 @@ struct Workspace {
   bool fixed = false;
   const char* name = "workspace";  // for the fixed workspace's capacity error
   hipEvent_t done = nullptr;  // recorded after the last launch of the last call that used it
+  hipStream_t last = nullptr;  // the stream that call ran on (compared, never used)
+  bool used_once = false;      // `last` is set
   int reserve(size_t bytes);  // makes `bytes` available (may reallocate; call before carving)
   template <class T>
   T* take(size_t count) {
@@ -81,8 +83,9 @@ struct Workspace {
 
 // Orders one call's use of a workspace after every earlier call's, whatever stream each
 // ran on: the constructor makes stream s wait (on the device) for the event the previous
-// user recorded; the destructor records it on s, after every launch the call queued that
-// reads the workspace.  The host-side order comes from the owner's mutex.
+// user recorded, unless that user ran on s itself (the stream orders them); the destructor
+// records it on s, after every launch the call queued that reads the workspace.  The
+// host-side order comes from the owner's mutex.
 class WsUse {
  public:
   WsUse(Workspace* w, hipStream_t s);
