@@ -1240,8 +1240,9 @@ constexpr int kMaxSeg = 1024;
 // sum over the segment counts maps a flat index to its segment) into a wave top-k of
 // capacity 64*E, and wave 0 merges the others' lists before the re-scoring.  Queries that
 // fail a certificate (or whose buffers overflowed) are appended to fb_list.
-template <int E, class Scorer, int WPS>
+template <int E, class Scorer, int WPS, bool STRIDE = false>
 __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs a, Scorer sc) {
+  static_assert(!STRIDE || WPS == 1, "striding waves share no barrier only with one wave a slot");
   constexpr int WAVES = WPS == 1 ? 4 : WPS;
   constexpr int PRE = WPS == 1 ? kMaxSeg : kMaxSeg / WPS;  // segments per wave
   __shared__ uint32_t pre_all[WAVES][PRE + 1];
@@ -1256,9 +1257,9 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   __shared__ uint32_t ys_all[kI8 ? WAVES : 1][kI8 ? 256 : 1];
   const int wave = threadIdx.x >> 6;
   const int lane = lane_id();
-  const int slot = WPS == 1 ? blockIdx.x * 4 + wave : blockIdx.x;
   const int sub = WPS == 1 ? 0 : wave;  // the wave's share of the slot's segments
   if (a.fb_acc != nullptr && blockIdx.x == 0 && threadIdx.x == 0) atomicAdd(a.fb_acc, *a.nslots_dev);
+  auto run = [&](const int slot) __attribute__((always_inline)) {
   if (slot >= a.nslots) return;
   if (a.nslots_dev != nullptr && uint32_t(slot) >= *a.nslots_dev) return;
   const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
@@ -1504,6 +1505,15 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     const uint32_t p = atomicAdd(a.fb_count, 1u);
     a.fb_list[p] = q;
   }
+  };
+  if constexpr (STRIDE) {
+    // a gated pass on a bounded grid: each wave strides over the slots the device count
+    // allows (the waves of one slot share nothing, so no barrier is involved)
+    const int n = int(min(*a.nslots_dev, uint32_t(a.nslots)));
+    for (int slot = int(blockIdx.x) * 4 + wave; slot < n; slot += int(gridDim.x) * 4) run(slot);
+  } else {
+    run(WPS == 1 ? int(blockIdx.x) * 4 + wave : int(blockIdx.x));
+  }
 }
 
 // ================================================================ exact scan
@@ -1519,18 +1529,23 @@ struct ScanArgs {
   int nsplit;
   uint2* part;            // [slot][split][64*E]
   uint32_t* part_counts;  // [slot][split]
-  const uint32_t* nslots_dev;  // nullable: slots at or past *nslots_dev exit
+  const uint32_t* nslots_dev;  // nullable: slots at or past *nslots_dev are not scanned
 };
 
-// Block = 4 waves on one (query, row split); each wave keeps a top-64E of its rows with
-// exact distances, then wave 0 merges the other three through LDS.
+// Grid of a gated exact re-scan pass (two blocks per CU of a 256-CU part).
+constexpr size_t kGatedScanBlocks = 512;
+
+// Block = 4 waves on one (query, row split) item at a time; each wave keeps a top-64E of its
+// rows with exact distances, then wave 0 merges the other three through LDS.  Items are
+// slot * nsplit + split.  With nslots_dev the grid is bounded (a pass queued for every query
+// but run for the few the pass before listed) and the blocks stride over the items the
+// device count allows, so a pass with nothing to do costs a small grid, not one block per
+// item.
 template <int E, class Scorer>
-__global__ __launch_bounds__(256) void k_exact_scan(ScanArgs a, Scorer sc) {
+__device__ __forceinline__ void exact_scan_item(const ScanArgs& a, const Scorer& sc, int slot,
+                                                int split, float (*md)[kWave * E],
+                                                uint32_t (*mi)[kWave * E]) {
   constexpr int N = kWave * E;
-  __shared__ float md[3][N];
-  __shared__ uint32_t mi[3][N];
-  const int slot = blockIdx.x, split = blockIdx.y;
-  if (a.nslots_dev != nullptr && uint32_t(slot) >= *a.nslots_dev) return;  // block-uniform
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const uint32_t q = a.qlist ? a.qlist[slot] : uint32_t(slot);
   const float* qv = a.Q + size_t(q) * a.pd;
@@ -1569,6 +1584,23 @@ __global__ __launch_bounds__(256) void k_exact_scan(ScanArgs a, Scorer sc) {
     valid += __popcll(__ballot(top.k.id[e] != kNoId));
   }
   if (lane == 0) a.part_counts[ps] = valid;
+}
+
+template <int E, class Scorer, bool GATED>
+__global__ __launch_bounds__(256) void k_exact_scan(ScanArgs a, Scorer sc) {
+  __shared__ float md[3][kWave * E];
+  __shared__ uint32_t mi[3][kWave * E];
+  if constexpr (!GATED) {  // one item per block: (slot, split) = (blockIdx.x, blockIdx.y)
+    exact_scan_item<E, Scorer>(a, sc, int(blockIdx.x), int(blockIdx.y), md, mi);
+  } else {
+    const uint32_t nslots = min(*a.nslots_dev, uint32_t(a.nslots));
+    const uint32_t items = nslots * uint32_t(a.nsplit);
+    for (uint32_t item = blockIdx.x; item < items; item += gridDim.x) {
+      exact_scan_item<E, Scorer>(a, sc, int(item / uint32_t(a.nsplit)),
+                                 int(item % uint32_t(a.nsplit)), md, mi);
+      __syncthreads();  // wave 0 has read md / mi before the next item writes them
+    }
+  }
 }
 
 // ================================================================ rerank
@@ -1678,12 +1710,22 @@ template <int E, class Scorer>
 static void launch_select(hipStream_t s, const SelectArgs& a, const Scorer& sc) {
   if (a.nslots <= 256 && a.nseg >= 16)
     k_select<E, Scorer, 4><<<dim3(a.nslots), 256, 0, s>>>(a, sc);
+  else if (a.nslots_dev != nullptr)  // gated: a bounded grid of striding waves
+    k_select<E, Scorer, 1, true><<<dim3(unsigned(std::min<size_t>((size_t(a.nslots) + 3) / 4,
+                                                                   kGatedScanBlocks))),
+                                   256, 0, s>>>(a, sc);
   else
     k_select<E, Scorer, 1><<<dim3((a.nslots + 3) / 4), 256, 0, s>>>(a, sc);
 }
 template <int E, class Scorer>
 static void launch_scan(hipStream_t s, const ScanArgs& a, const Scorer& sc) {
-  k_exact_scan<E, Scorer><<<dim3(a.nslots, a.nsplit), 256, 0, s>>>(a, sc);
+  if (a.nslots_dev == nullptr) {
+    k_exact_scan<E, Scorer, false><<<dim3(a.nslots, a.nsplit), 256, 0, s>>>(a, sc);
+  } else {  // a gated pass: a bounded grid striding over the items the device count allows
+    const size_t items = size_t(a.nslots) * size_t(a.nsplit);
+    const unsigned blocks = unsigned(std::max<size_t>(1, std::min<size_t>(items, kGatedScanBlocks)));
+    k_exact_scan<E, Scorer, true><<<dim3(blocks), 256, 0, s>>>(a, sc);
+  }
 }
 template <int V>
 static void launch_kth_v(hipStream_t s, const KthArgs& a) {
