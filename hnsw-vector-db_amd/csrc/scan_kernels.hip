@@ -170,6 +170,84 @@ __device__ __forceinline__ float int8_distance(const int8_t* X8, int c8, int met
   return -float(xy + c8 * xx + c8 * p.ysum + pd * c8 * c8);  // -0 for a zero dot, as -dot
 }
 
+// int8_distance of R rows per 8-lane group: lane j of the group takes each row's 16-byte
+// vectors j, j + 8, ... (128 contiguous bytes per group load, every row's loads in flight
+// together), and the integer partial sums add up in any order.  Every lane of a group returns
+// its rows' distances in d; all 64 lanes must be active.
+template <int R>
+__device__ __forceinline__ void int8_distance_g8n(const int8_t* X8, int c8, int metric, int pd,
+                                                  const Int8Query& p, const uint32_t (&rows)[R],
+                                                  float (&d)[R]) {
+  const int j = lane_id() & 7;
+  const int4* yr = reinterpret_cast<const int4*>(p.ys);
+  const int one = 0x01010101;
+  const int nv = pd / 16;
+  int xy[R], xx[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) xy[r] = xx[r] = 0;
+  for (int i = j; i < nv; i += 8) {
+    int4 x[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) x[r] = reinterpret_cast<const int4*>(X8 + size_t(rows[r]) * pd)[i];
+    const int4 y = yr[i];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      xy[r] = __builtin_amdgcn_sdot4(x[r].x, y.x, xy[r], false);
+      xy[r] = __builtin_amdgcn_sdot4(x[r].y, y.y, xy[r], false);
+      xy[r] = __builtin_amdgcn_sdot4(x[r].z, y.z, xy[r], false);
+      xy[r] = __builtin_amdgcn_sdot4(x[r].w, y.w, xy[r], false);
+      xx[r] = __builtin_amdgcn_sdot4(x[r].x, metric == 0 ? x[r].x : one, xx[r], false);
+      xx[r] = __builtin_amdgcn_sdot4(x[r].y, metric == 0 ? x[r].y : one, xx[r], false);
+      xx[r] = __builtin_amdgcn_sdot4(x[r].z, metric == 0 ? x[r].z : one, xx[r], false);
+      xx[r] = __builtin_amdgcn_sdot4(x[r].w, metric == 0 ? x[r].w : one, xx[r], false);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    int s = xy[r], t = xx[r];
+    s += int(lane_xor(uint32_t(s), 4));
+    t += int(lane_xor(uint32_t(t), 4));
+    s += int(lane_xor(uint32_t(s), 2));
+    t += int(lane_xor(uint32_t(t), 2));
+    s += int(lane_xor(uint32_t(s), 1));
+    t += int(lane_xor(uint32_t(t), 1));
+    d[r] = metric == 0 ? float(t - 2 * s + p.ysum)
+                       : -float(s + c8 * t + c8 * p.ysum + pd * c8 * c8);
+  }
+}
+
+// Scores the keys that lanes [b0, b1) of a 64-key pass hold (own: the lane's key id) eight
+// lanes a key, two keys per group a round while more than 8 remain: score(ids, d) fills d[r]
+// with the distance of row ids[r] for the lane's group (row 0 stands in where the group has no
+// key), and each lane in [b0, b1) receives its own key's distance in out (+inf for kNoId).
+// Wave-uniform b0, b1; all 64 lanes active.
+template <class F>
+__device__ __forceinline__ void group_pass(uint32_t own, int b0, int b1, float& out, F&& score) {
+  const int lane = lane_id();
+  auto key = [&](int m) {
+    const uint32_t id = __shfl(own, m & (kWave - 1));
+    return m < b1 && id != kNoId ? id : 0u;
+  };
+  auto take = [&](float d, int c0) {  // key c0 + g's distance sits in lane 8g
+    const float got = __shfl(d, ((lane - c0) & 7) << 3);
+    if (lane >= c0 && lane < c0 + 8 && lane < b1) out = own != kNoId ? got : __builtin_inff();
+  };
+  int c0 = b0;
+  for (; c0 + 8 < b1; c0 += 16) {
+    const uint32_t ids[2] = {key(c0 + (lane >> 3)), key(c0 + 8 + (lane >> 3))};
+    float d[2];
+    score(ids, d);
+    take(d[0], c0);
+    take(d[1], c0 + 8);
+  }
+  if (c0 < b1) {
+    const uint32_t ids[1] = {key(c0 + (lane >> 3))};
+    float d[1];
+    score(ids, d);
+    take(d[0], c0);
+  }
+}
+
 // Order-preserving float <-> uint32 map for atomicMin/atomicMax.
 __device__ __forceinline__ uint32_t ord_enc(float f) {
   uint32_t b = __float_as_uint(f);
@@ -1435,12 +1513,19 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     return;
   }
 
+  // Flat rows score eight lanes a row (metric_exact_g8, int8_distance_g8: whole 128-byte runs
+  // of a row per group load) where the scorer's order has that form; eight keys a round, each
+  // key's distance then handed to its own lane.
+  constexpr bool kGroup = std::is_same<Scorer, FlatScorer>::value || kI8;
+  bool group = false;
+  if constexpr (kGroup) group = (kI8 && p8.on) || sc.kset == kKsetAvx512;
+
   // exact re-scoring of the K' = N-1 best by GEMM value, in two stages.  Stage 1 re-scores
   // the best n1 = min(K', k + 8), rounded up to whole 64-lane passes when k + 8 takes more
-  // than one (the extra lanes cost no extra pass); its answer stands when every later
-  // candidate provably
-  // lies behind it: the (n1+1)-th GEMM value plus the shift minus the bound exceeds the k-th
-  // exact distance.  Rows outside the buffers have GEMM value > T, at least that (n1+1)-th
+  // than one (at k = 64 a stage of k + 8 keys fails the certificate often enough that its
+  // second stage costs more than scoring the extra keys at once); its answer stands when
+  // every later candidate provably lies behind it: the (n1+1)-th GEMM value plus the shift
+  // minus the bound exceeds the k-th exact distance.  Rows outside the buffers have GEMM value > T, at least that (n1+1)-th
   // value, so they lie behind it too.  When no later candidate exists, or in exact mode
   // (the GEMM order is the distance order), the outside rows are checked against T itself:
   // the k-th exact distance is at most T + shift - eb (always so when T came from the kk-th
@@ -1453,6 +1538,23 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   const bool exact = a.exact[q] != 0;
   WaveKeys<E> r;
   float ud[E];  // exact distances of the scored keys, in top.k's order
+  // R keys per group (rows ids[0..R)), every row's loads in flight together
+  auto score_g8 = [&](const auto& ids, auto& d) {
+    if constexpr (kI8) {
+      if (p8.on) {
+        int8_distance_g8n(sc.X8, sc.c8, sc.metric, sc.pd, p8, ids, d);
+        return;
+      }
+    }
+    if constexpr (kGroup) {
+      constexpr int R = sizeof(d) / sizeof(float);
+      const float* xs[R];
+#pragma unroll
+      for (int i = 0; i < R; ++i)
+        xs[i] = sc.X + size_t(sc.map != nullptr ? sc.map[ids[i]] : ids[i]) * sc.pd;
+      metric_exact_g8n<R>(sc.metric, qv, xs, sc.pd, d);
+    }
+  };
   // scores keys [lo, hi) of top.k (passes with no key in range are skipped), then sorts the
   // first hi scored keys into r
   auto rescore_first = [&](uint32_t lo, uint32_t hi) {
@@ -1460,6 +1562,15 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     for (int e = 0; e < E; ++e) {
       if (uint32_t(e + 1) * kWave <= lo || uint32_t(e) * kWave >= hi) continue;
       const uint32_t gi = e * kWave + lane;
+      if constexpr (kGroup) {
+        if (group) {
+          // lanes [b0, b1) of this pass hold the keys to score
+          const int b0 = int(max(lo, uint32_t(e) * kWave) - uint32_t(e) * kWave);
+          const int b1 = int(min(hi, uint32_t(e + 1) * kWave) - uint32_t(e) * kWave);
+          group_pass(top.k.id[e], b0, b1, ud[e], score_g8);
+          continue;
+        }
+      }
       if (gi >= lo && gi < hi) ud[e] = score(top.k.id[e]);
     }
 #pragma unroll

@@ -466,6 +466,86 @@ __device__ __forceinline__ float lane_xor(float v, int j) {
   return __uint_as_float(lane_xor(__float_as_uint(v), j));
 }
 
+// l2_exact / dot_exact (the AVX-512 set) of R rows per 8-lane group: lanes 8g..8g+7 score
+// the rows x[0..R) their group passes, every row's loads in flight together.  Lane j of a
+// group keeps accumulators 4j..4j+3 of l2_exact's 32 (acc0 is 0..15, acc1 16..31):
+// accumulator a sums dims a, a + 32, a + 64, ... in that order, and the tail of a row with
+// pd % 32 == 16 goes to acc0 (lanes 0..3), as there.  The reduction pairs the same operands
+// through lane exchanges: xor 4 forms acc0[m] + acc1[m], xor 2 and xor 1 the first two
+// levels of reduce16, and the lane the last two.  A group reads a row in 128-byte runs (one
+// lane scoring a row alone reads 16 bytes of it per load, 64 rows per wave load).  Every lane
+// of a group returns its rows' distances in d; all 64 lanes must be active.
+template <int R>
+__device__ __forceinline__ void metric_exact_g8n(int metric, const float* __restrict__ q,
+                                                 const float* const (&x)[R], int pd,
+                                                 float (&d)[R]) {
+  const int j = lane_id() & 7;
+  float a[R][4];
+#pragma unroll
+  for (int r = 0; r < R; ++r) a[r][0] = a[r][1] = a[r][2] = a[r][3] = 0.f;
+  auto add = [&](float (&acc)[4], const float4& u, const float4& v) {
+    if (metric == 0) {
+      const float d0 = u.x - v.x, d1 = u.y - v.y, d2 = u.z - v.z, d3 = u.w - v.w;
+      acc[0] = fmaf(d0, d0, acc[0]);
+      acc[1] = fmaf(d1, d1, acc[1]);
+      acc[2] = fmaf(d2, d2, acc[2]);
+      acc[3] = fmaf(d3, d3, acc[3]);
+    } else {
+      acc[0] = fmaf(u.x, v.x, acc[0]);
+      acc[1] = fmaf(u.y, v.y, acc[1]);
+      acc[2] = fmaf(u.z, v.z, acc[2]);
+      acc[3] = fmaf(u.w, v.w, acc[3]);
+    }
+  };
+  auto ld = [&](const float* p, int i) { return *reinterpret_cast<const float4*>(p + i + 4 * j); };
+  // 128 dims a round: the round's loads are all issued before the first is used
+  int i = 0;
+  for (; i + 128 <= pd; i += 128) {
+    float4 u[4], v[R][4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u[t] = ld(q, i + 32 * t);
+#pragma unroll
+      for (int r = 0; r < R; ++r) v[r][t] = ld(x[r], i + 32 * t);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) add(a[r], u[t], v[r][t]);
+    }
+  }
+  for (; i + 32 <= pd; i += 32) {
+    const float4 u = ld(q, i);
+#pragma unroll
+    for (int r = 0; r < R; ++r) add(a[r], u, ld(x[r], i));
+  }
+  if (i < pd && j < 4) {
+    const float4 u = ld(q, i);
+#pragma unroll
+    for (int r = 0; r < R; ++r) add(a[r], u, ld(x[r], i));
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[r][c] = a[r][c] + lane_xor(a[r][c], 4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[r][c] = a[r][c] + lane_xor(a[r][c], 2);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[r][c] = a[r][c] + lane_xor(a[r][c], 1);
+    const float s = (a[r][0] + a[r][2]) + (a[r][1] + a[r][3]);
+    d[r] = metric == 0 ? s : -s;
+  }
+}
+
+// metric_exact_g8n for one row per group.
+__device__ __forceinline__ float metric_exact_g8(int metric, const float* __restrict__ q,
+                                                 const float* __restrict__ x, int pd) {
+  const float* const xs[1] = {x};
+  float d[1];
+  metric_exact_g8n<1>(metric, q, xs, pd, d);
+  return d[0];
+}
+
 // One compare-exchange layer of a bitonic network over 64*E elements: partner g ^ j,
 // ascending in blocks where (g & size) == 0.
 template <int E>
