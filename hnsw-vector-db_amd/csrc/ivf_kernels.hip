@@ -236,6 +236,74 @@ __global__ void k_first_probe(const uint32_t* __restrict__ probe, int nprobe, in
   val[q] = uint32_t(q);
 }
 
+// The queries grouped by their nearest list (first[q], k_first_probe's keys, masked to their
+// low bits, bins = 2^bits <= kOrderBins), lists ascending: one block counts the queries of each list in LDS, scans the
+// counts and places every query at its list's next slot.  Within a list the order is that of
+// the atomics; only the scan's scheduling depends on it, not any result.  (One launch where a
+// device radix sort of the same keys takes five.)
+constexpr int kOrderBins = 16384;
+__global__ __launch_bounds__(1024) void k_order_first(const uint32_t* __restrict__ first,
+                                                      int nq, uint32_t mask,
+                                                      uint32_t* __restrict__ order) {
+  __shared__ uint32_t cnt[kOrderBins];
+  __shared__ uint32_t part[1024 / kWave];
+  const int t = threadIdx.x, lane = lane_id(), wave = t >> 6;
+  const int nbins = int(mask) + 1;
+  for (int b = t; b < nbins; b += 1024) cnt[b] = 0u;
+  __syncthreads();
+  // each thread's keys load kBatch at a time, all in flight together
+  constexpr int kBatch = 8;
+  auto keys = [&](int q0, uint32_t (&kv)[kBatch]) {
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const int q = q0 + i * 1024 + t;
+      kv[i] = q < nq ? first[q] & mask : ~0u;
+    }
+  };
+  for (int q0 = 0; q0 < nq; q0 += 1024 * kBatch) {
+    uint32_t kv[kBatch];
+    keys(q0, kv);
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (kv[i] != ~0u) atomicAdd(&cnt[kv[i]], 1u);
+  }
+  __syncthreads();
+  // exclusive scan: thread t owns bins [t * per, (t + 1) * per)
+  const int per = (nbins + 1023) / 1024;
+  uint32_t own = 0;
+  for (int i = 0; i < per; ++i) {
+    const int b = t * per + i;
+    if (b < nbins) own += cnt[b];
+  }
+  uint32_t incl = own;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t v = __shfl_up(incl, o);
+    if (lane >= o) incl += v;
+  }
+  if (lane == kWave - 1) part[wave] = incl;
+  __syncthreads();
+  uint32_t base = 0;
+  for (int w = 0; w < wave; ++w) base += part[w];
+  uint32_t run = base + incl - own;
+  for (int i = 0; i < per; ++i) {
+    const int b = t * per + i;
+    if (b < nbins) {
+      const uint32_t c = cnt[b];
+      cnt[b] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
+  for (int q0 = 0; q0 < nq; q0 += 1024 * kBatch) {
+    uint32_t kv[kBatch];
+    keys(q0, kv);
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i)
+      if (kv[i] != ~0u) order[atomicAdd(&cnt[kv[i]], 1u)] = uint32_t(q0 + i * 1024 + t);
+  }
+}
+
 // Each query's probed lists with their coarse distances, reordered: the nearest list stays
 // first (it tightens the top-R threshold early), the others follow in ascending list id.
 // Queries that run together probe mostly the same lists, and walking them in one global
@@ -978,8 +1046,6 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
     float* offs = reinterpret_cast<float*>(order + nq);
     uint32_t* sprobe = reinterpret_cast<uint32_t*>(offs + nq * a.nprobe);
     float* sprobe_d = reinterpret_cast<float*>(sprobe + nq * a.nprobe);
-    k_first_probe<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, key, val);
-    VDBG_HIP(hipGetLastError());
     // with row sums: one block per query (k_ivf_scan_rs) walking its lists nearest first, so
     // the threshold falls early; otherwise one wave per query
     const bool rs = l2 && a.rowsum != nullptr && a.t2abs != nullptr && a.qmax != nullptr &&
@@ -1000,13 +1066,21 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
     // the keys are list ids below nlist (dc_base): only their low bits take sort passes
     int end_bit = 1;
     while (end_bit < 32 && (uint64_t(1) << end_bit) < a.dc_base) ++end_bit;
-    size_t tmp_bytes = 0;
-    VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, key2, val, order, a.nq, 0,
-                                                end_bit, s));
     void* tmp = nullptr;
-    VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
-    VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, key2, val, order, a.nq, 0,
-                                                end_bit, s));
+    k_first_probe<<<dim3(unsigned((nq + 255) / 256)), 256, 0, s>>>(a.probe, a.nprobe, a.nq, key, val);
+    VDBG_HIP(hipGetLastError());
+    if ((uint64_t(1) << end_bit) <= uint64_t(kOrderBins)) {
+      k_order_first<<<dim3(1), 1024, 0, s>>>(key, a.nq, uint32_t((uint64_t(1) << end_bit) - 1),
+                                             order);
+      VDBG_HIP(hipGetLastError());
+    } else {
+      size_t tmp_bytes = 0;
+      VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(nullptr, tmp_bytes, key, key2, val, order, a.nq,
+                                                  0, end_bit, s));
+      VDBG_HIP(hipMallocAsync(&tmp, tmp_bytes + 16, s));
+      VDBG_HIP(hipcub::DeviceRadixSort::SortPairs(tmp, tmp_bytes, key, key2, val, order, a.nq, 0,
+                                                  end_bit, s));
+    }
     if (!l2) {
       k_ivf_offsets<<<dim3(unsigned((nq * a.nprobe + 255) / 256)), 256, 0, s>>>(
           a.Q, a.pd, a.dim, a.coarse, as.probe, a.nprobe, a.nq, a.nlist, offs);
@@ -1033,7 +1107,7 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
       }
       if (rc == kOk && hipGetLastError() != hipSuccess) rc = SetError(kInternal, "ivf scan launch");
     }
-    (void)hipFreeAsync(tmp, s);
+    if (tmp != nullptr) (void)hipFreeAsync(tmp, s);
     (void)hipFreeAsync(buf, s);
     return rc;
   }
