@@ -860,10 +860,12 @@ struct ScanInit {
   int* all16;            // nullable, [2] 1
   uint32_t* ones;        // nullable, [1] all ones
   int* e8;               // nullable, [2] 0
+  uint32_t* fb_zero;     // nullable: the context's count of device-gated re-scans, 0
 };
 __global__ void k_scan_init(ScanInit a) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < a.nq) a.ovf[i] = 0;
+  if (i == 0 && a.fb_zero != nullptr) *a.fb_zero = 0;
   if (i < 2) {
     a.fb_count[i] = 0;
     if (a.all16 != nullptr) a.all16[i] = 1;
@@ -2922,7 +2924,16 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // (the tiny path clears the call's fallback count itself, in its scan kernel)
   const bool tiny = nq > 0 && kk > 0 && kk <= 10000 && src->N > 0 &&
                     GemmSupported(src->pd) && TinyEligible(c, *src, nq, kk, W);
-  if (!tiny) VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
+  // the GEMM path clears the device count in its init kernel (no launch of its own)
+  const bool main_path = !tiny && nq > 0 && kk > 0 && kk <= 240 && src->N >= 1024 &&
+                         GemmSupported(src->pd);
+  uint32_t* fb_zero = nullptr;
+  if (main_path && !c->fb_accumulate) {
+    c->last_fallbacks = 0;
+    if (c->fb_dev_used) fb_zero = c->fb_dev;
+  } else if (!tiny) {
+    VDBG_RETURN_IF_ERROR(ResetFallbacks(c, s));
+  }
   c->last_gemm_bits = 0;
   c->last_gemm_gate = nullptr;
   if (nq == 0 || kk == 0) return kOk;
@@ -3103,7 +3114,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   uint32_t* ones = try16 || try8any ? w.take<uint32_t>(1) : nullptr;
   int* fit8q = gated ? w.take<int>(nq) : nullptr;  // per query: inside the int8 bounds
   {
-    const ScanInit si{ovf, int(nq), fb_count, all16, ones, try8op ? e8 : nullptr};
+    const ScanInit si{ovf, int(nq), fb_count, all16, ones, try8op ? e8 : nullptr, fb_zero};
     k_scan_init<<<dim3(unsigned((std::max<size_t>(nq, 2) + 255) / 256)), 256, 0, s>>>(si);
     VDBG_HIP(hipGetLastError());
   }
