@@ -573,6 +573,21 @@ constexpr int kRsWaves = 4;
 constexpr int kRsChunk = kWave;  // probed lists whose metadata sits in LDS at a time
 constexpr int kQtabQueries = 32; // queries per block of k_ivf_qtab_rs
 
+// One level of a max over the lanes of many values at once: lanes l and l ^ O exchange the
+// halves of ax[0, 2N) that the other keeps (bit O of the lane picks the upper half), and each
+// keeps the max of the pair in ax[0, N).
+template <int O, int N>
+__device__ __forceinline__ void halve_max(float (&ax)[32], int lane) {
+  static_assert(2 * N <= 32, "the halves lie in the 32 values");
+  const bool hi = (lane & O) != 0;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float keep = hi ? ax[i + N] : ax[i];
+    const float give = hi ? ax[i] : ax[i + N];
+    ax[i] = fmaxf(keep, lane_xor(give, O));
+  }
+}
+
 // The per-query tables of the row-sum scan: qtab[q][j][c] = 2 * (-DotAny(q_j, C_j[c])), the
 // same operations as k_ivf_qtab (ivf_pq.cc:192-196), and qmax[q][j] = max_c |qtab[q][j][c]|.
 // grid (m, query groups of 32), one thread per centroid c: with DS = dsub known at compile
@@ -594,7 +609,12 @@ __global__ __launch_bounds__(256) void k_ivf_qtab_rs(const float* __restrict__ Q
 #pragma unroll
     for (int i = 0; i < DS; ++i) cr[i] = cc[i];
   }
-  for (int t = 0; t < nqb; ++t) {
+  static_assert(kQtabQueries == 32, "the max reduction below halves 32 values five times");
+  float ax[kQtabQueries];  // |qtab| of this thread's centroid for each query of the block
+#pragma unroll
+  for (int t = 0; t < kQtabQueries; ++t) {
+    ax[t] = 0.f;
+    if (t >= nqb) continue;
     const int q = q0 + t;
     const float* qv = Q + size_t(q) * pd + size_t(j) * dsub;
     float v;
@@ -615,10 +635,21 @@ __global__ __launch_bounds__(256) void k_ivf_qtab_rs(const float* __restrict__ Q
     }
     const float x = v * 2.f;
     qtab[(size_t(q) * m + j) * kKsub + c] = x;
-    float mx = fabsf(x);
-#pragma unroll
-    for (int o = kWave / 2; o > 0; o >>= 1) mx = fmaxf(mx, lane_xor(mx, o));
-    if (lane == 0) wmax[wave][t] = mx;
+    ax[t] = fabsf(x);
+  }
+  // The wave's maxima of all 32 queries at once: each exchange of lanes xor o (o = 32, 16,
+  // 8, 4, 2) keeps half of the values, the half the lane's bit o selects, at the max of the
+  // pair; then xor 1 completes the max over the 64 lanes.  Lane L ends with query
+  // (L >> 1) & 31's maximum (bit 5 of the lane selects the upper 16 queries, ..., bit 1 the
+  // odd one).
+  halve_max<32, 16>(ax, lane);
+  halve_max<16, 8>(ax, lane);
+  halve_max<8, 4>(ax, lane);
+  halve_max<4, 2>(ax, lane);
+  halve_max<2, 1>(ax, lane);
+  {
+    const float mx = fmaxf(ax[0], lane_xor(ax[0], 1));
+    if ((lane & 1) == 0) wmax[wave][(lane >> 1) & 31] = mx;
   }
   __syncthreads();
   if (c < nqb)
