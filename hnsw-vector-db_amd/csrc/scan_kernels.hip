@@ -205,8 +205,8 @@ __device__ __forceinline__ void int8_distance_g8n(const int8_t* X8, int c8, int 
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     int s = xy[r], t = xx[r];
-    s += int(lane_xor(uint32_t(s), 4));
-    t += int(lane_xor(uint32_t(t), 4));
+    s += int(lane_mirror8(uint32_t(s)));
+    t += int(lane_mirror8(uint32_t(t)));
     s += int(lane_xor(uint32_t(s), 2));
     t += int(lane_xor(uint32_t(t), 2));
     s += int(lane_xor(uint32_t(s), 1));

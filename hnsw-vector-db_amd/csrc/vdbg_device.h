@@ -465,21 +465,32 @@ __device__ __forceinline__ uint32_t lane_xor(uint32_t v, int j) {
 __device__ __forceinline__ float lane_xor(float v, int j) {
   return __uint_as_float(lane_xor(__float_as_uint(v), j));
 }
+// v of lane 7 - (lane & 7) of the lane's group of eight (DPP row_half_mirror).
+__device__ __forceinline__ uint32_t lane_mirror8(uint32_t v) {
+  return uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float lane_mirror8(float v) {
+  return __uint_as_float(lane_mirror8(__float_as_uint(v)));
+}
 
 // l2_exact / dot_exact (the AVX-512 set) of R rows per 8-lane group: lanes 8g..8g+7 score
-// the rows x[0..R) their group passes, every row's loads in flight together.  Lane j of a
-// group keeps accumulators 4j..4j+3 of l2_exact's 32 (acc0 is 0..15, acc1 16..31):
-// accumulator a sums dims a, a + 32, a + 64, ... in that order, and the tail of a row with
-// pd % 32 == 16 goes to acc0 (lanes 0..3), as there.  The reduction pairs the same operands
-// through lane exchanges: xor 4 forms acc0[m] + acc1[m], xor 2 and xor 1 the first two
-// levels of reduce16, and the lane the last two.  A group reads a row in 128-byte runs (one
-// lane scoring a row alone reads 16 bytes of it per load, 64 rows per wave load).  Every lane
-// of a group returns its rows' distances in d; all 64 lanes must be active.
+// the rows x[0..R) their group passes, every row's loads in flight together.  The 32
+// accumulators of l2_exact (acc0 is 0..15, acc1 16..31) come in 8 runs of four, run k being
+// accumulators 4k..4k+3; lane j of a group keeps run k = j for j < 4 and k = 11 - j above, so
+// run k and run k + 4 sit in lanes j and 7 - j.  Accumulator a sums dims a, a + 32, a + 64,
+// ... in that order, and the tail of a row with pd % 32 == 16 goes to acc0 (runs 0..3), as
+// there.  The reduction pairs the same operands through lane exchanges: the mirror j <-> 7 - j
+// forms acc0[m] + acc1[m], xor 2 and xor 1 the first two levels of reduce16 (runs k <-> k + 2,
+// then 0 <-> 1), and the lane the last two; each exchange is one DPP operand of the add.  A
+// group reads a row in 128-byte runs (one lane scoring a row alone reads 16 bytes of it per
+// load, 64 rows per wave load).  Every lane of a group returns its rows' distances in d; all
+// 64 lanes must be active.
 template <int R>
 __device__ __forceinline__ void metric_exact_g8n(int metric, const float* __restrict__ q,
                                                  const float* const (&x)[R], int pd,
                                                  float (&d)[R]) {
   const int j = lane_id() & 7;
+  const int run = j < 4 ? j : 11 - j;
   float a[R][4];
 #pragma unroll
   for (int r = 0; r < R; ++r) a[r][0] = a[r][1] = a[r][2] = a[r][3] = 0.f;
@@ -497,7 +508,7 @@ __device__ __forceinline__ void metric_exact_g8n(int metric, const float* __rest
       acc[3] = fmaf(u.w, v.w, acc[3]);
     }
   };
-  auto ld = [&](const float* p, int i) { return *reinterpret_cast<const float4*>(p + i + 4 * j); };
+  auto ld = [&](const float* p, int i) { return *reinterpret_cast<const float4*>(p + i + 4 * run); };
   // 128 dims a round: the round's loads are all issued before the first is used
   int i = 0;
   for (; i + 128 <= pd; i += 128) {
@@ -519,7 +530,7 @@ __device__ __forceinline__ void metric_exact_g8n(int metric, const float* __rest
 #pragma unroll
     for (int r = 0; r < R; ++r) add(a[r], u, ld(x[r], i));
   }
-  if (i < pd && j < 4) {
+  if (i < pd && run < 4) {
     const float4 u = ld(q, i);
 #pragma unroll
     for (int r = 0; r < R; ++r) add(a[r], u, ld(x[r], i));
@@ -527,7 +538,7 @@ __device__ __forceinline__ void metric_exact_g8n(int metric, const float* __rest
 #pragma unroll
   for (int r = 0; r < R; ++r) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) a[r][c] = a[r][c] + lane_xor(a[r][c], 4);
+    for (int c = 0; c < 4; ++c) a[r][c] = a[r][c] + lane_mirror8(a[r][c]);
 #pragma unroll
     for (int c = 0; c < 4; ++c) a[r][c] = a[r][c] + lane_xor(a[r][c], 2);
 #pragma unroll
