@@ -160,13 +160,32 @@ int CombinedScan(Ctx* c, const vdbg_segment* segs, size_t nseg, const std::vecto
   float* cd = w.take<float>(nq * kk);
   {
     ProfScope ps(c, "compact", s);
+    // the segments' masks compacted in one launch and their rows gathered in another, up to
+    // kMultiParts segments at a time
+    CompactMulti cm{};
+    GatherMulti gm{};
+    auto flush = [&]() -> int {
+      VDBG_RETURN_IF_ERROR(CompactGatherMulti(cm, gm, s));
+      cm.n = 0;
+      gm.n = 0;
+      return kOk;
+    };
     size_t at = 0;
     for (size_t p = 0; p < nseg; ++p) {
       const Dataset& d = segs[p].rows->d;
       const uint32_t n = uint32_t(rows[p]);
       if (n == 0) continue;
-      if (allow[p] != nullptr)
-        VDBG_RETURN_IF_ERROR(CompactIdsSmall(allow[p], uint32_t(d.n), n, ids + at, s));
+      if (cm.n == kMultiParts || gm.n == kMultiParts) VDBG_RETURN_IF_ERROR(flush());
+      if (allow[p] != nullptr) {
+        const size_t nwords = (d.n + 63) / 64;
+        if (nwords > size_t(kCompactBlockWords) || n > kCompactBlockIds)
+          return SetError(kInternal, "combined scan: mask too large");
+        cm.w[cm.n] = allow[p];
+        cm.ids[cm.n] = ids + at;
+        cm.nwords[cm.n] = uint32_t(nwords);
+        cm.N[cm.n] = uint32_t(d.n);
+        ++cm.n;
+      }
       GatherParts g{};
       g.a = reinterpret_cast<const uint4*>(d.src.X);
       g.ao = reinterpret_cast<uint4*>(X + at * pd);
@@ -182,9 +201,12 @@ int CombinedScan(Ctx* c, const vdbg_segment* segs, size_t nseg, const std::vecto
       g.exto = ext + at;
       g.ids = allow[p] != nullptr ? ids + at : nullptr;
       g.n = n;
-      VDBG_RETURN_IF_ERROR(GatherRows(g, s));
+      gm.g[gm.n] = g;
+      gm.start[gm.n + 1] = gm.start[gm.n] + uint64_t(n) * (g.wa + g.wb + g.wc + 1);
+      ++gm.n;
       at += n;
     }
+    VDBG_RETURN_IF_ERROR(flush());
   }
   cs.X = X;
   cs.X16 = X16;

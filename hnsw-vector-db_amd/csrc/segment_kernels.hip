@@ -53,10 +53,9 @@ __global__ void k_compact_ids(const uint64_t* __restrict__ w, size_t nwords, uin
 // kCompactBlockIds allowed rows, in one block: each thread takes a run of consecutive words,
 // the block scans the runs' counts in LDS, and each thread writes its run's ids from its
 // offset.  (One launch instead of the count / scan / write sequence, for sparse masks.)
-__global__ __launch_bounds__(1024) void k_compact_block(const uint64_t* __restrict__ w,
-                                                        uint32_t nwords, uint32_t N,
-                                                        uint32_t* __restrict__ ids) {
-  __shared__ uint32_t wave_tot[16];
+__device__ __forceinline__ void compact_block(const uint64_t* __restrict__ w, uint32_t nwords,
+                                              uint32_t N, uint32_t* __restrict__ ids,
+                                              uint32_t (&wave_tot)[16]) {
   const uint32_t t = threadIdx.x;
   const uint32_t per = (nwords + 1023) / 1024;
   const uint32_t lo = min(nwords, t * per), hi = min(nwords, lo + per);
@@ -90,11 +89,22 @@ __global__ __launch_bounds__(1024) void k_compact_block(const uint64_t* __restri
     }
   }
 }
+__global__ __launch_bounds__(1024) void k_compact_block(const uint64_t* __restrict__ w,
+                                                        uint32_t nwords, uint32_t N,
+                                                        uint32_t* __restrict__ ids) {
+  __shared__ uint32_t wave_tot[16];
+  compact_block(w, nwords, N, ids, wave_tot);
+}
+// Several masks, one block each (CompactMulti).
+__global__ __launch_bounds__(1024) void k_compact_multi(CompactMulti m) {
+  __shared__ uint32_t wave_tot[16];
+  const int b = blockIdx.x;
+  compact_block(m.w[b], m.nwords[b], m.N[b], m.ids[b], wave_tot);
+}
 
-// The compacted rows' parts in one launch (GatherParts, vdbg_internal.h).
-__global__ __launch_bounds__(256) void k_gather_compact(GatherParts g) {
+// Thread t of a gather: row t / W, 16-byte column t % W of the parts (GatherParts).
+__device__ __forceinline__ void gather_one(const GatherParts& g, size_t t) {
   const uint32_t W = g.wa + g.wb + g.wc + 1;
-  const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
   if (t >= size_t(g.n) * W) return;
   const uint32_t r = uint32_t(t / W), col = uint32_t(t - size_t(r) * W);
   const size_t src = g.ids != nullptr ? g.ids[r] : r;
@@ -111,6 +121,31 @@ __global__ __launch_bounds__(256) void k_gather_compact(GatherParts g) {
     if (g.i8 != nullptr) g.i8o[r] = g.i8[src];
     if (g.ext != nullptr) g.exto[r] = g.ext[src];
   }
+}
+
+// The compacted rows' parts in one launch (GatherParts, vdbg_internal.h).
+__global__ __launch_bounds__(256) void k_gather_compact(GatherParts g) {
+  gather_one(g, blockIdx.x * size_t(blockDim.x) + threadIdx.x);
+}
+// Several row sets' gathers in one launch: part p takes threads [start[p], start[p + 1]).
+__global__ __launch_bounds__(256) void k_gather_multi(GatherMulti m) {
+  const uint64_t t = blockIdx.x * uint64_t(blockDim.x) + threadIdx.x;
+  if (t >= m.start[m.n]) return;
+  int p = 0;
+  while (t >= m.start[p + 1]) ++p;
+  gather_one(m.g[p], t - m.start[p]);
+}
+
+int CompactGatherMulti(const CompactMulti& cm, const GatherMulti& gm, hipStream_t s) {
+  if (cm.n > 0) {
+    k_compact_multi<<<dim3(unsigned(cm.n)), 1024, 0, s>>>(cm);
+    VDBG_HIP(hipGetLastError());
+  }
+  if (gm.n > 0 && gm.start[gm.n] > 0) {
+    k_gather_multi<<<dim3(unsigned((gm.start[gm.n] + 255) / 256)), 256, 0, s>>>(gm);
+    VDBG_HIP(hipGetLastError());
+  }
+  return kOk;
 }
 
 int GatherRows(const GatherParts& g, hipStream_t s) {
@@ -322,12 +357,17 @@ ScanScratch::~ScanScratch() {
 // PrepareQuery (collection_impl.cc:1023-1034): one wave per query copies dim values into a
 // zero-padded row and flags a non-finite value; for cosine, NormalizeVector
 // (dataset.cc:33-41): fp64 sum of squares in index order, inv = float(1 / sqrt(sum)), fp32
-// multiply.  status: 0 ok, 1 non-finite, 2 zero vector under cosine.
+// multiply.  status: 0 ok, 1 non-finite, 2 zero vector under cosine.  The sum is one chain
+// of adds in index order, so one lane runs it, over the query staged in LDS by the whole wave
+// (kPrepChunk values at a time), not over its own global loads.
+constexpr int kPrepChunk = 512;
 __global__ __launch_bounds__(256) void k_prepare(const float* __restrict__ raw, int nq, int dim,
                                                  int pd, int cosine, float* __restrict__ out,
                                                  int* __restrict__ status) {
+  __shared__ float stage_all[4][kPrepChunk];
   const int q = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (q >= nq) return;
+  float* stage = stage_all[threadIdx.x >> 6];
   const int lane = lane_id();
   const float* v = raw + size_t(q) * dim;
   float* o = out + size_t(q) * pd;
@@ -341,9 +381,21 @@ __global__ __launch_bounds__(256) void k_prepare(const float* __restrict__ raw, 
   int st = bad ? 1 : 0;
   float inv = 1.f;
   if (!bad && cosine) {
+    double norm = 0;
+    for (int c0 = 0; c0 < dim; c0 += kPrepChunk) {
+      const int n = min(kPrepChunk, dim - c0);
+      for (int i = lane; i < n; i += kWave) stage[i] = v[c0 + i];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (lane == 0)
+        for (int i = 0; i < n; ++i)
+          norm += static_cast<double>(stage[i]) * static_cast<double>(stage[i]);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
     if (lane == 0) {
-      double norm = 0;
-      for (int i = 0; i < dim; ++i) norm += static_cast<double>(v[i]) * static_cast<double>(v[i]);
       if (!(norm > 0) || !isfinite(norm))
         st = 2;
       else

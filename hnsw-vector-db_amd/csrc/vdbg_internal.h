@@ -449,6 +449,21 @@ constexpr int kCompactBlockWords = 32 * 1024;
 constexpr uint32_t kCompactBlockIds = 65536;
 int CompactIdsSmall(const uint64_t* allow, uint32_t N, uint32_t count, uint32_t* ids,
                     hipStream_t s);
+// Up to kMultiParts masks compacted in one launch (one block each, the limits of
+// CompactIdsSmall per mask) and up to kMultiParts row sets gathered in another.
+constexpr int kMultiParts = 16;
+struct CompactMulti {
+  const uint64_t* w[kMultiParts];
+  uint32_t* ids[kMultiParts];
+  uint32_t nwords[kMultiParts], N[kMultiParts];
+  int n;
+};
+struct GatherMulti {
+  GatherParts g[kMultiParts];
+  uint64_t start[kMultiParts + 1];  // part p's threads: [start[p], start[p + 1])
+  int n;
+};
+int CompactGatherMulti(const CompactMulti& cm, const GatherMulti& gm, hipStream_t s);
 
 // The exhaustive scan under dense allow words (null: every row): rows compacted when at most
 // half are allowed.  allowed: the number of allowed rows when the caller knows it (read on the
