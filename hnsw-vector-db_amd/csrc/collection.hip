@@ -379,8 +379,11 @@ int CollectionSearch(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg, size_
     raw_q = static_cast<const float*>(raw.p);
   }
   VDBG_RETURN_IF_ERROR(Alloc(&Q, nq * pd * 4, s));
-  VDBG_RETURN_IF_ERROR(PrepareQueries(c, raw_q, nq, dim, pd, metric,
-                                      static_cast<float*>(Q.p), s));
+  // the preparation runs while the host sets up the rest; its status is checked before any
+  // search is queued
+  PrepPending prep;
+  VDBG_RETURN_IF_ERROR(PrepareQueriesLaunch(c, raw_q, nq, dim, pd, metric,
+                                            static_cast<float*>(Q.p), s, &prep));
   const float* q = static_cast<const float*>(Q.p);
 
   const size_t np = std::max<size_t>(nseg, 1), slice = nq * k;
@@ -398,6 +401,7 @@ int CollectionSearch(vdbg_ctx* ctx, const vdbg_segment* segs, size_t nseg, size_
   if (!allow_all.empty())
     VDBG_HIP(hipMemcpyAsync(allow_dev.p, allow_all.data(), allow_all.size() * 8,
                             hipMemcpyHostToDevice, s));
+  VDBG_RETURN_IF_ERROR(PrepareQueriesCheck(&prep));
   std::vector<uint64_t> dch(nq);
 
   // One index search of segment p into (ids, dists) [nq][kk] with the given allow words:

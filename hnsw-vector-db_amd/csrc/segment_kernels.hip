@@ -409,26 +409,42 @@ __global__ __launch_bounds__(256) void k_prepare(const float* __restrict__ raw, 
   if (lane == 0) status[q] = st;
 }
 
-int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
-                   float* out, hipStream_t s) {
+PrepPending::~PrepPending() {
+  if (st != nullptr) (void)hipFreeAsync(st, s);
+}
+
+int PrepareQueriesLaunch(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
+                         float* out, hipStream_t s, PrepPending* pp) {
+  pp->nq = nq;
+  pp->s = s;
   if (nq == 0) return kOk;
-  int* st = nullptr;
-  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&st), nq * sizeof(int), s));
-  {
-    ProfScope ps(c, "prepare_queries", s);
-    k_prepare<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(raw, int(nq), int(dim), int(pd),
-                                                           metric == 2 ? 1 : 0, out, st);
-    VDBG_HIP(hipGetLastError());
-  }
-  std::vector<int> h(nq);
-  VDBG_HIP(hipMemcpyAsync(h.data(), st, nq * sizeof(int), hipMemcpyDeviceToHost, s));
-  VDBG_HIP(hipStreamSynchronize(s));
-  (void)hipFreeAsync(st, s);
-  for (size_t i = 0; i < nq; ++i) {
+  VDBG_HIP(hipMallocAsync(reinterpret_cast<void**>(&pp->st), nq * sizeof(int), s));
+  ProfScope ps(c, "prepare_queries", s);
+  k_prepare<<<dim3(unsigned((nq + 3) / 4)), 256, 0, s>>>(raw, int(nq), int(dim), int(pd),
+                                                         metric == 2 ? 1 : 0, out, pp->st);
+  VDBG_HIP(hipGetLastError());
+  return kOk;
+}
+
+int PrepareQueriesCheck(PrepPending* pp) {
+  if (pp->nq == 0 || pp->st == nullptr) return kOk;
+  std::vector<int> h(pp->nq);
+  VDBG_HIP(hipMemcpyAsync(h.data(), pp->st, pp->nq * sizeof(int), hipMemcpyDeviceToHost, pp->s));
+  VDBG_HIP(hipStreamSynchronize(pp->s));
+  (void)hipFreeAsync(pp->st, pp->s);
+  pp->st = nullptr;
+  for (size_t i = 0; i < pp->nq; ++i) {
     if (h[i] == 1) return SetError(kInvalidArgument, "query has a NaN or infinite value");
     if (h[i] == 2) return SetError(kInvalidArgument, "a zero query cannot be normalized for cosine");
   }
   return kOk;
+}
+
+int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
+                   float* out, hipStream_t s) {
+  PrepPending pp;
+  VDBG_RETURN_IF_ERROR(PrepareQueriesLaunch(c, raw, nq, dim, pd, metric, out, s, &pp));
+  return PrepareQueriesCheck(&pp);
 }
 
 // ---------------------------------------------------------------- merge

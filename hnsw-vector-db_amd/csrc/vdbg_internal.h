@@ -420,6 +420,21 @@ int MergeParts(Ctx* c, const MergeArgs& a, hipStream_t s);
 // (a query with a non-finite value, or a zero query under cosine, is InvalidArgument).
 int PrepareQueries(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
                    float* out, hipStream_t s);
+// The same in two halves, so that host work can run between the launch and the wait: the
+// launch queues the preparation and its per-query status, the check waits for the status and
+// turns it into the error (the pending status is freed on the stream either way).
+struct PrepPending {
+  int* st = nullptr;
+  size_t nq = 0;
+  hipStream_t s = nullptr;
+  PrepPending() = default;
+  PrepPending(const PrepPending&) = delete;
+  PrepPending& operator=(const PrepPending&) = delete;
+  ~PrepPending();
+};
+int PrepareQueriesLaunch(Ctx* c, const float* raw, size_t nq, size_t dim, size_t pd, int metric,
+                         float* out, hipStream_t s, PrepPending* pp);
+int PrepareQueriesCheck(PrepPending* pp);
 // The scratch of one scan pipeline other than the context's own (a lane of a collection
 // search running several segments' scans side by side on their own streams).
 struct ScanScratch {
