@@ -212,7 +212,8 @@ int CombinedScan(Ctx* c, const vdbg_segment* segs, size_t nseg, const std::vecto
   cs.X16 = X16;
   cs.rn = rn;
   cs.Sbuf = nullptr;
-  VDBG_RETURN_IF_ERROR(GatherSample(c, &cs, s, sample));
+  // only as many sample rows as the one scan below uses
+  VDBG_RETURN_IF_ERROR(GatherSample(c, &cs, s, sample, SampleWant(c, cs, nq, kk)));
   int rc = RunScan(c, &cs, q, nq, kk, nullptr, cids, cd, s);
   if (rc == kOk) {
     MergeArgs a{int(nq), 1, int(kk), cd, cids, ext, nullptr, out_ext, out_d};

@@ -561,8 +561,10 @@ size_t SampleBytes(const ScanSource& src, uint32_t smax) {
                             : 0) + 256;
 }
 
-int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf) {
-  const uint32_t smax = SampleRows(src->N);
+int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf, uint32_t cap) {
+  // (a power-of-two prefix of a larger sample holds the same rows in the same positions, so
+  // a sample gathered only as large as its one scan uses is that scan's sample exactly)
+  const uint32_t smax = std::min(SampleRows(src->N), std::max<uint32_t>(cap, 1));
   int bits = 0;
   while ((1u << bits) < smax) ++bits;
   const size_t pd = src->pd;
@@ -600,7 +602,7 @@ int BuildSample(Ctx* c, ScanSource* src, hipStream_t s) {
   if (src->Smax != 0) return kOk;
   void* buf = nullptr;
   VDBG_HIP(hipMalloc(&buf, SampleBytes(*src, SampleRows(src->N))));
-  const int rc = GatherSample(c, src, s, buf);
+  const int rc = GatherSample(c, src, s, buf, ~0u);
   if (rc != kOk) {
     (void)hipFree(buf);
     return rc;
@@ -2916,6 +2918,21 @@ static int TinyScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t k
   return kOk;
 }
 
+// The sample size RunScan plans for a batch (before the cap of the source's sample): S >=
+// kk * N / P, P = 160 for large batches on the exact GEMMs, 640 otherwise, and at least
+// 16 * max(128, 4 kk) rows and N / 64, rounded up to a power of two.
+uint32_t SampleWant(const Ctx* c, const ScanSource& src, size_t nq, size_t kk) {
+  const uint32_t N = src.N;
+  const bool try16 = c->fp16_gemm && src.X16 != nullptr;
+  const int split = src.kind == 1 ? 1 : (src.x16_parts == 2 ? 2 : (src.x16_approx ? 3 : 0));
+  const uint64_t passes = try16 && split == 0 && nq >= 1024 ? 160 : 640;  // (int8 too)
+  const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,
+                                              uint64_t(N) * kk / passes});
+  uint32_t S = 1;
+  while (S < s_want && S < (1u << 30)) S *= 2;
+  return S;
+}
+
 int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
             const uint64_t* allow, uint32_t* out_ids, float* out_d, hipStream_t s,
             Workspace* ws, Workspace* ws2) {
@@ -2992,11 +3009,7 @@ int RunScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   // smallest, 640 otherwise (N / 64 at k = 10).  (Measured at 1M x 128, k = 10, on the int8
   // GEMM: a 16,384-row sample saved 0.07 ms of pre-pass but its threshold admitted ~300 rows
   // per query instead of ~110, and the main pass and select lost 0.17 ms.)
-  uint32_t S = 1;
-  const uint64_t passes = try16 && split == 0 && nq >= 1024 ? 160 : 640;  // (int8 too)
-  const uint64_t s_want = std::max<uint64_t>({16ull * std::max<uint64_t>(128, 4 * kk), N / 64,
-                                              uint64_t(N) * kk / passes});
-  while (S < s_want && S < (1u << 30)) S *= 2;
+  uint32_t S = SampleWant(c, *src, nq, kk);
   // Small batches of integer rows (at most 128 queries) choose between the int8 and the
   // fp32 main pass on the device (no host round trip before the main pass).
   const bool gated = nq <= 128 && split == 0 && try8 && !try8op;

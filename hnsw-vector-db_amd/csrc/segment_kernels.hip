@@ -196,6 +196,8 @@ int CountAllowed(Ctx* c, const uint64_t* allow, uint32_t N, uint32_t* count, hip
 
 // The scan over the allowed rows only: compact rows (ascending), scan without a mask, map
 // the compact indexes back to row ids.
+constexpr uint32_t kCompactOneBlock = 16384;
+
 int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
                 const uint64_t* allow, uint32_t count, uint32_t* out_ids, float* out_d,
                 hipStream_t s, ScanScratch* lane) {
@@ -251,7 +253,9 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   void* tmp = nullptr;
   {
     ProfScope ps(c, "compact", s);
-    if (nwords <= size_t(kCompactBlockWords) && count <= kCompactBlockIds) {
+    // one block for sparse masks; the device-wide count, scan and write past kCompactOneBlock
+    // ids (one block writing 61k ids took 41-55 us)
+    if (nwords <= size_t(kCompactBlockWords) && count <= kCompactOneBlock) {
       k_compact_block<<<1, 1024, 0, s>>>(allow, uint32_t(nwords), N, ids);
     } else {
       k_word_counts<<<dim3(unsigned((nwords + 255) / 256)), 256, 0, s>>>(allow, nwords, N, cnt);
@@ -298,7 +302,8 @@ int CompactScan(Ctx* c, ScanSource* src, const float* Q, size_t nq, size_t kk,
   cs.C = src->kind == 1 ? static_cast<const uint8_t*>(rows) : nullptr;
   cs.rn = rn;
   cs.Sbuf = nullptr;
-  int rc = GatherSample(c, &cs, s, sample);
+  // only as many sample rows as this one scan uses
+  int rc = GatherSample(c, &cs, s, sample, SampleWant(c, cs, nq, kk));
   if (rc == kOk)
     rc = RunScan(c, &cs, Q, nq, kk, nullptr, out_ids, out_d, s,
                  lane != nullptr ? &lane->ws : nullptr, lane != nullptr ? &lane->ws2 : nullptr);

@@ -490,10 +490,12 @@ int BuildSample(Ctx* c, ScanSource* src, hipStream_t s);
 // Starts a call's count of exact re-scans at zero (host and, when needed, device).
 int ResetFallbacks(Ctx* c, hipStream_t s);
 // The sample rows of an N-row source, its buffer size, and the gather into caller memory
-// (at least SampleBytes, any alignment) for sources that live one call.
+// (at least SampleBytes, any alignment) for sources that live one call, of at most cap rows
+// (SampleWant: the rows that call's scan uses).  SampleWant is the sample size RunScan plans.
 uint32_t SampleRows(uint32_t N);
 size_t SampleBytes(const ScanSource& src, uint32_t smax);
-int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf);
+int GatherSample(Ctx* c, ScanSource* src, hipStream_t s, void* buf, uint32_t cap);
+uint32_t SampleWant(const Ctx* c, const ScanSource& src, size_t nq, size_t kk);
 void FreeSample(ScanSource* src);
 
 // Host-pointer staging shared by the _host entry points.  The host writes the queries (and
