@@ -1517,7 +1517,7 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
     return;
   }
 
-  // Flat rows score eight lanes a row (metric_exact_g8, int8_distance_g8: whole 128-byte runs
+  // Flat rows score eight lanes a row (metric_exact_g8n, int8_distance_g8n: whole 128-byte runs
   // of a row per group load) where the scorer's order has that form; eight keys a round, each
   // key's distance then handed to its own lane.
   constexpr bool kGroup = std::is_same<Scorer, FlatScorer>::value || kI8;

@@ -148,24 +148,6 @@ int CompactGatherMulti(const CompactMulti& cm, const GatherMulti& gm, hipStream_
   return kOk;
 }
 
-int GatherRows(const GatherParts& g, hipStream_t s) {
-  const size_t total = size_t(g.n) * (g.wa + g.wb + g.wc + 1);
-  if (total == 0) return kOk;
-  k_gather_compact<<<dim3(unsigned((total + 255) / 256)), 256, 0, s>>>(g);
-  VDBG_HIP(hipGetLastError());
-  return kOk;
-}
-
-int CompactIdsSmall(const uint64_t* allow, uint32_t N, uint32_t count, uint32_t* ids,
-                    hipStream_t s) {
-  const size_t nwords = (size_t(N) + 63) / 64;
-  if (nwords > size_t(kCompactBlockWords) || count > kCompactBlockIds)
-    return SetError(kInternal, "CompactIdsSmall: mask too large");
-  k_compact_block<<<1, 1024, 0, s>>>(allow, uint32_t(nwords), N, ids);
-  VDBG_HIP(hipGetLastError());
-  return kOk;
-}
-
 __global__ void k_map_ids(uint32_t* __restrict__ out, size_t n, const uint32_t* __restrict__ ids) {
   const size_t t = blockIdx.x * size_t(blockDim.x) + threadIdx.x;
   if (t < n && out[t] != kNoId) out[t] = ids[out[t]];

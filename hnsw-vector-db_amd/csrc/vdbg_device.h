@@ -548,15 +548,6 @@ __device__ __forceinline__ void metric_exact_g8n(int metric, const float* __rest
   }
 }
 
-// metric_exact_g8n for one row per group.
-__device__ __forceinline__ float metric_exact_g8(int metric, const float* __restrict__ q,
-                                                 const float* __restrict__ x, int pd) {
-  const float* const xs[1] = {x};
-  float d[1];
-  metric_exact_g8n<1>(metric, q, xs, pd, d);
-  return d[0];
-}
-
 // One compare-exchange layer of a bitonic network over 64*E elements: partner g ^ j,
 // ascending in blocks where (g & size) == 0.
 template <int E>

@@ -457,15 +457,11 @@ struct GatherParts {
   const uint32_t* ids;                        // null: rows 0..n-1
   uint32_t n;
 };
-int GatherRows(const GatherParts& g, hipStream_t s);
-// The ascending ids of the rows a mask allows, in one launch, for masks of at most
-// kCompactBlockWords words allowing at most kCompactBlockIds rows (count, known).
+// Masks of at most kCompactBlockWords words allowing at most kCompactBlockIds rows compact
+// in one block each (k_compact_block, k_compact_multi): up to kMultiParts masks in one launch,
+// and up to kMultiParts row sets gathered in another.
 constexpr int kCompactBlockWords = 32 * 1024;
 constexpr uint32_t kCompactBlockIds = 65536;
-int CompactIdsSmall(const uint64_t* allow, uint32_t N, uint32_t count, uint32_t* ids,
-                    hipStream_t s);
-// Up to kMultiParts masks compacted in one launch (one block each, the limits of
-// CompactIdsSmall per mask) and up to kMultiParts row sets gathered in another.
 constexpr int kMultiParts = 16;
 struct CompactMulti {
   const uint64_t* w[kMultiParts];
