@@ -232,11 +232,14 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
   float* qmax = rs ? reinterpret_cast<float*>(take(nq * x->m * 4)) : nullptr;
   uint32_t* ti = R == k ? out_ids : reinterpret_cast<uint32_t*>(take(nq * R * 4));
   float* td = R == k ? out_d : reinterpret_cast<float*>(take(nq * R * 4));
-  int rc = RunScan(c, &x->coarse_ds->d.src, Q, nq, nprobe, nullptr, probe, probe_d, s);
-  if (rc == kOk && rs)
+  // the tables depend on the queries alone: queued first, they keep the GPU busy while the
+  // host plans and queues the coarse probe
+  int rc = kOk;
+  if (rs)
     rc = IvfQtabRs(c, Q, x->pd, int(nq), x->cen, x->m, x->dsub, qtab, qmax, s);
-  else if (rc == kOk && qtab != nullptr)
+  else if (qtab != nullptr)
     rc = IvfQtab(c, Q, x->pd, int(nq), x->cen, x->m, x->dsub, pre ? 1 : 0, qtab, s);
+  if (rc == kOk) rc = RunScan(c, &x->coarse_ds->d.src, Q, nq, nprobe, nullptr, probe, probe_d, s);
   if (rc == kOk) {
     IvfScanArgs a{Q, x->pd, x->dim, x->m, x->dsub, x->metric, x->coarse_ds->d.rows, x->cen,
                   x->off, x->ids, x->codes, x->term2, qtab, probe, probe_d, int(nprobe),
