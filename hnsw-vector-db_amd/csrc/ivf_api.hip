@@ -19,7 +19,8 @@ int IvfRowSums(Ctx* c, const uint32_t* off, int nlist, const uint8_t* codes, int
                const float* term2, float* rowsum, float* t2abs, hipStream_t s);
 int IvfQtab(Ctx* c, const float* Q, int pd, int nq, const float* cen, int m, int dsub,
             int twice, float* qtab, hipStream_t s);
-int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s);
+int IvfScan(Ctx* c, const IvfScanArgs& a, hipStream_t s, void* scratch);
+size_t IvfScanScratchBytes(size_t nq, size_t nprobe);
 int IvfScanDeep(Ctx* c, const IvfScanArgs& a, hipStream_t s);
 
 namespace {
@@ -217,8 +218,9 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
                   (x->m == 4 || x->m == 8 || x->m == 16);
   const bool want_qtab = pre || !l2;
   void* buf = nullptr;
+  const size_t scan_bytes = R <= 256 ? IvfScanScratchBytes(nq, nprobe) : 0;
   const size_t bytes = nq * nprobe * 8 + (want_qtab ? nq * ts * 4 : 0) + (rs ? nq * x->m * 4 : 0) +
-                       nq * R * 8 + 4096;
+                       nq * R * 8 + scan_bytes + 4096 + 256;
   VDBG_HIP(hipMallocAsync(&buf, bytes, s));
   char* p = static_cast<char*>(buf);
   auto take = [&](size_t b) {
@@ -232,6 +234,9 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
   float* qmax = rs ? reinterpret_cast<float*>(take(nq * x->m * 4)) : nullptr;
   uint32_t* ti = R == k ? out_ids : reinterpret_cast<uint32_t*>(take(nq * R * 4));
   float* td = R == k ? out_d : reinterpret_cast<float*>(take(nq * R * 4));
+  // the scan's own scratch, allocated here with the rest (no allocation between the coarse
+  // probe and the scan)
+  void* scan_scratch = scan_bytes != 0 ? take(scan_bytes) : nullptr;
   // the tables depend on the queries alone: queued first, they keep the GPU busy while the
   // host plans and queues the coarse probe
   int rc = kOk;
@@ -250,7 +255,7 @@ static int IvfSearch(IvfIndex* x, const float* Q, size_t nq, size_t k, size_t np
       a.t2abs = x->t2abs;
       a.qmax = qmax;
     }
-    rc = R <= 256 ? IvfScan(c, a, s) : IvfScanDeep(c, a, s);
+    rc = R <= 256 ? IvfScan(c, a, s, scan_scratch) : IvfScanDeep(c, a, s);
   }
   if (rc == kOk && depth > 0) {
     rc = Rerank(c, x->ds->rows, x->pd, x->metric, Q, nq, ti, R, k, out_ids, out_d, s,

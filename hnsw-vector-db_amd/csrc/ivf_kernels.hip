@@ -1057,7 +1057,11 @@ int IvfRowSums(Ctx* c, const uint32_t* off, int nlist, const uint8_t* codes, int
   return kOk;
 }
 
-int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
+// scratch: null, or at least IvfScanScratchBytes(nq, nprobe) bytes the caller owns (no
+// allocation of its own then)
+size_t IvfScanScratchBytes(size_t nq, size_t nprobe) { return nq * 16 + nq * nprobe * 12 + 4096; }
+
+int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s, void* scratch) {
   if (a_in.nq == 0) return kOk;
   IvfScanArgs a = a_in;
   a.ondemand = a.m * kKsub > kMaxTable ? 1 : 0;  // tables above 32 KB: entries per lookup
@@ -1067,9 +1071,9 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
   const bool fast_ok = (a.m == 4 || a.m == 8 || a.m == 16) && (!l2 || a.term2 != nullptr);
   if (fast_ok) {
     // queries in nearest-list order; offsets for the inner-product table
-    void* buf = nullptr;
+    void* buf = scratch;
     const size_t nq = size_t(a.nq);
-    VDBG_HIP(hipMallocAsync(&buf, nq * 16 + nq * a.nprobe * 12 + 4096, s));
+    if (buf == nullptr) VDBG_HIP(hipMallocAsync(&buf, IvfScanScratchBytes(nq, size_t(a.nprobe)), s));
     uint32_t* key = static_cast<uint32_t*>(buf);
     uint32_t* val = key + nq;
     uint32_t* key2 = val + nq;
@@ -1139,7 +1143,7 @@ int IvfScan(Ctx* c, const IvfScanArgs& a_in, hipStream_t s) {
       if (rc == kOk && hipGetLastError() != hipSuccess) rc = SetError(kInternal, "ivf scan launch");
     }
     if (tmp != nullptr) (void)hipFreeAsync(tmp, s);
-    (void)hipFreeAsync(buf, s);
+    if (scratch == nullptr) (void)hipFreeAsync(buf, s);
     return rc;
   }
   const size_t lds = size_t(kIvfWaves) * ((a.ondemand ? 0 : a.m * kKsub) + 4 * kWave) * sizeof(float);
