@@ -540,3 +540,49 @@ def test_collection_schedules_agree(ctx, oracle, metric, memory):
         ctx.set_collection_schedule(True, 2, True)
         for ds in handles:
             ds.close()
+
+
+def test_combined_scan_over_many_segments(ctx, oracle):
+    """Twenty flat segments (more than one launch's sixteen: the masks compact and the rows
+    gather in two rounds of launches), filters of 1 % and 20 % on some segments and none on
+    others, deletes on all: the one combined scan (k x segments <= 240) returns the oracle's
+    composition of vdb's per-segment searches and merge, and so do the lanes past it."""
+    dim = 32
+    pd = vdbg.padded_dim(dim)
+    nseg = 20
+    segs, handles = [], []
+    for i in range(nseg):
+        n = 1500 + 97 * i
+        base = datagen.pad(datagen.uniform_rows(n, dim, 2100 + i) * 4, pd)
+        ext = np.arange(n, dtype=np.uint64) * 3 + 50000 * i
+        ds = vdbg.Dataset(ctx, base, dim)
+        ds.set_external_ids(ext)
+        frac = None if i % 5 == 3 else (0.01 if i % 2 == 0 else 0.2)
+        segs.append({"base": base, "ext": ext, "kind": "flat",
+                     "deleted": _mask(n, 0.03, 2140 + i),
+                     "filter": None if frac is None else _mask(n, frac, 2160 + i)})
+        handles.append(ds)
+    raw = (datagen.uniform_rows(40, dim, 2190) * 4).astype(np.float32)
+    try:
+        ctx.set_collection_schedule(True, 2, True)
+        for k in (1, 10, 30):
+            print(f"many segments k={k}", flush=True)
+            oi, od, odc, op = oracle.collection_search(segs, dim, "l2", raw, k)
+            ctx.profile(True)
+            ctx.profile_reset()
+            gi, gd, gdc, gp = vdbg.collection_search(
+                ctx, [(ds, None, sg["deleted"], sg["filter"], False)
+                      for ds, sg in zip(handles, segs)], dim, "l2", raw, k)
+            if k * nseg <= 240:
+                assert ctx.profile_get("compact")[1] == 1  # the combined scan's one gather
+            else:
+                assert ctx.profile_get("compact")[1] > 1  # the segments' own compactions
+            ctx.profile(False)
+            assert gp == op, k
+            assert np.array_equal(gi, oi), k
+            assert np.array_equal(gd.view(np.uint32), od.view(np.uint32)), k
+            assert np.array_equal(gdc, odc), k
+    finally:
+        ctx.profile(False)
+        for ds in handles:
+            ds.close()
