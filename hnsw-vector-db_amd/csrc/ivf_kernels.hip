@@ -237,10 +237,10 @@ __global__ void k_first_probe(const uint32_t* __restrict__ probe, int nprobe, in
 }
 
 // The queries grouped by their nearest list (first[q], k_first_probe's keys, masked to their
-// low bits, bins = 2^bits <= kOrderBins), lists ascending: one block counts the queries of each list in LDS, scans the
-// counts and places every query at its list's next slot.  Within a list the order is that of
-// the atomics; only the scan's scheduling depends on it, not any result.  (One launch where a
-// device radix sort of the same keys takes five.)
+// low bits, bins = 2^bits <= kOrderBins), lists ascending: one block counts the queries of
+// each list in LDS, scans the counts and places every query at its list's next slot.  Within
+// a list the order is that of the atomics; only the scan's scheduling depends on it, not any
+// result.  (One launch where a device radix sort of the same keys takes five.)
 constexpr int kOrderBins = 16384;
 __global__ __launch_bounds__(1024) void k_order_first(const uint32_t* __restrict__ first,
                                                       int nq, uint32_t mask,

@@ -1529,9 +1529,10 @@ __global__ __launch_bounds__(WPS == 1 ? 256 : 64 * WPS) void k_select(SelectArgs
   // than one (at k = 64 a stage of k + 8 keys fails the certificate often enough that its
   // second stage costs more than scoring the extra keys at once); its answer stands when
   // every later candidate provably lies behind it: the (n1+1)-th GEMM value plus the shift
-  // minus the bound exceeds the k-th exact distance.  Rows outside the buffers have GEMM value > T, at least that (n1+1)-th
-  // value, so they lie behind it too.  When no later candidate exists, or in exact mode
-  // (the GEMM order is the distance order), the outside rows are checked against T itself:
+  // minus the bound exceeds the k-th exact distance.  Rows outside the buffers have GEMM
+  // value > T, at least that (n1+1)-th value, so they lie behind it too.  When no later
+  // candidate exists, or in exact mode (the GEMM order is the distance order), the outside
+  // rows are checked against T itself:
   // the k-th exact distance is at most T + shift - eb (always so when T came from the kk-th
   // group minimum; a threshold of lower rank fails it when it kept fewer than the top k).
   // Otherwise stage 2 scores the rest of the K' and checks the same certificate at K'+1.
